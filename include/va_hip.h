@@ -1,0 +1,201 @@
+/*
+ * va_hip.h — C ABI of the MI355X (gfx950) flat/IVF vector-search library (libva_hip.so).
+ *
+ * This is the drop-in boundary that replaces gifton/VectorAccelerate's Metal path.
+ * Every entry point names the reference interface it replaces
+ * (paths relative to the reference's Sources/VectorAccelerate/).
+ *
+ * Conventions
+ *  - Plain C: opaque handles, device pointers, sizes, int status.  No C++/torch types.
+ *  - All compute entry points take DEVICE pointers (caller-owned, the reference's
+ *    encode(into:) tier, KernelProtocol.swift:42-63) and enqueue on the context's
+ *    stream.  They return once the work is enqueued unless stated otherwise; call
+ *    va_context_synchronize() before reading results on the host (the reference's
+ *    executeAndWait, Core/Metal4Context.swift:342-410).
+ *  - A context is externally synchronised: one caller at a time per context (the
+ *    reference's actor contract).  Different contexts may be used concurrently.
+ *  - Missing results use index VA_SENTINEL_INDEX (0xFFFFFFFF) and distance +inf
+ *    (int32 paths: INT32_MAX; Hamming: 0xFFFFFFFF), as FusedL2TopKKernel.swift:166 and
+ *    IVFKernels.swift:269-287 skip them.
+ *  - Top-K order everywhere: (distance ascending, index ascending); MAX mode orders
+ *    (value descending, index ascending).  NaN orders after every number.
+ *  - Row-major matrices; counts are uint32 (indices must fit below 0xFFFFFFFF).
+ */
+#ifndef VA_HIP_H
+#define VA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VA_HIP_ABI_VERSION 1
+#define VA_SENTINEL_INDEX 0xFFFFFFFFu
+/* largest k accepted by the top-K entry points */
+#define VA_MAX_K 1024u
+
+/* Status codes.  Mirror VectorError / IndexError (VectorCore; Index/Types/IndexError.swift):
+ * INVALID_ARG ~ invalidInput, DIMENSION_MISMATCH ~ dimensionMismatch,
+ * OOM ~ bufferAllocationFailed, HIP ~ computeFailed. */
+typedef enum {
+    VA_OK = 0,
+    VA_ERR_INVALID_ARG = 1,
+    VA_ERR_DIMENSION_MISMATCH = 2,
+    VA_ERR_OOM = 3,
+    VA_ERR_HIP = 4,
+    VA_ERR_UNSUPPORTED = 5
+} va_status;
+
+/* Distance metrics.  L2SQ is the index's native distance (FlatIndexSearchTests.swift:577-595);
+ * COSINE = 1 - similarity (MetalComputeProvider.swift:136); DOT = -dot (maximum inner product
+ * as an ascending distance, MetalComputeProvider.swift:221-225); L2 = sqrt(L2SQ). */
+typedef enum { VA_METRIC_L2SQ = 0, VA_METRIC_COSINE = 1, VA_METRIC_DOT = 2, VA_METRIC_L2 = 3 } va_metric;
+
+/* Metal4SelectionMode (Kernels/Metal4/TopKSelectionKernel.swift:23-29) */
+typedef enum { VA_SELECT_MIN = 0, VA_SELECT_MAX = 1 } va_select_mode;
+
+typedef struct va_context va_context;
+typedef struct va_ivf va_ivf;
+
+int va_abi_version(void);
+const char* va_status_string(va_status status);
+
+/* ---- context: replaces Metal4Context / GPUContext (VectorAccelerate.swift:254;
+ *      Core/Metal4Context.swift:183-269) ------------------------------------- */
+/* Create a context on HIP device `device` with its own stream. */
+va_status va_context_create(int device, va_context** out);
+/* Create a context that enqueues on a caller-owned hipStream_t (passed as void*). */
+va_status va_context_create_with_stream(int device, void* hip_stream, va_context** out);
+va_status va_context_destroy(va_context* ctx);
+/* The hipStream_t the context enqueues on. */
+void* va_context_stream(va_context* ctx);
+int va_context_device(const va_context* ctx);
+/* executeAndWait: block until all work enqueued on the context has finished. */
+va_status va_context_synchronize(va_context* ctx);
+/* Text of the last error on this context ("" when none). */
+const char* va_last_error_message(const va_context* ctx);
+
+/* Tuning overrides of the exact top-k scan (0 restores the automatic choice).  They play the
+ * role of Metal4FusedL2Config's maxDistanceMatrixBytes / enableChunkedFallback
+ * (Kernels/Metal4/FusedL2TopKKernel.swift:91-136): CANDIDATE_CAP bounds the per-query
+ * candidate list (rows that overflow it take the exact chunked path), SAMPLE_ROWS sets the
+ * size of the threshold sample (>= num_database forces the dense path). */
+typedef enum { VA_OPT_CANDIDATE_CAP = 1, VA_OPT_SAMPLE_ROWS = 2 } va_option;
+va_status va_context_set_option(va_context* ctx, va_option option, uint64_t value);
+
+/* ---- buffers: replace getBuffer / BufferToken (Core/Metal4Context.swift:471-488;
+ *      Core/BufferPool.swift:89-200) ------------------------------------------ */
+va_status va_buffer_alloc(va_context* ctx, size_t bytes, void** device_ptr);
+va_status va_buffer_free(va_context* ctx, void* device_ptr);
+/* Stream-ordered copies.  Host memory must stay valid until the context is synchronised. */
+va_status va_buffer_upload(va_context* ctx, void* dst_device, const void* src_host, size_t bytes);
+va_status va_buffer_download(va_context* ctx, void* dst_host, const void* src_device, size_t bytes);
+
+/* ---- distances ---------------------------------------------------------------- */
+/* 1:1 pairs: out[i] = |q_i - t_i|^2 (sqrt when compute_sqrt).
+ * Replaces L2DistanceKernel.encode (Kernels/Metal4/L2DistanceKernel.swift:49-86). */
+va_status va_l2_pairs(va_context* ctx, const float* queries, const float* targets, float* out,
+                      uint32_t num_pairs, uint32_t dim, int compute_sqrt);
+/* 1:1 pairs: cosine similarity (or 1 - similarity when output_distance).
+ * Replaces CosineSimilarityKernel.encode (Kernels/Metal4/CosineSimilarityKernel.swift:50-87). */
+va_status va_cosine_pairs(va_context* ctx, const float* queries, const float* targets, float* out,
+                          uint32_t num_pairs, uint32_t dim, int output_distance);
+/* All pairs out[Q x N] = L2^2 (or L2).  Replaces the l2_distance_kernel dispatch of
+ * FusedL2TopKKernel.encodeAllPairsL2 (Kernels/Metal4/FusedL2TopKKernel.swift:1111-1150). */
+va_status va_l2_all_pairs(va_context* ctx, const float* queries, const float* database, float* out,
+                          uint32_t num_queries, uint32_t num_database, uint32_t dim, int compute_sqrt);
+/* All pairs cosine similarity (or 1 - s).  All-pairs form of CosineSimilarityKernel
+ * (orphaned cosine_similarity_general_kernel, Metal/Shaders/CosineSimilarity.metal:42-565). */
+va_status va_cosine_all_pairs(va_context* ctx, const float* queries, const float* database, float* out,
+                              uint32_t num_queries, uint32_t num_database, uint32_t dim, int output_distance);
+/* All pairs dot (|dot| when absolute_value).  Replaces DotProductKernel.encode/execute
+ * (Kernels/Metal4/DotProductKernel.swift:216-305; DotProductParameters :25-96). */
+va_status va_dot_all_pairs(va_context* ctx, const float* queries, const float* database, float* out,
+                           uint32_t num_queries, uint32_t num_database, uint32_t dim, int absolute_value);
+
+/* ---- top-K -------------------------------------------------------------------- */
+/* Fused distance + exact top-k (the Q x N matrix is never materialised).
+ * Replaces FusedL2TopKKernel.execute (Kernels/Metal4/FusedL2TopKKernel.swift:367-427) without
+ * its K <= 128 / D <= 768 limits; FusedTopKKernel is its alias (VectorAccelerate.swift:288).
+ * out_idx[Q x k], out_dist[Q x k] (out_dist may be NULL: includeDistances = false).
+ * Synchronises the context once (it reads back an overflow counter). */
+va_status va_fused_topk(va_context* ctx, va_metric metric, const float* queries, const float* database,
+                        uint32_t num_queries, uint32_t num_database, uint32_t dim, uint32_t k,
+                        uint32_t* out_idx, float* out_dist);
+/* Row-wise top-k of a value matrix values[Q x N] (sorted output).
+ * Replaces TopKSelectionKernel.encode/execute (Kernels/Metal4/TopKSelectionKernel.swift:228-368). */
+va_status va_topk_select(va_context* ctx, const float* values, uint32_t num_rows, uint32_t num_elements,
+                         uint32_t k, va_select_mode mode, uint32_t* out_idx, float* out_values);
+/* Merge two sorted top-k lists per row; b's indices are offset by chunk_base.
+ * Replaces TopKMergeKernel / merge_topk_sorted_kernel (Metal/Shaders/SearchAndRetrieval.metal:320-385). */
+va_status va_topk_merge(va_context* ctx, const uint32_t* a_idx, const float* a_dist, const uint32_t* b_idx,
+                        const float* b_dist, uint32_t num_rows, uint32_t k, uint32_t chunk_base,
+                        uint32_t* out_idx, float* out_dist);
+
+/* ---- scalar int8 quantization --------------------------------------------------- */
+/* Per-dimension affine parameters of x[N x D]: min, max, scale = max((max-min)/255, 1e-8),
+ * zero_point = -128 - round(min/scale) (int32).  Replaces ScalarQuantizationKernel's
+ * computeQuantizationParams (Kernels/Metal4/ScalarQuantizationKernel.swift:496-520) per dimension. */
+va_status va_sq_params_per_dim(va_context* ctx, const float* x, uint32_t num_vectors, uint32_t dim,
+                               float* out_min, float* out_max, float* out_scale, int32_t* out_zero_point);
+/* codes[i,d] = clamp(rint(x[i,d]/scale[d] + zp[d]), -128, 127).
+ * Replaces quantize_int8_kernel (Metal/Shaders/DataTransformations.metal:174-201) via
+ * ScalarQuantizationKernel.encodeQuantize (ScalarQuantizationKernel.swift:214-252). */
+va_status va_sq_quantize_i8(va_context* ctx, const float* x, uint64_t num_vectors, uint32_t dim,
+                            const float* scale, const int32_t* zero_point, int8_t* codes);
+/* x[i,d] = (codes[i,d] - zp[d]) * scale[d].  Replaces dequantize_int8_kernel
+ * (DataTransformations.metal:203-221). */
+va_status va_sq_dequantize_i8(va_context* ctx, const int8_t* codes, uint64_t num_vectors, uint32_t dim,
+                              const float* scale, const int32_t* zero_point, float* out);
+/* int8 scan: distance = -sum(qc * xc) accumulated in int32, exact top-k.
+ * No reference counterpart (the reference has no int8-domain distance); defined by the
+ * scalar-int8 quantize-and-scan search path.  out_dist may be NULL. */
+va_status va_i8_scan_topk(va_context* ctx, const int8_t* query_codes, const int8_t* database_codes,
+                          uint32_t num_queries, uint32_t num_database, uint32_t dim, uint32_t k,
+                          uint32_t* out_idx, int32_t* out_dist);
+
+/* ---- binary quantization -------------------------------------------------------- */
+/* codes[N x ceil(D/32)]: bit d = (x_d > 0), LSB-first.  Replaces binaryQuantize
+ * (Metal/Shaders/QuantizationShaders.metal:132-160; BinaryQuantizationKernel.swift:335-401). */
+va_status va_bq_pack(va_context* ctx, const float* x, uint32_t num_vectors, uint32_t dim, uint32_t* codes);
+/* Hamming matrix out[Q x N] (uint32).  Replaces hamming_distance_batch
+ * (Metal/Shaders/HammingDistance.metal:28-127; HammingDistanceKernel.swift:313-363) and the
+ * 1 x N binaryHammingDistance (QuantizationShaders.metal:163-187). */
+va_status va_hamming_matrix(va_context* ctx, const uint32_t* query_codes, const uint32_t* database_codes,
+                            uint32_t num_queries, uint32_t num_database, uint32_t words, uint32_t* out);
+/* Hamming scan + exact top-k, ties to the lower index (Metal4HammingResult.nearestNeighbors,
+ * HammingDistanceKernel.swift:114-120).  out_dist may be NULL. */
+va_status va_hamming_topk(va_context* ctx, const uint32_t* query_codes, const uint32_t* database_codes,
+                          uint32_t num_queries, uint32_t num_database, uint32_t words, uint32_t k,
+                          uint32_t* out_idx, uint32_t* out_dist);
+
+/* ---- IVF-Flat (L2^2) -------------------------------------------------------------- */
+/* Build an IVF index: assign every row of x to its nearest centroid (ties to the lower id,
+ * IVFStructure.findNearestCentroid, Index/Internal/IVFStructure.swift:292-307) and lay the
+ * lists out in device CSR order with insertion order inside each list
+ * (IVFStructure.prepareGPUStructure, IVFStructure.swift:347-467).  The index copies what it
+ * needs; x and centroids may be freed afterwards.  Synchronises the context. */
+va_status va_ivf_build(va_context* ctx, const float* centroids, uint32_t num_centroids, const float* x,
+                       uint32_t num_vectors, uint32_t dim, va_ivf** out);
+va_status va_ivf_destroy(va_ivf* ivf);
+/* Copy the CSR structure to the host: offsets[C+1], ids[N] (row ids in list order). */
+va_status va_ivf_get_lists(va_context* ctx, const va_ivf* ivf, uint32_t* host_offsets, uint32_t* host_ids);
+/* Coarse quantizer: probes[Q x nprobe] = the nprobe nearest centroids by (L2^2, id).
+ * Replaces IVFCoarseQuantizerKernel.findNearestCentroids (IVFCoarseQuantizerKernel.swift:133-174). */
+va_status va_ivf_probe(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
+                       uint32_t nprobe, uint32_t* probes);
+/* List scan over given probes + exact top-k over original row ids (L2^2).
+ * Replaces IVFListSearchKernel / ivf_list_search (Metal/Shaders/IVFListSearch.metal:199-339). */
+va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
+                      const uint32_t* probes, uint32_t nprobe, uint32_t k, uint32_t* out_idx, float* out_dist);
+/* Full IVF search = probe + scan.  Replaces IVFSearchPipeline.search
+ * (Index/Kernels/IVF/IVFSearchPipeline.swift:197-568). */
+va_status va_ivf_search(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
+                        uint32_t nprobe, uint32_t k, uint32_t* out_idx, float* out_dist);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VA_HIP_H */

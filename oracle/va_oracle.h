@@ -1,0 +1,119 @@
+/*
+ * va_oracle.h — CPU oracle for the flat/IVF search path (TEST INFRASTRUCTURE ONLY).
+ *
+ * This library is the checker, never the product: only tests/, the smoke check in
+ * __graft_entry__.py and the cpu_baseline leg of bench.py may load it.  The product
+ * path (libva_hip.so) never links, calls or falls back to it.
+ *
+ * It restates, in plain C, the CPU semantics of gifton/VectorAccelerate 0.5.0
+ * (Swift + Metal; the reference cannot be built on Linux, so there is no
+ * oracle/_ref build).  Each function cites the reference file:line it follows.
+ *
+ * Conventions shared with the GPU library:
+ *   - missing results: index 0xFFFFFFFF, distance +inf (int paths: INT32_MAX / 0xFFFFFFFF);
+ *   - top-K order: (distance ascending, index ascending) everywhere
+ *     (Metal4Common.h:142-159, AdvancedTopK.metal:48-52);
+ *   - a NaN distance orders after +inf (it is treated as the largest key).
+ *
+ * Pinning (how each function is checked, see tests/test_oracle.py):
+ *   fp distances        closed forms + numpy/scipy float64 on small inputs + reference KATs
+ *   top-K               numpy lexsort on small inputs + reference KATs
+ *   int8 params/codes   closed form on hand-made inputs + numpy re-derivation
+ *   int8 top-K          numpy int64 matmul + lexsort
+ *   binary pack/hamming reference KATs (packBinary, hamming 0/4/2) + numpy unpackbits
+ *   IVF                 brute-force numpy re-derivation on small inputs
+ */
+#ifndef VA_ORACLE_H
+#define VA_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* metric codes (same values as VA_METRIC_* in include/va_hip.h) */
+enum {
+    VO_METRIC_L2SQ = 0,   /* sum (q-x)^2                                     */
+    VO_METRIC_COSINE = 1, /* 1 - clamp(dot / (|q||x|)), 0 similarity if |q||x| < FLT_MIN */
+    VO_METRIC_DOT = 2,    /* -dot  (ascending order = maximum inner product) */
+    VO_METRIC_L2 = 3      /* sqrt(sum (q-x)^2)                               */
+};
+
+int vo_version(void);
+int vo_num_threads(void);
+
+/* ---- distances ---------------------------------------------------------- */
+/* 1:1 pairs, L2DistanceKernel / l2_distance (DistanceShaders.metal:169-226). */
+void vo_l2_pairs(const float* q, const float* t, int64_t P, int64_t D, int compute_sqrt, float* out);
+/* 1:1 pairs, cosine_similarity (DistanceShaders.metal:239-321). */
+void vo_cosine_pairs(const float* q, const float* t, int64_t P, int64_t D, int output_distance, float* out);
+/* All-pairs matrices, out[Q x N] row-major.
+ *   kind 0: L2^2, 1: L2, 2: cosine similarity, 3: cosine distance, 4: dot, 5: |dot|.
+ * l2_distance_kernel (L2Distance.metal:34-91), dot_product_kernel (DotProduct.metal:29-96),
+ * AccelerateFallback.batchCosineSimilarity (AccelerateFallback.swift:209-237). */
+void vo_distance_matrix(int kind, const float* q, const float* x, int64_t Q, int64_t N, int64_t D, float* out);
+/* Single (query, row) distance in double, metric as VO_METRIC_*. */
+double vo_distance(int metric, const float* q, const float* x, int64_t D);
+
+/* ---- top-K -------------------------------------------------------------- */
+/* Row-wise top-k of a value matrix (TopKSelectionKernel, SearchAndRetrieval.metal:88-156),
+ * with the (value, index) tie rule.  mode 0 = minimum, 1 = maximum (value desc, index asc).
+ * Missing slots (k > N) get index 0xFFFFFFFF and value +inf (min) / -inf (max). */
+void vo_topk_rows(const float* in, int64_t Q, int64_t N, int64_t k, int mode, uint32_t* idx, float* val);
+/* Flat exact top-k: CPUTopK.search (CPU/CPUTopK.swift:34-84) generalised to the three
+ * metrics.  accum_double=1 accumulates in double (the parity oracle); 0 accumulates in
+ * float with eight partial sums like vDSP_distancesq / vDSP_dotpr (the CPU baseline port). */
+void vo_flat_topk(int metric, const float* q, const float* x, int64_t Q, int64_t N, int64_t D,
+                  int64_t k, int accum_double, uint32_t* idx, float* dist);
+/* Merge two sorted top-k lists; b indices are offset by chunk_base
+ * (merge_topk_sorted_kernel, SearchAndRetrieval.metal:320-385). */
+void vo_topk_merge(const uint32_t* a_idx, const float* a_d, const uint32_t* b_idx, const float* b_d,
+                   int64_t Q, int64_t k, uint32_t chunk_base, uint32_t* out_idx, float* out_d);
+
+/* ---- scalar int8 quantization ------------------------------------------- */
+/* Per-dimension affine parameters over a row-major [N x D] matrix.
+ *   mn/mx = per-dimension min/max; scale = max((mx-mn)/255, 1e-8)
+ *   (ScalarQuantizationKernel.swift:496-520, asymmetric branch);
+ *   zp = -128 - round_half_away(mn/scale) as int32, so that codes span [-128, 127]
+ *   (the reference's Int8(clamping:) zero point saturates). */
+void vo_sq_params_per_dim(const float* x, int64_t N, int64_t D, float* mn, float* mx, float* scale, int32_t* zp);
+/* q = clamp(rint(x/scale + zp), -128, 127); |scale| < 1e-9 -> clamp(zp)
+ * (quantize_int8_kernel, DataTransformations.metal:174-201), per dimension d = i % D. */
+void vo_sq_quantize(const float* x, int64_t N, int64_t D, const float* scale, const int32_t* zp, int8_t* codes);
+/* x = (q - zp) * scale (dequantize_int8_kernel, DataTransformations.metal:203-221). */
+void vo_sq_dequantize(const int8_t* codes, int64_t N, int64_t D, const float* scale, const int32_t* zp, float* out);
+/* Exact int32 dot of int8 codes; distance = -dot; top-k by (distance, index). */
+void vo_i8_topk(const int8_t* qc, const int8_t* xc, int64_t Q, int64_t N, int64_t D, int64_t k,
+                uint32_t* idx, int32_t* dist);
+void vo_i8_dot_matrix(const int8_t* qc, const int8_t* xc, int64_t Q, int64_t N, int64_t D, int32_t* out);
+
+/* ---- binary quantization ------------------------------------------------ */
+/* bit d = (x_d > 0.0f), word w bit b = dimension 32w+b (binaryQuantize,
+ * QuantizationShaders.metal:132-160; Metal4BinaryVector, BinaryQuantizationKernel.swift:23-75). */
+void vo_bq_pack(const float* x, int64_t N, int64_t D, uint32_t* codes);
+/* sum popcount(q ^ x) (Metal4BinaryVector.hammingDistance, BinaryQuantizationKernel.swift:65-74). */
+void vo_hamming_matrix(const uint32_t* q, const uint32_t* x, int64_t Q, int64_t N, int64_t W, uint32_t* out);
+/* top-k of Hamming distances, stable (ties -> lower index)
+ * (Metal4HammingResult.nearestNeighbors, HammingDistanceKernel.swift:114-120). */
+void vo_hamming_topk(const uint32_t* q, const uint32_t* x, int64_t Q, int64_t N, int64_t W, int64_t k,
+                     uint32_t* idx, uint32_t* dist);
+
+/* ---- IVF ------------------------------------------------------------------ */
+/* Nearest centroid by L2^2, strict < so ties go to the lowest centroid id
+ * (IVFStructure.findNearestCentroid, IVFStructure.swift:292-307). */
+void vo_ivf_assign(const float* x, int64_t N, const float* c, int64_t C, int64_t D, int32_t* list);
+/* CSR in centroid order, entries in insertion (row) order (IVFStructure.swift:370-381).
+ * offsets[C+1], ids[N]. */
+void vo_ivf_csr(const int32_t* list, int64_t N, int64_t C, uint32_t* offsets, uint32_t* ids);
+/* Coarse probe: nprobe nearest centroids by (L2^2, id) (IVFCoarseQuantizerKernel.swift:133-174). */
+void vo_ivf_probe(const float* q, int64_t Q, const float* c, int64_t C, int64_t D, int64_t nprobe, uint32_t* probes);
+/* List scan over given probes + exact top-k by (L2^2, id) over the original row ids
+ * (ivf_list_search, IVFListSearch.metal:247-338; exact for every k). */
+void vo_ivf_scan(const float* q, int64_t Q, const float* x, int64_t D, const uint32_t* offsets, const uint32_t* ids,
+                 int64_t C, const uint32_t* probes, int64_t nprobe, int64_t k, uint32_t* idx, float* dist);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

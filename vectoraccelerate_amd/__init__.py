@@ -1,0 +1,44 @@
+"""vectoraccelerate_amd — MI355X (gfx950) flat/IVF vector search behind VectorAccelerate's API.
+
+The product is ``libva_hip.so`` (hand-written HIP, C ABI in ``include/va_hip.h``).  This
+package is the host-side mirror of the reference's kernel / index classes over that ABI.
+"""
+from ._lib import VA_MAX_K, VA_SENTINEL_INDEX, LibraryMissing
+from .context import GPUContext, Metal4Context, VectorError
+from .kernels import (
+    CosineSimilarityKernel,
+    DotProductKernel,
+    DotProductParameters,
+    FusedL2TopKKernel,
+    FusedL2TopKParameters,
+    FusedTopKKernel,
+    L2DistanceKernel,
+    Metal4FusedL2Config,
+    Metal4FusedL2TopKResult,
+    Metal4SelectionMode,
+    Metric,
+    TopKMergeKernel,
+    TopKSelectionKernel,
+)
+
+__all__ = [
+    "VA_MAX_K",
+    "VA_SENTINEL_INDEX",
+    "LibraryMissing",
+    "GPUContext",
+    "Metal4Context",
+    "VectorError",
+    "CosineSimilarityKernel",
+    "DotProductKernel",
+    "DotProductParameters",
+    "FusedL2TopKKernel",
+    "FusedL2TopKParameters",
+    "FusedTopKKernel",
+    "L2DistanceKernel",
+    "Metal4FusedL2Config",
+    "Metal4FusedL2TopKResult",
+    "Metal4SelectionMode",
+    "Metric",
+    "TopKMergeKernel",
+    "TopKSelectionKernel",
+]

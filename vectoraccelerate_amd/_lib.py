@@ -1,0 +1,103 @@
+"""ctypes binding of libva_hip.so (the C ABI declared in include/va_hip.h).
+
+The library is built in-tree by ``vectoraccelerate_amd/build.py``.  Loading fails loudly
+when it is missing: there is no CPU fallback anywhere in the product path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libva_hip.so"
+
+VA_OK = 0
+VA_ERR_INVALID_ARG = 1
+VA_ERR_DIMENSION_MISMATCH = 2
+VA_ERR_OOM = 3
+VA_ERR_HIP = 4
+VA_ERR_UNSUPPORTED = 5
+
+VA_METRIC_L2SQ = 0
+VA_METRIC_COSINE = 1
+VA_METRIC_DOT = 2
+VA_METRIC_L2 = 3
+
+VA_SELECT_MIN = 0
+VA_SELECT_MAX = 1
+
+VA_OPT_CANDIDATE_CAP = 1
+VA_OPT_SAMPLE_ROWS = 2
+
+VA_SENTINEL_INDEX = 0xFFFFFFFF
+VA_MAX_K = 1024
+
+_p = C.c_void_p
+_u32 = C.c_uint32
+_u64 = C.c_uint64
+_i32 = C.c_int
+_st = C.c_int
+
+# name -> (restype, argtypes); must list every entry point of include/va_hip.h
+SIGNATURES: dict[str, tuple] = {
+    "va_abi_version": (C.c_int, []),
+    "va_status_string": (C.c_char_p, [_st]),
+    "va_context_create": (_st, [_i32, C.POINTER(_p)]),
+    "va_context_create_with_stream": (_st, [_i32, _p, C.POINTER(_p)]),
+    "va_context_destroy": (_st, [_p]),
+    "va_context_stream": (_p, [_p]),
+    "va_context_device": (C.c_int, [_p]),
+    "va_context_synchronize": (_st, [_p]),
+    "va_last_error_message": (C.c_char_p, [_p]),
+    "va_context_set_option": (_st, [_p, _i32, _u64]),
+    "va_buffer_alloc": (_st, [_p, C.c_size_t, C.POINTER(_p)]),
+    "va_buffer_free": (_st, [_p, _p]),
+    "va_buffer_upload": (_st, [_p, _p, _p, C.c_size_t]),
+    "va_buffer_download": (_st, [_p, _p, _p, C.c_size_t]),
+    "va_l2_pairs": (_st, [_p, _p, _p, _p, _u32, _u32, _i32]),
+    "va_cosine_pairs": (_st, [_p, _p, _p, _p, _u32, _u32, _i32]),
+    "va_l2_all_pairs": (_st, [_p, _p, _p, _p, _u32, _u32, _u32, _i32]),
+    "va_cosine_all_pairs": (_st, [_p, _p, _p, _p, _u32, _u32, _u32, _i32]),
+    "va_dot_all_pairs": (_st, [_p, _p, _p, _p, _u32, _u32, _u32, _i32]),
+    "va_fused_topk": (_st, [_p, _i32, _p, _p, _u32, _u32, _u32, _u32, _p, _p]),
+    "va_topk_select": (_st, [_p, _p, _u32, _u32, _u32, _i32, _p, _p]),
+    "va_topk_merge": (_st, [_p, _p, _p, _p, _p, _u32, _u32, _u32, _p, _p]),
+    "va_sq_params_per_dim": (_st, [_p, _p, _u32, _u32, _p, _p, _p, _p]),
+    "va_sq_quantize_i8": (_st, [_p, _p, _u64, _u32, _p, _p, _p]),
+    "va_sq_dequantize_i8": (_st, [_p, _p, _u64, _u32, _p, _p, _p]),
+    "va_i8_scan_topk": (_st, [_p, _p, _p, _u32, _u32, _u32, _u32, _p, _p]),
+    "va_bq_pack": (_st, [_p, _p, _u32, _u32, _p]),
+    "va_hamming_matrix": (_st, [_p, _p, _p, _u32, _u32, _u32, _p]),
+    "va_hamming_topk": (_st, [_p, _p, _p, _u32, _u32, _u32, _u32, _p, _p]),
+    "va_ivf_build": (_st, [_p, _p, _u32, _p, _u32, _u32, C.POINTER(_p)]),
+    "va_ivf_destroy": (_st, [_p]),
+    "va_ivf_get_lists": (_st, [_p, _p, _p, _p]),
+    "va_ivf_probe": (_st, [_p, _p, _p, _u32, _u32, _p]),
+    "va_ivf_scan": (_st, [_p, _p, _p, _u32, _p, _u32, _u32, _p, _p]),
+    "va_ivf_search": (_st, [_p, _p, _p, _u32, _u32, _u32, _p, _p]),
+}
+
+_LIB: C.CDLL | None = None
+
+
+class LibraryMissing(RuntimeError):
+    """libva_hip.so is not built: run ``python -c 'import __graft_entry__ as g; g.build()'``."""
+
+
+def load(path: Path | None = None) -> C.CDLL:
+    """Load (once) and type libva_hip.so.  Raises when the library is absent."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise LibraryMissing(f"{p} not found; build it with vectoraccelerate_amd/build.py")
+    lib = C.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name, None)
+        if fn is None:  # a missing export raises AttributeError at its first use
+            continue
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _LIB = lib
+    return lib

@@ -1,0 +1,212 @@
+// va_context.hip — GPUContext (hipStream + scratch arena), buffers, status text.
+//
+// Replaces Metal4Context / GPUContext (Core/Metal4Context.swift:183-269, executeAndWait
+// :342-410, getBuffer :471-488) and BufferPool tokens (Core/BufferPool.swift:89-200).
+#include <cstdlib>
+#include <cstring>
+
+#include "va_internal.hpp"
+
+namespace va {
+
+va_status fail(va_context* ctx, va_status st, const char* fmt, ...) {
+    if (ctx) {
+        char buf[1024];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof(buf), fmt, ap);
+        va_end(ap);
+        ctx->last_error = buf;
+    }
+    return st;
+}
+
+va_status Scratch::reserve(size_t total) {
+    if (total <= ctx->scratch_bytes) return VA_OK;
+    // grow: wait for in-flight users of the old arena, then replace it
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->scratch) {
+        VA_CHECK_HIP(ctx, hipFree(ctx->scratch));
+        ctx->scratch = nullptr;
+        ctx->scratch_bytes = 0;
+    }
+    size_t want = total + total / 4;  // headroom to avoid regrowth on similar shapes
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, want);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        want = total;
+        e = hipMalloc(&p, want);
+    }
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(ctx, VA_ERR_OOM, "scratch allocation of %zu bytes failed: %s", want, hipGetErrorString(e));
+    }
+    ctx->scratch = static_cast<char*>(p);
+    ctx->scratch_bytes = want;
+    return VA_OK;
+}
+
+__global__ void fill_u32_kernel(uint32_t* p, uint64_t n, uint32_t v) {
+    uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    uint64_t step = uint64_t(gridDim.x) * blockDim.x;
+    for (; i < n; i += step) p[i] = v;
+}
+
+va_status fill_u32(va_context* ctx, uint32_t* p, uint64_t n, uint32_t v) {
+    if (n == 0) return VA_OK;
+    uint64_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    fill_u32_kernel<<<dim3(uint32_t(blocks)), dim3(256), 0, ctx->stream>>>(p, n, v);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
+DistOp metric_op(va_metric m) {
+    switch (m) {
+        case VA_METRIC_L2SQ: return OP_L2SQ;
+        case VA_METRIC_L2: return OP_L2;
+        case VA_METRIC_COSINE: return OP_COS_DIST;
+        case VA_METRIC_DOT:
+        default: return OP_NEG_DOT;
+    }
+}
+
+}  // namespace va
+
+extern "C" {
+
+int va_abi_version(void) { return VA_HIP_ABI_VERSION; }
+
+const char* va_status_string(va_status s) {
+    switch (s) {
+        case VA_OK: return "ok";
+        case VA_ERR_INVALID_ARG: return "invalid argument";
+        case VA_ERR_DIMENSION_MISMATCH: return "dimension mismatch";
+        case VA_ERR_OOM: return "device allocation failed";
+        case VA_ERR_HIP: return "HIP runtime error";
+        case VA_ERR_UNSUPPORTED: return "unsupported";
+    }
+    return "unknown status";
+}
+
+static va_status create_impl(int device, void* stream, va_context** out) {
+    if (!out) return VA_ERR_INVALID_ARG;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        return VA_ERR_HIP;
+    }
+    if (device < 0 || device >= n) return VA_ERR_INVALID_ARG;
+    va_context* ctx = new va_context();
+    ctx->device = device;
+    va::DeviceGuard g(device);
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess) ctx->num_cus = prop.multiProcessorCount;
+    if (stream) {
+        ctx->stream = static_cast<hipStream_t>(stream);
+        ctx->owns_stream = false;
+    } else {
+        // default priority, non-blocking w.r.t. the legacy null stream
+        if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+            delete ctx;
+            return VA_ERR_HIP;
+        }
+        ctx->owns_stream = true;
+    }
+    void* hw = nullptr;
+    if (hipHostMalloc(&hw, 64, hipHostMallocDefault) != hipSuccess) {
+        if (ctx->owns_stream) (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return VA_ERR_OOM;
+    }
+    ctx->host_word = static_cast<uint32_t*>(hw);
+    *out = ctx;
+    return VA_OK;
+}
+
+va_status va_context_create(int device, va_context** out) { return create_impl(device, nullptr, out); }
+
+va_status va_context_create_with_stream(int device, void* hip_stream, va_context** out) {
+    if (!hip_stream) return VA_ERR_INVALID_ARG;
+    return create_impl(device, hip_stream, out);
+}
+
+va_status va_context_destroy(va_context* ctx) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    {
+        va::DeviceGuard g(ctx->device);
+        (void)hipStreamSynchronize(ctx->stream);
+        if (ctx->scratch) (void)hipFree(ctx->scratch);
+        if (ctx->host_word) (void)hipHostFree(ctx->host_word);
+        if (ctx->owns_stream) (void)hipStreamDestroy(ctx->stream);
+    }
+    delete ctx;
+    return VA_OK;
+}
+
+void* va_context_stream(va_context* ctx) { return ctx ? static_cast<void*>(ctx->stream) : nullptr; }
+
+int va_context_device(const va_context* ctx) { return ctx ? ctx->device : -1; }
+
+va_status va_context_synchronize(va_context* ctx) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    va::DeviceGuard g(ctx->device);
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return VA_OK;
+}
+
+const char* va_last_error_message(const va_context* ctx) { return ctx ? ctx->last_error.c_str() : ""; }
+
+va_status va_context_set_option(va_context* ctx, va_option option, uint64_t value) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    switch (option) {
+        case VA_OPT_CANDIDATE_CAP: ctx->opt_candidate_cap = value; return VA_OK;
+        case VA_OPT_SAMPLE_ROWS: ctx->opt_sample_rows = value; return VA_OK;
+    }
+    return va::fail(ctx, VA_ERR_INVALID_ARG, "va_context_set_option: unknown option %d", int(option));
+}
+
+va_status va_buffer_alloc(va_context* ctx, size_t bytes, void** device_ptr) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    VA_REQUIRE(ctx, device_ptr != nullptr, "va_buffer_alloc: device_ptr is NULL");
+    VA_REQUIRE(ctx, bytes > 0, "va_buffer_alloc: size must be positive");
+    va::DeviceGuard g(ctx->device);
+    *device_ptr = nullptr;
+    hipError_t e = hipMalloc(device_ptr, bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return va::fail(ctx, VA_ERR_OOM, "va_buffer_alloc: %zu bytes: %s", bytes, hipGetErrorString(e));
+    }
+    return VA_OK;
+}
+
+va_status va_buffer_free(va_context* ctx, void* device_ptr) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    if (!device_ptr) return VA_OK;
+    va::DeviceGuard g(ctx->device);
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    VA_CHECK_HIP(ctx, hipFree(device_ptr));
+    return VA_OK;
+}
+
+va_status va_buffer_upload(va_context* ctx, void* dst_device, const void* src_host, size_t bytes) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    VA_REQUIRE(ctx, dst_device && src_host, "va_buffer_upload: NULL pointer");
+    if (bytes == 0) return VA_OK;
+    va::DeviceGuard g(ctx->device);
+    VA_CHECK_HIP(ctx, hipMemcpyAsync(dst_device, src_host, bytes, hipMemcpyHostToDevice, ctx->stream));
+    return VA_OK;
+}
+
+va_status va_buffer_download(va_context* ctx, void* dst_host, const void* src_device, size_t bytes) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    VA_REQUIRE(ctx, dst_host && src_device, "va_buffer_download: NULL pointer");
+    if (bytes == 0) return VA_OK;
+    va::DeviceGuard g(ctx->device);
+    VA_CHECK_HIP(ctx, hipMemcpyAsync(dst_host, src_device, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    return VA_OK;
+}
+
+}  // extern "C"

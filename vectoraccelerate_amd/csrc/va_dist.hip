@@ -1,0 +1,270 @@
+// va_dist.hip — fp32 distance GEMM on CDNA4 MFMA (v_mfma_f32_32x32x2_f32).
+//
+// One kernel computes every Q x N distance family of the search path:
+//   dist(q, x) from the contraction q.x and the squared norms |q|^2, |x|^2, where the
+//   norms are accumulated on the VALU from the same LDS fragments that feed the MFMA
+//   (no separate norm pass over the database).
+// Replaces the reference's per-pair scalar loops: l2_distance_kernel
+// (Metal/Shaders/L2Distance.metal:34-91), dot_product_kernel (DotProduct.metal:29-96) and the
+// distance loop of fused_l2_topk (AdvancedTopK.metal:238-242).
+//
+// Tile geometry (256 threads = 4 wave64):
+//   wave tile      = 32 queries x 128 database rows = 4 MFMA blocks of 32x32, 64 acc/lane
+//   workgroup tile = (32*WQ) queries x (128*WN) rows, WQ*WN = 4
+//   K loop         = LDS stages of KC=16 d-values, double buffered, one barrier per stage
+// MFMA operand map: A = database rows (M), B = queries (N).  The contraction index is
+// permuted so one ds_read_b128 per lane feeds four MFMA steps: at step s of an 8-wide
+// d-group, lane half h supplies d = d0 + 4h + s for both A and B.
+// Output map of a 32x32 block (lane l, acc v): row m = 8*(v/4) + 4*(l/32) + v%4,
+// column n = l%32 — so each lane owns ONE query and 64 database rows.
+#include <cfloat>
+
+#include "va_internal.hpp"
+
+namespace va {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+constexpr int KC = 16;               // d-values per LDS stage
+constexpr int LDS_STRIDE = KC + 4;   // 80-byte rows: conflict-free ds_read_b128 / ds_write_b128
+
+template <int WQ>
+struct Tile {
+    static constexpr int WN = 4 / WQ;
+    static constexpr int TQ = 32 * WQ;
+    static constexpr int TN = 128 * WN;
+    static constexpr int ROWS = TQ + TN;
+    static constexpr int CHUNKS = ROWS * (KC / 4);
+    static constexpr int CPT = (CHUNKS + 255) / 256;
+    static constexpr int STAGE = ROWS * LDS_STRIDE;
+    static constexpr size_t LDS_BYTES = size_t(2 * STAGE + 4 * 128) * sizeof(float);
+};
+
+__device__ __forceinline__ float apply_op(int op, float dot, float qq, float xx) {
+    switch (op) {
+        case OP_L2SQ:
+        case OP_L2: {
+            // cancellation can leave a tiny negative: clamp at 0, but let NaN through
+            float v = qq + xx - 2.0f * dot;
+            v = (v < 0.0f) ? 0.0f : v;
+            return op == OP_L2 ? sqrtf(v) : v;
+        }
+        case OP_COS_SIM:
+        case OP_COS_DIST: {
+            // cosine_similarity finalisation (DistanceShaders.metal:300-319)
+            float denom = sqrtf(qq) * sqrtf(xx);
+            float raw = (denom < FLT_MIN) ? 0.0f : dot / denom;
+            float s = (raw != raw) ? raw : fminf(fmaxf(raw, -1.0f), 1.0f);
+            return op == OP_COS_SIM ? s : 1.0f - s;
+        }
+        case OP_DOT: return dot;
+        case OP_ABS_DOT: return fabsf(dot);
+        default: return -dot;
+    }
+}
+
+template <int WQ, bool VEC>
+__global__ __launch_bounds__(256, 2) void dist_gemm_kernel(DistArgs a) {
+    using T = Tile<WQ>;
+    extern __shared__ float lds[];
+    float* nrm = lds + 2 * T::STAGE;  // [4 waves][128] squared norms of the wave's rows
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wq = wave % WQ;
+    const int wn = wave / WQ;
+    const int l32 = lane & 31;
+    const int hh = lane >> 5;
+
+    const uint32_t nqb = (a.Q + T::TQ - 1) / T::TQ;
+    const uint32_t qb = blockIdx.x % nqb;  // query block varies fastest: a database tile is
+    const uint32_t tb = blockIdx.x / nqb;  // consumed by consecutive workgroups (L2 / MALL reuse)
+    const uint32_t q0 = qb * T::TQ;
+    const uint32_t n0 = tb * T::TN;
+
+    // source row pointers of this thread's load chunks (fixed across stages)
+    const float* src[T::CPT];
+    int ldsoff[T::CPT];
+    uint32_t colv[T::CPT];
+#pragma unroll
+    for (int j = 0; j < T::CPT; ++j) {
+        const int c = tid + 256 * j;
+        src[j] = nullptr;
+        ldsoff[j] = -1;
+        colv[j] = 0;
+        if (c < T::CHUNKS) {
+            const int row = c >> 2;
+            const int col = (c & 3) * 4;
+            ldsoff[j] = row * LDS_STRIDE + col;
+            colv[j] = uint32_t(col);
+            if (row < T::TQ) {
+                const uint32_t qi = q0 + row;
+                if (qi < a.Q) {
+                    const uint32_t r = a.qrow ? a.qrow[qi] : qi;
+                    src[j] = a.q + int64_t(r) * a.ldq + col;
+                }
+            } else {
+                const uint32_t ni = n0 + uint32_t(row - T::TQ);
+                if (ni < a.N) src[j] = a.x + int64_t(ni) * a.ldx + col;
+            }
+        }
+    }
+
+    f32x4v pre[T::CPT];
+    auto load = [&](uint32_t d0) {
+#pragma unroll
+        for (int j = 0; j < T::CPT; ++j) {
+            f32x4v v = {0.0f, 0.0f, 0.0f, 0.0f};
+            const uint32_t d = d0 + colv[j];
+            if (src[j]) {
+                if (VEC) {
+                    if (d < a.D) v = *reinterpret_cast<const f32x4v*>(src[j] + d0);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (d + e < a.D) v[e] = src[j][d0 + e];
+                }
+            }
+            pre[j] = v;
+        }
+    };
+    auto store = [&](float* stage) {
+#pragma unroll
+        for (int j = 0; j < T::CPT; ++j)
+            if (ldsoff[j] >= 0) *reinterpret_cast<f32x4v*>(stage + ldsoff[j]) = pre[j];
+    };
+
+    f32x16 acc[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[b][v] = 0.0f;
+    float qss = 0.0f;
+    float xss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int nstages = int((a.D + KC - 1) / KC);
+    load(0);
+    store(lds);
+    __syncthreads();
+
+    const int boff = (wq * 32 + l32) * LDS_STRIDE + hh * 4;
+    const int aoff = (T::TQ + wn * 128 + l32) * LDS_STRIDE + hh * 4;
+
+    for (int s = 0; s < nstages; ++s) {
+        const bool more = (s + 1) < nstages;
+        if (more) load(uint32_t(s + 1) * KC);
+        const float* st = lds + (s & 1) * T::STAGE;
+#pragma unroll
+        for (int g = 0; g < KC / 8; ++g) {
+            const f32x4v bv = *reinterpret_cast<const f32x4v*>(st + boff + g * 8);
+            qss = fmaf(bv[0], bv[0], qss);
+            qss = fmaf(bv[1], bv[1], qss);
+            qss = fmaf(bv[2], bv[2], qss);
+            qss = fmaf(bv[3], bv[3], qss);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const f32x4v av = *reinterpret_cast<const f32x4v*>(st + aoff + b * 32 * LDS_STRIDE + g * 8);
+                xss[b] = fmaf(av[0], av[0], xss[b]);
+                xss[b] = fmaf(av[1], av[1], xss[b]);
+                xss[b] = fmaf(av[2], av[2], xss[b]);
+                xss[b] = fmaf(av[3], av[3], xss[b]);
+                acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[0], bv[0], acc[b], 0, 0, 0);
+                acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[1], bv[1], acc[b], 0, 0, 0);
+                acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[2], bv[2], acc[b], 0, 0, 0);
+                acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[3], bv[3], acc[b], 0, 0, 0);
+            }
+        }
+        if (more) store(lds + ((s + 1) & 1) * T::STAGE);
+        __syncthreads();
+    }
+
+    // combine the two lane halves of every partial sum of squares
+    const float qq = qss + __shfl_xor(qss, 32);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const float t = xss[b] + __shfl_xor(xss[b], 32);
+        if (hh == 0) nrm[wave * 128 + b * 32 + l32] = t;
+    }
+    __syncthreads();
+
+    const uint32_t qi = q0 + uint32_t(wq * 32 + l32);
+    if (qi >= a.Q) return;
+    const uint32_t nbase = n0 + uint32_t(wn * 128);
+    uint32_t thr = 0;
+    if (a.out == OUT_FILTER) thr = a.thr[qi];
+
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int mloc = b * 32 + 8 * j + 4 * hh;
+            const f32x4v xx = *reinterpret_cast<const f32x4v*>(nrm + wave * 128 + mloc);
+            float val[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) val[e] = apply_op(a.op, acc[b][4 * j + e], qq, xx[e]);
+            const uint32_t m = nbase + uint32_t(mloc);
+            if (a.out == OUT_FILTER) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t key = key_of_float(val[e]);
+                    if (m + e < a.N && key <= thr) {
+                        const uint32_t pos = atomicAdd(a.cnt + qi, 1u);
+                        if (pos < a.cap) {
+                            const int64_t o = int64_t(qi) * a.cap + pos;
+                            a.cand_key[o] = key;
+                            a.cand_id[o] = a.id_base + m + uint32_t(e);
+                        }
+                    }
+                }
+            } else if (a.out == OUT_KEYS) {
+                uint32_t* o = a.out_k + int64_t(qi) * a.ldo + m;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (m + e < a.N) o[e] = key_of_float(val[e]);
+            } else {
+                float* o = a.out_f + int64_t(qi) * a.ldo + m;
+                if (m + 3 < a.N && ((a.ldo & 3) == 0) && ((reinterpret_cast<uintptr_t>(o) & 15) == 0)) {
+                    f32x4v w = {val[0], val[1], val[2], val[3]};
+                    *reinterpret_cast<f32x4v*>(o) = w;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (m + e < a.N) o[e] = val[e];
+                }
+            }
+        }
+    }
+}
+
+template <int WQ, bool VEC>
+va_status launch_tile(va_context* ctx, const DistArgs& a) {
+    using T = Tile<WQ>;
+    const uint64_t nqb = (a.Q + T::TQ - 1) / T::TQ;
+    const uint64_t ntb = (a.N + T::TN - 1) / T::TN;
+    const uint64_t grid = nqb * ntb;
+    if (grid == 0) return VA_OK;
+    if (grid > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "distance grid too large (%llu tiles)", (unsigned long long)grid);
+    if (T::LDS_BYTES > 65536) {
+        VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(&dist_gemm_kernel<WQ, VEC>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, int(T::LDS_BYTES)));
+    }
+    dist_gemm_kernel<WQ, VEC><<<dim3(uint32_t(grid)), dim3(256), T::LDS_BYTES, ctx->stream>>>(a);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
+}  // namespace
+
+va_status launch_dist(va_context* ctx, const DistArgs& a) {
+    if (a.Q == 0 || a.N == 0) return VA_OK;
+    const bool vec = (a.D % 4 == 0) && (a.ldq % 4 == 0) && (a.ldx % 4 == 0) &&
+                     ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
+    if (a.Q <= 32) return vec ? launch_tile<1, true>(ctx, a) : launch_tile<1, false>(ctx, a);
+    if (a.Q <= 64) return vec ? launch_tile<2, true>(ctx, a) : launch_tile<2, false>(ctx, a);
+    return vec ? launch_tile<4, true>(ctx, a) : launch_tile<4, false>(ctx, a);
+}
+
+}  // namespace va

@@ -1,0 +1,235 @@
+// va_internal.hpp — shared host/device internals of libva_hip.so (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/va_hip.h"
+
+// ---------------------------------------------------------------------------
+// context
+// ---------------------------------------------------------------------------
+
+// The GPU context: one device, one stream, a grow-only scratch arena.
+// Replaces Metal4Context (device + command queue, Core/Metal4Context.swift:183-269)
+// and its BufferPool (Core/BufferPool.swift:89-200).
+struct va_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool owns_stream = false;
+    int num_cus = 256;
+    std::string last_error;
+    // test/tuning overrides of the exact top-k scan (0 = automatic)
+    uint64_t opt_candidate_cap = 0;
+    uint64_t opt_sample_rows = 0;
+    // scratch arena: partial results, counters, candidate buffers
+    char* scratch = nullptr;
+    size_t scratch_bytes = 0;
+    // pinned host word used to read back small counters
+    uint32_t* host_word = nullptr;
+};
+
+namespace va {
+
+// Records an error message on the context and returns the status.
+va_status fail(va_context* ctx, va_status st, const char* fmt, ...);
+
+// Makes `ctx->device` current for the lifetime of the guard.
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        (void)hipGetDevice(&prev);
+        if (prev != dev) (void)hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        (void)hipGetDevice(&cur);
+        if (prev >= 0 && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+// Bump allocator over the context's scratch arena.  Sizes are rounded to 256 B.
+// reserve() grows the arena (synchronising the stream first) before any carve().
+struct Scratch {
+    va_context* ctx;
+    size_t off = 0;
+    explicit Scratch(va_context* c) : ctx(c) {}
+    static size_t round(size_t b) { return (b + 255) & ~size_t(255); }
+    va_status reserve(size_t total);
+    template <typename T>
+    T* carve(size_t count) {
+        size_t b = round(count * sizeof(T));
+        T* p = reinterpret_cast<T*>(ctx->scratch + off);
+        off += b;
+        return p;
+    }
+};
+
+}  // namespace va
+
+#define VA_CHECK_HIP(ctx, expr)                                                                   \
+    do {                                                                                          \
+        hipError_t _e = (expr);                                                                   \
+        if (_e != hipSuccess)                                                                     \
+            return va::fail((ctx), _e == hipErrorOutOfMemory ? VA_ERR_OOM : VA_ERR_HIP, "%s: %s (%s:%d)", \
+                            #expr, hipGetErrorString(_e), __FILE__, __LINE__);                    \
+    } while (0)
+
+#define VA_CHECK_LAUNCH(ctx) VA_CHECK_HIP(ctx, hipGetLastError())
+
+#define VA_CHECK_STATUS(expr)          \
+    do {                               \
+        va_status _s = (expr);         \
+        if (_s != VA_OK) return _s;    \
+    } while (0)
+
+#define VA_REQUIRE(ctx, cond, ...)                                     \
+    do {                                                               \
+        if (!(cond)) return va::fail((ctx), VA_ERR_INVALID_ARG, __VA_ARGS__); \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// ordering keys shared by every top-K kernel
+// ---------------------------------------------------------------------------
+namespace va {
+
+constexpr uint32_t kSentinel = 0xFFFFFFFFu;
+
+// Ascending-orderable key of a float: -0 and +0 map to one key, NaN to the largest key.
+__host__ __device__ inline uint32_t key_of_float(float f) {
+    if (f != f) return 0xFFFFFFFFu;
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if (f == 0.0f) u = 0u;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__host__ __device__ inline float float_of_key(uint32_t k) {
+    uint32_t u = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+    return __builtin_bit_cast(float, u);
+}
+// Descending order (MAX mode), NaN still last.
+__host__ __device__ inline uint32_t key_of_float_desc(float f) {
+    if (f != f) return 0xFFFFFFFFu;
+    return ~key_of_float(f);
+}
+__host__ __device__ inline float float_of_key_desc(uint32_t k) { return float_of_key(~k); }
+// int32 ascending key
+__host__ __device__ inline uint32_t key_of_i32(int32_t v) { return uint32_t(v) ^ 0x80000000u; }
+__host__ __device__ inline int32_t i32_of_key(uint32_t k) { return int32_t(k ^ 0x80000000u); }
+
+inline uint32_t ceil_div(uint64_t a, uint64_t b) { return uint32_t((a + b - 1) / b); }
+
+}  // namespace va
+
+// ---------------------------------------------------------------------------
+// internal launchers shared between translation units
+// ---------------------------------------------------------------------------
+namespace va {
+
+// Epilogue operations of the distance GEMM.
+enum DistOp : int {
+    OP_L2SQ = 0,     // |q|^2 + |x|^2 - 2 q.x  (clamped at 0)
+    OP_L2 = 1,       // sqrt(OP_L2SQ)
+    OP_COS_SIM = 2,  // q.x / (|q||x|), 0 below FLT_MIN, clamped to [-1, 1]
+    OP_COS_DIST = 3, // 1 - OP_COS_SIM
+    OP_DOT = 4,      // q.x
+    OP_ABS_DOT = 5,  // |q.x|
+    OP_NEG_DOT = 6,  // -q.x
+};
+DistOp metric_op(va_metric m);
+
+// Output modes of the distance GEMM.
+enum DistOut : int {
+    OUT_VALUES = 0,  // out_f[q * ldo + n] = value
+    OUT_KEYS = 1,    // out_k[q * ldo + n] = key_of_float(value)
+    OUT_FILTER = 2,  // append (key, n) to the query's candidate list when key <= thr[q]
+};
+
+struct DistArgs {
+    const float* q = nullptr;   // query rows
+    const uint32_t* qrow = nullptr;  // optional query-row indirection (query i reads row qrow[i])
+    int64_t ldq = 0;
+    const float* x = nullptr;   // database rows
+    int64_t ldx = 0;
+    uint32_t Q = 0, N = 0, D = 0;
+    DistOp op = OP_L2SQ;
+    DistOut out = OUT_VALUES;
+    float* out_f = nullptr;
+    uint32_t* out_k = nullptr;
+    int64_t ldo = 0;
+    // filter mode
+    const uint32_t* thr = nullptr;
+    uint32_t* cnt = nullptr;
+    uint32_t* cand_key = nullptr;
+    uint32_t* cand_id = nullptr;
+    uint32_t cap = 0;
+    uint32_t id_base = 0;  // added to database row ids in filter mode
+};
+
+// Launch the MFMA distance GEMM.  Chooses the tile shape from Q.
+va_status launch_dist(va_context* ctx, const DistArgs& a);
+
+// Row-wise exact top-k selection (one workgroup per row).
+struct SelectArgs {
+    // source of items: either a dense key matrix (ids = column index) or candidate lists
+    const uint32_t* keys = nullptr;  // [rows x ld] keys, or candidate keys [rows x cap]
+    const uint32_t* ids = nullptr;   // candidate ids [rows x cap] (nullptr: id = column index)
+    const uint32_t* counts = nullptr; // per-row counts (candidate mode); nullptr: n for every row
+    int64_t ld = 0;
+    uint32_t n = 0;        // items per row (dense) or capacity (candidate mode)
+    uint32_t rows = 0;
+    uint32_t k = 0;
+    uint32_t id_offset = 0;        // added to output ids
+    const uint32_t* row_map = nullptr;  // output row for each input row (nullptr: identity)
+    // outputs (row stride out_ld, default k)
+    int64_t out_ld = 0;
+    uint32_t* out_idx = nullptr;   // [rows x k]
+    uint32_t* out_key = nullptr;   // [rows x k] keys (optional)
+    float* out_f = nullptr;        // [rows x k] float values (optional)
+    int32_t* out_i32 = nullptr;    // [rows x k] int32 values (optional)
+    int key_kind = 0;              // 0 float asc, 1 float desc, 2 int32, 3 uint32 (for value outputs)
+    // threshold mode: write only the k-th smallest key per row (ignores outputs above)
+    uint32_t* out_kth = nullptr;
+    // overflow detection (candidate mode): rows whose count exceeds n are listed here
+    uint32_t* overflow_count = nullptr;
+    uint32_t* overflow_rows = nullptr;
+};
+va_status launch_select(va_context* ctx, const SelectArgs& a);
+
+// fill a device u32 array (graph-safe replacement for hipMemsetAsync)
+va_status fill_u32(va_context* ctx, uint32_t* p, uint64_t n, uint32_t v);
+
+// Exact top-k over any key producer (fp32 distances, int8 dots, Hamming distances).
+// The Q x N key matrix is never materialised:
+//   1. sample pass: keys of every query against a strided sample of S rows; the k-th
+//      smallest sample key is an upper bound tau_q of the query's true k-th key;
+//   2. filter pass: every (query, row) key <= tau_q is appended to the query's candidate
+//      list (atomic counter, capacity `cap`);
+//   3. select: exact (key, id) top-k of each candidate list;
+//   4. rows whose list overflowed are recomputed exactly, chunk by chunk (rare).
+// Small databases (N <= sample) go straight to dense keys + select.
+struct KeyProducer {
+    // keys for queries [q0, q0+nq) (or rows qrow[0..nq) when qrow != nullptr) against
+    // database rows c0 + j*stride, j < cols, written to out_k[i * ldo + j]
+    virtual va_status dense(const uint32_t* qrow, uint32_t q0, uint32_t nq, uint32_t c0, uint32_t cols,
+                            uint32_t stride, uint32_t* out_k, int64_t ldo) = 0;
+    // filter pass over all queries and all rows
+    virtual va_status filter(const uint32_t* thr, uint32_t* cnt, uint32_t* ckey, uint32_t* cid, uint32_t cap) = 0;
+    virtual ~KeyProducer() = default;
+};
+
+struct ScanOutputs {
+    uint32_t* idx = nullptr;
+    float* f = nullptr;        // key_kind 0
+    int32_t* i32 = nullptr;    // key_kind 2
+    uint32_t* key = nullptr;   // raw keys (Hamming distances)
+    int key_kind = 0;
+};
+
+va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t N, uint32_t k,
+                          const ScanOutputs& out);
+
+}  // namespace va

@@ -1,0 +1,171 @@
+// va_scan.hip — exact top-k scan driver shared by the fp32, int8 and binary search paths.
+//
+// The reference picks between a fused K<=8 shader and a two-pass path that materialises
+// the Q x N distance matrix in 64 MB chunks (FusedL2TopKKernel.execute,
+// Kernels/Metal4/FusedL2TopKKernel.swift:367-427, :765-1090).  Here every k takes one path
+// and the full matrix is never stored:
+//   1. sample:  dense keys of each query against S strided rows; tau_q = k-th smallest
+//               (an upper bound of the true k-th key: the sample rows are real rows and the
+//               filter pass computes bit-identical keys for them);
+//   2. filter:  the scan kernel appends every key <= tau_q to the query's candidate list;
+//   3. select:  exact (key, id) top-k of every candidate list;
+//   4. overflow: rows whose list outgrew its capacity are recomputed exactly by chunked
+//               dense keys + select + a final select over the per-chunk winners.
+#include <algorithm>
+#include <vector>
+
+#include "va_internal.hpp"
+
+namespace va {
+
+namespace {
+constexpr uint64_t kDenseBudgetBytes = 256ull << 20;  // dense key matrix per launch
+constexpr uint32_t kMinSample = 16384;
+}  // namespace
+
+va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t N, uint32_t k,
+                          const ScanOutputs& out) {
+    SelectArgs base;
+    base.k = k;
+    base.out_idx = out.idx;
+    base.out_f = out.f;
+    base.out_i32 = out.i32;
+    base.out_key = out.key;
+    base.key_kind = out.key_kind;
+
+    // ---- plan ------------------------------------------------------------------------
+    uint64_t S = ctx->opt_sample_rows ? ctx->opt_sample_rows : std::max<uint64_t>(kMinSample, N / 64);
+    const bool direct = S >= N;
+    if (direct) {
+        // small database: dense keys in query chunks + select
+        const uint64_t per_q = uint64_t(N) * 4;
+        uint32_t qc = uint32_t(std::max<uint64_t>(1, std::min<uint64_t>(Q, kDenseBudgetBytes / per_q)));
+        Scratch s(ctx);
+        VA_CHECK_STATUS(s.reserve(Scratch::round(uint64_t(qc) * per_q)));
+        uint32_t* keys = s.carve<uint32_t>(uint64_t(qc) * N);
+        for (uint32_t q0 = 0; q0 < Q; q0 += qc) {
+            const uint32_t nq = std::min(qc, Q - q0);
+            VA_CHECK_STATUS(kp.dense(nullptr, q0, nq, 0, N, 1, keys, N));
+            SelectArgs a = base;
+            a.keys = keys;
+            a.ld = N;
+            a.n = N;
+            a.rows = nq;
+            if (out.idx) a.out_idx = out.idx + int64_t(q0) * k;
+            if (out.f) a.out_f = out.f + int64_t(q0) * k;
+            if (out.i32) a.out_i32 = out.i32 + int64_t(q0) * k;
+            if (out.key) a.out_key = out.key + int64_t(q0) * k;
+            VA_CHECK_STATUS(launch_select(ctx, a));
+        }
+        return VA_OK;
+    }
+    const uint32_t stride = uint32_t(N / S);
+    const uint64_t ratio = (uint64_t(N) + S - 1) / S;
+    uint64_t cap = ctx->opt_candidate_cap ? ctx->opt_candidate_cap
+                                          : std::max<uint64_t>(3ull * k, uint64_t(k) + 32) * ratio + 1024;
+    cap = std::min<uint64_t>(cap, N);
+    cap = (cap + 63) & ~uint64_t(63);
+    const uint64_t per_q_sample = S * 4;
+    const uint32_t qs = uint32_t(std::max<uint64_t>(1, std::min<uint64_t>(Q, kDenseBudgetBytes / per_q_sample)));
+
+    Scratch s(ctx);
+    const size_t need = Scratch::round(uint64_t(Q) * 4) * 3 + Scratch::round(uint64_t(Q) * cap * 4) * 2 +
+                        Scratch::round(256) + Scratch::round(uint64_t(qs) * per_q_sample);
+    VA_CHECK_STATUS(s.reserve(need));
+    uint32_t* thr = s.carve<uint32_t>(Q);
+    uint32_t* cnt = s.carve<uint32_t>(Q);
+    uint32_t* ovf_rows = s.carve<uint32_t>(Q);
+    uint32_t* ckey = s.carve<uint32_t>(uint64_t(Q) * cap);
+    uint32_t* cid = s.carve<uint32_t>(uint64_t(Q) * cap);
+    uint32_t* ovf_cnt = s.carve<uint32_t>(64);
+    uint32_t* skeys = s.carve<uint32_t>(uint64_t(qs) * S);
+
+    // ---- 1. sample thresholds -----------------------------------------------------------
+    for (uint32_t q0 = 0; q0 < Q; q0 += qs) {
+        const uint32_t nq = std::min(qs, Q - q0);
+        VA_CHECK_STATUS(kp.dense(nullptr, q0, nq, 0, uint32_t(S), stride, skeys, int64_t(S)));
+        SelectArgs a;
+        a.keys = skeys;
+        a.ld = int64_t(S);
+        a.n = uint32_t(S);
+        a.rows = nq;
+        a.k = k;
+        a.out_kth = thr + q0;
+        VA_CHECK_STATUS(launch_select(ctx, a));
+    }
+    // ---- 2. filter --------------------------------------------------------------------
+    VA_CHECK_STATUS(fill_u32(ctx, cnt, Q, 0));
+    VA_CHECK_STATUS(fill_u32(ctx, ovf_cnt, 1, 0));
+    VA_CHECK_STATUS(kp.filter(thr, cnt, ckey, cid, uint32_t(cap)));
+    // ---- 3. select ----------------------------------------------------------------------
+    {
+        SelectArgs a = base;
+        a.keys = ckey;
+        a.ids = cid;
+        a.counts = cnt;
+        a.ld = int64_t(cap);
+        a.n = uint32_t(cap);
+        a.rows = Q;
+        a.overflow_count = ovf_cnt;
+        a.overflow_rows = ovf_rows;
+        VA_CHECK_STATUS(launch_select(ctx, a));
+    }
+    VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->host_word, ovf_cnt, 4, hipMemcpyDeviceToHost, ctx->stream));
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    const uint32_t n_ovf = ctx->host_word[0];
+    if (n_ovf == 0) return VA_OK;
+
+    // ---- 4. exact chunked recomputation of overflowed rows ---------------------------------
+    // rows are processed in batches of R; each batch scans the database in chunks of C rows
+    const uint32_t R = std::min<uint32_t>(n_ovf, 64);
+    const uint32_t C = uint32_t(std::max<uint64_t>(k, std::min<uint64_t>(N, kDenseBudgetBytes / (uint64_t(R) * 4))));
+    const uint32_t nch = (N + C - 1) / C;
+    // The first part of the arena (thr .. ovf_rows) stays live; the rest is reused.
+    Scratch f(ctx);
+    f.off = Scratch::round(uint64_t(Q) * 4) * 3;
+    const size_t need2 = f.off + Scratch::round(uint64_t(R) * C * 4) + Scratch::round(uint64_t(R) * nch * k * 4) * 2;
+    if (need2 > ctx->scratch_bytes) {
+        // keep the overflow list across the arena regrowth
+        std::vector<uint32_t> keep(n_ovf);
+        VA_CHECK_HIP(ctx, hipMemcpy(keep.data(), ovf_rows, size_t(n_ovf) * 4, hipMemcpyDeviceToHost));
+        VA_CHECK_STATUS(f.reserve(need2));
+        VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->scratch + Scratch::round(uint64_t(Q) * 4) * 2, keep.data(),
+                                         size_t(n_ovf) * 4, hipMemcpyHostToDevice, ctx->stream));
+        VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        ovf_rows = reinterpret_cast<uint32_t*>(ctx->scratch + Scratch::round(uint64_t(Q) * 4) * 2);
+    }
+    uint32_t* dkeys = f.carve<uint32_t>(uint64_t(R) * C);
+    uint32_t* wkey = f.carve<uint32_t>(uint64_t(R) * nch * k);
+    uint32_t* wid = f.carve<uint32_t>(uint64_t(R) * nch * k);
+    for (uint32_t r0 = 0; r0 < n_ovf; r0 += R) {
+        const uint32_t nr = std::min(R, n_ovf - r0);
+        const uint32_t* rows = ovf_rows + r0;
+        for (uint32_t c = 0; c < nch; ++c) {
+            const uint32_t c0 = c * C;
+            const uint32_t cols = std::min(C, N - c0);
+            VA_CHECK_STATUS(kp.dense(rows, 0, nr, c0, cols, 1, dkeys, C));
+            SelectArgs a;
+            a.keys = dkeys;
+            a.ld = C;
+            a.n = cols;
+            a.rows = nr;
+            a.k = k;
+            a.id_offset = c0;
+            a.out_ld = int64_t(nch) * k;
+            a.out_idx = wid + int64_t(c) * k;
+            a.out_key = wkey + int64_t(c) * k;
+            VA_CHECK_STATUS(launch_select(ctx, a));
+        }
+        SelectArgs a = base;
+        a.keys = wkey;
+        a.ids = wid;
+        a.ld = int64_t(nch) * k;
+        a.n = nch * k;
+        a.rows = nr;
+        a.row_map = rows;
+        VA_CHECK_STATUS(launch_select(ctx, a));
+    }
+    return VA_OK;
+}
+
+}  // namespace va
