@@ -85,6 +85,24 @@ const char* va_last_error_message(const va_context* ctx);
 typedef enum { VA_OPT_CANDIDATE_CAP = 1, VA_OPT_SAMPLE_ROWS = 2 } va_option;
 va_status va_context_set_option(va_context* ctx, va_option option, uint64_t value);
 
+/* Phase timings of the last top-k scan, from hipEvents on the context stream.  Replaces
+ * Metal4Configuration.enableProfiling + GPUTimingInfo (Core/Metal4Context.swift:17,48-64,389-404)
+ * and IVFPhaseTimings (Index/Kernels/IVF/IVFKernels.swift:295).  With profiling on, every
+ * scan synchronises at its end to read the events. */
+typedef struct {
+    float sample_ms;        /* threshold sample: dense keys + k-th selection          */
+    float scan_ms;          /* the filtering scan kernel (the dominant kernel)         */
+    float select_ms;        /* candidate-list selection                               */
+    float fallback_ms;      /* exact recomputation of overflowed rows (0 when none)   */
+    float total_ms;         /* whole scan                                             */
+    uint32_t sample_rows;   /* 0 when the dense path ran                              */
+    uint32_t candidate_cap; /* per-query candidate capacity                            */
+    uint32_t overflow_rows; /* queries that took the exact chunked path               */
+    uint32_t scan_launches; /* number of scan-kernel launches timed in scan_ms        */
+} va_scan_timings;
+va_status va_context_set_profiling(va_context* ctx, int enable);
+va_status va_context_last_scan(const va_context* ctx, va_scan_timings* out);
+
 /* ---- buffers: replace getBuffer / BufferToken (Core/Metal4Context.swift:471-488;
  *      Core/BufferPool.swift:89-200) ------------------------------------------ */
 va_status va_buffer_alloc(va_context* ctx, size_t bytes, void** device_ptr);

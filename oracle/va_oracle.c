@@ -369,7 +369,7 @@ void vo_sq_params_per_dim(const float* x, int64_t N, int64_t D, float* mn, float
         }
     }
     for (int64_t d = 0; d < D; d++) {
-        if (N == 0) {
+        if (N == 0 || mn[d] > mx[d]) { /* no rows, or only NaN values in this dimension */
             mn[d] = 0.0f;
             mx[d] = 0.0f;
         }

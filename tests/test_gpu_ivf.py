@@ -1,0 +1,135 @@
+"""GPU parity of IVF-Flat: list assignment, CSR layout, coarse probes and the list scan against
+the CPU oracle (fp32 distances: 1e-4 relative, ids equal up to near-ties)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests.helpers import L2SQ, SENT, check_topk
+
+pytestmark = pytest.mark.gpu
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def clustered(C, D, N, Q, seed, zipf=None):
+    """configs[4] generator at reduced size: centroids N(0, 4^2), points = centroid + N(0,1),
+    cluster sizes Zipf(s) over centroid ranks (uniform when zipf is None)."""
+    g = rng(seed)
+    c = (g.standard_normal((C, D)) * 4).astype(np.float32)
+    if zipf is None:
+        p = np.full(C, 1.0 / C)
+    else:
+        p = 1.0 / np.arange(1, C + 1) ** zipf
+        p /= p.sum()
+    lab = g.choice(C, N, p=p)
+    x = (c[lab] + g.standard_normal((N, D))).astype(np.float32)
+    ql = g.choice(C, Q, p=p)
+    q = (c[ql] + g.standard_normal((Q, D))).astype(np.float32)
+    return c, x, q
+
+
+def _assignment_matches(oracle, x, c, gpu_lists):
+    """GPU list ids equal the oracle's nearest centroid except for near-ties (1e-4 relative)."""
+    ref = oracle.ivf_assign(x, c)
+    bad = np.nonzero(ref != gpu_lists)[0]
+    for i in bad:
+        d_ref = oracle.distance(0, x[i], c[ref[i]])
+        d_gpu = oracle.distance(0, x[i], c[gpu_lists[i]])
+        scale = float((x[i].astype(np.float64) ** 2).sum() + (c[ref[i]].astype(np.float64) ** 2).sum())
+        assert abs(d_gpu - d_ref) <= 1e-4 * scale, f"row {i}: gpu list {gpu_lists[i]} vs {ref[i]}"
+    return len(bad)
+
+
+def _lists_from_csr(off, ids, N):
+    lists = np.empty(N, np.int64)
+    for l in range(len(off) - 1):
+        lists[ids[off[l]:off[l + 1]]] = l
+    return lists
+
+
+@pytest.mark.parametrize("C,D,N,Q,nprobe,k,zipf", [(16, 12, 800, 20, 4, 10, 1.1), (64, 96, 20000, 50, 8, 10, 1.1),
+                                                    (256, 768, 30000, 64, 32, 10, 1.1),
+                                                    (32, 40, 5000, 30, 32, 100, None)])
+def test_ivf_build_probe_scan_match_oracle(ctx, oracle, C, D, N, Q, nprobe, k, zipf):
+    from vectoraccelerate_amd import IVFSearchConfiguration, IVFSearchPipeline
+
+    c, x, q = clustered(C, D, N, Q, C + N, zipf)
+    pipe = IVFSearchPipeline(ctx, IVFSearchConfiguration(C, nprobe, D))
+    st = pipe.prepareIndexStructure(c, x)
+    off, ids = st.lists()
+    lists = _lists_from_csr(off, ids, N)
+    _assignment_matches(oracle, x, c, lists)
+    # CSR: centroid order, insertion order inside each list (IVFStructure.swift:370-381)
+    ooff, oids = oracle.ivf_csr(lists.astype(np.int32), C)
+    np.testing.assert_array_equal(off, ooff)
+    np.testing.assert_array_equal(ids, oids)
+    # coarse probes: the nprobe nearest centroids by (L2^2, id) -- compared as a top-k
+    probes = pipe.findNearestCentroids(q, st).cpu().numpy().view(np.uint32)
+    op = oracle.ivf_probe(q, c, nprobe)
+    check_topk(L2SQ, q, c, nprobe, probes, None, op, None)
+    # list scan over the GPU's probes vs the oracle scan over the same probes and lists
+    res = pipe.searchLists(q, st, probes, k)
+    gi = res.indices.cpu().numpy().view(np.uint32)
+    gd = res.distances.cpu().numpy()
+    oi, od = oracle.ivf_scan(q, x, off, ids, probes, k)
+    check_topk(L2SQ, q, x, k, gi, gd, oi, od)
+    # the full search equals probe + scan
+    full = pipe.search(q, st, k)
+    np.testing.assert_array_equal(full.indices.cpu().numpy().view(np.uint32), gi)
+    st.close()
+
+
+def test_ivf_scan_overflow_path(ctx, oracle):
+    from vectoraccelerate_amd import IVFSearchConfiguration, IVFSearchPipeline, _lib
+
+    c, x, q = clustered(16, 32, 8000, 25, 7, 1.1)
+    pipe = IVFSearchPipeline(ctx, IVFSearchConfiguration(16, 6, 32))
+    st = pipe.prepareIndexStructure(c, x)
+    off, ids = st.lists()
+    probes = pipe.findNearestCentroids(q, st).cpu().numpy().view(np.uint32)
+    try:
+        ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 16)
+        res = pipe.searchLists(q, st, probes, 10)
+    finally:
+        ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 0)
+    oi, od = oracle.ivf_scan(q, x, off, ids, probes, 10)
+    check_topk(L2SQ, q, x, 10, res.indices.cpu().numpy().view(np.uint32), res.distances.cpu().numpy(), oi, od)
+    st.close()
+
+
+def test_ivf_probe_edge_cases(ctx, oracle):
+    """Sentinel / duplicate probes are skipped; too few candidates pad with sentinels."""
+    from vectoraccelerate_amd import IVFSearchConfiguration, IVFSearchPipeline
+
+    c, x, q = clustered(8, 16, 60, 4, 9)
+    pipe = IVFSearchPipeline(ctx, IVFSearchConfiguration(8, 2, 16))
+    st = pipe.prepareIndexStructure(c, x)
+    off, ids = st.lists()
+    probes = np.array([[0, 0], [1, SENT], [SENT, SENT], [7, 3]], np.uint32)
+    res = pipe.searchLists(q, st, probes, 50)
+    gi = res.indices.cpu().numpy().view(np.uint32)
+    oi, od = oracle.ivf_scan(q, x, off, ids, np.array([[0, SENT], [1, SENT], [SENT, SENT], [7, 3]], np.uint32), 50)
+    check_topk(L2SQ, q, x, 50, gi, res.distances.cpu().numpy(), oi, od)
+    assert np.all(gi[2] == SENT)
+    st.close()
+
+
+def test_ivf_recall_vs_flat(ctx, oracle):
+    """IVFValidationTests: recall against flat search grows with nprobe; nprobe = C is exact."""
+    from vectoraccelerate_amd import FusedL2TopKKernel, IVFSearchConfiguration, IVFSearchPipeline
+
+    c, x, q = clustered(32, 64, 10000, 40, 11)
+    flat = FusedL2TopKKernel(ctx).findNearestNeighbors(q, x, 10)
+    truth = [set(i for i, _ in r) for r in flat]
+    recalls = []
+    for nprobe in (1, 4, 32):
+        pipe = IVFSearchPipeline(ctx, IVFSearchConfiguration(32, nprobe, 64))
+        st = pipe.prepareIndexStructure(c, x)
+        res = pipe.search(q, st, 10).allResults()
+        recalls.append(np.mean([len(truth[i] & set(j for j, _ in res[i])) / 10 for i in range(len(res))]))
+        st.close()
+    assert recalls[0] <= recalls[1] <= recalls[2]
+    assert recalls[2] == 1.0

@@ -20,8 +20,33 @@ from .kernels import (
     TopKMergeKernel,
     TopKSelectionKernel,
 )
+from .ivf import IVFGPUIndexStructure, IVFSearchConfiguration, IVFSearchPipeline, IVFSearchResult
+from .quantization import (
+    BinaryQuantizationKernel,
+    BinaryQuantKernel,
+    HammingDistanceKernel,
+    Metal4BinaryVector,
+    Metal4BinaryVectorBatch,
+    Metal4QuantizationType,
+    PerDimensionParameters,
+    ScalarQuantizationKernel,
+    ScalarQuantKernel,
+)
 
 __all__ = [
+    "IVFGPUIndexStructure",
+    "IVFSearchConfiguration",
+    "IVFSearchPipeline",
+    "IVFSearchResult",
+    "BinaryQuantizationKernel",
+    "BinaryQuantKernel",
+    "HammingDistanceKernel",
+    "Metal4BinaryVector",
+    "Metal4BinaryVectorBatch",
+    "Metal4QuantizationType",
+    "PerDimensionParameters",
+    "ScalarQuantizationKernel",
+    "ScalarQuantKernel",
     "VA_MAX_K",
     "VA_SENTINEL_INDEX",
     "LibraryMissing",

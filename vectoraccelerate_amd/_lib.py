@@ -49,6 +49,8 @@ SIGNATURES: dict[str, tuple] = {
     "va_context_synchronize": (_st, [_p]),
     "va_last_error_message": (C.c_char_p, [_p]),
     "va_context_set_option": (_st, [_p, _i32, _u64]),
+    "va_context_set_profiling": (_st, [_p, _i32]),
+    "va_context_last_scan": (_st, [_p, _p]),
     "va_buffer_alloc": (_st, [_p, C.c_size_t, C.POINTER(_p)]),
     "va_buffer_free": (_st, [_p, _p]),
     "va_buffer_upload": (_st, [_p, _p, _p, C.c_size_t]),
@@ -75,6 +77,27 @@ SIGNATURES: dict[str, tuple] = {
     "va_ivf_scan": (_st, [_p, _p, _p, _u32, _p, _u32, _u32, _p, _p]),
     "va_ivf_search": (_st, [_p, _p, _p, _u32, _u32, _u32, _p, _p]),
 }
+
+
+
+class ScanTimings(C.Structure):
+    """va_scan_timings (include/va_hip.h)."""
+
+    _fields_ = [
+        ("sample_ms", C.c_float),
+        ("scan_ms", C.c_float),
+        ("select_ms", C.c_float),
+        ("fallback_ms", C.c_float),
+        ("total_ms", C.c_float),
+        ("sample_rows", C.c_uint32),
+        ("candidate_cap", C.c_uint32),
+        ("overflow_rows", C.c_uint32),
+        ("scan_launches", C.c_uint32),
+    ]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
 
 _LIB: C.CDLL | None = None
 

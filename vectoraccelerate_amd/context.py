@@ -119,6 +119,15 @@ class GPUContext:
         """Make work queued on torch's current stream visible to the context stream."""
         _torch().cuda.current_stream(self.device).synchronize()
 
+    def set_profiling(self, enable: bool) -> None:
+        """Metal4Configuration.enableProfiling: time every scan phase with hipEvents."""
+        self.check(self.lib.va_context_set_profiling(self.handle, int(bool(enable))), "va_context_set_profiling")
+
+    def last_scan_timings(self) -> dict:
+        t = _lib.ScanTimings()
+        self.check(self.lib.va_context_last_scan(self.handle, C.byref(t)), "va_context_last_scan")
+        return t.as_dict()
+
     def set_option(self, option: int, value: int) -> None:
         self.check(self.lib.va_context_set_option(self.handle, int(option), int(value)), "va_context_set_option")
 

@@ -140,6 +140,8 @@ va_status va_context_destroy(va_context* ctx) {
         (void)hipStreamSynchronize(ctx->stream);
         if (ctx->scratch) (void)hipFree(ctx->scratch);
         if (ctx->host_word) (void)hipHostFree(ctx->host_word);
+        for (auto& e : ctx->ev)
+            if (e) (void)hipEventDestroy(e);
         if (ctx->owns_stream) (void)hipStreamDestroy(ctx->stream);
     }
     delete ctx;
@@ -158,6 +160,22 @@ va_status va_context_synchronize(va_context* ctx) {
 }
 
 const char* va_last_error_message(const va_context* ctx) { return ctx ? ctx->last_error.c_str() : ""; }
+
+va_status va_context_set_profiling(va_context* ctx, int enable) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    va::DeviceGuard g(ctx->device);
+    if (enable && !ctx->ev[0]) {
+        for (auto& e : ctx->ev) VA_CHECK_HIP(ctx, hipEventCreate(&e));
+    }
+    ctx->profiling = enable != 0;
+    return VA_OK;
+}
+
+va_status va_context_last_scan(const va_context* ctx, va_scan_timings* out) {
+    if (!ctx || !out) return VA_ERR_INVALID_ARG;
+    *out = ctx->last_scan;
+    return VA_OK;
+}
 
 va_status va_context_set_option(va_context* ctx, va_option option, uint64_t value) {
     if (!ctx) return VA_ERR_INVALID_ARG;

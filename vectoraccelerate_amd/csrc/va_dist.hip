@@ -65,7 +65,7 @@ __device__ __forceinline__ float apply_op(int op, float dot, float qq, float xx)
     }
 }
 
-template <int WQ, bool VEC>
+template <int WQ, bool VEC, int OUT>
 __global__ __launch_bounds__(256, 2) void dist_gemm_kernel(DistArgs a) {
     using T = Tile<WQ>;
     extern __shared__ float lds[];
@@ -79,11 +79,24 @@ __global__ __launch_bounds__(256, 2) void dist_gemm_kernel(DistArgs a) {
     const int l32 = lane & 31;
     const int hh = lane >> 5;
 
-    const uint32_t nqb = (a.Q + T::TQ - 1) / T::TQ;
+    const uint32_t nqb = a.tiles ? 1u : (a.Q + T::TQ - 1) / T::TQ;
     const uint32_t qb = blockIdx.x % nqb;  // query block varies fastest: a database tile is
     const uint32_t tb = blockIdx.x / nqb;  // consumed by consecutive workgroups (L2 / MALL reuse)
-    const uint32_t q0 = qb * T::TQ;
-    const uint32_t n0 = tb * T::TN;
+    // Tile extent: queries qs + i (i < qc; through qrow when given) and database rows at
+    // positions rs + j*rstride (j < rc).  Flat launches derive it from blockIdx; list-major
+    // (IVF) launches read one descriptor {qs, qc, rs, rc} per workgroup.
+    uint32_t qs = qb * T::TQ, rs = tb * T::TN, qc, rc, rstride = 1;
+    if (a.tiles) {
+        const uint32_t* td = a.tiles + 4 * int64_t(blockIdx.x);
+        qs = td[0];
+        qc = td[1];
+        rs = td[2];
+        rc = td[3];
+        rstride = a.rstride;
+    } else {
+        qc = min(uint32_t(T::TQ), a.Q - qs);
+        rc = min(uint32_t(T::TN), a.N - rs);
+    }
 
     // source row pointers of this thread's load chunks (fixed across stages)
     const float* src[T::CPT];
@@ -101,14 +114,13 @@ __global__ __launch_bounds__(256, 2) void dist_gemm_kernel(DistArgs a) {
             ldsoff[j] = row * LDS_STRIDE + col;
             colv[j] = uint32_t(col);
             if (row < T::TQ) {
-                const uint32_t qi = q0 + row;
-                if (qi < a.Q) {
-                    const uint32_t r = a.qrow ? a.qrow[qi] : qi;
+                if (uint32_t(row) < qc) {
+                    const uint32_t r = a.qrow ? a.qrow[qs + row] : qs + row;
                     src[j] = a.q + int64_t(r) * a.ldq + col;
                 }
             } else {
-                const uint32_t ni = n0 + uint32_t(row - T::TQ);
-                if (ni < a.N) src[j] = a.x + int64_t(ni) * a.ldx + col;
+                const uint32_t jr = uint32_t(row - T::TQ);
+                if (jr < rc) src[j] = a.x + int64_t(rs + jr * rstride) * a.ldx + col;
             }
         }
     }
@@ -190,11 +202,12 @@ __global__ __launch_bounds__(256, 2) void dist_gemm_kernel(DistArgs a) {
     }
     __syncthreads();
 
-    const uint32_t qi = q0 + uint32_t(wq * 32 + l32);
-    if (qi >= a.Q) return;
-    const uint32_t nbase = n0 + uint32_t(wn * 128);
+    const uint32_t li = uint32_t(wq * 32 + l32);  // query slot of this lane in the tile
+    if (li >= qc) return;
+    const uint32_t orow = qs + li;                                   // dense output row
+    const uint32_t qi = (OUT == OUT_FILTER && a.qrow) ? a.qrow[orow] : orow;  // query id (filter)
     uint32_t thr = 0;
-    if (a.out == OUT_FILTER) thr = a.thr[qi];
+    if (OUT == OUT_FILTER) thr = a.thr[qi];
 
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -205,53 +218,54 @@ __global__ __launch_bounds__(256, 2) void dist_gemm_kernel(DistArgs a) {
             float val[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) val[e] = apply_op(a.op, acc[b][4 * j + e], qq, xx[e]);
-            const uint32_t m = nbase + uint32_t(mloc);
-            if (a.out == OUT_FILTER) {
+            const uint32_t jr = uint32_t(wn * 128 + mloc);  // row slot of acc element e = 0
+            if (OUT == OUT_FILTER) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const uint32_t key = key_of_float(val[e]);
-                    if (m + e < a.N && key <= thr) {
+                    if (jr + e < rc && key <= thr) {
                         const uint32_t pos = atomicAdd(a.cnt + qi, 1u);
                         if (pos < a.cap) {
+                            const uint32_t p = rs + (jr + e) * rstride;
                             const int64_t o = int64_t(qi) * a.cap + pos;
                             a.cand_key[o] = key;
-                            a.cand_id[o] = a.id_base + m + uint32_t(e);
+                            a.cand_id[o] = a.ids ? a.ids[p] : a.id_base + p;
                         }
                     }
                 }
-            } else if (a.out == OUT_KEYS) {
-                uint32_t* o = a.out_k + int64_t(qi) * a.ldo + m;
+            } else if (OUT == OUT_KEYS) {
+                uint32_t* o = a.out_k + int64_t(orow) * a.ldo + rs + jr;
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    if (m + e < a.N) o[e] = key_of_float(val[e]);
+                    if (jr + e < rc) o[e] = key_of_float(val[e]);
             } else {
-                float* o = a.out_f + int64_t(qi) * a.ldo + m;
-                if (m + 3 < a.N && ((a.ldo & 3) == 0) && ((reinterpret_cast<uintptr_t>(o) & 15) == 0)) {
+                float* o = a.out_f + int64_t(orow) * a.ldo + rs + jr;
+                if (jr + 3 < rc && ((a.ldo & 3) == 0) && ((reinterpret_cast<uintptr_t>(o) & 15) == 0)) {
                     f32x4v w = {val[0], val[1], val[2], val[3]};
                     *reinterpret_cast<f32x4v*>(o) = w;
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        if (m + e < a.N) o[e] = val[e];
+                        if (jr + e < rc) o[e] = val[e];
                 }
             }
         }
     }
 }
 
-template <int WQ, bool VEC>
+template <int WQ, bool VEC, int OUT>
 va_status launch_tile(va_context* ctx, const DistArgs& a) {
     using T = Tile<WQ>;
     const uint64_t nqb = (a.Q + T::TQ - 1) / T::TQ;
     const uint64_t ntb = (a.N + T::TN - 1) / T::TN;
-    const uint64_t grid = nqb * ntb;
+    const uint64_t grid = a.tiles ? a.ntiles : nqb * ntb;
     if (grid == 0) return VA_OK;
     if (grid > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "distance grid too large (%llu tiles)", (unsigned long long)grid);
     if (T::LDS_BYTES > 65536) {
-        VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(&dist_gemm_kernel<WQ, VEC>),
+        VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(&dist_gemm_kernel<WQ, VEC, OUT>),
                                               hipFuncAttributeMaxDynamicSharedMemorySize, int(T::LDS_BYTES)));
     }
-    dist_gemm_kernel<WQ, VEC><<<dim3(uint32_t(grid)), dim3(256), T::LDS_BYTES, ctx->stream>>>(a);
+    dist_gemm_kernel<WQ, VEC, OUT><<<dim3(uint32_t(grid)), dim3(256), T::LDS_BYTES, ctx->stream>>>(a);
     VA_CHECK_LAUNCH(ctx);
     return VA_OK;
 }
@@ -259,12 +273,17 @@ va_status launch_tile(va_context* ctx, const DistArgs& a) {
 }  // namespace
 
 va_status launch_dist(va_context* ctx, const DistArgs& a) {
-    if (a.Q == 0 || a.N == 0) return VA_OK;
+    if (a.tiles ? a.ntiles == 0 : (a.Q == 0 || a.N == 0)) return VA_OK;
     const bool vec = (a.D % 4 == 0) && (a.ldq % 4 == 0) && (a.ldx % 4 == 0) &&
                      ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
-    if (a.Q <= 32) return vec ? launch_tile<1, true>(ctx, a) : launch_tile<1, false>(ctx, a);
-    if (a.Q <= 64) return vec ? launch_tile<2, true>(ctx, a) : launch_tile<2, false>(ctx, a);
-    return vec ? launch_tile<4, true>(ctx, a) : launch_tile<4, false>(ctx, a);
+    const int wq = a.wq ? a.wq : (a.Q <= 32 ? 1 : (a.Q <= 64 ? 2 : 4));
+#define VA_DIST_CASE(W, O)                                                                 \
+    if (wq == W && a.out == O) return vec ? launch_tile<W, true, O>(ctx, a) : launch_tile<W, false, O>(ctx, a);
+    VA_DIST_CASE(1, OUT_VALUES) VA_DIST_CASE(1, OUT_KEYS) VA_DIST_CASE(1, OUT_FILTER)
+    VA_DIST_CASE(2, OUT_VALUES) VA_DIST_CASE(2, OUT_KEYS) VA_DIST_CASE(2, OUT_FILTER)
+    VA_DIST_CASE(4, OUT_VALUES) VA_DIST_CASE(4, OUT_KEYS) VA_DIST_CASE(4, OUT_FILTER)
+#undef VA_DIST_CASE
+    return fail(ctx, VA_ERR_INVALID_ARG, "launch_dist: bad output mode %d", int(a.out));
 }
 
 }  // namespace va

@@ -31,6 +31,10 @@ struct va_context {
     size_t scratch_bytes = 0;
     // pinned host word used to read back small counters
     uint32_t* host_word = nullptr;
+    // phase profiling of the top-k scan (va_context_set_profiling)
+    bool profiling = false;
+    hipEvent_t ev[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    va_scan_timings last_scan{};
 };
 
 namespace va {
@@ -167,7 +171,19 @@ struct DistArgs {
     uint32_t* cand_id = nullptr;
     uint32_t cap = 0;
     uint32_t id_base = 0;  // added to database row ids in filter mode
+    // list-major (IVF) launches: one {qs, qc, rs, rc} descriptor per workgroup; query i of a
+    // tile is row qrow[qs + i], database row j is at position rs + j*rstride, whose id is
+    // ids[position].  Q / N are ignored then.
+    const uint32_t* tiles = nullptr;
+    uint32_t ntiles = 0;
+    uint32_t rstride = 1;
+    const uint32_t* ids = nullptr;
+    int wq = 0;  // waves along queries (1, 2 or 4: tiles of 32*wq queries x 512/wq rows); 0 = from Q
 };
+
+// Tile shape of launch_dist for a given wq: queries and database rows per workgroup.
+inline uint32_t dist_tile_queries(int wq) { return 32u * uint32_t(wq); }
+inline uint32_t dist_tile_rows(int wq) { return 128u * uint32_t(4 / wq); }
 
 // Launch the MFMA distance GEMM.  Chooses the tile shape from Q.
 va_status launch_dist(va_context* ctx, const DistArgs& a);

@@ -1,0 +1,501 @@
+// va_ivf.hip — IVF-Flat (L2^2) build, coarse probe and list-major scan.
+//
+// Build (IVFStructure.assignToCluster / prepareGPUStructure, Index/Internal/IVFStructure.swift:
+// 280-307, 347-467): nearest-centroid assignment on the fp32 MFMA distance kernel (k = 1,
+// ties to the lower centroid id), CSR offsets and row ids built on the host in centroid order
+// with insertion order inside each list (as the reference does), and the list vectors gathered
+// into CSR order by a device copy kernel (the reference memcpy-gathers on the host).
+//
+// Search (IVFSearchPipeline.search, Index/Kernels/IVF/IVFSearchPipeline.swift:197-568):
+//   probe : the nprobe nearest centroids by (L2^2, id) through the exact top-k scan;
+//   scan  : list-major — every (list, block of the queries that probe it, block of its rows)
+//           is one MFMA tile of the distance kernel, so a list's rows are read once per block
+//           of up to 128 probing queries instead of once per query (ivf_list_search,
+//           Metal/Shaders/IVFListSearch.metal:199-339, streams each query's lists separately);
+//   top-k : a strided in-list sample (every 64th row of each probed list) gives each query an
+//           upper bound tau_q of its k-th distance; the full scan appends only keys <= tau_q;
+//           exact (L2^2, row id) selection follows.  Queries whose candidate list overflows
+//           are rescanned with room for every candidate they have.
+// The reference's per-thread heap (K_PRIVATE = 8) is only exact for k <= 8; this is exact
+// for every k <= VA_MAX_K.
+#include <algorithm>
+#include <vector>
+
+#include "va_internal.hpp"
+
+struct va_ivf {
+    int device = 0;
+    uint32_t C = 0, D = 0, N = 0;
+    float* centroids = nullptr;     // [C x D]
+    float* list_vectors = nullptr;  // [N x D] in CSR order
+    uint32_t* ids = nullptr;        // [N] original row id of every CSR position
+    uint32_t* offsets = nullptr;    // [C + 1]
+    std::vector<uint32_t> h_offsets;
+    uint32_t* probe_buf = nullptr;  // probes of va_ivf_search
+    size_t probe_cap = 0;
+};
+
+namespace va {
+namespace {
+
+constexpr uint32_t kSampleStride = 64;
+
+__global__ __launch_bounds__(256) void gather_rows(const float* __restrict__ x, const uint32_t* __restrict__ ids,
+                                                   uint32_t N, uint32_t D, float* __restrict__ out) {
+    for (uint32_t p = blockIdx.x; p < N; p += gridDim.x) {
+        const float* src = x + uint64_t(ids[p]) * D;
+        float* dst = out + uint64_t(p) * D;
+        if ((D & 3) == 0) {
+            for (uint32_t d = threadIdx.x * 4; d < D; d += 1024)
+                *reinterpret_cast<float4*>(dst + d) = *reinterpret_cast<const float4*>(src + d);
+        } else {
+            for (uint32_t d = threadIdx.x; d < D; d += 256) dst[d] = src[d];
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void gather_queries(const float* __restrict__ q, const uint32_t* __restrict__ rows,
+                                                      uint32_t R, uint32_t D, float* __restrict__ out) {
+    for (uint32_t r = blockIdx.x; r < R; r += gridDim.x) {
+        const float* src = q + uint64_t(rows[r]) * D;
+        for (uint32_t d = threadIdx.x; d < D; d += 256) out[uint64_t(r) * D + d] = src[d];
+    }
+}
+
+struct F32Keys final : KeyProducer {
+    va_context* ctx;
+    const float* q;
+    const float* x;
+    uint32_t Q, N, D;
+    va_status dense(const uint32_t* qrow, uint32_t q0, uint32_t nq, uint32_t c0, uint32_t cols, uint32_t stride,
+                    uint32_t* out_k, int64_t ldo) override {
+        DistArgs a;
+        a.q = qrow ? q : q + int64_t(q0) * D;
+        a.qrow = qrow;
+        a.ldq = D;
+        a.x = x + int64_t(c0) * D;
+        a.ldx = int64_t(stride) * D;
+        a.Q = nq;
+        a.N = cols;
+        a.D = D;
+        a.op = OP_L2SQ;
+        a.out = OUT_KEYS;
+        a.out_k = out_k;
+        a.ldo = ldo;
+        return launch_dist(ctx, a);
+    }
+    va_status filter(const uint32_t* thr, uint32_t* cnt, uint32_t* ckey, uint32_t* cid, uint32_t cap) override {
+        DistArgs a;
+        a.q = q;
+        a.ldq = D;
+        a.x = x;
+        a.ldx = D;
+        a.Q = Q;
+        a.N = N;
+        a.D = D;
+        a.op = OP_L2SQ;
+        a.out = OUT_FILTER;
+        a.thr = thr;
+        a.cnt = cnt;
+        a.cand_key = ckey;
+        a.cand_id = cid;
+        a.cap = cap;
+        return launch_dist(ctx, a);
+    }
+};
+
+// Tile descriptors {qs, qc, rs, rc} of one list-major pass, grouped by tile shape.
+struct TilePlan {
+    std::vector<uint32_t> t[3];  // wq = 1, 2, 4
+    static int slot(int wq) { return wq == 1 ? 0 : (wq == 2 ? 1 : 2); }
+    static int wq_for(uint32_t nq) { return nq > 64 ? 4 : (nq > 32 ? 2 : 1); }
+    // rows of list l: positions off + j*stride, j < nrows
+    void add(uint32_t lq_start, uint32_t nq, uint32_t off, uint32_t nrows) {
+        if (nq == 0 || nrows == 0) return;
+        const int wq = wq_for(nq);
+        const uint32_t TQ = dist_tile_queries(wq), TN = dist_tile_rows(wq);
+        auto& v = t[slot(wq)];
+        for (uint32_t qb = 0; qb < nq; qb += TQ)
+            for (uint32_t r = 0; r < nrows; r += TN) {
+                v.push_back(lq_start + qb);
+                v.push_back(std::min(TQ, nq - qb));
+                v.push_back(off + r);  // position index (scaled by the pass stride in the kernel)
+                v.push_back(std::min(TN, nrows - r));
+            }
+    }
+    size_t words() const { return t[0].size() + t[1].size() + t[2].size(); }
+};
+
+// Runs one list-major filter pass; tiles hold "rs" as an index into the strided row space
+// (the kernel multiplies j by rstride; rs must already be the first position).
+va_status run_pass(va_context* ctx, const TilePlan& plan, uint32_t* dev_tiles, const float* q, const uint32_t* lq,
+                   const va_ivf* ivf, uint32_t rstride, const uint32_t* thr, uint32_t* cnt, uint32_t* ckey,
+                   uint32_t* cid, uint32_t cap) {
+    size_t off = 0;
+    for (int wq : {1, 2, 4}) {
+        const auto& v = plan.t[TilePlan::slot(wq)];
+        if (v.empty()) continue;
+        VA_CHECK_HIP(ctx, hipMemcpyAsync(dev_tiles + off, v.data(), v.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+        DistArgs a;
+        a.q = q;
+        a.qrow = lq;
+        a.ldq = ivf->D;
+        a.x = ivf->list_vectors;
+        a.ldx = ivf->D;
+        a.D = ivf->D;
+        a.op = OP_L2SQ;
+        a.out = OUT_FILTER;
+        a.thr = thr;
+        a.cnt = cnt;
+        a.cand_key = ckey;
+        a.cand_id = cid;
+        a.cap = cap;
+        a.tiles = dev_tiles + off;
+        a.ntiles = uint32_t(v.size() / 4);
+        a.rstride = rstride;
+        a.ids = ivf->ids;
+        a.wq = wq;
+        VA_CHECK_STATUS(launch_dist(ctx, a));
+        off += v.size();
+    }
+    return VA_OK;
+}
+
+}  // namespace
+}  // namespace va
+
+extern "C" {
+
+va_status va_ivf_build(va_context* ctx, const float* centroids, uint32_t num_centroids, const float* x,
+                       uint32_t num_vectors, uint32_t dim, va_ivf** out) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    VA_REQUIRE(ctx, centroids && x && out, "va_ivf_build: NULL pointer");
+    // IVFSearchConfiguration.validate (Index/Kernels/IVF/IVFKernels.swift:68-82)
+    VA_REQUIRE(ctx, num_centroids >= 1, "numCentroids must be at least 1, got %u", num_centroids);
+    VA_REQUIRE(ctx, dim >= 1 && dim <= 4096, "dimension must be 1-4096, got %u", dim);
+    VA_REQUIRE(ctx, num_vectors >= 1, "va_ivf_build: no vectors");
+    va::DeviceGuard g(ctx->device);
+    *out = nullptr;
+    va_ivf* ivf = new va_ivf();
+    ivf->device = ctx->device;
+    ivf->C = num_centroids;
+    ivf->D = dim;
+    ivf->N = num_vectors;
+    auto cleanup = [&](va_status st) {
+        va_ivf_destroy(ivf);
+        return st;
+    };
+    const uint64_t cbytes = uint64_t(num_centroids) * dim * 4, xbytes = uint64_t(num_vectors) * dim * 4;
+    if (hipMalloc(&ivf->centroids, cbytes) != hipSuccess || hipMalloc(&ivf->list_vectors, xbytes) != hipSuccess ||
+        hipMalloc(&ivf->ids, uint64_t(num_vectors) * 4) != hipSuccess ||
+        hipMalloc(&ivf->offsets, uint64_t(num_centroids + 1) * 4) != hipSuccess) {
+        (void)hipGetLastError();
+        return cleanup(va::fail(ctx, VA_ERR_OOM, "va_ivf_build: device allocation failed"));
+    }
+    if (hipMemcpyAsync(ivf->centroids, centroids, cbytes, hipMemcpyDeviceToDevice, ctx->stream) != hipSuccess)
+        return cleanup(va::fail(ctx, VA_ERR_HIP, "va_ivf_build: centroid copy failed"));
+
+    // nearest-centroid assignment, in row batches (k = 1 exact scan; ties -> lower id)
+    uint32_t* assign = nullptr;
+    if (hipMalloc(&assign, uint64_t(num_vectors) * 4) != hipSuccess) {
+        (void)hipGetLastError();
+        return cleanup(va::fail(ctx, VA_ERR_OOM, "va_ivf_build: assignment buffer"));
+    }
+    const uint32_t batch = 1u << 18;
+    for (uint32_t r0 = 0; r0 < num_vectors; r0 += batch) {
+        const uint32_t nr = std::min(batch, num_vectors - r0);
+        va::F32Keys kp;
+        kp.ctx = ctx;
+        kp.q = x + uint64_t(r0) * dim;
+        kp.x = ivf->centroids;
+        kp.Q = nr;
+        kp.N = num_centroids;
+        kp.D = dim;
+        va::ScanOutputs o;
+        o.idx = assign + r0;
+        va_status st = va::exact_topk_scan(ctx, kp, nr, num_centroids, 1, o);
+        if (st != VA_OK) {
+            (void)hipFree(assign);
+            return cleanup(st);
+        }
+    }
+    std::vector<uint32_t> h_assign(num_vectors);
+    if (hipMemcpyAsync(h_assign.data(), assign, uint64_t(num_vectors) * 4, hipMemcpyDeviceToHost, ctx->stream) !=
+            hipSuccess ||
+        hipStreamSynchronize(ctx->stream) != hipSuccess) {
+        (void)hipFree(assign);
+        return cleanup(va::fail(ctx, VA_ERR_HIP, "va_ivf_build: assignment read-back failed"));
+    }
+    (void)hipFree(assign);
+    // CSR in centroid order, insertion order inside each list (IVFStructure.swift:370-381)
+    ivf->h_offsets.assign(num_centroids + 1, 0);
+    for (uint32_t i = 0; i < num_vectors; ++i) ivf->h_offsets[h_assign[i] + 1]++;
+    for (uint32_t c = 0; c < num_centroids; ++c) ivf->h_offsets[c + 1] += ivf->h_offsets[c];
+    std::vector<uint32_t> fill(ivf->h_offsets.begin(), ivf->h_offsets.end() - 1), h_ids(num_vectors);
+    for (uint32_t i = 0; i < num_vectors; ++i) h_ids[fill[h_assign[i]]++] = i;
+    if (hipMemcpyAsync(ivf->ids, h_ids.data(), uint64_t(num_vectors) * 4, hipMemcpyHostToDevice, ctx->stream) !=
+            hipSuccess ||
+        hipMemcpyAsync(ivf->offsets, ivf->h_offsets.data(), uint64_t(num_centroids + 1) * 4, hipMemcpyHostToDevice,
+                       ctx->stream) != hipSuccess)
+        return cleanup(va::fail(ctx, VA_ERR_HIP, "va_ivf_build: CSR upload failed"));
+    va::gather_rows<<<dim3(std::min<uint32_t>(num_vectors, 65536)), dim3(256), 0, ctx->stream>>>(
+        x, ivf->ids, num_vectors, dim, ivf->list_vectors);
+    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(ctx->stream) != hipSuccess)
+        return cleanup(va::fail(ctx, VA_ERR_HIP, "va_ivf_build: gather failed"));
+    *out = ivf;
+    return VA_OK;
+}
+
+va_status va_ivf_destroy(va_ivf* ivf) {
+    if (!ivf) return VA_ERR_INVALID_ARG;
+    va::DeviceGuard g(ivf->device);
+    (void)hipDeviceSynchronize();
+    if (ivf->centroids) (void)hipFree(ivf->centroids);
+    if (ivf->list_vectors) (void)hipFree(ivf->list_vectors);
+    if (ivf->ids) (void)hipFree(ivf->ids);
+    if (ivf->offsets) (void)hipFree(ivf->offsets);
+    if (ivf->probe_buf) (void)hipFree(ivf->probe_buf);
+    delete ivf;
+    return VA_OK;
+}
+
+va_status va_ivf_get_lists(va_context* ctx, const va_ivf* ivf, uint32_t* host_offsets, uint32_t* host_ids) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    VA_REQUIRE(ctx, ivf && host_offsets && host_ids, "va_ivf_get_lists: NULL pointer");
+    va::DeviceGuard g(ctx->device);
+    std::copy(ivf->h_offsets.begin(), ivf->h_offsets.end(), host_offsets);
+    VA_CHECK_HIP(ctx, hipMemcpyAsync(host_ids, ivf->ids, uint64_t(ivf->N) * 4, hipMemcpyDeviceToHost, ctx->stream));
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return VA_OK;
+}
+
+va_status va_ivf_probe(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
+                       uint32_t nprobe, uint32_t* probes) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    VA_REQUIRE(ctx, ivf && queries && probes, "va_ivf_probe: NULL pointer");
+    VA_REQUIRE(ctx, num_queries > 0, "Queries cannot be empty");
+    VA_REQUIRE(ctx, nprobe >= 1 && nprobe <= VA_MAX_K, "nprobe must be in [1, %u], got %u", VA_MAX_K, nprobe);
+    va::DeviceGuard g(ctx->device);
+    va::F32Keys kp;
+    kp.ctx = ctx;
+    kp.q = queries;
+    kp.x = ivf->centroids;
+    kp.Q = num_queries;
+    kp.N = ivf->C;
+    kp.D = ivf->D;
+    va::ScanOutputs o;
+    o.idx = probes;
+    return va::exact_topk_scan(ctx, kp, num_queries, ivf->C, nprobe, o);
+}
+
+va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
+                      const uint32_t* probes, uint32_t nprobe, uint32_t k, uint32_t* out_idx, float* out_dist) {
+    using va::Scratch;
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    VA_REQUIRE(ctx, ivf && queries && probes && out_idx, "va_ivf_scan: NULL pointer");
+    VA_REQUIRE(ctx, num_queries > 0, "Queries cannot be empty");
+    VA_REQUIRE(ctx, k > 0 && k <= VA_MAX_K, "k must be in [1, %u], got %u", VA_MAX_K, k);
+    VA_REQUIRE(ctx, nprobe >= 1, "nprobe must be at least 1, got %u", nprobe);
+    va::DeviceGuard g(ctx->device);
+    const uint32_t Q = num_queries, C = ivf->C;
+    const auto& off = ivf->h_offsets;
+
+    // ---- host plan: the queries probing every list, per-query candidate totals ------------------
+    std::vector<uint32_t> P(uint64_t(Q) * nprobe);
+    VA_CHECK_HIP(ctx, hipMemcpyAsync(P.data(), probes, P.size() * 4, hipMemcpyDeviceToHost, ctx->stream));
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    std::vector<uint32_t> lq_off(C + 1, 0), seen(C, 0xFFFFFFFFu);
+    std::vector<uint64_t> total(Q, 0), sampled(Q, 0);
+    for (uint32_t q = 0; q < Q; ++q)
+        for (uint32_t p = 0; p < nprobe; ++p) {
+            uint32_t& l = P[uint64_t(q) * nprobe + p];
+            // sentinel / out-of-range probes are skipped (IVFListSearch.metal:249-251); a list
+            // probed twice by one query is scanned once
+            if (l >= C || seen[l] == q) {
+                l = 0xFFFFFFFFu;
+                continue;
+            }
+            seen[l] = q;
+            lq_off[l + 1]++;
+            const uint32_t n = off[l + 1] - off[l];
+            total[q] += n;
+            sampled[q] += (n + va::kSampleStride - 1) / va::kSampleStride;
+        }
+    for (uint32_t l = 0; l < C; ++l) lq_off[l + 1] += lq_off[l];
+    std::vector<uint32_t> lq(lq_off[C]), fillp(lq_off.begin(), lq_off.end() - 1);
+    for (uint32_t q = 0; q < Q; ++q)
+        for (uint32_t p = 0; p < nprobe; ++p) {
+            const uint32_t l = P[uint64_t(q) * nprobe + p];
+            if (l < C) lq[fillp[l]++] = q;
+        }
+    va::TilePlan sample_plan, main_plan;
+    for (uint32_t l = 0; l < C; ++l) {
+        const uint32_t nq = lq_off[l + 1] - lq_off[l];
+        const uint32_t n = off[l + 1] - off[l];
+        main_plan.add(lq_off[l], nq, off[l], n);
+    }
+    // sampled rows: positions off[l] + j*stride; tile rs values are first positions
+    for (uint32_t l = 0; l < C; ++l) {
+        const uint32_t nq = lq_off[l + 1] - lq_off[l];
+        const uint32_t n = off[l + 1] - off[l];
+        const uint32_t ns = (n + va::kSampleStride - 1) / va::kSampleStride;
+        if (nq == 0 || ns == 0) continue;
+        const int wq = va::TilePlan::wq_for(nq);
+        const uint32_t TQ = va::dist_tile_queries(wq), TN = va::dist_tile_rows(wq);
+        auto& v = sample_plan.t[va::TilePlan::slot(wq)];
+        for (uint32_t qb = 0; qb < nq; qb += TQ)
+            for (uint32_t r = 0; r < ns; r += TN) {
+                v.push_back(lq_off[l] + qb);
+                v.push_back(std::min(TQ, nq - qb));
+                v.push_back(off[l] + r * va::kSampleStride);
+                v.push_back(std::min(TN, ns - r));
+            }
+    }
+    const uint64_t cap_s = std::max<uint64_t>(1, *std::max_element(sampled.begin(), sampled.end()));
+    const uint64_t max_total = std::max<uint64_t>(1, *std::max_element(total.begin(), total.end()));
+    uint64_t cap = ctx->opt_candidate_cap ? ctx->opt_candidate_cap
+                                          : std::max<uint64_t>(3ull * k, uint64_t(k) + 32) * va::kSampleStride + 1024;
+    cap = std::min(cap, max_total);
+    const uint64_t cand = std::max(cap_s, cap);
+
+    Scratch s(ctx);
+    const size_t tile_words = std::max(sample_plan.words(), main_plan.words());
+    const size_t need = Scratch::round(uint64_t(Q) * 4) * 3 + Scratch::round(256) + Scratch::round(lq.size() * 4 + 4) +
+                        Scratch::round(tile_words * 4 + 4) + Scratch::round(uint64_t(Q) * cand * 4) * 2;
+    VA_CHECK_STATUS(s.reserve(need));
+    uint32_t* thr = s.carve<uint32_t>(Q);
+    uint32_t* cnt = s.carve<uint32_t>(Q);
+    uint32_t* ovf_rows = s.carve<uint32_t>(Q);
+    uint32_t* ovf_cnt = s.carve<uint32_t>(64);
+    uint32_t* d_lq = s.carve<uint32_t>(lq.size() + 1);
+    uint32_t* d_tiles = s.carve<uint32_t>(tile_words + 1);
+    uint32_t* ckey = s.carve<uint32_t>(uint64_t(Q) * cand);
+    uint32_t* cid = s.carve<uint32_t>(uint64_t(Q) * cand);
+    if (!lq.empty())
+        VA_CHECK_HIP(ctx, hipMemcpyAsync(d_lq, lq.data(), lq.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+
+    // ---- 1. sample pass: every sampled candidate, then tau = k-th smallest ----------------------
+    VA_CHECK_STATUS(va::fill_u32(ctx, thr, Q, 0xFFFFFFFFu));
+    VA_CHECK_STATUS(va::fill_u32(ctx, cnt, Q, 0));
+    VA_CHECK_STATUS(va::run_pass(ctx, sample_plan, d_tiles, queries, d_lq, ivf, va::kSampleStride, thr, cnt, ckey, cid,
+                                 uint32_t(cap_s)));
+    {
+        va::SelectArgs a;
+        a.keys = ckey;
+        a.ids = cid;
+        a.counts = cnt;
+        a.ld = int64_t(cap_s);
+        a.n = uint32_t(cap_s);
+        a.rows = Q;
+        a.k = k;
+        a.out_kth = thr;
+        VA_CHECK_STATUS(va::launch_select(ctx, a));
+    }
+    // ---- 2. full pass with the thresholds, 3. exact selection -----------------------------------
+    VA_CHECK_STATUS(va::fill_u32(ctx, cnt, Q, 0));
+    VA_CHECK_STATUS(va::fill_u32(ctx, ovf_cnt, 1, 0));
+    VA_CHECK_STATUS(va::run_pass(ctx, main_plan, d_tiles, queries, d_lq, ivf, 1, thr, cnt, ckey, cid, uint32_t(cap)));
+    {
+        va::SelectArgs a;
+        a.keys = ckey;
+        a.ids = cid;
+        a.counts = cnt;
+        a.ld = int64_t(cap);
+        a.n = uint32_t(cap);
+        a.rows = Q;
+        a.k = k;
+        a.out_idx = out_idx;
+        a.out_f = out_dist;
+        a.overflow_count = ovf_cnt;
+        a.overflow_rows = ovf_rows;
+        VA_CHECK_STATUS(va::launch_select(ctx, a));
+    }
+    VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->host_word, ovf_cnt, 4, hipMemcpyDeviceToHost, ctx->stream));
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    const uint32_t n_ovf = ctx->host_word[0];
+    if (n_ovf == 0) return VA_OK;
+
+    // ---- 4. overflowed queries: rescan with room for all of their candidates ---------------------
+    std::vector<uint32_t> rows(n_ovf), h_thr(Q);
+    VA_CHECK_HIP(ctx, hipMemcpyAsync(rows.data(), ovf_rows, uint64_t(n_ovf) * 4, hipMemcpyDeviceToHost, ctx->stream));
+    VA_CHECK_HIP(ctx, hipMemcpyAsync(h_thr.data(), thr, uint64_t(Q) * 4, hipMemcpyDeviceToHost, ctx->stream));
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    std::sort(rows.begin(), rows.end());
+    std::vector<uint32_t> compact(Q, 0xFFFFFFFFu), c_thr(n_ovf);
+    uint64_t cap2 = 1;
+    for (uint32_t i = 0; i < n_ovf; ++i) {
+        compact[rows[i]] = i;
+        c_thr[i] = h_thr[rows[i]];
+        cap2 = std::max<uint64_t>(cap2, total[rows[i]]);
+    }
+    std::vector<uint32_t> lq2_off(C + 1, 0), lq2;
+    for (uint32_t l = 0; l < C; ++l) {
+        for (uint32_t e = lq_off[l]; e < lq_off[l + 1]; ++e)
+            if (compact[lq[e]] != 0xFFFFFFFFu) lq2.push_back(compact[lq[e]]);
+        lq2_off[l + 1] = uint32_t(lq2.size());
+    }
+    va::TilePlan plan2;
+    for (uint32_t l = 0; l < C; ++l) plan2.add(lq2_off[l], lq2_off[l + 1] - lq2_off[l], off[l], off[l + 1] - off[l]);
+    Scratch f(ctx);
+    const size_t need2 = Scratch::round(uint64_t(n_ovf) * ivf->D * 4) + Scratch::round(uint64_t(n_ovf) * 4) * 3 +
+                         Scratch::round(lq2.size() * 4 + 4) + Scratch::round(plan2.words() * 4 + 4) +
+                         Scratch::round(uint64_t(n_ovf) * cap2 * 4) * 2;
+    VA_CHECK_STATUS(f.reserve(need2));
+    float* cq = f.carve<float>(uint64_t(n_ovf) * ivf->D);
+    uint32_t* d_rows = f.carve<uint32_t>(n_ovf);
+    uint32_t* d_thr = f.carve<uint32_t>(n_ovf);
+    uint32_t* d_cnt = f.carve<uint32_t>(n_ovf);
+    uint32_t* d_lq2 = f.carve<uint32_t>(lq2.size() + 1);
+    uint32_t* d_t2 = f.carve<uint32_t>(plan2.words() + 1);
+    uint32_t* k2 = f.carve<uint32_t>(uint64_t(n_ovf) * cap2);
+    uint32_t* i2 = f.carve<uint32_t>(uint64_t(n_ovf) * cap2);
+    VA_CHECK_HIP(ctx, hipMemcpyAsync(d_rows, rows.data(), uint64_t(n_ovf) * 4, hipMemcpyHostToDevice, ctx->stream));
+    VA_CHECK_HIP(ctx, hipMemcpyAsync(d_thr, c_thr.data(), uint64_t(n_ovf) * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (!lq2.empty())
+        VA_CHECK_HIP(ctx, hipMemcpyAsync(d_lq2, lq2.data(), lq2.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+    va::gather_queries<<<dim3(std::min<uint32_t>(n_ovf, 4096)), dim3(256), 0, ctx->stream>>>(queries, d_rows, n_ovf,
+                                                                                            ivf->D, cq);
+    VA_CHECK_LAUNCH(ctx);
+    VA_CHECK_STATUS(va::fill_u32(ctx, d_cnt, n_ovf, 0));
+    VA_CHECK_STATUS(va::run_pass(ctx, plan2, d_t2, cq, d_lq2, ivf, 1, d_thr, d_cnt, k2, i2, uint32_t(cap2)));
+    va::SelectArgs a;
+    a.keys = k2;
+    a.ids = i2;
+    a.counts = d_cnt;
+    a.ld = int64_t(cap2);
+    a.n = uint32_t(cap2);
+    a.rows = n_ovf;
+    a.k = k;
+    a.row_map = d_rows;
+    a.out_idx = out_idx;
+    a.out_f = out_dist;
+    VA_CHECK_STATUS(va::launch_select(ctx, a));
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));  // host vectors above must outlive the copies
+    return VA_OK;
+}
+
+va_status va_ivf_search(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
+                        uint32_t nprobe, uint32_t k, uint32_t* out_idx, float* out_dist) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    VA_REQUIRE(ctx, ivf && queries && out_idx, "va_ivf_search: NULL pointer");
+    VA_REQUIRE(ctx, num_queries > 0, "Queries cannot be empty");
+    VA_REQUIRE(ctx, k > 0 && k <= VA_MAX_K, "k must be in [1, %u], got %u", VA_MAX_K, k);
+    // IVFSearchConfiguration clamps nprobe to numCentroids (IVFKernels.swift:62)
+    VA_REQUIRE(ctx, nprobe >= 1, "nprobe must be at least 1, got %u", nprobe);
+    nprobe = std::min(nprobe, ivf->C);
+    va::DeviceGuard g(ctx->device);
+    va_ivf* m = const_cast<va_ivf*>(ivf);
+    const size_t need = uint64_t(num_queries) * nprobe * 4;
+    if (m->probe_cap < need) {
+        VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (m->probe_buf) (void)hipFree(m->probe_buf);
+        m->probe_buf = nullptr;
+        m->probe_cap = 0;
+        VA_CHECK_HIP(ctx, hipMalloc(&m->probe_buf, need));
+        m->probe_cap = need;
+    }
+    VA_CHECK_STATUS(va_ivf_probe(ctx, ivf, queries, num_queries, nprobe, m->probe_buf));
+    return va_ivf_scan(ctx, ivf, queries, num_queries, m->probe_buf, nprobe, k, out_idx, out_dist);
+}
+
+}  // extern "C"

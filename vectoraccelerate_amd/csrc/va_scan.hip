@@ -21,6 +21,45 @@ namespace va {
 namespace {
 constexpr uint64_t kDenseBudgetBytes = 256ull << 20;  // dense key matrix per launch
 constexpr uint32_t kMinSample = 16384;
+
+// hipEvent marks of the scan phases (no-ops unless profiling is on)
+struct PhaseMarks {
+    va_context* ctx;
+    explicit PhaseMarks(va_context* c) : ctx(c) {}
+    va_status mark(int i) {
+        if (!ctx->profiling) return VA_OK;
+        VA_CHECK_HIP(ctx, hipEventRecord(ctx->ev[i], ctx->stream));
+        return VA_OK;
+    }
+    float ms(int a, int b) {
+        float t = 0.0f;
+        if (hipEventElapsedTime(&t, ctx->ev[a], ctx->ev[b]) != hipSuccess) {
+            (void)hipGetLastError();
+            return -1.0f;
+        }
+        return t;
+    }
+    // events: 0 start, 1 after sample, 2 after scan, 3 after select, 4 end
+    va_status finish(bool sampled, bool fallback) {
+        if (!ctx->profiling) return VA_OK;
+        VA_CHECK_STATUS(mark(4));
+        VA_CHECK_HIP(ctx, hipEventSynchronize(ctx->ev[4]));
+        va_scan_timings& t = ctx->last_scan;
+        t.total_ms = ms(0, 4);
+        if (sampled) {
+            t.sample_ms = ms(0, 1);
+            t.scan_ms = ms(1, 2);
+            t.select_ms = ms(2, 3);
+            t.fallback_ms = fallback ? ms(3, 4) : 0.0f;
+        } else {
+            t.sample_ms = 0.0f;
+            t.scan_ms = t.total_ms;
+            t.select_ms = 0.0f;
+            t.fallback_ms = 0.0f;
+        }
+        return VA_OK;
+    }
+};
 }  // namespace
 
 va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t N, uint32_t k,
@@ -36,7 +75,11 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
     // ---- plan ------------------------------------------------------------------------
     uint64_t S = ctx->opt_sample_rows ? ctx->opt_sample_rows : std::max<uint64_t>(kMinSample, N / 64);
     const bool direct = S >= N;
+    PhaseMarks pm(ctx);
+    ctx->last_scan = va_scan_timings{};
+    VA_CHECK_STATUS(pm.mark(0));
     if (direct) {
+        ctx->last_scan.scan_launches = 0;
         // small database: dense keys in query chunks + select
         const uint64_t per_q = uint64_t(N) * 4;
         uint32_t qc = uint32_t(std::max<uint64_t>(1, std::min<uint64_t>(Q, kDenseBudgetBytes / per_q)));
@@ -46,6 +89,7 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
         for (uint32_t q0 = 0; q0 < Q; q0 += qc) {
             const uint32_t nq = std::min(qc, Q - q0);
             VA_CHECK_STATUS(kp.dense(nullptr, q0, nq, 0, N, 1, keys, N));
+            ctx->last_scan.scan_launches++;
             SelectArgs a = base;
             a.keys = keys;
             a.ld = N;
@@ -57,7 +101,7 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
             if (out.key) a.out_key = out.key + int64_t(q0) * k;
             VA_CHECK_STATUS(launch_select(ctx, a));
         }
-        return VA_OK;
+        return pm.finish(false, false);
     }
     const uint32_t stride = uint32_t(N / S);
     const uint64_t ratio = (uint64_t(N) + S - 1) / S;
@@ -96,7 +140,12 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
     // ---- 2. filter --------------------------------------------------------------------
     VA_CHECK_STATUS(fill_u32(ctx, cnt, Q, 0));
     VA_CHECK_STATUS(fill_u32(ctx, ovf_cnt, 1, 0));
+    VA_CHECK_STATUS(pm.mark(1));
     VA_CHECK_STATUS(kp.filter(thr, cnt, ckey, cid, uint32_t(cap)));
+    VA_CHECK_STATUS(pm.mark(2));
+    ctx->last_scan.scan_launches = 1;
+    ctx->last_scan.sample_rows = uint32_t(S);
+    ctx->last_scan.candidate_cap = uint32_t(cap);
     // ---- 3. select ----------------------------------------------------------------------
     {
         SelectArgs a = base;
@@ -110,10 +159,12 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
         a.overflow_rows = ovf_rows;
         VA_CHECK_STATUS(launch_select(ctx, a));
     }
+    VA_CHECK_STATUS(pm.mark(3));
     VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->host_word, ovf_cnt, 4, hipMemcpyDeviceToHost, ctx->stream));
     VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
     const uint32_t n_ovf = ctx->host_word[0];
-    if (n_ovf == 0) return VA_OK;
+    ctx->last_scan.overflow_rows = n_ovf;
+    if (n_ovf == 0) return pm.finish(true, false);
 
     // ---- 4. exact chunked recomputation of overflowed rows ---------------------------------
     // rows are processed in batches of R; each batch scans the database in chunks of C rows
@@ -165,7 +216,7 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
         a.row_map = rows;
         VA_CHECK_STATUS(launch_select(ctx, a));
     }
-    return VA_OK;
+    return pm.finish(true, true);
 }
 
 }  // namespace va
