@@ -1,19 +1,21 @@
-"""Benchmark of the flat search hot path on one MI355X.
+"""Benchmark of the flat/IVF search hot path on one MI355X.
 
-Headline workload = BASELINE.json configs[1]: flat cosine top-100 over N=1,000,000 x d=1536
-fp32 (rows N(0,1) then L2-normalised), Q=1024 queries = database rows + N(0, 0.05) noise,
-renormalised.  A "step" is one va_fused_topk call over the resident database (sample ->
-filtering MFMA scan -> candidate selection); inputs are in HBM before the timed region.
+Headline (the JSON line's ``value``) = BASELINE.json configs[1]: flat cosine top-100 over
+N=1,000,000 x d=1536 fp32 (rows N(0,1) then L2-normalised), Q=1024 queries = database rows +
+N(0, 0.05) noise, renormalised.  A "step" is one va_fused_topk call over the resident
+database (threshold sample -> filtering MFMA scan -> candidate selection); inputs are in HBM
+before the timed region.  The other configs are measured the same way at full size and
+reported under ``extra`` (configs[2] int8 top-10, configs[3] binary top-100, configs[4]
+IVF-Flat top-10; configs[0] is the CPU-runnable parity case covered by the tests).
 
-Prints ONE JSON line (rank 0).  Extras: L2^2 top-10 at the same shape (the north-star's
-stated target), scan-phase timings, and the CPU baseline (the C oracle's float port of the
-reference CPU path, timed on a bounded query sample on this host).
+CPU baseline: the C oracle's float-accumulation port of the reference CPU path
+(CPUTopK / AccelerateFallback), timed on this host's cores on a bounded query sample.
+Prints ONE JSON line on stdout; progress goes to stderr.
 """
 from __future__ import annotations
 
 import argparse
 import json
-import os
 import sys
 import time
 from pathlib import Path
@@ -22,8 +24,12 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 METRIC = json.loads((ROOT / "BASELINE.json").read_text())["metric"]
-PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 MFMA
-PEAK_HBM_GBS = 8000.0
+PEAK = {
+    "fp32_mfma_tflops": 157.3,
+    "int8_mfma_tops": 5000.0,
+    "valu_int32_tops": 39.3,  # 256 CU x 64 lanes x 2.4 GHz, non-packed 32-bit integer ops
+    "hbm_gbs": 8000.0,
+}
 
 
 def parse():
@@ -31,13 +37,10 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=2)
-    p.add_argument("--N", type=int, default=1_000_000)
-    p.add_argument("--D", type=int, default=1536)
-    p.add_argument("--Q", type=int, default=1024)
-    p.add_argument("--k", type=int, default=100)
-    p.add_argument("--cpu-queries", type=int, default=32, help="query sample of the CPU baseline")
-    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
-    p.add_argument("--no-extra", action="store_true", help="skip the L2 top-10 extra measurement")
+    p.add_argument("--workload", default="all", choices=["all", "c2", "c3", "c4", "c5"],
+                   help="all = configs[1] headline + configs[2..4] extras")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines (profiling runs)")
+    p.add_argument("--no-extra", action="store_true", help="headline only (no L2 top-10 extra)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="first run a plain 1 GiB device copy (reference point for rocprofv3 FETCH/WRITE_SIZE)")
     return p.parse_args()
@@ -47,10 +50,47 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def make_c2(N: int, D: int, Q: int):
-    """configs[1] data on the device (torch is data plumbing only)."""
+def timed(ctx, fn, steps: int, warmup: int, scan_timings: bool = True):
+    """Run `warmup` untimed steps, then time exactly `steps` steps between synchronisations."""
     import torch
 
+    for _ in range(warmup):
+        fn()
+    ctx.synchronize()
+    torch.cuda.synchronize()
+    phases = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+        if scan_timings:
+            phases.append(ctx.last_scan_timings())
+    ctx.synchronize()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps, phases
+
+
+def mean_phases(phases):
+    import numpy as np
+
+    if not phases:
+        return {}
+    keys = ("sample_ms", "scan_ms", "select_ms", "fallback_ms", "total_ms")
+    out = {k: float(np.mean([p[k] for p in phases])) for k in keys}
+    out.update({k: phases[-1][k] for k in ("sample_rows", "candidate_cap", "overflow_rows")})
+    return out
+
+
+# ---------------------------------------------------------------------------------------
+# configs[1]: flat cosine top-100, 1M x 1536 fp32, Q = 1024 (headline)
+# ---------------------------------------------------------------------------------------
+def run_c2(ctx, a, cpu: bool, extra_l2: bool):
+    import numpy as np
+    import torch
+
+    from vectoraccelerate_amd import FusedL2TopKKernel, FusedL2TopKParameters, Metric
+
+    N, D, Q, k = 1_000_000, 1536, 1024, 100
+    log(f"configs[1]: generating N={N} D={D} Q={Q}")
     g = torch.Generator(device="cuda").manual_seed(0)
     x = torch.randn(N, D, device="cuda", generator=g, dtype=torch.float32)
     x /= x.norm(dim=1, keepdim=True)
@@ -58,26 +98,259 @@ def make_c2(N: int, D: int, Q: int):
     src = torch.randint(0, N, (Q,), device="cuda", generator=gq)
     q = x[src] + 0.05 * torch.randn(Q, D, device="cuda", generator=gq, dtype=torch.float32)
     q /= q.norm(dim=1, keepdim=True)
+    q = q.contiguous()
     torch.cuda.synchronize()
-    return x.contiguous(), q.contiguous(), src
+    kern = FusedL2TopKKernel(ctx)
+    idx = ctx.empty((Q, k), torch.int32)
+    dist = ctx.empty((Q, k), torch.float32)
+    params = FusedL2TopKParameters(Q, N, D, k)
+    ms, phases = timed(ctx, lambda: kern.encode(q, x, idx, dist, params, Metric.cosine), a.steps, a.warmup)
+    ph = mean_phases(phases)
+    flops = 2.0 * Q * N * D
+    tflops = flops / (ph["scan_ms"] * 1e-3) / 1e12
+    res = {
+        "ms_per_step": ms,
+        "qps": Q / (ms * 1e-3),
+        "phases_ms": ph,
+        "scan_tflops": tflops,
+        "rank1_is_source_row": float((idx[:, 0].long() == src).float().mean().item()),
+        "roofline": {
+            "bound": "mfma", "achieved": tflops, "peak": PEAK["fp32_mfma_tflops"], "unit": "TFLOP/s",
+            "frac": tflops / PEAK["fp32_mfma_tflops"], "traffic": None,
+            "kernel": "dist_gemm_kernel<4, true, 2> (filtering scan)",
+            "algorithmic": f"2*Q*N*D = {flops:.4g} FLOP per launch",
+        },
+    }
+    log(f"configs[1] cosine top-100: {ms:.3f} ms/step = {res['qps']:.0f} QPS; scan {ph['scan_ms']:.3f} ms = "
+        f"{tflops:.1f} TFLOP/s ({100 * tflops / PEAK['fp32_mfma_tflops']:.1f}% fp32 MFMA)")
+    if extra_l2:
+        idx10 = ctx.empty((Q, 10), torch.int32)
+        dist10 = ctx.empty((Q, 10), torch.float32)
+        p10 = FusedL2TopKParameters(Q, N, D, 10)
+        ms10, ph10 = timed(ctx, lambda: kern.encode(q, x, idx10, dist10, p10, Metric.euclideanSquared),
+                           max(3, a.steps // 2), 1)
+        s10 = mean_phases(ph10)["scan_ms"]
+        res["l2sq_top10_same_shape"] = {"ms_per_step": ms10, "qps": Q / (ms10 * 1e-3), "scan_ms": s10,
+                                        "scan_tflops": flops / (s10 * 1e-3) / 1e12,
+                                        "mfma_frac": flops / (s10 * 1e-3) / 1e12 / PEAK["fp32_mfma_tflops"]}
+        log(f"configs[1] shape, L2^2 top-10: {ms10:.3f} ms/step, scan {s10:.3f} ms")
+    if cpu:
+        from oracle import oracle
+
+        nq = 512
+        log(f"configs[1] CPU baseline: {nq} queries on {oracle.num_threads()} threads")
+        xh = x.cpu().numpy()
+        qh = q[:nq].cpu().numpy()
+        t0 = time.perf_counter()
+        ci, _ = oracle.flat_topk(oracle.COSINE, qh, xh, k, accum_double=False)
+        dt = time.perf_counter() - t0
+        gi = idx[:nq].cpu().numpy().view(np.uint32)
+        res["cpu_baseline"] = {
+            "value": nq / dt, "unit": "queries/s", "cores": oracle.num_threads(), "kind": "port",
+            "sample": (f"{nq} of the {Q} configs[1] queries against the full {N}x{D} database; C port of "
+                       "AccelerateFallback.batchCosineSimilarity + CPUTopK's bounded heap (float accumulation)"),
+            "seconds": dt,
+            "topk_id_overlap_with_gpu": float(np.mean([len(set(gi[r]) & set(ci[r])) / k for r in range(nq)])),
+        }
+        log(f"configs[1] CPU baseline: {nq / dt:.2f} QPS ({dt:.1f} s)")
+        del xh
+    del x, q
+    torch.cuda.empty_cache()
+    return res
 
 
-def time_steps(ctx, fn, steps: int, warmup: int):
+# ---------------------------------------------------------------------------------------
+# scalar int8, 10M x 512, Q = 4096, top-10
+# ---------------------------------------------------------------------------------------
+def run_c3(ctx, a, cpu: bool):
+    import numpy as np
     import torch
 
-    for _ in range(warmup):
-        fn()
-    ctx.synchronize()
+    from vectoraccelerate_amd import ScalarQuantizationKernel
+
+    N, D, Q, k = 10_000_000, 512, 4096, 10
+    log(f"configs[2]: generating N={N} D={D} Q={Q}")
+    g = torch.Generator(device="cuda").manual_seed(2)
+    s = torch.rand(D, device="cuda", generator=g) * 1.5 + 0.5  # U(0.5, 2) per dimension
+    x = (torch.rand(N, D, device="cuda", generator=g) * 2 - 1).mul_(s)  # U(-1, 1) * s_d
+    qf = ((torch.rand(Q, D, device="cuda", generator=g) * 2 - 1) * s).contiguous()
     torch.cuda.synchronize()
-    scan_ms = []
+    sq = ScalarQuantizationKernel(ctx)
+    mn, mx = ctx.empty((D,), torch.float32), ctx.empty((D,), torch.float32)
+    sc, zp = ctx.empty((D,), torch.float32), ctx.empty((D,), torch.int32)
+    codes = ctx.empty((N, D), torch.int8)
+    qcodes = ctx.empty((Q, D), torch.int8)
+    ctx.order_after_torch()
+
+    def quantize_db():
+        sq.encodeComputeParameters(x, N, D, mn, mx, sc, zp)
+        sq.encodeQuantize(x, codes, sc, zp, N, D)
+
+    qms, _ = timed(ctx, quantize_db, 2, 1, scan_timings=False)
+    sq.encodeQuantize(qf, qcodes, sc, zp, Q, D)
+    ctx.synchronize()
+    del x, qf
+    torch.cuda.empty_cache()
+    idx = ctx.empty((Q, k), torch.int32)
+    dist = ctx.empty((Q, k), torch.int32)
+    ms, phases = timed(ctx, lambda: sq.encodeScanTopK(qcodes, codes, idx, dist, Q, N, D, k), max(3, a.steps // 2), 1)
+    ph = mean_phases(phases)
+    ops = 2.0 * Q * N * D
+    tops = ops / (ph["scan_ms"] * 1e-3) / 1e12
+    res = {
+        "workload": "configs[2]: int8 top-10, N=10,000,000 x d=512, Q=4096, per-dimension min/max affine codes",
+        "ms_per_step": ms, "qps": Q / (ms * 1e-3), "phases_ms": ph,
+        "quantize_database_ms": qms,
+        "quantize_hbm_gbs": (N * D * 4 * 2 + N * D) / (qms * 1e-3) / 1e9,
+        "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK["int8_mfma_tops"], "unit": "TOP/s",
+                     "frac": tops / PEAK["int8_mfma_tops"], "kernel": "i8_scan_kernel<4, true, true>",
+                     "algorithmic": f"2*Q*N*D = {ops:.4g} int ops per launch"},
+    }
+    log(f"configs[2] int8 top-10: {ms:.3f} ms/step = {res['qps']:.0f} QPS; scan {ph['scan_ms']:.3f} ms = "
+        f"{tops:.0f} TOP/s; quantize 10M x 512 in {qms:.2f} ms")
+    if cpu:
+        from oracle import oracle
+
+        nq = 16
+        xh = codes.cpu().numpy()
+        qh = qcodes[:nq].cpu().numpy()
+        t0 = time.perf_counter()
+        ci, cd = oracle.i8_topk(qh, xh, k)
+        dt = time.perf_counter() - t0
+        gi = idx[:nq].cpu().numpy().view(np.uint32)
+        res["cpu_baseline"] = {"value": nq / dt, "unit": "queries/s", "cores": oracle.num_threads(), "kind": "port",
+                               "sample": f"{nq} queries x the full 10M x 512 int8 database (int32 dot + heap)",
+                               "seconds": dt, "ids_bit_exact_vs_gpu": bool(np.array_equal(gi, ci))}
+        log(f"configs[2] CPU baseline: {nq / dt:.2f} QPS; ids bit-exact vs GPU: {np.array_equal(gi, ci)}")
+        del xh
+    del codes
+    torch.cuda.empty_cache()
+    return res
+
+
+# ---------------------------------------------------------------------------------------
+# binary Hamming, 50M x 768 bits, Q = 256, top-100
+# ---------------------------------------------------------------------------------------
+def run_c4(ctx, a, cpu: bool):
+    import numpy as np
+    import torch
+
+    from vectoraccelerate_amd import HammingDistanceKernel
+
+    N, W, Q, k = 50_000_000, 24, 256, 100
+    log(f"configs[3]: generating N={N} x {W} words, Q={Q}")
+    # sign bits of i.i.d. N(0,1) floats are i.i.d. fair bits: draw the packed words directly
+    g = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randint(-2**31, 2**31 - 1, (N, W), device="cuda", generator=g, dtype=torch.int32)
+    q = torch.randint(-2**31, 2**31 - 1, (Q, W), device="cuda", generator=g, dtype=torch.int32)
+    torch.cuda.synchronize()
+    h = HammingDistanceKernel(ctx)
+    idx = ctx.empty((Q, k), torch.int32)
+    dist = ctx.empty((Q, k), torch.int32)
+    ctx.order_after_torch()
+    ms, phases = timed(ctx, lambda: h.encodeTopK(q, x, idx, dist, Q, N, W, k), max(3, a.steps // 2), 1)
+    ph = mean_phases(phases)
+    ops = 2.0 * Q * N * W
+    tops = ops / (ph["scan_ms"] * 1e-3) / 1e12
+    gbs = N * W * 4 / (ph["scan_ms"] * 1e-3) / 1e9
+    res = {
+        "workload": "configs[3]: binary Hamming top-100, N=50,000,000 x 768 bits (96 B), Q=256",
+        "ms_per_step": ms, "qps": Q / (ms * 1e-3), "phases_ms": ph,
+        "roofline": {"bound": "valu", "achieved": tops, "peak": PEAK["valu_int32_tops"], "unit": "TOP/s",
+                     "frac": tops / PEAK["valu_int32_tops"], "kernel": "hamming_scan_kernel<true>",
+                     "algorithmic": f"2 ops (xor, popcount-add) per 32-bit word: {ops:.4g} per launch",
+                     "hbm_gbs_database_once": gbs, "hbm_frac": gbs / PEAK["hbm_gbs"]},
+    }
+    log(f"configs[3] binary top-100: {ms:.3f} ms/step = {res['qps']:.0f} QPS; scan {ph['scan_ms']:.3f} ms = "
+        f"{tops:.1f} TOP/s VALU ({100 * tops / PEAK['valu_int32_tops']:.0f}%), {gbs:.0f} GB/s")
+    if cpu:
+        from oracle import oracle
+
+        nq = 16
+        xh = x.cpu().numpy().view(np.uint32)
+        qh = q[:nq].cpu().numpy().view(np.uint32)
+        t0 = time.perf_counter()
+        ci, cd = oracle.hamming_topk(qh, xh, k)
+        dt = time.perf_counter() - t0
+        gi = idx[:nq].cpu().numpy().view(np.uint32)
+        res["cpu_baseline"] = {"value": nq / dt, "unit": "queries/s", "cores": oracle.num_threads(), "kind": "port",
+                               "sample": f"{nq} queries x the full 50M-code database (popcount + stable top-k)",
+                               "seconds": dt, "ids_bit_exact_vs_gpu": bool(np.array_equal(gi, ci))}
+        log(f"configs[3] CPU baseline: {nq / dt:.2f} QPS; ids bit-exact vs GPU: {np.array_equal(gi, ci)}")
+        del xh
+    del x
+    torch.cuda.empty_cache()
+    return res
+
+
+# ---------------------------------------------------------------------------------------
+# IVF-Flat, 4096 lists, 4M x 768, Zipf(1.1) cluster sizes, Q=1024, nprobe 32
+# ---------------------------------------------------------------------------------------
+def run_c5(ctx, a, cpu: bool):
+    import numpy as np
+    import torch
+
+    from vectoraccelerate_amd import IVFSearchConfiguration, IVFSearchPipeline
+
+    C, D, N, Q, nprobe, k = 4096, 768, 4_000_000, 1024, 32, 10
+    log(f"configs[4]: generating C={C} N={N} D={D} Q={Q}")
+    g = torch.Generator(device="cuda").manual_seed(4)
+    cen = torch.randn(C, D, device="cuda", generator=g) * 4.0
+    p = 1.0 / torch.arange(1, C + 1, device="cuda", dtype=torch.float64) ** 1.1
+    p = (p / p.sum()).float()
+    lab = torch.multinomial(p, N, replacement=True, generator=g)
+    x = cen[lab] + torch.randn(N, D, device="cuda", generator=g)
+    qlab = torch.multinomial(p, Q, replacement=True, generator=g)
+    q = (cen[qlab] + torch.randn(Q, D, device="cuda", generator=g)).contiguous()
+    torch.cuda.synchronize()
+    pipe = IVFSearchPipeline(ctx, IVFSearchConfiguration(C, nprobe, D))
     t0 = time.perf_counter()
-    for _ in range(steps):
-        fn()
-        scan_ms.append(ctx.last_scan_timings())
-    ctx.synchronize()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    return (t1 - t0) * 1e3 / steps, scan_ms
+    st = pipe.prepareIndexStructure(cen, x)
+    build_s = time.perf_counter() - t0
+    off, ids = st.lists()
+    probes = pipe.findNearestCentroids(q, st).cpu().numpy().view(np.uint32)
+    sizes = np.diff(off.astype(np.int64))
+    cand = int(sizes[probes].sum())
+    distinct = np.unique(probes)
+    idx = ctx.empty((Q, k), torch.int32)
+    dist = ctx.empty((Q, k), torch.float32)
+    ms, _ = timed(ctx, lambda: pipe.encodeSearch(q, st, idx, dist, k), max(3, a.steps // 2), 1, scan_timings=False)
+    flops = 2.0 * Q * C * D + 2.0 * D * cand
+    tflops = flops / (ms * 1e-3) / 1e12
+    b_min = float(sizes[distinct].sum()) * D * 4 + C * D * 4
+    res = {
+        "workload": "configs[4]: IVF-Flat L2^2 top-10, 4096 lists, N=4,000,000 x d=768 (Zipf 1.1), Q=1024, nprobe 32",
+        "ms_per_step": ms, "qps": Q / (ms * 1e-3), "build_s": build_s,
+        "candidates_scanned": cand, "largest_list": int(sizes.max()),
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK["fp32_mfma_tflops"], "unit": "TFLOP/s",
+                     "frac": tflops / PEAK["fp32_mfma_tflops"], "kernel": "whole search (probe + sample + scan + select)",
+                     "algorithmic": f"2QCD + 2D*sum|L_p| = {flops:.4g} FLOP; distinct probed lists {b_min / 1e9:.2f} GB"},
+    }
+    log(f"configs[4] IVF top-10: {ms:.3f} ms/step = {res['qps']:.0f} QPS, {tflops:.1f} TFLOP/s effective; "
+        f"{cand / 1e6:.1f}M candidates; build {build_s:.1f} s")
+    if cpu:
+        from oracle import oracle
+
+        nq = 64
+        xh = x.cpu().numpy()
+        qh = q[:nq].cpu().numpy()
+        ch = cen.cpu().numpy()
+        t0 = time.perf_counter()
+        op = oracle.ivf_probe(qh, ch, nprobe)
+        ci, cd = oracle.ivf_scan(qh, xh, off, ids, op, k)
+        dt = time.perf_counter() - t0
+        gi = idx[:nq].cpu().numpy().view(np.uint32)
+        res["cpu_baseline"] = {"value": nq / dt, "unit": "queries/s", "cores": oracle.num_threads(), "kind": "port",
+                               "sample": f"{nq} queries: exact coarse probe + list scan over the same lists",
+                               "seconds": dt,
+                               "topk_id_overlap_with_gpu": float(np.mean([len(set(gi[r]) & set(ci[r])) / k
+                                                                          for r in range(nq)]))}
+        log(f"configs[4] CPU baseline: {nq / dt:.2f} QPS")
+        del xh
+    st.close()
+    del x, cen, q
+    torch.cuda.empty_cache()
+    return res
 
 
 def main() -> int:
@@ -86,12 +359,10 @@ def main() -> int:
         print(f"bench.py measures one GPU only (every box in this build has one); --gpus {a.gpus} is not supported",
               file=sys.stderr)
         return 2
-    import numpy as np
     import torch
 
-    from vectoraccelerate_amd import FusedL2TopKKernel, FusedL2TopKParameters, GPUContext, Metric
+    from vectoraccelerate_amd import GPUContext
 
-    N, D, Q, k = a.N, a.D, a.Q, a.k
     if a.copy_calibration:
         src_t = torch.ones(1 << 28, device="cuda", dtype=torch.float32)  # 1 GiB
         dst_t = torch.empty_like(src_t)
@@ -99,109 +370,49 @@ def main() -> int:
         torch.cuda.synchronize()
         log("copy calibration: 1 GiB read + 1 GiB written by one copy kernel")
         del src_t, dst_t
-    log(f"generating configs[1] data N={N} D={D} Q={Q} on cuda:0")
-    x, q, src = make_c2(N, D, Q)
     ctx = GPUContext(0)
     ctx.set_profiling(True)
-    kern = FusedL2TopKKernel(ctx)
-    idx = ctx.empty((Q, k), torch.int32)
-    dist = ctx.empty((Q, k), torch.float32)
-    params = FusedL2TopKParameters(Q, N, D, k)
-
-    def step_cos():
-        kern.encode(q, x, idx, dist, params, Metric.cosine)
-
-    log(f"timing cosine top-{k}: warmup {a.warmup}, steps {a.steps}")
-    ms, phases = time_steps(ctx, step_cos, a.steps, a.warmup)
-    scan = float(np.mean([p["scan_ms"] for p in phases]))
-    flops = 2.0 * Q * N * D
-    achieved = flops / (scan * 1e-3) / 1e12
-    qps = Q / (ms * 1e-3)
-    rank1 = float((idx[:, 0].long() == src).float().mean().item())
-    log(f"cosine top-{k}: {ms:.3f} ms/step, {qps:.0f} QPS, scan kernel {scan:.3f} ms = {achieved:.1f} TFLOP/s")
-
-    extra = {
-        "phases_ms": {kk: float(np.mean([p[kk] for p in phases])) for kk in
-                      ("sample_ms", "scan_ms", "select_ms", "fallback_ms", "total_ms")},
-        "candidate_cap": phases[-1]["candidate_cap"],
-        "sample_rows": phases[-1]["sample_rows"],
-        "overflow_rows": phases[-1]["overflow_rows"],
-        "rank1_is_source_row": rank1,
-    }
-
-    if not a.no_extra:
-        idx10 = ctx.empty((Q, 10), torch.int32)
-        dist10 = ctx.empty((Q, 10), torch.float32)
-        p10 = FusedL2TopKParameters(Q, N, D, 10)
-        ms10, ph10 = time_steps(ctx, lambda: kern.encode(q, x, idx10, dist10, p10, Metric.euclideanSquared),
-                                max(3, a.steps // 2), 1)
-        scan10 = float(np.mean([p["scan_ms"] for p in ph10]))
-        extra["l2sq_top10_same_shape"] = {
-            "ms_per_step": ms10,
-            "qps": Q / (ms10 * 1e-3),
-            "scan_ms": scan10,
-            "scan_tflops": flops / (scan10 * 1e-3) / 1e12,
-            "mfma_frac": flops / (scan10 * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS,
-        }
-        log(f"L2^2 top-10: {ms10:.3f} ms/step, scan {scan10:.3f} ms")
-
-    cpu = None
-    if not a.no_cpu:
-        from oracle import oracle
-
-        nq = min(a.cpu_queries, Q)
-        log(f"CPU baseline: copying the database to the host, {nq} queries on {oracle.num_threads()} threads")
-        xh = x.cpu().numpy()
-        qh = q[:nq].cpu().numpy()
-        t0 = time.perf_counter()
-        ci, cd = oracle.flat_topk(oracle.COSINE, qh, xh, k, accum_double=False)
-        t1 = time.perf_counter()
-        gi = idx[:nq].cpu().numpy().view(np.uint32)
-        agree = float(np.mean([len(set(gi[r]) & set(ci[r])) / k for r in range(nq)]))
-        cpu = {
-            "value": nq / (t1 - t0),
-            "unit": "queries/s",
-            "cores": oracle.num_threads(),
-            "kind": "port",
-            "sample": (f"{nq} of the {Q} configs[1] queries against the full {N}x{D} database; C port of "
-                       f"AccelerateFallback.batchCosineSimilarity + bounded heap (float accumulation)"),
-            "seconds": t1 - t0,
-            "topk_overlap_with_gpu": agree,
-        }
-        log(f"CPU baseline: {cpu['value']:.2f} QPS in {t1 - t0:.1f} s (overlap with GPU {agree:.4f})")
-
+    cpu = not a.no_cpu
+    extra = {}
+    if a.workload in ("all", "c2"):
+        c2 = run_c2(ctx, a, cpu, extra_l2=not a.no_extra)
+    else:
+        c2 = None
+    if a.workload in ("all", "c3"):
+        extra["configs2_int8"] = run_c3(ctx, a, cpu)
+    if a.workload in ("all", "c4"):
+        extra["configs3_binary"] = run_c4(ctx, a, cpu)
+    if a.workload in ("all", "c5"):
+        extra["configs4_ivf"] = run_c5(ctx, a, cpu)
+    ctx.close()
+    if c2 is None:
+        print(json.dumps({"metric": METRIC, "value": None, "extra": extra}), flush=True)
+        return 0
+    cpu_base = c2.pop("cpu_baseline", None)
+    roof = c2.pop("roofline")
     line = {
         "metric": METRIC,
-        "value": qps,
+        "value": c2["qps"],
         "unit": "queries/s",
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
-        "ms_per_step": ms,
+        "ms_per_step": c2["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (torch seeded N(0,1), configs[1] construction)",
+        "data": "synthetic (torch seeded generators, BASELINE configs constructions)",
         "config": {
             "workload": "BASELINE configs[1]: flat cosine top-100, N=1,000,000 x d=1536 fp32, Q=1024",
-            "N": N, "D": D, "Q": Q, "k": k, "metric": "cosine (1 - s)", "parallelism": "single GPU",
+            "N": 1_000_000, "D": 1536, "Q": 1024, "k": 100, "metric": "cosine (1 - s)",
+            "parallelism": "single GPU",
         },
-        "roofline": {
-            "bound": "mfma",
-            "achieved": achieved,
-            "peak": PEAK_FP32_MFMA_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": achieved / PEAK_FP32_MFMA_TFLOPS,
-            "traffic": None,
-            "kernel": "dist_gemm_kernel<4,true> (filter epilogue)",
-            "algorithmic": f"2*Q*N*D = {flops:.4g} FLOP per launch",
-        },
-        "cpu_baseline": cpu,
-        "extra": extra,
+        "roofline": roof,
+        "cpu_baseline": cpu_base,
+        "extra": {"configs1_cosine_top100": c2, **extra},
     }
     print(json.dumps(line), flush=True)
-    ctx.close()
     return 0
 
 

@@ -114,6 +114,13 @@ def load(path: Path | None = None) -> C.CDLL:
     p = Path(path) if path else LIB_PATH
     if not p.exists():
         raise LibraryMissing(f"{p} not found; build it with vectoraccelerate_amd/build.py")
+    # PyTorch-ROCm wheels ship their own libamdhip64.so.  Loading torch first makes this
+    # library bind to that same HIP runtime; loading ours first would put a second runtime
+    # in the process and torch's device initialisation would then fail.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = C.CDLL(str(p))
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name, None)

@@ -72,18 +72,22 @@ __device__ __forceinline__ uint32_t uniform_load(const uint32_t* p) {
     return *(const __attribute__((address_space(4))) uint32_t*)(p);
 }
 
-template <bool FILTER>
+// WC > 0: compile-time word count (fully unrolled; query words arrive in wide scalar loads);
+// WC = 0: any W <= kMaxWords.
+template <int WC, bool FILTER>
 __global__ __launch_bounds__(256) void hamming_scan_kernel(HamArgs a) {
+    constexpr uint32_t WR = WC > 0 ? uint32_t(WC) : kMaxWords;
+    const uint32_t W = WC > 0 ? uint32_t(WC) : a.W;
     const uint32_t j = blockIdx.x * 256 + threadIdx.x;
     const bool valid = j < a.cols;
     const uint32_t row = a.c0 + (valid ? j : 0) * a.stride;
     // the row, word by word, in VGPRs (uint4 loads; rows are 16-byte aligned when W % 4 == 0)
-    uint32_t xr[kMaxWords];
-    const uint32_t* xp = a.x + uint64_t(row) * a.W;
-    if ((a.W & 3) == 0) {
+    uint32_t xr[WR];
+    const uint32_t* xp = a.x + uint64_t(row) * W;
+    if ((W & 3) == 0) {
 #pragma unroll
-        for (uint32_t w = 0; w < kMaxWords; w += 4) {
-            if (w < a.W) {
+        for (uint32_t w = 0; w < WR; w += 4) {
+            if (w < W) {
                 const uint4 v = *reinterpret_cast<const uint4*>(xp + w);
                 xr[w] = v.x;
                 xr[w + 1] = v.y;
@@ -93,16 +97,17 @@ __global__ __launch_bounds__(256) void hamming_scan_kernel(HamArgs a) {
         }
     } else {
 #pragma unroll
-        for (uint32_t w = 0; w < kMaxWords; ++w)
-            if (w < a.W) xr[w] = xp[w];
+        for (uint32_t w = 0; w < WR; ++w)
+            if (w < W) xr[w] = xp[w];
     }
+#pragma unroll 2
     for (uint32_t i = 0; i < a.nq; ++i) {
         const uint32_t qr = a.qrow ? uniform_load(a.qrow + i) : a.q0 + i;
-        const uint32_t* qw = a.q + uint64_t(qr) * a.W;
+        const uint32_t* qw = a.q + uint64_t(qr) * W;
         uint32_t d = 0;
 #pragma unroll
-        for (uint32_t w = 0; w < kMaxWords; ++w)
-            if (w < a.W) d += __popc(xr[w] ^ uniform_load(qw + w));
+        for (uint32_t w = 0; w < WR; ++w)
+            if (w < W) d += __popc(xr[w] ^ uniform_load(qw + w));
         if (!valid) continue;
         if (FILTER) {
             const uint32_t qi = a.q0 + i;
@@ -153,10 +158,23 @@ va_status launch_ham(va_context* ctx, const HamArgs& a, bool filter) {
     const dim3 grid((a.cols + 255) / 256);
     const bool aligned = (a.W & 3) == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0;
     if (a.W <= kMaxWords && (aligned || (a.W & 3) != 0)) {
-        if (filter)
-            hamming_scan_kernel<true><<<grid, dim3(256), 0, ctx->stream>>>(a);
-        else
-            hamming_scan_kernel<false><<<grid, dim3(256), 0, ctx->stream>>>(a);
+#define VA_HAM_CASE(WC)                                                                       \
+    if (filter)                                                                               \
+        hamming_scan_kernel<WC, true><<<grid, dim3(256), 0, ctx->stream>>>(a);               \
+    else                                                                                      \
+        hamming_scan_kernel<WC, false><<<grid, dim3(256), 0, ctx->stream>>>(a);
+        if (a.W == 8 && aligned) {
+            VA_HAM_CASE(8)
+        } else if (a.W == 16 && aligned) {
+            VA_HAM_CASE(16)
+        } else if (a.W == 24 && aligned) {
+            VA_HAM_CASE(24)
+        } else if (a.W == 32 && aligned) {
+            VA_HAM_CASE(32)
+        } else {
+            VA_HAM_CASE(0)
+        }
+#undef VA_HAM_CASE
     } else {
         if (filter)
             hamming_scan_wide_kernel<true><<<grid, dim3(256), 0, ctx->stream>>>(a);

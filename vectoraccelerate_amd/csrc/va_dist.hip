@@ -79,9 +79,14 @@ __global__ __launch_bounds__(256, 2) void dist_gemm_kernel(DistArgs a) {
     const int l32 = lane & 31;
     const int hh = lane >> 5;
 
+    // XCD-aware order: workgroup w runs on XCD w % 8.  XCD x takes database tiles x, x+8, ...
+    // and runs every query block of a tile back to back, so each tile crosses the fabric once
+    // and is reused from that XCD's L2 (the grid is padded to a multiple of 8 tiles).
     const uint32_t nqb = a.tiles ? 1u : (a.Q + T::TQ - 1) / T::TQ;
-    const uint32_t qb = blockIdx.x % nqb;  // query block varies fastest: a database tile is
-    const uint32_t tb = blockIdx.x / nqb;  // consumed by consecutive workgroups (L2 / MALL reuse)
+    const uint32_t xcd = blockIdx.x % kXcds, seq = blockIdx.x / kXcds;
+    const uint32_t qb = seq % nqb;
+    const uint32_t tb = (seq / nqb) * kXcds + xcd;
+    if (!a.tiles && tb * uint32_t(T::TN) >= a.N) return;  // padding workgroup
     // Tile extent: queries qs + i (i < qc; through qrow when given) and database rows at
     // positions rs + j*rstride (j < rc).  Flat launches derive it from blockIdx; list-major
     // (IVF) launches read one descriptor {qs, qc, rs, rc} per workgroup.
@@ -206,8 +211,42 @@ __global__ __launch_bounds__(256, 2) void dist_gemm_kernel(DistArgs a) {
     if (li >= qc) return;
     const uint32_t orow = qs + li;                                   // dense output row
     const uint32_t qi = (OUT == OUT_FILTER && a.qrow) ? a.qrow[orow] : orow;  // query id (filter)
-    uint32_t thr = 0;
-    if (OUT == OUT_FILTER) thr = a.thr[qi];
+    if (OUT == OUT_FILTER) {
+        // Count this lane's passing keys, reserve them with one atomic, then write them.
+        const uint32_t thr = a.thr[qi];
+        uint64_t pass = 0;  // bit 16b + 4j + e
+        uint32_t keys[64];
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int mloc = b * 32 + 8 * j + 4 * hh;
+                const f32x4v xx = *reinterpret_cast<const f32x4v*>(nrm + wave * 128 + mloc);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t key = key_of_float(apply_op(a.op, acc[b][4 * j + e], qq, xx[e]));
+                    keys[16 * b + 4 * j + e] = key;
+                    const bool p = uint32_t(wn * 128 + mloc + e) < rc && key <= thr;
+                    pass |= uint64_t(p) << (16 * b + 4 * j + e);
+                }
+            }
+        if (pass) {
+            uint32_t pos = atomicAdd(a.cnt + qi, uint32_t(__popcll(pass)));
+#pragma unroll
+            for (int t = 0; t < 64; ++t) {
+                if (!((pass >> t) & 1)) continue;
+                if (pos < a.cap) {
+                    const int b = t >> 4, j = (t >> 2) & 3, e = t & 3;
+                    const uint32_t p = rs + uint32_t(wn * 128 + b * 32 + 8 * j + 4 * hh + e) * rstride;
+                    const int64_t o = int64_t(qi) * a.cap + pos;
+                    a.cand_key[o] = keys[t];
+                    a.cand_id[o] = a.ids ? a.ids[p] : a.id_base + p;
+                }
+                ++pos;
+            }
+        }
+        return;
+    }
 
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -219,21 +258,7 @@ __global__ __launch_bounds__(256, 2) void dist_gemm_kernel(DistArgs a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) val[e] = apply_op(a.op, acc[b][4 * j + e], qq, xx[e]);
             const uint32_t jr = uint32_t(wn * 128 + mloc);  // row slot of acc element e = 0
-            if (OUT == OUT_FILTER) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t key = key_of_float(val[e]);
-                    if (jr + e < rc && key <= thr) {
-                        const uint32_t pos = atomicAdd(a.cnt + qi, 1u);
-                        if (pos < a.cap) {
-                            const uint32_t p = rs + (jr + e) * rstride;
-                            const int64_t o = int64_t(qi) * a.cap + pos;
-                            a.cand_key[o] = key;
-                            a.cand_id[o] = a.ids ? a.ids[p] : a.id_base + p;
-                        }
-                    }
-                }
-            } else if (OUT == OUT_KEYS) {
+            if (OUT == OUT_KEYS) {
                 uint32_t* o = a.out_k + int64_t(orow) * a.ldo + rs + jr;
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
@@ -258,7 +283,7 @@ va_status launch_tile(va_context* ctx, const DistArgs& a) {
     using T = Tile<WQ>;
     const uint64_t nqb = (a.Q + T::TQ - 1) / T::TQ;
     const uint64_t ntb = (a.N + T::TN - 1) / T::TN;
-    const uint64_t grid = a.tiles ? a.ntiles : nqb * ntb;
+    const uint64_t grid = a.tiles ? a.ntiles : nqb * ((ntb + kXcds - 1) / kXcds) * kXcds;
     if (grid == 0) return VA_OK;
     if (grid > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "distance grid too large (%llu tiles)", (unsigned long long)grid);
     if (T::LDS_BYTES > 65536) {

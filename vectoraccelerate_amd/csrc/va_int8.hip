@@ -119,8 +119,11 @@ __global__ __launch_bounds__(256) void dequantize_kernel(const int8_t* __restric
 // ---------------------------------------------------------------------------------------
 // int8 MFMA scan
 // ---------------------------------------------------------------------------------------
-constexpr int KB = 64;                 // bytes of each row per LDS stage (two 32-byte k-steps)
-constexpr int ROWB = KB + 16;          // 80-byte LDS rows: conflict-free ds_read_b128
+#ifndef VA_I8_KB
+#define VA_I8_KB 64
+#endif
+constexpr int KB = VA_I8_KB;           // bytes of each row per LDS stage (32-byte k-steps)
+constexpr int ROWB = KB + 16;          // +16 B pad: conflict-free ds_read_b128 across 16 rows
 
 struct I8Args {
     const int8_t* q = nullptr;
@@ -138,21 +141,25 @@ struct I8Args {
     uint32_t cap = 0;
 };
 
-template <int WQ>
+// Tile shapes: QBW query blocks of 32 per wave, WQ x WN waves; wave tile = 32*QBW queries x
+// 128 rows; workgroup tile = 32*QBW*WQ queries x 128*WN rows.  The 8-wave 256 x 256 shape is
+// used for large Q: it halves the L2-to-CU bytes per MFMA op of the 128 x 128 shape (the
+// int8 MFMA rate otherwise outruns the ~64 B/clk/CU the L2 can deliver).
+template <int QBW, int WQ, int WN>
 struct I8Tile {
-    static constexpr int WN = 4 / WQ;
-    static constexpr int TQ = 32 * WQ;
+    static constexpr int THREADS = 64 * WQ * WN;
+    static constexpr int TQ = 32 * QBW * WQ;
     static constexpr int TN = 128 * WN;
     static constexpr int ROWS = TQ + TN;
     static constexpr int CHUNKS = ROWS * (KB / 16);
-    static constexpr int CPT = (CHUNKS + 255) / 256;
+    static constexpr int CPT = (CHUNKS + THREADS - 1) / THREADS;
     static constexpr int STAGE = ROWS * ROWB;  // bytes
     static constexpr size_t LDS_BYTES = size_t(2 * STAGE);
 };
 
-template <int WQ, bool VEC, bool FILTER>
-__global__ __launch_bounds__(256, 2) void i8_scan_kernel(I8Args a) {
-    using T = I8Tile<WQ>;
+template <int QBW, int WQ, int WN, bool VEC, bool FILTER>
+__global__ __launch_bounds__(64 * WQ * WN) void i8_scan_kernel(I8Args a) {
+    using T = I8Tile<QBW, WQ, WN>;
     extern __shared__ __attribute__((aligned(16))) char lds8[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -162,24 +169,28 @@ __global__ __launch_bounds__(256, 2) void i8_scan_kernel(I8Args a) {
     const int l32 = lane & 31;
     const int hh = lane >> 5;
 
+    // XCD-aware order (workgroup w runs on XCD w % 8): XCD x takes database tiles x, x+8, ...
+    // and runs every query block of a tile back to back, so a tile crosses the fabric once.
     const uint32_t nqb = (a.Q + T::TQ - 1) / T::TQ;
-    const uint32_t qb = blockIdx.x % nqb;
-    const uint32_t tb = blockIdx.x / nqb;
+    const uint32_t xcd = blockIdx.x % kXcds, seq = blockIdx.x / kXcds;
+    const uint32_t qb = seq % nqb;
+    const uint32_t tb = (seq / nqb) * kXcds + xcd;
     const uint32_t q0 = qb * T::TQ;
     const uint32_t n0 = tb * T::TN;
+    if (n0 >= a.N) return;  // padding workgroup
 
     const int8_t* src[T::CPT];
     int ldsoff[T::CPT];
     uint32_t colv[T::CPT];
 #pragma unroll
     for (int j = 0; j < T::CPT; ++j) {
-        const int c = tid + 256 * j;
+        const int c = tid + T::THREADS * j;
         src[j] = nullptr;
         ldsoff[j] = -1;
         colv[j] = 0;
         if (c < T::CHUNKS) {
-            const int row = c >> 2;
-            const int col = (c & 3) * 16;
+            const int row = c / (KB / 16);
+            const int col = (c % (KB / 16)) * 16;
             ldsoff[j] = row * ROWB + col;
             colv[j] = uint32_t(col);
             if (row < T::TQ) {
@@ -217,17 +228,19 @@ __global__ __launch_bounds__(256, 2) void i8_scan_kernel(I8Args a) {
             if (ldsoff[j] >= 0) *reinterpret_cast<i32x4v*>(stage + ldsoff[j]) = pre[j];
     };
 
-    i32x16 acc[4];
+    i32x16 acc[QBW][4];
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int u = 0; u < QBW; ++u)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[b][v] = 0;
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[u][b][v] = 0;
 
     const int nstages = int((a.D + KB - 1) / KB);
     load(0);
     store(lds8);
     __syncthreads();
-    const int boff = (wq * 32 + l32) * ROWB + hh * 16;
+    const int boff = (wq * QBW * 32 + l32) * ROWB + hh * 16;
     const int aoff = (T::TQ + wn * 128 + l32) * ROWB + hh * 16;
     for (int s = 0; s < nstages; ++s) {
         const bool more = (s + 1) < nstages;
@@ -235,75 +248,97 @@ __global__ __launch_bounds__(256, 2) void i8_scan_kernel(I8Args a) {
         const char* st = lds8 + (s & 1) * T::STAGE;
 #pragma unroll
         for (int g = 0; g < KB / 32; ++g) {
-            const i32x4v bv = *reinterpret_cast<const i32x4v*>(st + boff + g * 32);
+            i32x4v bv[QBW];
+#pragma unroll
+            for (int u = 0; u < QBW; ++u)
+                bv[u] = *reinterpret_cast<const i32x4v*>(st + boff + u * 32 * ROWB + g * 32);
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
                 const i32x4v av = *reinterpret_cast<const i32x4v*>(st + aoff + b * 32 * ROWB + g * 32);
-                acc[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, acc[b], 0, 0, 0);
+#pragma unroll
+                for (int u = 0; u < QBW; ++u)
+                    acc[u][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[u], acc[u][b], 0, 0, 0);
             }
         }
         if (more) store(lds8 + ((s + 1) & 1) * T::STAGE);
         __syncthreads();
     }
 
-    const uint32_t qi = q0 + uint32_t(wq * 32 + l32);
-    if (qi >= a.Q) return;
     const uint32_t nbase = n0 + uint32_t(wn * 128);
-    uint32_t thr = 0;
-    if (FILTER) thr = a.thr[qi];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
+    for (int u = 0; u < QBW; ++u) {
+        const uint32_t qi = q0 + uint32_t((wq * QBW + u) * 32 + l32);
+        if (qi >= a.Q) continue;
+        if (FILTER) {
+            const uint32_t thr = a.thr[qi];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t m = nbase + uint32_t(b * 32 + 8 * j + 4 * hh);
+            for (int b = 0; b < 4; ++b)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                if (m + e >= a.N) continue;
-                const uint32_t key = key_of_i32(-acc[b][4 * j + e]);
-                if (FILTER) {
-                    if (key <= thr) {
-                        const uint32_t pos = atomicAdd(a.cnt + qi, 1u);
-                        if (pos < a.cap) {
-                            const int64_t o = int64_t(qi) * a.cap + pos;
-                            a.cand_key[o] = key;
-                            a.cand_id[o] = m + uint32_t(e);
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t m = nbase + uint32_t(b * 32 + 8 * j + 4 * hh + e);
+                        const uint32_t key = key_of_i32(-acc[u][b][4 * j + e]);
+                        if (m < a.N && key <= thr) {
+                            const uint32_t pos = atomicAdd(a.cnt + qi, 1u);
+                            if (pos < a.cap) {
+                                const int64_t o = int64_t(qi) * a.cap + pos;
+                                a.cand_key[o] = key;
+                                a.cand_id[o] = m;
+                            }
                         }
                     }
-                } else {
-                    a.out_k[int64_t(qi) * a.ldo + m + e] = key;
+        } else {
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t m = nbase + uint32_t(b * 32 + 8 * j + 4 * hh);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (m + e < a.N) a.out_k[int64_t(qi) * a.ldo + m + e] = key_of_i32(-acc[u][b][4 * j + e]);
                 }
-            }
         }
     }
 }
 
-template <int WQ, bool VEC, bool FILTER>
+template <int QBW, int WQ, int WN, bool VEC, bool FILTER>
 va_status launch_i8_tile(va_context* ctx, const I8Args& a) {
-    using T = I8Tile<WQ>;
-    const uint64_t grid = uint64_t((a.Q + T::TQ - 1) / T::TQ) * ((a.N + T::TN - 1) / T::TN);
+    using T = I8Tile<QBW, WQ, WN>;
+    const uint64_t ntb = (a.N + T::TN - 1) / T::TN;
+    const uint64_t grid = uint64_t((a.Q + T::TQ - 1) / T::TQ) * ((ntb + kXcds - 1) / kXcds) * kXcds;
     if (grid == 0) return VA_OK;
     if (grid > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "int8 scan grid too large");
+    auto kern = &i8_scan_kernel<QBW, WQ, WN, VEC, FILTER>;
     if (T::LDS_BYTES > 65536)
-        VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(&i8_scan_kernel<WQ, VEC, FILTER>),
+        VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                               hipFuncAttributeMaxDynamicSharedMemorySize, int(T::LDS_BYTES)));
-    i8_scan_kernel<WQ, VEC, FILTER><<<dim3(uint32_t(grid)), dim3(256), T::LDS_BYTES, ctx->stream>>>(a);
+    kern<<<dim3(uint32_t(grid)), dim3(T::THREADS), T::LDS_BYTES, ctx->stream>>>(a);
     VA_CHECK_LAUNCH(ctx);
     return VA_OK;
+}
+
+template <int QBW, int WQ, int WN>
+va_status launch_i8_shape(va_context* ctx, const I8Args& a, bool vec, bool filter) {
+    if (filter) return vec ? launch_i8_tile<QBW, WQ, WN, true, true>(ctx, a) : launch_i8_tile<QBW, WQ, WN, false, true>(ctx, a);
+    return vec ? launch_i8_tile<QBW, WQ, WN, true, false>(ctx, a) : launch_i8_tile<QBW, WQ, WN, false, false>(ctx, a);
 }
 
 va_status launch_i8(va_context* ctx, const I8Args& a, bool filter) {
     if (a.Q == 0 || a.N == 0) return VA_OK;
     const bool vec = (a.D % 16 == 0) && (a.ldq % 16 == 0) && (a.ldx % 16 == 0) &&
                      ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
-    const int wq = a.Q <= 32 ? 1 : (a.Q <= 64 ? 2 : 4);
-#define VA_I8_CASE(W)                                                                                  \
-    if (wq == W) {                                                                                     \
-        if (filter) return vec ? launch_i8_tile<W, true, true>(ctx, a) : launch_i8_tile<W, false, true>(ctx, a); \
-        return vec ? launch_i8_tile<W, true, false>(ctx, a) : launch_i8_tile<W, false, false>(ctx, a);   \
-    }
-    VA_I8_CASE(1) VA_I8_CASE(2) VA_I8_CASE(4)
-#undef VA_I8_CASE
-    return VA_ERR_INVALID_ARG;
+    if (a.Q <= 32) return launch_i8_shape<1, 1, 4>(ctx, a, vec, filter);
+    if (a.Q <= 64) return launch_i8_shape<1, 2, 2>(ctx, a, vec, filter);
+// Large-Q shape: 0 = 128 x 128 (4 waves), 1 = 128 x 256 (4 waves), 2 = 256 x 256 (8 waves).
+// Measured on configs[2] (10M x 512, Q=4096): 0 is fastest with 64-byte register-staged
+// stages (each stage's MFMA work is shorter than its load round trip).
+#ifndef VA_I8_LARGE_SHAPE
+#define VA_I8_LARGE_SHAPE 0
+#endif
+    if (a.Q <= 192 || VA_I8_LARGE_SHAPE == 0) return launch_i8_shape<1, 4, 1>(ctx, a, vec, filter);
+    if (VA_I8_LARGE_SHAPE == 1) return launch_i8_shape<2, 2, 2>(ctx, a, vec, filter);
+    return launch_i8_shape<2, 4, 2>(ctx, a, vec, filter);
 }
 
 struct I8Producer final : KeyProducer {

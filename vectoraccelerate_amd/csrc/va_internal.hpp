@@ -102,6 +102,8 @@ struct Scratch {
 namespace va {
 
 constexpr uint32_t kSentinel = 0xFFFFFFFFu;
+// MI355X: 8 XCDs of 32 CUs, each with its own 4 MB L2; workgroup w is dispatched to XCD w % 8.
+constexpr uint32_t kXcds = 8;
 
 // Ascending-orderable key of a float: -0 and +0 map to one key, NaN to the largest key.
 __host__ __device__ inline uint32_t key_of_float(float f) {

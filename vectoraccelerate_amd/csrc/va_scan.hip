@@ -73,7 +73,11 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
     base.key_kind = out.key_kind;
 
     // ---- plan ------------------------------------------------------------------------
-    uint64_t S = ctx->opt_sample_rows ? ctx->opt_sample_rows : std::max<uint64_t>(kMinSample, N / 64);
+    // Sample size: N/64 rows keeps ~64k candidates per query, but the dense sample costs Q*S
+    // keys, so it is capped at kDenseBudgetBytes of keys in total (16384 rows minimum).
+    uint64_t S = ctx->opt_sample_rows
+                     ? ctx->opt_sample_rows
+                     : std::max<uint64_t>(kMinSample, std::min<uint64_t>(N / 64, kDenseBudgetBytes / 4 / Q));
     const bool direct = S >= N;
     PhaseMarks pm(ctx);
     ctx->last_scan = va_scan_timings{};
