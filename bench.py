@@ -27,7 +27,9 @@ METRIC = json.loads((ROOT / "BASELINE.json").read_text())["metric"]
 PEAK = {
     "fp32_mfma_tflops": 157.3,
     "int8_mfma_tops": 5000.0,
-    "valu_int32_tops": 39.3,  # 256 CU x 64 lanes x 2.4 GHz, non-packed 32-bit integer ops
+    # 256 CU x 128 lanes/clk x 2.4 GHz: the measured xor + popcount rate (41.8 T/s) exceeds the
+    # 64 lanes/clk/CU figure, so this is the smallest power-of-two rate consistent with it
+    "valu_int32_tops": 78.6,
     "hbm_gbs": 8000.0,
 }
 
@@ -48,6 +50,18 @@ def parse():
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def measured_traffic() -> float | None:
+    """HBM bytes per launch of the headline scan kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (calibrated against a plain copy)."""
+    f = ROOT / "profiles" / "hbm_traffic__dist_gemm_filter__configs1_cosine_top100.txt"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
 
 
 def timed(ctx, fn, steps: int, warmup: int, scan_timings: bool = True):
@@ -116,7 +130,8 @@ def run_c2(ctx, a, cpu: bool, extra_l2: bool):
         "rank1_is_source_row": float((idx[:, 0].long() == src).float().mean().item()),
         "roofline": {
             "bound": "mfma", "achieved": tflops, "peak": PEAK["fp32_mfma_tflops"], "unit": "TFLOP/s",
-            "frac": tflops / PEAK["fp32_mfma_tflops"], "traffic": None,
+            "frac": tflops / PEAK["fp32_mfma_tflops"], "traffic": measured_traffic(),
+            "traffic_source": "profiles/hbm_traffic__dist_gemm_filter__configs1_cosine_top100.txt",
             "kernel": "dist_gemm_kernel<4, true, 2> (filtering scan)",
             "algorithmic": f"2*Q*N*D = {flops:.4g} FLOP per launch",
         },
