@@ -1,0 +1,162 @@
+"""Parity at the BASELINE configs' full sizes.
+
+Each test builds the config's data on the GPU (torch generators; data plumbing only), runs the
+search through the C ABI, and checks (a) size-independent properties over every query and (b) a
+query subset against the CPU oracle over the full database (the oracle finishes it in seconds on
+the box's cores).  Integer paths bit-exact; fp32 within the tolerance of tests/helpers.py.
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+from tests.helpers import COSINE, L2SQ, SENT, check_topk, check_topk_exact
+
+pytestmark = pytest.mark.gpu
+
+
+def note(msg):
+    print(f"[fullsize] {msg}", file=sys.stderr, flush=True)
+
+
+def test_configs1_cosine_top100_full(ctx, oracle):
+    """1,000,000 x 1536 normalised rows, Q=1024 noisy copies of rows, cosine top-100."""
+    import torch
+    from vectoraccelerate_amd import FusedL2TopKKernel, FusedL2TopKParameters, Metric
+
+    N, D, Q, k = 1_000_000, 1536, 1024, 100
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(N, D, device="cuda", generator=g)
+    x /= x.norm(dim=1, keepdim=True)
+    gq = torch.Generator(device="cuda").manual_seed(1)
+    src = torch.randint(0, N, (Q,), device="cuda", generator=gq)
+    q = x[src] + 0.05 * torch.randn(Q, D, device="cuda", generator=gq)
+    q = (q / q.norm(dim=1, keepdim=True)).contiguous()
+    res = FusedL2TopKKernel(ctx).execute(q, x, FusedL2TopKParameters(Q, N, D, k), metric=Metric.cosine)
+    gi = res.indices.cpu().numpy().view(np.uint32)
+    gd = res.distances.cpu().numpy()
+    note("configs[1] searched")
+    # properties over all queries: the source row ranks first, rows sorted, no sentinel, unique
+    np.testing.assert_array_equal(gi[:, 0], src.cpu().numpy())
+    assert np.all(np.diff(gd, axis=1) >= 0)
+    assert np.all(gi != SENT)
+    assert all(len(set(r)) == k for r in gi)
+    # oracle on a subset against the full database
+    xh = x.cpu().numpy()
+    qh = q.cpu().numpy()
+    sub = np.array([0, 1, 511, 1023])
+    oi, od = oracle.flat_topk(COSINE, qh[sub], xh, k)
+    check_topk(COSINE, qh[sub], xh, k, gi[sub], gd[sub], oi, od)
+    # batch == sequential for one query
+    one = FusedL2TopKKernel(ctx).execute(q[7:8].contiguous(), x, FusedL2TopKParameters(1, N, D, k),
+                                         metric=Metric.cosine)
+    np.testing.assert_array_equal(one.indices.cpu().numpy().view(np.uint32)[0], gi[7])
+
+
+def test_configs2_int8_top10_full(ctx, oracle):
+    """10,000,000 x 512 U(-1,1)*s_d, per-dimension affine int8, Q=4096, top-10, bit-exact."""
+    import torch
+    from vectoraccelerate_amd import ScalarQuantizationKernel
+
+    N, D, Q, k = 10_000_000, 512, 4096, 10
+    g = torch.Generator(device="cuda").manual_seed(2)
+    s = torch.rand(D, device="cuda", generator=g) * 1.5 + 0.5
+    x = (torch.rand(N, D, device="cuda", generator=g) * 2 - 1).mul_(s)
+    qf = ((torch.rand(Q, D, device="cuda", generator=g) * 2 - 1) * s).contiguous()
+    sq = ScalarQuantizationKernel(ctx)
+    p = sq.computePerDimensionParameters(x)
+    xc = sq.quantizePerDimension(x, p)
+    qc = sq.quantizePerDimension(qf, p)
+    note("configs[2] quantised")
+    xh = x.cpu().numpy()
+    mn, mx, sc, zp = oracle.sq_params_per_dim(xh)
+    np.testing.assert_array_equal(p.min, mn)
+    np.testing.assert_array_equal(p.max, mx)
+    np.testing.assert_array_equal(p.scale, sc)
+    np.testing.assert_array_equal(p.zeroPoint, zp)
+    xch = xc.cpu().numpy()
+    rows = np.r_[0:20000, N - 20000:N]
+    np.testing.assert_array_equal(xch[rows], oracle.sq_quantize(xh[rows], sc, zp))
+    np.testing.assert_array_equal(qc.cpu().numpy(), oracle.sq_quantize(qf.cpu().numpy(), sc, zp))
+    del xh
+    assert xch.min() == -128 and xch.max() >= 126
+    gi, gd = sq.searchTopK(qc, xc, k)
+    note("configs[2] searched")
+    assert np.all(np.diff(gd, axis=1) >= 0)
+    sub = np.array([0, 1, 2047, 4095])
+    oi, od = oracle.i8_topk(qc.cpu().numpy()[sub], xch, k)
+    check_topk_exact(gi[sub], gd[sub], oi, od)
+
+
+def test_configs3_binary_top100_full(ctx, oracle):
+    """50,000,000 x 768-bit codes, Q=256, top-100 with ties to the lower id, bit-exact."""
+    import torch
+    from vectoraccelerate_amd import BinaryQuantizationKernel, HammingDistanceKernel
+
+    N, W, Q, k = 50_000_000, 24, 256, 100
+    # pack path at scale: sign bits of N(0,1) floats for the first 1M rows, checked bit-exactly
+    g = torch.Generator(device="cuda").manual_seed(3)
+    xf = torch.randn(1_000_000, 768, device="cuda", generator=g)
+    packed = BinaryQuantizationKernel(ctx).pack(xf)
+    np.testing.assert_array_equal(packed.cpu().numpy().view(np.uint32), oracle.bq_pack(xf.cpu().numpy()))
+    del xf
+    x = torch.empty(N, W, device="cuda", dtype=torch.int32)
+    x[:1_000_000] = packed
+    x[1_000_000:] = torch.randint(-2**31, 2**31 - 1, (N - 1_000_000, W), device="cuda", generator=g,
+                                  dtype=torch.int32)
+    q = torch.randint(-2**31, 2**31 - 1, (Q, W), device="cuda", generator=g, dtype=torch.int32)
+    q[:4] = x[torch.tensor([5, 123456, 30_000_000, N - 1], device="cuda")]  # exact matches
+    gi, gd = HammingDistanceKernel(ctx).nearestNeighbors(q, x, k)
+    note("configs[3] searched")
+    np.testing.assert_array_equal(gi[:4, 0], [5, 123456, 30_000_000, N - 1])
+    assert np.all(gd[:4, 0] == 0)
+    assert np.all(np.diff(gd.astype(np.int64), axis=1) >= 0)
+    sub = np.array([0, 3, 100, 255])
+    xh = x.cpu().numpy().view(np.uint32)
+    oi, od = oracle.hamming_topk(q.cpu().numpy().view(np.uint32)[sub], xh, k)
+    check_topk_exact(gi[sub], gd[sub], oi, od)
+
+
+def test_configs4_ivf_top10_full(ctx, oracle):
+    """4096 centroids N(0,4^2), 4,000,000 points with Zipf(1.1) cluster sizes, Q=1024, nprobe 32."""
+    import torch
+    from tests.test_gpu_ivf import _assignment_matches
+    from vectoraccelerate_amd import IVFSearchConfiguration, IVFSearchPipeline
+
+    C, D, N, Q, nprobe, k = 4096, 768, 4_000_000, 1024, 32, 10
+    g = torch.Generator(device="cuda").manual_seed(4)
+    cen = torch.randn(C, D, device="cuda", generator=g) * 4.0
+    p = 1.0 / torch.arange(1, C + 1, device="cuda", dtype=torch.float64) ** 1.1
+    p = (p / p.sum()).float()
+    x = cen[torch.multinomial(p, N, replacement=True, generator=g)] + torch.randn(N, D, device="cuda", generator=g)
+    q = (cen[torch.multinomial(p, Q, replacement=True, generator=g)]
+         + torch.randn(Q, D, device="cuda", generator=g)).contiguous()
+    pipe = IVFSearchPipeline(ctx, IVFSearchConfiguration(C, nprobe, D))
+    st = pipe.prepareIndexStructure(cen, x)
+    off, ids = st.lists()
+    note("configs[4] built")
+    assert off[-1] == N and np.all(np.diff(off.astype(np.int64)) >= 0)
+    assert np.array_equal(np.sort(ids), np.arange(N, dtype=np.uint32))
+    # assignment of a row sample against the oracle (near-ties allowed)
+    xh = x.cpu().numpy()
+    ch = cen.cpu().numpy()
+    lists = np.empty(N, np.int64)
+    for l in range(C):
+        lists[ids[off[l]:off[l + 1]]] = l
+    rows = np.random.default_rng(0).choice(N, 20000, replace=False)
+    _assignment_matches(oracle, xh[rows], ch, lists[rows])
+    probes = pipe.findNearestCentroids(q, st).cpu().numpy().view(np.uint32)
+    res = pipe.search(q, st, k)
+    gi = res.indices.cpu().numpy().view(np.uint32)
+    gd = res.distances.cpu().numpy()
+    note("configs[4] searched")
+    assert np.all(np.diff(gd, axis=1) >= 0)
+    qh = q.cpu().numpy()
+    sub = np.arange(0, Q, 64)
+    op = oracle.ivf_probe(qh[sub], ch, nprobe)
+    check_topk(L2SQ, qh[sub], ch, nprobe, probes[sub], None, op, None)
+    oi, od = oracle.ivf_scan(qh[sub], xh, off, ids, probes[sub], k)
+    check_topk(L2SQ, qh[sub], xh, k, gi[sub], gd[sub], oi, od)
+    st.close()
