@@ -20,6 +20,13 @@ from .kernels import (
     TopKMergeKernel,
     TopKSelectionKernel,
 )
+from .index import (
+    AcceleratedVectorIndex,
+    IndexConfiguration,
+    IndexSearchResult,
+    SearchResults,
+    VectorHandle,
+)
 from .ivf import IVFGPUIndexStructure, IVFSearchConfiguration, IVFSearchPipeline, IVFSearchResult
 from .quantization import (
     BinaryQuantizationKernel,
@@ -34,6 +41,11 @@ from .quantization import (
 )
 
 __all__ = [
+    "AcceleratedVectorIndex",
+    "IndexConfiguration",
+    "IndexSearchResult",
+    "SearchResults",
+    "VectorHandle",
     "IVFGPUIndexStructure",
     "IVFSearchConfiguration",
     "IVFSearchPipeline",
