@@ -90,7 +90,11 @@ def test_global_quantize_roundtrip(ctx):
 
 
 @pytest.mark.parametrize("Q,N,D,k", [(1, 50, 16, 5), (40, 3000, 512, 10), (130, 20000, 64, 100), (9, 40000, 100, 7),
-                                     (300, 5000, 48, 1)])
+                                     (300, 5000, 48, 1),
+                                     # large-Q tiles (256 queries x 128 rows): ragged Q and N,
+                                     # several 64-byte stages, a partial last stage, one-stage D
+                                     (257, 3001, 512, 10), (450, 20000, 160, 50), (1000, 7000, 1024, 5),
+                                     (513, 129, 16, 3)])
 def test_i8_scan_topk_bit_exact(ctx, oracle, Q, N, D, k):
     from vectoraccelerate_amd import ScalarQuantizationKernel
 
@@ -119,6 +123,29 @@ def test_i8_sampled_and_overflow_paths(ctx, oracle):
             ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 0)
             ctx.set_option(_lib.VA_OPT_SAMPLE_ROWS, 0)
         check_topk_exact(gi, gd, oi, od)
+
+
+def test_i8_large_q_overflow_rescan(ctx, oracle):
+    """Large-Q tiles on the overflow path: a tiny candidate cap sends most queries to the
+    exact rescan, which runs them compacted through the query-row indirection."""
+    from vectoraccelerate_amd import ScalarQuantizationKernel, _lib
+
+    g = rng(22)
+    qc = g.integers(-128, 128, (600, 128)).astype(np.int8)
+    xc = g.integers(-128, 128, (40000, 128)).astype(np.int8)
+    qc[5] = xc[17]
+    oi, od = oracle.i8_topk(qc, xc, 20)
+    try:
+        ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 24)
+        ctx.set_option(_lib.VA_OPT_SAMPLE_ROWS, 3000)
+        gi, gd = ScalarQuantizationKernel(ctx).searchTopK(qc, xc, 20)
+        t = ctx.last_scan_timings()
+    finally:
+        ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 0)
+        ctx.set_option(_lib.VA_OPT_SAMPLE_ROWS, 0)
+    check_topk_exact(gi, gd, oi, od)
+    assert gi[5, 0] == 17
+    assert t["overflow_rows"] > 192  # the rescan itself ran on large-Q tiles
 
 
 def test_c3_pipeline_small(ctx, oracle):

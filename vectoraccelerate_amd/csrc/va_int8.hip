@@ -318,6 +318,236 @@ va_status launch_i8_tile(va_context* ctx, const I8Args& a) {
     return VA_OK;
 }
 
+// ---------------------------------------------------------------------------------------
+// int8 scan with an LDS-DMA pipeline (large Q)
+// ---------------------------------------------------------------------------------------
+// Workgroup tile 256 queries x 128 rows; four waves as 2 x 2, wave tile 128 queries x 64 rows
+// (4 x 2 MFMA blocks, 128 accumulators).  Stages of 64 bytes per row move global -> LDS by
+// direct buffer loads (no register staging) into a ring of three slots, issued two stages
+// ahead of the MFMAs that read them.  Rows and columns outside the tile load from an offset
+// past the descriptor and land as zeros.  LDS rows are 64 bytes, unpadded: 16-byte chunk c of
+// row r sits at chunk c ^ swz(r), spreading the 32 rows of a fragment read over the banks.
+// 256 x 128 halves the L2-to-CU bytes per MFMA op of a 128 x 128 tile; 78 KiB of LDS (ring +
+// candidate staging) leaves room for two workgroups per CU.
+//
+// At d = 512 a tile is only 16 MFMA k-steps deep, so the epilogue must cost far less than the
+// MFMAs: the filter epilogue rejects with a per-lane max, tests surviving positions with one
+// wave-wide compare each, and stages passes in LDS (see below).
+namespace dmai8 {
+constexpr int TQ = 256, TN = 128, ROWS = TQ + TN, SKB = 64, NS = 3;
+constexpr int STAGE = ROWS * SKB;                  // 24 KiB per ring slot
+constexpr int RING = NS * STAGE;                   // 72 KiB
+// candidate staging: 512 (query, key, id) entries + a counter
+constexpr int STAGED = 512;
+constexpr size_t LDS_BYTES = size_t(RING) + 3 * 4 * STAGED + 16;
+constexpr int GPW = ROWS / 16 / 4;                 // 16-row DMA groups per wave and stage (6)
+constexpr int QGPW = TQ / 16 / 4;                  // of which query groups (4)
+__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+}  // namespace dmai8
+
+template <bool FILTER>
+__global__ __launch_bounds__(256, 2) void i8_dma_kernel(I8Args a) {
+    using namespace dmai8;
+    extern __shared__ __attribute__((aligned(16))) char lds8[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wq = wave & 1, wn = wave >> 1;
+    const int l32 = lane & 31, hh = lane >> 5;
+
+    // XCD-aware order, as in i8_scan_kernel
+    const uint32_t nqb = (a.Q + TQ - 1) / TQ;
+    const uint32_t xcd = blockIdx.x % kXcds, seq = blockIdx.x / kXcds;
+    const uint32_t qb = seq % nqb;
+    const uint32_t tb = (seq / nqb) * kXcds + xcd;
+    const uint32_t q0 = qb * TQ;
+    const uint32_t n0 = tb * TN;
+    if (n0 >= a.N) return;  // padding workgroup
+    const uint32_t rc = min(uint32_t(TN), a.N - n0);
+
+    const dma_rsrc qres = make_dma_rsrc(a.q, uint32_t(int64_t(a.Q - 1) * a.ldq + a.D));
+    const dma_rsrc xres = make_dma_rsrc(a.x + int64_t(n0) * a.ldx, uint32_t(int64_t(rc - 1) * a.ldx + a.D));
+
+    // This lane's source offset and 16-byte column in each of the wave's DMA groups.
+    uint32_t base[GPW], colb[GPW];
+#pragma unroll
+    for (int i = 0; i < GPW; ++i) {
+        const int row = 16 * (wave + 4 * i) + (lane >> 2);
+        const int col = 16 * ((lane & 3) ^ swz(row));
+        colb[i] = uint32_t(col);
+        if (i < QGPW) {
+            const uint32_t qi = q0 + uint32_t(row);
+            base[i] = qi < a.Q ? uint32_t(int64_t(qi) * a.ldq) + col : kDmaSkip;
+        } else {
+            const uint32_t jr = uint32_t(row - TQ);
+            base[i] = jr < rc ? uint32_t(int64_t(jr) * a.ldx) + col : kDmaSkip;
+        }
+    }
+    const uint32_t lds0 = lds_addr_of(lds8);
+    auto issue = [&](uint32_t stage, uint32_t slot) {
+        const uint32_t d0 = stage * SKB;
+#pragma unroll
+        for (int i = 0; i < GPW; ++i) {
+            const uint32_t voff = (base[i] != kDmaSkip && d0 + colb[i] < a.D) ? base[i] + d0 : kDmaSkip;
+            const uint32_t dst = lds0 + slot * STAGE + uint32_t(wave + 4 * i) * 1024u;
+            lds_dma16(i < QGPW ? qres : xres, voff, dst);
+        }
+    };
+
+    i32x16 acc[4][2];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[u][b][v] = 0;
+
+    // fragment rows: bases are multiples of 32, so every fragment row has swz(row) == swz(l32)
+    const int sw = swz(l32);
+    const int qfrag = (wq * 128 + l32) * SKB;
+    const int xfrag = (TQ + wn * 64 + l32) * SKB;
+    int koff[SKB / 32];
+#pragma unroll
+    for (int g = 0; g < SKB / 32; ++g) koff[g] = ((2 * g + hh) ^ sw) * 16;
+
+    const uint32_t nst = (a.D + SKB - 1) / SKB;
+    issue(0, 0);
+    if (nst > 1) issue(1, 1);
+    uint32_t slot = 0;
+    for (uint32_t s = 0; s < nst; ++s) {
+        if (s + 1 < nst) wait_vmcnt<GPW>();
+        else wait_vmcnt<0>();
+        __syncthreads();  // stage s visible; every wave is past the reads of slot (s + 2) % 3
+        if (s + 2 < nst) issue(s + 2, slot == 0 ? 2u : slot - 1);
+        const char* st = lds8 + slot * STAGE;
+#pragma unroll
+        for (int g = 0; g < SKB / 32; ++g) {
+            i32x4v bq[4], ax[2];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) bq[u] = *reinterpret_cast<const i32x4v*>(st + qfrag + u * 32 * SKB + koff[g]);
+#pragma unroll
+            for (int b = 0; b < 2; ++b) ax[b] = *reinterpret_cast<const i32x4v*>(st + xfrag + b * 32 * SKB + koff[g]);
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    acc[u][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ax[b], bq[u], acc[u][b], 0, 0, 0);
+        }
+        slot = slot == 2 ? 0u : slot + 1;
+    }
+
+    const uint32_t nbase = n0 + uint32_t(wn * 64);
+    // rows of this lane's values that exist: offsets 32b + 8j + e (+4hh) below lim
+    const int64_t lim = int64_t(a.N) - int64_t(nbase) - 4 * hh;
+    if (FILTER) {
+        // A value passes when its dot is >= the query's bound (the threshold key turned back
+        // into an int32 dot).  A lane's 32 values of a query are reduced with max first, so a
+        // wave skips a query column when no lane passes; otherwise each value position is
+        // tested with one wave-wide compare and, where some lane passes, the wave appends its
+        // passes to the workgroup's LDS staging list with one LDS atomic.  After a barrier the
+        // list is flushed with one global reservation per entry, all in flight at once.
+        uint32_t* s_qi = reinterpret_cast<uint32_t*>(lds8 + RING);
+        uint32_t* s_key = s_qi + STAGED;
+        uint32_t* s_id = s_key + STAGED;
+        uint32_t* s_cnt = s_id + STAGED;
+        __syncthreads();  // every wave is done with the ring before the staging area is used
+        if (tid == 0) *s_cnt = 0;
+        if (nbase + 64 > a.N) {  // last tile: rows past N never pass
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+                        if (int64_t(b * 32 + 8 * (v >> 2) + (v & 3)) >= lim) acc[u][b][v] = INT32_MIN;
+        }
+        int32_t bound[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t qi = q0 + uint32_t(wq * 128 + u * 32 + l32);
+            const int32_t t = i32_of_key(a.thr[qi < a.Q ? qi : 0u]);  // pass iff -dot <= t
+            bound[u] = (qi >= a.Q || t == INT32_MIN) ? INT32_MAX : -t;
+        }
+        __syncthreads();  // counter cleared
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            int32_t m = acc[u][0][0];
+#pragma unroll
+            for (int w = 1; w < 32; ++w) m = max(m, acc[u][w >> 4][w & 15]);
+            if (!__ballot(m >= bound[u])) continue;  // no lane of the wave passes
+            const uint32_t qloc = uint32_t(wq * 128 + u * 32 + l32);
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const bool p = acc[u][b][v] >= bound[u];
+                    const uint64_t mk = __ballot(p);  // lanes passing at this position
+                    if (!mk) continue;
+                    const uint32_t first = uint32_t(__builtin_ctzll(mk));
+                    uint32_t base0 = 0;
+                    if (uint32_t(lane) == first) base0 = atomicAdd(s_cnt, uint32_t(__popcll(mk)));
+                    base0 = __builtin_amdgcn_readlane(base0, first);
+                    if (!p) continue;
+                    const uint32_t e =
+                        base0 + __builtin_amdgcn_mbcnt_hi(uint32_t(mk >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mk), 0u));
+                    const uint32_t key = key_of_i32(-acc[u][b][v]);
+                    const uint32_t id = nbase + uint32_t(b * 32 + 8 * (v >> 2) + 4 * hh + (v & 3));
+                    if (e < uint32_t(STAGED)) {
+                        s_qi[e] = qloc;
+                        s_key[e] = key;
+                        s_id[e] = id;
+                    } else {  // staging full: reserve and write directly
+                        const uint32_t qi = q0 + qloc;
+                        const uint32_t pos = atomicAdd(a.cnt + qi, 1u);
+                        if (pos < a.cap) {
+                            a.cand_key[int64_t(qi) * a.cap + pos] = key;
+                            a.cand_id[int64_t(qi) * a.cap + pos] = id;
+                        }
+                    }
+                }
+        }
+        __syncthreads();  // staged entries visible
+        const uint32_t n = min(*s_cnt, uint32_t(STAGED));
+        for (uint32_t e = uint32_t(tid); e < n; e += 256) {
+            const uint32_t qi = q0 + s_qi[e];
+            const uint32_t pos = atomicAdd(a.cnt + qi, 1u);
+            if (pos < a.cap) {
+                a.cand_key[int64_t(qi) * a.cap + pos] = s_key[e];
+                a.cand_id[int64_t(qi) * a.cap + pos] = s_id[e];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t qi = q0 + uint32_t(wq * 128 + u * 32 + l32);
+            if (qi >= a.Q) continue;
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t m = nbase + uint32_t(b * 32 + 8 * j + 4 * hh);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (m + e < a.N) a.out_k[int64_t(qi) * a.ldo + m + e] = key_of_i32(-acc[u][b][4 * j + e]);
+                }
+        }
+    }
+}
+
+template <bool FILTER>
+va_status launch_i8_dma(va_context* ctx, const I8Args& a) {
+    using namespace dmai8;
+    const uint64_t ntb = (a.N + TN - 1) / TN;
+    const uint64_t grid = uint64_t((a.Q + TQ - 1) / TQ) * ((ntb + kXcds - 1) / kXcds) * kXcds;
+    if (grid > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "int8 scan grid too large");
+    auto kern = &i8_dma_kernel<FILTER>;
+    VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, int(LDS_BYTES)));
+    kern<<<dim3(uint32_t(grid)), dim3(256), LDS_BYTES, ctx->stream>>>(a);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
 template <int QBW, int WQ, int WN>
 va_status launch_i8_shape(va_context* ctx, const I8Args& a, bool vec, bool filter) {
     if (filter) return vec ? launch_i8_tile<QBW, WQ, WN, true, true>(ctx, a) : launch_i8_tile<QBW, WQ, WN, false, true>(ctx, a);
@@ -328,6 +558,15 @@ va_status launch_i8(va_context* ctx, const I8Args& a, bool filter) {
     if (a.Q == 0 || a.N == 0) return VA_OK;
     const bool vec = (a.D % 16 == 0) && (a.ldq % 16 == 0) && (a.ldx % 16 == 0) &&
                      ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
+#ifndef VA_I8_DMA
+#define VA_I8_DMA 1
+#endif
+    // The DMA pipeline needs whole 16-byte chunks, dense query rows (no indirection) and
+    // descriptor offsets below 2^31.
+    const bool dma_ok = VA_I8_DMA && vec && !a.qrow && a.Q > 192 && a.D <= 131071 &&
+                        uint64_t(a.Q - 1) * uint64_t(a.ldq) + a.D <= kDmaMaxBytes &&
+                        uint64_t(dmai8::TN - 1) * uint64_t(a.ldx) + a.D <= kDmaMaxBytes;
+    if (dma_ok) return filter ? launch_i8_dma<true>(ctx, a) : launch_i8_dma<false>(ctx, a);
     if (a.Q <= 32) return launch_i8_shape<1, 1, 4>(ctx, a, vec, filter);
     if (a.Q <= 64) return launch_i8_shape<1, 2, 2>(ctx, a, vec, filter);
 // Large-Q shape: 0 = 128 x 128 (4 waves), 1 = 128 x 256 (4 waves), 2 = 256 x 256 (8 waves).

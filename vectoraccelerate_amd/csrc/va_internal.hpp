@@ -128,6 +128,52 @@ __host__ __device__ inline int32_t i32_of_key(uint32_t k) { return int32_t(k ^ 0
 
 inline uint32_t ceil_div(uint64_t a, uint64_t b) { return uint32_t((a + b - 1) / b); }
 
+// ---------------------------------------------------------------------------
+// Global -> LDS direct loads (CDNA buffer loads with the lds modifier)
+// ---------------------------------------------------------------------------
+// A buffer resource covers [base, base + bytes); a load whose offset is at or past `bytes`
+// reads nothing and returns zeros, which is how out-of-tile rows and columns are padded.
+// Offsets are kept below 2^31 so kDmaSkip is always out of range.
+typedef int dma_rsrc __attribute__((ext_vector_type(4)));
+constexpr uint32_t kDmaSkip = 0x80000000u;
+constexpr uint32_t kDmaMaxBytes = 0x7FFFFFF0u;
+
+__device__ __forceinline__ dma_rsrc make_dma_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t p = reinterpret_cast<uint64_t>(base);
+    dma_rsrc r;
+    r[0] = __builtin_amdgcn_readfirstlane(int(uint32_t(p)));
+    r[1] = __builtin_amdgcn_readfirstlane(int(uint32_t(p >> 32) & 0xFFFFu));  // stride 0
+    r[2] = __builtin_amdgcn_readfirstlane(int(bytes));                        // num_records
+    r[3] = 0x00020000;                                                         // gfx9 data format
+    return r;
+}
+
+// One wave-wide 16-byte-per-lane load into LDS: lane i's bytes land at lds_addr + 16*i, so a
+// wave fills 1 KiB of contiguous LDS per call.  lds_addr must be wave-uniform.  The load is
+// invisible to the compiler's wait-count tracking: callers wait with wait_vmcnt<> themselves
+// before a barrier that publishes the data.  M0 is set here and nowhere else in the kernels
+// that use this (the compiler keeps nothing in M0 on gfx9 across these loops); M0 is a
+// reserved register, whose clobbers the compiler does not honour, so it is not listed.
+__device__ __forceinline__ void lds_dma16(const dma_rsrc& rsrc, uint32_t voff, uint32_t lds_addr) {
+    // one wait state between the M0 write and the LDS-DMA load that reads it
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_addr), "v"(voff), "s"(rsrc)
+                 : "memory");
+}
+
+// s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding: vmcnt in bits 3:0 and 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// LDS byte address of a pointer into __shared__ memory (low half of the flat address).
+__device__ __forceinline__ uint32_t lds_addr_of(const void* p) {
+    return uint32_t(reinterpret_cast<uintptr_t>(p));
+}
+
 }  // namespace va
 
 // ---------------------------------------------------------------------------
