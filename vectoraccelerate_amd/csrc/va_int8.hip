@@ -326,7 +326,9 @@ va_status launch_i8_tile(va_context* ctx, const I8Args& a) {
 // direct buffer loads (no register staging) into a ring of three slots, issued two stages
 // ahead of the MFMAs that read them.  Rows and columns outside the tile load from an offset
 // past the descriptor and land as zeros.  LDS rows are 64 bytes, unpadded: 16-byte chunk c of
-// row r sits at chunk c ^ swz(r), spreading the 32 rows of a fragment read over the banks.
+// row r sits at chunk c ^ swz(r).  ds_read_b128 serves 16 lanes per clock from 64 banks, so the
+// 16 rows read together must cover 16 distinct 16-byte bank groups: rows r..r+3 already do
+// (64-byte stride), and swz = (r >> 2) & 3 shifts each following group of four by one chunk.
 // 256 x 128 halves the L2-to-CU bytes per MFMA op of a 128 x 128 tile; 78 KiB of LDS (ring +
 // candidate staging) leaves room for two workgroups per CU.
 //
@@ -342,7 +344,7 @@ constexpr int STAGED = 512;
 constexpr size_t LDS_BYTES = size_t(RING) + 3 * 4 * STAGED + 16;
 constexpr int GPW = ROWS / 16 / 4;                 // 16-row DMA groups per wave and stage (6)
 constexpr int QGPW = TQ / 16 / 4;                  // of which query groups (4)
-__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
 }  // namespace dmai8
 
 template <bool FILTER>
