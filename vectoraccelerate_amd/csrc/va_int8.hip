@@ -339,7 +339,7 @@ namespace dmai8 {
 constexpr int TQ = 256, TN = 128, ROWS = TQ + TN, SKB = 64, NS = 3;
 constexpr int STAGE = ROWS * SKB;                  // 24 KiB per ring slot
 constexpr int RING = NS * STAGE;                   // 72 KiB
-// candidate staging: 512 (query, key, id) entries + a counter
+// candidate staging: 512 (query, key, id) entries, a 128-entry slice per wave, + 4 counts
 constexpr int STAGED = 512;
 constexpr size_t LDS_BYTES = size_t(RING) + 3 * 4 * STAGED + 16;
 constexpr int GPW = ROWS / 16 / 4;                 // 16-row DMA groups per wave and stage (6)
@@ -412,6 +412,16 @@ __global__ __launch_bounds__(256, 2) void i8_dma_kernel(I8Args a) {
 #pragma unroll
     for (int g = 0; g < SKB / 32; ++g) koff[g] = ((2 * g + hh) ^ sw) * 16;
 
+    // The filter's thresholds load before the stream starts, so their latency hides behind
+    // the MFMA loop instead of stalling the epilogue.
+    uint32_t thr0[4] = {0u, 0u, 0u, 0u};
+    if (FILTER) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t qi = q0 + uint32_t(wq * 128 + u * 32 + l32);
+            thr0[u] = a.thr[qi < a.Q ? qi : 0u];
+        }
+    }
     const uint32_t nst = (a.D + SKB - 1) / SKB;
     issue(0, 0);
     if (nst > 1) issue(1, 1);
@@ -445,15 +455,18 @@ __global__ __launch_bounds__(256, 2) void i8_dma_kernel(I8Args a) {
         // A value passes when its dot is >= the query's bound (the threshold key turned back
         // into an int32 dot).  A lane's 32 values of a query are reduced with max first, so a
         // wave skips a query column when no lane passes; otherwise each value position is
-        // tested with one wave-wide compare and, where some lane passes, the wave appends its
-        // passes to the workgroup's LDS staging list with one LDS atomic.  After a barrier the
-        // list is flushed with one global reservation per entry, all in flight at once.
+        // tested with one wave-wide compare, and where some lane passes the wave appends its
+        // passes to its own slice of the LDS staging list.  Slots come from a wave-uniform
+        // running count plus the lane's rank in the compare mask: no atomics (an LDS atomic
+        // round trip per appending position cost as much as a third of the kernel).  After a
+        // barrier the four slices are flushed with one global reservation per entry, all in
+        // flight at once.
         uint32_t* s_qi = reinterpret_cast<uint32_t*>(lds8 + RING);
         uint32_t* s_key = s_qi + STAGED;
         uint32_t* s_id = s_key + STAGED;
-        uint32_t* s_cnt = s_id + STAGED;
-        __syncthreads();  // every wave is done with the ring before the staging area is used
-        if (tid == 0) *s_cnt = 0;
+        uint32_t* s_cnt = s_id + STAGED;  // per-wave entry counts
+        constexpr uint32_t WCAP = STAGED / 4;
+        const uint32_t wbase = uint32_t(wave) * WCAP;
         if (nbase + 64 > a.N) {  // last tile: rows past N never pass
 #pragma unroll
             for (int u = 0; u < 4; ++u)
@@ -467,50 +480,61 @@ __global__ __launch_bounds__(256, 2) void i8_dma_kernel(I8Args a) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const uint32_t qi = q0 + uint32_t(wq * 128 + u * 32 + l32);
-            const int32_t t = i32_of_key(a.thr[qi < a.Q ? qi : 0u]);  // pass iff -dot <= t
+            const int32_t t = i32_of_key(thr0[u]);  // pass iff -dot <= t
             bound[u] = (qi >= a.Q || t == INT32_MIN) ? INT32_MAX : -t;
         }
-        __syncthreads();  // counter cleared
+        __syncthreads();  // every wave is done with the ring before the staging area is used
+        uint32_t wc = 0;  // entries this wave has staged (wave-uniform)
+        // Branches are the cost here (a wave-uniform branch per value position took as long as
+        // the MFMAs), so the test is hierarchical: the maximum of a lane's 32 values, then of
+        // each group of 8, and only then single positions.
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            int32_t m = acc[u][0][0];
+            int32_t m8[4];
 #pragma unroll
-            for (int w = 1; w < 32; ++w) m = max(m, acc[u][w >> 4][w & 15]);
+            for (int g = 0; g < 4; ++g) {
+                m8[g] = acc[u][(8 * g) >> 4][(8 * g) & 15];
+#pragma unroll
+                for (int w = 8 * g + 1; w < 8 * g + 8; ++w) m8[g] = max(m8[g], acc[u][w >> 4][w & 15]);
+            }
+            const int32_t m = max(max(m8[0], m8[1]), max(m8[2], m8[3]));
             if (!__ballot(m >= bound[u])) continue;  // no lane of the wave passes
             const uint32_t qloc = uint32_t(wq * 128 + u * 32 + l32);
 #pragma unroll
-            for (int b = 0; b < 2; ++b)
+            for (int g = 0; g < 4; ++g) {
+                if (!__ballot(m8[g] >= bound[u])) continue;
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
+                for (int w = 8 * g; w < 8 * g + 8; ++w) {
+                    const int b = w >> 4, v = w & 15;
                     const bool p = acc[u][b][v] >= bound[u];
                     const uint64_t mk = __ballot(p);  // lanes passing at this position
                     if (!mk) continue;
-                    const uint32_t first = uint32_t(__builtin_ctzll(mk));
-                    uint32_t base0 = 0;
-                    if (uint32_t(lane) == first) base0 = atomicAdd(s_cnt, uint32_t(__popcll(mk)));
-                    base0 = __builtin_amdgcn_readlane(base0, first);
-                    if (!p) continue;
-                    const uint32_t e =
-                        base0 + __builtin_amdgcn_mbcnt_hi(uint32_t(mk >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mk), 0u));
-                    const uint32_t key = key_of_i32(-acc[u][b][v]);
-                    const uint32_t id = nbase + uint32_t(b * 32 + 8 * (v >> 2) + 4 * hh + (v & 3));
-                    if (e < uint32_t(STAGED)) {
-                        s_qi[e] = qloc;
-                        s_key[e] = key;
-                        s_id[e] = id;
-                    } else {  // staging full: reserve and write directly
-                        const uint32_t qi = q0 + qloc;
-                        const uint32_t pos = atomicAdd(a.cnt + qi, 1u);
-                        if (pos < a.cap) {
-                            a.cand_key[int64_t(qi) * a.cap + pos] = key;
-                            a.cand_id[int64_t(qi) * a.cap + pos] = id;
+                    if (p) {
+                        const uint32_t e =
+                            wc + __builtin_amdgcn_mbcnt_hi(uint32_t(mk >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mk), 0u));
+                        const uint32_t key = key_of_i32(-acc[u][b][v]);
+                        const uint32_t id = nbase + uint32_t(b * 32 + 8 * (v >> 2) + 4 * hh + (v & 3));
+                        if (e < WCAP) {
+                            s_qi[wbase + e] = qloc;
+                            s_key[wbase + e] = key;
+                            s_id[wbase + e] = id;
+                        } else {  // slice full: reserve and write directly
+                            const uint32_t qi = q0 + qloc;
+                            const uint32_t pos = atomicAdd(a.cnt + qi, 1u);
+                            if (pos < a.cap) {
+                                a.cand_key[int64_t(qi) * a.cap + pos] = key;
+                                a.cand_id[int64_t(qi) * a.cap + pos] = id;
+                            }
                         }
                     }
+                    wc += uint32_t(__popcll(mk));
                 }
+            }
         }
-        __syncthreads();  // staged entries visible
-        const uint32_t n = min(*s_cnt, uint32_t(STAGED));
-        for (uint32_t e = uint32_t(tid); e < n; e += 256) {
+        if (lane == 0) s_cnt[wave] = min(wc, WCAP);
+        __syncthreads();  // staged entries and counts visible
+        for (uint32_t e = uint32_t(tid); e < uint32_t(STAGED); e += 256) {
+            if (e % WCAP >= s_cnt[e / WCAP]) continue;
             const uint32_t qi = q0 + s_qi[e];
             const uint32_t pos = atomicAdd(a.cnt + qi, 1u);
             if (pos < a.cap) {
