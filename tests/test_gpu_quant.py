@@ -24,7 +24,8 @@ def c3_like(n, d, seed):
 # ---------------------------------------------------------------------------------------
 # scalar int8
 # ---------------------------------------------------------------------------------------
-@pytest.mark.parametrize("N,D", [(1, 1), (7, 3), (1000, 512), (3001, 100), (20000, 64)])
+@pytest.mark.parametrize("N,D", [(1, 1), (7, 3), (1000, 512), (3001, 100), (20000, 64), (513, 1024), (300, 1028),
+                                 (40001, 8)])
 def test_sq_params_and_codes_bit_exact(ctx, oracle, N, D):
     from vectoraccelerate_amd import ScalarQuantizationKernel
 
@@ -58,6 +59,28 @@ def test_sq_golden_and_edge_values(ctx, oracle):
     got = k.quantizePerDimension(v, p).cpu().numpy()
     np.testing.assert_array_equal(got, oracle.sq_quantize(v, sc, zp))
     np.testing.assert_array_equal(got, [[0, 2, 2, 0, -2, 127, -128, 0, 127]])
+
+
+def test_sq_params_with_nan_and_signed_zero(ctx, oracle):
+    """NaN never wins a min/max comparison (a column of only NaN gets min = max = 0), and -0/+0
+    compare equal; checked on the vectorised (D % 4 == 0) and the scalar paths."""
+    from vectoraccelerate_amd import ScalarQuantizationKernel
+
+    g = rng(23)
+    for d in (16, 7):
+        x = g.standard_normal((2000, d)).astype(np.float32)
+        x[g.random(x.shape) < 0.01] = np.nan
+        x[:, 1] = np.nan
+        x[:, 2] = -0.0
+        x[5, 2] = 0.0
+        k = ScalarQuantizationKernel(ctx)
+        p = k.computePerDimensionParameters(x)
+        mn, mx, sc, zp = oracle.sq_params_per_dim(x)
+        np.testing.assert_array_equal(p.min, mn)
+        np.testing.assert_array_equal(p.max, mx)
+        np.testing.assert_array_equal(p.scale, sc)
+        np.testing.assert_array_equal(p.zeroPoint, zp)
+        np.testing.assert_array_equal(k.quantizePerDimension(x, p).cpu().numpy(), oracle.sq_quantize(x, sc, zp))
 
 
 def test_sq_constant_columns(ctx, oracle):

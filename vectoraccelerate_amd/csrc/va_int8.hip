@@ -47,6 +47,62 @@ __global__ __launch_bounds__(256) void minmax_kernel(const float* __restrict__ x
     }
 }
 
+// D % 4 == 0 and 16-byte aligned rows: each thread owns 4 dimensions (one float4 column) of
+// a row slab; a block covers 256 / (D/4) rows per step and strides over the rows, keeping
+// four independent loads in flight per thread; partial min/max meet in LDS, then one atomic
+// per dimension and block.  HBM-bound: every byte of x is read once.
+__global__ __launch_bounds__(256) void minmax_kernel_v4(const float4* __restrict__ x, uint64_t N, uint32_t D4,
+                                                        uint32_t* kmin, uint32_t* kmax) {
+    __shared__ uint32_t smin[1024], smax[1024];
+    const uint32_t t = threadIdx.x;
+    const uint32_t rpb = 256 / D4;  // rows per block step (D4 <= 256)
+    const uint32_t c = t % D4, r0 = t / D4;
+    const bool active = r0 < rpb;
+    uint32_t lo[4] = {0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu}, hi[4] = {0u, 0u, 0u, 0u};
+    auto take = [&](const float4 v) {
+        const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (e[i] != e[i]) continue;  // NaN never wins a comparison (the CPU rule)
+            const uint32_t k = key_of_float(e[i]);
+            lo[i] = k < lo[i] ? k : lo[i];
+            hi[i] = k > hi[i] ? k : hi[i];
+        }
+    };
+    if (active) {
+        const uint64_t step = uint64_t(gridDim.x) * rpb;
+        uint64_t r = uint64_t(blockIdx.x) * rpb + r0;
+        for (; r + 3 * step < N; r += 4 * step) {
+            const float4 a = x[r * D4 + c], b = x[(r + step) * D4 + c];
+            const float4 cc = x[(r + 2 * step) * D4 + c], d = x[(r + 3 * step) * D4 + c];
+            take(a);
+            take(b);
+            take(cc);
+            take(d);
+        }
+        for (; r < N; r += step) take(x[r * D4 + c]);
+    }
+    // reduce the rpb partials of each column in LDS
+    for (uint32_t i = t; i < 4 * D4; i += 256) {
+        smin[i] = 0xFFFFFFFFu;
+        smax[i] = 0u;
+    }
+    __syncthreads();
+    if (active) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            atomicMin(smin + 4 * c + i, lo[i]);
+            atomicMax(smax + 4 * c + i, hi[i]);
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = t; i < 4 * D4; i += 256) {
+        if (smin[i] == 0xFFFFFFFFu) continue;  // only NaN (or nothing) seen in this column
+        atomicMin(kmin + i, smin[i]);
+        atomicMax(kmax + i, smax[i]);
+    }
+}
+
 __global__ void params_finalize(const uint32_t* kmin, const uint32_t* kmax, uint32_t D, float* mn, float* mx,
                                 float* scale, int32_t* zp) {
     const uint32_t d = blockIdx.x * blockDim.x + threadIdx.x;
@@ -89,23 +145,37 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
     }
 }
 
-// D % 4 == 0 and 16-byte aligned rows: float4 in, char4 out
+// D % 4 == 0 and 16-byte aligned rows: float4 in, char4 out.  Each thread owns one float4
+// column of a row slab (256 / (D/4) rows per block step, D <= 1024), so the column's scale and
+// zero point stay in registers and four rows are in flight per thread.
 __global__ __launch_bounds__(256) void quantize_kernel_v4(const float4* __restrict__ x, uint64_t N, uint32_t D4,
                                                           const float4* __restrict__ scale,
                                                           const int4* __restrict__ zp, char4* __restrict__ out) {
-    for (uint64_t r = blockIdx.x; r < N; r += gridDim.x) {
-        for (uint32_t c = threadIdx.x; c < D4; c += 256) {
-            const float4 v = x[r * D4 + c];
-            const float4 s = scale[c];
-            const int4 z = zp[c];
-            char4 q;
-            q.x = quantize_one(v.x, s.x, z.x);
-            q.y = quantize_one(v.y, s.y, z.y);
-            q.z = quantize_one(v.z, s.z, z.z);
-            q.w = quantize_one(v.w, s.w, z.w);
-            out[r * D4 + c] = q;
-        }
+    const uint32_t t = threadIdx.x;
+    const uint32_t rpb = 256 / D4;
+    const uint32_t c = t % D4, r0 = t / D4;
+    if (r0 >= rpb) return;
+    const float4 sc = scale[c];
+    const int4 z = zp[c];
+    auto q4 = [&](const float4 v) {
+        char4 o;
+        o.x = quantize_one(v.x, sc.x, z.x);
+        o.y = quantize_one(v.y, sc.y, z.y);
+        o.z = quantize_one(v.z, sc.z, z.z);
+        o.w = quantize_one(v.w, sc.w, z.w);
+        return o;
+    };
+    const uint64_t step = uint64_t(gridDim.x) * rpb;
+    uint64_t r = uint64_t(blockIdx.x) * rpb + r0;
+    for (; r + 3 * step < N; r += 4 * step) {
+        const float4 a = x[r * D4 + c], b = x[(r + step) * D4 + c];
+        const float4 e = x[(r + 2 * step) * D4 + c], f = x[(r + 3 * step) * D4 + c];
+        out[r * D4 + c] = q4(a);
+        out[(r + step) * D4 + c] = q4(b);
+        out[(r + 2 * step) * D4 + c] = q4(e);
+        out[(r + 3 * step) * D4 + c] = q4(f);
     }
+    for (; r < N; r += step) out[r * D4 + c] = q4(x[r * D4 + c]);
 }
 
 __global__ __launch_bounds__(256) void dequantize_kernel(const int8_t* __restrict__ c, uint64_t N, uint32_t D,
@@ -663,13 +733,21 @@ va_status va_sq_params_per_dim(va_context* ctx, const float* x, uint32_t num_vec
     uint32_t* kmax = s.carve<uint32_t>(dim);
     VA_CHECK_STATUS(va::fill_u32(ctx, kmin, dim, 0xFFFFFFFFu));
     VA_CHECK_STATUS(va::fill_u32(ctx, kmax, dim, 0u));
-    const uint32_t ycols = (dim + 255) / 256;
-    // enough row blocks to cover the chip (about 2048 workgroups in total)
-    uint64_t xblocks = std::max<uint64_t>(1, std::min<uint64_t>(num_vectors, 2048 / ycols + 1));
-    const uint64_t rpb = (uint64_t(num_vectors) + xblocks - 1) / xblocks;
-    xblocks = (uint64_t(num_vectors) + rpb - 1) / rpb;
-    va::minmax_kernel<<<dim3(uint32_t(xblocks), ycols), dim3(256), 0, ctx->stream>>>(x, num_vectors, dim, rpb, kmin,
-                                                                                       kmax);
+    if (dim % 4 == 0 && dim <= 1024 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+        const uint32_t rows_per_step = 256 / (dim / 4);
+        const uint64_t blocks = std::max<uint64_t>(
+            1, std::min<uint64_t>(2048, (uint64_t(num_vectors) + rows_per_step - 1) / rows_per_step));
+        va::minmax_kernel_v4<<<dim3(uint32_t(blocks)), dim3(256), 0, ctx->stream>>>(
+            reinterpret_cast<const float4*>(x), num_vectors, dim / 4, kmin, kmax);
+    } else {
+        const uint32_t ycols = (dim + 255) / 256;
+        // enough row blocks to cover the chip (about 2048 workgroups in total)
+        uint64_t xblocks = std::max<uint64_t>(1, std::min<uint64_t>(num_vectors, 2048 / ycols + 1));
+        const uint64_t rpb = (uint64_t(num_vectors) + xblocks - 1) / xblocks;
+        xblocks = (uint64_t(num_vectors) + rpb - 1) / rpb;
+        va::minmax_kernel<<<dim3(uint32_t(xblocks), ycols), dim3(256), 0, ctx->stream>>>(x, num_vectors, dim, rpb,
+                                                                                           kmin, kmax);
+    }
     VA_CHECK_LAUNCH(ctx);
     va::params_finalize<<<dim3((dim + 255) / 256), dim3(256), 0, ctx->stream>>>(kmin, kmax, dim, out_min, out_max,
                                                                                  out_scale, out_zero_point);
@@ -683,14 +761,18 @@ va_status va_sq_quantize_i8(va_context* ctx, const float* x, uint64_t num_vector
     VA_REQUIRE(ctx, x && scale && zero_point && codes, "va_sq_quantize_i8: NULL pointer");
     VA_REQUIRE(ctx, num_vectors > 0 && dim > 0, "Empty input data");
     va::DeviceGuard g(ctx->device);
-    const bool v4 = dim % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(scale) |
-                                      reinterpret_cast<uintptr_t>(zero_point)) & 15) == 0 &&
+    const bool v4 = dim % 4 == 0 && dim <= 1024 &&
+                    ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(scale) |
+                      reinterpret_cast<uintptr_t>(zero_point)) & 15) == 0 &&
                     (reinterpret_cast<uintptr_t>(codes) & 3) == 0;
-    if (v4)
-        va::quantize_kernel_v4<<<dim3(va::grid_rows(num_vectors)), dim3(256), 0, ctx->stream>>>(
+    if (v4) {
+        const uint32_t rows_per_step = 256 / (dim / 4);
+        const uint64_t blocks = std::max<uint64_t>(
+            1, std::min<uint64_t>(8192, (num_vectors + rows_per_step - 1) / rows_per_step));
+        va::quantize_kernel_v4<<<dim3(uint32_t(blocks)), dim3(256), 0, ctx->stream>>>(
             reinterpret_cast<const float4*>(x), num_vectors, dim / 4, reinterpret_cast<const float4*>(scale),
             reinterpret_cast<const int4*>(zero_point), reinterpret_cast<char4*>(codes));
-    else
+    } else
         va::quantize_kernel<<<dim3(va::grid_rows(num_vectors)), dim3(256), 0, ctx->stream>>>(x, num_vectors, dim,
                                                                                            scale, zero_point, codes);
     VA_CHECK_LAUNCH(ctx);
