@@ -30,16 +30,18 @@ typedef float f32x4v __attribute__((ext_vector_type(4)));
 constexpr int KC = 16;               // d-values per LDS stage
 constexpr int LDS_STRIDE = KC + 4;   // 80-byte rows: conflict-free ds_read_b128 / ds_write_b128
 
-template <int WQ>
+// WQ x WN waves of 64 lanes; each wave owns 32 queries x 128 rows (4 MFMA blocks).
+template <int WQ, int WN>
 struct Tile {
-    static constexpr int WN = 4 / WQ;
+    static constexpr int NW = WQ * WN;
+    static constexpr int NT = 64 * NW;
     static constexpr int TQ = 32 * WQ;
     static constexpr int TN = 128 * WN;
     static constexpr int ROWS = TQ + TN;
     static constexpr int CHUNKS = ROWS * (KC / 4);
-    static constexpr int CPT = (CHUNKS + 255) / 256;
+    static constexpr int CPT = (CHUNKS + NT - 1) / NT;
     static constexpr int STAGE = ROWS * LDS_STRIDE;
-    static constexpr size_t LDS_BYTES = size_t(2 * STAGE + 4 * 128) * sizeof(float);
+    static constexpr size_t LDS_BYTES = size_t(2 * STAGE + NW * 128) * sizeof(float);
 };
 
 __device__ __forceinline__ float apply_op(int op, float dot, float qq, float xx) {
@@ -65,11 +67,11 @@ __device__ __forceinline__ float apply_op(int op, float dot, float qq, float xx)
     }
 }
 
-template <int WQ, bool VEC, int OUT>
-__global__ __launch_bounds__(256, 2) void dist_gemm_kernel(DistArgs a) {
-    using T = Tile<WQ>;
+template <int WQ, int WN, bool VEC, int OUT>
+__global__ __launch_bounds__(64 * WQ * WN, 2) void dist_gemm_kernel(DistArgs a) {  // 2 waves per SIMD
+    using T = Tile<WQ, WN>;
     extern __shared__ float lds[];
-    float* nrm = lds + 2 * T::STAGE;  // [4 waves][128] squared norms of the wave's rows
+    float* nrm = lds + 2 * T::STAGE;  // [waves][128] squared norms of the wave's rows
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -109,7 +111,7 @@ __global__ __launch_bounds__(256, 2) void dist_gemm_kernel(DistArgs a) {
     uint32_t colv[T::CPT];
 #pragma unroll
     for (int j = 0; j < T::CPT; ++j) {
-        const int c = tid + 256 * j;
+        const int c = tid + T::NT * j;
         src[j] = nullptr;
         ldsoff[j] = -1;
         colv[j] = 0;
@@ -278,19 +280,20 @@ __global__ __launch_bounds__(256, 2) void dist_gemm_kernel(DistArgs a) {
     }
 }
 
-template <int WQ, bool VEC, int OUT>
+template <int WQ, int WN, bool VEC, int OUT>
 va_status launch_tile(va_context* ctx, const DistArgs& a) {
-    using T = Tile<WQ>;
+    using T = Tile<WQ, WN>;
     const uint64_t nqb = (a.Q + T::TQ - 1) / T::TQ;
     const uint64_t ntb = (a.N + T::TN - 1) / T::TN;
     const uint64_t grid = a.tiles ? a.ntiles : nqb * ((ntb + kXcds - 1) / kXcds) * kXcds;
     if (grid == 0) return VA_OK;
     if (grid > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "distance grid too large (%llu tiles)", (unsigned long long)grid);
+    auto kern = &dist_gemm_kernel<WQ, WN, VEC, OUT>;
     if (T::LDS_BYTES > 65536) {
-        VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(&dist_gemm_kernel<WQ, VEC, OUT>),
+        VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                               hipFuncAttributeMaxDynamicSharedMemorySize, int(T::LDS_BYTES)));
     }
-    dist_gemm_kernel<WQ, VEC, OUT><<<dim3(uint32_t(grid)), dim3(256), T::LDS_BYTES, ctx->stream>>>(a);
+    kern<<<dim3(uint32_t(grid)), dim3(T::NT), T::LDS_BYTES, ctx->stream>>>(a);
     VA_CHECK_LAUNCH(ctx);
     return VA_OK;
 }
@@ -302,13 +305,17 @@ va_status launch_dist(va_context* ctx, const DistArgs& a) {
     const bool vec = (a.D % 4 == 0) && (a.ldq % 4 == 0) && (a.ldx % 4 == 0) &&
                      ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
     const int wq = a.wq ? a.wq : (a.Q <= 32 ? 1 : (a.Q <= 64 ? 2 : 4));
-#define VA_DIST_CASE(W, O)                                                                 \
-    if (wq == W && a.out == O) return vec ? launch_tile<W, true, O>(ctx, a) : launch_tile<W, false, O>(ctx, a);
-    VA_DIST_CASE(1, OUT_VALUES) VA_DIST_CASE(1, OUT_KEYS) VA_DIST_CASE(1, OUT_FILTER)
-    VA_DIST_CASE(2, OUT_VALUES) VA_DIST_CASE(2, OUT_KEYS) VA_DIST_CASE(2, OUT_FILTER)
-    VA_DIST_CASE(4, OUT_VALUES) VA_DIST_CASE(4, OUT_KEYS) VA_DIST_CASE(4, OUT_FILTER)
+    const int wn = a.wn ? a.wn : 4 / wq;
+#define VA_DIST_CASE(W, N, O)                                                              \
+    if (wq == W && wn == N && a.out == O)                                                  \
+        return vec ? launch_tile<W, N, true, O>(ctx, a) : launch_tile<W, N, false, O>(ctx, a);
+    VA_DIST_CASE(1, 4, OUT_VALUES) VA_DIST_CASE(1, 4, OUT_KEYS) VA_DIST_CASE(1, 4, OUT_FILTER)
+    VA_DIST_CASE(2, 2, OUT_VALUES) VA_DIST_CASE(2, 2, OUT_KEYS) VA_DIST_CASE(2, 2, OUT_FILTER)
+    VA_DIST_CASE(4, 1, OUT_VALUES) VA_DIST_CASE(4, 1, OUT_KEYS) VA_DIST_CASE(4, 1, OUT_FILTER)
+    // small list-major tiles (one or two waves) for sparse IVF work
+    VA_DIST_CASE(1, 1, OUT_FILTER) VA_DIST_CASE(2, 1, OUT_FILTER)
 #undef VA_DIST_CASE
-    return fail(ctx, VA_ERR_INVALID_ARG, "launch_dist: bad output mode %d", int(a.out));
+    return fail(ctx, VA_ERR_INVALID_ARG, "launch_dist: no %dx%d tile for output mode %d", wq, wn, int(a.out));
 }
 
 }  // namespace va

@@ -226,12 +226,14 @@ struct DistArgs {
     uint32_t ntiles = 0;
     uint32_t rstride = 1;
     const uint32_t* ids = nullptr;
-    int wq = 0;  // waves along queries (1, 2 or 4: tiles of 32*wq queries x 512/wq rows); 0 = from Q
+    int wq = 0;  // waves along queries (tiles of 32*wq queries); 0 = from Q
+    int wn = 0;  // waves along rows (tiles of 128*wn rows); 0 = 4/wq.  wq x wn in {1x4, 2x2, 4x1}, and
+                 // for OUT_FILTER also 1x1, 2x1
 };
 
 // Tile shape of launch_dist for a given wq: queries and database rows per workgroup.
 inline uint32_t dist_tile_queries(int wq) { return 32u * uint32_t(wq); }
-inline uint32_t dist_tile_rows(int wq) { return 128u * uint32_t(4 / wq); }
+inline uint32_t dist_tile_rows(int wn) { return 128u * uint32_t(wn); }
 
 // Launch the MFMA distance GEMM.  Chooses the tile shape from Q.
 va_status launch_dist(va_context* ctx, const DistArgs& a);

@@ -38,7 +38,15 @@ struct va_ivf {
 namespace va {
 namespace {
 
-constexpr uint32_t kSampleStride = 64;
+// Threshold sample: a prefix of every probed list (rows are in insertion order, so a prefix is
+// an unbiased subset) of at least 1/kSampleRate of its rows and at least kSampleMin rows.
+// Every list is sampled at rate >= 1/kSampleRate, so a query's candidate count stays within
+// about kSampleRate x k; the floor keeps small lists' sample tiles full.
+constexpr uint32_t kSampleRate = 64;
+constexpr uint32_t kSampleMin = 128;
+inline uint32_t sample_rows(uint32_t n) {
+    return std::min(n, std::max((n + kSampleRate - 1) / kSampleRate, kSampleMin));
+}
 
 __global__ __launch_bounds__(256) void gather_rows(const float* __restrict__ x, const uint32_t* __restrict__ ids,
                                                    uint32_t N, uint32_t D, float* __restrict__ out) {
@@ -104,26 +112,51 @@ struct F32Keys final : KeyProducer {
     }
 };
 
-// Tile descriptors {qs, qc, rs, rc} of one list-major pass, grouped by tile shape.
+// Tile descriptors {qs, qc, rs, rc} of one list-major pass, grouped by tile shape.  A tile of
+// wq x wn waves covers 32*wq queries x 128*wn rows.  A list with nq probing queries and n
+// rows gets the shape with the least estimated time: tiles x waves x the measured cost of
+// one wave tile (32 x 128) in that shape on MI355X (shapes with more waves share their LDS
+// stages across more MFMA work and run more workgroups per CU, except 1 x 4, whose 87 KB of
+// LDS leaves one workgroup per CU).  The one- and two-wave shapes keep lists with few
+// queries or few rows from paying for a 4-wave tile.
 struct TilePlan {
-    std::vector<uint32_t> t[3];  // wq = 1, 2, 4
-    static int slot(int wq) { return wq == 1 ? 0 : (wq == 2 ? 1 : 2); }
-    static int wq_for(uint32_t nq) { return nq > 64 ? 4 : (nq > 32 ? 2 : 1); }
-    // rows of list l: positions off + j*stride, j < nrows
+    static constexpr int NS = 5;
+    static constexpr int WQ[NS] = {4, 2, 2, 1, 1};
+    static constexpr int WN[NS] = {1, 2, 1, 1, 4};
+    static constexpr uint32_t COST[NS] = {100, 120, 135, 175, 195};  // per wave tile, relative
+    std::vector<uint32_t> t[NS];
+    static int shape_for(uint32_t nq, uint32_t nrows) {
+        int best = 0;
+        uint64_t best_cost = ~0ull;
+        for (int i = 0; i < NS; ++i) {
+            const uint64_t cost = uint64_t((nq + 32 * WQ[i] - 1) / (32 * WQ[i])) *
+                                  ((nrows + 128 * WN[i] - 1) / (128 * WN[i])) * (WQ[i] * WN[i]) * COST[i];
+            if (cost < best_cost) {
+                best = i;
+                best_cost = cost;
+            }
+        }
+        return best;
+    }
+    // rows of a list: positions off + j, j < nrows
     void add(uint32_t lq_start, uint32_t nq, uint32_t off, uint32_t nrows) {
         if (nq == 0 || nrows == 0) return;
-        const int wq = wq_for(nq);
-        const uint32_t TQ = dist_tile_queries(wq), TN = dist_tile_rows(wq);
-        auto& v = t[slot(wq)];
+        const int sh = shape_for(nq, nrows);
+        const uint32_t TQ = dist_tile_queries(WQ[sh]), TN = dist_tile_rows(WN[sh]);
+        auto& v = t[sh];
         for (uint32_t qb = 0; qb < nq; qb += TQ)
             for (uint32_t r = 0; r < nrows; r += TN) {
                 v.push_back(lq_start + qb);
                 v.push_back(std::min(TQ, nq - qb));
-                v.push_back(off + r);  // position index (scaled by the pass stride in the kernel)
+                v.push_back(off + r);
                 v.push_back(std::min(TN, nrows - r));
             }
     }
-    size_t words() const { return t[0].size() + t[1].size() + t[2].size(); }
+    size_t words() const {
+        size_t w = 0;
+        for (const auto& v : t) w += v.size();
+        return w;
+    }
 };
 
 // Runs one list-major filter pass; tiles hold "rs" as an index into the strided row space
@@ -132,8 +165,8 @@ va_status run_pass(va_context* ctx, const TilePlan& plan, uint32_t* dev_tiles, c
                    const va_ivf* ivf, uint32_t rstride, const uint32_t* thr, uint32_t* cnt, uint32_t* ckey,
                    uint32_t* cid, uint32_t cap) {
     size_t off = 0;
-    for (int wq : {1, 2, 4}) {
-        const auto& v = plan.t[TilePlan::slot(wq)];
+    for (int sh = 0; sh < TilePlan::NS; ++sh) {
+        const auto& v = plan.t[sh];
         if (v.empty()) continue;
         VA_CHECK_HIP(ctx, hipMemcpyAsync(dev_tiles + off, v.data(), v.size() * 4, hipMemcpyHostToDevice, ctx->stream));
         DistArgs a;
@@ -154,7 +187,8 @@ va_status run_pass(va_context* ctx, const TilePlan& plan, uint32_t* dev_tiles, c
         a.ntiles = uint32_t(v.size() / 4);
         a.rstride = rstride;
         a.ids = ivf->ids;
-        a.wq = wq;
+        a.wq = TilePlan::WQ[sh];
+        a.wn = TilePlan::WN[sh];
         VA_CHECK_STATUS(launch_dist(ctx, a));
         off += v.size();
     }
@@ -319,7 +353,7 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
             lq_off[l + 1]++;
             const uint32_t n = off[l + 1] - off[l];
             total[q] += n;
-            sampled[q] += (n + va::kSampleStride - 1) / va::kSampleStride;
+            sampled[q] += va::sample_rows(n);
         }
     for (uint32_t l = 0; l < C; ++l) lq_off[l + 1] += lq_off[l];
     std::vector<uint32_t> lq(lq_off[C]), fillp(lq_off.begin(), lq_off.end() - 1);
@@ -334,27 +368,14 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
         const uint32_t n = off[l + 1] - off[l];
         main_plan.add(lq_off[l], nq, off[l], n);
     }
-    // sampled rows: positions off[l] + j*stride; tile rs values are first positions
-    for (uint32_t l = 0; l < C; ++l) {
-        const uint32_t nq = lq_off[l + 1] - lq_off[l];
-        const uint32_t n = off[l + 1] - off[l];
-        const uint32_t ns = (n + va::kSampleStride - 1) / va::kSampleStride;
-        if (nq == 0 || ns == 0) continue;
-        const int wq = va::TilePlan::wq_for(nq);
-        const uint32_t TQ = va::dist_tile_queries(wq), TN = va::dist_tile_rows(wq);
-        auto& v = sample_plan.t[va::TilePlan::slot(wq)];
-        for (uint32_t qb = 0; qb < nq; qb += TQ)
-            for (uint32_t r = 0; r < ns; r += TN) {
-                v.push_back(lq_off[l] + qb);
-                v.push_back(std::min(TQ, nq - qb));
-                v.push_back(off[l] + r * va::kSampleStride);
-                v.push_back(std::min(TN, ns - r));
-            }
-    }
+    for (uint32_t l = 0; l < C; ++l)
+        sample_plan.add(lq_off[l], lq_off[l + 1] - lq_off[l], off[l], va::sample_rows(off[l + 1] - off[l]));
     const uint64_t cap_s = std::max<uint64_t>(1, *std::max_element(sampled.begin(), sampled.end()));
     const uint64_t max_total = std::max<uint64_t>(1, *std::max_element(total.begin(), total.end()));
+    // every list is sampled at rate >= 1/kSampleRate: a query's candidates stay near
+    // kSampleRate x k; queries that still outgrow the list take the exact rescan below
     uint64_t cap = ctx->opt_candidate_cap ? ctx->opt_candidate_cap
-                                          : std::max<uint64_t>(3ull * k, uint64_t(k) + 32) * va::kSampleStride + 1024;
+                                          : std::max<uint64_t>(3ull * k, uint64_t(k) + 32) * va::kSampleRate + 1024;
     cap = std::min(cap, max_total);
     const uint64_t cand = std::max(cap_s, cap);
 
@@ -377,7 +398,7 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
     // ---- 1. sample pass: every sampled candidate, then tau = k-th smallest ----------------------
     VA_CHECK_STATUS(va::fill_u32(ctx, thr, Q, 0xFFFFFFFFu));
     VA_CHECK_STATUS(va::fill_u32(ctx, cnt, Q, 0));
-    VA_CHECK_STATUS(va::run_pass(ctx, sample_plan, d_tiles, queries, d_lq, ivf, va::kSampleStride, thr, cnt, ckey, cid,
+    VA_CHECK_STATUS(va::run_pass(ctx, sample_plan, d_tiles, queries, d_lq, ivf, 1, thr, cnt, ckey, cid,
                                  uint32_t(cap_s)));
     {
         va::SelectArgs a;
