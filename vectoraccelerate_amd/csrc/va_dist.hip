@@ -19,6 +19,8 @@
 // column n = l%32 — so each lane owns ONE query and 64 database rows.
 #include <cfloat>
 
+#include <algorithm>
+
 #include "va_internal.hpp"
 
 namespace va {
@@ -28,7 +30,31 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
 constexpr int KC = 16;               // d-values per LDS stage
+#ifndef VA_DIST_SWZ
+#define VA_DIST_SWZ 1
+#endif
+#ifndef VA_DIST_WPE
+#define VA_DIST_WPE 2      // waves per SIMD the register-staged kernel is compiled for
+#endif
+#ifndef VA_DIST_DMA_WPE
+#define VA_DIST_DMA_WPE 4  // ... and the direct-load kernel
+#endif
+#ifndef VA_DIST_DMA
+#define VA_DIST_DMA 1
+#endif
+#ifndef VA_DIST_DMA_SLOTS
+#define VA_DIST_DMA_SLOTS 2  // LDS ring slots of the direct-load kernel (stages in flight + 1)
+#endif
+#if VA_DIST_SWZ
+// 64-byte rows, unpadded: 16-byte chunk c of row r sits at chunk c ^ ((r >> 2) & 3).
+// ds_read_b128 / ds_write_b128 serve 16 lanes per clock across 64 banks; the 16 rows of a
+// fragment read (and the 4 x 4 chunks of a 16-lane write) land in 16 distinct bank groups.
+constexpr int LDS_STRIDE = KC;
+__device__ __forceinline__ int lds_chunk(int row, int c) { return c ^ ((row >> 2) & 3); }
+#else
 constexpr int LDS_STRIDE = KC + 4;   // 80-byte rows: conflict-free ds_read_b128 / ds_write_b128
+__device__ __forceinline__ int lds_chunk(int row, int c) { return c; }
+#endif
 
 // WQ x WN waves of 64 lanes; each wave owns 32 queries x 128 rows (4 MFMA blocks).
 template <int WQ, int WN>
@@ -42,6 +68,12 @@ struct Tile {
     static constexpr int CPT = (CHUNKS + NT - 1) / NT;
     static constexpr int STAGE = ROWS * LDS_STRIDE;
     static constexpr size_t LDS_BYTES = size_t(2 * STAGE + NW * 128) * sizeof(float);
+    // direct-to-LDS loads: 16-row groups of 1 KiB (one wave-wide load each), the same number
+    // per wave (the last few may be padding), two ring slots
+    static constexpr int GROUPS = ROWS / 16;
+    static constexpr int GPW = (GROUPS + NW - 1) / NW;
+    static constexpr int DSTAGE = GPW * NW * 256;  // floats per slot
+    static constexpr size_t DMA_LDS_BYTES = size_t(VA_DIST_DMA_SLOTS * DSTAGE + NW * 128) * sizeof(float);
 };
 
 __device__ __forceinline__ float apply_op(int op, float dot, float qq, float xx) {
@@ -67,15 +99,19 @@ __device__ __forceinline__ float apply_op(int op, float dot, float qq, float xx)
     }
 }
 
-template <int WQ, int WN, bool VEC, int OUT>
-__global__ __launch_bounds__(64 * WQ * WN, 2) void dist_gemm_kernel(DistArgs a) {  // 2 waves per SIMD
+// DMA = true: the stages move global -> LDS by direct buffer loads (no register staging, so
+// fewer VGPRs and more waves per SIMD); needs 16-byte rows (VEC) and the swizzled 64-byte LDS
+// rows.  DMA = false: register-staged loads, any row alignment.
+template <int WQ, int WN, bool VEC, int OUT, bool DMA>
+__global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) void dist_gemm_kernel(DistArgs a) {
     using T = Tile<WQ, WN>;
+    static_assert(!DMA || (VEC && LDS_STRIDE == KC), "direct loads need 16-byte rows and unpadded LDS rows");
     extern __shared__ float lds[];
-    float* nrm = lds + 2 * T::STAGE;  // [waves][128] squared norms of the wave's rows
+    float* nrm = lds + (DMA ? VA_DIST_DMA_SLOTS * T::DSTAGE : 2 * T::STAGE);  // [waves][128] squared norms of the wave's rows
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wq = wave % WQ;
     const int wn = wave / WQ;
     const int l32 = lane & 31;
@@ -105,57 +141,6 @@ __global__ __launch_bounds__(64 * WQ * WN, 2) void dist_gemm_kernel(DistArgs a) 
         rc = min(uint32_t(T::TN), a.N - rs);
     }
 
-    // source row pointers of this thread's load chunks (fixed across stages)
-    const float* src[T::CPT];
-    int ldsoff[T::CPT];
-    uint32_t colv[T::CPT];
-#pragma unroll
-    for (int j = 0; j < T::CPT; ++j) {
-        const int c = tid + T::NT * j;
-        src[j] = nullptr;
-        ldsoff[j] = -1;
-        colv[j] = 0;
-        if (c < T::CHUNKS) {
-            const int row = c >> 2;
-            const int col = (c & 3) * 4;
-            ldsoff[j] = row * LDS_STRIDE + col;
-            colv[j] = uint32_t(col);
-            if (row < T::TQ) {
-                if (uint32_t(row) < qc) {
-                    const uint32_t r = a.qrow ? a.qrow[qs + row] : qs + row;
-                    src[j] = a.q + int64_t(r) * a.ldq + col;
-                }
-            } else {
-                const uint32_t jr = uint32_t(row - T::TQ);
-                if (jr < rc) src[j] = a.x + int64_t(rs + jr * rstride) * a.ldx + col;
-            }
-        }
-    }
-
-    f32x4v pre[T::CPT];
-    auto load = [&](uint32_t d0) {
-#pragma unroll
-        for (int j = 0; j < T::CPT; ++j) {
-            f32x4v v = {0.0f, 0.0f, 0.0f, 0.0f};
-            const uint32_t d = d0 + colv[j];
-            if (src[j]) {
-                if (VEC) {
-                    if (d < a.D) v = *reinterpret_cast<const f32x4v*>(src[j] + d0);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (d + e < a.D) v[e] = src[j][d0 + e];
-                }
-            }
-            pre[j] = v;
-        }
-    };
-    auto store = [&](float* stage) {
-#pragma unroll
-        for (int j = 0; j < T::CPT; ++j)
-            if (ldsoff[j] >= 0) *reinterpret_cast<f32x4v*>(stage + ldsoff[j]) = pre[j];
-    };
-
     f32x16 acc[4];
 #pragma unroll
     for (int b = 0; b < 4; ++b)
@@ -163,29 +148,24 @@ __global__ __launch_bounds__(64 * WQ * WN, 2) void dist_gemm_kernel(DistArgs a) 
         for (int v = 0; v < 16; ++v) acc[b][v] = 0.0f;
     float qss = 0.0f;
     float xss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-
-    const int nstages = int((a.D + KC - 1) / KC);
-    load(0);
-    store(lds);
-    __syncthreads();
-
-    const int boff = (wq * 32 + l32) * LDS_STRIDE + hh * 4;
-    const int aoff = (T::TQ + wn * 128 + l32) * LDS_STRIDE + hh * 4;
-
-    for (int s = 0; s < nstages; ++s) {
-        const bool more = (s + 1) < nstages;
-        if (more) load(uint32_t(s + 1) * KC);
-        const float* st = lds + (s & 1) * T::STAGE;
+    // fragment rows start at multiples of 32, so every fragment row shares l32's chunk swizzle
+    const int boff = (wq * 32 + l32) * LDS_STRIDE;
+    const int aoff = (T::TQ + wn * 128 + l32) * LDS_STRIDE;
+    int koff[KC / 8];
+#pragma unroll
+    for (int g = 0; g < KC / 8; ++g) koff[g] = 4 * lds_chunk(l32, 2 * g + hh);
+    // one 16-value stage of MFMAs from an LDS slot; norms accumulate from the same fragments
+    auto compute = [&](const float* st) {
 #pragma unroll
         for (int g = 0; g < KC / 8; ++g) {
-            const f32x4v bv = *reinterpret_cast<const f32x4v*>(st + boff + g * 8);
+            const f32x4v bv = *reinterpret_cast<const f32x4v*>(st + boff + koff[g]);
             qss = fmaf(bv[0], bv[0], qss);
             qss = fmaf(bv[1], bv[1], qss);
             qss = fmaf(bv[2], bv[2], qss);
             qss = fmaf(bv[3], bv[3], qss);
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
-                const f32x4v av = *reinterpret_cast<const f32x4v*>(st + aoff + b * 32 * LDS_STRIDE + g * 8);
+                const f32x4v av = *reinterpret_cast<const f32x4v*>(st + aoff + b * 32 * LDS_STRIDE + koff[g]);
                 xss[b] = fmaf(av[0], av[0], xss[b]);
                 xss[b] = fmaf(av[1], av[1], xss[b]);
                 xss[b] = fmaf(av[2], av[2], xss[b]);
@@ -196,8 +176,132 @@ __global__ __launch_bounds__(64 * WQ * WN, 2) void dist_gemm_kernel(DistArgs a) 
                 acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[3], bv[3], acc[b], 0, 0, 0);
             }
         }
-        if (more) store(lds + ((s + 1) & 1) * T::STAGE);
+    };
+    const int nstages = int((a.D + KC - 1) / KC);
+    if constexpr (DMA) {
+        // 16-row group gi of a slot is rows 16*gi .. 16*gi+15 (queries first, then database
+        // rows); lane L loads row 16*gi + L/4, physical chunk L%4 = logical chunk
+        // (L%4) ^ swizzle(row).  Rows outside the tile and columns past D load from an offset
+        // past the descriptor and land as zeros.
+        // every offset below addresses a real row (checked by the launcher to stay under
+        // kDmaMaxBytes), so the descriptors only need to bound kDmaSkip
+        const dma_rsrc qres = make_dma_rsrc(a.q, kDmaMaxBytes);
+        const dma_rsrc xres = make_dma_rsrc(a.x + int64_t(rs) * a.ldx, kDmaMaxBytes);
+        uint32_t base[T::GPW], colb[T::GPW];
+#pragma unroll
+        for (int i = 0; i < T::GPW; ++i) {
+            const int row = 16 * (wave + T::NW * i) + (lane >> 2);
+            const int c = lds_chunk(row, lane & 3);
+            colb[i] = uint32_t(4 * c);
+            base[i] = kDmaSkip;
+            if (row < T::TQ) {
+                if (uint32_t(row) < qc) {
+                    const uint32_t r = a.qrow ? a.qrow[qs + row] : qs + row;
+                    base[i] = uint32_t(int64_t(r) * a.ldq * 4) + 16u * uint32_t(c);
+                }
+            } else if (row < T::ROWS) {
+                const uint32_t jr = uint32_t(row - T::TQ);
+                if (jr < rc) base[i] = uint32_t(int64_t(jr) * rstride * a.ldx * 4) + 16u * uint32_t(c);
+            }
+        }
+        const uint32_t lds0 = lds_addr_of(lds);
+        auto issue = [&](uint32_t d0, int slot) {
+#pragma unroll
+            for (int i = 0; i < T::GPW; ++i) {
+                const uint32_t voff = (base[i] != kDmaSkip && d0 + colb[i] < a.D) ? base[i] + d0 * 4u : kDmaSkip;
+                const int grp = wave + T::NW * i;
+                lds_dma16(16 * grp < T::TQ ? qres : xres, voff,
+                          lds0 + uint32_t(slot * T::DSTAGE + grp * 256) * 4u);
+            }
+        };
+        if constexpr (VA_DIST_DMA_SLOTS == 2) {
+            issue(0, 0);
+            wait_vmcnt<0>();
+            __syncthreads();
+            for (int s = 0; s < nstages; ++s) {
+                const bool more = (s + 1) < nstages;
+                if (more) issue(uint32_t(s + 1) * KC, (s + 1) & 1);  // slot last read before the previous barrier
+                compute(lds + (s & 1) * T::DSTAGE);
+                if (more) wait_vmcnt<0>();
+                __syncthreads();
+            }
+        } else {
+            // three slots: stage s+2 loads while stage s computes
+            issue(0, 0);
+            if (nstages > 1) issue(KC, 1);
+            int slot = 0;
+            for (int s = 0; s < nstages; ++s) {
+                if (s + 1 < nstages) wait_vmcnt<T::GPW>();
+                else wait_vmcnt<0>();
+                __syncthreads();  // stage s visible; every wave is past the reads of slot (s + 2) % 3
+                if (s + 2 < nstages) issue(uint32_t(s + 2) * KC, slot == 0 ? 2 : slot - 1);
+                compute(lds + slot * T::DSTAGE);
+                slot = slot == 2 ? 0 : slot + 1;
+            }
+            __syncthreads();  // the epilogue reuses LDS only after every wave's last reads
+        }
+    } else {
+        // source row pointers of this thread's load chunks (fixed across stages)
+        const float* src[T::CPT];
+        int ldsoff[T::CPT];
+        uint32_t colv[T::CPT];
+#pragma unroll
+        for (int j = 0; j < T::CPT; ++j) {
+            const int c = tid + T::NT * j;
+            src[j] = nullptr;
+            ldsoff[j] = -1;
+            colv[j] = 0;
+            if (c < T::CHUNKS) {
+                const int row = c >> 2;
+                const int col = (c & 3) * 4;
+                ldsoff[j] = row * LDS_STRIDE + 4 * lds_chunk(row, col / 4);
+                colv[j] = uint32_t(col);
+                if (row < T::TQ) {
+                    if (uint32_t(row) < qc) {
+                        const uint32_t r = a.qrow ? a.qrow[qs + row] : qs + row;
+                        src[j] = a.q + int64_t(r) * a.ldq + col;
+                    }
+                } else {
+                    const uint32_t jr = uint32_t(row - T::TQ);
+                    if (jr < rc) src[j] = a.x + int64_t(rs + jr * rstride) * a.ldx + col;
+                }
+            }
+        }
+
+        f32x4v pre[T::CPT];
+        auto load = [&](uint32_t d0) {
+#pragma unroll
+            for (int j = 0; j < T::CPT; ++j) {
+                f32x4v v = {0.0f, 0.0f, 0.0f, 0.0f};
+                const uint32_t d = d0 + colv[j];
+                if (src[j]) {
+                    if (VEC) {
+                        if (d < a.D) v = *reinterpret_cast<const f32x4v*>(src[j] + d0);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (d + e < a.D) v[e] = src[j][d0 + e];
+                    }
+                }
+                pre[j] = v;
+            }
+        };
+        auto store = [&](float* stage) {
+#pragma unroll
+            for (int j = 0; j < T::CPT; ++j)
+                if (ldsoff[j] >= 0) *reinterpret_cast<f32x4v*>(stage + ldsoff[j]) = pre[j];
+        };
+
+        load(0);
+        store(lds);
         __syncthreads();
+        for (int s = 0; s < nstages; ++s) {
+            const bool more = (s + 1) < nstages;
+            if (more) load(uint32_t(s + 1) * KC);
+            compute(lds + (s & 1) * T::STAGE);
+            if (more) store(lds + ((s + 1) & 1) * T::STAGE);
+            __syncthreads();
+        }
     }
 
     // combine the two lane halves of every partial sum of squares
@@ -217,7 +321,8 @@ __global__ __launch_bounds__(64 * WQ * WN, 2) void dist_gemm_kernel(DistArgs a) 
         // Count this lane's passing keys, reserve them with one atomic, then write them.
         const uint32_t thr = a.thr[qi];
         uint64_t pass = 0;  // bit 16b + 4j + e
-        uint32_t keys[64];
+        // keys are recomputed for the (rare) passing values when they are written rather than
+        // kept for all 64, which keeps the epilogue within the main loop's register budget
 #pragma unroll
         for (int b = 0; b < 4; ++b)
 #pragma unroll
@@ -227,8 +332,7 @@ __global__ __launch_bounds__(64 * WQ * WN, 2) void dist_gemm_kernel(DistArgs a) 
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const uint32_t key = key_of_float(apply_op(a.op, acc[b][4 * j + e], qq, xx[e]));
-                    keys[16 * b + 4 * j + e] = key;
-                    const bool p = uint32_t(wn * 128 + mloc + e) < rc && key <= thr;
+                    const bool p = (uint32_t(wn * 128 + mloc + e) < rc) & (key <= thr);
                     pass |= uint64_t(p) << (16 * b + 4 * j + e);
                 }
             }
@@ -241,7 +345,8 @@ __global__ __launch_bounds__(64 * WQ * WN, 2) void dist_gemm_kernel(DistArgs a) 
                     const int b = t >> 4, j = (t >> 2) & 3, e = t & 3;
                     const uint32_t p = rs + uint32_t(wn * 128 + b * 32 + 8 * j + 4 * hh + e) * rstride;
                     const int64_t o = int64_t(qi) * a.cap + pos;
-                    a.cand_key[o] = keys[t];
+                    const float xx = nrm[wave * 128 + b * 32 + 8 * j + 4 * hh + e];
+                    a.cand_key[o] = key_of_float(apply_op(a.op, acc[b][t & 15], qq, xx));
                     a.cand_id[o] = a.ids ? a.ids[p] : a.id_base + p;
                 }
                 ++pos;
@@ -280,7 +385,7 @@ __global__ __launch_bounds__(64 * WQ * WN, 2) void dist_gemm_kernel(DistArgs a) 
     }
 }
 
-template <int WQ, int WN, bool VEC, int OUT>
+template <int WQ, int WN, bool VEC, int OUT, bool DMA>
 va_status launch_tile(va_context* ctx, const DistArgs& a) {
     using T = Tile<WQ, WN>;
     const uint64_t nqb = (a.Q + T::TQ - 1) / T::TQ;
@@ -288,14 +393,35 @@ va_status launch_tile(va_context* ctx, const DistArgs& a) {
     const uint64_t grid = a.tiles ? a.ntiles : nqb * ((ntb + kXcds - 1) / kXcds) * kXcds;
     if (grid == 0) return VA_OK;
     if (grid > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "distance grid too large (%llu tiles)", (unsigned long long)grid);
-    auto kern = &dist_gemm_kernel<WQ, WN, VEC, OUT>;
-    if (T::LDS_BYTES > 65536) {
+    auto kern = &dist_gemm_kernel<WQ, WN, VEC, OUT, DMA>;
+    const size_t lds_bytes = DMA ? T::DMA_LDS_BYTES : T::LDS_BYTES;
+    if (lds_bytes > 65536) {
         VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, int(T::LDS_BYTES)));
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)));
     }
-    kern<<<dim3(uint32_t(grid)), dim3(T::NT), T::LDS_BYTES, ctx->stream>>>(a);
+    kern<<<dim3(uint32_t(grid)), dim3(T::NT), lds_bytes, ctx->stream>>>(a);
     VA_CHECK_LAUNCH(ctx);
     return VA_OK;
+}
+
+// Direct loads address rows through 32-bit offsets below kDmaMaxBytes: every query row the
+// launch can name, and every row of one tile relative to the tile's first row.
+template <int WQ, int WN>
+bool dma_fits(const DistArgs& a, bool vec) {
+    if (!VA_DIST_DMA || !vec || LDS_STRIDE != KC) return false;
+    const uint64_t qrows = a.qrow ? a.q_rows : a.Q;
+    if (qrows == 0) return false;
+    const uint64_t tn = a.tiles ? Tile<WQ, WN>::TN : std::min<uint64_t>(Tile<WQ, WN>::TN, a.N);
+    const uint64_t rstride = a.tiles ? a.rstride : 1;
+    return (qrows - 1) * uint64_t(a.ldq) * 4 + uint64_t(a.D) * 4 <= kDmaMaxBytes &&
+           (tn - 1) * rstride * uint64_t(a.ldx) * 4 + uint64_t(a.D) * 4 <= kDmaMaxBytes;
+}
+
+template <int WQ, int WN, int OUT>
+va_status launch_shape(va_context* ctx, const DistArgs& a, bool vec) {
+    if constexpr (LDS_STRIDE == KC)
+        if (dma_fits<WQ, WN>(a, vec)) return launch_tile<WQ, WN, true, OUT, true>(ctx, a);
+    return vec ? launch_tile<WQ, WN, true, OUT, false>(ctx, a) : launch_tile<WQ, WN, false, OUT, false>(ctx, a);
 }
 
 }  // namespace
@@ -306,9 +432,8 @@ va_status launch_dist(va_context* ctx, const DistArgs& a) {
                      ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
     const int wq = a.wq ? a.wq : (a.Q <= 32 ? 1 : (a.Q <= 64 ? 2 : 4));
     const int wn = a.wn ? a.wn : 4 / wq;
-#define VA_DIST_CASE(W, N, O)                                                              \
-    if (wq == W && wn == N && a.out == O)                                                  \
-        return vec ? launch_tile<W, N, true, O>(ctx, a) : launch_tile<W, N, false, O>(ctx, a);
+#define VA_DIST_CASE(W, N, O) \
+    if (wq == W && wn == N && a.out == O) return launch_shape<W, N, O>(ctx, a, vec);
     VA_DIST_CASE(1, 4, OUT_VALUES) VA_DIST_CASE(1, 4, OUT_KEYS) VA_DIST_CASE(1, 4, OUT_FILTER)
     VA_DIST_CASE(2, 2, OUT_VALUES) VA_DIST_CASE(2, 2, OUT_KEYS) VA_DIST_CASE(2, 2, OUT_FILTER)
     VA_DIST_CASE(4, 1, OUT_VALUES) VA_DIST_CASE(4, 1, OUT_KEYS) VA_DIST_CASE(4, 1, OUT_FILTER)

@@ -113,6 +113,7 @@ struct F32Producer final : KeyProducer {
         DistArgs a;
         a.q = qrow ? q : q + int64_t(q0) * D;
         a.qrow = qrow;
+        a.q_rows = Q;
         a.ldq = D;
         a.x = x + int64_t(c0) * D;
         a.ldx = int64_t(stride) * D;

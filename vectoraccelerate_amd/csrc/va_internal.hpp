@@ -203,6 +203,7 @@ enum DistOut : int {
 struct DistArgs {
     const float* q = nullptr;   // query rows
     const uint32_t* qrow = nullptr;  // optional query-row indirection (query i reads row qrow[i])
+    uint64_t q_rows = 0;             // rows addressable from q when qrow is set (0 = unknown)
     int64_t ldq = 0;
     const float* x = nullptr;   // database rows
     int64_t ldx = 0;

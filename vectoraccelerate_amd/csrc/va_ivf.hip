@@ -80,6 +80,7 @@ struct F32Keys final : KeyProducer {
         DistArgs a;
         a.q = qrow ? q : q + int64_t(q0) * D;
         a.qrow = qrow;
+        a.q_rows = Q;
         a.ldq = D;
         a.x = x + int64_t(c0) * D;
         a.ldx = int64_t(stride) * D;
@@ -161,9 +162,9 @@ struct TilePlan {
 
 // Runs one list-major filter pass; tiles hold "rs" as an index into the strided row space
 // (the kernel multiplies j by rstride; rs must already be the first position).
-va_status run_pass(va_context* ctx, const TilePlan& plan, uint32_t* dev_tiles, const float* q, const uint32_t* lq,
-                   const va_ivf* ivf, uint32_t rstride, const uint32_t* thr, uint32_t* cnt, uint32_t* ckey,
-                   uint32_t* cid, uint32_t cap) {
+va_status run_pass(va_context* ctx, const TilePlan& plan, uint32_t* dev_tiles, const float* q, uint32_t q_rows,
+                   const uint32_t* lq, const va_ivf* ivf, uint32_t rstride, const uint32_t* thr, uint32_t* cnt,
+                   uint32_t* ckey, uint32_t* cid, uint32_t cap) {
     size_t off = 0;
     for (int sh = 0; sh < TilePlan::NS; ++sh) {
         const auto& v = plan.t[sh];
@@ -172,6 +173,7 @@ va_status run_pass(va_context* ctx, const TilePlan& plan, uint32_t* dev_tiles, c
         DistArgs a;
         a.q = q;
         a.qrow = lq;
+        a.q_rows = q_rows;
         a.ldq = ivf->D;
         a.x = ivf->list_vectors;
         a.ldx = ivf->D;
@@ -398,7 +400,7 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
     // ---- 1. sample pass: every sampled candidate, then tau = k-th smallest ----------------------
     VA_CHECK_STATUS(va::fill_u32(ctx, thr, Q, 0xFFFFFFFFu));
     VA_CHECK_STATUS(va::fill_u32(ctx, cnt, Q, 0));
-    VA_CHECK_STATUS(va::run_pass(ctx, sample_plan, d_tiles, queries, d_lq, ivf, 1, thr, cnt, ckey, cid,
+    VA_CHECK_STATUS(va::run_pass(ctx, sample_plan, d_tiles, queries, Q, d_lq, ivf, 1, thr, cnt, ckey, cid,
                                  uint32_t(cap_s)));
     {
         va::SelectArgs a;
@@ -415,7 +417,7 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
     // ---- 2. full pass with the thresholds, 3. exact selection -----------------------------------
     VA_CHECK_STATUS(va::fill_u32(ctx, cnt, Q, 0));
     VA_CHECK_STATUS(va::fill_u32(ctx, ovf_cnt, 1, 0));
-    VA_CHECK_STATUS(va::run_pass(ctx, main_plan, d_tiles, queries, d_lq, ivf, 1, thr, cnt, ckey, cid, uint32_t(cap)));
+    VA_CHECK_STATUS(va::run_pass(ctx, main_plan, d_tiles, queries, Q, d_lq, ivf, 1, thr, cnt, ckey, cid, uint32_t(cap)));
     {
         va::SelectArgs a;
         a.keys = ckey;
@@ -478,7 +480,7 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
                                                                                             ivf->D, cq);
     VA_CHECK_LAUNCH(ctx);
     VA_CHECK_STATUS(va::fill_u32(ctx, d_cnt, n_ovf, 0));
-    VA_CHECK_STATUS(va::run_pass(ctx, plan2, d_t2, cq, d_lq2, ivf, 1, d_thr, d_cnt, k2, i2, uint32_t(cap2)));
+    VA_CHECK_STATUS(va::run_pass(ctx, plan2, d_t2, cq, n_ovf, d_lq2, ivf, 1, d_thr, d_cnt, k2, i2, uint32_t(cap2)));
     va::SelectArgs a;
     a.keys = k2;
     a.ids = i2;
