@@ -321,8 +321,10 @@ __global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) 
         // Count this lane's passing keys, reserve them with one atomic, then write them.
         const uint32_t thr = a.thr[qi];
         uint64_t pass = 0;  // bit 16b + 4j + e
-        // keys are recomputed for the (rare) passing values when they are written rather than
-        // kept for all 64, which keeps the epilogue within the main loop's register budget
+        // The direct-load kernel recomputes the keys of the (rare) passing values when it
+        // writes them, which keeps its epilogue near the main loop's register budget; the
+        // register-staged kernel keeps all 64.
+        uint32_t keys[DMA ? 1 : 64];
 #pragma unroll
         for (int b = 0; b < 4; ++b)
 #pragma unroll
@@ -332,6 +334,7 @@ __global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) 
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const uint32_t key = key_of_float(apply_op(a.op, acc[b][4 * j + e], qq, xx[e]));
+                    if constexpr (!DMA) keys[16 * b + 4 * j + e] = key;
                     const bool p = (uint32_t(wn * 128 + mloc + e) < rc) & (key <= thr);
                     pass |= uint64_t(p) << (16 * b + 4 * j + e);
                 }
@@ -345,8 +348,12 @@ __global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) 
                     const int b = t >> 4, j = (t >> 2) & 3, e = t & 3;
                     const uint32_t p = rs + uint32_t(wn * 128 + b * 32 + 8 * j + 4 * hh + e) * rstride;
                     const int64_t o = int64_t(qi) * a.cap + pos;
-                    const float xx = nrm[wave * 128 + b * 32 + 8 * j + 4 * hh + e];
-                    a.cand_key[o] = key_of_float(apply_op(a.op, acc[b][t & 15], qq, xx));
+                    if constexpr (DMA) {
+                        const float xx = nrm[wave * 128 + b * 32 + 8 * j + 4 * hh + e];
+                        a.cand_key[o] = key_of_float(apply_op(a.op, acc[b][t & 15], qq, xx));
+                    } else {
+                        a.cand_key[o] = keys[t];
+                    }
                     a.cand_id[o] = a.ids ? a.ids[p] : a.id_base + p;
                 }
                 ++pos;
