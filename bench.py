@@ -133,7 +133,7 @@ def run_c2(ctx, a, cpu: bool, extra_l2: bool):
             "bound": "mfma", "achieved": tflops, "peak": PEAK["fp32_mfma_tflops"], "unit": "TFLOP/s",
             "frac": tflops / PEAK["fp32_mfma_tflops"], "traffic": measured_traffic(),
             "traffic_source": "profiles/hbm_traffic__dist_gemm_filter__configs1_cosine_top100.txt",
-            "kernel": "dist_gemm_kernel<4, true, 2> (filtering scan)",
+            "kernel": "dist_gemm_kernel<4, 1, true, 2, true> (filtering scan)",
             "algorithmic": f"2*Q*N*D = {flops:.4g} FLOP per launch",
         },
     }

@@ -318,42 +318,41 @@ __global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) 
     const uint32_t orow = qs + li;                                   // dense output row
     const uint32_t qi = (OUT == OUT_FILTER && a.qrow) ? a.qrow[orow] : orow;  // query id (filter)
     if (OUT == OUT_FILTER) {
-        // Count this lane's passing keys, reserve them with one atomic, then write them.
         const uint32_t thr = a.thr[qi];
-        uint64_t pass = 0;  // bit 16b + 4j + e
-        // The direct-load kernel recomputes the keys of the (rare) passing values when it
-        // writes them, which keeps its epilogue near the main loop's register budget; the
-        // register-staged kernel keeps all 64.
-        uint32_t keys[DMA ? 1 : 64];
+        // Keys of passing values are reserved with one atomic and written; the direct-load
+        // kernel does this for half of the lane's 64 values at a time, which keeps its
+        // epilogue within the main loop's 128-VGPR budget (4 waves per SIMD).
+        constexpr int HALVES = DMA ? 2 : 1;
+        constexpr int NB = 4 / HALVES;  // MFMA blocks per half
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+        for (int h = 0; h < HALVES; ++h) {
+            uint64_t pass = 0;  // bit 16(b - NB h) + 4j + e
+            uint32_t keys[16 * NB];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int mloc = b * 32 + 8 * j + 4 * hh;
-                const f32x4v xx = *reinterpret_cast<const f32x4v*>(nrm + wave * 128 + mloc);
+            for (int bb = 0; bb < NB; ++bb)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t key = key_of_float(apply_op(a.op, acc[b][4 * j + e], qq, xx[e]));
-                    if constexpr (!DMA) keys[16 * b + 4 * j + e] = key;
-                    const bool p = (uint32_t(wn * 128 + mloc + e) < rc) & (key <= thr);
-                    pass |= uint64_t(p) << (16 * b + 4 * j + e);
+                for (int j = 0; j < 4; ++j) {
+                    const int b = NB * h + bb;
+                    const int mloc = b * 32 + 8 * j + 4 * hh;
+                    const f32x4v xx = *reinterpret_cast<const f32x4v*>(nrm + wave * 128 + mloc);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t key = key_of_float(apply_op(a.op, acc[b][4 * j + e], qq, xx[e]));
+                        keys[16 * bb + 4 * j + e] = key;
+                        const bool p = (uint32_t(wn * 128 + mloc + e) < rc) & (key <= thr);
+                        pass |= uint64_t(p) << (16 * bb + 4 * j + e);
+                    }
                 }
-            }
-        if (pass) {
+            if (!pass) continue;
             uint32_t pos = atomicAdd(a.cnt + qi, uint32_t(__popcll(pass)));
 #pragma unroll
-            for (int t = 0; t < 64; ++t) {
+            for (int t = 0; t < 16 * NB; ++t) {
                 if (!((pass >> t) & 1)) continue;
                 if (pos < a.cap) {
-                    const int b = t >> 4, j = (t >> 2) & 3, e = t & 3;
+                    const int b = NB * h + (t >> 4), j = (t >> 2) & 3, e = t & 3;
                     const uint32_t p = rs + uint32_t(wn * 128 + b * 32 + 8 * j + 4 * hh + e) * rstride;
                     const int64_t o = int64_t(qi) * a.cap + pos;
-                    if constexpr (DMA) {
-                        const float xx = nrm[wave * 128 + b * 32 + 8 * j + 4 * hh + e];
-                        a.cand_key[o] = key_of_float(apply_op(a.op, acc[b][t & 15], qq, xx));
-                    } else {
-                        a.cand_key[o] = keys[t];
-                    }
+                    a.cand_key[o] = keys[t];
                     a.cand_id[o] = a.ids ? a.ids[p] : a.id_base + p;
                 }
                 ++pos;
