@@ -219,7 +219,7 @@ def run_c3(ctx, a, cpu: bool):
         "quantize_database_ms": qms,
         "quantize_hbm_gbs": (N * D * 4 * 2 + N * D) / (qms * 1e-3) / 1e9,
         "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK["int8_mfma_tops"], "unit": "TOP/s",
-                     "frac": tops / PEAK["int8_mfma_tops"], "kernel": "i8_dma_kernel<true>",
+                     "frac": tops / PEAK["int8_mfma_tops"], "kernel": "i8_resq_kernel<512>",
                      "algorithmic": f"2*Q*N*D = {ops:.4g} int ops per launch"},
     }
     log(f"configs[2] int8 top-10: {ms:.3f} ms/step = {res['qps']:.0f} QPS; scan {ph['scan_ms']:.3f} ms = "

@@ -130,6 +130,22 @@ def test_i8_scan_topk_bit_exact(ctx, oracle, Q, N, D, k):
     check_topk_exact(gi, gd, oi, od)
 
 
+@pytest.mark.parametrize("Q,N,D,k", [(300, 6000, 96, 20), (260, 4000, 512, 10), (700, 3000, 256, 40)])
+def test_i8_large_q_many_passes(ctx, oracle, Q, N, D, k):
+    """Large-Q filter scan where every query has hundreds of tied passes (the database is 40
+    distinct rows repeated): each wave stages and flushes many batches of passes, and ties are
+    broken by the smaller id.  D=96 also has a zero-padding k-step."""
+    from vectoraccelerate_amd import ScalarQuantizationKernel
+
+    g = rng(Q * 7 + D)
+    base = g.integers(-128, 128, (40, D)).astype(np.int8)
+    xc = base[g.integers(0, 40, N)]
+    qc = g.integers(-128, 128, (Q, D)).astype(np.int8)
+    gi, gd = ScalarQuantizationKernel(ctx).searchTopK(qc, xc, k)
+    oi, od = oracle.i8_topk(qc, xc, k)
+    check_topk_exact(gi, gd, oi, od)
+
+
 def test_i8_sampled_and_overflow_paths(ctx, oracle):
     from vectoraccelerate_amd import ScalarQuantizationKernel, _lib
 

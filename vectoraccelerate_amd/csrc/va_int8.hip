@@ -644,16 +644,307 @@ va_status launch_i8_dma(va_context* ctx, const I8Args& a) {
     return VA_OK;
 }
 
+// ---------------------------------------------------------------------------------------
+// int8 filter scan with resident queries (large Q, d <= 512)
+// ---------------------------------------------------------------------------------------
+// A workgroup keeps 256 queries resident in LDS for its whole life and streams a contiguous
+// range of database tiles past them.  Each of its eight waves owns 32 rows of a 256-row tile
+// and moves them through a private 3-slot LDS ring (a slot is one 32-byte k-step of its 32
+// rows, 1 KiB) by direct buffer loads issued two k-steps ahead.  Nothing but the initial
+// query load is shared between waves, so the main loop has no workgroup barrier: with one
+// 8-wave workgroup per CU (the queries take 128 KiB of the 160 KiB LDS) a barrier per k-step
+// cost about a third of the MFMA rate.  Wave tile 256 queries x 32 rows = 8 MFMA blocks (128
+// accumulators); the operands of k-step t+1 are read from LDS while the MFMAs of step t run.
+// Workgroup w runs on XCD w % 8 and the q-blocks that share a database range sit on one XCD,
+// so a range comes from HBM once per XCD L2 and then from L2 for the other q-blocks.
+// Filter passes are staged in a per-wave LDS list and appended to the per-query candidate
+// lists only when the list fills (and at the end): a global reservation is an atomic whose
+// result the wave must wait for, and even plain stores count in the same in-order wait
+// counter as the stage loads, so writing passes out at every tile stalled the stream.
+namespace resq {
+constexpr int TQ = 256, NW = 8, WR = 32, NS = 3, SLOT = WR * 32;
+constexpr int TN = NW * WR;           // rows per tile
+constexpr int RING = NW * NS * SLOT;  // 24 KiB
+constexpr int LCAP = 80;              // staged passes per wave
+constexpr int STAGE = NW * LCAP * 12;
+template <int QS>
+constexpr int lds_bytes() { return TQ * QS + RING + STAGE; }
+}  // namespace resq
+
+template <int QS>
+__global__ __launch_bounds__(512, 2) void i8_resq_kernel(I8Args a, uint32_t R) {
+    using namespace resq;
+    constexpr int QBYTES = TQ * QS;
+    constexpr int RPI = 1024 / QS;  // query rows per 1 KiB load instruction
+    constexpr int CPR = QS / 16;    // 16-byte chunks per resident query row
+    extern __shared__ __attribute__((aligned(16))) char lds8[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, hh = lane >> 5;
+
+    const uint32_t nqb = (a.Q + TQ - 1) / TQ;
+    const uint32_t xcd = blockIdx.x % kXcds, seq = blockIdx.x / kXcds;
+    const uint32_t qb = seq % nqb;
+    const uint32_t range = (seq / nqb) * kXcds + xcd;
+    const uint32_t ntiles = (a.N + TN - 1) / TN;
+    const uint32_t tpr = (ntiles + R - 1) / R;
+    const uint32_t t0 = range * tpr;
+    if (t0 >= ntiles) return;  // the whole workgroup: no range left
+    const uint32_t tcount = min(tpr, ntiles - t0);
+    const uint32_t q0 = qb * TQ;
+    const uint32_t qn = min(uint32_t(TQ), a.Q - q0);
+    const uint32_t lds0 = lds_addr_of(lds8);
+
+    // Resident queries: row r at r * QS, its 16-byte chunk c at position c ^ (r & 15), so the
+    // 16 rows one ds_read_b128 clock serves fall in 16 distinct bank groups.  Rows past Q and
+    // chunks past D load as zeros.
+    {
+        const dma_rsrc qres = make_dma_rsrc(a.q + int64_t(q0) * a.ldq, uint32_t(int64_t(qn - 1) * a.ldq + a.D));
+        for (int m = wave; m < TQ / RPI; m += NW) {
+            const int row = m * RPI + lane / CPR;
+            const int c = (lane % CPR) ^ (row & 15);
+            const uint32_t voff = (uint32_t(row) < qn && uint32_t(16 * c) < a.D)
+                                      ? uint32_t(int64_t(row) * a.ldq) + uint32_t(16 * c)
+                                      : kDmaSkip;
+            lds_dma16(qres, voff, lds0 + uint32_t(m) * 1024u);
+        }
+    }
+    // A value passes when its dot is >= the query's bound (the threshold key turned back into
+    // an int32 dot); padding queries never pass.
+    int32_t bound[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const uint32_t ql = uint32_t(u * 32 + l32);
+        const int32_t t = i32_of_key(a.thr[q0 + (ql < qn ? ql : 0u)]);
+        bound[u] = (ql >= qn || t == INT32_MIN) ? INT32_MAX : -t;
+    }
+    wait_vmcnt<0>();
+    __syncthreads();  // resident queries visible; the only workgroup barrier
+
+    // ---- this wave's database stream ------------------------------------------------------
+    const uint32_t nst = (a.D + 63) / 64 * 2;  // k-steps per tile, even (a padding step loads zeros)
+    const uint32_t steps = tcount * nst;
+    const uint32_t ring = lds0 + uint32_t(QBYTES) + uint32_t(wave) * uint32_t(NS * SLOT);
+    const char* ringp = lds8 + QBYTES + wave * (NS * SLOT);
+    // DMA lane map: row lane / 2; slot position lane & 1 holds the row's 16-byte chunk
+    // (lane & 1) ^ ((row >> 3) & 1), which keeps rows r and r + 8 apart in the banks.
+    const int drow = lane >> 1;
+    const uint32_t dcol = 16u * uint32_t((lane & 1) ^ ((drow >> 3) & 1));
+    const uint32_t drow_off = uint32_t(int64_t(drow) * a.ldx);
+    uint32_t ltile = 0, lst = 0, lslot = 0;
+    dma_rsrc xres = make_dma_rsrc(a.x, 0u);
+    auto issue = [&]() {
+        if (lst == 0) {  // a new tile: rebase the descriptor on this wave's 32 rows
+            const uint64_t r0 = uint64_t(t0 + ltile) * TN + uint32_t(wave) * WR;
+            const uint32_t rows = r0 < a.N ? uint32_t(min(uint64_t(WR), uint64_t(a.N) - r0)) : 0u;
+            xres = make_dma_rsrc(a.x + int64_t(r0) * a.ldx, rows ? uint32_t(int64_t(rows - 1) * a.ldx + a.D) : 0u);
+        }
+        const uint32_t d = lst * 32 + dcol;
+        lds_dma16(xres, d < a.D ? drow_off + d : kDmaSkip, ring + lslot * uint32_t(SLOT));
+        lslot = lslot == NS - 1 ? 0u : lslot + 1;
+        if (++lst == nst) {
+            lst = 0;
+            ++ltile;
+        }
+    };
+
+    // Operand reads: query block u row 32u + l32, database row l32, k-chunk 2 * step + hh.
+    // One register set: the query fragment u of k-step t+1 is read right after the MFMA of
+    // step t that consumed fragment u (eight MFMAs cover the read latency); the database
+    // fragment alternates between two registers.  The first k-step of a tile starts from a
+    // zero accumulator (inline constant), so tiles need no clearing pass.
+    const char* qrd = lds8 + l32 * QS;
+    const int xrd = l32 * 32 + 16 * (hh ^ ((l32 >> 3) & 1));
+    auto rd_q = [&](uint32_t st, int u) {
+        const int cq = (int(st) * 2 + hh) ^ (l32 & 15);
+        return *reinterpret_cast<const i32x4v*>(qrd + u * 32 * QS + 16 * cq);
+    };
+    auto rd_x = [&](uint32_t slot) { return *reinterpret_cast<const i32x4v*>(ringp + slot * SLOT + xrd); };
+
+    i32x16 acc[8];
+
+    // ---- filter epilogue ------------------------------------------------------------------
+    uint32_t* s_qi = reinterpret_cast<uint32_t*>(lds8 + QBYTES + RING) + wave * 3 * LCAP;
+    uint32_t* s_key = s_qi + LCAP;
+    uint32_t* s_id = s_key + LCAP;
+    uint32_t lc = 0;  // staged passes (wave-uniform)
+    uint32_t mtile = 0;
+    // Appends the staged passes to the candidate lists: count every pass, keep a query's first
+    // cap.  The reservations are waited for once per 64 entries.
+    auto flush = [&]() {
+        for (uint32_t b0 = 0; b0 < lc; b0 += 64) {
+            const uint32_t e = b0 + uint32_t(lane);
+            if (e < lc) {
+                const uint32_t qi = s_qi[e];
+                const uint32_t pos = atomicAdd(a.cnt + qi, 1u);
+                if (pos < a.cap) {
+                    a.cand_key[int64_t(qi) * a.cap + pos] = s_key[e];
+                    a.cand_id[int64_t(qi) * a.cap + pos] = s_id[e];
+                }
+            }
+        }
+        lc = 0;
+    };
+    // Lane value v of an MFMA block is row 8 * (v >> 2) + 4 * hh + (v & 3) of the wave's 32.
+    // Passes are rare, so the test is cheap first (a lane's 16 values of a query reduced to a
+    // maximum, one wave-wide vote per query block) and exact only where that vote passes: one
+    // vote per value position, then a rolled loop over the positions some lane passes at (a
+    // wave-uniform position, so the value is read with an indexed register move).  Rows past
+    // N hold zero dots and are rejected there.  The code stays compact: an unrolled test of all
+    // 128 positions with the append logic inlined in each outgrew the instruction cache and the
+    // register budget.
+    auto epilogue = [&]() {
+        const uint64_t r64 = uint64_t(t0 + mtile) * TN + uint32_t(wave) * WR;
+        const uint32_t r0 = uint32_t(r64);  // ids of rows below N fit 32 bits
+        const int32_t lim = int32_t(r64 < a.N ? min(uint64_t(a.N) - r64, uint64_t(WR)) : 0) - 4 * hh;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int32_t b = bound[u];
+            int32_t m = acc[u][0];
+#pragma unroll
+            for (int v = 1; v < 16; ++v) m = max(m, acc[u][v]);
+            if (!__ballot(m >= b)) continue;
+            const uint32_t qi = q0 + uint32_t(u * 32 + l32);
+            // value positions where some lane passes (wave-uniform bits)
+            uint32_t vm = 0;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) vm |= __ballot(acc[u][v] >= b) ? (1u << v) : 0u;
+#pragma unroll 1
+            while (vm) {
+                const uint32_t v = __builtin_ctz(vm);
+                vm &= vm - 1;
+                const int32_t dot = acc[u][v];
+                const uint32_t roff = 8 * (v >> 2) + (v & 3);
+                const bool p = dot >= b && int32_t(roff) < lim;
+                const uint64_t mk = __ballot(p);
+                if (!mk) continue;
+                const uint32_t n = uint32_t(__popcll(mk));
+                if (lc + n > uint32_t(LCAP)) flush();  // wave-uniform
+                if (p) {
+                    const uint32_t e =
+                        lc + __builtin_amdgcn_mbcnt_hi(uint32_t(mk >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mk), 0u));
+                    s_qi[e] = qi;
+                    s_key[e] = key_of_i32(-dot);
+                    s_id[e] = r0 + roff + 4 * uint32_t(hh);
+                }
+                lc += n;
+            }
+        }
+    };
+
+    // ---- main loop ------------------------------------------------------------------------
+    // k-steps run in pairs; nst is even, so a tile ends only after the second of a pair and the
+    // epilogue has one call site.
+    for (int i = 0; i < NS - 1; ++i)
+        if (uint32_t(i) < steps) issue();
+    i32x4v bq[8], xa, xb;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) bq[u] = rd_q(0, u);
+    {
+        const uint32_t after = min(uint32_t(NS - 1), steps) - 1;  // stages issued after stage 0
+        if (after >= 1) wait_vmcnt<1>();
+        else wait_vmcnt<0>();
+    }
+    xa = rd_x(0);
+    uint32_t mst = 0;  // k-step within the tile
+    // k-step t with database fragment cx; reads the next step's operands: the database
+    // fragment first (a whole step ahead of its use), then each query fragment right after the
+    // MFMA that consumed its register.
+    auto step = [&](uint32_t t, const i32x4v& cx, i32x4v& nx, bool first) {
+        // Refills the slot of stage t-1, read at the start of step t-2; 17 LDS reads were
+        // issued after that one and at most 15 can be outstanding, so it has completed.
+        if (t + NS - 1 < steps) issue();
+        if (t + 1 < steps) {
+            const uint32_t after = min(t + NS, steps) - (t + 2);  // stages issued after stage t+1
+            if (after >= 1) wait_vmcnt<1>();
+            else wait_vmcnt<0>();
+            nx = rd_x((t + 1) % NS);
+        }
+        const uint32_t nst1 = mst + 1 == nst ? 0u : mst + 1;  // k-step of t+1 within its tile
+        if (first) {
+            const i32x16 z = {};
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                acc[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cx, bq[u], z, 0, 0, 0);
+                bq[u] = rd_q(nst1, u);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                acc[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cx, bq[u], acc[u], 0, 0, 0);
+                bq[u] = rd_q(nst1, u);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+        }
+        mst = nst1;
+    };
+    for (uint32_t t = 0; t < steps; t += 2) {
+        if (mst == 0) step(t, xa, xb, true);
+        else step(t, xa, xb, false);
+        step(t + 1, xb, xa, false);
+        if (mst == 0) {
+            epilogue();
+            ++mtile;
+        }
+    }
+    flush();
+}
+
+// The resident-query scan needs dense 16-byte query and database rows, d <= 512, enough
+// queries to fill a 256-query block reasonably, and 32-bit descriptor offsets within a
+// 256-query block and within a wave's 32 rows.
+bool resq_ok(const I8Args& a, bool vec) {
+#ifndef VA_I8_RESQ
+#define VA_I8_RESQ 1
+#endif
+    return VA_I8_RESQ && vec && !a.qrow && a.Q > 192 && a.D <= 512 &&
+           uint64_t(resq::TQ - 1) * uint64_t(a.ldq) + a.D <= kDmaMaxBytes &&
+           uint64_t(resq::WR - 1) * uint64_t(a.ldx) + a.D <= kDmaMaxBytes;
+}
+
+va_status launch_i8_resq(va_context* ctx, const I8Args& a) {
+    using namespace resq;
+    // one workgroup per CU (LDS-bound), the number of ranges a multiple of the XCD count
+    const uint32_t nqb = (a.Q + TQ - 1) / TQ;
+    const uint32_t per = (uint32_t(std::max(ctx->num_cus, 8)) + nqb - 1) / nqb;
+    const uint32_t R = std::max<uint32_t>(kXcds, (per + kXcds - 1) / kXcds * kXcds);
+    const uint64_t grid = uint64_t(nqb) * R;
+    if (grid > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "int8 scan grid too large");
+    if (a.D <= 256) {
+        auto kern = &i8_resq_kernel<256>;
+        VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes<256>()));
+        kern<<<dim3(uint32_t(grid)), dim3(512), lds_bytes<256>(), ctx->stream>>>(a, R);
+    } else {
+        auto kern = &i8_resq_kernel<512>;
+        VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes<512>()));
+        kern<<<dim3(uint32_t(grid)), dim3(512), lds_bytes<512>(), ctx->stream>>>(a, R);
+    }
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
 template <int QBW, int WQ, int WN>
 va_status launch_i8_shape(va_context* ctx, const I8Args& a, bool vec, bool filter) {
     if (filter) return vec ? launch_i8_tile<QBW, WQ, WN, true, true>(ctx, a) : launch_i8_tile<QBW, WQ, WN, false, true>(ctx, a);
     return vec ? launch_i8_tile<QBW, WQ, WN, true, false>(ctx, a) : launch_i8_tile<QBW, WQ, WN, false, false>(ctx, a);
 }
 
+// whole, aligned 16-byte chunks in every query and database row
+bool i8_vec(const I8Args& a) {
+    return (a.D % 16 == 0) && (a.ldq % 16 == 0) && (a.ldx % 16 == 0) &&
+           ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
+}
+
 va_status launch_i8(va_context* ctx, const I8Args& a, bool filter) {
     if (a.Q == 0 || a.N == 0) return VA_OK;
-    const bool vec = (a.D % 16 == 0) && (a.ldq % 16 == 0) && (a.ldx % 16 == 0) &&
-                     ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
+    const bool vec = i8_vec(a);
+    if (filter && resq_ok(a, vec)) return launch_i8_resq(ctx, a);
 #ifndef VA_I8_DMA
 #define VA_I8_DMA 1
 #endif
@@ -696,7 +987,7 @@ struct I8Producer final : KeyProducer {
         a.ldo = ldo;
         return launch_i8(ctx, a, false);
     }
-    va_status filter(const uint32_t* thr, uint32_t* cnt, uint32_t* ckey, uint32_t* cid, uint32_t cap) override {
+    I8Args filter_args() const {
         I8Args a;
         a.q = q;
         a.ldq = D;
@@ -705,6 +996,10 @@ struct I8Producer final : KeyProducer {
         a.Q = Q;
         a.N = N;
         a.D = D;
+        return a;
+    }
+    va_status filter(const uint32_t* thr, uint32_t* cnt, uint32_t* ckey, uint32_t* cid, uint32_t cap) override {
+        I8Args a = filter_args();
         a.thr = thr;
         a.cnt = cnt;
         a.cand_key = ckey;

@@ -155,10 +155,18 @@ __device__ __forceinline__ dma_rsrc make_dma_rsrc(const void* base, uint32_t byt
 // that use this (the compiler keeps nothing in M0 on gfx9 across these loops); M0 is a
 // reserved register, whose clobbers the compiler does not honour, so it is not listed.
 __device__ __forceinline__ void lds_dma16(const dma_rsrc& rsrc, uint32_t voff, uint32_t lds_addr) {
+    // The operands are wave-uniform by contract; readfirstlane keeps them in SGPRs where the
+    // compiler's divergence analysis cannot prove it (a no-op for values already in SGPRs).
+    dma_rsrc r;
+    r[0] = __builtin_amdgcn_readfirstlane(rsrc[0]);
+    r[1] = __builtin_amdgcn_readfirstlane(rsrc[1]);
+    r[2] = __builtin_amdgcn_readfirstlane(rsrc[2]);
+    r[3] = __builtin_amdgcn_readfirstlane(rsrc[3]);
+    const uint32_t l = __builtin_amdgcn_readfirstlane(lds_addr);
     // one wait state between the M0 write and the LDS-DMA load that reads it
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                  :
-                 : "s"(lds_addr), "v"(voff), "s"(rsrc)
+                 : "s"(l), "v"(voff), "s"(r)
                  : "memory");
 }
 
