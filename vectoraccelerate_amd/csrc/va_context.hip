@@ -62,6 +62,28 @@ va_status fill_u32(va_context* ctx, uint32_t* p, uint64_t n, uint32_t v) {
     return VA_OK;
 }
 
+va_status aux_fork(va_context* ctx) {
+    if (!ctx->fork_ev) {
+        VA_CHECK_HIP(ctx, hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming));
+        for (int i = 0; i < va_context::kAux; ++i) {
+            // default priority, like the main stream
+            VA_CHECK_HIP(ctx, hipStreamCreateWithFlags(&ctx->aux[i], hipStreamNonBlocking));
+            VA_CHECK_HIP(ctx, hipEventCreateWithFlags(&ctx->join_ev[i], hipEventDisableTiming));
+        }
+    }
+    VA_CHECK_HIP(ctx, hipEventRecord(ctx->fork_ev, ctx->stream));
+    for (int i = 0; i < va_context::kAux; ++i) VA_CHECK_HIP(ctx, hipStreamWaitEvent(ctx->aux[i], ctx->fork_ev, 0));
+    return VA_OK;
+}
+
+va_status aux_join(va_context* ctx) {
+    for (int i = 0; i < va_context::kAux; ++i) {
+        VA_CHECK_HIP(ctx, hipEventRecord(ctx->join_ev[i], ctx->aux[i]));
+        VA_CHECK_HIP(ctx, hipStreamWaitEvent(ctx->stream, ctx->join_ev[i], 0));
+    }
+    return VA_OK;
+}
+
 DistOp metric_op(va_metric m) {
     switch (m) {
         case VA_METRIC_L2SQ: return OP_L2SQ;
@@ -142,6 +164,14 @@ va_status va_context_destroy(va_context* ctx) {
         if (ctx->host_word) (void)hipHostFree(ctx->host_word);
         for (auto& e : ctx->ev)
             if (e) (void)hipEventDestroy(e);
+        for (int i = 0; i < va_context::kAux; ++i) {
+            if (ctx->aux[i]) {
+                (void)hipStreamSynchronize(ctx->aux[i]);
+                (void)hipStreamDestroy(ctx->aux[i]);
+            }
+            if (ctx->join_ev[i]) (void)hipEventDestroy(ctx->join_ev[i]);
+        }
+        if (ctx->fork_ev) (void)hipEventDestroy(ctx->fork_ev);
         if (ctx->owns_stream) (void)hipStreamDestroy(ctx->stream);
     }
     delete ctx;

@@ -35,12 +35,26 @@ struct va_context {
     bool profiling = false;
     hipEvent_t ev[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
     va_scan_timings last_scan{};
+    // extra streams for independent launches that overlap (default priority); created on
+    // first use, with the events that fork them from and join them back into `stream`.  Three,
+    // so that with `stream` they fit HIP's default of four hardware queues per process
+    // (streams beyond that share a queue and serialise).
+    static constexpr int kAux = 3;
+    hipStream_t aux[kAux] = {nullptr, nullptr, nullptr};
+    hipEvent_t fork_ev = nullptr;
+    hipEvent_t join_ev[kAux] = {nullptr, nullptr, nullptr};
 };
 
 namespace va {
 
 // Records an error message on the context and returns the status.
 va_status fail(va_context* ctx, va_status st, const char* fmt, ...);
+
+// Makes every ctx->aux[i] wait for the work queued so far on ctx->stream (creating them on
+// first use).
+va_status aux_fork(va_context* ctx);
+// Makes ctx->stream wait for the work queued so far on every ctx->aux[i].
+va_status aux_join(va_context* ctx);
 
 // Makes `ctx->device` current for the lifetime of the guard.
 struct DeviceGuard {

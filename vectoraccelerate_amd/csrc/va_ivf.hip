@@ -113,6 +113,143 @@ struct F32Keys final : KeyProducer {
     }
 };
 
+// ---------------------------------------------------------------------------------------
+// Lists probed by few queries: 16-query tiles
+// ---------------------------------------------------------------------------------------
+// Most probed lists of an IVF search are probed by a handful of queries (configs[4]: 2,000 of
+// 2,550 lists by at most 16), so a 32-query MFMA tile of the distance kernel is mostly
+// padding there, and such a list's rows are read once per search anyway: the scan of these
+// lists is bound by streaming their rows from HBM, not by the MFMA.  This kernel covers a
+// tile of 16 queries x 128 rows per wave with v_mfma_f32_16x16x4f32 (8 blocks of 16 rows),
+// loads both operands straight from global memory into registers (no LDS staging, no
+// barrier: the four waves of a workgroup are independent tiles), and prefetches the next
+// 16-float k-chunk while the current one runs.  K mapping: in k-chunk c, lane l (query or
+// row l % 16, group g = l / 16) holds elements 16c + 4g .. 16c + 4g + 3 of its row as one
+// 16-byte load, and MFMA e of the chunk takes element e of it from both operands, so the four
+// lanes of a row read 64 contiguous bytes.  Squared norms accumulate on the VALU from the same
+// registers.  Filter epilogue as in the distance kernel (L2^2 keys, key <= tau).  Keys differ
+// in rounding from the 32-query kernel's, so a list takes the same kernel in every pass of a
+// search (its probing-query count decides).
+namespace ivfs {
+constexpr uint32_t TQ = 16, TN = 128, WAVES = 4;
+}
+typedef float f32x4s __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void ivf_small_kernel(DistArgs a) {
+    using namespace ivfs;
+    __shared__ __attribute__((aligned(16))) float xnorm[WAVES][TN];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+    const uint32_t tile = blockIdx.x * WAVES + uint32_t(wave);
+    if (tile >= a.ntiles) return;  // whole wave; the waves never synchronise
+    const uint32_t qs = a.tiles[4 * tile], qc = a.tiles[4 * tile + 1];
+    const uint32_t rs = a.tiles[4 * tile + 2], rc = a.tiles[4 * tile + 3];
+    const int j = lane & 15, g = lane >> 4;
+    const uint32_t D = a.D;
+    // this lane's query row (zeros past the tile's queries)
+    const bool qv = uint32_t(j) < qc;
+    const uint32_t qi = qv ? a.qrow[qs + j] : 0u;
+    const float* qp = a.q + int64_t(qi) * a.ldq;
+    // the tile's rows through a buffer descriptor: rows past rc read as zeros
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(a.x + int64_t(rs) * a.ldx), 0, int(uint32_t(rc) * uint32_t(a.ldx) * 4u), 0x00020000);
+    const uint32_t rowoff = uint32_t(j) * uint32_t(a.ldx) * 4u;  // byte offset of row j
+    const uint32_t blkoff = 16u * uint32_t(a.ldx) * 4u;          // 16 rows further
+    const uint32_t nch = (D + 31) / 32 * 2;  // even; chunks past D load zeros
+    f32x4s qa, qb, ra[8], rb[8];
+    // Branch-free loads (the compiler's wait counts stay exact, so chunk c+1 stays in flight
+    // while chunk c computes): past D or the tile's queries a load reads a valid address and
+    // is zeroed, past the tile's rows the descriptor returns zeros.
+    auto load = [&](uint32_t c, f32x4s& qv4, f32x4s(&rv)[8]) {
+        const uint32_t k = 16 * c + 4 * uint32_t(g);
+        const bool kin = k < D;  // D % 4 == 0: a 4-element group is whole or absent
+        const f32x4s t = *reinterpret_cast<const f32x4s*>(qp + (kin ? k : 0u));
+        const bool use = qv && kin;
+        qv4 = f32x4s{use ? t[0] : 0.f, use ? t[1] : 0.f, use ? t[2] : 0.f, use ? t[3] : 0.f};
+        const uint32_t vo = kin ? rowoff + 4 * k : 0x80000000u;
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+            rv[b] = __builtin_bit_cast(f32x4s, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   xr, kin ? vo + uint32_t(b) * blkoff : vo, 0, 0));
+    };
+    f32x4s acc[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) acc[b] = f32x4s{0.f, 0.f, 0.f, 0.f};
+    float xs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, qsum = 0.f;
+    auto compute = [&](const f32x4s& qv4, const f32x4s(&rv)[8]) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            qsum = fmaf(qv4[e], qv4[e], qsum);
+#pragma unroll
+            for (int b = 0; b < 8; ++b) xs[b] = fmaf(rv[b][e], rv[b][e], xs[b]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int b = 0; b < 8; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(rv[b][e], qv4[e], acc[b], 0, 0, 0);
+    };
+    // two register sets: the loads of chunk c+1 are in flight while chunk c computes (the
+    // scheduling barriers keep the compiler from hoisting a third set's loads)
+    load(0, qa, ra);
+    for (uint32_t c = 0; c < nch; c += 2) {
+        load(c + 1, qb, rb);
+        compute(qa, ra);
+        __builtin_amdgcn_sched_barrier(0);
+        load(c + 2, qa, ra);  // past the end: zeros, unused
+        compute(qb, rb);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // norms: the four k groups of a row or query hold partial sums
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        xs[b] += __shfl_xor(xs[b], 16);
+        xs[b] += __shfl_xor(xs[b], 32);
+    }
+    qsum += __shfl_xor(qsum, 16);
+    qsum += __shfl_xor(qsum, 32);
+    if (g == 0) {
+#pragma unroll
+        for (int b = 0; b < 8; ++b) xnorm[wave][16 * b + j] = xs[b];
+    }
+    // (one wave writes and reads its own LDS row: in order, no barrier)
+    if (!qv) return;
+    // lane (j, g) holds query j's dots with rows 16b + 4g + v, v < 4; two halves of four
+    // blocks keep the epilogue's registers within the main loop's
+    const uint32_t thr = a.thr[qi];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        uint32_t keys[16];
+        uint32_t pass = 0;
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) {
+            const int b = 4 * h + bb;
+            const f32x4s xx = *reinterpret_cast<const f32x4s*>(&xnorm[wave][16 * b + 4 * g]);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                float d = qsum + xx[v] - 2.0f * acc[b][v];  // L2^2; cancellation can leave a tiny negative
+                d = (d < 0.0f) ? 0.0f : d;
+                const uint32_t key = key_of_float(d);
+                keys[4 * bb + v] = key;
+                const bool p = (uint32_t(16 * b + 4 * g + v) < rc) & (key <= thr);
+                pass |= uint32_t(p) << (4 * bb + v);
+            }
+        }
+        if (!pass) continue;
+        uint32_t pos = atomicAdd(a.cnt + qi, uint32_t(__popc(pass)));
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            if (!((pass >> t) & 1)) continue;
+            if (pos < a.cap) {
+                const uint32_t r = rs + uint32_t(16 * (4 * h + (t >> 2)) + 4 * g + (t & 3));
+                const int64_t o = int64_t(qi) * a.cap + pos;
+                a.cand_key[o] = keys[t];
+                a.cand_id[o] = a.ids ? a.ids[r] : a.id_base + r;
+            }
+            ++pos;
+        }
+    }
+}
+
 // Tile descriptors {qs, qc, rs, rc} of one list-major pass, grouped by tile shape.  A tile of
 // wq x wn waves covers 32*wq queries x 128*wn rows.  A list with nq probing queries and n
 // rows gets the shape with the least estimated time: tiles x waves x the measured cost of
@@ -126,6 +263,10 @@ struct TilePlan {
     static constexpr int WN[NS] = {1, 2, 1, 1, 4};
     static constexpr uint32_t COST[NS] = {100, 120, 135, 175, 195};  // per wave tile, relative
     std::vector<uint32_t> t[NS];
+    std::vector<uint32_t> small;  // 16-query tiles (ivf_small_kernel)
+    // every group back to back, as uploaded by run_pass (kept with the plan, which outlives
+    // the asynchronous copy)
+    mutable std::vector<uint32_t> packed;
     static int shape_for(uint32_t nq, uint32_t nrows) {
         int best = 0;
         uint64_t best_cost = ~0ull;
@@ -139,9 +280,19 @@ struct TilePlan {
         }
         return best;
     }
-    // rows of a list: positions off + j, j < nrows
-    void add(uint32_t lq_start, uint32_t nq, uint32_t off, uint32_t nrows) {
+    // rows of a list: positions off + j, j < nrows; small_list: the list takes 16-query tiles
+    void add(uint32_t lq_start, uint32_t nq, uint32_t off, uint32_t nrows, bool small_list = false) {
         if (nq == 0 || nrows == 0) return;
+        if (small_list) {
+            for (uint32_t qb = 0; qb < nq; qb += ivfs::TQ)
+                for (uint32_t r = 0; r < nrows; r += ivfs::TN) {
+                    small.push_back(lq_start + qb);
+                    small.push_back(std::min(ivfs::TQ, nq - qb));
+                    small.push_back(off + r);
+                    small.push_back(std::min(ivfs::TN, nrows - r));
+                }
+            return;
+        }
         const int sh = shape_for(nq, nrows);
         const uint32_t TQ = dist_tile_queries(WQ[sh]), TN = dist_tile_rows(WN[sh]);
         auto& v = t[sh];
@@ -154,7 +305,7 @@ struct TilePlan {
             }
     }
     size_t words() const {
-        size_t w = 0;
+        size_t w = small.size();
         for (const auto& v : t) w += v.size();
         return w;
     }
@@ -165,11 +316,38 @@ struct TilePlan {
 va_status run_pass(va_context* ctx, const TilePlan& plan, uint32_t* dev_tiles, const float* q, uint32_t q_rows,
                    const uint32_t* lq, const va_ivf* ivf, uint32_t rstride, const uint32_t* thr, uint32_t* cnt,
                    uint32_t* ckey, uint32_t* cid, uint32_t cap) {
-    size_t off = 0;
-    for (int sh = 0; sh < TilePlan::NS; ++sh) {
-        const auto& v = plan.t[sh];
+    // One upload of every group's tile descriptors, then one launch per group.  The groups are
+    // independent (they meet only in the per-query atomics of the candidate lists), so the
+    // largest runs on the context's stream and the others on the auxiliary streams: the
+    // smaller launches leave most of the chip idle on their own, and the 16-query tiles stream
+    // their rows from HBM while the larger tiles are MFMA-bound.
+    constexpr int NG = TilePlan::NS + 1;  // group NS: the 16-query tiles
+    const std::vector<uint32_t>* groups[NG];
+    for (int sh = 0; sh < TilePlan::NS; ++sh) groups[sh] = &plan.t[sh];
+    groups[TilePlan::NS] = &plan.small;
+    std::vector<uint32_t>& all = plan.packed;
+    all.clear();
+    all.reserve(plan.words());
+    size_t goff[NG];
+    int ngroups = 0, biggest = -1;
+    for (int gi = 0; gi < NG; ++gi) {
+        goff[gi] = all.size();
+        all.insert(all.end(), groups[gi]->begin(), groups[gi]->end());
+        if (groups[gi]->empty()) continue;
+        ++ngroups;
+        if (biggest < 0 || groups[gi]->size() > groups[biggest]->size()) biggest = gi;
+    }
+    if (ngroups == 0) return VA_OK;
+    VA_CHECK_HIP(ctx, hipMemcpyAsync(dev_tiles, all.data(), all.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (ngroups > 1) VA_CHECK_STATUS(aux_fork(ctx));
+    hipStream_t const main_stream = ctx->stream;
+    int next_aux = 0;
+    va_status st = VA_OK;
+    for (int gi = 0; gi < NG && st == VA_OK; ++gi) {
+        const auto& v = *groups[gi];
         if (v.empty()) continue;
-        VA_CHECK_HIP(ctx, hipMemcpyAsync(dev_tiles + off, v.data(), v.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+        hipStream_t s = main_stream;
+        if (gi != biggest) s = ctx->aux[next_aux++ % va_context::kAux];
         DistArgs a;
         a.q = q;
         a.qrow = lq;
@@ -185,17 +363,41 @@ va_status run_pass(va_context* ctx, const TilePlan& plan, uint32_t* dev_tiles, c
         a.cand_key = ckey;
         a.cand_id = cid;
         a.cap = cap;
-        a.tiles = dev_tiles + off;
+        a.tiles = dev_tiles + goff[gi];
         a.ntiles = uint32_t(v.size() / 4);
         a.rstride = rstride;
         a.ids = ivf->ids;
-        a.wq = TilePlan::WQ[sh];
-        a.wn = TilePlan::WN[sh];
-        VA_CHECK_STATUS(launch_dist(ctx, a));
-        off += v.size();
+        if (gi == TilePlan::NS) {
+            const uint32_t blocks = (a.ntiles + ivfs::WAVES - 1) / ivfs::WAVES;
+            ivf_small_kernel<<<dim3(blocks), dim3(64 * ivfs::WAVES), 0, s>>>(a);
+            if (hipGetLastError() != hipSuccess) st = fail(ctx, VA_ERR_HIP, "ivf_small_kernel launch failed");
+        } else {
+            a.wq = TilePlan::WQ[gi];
+            a.wn = TilePlan::WN[gi];
+            ctx->stream = s;  // launch_dist enqueues on the context's stream
+            st = launch_dist(ctx, a);
+            ctx->stream = main_stream;
+        }
     }
-    return VA_OK;
+    if (ngroups > 1) {
+        const va_status j = aux_join(ctx);
+        if (st == VA_OK) st = j;
+    }
+    return st;
 }
+
+// A list takes 16-query tiles when few queries probe it (decided once per search from the
+// full probe lists, so every pass of the search scans the list with the same kernel).  Needs
+// whole, aligned 16-byte groups (D % 4 == 0) and 32-bit byte offsets within a tile.
+bool small_tiles_ok(const va_ivf* ivf, const float* q) {
+#ifndef VA_IVF_SMALL
+#define VA_IVF_SMALL 1
+#endif
+    return VA_IVF_SMALL && ivf->D % 4 == 0 && (reinterpret_cast<uintptr_t>(q) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(ivf->list_vectors) & 15) == 0 &&
+           uint64_t(ivfs::TN) * ivf->D * 4 + 16 <= 0x7FFFFFF0ull;
+}
+constexpr uint32_t kSmallListQueries = 16;
 
 }  // namespace
 }  // namespace va
@@ -365,13 +567,16 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
             if (l < C) lq[fillp[l]++] = q;
         }
     va::TilePlan sample_plan, main_plan;
+    const bool small_ok = va::small_tiles_ok(ivf, queries);
+    auto small_list = [&](uint32_t l) { return small_ok && lq_off[l + 1] - lq_off[l] <= va::kSmallListQueries; };
     for (uint32_t l = 0; l < C; ++l) {
         const uint32_t nq = lq_off[l + 1] - lq_off[l];
         const uint32_t n = off[l + 1] - off[l];
-        main_plan.add(lq_off[l], nq, off[l], n);
+        main_plan.add(lq_off[l], nq, off[l], n, small_list(l));
     }
     for (uint32_t l = 0; l < C; ++l)
-        sample_plan.add(lq_off[l], lq_off[l + 1] - lq_off[l], off[l], va::sample_rows(off[l + 1] - off[l]));
+        sample_plan.add(lq_off[l], lq_off[l + 1] - lq_off[l], off[l], va::sample_rows(off[l + 1] - off[l]),
+                        small_list(l));
     const uint64_t cap_s = std::max<uint64_t>(1, *std::max_element(sampled.begin(), sampled.end()));
     const uint64_t max_total = std::max<uint64_t>(1, *std::max_element(total.begin(), total.end()));
     // every list is sampled at rate >= 1/kSampleRate: a query's candidates stay near
@@ -458,7 +663,8 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
         lq2_off[l + 1] = uint32_t(lq2.size());
     }
     va::TilePlan plan2;
-    for (uint32_t l = 0; l < C; ++l) plan2.add(lq2_off[l], lq2_off[l + 1] - lq2_off[l], off[l], off[l + 1] - off[l]);
+    for (uint32_t l = 0; l < C; ++l)
+        plan2.add(lq2_off[l], lq2_off[l + 1] - lq2_off[l], off[l], off[l + 1] - off[l], small_list(l));
     Scratch f(ctx);
     const size_t need2 = Scratch::round(uint64_t(n_ovf) * ivf->D * 4) + Scratch::round(uint64_t(n_ovf) * 4) * 3 +
                          Scratch::round(lq2.size() * 4 + 4) + Scratch::round(plan2.words() * 4 + 4) +
