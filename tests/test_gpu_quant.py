@@ -272,7 +272,11 @@ def test_hamming_matrix_bit_exact(ctx, oracle, Q, N, W):
 
 
 @pytest.mark.parametrize("Q,N,W,k", [(1, 10, 1, 3), (32, 20000, 24, 100), (256, 5000, 24, 100), (7, 40000, 24, 10),
-                                     (3, 2000, 40, 5), (4, 100, 3, 200)])
+                                     (3, 2000, 40, 5), (4, 100, 3, 200),
+                                     # large Q (fp4 MFMA filter scan): ragged Q and N, every row width
+                                     # it takes, a database shorter than one 256-row tile
+                                     (300, 20000, 8, 10), (257, 3001, 16, 50), (513, 70000, 24, 100),
+                                     (450, 100, 24, 7)])
 def test_hamming_topk_bit_exact(ctx, oracle, Q, N, W, k):
     from vectoraccelerate_amd import HammingDistanceKernel
 
@@ -282,6 +286,29 @@ def test_hamming_topk_bit_exact(ctx, oracle, Q, N, W, k):
     gi, gd = HammingDistanceKernel(ctx).nearestNeighbors(q, x, k)
     oi, od = oracle.hamming_topk(q, x, k)
     check_topk_exact(gi, gd, oi, od)
+
+
+def test_hamming_large_q_many_ties_and_overflow(ctx, oracle):
+    """fp4 MFMA filter scan with hundreds of tied passes per query (40 distinct rows repeated),
+    repeated staging flushes, and a tiny candidate cap that sends queries to the rescan."""
+    from vectoraccelerate_amd import HammingDistanceKernel, _lib
+
+    g = rng(32)
+    base = g.integers(0, 2**32, (40, 24), dtype=np.uint64).astype(np.uint32)
+    x = base[g.integers(0, 40, 9000)]
+    q = g.integers(0, 2**32, (300, 24), dtype=np.uint64).astype(np.uint32)
+    q[7] = x[123]
+    oi, od = oracle.hamming_topk(q, x, 20)
+    for cap, sample in [(0, 0), (32, 1000)]:
+        try:
+            ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, cap)
+            ctx.set_option(_lib.VA_OPT_SAMPLE_ROWS, sample)
+            gi, gd = HammingDistanceKernel(ctx).nearestNeighbors(q, x, 20)
+        finally:
+            ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 0)
+            ctx.set_option(_lib.VA_OPT_SAMPLE_ROWS, 0)
+        check_topk_exact(gi, gd, oi, od)
+        assert gd[7, 0] == 0
 
 
 def test_hamming_sampled_and_overflow_paths(ctx, oracle):

@@ -153,8 +153,287 @@ __global__ __launch_bounds__(256) void hamming_scan_wide_kernel(HamArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Filter scan on the fp4 MFMA (large Q, rows of 8/16/24 words)
+// ---------------------------------------------------------------------------------------
+// Hamming distance as |a| + |b| - 2 a.b over {0,1} vectors: a.b is a dot product of bits,
+// which the gfx950 matrix cores compute exactly with every bit widened to an fp4 (e2m1)
+// value 0 or 1.0 (v_mfma_scale_f32_32x32x64_f8f6f4, unit scales, fp32 sums of integers
+// <= 1024).  fp4 runs the 32x32x64 MFMA at 8 dense TFLOP/s-equivalents per CU per clock pair
+// of the int8 rate, so the 2·Q·N·32W bit products cost a fraction of the xor + popcount
+// VALU scan, which is bound by VALU issue (two ops per word per pair).
+// Layout and pipeline follow i8_resq_kernel: a workgroup keeps 256 queries resident in LDS
+// (already widened: 16 bytes per 32-bit word, rows padded to 16W + 16 bytes, which puts the
+// 16 rows of one ds_read_b128 clock in 16 distinct bank groups) and streams a contiguous range
+// of 256-row tiles past them; each of its eight waves owns 32 rows of a tile and loads them
+// straight into registers (lane: row l % 32, half h = l / 32 of its words, 16-byte loads;
+// the next tile in flight while this one computes), widens one 32-bit word per k-step into
+// the A fragment and runs 8 MFMAs against the 8 resident query blocks.  K mapping: k-step s
+// takes word h·W/2 + s of the half, bit i of the word pairs with bit i of the same query
+// word (fragment nibble i).  No workgroup barrier after the query load.  Filter epilogue as
+// in i8_resq_kernel: a pass is d <= tau, i.e. 2 a.b - |x| >= |q| - tau, tested with a
+// per-lane maximum first; passes go to a per-wave LDS list flushed when full.
+namespace hmf {
+constexpr int TQ = 256, NW = 8, WR = 32, TN = NW * WR, LCAP = 80;
+constexpr int STAGE = NW * LCAP * 12;
+constexpr int PA = NW * WR * 4;  // per-wave row popcounts
+constexpr int PB = TQ * 4;       // query popcounts
+constexpr int qstride(int W) { return 16 * W + 16; }
+constexpr int rows_bytes(int W) { return NW * WR * (W + 1) * 4; }  // per-wave row words, rows W + 1 apart
+constexpr size_t lds_bytes(int W) { return size_t(TQ) * qstride(W) + STAGE + PA + PB + rows_bytes(W); }
+}  // namespace hmf
+
+// 8 bits -> 8 fp4 nibbles: bit i -> nibble i, 1 -> 1.0 (e2m1 0b0010), 0 -> 0
+__device__ __forceinline__ uint32_t widen8(uint32_t b) {
+    uint32_t t = b & 0xFFu;
+    t = (t | (t << 12)) & 0x000F000Fu;
+    t = (t | (t << 6)) & 0x03030303u;
+    t = (t | (t << 3)) & 0x11111111u;
+    return t << 1;
+}
+
+typedef int i32x8h __attribute__((ext_vector_type(8)));
+typedef int i32x4h __attribute__((ext_vector_type(4)));
+// an fp4 MFMA operand: the instruction reads the first four registers of the eight
+__device__ __forceinline__ i32x8h fp4_operand(const i32x4h& v) { return i32x8h{v[0], v[1], v[2], v[3], 0, 0, 0, 0}; }
+typedef float f32x16h __attribute__((ext_vector_type(16)));
+typedef float f32x4h __attribute__((ext_vector_type(4)));
+
+template <int W>
+__global__ __launch_bounds__(512, 2) void hamming_mfma_kernel(HamArgs a, uint32_t R) {
+    using namespace hmf;
+    constexpr int HW = W / 2;  // words per lane half = k-steps per tile
+    constexpr int QS = qstride(W);
+    extern __shared__ __attribute__((aligned(16))) char lds8[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, hh = lane >> 5;
+    const uint32_t Q = a.nq, N = a.cols;
+
+    const uint32_t nqb = (Q + TQ - 1) / TQ;
+    const uint32_t xcd = blockIdx.x % kXcds, seq = blockIdx.x / kXcds;
+    const uint32_t qb = seq % nqb;
+    const uint32_t range = (seq / nqb) * kXcds + xcd;
+    const uint32_t ntiles = (N + TN - 1) / TN;
+    const uint32_t tpr = (ntiles + R - 1) / R;
+    const uint32_t t0 = range * tpr;
+    if (t0 >= ntiles) return;  // the whole workgroup: no range left
+    const uint32_t tcount = min(tpr, ntiles - t0);
+    const uint32_t q0 = qb * TQ;
+    const uint32_t qn = min(uint32_t(TQ), Q - q0);
+
+    float* s_pa = reinterpret_cast<float*>(lds8 + TQ * QS + STAGE) + wave * WR;
+    float* s_pb = reinterpret_cast<float*>(lds8 + TQ * QS + STAGE + PA);
+    uint32_t* s_rw = reinterpret_cast<uint32_t*>(lds8 + TQ * QS + STAGE + PA + PB) + wave * WR * (W + 1);
+    // resident queries, widened: word w of query r -> chunk 2 (w % HW) + w / HW of row r
+    for (int e = tid; e < TQ * W; e += 512) {
+        const int r = e / W, w = e % W;
+        const uint32_t v = uint32_t(r) < qn ? a.q[uint64_t(q0 + r) * W + w] : 0u;
+        const int c = 2 * (w % HW) + w / HW;
+        const uint4 o = {widen8(v), widen8(v >> 8), widen8(v >> 16), widen8(v >> 24)};
+        *reinterpret_cast<uint4*>(lds8 + r * QS + 16 * c) = o;
+    }
+    for (int r = tid; r < TQ; r += 512) {
+        uint32_t pb = 0;
+        if (uint32_t(r) < qn)
+            for (int w = 0; w < W; ++w) pb += __popc(a.q[uint64_t(q0 + r) * W + w]);
+        s_pb[r] = float(pb);
+    }
+    __syncthreads();  // resident queries visible; the only workgroup barrier
+    // pass iff 2 a.b - |x| >= |q| - tau; tau >= 32 W passes everything; padding never passes
+    float cq[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const uint32_t ql = uint32_t(u * 32 + l32);
+        const uint32_t t = a.thr[q0 + (ql < qn ? ql : 0u)];
+        cq[u] = ql >= qn ? __builtin_inff() : (t >= uint32_t(32 * W) ? -__builtin_inff() : s_pb[ql] - float(t));
+    }
+
+    // ---- this wave's rows -------------------------------------------------------------------
+    // lane: row l32 of the wave's 32, words [hh HW, hh HW + HW); rows past N read as zeros
+    auto load_tile = [&](uint32_t lt, uint32_t (&xw)[HW]) {
+        const uint64_t r0 = uint64_t(t0 + lt) * TN + uint32_t(wave) * WR;
+        const uint32_t rows = r0 < N ? uint32_t(min(uint64_t(WR), uint64_t(N) - r0)) : 0u;
+        const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint32_t*>(a.x + r0 * W), 0, int(rows * uint32_t(W) * 4u), 0x00020000);
+        const uint32_t off = (uint32_t(l32) * W + uint32_t(hh) * HW) * 4u;
+#pragma unroll
+        for (int i = 0; i < HW / 4; ++i) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16u * i, 0, 0);
+            xw[4 * i] = uint32_t(v[0]);
+            xw[4 * i + 1] = uint32_t(v[1]);
+            xw[4 * i + 2] = uint32_t(v[2]);
+            xw[4 * i + 3] = uint32_t(v[3]);
+        }
+    };
+    const char* qrd = lds8 + l32 * QS + 16 * hh;
+    // The query fragments are the same for every tile; an opaque per-tile zero in their
+    // address keeps the compiler from hoisting all 8 x W/2 of them out of the tile loop into
+    // registers (it would spill them).
+    uint32_t qz = 0;
+    auto rd_q = [&](int st, int u) { return *reinterpret_cast<const i32x4h*>(qrd + qz + u * 32 * QS + 32 * st); };
+
+    // ---- filter epilogue ------------------------------------------------------------------
+    uint32_t* s_qi = reinterpret_cast<uint32_t*>(lds8 + TQ * QS) + wave * 3 * LCAP;
+    uint32_t* s_key = s_qi + LCAP;
+    uint32_t* s_id = s_key + LCAP;
+    uint32_t lc = 0;  // staged passes (wave-uniform)
+    auto flush = [&]() {
+        for (uint32_t b0 = 0; b0 < lc; b0 += 64) {
+            const uint32_t e = b0 + uint32_t(lane);
+            if (e < lc) {
+                const uint32_t qi = s_qi[e];
+                const uint32_t pos = atomicAdd(a.cnt + qi, 1u);
+                if (pos < a.cap) {
+                    a.cand_key[int64_t(qi) * a.cap + pos] = s_key[e];
+                    a.cand_id[int64_t(qi) * a.cap + pos] = s_id[e];
+                }
+            }
+        }
+        lc = 0;
+    };
+    f32x16h acc[8];
+    // lane value v of a block is row 8 (v >> 2) + 4 hh + (v & 3) of the wave's 32
+    auto epilogue = [&](uint32_t lt) {
+        const uint64_t r64 = uint64_t(t0 + lt) * TN + uint32_t(wave) * WR;
+        const uint32_t r0 = uint32_t(r64);  // ids of rows below N fit 32 bits
+        const int32_t lim = int32_t(r64 < N ? min(uint64_t(N) - r64, uint64_t(WR)) : 0) - 4 * hh;
+        float pv[16];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const f32x4h t = *reinterpret_cast<const f32x4h*>(s_pa + 8 * g + 4 * hh);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) pv[4 * g + e] = t[e];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const float c = cq[u];
+            float m = fmaf(2.0f, acc[u][0], -pv[0]);
+#pragma unroll
+            for (int v = 1; v < 16; ++v) m = fmaxf(m, fmaf(2.0f, acc[u][v], -pv[v]));
+            if (!__ballot(m >= c)) continue;
+            const uint32_t ql = uint32_t(u * 32 + l32);
+            uint32_t vm = 0;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) vm |= __ballot(fmaf(2.0f, acc[u][v], -pv[v]) >= c) ? (1u << v) : 0u;
+#pragma unroll 1
+            while (vm) {
+                const uint32_t v = __builtin_ctz(vm);
+                vm &= vm - 1;
+                const float dot = acc[u][v];
+                const float pa = pv[v];
+                const uint32_t roff = 8 * (v >> 2) + (v & 3);
+                const bool p = fmaf(2.0f, dot, -pa) >= c && int32_t(roff) < lim;
+                const uint64_t mk = __ballot(p);
+                if (!mk) continue;
+                const uint32_t n = uint32_t(__popcll(mk));
+                if (lc + n > uint32_t(LCAP)) flush();  // wave-uniform
+                if (p) {
+                    const uint32_t e =
+                        lc + __builtin_amdgcn_mbcnt_hi(uint32_t(mk >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mk), 0u));
+                    s_qi[e] = q0 + ql;
+                    s_key[e] = uint32_t(pa + s_pb[ql] - 2.0f * dot);  // exact: integers below 2^24
+                    s_id[e] = r0 + roff + 4 * uint32_t(hh);
+                }
+                lc += n;
+            }
+        }
+    };
+
+    // ---- main loop ------------------------------------------------------------------------
+    // A tile's row words go through a per-wave LDS buffer (rows W + 1 words apart: the 32 rows
+    // of one read fall in distinct banks), so the k-steps are a rolled loop that reads its word
+    // by step index; the epilogue of tile lt runs at the top of iteration lt + 1, where the
+    // accumulators reach it through the loop's back edge.  (Fully unrolled steps with the
+    // epilogue after them let the compiler sink each block's MFMA chain into the epilogue,
+    // which kept every step's fragments alive at once and spilled.)
+    uint32_t xw[HW], xn[HW];
+    load_tile(0, xw);
+    i32x4h bq[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) bq[u] = rd_q(0, u);
+    uint32_t* myrow = s_rw + l32 * (W + 1) + hh * HW;
+    auto widen_word = [&](uint32_t w) {
+        return fp4_operand(i32x4h{int(widen8(w)), int(widen8(w >> 8)), int(widen8(w >> 16)), int(widen8(w >> 24))});
+    };
+    for (uint32_t lt = 0; lt <= tcount; ++lt) {
+        if (lt > 0) epilogue(lt - 1);
+        if (lt == tcount) break;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(qz));
+        uint32_t pa = 0;
+#pragma unroll
+        for (int i = 0; i < HW; ++i) {
+            myrow[i] = xw[i];
+            pa += __popc(xw[i]);
+        }
+        load_tile(lt + 1 < tcount ? lt + 1 : lt, xn);  // the next tile in flight
+        // row popcounts: the two halves of a row
+        const float pr = float(pa + __shfl_xor(pa, 32));
+        if (hh == 0) s_pa[l32] = pr;
+        {  // k-step 0: accumulators start from zero
+            const i32x8h af = widen_word(myrow[0]);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                acc[u] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af, fp4_operand(bq[u]), f32x16h{}, 4, 4, 0, 127, 0, 127);
+                bq[u] = rd_q(HW > 1 ? 1 : 0, u);
+            }
+        }
+#pragma unroll 2
+        for (int st = 1; st < HW; ++st) {
+            const i32x8h af = widen_word(myrow[st]);
+            const int nxt = st + 1 < HW ? st + 1 : 0;  // the next tile starts at step 0
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                acc[u] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af, fp4_operand(bq[u]), acc[u], 4, 4, 0, 127, 0, 127);
+                bq[u] = rd_q(nxt, u);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < HW; ++i) xw[i] = xn[i];
+    }
+    flush();
+}
+
+// The fp4 MFMA filter scan needs whole 16-byte loads of each half row (W % 8 == 0), rows
+// whose widened queries fit the LDS with the row buffers (W <= 24), enough queries to fill a
+// 256-query block reasonably and dense rows.
+bool hmf_ok(const HamArgs& a) {
+#ifndef VA_HAM_MFMA
+#define VA_HAM_MFMA 1
+#endif
+    return VA_HAM_MFMA && !a.qrow && a.q0 == 0 && a.c0 == 0 && a.stride == 1 && a.nq > 192 &&
+           (a.W == 8 || a.W == 16 || a.W == 24) && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
+           uint64_t(a.cols) * a.W * 4 <= 0xFFFFFFFFFFFFull;
+}
+
+template <int W>
+va_status launch_hmf_w(va_context* ctx, const HamArgs& a) {
+    using namespace hmf;
+    const uint32_t nqb = (a.nq + TQ - 1) / TQ;
+    const uint32_t per = (uint32_t(std::max(ctx->num_cus, 8)) + nqb - 1) / nqb;
+    const uint32_t R = std::max<uint32_t>(kXcds, (per + kXcds - 1) / kXcds * kXcds);
+    const uint64_t grid = uint64_t(nqb) * R;
+    if (grid > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "Hamming scan grid too large");
+    auto kern = &hamming_mfma_kernel<W>;
+    VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes(W))));
+    kern<<<dim3(uint32_t(grid)), dim3(512), lds_bytes(W), ctx->stream>>>(a, R);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
+va_status launch_hmf(va_context* ctx, const HamArgs& a) {
+    switch (a.W) {
+        case 8: return launch_hmf_w<8>(ctx, a);
+        case 16: return launch_hmf_w<16>(ctx, a);
+        default: return launch_hmf_w<24>(ctx, a);
+    }
+}
+
 va_status launch_ham(va_context* ctx, const HamArgs& a, bool filter) {
     if (a.nq == 0 || a.cols == 0) return VA_OK;
+    if (filter && hmf_ok(a)) return launch_hmf(ctx, a);
     const dim3 grid((a.cols + 255) / 256);
     const bool aligned = (a.W & 3) == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0;
     if (a.W <= kMaxWords && (aligned || (a.W & 3) != 0)) {
