@@ -469,6 +469,8 @@ struct HamProducer final : KeyProducer {
     const uint32_t* q;
     const uint32_t* x;
     uint32_t Q, N, W;
+    // distances are at most 32 W
+    uint32_t key_bits() const override { return 32u - uint32_t(__builtin_clz(32u * W)); }
     va_status dense(const uint32_t* qrow, uint32_t q0, uint32_t nq, uint32_t c0, uint32_t cols, uint32_t stride,
                     uint32_t* out_k, int64_t ldo) override {
         HamArgs a;

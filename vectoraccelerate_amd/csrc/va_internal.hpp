@@ -285,6 +285,9 @@ struct SelectArgs {
     // overflow detection (candidate mode): rows whose count exceeds n are listed here
     uint32_t* overflow_count = nullptr;
     uint32_t* overflow_rows = nullptr;
+    // every key is below 2^key_bits (Hamming distances: a few bits); up to 11 bits the k-th
+    // smallest key comes from one histogram pass instead of four byte passes
+    uint32_t key_bits = 32;
 };
 va_status launch_select(va_context* ctx, const SelectArgs& a);
 
@@ -307,6 +310,8 @@ struct KeyProducer {
                             uint32_t stride, uint32_t* out_k, int64_t ldo) = 0;
     // filter pass over all queries and all rows
     virtual va_status filter(const uint32_t* thr, uint32_t* cnt, uint32_t* ckey, uint32_t* cid, uint32_t cap) = 0;
+    // every key the producer makes is below 2^key_bits()
+    virtual uint32_t key_bits() const { return 32; }
     virtual ~KeyProducer() = default;
 };
 

@@ -71,6 +71,7 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
     base.out_i32 = out.i32;
     base.out_key = out.key;
     base.key_kind = out.key_kind;
+    base.key_bits = kp.key_bits();
 
     // ---- plan ------------------------------------------------------------------------
     // Sample size: N/64 rows keeps ~64k candidates per query, but the dense sample costs Q*S
@@ -139,6 +140,7 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
         a.rows = nq;
         a.k = k;
         a.out_kth = thr + q0;
+        a.key_bits = kp.key_bits();
         VA_CHECK_STATUS(launch_select(ctx, a));
     }
     // ---- 2. filter --------------------------------------------------------------------

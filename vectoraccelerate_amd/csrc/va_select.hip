@@ -8,6 +8,8 @@
 // The (distance, index) order is the reference's tie rule (Metal4Common.h:142-159,
 // SearchAndRetrieval.metal:313-317); unlike topk_select_batch_kernel
 // (SearchAndRetrieval.metal:88-156, value-only compares) the result is deterministic.
+#include <algorithm>
+
 #include "va_internal.hpp"
 
 namespace va {
@@ -16,8 +18,14 @@ namespace {
 constexpr int SEL_THREADS = 256;
 constexpr uint32_t SEL_BUF = VA_MAX_K;  // winners buffer (k <= VA_MAX_K)
 
+// Rows of up to kSelCache keys are first copied into LDS (one pass with many loads in flight);
+// the radix passes then read LDS instead of re-reading the row from memory once per pass with
+// one load in flight per thread, which left a short row's workgroup waiting on memory latency.
+constexpr uint32_t kSelCache = 24576;  // 96 KiB
+
+template <bool CACHED>
 struct RowView {
-    const uint32_t* keys;
+    const uint32_t* keys;  // the row in memory, or its copy in LDS
     const uint32_t* ids;
     uint32_t n;
     __device__ uint32_t key(uint32_t i) const { return keys[i]; }
@@ -58,17 +66,75 @@ __device__ void find_digit(const uint32_t* hist, uint32_t need, uint32_t* s_digi
     }
 }
 
+// The bin of a histogram of nb <= 2048 bins holding the need-th item: each thread sums eight
+// bins, a block-wide scan of the sums, then the thread whose range holds the item finds it.
+__device__ void find_bin_wide(const uint32_t* hist, uint32_t nb, uint32_t need, uint32_t* s_digit,
+                              uint32_t* s_before, uint32_t* s_bin) {
+    __shared__ uint32_t wsum[SEL_THREADS / 64];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    uint32_t c[8], sum = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t b = uint32_t(tid) * 8 + i;
+        c[i] = b < nb ? hist[b] : 0u;
+        sum += c[i];
+    }
+    uint32_t incl = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = __shfl_up(incl, off);
+        if (lane >= off) incl += o;
+    }
+    if (lane == 63) wsum[w] = incl;
+    __syncthreads();
+    uint32_t base = 0;
+    for (int i = 0; i < w; ++i) base += wsum[i];
+    incl += base;
+    const uint32_t excl = incl - sum;
+    if (excl < need && need <= incl) {
+        uint32_t run = excl;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (run < need && need <= run + c[i]) {
+                *s_digit = uint32_t(tid) * 8 + i;
+                *s_before = run;
+                *s_bin = c[i];
+            }
+            run += c[i];
+        }
+    }
+}
+
+// Adds this lane's item to the histogram when m.  Keys of one search crowd into few digits
+// (the top bytes of nearby distances are equal; Hamming distances are below 1024), and 256
+// threads incrementing one LDS bin serialise: when every active lane of the wave adds to the
+// same bin, one lane adds the wave's count.
+__device__ __forceinline__ void hist_add(uint32_t* hist, bool m, uint32_t d) {
+    const uint32_t dd = m ? d : 0xFFFFFFFFu;
+    const uint32_t first = __builtin_amdgcn_readfirstlane(dd);
+    const uint64_t act = __ballot(1);
+    if (__ballot(dd == first) == act) {
+        if (first != 0xFFFFFFFFu && (threadIdx.x & 63) == uint32_t(__builtin_ctzll(act)))
+            atomicAdd(&hist[first], uint32_t(__popcll(act)));
+    } else if (m) {
+        atomicAdd(&hist[d], 1u);
+    }
+}
+
+template <bool CACHED>
 __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelectArgs a) {
     __shared__ uint32_t hist[256];
     __shared__ uint32_t s_digit, s_before, s_bin, s_cnt;
     __shared__ uint32_t okey[SEL_BUF];
     __shared__ uint32_t oid[SEL_BUF];
+    __shared__ uint32_t whist[2048];     // one-pass histogram of keys below 2^11
+    extern __shared__ uint32_t s_row[];  // CACHED: the row's keys
 
     const uint32_t row = blockIdx.x;
     const int tid = threadIdx.x;
     const uint32_t orow = a.row_map ? a.row_map[row] : row;
 
-    RowView rv;
+    RowView<CACHED> rv;
     rv.keys = a.keys + int64_t(row) * a.ld;
     rv.ids = a.ids ? a.ids + int64_t(row) * a.ld : nullptr;
     rv.n = a.n;
@@ -85,6 +151,24 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelectArgs a) {
         rv.n = c;
     }
     const uint32_t n = rv.n;
+    if (CACHED) {
+        // eight independent loads per thread per round
+        for (uint32_t i0 = 0; i0 < n; i0 += 8 * SEL_THREADS) {
+            uint32_t v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t i = i0 + uint32_t(j * SEL_THREADS + tid);
+                v[j] = i < n ? rv.keys[i] : 0u;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t i = i0 + uint32_t(j * SEL_THREADS + tid);
+                if (i < n) s_row[i] = v[j];
+            }
+        }
+        rv.keys = s_row;
+        __syncthreads();
+    }
     const uint32_t K = a.k < n ? a.k : n;
 
     uint32_t T = 0xFFFFFFFFu, Tid = 0xFFFFFFFFu;
@@ -93,12 +177,30 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelectArgs a) {
         // ---- phase 1: k-th smallest key ---------------------------------------------
         uint32_t prefix = 0, mask = 0, need = K;
         uint32_t eq = 0;
-        for (int shift = 24; shift >= 0; shift -= 8) {
+        int top = 24;  // first byte pass
+        if (a.key_bits <= 11) {
+            // small keys: one histogram over all key values
+            const uint32_t nb = 1u << a.key_bits;
+            for (uint32_t b = tid; b < nb; b += SEL_THREADS) whist[b] = 0;
+            __syncthreads();
+            // (a sentinel key, above every real one, lands in the top bin)
+            for (uint32_t i = tid; i < n; i += SEL_THREADS) hist_add(whist, true, min(rv.key(i), nb - 1u));
+            __syncthreads();
+            find_bin_wide(whist, nb, need, &s_digit, &s_before, &s_bin);
+            __syncthreads();
+            prefix = s_digit;
+            mask = 0xFFFFFFFFu;
+            need -= s_before;
+            eq = s_bin;
+            __syncthreads();
+            top = -8;  // no byte passes left
+        }
+        for (int shift = top; shift >= 0; shift -= 8) {
             hist[tid] = 0;
             __syncthreads();
             for (uint32_t i = tid; i < n; i += SEL_THREADS) {
                 const uint32_t k = rv.key(i);
-                if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+                hist_add(hist, (k & mask) == prefix, (k >> shift) & 255u);
             }
             __syncthreads();
             find_digit(hist, need, &s_digit, &s_before, &s_bin);
@@ -121,9 +223,9 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelectArgs a) {
                 hist[tid] = 0;
                 __syncthreads();
                 for (uint32_t i = tid; i < n; i += SEL_THREADS) {
-                    if (rv.key(i) != T) continue;
-                    const uint32_t id = rv.id(i);
-                    if ((id & im) == ip) atomicAdd(&hist[(id >> shift) & 255u], 1u);
+                    const bool t = rv.key(i) == T;
+                    const uint32_t id = t ? rv.id(i) : 0u;
+                    hist_add(hist, t && (id & im) == ip, (id >> shift) & 255u);
                 }
                 __syncthreads();
                 find_digit(hist, ineed, &s_digit, &s_before, &s_bin);
@@ -234,7 +336,15 @@ __global__ void merge_gather(const uint32_t* ai, const float* ad, const uint32_t
 va_status launch_select(va_context* ctx, const SelectArgs& a) {
     if (a.rows == 0) return VA_OK;
     if (a.k > SEL_BUF) return fail(ctx, VA_ERR_INVALID_ARG, "k=%u exceeds the maximum %u", a.k, SEL_BUF);
-    select_kernel<<<dim3(a.rows), dim3(SEL_THREADS), 0, ctx->stream>>>(a);
+    if (a.n <= kSelCache) {
+        const size_t lds = size_t(std::max<uint32_t>(a.n, 1)) * 4;
+        if (lds > 48 * 1024)
+            VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(&select_kernel<true>),
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+        select_kernel<true><<<dim3(a.rows), dim3(SEL_THREADS), lds, ctx->stream>>>(a);
+    } else {
+        select_kernel<false><<<dim3(a.rows), dim3(SEL_THREADS), 0, ctx->stream>>>(a);
+    }
     VA_CHECK_LAUNCH(ctx);
     return VA_OK;
 }
