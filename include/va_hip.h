@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define VA_HIP_ABI_VERSION 1
+#define VA_HIP_ABI_VERSION 2
 #define VA_SENTINEL_INDEX 0xFFFFFFFFu
 /* largest k accepted by the top-K entry points */
 #define VA_MAX_K 1024u
@@ -81,8 +81,12 @@ const char* va_last_error_message(const va_context* ctx);
  * role of Metal4FusedL2Config's maxDistanceMatrixBytes / enableChunkedFallback
  * (Kernels/Metal4/FusedL2TopKKernel.swift:91-136): CANDIDATE_CAP bounds the per-query
  * candidate list (rows that overflow it take the exact chunked path), SAMPLE_ROWS sets the
- * size of the threshold sample (>= num_database forces the dense path). */
-typedef enum { VA_OPT_CANDIDATE_CAP = 1, VA_OPT_SAMPLE_ROWS = 2 } va_option;
+ * size of the threshold sample (>= num_database forces the dense path).  SCREEN selects the
+ * filtering scan of va_fused_topk: 0 = automatic (fp16 screening pass with an exact fp32
+ * rerank wherever it applies), 1 = never screen (fp32 scan only), 2 = screen whenever the
+ * metric and layout allow it.  Screening changes no result: the ids and distances are the
+ * fp32 scan's, bit for bit. */
+typedef enum { VA_OPT_CANDIDATE_CAP = 1, VA_OPT_SAMPLE_ROWS = 2, VA_OPT_SCREEN = 3 } va_option;
 va_status va_context_set_option(va_context* ctx, va_option option, uint64_t value);
 
 /* Phase timings of the last top-k scan, from hipEvents on the context stream.  Replaces
@@ -99,6 +103,8 @@ typedef struct {
     uint32_t candidate_cap; /* per-query candidate capacity                            */
     uint32_t overflow_rows; /* queries that took the exact chunked path               */
     uint32_t scan_launches; /* number of scan-kernel launches timed in scan_ms        */
+    uint32_t screened;      /* 1 when an fp32 search ran the fp16 screening scan      */
+    uint32_t rerank_rows;   /* screened search: rows re-scored exactly, all queries   */
 } va_scan_timings;
 va_status va_context_set_profiling(va_context* ctx, int enable);
 va_status va_context_last_scan(const va_context* ctx, va_scan_timings* out);

@@ -27,6 +27,7 @@ VA_SELECT_MAX = 1
 
 VA_OPT_CANDIDATE_CAP = 1
 VA_OPT_SAMPLE_ROWS = 2
+VA_OPT_SCREEN = 3
 
 VA_SENTINEL_INDEX = 0xFFFFFFFF
 VA_MAX_K = 1024
@@ -93,6 +94,8 @@ class ScanTimings(C.Structure):
         ("candidate_cap", C.c_uint32),
         ("overflow_rows", C.c_uint32),
         ("scan_launches", C.c_uint32),
+        ("screened", C.c_uint32),
+        ("rerank_rows", C.c_uint32),
     ]
 
     def as_dict(self) -> dict:

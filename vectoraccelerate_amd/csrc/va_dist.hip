@@ -120,16 +120,24 @@ __global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) 
     // XCD-aware order: workgroup w runs on XCD w % 8.  XCD x takes database tiles x, x+8, ...
     // and runs every query block of a tile back to back, so each tile crosses the fabric once
     // and is reused from that XCD's L2 (the grid is padded to a multiple of 8 tiles).
-    const uint32_t nqb = a.tiles ? 1u : (a.Q + T::TQ - 1) / T::TQ;
+    const uint32_t nqb = (a.tiles || a.gather) ? 1u : (a.Q + T::TQ - 1) / T::TQ;
     const uint32_t xcd = blockIdx.x % kXcds, seq = blockIdx.x / kXcds;
     const uint32_t qb = seq % nqb;
     const uint32_t tb = (seq / nqb) * kXcds + xcd;
-    if (!a.tiles && tb * uint32_t(T::TN) >= a.N) return;  // padding workgroup
+    if (!a.tiles && !a.gather && tb * uint32_t(T::TN) >= a.N) return;  // padding workgroup
     // Tile extent: queries qs + i (i < qc; through qrow when given) and database rows at
     // positions rs + j*rstride (j < rc).  Flat launches derive it from blockIdx; list-major
-    // (IVF) launches read one descriptor {qs, qc, rs, rc} per workgroup.
+    // (IVF) launches read one descriptor {qs, qc, rs, rc} per workgroup; gather launches take
+    // one query and up to 128 rows of its gather list.
     uint32_t qs = qb * T::TQ, rs = tb * T::TN, qc, rc, rstride = 1;
-    if (a.tiles) {
+    if (a.gather) {
+        qs = blockIdx.x / a.gtiles;
+        rs = (blockIdx.x % a.gtiles) * uint32_t(T::TN);
+        const uint32_t m = min(a.gcount[qs], a.gcap);
+        if (rs >= m) return;  // empty tile (uniform)
+        qc = 1;
+        rc = min(uint32_t(T::TN), m - rs);
+    } else if (a.tiles) {
         const uint32_t* td = a.tiles + 4 * int64_t(blockIdx.x);
         qs = td[0];
         qc = td[1];
@@ -263,7 +271,11 @@ __global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) 
                     }
                 } else {
                     const uint32_t jr = uint32_t(row - T::TQ);
-                    if (jr < rc) src[j] = a.x + int64_t(rs + jr * rstride) * a.ldx + col;
+                    if (jr < rc) {
+                        const int64_t xr = a.gather ? int64_t(a.gather[int64_t(qs) * a.gcap + rs + jr])
+                                                    : int64_t(rs + jr * rstride);
+                        src[j] = a.x + xr * a.ldx + col;
+                    }
                 }
             }
         }
@@ -396,7 +408,8 @@ va_status launch_tile(va_context* ctx, const DistArgs& a) {
     using T = Tile<WQ, WN>;
     const uint64_t nqb = (a.Q + T::TQ - 1) / T::TQ;
     const uint64_t ntb = (a.N + T::TN - 1) / T::TN;
-    const uint64_t grid = a.tiles ? a.ntiles : nqb * ((ntb + kXcds - 1) / kXcds) * kXcds;
+    const uint64_t grid = a.gather ? uint64_t(a.Q) * a.gtiles
+                          : a.tiles ? a.ntiles : nqb * ((ntb + kXcds - 1) / kXcds) * kXcds;
     if (grid == 0) return VA_OK;
     if (grid > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "distance grid too large (%llu tiles)", (unsigned long long)grid);
     auto kern = &dist_gemm_kernel<WQ, WN, VEC, OUT, DMA>;
@@ -436,6 +449,12 @@ va_status launch_dist(va_context* ctx, const DistArgs& a) {
     if (a.tiles ? a.ntiles == 0 : (a.Q == 0 || a.N == 0)) return VA_OK;
     const bool vec = (a.D % 4 == 0) && (a.ldq % 4 == 0) && (a.ldx % 4 == 0) &&
                      ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
+    if (a.gather) {
+        // rows come from anywhere in the database (64-bit addresses): register-staged loads
+        if (a.out != OUT_KEYS || a.tiles || a.qrow || a.gtiles == 0 || a.gcap == 0 || !a.gcount)
+            return fail(ctx, VA_ERR_INVALID_ARG, "launch_dist: malformed gather launch");
+        return vec ? launch_tile<1, 1, true, OUT_KEYS, false>(ctx, a) : launch_tile<1, 1, false, OUT_KEYS, false>(ctx, a);
+    }
     const int wq = a.wq ? a.wq : (a.Q <= 32 ? 1 : (a.Q <= 64 ? 2 : 4));
     const int wn = a.wn ? a.wn : 4 / wq;
 #define VA_DIST_CASE(W, N, O) \

@@ -213,6 +213,14 @@ va_status va_fused_topk(va_context* ctx, va_metric metric, const float* queries,
     o.idx = out_idx;
     o.f = out_dist;
     o.key_kind = 0;
+    va::ScreenInput si;
+    si.q = queries;
+    si.x = database;
+    si.Q = num_queries;
+    si.N = num_database;
+    si.D = dim;
+    si.op = p.op;
+    if (va::screen_applies(ctx, si, k)) return va::screened_topk_scan(ctx, si, p, k, o);
     return va::exact_topk_scan(ctx, p, num_queries, num_database, k, o);
 }
 

@@ -26,6 +26,7 @@ struct va_context {
     // test/tuning overrides of the exact top-k scan (0 = automatic)
     uint64_t opt_candidate_cap = 0;
     uint64_t opt_sample_rows = 0;
+    uint32_t opt_screen = 0;  // VA_OPT_SCREEN: 0 auto, 1 off, 2 forced where it applies
     // scratch arena: partial results, counters, candidate buffers
     char* scratch = nullptr;
     size_t scratch_bytes = 0;
@@ -249,6 +250,14 @@ struct DistArgs {
     uint32_t ntiles = 0;
     uint32_t rstride = 1;
     const uint32_t* ids = nullptr;
+    // gather launches (the exact rerank of screened candidates): workgroup b takes query
+    // b / gtiles and the rows gather[q * gcap + j] for j in [128 t, 128 t + 128) of its list of
+    // min(gcount[q], gcap) rows, t = b % gtiles; keys go to out_k[q * ldo + j].  1x1 tiles,
+    // OUT_KEYS only.
+    const uint32_t* gather = nullptr;
+    const uint32_t* gcount = nullptr;
+    uint32_t gcap = 0;
+    uint32_t gtiles = 0;
     int wq = 0;  // waves along queries (tiles of 32*wq queries); 0 = from Q
     int wn = 0;  // waves along rows (tiles of 128*wn rows); 0 = 4/wq.  wq x wn in {1x4, 2x2, 4x1}, and
                  // for OUT_FILTER also 1x1, 2x1
@@ -325,5 +334,74 @@ struct ScanOutputs {
 
 va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t N, uint32_t k,
                           const ScanOutputs& out);
+
+// Plan of the sampled scan: S sample rows (every stride-th row), candidate capacity per query,
+// queries per sample launch; direct = the database is small enough for dense keys.
+struct ScanPlan {
+    uint64_t S = 0;
+    bool direct = false;
+    uint32_t stride = 1;
+    uint64_t cap = 0;
+    uint32_t qs = 1;
+};
+ScanPlan plan_scan(const va_context* ctx, uint32_t Q, uint32_t N, uint32_t k);
+
+// Exact top-k of the listed query rows (device list) by dense keys over the whole database in
+// chunks (the path of queries whose candidate list overflowed).  Writes base's outputs at the
+// listed rows.  Synchronises the stream.
+va_status rescan_rows(va_context* ctx, KeyProducer& kp, uint32_t N, uint32_t k, const SelectArgs& base,
+                      const uint32_t* rows_dev, uint32_t n_rows);
+
+// hipEvent marks of the scan phases (no-ops unless profiling is on)
+struct ScanPhaseMarks {
+    va_context* ctx;
+    explicit ScanPhaseMarks(va_context* c) : ctx(c) {}
+    va_status mark(int i) {
+        if (!ctx->profiling) return VA_OK;
+        VA_CHECK_HIP(ctx, hipEventRecord(ctx->ev[i], ctx->stream));
+        return VA_OK;
+    }
+    float ms(int a, int b) {
+        float t = 0.0f;
+        if (hipEventElapsedTime(&t, ctx->ev[a], ctx->ev[b]) != hipSuccess) {
+            (void)hipGetLastError();
+            return -1.0f;
+        }
+        return t;
+    }
+    // events: 0 start, 1 after sample, 2 after scan, 3 after select, 4 end
+    va_status finish(bool sampled, bool fallback) {
+        if (!ctx->profiling) return VA_OK;
+        VA_CHECK_STATUS(mark(4));
+        VA_CHECK_HIP(ctx, hipEventSynchronize(ctx->ev[4]));
+        va_scan_timings& t = ctx->last_scan;
+        t.total_ms = ms(0, 4);
+        if (sampled) {
+            t.sample_ms = ms(0, 1);
+            t.scan_ms = ms(1, 2);
+            t.select_ms = ms(2, 3);
+            t.fallback_ms = fallback ? ms(3, 4) : 0.0f;
+        } else {
+            t.sample_ms = 0.0f;
+            t.scan_ms = t.total_ms;
+            t.select_ms = 0.0f;
+            t.fallback_ms = 0.0f;
+        }
+        return VA_OK;
+    }
+};
+
+// The fp32 top-k with an fp16 screening pass (va_screen.hip): the same result as
+// exact_topk_scan over F32 keys, bit for bit, from a cheaper filtering scan.
+struct ScreenInput {
+    const float* q = nullptr;
+    const float* x = nullptr;
+    uint32_t Q = 0, N = 0, D = 0;
+    DistOp op = OP_L2SQ;
+};
+// Whether the screened path applies (metric, alignment, sizes, VA_OPT_SCREEN).
+bool screen_applies(const va_context* ctx, const ScreenInput& in, uint32_t k);
+va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer& exact, uint32_t k,
+                             const ScanOutputs& out);
 
 }  // namespace va

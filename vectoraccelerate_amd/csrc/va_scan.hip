@@ -22,45 +22,83 @@ namespace {
 constexpr uint64_t kDenseBudgetBytes = 256ull << 20;  // dense key matrix per launch
 constexpr uint32_t kMinSample = 16384;
 
-// hipEvent marks of the scan phases (no-ops unless profiling is on)
-struct PhaseMarks {
-    va_context* ctx;
-    explicit PhaseMarks(va_context* c) : ctx(c) {}
-    va_status mark(int i) {
-        if (!ctx->profiling) return VA_OK;
-        VA_CHECK_HIP(ctx, hipEventRecord(ctx->ev[i], ctx->stream));
-        return VA_OK;
-    }
-    float ms(int a, int b) {
-        float t = 0.0f;
-        if (hipEventElapsedTime(&t, ctx->ev[a], ctx->ev[b]) != hipSuccess) {
-            (void)hipGetLastError();
-            return -1.0f;
-        }
-        return t;
-    }
-    // events: 0 start, 1 after sample, 2 after scan, 3 after select, 4 end
-    va_status finish(bool sampled, bool fallback) {
-        if (!ctx->profiling) return VA_OK;
-        VA_CHECK_STATUS(mark(4));
-        VA_CHECK_HIP(ctx, hipEventSynchronize(ctx->ev[4]));
-        va_scan_timings& t = ctx->last_scan;
-        t.total_ms = ms(0, 4);
-        if (sampled) {
-            t.sample_ms = ms(0, 1);
-            t.scan_ms = ms(1, 2);
-            t.select_ms = ms(2, 3);
-            t.fallback_ms = fallback ? ms(3, 4) : 0.0f;
-        } else {
-            t.sample_ms = 0.0f;
-            t.scan_ms = t.total_ms;
-            t.select_ms = 0.0f;
-            t.fallback_ms = 0.0f;
-        }
-        return VA_OK;
-    }
-};
 }  // namespace
+
+ScanPlan plan_scan(const va_context* ctx, uint32_t Q, uint32_t N, uint32_t k) {
+    ScanPlan p;
+    // Sample size: N/64 rows keeps ~64k candidates per query, but the dense sample costs Q*S
+    // keys, so it is capped at kDenseBudgetBytes of keys in total (16384 rows minimum).
+    p.S = ctx->opt_sample_rows
+              ? ctx->opt_sample_rows
+              : std::max<uint64_t>(kMinSample, std::min<uint64_t>(N / 64, kDenseBudgetBytes / 4 / Q));
+    p.direct = p.S >= N;
+    if (p.direct) return p;
+    p.stride = uint32_t(N / p.S);
+    const uint64_t ratio = (uint64_t(N) + p.S - 1) / p.S;
+    uint64_t cap = ctx->opt_candidate_cap ? ctx->opt_candidate_cap
+                                          : std::max<uint64_t>(3ull * k, uint64_t(k) + 32) * ratio + 1024;
+    cap = std::min<uint64_t>(cap, N);
+    p.cap = (cap + 63) & ~uint64_t(63);
+    p.qs = uint32_t(std::max<uint64_t>(1, std::min<uint64_t>(Q, kDenseBudgetBytes / (p.S * 4))));
+    return p;
+}
+
+va_status rescan_rows(va_context* ctx, KeyProducer& kp, uint32_t N, uint32_t k, const SelectArgs& base,
+                      const uint32_t* rows_dev, uint32_t n_rows) {
+    if (n_rows == 0) return VA_OK;
+    // The row list is read back first: the arena below may be regrown (which frees it).
+    std::vector<uint32_t> rows_host(n_rows);
+    VA_CHECK_HIP(ctx, hipMemcpyAsync(rows_host.data(), rows_dev, size_t(n_rows) * 4, hipMemcpyDeviceToHost,
+                                     ctx->stream));
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    // rows are processed in batches of R; each batch scans the database in chunks of C rows
+    const uint32_t R = std::min<uint32_t>(n_rows, 64);
+    const uint32_t C = uint32_t(std::max<uint64_t>(k, std::min<uint64_t>(N, kDenseBudgetBytes / (uint64_t(R) * 4))));
+    const uint32_t nch = (N + C - 1) / C;
+    Scratch f(ctx);
+    VA_CHECK_STATUS(f.reserve(Scratch::round(uint64_t(n_rows) * 4) + Scratch::round(uint64_t(R) * C * 4) +
+                              Scratch::round(uint64_t(R) * nch * k * 4) * 2));
+    uint32_t* ovf_rows = f.carve<uint32_t>(n_rows);
+    uint32_t* dkeys = f.carve<uint32_t>(uint64_t(R) * C);
+    uint32_t* wkey = f.carve<uint32_t>(uint64_t(R) * nch * k);
+    uint32_t* wid = f.carve<uint32_t>(uint64_t(R) * nch * k);
+    VA_CHECK_HIP(ctx, hipMemcpyAsync(ovf_rows, rows_host.data(), size_t(n_rows) * 4, hipMemcpyHostToDevice,
+                                     ctx->stream));
+    for (uint32_t r0 = 0; r0 < n_rows; r0 += R) {
+        const uint32_t nr = std::min(R, n_rows - r0);
+        const uint32_t* rows = ovf_rows + r0;
+        for (uint32_t c = 0; c < nch; ++c) {
+            const uint32_t c0 = c * C;
+            const uint32_t cols = std::min(C, N - c0);
+            VA_CHECK_STATUS(kp.dense(rows, 0, nr, c0, cols, 1, dkeys, C));
+            SelectArgs a;
+            a.keys = dkeys;
+            a.ld = C;
+            a.n = cols;
+            a.rows = nr;
+            a.k = k;
+            a.id_offset = c0;
+            a.out_ld = int64_t(nch) * k;
+            a.out_idx = wid + int64_t(c) * k;
+            a.out_key = wkey + int64_t(c) * k;
+            VA_CHECK_STATUS(launch_select(ctx, a));
+        }
+        SelectArgs a = base;
+        a.keys = wkey;
+        a.ids = wid;
+        a.counts = nullptr;
+        a.ld = int64_t(nch) * k;
+        a.n = nch * k;
+        a.rows = nr;
+        a.row_map = rows;
+        a.overflow_count = nullptr;
+        a.overflow_rows = nullptr;
+        VA_CHECK_STATUS(launch_select(ctx, a));
+    }
+    // the host copy of the row list must outlive the upload above
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return VA_OK;
+}
 
 va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t N, uint32_t k,
                           const ScanOutputs& out) {
@@ -74,13 +112,10 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
     base.key_bits = kp.key_bits();
 
     // ---- plan ------------------------------------------------------------------------
-    // Sample size: N/64 rows keeps ~64k candidates per query, but the dense sample costs Q*S
-    // keys, so it is capped at kDenseBudgetBytes of keys in total (16384 rows minimum).
-    uint64_t S = ctx->opt_sample_rows
-                     ? ctx->opt_sample_rows
-                     : std::max<uint64_t>(kMinSample, std::min<uint64_t>(N / 64, kDenseBudgetBytes / 4 / Q));
-    const bool direct = S >= N;
-    PhaseMarks pm(ctx);
+    const ScanPlan plan = plan_scan(ctx, Q, N, k);
+    const uint64_t S = plan.S;
+    const bool direct = plan.direct;
+    ScanPhaseMarks pm(ctx);
     ctx->last_scan = va_scan_timings{};
     VA_CHECK_STATUS(pm.mark(0));
     if (direct) {
@@ -108,14 +143,10 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
         }
         return pm.finish(false, false);
     }
-    const uint32_t stride = uint32_t(N / S);
-    const uint64_t ratio = (uint64_t(N) + S - 1) / S;
-    uint64_t cap = ctx->opt_candidate_cap ? ctx->opt_candidate_cap
-                                          : std::max<uint64_t>(3ull * k, uint64_t(k) + 32) * ratio + 1024;
-    cap = std::min<uint64_t>(cap, N);
-    cap = (cap + 63) & ~uint64_t(63);
+    const uint32_t stride = plan.stride;
+    const uint64_t cap = plan.cap;
     const uint64_t per_q_sample = S * 4;
-    const uint32_t qs = uint32_t(std::max<uint64_t>(1, std::min<uint64_t>(Q, kDenseBudgetBytes / per_q_sample)));
+    const uint32_t qs = plan.qs;
 
     Scratch s(ctx);
     const size_t need = Scratch::round(uint64_t(Q) * 4) * 3 + Scratch::round(uint64_t(Q) * cap * 4) * 2 +
@@ -173,55 +204,7 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
     if (n_ovf == 0) return pm.finish(true, false);
 
     // ---- 4. exact chunked recomputation of overflowed rows ---------------------------------
-    // rows are processed in batches of R; each batch scans the database in chunks of C rows
-    const uint32_t R = std::min<uint32_t>(n_ovf, 64);
-    const uint32_t C = uint32_t(std::max<uint64_t>(k, std::min<uint64_t>(N, kDenseBudgetBytes / (uint64_t(R) * 4))));
-    const uint32_t nch = (N + C - 1) / C;
-    // The first part of the arena (thr .. ovf_rows) stays live; the rest is reused.
-    Scratch f(ctx);
-    f.off = Scratch::round(uint64_t(Q) * 4) * 3;
-    const size_t need2 = f.off + Scratch::round(uint64_t(R) * C * 4) + Scratch::round(uint64_t(R) * nch * k * 4) * 2;
-    if (need2 > ctx->scratch_bytes) {
-        // keep the overflow list across the arena regrowth
-        std::vector<uint32_t> keep(n_ovf);
-        VA_CHECK_HIP(ctx, hipMemcpy(keep.data(), ovf_rows, size_t(n_ovf) * 4, hipMemcpyDeviceToHost));
-        VA_CHECK_STATUS(f.reserve(need2));
-        VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->scratch + Scratch::round(uint64_t(Q) * 4) * 2, keep.data(),
-                                         size_t(n_ovf) * 4, hipMemcpyHostToDevice, ctx->stream));
-        VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
-        ovf_rows = reinterpret_cast<uint32_t*>(ctx->scratch + Scratch::round(uint64_t(Q) * 4) * 2);
-    }
-    uint32_t* dkeys = f.carve<uint32_t>(uint64_t(R) * C);
-    uint32_t* wkey = f.carve<uint32_t>(uint64_t(R) * nch * k);
-    uint32_t* wid = f.carve<uint32_t>(uint64_t(R) * nch * k);
-    for (uint32_t r0 = 0; r0 < n_ovf; r0 += R) {
-        const uint32_t nr = std::min(R, n_ovf - r0);
-        const uint32_t* rows = ovf_rows + r0;
-        for (uint32_t c = 0; c < nch; ++c) {
-            const uint32_t c0 = c * C;
-            const uint32_t cols = std::min(C, N - c0);
-            VA_CHECK_STATUS(kp.dense(rows, 0, nr, c0, cols, 1, dkeys, C));
-            SelectArgs a;
-            a.keys = dkeys;
-            a.ld = C;
-            a.n = cols;
-            a.rows = nr;
-            a.k = k;
-            a.id_offset = c0;
-            a.out_ld = int64_t(nch) * k;
-            a.out_idx = wid + int64_t(c) * k;
-            a.out_key = wkey + int64_t(c) * k;
-            VA_CHECK_STATUS(launch_select(ctx, a));
-        }
-        SelectArgs a = base;
-        a.keys = wkey;
-        a.ids = wid;
-        a.ld = int64_t(nch) * k;
-        a.n = nch * k;
-        a.rows = nr;
-        a.row_map = rows;
-        VA_CHECK_STATUS(launch_select(ctx, a));
-    }
+    VA_CHECK_STATUS(rescan_rows(ctx, kp, N, k, base, ovf_rows, n_ovf));
     return pm.finish(true, true);
 }
 

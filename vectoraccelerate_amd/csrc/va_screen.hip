@@ -1,0 +1,842 @@
+// va_screen.hip — fp32 flat top-k with an fp16 screening pass on v_mfma_f32_32x32x16_f16.
+//
+// The fp32 filtering scan (va_dist.hip) runs at the fp32 MFMA rate.  This path finds the same
+// top-k with the expensive pass at the fp16 MFMA rate, and returns exactly what the fp32 scan
+// returns (same ids, same fp32 distances, bit for bit):
+//
+//   1. prep:    queries -> fp16, each scaled by a power of two (exact) so its largest entry
+//               sits in [2^14, 2^15); fp32 |q|^2 on the side;
+//   2. sample:  screened keys of every query against S strided rows; a screened key is an
+//               interval [lo, hi] that provably contains the fp32 scan's key s for that pair;
+//               tau_q = k-th smallest hi, so the true k-th key s_k <= tau_q;
+//   3. screen:  the full pass appends (hi, lo, id) for every pair with lo <= tau_q (every row
+//               with s <= s_k is among them);
+//   4. bound:   U_q = k-th smallest hi among the candidates (>= s_k again);
+//   5. compact: the rows with lo <= U_q (a superset of the fp32 top-k, ~k + a thin band);
+//   6. rerank:  the fp32 distance kernel (the same kernel, k order and epilogue as the fp32
+//               scan, so the same bits) computes the exact keys of those rows;
+//   7. select:  exact (key, id) top-k.  Lists that overflow take the exact chunked path.
+//
+// The interval comes from a bound on |s_fp16 - s_fp32| (below): rounding each entry to fp16
+// (relative 2^-11, absolute 2^-25 for subnormals; the query's scale makes the query side
+// relative only), the fp32 accumulation of the exact fp16 products in the MFMA (n * 2^-23 for
+// n terms, whatever the adder's order or rounding), the fp32 scan's own accumulation error
+// (2D terms), the norms computed in two different orders, and the rounding of the key
+// formula.  Anything non-finite (an entry beyond the fp16 range, NaN, inf) makes the pair's
+// interval (-inf, NaN-key], so such rows always reach the exact rerank.
+//
+// Scan kernel: 256 queries x 256 rows per workgroup, 4 waves of 128 x 128 (4 x 4 MFMA blocks,
+// 256 accumulators per lane), 64 d-values per LDS stage, two stages in LDS.  Database rows are
+// read as fp32 (buffer loads, 16 B per lane, 4 rows x 256 B per wave-wide load), converted to
+// fp16 in registers and written to LDS; the fp16 queries go global -> LDS by direct loads.
+// One workgroup per CU (130 KiB of LDS).
+#include <cfloat>
+#include <cmath>
+
+#include <algorithm>
+#include <type_traits>
+#include <vector>
+
+#include "va_internal.hpp"
+
+namespace va {
+namespace {
+
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+namespace scr {
+constexpr int TQ = 256;              // queries per workgroup tile
+constexpr int TN = 256;              // database rows per workgroup tile
+constexpr int KC = 64;               // d-values per LDS stage
+constexpr int ROWB = KC * 2;         // bytes per LDS row (fp16)
+constexpr int QBYTES = TQ * ROWB;    // 32 KiB of queries per stage
+constexpr int XBYTES = TN * ROWB;    // 32 KiB of rows per stage
+constexpr int SLOT = QBYTES + XBYTES;
+constexpr int QDMA = QBYTES / 1024 / 4;   // 1 KiB direct loads per wave per stage (8)
+constexpr int XLD = TN * KC / 4 / 256;    // float4 row loads per thread per stage (16)
+constexpr int DP_ALIGN = KC;              // fp16 query rows are padded to a multiple of KC
+}  // namespace scr
+
+enum ScreenMode : int { SCREEN_KEYS = 0, SCREEN_FILTER = 1 };
+
+struct ScreenArgs {
+    const float* x = nullptr;     // database rows, row j at x + j * ldx
+    int64_t ldx = 0;
+    uint32_t N = 0, D = 0, Dp = 0, Q = 0;
+    const _Float16* qh = nullptr;  // [Q x Dp] scaled fp16 queries
+    const float4* qinfo = nullptr; // {|q|^2, |q|, 2^-scale, c0q}
+    int op = OP_L2SQ;
+    float c1 = 0, cn = 0, c0x = 0, kabs = 0;  // bound coefficients (see screen_bounds)
+    // SCREEN_KEYS: out_dot[q * ldo + j] = fp16 dot of query q and row j; out_xx[j] = |x_j|^2
+    float* out_dot = nullptr;
+    float* out_xx = nullptr;
+    int64_t ldo = 0;
+    // SCREEN_FILTER: append (dot, |x|^2, id) of every pair that passes the pre-test of thr[q]
+    const uint32_t* thr = nullptr;
+    uint32_t* cnt = nullptr;
+    float* cand_dot = nullptr;
+    float* cand_xx = nullptr;
+    uint32_t* cand_id = nullptr;
+    uint32_t cap = 0;
+    uint32_t id_base = 0;
+};
+
+// ---- bound of the screened key ----------------------------------------------------------
+// dot: the fp16 dot (already unscaled); qq, nq: fp32 |q|^2, |q|; xx, nx: |x|^2, |x| (fp32, in
+// another order than the fp32 scan's); c0q: the query's absolute-rounding coefficient.
+// Returns false when the pair cannot be bounded (it is then always a candidate).
+__device__ __forceinline__ bool screen_bounds(const ScreenArgs& a, float dot, float qq, float nq, float xx, float nx,
+                                              float c0q, float& lo, float& hi) {
+    if (!(fabsf(dot) <= FLT_MAX)) return false;   // non-finite products: entry beyond fp16 range, NaN, inf
+    const float cabs = fmaf(c0q, a.kabs, 1e-36f);  // products of two rounding floors, fp32 subnormals
+    const float eabs = fmaf(a.c0x, nq, fmaf(c0q, nx, cabs));  // absolute part of the dot bound
+    float s, e;
+    switch (a.op) {
+        case OP_COS_DIST: {
+            const float den = nq * nx;
+            if (!(den >= 0x1p-100f)) return false;  // near the FLT_MIN floor (or NaN)
+            const float raw = dot / den;
+            s = 1.0f - fminf(fmaxf(raw, -1.0f), 1.0f);
+            e = a.c1 + a.cn + eabs / den;
+            break;
+        }
+        case OP_NEG_DOT:
+            s = -dot;
+            e = fmaf(a.c1, nq * nx, eabs);
+            break;
+        default: {  // OP_L2SQ, OP_L2 (bounded in the squared domain first)
+            float v = qq + xx - 2.0f * dot;
+            s = v < 0.0f ? 0.0f : v;
+            e = fmaf(a.c1 + a.cn, qq + xx, 2.0f * eabs);
+            break;
+        }
+    }
+    // room for the rounding of s +- e itself
+    e = fmaf(fmaf(0x1p-21f, fabsf(s), e), 1.0f + 0x1p-20f, 0x1p-126f);
+    if (!(e <= FLT_MAX) || !(fabsf(s) <= FLT_MAX)) return false;
+    lo = s - e;
+    hi = s + e;
+    if (a.op == OP_L2) {
+        lo = sqrtf(fmaxf(lo, 0.0f)) * (1.0f - 0x1p-22f);
+        hi = sqrtf(hi) * (1.0f + 0x1p-22f);
+    } else if (a.op == OP_L2SQ) {
+        lo = fmaxf(lo, 0.0f);
+    }
+    return true;
+}
+
+__device__ __forceinline__ void screen_keys(const ScreenArgs& a, float dot, float qq, float nq, float xx, float nx,
+                                            float c0q, uint32_t& klo, uint32_t& khi) {
+    float lo, hi;
+    if (screen_bounds(a, dot, qq, nq, xx, nx, c0q, lo, hi)) {
+        klo = key_of_float(lo);
+        khi = key_of_float(hi);
+    } else {
+        klo = 0u;
+        khi = 0xFFFFFFFFu;
+    }
+}
+
+// ---- the scan's pre-test ----------------------------------------------------------------------
+// A pair whose fp32 key can be <= tau must satisfy  acc >= A |x|^2 + B |x| + C  (acc = the scaled
+// fp16 dot).  The constants follow from the same bound as screen_bounds, solved for the dot and
+// loosened by 2^-18 of every term (more than the fp32 rounding of the constants and of the two
+// fmas); the test is written !(acc < rhs), so a NaN rhs (a flagged row) always passes.  Queries
+// the form cannot serve get C = -inf (every row passes).
+struct PreTest {
+    float A, B, C;
+};
+__device__ __forceinline__ PreTest pretest_consts(const ScreenArgs& a, float4 info, uint32_t thr_key) {
+    const float qq = info.x, nq = info.y, inv = info.z, c0q = info.w;
+    const PreTest all = {0.0f, 0.0f, -INFINITY};
+    if (thr_key == 0xFFFFFFFFu) return all;  // the NaN key: every key passes
+    const float tau = float_of_key(thr_key);
+    if (!(fabsf(tau) <= FLT_MAX) || !(qq <= FLT_MAX)) return all;
+    const float sig = 1.0f / inv;  // 2^scale, exact
+    const float cabs = fmaf(c0q, a.kabs, 1e-36f);
+    const float w = 1.0f + 0x1p-20f;
+    const float r = 0x1p-18f;
+    float A = 0.0f, B, C;
+    switch (a.op) {
+        case OP_COS_DIST: {
+            // clamp(dot/den) >= 1 - tau - E with 1 - tau - E > -1 (tau < 1.5 and the query and row
+            // terms of E below 1/8 each; rows with |x| < 8 c0x are flagged)
+            if (tau >= 1.5f || c0q > 0.125f * nq) return all;
+            const float e0 = (a.c1 + a.cn + 0x1p-20f) * w;
+            B = sig * ((1.0f - tau - e0) * nq - w * c0q - 0x1p-126f * nq);
+            C = -sig * w * fmaf(a.c0x, nq, cabs);
+            B = B - fabsf(B) * r - sig * nq * 0x1p-20f;
+            C = C - fabsf(C) * r;
+            break;
+        }
+        case OP_NEG_DOT: {
+            // -dot <= tau + E_dot
+            B = -sig * w * fmaf(a.c1, nq, c0q);
+            C = -sig * (tau + w * fmaf(a.c0x, nq, cabs));
+            B = B - fabsf(B) * r;
+            C = C - fabsf(C) * r - sig * fabsf(tau) * 0x1p-21f;
+            break;
+        }
+        default: {
+            // |q|^2 + |x|^2 - 2 dot <= tau + E (L2: tau squared, with room for the sqrt's rounding)
+            const float t = a.op == OP_L2 ? tau * tau * (1.0f + 0x1p-20f) : tau;
+            const float alpha = (a.c1 + a.cn + 0x1p-20f) * w;
+            A = sig * (1.0f - alpha) * 0.5f;
+            B = -sig * w * c0q;
+            C = sig * 0.5f * ((1.0f - alpha) * qq - t - 2.0f * w * fmaf(a.c0x, nq, cabs) - 0x1p-126f);
+            A = A * (1.0f - r);
+            B = B - fabsf(B) * r;
+            C = C - fabsf(C) * r - sig * (qq + fabsf(t)) * 0x1p-21f;
+            break;
+        }
+    }
+    if (!(fabsf(A) <= FLT_MAX) || !(fabsf(B) <= FLT_MAX) || !(fabsf(C) <= FLT_MAX)) return all;
+    return PreTest{A, B, C};
+}
+
+// ---- query preparation: one wave per query ------------------------------------------------
+__global__ __launch_bounds__(256) void screen_prep_kernel(const float* __restrict__ q, int64_t ldq, uint32_t Q,
+                                                          uint32_t D, uint32_t Dp, _Float16* __restrict__ qh,
+                                                          float4* __restrict__ qinfo, float c0) {
+    const uint32_t qi = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (qi >= Q) return;
+    const float* row = q + int64_t(qi) * ldq;
+    float m = 0.0f, ss = 0.0f;
+    bool bad = false;
+    for (uint32_t d = lane; d < D; d += 64) {
+        const float v = row[d];
+        bad |= !(fabsf(v) <= FLT_MAX);
+        m = fmaxf(m, fabsf(v));
+        ss = fmaf(v, v, ss);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        m = fmaxf(m, __shfl_xor(m, off));
+        ss += __shfl_xor(ss, off);
+        bad |= __shfl_xor(int(bad), off) != 0;
+    }
+    // scale 2^sc puts the largest entry in [2^14, 2^15): products and sums stay far from fp16
+    // and fp32 overflow, and subnormal rounding on the query side is 2^-39 of its largest entry.
+    // At most 2^40, so that the scan's pre-test constants stay finite.
+    int sc = 0;
+    if (!bad && m > 0.0f) {
+        int e = 0;
+        (void)frexpf(m, &e);  // m in [2^(e-1), 2^e)
+        sc = std::min(40, 15 - e);
+    }
+    const float scale = ldexpf(1.0f, sc);
+    _Float16* out = qh + int64_t(qi) * Dp;
+    for (uint32_t d = lane; d < Dp; d += 64) out[d] = d < D ? _Float16(row[d] * scale) : _Float16(0.0f);
+    if (lane == 0) {
+        const float inv = ldexpf(1.0f, -sc);
+        qinfo[qi] = make_float4(ss, sqrtf(ss), inv, c0 * 0x1p-25f * inv);
+    }
+}
+
+// ---- the screening scan -----------------------------------------------------------------------
+template <int MODE>
+__global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
+    using namespace scr;
+    // the two stage slots are separate objects, so the compiler sees that the conversion's
+    // writes to one slot never alias the fragment reads of the other
+    __shared__ __attribute__((aligned(1024))) char slot0[SLOT];
+    __shared__ __attribute__((aligned(1024))) char slot1[SLOT];
+    // |x|^2 and |x| of the tile's rows, and the pre-test's copies (NaN for flagged rows)
+    __shared__ __attribute__((aligned(16))) float norms[4 * TN];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wq = wave & 1;   // query half of the tile
+    const int wn = wave >> 1;  // row half of the tile
+    const int l32 = lane & 31;
+    const int hh = lane >> 5;
+
+    // XCD-aware order (as in the fp32 scan): XCD x takes row tiles x, x+8, ... and runs every
+    // query block of a tile back to back
+    const uint32_t nqb = (a.Q + TQ - 1) / TQ;
+    const uint32_t xcd = blockIdx.x % kXcds, seq = blockIdx.x / kXcds;
+    const uint32_t qb = seq % nqb;
+    const uint32_t tb = (seq / nqb) * kXcds + xcd;
+    if (tb * uint32_t(TN) >= a.N) return;  // padding workgroup
+    const uint32_t qs = qb * TQ, rs = tb * TN;
+    const uint32_t qc = min(uint32_t(TQ), a.Q - qs);
+    const uint32_t rc = min(uint32_t(TN), a.N - rs);
+    const uint32_t nst = a.Dp / KC;
+
+    // query direct loads: wave w fills 1 KiB groups g = w + 4i, rows 8g .. 8g+7; lane L loads
+    // row 8g + L/8 at physical chunk L%8 = logical chunk (L%8) ^ ((row >> 1) & 7).  Rows past qc
+    // read past the descriptor and land as zeros.
+    const dma_rsrc qres = make_dma_rsrc(a.qh + int64_t(qs) * a.Dp, qc * a.Dp * 2u);
+    uint32_t qoff[QDMA];
+#pragma unroll
+    for (int i = 0; i < QDMA; ++i) {
+        const int row = 8 * (wave + 4 * i) + (lane >> 3);
+        const int c = (lane & 7) ^ ((row >> 1) & 7);
+        qoff[i] = uint32_t(row) * a.Dp * 2u + 16u * uint32_t(c);
+    }
+    // row loads: lane L of wave w reads rows 64w + 4i + L/16 (i < 16), d-values 4(L%16) .. +3 of
+    // the stage.  The descriptor ends at the tile's last valid byte, so rows past rc read zeros;
+    // d-values past D are skipped explicitly (they would alias the next row).
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(a.x + int64_t(rs) * a.ldx), 0, int((uint64_t(rc - 1) * a.ldx + a.D) * 4), 0x00020000);
+    const uint32_t xcol = 4u * uint32_t(lane & 15);
+    const uint32_t xbase = (uint32_t(64 * wave) + uint32_t(lane >> 4)) * uint32_t(a.ldx) * 4u + xcol * 4u;
+    const uint32_t xstep = 4u * uint32_t(a.ldx) * 4u;
+    // LDS byte offsets of this lane's converted values: row r = 64w + 4i + L/16, logical chunk
+    // (L%16)/2, half L%2; physical chunk = logical ^ ((r >> 1) & 7)
+    const int wc = (lane & 15) >> 1;
+    const int wr0 = 64 * wave + (lane >> 4);
+    auto xw_off = [&](int i) -> uint32_t {
+        const int r = wr0 + 4 * i;
+        return uint32_t(QBYTES + r * ROWB + 16 * (wc ^ ((r >> 1) & 7)) + 8 * (lane & 1));
+    };
+    // fragment offsets: rows 32-aligned + l32, so the swizzle is (l32 >> 1) & 7 for both operands
+    const int swz = (l32 >> 1) & 7;
+    const uint32_t a_off = uint32_t(QBYTES + (wn * 128 + l32) * ROWB);
+    const uint32_t b_off = uint32_t((wq * 128 + l32) * ROWB);
+
+    f32x4v st[XLD];
+    float xs[XLD];
+#pragma unroll
+    for (int i = 0; i < XLD; ++i) xs[i] = 0.0f;
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[m][n][v] = 0.0f;
+
+    auto slot_ptr = [&](int slot) -> char* { return slot ? slot1 : slot0; };
+
+    auto issue_q = [&](uint32_t s, int slot) {
+        const uint32_t d0 = s * KC;
+        const bool ok = d0 < a.Dp;
+#pragma unroll
+        for (int i = 0; i < QDMA; ++i) {
+            const int grp = wave + 4 * i;
+            lds_dma16(qres, ok ? qoff[i] + d0 * 2u : kDmaSkip, lds_addr_of(slot_ptr(slot) + grp * 1024));
+        }
+    };
+    auto convert_row = [&](int slot, int i) {
+        const f32x4v v = st[i];
+        xs[i] = fmaf(v[0], v[0], xs[i]);
+        xs[i] = fmaf(v[1], v[1], xs[i]);
+        xs[i] = fmaf(v[2], v[2], xs[i]);
+        xs[i] = fmaf(v[3], v[3], xs[i]);
+        const h4v h = __builtin_convertvector(v, h4v);
+        *reinterpret_cast<h4v*>(slot_ptr(slot) + xw_off(i)) = h;
+    };
+    auto convert_x = [&](int slot) {
+#pragma unroll
+        for (int i = 0; i < XLD; ++i) convert_row(slot, i);
+    };
+    auto load_row = [&](uint32_t coff, int i) {
+        const uint32_t off = xbase + uint32_t(i) * xstep + coff;
+        st[i] = __builtin_bit_cast(f32x4v, __builtin_amdgcn_raw_buffer_load_b128(xres, int(off), 0, 0));
+    };
+    auto col_off = [&](uint32_t s) -> uint32_t {
+        const uint32_t d0 = s * KC;
+        uint32_t coff = d0 + xcol < a.D ? d0 * 4u : 0x80000000u;
+        asm volatile("" : "+v"(coff));
+        return coff;
+    };
+    // d-values past D: an offset of 2^31 + (< 2^31) lies past the descriptor and reads zeros
+    // (the select is hidden from the optimizer, which would otherwise branch around each load)
+    auto load_x = [&](uint32_t s) {
+        const uint32_t coff = col_off(s);
+#pragma unroll
+        for (int i = 0; i < XLD; ++i) load_row(coff, i);
+    };
+    h8v av[4], bv[4];
+    auto frags = [&](int slot, int t) {
+        const char* base = slot_ptr(slot);
+        const uint32_t ko = 16u * uint32_t((2 * t + hh) ^ swz);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) av[m] = *reinterpret_cast<const h8v*>(base + a_off + m * 32 * ROWB + ko);
+#pragma unroll
+        for (int n = 0; n < 4; ++n) bv[n] = *reinterpret_cast<const h8v*>(base + b_off + n * 32 * ROWB + ko);
+    };
+    auto mma = [&]() {
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int n = 0; n < 4; ++n)
+                acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[m], bv[n], acc[m][n], 0, 0, 0);
+    };
+
+    // prologue: stage 0 in slot 0, stage 1's rows in registers
+    load_x(0);
+    issue_q(0, 0);
+    convert_x(0);
+    load_x(1);
+    wait_vmcnt<XLD>();  // the query loads of stage 0 (older than the row loads of stage 1)
+    __syncthreads();
+    // Stage s computes from slot s&1 while stage s+1 is written to the other slot (last read in
+    // stage s-1, before the previous barrier).  Past the last stage the loads skip (zeros).
+    // The first k-step's fragments are read before the conversion's LDS writes (which the
+    // compiler must keep after them), so its MFMAs can overlap the conversion; scheduling
+    // barriers keep each stage's work inside its stage.
+    // Order inside a stage: the rows of stage s+1 (loaded during stage s-1) are complete; the
+    // query loads of stage s+1 are issued (invisible to the compiler's wait counts, so they go
+    // after that wait); the conversion of stage s+1 and the row loads of stage s+2 are
+    // interleaved with the MFMAs of the first two k-steps (one wave per SIMD: the VALU work
+    // would otherwise leave the matrix unit idle).
+    auto stage = [&](uint32_t s, auto cur) {
+        constexpr int C = decltype(cur)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<0>();
+        issue_q(s + 1, C ^ 1);
+        frags(C, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        // k-step 0: each MFMA is followed by the conversion of one row load
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            acc[i >> 2][i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i >> 2], bv[i & 3], acc[i >> 2][i & 3], 0, 0, 0);
+            convert_row(C ^ 1, i);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // k-step 1: each MFMA is followed by one row load of stage s+2
+        frags(C, 1);
+        const uint32_t coff = col_off(s + 2);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            acc[i >> 2][i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i >> 2], bv[i & 3], acc[i >> 2][i & 3], 0, 0, 0);
+            load_row(coff, i);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int t = 2; t < KC / 16; ++t) {
+            frags(C, t);
+            mma();
+        }
+        wait_vmcnt<XLD>();
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    uint32_t s = 0;
+    for (; s + 1 < nst; s += 2) {
+        stage(s, std::integral_constant<int, 0>());
+        stage(s + 1, std::integral_constant<int, 1>());
+    }
+    if (s < nst) stage(s, std::integral_constant<int, 0>());
+    wait_vmcnt<0>();
+
+    // squared norms of the tile's rows: the 16 lanes of a row hold 4 columns each.  The pre-test
+    // copies flag (NaN) rows whose fp16 image may hold an infinity (|x| near 65504 or more) and,
+    // for cosine, rows too small for the linear form.
+    float* xxs = norms;
+    float* nxs = norms + TN;
+    float* xxp = norms + 2 * TN;
+    float* nxp = norms + 3 * TN;
+    const float tiny = a.op == OP_COS_DIST ? 8.0f * a.c0x : 0.0f;
+#pragma unroll
+    for (int i = 0; i < XLD; ++i) {
+        float t = xs[i];
+        t += __shfl_xor(t, 1);
+        t += __shfl_xor(t, 2);
+        t += __shfl_xor(t, 4);
+        t += __shfl_xor(t, 8);
+        if ((lane & 15) == 0) {
+            const int r = wr0 + 4 * i;
+            const float nx = sqrtf(t);
+            xxs[r] = t;
+            nxs[r] = nx;
+            const bool flag = !(t < 4.29e9f) || nx < tiny;
+            xxp[r] = flag ? __builtin_nanf("") : t;
+            nxp[r] = flag ? __builtin_nanf("") : nx;
+        }
+    }
+    __syncthreads();
+
+    if constexpr (MODE == SCREEN_KEYS) {
+        // dense fp16 dots (the bounds are computed by screen_bound_kernel) and the row norms
+        if (qb == 0 && wave == 0)
+            for (uint32_t r = uint32_t(lane); r < rc; r += 64) a.out_xx[rs + r] = xxs[r];
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+            const uint32_t ql = uint32_t(wq * 128 + 32 * n + l32);
+            if (ql >= qc) continue;
+            const uint32_t qi = qs + ql;
+            const float inv = a.qinfo[qi].z;
+            float* o = a.out_dot + int64_t(qi) * a.ldo + rs;
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int r = wn * 128 + 32 * m + 8 * j + 4 * hh;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (uint32_t(r + e) < rc) o[r + e] = acc[m][n][4 * j + e] * inv;
+                }
+        }
+        return;
+    } else {
+        // Pairs that pass the pre-test are staged per lane in this wave's quarter of the (now free)
+        // stage slots: 64 entries x 64 lanes of (scaled dot, row), then appended with one atomic
+        // per lane and query block.
+        char* stg = (wave < 2 ? slot0 : slot1) + (wave & 1) * (SLOT / 2);
+        float* stg_v = reinterpret_cast<float*>(stg);
+        uint32_t* stg_r = reinterpret_cast<uint32_t*>(stg) + 64 * 64;
+        static_assert(SLOT / 2 >= 64 * 64 * 8, "staging needs 32 KiB per wave");
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+            const uint32_t ql = uint32_t(wq * 128 + 32 * n + l32);
+            if (ql >= qc) continue;
+            const uint32_t qi = qs + ql;
+            const float4 info = a.qinfo[qi];
+            const PreTest pt = pretest_consts(a, info, a.thr[qi]);
+            uint32_t ns = 0;
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int r = wn * 128 + 32 * m + 8 * j + 4 * hh;
+                    const f32x4v xx = *reinterpret_cast<const f32x4v*>(xxp + r);
+                    const f32x4v nx = *reinterpret_cast<const f32x4v*>(nxp + r);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float v = acc[m][n][4 * j + e];
+                        const float rhs = fmaf(pt.A, xx[e], fmaf(pt.B, nx[e], pt.C));
+                        if (!(v < rhs) && uint32_t(r + e) < rc) {
+                            stg_v[ns * 64 + lane] = v;
+                            stg_r[ns * 64 + lane] = uint32_t(r + e);
+                            ++ns;
+                        }
+                    }
+                }
+            if (ns == 0) continue;
+            const uint32_t pos = atomicAdd(a.cnt + qi, ns);
+            for (uint32_t i = 0; i < ns; ++i) {
+                if (pos + i >= a.cap) break;
+                const uint32_t r = stg_r[i * 64 + lane];
+                const int64_t o = int64_t(qi) * a.cap + pos + i;
+                a.cand_dot[o] = stg_v[i * 64 + lane] * info.z;
+                a.cand_xx[o] = xxs[r];
+                a.cand_id[o] = a.id_base + rs + r;
+            }
+        }
+    }
+}
+
+// ---- exact intervals of the screened pairs -----------------------------------------------------
+// Dense (the sample): keys[q * ld + j] = key(hi) from dot[q * ld + j] and xx[j], in place.
+// Lists (the scan's candidates): (dot, xx) -> (key(hi), key(lo)), in place, for i < min(cnt, cap).
+__global__ __launch_bounds__(256) void screen_bound_kernel(ScreenArgs a, float* dot, const float* xx_dense, float* xx_list,
+                                                           const uint32_t* cnt, uint32_t n, int64_t ld) {
+    const uint32_t q = blockIdx.y;
+    const float4 info = a.qinfo[q];
+    const uint32_t m = cnt ? min(cnt[q], n) : n;
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < m; i += gridDim.x * 256) {
+        const int64_t o = int64_t(q) * ld + i;
+        const float xx = cnt ? xx_list[o] : xx_dense[i];
+        uint32_t klo, khi;
+        screen_keys(a, dot[o], info.x, info.y, xx, sqrtf(xx), info.w, klo, khi);
+        reinterpret_cast<uint32_t*>(dot)[o] = khi;
+        if (cnt) reinterpret_cast<uint32_t*>(xx_list)[o] = klo;
+    }
+}
+
+// ---- rerank list: the candidates whose lower bound is within the k-th upper bound -------------
+// One workgroup per query.  Lists that overflowed (count > cap) or whose rerank list outgrows
+// rcap are put on the overflow list and left empty here.
+__global__ __launch_bounds__(256) void screen_compact_kernel(const uint32_t* __restrict__ cnt,
+                                                             const uint32_t* __restrict__ cand_lo,
+                                                             const uint32_t* __restrict__ cand_id,
+                                                             const uint32_t* __restrict__ bound, uint32_t cap,
+                                                             uint32_t* __restrict__ rr, uint32_t* __restrict__ rcount,
+                                                             uint32_t rcap, uint32_t* __restrict__ ovf_cnt,
+                                                             uint32_t* __restrict__ ovf_rows) {
+    __shared__ uint32_t s_n;
+    const uint32_t q = blockIdx.x;
+    const int tid = threadIdx.x;
+    const uint32_t n = cnt[q];
+    if (n > cap) {
+        // the candidate select has already listed this query as overflowed
+        if (tid == 0) rcount[q] = 0;
+        return;
+    }
+    if (tid == 0) s_n = 0;
+    __syncthreads();
+    const uint32_t u = bound[q];
+    const uint32_t* lo = cand_lo + int64_t(q) * cap;
+    const uint32_t* id = cand_id + int64_t(q) * cap;
+    uint32_t* out = rr + int64_t(q) * rcap;
+    for (uint32_t i0 = 0; i0 < n; i0 += 256) {
+        const uint32_t i = i0 + uint32_t(tid);
+        const bool p = i < n && lo[i] <= u;
+        const uint64_t b = __ballot(p);
+        const int lane = tid & 63;
+        uint32_t base = 0;
+        if (lane == 0 && b) base = atomicAdd(&s_n, uint32_t(__popcll(b)));
+        base = __shfl(base, 0);
+        if (p) {
+            const uint32_t pos = base + uint32_t(__popcll(b & ((1ull << lane) - 1)));
+            if (pos < rcap) out[pos] = id[i];
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t m = s_n;
+        if (m > rcap) {
+            rcount[q] = 0;
+            const uint32_t p = atomicAdd(ovf_cnt, 1u);
+            ovf_rows[p] = q;
+        } else {
+            rcount[q] = m;
+        }
+    }
+}
+
+// Coefficients of the bound (host, double precision; every term rounded up by 1/16).
+struct Bound {
+    float c1, cn, c0, kabs;
+};
+Bound make_bound(uint32_t D) {
+    const double u = std::ldexp(1.0, -11);   // fp16 unit roundoff
+    const double up = std::ldexp(1.0, -23);  // any fp32 rounding (nearest or toward zero)
+    auto gam = [&](double n) { return n * up / (1.0 - n * up); };
+    const double gD = gam(D), g2D = gam(2.0 * D);
+    const double slack = 1.0625;
+    Bound b;
+    // |dot16 - dot| + |dot32 - dot| <= c1 |q||x| + c0 (2^-25 |q| + eta_q |x|) + ...
+    b.c1 = float(slack * (2 * u + u * u + gD * (1 + 3 * u) + g2D));
+    // the two orders of the norms and the key formula's roundings (relative to |q|^2 + |x|^2, or
+    // to 1 for cosine)
+    b.cn = float(slack * (2 * gD + std::ldexp(1.0, -20)));
+    b.c0 = float(slack * (1 + u) * (1 + gD) * std::sqrt(double(D)));
+    // the product of the two absolute floors: D * 2^-25 * eta_q = c0q * D * 2^-25 / c0
+    b.kabs = float(slack * double(D) * std::ldexp(1.0, -25) / double(b.c0));
+    return b;
+}
+
+template <int MODE>
+va_status launch_screen(va_context* ctx, const ScreenArgs& a) {
+    using namespace scr;
+    const uint64_t nqb = (a.Q + TQ - 1) / TQ;
+    const uint64_t ntb = (a.N + TN - 1) / TN;
+    const uint64_t grid = nqb * ((ntb + kXcds - 1) / kXcds) * kXcds;
+    if (grid == 0) return VA_OK;
+    if (grid > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "screen grid too large (%llu)", (unsigned long long)grid);
+    screen_kernel<MODE><<<dim3(uint32_t(grid)), dim3(256), 0, ctx->stream>>>(a);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
+va_status launch_bounds(va_context* ctx, const ScreenArgs& a, float* dot, const float* xx_dense, float* xx_list,
+                        const uint32_t* cnt, uint32_t n, int64_t ld, uint32_t rows) {
+    if (rows == 0 || n == 0) return VA_OK;
+    // lists are short (a few thousand): one block per query row; the dense sample: up to 16
+    const uint32_t bx = cnt ? std::min<uint32_t>(4, (n + 255) / 256) : std::min<uint32_t>(16, (n + 255) / 256);
+    screen_bound_kernel<<<dim3(bx, rows), dim3(256), 0, ctx->stream>>>(a, dot, xx_dense, xx_list, cnt, n, ld);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
+uint32_t padded_dim(uint32_t D) { return (D + scr::DP_ALIGN - 1) / scr::DP_ALIGN * scr::DP_ALIGN; }
+
+// Tile offsets of the scan are 32-bit: 256 rows at stride ldx, and a query block.
+bool offsets_fit(uint64_t ldx, uint32_t D) {
+    return uint64_t(scr::TN) * ldx * 4 + uint64_t(D) * 4 < 0x7FFFFFF0ull &&
+           uint64_t(scr::TQ) * padded_dim(D) * 2 < 0x7FFFFFF0ull;
+}
+
+}  // namespace
+
+bool screen_applies(const va_context* ctx, const ScreenInput& in, uint32_t k) {
+    if (ctx->opt_screen == 1) return false;
+    if (in.op != OP_L2SQ && in.op != OP_L2 && in.op != OP_COS_DIST && in.op != OP_NEG_DOT) return false;
+    if (in.D % 4 != 0 || (reinterpret_cast<uintptr_t>(in.x) & 15) != 0) return false;
+    const ScanPlan plan = plan_scan(ctx, in.Q, in.N, k);
+    if (plan.direct) return false;
+    if (!offsets_fit(uint64_t(plan.stride) * in.D, in.D)) return false;
+    if (ctx->opt_screen == 2) return true;
+    // automatic: enough queries to fill the 256-query tiles of the screening scan
+    return in.Q >= 192;
+}
+
+va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer& exact, uint32_t k,
+                             const ScanOutputs& out) {
+    const uint32_t Q = in.Q, N = in.N, D = in.D;
+    const uint32_t Dp = padded_dim(D);
+    const ScanPlan plan = plan_scan(ctx, Q, N, k);
+    const uint64_t S = plan.S;
+    const uint64_t cap = plan.cap;
+    // rerank capacity: k plus the band of rows whose interval straddles the k-th bound
+    const uint64_t rcap = std::min<uint64_t>(N, (std::max<uint64_t>(2ull * k + 256, cap / 8) + 127) / 128 * 128);
+    const uint32_t gtiles = uint32_t((rcap + 127) / 128);
+    const Bound bnd = make_bound(D);
+
+    SelectArgs base;
+    base.k = k;
+    base.out_idx = out.idx;
+    base.out_f = out.f;
+    base.key_kind = 0;
+
+    ScanPhaseMarks pm(ctx);
+    ctx->last_scan = va_scan_timings{};
+    VA_CHECK_STATUS(pm.mark(0));
+
+    Scratch s(ctx);
+    const size_t q4 = Scratch::round(uint64_t(Q) * 4);
+    const size_t need = q4 * 5 + Scratch::round(256) + Scratch::round(uint64_t(Q) * 16) +
+                        Scratch::round(uint64_t(Q) * Dp * 2) + Scratch::round(uint64_t(plan.qs) * S * 4) +
+                        Scratch::round(S * 4) +
+                        Scratch::round(uint64_t(Q) * cap * 4) * 3 + Scratch::round(uint64_t(Q) * rcap * 4) * 2;
+    VA_CHECK_STATUS(s.reserve(need));
+    uint32_t* thr = s.carve<uint32_t>(Q);
+    uint32_t* cnt = s.carve<uint32_t>(Q);
+    uint32_t* ubound = s.carve<uint32_t>(Q);
+    uint32_t* rcount = s.carve<uint32_t>(Q);
+    uint32_t* ovf_rows = s.carve<uint32_t>(Q);
+    uint32_t* ovf_cnt = s.carve<uint32_t>(64);
+    float4* qinfo = s.carve<float4>(Q);
+    _Float16* qh = s.carve<_Float16>(uint64_t(Q) * Dp);
+    uint32_t* skeys = s.carve<uint32_t>(uint64_t(plan.qs) * S);
+    float* sxx = s.carve<float>(S);
+    uint32_t* chi = s.carve<uint32_t>(uint64_t(Q) * cap);
+    uint32_t* clo = s.carve<uint32_t>(uint64_t(Q) * cap);
+    uint32_t* cid = s.carve<uint32_t>(uint64_t(Q) * cap);
+    uint32_t* rr = s.carve<uint32_t>(uint64_t(Q) * rcap);
+    uint32_t* rkey = s.carve<uint32_t>(uint64_t(Q) * rcap);
+
+    // ---- 1. queries -> scaled fp16 ---------------------------------------------------------
+    screen_prep_kernel<<<dim3((Q + 3) / 4), dim3(256), 0, ctx->stream>>>(in.q, int64_t(D), Q, D, Dp, qh, qinfo,
+                                                                       bnd.c0);
+    VA_CHECK_LAUNCH(ctx);
+
+    ScreenArgs sa;
+    sa.D = D;
+    sa.Dp = Dp;
+    sa.op = in.op;
+    sa.c1 = bnd.c1;
+    sa.cn = bnd.cn;
+    sa.c0x = bnd.c0 * 0x1p-25f;
+    sa.kabs = bnd.kabs;
+
+    // ---- 2. sample: k-th smallest upper bound over S strided rows ------------------------------
+    for (uint32_t q0 = 0; q0 < Q; q0 += plan.qs) {
+        const uint32_t nq = std::min(plan.qs, Q - q0);
+        ScreenArgs a = sa;
+        a.x = in.x;
+        a.ldx = int64_t(plan.stride) * D;
+        a.N = uint32_t(S);
+        a.Q = nq;
+        a.qh = qh + int64_t(q0) * Dp;
+        a.qinfo = qinfo + q0;
+        a.out_dot = reinterpret_cast<float*>(skeys);
+        a.out_xx = sxx;
+        a.ldo = int64_t(S);
+        VA_CHECK_STATUS(launch_screen<SCREEN_KEYS>(ctx, a));
+        VA_CHECK_STATUS(launch_bounds(ctx, a, reinterpret_cast<float*>(skeys), sxx, nullptr, nullptr, uint32_t(S),
+                                      int64_t(S), nq));
+        SelectArgs sel;
+        sel.keys = skeys;
+        sel.ld = int64_t(S);
+        sel.n = uint32_t(S);
+        sel.rows = nq;
+        sel.k = k;
+        sel.out_kth = thr + q0;
+        VA_CHECK_STATUS(launch_select(ctx, sel));
+    }
+    // ---- 3. screening scan -------------------------------------------------------------------
+    VA_CHECK_STATUS(fill_u32(ctx, cnt, Q, 0));
+    VA_CHECK_STATUS(fill_u32(ctx, ovf_cnt, 1, 0));
+    VA_CHECK_STATUS(pm.mark(1));
+    {
+        ScreenArgs a = sa;
+        a.x = in.x;
+        a.ldx = D;
+        a.N = N;
+        a.Q = Q;
+        a.qh = qh;
+        a.qinfo = qinfo;
+        a.thr = thr;
+        a.cnt = cnt;
+        a.cand_dot = reinterpret_cast<float*>(chi);
+        a.cand_xx = reinterpret_cast<float*>(clo);
+        a.cand_id = cid;
+        a.cap = uint32_t(cap);
+        VA_CHECK_STATUS(launch_screen<SCREEN_FILTER>(ctx, a));
+        // (dot, |x|^2) -> (key of hi, key of lo), in place
+        VA_CHECK_STATUS(launch_bounds(ctx, a, reinterpret_cast<float*>(chi), nullptr, reinterpret_cast<float*>(clo), cnt,
+                                      uint32_t(cap), int64_t(cap), Q));
+    }
+    VA_CHECK_STATUS(pm.mark(2));
+    ctx->last_scan.scan_launches = 1;
+    ctx->last_scan.sample_rows = uint32_t(S);
+    ctx->last_scan.candidate_cap = uint32_t(cap);
+    ctx->last_scan.screened = 1;
+    // ---- 4. k-th smallest upper bound among the candidates (overflowed lists are listed) ------
+    {
+        SelectArgs a;
+        a.keys = chi;
+        a.ids = cid;
+        a.counts = cnt;
+        a.ld = int64_t(cap);
+        a.n = uint32_t(cap);
+        a.rows = Q;
+        a.k = k;
+        a.out_kth = ubound;
+        a.overflow_count = ovf_cnt;
+        a.overflow_rows = ovf_rows;
+        VA_CHECK_STATUS(launch_select(ctx, a));
+    }
+    // ---- 5. rerank lists ------------------------------------------------------------------------
+    screen_compact_kernel<<<dim3(Q), dim3(256), 0, ctx->stream>>>(cnt, clo, cid, ubound, uint32_t(cap), rr, rcount,
+                                                                 uint32_t(rcap), ovf_cnt, ovf_rows);
+    VA_CHECK_LAUNCH(ctx);
+    // ---- 6. exact fp32 keys of the rerank rows ---------------------------------------------------
+    {
+        DistArgs a;
+        a.q = in.q;
+        a.ldq = D;
+        a.x = in.x;
+        a.ldx = D;
+        a.Q = Q;
+        a.N = uint32_t(rcap);
+        a.D = D;
+        a.op = in.op;
+        a.out = OUT_KEYS;
+        a.out_k = rkey;
+        a.ldo = int64_t(rcap);
+        a.gather = rr;
+        a.gcount = rcount;
+        a.gcap = uint32_t(rcap);
+        a.gtiles = gtiles;
+        VA_CHECK_STATUS(launch_dist(ctx, a));
+    }
+    // ---- 7. exact (key, id) top-k ----------------------------------------------------------------
+    {
+        SelectArgs a = base;
+        a.keys = rkey;
+        a.ids = rr;
+        a.counts = rcount;
+        a.ld = int64_t(rcap);
+        a.n = uint32_t(rcap);
+        a.rows = Q;
+        VA_CHECK_STATUS(launch_select(ctx, a));
+    }
+    VA_CHECK_STATUS(pm.mark(3));
+    VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->host_word, ovf_cnt, 4, hipMemcpyDeviceToHost, ctx->stream));
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    const uint32_t n_ovf = ctx->host_word[0];
+    ctx->last_scan.overflow_rows = n_ovf;
+    if (ctx->profiling) {
+        // diagnostics only: how many rows the exact rerank scored
+        std::vector<uint32_t> rc(Q);
+        VA_CHECK_HIP(ctx, hipMemcpy(rc.data(), rcount, size_t(Q) * 4, hipMemcpyDeviceToHost));
+        uint64_t total = 0;
+        for (uint32_t v : rc) total += v;
+        ctx->last_scan.rerank_rows = uint32_t(std::min<uint64_t>(total, 0xFFFFFFFFu));
+    }
+    if (n_ovf == 0) return pm.finish(true, false);
+    VA_CHECK_STATUS(rescan_rows(ctx, exact, N, k, base, ovf_rows, n_ovf));
+    return pm.finish(true, true);
+}
+
+}  // namespace va
