@@ -54,7 +54,6 @@ constexpr int KC = 64;               // d-values per LDS stage
 constexpr int ROWB = KC * 2;         // bytes per LDS row (fp16)
 constexpr int QBYTES = TQ * ROWB;    // 32 KiB of queries per stage
 constexpr int XBYTES = TN * ROWB;    // 32 KiB of rows per stage
-constexpr int SLOT = QBYTES + XBYTES;
 constexpr int QDMA = QBYTES / 1024 / 4;   // 1 KiB direct loads per wave per stage (8)
 constexpr int XLD = TN * KC / 4 / 256;    // float4 row loads per thread per stage (16)
 constexpr int DP_ALIGN = KC;              // fp16 query rows are padded to a multiple of KC
@@ -241,12 +240,13 @@ __global__ __launch_bounds__(256) void screen_prep_kernel(const float* __restric
 template <int MODE>
 __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
     using namespace scr;
-    // the two stage slots are separate objects, so the compiler sees that the conversion's
-    // writes to one slot never alias the fragment reads of the other
-    __shared__ __attribute__((aligned(1024))) char slot0[SLOT];
-    __shared__ __attribute__((aligned(1024))) char slot1[SLOT];
-    // |x|^2 and |x| of the tile's rows, and the pre-test's copies (NaN for flagged rows)
-    __shared__ __attribute__((aligned(16))) float norms[4 * TN];
+    // LDS (160 KiB): a ring of three query stages (direct loads run two stages ahead) and two
+    // row stages.  The row slots are separate objects, so the compiler sees that the
+    // conversion's writes to one never alias the fragment reads of the other.  After the main
+    // loop the query ring holds the epilogue's staging and the row norms.
+    __shared__ __attribute__((aligned(1024))) char qring[3 * QBYTES];
+    __shared__ __attribute__((aligned(1024))) char xslot0[XBYTES];
+    __shared__ __attribute__((aligned(1024))) char xslot1[XBYTES];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -292,12 +292,23 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
     const int wr0 = 64 * wave + (lane >> 4);
     auto xw_off = [&](int i) -> uint32_t {
         const int r = wr0 + 4 * i;
-        return uint32_t(QBYTES + r * ROWB + 16 * (wc ^ ((r >> 1) & 7)) + 8 * (lane & 1));
+        return uint32_t(r * ROWB + 16 * (wc ^ ((r >> 1) & 7)) + 8 * (lane & 1));
     };
     // fragment offsets: rows 32-aligned + l32, so the swizzle is (l32 >> 1) & 7 for both operands
     const int swz = (l32 >> 1) & 7;
-    const uint32_t a_off = uint32_t(QBYTES + (wn * 128 + l32) * ROWB);
+    const uint32_t a_off = uint32_t((wn * 128 + l32) * ROWB);
     const uint32_t b_off = uint32_t((wq * 128 + l32) * ROWB);
+
+    // the lane's four queries (one per 32-query block): their data is loaded before the main loop
+    // so that the epilogue does not wait for it
+    float4 qinf[4];
+    uint32_t qthr[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+        const uint32_t qi = qs + min(uint32_t(wq * 128 + 32 * n + l32), qc - 1);
+        qinf[n] = a.qinfo[qi];
+        qthr[n] = MODE == SCREEN_FILTER ? a.thr[qi] : 0u;
+    }
 
     f32x4v st[XLD];
     float xs[XLD];
@@ -311,15 +322,15 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[m][n][v] = 0.0f;
 
-    auto slot_ptr = [&](int slot) -> char* { return slot ? slot1 : slot0; };
+    auto slot_ptr = [&](int slot) -> char* { return slot ? xslot1 : xslot0; };
 
-    auto issue_q = [&](uint32_t s, int slot) {
+    auto issue_q = [&](uint32_t s, uint32_t qslot) {
         const uint32_t d0 = s * KC;
         const bool ok = d0 < a.Dp;
 #pragma unroll
         for (int i = 0; i < QDMA; ++i) {
             const int grp = wave + 4 * i;
-            lds_dma16(qres, ok ? qoff[i] + d0 * 2u : kDmaSkip, lds_addr_of(slot_ptr(slot) + grp * 1024));
+            lds_dma16(qres, ok ? qoff[i] + d0 * 2u : kDmaSkip, lds_addr_of(qring + qslot * QBYTES + grp * 1024));
         }
     };
     auto convert_row = [&](int slot, int i) {
@@ -353,13 +364,13 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
         for (int i = 0; i < XLD; ++i) load_row(coff, i);
     };
     h8v av[4], bv[4];
-    auto frags = [&](int slot, int t) {
+    auto frags = [&](int slot, const char* qbase, int t) {
         const char* base = slot_ptr(slot);
         const uint32_t ko = 16u * uint32_t((2 * t + hh) ^ swz);
 #pragma unroll
         for (int m = 0; m < 4; ++m) av[m] = *reinterpret_cast<const h8v*>(base + a_off + m * 32 * ROWB + ko);
 #pragma unroll
-        for (int n = 0; n < 4; ++n) bv[n] = *reinterpret_cast<const h8v*>(base + b_off + n * 32 * ROWB + ko);
+        for (int n = 0; n < 4; ++n) bv[n] = *reinterpret_cast<const h8v*>(qbase + b_off + n * 32 * ROWB + ko);
     };
     auto mma = [&]() {
 #pragma unroll
@@ -369,83 +380,86 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
                 acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[m], bv[n], acc[m][n], 0, 0, 0);
     };
 
-    // prologue: stage 0 in slot 0, stage 1's rows in registers
-    load_x(0);
+    // prologue: query stages 0 and 1 in flight, row stage 0 in slot 0, row stage 1 in registers
     issue_q(0, 0);
+    issue_q(1, 1);
+    load_x(0);
     convert_x(0);
     load_x(1);
-    wait_vmcnt<XLD>();  // the query loads of stage 0 (older than the row loads of stage 1)
+    wait_vmcnt<XLD>();  // the query loads (older than the row loads of stage 1)
     __syncthreads();
-    // Stage s computes from slot s&1 while stage s+1 is written to the other slot (last read in
-    // stage s-1, before the previous barrier).  Past the last stage the loads skip (zeros).
-    // The first k-step's fragments are read before the conversion's LDS writes (which the
-    // compiler must keep after them), so its MFMAs can overlap the conversion; scheduling
-    // barriers keep each stage's work inside its stage.
-    // Order inside a stage: the rows of stage s+1 (loaded during stage s-1) are complete; the
-    // query loads of stage s+1 are issued (invisible to the compiler's wait counts, so they go
-    // after that wait); the conversion of stage s+1 and the row loads of stage s+2 are
-    // interleaved with the MFMAs of the first two k-steps (one wave per SIMD: the VALU work
-    // would otherwise leave the matrix unit idle).
-    auto stage = [&](uint32_t s, auto cur) {
+    // Stage s computes from row slot s&1 and query slot s%3.  Its rows for stage s+1 (loaded
+    // during stage s-1) and its query loads for stage s+1 (issued at the start of stage s-1) are
+    // complete at its start; it issues the query loads of stage s+2 into slot (s+2)%3 (last read
+    // in stage s-1, before the previous barrier), converts stage s+1's rows into the other row
+    // slot (last read in stage s-1 as well) and loads stage s+2's rows, interleaved with the
+    // MFMAs of its first k-step: one wave per SIMD, so VALU work not hidden under MFMAs leaves the
+    // matrix unit idle.  The barrier at its end publishes stage s+1.  Past the last stage the
+    // loads skip (zeros).  Scheduling barriers keep each stage's work inside its stage.
+    auto stage = [&](uint32_t s, auto cur, uint32_t qcur) {
         constexpr int C = decltype(cur)::value;
         __builtin_amdgcn_sched_barrier(0);
         wait_vmcnt<0>();
-        issue_q(s + 1, C ^ 1);
-        frags(C, 0);
+        issue_q(s + 2, qcur == 0 ? 2u : qcur - 1);
+        const char* qbase = qring + qcur * QBYTES;
+        frags(C, qbase, 0);
         __builtin_amdgcn_sched_barrier(0);
-        // k-step 0: each MFMA is followed by the conversion of one row load
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            acc[i >> 2][i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i >> 2], bv[i & 3], acc[i >> 2][i & 3], 0, 0, 0);
-            convert_row(C ^ 1, i);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        // k-step 1: each MFMA is followed by one row load of stage s+2
-        frags(C, 1);
+        // k-step 0: each MFMA is followed by the conversion of one row of stage s+1 and the load
+        // of the same row of stage s+2 into the registers just freed
         const uint32_t coff = col_off(s + 2);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             acc[i >> 2][i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i >> 2], bv[i & 3], acc[i >> 2][i & 3], 0, 0, 0);
+            convert_row(C ^ 1, i);
             load_row(coff, i);
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int t = 2; t < KC / 16; ++t) {
-            frags(C, t);
+        for (int t = 1; t < KC / 16; ++t) {
+            frags(C, qbase, t);
             mma();
         }
-        wait_vmcnt<XLD>();
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
     };
-    uint32_t s = 0;
+    uint32_t s = 0, qcur = 0;
+    auto next3 = [](uint32_t v) { return v == 2 ? 0u : v + 1; };
     for (; s + 1 < nst; s += 2) {
-        stage(s, std::integral_constant<int, 0>());
-        stage(s + 1, std::integral_constant<int, 1>());
+        stage(s, std::integral_constant<int, 0>(), qcur);
+        qcur = next3(qcur);
+        stage(s + 1, std::integral_constant<int, 1>(), qcur);
+        qcur = next3(qcur);
     }
-    if (s < nst) stage(s, std::integral_constant<int, 0>());
+    if (s < nst) stage(s, std::integral_constant<int, 0>(), qcur);
+    // the query loads issued past the last stage (zeros) land in the ring, which the epilogue reuses
     wait_vmcnt<0>();
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
 
-    // squared norms of the tile's rows: the 16 lanes of a row hold 4 columns each.  The pre-test
-    // copies flag (NaN) rows whose fp16 image may hold an infinity (|x| near 65504 or more) and,
-    // for cosine, rows too small for the linear form.
-    float* xxs = norms;
-    float* nxs = norms + TN;
-    float* xxp = norms + 2 * TN;
-    float* nxp = norms + 3 * TN;
+    // squared norms of the tile's rows: the 16 lanes of a row hold 4 columns each; summed across
+    // them with DPP (quad xor 1, quad xor 2, mirror within 8, mirror within 16: every lane ends
+    // with the total, in one fixed order).  The pre-test copies flag (NaN) rows whose fp16 image
+    // may hold an infinity (|x| near 65504 or more) and, for cosine, rows too small for the linear
+    // form; their |x| is the hardware square root (the pre-test's 2^-18 margin covers its ulp).
+    float* xxs = reinterpret_cast<float*>(qring + 2 * QBYTES);
+    float* xxp = xxs + TN;
+    float* nxp = xxs + 2 * TN;
     const float tiny = a.op == OP_COS_DIST ? 8.0f * a.c0x : 0.0f;
+    auto dpp_add = [](float v, auto CTRL) -> float {
+        constexpr int ctrl = decltype(CTRL)::value;
+        return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false));
+    };
 #pragma unroll
     for (int i = 0; i < XLD; ++i) {
         float t = xs[i];
-        t += __shfl_xor(t, 1);
-        t += __shfl_xor(t, 2);
-        t += __shfl_xor(t, 4);
-        t += __shfl_xor(t, 8);
+        t = dpp_add(t, std::integral_constant<int, 0xB1>());   // quad_perm [1,0,3,2]
+        t = dpp_add(t, std::integral_constant<int, 0x4E>());   // quad_perm [2,3,0,1]
+        t = dpp_add(t, std::integral_constant<int, 0x141>());  // row_half_mirror
+        t = dpp_add(t, std::integral_constant<int, 0x140>());  // row_mirror
         if ((lane & 15) == 0) {
             const int r = wr0 + 4 * i;
-            const float nx = sqrtf(t);
+            const float nx = __builtin_amdgcn_sqrtf(t);
             xxs[r] = t;
-            nxs[r] = nx;
             const bool flag = !(t < 4.29e9f) || nx < tiny;
             xxp[r] = flag ? __builtin_nanf("") : t;
             nxp[r] = flag ? __builtin_nanf("") : nx;
@@ -462,7 +476,7 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
             const uint32_t ql = uint32_t(wq * 128 + 32 * n + l32);
             if (ql >= qc) continue;
             const uint32_t qi = qs + ql;
-            const float inv = a.qinfo[qi].z;
+            const float inv = qinf[n].z;
             float* o = a.out_dot + int64_t(qi) * a.ldo + rs;
 #pragma unroll
             for (int m = 0; m < 4; ++m)
@@ -476,21 +490,37 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
         }
         return;
     } else {
-        // Pairs that pass the pre-test are staged per lane in this wave's quarter of the (now free)
-        // stage slots: 64 entries x 64 lanes of (scaled dot, row), then appended with one atomic
-        // per lane and query block.
-        char* stg = (wave < 2 ? slot0 : slot1) + (wave & 1) * (SLOT / 2);
-        float* stg_v = reinterpret_cast<float*>(stg);
-        uint32_t* stg_r = reinterpret_cast<uint32_t*>(stg) + 64 * 64;
-        static_assert(SLOT / 2 >= 64 * 64 * 8, "staging needs 32 KiB per wave");
+        // The accumulators leave the AGPRs only through LDS stores (two query blocks at a time,
+        // 32 KiB per wave of the free LDS), so they are never copied to VGPRs wholesale.  Per
+        // query block the pre-test over the lane's 64 values (read back from LDS) builds a bit
+        // mask without branches; one atomic per lane reserves list space; the appends of a pair
+        // of blocks run after both atomics are issued, so the round trips overlap.
+        static_assert(XBYTES >= 2 * 64 * 64 * 4 && 2 * XBYTES <= 2 * QBYTES, "dump: 32 KiB per wave below the norms");
+        f32x4v* dump = reinterpret_cast<f32x4v*>(wave < 2 ? qring + wave * XBYTES : (wave == 2 ? xslot0 : xslot1));
+        uint64_t valid = 0;  // rows of the tile (the last tile is partial)
 #pragma unroll
-        for (int n = 0; n < 4; ++n) {
-            const uint32_t ql = uint32_t(wq * 128 + 32 * n + l32);
-            if (ql >= qc) continue;
-            const uint32_t qi = qs + ql;
-            const float4 info = a.qinfo[qi];
-            const PreTest pt = pretest_consts(a, info, a.thr[qi]);
-            uint32_t ns = 0;
+        for (int t = 0; t < 64; ++t) {
+            const int r = wn * 128 + 32 * (t >> 4) + 8 * ((t >> 2) & 3) + 4 * hh + (t & 3);
+            valid |= uint64_t(uint32_t(r) < rc) << t;
+        }
+        auto dump_half = [&](auto HC) {
+            constexpr int h = decltype(HC)::value;
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        f32x4v v;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = acc[m][2 * h + b][4 * j + e];
+                        dump[(16 * b + 4 * m + j) * 64 + lane] = v;
+                    }
+        };
+        auto test_block = [&](int n) -> uint64_t {
+            const PreTest pt = pretest_consts(a, qinf[n], qthr[n]);
+            const f32x4v* src = dump + 16 * (n & 1) * 64 + lane;
+            uint64_t mk = 0;
 #pragma unroll
             for (int m = 0; m < 4; ++m)
 #pragma unroll
@@ -498,27 +528,51 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
                     const int r = wn * 128 + 32 * m + 8 * j + 4 * hh;
                     const f32x4v xx = *reinterpret_cast<const f32x4v*>(xxp + r);
                     const f32x4v nx = *reinterpret_cast<const f32x4v*>(nxp + r);
+                    const f32x4v v = src[(4 * m + j) * 64];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const float v = acc[m][n][4 * j + e];
                         const float rhs = fmaf(pt.A, xx[e], fmaf(pt.B, nx[e], pt.C));
-                        if (!(v < rhs) && uint32_t(r + e) < rc) {
-                            stg_v[ns * 64 + lane] = v;
-                            stg_r[ns * 64 + lane] = uint32_t(r + e);
-                            ++ns;
-                        }
+                        mk |= uint64_t(!(v[e] < rhs)) << (16 * m + 4 * j + e);
                     }
                 }
-            if (ns == 0) continue;
-            const uint32_t pos = atomicAdd(a.cnt + qi, ns);
-            for (uint32_t i = 0; i < ns; ++i) {
-                if (pos + i >= a.cap) break;
-                const uint32_t r = stg_r[i * 64 + lane];
-                const int64_t o = int64_t(qi) * a.cap + pos + i;
-                a.cand_dot[o] = stg_v[i * 64 + lane] * info.z;
+            return (uint32_t(wq * 128 + 32 * n + l32) < qc) ? (mk & valid) : 0;
+        };
+        auto reserve = [&](int n, uint64_t mk) -> uint32_t {
+            const uint32_t qi = qs + uint32_t(wq * 128 + 32 * n + l32);
+            return mk ? atomicAdd(a.cnt + qi, uint32_t(__popcll(mk))) : 0u;
+        };
+        auto append = [&](int n, uint64_t mk, uint32_t pos) {
+            const uint32_t qi = qs + uint32_t(wq * 128 + 32 * n + l32);
+            const float inv = qinf[n].z;
+            const float* src = reinterpret_cast<const float*>(dump + 16 * (n & 1) * 64 + lane);
+            for (uint32_t i = pos; mk && i < a.cap; ++i) {
+                const int t = __builtin_ctzll(mk);
+                mk &= mk - 1;
+                const int r = wn * 128 + 32 * (t >> 4) + 8 * ((t >> 2) & 3) + 4 * hh + (t & 3);
+                const float v = src[(t >> 2) * 256 + (t & 3)];
+                const int64_t o = int64_t(qi) * a.cap + i;
+                a.cand_dot[o] = v * inv;
                 a.cand_xx[o] = xxs[r];
-                a.cand_id[o] = a.id_base + rs + r;
+                a.cand_id[o] = a.id_base + rs + uint32_t(r);
             }
+        };
+        dump_half(std::integral_constant<int, 0>());
+        {
+            const uint64_t m0 = test_block(0);
+            const uint32_t p0 = reserve(0, m0);
+            const uint64_t m1 = test_block(1);
+            const uint32_t p1 = reserve(1, m1);
+            append(0, m0, p0);
+            append(1, m1, p1);
+        }
+        dump_half(std::integral_constant<int, 1>());
+        {
+            const uint64_t m2 = test_block(2);
+            const uint32_t p2 = reserve(2, m2);
+            const uint64_t m3 = test_block(3);
+            const uint32_t p3 = reserve(3, m3);
+            append(2, m2, p2);
+            append(3, m3, p3);
         }
     }
 }
