@@ -3,8 +3,10 @@
 Headline (the JSON line's ``value``) = BASELINE.json configs[1]: flat cosine top-100 over
 N=1,000,000 x d=1536 fp32 (rows N(0,1) then L2-normalised), Q=1024 queries = database rows +
 N(0, 0.05) noise, renormalised.  A "step" is one va_fused_topk call over the resident
-database (threshold sample -> filtering MFMA scan -> candidate selection); inputs are in HBM
-before the timed region.  The other configs are measured the same way at full size and
+database (threshold sample -> fp16 MFMA screening scan -> exact fp32 rerank of the band the
+screen's error bound leaves open -> selection); inputs are in HBM before the timed region.  The
+same search on the fp32 scan alone is timed beside it and must return the same ids and
+distances bit for bit (``fp32_scan_only``, ``screened_equals_fp32_scan``).  The other configs are measured the same way at full size and
 reported under ``extra`` (configs[2] int8 top-10, configs[3] binary top-100, configs[4]
 IVF-Flat top-10; configs[0] is the CPU-runnable parity case covered by the tests).
 
@@ -33,6 +35,8 @@ PEAK = {
     "valu_int32_tops": 39.3,
     # dense fp4 (e2m1) MFMA, MI355X published figure (fp6 the same)
     "fp4_mfma_tflops": 10100.0,
+    # dense fp16 MFMA, MI355X published figure
+    "fp16_mfma_tflops": 2500.0,
     "hbm_gbs": 8000.0,
 }
 
@@ -55,10 +59,14 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def measured_traffic() -> float | None:
-    """HBM bytes per launch of the headline scan kernel, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE passes (calibrated against a plain copy)."""
-    f = ROOT / "profiles" / "hbm_traffic__dist_gemm_filter__configs1_cosine_top100.txt"
+TRAFFIC_SCREEN = "profiles/hbm_traffic__screen_filter__configs1_cosine_top100.txt"
+TRAFFIC_FP32 = "profiles/hbm_traffic__dist_gemm_filter__configs1_cosine_top100.txt"
+
+
+def measured_traffic(rel: str = TRAFFIC_SCREEN) -> float | None:
+    """HBM bytes per launch of a scan kernel, from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (calibrated against a plain copy)."""
+    f = ROOT / rel
     if not f.exists():
         return None
     for line in f.read_text().splitlines():
@@ -93,7 +101,8 @@ def mean_phases(phases):
         return {}
     keys = ("sample_ms", "scan_ms", "select_ms", "fallback_ms", "total_ms")
     out = {k: float(np.mean([p[k] for p in phases])) for k in keys}
-    out.update({k: phases[-1][k] for k in ("sample_rows", "candidate_cap", "overflow_rows")})
+    out.update({k: phases[-1][k] for k in ("sample_rows", "candidate_cap", "overflow_rows", "screened",
+                                            "rerank_rows") if k in phases[-1]})
     return out
 
 
@@ -125,6 +134,8 @@ def run_c2(ctx, a, cpu: bool, extra_l2: bool):
     ph = mean_phases(phases)
     flops = 2.0 * Q * N * D
     tflops = flops / (ph["scan_ms"] * 1e-3) / 1e12
+    screened = bool(ph.get("screened", 0))
+    peak = PEAK["fp16_mfma_tflops"] if screened else PEAK["fp32_mfma_tflops"]
     res = {
         "ms_per_step": ms,
         "qps": Q / (ms * 1e-3),
@@ -132,15 +143,44 @@ def run_c2(ctx, a, cpu: bool, extra_l2: bool):
         "scan_tflops": tflops,
         "rank1_is_source_row": float((idx[:, 0].long() == src).float().mean().item()),
         "roofline": {
-            "bound": "mfma", "achieved": tflops, "peak": PEAK["fp32_mfma_tflops"], "unit": "TFLOP/s",
-            "frac": tflops / PEAK["fp32_mfma_tflops"], "traffic": measured_traffic(),
-            "traffic_source": "profiles/hbm_traffic__dist_gemm_filter__configs1_cosine_top100.txt",
-            "kernel": "dist_gemm_kernel<4, 1, true, 2, true> (filtering scan)",
+            "bound": "mfma", "achieved": tflops, "peak": peak, "unit": "TFLOP/s",
+            "frac": tflops / peak,
+            "traffic": measured_traffic(TRAFFIC_SCREEN if screened else TRAFFIC_FP32),
+            "traffic_source": TRAFFIC_SCREEN if screened else TRAFFIC_FP32,
+            "kernel": ("screen_kernel<1> (fp16 MFMA screening scan; exact fp32 rerank of a proven band)" if screened
+                       else "dist_gemm_kernel<4, 1, true, 2, true> (fp32 filtering scan)"),
             "algorithmic": f"2*Q*N*D = {flops:.4g} FLOP per launch",
+            "fp32_mfma_equivalent_frac": tflops / PEAK["fp32_mfma_tflops"],
         },
     }
     log(f"configs[1] cosine top-100: {ms:.3f} ms/step = {res['qps']:.0f} QPS; scan {ph['scan_ms']:.3f} ms = "
-        f"{tflops:.1f} TFLOP/s ({100 * tflops / PEAK['fp32_mfma_tflops']:.1f}% fp32 MFMA)")
+        f"{tflops:.1f} TFLOP/s ({100 * tflops / peak:.1f}% of the {'fp16' if screened else 'fp32'} MFMA peak)")
+    if screened:
+        # the same search on the fp32 scan alone: it must return the same ids and distances, bit for bit
+        from vectoraccelerate_amd import _lib
+
+        idx32 = ctx.empty((Q, k), torch.int32)
+        dist32 = ctx.empty((Q, k), torch.float32)
+        ctx.set_option(_lib.VA_OPT_SCREEN, 1)
+        try:
+            ms32, ph32 = timed(ctx, lambda: kern.encode(q, x, idx32, dist32, params, Metric.cosine),
+                               max(3, a.steps // 2), 1)
+        finally:
+            ctx.set_option(_lib.VA_OPT_SCREEN, 0)
+        s32 = mean_phases(ph32)["scan_ms"]
+        same = bool(torch.equal(idx, idx32)) and bool(torch.equal(dist.view(torch.int32), dist32.view(torch.int32)))
+        res["fp32_scan_only"] = {
+            "ms_per_step": ms32, "qps": Q / (ms32 * 1e-3), "scan_ms": s32,
+            "scan_tflops": flops / (s32 * 1e-3) / 1e12,
+            "mfma_frac": flops / (s32 * 1e-3) / 1e12 / PEAK["fp32_mfma_tflops"],
+            "kernel": "dist_gemm_kernel<4, 1, true, 2, true>",
+            "traffic": measured_traffic(TRAFFIC_FP32), "traffic_source": TRAFFIC_FP32,
+        }
+        res["screened_equals_fp32_scan"] = same
+        log(f"configs[1] fp32 scan only: {ms32:.3f} ms/step, scan {s32:.3f} ms; screened result identical: {same}")
+        if not same:
+            raise SystemExit("screened search differs from the fp32 scan")
+        del idx32, dist32
     if extra_l2:
         idx10 = ctx.empty((Q, 10), torch.int32)
         dist10 = ctx.empty((Q, 10), torch.float32)
@@ -150,7 +190,7 @@ def run_c2(ctx, a, cpu: bool, extra_l2: bool):
         s10 = mean_phases(ph10)["scan_ms"]
         res["l2sq_top10_same_shape"] = {"ms_per_step": ms10, "qps": Q / (ms10 * 1e-3), "scan_ms": s10,
                                         "scan_tflops": flops / (s10 * 1e-3) / 1e12,
-                                        "mfma_frac": flops / (s10 * 1e-3) / 1e12 / PEAK["fp32_mfma_tflops"]}
+                                        "mfma_frac": flops / (s10 * 1e-3) / 1e12 / peak}
         log(f"configs[1] shape, L2^2 top-10: {ms10:.3f} ms/step, scan {s10:.3f} ms")
     if cpu:
         from oracle import oracle

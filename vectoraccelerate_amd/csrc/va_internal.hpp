@@ -185,6 +185,21 @@ __device__ __forceinline__ void lds_dma16(const dma_rsrc& rsrc, uint32_t voff, u
                  : "memory");
 }
 
+// The one-dword form: lane i's 4 bytes land at lds_addr + 4*i (256 B per wave).  Used as an L2
+// prefetch whose data is not needed.
+__device__ __forceinline__ void lds_dma4(const dma_rsrc& rsrc, uint32_t voff, uint32_t lds_addr) {
+    dma_rsrc r;
+    r[0] = __builtin_amdgcn_readfirstlane(rsrc[0]);
+    r[1] = __builtin_amdgcn_readfirstlane(rsrc[1]);
+    r[2] = __builtin_amdgcn_readfirstlane(rsrc[2]);
+    r[3] = __builtin_amdgcn_readfirstlane(rsrc[3]);
+    const uint32_t l = __builtin_amdgcn_readfirstlane(lds_addr);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                 :
+                 : "s"(l), "v"(voff), "s"(r)
+                 : "memory");
+}
+
 // s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding: vmcnt in bits 3:0 and 15:14).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

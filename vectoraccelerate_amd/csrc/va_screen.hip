@@ -56,6 +56,8 @@ constexpr int QBYTES = TQ * ROWB;    // 32 KiB of queries per stage
 constexpr int XBYTES = TN * ROWB;    // 32 KiB of rows per stage
 constexpr int QDMA = QBYTES / 1024 / 4;   // 1 KiB direct loads per wave per stage (8)
 constexpr int XLD = TN * KC / 4 / 256;    // float4 row loads per thread per stage (16)
+constexpr int PF_OPS = 2;                 // one-dword L2 prefetches per wave per stage (64 rows x 2 lines)
+constexpr int PF_AHEAD = 3;               // stages between a row prefetch and the compute
 constexpr int DP_ALIGN = KC;              // fp16 query rows are padded to a multiple of KC
 }  // namespace scr
 
@@ -240,13 +242,16 @@ __global__ __launch_bounds__(256) void screen_prep_kernel(const float* __restric
 template <int MODE>
 __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
     using namespace scr;
-    // LDS (160 KiB): a ring of three query stages (direct loads run two stages ahead) and two
-    // row stages.  The row slots are separate objects, so the compiler sees that the
-    // conversion's writes to one never alias the fragment reads of the other.  After the main
-    // loop the query ring holds the epilogue's staging and the row norms.
-    __shared__ __attribute__((aligned(1024))) char qring[3 * QBYTES];
+    // LDS: two query stages and two row stages (separate objects, so the compiler sees that the
+    // conversion's writes to one row slot never alias the fragment reads of the other), the
+    // landing area of the L2 prefetches, and the row norms.  After the main loop the four
+    // stage slots hold the epilogue's accumulator dumps.
+    __shared__ __attribute__((aligned(1024))) char qslot0[QBYTES];
+    __shared__ __attribute__((aligned(1024))) char qslot1[QBYTES];
     __shared__ __attribute__((aligned(1024))) char xslot0[XBYTES];
     __shared__ __attribute__((aligned(1024))) char xslot1[XBYTES];
+    __shared__ __attribute__((aligned(1024))) char pf_sink[4 * PF_OPS * 256];
+    __shared__ __attribute__((aligned(16))) float norms[3 * TN];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -324,13 +329,13 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
 
     auto slot_ptr = [&](int slot) -> char* { return slot ? xslot1 : xslot0; };
 
-    auto issue_q = [&](uint32_t s, uint32_t qslot) {
+    auto issue_q = [&](uint32_t s, int qslot) {
         const uint32_t d0 = s * KC;
         const bool ok = d0 < a.Dp;
 #pragma unroll
         for (int i = 0; i < QDMA; ++i) {
             const int grp = wave + 4 * i;
-            lds_dma16(qres, ok ? qoff[i] + d0 * 2u : kDmaSkip, lds_addr_of(qring + qslot * QBYTES + grp * 1024));
+            lds_dma16(qres, ok ? qoff[i] + d0 * 2u : kDmaSkip, lds_addr_of((qslot ? qslot1 : qslot0) + grp * 1024));
         }
     };
     auto convert_row = [&](int slot, int i) {
@@ -363,9 +368,24 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
 #pragma unroll
         for (int i = 0; i < XLD; ++i) load_row(coff, i);
     };
+    // L2 prefetch of this wave's rows of stage s: one dword per 128-byte line (rows 64w + 32i +
+    // L/2, line L%2 of the row's 256 bytes), landing in a per-wave sink of the LDS.  Invisible
+    // to the compiler's wait counts, like the query loads.
+    const uint32_t pf_base = (uint32_t(64 * wave) + uint32_t(lane >> 1)) * uint32_t(a.ldx) * 4u + 128u * uint32_t(lane & 1);
+    const dma_rsrc pres = make_dma_rsrc(a.x + int64_t(rs) * a.ldx, uint32_t((uint64_t(rc - 1) * a.ldx + a.D) * 4));
+    auto prefetch = [&](uint32_t s) {
+        const uint32_t d0 = s * KC;
+        const bool ok = d0 + 32u * uint32_t(lane & 1) < a.D;
+#pragma unroll
+        for (int i = 0; i < PF_OPS; ++i) {
+            const uint32_t off = ok ? pf_base + uint32_t(i) * 32u * uint32_t(a.ldx) * 4u + d0 * 4u : kDmaSkip;
+            lds_dma4(pres, off, lds_addr_of(pf_sink + (wave * PF_OPS + i) * 256));
+        }
+    };
     h8v av[4], bv[4];
-    auto frags = [&](int slot, const char* qbase, int t) {
+    auto frags = [&](int slot, int t) {
         const char* base = slot_ptr(slot);
+        const char* qbase = slot ? qslot1 : qslot0;
         const uint32_t ko = 16u * uint32_t((2 * t + hh) ^ swz);
 #pragma unroll
         for (int m = 0; m < 4; ++m) av[m] = *reinterpret_cast<const h8v*>(base + a_off + m * 32 * ROWB + ko);
@@ -380,29 +400,30 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
                 acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[m], bv[n], acc[m][n], 0, 0, 0);
     };
 
-    // prologue: query stages 0 and 1 in flight, row stage 0 in slot 0, row stage 1 in registers
+    // prologue: query stage 0 and row stage 0 in slot 0, row stage 1 in registers, rows of stages
+    // 1 .. PF_AHEAD-1 prefetched
     issue_q(0, 0);
-    issue_q(1, 1);
     load_x(0);
     convert_x(0);
     load_x(1);
-    wait_vmcnt<XLD>();  // the query loads (older than the row loads of stage 1)
+#pragma unroll
+    for (uint32_t p = 1; p < PF_AHEAD; ++p) prefetch(p);
+    wait_vmcnt<XLD + PF_OPS * (PF_AHEAD - 1)>();  // the query loads (older than the rest)
     __syncthreads();
-    // Stage s computes from row slot s&1 and query slot s%3.  Its rows for stage s+1 (loaded
-    // during stage s-1) and its query loads for stage s+1 (issued at the start of stage s-1) are
-    // complete at its start; it issues the query loads of stage s+2 into slot (s+2)%3 (last read
-    // in stage s-1, before the previous barrier), converts stage s+1's rows into the other row
-    // slot (last read in stage s-1 as well) and loads stage s+2's rows, interleaved with the
-    // MFMAs of its first k-step: one wave per SIMD, so VALU work not hidden under MFMAs leaves the
-    // matrix unit idle.  The barrier at its end publishes stage s+1.  Past the last stage the
-    // loads skip (zeros).  Scheduling barriers keep each stage's work inside its stage.
-    auto stage = [&](uint32_t s, auto cur, uint32_t qcur) {
+    // Stage s computes from slot s&1.  At its start the rows of stage s+1 (loaded during stage
+    // s-1) are complete (only younger prefetches may be in flight); it issues the query loads of
+    // stage s+1 into the other query slot and converts stage s+1's rows into the other row slot
+    // (both last read in stage s-1, before the previous barrier), loads stage s+2's rows and
+    // prefetches stage s+PF_AHEAD's, interleaved with the MFMAs of its first k-step: one wave per
+    // SIMD, so VALU work not hidden under MFMAs leaves the matrix unit idle.  Before its closing
+    // barrier (which publishes stage s+1) it waits for its query loads only.  Past the last stage
+    // the loads skip (zeros).  Scheduling barriers keep each stage's work inside its stage.
+    auto stage = [&](uint32_t s, auto cur) {
         constexpr int C = decltype(cur)::value;
         __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt<0>();
-        issue_q(s + 2, qcur == 0 ? 2u : qcur - 1);
-        const char* qbase = qring + qcur * QBYTES;
-        frags(C, qbase, 0);
+        wait_vmcnt<PF_OPS * (PF_AHEAD - 2)>();
+        issue_q(s + 1, C ^ 1);
+        frags(C, 0);
         __builtin_amdgcn_sched_barrier(0);
         // k-step 0: each MFMA is followed by the conversion of one row of stage s+1 and the load
         // of the same row of stage s+2 into the registers just freed
@@ -414,24 +435,24 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
             load_row(coff, i);
             __builtin_amdgcn_sched_barrier(0);
         }
+        prefetch(s + PF_AHEAD);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int t = 1; t < KC / 16; ++t) {
-            frags(C, qbase, t);
+            frags(C, t);
             mma();
         }
+        wait_vmcnt<XLD + PF_OPS>();  // younger than the query loads: stage s+2's rows and prefetch
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
     };
-    uint32_t s = 0, qcur = 0;
-    auto next3 = [](uint32_t v) { return v == 2 ? 0u : v + 1; };
+    uint32_t s = 0;
     for (; s + 1 < nst; s += 2) {
-        stage(s, std::integral_constant<int, 0>(), qcur);
-        qcur = next3(qcur);
-        stage(s + 1, std::integral_constant<int, 1>(), qcur);
-        qcur = next3(qcur);
+        stage(s, std::integral_constant<int, 0>());
+        stage(s + 1, std::integral_constant<int, 1>());
     }
-    if (s < nst) stage(s, std::integral_constant<int, 0>(), qcur);
-    // the query loads issued past the last stage (zeros) land in the ring, which the epilogue reuses
+    if (s < nst) stage(s, std::integral_constant<int, 0>());
+    // loads issued past the last stage (zeros) land in LDS the epilogue reuses
     wait_vmcnt<0>();
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
@@ -441,9 +462,9 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
     // with the total, in one fixed order).  The pre-test copies flag (NaN) rows whose fp16 image
     // may hold an infinity (|x| near 65504 or more) and, for cosine, rows too small for the linear
     // form; their |x| is the hardware square root (the pre-test's 2^-18 margin covers its ulp).
-    float* xxs = reinterpret_cast<float*>(qring + 2 * QBYTES);
-    float* xxp = xxs + TN;
-    float* nxp = xxs + 2 * TN;
+    float* xxs = norms;
+    float* xxp = norms + TN;
+    float* nxp = norms + 2 * TN;
     const float tiny = a.op == OP_COS_DIST ? 8.0f * a.c0x : 0.0f;
     auto dpp_add = [](float v, auto CTRL) -> float {
         constexpr int ctrl = decltype(CTRL)::value;
@@ -495,8 +516,8 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
         // query block the pre-test over the lane's 64 values (read back from LDS) builds a bit
         // mask without branches; one atomic per lane reserves list space; the appends of a pair
         // of blocks run after both atomics are issued, so the round trips overlap.
-        static_assert(XBYTES >= 2 * 64 * 64 * 4 && 2 * XBYTES <= 2 * QBYTES, "dump: 32 KiB per wave below the norms");
-        f32x4v* dump = reinterpret_cast<f32x4v*>(wave < 2 ? qring + wave * XBYTES : (wave == 2 ? xslot0 : xslot1));
+        static_assert(XBYTES >= 2 * 64 * 64 * 4 && QBYTES >= 2 * 64 * 64 * 4, "dump: 32 KiB per wave");
+        f32x4v* dump = reinterpret_cast<f32x4v*>(wave == 0 ? qslot0 : wave == 1 ? qslot1 : wave == 2 ? xslot0 : xslot1);
         uint64_t valid = 0;  // rows of the tile (the last tile is partial)
 #pragma unroll
         for (int t = 0; t < 64; ++t) {
@@ -816,11 +837,11 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
         a.cand_id = cid;
         a.cap = uint32_t(cap);
         VA_CHECK_STATUS(launch_screen<SCREEN_FILTER>(ctx, a));
+        VA_CHECK_STATUS(pm.mark(2));
         // (dot, |x|^2) -> (key of hi, key of lo), in place
         VA_CHECK_STATUS(launch_bounds(ctx, a, reinterpret_cast<float*>(chi), nullptr, reinterpret_cast<float*>(clo), cnt,
                                       uint32_t(cap), int64_t(cap), Q));
     }
-    VA_CHECK_STATUS(pm.mark(2));
     ctx->last_scan.scan_launches = 1;
     ctx->last_scan.sample_rows = uint32_t(S);
     ctx->last_scan.candidate_cap = uint32_t(cap);
