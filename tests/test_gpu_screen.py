@@ -128,3 +128,40 @@ def test_large_magnitudes_scale_exactly(ctx):
     q = (g.standard_normal((300, 256)) * 1e-3).astype(np.float32)
     for metric in (L2SQ, DOT):
         _same(ctx, metric, q, x, 25)
+
+
+@pytest.mark.parametrize("metric", [L2SQ, COSINE, DOT, L2])
+def test_mixed_norms_and_large_k(ctx, metric):
+    """Rows whose norms span twelve decades and a k of 1000: the bound's relative and absolute
+    terms all matter, and the k-th distance sits deep in the distribution."""
+    g = np.random.default_rng(21 + metric)
+    x = g.standard_normal((40000, 96), dtype=np.float32)
+    x *= (10.0 ** g.uniform(-6, 6, size=(40000, 1))).astype(np.float32)
+    q = g.standard_normal((260, 96), dtype=np.float32)
+    q *= (10.0 ** g.uniform(-3, 3, size=(260, 1))).astype(np.float32)
+    _same(ctx, metric, q, x, 1000)
+
+
+def test_cosine_anticorrelated_queries(ctx):
+    """Queries pointing away from every row: the k-th cosine distance is near 2, where the
+    pre-test's linear form does not hold and every row must pass."""
+    g = np.random.default_rng(22)
+    x = np.abs(g.standard_normal((30000, 64), dtype=np.float32)) + 0.1
+    q = -np.abs(g.standard_normal((200, 64), dtype=np.float32)) - 0.1
+    _same(ctx, COSINE, q, x, 50)
+    # half the queries correlated, half anti-correlated, in one launch
+    q[::2] *= -1.0
+    _same(ctx, COSINE, q, x, 50)
+
+
+@pytest.mark.parametrize("metric", [L2SQ, COSINE])
+def test_duplicate_queries_and_rows_at_scale(ctx, metric):
+    """Repeated queries and exact duplicate rows across the sample and the scan."""
+    g = np.random.default_rng(23)
+    base = g.standard_normal((3000, 128), dtype=np.float32)
+    x = np.concatenate([base] * 12)  # 36,000 rows, every row 12 times
+    q = np.repeat(base[:40], 7, axis=0) + 0.0  # 280 queries, each repeated 7 times
+    si, sd, _ = _same(ctx, metric, q, x, 36)
+    # the exact duplicates of the query's source row come first, in index order
+    for r in range(0, 280, 7):
+        np.testing.assert_array_equal(si[r, :12], (r // 7) + 3000 * np.arange(12))
