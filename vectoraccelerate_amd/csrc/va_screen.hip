@@ -625,7 +625,8 @@ __global__ __launch_bounds__(256) void screen_compact_kernel(const uint32_t* __r
                                                              const uint32_t* __restrict__ bound, uint32_t cap,
                                                              uint32_t* __restrict__ rr, uint32_t* __restrict__ rcount,
                                                              uint32_t rcap, uint32_t* __restrict__ ovf_cnt,
-                                                             uint32_t* __restrict__ ovf_rows) {
+                                                             uint32_t* __restrict__ ovf_rows,
+                                                             uint32_t* __restrict__ max_count) {
     __shared__ uint32_t s_n;
     const uint32_t q = blockIdx.x;
     const int tid = threadIdx.x;
@@ -663,6 +664,7 @@ __global__ __launch_bounds__(256) void screen_compact_kernel(const uint32_t* __r
             ovf_rows[p] = q;
         } else {
             rcount[q] = m;
+            atomicMax(max_count, m);
         }
     }
 }
@@ -741,9 +743,9 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     const ScanPlan plan = plan_scan(ctx, Q, N, k);
     const uint64_t S = plan.S;
     const uint64_t cap = plan.cap;
-    // rerank capacity: k plus the band of rows whose interval straddles the k-th bound
-    const uint64_t rcap = std::min<uint64_t>(N, (std::max<uint64_t>(2ull * k + 256, cap / 8) + 127) / 128 * 128);
-    const uint32_t gtiles = uint32_t((rcap + 127) / 128);
+    // rerank capacity: k plus the band of rows whose interval straddles the k-th bound (the
+    // launch covers only the longest list actually built)
+    const uint64_t rcap = std::min<uint64_t>(N, (std::max<uint64_t>(2ull * k + 256, cap / 4) + 127) / 128 * 128);
     const Bound bnd = make_bound(D);
 
     SelectArgs base;
@@ -820,7 +822,7 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     }
     // ---- 3. screening scan -------------------------------------------------------------------
     VA_CHECK_STATUS(fill_u32(ctx, cnt, Q, 0));
-    VA_CHECK_STATUS(fill_u32(ctx, ovf_cnt, 1, 0));
+    VA_CHECK_STATUS(fill_u32(ctx, ovf_cnt, 2, 0));  // [0] overflowed queries, [1] longest rerank list
     VA_CHECK_STATUS(pm.mark(1));
     {
         ScreenArgs a = sa;
@@ -863,8 +865,13 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     }
     // ---- 5. rerank lists ------------------------------------------------------------------------
     screen_compact_kernel<<<dim3(Q), dim3(256), 0, ctx->stream>>>(cnt, clo, cid, ubound, uint32_t(cap), rr, rcount,
-                                                                 uint32_t(rcap), ovf_cnt, ovf_rows);
+                                                                 uint32_t(rcap), ovf_cnt, ovf_rows, ovf_cnt + 1);
     VA_CHECK_LAUNCH(ctx);
+    // the overflow count and the longest list (sizes the rerank grid): the one read-back
+    VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->host_word, ovf_cnt, 8, hipMemcpyDeviceToHost, ctx->stream));
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    const uint32_t n_ovf = ctx->host_word[0];
+    const uint32_t gtiles = std::max<uint32_t>(1, (ctx->host_word[1] + 127) / 128);
     // ---- 6. exact fp32 keys of the rerank rows ---------------------------------------------------
     {
         DistArgs a;
@@ -897,9 +904,6 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
         VA_CHECK_STATUS(launch_select(ctx, a));
     }
     VA_CHECK_STATUS(pm.mark(3));
-    VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->host_word, ovf_cnt, 4, hipMemcpyDeviceToHost, ctx->stream));
-    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    const uint32_t n_ovf = ctx->host_word[0];
     ctx->last_scan.overflow_rows = n_ovf;
     if (ctx->profiling) {
         // diagnostics only: how many rows the exact rerank scored
