@@ -148,6 +148,18 @@ va_status va_dot_all_pairs(va_context* ctx, const float* queries, const float* d
 va_status va_fused_topk(va_context* ctx, va_metric metric, const float* queries, const float* database,
                         uint32_t num_queries, uint32_t num_database, uint32_t dim, uint32_t k,
                         uint32_t* out_idx, float* out_dist);
+/* The same search over a database in HOST memory (larger than HBM, or not resident): the
+ * database is streamed in chunks of chunk_rows rows (0 = ~512 MiB) through two device buffers,
+ * uploads on an auxiliary stream overlapping the scan of the previous chunk, and the per-chunk
+ * top-k lists are merged into a running top-k (ids offset by each chunk's first row).  Results
+ * equal va_fused_topk's on the same database.  host_database should be pinned (hipHostMalloc /
+ * torch pin_memory) for the uploads to overlap; queries and outputs are device pointers.
+ * Synchronous (returns when the outputs are complete).  Replaces FusedL2TopKKernel's chunked
+ * fallback with a running GPU merge (Kernels/Metal4/FusedL2TopKKernel.swift:765-931), which on
+ * Apple's unified memory reads the dataset buffer in place. */
+va_status va_fused_topk_streamed(va_context* ctx, va_metric metric, const float* queries, const float* host_database,
+                                 uint32_t num_queries, uint32_t num_database, uint32_t dim, uint32_t k,
+                                 uint32_t chunk_rows, uint32_t* out_idx, float* out_dist);
 /* Row-wise top-k of a value matrix values[Q x N] (sorted output).
  * Replaces TopKSelectionKernel.encode/execute (Kernels/Metal4/TopKSelectionKernel.swift:228-368). */
 va_status va_topk_select(va_context* ctx, const float* values, uint32_t num_rows, uint32_t num_elements,

@@ -288,3 +288,45 @@ def test_topk_merge_matches_oracle(ctx, oracle):
     ctx.synchronize()
     np.testing.assert_array_equal(out_i.cpu().numpy().view(np.uint32), oi)
     np.testing.assert_array_equal(out_d.cpu().numpy(), od)
+
+
+# ---------------------------------------------------------------------------------------
+# streamed search over a host-resident database (chunked upload + running merge)
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("metric", [L2SQ, COSINE, DOT, L2])
+@pytest.mark.parametrize("Q,N,D,k,chunk", [(300, 50000, 128, 10, 7000), (64, 20011, 96, 50, 4096),
+                                           (5, 3000, 40, 20, 7), (257, 40000, 768, 100, 0)])
+def test_streamed_equals_resident(ctx, metric, Q, N, D, k, chunk):
+    """The host-streamed search returns the resident search's ids and distances bit for bit,
+    for chunk sizes that do not divide N and chunks smaller than k."""
+    import torch
+    from vectoraccelerate_amd import FusedL2TopKKernel, FusedL2TopKParameters, Metric
+
+    g = rng(Q + N + D + metric)
+    x = g.standard_normal((N, D)).astype(np.float32)
+    q = g.standard_normal((Q, D)).astype(np.float32)
+    kern = FusedL2TopKKernel(ctx)
+    p = FusedL2TopKParameters(Q, N, D, k)
+    ri, rd = _fused(ctx, metric, q, x, k)
+    host = torch.from_numpy(x).pin_memory()
+    res = kern.executeStreamed(ctx.buffer(q), host, p, Metric(metric), chunkRows=chunk)
+    si = res.indices.cpu().numpy().view(np.uint32)
+    sd = res.distances.cpu().numpy()
+    np.testing.assert_array_equal(si, ri)
+    np.testing.assert_array_equal(sd.view(np.uint32), rd.view(np.uint32))
+
+
+def test_streamed_pageable_and_errors(ctx):
+    import torch
+    from vectoraccelerate_amd import FusedL2TopKKernel, FusedL2TopKParameters, Metric, VectorError
+
+    g = rng(91)
+    x = g.standard_normal((9000, 32)).astype(np.float32)
+    q = g.standard_normal((10, 32)).astype(np.float32)
+    kern = FusedL2TopKKernel(ctx)
+    p = FusedL2TopKParameters(10, 9000, 32, 5)
+    ri, rd = _fused(ctx, L2SQ, q, x, 5)
+    res = kern.executeStreamed(ctx.buffer(q), torch.from_numpy(x), p, Metric(L2SQ), chunkRows=2500)  # pageable
+    np.testing.assert_array_equal(res.indices.cpu().numpy().view(np.uint32), ri)
+    with pytest.raises(VectorError):
+        kern.executeStreamed(ctx.buffer(q), ctx.buffer(x), p, Metric(L2SQ))  # a device tensor is refused

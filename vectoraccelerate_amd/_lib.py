@@ -62,6 +62,7 @@ SIGNATURES: dict[str, tuple] = {
     "va_cosine_all_pairs": (_st, [_p, _p, _p, _p, _u32, _u32, _u32, _i32]),
     "va_dot_all_pairs": (_st, [_p, _p, _p, _p, _u32, _u32, _u32, _i32]),
     "va_fused_topk": (_st, [_p, _i32, _p, _p, _u32, _u32, _u32, _u32, _p, _p]),
+    "va_fused_topk_streamed": (_st, [_p, _i32, _p, _p, _u32, _u32, _u32, _u32, _u32, _p, _p]),
     "va_topk_select": (_st, [_p, _p, _u32, _u32, _u32, _i32, _p, _p]),
     "va_topk_merge": (_st, [_p, _p, _p, _p, _p, _u32, _u32, _u32, _p, _p]),
     "va_sq_params_per_dim": (_st, [_p, _p, _u32, _u32, _p, _p, _p, _p]),

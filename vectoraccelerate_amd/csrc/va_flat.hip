@@ -1,5 +1,6 @@
 // va_flat.hip — fp32 distance entry points and the fused flat top-k search.
 #include <algorithm>
+#include <vector>
 
 #include "va_internal.hpp"
 
@@ -147,6 +148,34 @@ struct F32Producer final : KeyProducer {
 };
 
 }  // namespace
+
+// Exact top-k of queries (device) against a device database: the screened path where it applies,
+// else the fp32 scan.  Synchronises the stream (the scan reads back an overflow counter).
+va_status flat_topk(va_context* ctx, DistOp op, const float* q, const float* x, uint32_t Q, uint32_t N, uint32_t D,
+                    uint32_t k, uint32_t* out_idx, float* out_dist) {
+    F32Producer p;
+    p.ctx = ctx;
+    p.q = q;
+    p.x = x;
+    p.Q = Q;
+    p.N = N;
+    p.D = D;
+    p.op = op;
+    ScanOutputs o;
+    o.idx = out_idx;
+    o.f = out_dist;
+    o.key_kind = 0;
+    ScreenInput si;
+    si.q = q;
+    si.x = x;
+    si.Q = Q;
+    si.N = N;
+    si.D = D;
+    si.op = op;
+    if (screen_applies(ctx, si, k)) return screened_topk_scan(ctx, si, p, k, o);
+    return exact_topk_scan(ctx, p, Q, N, k, o);
+}
+
 }  // namespace va
 
 extern "C" {
@@ -201,27 +230,107 @@ va_status va_fused_topk(va_context* ctx, va_metric metric, const float* queries,
     VA_REQUIRE(ctx, k <= VA_MAX_K, "k %u exceeds maximum supported k %u", k, VA_MAX_K);
     VA_REQUIRE(ctx, metric >= VA_METRIC_L2SQ && metric <= VA_METRIC_L2, "va_fused_topk: unknown metric %d", int(metric));
     va::DeviceGuard g(ctx->device);
-    va::F32Producer p;
-    p.ctx = ctx;
-    p.q = queries;
-    p.x = database;
-    p.Q = num_queries;
-    p.N = num_database;
-    p.D = dim;
-    p.op = va::metric_op(metric);
-    va::ScanOutputs o;
-    o.idx = out_idx;
-    o.f = out_dist;
-    o.key_kind = 0;
-    va::ScreenInput si;
-    si.q = queries;
-    si.x = database;
-    si.Q = num_queries;
-    si.N = num_database;
-    si.D = dim;
-    si.op = p.op;
-    if (va::screen_applies(ctx, si, k)) return va::screened_topk_scan(ctx, si, p, k, o);
-    return va::exact_topk_scan(ctx, p, num_queries, num_database, k, o);
+    return va::flat_topk(ctx, va::metric_op(metric), queries, database, num_queries, num_database, dim, k, out_idx,
+                         out_dist);
+}
+
+va_status va_fused_topk_streamed(va_context* ctx, va_metric metric, const float* queries, const float* host_database,
+                                 uint32_t num_queries, uint32_t num_database, uint32_t dim, uint32_t k,
+                                 uint32_t chunk_rows, uint32_t* out_idx, float* out_dist) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    VA_REQUIRE(ctx, queries && host_database && out_idx, "va_fused_topk_streamed: NULL pointer");
+    VA_REQUIRE(ctx, num_queries > 0, "numQueries must be positive, got %u", num_queries);
+    VA_REQUIRE(ctx, num_database > 0, "numDataset must be positive, got %u", num_database);
+    VA_REQUIRE(ctx, dim > 0, "dimension must be positive, got %u", dim);
+    VA_REQUIRE(ctx, k > 0, "k must be positive, got %u", k);
+    VA_REQUIRE(ctx, k <= VA_MAX_K, "k %u exceeds maximum supported k %u", k, VA_MAX_K);
+    VA_REQUIRE(ctx, metric >= VA_METRIC_L2SQ && metric <= VA_METRIC_L2, "va_fused_topk_streamed: unknown metric %d",
+               int(metric));
+    va::DeviceGuard g(ctx->device);
+    const va::DistOp op = va::metric_op(metric);
+    const uint64_t row_bytes = uint64_t(dim) * 4;
+    // chunks of ~512 MiB by default (two are resident: the one being scanned and the next)
+    uint64_t rows = chunk_rows ? chunk_rows : std::max<uint64_t>(1, (512ull << 20) / row_bytes);
+    rows = std::min<uint64_t>(rows, num_database);
+    const uint32_t C = uint32_t(rows);
+    const uint32_t nch = uint32_t((uint64_t(num_database) + C - 1) / C);
+    const uint64_t qk = uint64_t(num_queries) * k;
+
+    // Buffers of this call (the scan and the merge use the context's scratch arena in turn, so the
+    // running lists and the chunks cannot live there).
+    struct Owned {
+        std::vector<void*> p;
+        std::vector<hipEvent_t> e;
+        ~Owned() {
+            for (void* q : p) (void)hipFree(q);
+            for (hipEvent_t ev : e) (void)hipEventDestroy(ev);
+        }
+    } own;
+    auto alloc = [&](size_t bytes, void** out) -> va_status {
+        VA_CHECK_HIP(ctx, hipMalloc(out, bytes));
+        own.p.push_back(*out);
+        return VA_OK;
+    };
+    float* buf[2] = {nullptr, nullptr};
+    uint32_t* run_idx[2];
+    float* run_dist[2];
+    uint32_t* ch_idx;
+    float* ch_dist;
+    for (int b = 0; b < (nch > 1 ? 2 : 1); ++b)
+        VA_CHECK_STATUS(alloc(size_t(C) * row_bytes, reinterpret_cast<void**>(&buf[b])));
+    for (int b = 0; b < 2; ++b) {
+        VA_CHECK_STATUS(alloc(qk * 4, reinterpret_cast<void**>(&run_idx[b])));
+        VA_CHECK_STATUS(alloc(qk * 4, reinterpret_cast<void**>(&run_dist[b])));
+    }
+    VA_CHECK_STATUS(alloc(qk * 4, reinterpret_cast<void**>(&ch_idx)));
+    VA_CHECK_STATUS(alloc(qk * 4, reinterpret_cast<void**>(&ch_dist)));
+    hipEvent_t up_ev[2], use_ev[2];
+    for (int b = 0; b < 2; ++b) {
+        VA_CHECK_HIP(ctx, hipEventCreateWithFlags(&up_ev[b], hipEventDisableTiming));
+        own.e.push_back(up_ev[b]);
+        VA_CHECK_HIP(ctx, hipEventCreateWithFlags(&use_ev[b], hipEventDisableTiming));
+        own.e.push_back(use_ev[b]);
+    }
+    // uploads run on an auxiliary stream (after the work already queued on the context's stream)
+    VA_CHECK_STATUS(va::aux_fork(ctx));
+    hipStream_t cs = ctx->aux[0];
+    auto upload = [&](uint32_t c) -> va_status {
+        const uint64_t r0 = uint64_t(c) * C;
+        const uint64_t n = std::min<uint64_t>(C, num_database - r0);
+        VA_CHECK_HIP(ctx, hipMemcpyAsync(buf[c & 1], host_database + r0 * dim, size_t(n * row_bytes),
+                                         hipMemcpyHostToDevice, cs));
+        VA_CHECK_HIP(ctx, hipEventRecord(up_ev[c & 1], cs));
+        return VA_OK;
+    };
+    VA_CHECK_STATUS(upload(0));
+    if (nch > 1) VA_CHECK_STATUS(upload(1));
+    int cur = 0;
+    for (uint32_t c = 0; c < nch; ++c) {
+        const int b = int(c & 1);
+        const uint32_t r0 = c * C;
+        const uint32_t n = std::min(C, num_database - r0);
+        VA_CHECK_HIP(ctx, hipStreamWaitEvent(ctx->stream, up_ev[b], 0));
+        // the scan synchronises the host, so the upload of chunk c+1 (queued before) overlaps it
+        VA_CHECK_STATUS(va::flat_topk(ctx, op, queries, buf[b], num_queries, n, dim, k, c == 0 ? run_idx[0] : ch_idx,
+                                      c == 0 ? run_dist[0] : ch_dist));
+        VA_CHECK_HIP(ctx, hipEventRecord(use_ev[b], ctx->stream));
+        if (c > 0) {
+            VA_CHECK_STATUS(va_topk_merge(ctx, run_idx[cur], run_dist[cur], ch_idx, ch_dist, num_queries, k, r0,
+                                          run_idx[cur ^ 1], run_dist[cur ^ 1]));
+            cur ^= 1;
+        }
+        if (c + 2 < nch) {
+            VA_CHECK_HIP(ctx, hipStreamWaitEvent(cs, use_ev[b], 0));
+            VA_CHECK_STATUS(upload(c + 2));
+        }
+    }
+    VA_CHECK_HIP(ctx, hipMemcpyAsync(out_idx, run_idx[cur], size_t(qk) * 4, hipMemcpyDeviceToDevice, ctx->stream));
+    if (out_dist)
+        VA_CHECK_HIP(ctx, hipMemcpyAsync(out_dist, run_dist[cur], size_t(qk) * 4, hipMemcpyDeviceToDevice, ctx->stream));
+    // the buffers of this call are freed on return
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(cs));
+    return VA_OK;
 }
 
 }  // extern "C"

@@ -414,6 +414,9 @@ struct ScreenInput {
     uint32_t Q = 0, N = 0, D = 0;
     DistOp op = OP_L2SQ;
 };
+// Exact top-k of device queries against a device database (va_fused_topk's body).
+va_status flat_topk(va_context* ctx, DistOp op, const float* q, const float* x, uint32_t Q, uint32_t N, uint32_t D,
+                    uint32_t k, uint32_t* out_idx, float* out_dist);
 // Whether the screened path applies (metric, alignment, sizes, VA_OPT_SCREEN).
 bool screen_applies(const va_context* ctx, const ScreenInput& in, uint32_t k);
 va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer& exact, uint32_t k,

@@ -284,6 +284,34 @@ class FusedL2TopKKernel:
         c.synchronize()
         return Metal4FusedL2TopKResult(idx, dist, p.numQueries, p.k)
 
+    def encodeStreamed(self, queries, hostDataset, outputIndices, outputDistances, parameters: FusedL2TopKParameters,
+                       metric: Metric = Metric.euclideanSquared, chunkRows: int = 0):
+        """The same search over a dataset in host memory (a contiguous float32 CPU tensor, pinned for
+        overlapped uploads), streamed through the device in chunks of ``chunkRows`` rows (0 = ~512 MiB)
+        and merged into a running top-k: the reference's chunked fallback with GPU merge
+        (FusedL2TopKKernel.swift:765-931).  Synchronous."""
+        c = self.context
+        p = parameters
+        if hostDataset.is_cuda or not hostDataset.is_contiguous():
+            raise VectorError.invalidInput("hostDataset must be a contiguous host tensor")
+        c.check(
+            c.lib.va_fused_topk_streamed(c.handle, int(metric), dptr(queries), int(hostDataset.data_ptr()),
+                                         p.numQueries, p.numDataset, p.dimension, p.k, int(chunkRows),
+                                         dptr(outputIndices), dptr(outputDistances)),
+            "FusedL2TopKKernel.encodeStreamed",
+        )
+
+    def executeStreamed(self, queries, hostDataset, parameters: FusedL2TopKParameters,
+                        metric: Metric = Metric.euclideanSquared, chunkRows: int = 0) -> Metal4FusedL2TopKResult:
+        torch = _torch()
+        c = self.context
+        p = parameters
+        idx = c.empty((p.numQueries, p.k), torch.int32)
+        dist = c.empty((p.numQueries, p.k), torch.float32)
+        c.order_after_torch()
+        self.encodeStreamed(queries, hostDataset, idx, dist, p, metric, chunkRows)
+        return Metal4FusedL2TopKResult(idx, dist, p.numQueries, p.k)
+
     def findNearestNeighbors(self, queries, dataset, k: int, includeDistances: bool = True,
                              metric: Metric = Metric.euclideanSquared) -> list[list[tuple[int, float]]]:
         q = _as_matrix(queries, "arrays")
