@@ -231,6 +231,34 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
 va_status va_ivf_search(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
                         uint32_t nprobe, uint32_t k, uint32_t* out_idx, float* out_dist);
 
+/* ---- k-means (IVF centroid training) ------------------------------------------------ */
+typedef struct {
+    uint32_t iterations;  /* Lloyd iterations run */
+    int32_t converged;    /* 1 when the last iteration's largest centroid movement < threshold */
+    double inertia;       /* sum over points of the L2 distance to the assigned centroid */
+    float max_movement;   /* largest centroid movement (L2) of the last iteration */
+} va_kmeans_info;
+/* Lloyd k-means from initial centroids [num_clusters x dim].  Replaces KMeansPipeline.fit
+ * (Index/Kernels/Clustering/KMeansPipeline.swift:102-270): per iteration, assignment to the
+ * nearest centroid (L2^2, ties to the lower id; distance = L2), centroid = mean of its points
+ * (sum * (1/count)), empty clusters keep their centroid and are then re-seeded, in index
+ * order, with the points farthest from their centroids (KMeansUpdateKernel.handleEmptyClusters,
+ * KMeansUpdateKernel.swift:228-283); stops after max_iterations or when the largest movement
+ * is below convergence_threshold (KMeansConvergenceKernel.swift:76-127).  out_assignments and
+ * out_distances [num_vectors] are the last iteration's assignment; out_counts [num_clusters]
+ * the updated sizes (1 for a re-seeded cluster).  out_distances, out_counts and out_info may be
+ * NULL.  Deterministic: the same inputs give the same bits.  Synchronises the context. */
+va_status va_kmeans_fit(va_context* ctx, const float* vectors, uint32_t num_vectors, uint32_t dim,
+                        uint32_t num_clusters, const float* initial_centroids, uint32_t max_iterations,
+                        float convergence_threshold, float* out_centroids, uint32_t* out_assignments,
+                        float* out_distances, uint32_t* out_counts, va_kmeans_info* out_info);
+/* k-means++ seeding: k rows of vectors chosen by D^2 sampling, copied to out_centroids
+ * [k x dim], their row ids to out_indices [k] (may be NULL).  Replaces
+ * KMeansPlusPlusKernel.selectCentroids (KMeansPlusPlusKernel.swift:94-203); the uniform draws
+ * come from splitmix64(seed) instead of the system generator.  Synchronises the context. */
+va_status va_kmeans_plusplus(va_context* ctx, const float* vectors, uint32_t num_vectors, uint32_t dim, uint32_t k,
+                             uint64_t seed, float* out_centroids, uint32_t* out_indices);
+
 #ifdef __cplusplus
 }
 #endif

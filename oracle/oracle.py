@@ -218,3 +218,28 @@ def ivf_scan(q, x, offsets, ids, probes, k):
     lib().vo_ivf_scan(_p(q), _i(Q), _p(x), _i(D), _p(offsets), _p(ids), _i(offsets.shape[0] - 1), _p(probes),
                       _i(probes.shape[1]), _i(k), _p(idx), _p(dist))
     return idx, dist
+
+
+def kmeans_fit(x, init, max_iter, threshold):
+    """Lloyd k-means: (centroids, assignments, distances, counts, iterations, converged, inertia,
+    max_movement)."""
+    x, init = _f32(x), _f32(init)
+    N, D = x.shape
+    C_ = init.shape[0]
+    cen = np.empty((C_, D), np.float32)
+    assign = np.empty(N, np.uint32)
+    dist = np.empty(N, np.float32)
+    counts = np.empty(C_, np.uint32)
+    iu = np.empty(2, np.uint32)
+    fi = np.empty(2, np.float32)
+    lib().vo_kmeans_fit(_p(x), _i(N), _i(D), _i(C_), _p(init), _i(max_iter), C.c_float(threshold), _p(cen),
+                        _p(assign), _p(dist), _p(counts), _p(iu), _p(fi))
+    return cen, assign, dist, counts, int(iu[0]), bool(iu[1]), float(fi[0]), float(fi[1])
+
+
+def kmeans_plusplus(x, k, seed):
+    """Row ids chosen by k-means++ D^2 sampling with splitmix64(seed) draws."""
+    x = _f32(x)
+    idx = np.empty(k, np.uint32)
+    lib().vo_kmeans_plusplus(_p(x), _i(x.shape[0]), _i(x.shape[1]), _i(k), C.c_uint64(seed), _p(idx))
+    return idx

@@ -577,3 +577,169 @@ void vo_ivf_scan(const float* q, int64_t Q, const float* x, int64_t D, const uin
         free(h.a);
     }
 }
+
+/* ------------------------------------------------------------------------ */
+/* k-means                                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* kmeans_assign_points (ClusteringShaders.metal:16-120): float difference form, strict < */
+static void km_assign(const float* x, int64_t N, int64_t D, const float* c, int64_t C, uint32_t* assign,
+                      float* dist) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < N; ++i) {
+        float best = INFINITY;
+        uint32_t bi = 0;
+        for (int64_t j = 0; j < C; ++j) {
+            float s = 0.0f;
+            for (int64_t d = 0; d < D; ++d) {
+                float diff = x[i * D + d] - c[j * D + d];
+                s += diff * diff;
+            }
+            if (s < best) {
+                best = s;
+                bi = (uint32_t)j;
+            }
+        }
+        assign[i] = bi;
+        dist[i] = sqrtf(best);
+    }
+}
+
+void vo_kmeans_fit(const float* x, int64_t N, int64_t D, int64_t C, const float* init, int64_t max_iter,
+                   float threshold, float* centroids, uint32_t* assign, float* dist, uint32_t* counts,
+                   uint32_t* info_u32, float* info_f) {
+    float* cur = (float*)malloc(sizeof(float) * C * D);
+    float* nxt = (float*)malloc(sizeof(float) * C * D);
+    float* sums = (float*)malloc(sizeof(float) * C * D);
+    unsigned char* used = (unsigned char*)malloc(N);
+    memcpy(cur, init, sizeof(float) * C * D);
+    int64_t it = 0;
+    int converged = 0;
+    float max_move = 0.0f;
+    while (it < max_iter && !converged) {
+        km_assign(x, N, D, cur, C, assign, dist);
+        /* update: sums in point order, times 1/count; empty keeps the old centroid */
+        memset(sums, 0, sizeof(float) * C * D);
+        memset(counts, 0, sizeof(uint32_t) * C);
+        for (int64_t i = 0; i < N; ++i) {
+            uint32_t a = assign[i];
+            counts[a]++;
+            for (int64_t d = 0; d < D; ++d) sums[a * D + d] += x[i * D + d];
+        }
+        for (int64_t c = 0; c < C; ++c) {
+            if (counts[c] > 0) {
+                float inv = 1.0f / (float)counts[c];
+                for (int64_t d = 0; d < D; ++d) nxt[c * D + d] = sums[c * D + d] * inv;
+            } else {
+                for (int64_t d = 0; d < D; ++d) nxt[c * D + d] = cur[c * D + d];
+            }
+        }
+        /* handleEmptyClusters: empty clusters in index order take the unused point of largest
+         * distance (`>` from -1, so the first index on ties and never a NaN) */
+        memset(used, 0, N);
+        for (int64_t c = 0; c < C; ++c) {
+            if (counts[c] != 0) continue;
+            float md = -1.0f;
+            int64_t bv = -1;
+            for (int64_t i = 0; i < N; ++i)
+                if (!used[i] && dist[i] > md) {
+                    md = dist[i];
+                    bv = i;
+                }
+            if (bv >= 0) {
+                used[bv] = 1;
+                memcpy(nxt + c * D, x + bv * D, sizeof(float) * D);
+                counts[c] = 1;
+            }
+        }
+        /* checkConvergence: max over centroids of sqrt(sum (new - old)^2) */
+        max_move = 0.0f;
+        for (int64_t c = 0; c < C; ++c) {
+            float s = 0.0f;
+            for (int64_t d = 0; d < D; ++d) {
+                float diff = nxt[c * D + d] - cur[c * D + d];
+                s += diff * diff;
+            }
+            float m = sqrtf(s);
+            if (m > max_move) max_move = m;
+        }
+        converged = max_move < threshold;
+        float* t = cur;
+        cur = nxt;
+        nxt = t;
+        ++it;
+    }
+    if (it == 0) {
+        km_assign(x, N, D, cur, C, assign, dist);
+        memset(counts, 0, sizeof(uint32_t) * C);
+        for (int64_t i = 0; i < N; ++i) counts[assign[i]]++;
+    }
+    float inertia = 0.0f;
+    for (int64_t i = 0; i < N; ++i) inertia += dist[i];
+    memcpy(centroids, cur, sizeof(float) * C * D);
+    info_u32[0] = (uint32_t)it;
+    info_u32[1] = (uint32_t)converged;
+    info_f[0] = inertia;
+    info_f[1] = max_move;
+    free(cur);
+    free(nxt);
+    free(sums);
+    free(used);
+}
+
+static uint64_t vo_splitmix64(uint64_t* s) {
+    uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+void vo_kmeans_plusplus(const float* x, int64_t N, int64_t D, int64_t k, uint64_t seed, uint32_t* idx) {
+    float* mind = (float*)malloc(sizeof(float) * N);
+    unsigned char* sel = (unsigned char*)calloc((size_t)N, 1);
+    uint64_t s = seed;
+    double u0 = (double)(vo_splitmix64(&s) >> 11) * 0x1.0p-53;
+    int64_t first = (int64_t)(u0 * (double)N);
+    if (first >= N) first = N - 1;
+    idx[0] = (uint32_t)first;
+    sel[first] = 1;
+    for (int64_t i = 0; i < N; ++i) mind[i] = INFINITY;
+    for (int64_t j = 1; j < k; ++j) {
+        const float* c = x + (int64_t)idx[j - 1] * D;
+        /* compute_min_distances over all chosen centroids = running min against the newest */
+        for (int64_t i = 0; i < N; ++i) {
+            float t = 0.0f;
+            for (int64_t d = 0; d < D; ++d) {
+                float diff = x[i * D + d] - c[d];
+                t = fmaf(diff, diff, t);
+            }
+            if (t < mind[i]) mind[i] = t;
+        }
+        double u = (double)(vo_splitmix64(&s) >> 11) * 0x1.0p-53;
+        double total = 0.0;
+        for (int64_t i = 0; i < N; ++i)
+            if (!sel[i]) total += (double)mind[i];
+        int64_t next = 0;
+        if (total > 0.0) {
+            double thr = u * total, cum = 0.0;
+            for (int64_t i = 0; i < N; ++i) {
+                if (sel[i]) continue;
+                cum += (double)mind[i];
+                if (cum >= thr) {
+                    next = i;
+                    break;
+                }
+            }
+        } else {
+            for (int64_t i = 0; i < N; ++i)
+                if (!sel[i]) {
+                    next = i;
+                    break;
+                }
+        }
+        idx[j] = (uint32_t)next;
+        sel[next] = 1;
+    }
+    free(mind);
+    free(sel);
+}

@@ -113,6 +113,27 @@ void vo_ivf_probe(const float* q, int64_t Q, const float* c, int64_t C, int64_t 
 void vo_ivf_scan(const float* q, int64_t Q, const float* x, int64_t D, const uint32_t* offsets, const uint32_t* ids,
                  int64_t C, const uint32_t* probes, int64_t nprobe, int64_t k, uint32_t* idx, float* dist);
 
+/* ---- k-means (IVF centroid training) ------------------------------------------ */
+/* Lloyd k-means (KMeansPipeline.fit, Index/Kernels/Clustering/KMeansPipeline.swift:102-270):
+ * assignment = argmin_c sum_d (x_d - c_d)^2 in float, d in order, strict < (lowest centroid
+ * wins ties), distance = sqrt (kmeans_assign_points, ClusteringShaders.metal:16-120);
+ * centroid = (float sum of its points in point order) * (1/count), empty keeps the old one
+ * (kmeans_update_normalize, ClusteringShaders.metal:585-613); each empty cluster, in index
+ * order, takes the unused point of largest distance, first index on ties, count = 1
+ * (KMeansUpdateKernel.handleEmptyClusters, KMeansUpdateKernel.swift:228-283); converged when
+ * max_c sqrt(sum_d (new - old)^2) < threshold (KMeansConvergenceKernel.swift:76-127); inertia =
+ * float sum of the distances in point order (KMeansConvergenceKernel.swift:176-182).
+ * info_u32 = {iterations, converged}; info_f = {inertia, max_movement}. */
+void vo_kmeans_fit(const float* x, int64_t N, int64_t D, int64_t C, const float* init, int64_t max_iter,
+                   float threshold, float* centroids, uint32_t* assign, float* dist, uint32_t* counts,
+                   uint32_t* info_u32, float* info_f);
+/* k-means++ seeding (KMeansPlusPlusKernel.selectCentroids, KMeansPlusPlusKernel.swift:94-203):
+ * u_j = (splitmix64(seed) >> 11) * 2^-53 for j = 0..k-1; first = floor(u_0 * N); then
+ * min squared distance (fmaf over d in order, compute_min_distances, ClusteringShaders.metal:419-447),
+ * total = double sum over unselected points, pick the first unselected i whose cumulative
+ * double sum reaches u_j * total (the first unselected point when total is 0). */
+void vo_kmeans_plusplus(const float* x, int64_t N, int64_t D, int64_t k, uint64_t seed, uint32_t* idx);
+
 #ifdef __cplusplus
 }
 #endif

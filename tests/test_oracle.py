@@ -387,3 +387,134 @@ def test_config1_oracle_is_self_consistent(oracle):
     check_topk(L2SQ, q, x, 10, i2, d2, i1, d1)
     # the nearest neighbour distance of i.i.d. N(0,1) in 768-d is ~2*768 minus a few sigma
     assert np.all(d1[:, 0] > 1000) and np.all(d1[:, 0] < 1536)
+
+
+# ---------------------------------------------------------------------------
+# k-means (IVF centroid training)
+# ---------------------------------------------------------------------------
+
+def _blobs(C_, D, per, seed, spread=0.05, sep=10.0):
+    r = np.random.default_rng(seed)
+    centers = (r.standard_normal((C_, D)) * sep).astype(np.float32)
+    lab = np.repeat(np.arange(C_), per)
+    r.shuffle(lab)
+    x = (centers[lab] + r.standard_normal((lab.size, D)).astype(np.float32) * spread).astype(np.float32)
+    return x, lab, centers
+
+
+def test_kmeans_matches_sklearn_lloyd(oracle):
+    """A textbook Lloyd (scikit-learn, given init, tol=0) reaches the same centroids after the
+    same number of iterations; a dropped 1/count, a wrong argmin or an off-by-one iteration fails."""
+    from sklearn.cluster import KMeans
+
+    r = np.random.default_rng(5)
+    x = r.standard_normal((600, 8)).astype(np.float32)
+    init = x[r.choice(600, 12, replace=False)].copy()
+    for iters in (1, 2, 5):
+        cen, assign, dist, counts, it, conv, inertia, mm = oracle.kmeans_fit(x, init, iters, 0.0)
+        assert it == iters and not conv
+        km = KMeans(12, init=init.astype(np.float64), n_init=1, max_iter=iters, tol=0.0, algorithm="lloyd")
+        km.fit(x.astype(np.float64))
+        np.testing.assert_allclose(cen, km.cluster_centers_, rtol=1e-5, atol=1e-5)
+    # the last assignment is the nearest centroid by brute force (float64), distances are L2
+    d2 = ((x[:, None, :].astype(np.float64) - init_prev(oracle, x, init, 5)[None]) ** 2).sum(-1)
+    np.testing.assert_array_equal(assign, d2.argmin(1))
+    np.testing.assert_allclose(dist, np.sqrt(d2.min(1)), rtol=1e-5, atol=1e-6)
+    np.testing.assert_array_equal(counts, np.bincount(assign, minlength=12))
+    assert abs(inertia - float(np.sqrt(d2.min(1)).sum())) <= 1e-4 * inertia
+
+
+def init_prev(oracle, x, init, iters):
+    """Centroids the iters-th assignment saw (those after iters-1 iterations)."""
+    if iters == 1:
+        return init.astype(np.float64)
+    return oracle.kmeans_fit(x, init, iters - 1, 0.0)[0].astype(np.float64)
+
+
+def test_kmeans_blobs_converge_to_blob_means(oracle):
+    x, lab, centers = _blobs(6, 16, 200, 1)
+    init = centers + 0.5  # one seed near each blob
+    cen, assign, dist, counts, it, conv, inertia, mm = oracle.kmeans_fit(x, init, 50, 1e-4)
+    assert conv and it >= 2 and mm < 1e-4
+    np.testing.assert_array_equal(assign, lab)
+    means = np.stack([x[lab == c].astype(np.float64).mean(0) for c in range(6)])
+    np.testing.assert_allclose(cen, means, rtol=1e-5, atol=1e-5)
+    np.testing.assert_array_equal(counts, np.full(6, 200))
+    # a second fit from the converged centroids stops after one iteration
+    cen2, *_, it2, conv2, _, mm2 = oracle.kmeans_fit(x, cen, 50, 1e-4)
+    assert it2 == 1 and conv2 and mm2 < 1e-4
+
+
+def test_kmeans_empty_clusters_take_farthest_points(oracle):
+    """Clusters that receive no point take, in index order, the points farthest from their
+    assigned centroid (first index on ties), each point once, with count 1."""
+    x = np.array([[0, 0], [1, 0], [0, 1], [10, 0], [13, 0], [10, 4]], np.float32)
+    init = np.array([[100, 100], [0.3, 0.3], [-100, -100], [11, 1], [200, 0]], np.float32)
+    cen, assign, dist, counts, it, conv, inertia, mm = oracle.kmeans_fit(x, init, 1, 0.0)
+    np.testing.assert_array_equal(assign, [1, 1, 1, 3, 3, 3])
+    d = np.sqrt(((x - init[assign]) ** 2).sum(1))
+    np.testing.assert_allclose(dist, d, rtol=1e-6)
+    order = sorted(range(6), key=lambda i: (-d[i], i))
+    np.testing.assert_array_equal(cen[0], x[order[0]])
+    np.testing.assert_array_equal(cen[2], x[order[1]])
+    np.testing.assert_array_equal(cen[4], x[order[2]])
+    np.testing.assert_allclose(cen[1], x[:3].mean(0), rtol=1e-6)
+    np.testing.assert_allclose(cen[3], x[3:].mean(0), rtol=1e-6)
+    np.testing.assert_array_equal(counts, [1, 3, 1, 3, 1])
+    # ties: equal distances go to the lower point
+    x2 = np.array([[1, 0], [-1, 0], [0, 1], [0, -1]], np.float32)
+    init2 = np.array([[0, 0], [50, 50]], np.float32)
+    cen2, assign2, *_ = oracle.kmeans_fit(x2, init2, 1, 0.0)
+    np.testing.assert_array_equal(assign2, [0, 0, 0, 0])
+    np.testing.assert_array_equal(cen2[1], x2[0])
+
+
+def test_kmeans_zero_iterations_and_ties(oracle):
+    x = np.array([[0, 0], [2, 0], [1, 0]], np.float32)
+    init = np.array([[0, 0], [2, 0]], np.float32)
+    cen, assign, dist, counts, it, conv, inertia, mm = oracle.kmeans_fit(x, init, 0, 1e-4)
+    assert it == 0 and not conv
+    np.testing.assert_array_equal(cen, init)
+    np.testing.assert_array_equal(assign, [0, 1, 0])  # the midpoint ties: lower centroid
+    np.testing.assert_array_equal(counts, [2, 1])
+    np.testing.assert_allclose(dist, [0, 0, 1])
+
+
+def test_kmeans_plusplus_properties(oracle):
+    """D^2 seeding: distinct rows; with k distinct locations (each repeated) it picks one of each;
+    the first row is floor(u0 * N) of the splitmix64 stream."""
+    r = np.random.default_rng(2)
+    x = r.standard_normal((300, 5)).astype(np.float32)
+    for seed in (0, 1, 99):
+        idx = oracle.kmeans_plusplus(x, 40, seed)
+        assert len(set(idx.tolist())) == 40
+        s = (seed + 0x9E3779B97F4A7C15) & (2**64 - 1)
+        z = s
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & (2**64 - 1)
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & (2**64 - 1)
+        z ^= z >> 31
+        assert idx[0] == int((z >> 11) * 2.0**-53 * 300)
+    locs = r.standard_normal((7, 5)).astype(np.float32) * 5
+    dup = np.repeat(locs, 9, axis=0)
+    for seed in range(5):
+        idx = oracle.kmeans_plusplus(dup, 7, seed)
+        assert sorted(set((idx // 9).tolist())) == list(range(7))
+
+
+def test_kmeans_plusplus_samples_proportional_to_squared_distance(oracle):
+    """Three points on a line: with the first pick fixed by the draw, the second is taken with
+    probability d^2 / sum d^2 over many seeds (a d-weighted or uniform draw fails)."""
+    x = np.array([[0.0], [1.0], [3.0]], np.float32)
+    seen = {0: {}, 1: {}, 2: {}}
+    for seed in range(3000):
+        a, b = oracle.kmeans_plusplus(x, 2, seed).tolist()
+        seen[a][b] = seen[a].get(b, 0) + 1
+    for first, hist in seen.items():
+        n = sum(hist.values())
+        if n < 300:
+            continue
+        w = {j: float((x[j, 0] - x[first, 0]) ** 2) for j in range(3) if j != first}
+        tot = sum(w.values())
+        for j, wj in w.items():
+            p = wj / tot
+            assert abs(hist.get(j, 0) / n - p) < 4 * np.sqrt(p * (1 - p) / n) + 1e-9

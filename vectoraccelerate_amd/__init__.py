@@ -27,6 +27,7 @@ from .index import (
     SearchResults,
     VectorHandle,
 )
+from .clustering import KMeansConfiguration, KMeansPipeline, KMeansPlusPlusKernel, KMeansResult
 from .ivf import IVFGPUIndexStructure, IVFSearchConfiguration, IVFSearchPipeline, IVFSearchResult
 from .quantization import (
     BinaryQuantizationKernel,
@@ -47,6 +48,10 @@ __all__ = [
     "SearchResults",
     "VectorHandle",
     "IVFGPUIndexStructure",
+    "KMeansConfiguration",
+    "KMeansPipeline",
+    "KMeansPlusPlusKernel",
+    "KMeansResult",
     "IVFSearchConfiguration",
     "IVFSearchPipeline",
     "IVFSearchResult",

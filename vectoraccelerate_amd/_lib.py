@@ -78,6 +78,8 @@ SIGNATURES: dict[str, tuple] = {
     "va_ivf_probe": (_st, [_p, _p, _p, _u32, _u32, _p]),
     "va_ivf_scan": (_st, [_p, _p, _p, _u32, _p, _u32, _u32, _p, _p]),
     "va_ivf_search": (_st, [_p, _p, _p, _u32, _u32, _u32, _p, _p]),
+    "va_kmeans_fit": (_st, [_p, _p, _u32, _u32, _u32, _p, _u32, C.c_float, _p, _p, _p, _p, _p]),
+    "va_kmeans_plusplus": (_st, [_p, _p, _u32, _u32, _u32, _u64, _p, _p]),
 }
 
 
@@ -101,6 +103,17 @@ class ScanTimings(C.Structure):
 
     def as_dict(self) -> dict:
         return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+class KMeansInfo(C.Structure):
+    """va_kmeans_info (include/va_hip.h)."""
+
+    _fields_ = [
+        ("iterations", C.c_uint32),
+        ("converged", C.c_int32),
+        ("inertia", C.c_double),
+        ("max_movement", C.c_float),
+    ]
 
 
 _LIB: C.CDLL | None = None

@@ -328,6 +328,33 @@ __global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) 
     const uint32_t li = uint32_t(wq * 32 + l32);  // query slot of this lane in the tile
     if (li >= qc) return;
     const uint32_t orow = qs + li;                                   // dense output row
+    if (OUT == OUT_ARGMIN) {
+        // the lane's 64 rows in increasing id order, strict < : ties keep the lower row id; the two
+        // lane halves hold the same query and the other rows of each 8-row group
+        uint32_t bk = 0xFFFFFFFFu, bi = 0xFFFFFFFFu;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int mloc = b * 32 + 8 * j + 4 * hh;
+                const f32x4v xx = *reinterpret_cast<const f32x4v*>(nrm + wave * 128 + mloc);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t r = uint32_t(wn * 128 + mloc + e);
+                    const uint32_t key = key_of_float(apply_op(a.op, acc[b][4 * j + e], qq, xx[e]));
+                    if (r < rc && key < bk) {
+                        bk = key;
+                        bi = rs + r;
+                    }
+                }
+            }
+        unsigned long long best = (static_cast<unsigned long long>(bk) << 32) | bi;
+        const unsigned long long other =
+            (static_cast<unsigned long long>(uint32_t(__shfl_xor(int(bk), 32))) << 32) | uint32_t(__shfl_xor(int(bi), 32));
+        best = other < best ? other : best;
+        if (hh == 0 && best != ~0ull) atomicMin(a.best + orow, best);
+        return;
+    }
     const uint32_t qi = (OUT == OUT_FILTER && a.qrow) ? a.qrow[orow] : orow;  // query id (filter)
     if (OUT == OUT_FILTER) {
         const uint32_t thr = a.thr[qi];
@@ -462,6 +489,7 @@ va_status launch_dist(va_context* ctx, const DistArgs& a) {
     VA_DIST_CASE(1, 4, OUT_VALUES) VA_DIST_CASE(1, 4, OUT_KEYS) VA_DIST_CASE(1, 4, OUT_FILTER)
     VA_DIST_CASE(2, 2, OUT_VALUES) VA_DIST_CASE(2, 2, OUT_KEYS) VA_DIST_CASE(2, 2, OUT_FILTER)
     VA_DIST_CASE(4, 1, OUT_VALUES) VA_DIST_CASE(4, 1, OUT_KEYS) VA_DIST_CASE(4, 1, OUT_FILTER)
+    VA_DIST_CASE(1, 4, OUT_ARGMIN) VA_DIST_CASE(2, 2, OUT_ARGMIN) VA_DIST_CASE(4, 1, OUT_ARGMIN)
     // small list-major tiles (one or two waves) for sparse IVF work
     VA_DIST_CASE(1, 1, OUT_FILTER) VA_DIST_CASE(2, 1, OUT_FILTER)
 #undef VA_DIST_CASE

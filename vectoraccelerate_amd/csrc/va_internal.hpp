@@ -236,6 +236,7 @@ enum DistOut : int {
     OUT_VALUES = 0,  // out_f[q * ldo + n] = value
     OUT_KEYS = 1,    // out_k[q * ldo + n] = key_of_float(value)
     OUT_FILTER = 2,  // append (key, n) to the query's candidate list when key <= thr[q]
+    OUT_ARGMIN = 3,  // best[q] = min over rows of (key << 32 | row id) (64-bit atomic min)
 };
 
 struct DistArgs {
@@ -258,6 +259,8 @@ struct DistArgs {
     uint32_t* cand_id = nullptr;
     uint32_t cap = 0;
     uint32_t id_base = 0;  // added to database row ids in filter mode
+    // argmin mode: packed (key, row) minimum per query, initialised to ~0 by the caller
+    unsigned long long* best = nullptr;
     // list-major (IVF) launches: one {qs, qc, rs, rc} descriptor per workgroup; query i of a
     // tile is row qrow[qs + i], database row j is at position rs + j*rstride, whose id is
     // ids[position].  Q / N are ignored then.
