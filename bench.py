@@ -48,7 +48,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=2)
-    p.add_argument("--workload", default="all", choices=["all", "c2", "c3", "c4", "c5"],
+    p.add_argument("--workload", default="all", choices=["all", "c2", "c3", "c4", "c5", "kmeans"],
                    help="all = configs[1] headline + configs[2..4] extras")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines (profiling runs)")
     p.add_argument("--no-extra", action="store_true", help="headline only (no L2 top-10 extra)")
@@ -439,6 +439,65 @@ def run_c5(ctx, a, cpu: bool):
     return res
 
 
+def run_kmeans(ctx, a, cpu: bool):
+    """IVF training at configs[4]'s shape: 4096 centroids, d=768, on a 262,144-point sample of
+    the configs[4] construction; 10 Lloyd iterations (threshold 0, so all ten run)."""
+    import numpy as np
+    import torch
+
+    from vectoraccelerate_amd import KMeansConfiguration, KMeansPipeline, KMeansPlusPlusKernel
+
+    C, D, N, iters = 4096, 768, 262_144, 10
+    g = torch.Generator(device="cuda").manual_seed(14)
+    cen = torch.randn(C, D, device="cuda", generator=g) * 4.0
+    p = 1.0 / torch.arange(1, C + 1, device="cuda", dtype=torch.float64) ** 1.1
+    lab = torch.multinomial((p / p.sum()).float(), N, replacement=True, generator=g)
+    x = (cen[lab] + torch.randn(N, D, device="cuda", generator=g)).contiguous()
+    del cen, lab
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    init, _ = KMeansPlusPlusKernel(ctx).selectCentroidsBuffer(x, C, 7)
+    pp_s = time.perf_counter() - t0
+    pipe = KMeansPipeline(ctx, KMeansConfiguration(C, D, maxIterations=iters, convergenceThreshold=0.0))
+    KMeansPipeline(ctx, KMeansConfiguration(C, D, maxIterations=1, convergenceThreshold=0.0)).fit(x, init)  # warm-up
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    r = pipe.fit(x, init)
+    fit_s = time.perf_counter() - t0
+    ms_it = fit_s * 1e3 / r.iterations
+    flops = 2.0 * N * C * D
+    tflops = flops / (ms_it * 1e-3) / 1e12
+    res = {
+        "workload": "IVF training (k-means) at configs[4]'s shape: 4096 centroids, d=768, 262,144 points, "
+                    "k-means++ seeding then 10 Lloyd iterations",
+        "ms_per_iteration": ms_it, "kmeanspp_s": pp_s, "iterations": r.iterations, "inertia": r.inertia,
+        "assignment_tflops_effective": tflops,
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK["fp32_mfma_tflops"], "unit": "TFLOP/s",
+                     "frac": tflops / PEAK["fp32_mfma_tflops"],
+                     "kernel": "whole Lloyd iteration (assignment GEMM + grouping + means + convergence)",
+                     "algorithmic": f"2NCD = {flops:.4g} FLOP per iteration"},
+    }
+    log(f"k-means C={C} D={D} N={N}: {ms_it:.2f} ms/iteration ({tflops:.1f} TFLOP/s effective), "
+        f"k-means++ {pp_s:.2f} s, inertia {r.inertia:.4g}")
+    if cpu:
+        from oracle import oracle
+
+        ns = 4096
+        xh = x[:ns].cpu().numpy()
+        ih = init.cpu().numpy()
+        t0 = time.perf_counter()
+        oracle.kmeans_fit(xh, ih, 1, 0.0)
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": ns * C * D * 2 / dt / 1e12, "unit": "TFLOP/s (assignment)",
+                               "cores": oracle.num_threads(), "kind": "port",
+                               "sample": f"one Lloyd iteration of {ns} points against the same 4096 centroids",
+                               "seconds": dt}
+        log(f"k-means CPU baseline: {ns} points, one iteration in {dt:.2f} s")
+    del x, init, r
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     a = parse()
     if a.gpus != 1:
@@ -470,6 +529,8 @@ def main() -> int:
         extra["configs3_binary"] = run_c4(ctx, a, cpu)
     if a.workload in ("all", "c5"):
         extra["configs4_ivf"] = run_c5(ctx, a, cpu)
+    if a.workload in ("all", "kmeans"):
+        extra["ivf_training_kmeans"] = run_kmeans(ctx, a, cpu)
     ctx.close()
     if c2 is None:
         print(json.dumps({"metric": METRIC, "value": None, "extra": extra}), flush=True)

@@ -611,6 +611,8 @@ void vo_kmeans_fit(const float* x, int64_t N, int64_t D, int64_t C, const float*
     float* cur = (float*)malloc(sizeof(float) * C * D);
     float* nxt = (float*)malloc(sizeof(float) * C * D);
     float* sums = (float*)malloc(sizeof(float) * C * D);
+    float* chunk = (float*)malloc(sizeof(float) * C * D);
+    uint32_t* seen = (uint32_t*)malloc(sizeof(uint32_t) * C);
     unsigned char* used = (unsigned char*)malloc(N);
     memcpy(cur, init, sizeof(float) * C * D);
     int64_t it = 0;
@@ -618,13 +620,22 @@ void vo_kmeans_fit(const float* x, int64_t N, int64_t D, int64_t C, const float*
     float max_move = 0.0f;
     while (it < max_iter && !converged) {
         km_assign(x, N, D, cur, C, assign, dist);
-        /* update: sums in point order, times 1/count; empty keeps the old centroid */
+        /* update: a cluster's points in point order form chunks of 256; each chunk is summed in
+         * order, the chunk sums are added in order, times 1/count; empty keeps the old centroid */
         memset(sums, 0, sizeof(float) * C * D);
         memset(counts, 0, sizeof(uint32_t) * C);
+        for (int64_t i = 0; i < N; ++i) counts[assign[i]]++;
+        memset(seen, 0, sizeof(uint32_t) * C);
+        memset(chunk, 0, sizeof(float) * C * D);
         for (int64_t i = 0; i < N; ++i) {
             uint32_t a = assign[i];
-            counts[a]++;
-            for (int64_t d = 0; d < D; ++d) sums[a * D + d] += x[i * D + d];
+            for (int64_t d = 0; d < D; ++d) chunk[a * D + d] += x[i * D + d];
+            if (++seen[a] % 256 == 0 || seen[a] == counts[a]) {
+                for (int64_t d = 0; d < D; ++d) {
+                    sums[a * D + d] += chunk[a * D + d];
+                    chunk[a * D + d] = 0.0f;
+                }
+            }
         }
         for (int64_t c = 0; c < C; ++c) {
             if (counts[c] > 0) {
@@ -684,6 +695,8 @@ void vo_kmeans_fit(const float* x, int64_t N, int64_t D, int64_t C, const float*
     free(cur);
     free(nxt);
     free(sums);
+    free(chunk);
+    free(seen);
     free(used);
 }
 
@@ -706,14 +719,23 @@ void vo_kmeans_plusplus(const float* x, int64_t N, int64_t D, int64_t k, uint64_
     for (int64_t i = 0; i < N; ++i) mind[i] = INFINITY;
     for (int64_t j = 1; j < k; ++j) {
         const float* c = x + (int64_t)idx[j - 1] * D;
-        /* compute_min_distances over all chosen centroids = running min against the newest */
+        /* compute_min_distances over all chosen centroids = running min against the newest;
+         * the sum of squares in a fixed order: 64 partials (d = l, l + 64, ... with fmaf), then
+         * combined pairwise at strides 32, 16, ..., 1 */
+#pragma omp parallel for schedule(static)
         for (int64_t i = 0; i < N; ++i) {
-            float t = 0.0f;
-            for (int64_t d = 0; d < D; ++d) {
-                float diff = x[i * D + d] - c[d];
-                t = fmaf(diff, diff, t);
+            float part[64];
+            for (int l = 0; l < 64; ++l) {
+                float t = 0.0f;
+                for (int64_t d = l; d < D; d += 64) {
+                    float diff = x[i * D + d] - c[d];
+                    t = fmaf(diff, diff, t);
+                }
+                part[l] = t;
             }
-            if (t < mind[i]) mind[i] = t;
+            for (int m = 32; m > 0; m >>= 1)
+                for (int l = 0; l < m; ++l) part[l] = part[l] + part[l + m];
+            if (part[0] < mind[i]) mind[i] = part[0];
         }
         double u = (double)(vo_splitmix64(&s) >> 11) * 0x1.0p-53;
         double total = 0.0;

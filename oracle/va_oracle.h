@@ -117,7 +117,8 @@ void vo_ivf_scan(const float* q, int64_t Q, const float* x, int64_t D, const uin
 /* Lloyd k-means (KMeansPipeline.fit, Index/Kernels/Clustering/KMeansPipeline.swift:102-270):
  * assignment = argmin_c sum_d (x_d - c_d)^2 in float, d in order, strict < (lowest centroid
  * wins ties), distance = sqrt (kmeans_assign_points, ClusteringShaders.metal:16-120);
- * centroid = (float sum of its points in point order) * (1/count), empty keeps the old one
+ * centroid = (float sum) * (1/count), the sum taken over chunks of 256 of its points in point
+ * order, chunk sums added in order (the reference's float atomics fix no order), empty keeps the old one
  * (kmeans_update_normalize, ClusteringShaders.metal:585-613); each empty cluster, in index
  * order, takes the unused point of largest distance, first index on ties, count = 1
  * (KMeansUpdateKernel.handleEmptyClusters, KMeansUpdateKernel.swift:228-283); converged when
@@ -129,7 +130,8 @@ void vo_kmeans_fit(const float* x, int64_t N, int64_t D, int64_t C, const float*
                    uint32_t* info_u32, float* info_f);
 /* k-means++ seeding (KMeansPlusPlusKernel.selectCentroids, KMeansPlusPlusKernel.swift:94-203):
  * u_j = (splitmix64(seed) >> 11) * 2^-53 for j = 0..k-1; first = floor(u_0 * N); then
- * min squared distance (fmaf over d in order, compute_min_distances, ClusteringShaders.metal:419-447),
+ * min squared distance (compute_min_distances, ClusteringShaders.metal:419-447; summed as 64
+ * strided fmaf partials combined pairwise, the device's order),
  * total = double sum over unselected points, pick the first unselected i whose cumulative
  * double sum reaches u_j * total (the first unselected point when total is 0). */
 void vo_kmeans_plusplus(const float* x, int64_t N, int64_t D, int64_t k, uint64_t seed, uint32_t* idx);

@@ -3,9 +3,10 @@
 The oracle restates KMeansPipeline.fit (KMeansPipeline.swift:102-270) with the reference's
 float difference-form assignment; the device assigns with the fp32 MFMA distance kernel
 (|x|^2 + |c|^2 - 2 x.c).  On data whose nearest centroid is unambiguous both give the same
-assignments, and then the same centroid bits: both sum a cluster's points in point order in
-fp32 and multiply by 1/count.  The device recomputes each point's distance to its centroid in
-difference form (other summation order than the oracle's), so distances agree within
+assignments, and then the same centroid bits: both sum a cluster's points in chunks of 256 in
+point order, then the chunk sums in order, in fp32, times 1/count.  The device recomputes each
+point's distance to its centroid in difference form (other summation order than the oracle's),
+so distances agree within
 2 (D + 4) 2^-24 relative: each side's sum of D squares is within (D + 1) 2^-24 of the exact one.
 """
 from __future__ import annotations

@@ -16,8 +16,8 @@
 //      (ties to the lower point, each point once) with count 1;
 //   4. converged when the largest centroid movement (L2) is below the threshold.
 // The reference sums with float atomics, in an order that varies from run to run; here the
-// points are grouped by cluster with a stable radix sort and summed in point order, so every
-// run gives the same bits.
+// points are grouped by cluster with a stable radix sort and summed in a fixed order (chunks of
+// 256 points in point order, then the chunk sums in order), so every run gives the same bits.
 //
 // va_kmeans_plusplus replaces KMeansPlusPlusKernel.selectCentroids (KMeansPlusPlusKernel.swift:94-203)
 // with compute_min_distances (ClusteringShaders.metal:419-447): D^2 sampling with the running
@@ -37,6 +37,8 @@
 
 namespace va {
 namespace {
+
+constexpr uint32_t kChunk = 256;  // points per partial centroid sum
 
 __global__ __launch_bounds__(256) void fill_u64(unsigned long long* p, uint64_t n, unsigned long long v) {
     for (uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += uint64_t(gridDim.x) * 256) p[i] = v;
@@ -84,7 +86,8 @@ __global__ __launch_bounds__(256) void refine_dist(const float* __restrict__ x, 
 // first position of each cluster in the sorted assignments and its size
 __global__ __launch_bounds__(256) void cluster_ranges(const uint32_t* __restrict__ sorted_assign, uint32_t N,
                                                       uint32_t C, uint32_t* __restrict__ first,
-                                                      uint32_t* __restrict__ counts, uint32_t* __restrict__ n_empty) {
+                                                      uint32_t* __restrict__ counts, uint32_t* __restrict__ chunks,
+                                                      uint32_t* __restrict__ n_empty) {
     const uint32_t c = blockIdx.x * 256 + threadIdx.x;
     if (c >= C) return;
     auto lower = [&](uint32_t v) {
@@ -99,27 +102,63 @@ __global__ __launch_bounds__(256) void cluster_ranges(const uint32_t* __restrict
     const uint32_t a = lower(c), b = lower(c + 1);
     first[c] = a;
     counts[c] = b - a;
+    chunks[c] = (b - a + kChunk - 1) / kChunk;
     if (b == a) atomicAdd(n_empty, 1u);
 }
 
-// One workgroup per cluster: the fp32 sum of its points in point order, times 1/count
-// (kmeans_update_normalize); an empty cluster keeps its previous centroid.
-__global__ __launch_bounds__(256) void cluster_means(const float* __restrict__ x, uint32_t D,
-                                                     const uint32_t* __restrict__ members,
-                                                     const uint32_t* __restrict__ first,
-                                                     const uint32_t* __restrict__ counts,
+// Centroid sums in a fixed order: a cluster's points (in point order) form chunks of kChunk;
+// each chunk is summed in order in fp32 by one workgroup, then a cluster's chunk sums are added
+// in chunk order and multiplied by 1/count (kmeans_update_normalize).  Chunking spreads a large
+// cluster over many workgroups; the order never depends on scheduling.
+// workgroup b -> (cluster, chunk): chunk_end is the inclusive scan of chunks per cluster
+__global__ __launch_bounds__(256) void chunk_sums(const float* __restrict__ x, uint32_t D, uint32_t C,
+                                                  const uint32_t* __restrict__ members,
+                                                  const uint32_t* __restrict__ first,
+                                                  const uint32_t* __restrict__ counts,
+                                                  const uint32_t* __restrict__ chunk_end,
+                                                  float* __restrict__ partial) {
+    __shared__ uint32_t rows[kChunk];
+    const uint32_t b = blockIdx.x;
+    if (b >= chunk_end[C - 1]) return;
+    uint32_t lo = 0, hi = C - 1;  // first cluster whose chunk_end exceeds b
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (chunk_end[mid] > b) hi = mid;
+        else lo = mid + 1;
+    }
+    const uint32_t c = lo, n = counts[c];
+    const uint32_t nch = (n + kChunk - 1) / kChunk;
+    const uint32_t t = b - (chunk_end[c] - nch);
+    const uint32_t p0 = first[c] + t * kChunk;
+    const uint32_t m = min(kChunk, n - t * kChunk);
+    if (threadIdx.x < m) rows[threadIdx.x] = members[p0 + threadIdx.x];
+    __syncthreads();
+    for (uint32_t d = threadIdx.x; d < D; d += 256) {
+        float s = 0.0f;
+#pragma unroll 8
+        for (uint32_t i = 0; i < m; ++i) s += x[int64_t(rows[i]) * D + d];
+        partial[int64_t(b) * D + d] = s;
+    }
+}
+
+// one workgroup per cluster: its chunk sums in chunk order, times 1/count; an empty cluster keeps
+// its previous centroid
+__global__ __launch_bounds__(256) void cluster_means(uint32_t D, const uint32_t* __restrict__ counts,
+                                                     const uint32_t* __restrict__ chunk_end,
+                                                     const float* __restrict__ partial,
                                                      const float* __restrict__ old_c, float* __restrict__ new_c) {
     const uint32_t c = blockIdx.x;
-    const uint32_t n = counts[c], f = first[c];
+    const uint32_t n = counts[c];
     float* out = new_c + int64_t(c) * D;
     if (n == 0) {
         for (uint32_t d = threadIdx.x; d < D; d += 256) out[d] = old_c[int64_t(c) * D + d];
         return;
     }
+    const uint32_t nch = (n + kChunk - 1) / kChunk, b0 = chunk_end[c] - nch;
     const float inv = 1.0f / float(n);
     for (uint32_t d = threadIdx.x; d < D; d += 256) {
         float s = 0.0f;
-        for (uint32_t i = 0; i < n; ++i) s += x[int64_t(members[f + i]) * D + d];
+        for (uint32_t t = 0; t < nch; ++t) s += partial[int64_t(b0 + t) * D + d];
         out[d] = s * inv;
     }
 }
@@ -207,22 +246,29 @@ __global__ void sum_final(const double* __restrict__ part, uint32_t n, double* _
 
 // ---- k-means++ -------------------------------------------------------------------------
 
-// running minimum of |x - c|^2 against the newest centroid (difference form, d in order, fused
-// multiply-add), and the sampling weight (0 once the point is a centroid)
+// running minimum of |x - c|^2 against the newest centroid, and the sampling weight (0 once the
+// point is a centroid).  One wave per point: lane l sums (x_d - c_d)^2 over d = l, l + 64, ...
+// with fused multiply-adds, then the 64 partials combine by a butterfly (xor 32, 16, ..., 1).
 __global__ __launch_bounds__(256) void pp_update(const float* __restrict__ x, uint32_t N, uint32_t D,
                                                  const float* __restrict__ c, const uint8_t* __restrict__ sel,
                                                  float* __restrict__ mind, double* __restrict__ w, int first) {
-    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t i = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (i >= N) return;
     const float* xi = x + int64_t(i) * D;
     float s = 0.0f;
-    for (uint32_t d = 0; d < D; ++d) {
+#pragma unroll 4
+    for (uint32_t d = lane; d < D; d += 64) {
         const float diff = xi[d] - c[d];
         s = __builtin_fmaf(diff, diff, s);
     }
-    const float m = first ? s : fminf(mind[i], s);
-    mind[i] = m;
-    w[i] = sel[i] ? 0.0 : double(m);
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) s += __shfl_xor(s, m);
+    if (lane == 0) {
+        const float m = first ? s : fminf(mind[i], s);
+        mind[i] = m;
+        w[i] = sel[i] ? 0.0 : double(m);
+    }
 }
 
 // pick step j: the first unselected point whose cumulative weight reaches u * total (the first
@@ -356,7 +402,7 @@ va_status va_kmeans_plusplus(va_context* ctx, const float* vectors, uint32_t num
     va::pp_pick<<<dim3(1), dim3(256), 0, ctx->stream>>>(vectors, N, D, cum, u, 0, sel, idx, out_centroids);
     VA_CHECK_LAUNCH(ctx);
     for (uint32_t j = 1; j < k; ++j) {
-        va::pp_update<<<dim3(nb), dim3(256), 0, ctx->stream>>>(vectors, N, D, out_centroids + int64_t(j - 1) * D, sel,
+        va::pp_update<<<dim3((N + 3) / 4), dim3(256), 0, ctx->stream>>>(vectors, N, D, out_centroids + int64_t(j - 1) * D, sel,
                                                                mind, w, j == 1);
         VA_CHECK_LAUNCH(ctx);
         VA_CHECK_HIP(ctx, rocprim::inclusive_scan(scan_tmp, scan_bytes, w, cum, N, rocprim::plus<double>(), ctx->stream));
@@ -387,7 +433,8 @@ va_status va_kmeans_fit(va_context* ctx, const float* vectors, uint32_t num_vect
 
     va::Owned own;
     unsigned long long* best;
-    uint32_t *assign, *sort_vals, *sorted_keys, *members, *first, *counts, *flags, *keys, *empty_ids;
+    uint32_t *assign, *sort_vals, *sorted_keys, *members, *first, *counts, *flags, *keys, *empty_ids, *chunks,
+        *chunk_end;
     float *dist, *cur, *next;
     double* partials;
     const uint32_t nparts = std::min<uint32_t>(1024, (N + 255) / 256);
@@ -401,6 +448,12 @@ va_status va_kmeans_fit(va_context* ctx, const float* vectors, uint32_t num_vect
     VA_CHECK_STATUS(va::alloc(ctx, own, size_t(C) * 4, &first));
     VA_CHECK_STATUS(va::alloc(ctx, own, size_t(C) * 4, &counts));
     VA_CHECK_STATUS(va::alloc(ctx, own, size_t(C) * 4, &empty_ids));
+    VA_CHECK_STATUS(va::alloc(ctx, own, size_t(C) * 4, &chunks));
+    VA_CHECK_STATUS(va::alloc(ctx, own, size_t(C) * 4, &chunk_end));
+    // sum over clusters of ceil(count / kChunk) <= N / kChunk + C
+    const uint64_t max_chunks = uint64_t(N) / va::kChunk + C;
+    float* partial;
+    VA_CHECK_STATUS(va::alloc(ctx, own, size_t(max_chunks) * D * 4, &partial));
     VA_CHECK_STATUS(va::alloc(ctx, own, 64, &flags));  // [0] empty clusters, [1] largest movement (bits)
     VA_CHECK_STATUS(va::alloc(ctx, own, size_t(C) * D * 4, &cur));
     VA_CHECK_STATUS(va::alloc(ctx, own, size_t(C) * D * 4, &next));
@@ -410,7 +463,10 @@ va_status va_kmeans_fit(va_context* ctx, const float* vectors, uint32_t num_vect
                                                 bits, ctx->stream));
     VA_CHECK_HIP(ctx, rocprim::radix_sort_pairs(nullptr, sort_bytes32, keys, sorted_keys, sort_vals, members, N, 0,
                                                 32, ctx->stream));
-    sort_bytes = std::max(sort_bytes, sort_bytes32);
+    size_t scan_bytes = 0;
+    VA_CHECK_HIP(ctx, rocprim::inclusive_scan(nullptr, scan_bytes, chunks, chunk_end, C, rocprim::plus<uint32_t>(),
+                                              ctx->stream));
+    sort_bytes = std::max(std::max(sort_bytes, sort_bytes32), scan_bytes);
     void* sort_tmp;
     VA_CHECK_STATUS(va::alloc(ctx, own, sort_bytes, &sort_tmp));
     VA_CHECK_HIP(ctx, hipMemcpyAsync(cur, initial_centroids, size_t(C) * D * 4, hipMemcpyDeviceToDevice, ctx->stream));
@@ -424,14 +480,19 @@ va_status va_kmeans_fit(va_context* ctx, const float* vectors, uint32_t num_vect
         VA_CHECK_HIP(ctx, rocprim::radix_sort_pairs(sort_tmp, sort_bytes, assign, sorted_keys, sort_vals, members, N,
                                                     0, bits, ctx->stream));
         VA_CHECK_STATUS(va::fill_u32(ctx, flags, 2, 0));
-        va::cluster_ranges<<<dim3(cb), dim3(256), 0, ctx->stream>>>(sorted_keys, N, C, first, counts, flags);
+        va::cluster_ranges<<<dim3(cb), dim3(256), 0, ctx->stream>>>(sorted_keys, N, C, first, counts, chunks, flags);
         VA_CHECK_LAUNCH(ctx);
         return VA_OK;
     };
     while (it < max_iterations && !converged) {
         VA_CHECK_STATUS(va::assign_points(ctx, vectors, cur, N, C, D, best, assign, dist, sort_vals));
         VA_CHECK_STATUS(group());
-        va::cluster_means<<<dim3(C), dim3(256), 0, ctx->stream>>>(vectors, D, members, first, counts, cur, next);
+        VA_CHECK_HIP(ctx, rocprim::inclusive_scan(sort_tmp, scan_bytes, chunks, chunk_end, C,
+                                                  rocprim::plus<uint32_t>(), ctx->stream));
+        va::chunk_sums<<<dim3(uint32_t(max_chunks)), dim3(256), 0, ctx->stream>>>(vectors, D, C, members, first, counts,
+                                                                                  chunk_end, partial);
+        VA_CHECK_LAUNCH(ctx);
+        va::cluster_means<<<dim3(C), dim3(256), 0, ctx->stream>>>(D, counts, chunk_end, partial, cur, next);
         VA_CHECK_LAUNCH(ctx);
         VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->host_word, flags, 4, hipMemcpyDeviceToHost, ctx->stream));
         VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
