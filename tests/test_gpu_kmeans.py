@@ -148,3 +148,31 @@ def test_kmeans_plusplus_duplicates_and_full_pipeline(ctx, oracle):
     ocen, oassign, *_rest = oracle.kmeans_fit(x, init, 50, 1e-4)
     np.testing.assert_array_equal(r.assignments.cpu().numpy().view(np.uint32), oassign)
     np.testing.assert_array_equal(r.centroids.cpu().numpy(), ocen)
+
+
+def test_index_train_without_centroids(ctx, oracle):
+    """AcceleratedVectorIndex.train() with no centroids: device k-means (k-means++ seed, 25
+    iterations, threshold 0.001) over the live vectors, then the IVF lists from them
+    (AcceleratedVectorIndex.swift:406-446, IVFStructure.swift:202-259)."""
+    from vectoraccelerate_amd import AcceleratedVectorIndex, IndexConfiguration, VectorError
+
+    x, lab, centers = _blobs(16, 32, 60, seed=31)
+    idx = AcceleratedVectorIndex(IndexConfiguration.ivf(dimension=32, nlist=16, nprobe=4, capacity=2000), ctx)
+    with pytest.raises(VectorError):
+        idx.train()  # no vectors
+    hs = idx.insert(vectors=x)
+    idx.remove(hs[0])
+    idx.train(seed=77)
+    live = x[1:]
+    init = live[oracle.kmeans_plusplus(live, 16, 77)]
+    ocen, oassign, *_ = oracle.kmeans_fit(live, init, 25, 0.001)
+    np.testing.assert_array_equal(idx._centroids.cpu().numpy(), ocen)
+    # the lists: every stored row under its nearest trained centroid, in row order
+    off, ids = idx._ivf_structure().lists()
+    stored = idx._storage[:idx._slots].cpu().numpy()
+    lists = oracle.ivf_assign(stored, ocen)
+    ooff, oids = oracle.ivf_csr(lists, 16)
+    np.testing.assert_array_equal(off, ooff)
+    np.testing.assert_array_equal(ids, oids)
+    res = idx.search(queries=centers, k=5)
+    assert all(len(r.results) == 5 for r in res)

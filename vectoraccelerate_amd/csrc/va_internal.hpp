@@ -318,6 +318,15 @@ struct SelectArgs {
 };
 va_status launch_select(va_context* ctx, const SelectArgs& a);
 
+// assign[i] = the nearest centroid of row i by L2^2 (ties -> lower centroid) on the fp32 MFMA
+// distance kernel with the argmin epilogue; best is N words of scratch
+va_status nearest_centroids(va_context* ctx, const float* x, const float* cen, uint32_t N, uint32_t C, uint32_t D,
+                            unsigned long long* best, uint32_t* assign);
+// CSR lists from assignments: ids = row ids grouped by centroid in row order (stable sort),
+// offsets[C + 1].  Synchronises the context's stream.
+va_status csr_from_assignments(va_context* ctx, const uint32_t* assign, uint32_t N, uint32_t C, uint32_t* ids,
+                               uint32_t* offsets);
+
 // fill a device u32 array (graph-safe replacement for hipMemsetAsync)
 va_status fill_u32(va_context* ctx, uint32_t* p, uint64_t n, uint32_t v);
 

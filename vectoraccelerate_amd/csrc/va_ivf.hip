@@ -433,49 +433,26 @@ va_status va_ivf_build(va_context* ctx, const float* centroids, uint32_t num_cen
     if (hipMemcpyAsync(ivf->centroids, centroids, cbytes, hipMemcpyDeviceToDevice, ctx->stream) != hipSuccess)
         return cleanup(va::fail(ctx, VA_ERR_HIP, "va_ivf_build: centroid copy failed"));
 
-    // nearest-centroid assignment, in row batches (k = 1 exact scan; ties -> lower id)
+    // nearest-centroid assignment (fp32 MFMA argmin; ties -> lower id, IVFStructure.findNearestCentroid),
+    // then the CSR lists on the device: centroid order, insertion order inside each list
+    // (IVFStructure.swift:370-381) from a stable radix sort of the assignments
     uint32_t* assign = nullptr;
-    if (hipMalloc(&assign, uint64_t(num_vectors) * 4) != hipSuccess) {
+    unsigned long long* best = nullptr;
+    if (hipMalloc(&assign, uint64_t(num_vectors) * 4) != hipSuccess ||
+        hipMalloc(&best, uint64_t(num_vectors) * 8) != hipSuccess) {
         (void)hipGetLastError();
-        return cleanup(va::fail(ctx, VA_ERR_OOM, "va_ivf_build: assignment buffer"));
+        if (assign) (void)hipFree(assign);
+        return cleanup(va::fail(ctx, VA_ERR_OOM, "va_ivf_build: assignment buffers"));
     }
-    const uint32_t batch = 1u << 18;
-    for (uint32_t r0 = 0; r0 < num_vectors; r0 += batch) {
-        const uint32_t nr = std::min(batch, num_vectors - r0);
-        va::F32Keys kp;
-        kp.ctx = ctx;
-        kp.q = x + uint64_t(r0) * dim;
-        kp.x = ivf->centroids;
-        kp.Q = nr;
-        kp.N = num_centroids;
-        kp.D = dim;
-        va::ScanOutputs o;
-        o.idx = assign + r0;
-        va_status st = va::exact_topk_scan(ctx, kp, nr, num_centroids, 1, o);
-        if (st != VA_OK) {
-            (void)hipFree(assign);
-            return cleanup(st);
-        }
-    }
-    std::vector<uint32_t> h_assign(num_vectors);
-    if (hipMemcpyAsync(h_assign.data(), assign, uint64_t(num_vectors) * 4, hipMemcpyDeviceToHost, ctx->stream) !=
-            hipSuccess ||
-        hipStreamSynchronize(ctx->stream) != hipSuccess) {
-        (void)hipFree(assign);
-        return cleanup(va::fail(ctx, VA_ERR_HIP, "va_ivf_build: assignment read-back failed"));
-    }
+    va_status st = va::nearest_centroids(ctx, x, ivf->centroids, num_vectors, num_centroids, dim, best, assign);
+    if (st == VA_OK) st = va::csr_from_assignments(ctx, assign, num_vectors, num_centroids, ivf->ids, ivf->offsets);
+    (void)hipFree(best);
     (void)hipFree(assign);
-    // CSR in centroid order, insertion order inside each list (IVFStructure.swift:370-381)
+    if (st != VA_OK) return cleanup(st);
     ivf->h_offsets.assign(num_centroids + 1, 0);
-    for (uint32_t i = 0; i < num_vectors; ++i) ivf->h_offsets[h_assign[i] + 1]++;
-    for (uint32_t c = 0; c < num_centroids; ++c) ivf->h_offsets[c + 1] += ivf->h_offsets[c];
-    std::vector<uint32_t> fill(ivf->h_offsets.begin(), ivf->h_offsets.end() - 1), h_ids(num_vectors);
-    for (uint32_t i = 0; i < num_vectors; ++i) h_ids[fill[h_assign[i]]++] = i;
-    if (hipMemcpyAsync(ivf->ids, h_ids.data(), uint64_t(num_vectors) * 4, hipMemcpyHostToDevice, ctx->stream) !=
-            hipSuccess ||
-        hipMemcpyAsync(ivf->offsets, ivf->h_offsets.data(), uint64_t(num_centroids + 1) * 4, hipMemcpyHostToDevice,
-                       ctx->stream) != hipSuccess)
-        return cleanup(va::fail(ctx, VA_ERR_HIP, "va_ivf_build: CSR upload failed"));
+    if (hipMemcpy(ivf->h_offsets.data(), ivf->offsets, uint64_t(num_centroids + 1) * 4, hipMemcpyDeviceToHost) !=
+        hipSuccess)
+        return cleanup(va::fail(ctx, VA_ERR_HIP, "va_ivf_build: offsets read-back failed"));
     va::gather_rows<<<dim3(std::min<uint32_t>(num_vectors, 65536)), dim3(256), 0, ctx->stream>>>(
         x, ivf->ids, num_vectors, dim, ivf->list_vectors);
     if (hipGetLastError() != hipSuccess || hipStreamSynchronize(ctx->stream) != hipSuccess)

@@ -310,6 +310,11 @@ __global__ __launch_bounds__(256) void pp_pick(const float* __restrict__ x, uint
     for (uint32_t d = threadIdx.x; d < D; d += 256) centroids[int64_t(j) * D + d] = x[int64_t(p) * D + d];
 }
 
+__global__ __launch_bounds__(256) void fill_iota(uint32_t* p, uint32_t n) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = i;
+}
+
 __global__ __launch_bounds__(256) void fill_u8(uint8_t* p, uint32_t n) {
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
     if (i < n) p[i] = 0;
@@ -362,7 +367,74 @@ va_status assign_points(va_context* ctx, const float* x, const float* cen, uint3
     return VA_OK;
 }
 
+// packed minimum -> nearest centroid (0 when no distance is finite, as the reference's search
+// from bestIdx = 0 leaves it)
+__global__ __launch_bounds__(256) void unpack_nearest(const unsigned long long* __restrict__ best, uint32_t N,
+                                                      uint32_t* __restrict__ assign) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < N) assign[i] = best[i] == ~0ull ? 0u : uint32_t(best[i]);
+}
+
+// offsets[c] = first position of cluster c in the sorted assignments, offsets[C] = N
+__global__ __launch_bounds__(256) void csr_offsets(const uint32_t* __restrict__ sorted_assign, uint32_t N, uint32_t C,
+                                                   uint32_t* __restrict__ offsets) {
+    const uint32_t c = blockIdx.x * 256 + threadIdx.x;
+    if (c > C) return;
+    uint32_t lo = 0, hi = N;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (sorted_assign[mid] < c) lo = mid + 1;
+        else hi = mid;
+    }
+    offsets[c] = lo;
+}
+
 }  // namespace
+
+va_status nearest_centroids(va_context* ctx, const float* x, const float* cen, uint32_t N, uint32_t C, uint32_t D,
+                            unsigned long long* best, uint32_t* assign) {
+    const uint32_t nb = (N + 255) / 256;
+    fill_u64<<<dim3(std::min<uint32_t>(nb, 4096)), dim3(256), 0, ctx->stream>>>(best, N, ~0ull);
+    VA_CHECK_LAUNCH(ctx);
+    DistArgs a;
+    a.q = x;
+    a.ldq = D;
+    a.x = cen;
+    a.ldx = D;
+    a.Q = N;
+    a.N = C;
+    a.D = D;
+    a.op = OP_L2SQ;
+    a.out = OUT_ARGMIN;
+    a.best = best;
+    VA_CHECK_STATUS(launch_dist(ctx, a));
+    unpack_nearest<<<dim3(nb), dim3(256), 0, ctx->stream>>>(best, N, assign);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
+va_status csr_from_assignments(va_context* ctx, const uint32_t* assign, uint32_t N, uint32_t C, uint32_t* ids,
+                               uint32_t* offsets) {
+    Owned own;
+    uint32_t *iota, *sorted;
+    VA_CHECK_STATUS(alloc(ctx, own, size_t(N) * 4, &iota));
+    VA_CHECK_STATUS(alloc(ctx, own, size_t(N) * 4, &sorted));
+    int bits = 1;
+    while (bits < 32 && (1ull << bits) < C) ++bits;
+    size_t tmp_bytes = 0;
+    VA_CHECK_HIP(ctx, rocprim::radix_sort_pairs(nullptr, tmp_bytes, assign, sorted, iota, ids, N, 0, bits, ctx->stream));
+    void* tmp;
+    VA_CHECK_STATUS(alloc(ctx, own, tmp_bytes, &tmp));
+    fill_iota<<<dim3((N + 255) / 256), dim3(256), 0, ctx->stream>>>(iota, N);
+    VA_CHECK_LAUNCH(ctx);
+    VA_CHECK_HIP(ctx, rocprim::radix_sort_pairs(tmp, tmp_bytes, assign, sorted, iota, ids, N, 0, bits, ctx->stream));
+    csr_offsets<<<dim3((C + 1 + 255) / 256), dim3(256), 0, ctx->stream>>>(sorted, N, C, offsets);
+    VA_CHECK_LAUNCH(ctx);
+    // the temporaries are freed on return: finish the work that reads them first
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return VA_OK;
+}
+
 }  // namespace va
 
 extern "C" {

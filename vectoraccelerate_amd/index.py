@@ -225,14 +225,35 @@ class AcceleratedVectorIndex:
         return handle.stableID in self._handle_slot
 
     # -- IVF ---------------------------------------------------------------------------------
-    def train(self, centroids):
-        """Install IVF centroids ([nlist x D]); the lists are built from the stored vectors."""
+    def train(self, centroids=None, seed: int = 0x5EED):
+        """Train the IVF centroids; the lists are then built from the stored vectors.
+
+        Without ``centroids``: k-means on the device over the live (not deleted) vectors with
+        k-means++ seeding, 25 iterations at most, threshold 0.001, as IVFStructure.train
+        (Index/Internal/IVFStructure.swift:202-259) called by AcceleratedVectorIndex.train
+        (AcceleratedVectorIndex.swift:406-446).  With ``centroids`` ([nlist x D]): installs them.
+        """
         if not self.isIVF:
             raise VectorError.invalidInput("train() needs an IVF index")
-        c = np.asarray(centroids, np.float32)
-        if c.shape != (self.configuration.indexType[1], self.dimension):
-            raise VectorError.invalidInput(f"centroids must be {self.configuration.indexType[1]} x {self.dimension}")
-        self._centroids = self.context.buffer(c)
+        nlist = self.configuration.indexType[1]
+        if centroids is None:
+            from .clustering import KMeansConfiguration, KMeansPipeline
+
+            live = np.nonzero(~self._deleted[:self._slots])[0]
+            if live.size == 0:
+                raise VectorError.invalidInput("Cannot train IVF index with no vectors")
+            if live.size < nlist:
+                raise VectorError.invalidInput(
+                    f"Need at least {nlist} vectors for {nlist} clusters, got {live.size}")
+            torch = _torch()
+            rows = self._storage[torch.as_tensor(live, device=self._storage.device)].contiguous()
+            cfg = KMeansConfiguration(nlist, self.dimension, maxIterations=25, convergenceThreshold=0.001, seed=seed)
+            self._centroids = KMeansPipeline(self.context, cfg).fit(rows).centroids
+        else:
+            c = np.asarray(centroids, np.float32)
+            if c.shape != (nlist, self.dimension):
+                raise VectorError.invalidInput(f"centroids must be {nlist} x {self.dimension}")
+            self._centroids = self.context.buffer(c)
         self._ivf_dirty = True
 
     def _ivf_structure(self) -> IVFGPUIndexStructure:
