@@ -259,6 +259,37 @@ va_status va_kmeans_fit(va_context* ctx, const float* vectors, uint32_t num_vect
 va_status va_kmeans_plusplus(va_context* ctx, const float* vectors, uint32_t num_vectors, uint32_t dim, uint32_t k,
                              uint64_t seed, float* out_centroids, uint32_t* out_indices);
 
+/* ---- product quantization (ADC) --------------------------------------------------- */
+/* Layout: codebooks [M x K x (dim / M)] fp32, codes [N x M] bytes, tables [Q x M x K] fp32.
+ * dim % M == 0 and K <= 256 (Metal4PQConfig, Kernels/Metal4/ProductQuantizationKernel.swift:23-60).
+ * Sub-vector distances use the reference shader's order (calculate_l2_sq_dist,
+ * Metal/Shaders/ProductQuantization.metal:30-58), so codes and tables are reproducible. */
+/* Lloyd training of the M codebooks (ProductQuantizationKernel.train, :260-369): up to
+ * `iterations` rounds of assignment (nearest centroid, lowest k on ties) and update (mean of
+ * the members; an empty centroid keeps its value); stops after the round whose movement
+ * sqrt(sum of squared moves / (M K)) is below threshold.  Initial codebooks: initial_codebooks
+ * when not NULL, else sub-vectors of training rows drawn by splitmix64(seed)
+ * (initializeCodebooks, :548-572).  *out_iterations = rounds run (may be NULL).  Synchronises. */
+va_status va_pq_train(va_context* ctx, const float* data, uint32_t count, uint32_t dim, uint32_t M, uint32_t K,
+                      uint32_t iterations, float threshold, uint64_t seed, const float* initial_codebooks,
+                      float* out_codebooks, uint32_t* out_iterations);
+/* codes[n * M + m] = nearest centroid of sub-vector m (pq_assignment_or_encoding, :61-101;
+ * ProductQuantizationKernel.encode, :372-406). */
+va_status va_pq_encode(va_context* ctx, const float* x, uint32_t num_vectors, uint32_t dim, uint32_t M, uint32_t K,
+                       const float* codebooks, uint8_t* codes);
+/* tables[q][m][k] = |q_m - c_mk|^2 (pq_precompute_distance_table, :191-213). */
+va_status va_pq_distance_tables(va_context* ctx, const float* queries, uint32_t num_queries, uint32_t dim, uint32_t M,
+                                uint32_t K, const float* codebooks, float* tables);
+/* out[q * N + n] = sum_m tables[q][m][codes[n][m]], added in m order (pq_compute_distances_adc,
+ * :215-254; computeDistances, :409-478). */
+va_status va_pq_adc_distances(va_context* ctx, const float* tables, uint32_t num_queries, const uint8_t* codes,
+                              uint32_t num_vectors, uint32_t M, uint32_t K, float* out);
+/* Exact ADC top-k: tables, then the k smallest ADC sums per query by (sum, row id), reported as
+ * sqrt(sum) (findNearestNeighbors, :504-540, batched over queries).  out_dist may be NULL. */
+va_status va_pq_search(va_context* ctx, const float* queries, uint32_t num_queries, uint32_t dim, uint32_t M,
+                       uint32_t K, const float* codebooks, const uint8_t* codes, uint32_t num_vectors, uint32_t k,
+                       uint32_t* out_idx, float* out_dist);
+
 #ifdef __cplusplus
 }
 #endif

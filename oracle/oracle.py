@@ -243,3 +243,52 @@ def kmeans_plusplus(x, k, seed):
     idx = np.empty(k, np.uint32)
     lib().vo_kmeans_plusplus(_p(x), _i(x.shape[0]), _i(x.shape[1]), _i(k), C.c_uint64(seed), _p(idx))
     return idx
+
+
+def pq_sub_l2sq(v, c):
+    v, c = _f32(v), _f32(c)
+    lib().vo_pq_sub_l2sq.restype = C.c_float
+    return float(lib().vo_pq_sub_l2sq(_p(v), _p(c), _i(v.shape[0])))
+
+
+def pq_encode(x, cb, M, K):
+    x, cb = _f32(x), _f32(cb)
+    codes = np.empty((x.shape[0], M), np.uint8)
+    lib().vo_pq_encode(_p(x), _i(x.shape[0]), _i(x.shape[1]), _i(M), _i(K), _p(cb), _p(codes))
+    return codes
+
+
+def pq_tables(q, cb, M, K):
+    q, cb = _f32(q), _f32(cb)
+    t = np.empty((q.shape[0], M, K), np.float32)
+    lib().vo_pq_tables(_p(q), _i(q.shape[0]), _i(q.shape[1]), _i(M), _i(K), _p(cb), _p(t))
+    return t
+
+
+def pq_adc(tables, codes):
+    tables = _f32(tables)
+    codes = np.ascontiguousarray(codes, np.uint8)
+    Q, M, K = tables.shape
+    out = np.empty((Q, codes.shape[0]), np.float32)
+    lib().vo_pq_adc(_p(tables), _i(Q), _p(codes), _i(codes.shape[0]), _i(M), _i(K), _p(out))
+    return out
+
+
+def pq_search(q, cb, codes, M, K, k):
+    q, cb = _f32(q), _f32(cb)
+    codes = np.ascontiguousarray(codes, np.uint8)
+    idx = np.empty((q.shape[0], k), np.uint32)
+    dist = np.empty((q.shape[0], k), np.float32)
+    lib().vo_pq_search(_p(q), _i(q.shape[0]), _i(q.shape[1]), _i(M), _i(K), _p(cb), _p(codes), _i(codes.shape[0]),
+                       _i(k), _p(idx), _p(dist))
+    return idx, dist
+
+
+def pq_train(x, cb_init, M, K, iterations, threshold):
+    """(codebooks [M x K x D/M], rounds run)."""
+    x = _f32(x)
+    cb = np.array(cb_init, np.float32, copy=True, order="C")
+    lib().vo_pq_train.restype = C.c_int64
+    it = lib().vo_pq_train(_p(x), _i(x.shape[0]), _i(x.shape[1]), _i(M), _i(K), _i(iterations),
+                           C.c_float(threshold), _p(cb))
+    return cb, int(it)

@@ -765,3 +765,140 @@ void vo_kmeans_plusplus(const float* x, int64_t N, int64_t D, int64_t k, uint64_
     free(mind);
     free(sel);
 }
+
+/* ------------------------------------------------------------------------ */
+/* product quantization                                                      */
+/* ------------------------------------------------------------------------ */
+
+float vo_pq_sub_l2sq(const float* v, const float* c, int64_t n) {
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    int64_t n4 = n / 4;
+    for (int64_t d = 0; d < n4; ++d) {
+        float e0 = v[4 * d] - c[4 * d], e1 = v[4 * d + 1] - c[4 * d + 1];
+        float e2 = v[4 * d + 2] - c[4 * d + 2], e3 = v[4 * d + 3] - c[4 * d + 3];
+        a0 = fmaf(e0, e0, a0);
+        a1 = fmaf(e1, e1, a1);
+        a2 = fmaf(e2, e2, a2);
+        a3 = fmaf(e3, e3, a3);
+    }
+    float s = ((a0 + a1) + a2) + a3;
+    for (int64_t d = n4 * 4; d < n; ++d) {
+        float e = v[d] - c[d];
+        s += e * e;
+    }
+    return s;
+}
+
+void vo_pq_encode(const float* x, int64_t N, int64_t D, int64_t M, int64_t K, const float* cb, uint8_t* codes) {
+    int64_t ds = D / M;
+#pragma omp parallel for schedule(static)
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t m = 0; m < M; ++m) {
+            float best = INFINITY;
+            int64_t bk = 0;
+            for (int64_t k = 0; k < K; ++k) {
+                float d = vo_pq_sub_l2sq(x + n * D + m * ds, cb + (m * K + k) * ds, ds);
+                if (d < best) {
+                    best = d;
+                    bk = k;
+                }
+            }
+            codes[n * M + m] = (uint8_t)bk;
+        }
+}
+
+void vo_pq_tables(const float* q, int64_t Q, int64_t D, int64_t M, int64_t K, const float* cb, float* tables) {
+    int64_t ds = D / M;
+    for (int64_t i = 0; i < Q; ++i)
+        for (int64_t m = 0; m < M; ++m)
+            for (int64_t k = 0; k < K; ++k)
+                tables[(i * M + m) * K + k] = vo_pq_sub_l2sq(q + i * D + m * ds, cb + (m * K + k) * ds, ds);
+}
+
+void vo_pq_adc(const float* tables, int64_t Q, const uint8_t* codes, int64_t N, int64_t M, int64_t K, float* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < Q; ++i)
+        for (int64_t n = 0; n < N; ++n) {
+            float s = 0.0f;
+            for (int64_t m = 0; m < M; ++m) s += tables[(i * M + m) * K + codes[n * M + m]];
+            out[i * N + n] = s;
+        }
+}
+
+void vo_pq_search(const float* q, int64_t Q, int64_t D, int64_t M, int64_t K, const float* cb, const uint8_t* codes,
+                  int64_t N, int64_t k, uint32_t* idx, float* dist) {
+    float* tables = (float*)malloc(sizeof(float) * Q * M * K);
+    vo_pq_tables(q, Q, D, M, K, cb, tables);
+#pragma omp parallel for schedule(dynamic)
+    for (int64_t i = 0; i < Q; ++i) {
+        vo_heap h;
+        h.a = (vo_item*)malloc(sizeof(vo_item) * (size_t)(k > 0 ? k : 1));
+        h.n = 0;
+        h.cap = k;
+        const float* t = tables + i * M * K;
+        for (int64_t n = 0; n < N; ++n) {
+            float s = 0.0f;
+            for (int64_t m = 0; m < M; ++m) s += t[m * K + codes[n * M + m]];
+            heap_push(&h, (double)s, (uint32_t)n);
+        }
+        heap_emit(&h, k, idx + i * k, dist + i * k, INFINITY);
+        for (int64_t j = 0; j < k; ++j) dist[i * k + j] = sqrtf(dist[i * k + j]);
+        free(h.a);
+    }
+    free(tables);
+}
+
+int64_t vo_pq_train(const float* x, int64_t N, int64_t D, int64_t M, int64_t K, int64_t iterations, float threshold,
+                    float* cb) {
+    int64_t ds = D / M;
+    uint8_t* codes = (uint8_t*)malloc((size_t)(N * M));
+    float* sums = (float*)malloc(sizeof(float) * M * K * ds);
+    float* chunk = (float*)malloc(sizeof(float) * M * K * ds);
+    uint32_t* counts = (uint32_t*)malloc(sizeof(uint32_t) * M * K);
+    uint32_t* seen = (uint32_t*)malloc(sizeof(uint32_t) * M * K);
+    float* mv = (float*)malloc(sizeof(float) * M * K);
+    int64_t it = 0;
+    while (it < iterations) {
+        vo_pq_encode(x, N, D, M, K, cb, codes);
+        memset(sums, 0, sizeof(float) * M * K * ds);
+        memset(chunk, 0, sizeof(float) * M * K * ds);
+        memset(counts, 0, sizeof(uint32_t) * M * K);
+        memset(seen, 0, sizeof(uint32_t) * M * K);
+        for (int64_t n = 0; n < N; ++n)
+            for (int64_t m = 0; m < M; ++m) counts[m * K + codes[n * M + m]]++;
+        for (int64_t n = 0; n < N; ++n)
+            for (int64_t m = 0; m < M; ++m) {
+                int64_t c = m * K + codes[n * M + m];
+                for (int64_t d = 0; d < ds; ++d) chunk[c * ds + d] += x[n * D + m * ds + d];
+                if (++seen[c] % 256 == 0 || seen[c] == counts[c])
+                    for (int64_t d = 0; d < ds; ++d) {
+                        sums[c * ds + d] += chunk[c * ds + d];
+                        chunk[c * ds + d] = 0.0f;
+                    }
+            }
+        for (int64_t c = 0; c < M * K; ++c) {
+            float mvs = 0.0f;
+            if (counts[c] > 0) {
+                float inv = 1.0f / (float)counts[c];
+                for (int64_t d = 0; d < ds; ++d) {
+                    float nv = sums[c * ds + d] * inv, ov = cb[c * ds + d];
+                    cb[c * ds + d] = nv;
+                    float diff = ov - nv;
+                    mvs += diff * diff;
+                }
+            }
+            mv[c] = mvs;
+        }
+        float total = 0.0f;
+        for (int64_t c = 0; c < M * K; ++c) total += mv[c];
+        ++it;
+        if (sqrtf(total / (float)(M * K)) < threshold) break;
+    }
+    free(codes);
+    free(sums);
+    free(chunk);
+    free(counts);
+    free(seen);
+    free(mv);
+    return it;
+}

@@ -136,6 +136,28 @@ void vo_kmeans_fit(const float* x, int64_t N, int64_t D, int64_t C, const float*
  * double sum reaches u_j * total (the first unselected point when total is 0). */
 void vo_kmeans_plusplus(const float* x, int64_t N, int64_t D, int64_t k, uint64_t seed, uint32_t* idx);
 
+/* ---- product quantization --------------------------------------------------- */
+/* |v - c|^2 over n values in calculate_l2_sq_dist's order (ProductQuantization.metal:30-58):
+ * four lanes fmaf over the float4 blocks, ((x + y) + z) + w, then the tail one by one. */
+float vo_pq_sub_l2sq(const float* v, const float* c, int64_t n);
+/* codes[n*M + m] = argmin_k (strict <) (pq_assignment_or_encoding, ProductQuantization.metal:61-101). */
+void vo_pq_encode(const float* x, int64_t N, int64_t D, int64_t M, int64_t K, const float* cb, uint8_t* codes);
+/* tables[q][m][k] (pq_precompute_distance_table, ProductQuantization.metal:191-213). */
+void vo_pq_tables(const float* q, int64_t Q, int64_t D, int64_t M, int64_t K, const float* cb, float* tables);
+/* out[q][n] = sum_m tables[q][m][code] in m order (pq_compute_distances_adc, :215-254). */
+void vo_pq_adc(const float* tables, int64_t Q, const uint8_t* codes, int64_t N, int64_t M, int64_t K, float* out);
+/* top-k by (ADC sum, row id), distances sqrt(sum) (findNearestNeighbors,
+ * ProductQuantizationKernel.swift:504-540, with a deterministic tie rule). */
+void vo_pq_search(const float* q, int64_t Q, int64_t D, int64_t M, int64_t K, const float* cb, const uint8_t* codes,
+                  int64_t N, int64_t k, uint32_t* idx, float* dist);
+/* Lloyd training from cb (updated in place), ProductQuantizationKernel.train (:260-369):
+ * assignment, then per (m, k) the mean of its members (sums over chunks of 256 members in point
+ * order, chunk sums added in order; the reference's float atomics fix no order), empty keeps its
+ * value; movement_sq = sum_d (old - new)^2; stop after the round where
+ * sqrt(sum movement_sq / (M K)) < threshold.  Returns the rounds run. */
+int64_t vo_pq_train(const float* x, int64_t N, int64_t D, int64_t M, int64_t K, int64_t iterations, float threshold,
+                    float* cb);
+
 #ifdef __cplusplus
 }
 #endif

@@ -518,3 +518,69 @@ def test_kmeans_plusplus_samples_proportional_to_squared_distance(oracle):
         for j, wj in w.items():
             p = wj / tot
             assert abs(hist.get(j, 0) / n - p) < 4 * np.sqrt(p * (1 - p) / n) + 1e-9
+
+
+# ---------------------------------------------------------------------------
+# product quantization
+# ---------------------------------------------------------------------------
+
+def test_pq_sub_distance_order_and_value(oracle):
+    """The four-lane fmaf order agrees with float64 to fp32 rounding, and its lane structure is
+    visible: a sum that the lanes split exactly differs from a sequential one."""
+    r = np.random.default_rng(0)
+    for n in (1, 3, 4, 7, 12, 48, 97):
+        v = r.standard_normal(n).astype(np.float32)
+        c = r.standard_normal(n).astype(np.float32)
+        exact = float(((v.astype(np.float64) - c) ** 2).sum())
+        assert abs(oracle.pq_sub_l2sq(v, c) - exact) <= (n + 2) * 2.0**-24 * exact + 1e-30
+    # squares [1, e, e, e, 0, e, e, e], e = 2^-24: the lanes hold 1, 2e, 2e, 2e and add to 1 + 6e
+    # exactly; a sequential sum loses every e (1 + e rounds back to 1)
+    e = 2.0**-12
+    v = np.array([1.0, e, e, e, 0.0, e, e, e], np.float32)
+    assert oracle.pq_sub_l2sq(v, np.zeros(8, np.float32)) == np.float32(1.0 + 6 * 2.0**-24)
+
+
+def test_pq_encode_tables_adc_brute_force(oracle):
+    r = np.random.default_rng(1)
+    N, D, M, K = 300, 24, 6, 16
+    x = r.standard_normal((N, D)).astype(np.float32)
+    cb = r.standard_normal((M, K, D // M)).astype(np.float32)
+    codes = oracle.pq_encode(x, cb, M, K)
+    sub = x.reshape(N, M, 1, D // M).astype(np.float64) - cb[None].astype(np.float64)
+    d2 = (sub ** 2).sum(-1)  # [N, M, K]
+    np.testing.assert_array_equal(codes, d2.argmin(-1))
+    q = r.standard_normal((5, D)).astype(np.float32)
+    t = oracle.pq_tables(q, cb, M, K)
+    tq = ((q.reshape(5, M, 1, D // M).astype(np.float64) - cb[None]) ** 2).sum(-1)
+    np.testing.assert_allclose(t, tq, rtol=1e-5, atol=1e-6)
+    adc = oracle.pq_adc(t, codes)
+    ref = np.stack([t[i][np.arange(M)[None, :], codes].sum(1, dtype=np.float64) for i in range(5)])
+    np.testing.assert_allclose(adc, ref, rtol=1e-5)
+    # ADC of a row equals |q - decode(row)|^2 (the sub-spaces are orthogonal)
+    dec = cb[np.arange(M)[None, :], codes].reshape(N, D)
+    np.testing.assert_allclose(adc, ((q[:, None, :].astype(np.float64) - dec[None]) ** 2).sum(-1), rtol=1e-4)
+    idx, dist = oracle.pq_search(q, cb, codes, M, K, 7)
+    for i in range(5):
+        order = sorted(range(N), key=lambda n: (adc[i, n], n))[:7]
+        np.testing.assert_array_equal(idx[i], order)
+        np.testing.assert_allclose(dist[i], np.sqrt(adc[i, order]), rtol=1e-6)
+
+
+def test_pq_train_is_lloyd_per_subspace(oracle):
+    """Each subspace's training equals k-means on that sub-vector slice (the k-means oracle is
+    pinned against scikit-learn); the movement rule stops early on converged codebooks."""
+    r = np.random.default_rng(2)
+    N, D, M, K = 500, 12, 3, 8
+    x = r.standard_normal((N, D)).astype(np.float32)
+    init = x[r.choice(N, K, replace=False)].reshape(K, M, D // M).transpose(1, 0, 2).copy()
+    cb, it = oracle.pq_train(x, init, M, K, 4, 0.0)
+    assert it == 4
+    from sklearn.cluster import KMeans
+
+    for m in range(M):
+        xs = x[:, m * 4:(m + 1) * 4].astype(np.float64)
+        km = KMeans(K, init=init[m].astype(np.float64), n_init=1, max_iter=4, tol=0.0, algorithm="lloyd").fit(xs)
+        np.testing.assert_allclose(cb[m], km.cluster_centers_, rtol=1e-4, atol=1e-5)
+    cb2, it2 = oracle.pq_train(x, cb, M, K, 50, 1e-3)
+    cb3, it3 = oracle.pq_train(x, cb2, M, K, 50, 1e-3)
+    assert it3 == 1

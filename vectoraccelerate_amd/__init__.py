@@ -28,6 +28,7 @@ from .index import (
     VectorHandle,
 )
 from .clustering import KMeansConfiguration, KMeansPipeline, KMeansPlusPlusKernel, KMeansResult
+from .pq import Metal4EncodedVectors, Metal4PQConfig, Metal4PQModel, ProductQuantizationKernel
 from .ivf import IVFGPUIndexStructure, IVFSearchConfiguration, IVFSearchPipeline, IVFSearchResult
 from .quantization import (
     BinaryQuantizationKernel,
@@ -52,6 +53,10 @@ __all__ = [
     "KMeansPipeline",
     "KMeansPlusPlusKernel",
     "KMeansResult",
+    "Metal4EncodedVectors",
+    "Metal4PQConfig",
+    "Metal4PQModel",
+    "ProductQuantizationKernel",
     "IVFSearchConfiguration",
     "IVFSearchPipeline",
     "IVFSearchResult",

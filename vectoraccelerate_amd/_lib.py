@@ -80,6 +80,11 @@ SIGNATURES: dict[str, tuple] = {
     "va_ivf_search": (_st, [_p, _p, _p, _u32, _u32, _u32, _p, _p]),
     "va_kmeans_fit": (_st, [_p, _p, _u32, _u32, _u32, _p, _u32, C.c_float, _p, _p, _p, _p, _p]),
     "va_kmeans_plusplus": (_st, [_p, _p, _u32, _u32, _u32, _u64, _p, _p]),
+    "va_pq_train": (_st, [_p, _p, _u32, _u32, _u32, _u32, _u32, C.c_float, _u64, _p, _p, C.POINTER(_u32)]),
+    "va_pq_encode": (_st, [_p, _p, _u32, _u32, _u32, _u32, _p, _p]),
+    "va_pq_distance_tables": (_st, [_p, _p, _u32, _u32, _u32, _u32, _p, _p]),
+    "va_pq_adc_distances": (_st, [_p, _p, _u32, _p, _u32, _u32, _u32, _p]),
+    "va_pq_search": (_st, [_p, _p, _u32, _u32, _u32, _u32, _p, _p, _u32, _u32, _p, _p]),
 }
 
 

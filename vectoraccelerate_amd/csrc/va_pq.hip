@@ -1,0 +1,547 @@
+// va_pq.hip — product quantization: codebook training, encoding and the ADC (asymmetric distance)
+// top-k scan.
+//
+// Replaces Metal4ProductQuantizationKernel (Kernels/Metal4/ProductQuantizationKernel.swift:221-560)
+// and its shaders (Metal/Shaders/ProductQuantization.metal): pq_assignment_or_encoding (:61-101),
+// pq_train_update_accumulate / _finalize (:103-189), pq_precompute_distance_table (:191-213) and
+// pq_compute_distances_adc (:215-254).  A vector of dimension D is cut into M sub-vectors of
+// D_sub = D / M values; sub-vector m is coded by the nearest of the K <= 256 centroids of codebook
+// m (one byte).  The distance of a query to a coded row is sum_m table[m][code_m], table[m][k] =
+// |q_m - c_mk|^2.
+//
+// Sub-vector distances follow the shader's calculate_l2_sq_dist order exactly: four fp32 lanes
+// accumulate fma(diff, diff, acc) over the float4 blocks, the lanes add as ((x + y) + z) + w, the
+// D_sub % 4 tail adds diff * diff one by one; so codes and tables equal the oracle's bit for bit.
+// The ADC sum adds the M table entries in subspace order, as the shader does.
+//
+// Layout: codebooks [M x K x D_sub] fp32, codes [N x M] bytes (row-major, as the reference),
+// tables [Q x M x K] fp32.  The ADC scan keeps the tables of a group of queries in LDS (up to
+// 160 KB) and streams the code rows: every code row is read once per query group, and each
+// (query, row) pair costs M LDS lookups, which bound the scan.
+#include <cstring>
+
+#include <rocprim/device/device_radix_sort.hpp>
+#include <rocprim/device/device_scan.hpp>
+
+#include <algorithm>
+#include <vector>
+
+#include "va_internal.hpp"
+
+namespace va {
+namespace {
+
+constexpr uint32_t kPQChunk = 256;  // points per partial centroid sum (fixed summation order)
+
+__device__ __forceinline__ float sub_l2sq(const float* __restrict__ v, const float* __restrict__ c, uint32_t n) {
+#pragma clang fp contract(off)  // the tail's diff * diff + s rounds twice, as in the shader
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    const uint32_t n4 = n / 4;
+    for (uint32_t d = 0; d < n4; ++d) {
+        const float e0 = v[4 * d] - c[4 * d], e1 = v[4 * d + 1] - c[4 * d + 1];
+        const float e2 = v[4 * d + 2] - c[4 * d + 2], e3 = v[4 * d + 3] - c[4 * d + 3];
+        a0 = __builtin_fmaf(e0, e0, a0);
+        a1 = __builtin_fmaf(e1, e1, a1);
+        a2 = __builtin_fmaf(e2, e2, a2);
+        a3 = __builtin_fmaf(e3, e3, a3);
+    }
+    float s = ((a0 + a1) + a2) + a3;
+    for (uint32_t d = n4 * 4; d < n; ++d) {
+        const float e = v[d] - c[d];
+        s = s + e * e;  // not fused: the pragma above covers expressions written here
+    }
+    return s;
+}
+
+// codes[n * M + m] = argmin_k |x_nm - c_mk|^2 (strict <: the lowest k on ties); one thread per
+// (row, subspace), grid.y = subspace
+__global__ __launch_bounds__(256) void pq_assign(const float* __restrict__ x, uint32_t N, uint32_t D, uint32_t M,
+                                                 uint32_t K, const float* __restrict__ cb, uint8_t* __restrict__ codes) {
+    const uint32_t n = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
+    if (n >= N) return;
+    const uint32_t ds = D / M;
+    const float* v = x + int64_t(n) * D + int64_t(m) * ds;
+    const float* c = cb + int64_t(m) * K * ds;
+    float best = __builtin_inff();
+    uint32_t bk = 0;
+    for (uint32_t k = 0; k < K; ++k) {
+        const float d = sub_l2sq(v, c + int64_t(k) * ds, ds);
+        if (d < best) {
+            best = d;
+            bk = k;
+        }
+    }
+    codes[int64_t(n) * M + m] = uint8_t(bk);
+}
+
+// tables[q][m][k] = |q_m - c_mk|^2 (pq_precompute_distance_table)
+__global__ __launch_bounds__(256) void pq_tables(const float* __restrict__ q, uint32_t D, uint32_t M, uint32_t K,
+                                                 const float* __restrict__ cb, float* __restrict__ tables) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y, qi = blockIdx.z;
+    if (k >= K) return;
+    const uint32_t ds = D / M;
+    tables[(int64_t(qi) * M + m) * K + k] =
+        sub_l2sq(q + int64_t(qi) * D + int64_t(m) * ds, cb + (int64_t(m) * K + k) * ds, ds);
+}
+
+// ---- training: fixed-order sums per (subspace, centroid) -------------------------------------
+
+__global__ __launch_bounds__(256) void pq_column(const uint8_t* __restrict__ codes, uint32_t N, uint32_t M, uint32_t m,
+                                                 uint8_t* __restrict__ col, uint32_t* __restrict__ iota) {
+    const uint32_t n = blockIdx.x * 256 + threadIdx.x;
+    if (n >= N) return;
+    col[n] = codes[int64_t(n) * M + m];
+    iota[n] = n;
+}
+
+// first[k], counts[k], chunk counts of subspace m's sorted codes
+__global__ __launch_bounds__(256) void pq_ranges(const uint8_t* __restrict__ sorted, uint32_t N, uint32_t K,
+                                                 uint32_t* __restrict__ first, uint32_t* __restrict__ counts,
+                                                 uint32_t* __restrict__ chunks) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    if (k >= K) return;
+    auto lower = [&](uint32_t v) {
+        uint32_t lo = 0, hi = N;
+        while (lo < hi) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (uint32_t(sorted[mid]) < v) lo = mid + 1;
+            else hi = mid;
+        }
+        return lo;
+    };
+    const uint32_t a = lower(k), b = lower(k + 1);
+    first[k] = a;
+    counts[k] = b - a;
+    chunks[k] = (b - a + kPQChunk - 1) / kPQChunk;
+}
+
+// chunk sums of subspace m: chunk b (cluster from the inclusive scan chunk_end) sums its points'
+// sub-vectors in point order
+__global__ __launch_bounds__(256) void pq_chunk_sums(const float* __restrict__ x, uint32_t D, uint32_t ds, uint32_t m,
+                                                     uint32_t K, const uint32_t* __restrict__ members,
+                                                     const uint32_t* __restrict__ first,
+                                                     const uint32_t* __restrict__ counts,
+                                                     const uint32_t* __restrict__ chunk_end,
+                                                     float* __restrict__ partial) {
+    __shared__ uint32_t rows[kPQChunk];
+    const uint32_t b = blockIdx.x;
+    if (b >= chunk_end[K - 1]) return;
+    uint32_t lo = 0, hi = K - 1;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (chunk_end[mid] > b) hi = mid;
+        else lo = mid + 1;
+    }
+    const uint32_t c = lo, n = counts[c];
+    const uint32_t nch = (n + kPQChunk - 1) / kPQChunk;
+    const uint32_t t = b - (chunk_end[c] - nch);
+    const uint32_t p0 = first[c] + t * kPQChunk, cnt = min(kPQChunk, n - t * kPQChunk);
+    if (threadIdx.x < cnt) rows[threadIdx.x] = members[p0 + threadIdx.x];
+    __syncthreads();
+    for (uint32_t d = threadIdx.x; d < ds; d += 256) {
+        float s = 0.0f;
+        for (uint32_t i = 0; i < cnt; ++i) s += x[int64_t(rows[i]) * D + int64_t(m) * ds + d];
+        partial[int64_t(b) * ds + d] = s;
+    }
+}
+
+// new centroid = (chunk sums in order) * (1/count) (pq_train_update_finalize); empty keeps its
+// value; movement_sq[m * K + k] = sum_d (old - new)^2 (0 when empty)
+__global__ __launch_bounds__(64) void pq_finalize(uint32_t ds, uint32_t m, uint32_t K,
+                                                  const uint32_t* __restrict__ counts,
+                                                  const uint32_t* __restrict__ chunk_end,
+                                                  const float* __restrict__ partial, float* __restrict__ cb,
+                                                  float* __restrict__ movement) {
+#pragma clang fp contract(off)  // movement rounds diff * diff and the add separately
+    const uint32_t k = blockIdx.x * 64 + threadIdx.x;
+    if (k >= K) return;
+    const uint32_t n = counts[k];
+    float mv = 0.0f;
+    if (n > 0) {
+        const uint32_t nch = (n + kPQChunk - 1) / kPQChunk, b0 = chunk_end[k] - nch;
+        const float inv = 1.0f / float(n);
+        float* c = cb + (int64_t(m) * K + k) * ds;
+        for (uint32_t d = 0; d < ds; ++d) {
+            float s = 0.0f;
+            for (uint32_t t = 0; t < nch; ++t) s += partial[int64_t(b0 + t) * ds + d];
+            const float nv = s * inv, ov = c[d];
+            c[d] = nv;
+            const float diff = ov - nv;
+            mv = mv + diff * diff;
+        }
+    }
+    movement[int64_t(m) * K + k] = mv;
+}
+
+// total movement sqrt(sum / (M K)), summed in index order by one thread
+__global__ void pq_movement(const float* __restrict__ movement, uint32_t n, float* __restrict__ out) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    float t = 0.0f;
+    for (uint32_t i = 0; i < n; ++i) t += movement[i];
+    *out = sqrtf(t / float(n));
+}
+
+__global__ __launch_bounds__(256) void pq_init(const float* __restrict__ x, uint32_t D, uint32_t M, uint32_t K,
+                                               const uint32_t* __restrict__ rows, float* __restrict__ cb) {
+    const uint32_t mk = blockIdx.x, m = mk / K;
+    const uint32_t ds = D / M;
+    for (uint32_t d = threadIdx.x; d < ds; d += 256)
+        cb[int64_t(mk) * ds + d] = x[int64_t(rows[mk]) * D + int64_t(m) * ds + d];
+}
+
+// ---- ADC scan ----------------------------------------------------------------------------------
+
+struct AdcArgs {
+    const uint8_t* codes = nullptr;
+    const float* tables = nullptr;  // [Q x M x K]
+    uint32_t M = 0, K = 0;
+    uint32_t QB = 1;                // queries per workgroup (tables in LDS)
+    // queries q0 + i (or qrow[i]), i < nq; rows c0 + j * stride, j < cols
+    const uint32_t* qrow = nullptr;
+    uint32_t q0 = 0, nq = 0;
+    uint32_t c0 = 0, cols = 0, stride = 1;
+    // dense keys (or the fp32 sums themselves when out_f is set)
+    uint32_t* out_k = nullptr;
+    float* out_f = nullptr;
+    int64_t ldo = 0;
+    bool words = false;  // code rows 4-byte aligned (M % 4 == 0, aligned base): word loads
+    // filter
+    const uint32_t* thr = nullptr;
+    uint32_t* cnt = nullptr;
+    uint32_t* cand_key = nullptr;
+    uint32_t* cand_id = nullptr;
+    uint32_t cap = 0;
+};
+
+// grid: x = row blocks (each strides over the rows), y = query groups of QB
+template <bool FILTER>
+__global__ __launch_bounds__(256) void pq_adc_kernel(AdcArgs a) {
+    extern __shared__ float tab[];  // [QB x M x K]
+    const uint32_t g0 = blockIdx.y * a.QB;
+    const uint32_t nqg = min(a.QB, a.nq - g0);
+    const uint32_t MK = a.M * a.K;
+    for (uint32_t i = 0; i < nqg; ++i) {
+        const uint32_t qi = a.qrow ? a.qrow[g0 + i] : a.q0 + g0 + i;
+        const float* src = a.tables + int64_t(qi) * MK;
+        for (uint32_t e = threadIdx.x; e < MK; e += 256) tab[i * MK + e] = src[e];
+    }
+    __syncthreads();
+    for (uint32_t j = blockIdx.x * 256 + threadIdx.x; j < a.cols; j += gridDim.x * 256) {
+        const uint32_t row = a.c0 + j * a.stride;
+        const uint8_t* cr = a.codes + int64_t(row) * a.M;
+        for (uint32_t i = 0; i < nqg; ++i) {
+            const float* t = tab + i * MK;
+            float s = 0.0f;
+            uint32_t m = 0;
+            if (a.words)
+            for (; m + 4 <= a.M; m += 4) {
+                const uint32_t w = *reinterpret_cast<const uint32_t*>(cr + m);
+                s += t[m * a.K + (w & 0xFF)];
+                s += t[(m + 1) * a.K + ((w >> 8) & 0xFF)];
+                s += t[(m + 2) * a.K + ((w >> 16) & 0xFF)];
+                s += t[(m + 3) * a.K + (w >> 24)];
+            }
+            for (; m < a.M; ++m) s += t[m * a.K + cr[m]];
+            const uint32_t key = key_of_float(s);
+            if (FILTER) {
+                const uint32_t qi = a.q0 + g0 + i;
+                if (key <= a.thr[qi]) {
+                    const uint32_t pos = atomicAdd(a.cnt + qi, 1u);
+                    if (pos < a.cap) {
+                        const int64_t o = int64_t(qi) * a.cap + pos;
+                        a.cand_key[o] = key;
+                        a.cand_id[o] = row;
+                    }
+                }
+            } else if (a.out_f) {
+                a.out_f[int64_t(g0 + i) * a.ldo + j] = s;
+            } else {
+                a.out_k[int64_t(g0 + i) * a.ldo + j] = key;
+            }
+        }
+    }
+}
+
+// Query groups of QB (as many tables as fit in 160 KB of LDS, at most 16) on grid.y, in launches
+// of at most 65535 groups.
+template <bool FILTER>
+va_status launch_adc(va_context* ctx, AdcArgs a) {
+    if (a.nq == 0 || a.cols == 0) return VA_OK;
+    const size_t per_q = size_t(a.M) * a.K * 4;
+    const size_t lds_max = 160 * 1024;
+    if (per_q > lds_max) return fail(ctx, VA_ERR_UNSUPPORTED, "PQ table of %zu bytes exceeds LDS", per_q);
+    a.words = (a.M % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.codes) & 3) == 0);
+    a.QB = uint32_t(std::min<size_t>({size_t(16), lds_max / per_q, size_t(a.nq)}));
+    const uint64_t span = uint64_t(65535) * a.QB;
+    if (a.nq > span) {
+        AdcArgs b = a;
+        for (uint64_t s0 = 0; s0 < a.nq; s0 += span) {
+            b.nq = uint32_t(std::min<uint64_t>(span, a.nq - s0));
+            if (a.qrow) b.qrow = a.qrow + s0;
+            else b.q0 = a.q0 + uint32_t(s0);
+            if (a.out_k) b.out_k = a.out_k + int64_t(s0) * a.ldo;
+            if (a.out_f) b.out_f = a.out_f + int64_t(s0) * a.ldo;
+            VA_CHECK_STATUS(launch_adc<FILTER>(ctx, b));
+        }
+        return VA_OK;
+    }
+    const uint32_t groups = (a.nq + a.QB - 1) / a.QB;
+    // enough row blocks to fill the chip a few times over; each re-reads its group's tables
+    uint32_t rb = std::max<uint32_t>(1, uint32_t(std::min<uint64_t>((uint64_t(a.cols) + 255) / 256,
+                                                                     std::max<uint64_t>(1, 2048 / groups))));
+    const size_t lds = size_t(a.QB) * per_q;
+    auto kern = &pq_adc_kernel<FILTER>;
+    if (lds > 65536)
+        VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+    kern<<<dim3(rb, groups), dim3(256), lds, ctx->stream>>>(a);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
+struct AdcProducer final : KeyProducer {
+    va_context* ctx;
+    const uint8_t* codes;
+    const float* tables;
+    uint32_t Q, N, M, K;
+    va_status dense(const uint32_t* qrow, uint32_t q0, uint32_t nq, uint32_t c0, uint32_t cols, uint32_t stride,
+                    uint32_t* out_k, int64_t ldo) override {
+        AdcArgs a;
+        a.codes = codes;
+        a.tables = tables;
+        a.M = M;
+        a.K = K;
+        a.qrow = qrow;
+        a.q0 = q0;
+        a.nq = nq;
+        a.c0 = c0;
+        a.cols = cols;
+        a.stride = stride;
+        a.out_k = out_k;
+        a.ldo = ldo;
+        return launch_adc<false>(ctx, a);
+    }
+    va_status filter(const uint32_t* thr, uint32_t* cnt, uint32_t* ckey, uint32_t* cid, uint32_t cap) override {
+        AdcArgs a;
+        a.codes = codes;
+        a.tables = tables;
+        a.M = M;
+        a.K = K;
+        a.q0 = 0;
+        a.nq = Q;
+        a.c0 = 0;
+        a.cols = N;
+        a.thr = thr;
+        a.cnt = cnt;
+        a.cand_key = ckey;
+        a.cand_id = cid;
+        a.cap = cap;
+        return launch_adc<true>(ctx, a);
+    }
+};
+
+__global__ __launch_bounds__(256) void sqrt_inplace(float* __restrict__ v, uint64_t n) {
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n) v[i] = sqrtf(v[i]);
+}
+
+struct Owned {
+    std::vector<void*> p;
+    ~Owned() {
+        for (void* q : p) (void)hipFree(q);
+    }
+};
+template <class T>
+va_status alloc(va_context* ctx, Owned& own, size_t bytes, T** out) {
+    void* q = nullptr;
+    VA_CHECK_HIP(ctx, hipMalloc(&q, std::max<size_t>(bytes, 256)));
+    own.p.push_back(q);
+    *out = static_cast<T*>(q);
+    return VA_OK;
+}
+
+uint64_t splitmix64(uint64_t& s) {
+    uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+}  // namespace
+}  // namespace va
+
+#define VA_PQ_CHECK_SHAPE(ctx, D, M, K)                                                                       \
+    do {                                                                                                      \
+        VA_REQUIRE(ctx, (M) >= 1 && (D) >= 1 && (D) % (M) == 0, "Dimension must be divisible by M (D=%u, M=%u)", \
+                   (D), (M));                                                                                 \
+        VA_REQUIRE(ctx, (K) >= 1 && (K) <= 256, "K must be <= 256 for uint8 encoding, got %u", (K));           \
+    } while (0)
+
+extern "C" {
+
+va_status va_pq_train(va_context* ctx, const float* data, uint32_t count, uint32_t dim, uint32_t M, uint32_t K,
+                      uint32_t iterations, float threshold, uint64_t seed, const float* initial_codebooks,
+                      float* out_codebooks, uint32_t* out_iterations) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    VA_REQUIRE(ctx, data && out_codebooks, "va_pq_train: NULL pointer");
+    VA_PQ_CHECK_SHAPE(ctx, dim, M, K);
+    VA_REQUIRE(ctx, count >= 1, "va_pq_train: no training vectors");
+    va::DeviceGuard g(ctx->device);
+    const uint32_t N = count, D = dim, ds = dim / M;
+    va::Owned own;
+    uint8_t *codes, *col, *sorted;
+    uint32_t *iota, *members, *first, *counts, *chunks, *chunk_end, *rows;
+    float *partial, *movement, *mv;
+    const uint64_t max_chunks = uint64_t(N) / va::kPQChunk + K;
+    VA_CHECK_STATUS(va::alloc(ctx, own, size_t(N) * M, &codes));
+    VA_CHECK_STATUS(va::alloc(ctx, own, size_t(N), &col));
+    VA_CHECK_STATUS(va::alloc(ctx, own, size_t(N), &sorted));
+    VA_CHECK_STATUS(va::alloc(ctx, own, size_t(N) * 4, &iota));
+    VA_CHECK_STATUS(va::alloc(ctx, own, size_t(N) * 4, &members));
+    VA_CHECK_STATUS(va::alloc(ctx, own, size_t(K) * 4, &first));
+    VA_CHECK_STATUS(va::alloc(ctx, own, size_t(K) * 4, &counts));
+    VA_CHECK_STATUS(va::alloc(ctx, own, size_t(K) * 4, &chunks));
+    VA_CHECK_STATUS(va::alloc(ctx, own, size_t(K) * 4, &chunk_end));
+    VA_CHECK_STATUS(va::alloc(ctx, own, size_t(M) * K * 4, &rows));
+    VA_CHECK_STATUS(va::alloc(ctx, own, size_t(max_chunks) * ds * 4, &partial));
+    VA_CHECK_STATUS(va::alloc(ctx, own, size_t(M) * K * 4, &movement));
+    VA_CHECK_STATUS(va::alloc(ctx, own, 4, &mv));
+    size_t sort_bytes = 0, scan_bytes = 0;
+    VA_CHECK_HIP(ctx, rocprim::radix_sort_pairs(nullptr, sort_bytes, col, sorted, iota, members, N, 0, 8, ctx->stream));
+    VA_CHECK_HIP(ctx, rocprim::inclusive_scan(nullptr, scan_bytes, chunks, chunk_end, K, rocprim::plus<uint32_t>(),
+                                              ctx->stream));
+    void* tmp;
+    VA_CHECK_STATUS(va::alloc(ctx, own, std::max(sort_bytes, scan_bytes), &tmp));
+    // initial codebooks: given, or codebook (m, k) = sub-vector m of a random training row
+    // (initializeCodebooks, ProductQuantizationKernel.swift:548-572; rows from splitmix64(seed))
+    std::vector<uint32_t> hrows(size_t(M) * K);
+    if (initial_codebooks) {
+        VA_CHECK_HIP(ctx, hipMemcpyAsync(out_codebooks, initial_codebooks, size_t(M) * K * ds * 4,
+                                         hipMemcpyDeviceToDevice, ctx->stream));
+    } else {
+        uint64_t s = seed;
+        for (auto& r : hrows) r = uint32_t((double(va::splitmix64(s) >> 11) * 0x1.0p-53) * double(N)) % N;
+        VA_CHECK_HIP(ctx, hipMemcpyAsync(rows, hrows.data(), hrows.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+        va::pq_init<<<dim3(M * K), dim3(256), 0, ctx->stream>>>(data, D, M, K, rows, out_codebooks);
+        VA_CHECK_LAUNCH(ctx);
+    }
+    const uint32_t nb = (N + 255) / 256;
+    uint32_t it = 0;
+    for (; it < iterations;) {
+        va::pq_assign<<<dim3(nb, M), dim3(256), 0, ctx->stream>>>(data, N, D, M, K, out_codebooks, codes);
+        VA_CHECK_LAUNCH(ctx);
+        for (uint32_t m = 0; m < M; ++m) {
+            va::pq_column<<<dim3(nb), dim3(256), 0, ctx->stream>>>(codes, N, M, m, col, iota);
+            VA_CHECK_LAUNCH(ctx);
+            VA_CHECK_HIP(ctx, rocprim::radix_sort_pairs(tmp, sort_bytes, col, sorted, iota, members, N, 0, 8, ctx->stream));
+            va::pq_ranges<<<dim3((K + 255) / 256), dim3(256), 0, ctx->stream>>>(sorted, N, K, first, counts, chunks);
+            VA_CHECK_LAUNCH(ctx);
+            VA_CHECK_HIP(ctx, rocprim::inclusive_scan(tmp, scan_bytes, chunks, chunk_end, K, rocprim::plus<uint32_t>(),
+                                                      ctx->stream));
+            va::pq_chunk_sums<<<dim3(uint32_t(max_chunks)), dim3(256), 0, ctx->stream>>>(data, D, ds, m, K, members, first,
+                                                                                        counts, chunk_end, partial);
+            VA_CHECK_LAUNCH(ctx);
+            va::pq_finalize<<<dim3((K + 63) / 64), dim3(64), 0, ctx->stream>>>(ds, m, K, counts, chunk_end, partial,
+                                                                             out_codebooks, movement);
+            VA_CHECK_LAUNCH(ctx);
+        }
+        va::pq_movement<<<dim3(1), dim3(64), 0, ctx->stream>>>(movement, M * K, mv);
+        VA_CHECK_LAUNCH(ctx);
+        VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->host_word, mv, 4, hipMemcpyDeviceToHost, ctx->stream));
+        VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        ++it;
+        if (__builtin_bit_cast(float, ctx->host_word[0]) < threshold) break;
+    }
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (out_iterations) *out_iterations = it;
+    return VA_OK;
+}
+
+va_status va_pq_encode(va_context* ctx, const float* x, uint32_t num_vectors, uint32_t dim, uint32_t M, uint32_t K,
+                       const float* codebooks, uint8_t* codes) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    VA_REQUIRE(ctx, x && codebooks && codes, "va_pq_encode: NULL pointer");
+    VA_PQ_CHECK_SHAPE(ctx, dim, M, K);
+    if (num_vectors == 0) return VA_OK;
+    va::DeviceGuard g(ctx->device);
+    va::pq_assign<<<dim3((num_vectors + 255) / 256, M), dim3(256), 0, ctx->stream>>>(x, num_vectors, dim, M, K,
+                                                                                       codebooks, codes);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
+va_status va_pq_distance_tables(va_context* ctx, const float* queries, uint32_t num_queries, uint32_t dim, uint32_t M,
+                                uint32_t K, const float* codebooks, float* tables) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    VA_REQUIRE(ctx, queries && codebooks && tables, "va_pq_distance_tables: NULL pointer");
+    VA_PQ_CHECK_SHAPE(ctx, dim, M, K);
+    VA_REQUIRE(ctx, num_queries <= 65535, "va_pq_distance_tables: at most 65535 queries per call");
+    if (num_queries == 0) return VA_OK;
+    va::DeviceGuard g(ctx->device);
+    va::pq_tables<<<dim3((K + 255) / 256, M, num_queries), dim3(256), 0, ctx->stream>>>(queries, dim, M, K, codebooks,
+                                                                                          tables);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
+va_status va_pq_adc_distances(va_context* ctx, const float* tables, uint32_t num_queries, const uint8_t* codes,
+                              uint32_t num_vectors, uint32_t M, uint32_t K, float* out) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    VA_REQUIRE(ctx, tables && codes && out, "va_pq_adc_distances: NULL pointer");
+    VA_REQUIRE(ctx, M >= 1 && K >= 1 && K <= 256, "va_pq_adc_distances: bad M / K");
+    if (num_queries == 0 || num_vectors == 0) return VA_OK;
+    va::DeviceGuard g(ctx->device);
+    va::AdcArgs a;
+    a.codes = codes;
+    a.tables = tables;
+    a.M = M;
+    a.K = K;
+    a.q0 = 0;
+    a.nq = num_queries;
+    a.c0 = 0;
+    a.cols = num_vectors;
+    a.out_f = out;
+    a.ldo = num_vectors;
+    return va::launch_adc<false>(ctx, a);
+}
+
+va_status va_pq_search(va_context* ctx, const float* queries, uint32_t num_queries, uint32_t dim, uint32_t M,
+                       uint32_t K, const float* codebooks, const uint8_t* codes, uint32_t num_vectors, uint32_t k,
+                       uint32_t* out_idx, float* out_dist) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    VA_REQUIRE(ctx, queries && codebooks && codes && out_idx, "va_pq_search: NULL pointer");
+    VA_PQ_CHECK_SHAPE(ctx, dim, M, K);
+    VA_REQUIRE(ctx, k >= 1 && k <= VA_MAX_K, "k must be in [1, %u], got %u", VA_MAX_K, k);
+    if (num_queries == 0) return VA_OK;
+    va::DeviceGuard g(ctx->device);
+    va::Owned own;
+    float* tables;
+    VA_CHECK_STATUS(va::alloc(ctx, own, size_t(num_queries) * M * K * 4, &tables));
+    for (uint32_t q0 = 0; q0 < num_queries; q0 += 65535) {
+        const uint32_t nq = std::min<uint32_t>(65535, num_queries - q0);
+        VA_CHECK_STATUS(va_pq_distance_tables(ctx, queries + int64_t(q0) * dim, nq, dim, M, K, codebooks,
+                                              tables + int64_t(q0) * M * K));
+    }
+    va::AdcProducer kp;
+    kp.ctx = ctx;
+    kp.codes = codes;
+    kp.tables = tables;
+    kp.Q = num_queries;
+    kp.N = num_vectors;
+    kp.M = M;
+    kp.K = K;
+    va::ScanOutputs o;
+    o.idx = out_idx;
+    o.f = out_dist;
+    VA_CHECK_STATUS(va::exact_topk_scan(ctx, kp, num_queries, num_vectors, k, o));
+    // findNearestNeighbors reports sqrt of the ADC sum (ProductQuantizationKernel.swift:531-537)
+    if (out_dist) {
+        const uint64_t n = uint64_t(num_queries) * k;
+        va::sqrt_inplace<<<dim3(uint32_t((n + 255) / 256)), dim3(256), 0, ctx->stream>>>(out_dist, n);
+        VA_CHECK_LAUNCH(ctx);
+    }
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));  // the tables are freed on return
+    return VA_OK;
+}
+
+}  // extern "C"
