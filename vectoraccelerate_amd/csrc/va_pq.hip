@@ -262,6 +262,81 @@ __global__ __launch_bounds__(256) void pq_adc_kernel(AdcArgs a) {
     }
 }
 
+// K = 256 and M in {8, 16, 32, 64}: M and the query group QB = 64 / M are compile-time, so the
+// table entry of (query i, subspace m, code c) is LDS byte 4 c + a constant offset: one
+// ds_read_b32 with an immediate offset and one add per lookup, the code bytes unpacked once per
+// row for all QB queries.  QB x M x 1 KB = 64 KB of tables: two workgroups per CU.
+template <int M, bool FILTER>
+__global__ __launch_bounds__(256) void pq_adc_fast(AdcArgs a) {
+    constexpr int QB = 64 / M;
+    constexpr int MK = M * 256;
+    __shared__ float tab[QB * MK];
+    const uint32_t g0 = blockIdx.y * QB;
+    const uint32_t nqg = min(uint32_t(QB), a.nq - g0);
+    for (uint32_t i = 0; i < uint32_t(QB); ++i) {
+        const uint32_t qi = i < nqg ? (a.qrow ? a.qrow[g0 + i] : a.q0 + g0 + i) : 0u;
+        const float* src = a.tables + int64_t(qi) * MK;
+        for (uint32_t e = threadIdx.x; e < uint32_t(MK); e += 256) tab[i * MK + e] = i < nqg ? src[e] : 0.0f;
+    }
+    __syncthreads();
+    for (uint32_t j = blockIdx.x * 256 + threadIdx.x; j < a.cols; j += gridDim.x * 256) {
+        const uint32_t row = a.c0 + j * a.stride;
+        const uint4* cr = reinterpret_cast<const uint4*>(a.codes + int64_t(row) * M);
+        uint32_t w[M / 4];
+        if constexpr (M == 8) {
+            const uint2 v = *reinterpret_cast<const uint2*>(cr);
+            w[0] = v.x;
+            w[1] = v.y;
+        } else {
+#pragma unroll
+            for (int b = 0; b < M / 16; ++b) {
+                const uint4 v = cr[b];
+                w[4 * b] = v.x;
+                w[4 * b + 1] = v.y;
+                w[4 * b + 2] = v.z;
+                w[4 * b + 3] = v.w;
+            }
+        }
+        uint32_t off[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) off[m] = (w[m / 4] >> (8 * (m % 4))) & 0xFFu;
+#pragma unroll
+        for (int i = 0; i < QB; ++i) {
+            if (uint32_t(i) >= nqg) break;
+            float s = 0.0f;
+#pragma unroll
+            for (int m = 0; m < M; ++m) s += tab[i * MK + m * 256 + off[m]];
+            const uint32_t key = key_of_float(s);
+            if (FILTER) {
+                const uint32_t qi = a.q0 + g0 + i;
+                if (key <= a.thr[qi]) {
+                    const uint32_t pos = atomicAdd(a.cnt + qi, 1u);
+                    if (pos < a.cap) {
+                        const int64_t o = int64_t(qi) * a.cap + pos;
+                        a.cand_key[o] = key;
+                        a.cand_id[o] = row;
+                    }
+                }
+            } else if (a.out_f) {
+                a.out_f[int64_t(g0 + i) * a.ldo + j] = s;
+            } else {
+                a.out_k[int64_t(g0 + i) * a.ldo + j] = key;
+            }
+        }
+    }
+}
+
+template <int M, bool FILTER>
+va_status launch_adc_fast(va_context* ctx, const AdcArgs& a) {
+    constexpr uint32_t QB = 64 / M;
+    const uint32_t groups = (a.nq + QB - 1) / QB;
+    const uint32_t rb = std::max<uint32_t>(
+        1, uint32_t(std::min<uint64_t>((uint64_t(a.cols) + 255) / 256, std::max<uint64_t>(1, 4096 / groups))));
+    pq_adc_fast<M, FILTER><<<dim3(rb, groups), dim3(256), 0, ctx->stream>>>(a);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
 // Query groups of QB (as many tables as fit in 160 KB of LDS, at most 16) on grid.y, in launches
 // of at most 65535 groups.
 template <bool FILTER>
@@ -272,6 +347,9 @@ va_status launch_adc(va_context* ctx, AdcArgs a) {
     if (per_q > lds_max) return fail(ctx, VA_ERR_UNSUPPORTED, "PQ table of %zu bytes exceeds LDS", per_q);
     a.words = (a.M % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.codes) & 3) == 0);
     a.QB = uint32_t(std::min<size_t>({size_t(16), lds_max / per_q, size_t(a.nq)}));
+    const bool fast = a.K == 256 && (a.M == 8 || a.M == 16 || a.M == 32 || a.M == 64) &&
+                      (reinterpret_cast<uintptr_t>(a.codes) & 15) == 0;
+    if (fast) a.QB = 64 / a.M;
     const uint64_t span = uint64_t(65535) * a.QB;
     if (a.nq > span) {
         AdcArgs b = a;
@@ -284,6 +362,14 @@ va_status launch_adc(va_context* ctx, AdcArgs a) {
             VA_CHECK_STATUS(launch_adc<FILTER>(ctx, b));
         }
         return VA_OK;
+    }
+    if (fast) {
+        switch (a.M) {
+            case 8: return launch_adc_fast<8, FILTER>(ctx, a);
+            case 16: return launch_adc_fast<16, FILTER>(ctx, a);
+            case 32: return launch_adc_fast<32, FILTER>(ctx, a);
+            default: return launch_adc_fast<64, FILTER>(ctx, a);
+        }
     }
     const uint32_t groups = (a.nq + a.QB - 1) / a.QB;
     // enough row blocks to fill the chip a few times over; each re-reads its group's tables
