@@ -54,21 +54,53 @@ __device__ __forceinline__ float sub_l2sq(const float* __restrict__ v, const flo
 }
 
 // codes[n * M + m] = argmin_k |x_nm - c_mk|^2 (strict <: the lowest k on ties); one thread per
-// (row, subspace), grid.y = subspace
+// (row, subspace), grid.y = subspace.  Centroids go in chunks of kAssignChunk: the thread's four
+// values of a float4 block are loaded once and used for the whole chunk (4 accumulators per
+// centroid, the sub_l2sq order), the centroids' values are the same for the whole wave.
+constexpr uint32_t kAssignChunk = 16;
 __global__ __launch_bounds__(256) void pq_assign(const float* __restrict__ x, uint32_t N, uint32_t D, uint32_t M,
                                                  uint32_t K, const float* __restrict__ cb, uint8_t* __restrict__ codes) {
+#pragma clang fp contract(off)  // the tail's diff * diff + s rounds twice, as in the shader
     const uint32_t n = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
     if (n >= N) return;
-    const uint32_t ds = D / M;
+    const uint32_t ds = D / M, n4 = ds / 4;
     const float* v = x + int64_t(n) * D + int64_t(m) * ds;
-    const float* c = cb + int64_t(m) * K * ds;
+    const float* cm = cb + int64_t(m) * K * ds;
     float best = __builtin_inff();
     uint32_t bk = 0;
-    for (uint32_t k = 0; k < K; ++k) {
-        const float d = sub_l2sq(v, c + int64_t(k) * ds, ds);
-        if (d < best) {
-            best = d;
-            bk = k;
+    for (uint32_t k0 = 0; k0 < K; k0 += kAssignChunk) {
+        const uint32_t kn = min(kAssignChunk, K - k0);
+        float acc[kAssignChunk][4];
+#pragma unroll
+        for (uint32_t kk = 0; kk < kAssignChunk; ++kk) acc[kk][0] = acc[kk][1] = acc[kk][2] = acc[kk][3] = 0.0f;
+        for (uint32_t d = 0; d < n4; ++d) {
+            const float x0 = v[4 * d], x1 = v[4 * d + 1], x2 = v[4 * d + 2], x3 = v[4 * d + 3];
+#pragma unroll
+            for (uint32_t kk = 0; kk < kAssignChunk; ++kk) {
+                if (kk < kn) {
+                    const float* c = cm + int64_t(k0 + kk) * ds + 4 * d;
+                    const float e0 = x0 - c[0], e1 = x1 - c[1], e2 = x2 - c[2], e3 = x3 - c[3];
+                    acc[kk][0] = __builtin_fmaf(e0, e0, acc[kk][0]);
+                    acc[kk][1] = __builtin_fmaf(e1, e1, acc[kk][1]);
+                    acc[kk][2] = __builtin_fmaf(e2, e2, acc[kk][2]);
+                    acc[kk][3] = __builtin_fmaf(e3, e3, acc[kk][3]);
+                }
+            }
+        }
+#pragma unroll
+        for (uint32_t kk = 0; kk < kAssignChunk; ++kk) {
+            if (kk < kn) {
+                float t = ((acc[kk][0] + acc[kk][1]) + acc[kk][2]) + acc[kk][3];
+                const float* c = cm + int64_t(k0 + kk) * ds;
+                for (uint32_t d = n4 * 4; d < ds; ++d) {
+                    const float e = v[d] - c[d];
+                    t = t + e * e;
+                }
+                if (t < best) {
+                    best = t;
+                    bk = k0 + kk;
+                }
+            }
         }
     }
     codes[int64_t(n) * M + m] = uint8_t(bk);
