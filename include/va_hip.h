@@ -216,6 +216,14 @@ va_status va_hamming_topk(va_context* ctx, const uint32_t* query_codes, const ui
 va_status va_ivf_build(va_context* ctx, const float* centroids, uint32_t num_centroids, const float* x,
                        uint32_t num_vectors, uint32_t dim, va_ivf** out);
 va_status va_ivf_destroy(va_ivf* ivf);
+/* Add rows to a built index without rebuilding it: each row of x [num_vectors x dim] goes to the
+ * end of its nearest list (ties -> lower id), with id first_id + row; the lists stay in CSR order
+ * with insertion order inside each list, as a rebuild over all rows would lay them out
+ * (IVFStructure.assignToCluster, Index/Internal/IVFStructure.swift:280-287, then
+ * prepareGPUStructure).  Moves the existing list data once (no distance work for it).
+ * Synchronises the context. */
+va_status va_ivf_add(va_context* ctx, va_ivf* ivf, const float* x, uint32_t num_vectors, uint32_t dim,
+                     uint32_t first_id);
 /* Copy the CSR structure to the host: offsets[C+1], ids[N] (row ids in list order). */
 va_status va_ivf_get_lists(va_context* ctx, const va_ivf* ivf, uint32_t* host_offsets, uint32_t* host_ids);
 /* Coarse quantizer: probes[Q x nprobe] = the nprobe nearest centroids by (L2^2, id).

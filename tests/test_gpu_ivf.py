@@ -133,3 +133,35 @@ def test_ivf_recall_vs_flat(ctx, oracle):
         st.close()
     assert recalls[0] <= recalls[1] <= recalls[2]
     assert recalls[2] == 1.0
+
+
+@pytest.mark.parametrize("C,D,N0,adds", [(64, 48, 3000, [500, 1, 2500]), (7, 30, 1, [10, 1000]), (256, 96, 20000, [30000])])
+def test_ivf_add_matches_rebuild(ctx, oracle, C, D, N0, adds):
+    """va_ivf_add appends rows to their nearest lists: the CSR equals a build over all rows and
+    searches agree with the rebuilt index."""
+    import torch
+
+    from vectoraccelerate_amd import IVFSearchConfiguration, IVFSearchPipeline
+
+    N = N0 + sum(adds)
+    print(f"ivf add C={C} D={D} N0={N0} adds={adds}", flush=True)
+    c, x, q = clustered(C, D, N, 40, seed=C + D)[:3]
+    pipe = IVFSearchPipeline(ctx, IVFSearchConfiguration(C, min(8, C), D))
+    xd = ctx.buffer(x)
+    st = pipe.prepareIndexStructure(c, xd[:N0])
+    r0 = N0
+    for n in adds:
+        st.add(xd[r0:r0 + n], r0)
+        r0 += n
+    off, ids = st.lists()
+    lists = oracle.ivf_assign(x, c)
+    ooff, oids = oracle.ivf_csr(lists, C)
+    np.testing.assert_array_equal(off, ooff)
+    np.testing.assert_array_equal(ids, oids)
+    full = pipe.prepareIndexStructure(c, xd)
+    a = pipe.search(q, st, 10)
+    b = pipe.search(q, full, 10)
+    np.testing.assert_array_equal(a.indices.cpu().numpy(), b.indices.cpu().numpy())
+    np.testing.assert_array_equal(a.distances.cpu().numpy(), b.distances.cpu().numpy())
+    st.close()
+    full.close()

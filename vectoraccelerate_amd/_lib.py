@@ -74,6 +74,7 @@ SIGNATURES: dict[str, tuple] = {
     "va_hamming_topk": (_st, [_p, _p, _p, _u32, _u32, _u32, _u32, _p, _p]),
     "va_ivf_build": (_st, [_p, _p, _u32, _p, _u32, _u32, C.POINTER(_p)]),
     "va_ivf_destroy": (_st, [_p]),
+    "va_ivf_add": (_st, [_p, _p, _p, _u32, _u32, _u32]),
     "va_ivf_get_lists": (_st, [_p, _p, _p, _p]),
     "va_ivf_probe": (_st, [_p, _p, _p, _u32, _u32, _p]),
     "va_ivf_scan": (_st, [_p, _p, _p, _u32, _p, _u32, _u32, _p, _p]),

@@ -48,6 +48,50 @@ inline uint32_t sample_rows(uint32_t n) {
     return std::min(n, std::max((n + kSampleRate - 1) / kSampleRate, kSampleMin));
 }
 
+// va_ivf_add: old CSR position p of list c moves to p + pre[c] (the new rows of earlier lists
+// come before it)
+__global__ __launch_bounds__(256) void ivf_merge_old(const float* __restrict__ vecs, const uint32_t* __restrict__ ids,
+                                                     const uint32_t* __restrict__ off, const uint32_t* __restrict__ pre,
+                                                     uint32_t C, uint32_t N, uint32_t D, float* __restrict__ out_vecs,
+                                                     uint32_t* __restrict__ out_ids) {
+    for (uint32_t p = blockIdx.x; p < N; p += gridDim.x) {
+        uint32_t lo = 0, hi = C - 1;  // list of p: the last c with off[c] <= p
+        while (lo < hi) {
+            const uint32_t mid = (lo + hi + 1) >> 1;
+            if (off[mid] <= p) lo = mid;
+            else hi = mid - 1;
+        }
+        const uint32_t dst = p + pre[lo];
+        for (uint32_t d = threadIdx.x; d < D; d += 256) out_vecs[uint64_t(dst) * D + d] = vecs[uint64_t(p) * D + d];
+        if (threadIdx.x == 0) out_ids[dst] = ids[p];
+    }
+}
+
+// new row at grouped position s of list c goes after list c's old rows: off[c + 1] + s
+__global__ __launch_bounds__(256) void ivf_place_new(const float* __restrict__ x, const uint32_t* __restrict__ order,
+                                                     const uint32_t* __restrict__ pre,
+                                                     const uint32_t* __restrict__ off, uint32_t C, uint32_t n,
+                                                     uint32_t D, uint32_t first_id, float* __restrict__ out_vecs,
+                                                     uint32_t* __restrict__ out_ids) {
+    for (uint32_t s = blockIdx.x; s < n; s += gridDim.x) {
+        uint32_t lo = 0, hi = C - 1;  // the last c with pre[c] <= s
+        while (lo < hi) {
+            const uint32_t mid = (lo + hi + 1) >> 1;
+            if (pre[mid] <= s) lo = mid;
+            else hi = mid - 1;
+        }
+        const uint32_t dst = off[lo + 1] + s, r = order[s];
+        for (uint32_t d = threadIdx.x; d < D; d += 256) out_vecs[uint64_t(dst) * D + d] = x[uint64_t(r) * D + d];
+        if (threadIdx.x == 0) out_ids[dst] = first_id + r;
+    }
+}
+
+__global__ __launch_bounds__(256) void ivf_new_offsets(const uint32_t* __restrict__ off, const uint32_t* __restrict__ pre,
+                                                       uint32_t C, uint32_t* __restrict__ out) {
+    const uint32_t c = blockIdx.x * 256 + threadIdx.x;
+    if (c <= C) out[c] = off[c] + pre[c];
+}
+
 __global__ __launch_bounds__(256) void gather_rows(const float* __restrict__ x, const uint32_t* __restrict__ ids,
                                                    uint32_t N, uint32_t D, float* __restrict__ out) {
     for (uint32_t p = blockIdx.x; p < N; p += gridDim.x) {
@@ -459,6 +503,62 @@ va_status va_ivf_build(va_context* ctx, const float* centroids, uint32_t num_cen
         return cleanup(va::fail(ctx, VA_ERR_HIP, "va_ivf_build: gather failed"));
     *out = ivf;
     return VA_OK;
+}
+
+va_status va_ivf_add(va_context* ctx, va_ivf* ivf, const float* x, uint32_t num_vectors, uint32_t dim,
+                     uint32_t first_id) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    VA_REQUIRE(ctx, ivf && x, "va_ivf_add: NULL pointer");
+    VA_REQUIRE(ctx, dim == ivf->D, "va_ivf_add: dimension %u, index has %u", dim, ivf->D);
+    VA_REQUIRE(ctx, uint64_t(ivf->N) + num_vectors < 0xFFFFFFFFull, "va_ivf_add: too many vectors");
+    if (num_vectors == 0) return VA_OK;
+    va::DeviceGuard g(ctx->device);
+    const uint32_t C = ivf->C, D = ivf->D, No = ivf->N, n = num_vectors, Nn = No + n;
+    struct Bufs {
+        void* p[7] = {};
+        ~Bufs() {
+            for (void* q : p)
+                if (q) (void)hipFree(q);
+        }
+    } b;
+    auto get = [&](int i, size_t bytes) -> bool {
+        if (hipMalloc(&b.p[i], std::max<size_t>(bytes, 256)) != hipSuccess) {
+            (void)hipGetLastError();
+            return false;
+        }
+        return true;
+    };
+    if (!get(0, size_t(n) * 4) || !get(1, size_t(n) * 8) || !get(2, size_t(n) * 4) || !get(3, size_t(C + 1) * 4) ||
+        !get(4, size_t(Nn) * D * 4) || !get(5, size_t(Nn) * 4) || !get(6, size_t(C + 1) * 4))
+        return va::fail(ctx, VA_ERR_OOM, "va_ivf_add: device allocation failed");
+    uint32_t* assign = static_cast<uint32_t*>(b.p[0]);
+    auto* best = static_cast<unsigned long long*>(b.p[1]);
+    uint32_t* order = static_cast<uint32_t*>(b.p[2]);  // new rows grouped by list, row order inside
+    uint32_t* pre = static_cast<uint32_t*>(b.p[3]);    // new rows in lists before c
+    float* vecs = static_cast<float*>(b.p[4]);
+    uint32_t* ids = static_cast<uint32_t*>(b.p[5]);
+    uint32_t* offs = static_cast<uint32_t*>(b.p[6]);
+    // IVFStructure.assignToCluster (Index/Internal/IVFStructure.swift:280-287) for every new row:
+    // appended to its nearest list after the rows already there
+    VA_CHECK_STATUS(va::nearest_centroids(ctx, x, ivf->centroids, n, C, D, best, assign));
+    VA_CHECK_STATUS(va::csr_from_assignments(ctx, assign, n, C, order, pre));
+    va::ivf_merge_old<<<dim3(std::min<uint32_t>(std::max<uint32_t>(No, 1), 65536)), dim3(256), 0, ctx->stream>>>(
+        ivf->list_vectors, ivf->ids, ivf->offsets, pre, C, No, D, vecs, ids);
+    VA_CHECK_LAUNCH(ctx);
+    va::ivf_place_new<<<dim3(std::min<uint32_t>(n, 65536)), dim3(256), 0, ctx->stream>>>(
+        x, order, pre, ivf->offsets, C, n, D, first_id, vecs, ids);
+    VA_CHECK_LAUNCH(ctx);
+    va::ivf_new_offsets<<<dim3((C + 1 + 255) / 256), dim3(256), 0, ctx->stream>>>(ivf->offsets, pre, C, offs);
+    VA_CHECK_LAUNCH(ctx);
+    std::vector<uint32_t> h(C + 1);
+    VA_CHECK_HIP(ctx, hipMemcpyAsync(h.data(), offs, size_t(C + 1) * 4, hipMemcpyDeviceToHost, ctx->stream));
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    std::swap(ivf->list_vectors, reinterpret_cast<float*&>(b.p[4]));
+    std::swap(ivf->ids, reinterpret_cast<uint32_t*&>(b.p[5]));
+    std::swap(ivf->offsets, reinterpret_cast<uint32_t*&>(b.p[6]));
+    ivf->h_offsets = std::move(h);
+    ivf->N = Nn;
+    return VA_OK;  // the old arrays are freed with the scratch
 }
 
 va_status va_ivf_destroy(va_ivf* ivf) {

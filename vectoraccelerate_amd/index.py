@@ -178,8 +178,13 @@ class AcceleratedVectorIndex:
             if metadata is not None and not batch:
                 self._metadata[hid] = metadata
             handles.append(VectorHandle(hid))
+        first = self._slots
         self._slots += n
-        self._ivf_dirty = True
+        if self._ivf is not None and not self._ivf_dirty:
+            # built lists: append the new rows to their nearest lists (va_ivf_add) instead of a rebuild
+            self._ivf.add(self._storage[first:first + n], first)
+        else:
+            self._ivf_dirty = True
         return handles if batch else handles[0]
 
     def remove(self, handle):

@@ -78,6 +78,18 @@ class IVFGPUIndexStructure:
                                        ids.ctypes.data_as(C.c_void_p)), "va_ivf_get_lists")
         return off, ids
 
+    def add(self, vectors, firstId: int):
+        """Append rows (device tensor [n x D]) to their nearest lists, ids firstId + i (va_ivf_add)."""
+        c = self.context
+        if vectors.shape[0] == 0:
+            return
+        if vectors.shape[1] != self.dimension:
+            raise VectorError.dimensionMismatch(self.dimension, vectors.shape[1])
+        x = vectors.contiguous()
+        c.order_after_torch()
+        c.check(c.lib.va_ivf_add(c.handle, self._h, dptr(x), x.shape[0], x.shape[1], int(firstId)), "va_ivf_add")
+        self.totalVectors += x.shape[0]
+
     def listCount(self, listIndex: int) -> int:
         off, _ = self.lists()
         return int(off[listIndex + 1] - off[listIndex])
