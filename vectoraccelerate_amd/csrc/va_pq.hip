@@ -493,6 +493,7 @@ uint64_t splitmix64(uint64_t& s) {
         VA_REQUIRE(ctx, (M) >= 1 && (D) >= 1 && (D) % (M) == 0, "Dimension must be divisible by M (D=%u, M=%u)", \
                    (D), (M));                                                                                 \
         VA_REQUIRE(ctx, (K) >= 1 && (K) <= 256, "K must be <= 256 for uint8 encoding, got %u", (K));           \
+        VA_REQUIRE(ctx, (M) <= 65535, "at most 65535 subspaces, got %u", (M));                               \
     } while (0)
 
 extern "C" {
