@@ -1,0 +1,350 @@
+/*
+ * vectoraccelerate.hpp — header-only C++17 host mirror of the reference's Swift classes over the
+ * C ABI of libva_hip.so (va_hip.h).  Link with -lva_hip; no HIP headers are needed: device
+ * memory is allocated and copied through va_buffer_*.
+ *
+ * Mirrors (paths relative to the reference's Sources/VectorAccelerate/):
+ *   Context                    Metal4Context / GPUContext (Core/Metal4Context.swift:183-269)
+ *   DeviceBuffer<T>            BufferToken / getBuffer (Core/Metal4Context.swift:471-488)
+ *   VectorError                VectorError / IndexError (invalidInput, dimensionMismatch, ...)
+ *   FusedL2TopKKernel          Kernels/Metal4/FusedL2TopKKernel.swift (findNearestNeighbors, encode)
+ *   TopKSelectionKernel        Kernels/Metal4/TopKSelectionKernel.swift
+ *   ScalarQuantizationKernel   Kernels/Metal4/ScalarQuantizationKernel.swift (per-dimension int8)
+ *   BinaryQuantizationKernel   Kernels/Metal4/BinaryQuantizationKernel.swift + HammingDistanceKernel.swift
+ *   IVFIndex                   Index/Kernels/IVF/IVFSearchPipeline.swift + Index/Internal/IVFStructure.swift
+ *   KMeansPipeline             Index/Kernels/Clustering/KMeansPipeline.swift
+ *   ProductQuantizationKernel  Kernels/Metal4/ProductQuantizationKernel.swift
+ * Every call checks the status and throws VectorError with the library's message.
+ */
+#ifndef VECTORACCELERATE_HPP
+#define VECTORACCELERATE_HPP
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "va_hip.h"
+
+namespace vectoraccelerate {
+
+class VectorError : public std::runtime_error {
+   public:
+    VectorError(va_status st, const std::string& msg) : std::runtime_error(msg), status(st) {}
+    va_status status;
+    // VectorError / IndexError case of the status (invalidInput, dimensionMismatch, ...)
+    const char* kind() const {
+        switch (status) {
+            case VA_ERR_INVALID_ARG: return "invalidInput";
+            case VA_ERR_DIMENSION_MISMATCH: return "dimensionMismatch";
+            case VA_ERR_OOM: return "bufferAllocationFailed";
+            case VA_ERR_UNSUPPORTED: return "unsupported";
+            default: return "computeFailed";
+        }
+    }
+};
+
+class Context {
+   public:
+    explicit Context(int device = 0) {
+        va_status st = va_context_create(device, &h_);
+        if (st != VA_OK) throw VectorError(st, std::string("va_context_create: ") + va_status_string(st));
+    }
+    ~Context() {
+        if (h_) va_context_destroy(h_);
+    }
+    Context(const Context&) = delete;
+    Context& operator=(const Context&) = delete;
+    va_context* handle() const { return h_; }
+    void check(va_status st, const char* what) const {
+        if (st != VA_OK) throw VectorError(st, std::string(what) + ": " + va_last_error_message(h_));
+    }
+    // executeAndWait's wait
+    void synchronize() const { check(va_context_synchronize(h_), "va_context_synchronize"); }
+    void setOption(va_option o, uint64_t v) const { check(va_context_set_option(h_, o, v), "va_context_set_option"); }
+
+   private:
+    va_context* h_ = nullptr;
+};
+
+// Device array of n elements owned by a context.
+template <class T>
+class DeviceBuffer {
+   public:
+    DeviceBuffer() = default;
+    DeviceBuffer(const Context& ctx, size_t n) : ctx_(&ctx), n_(n) {
+        void* p = nullptr;
+        ctx.check(va_buffer_alloc(ctx.handle(), n * sizeof(T), &p), "va_buffer_alloc");
+        p_ = static_cast<T*>(p);
+    }
+    DeviceBuffer(const Context& ctx, const std::vector<T>& host) : DeviceBuffer(ctx, host.size()) { upload(host); }
+    ~DeviceBuffer() { release(); }
+    DeviceBuffer(DeviceBuffer&& o) noexcept { *this = std::move(o); }
+    DeviceBuffer& operator=(DeviceBuffer&& o) noexcept {
+        if (this != &o) {
+            release();
+            ctx_ = o.ctx_;
+            p_ = o.p_;
+            n_ = o.n_;
+            o.p_ = nullptr;
+            o.n_ = 0;
+        }
+        return *this;
+    }
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    T* data() const { return p_; }
+    size_t size() const { return n_; }
+    void upload(const std::vector<T>& host) {
+        if (host.size() != n_) throw VectorError(VA_ERR_INVALID_ARG, "upload: size mismatch");
+        ctx_->check(va_buffer_upload(ctx_->handle(), p_, host.data(), n_ * sizeof(T)), "va_buffer_upload");
+        ctx_->synchronize();
+    }
+    std::vector<T> download() const {
+        std::vector<T> host(n_);
+        ctx_->check(va_buffer_download(ctx_->handle(), host.data(), p_, n_ * sizeof(T)), "va_buffer_download");
+        ctx_->synchronize();
+        return host;
+    }
+
+   private:
+    void release() {
+        if (p_ && ctx_) va_buffer_free(ctx_->handle(), p_);
+        p_ = nullptr;
+    }
+    const Context* ctx_ = nullptr;
+    T* p_ = nullptr;
+    size_t n_ = 0;
+};
+
+// Row-major [rows x dim] host matrix.
+struct Matrix {
+    std::vector<float> data;
+    uint32_t rows = 0, dim = 0;
+};
+
+// Metal4FusedL2TopKResult / IVFSearchResult: idx[numQueries x k] (VA_SENTINEL_INDEX = empty).
+struct SearchResult {
+    std::vector<uint32_t> indices;
+    std::vector<float> distances;
+    uint32_t numQueries = 0, k = 0;
+    std::vector<std::pair<uint32_t, float>> results(uint32_t q) const {
+        std::vector<std::pair<uint32_t, float>> r;
+        for (uint32_t j = 0; j < k; ++j)
+            if (indices[size_t(q) * k + j] != VA_SENTINEL_INDEX)
+                r.emplace_back(indices[size_t(q) * k + j], distances[size_t(q) * k + j]);
+        return r;
+    }
+};
+
+class FusedL2TopKKernel {
+   public:
+    explicit FusedL2TopKKernel(const Context& c) : ctx_(c) {}
+    // encode tier: device inputs and outputs
+    void encode(va_metric metric, const float* q, const float* x, uint32_t Q, uint32_t N, uint32_t D, uint32_t k,
+                uint32_t* idx, float* dist) const {
+        ctx_.check(va_fused_topk(ctx_.handle(), metric, q, x, Q, N, D, k, idx, dist), "va_fused_topk");
+    }
+    SearchResult findNearestNeighbors(const Matrix& queries, const Matrix& dataset, uint32_t k,
+                                      va_metric metric = VA_METRIC_L2SQ) const {
+        if (queries.dim != dataset.dim) throw VectorError(VA_ERR_DIMENSION_MISMATCH, "query / dataset dimension");
+        DeviceBuffer<float> q(ctx_, queries.data), x(ctx_, dataset.data);
+        DeviceBuffer<uint32_t> idx(ctx_, size_t(queries.rows) * k);
+        DeviceBuffer<float> dist(ctx_, size_t(queries.rows) * k);
+        encode(metric, q.data(), x.data(), queries.rows, dataset.rows, dataset.dim, k, idx.data(), dist.data());
+        return SearchResult{idx.download(), dist.download(), queries.rows, k};
+    }
+
+   private:
+    const Context& ctx_;
+};
+
+class TopKSelectionKernel {
+   public:
+    explicit TopKSelectionKernel(const Context& c) : ctx_(c) {}
+    SearchResult select(const std::vector<float>& values, uint32_t rows, uint32_t n, uint32_t k,
+                        va_select_mode mode = VA_SELECT_MIN) const {
+        DeviceBuffer<float> v(ctx_, values);
+        DeviceBuffer<uint32_t> idx(ctx_, size_t(rows) * k);
+        DeviceBuffer<float> out(ctx_, size_t(rows) * k);
+        ctx_.check(va_topk_select(ctx_.handle(), v.data(), rows, n, k, mode, idx.data(), out.data()), "va_topk_select");
+        return SearchResult{idx.download(), out.download(), rows, k};
+    }
+
+   private:
+    const Context& ctx_;
+};
+
+// Per-dimension int8 scalar quantization and the int8 dot-product top-k scan.
+class ScalarQuantizationKernel {
+   public:
+    explicit ScalarQuantizationKernel(const Context& c) : ctx_(c) {}
+    struct Params {
+        DeviceBuffer<float> min, max, scale;
+        DeviceBuffer<int32_t> zeroPoint;
+    };
+    Params computeParameters(const DeviceBuffer<float>& x, uint32_t N, uint32_t D) const {
+        Params p{DeviceBuffer<float>(ctx_, D), DeviceBuffer<float>(ctx_, D), DeviceBuffer<float>(ctx_, D),
+                 DeviceBuffer<int32_t>(ctx_, D)};
+        ctx_.check(va_sq_params_per_dim(ctx_.handle(), x.data(), N, D, p.min.data(), p.max.data(), p.scale.data(),
+                                        p.zeroPoint.data()),
+                   "va_sq_params_per_dim");
+        return p;
+    }
+    DeviceBuffer<int8_t> quantize(const DeviceBuffer<float>& x, uint64_t N, uint32_t D, const Params& p) const {
+        DeviceBuffer<int8_t> codes(ctx_, size_t(N) * D);
+        ctx_.check(va_sq_quantize_i8(ctx_.handle(), x.data(), N, D, p.scale.data(), p.zeroPoint.data(), codes.data()),
+                   "va_sq_quantize_i8");
+        return codes;
+    }
+    // top-k by largest int8 dot product: (ids, dots)
+    std::pair<std::vector<uint32_t>, std::vector<int32_t>> scan(const DeviceBuffer<int8_t>& q, const DeviceBuffer<int8_t>& x,
+                                                                uint32_t Q, uint32_t N, uint32_t D, uint32_t k) const {
+        DeviceBuffer<uint32_t> idx(ctx_, size_t(Q) * k);
+        DeviceBuffer<int32_t> dot(ctx_, size_t(Q) * k);
+        ctx_.check(va_i8_scan_topk(ctx_.handle(), q.data(), x.data(), Q, N, D, k, idx.data(), dot.data()),
+                   "va_i8_scan_topk");
+        return {idx.download(), dot.download()};
+    }
+
+   private:
+    const Context& ctx_;
+};
+
+// Binary codes (bit d = x_d > 0, LSB first) and the Hamming top-k.
+class BinaryQuantizationKernel {
+   public:
+    explicit BinaryQuantizationKernel(const Context& c) : ctx_(c) {}
+    static uint32_t words(uint32_t D) { return (D + 31) / 32; }
+    DeviceBuffer<uint32_t> quantize(const DeviceBuffer<float>& x, uint32_t N, uint32_t D) const {
+        DeviceBuffer<uint32_t> codes(ctx_, size_t(N) * words(D));
+        ctx_.check(va_bq_pack(ctx_.handle(), x.data(), N, D, codes.data()), "va_bq_pack");
+        return codes;
+    }
+    std::pair<std::vector<uint32_t>, std::vector<uint32_t>> hammingTopK(const DeviceBuffer<uint32_t>& q,
+                                                                      const DeviceBuffer<uint32_t>& x, uint32_t Q,
+                                                                      uint32_t N, uint32_t W, uint32_t k) const {
+        DeviceBuffer<uint32_t> idx(ctx_, size_t(Q) * k), dist(ctx_, size_t(Q) * k);
+        ctx_.check(va_hamming_topk(ctx_.handle(), q.data(), x.data(), Q, N, W, k, idx.data(), dist.data()),
+                   "va_hamming_topk");
+        return {idx.download(), dist.download()};
+    }
+
+   private:
+    const Context& ctx_;
+};
+
+// IVF-Flat (L2^2): build from centroids, add rows, probe + list scan.
+class IVFIndex {
+   public:
+    IVFIndex(const Context& c, const DeviceBuffer<float>& centroids, uint32_t C, const DeviceBuffer<float>& x, uint32_t N,
+             uint32_t D, uint32_t nprobe)
+        : ctx_(c), D_(D), N_(N), nprobe_(nprobe) {
+        ctx_.check(va_ivf_build(c.handle(), centroids.data(), C, x.data(), N, D, &h_), "va_ivf_build");
+    }
+    ~IVFIndex() {
+        if (h_) va_ivf_destroy(h_);
+    }
+    IVFIndex(const IVFIndex&) = delete;
+    IVFIndex& operator=(const IVFIndex&) = delete;
+    void add(const DeviceBuffer<float>& x, uint32_t n) {
+        ctx_.check(va_ivf_add(ctx_.handle(), h_, x.data(), n, D_, N_), "va_ivf_add");
+        N_ += n;
+    }
+    SearchResult search(const DeviceBuffer<float>& q, uint32_t Q, uint32_t k) const {
+        DeviceBuffer<uint32_t> idx(ctx_, size_t(Q) * k);
+        DeviceBuffer<float> dist(ctx_, size_t(Q) * k);
+        ctx_.check(va_ivf_search(ctx_.handle(), h_, q.data(), Q, nprobe_, k, idx.data(), dist.data()), "va_ivf_search");
+        return SearchResult{idx.download(), dist.download(), Q, k};
+    }
+    uint32_t count() const { return N_; }
+
+   private:
+    const Context& ctx_;
+    va_ivf* h_ = nullptr;
+    uint32_t D_, N_, nprobe_;
+};
+
+// Lloyd k-means (KMeansConfiguration defaults: 100 iterations, threshold 1e-4).
+class KMeansPipeline {
+   public:
+    struct Result {
+        std::vector<float> centroids;
+        std::vector<uint32_t> assignments, clusterCounts;
+        va_kmeans_info info{};
+    };
+    KMeansPipeline(const Context& c, uint32_t numClusters, uint32_t maxIterations = 100,
+                   float convergenceThreshold = 1e-4f, uint64_t seed = 0x5EED)
+        : ctx_(c), C_(numClusters), iters_(maxIterations), thr_(convergenceThreshold), seed_(seed) {}
+    // initialCentroids empty: k-means++ seeding
+    Result fit(const DeviceBuffer<float>& x, uint32_t N, uint32_t D, const std::vector<float>& initialCentroids = {}) const {
+        DeviceBuffer<float> init(ctx_, size_t(C_) * D);
+        if (initialCentroids.empty())
+            ctx_.check(va_kmeans_plusplus(ctx_.handle(), x.data(), N, D, C_, seed_, init.data(), nullptr),
+                       "va_kmeans_plusplus");
+        else
+            init.upload(initialCentroids);
+        DeviceBuffer<float> cen(ctx_, size_t(C_) * D);
+        DeviceBuffer<uint32_t> assign(ctx_, N), counts(ctx_, C_);
+        Result r;
+        ctx_.check(va_kmeans_fit(ctx_.handle(), x.data(), N, D, C_, init.data(), iters_, thr_, cen.data(), assign.data(),
+                                 nullptr, counts.data(), &r.info),
+                   "va_kmeans_fit");
+        r.centroids = cen.download();
+        r.assignments = assign.download();
+        r.clusterCounts = counts.download();
+        return r;
+    }
+
+   private:
+    const Context& ctx_;
+    uint32_t C_, iters_;
+    float thr_;
+    uint64_t seed_;
+};
+
+// Product quantization (Metal4PQConfig defaults: M 8, K 256, 25 iterations, threshold 0.001).
+class ProductQuantizationKernel {
+   public:
+    struct Config {
+        uint32_t dimension, M = 8, K = 256, trainIterations = 25;
+        float convergenceThreshold = 0.001f;
+    };
+    ProductQuantizationKernel(const Context& c, Config cfg) : ctx_(c), cfg_(cfg) {
+        if (cfg.M == 0 || cfg.dimension % cfg.M != 0)
+            throw VectorError(VA_ERR_INVALID_ARG, "Dimension must be divisible by M");
+        if (cfg.K == 0 || cfg.K > 256) throw VectorError(VA_ERR_INVALID_ARG, "K must be <= 256 for uint8 encoding");
+    }
+    DeviceBuffer<float> train(const DeviceBuffer<float>& x, uint32_t N, uint64_t seed = 0x5EED) const {
+        DeviceBuffer<float> cb(ctx_, size_t(cfg_.M) * cfg_.K * (cfg_.dimension / cfg_.M));
+        uint32_t it = 0;
+        ctx_.check(va_pq_train(ctx_.handle(), x.data(), N, cfg_.dimension, cfg_.M, cfg_.K, cfg_.trainIterations,
+                               cfg_.convergenceThreshold, seed, nullptr, cb.data(), &it),
+                   "va_pq_train");
+        return cb;
+    }
+    DeviceBuffer<uint8_t> encode(const DeviceBuffer<float>& x, uint32_t N, const DeviceBuffer<float>& cb) const {
+        DeviceBuffer<uint8_t> codes(ctx_, size_t(N) * cfg_.M);
+        ctx_.check(va_pq_encode(ctx_.handle(), x.data(), N, cfg_.dimension, cfg_.M, cfg_.K, cb.data(), codes.data()),
+                   "va_pq_encode");
+        return codes;
+    }
+    SearchResult search(const DeviceBuffer<float>& q, uint32_t Q, const DeviceBuffer<float>& cb,
+                        const DeviceBuffer<uint8_t>& codes, uint32_t N, uint32_t k) const {
+        DeviceBuffer<uint32_t> idx(ctx_, size_t(Q) * k);
+        DeviceBuffer<float> dist(ctx_, size_t(Q) * k);
+        ctx_.check(va_pq_search(ctx_.handle(), q.data(), Q, cfg_.dimension, cfg_.M, cfg_.K, cb.data(), codes.data(), N,
+                                k, idx.data(), dist.data()),
+                   "va_pq_search");
+        return SearchResult{idx.download(), dist.download(), Q, k};
+    }
+
+   private:
+    const Context& ctx_;
+    Config cfg_;
+};
+
+}  // namespace vectoraccelerate
+
+#endif /* VECTORACCELERATE_HPP */

@@ -68,3 +68,16 @@ def build(jobs: int | None = None) -> Path:
 
 if __name__ == "__main__":
     print(build())
+
+
+def build_cpp_example() -> Path:
+    """Compile tests/cpp/example.cpp (the C++ host mirror's check program) against libva_hip.so."""
+    root = PKG.parent
+    src = root / "tests" / "cpp" / "example.cpp"
+    out = root / "tests" / "cpp" / "va_example"
+    cmd = ["g++", "-std=c++17", "-O2", "-Wall", "-Wextra", f"-I{root / 'include'}", str(src), f"-L{PKG}", "-lva_hip",
+           "-Wl,-rpath,$ORIGIN/../../vectoraccelerate_amd", "-Wl,-rpath-link,/opt/rocm/lib", "-o", str(out)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"g++ failed for {src.name}:\n{proc.stdout}\n{proc.stderr}")
+    return out
