@@ -121,12 +121,14 @@ __device__ __forceinline__ void hist_add(uint32_t* hist, bool m, uint32_t d) {
     }
 }
 
-template <bool CACHED>
+// KTH: threshold mode only (a.out_kth set): no winners buffer, so a cached row of up to
+// 16K keys leaves room for two workgroups per CU.
+template <bool CACHED, bool KTH = false>
 __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelectArgs a) {
     __shared__ uint32_t hist[256];
     __shared__ uint32_t s_digit, s_before, s_bin, s_cnt;
-    __shared__ uint32_t okey[SEL_BUF];
-    __shared__ uint32_t oid[SEL_BUF];
+    __shared__ uint32_t okey[KTH ? 1 : SEL_BUF];
+    __shared__ uint32_t oid[KTH ? 1 : SEL_BUF];
     __shared__ uint32_t whist[2048];     // one-pass histogram of keys below 2^11
     extern __shared__ uint32_t s_row[];  // CACHED: the row's keys
 
@@ -212,7 +214,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelectArgs a) {
             __syncthreads();
         }
         T = prefix;
-        if (a.out_kth) {
+        if (KTH || a.out_kth) {
             if (tid == 0) a.out_kth[orow] = T;
             return;
         }
@@ -244,6 +246,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelectArgs a) {
     }
 
     // ---- phase 3: gather the winners and sort them by (key, id) -----------------------
+    if constexpr (KTH) return;  // threshold launches always have out_kth (returned above)
     if (tid == 0) s_cnt = 0;
     __syncthreads();
     for (uint32_t i = tid; i < n; i += SEL_THREADS) {
@@ -338,10 +341,11 @@ va_status launch_select(va_context* ctx, const SelectArgs& a) {
     if (a.k > SEL_BUF) return fail(ctx, VA_ERR_INVALID_ARG, "k=%u exceeds the maximum %u", a.k, SEL_BUF);
     if (a.n <= kSelCache) {
         const size_t lds = size_t(std::max<uint32_t>(a.n, 1)) * 4;
+        auto kern = a.out_kth ? &select_kernel<true, true> : &select_kernel<true, false>;
         if (lds > 48 * 1024)
-            VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(&select_kernel<true>),
+            VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                   hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
-        select_kernel<true><<<dim3(a.rows), dim3(SEL_THREADS), lds, ctx->stream>>>(a);
+        kern<<<dim3(a.rows), dim3(SEL_THREADS), lds, ctx->stream>>>(a);
     } else {
         select_kernel<false><<<dim3(a.rows), dim3(SEL_THREADS), 0, ctx->stream>>>(a);
     }
