@@ -553,12 +553,16 @@ va_status va_ivf_add(va_context* ctx, va_ivf* ivf, const float* x, uint32_t num_
     std::vector<uint32_t> h(C + 1);
     VA_CHECK_HIP(ctx, hipMemcpyAsync(h.data(), offs, size_t(C + 1) * 4, hipMemcpyDeviceToHost, ctx->stream));
     VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    std::swap(ivf->list_vectors, reinterpret_cast<float*&>(b.p[4]));
-    std::swap(ivf->ids, reinterpret_cast<uint32_t*&>(b.p[5]));
-    std::swap(ivf->offsets, reinterpret_cast<uint32_t*&>(b.p[6]));
+    // the new arrays replace the index's; the old ones are freed with the scratch
+    b.p[4] = ivf->list_vectors;
+    b.p[5] = ivf->ids;
+    b.p[6] = ivf->offsets;
+    ivf->list_vectors = vecs;
+    ivf->ids = ids;
+    ivf->offsets = offs;
     ivf->h_offsets = std::move(h);
     ivf->N = Nn;
-    return VA_OK;  // the old arrays are freed with the scratch
+    return VA_OK;
 }
 
 va_status va_ivf_destroy(va_ivf* ivf) {
