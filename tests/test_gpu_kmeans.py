@@ -176,3 +176,20 @@ def test_index_train_without_centroids(ctx, oracle):
     np.testing.assert_array_equal(ids, oids)
     res = idx.search(queries=centers, k=5)
     assert all(len(r.results) == 5 for r in res)
+
+
+def test_kmeans_tiny_and_ivf_add_nothing(ctx, oracle):
+    """One point and one cluster; a zero-row add leaves the lists unchanged."""
+    from vectoraccelerate_amd import IVFSearchConfiguration, IVFSearchPipeline
+
+    x = np.array([[1.5, -2.0, 3.0]], np.float32)
+    _compare(ctx, oracle, x, x.copy(), 3, 1e-4)
+    xb, lab, centers = _blobs(4, 8, 20, seed=5)
+    pipe = IVFSearchPipeline(ctx, IVFSearchConfiguration(4, 2, 8))
+    st = pipe.prepareIndexStructure(centers, xb)
+    before = st.lists()
+    st.add(ctx.buffer(xb)[:0], xb.shape[0])
+    after = st.lists()
+    np.testing.assert_array_equal(before[0], after[0])
+    np.testing.assert_array_equal(before[1], after[1])
+    st.close()

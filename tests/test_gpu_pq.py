@@ -109,3 +109,32 @@ def test_pq_seeded_training_and_errors(ctx, oracle):
         Metal4PQConfig(64, 8, 300)
     with pytest.raises(VectorError):
         pq.encode(_data(10, 32, 1), model)
+
+
+def test_pq_edge_cases(ctx, oracle):
+    """k above N (sentinel slots), one row, one query, and a code array whose rows are not
+    16-byte aligned (the runtime-M kernel instead of the specialised one)."""
+    from vectoraccelerate_amd import Metal4EncodedVectors, Metal4PQConfig, Metal4PQModel, ProductQuantizationKernel
+
+    D, M, K = 32, 8, 256
+    x = _data(300, D, 41)
+    cb = _init(x, M, K, 42)
+    cfg = Metal4PQConfig(D, M, K)
+    pq = ProductQuantizationKernel(ctx)
+    model = Metal4PQModel(ctx.buffer(cb), cfg)
+    enc = pq.encode(x, model)
+    codes = enc.codes.cpu().numpy()
+    q = _data(3, D, 43)
+    for n, k in ((300, 400), (1, 5), (300, 1)):
+        e = Metal4EncodedVectors(enc.codes[:n], n, cfg)
+        idx, dist = pq.search(q[:1] if n == 1 else q, e, model, k)
+        oi, od = oracle.pq_search(q[:1] if n == 1 else q, cb, codes[:n], M, K, k)
+        np.testing.assert_array_equal(idx.cpu().numpy().view(np.uint32), oi)
+        np.testing.assert_array_equal(dist.cpu().numpy(), od)
+    # rows start 8 bytes into a 16-byte block: the generic kernel
+    e = Metal4EncodedVectors(enc.codes[1:], 299, cfg)
+    assert e.codes.data_ptr() % 16 == 8
+    idx, dist = pq.search(q, e, model, 10)
+    oi, od = oracle.pq_search(q, cb, codes[1:], M, K, 10)
+    np.testing.assert_array_equal(idx.cpu().numpy().view(np.uint32), oi)
+    np.testing.assert_array_equal(dist.cpu().numpy(), od)
