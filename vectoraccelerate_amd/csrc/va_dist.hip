@@ -67,7 +67,10 @@ struct Tile {
     static constexpr int CHUNKS = ROWS * (KC / 4);
     static constexpr int CPT = (CHUNKS + NT - 1) / NT;
     static constexpr int STAGE = ROWS * LDS_STRIDE;
-    static constexpr size_t LDS_BYTES = size_t(2 * STAGE + NW * 128) * sizeof(float);
+    // register-staged loads: a one-wave tile keeps one LDS stage (the next stage waits in
+    // registers), 44 KB instead of 87 KB, so three workgroups share a CU instead of one
+    static constexpr int NSTAGE = NW == 1 ? 1 : 2;
+    static constexpr size_t LDS_BYTES = size_t(NSTAGE * STAGE + NW * 128) * sizeof(float);
     // direct-to-LDS loads: 16-row groups of 1 KiB (one wave-wide load each), the same number
     // per wave (the last few may be padding), two ring slots
     static constexpr int GROUPS = ROWS / 16;
@@ -107,7 +110,7 @@ __global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) 
     using T = Tile<WQ, WN>;
     static_assert(!DMA || (VEC && LDS_STRIDE == KC), "direct loads need 16-byte rows and unpadded LDS rows");
     extern __shared__ float lds[];
-    float* nrm = lds + (DMA ? VA_DIST_DMA_SLOTS * T::DSTAGE : 2 * T::STAGE);  // [waves][128] squared norms of the wave's rows
+    float* nrm = lds + (DMA ? VA_DIST_DMA_SLOTS * T::DSTAGE : T::NSTAGE * T::STAGE);  // [waves][128] squared norms of the wave's rows
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -310,8 +313,14 @@ __global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) 
         for (int s = 0; s < nstages; ++s) {
             const bool more = (s + 1) < nstages;
             if (more) load(uint32_t(s + 1) * KC);
-            compute(lds + (s & 1) * T::STAGE);
-            if (more) store(lds + ((s + 1) & 1) * T::STAGE);
+            if constexpr (T::NSTAGE == 1) {
+                compute(lds);
+                __syncthreads();  // every read of the stage is done before it is overwritten
+                if (more) store(lds);
+            } else {
+                compute(lds + (s & 1) * T::STAGE);
+                if (more) store(lds + ((s + 1) & 1) * T::STAGE);
+            }
             __syncthreads();
         }
     }
