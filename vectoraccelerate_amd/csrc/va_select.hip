@@ -339,7 +339,13 @@ __global__ void merge_gather(const uint32_t* ai, const float* ad, const uint32_t
 va_status launch_select(va_context* ctx, const SelectArgs& a) {
     if (a.rows == 0) return VA_OK;
     if (a.k > SEL_BUF) return fail(ctx, VA_ERR_INVALID_ARG, "k=%u exceeds the maximum %u", a.k, SEL_BUF);
-    if (a.n <= kSelCache) {
+    // Candidate lists are mostly far below their capacity, which sizes the LDS copy: past 8K
+    // entries a large copy would leave one workgroup per CU, so such rows are read from memory
+    // (L2-resident lists) by many workgroups at once instead.
+    const bool cache = a.n <= kSelCache && !(a.counts && a.n > 8192);
+    if (!cache && a.out_kth) {
+        select_kernel<false, true><<<dim3(a.rows), dim3(SEL_THREADS), 0, ctx->stream>>>(a);
+    } else if (cache) {
         const size_t lds = size_t(std::max<uint32_t>(a.n, 1)) * 4;
         auto kern = a.out_kth ? &select_kernel<true, true> : &select_kernel<true, false>;
         if (lds > 48 * 1024)
