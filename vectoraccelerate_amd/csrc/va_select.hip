@@ -342,7 +342,7 @@ va_status launch_select(va_context* ctx, const SelectArgs& a) {
     // Candidate lists are mostly far below their capacity, which sizes the LDS copy: past 8K
     // entries a large copy would leave one workgroup per CU, so such rows are read from memory
     // (L2-resident lists) by many workgroups at once instead.
-    const bool cache = a.n <= kSelCache && !(a.counts && a.n > 8192);
+    const bool cache = a.n <= kSelCache && !((a.counts || a.out_kth) && a.n > 8192);
     if (!cache && a.out_kth) {
         select_kernel<false, true><<<dim3(a.rows), dim3(SEL_THREADS), 0, ctx->stream>>>(a);
     } else if (cache) {
