@@ -172,6 +172,20 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelectArgs a) {
         __syncthreads();
     }
     const uint32_t K = a.k < n ? a.k : n;
+    // f(key) over the row; rows read from memory load eight keys per thread before using them,
+    // so a long row's pass is not one load latency per key
+    auto for_keys = [&](auto&& f) {
+        uint32_t i = uint32_t(tid);
+        if (!CACHED)
+            for (; i + 7u * SEL_THREADS < n; i += 8u * SEL_THREADS) {
+                uint32_t v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = rv.key(i + uint32_t(j) * SEL_THREADS);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) f(v[j]);
+            }
+        for (; i < n; i += SEL_THREADS) f(rv.key(i));
+    };
 
     uint32_t T = 0xFFFFFFFFu, Tid = 0xFFFFFFFFu;
     bool take_all = (n <= a.k);
@@ -186,7 +200,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelectArgs a) {
             for (uint32_t b = tid; b < nb; b += SEL_THREADS) whist[b] = 0;
             __syncthreads();
             // (a sentinel key, above every real one, lands in the top bin)
-            for (uint32_t i = tid; i < n; i += SEL_THREADS) hist_add(whist, true, min(rv.key(i), nb - 1u));
+            for_keys([&](uint32_t k) { hist_add(whist, true, min(k, nb - 1u)); });
             __syncthreads();
             find_bin_wide(whist, nb, need, &s_digit, &s_before, &s_bin);
             __syncthreads();
@@ -200,10 +214,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelectArgs a) {
         for (int shift = top; shift >= 0; shift -= 8) {
             hist[tid] = 0;
             __syncthreads();
-            for (uint32_t i = tid; i < n; i += SEL_THREADS) {
-                const uint32_t k = rv.key(i);
-                hist_add(hist, (k & mask) == prefix, (k >> shift) & 255u);
-            }
+            for_keys([&](uint32_t k) { hist_add(hist, (k & mask) == prefix, (k >> shift) & 255u); });
             __syncthreads();
             find_digit(hist, need, &s_digit, &s_before, &s_bin);
             __syncthreads();
