@@ -311,10 +311,12 @@ __global__ __launch_bounds__(256) void pq_adc_fast(AdcArgs a) {
         for (uint32_t e = threadIdx.x; e < uint32_t(MK); e += 256) tab[i * MK + e] = i < nqg ? src[e] : 0.0f;
     }
     __syncthreads();
-    for (uint32_t j = blockIdx.x * 256 + threadIdx.x; j < a.cols; j += gridDim.x * 256) {
+    // the next row's codes are loaded while the current row's lookups run (two workgroups per CU
+    // leave too few waves to hide a load per row otherwise)
+    constexpr int NW4 = M / 4;
+    auto load_codes = [&](uint32_t j, uint32_t (&w)[NW4]) {
         const uint32_t row = a.c0 + j * a.stride;
         const uint4* cr = reinterpret_cast<const uint4*>(a.codes + int64_t(row) * M);
-        uint32_t w[M / 4];
         if constexpr (M == 8) {
             const uint2 v = *reinterpret_cast<const uint2*>(cr);
             w[0] = v.x;
@@ -329,6 +331,17 @@ __global__ __launch_bounds__(256) void pq_adc_fast(AdcArgs a) {
                 w[4 * b + 3] = v.w;
             }
         }
+    };
+    const uint32_t step = gridDim.x * 256;
+    uint32_t wn[NW4];
+    uint32_t j = blockIdx.x * 256 + threadIdx.x;
+    if (j < a.cols) load_codes(j, wn);
+    for (; j < a.cols; j = uint64_t(j) + step < a.cols ? j + step : a.cols) {
+        const uint32_t row = a.c0 + j * a.stride;
+        uint32_t w[NW4];
+#pragma unroll
+        for (int b = 0; b < NW4; ++b) w[b] = wn[b];
+        if (uint64_t(j) + step < a.cols) load_codes(j + step, wn);
         uint32_t off[M];
 #pragma unroll
         for (int m = 0; m < M; ++m) off[m] = (w[m / 4] >> (8 * (m % 4))) & 0xFFu;
