@@ -613,19 +613,28 @@ __global__ __launch_bounds__(256, 2) void i8_dma_kernel(I8Args a) {
             }
         }
     } else {
+        // Dense keys leave through LDS: each wave writes a 32-query x 64-row block of keys (rows
+        // padded to 65 words, conflict-free both ways), then stores it row by row with the 64
+        // lanes on consecutive rows of the output, 256 contiguous bytes per store instead of
+        // 64 scattered words.
+        __syncthreads();  // every wave is past its last read of the ring
+        uint32_t* tile = reinterpret_cast<uint32_t*>(lds8) + wave * (32 * 65);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const uint32_t qi = q0 + uint32_t(wq * 128 + u * 32 + l32);
-            if (qi >= a.Q) continue;
 #pragma unroll
             for (int b = 0; b < 2; ++b)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint32_t m = nbase + uint32_t(b * 32 + 8 * j + 4 * hh);
+                for (int j = 0; j < 4; ++j)
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        if (m + e < a.N) a.out_k[int64_t(qi) * a.ldo + m + e] = key_of_i32(-acc[u][b][4 * j + e]);
-                }
+                        tile[l32 * 65 + b * 32 + 8 * j + 4 * hh + e] = key_of_i32(-acc[u][b][4 * j + e]);
+            __syncthreads();
+            const uint32_t m = nbase + uint32_t(lane);
+            for (int q = 0; q < 32; ++q) {
+                const uint32_t qi = q0 + uint32_t(wq * 128 + u * 32 + q);
+                if (qi < a.Q && m < a.N) a.out_k[int64_t(qi) * a.ldo + m] = tile[q * 65 + lane];
+            }
+            __syncthreads();  // the block is read before the next one overwrites it
         }
     }
 }
