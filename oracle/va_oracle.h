@@ -76,7 +76,8 @@ void vo_topk_merge(const uint32_t* a_idx, const float* a_d, const uint32_t* b_id
  *   mn/mx = per-dimension min/max; scale = max((mx-mn)/255, 1e-8)
  *   (ScalarQuantizationKernel.swift:496-520, asymmetric branch);
  *   zp = -128 - round_half_away(mn/scale) as int32, so that codes span [-128, 127]
- *   (the reference's Int8(clamping:) zero point saturates). */
+ *   (the reference's Int8(clamping:) zero point saturates: with a range of 255 steps an Int8
+ *   zero point cannot place min at -128 for every data range). */
 void vo_sq_params_per_dim(const float* x, int64_t N, int64_t D, float* mn, float* mx, float* scale, int32_t* zp);
 /* q = clamp(rint(x/scale + zp), -128, 127); |scale| < 1e-9 -> clamp(zp)
  * (quantize_int8_kernel, DataTransformations.metal:174-201), per dimension d = i % D. */

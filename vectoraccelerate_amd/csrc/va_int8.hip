@@ -967,7 +967,8 @@ va_status launch_i8(va_context* ctx, const I8Args& a, bool filter) {
     if (a.Q <= 64) return launch_i8_shape<1, 2, 2>(ctx, a, vec, filter);
 // Large-Q shape: 0 = 128 x 128 (4 waves), 1 = 128 x 256 (4 waves), 2 = 256 x 256 (8 waves).
 // Measured on configs[2] (10M x 512, Q=4096): 0 is fastest with 64-byte register-staged
-// stages (each stage's MFMA work is shorter than its load round trip).
+// stages (each stage's MFMA work is shorter than its load round trip, so a bigger tile only
+// waits longer per stage).
 #ifndef VA_I8_LARGE_SHAPE
 #define VA_I8_LARGE_SHAPE 0
 #endif
