@@ -193,3 +193,18 @@ def test_kmeans_tiny_and_ivf_add_nothing(ctx, oracle):
     np.testing.assert_array_equal(before[0], after[0])
     np.testing.assert_array_equal(before[1], after[1])
     st.close()
+
+
+def test_kmeans_zipf_sized_clusters(ctx, oracle):
+    """configs[4]-like cluster sizes (Zipf 1.1) at 120,000 points: the largest clusters span
+    hundreds of 256-point chunks; centroids must still equal the oracle's bit for bit."""
+    r = np.random.default_rng(17)
+    C_, D, N = 128, 48, 120_000
+    centers = (r.standard_normal((C_, D)) * 10).astype(np.float32)
+    p = 1.0 / np.arange(1, C_ + 1) ** 1.1
+    lab = r.choice(C_, N, p=p / p.sum())
+    x = (centers[lab] + 0.05 * r.standard_normal((N, D))).astype(np.float32)
+    init = (centers + 0.3 * r.standard_normal(centers.shape)).astype(np.float32)
+    res = _compare(ctx, oracle, x, init, 4, 1e-4)
+    counts = res.clusterCounts.cpu().numpy().view(np.uint32)
+    assert counts.max() > 100 * 256
