@@ -138,3 +138,18 @@ def test_pq_edge_cases(ctx, oracle):
     oi, od = oracle.pq_search(q, cb, codes[1:], M, K, 10)
     np.testing.assert_array_equal(idx.cpu().numpy().view(np.uint32), oi)
     np.testing.assert_array_equal(dist.cpu().numpy(), od)
+
+
+def test_pq_train_multi_chunk(ctx, oracle):
+    """200,000 training rows over 16 centroids per subspace: each centroid's mean sums dozens
+    of 256-row chunks; codebooks must equal the oracle's bit for bit."""
+    from vectoraccelerate_amd import Metal4PQConfig, ProductQuantizationKernel
+
+    N, D, M, K = 200_000, 32, 4, 16
+    x = _data(N, D, 51)
+    init = _init(x, M, K, 52)
+    cfg = Metal4PQConfig(D, M, K, trainIterations=3, convergenceThreshold=0.0)
+    model = ProductQuantizationKernel(ctx).train(x, cfg, initialCodebooks=init)
+    ocb, oit = oracle.pq_train(x, init, M, K, 3, 0.0)
+    assert model.iterations == oit == 3
+    np.testing.assert_array_equal(model.codebooks.cpu().numpy(), ocb)
