@@ -492,22 +492,31 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
         // dense fp16 dots (the bounds are computed by screen_bound_kernel) and the row norms
         if (qb == 0 && wave == 0)
             for (uint32_t r = uint32_t(lane); r < rc; r += 64) a.out_xx[rs + r] = xxs[r];
+        // Each query block leaves through the wave's free LDS slot (32 queries x 128 rows, rows
+        // padded to 129 words) and is stored one output row at a time with the lanes on
+        // consecutive database rows: 256-byte stores instead of scattered words.
+        float* stg = reinterpret_cast<float*>(wave == 0 ? qslot0 : wave == 1 ? qslot1 : wave == 2 ? xslot0 : xslot1);
+        static_assert(XBYTES >= 32 * 129 * 4 && QBYTES >= 32 * 129 * 4, "key staging: 16.5 KiB per wave");
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
-            const uint32_t ql = uint32_t(wq * 128 + 32 * n + l32);
-            if (ql >= qc) continue;
-            const uint32_t qi = qs + ql;
             const float inv = qinf[n].z;
-            float* o = a.out_dot + int64_t(qi) * a.ldo + rs;
 #pragma unroll
             for (int m = 0; m < 4; ++m)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int r = wn * 128 + 32 * m + 8 * j + 4 * hh;
+                for (int j = 0; j < 4; ++j)
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        if (uint32_t(r + e) < rc) o[r + e] = acc[m][n][4 * j + e] * inv;
-                }
+                        stg[l32 * 129 + 32 * m + 8 * j + 4 * hh + e] = acc[m][n][4 * j + e] * inv;
+            __syncthreads();
+            const uint32_t r0 = uint32_t(wn * 128 + lane);
+            for (int q = 0; q < 32; ++q) {
+                const uint32_t ql = uint32_t(wq * 128 + 32 * n + q);
+                if (ql >= qc) break;
+                float* o = a.out_dot + int64_t(qs + ql) * a.ldo + rs;
+                if (r0 < rc) o[r0] = stg[q * 129 + lane];
+                if (r0 + 64 < rc) o[r0 + 64] = stg[q * 129 + 64 + lane];
+            }
+            __syncthreads();  // the block is stored before the next one overwrites it
         }
         return;
     } else {
