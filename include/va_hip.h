@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define VA_HIP_ABI_VERSION 2
+#define VA_HIP_ABI_VERSION 3
 #define VA_SENTINEL_INDEX 0xFFFFFFFFu
 /* largest k accepted by the top-K entry points */
 #define VA_MAX_K 1024u
@@ -160,6 +160,20 @@ va_status va_fused_topk(va_context* ctx, va_metric metric, const float* queries,
 va_status va_fused_topk_streamed(va_context* ctx, va_metric metric, const float* queries, const float* host_database,
                                  uint32_t num_queries, uint32_t num_database, uint32_t dim, uint32_t k,
                                  uint32_t chunk_rows, uint32_t* out_idx, float* out_dist);
+/* Size of the fixed device scratch block of va_fused_topk_noalloc (one block per GPU). */
+#define VA_NOALLOC_SCRATCH_BYTES (64u << 20)
+/* va_fused_topk without device allocation.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, results and synchronisation as
+ * va_fused_topk, but every scratch buffer comes from a fixed block of VA_NOALLOC_SCRATCH_BYTES
+ * that each GPU holds until the process ends (about 128 queries x 1M rows at k = 100 fit).
+ * A search that needs more fails with VA_ERR_INVALID_ARG before any work is enqueued, and the
+ * message gives the size it needs.  Every call on one GPU shares that GPU's block and leaves its
+ * contents behind (each call clears what it needs cleared): calls that overlap on one GPU, from
+ * different contexts or streams, race. */
+va_status va_fused_topk_noalloc(va_context* ctx, va_metric metric, const float* queries, const float* database,
+                                uint32_t num_queries, uint32_t num_database, uint32_t dim, uint32_t k,
+                                uint32_t* out_idx, float* out_dist);
 /* Row-wise top-k of a value matrix values[Q x N] (sorted output).
  * Replaces TopKSelectionKernel.encode/execute (Kernels/Metal4/TopKSelectionKernel.swift:228-368). */
 va_status va_topk_select(va_context* ctx, const float* values, uint32_t num_rows, uint32_t num_elements,

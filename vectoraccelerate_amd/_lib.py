@@ -31,6 +31,7 @@ VA_OPT_SCREEN = 3
 
 VA_SENTINEL_INDEX = 0xFFFFFFFF
 VA_MAX_K = 1024
+VA_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 _p = C.c_void_p
 _u32 = C.c_uint32
@@ -63,6 +64,7 @@ SIGNATURES: dict[str, tuple] = {
     "va_dot_all_pairs": (_st, [_p, _p, _p, _p, _u32, _u32, _u32, _i32]),
     "va_fused_topk": (_st, [_p, _i32, _p, _p, _u32, _u32, _u32, _u32, _p, _p]),
     "va_fused_topk_streamed": (_st, [_p, _i32, _p, _p, _u32, _u32, _u32, _u32, _u32, _p, _p]),
+    "va_fused_topk_noalloc": (_st, [_p, _i32, _p, _p, _u32, _u32, _u32, _u32, _p, _p]),
     "va_topk_select": (_st, [_p, _p, _u32, _u32, _u32, _i32, _p, _p]),
     "va_topk_merge": (_st, [_p, _p, _p, _p, _p, _u32, _u32, _u32, _p, _p]),
     "va_sq_params_per_dim": (_st, [_p, _p, _u32, _u32, _p, _p, _p, _p]),

@@ -22,6 +22,13 @@ va_status fail(va_context* ctx, va_status st, const char* fmt, ...) {
 }
 
 va_status Scratch::reserve(size_t total) {
+    if (ctx->fixed_scratch) {
+        if (total <= ctx->fixed_scratch_bytes) return VA_OK;
+        return fail(ctx, VA_ERR_INVALID_ARG,
+                    "this search needs %zu bytes of scratch; the allocation-free entry point has %zu "
+                    "(VA_NOALLOC_SCRATCH_BYTES): use va_fused_topk",
+                    total, ctx->fixed_scratch_bytes);
+    }
     if (total <= ctx->scratch_bytes) return VA_OK;
     // grow: wait for in-flight users of the old arena, then replace it
     VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -144,6 +151,7 @@ static va_status create_impl(int device, void* stream, va_context** out) {
         return VA_ERR_OOM;
     }
     ctx->host_word = static_cast<uint32_t*>(hw);
+    va::noalloc_setup_device(device);
     *out = ctx;
     return VA_OK;
 }

@@ -30,6 +30,10 @@ struct va_context {
     // scratch arena: partial results, counters, candidate buffers
     char* scratch = nullptr;
     size_t scratch_bytes = 0;
+    // while set (the allocation-free entry point), scratch comes from this fixed device block
+    // instead of the arena: reserve() checks the size and never allocates
+    char* fixed_scratch = nullptr;
+    size_t fixed_scratch_bytes = 0;
     // pinned host word used to read back small counters
     uint32_t* host_word = nullptr;
     // phase profiling of the top-k scan (va_context_set_profiling)
@@ -71,8 +75,9 @@ struct DeviceGuard {
     }
 };
 
-// Bump allocator over the context's scratch arena.  Sizes are rounded to 256 B.
-// reserve() grows the arena (synchronising the stream first) before any carve().
+// Bump allocator over the context's scratch arena (or its fixed block, see va_context).  Sizes
+// are rounded to 256 B.  reserve() grows the arena (synchronising the stream first) before any
+// carve(); with a fixed block it only checks that `total` fits.
 struct Scratch {
     va_context* ctx;
     size_t off = 0;
@@ -82,11 +87,19 @@ struct Scratch {
     template <typename T>
     T* carve(size_t count) {
         size_t b = round(count * sizeof(T));
-        T* p = reinterpret_cast<T*>(ctx->scratch + off);
+        T* p = reinterpret_cast<T*>((ctx->fixed_scratch ? ctx->fixed_scratch : ctx->scratch) + off);
         off += b;
         return p;
     }
 };
+
+// Bytes of dense keys one launch of the exact scan may write (the threshold sample, the dense
+// path, the overflow rescan): 256 MiB, or a quarter of a fixed scratch block.
+size_t dense_budget(const va_context* ctx);
+
+// Allocation-free entry point: resolves the device address of the fixed scratch block of
+// `device` (called once per device, with that device current, when a context is created).
+void noalloc_setup_device(int device);
 
 }  // namespace va
 

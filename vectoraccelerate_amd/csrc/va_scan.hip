@@ -19,18 +19,22 @@
 namespace va {
 
 namespace {
-constexpr uint64_t kDenseBudgetBytes = 256ull << 20;  // dense key matrix per launch
 constexpr uint32_t kMinSample = 16384;
-
 }  // namespace
+
+size_t dense_budget(const va_context* ctx) {
+    constexpr size_t kArena = 256ull << 20;
+    return ctx->fixed_scratch ? std::min(kArena, ctx->fixed_scratch_bytes / 4) : kArena;
+}
 
 ScanPlan plan_scan(const va_context* ctx, uint32_t Q, uint32_t N, uint32_t k) {
     ScanPlan p;
     // Sample size: N/64 rows keeps ~64k candidates per query, but the dense sample costs Q*S
-    // keys, so it is capped at kDenseBudgetBytes of keys in total (16384 rows minimum).
+    // keys, so it is capped at dense_budget() bytes of keys in total (16384 rows minimum).
+    const uint64_t budget = dense_budget(ctx);
     p.S = ctx->opt_sample_rows
               ? ctx->opt_sample_rows
-              : std::max<uint64_t>(kMinSample, std::min<uint64_t>(N / 64, kDenseBudgetBytes / 4 / Q));
+              : std::max<uint64_t>(kMinSample, std::min<uint64_t>(N / 64, budget / 4 / Q));
     p.direct = p.S >= N;
     if (p.direct) return p;
     p.stride = uint32_t(N / p.S);
@@ -39,7 +43,7 @@ ScanPlan plan_scan(const va_context* ctx, uint32_t Q, uint32_t N, uint32_t k) {
                                           : std::max<uint64_t>(3ull * k, uint64_t(k) + 32) * ratio + 1024;
     cap = std::min<uint64_t>(cap, N);
     p.cap = (cap + 63) & ~uint64_t(63);
-    p.qs = uint32_t(std::max<uint64_t>(1, std::min<uint64_t>(Q, kDenseBudgetBytes / (p.S * 4))));
+    p.qs = uint32_t(std::max<uint64_t>(1, std::min<uint64_t>(Q, budget / (p.S * 4))));
     return p;
 }
 
@@ -52,12 +56,20 @@ va_status rescan_rows(va_context* ctx, KeyProducer& kp, uint32_t N, uint32_t k, 
                                      ctx->stream));
     VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
     // rows are processed in batches of R; each batch scans the database in chunks of C rows
-    const uint32_t R = std::min<uint32_t>(n_rows, 64);
-    const uint32_t C = uint32_t(std::max<uint64_t>(k, std::min<uint64_t>(N, kDenseBudgetBytes / (uint64_t(R) * 4))));
-    const uint32_t nch = (N + C - 1) / C;
+    // (a fixed scratch block halves R until the batch fits)
+    const uint64_t budget = dense_budget(ctx);
+    uint32_t R = std::min<uint32_t>(n_rows, 64), C = 0, nch = 0;
+    size_t need = 0;
+    for (;;) {
+        C = uint32_t(std::max<uint64_t>(k, std::min<uint64_t>(N, budget / (uint64_t(R) * 4))));
+        nch = (N + C - 1) / C;
+        need = Scratch::round(uint64_t(n_rows) * 4) + Scratch::round(uint64_t(R) * C * 4) +
+               Scratch::round(uint64_t(R) * nch * k * 4) * 2;
+        if (!ctx->fixed_scratch || need <= ctx->fixed_scratch_bytes || R == 1) break;
+        R = (R + 1) / 2;
+    }
     Scratch f(ctx);
-    VA_CHECK_STATUS(f.reserve(Scratch::round(uint64_t(n_rows) * 4) + Scratch::round(uint64_t(R) * C * 4) +
-                              Scratch::round(uint64_t(R) * nch * k * 4) * 2));
+    VA_CHECK_STATUS(f.reserve(need));
     uint32_t* ovf_rows = f.carve<uint32_t>(n_rows);
     uint32_t* dkeys = f.carve<uint32_t>(uint64_t(R) * C);
     uint32_t* wkey = f.carve<uint32_t>(uint64_t(R) * nch * k);
@@ -122,7 +134,7 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
         ctx->last_scan.scan_launches = 0;
         // small database: dense keys in query chunks + select
         const uint64_t per_q = uint64_t(N) * 4;
-        uint32_t qc = uint32_t(std::max<uint64_t>(1, std::min<uint64_t>(Q, kDenseBudgetBytes / per_q)));
+        uint32_t qc = uint32_t(std::max<uint64_t>(1, std::min<uint64_t>(Q, dense_budget(ctx) / per_q)));
         Scratch s(ctx);
         VA_CHECK_STATUS(s.reserve(Scratch::round(uint64_t(qc) * per_q)));
         uint32_t* keys = s.carve<uint32_t>(uint64_t(qc) * N);
