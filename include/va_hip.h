@@ -253,6 +253,59 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
 va_status va_ivf_search(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
                         uint32_t nprobe, uint32_t k, uint32_t* out_idx, float* out_dist);
 
+/* ---- index with stable handles: replaces AcceleratedVectorIndex's flat storage, handle table
+ *      and search (Index/AcceleratedVectorIndex.swift:481-1265; Index/Internal/HandleAllocator.swift:39-242)
+ * The index keeps every row on the device in slots, with an fp16 shadow of each row (rounded at
+ * insert time; the screening scan reads it, results are the fp32 scan's) when dim % 4 == 0.
+ * Handles are stable ids in insertion order (VectorHandle.stableID); removing one leaves its
+ * slot excluded from every search until va_index_compact moves the live rows down (handles keep
+ * their ids).  An index is used through one context at a time (the actor contract). */
+typedef struct va_index va_index;
+typedef struct {
+    uint32_t count;        /* live vectors */
+    uint32_t deleted;      /* removed, not yet compacted */
+    uint32_t slots;        /* count + deleted */
+    uint32_t dimension;
+    uint64_t capacity;     /* slots allocated */
+    const float* rows;     /* device, [slots x dimension]; valid until the next insert or compact */
+    uint32_t next_handle;  /* the id the next inserted vector gets */
+} va_index_info;
+/* Returns nonzero to accept a result (IndexFilter, Index/AcceleratedVectorIndex.swift:1188-1265). */
+typedef int (*va_index_filter)(uint32_t handle, void* user);
+va_status va_index_create(va_context* ctx, uint32_t dim, uint32_t capacity, va_index** out);
+va_status va_index_destroy(va_index* index);
+/* Append num_vectors device rows; out_handles (host, may be NULL) gets their handles.  Grows the
+ * storage by doubling (synchronising the context then).  insert(_:) / insert(contentsOf:),
+ * AcceleratedVectorIndex.swift:481-700. */
+va_status va_index_insert(va_context* ctx, va_index* index, const float* vectors, uint32_t num_vectors,
+                          uint32_t* out_handles);
+/* Remove host-listed handles; unknown or already removed ones are skipped.  *out_removed (may be
+ * NULL) = how many were removed.  Synchronises.  remove(_:), AcceleratedVectorIndex.swift:771-833. */
+va_status va_index_remove(va_context* ctx, va_index* index, const uint32_t* handles, uint32_t num_handles,
+                          uint32_t* out_removed);
+/* Drop removed slots, keeping the live rows' order and handles.  Synchronises.
+ * compact(), AcceleratedVectorIndex.swift:834-893. */
+va_status va_index_compact(va_context* ctx, va_index* index);
+va_status va_index_get_info(const va_index* index, va_index_info* out);
+/* 1 when the handle names a live vector (contains(_:)). */
+int va_index_contains(const va_index* index, uint32_t handle);
+/* Copy a live vector to host memory out[dim] (synchronous; vector(for:)). */
+va_status va_index_get_vector(va_context* ctx, const va_index* index, uint32_t handle, float* out);
+/* Exact top-k over the live vectors for each device query: out_handles / out_dist [Q x k]
+ * (device), ordered by (distance, slot); slots past the number of live vectors hold
+ * VA_SENTINEL_INDEX / +inf.  k <= VA_MAX_K whatever the number of removed vectors.
+ * searchUnfiltered / searchBatchGPU, AcceleratedVectorIndex.swift:1103-1186, 1278-1374. */
+va_status va_index_search(va_context* ctx, const va_index* index, va_metric metric, const float* queries,
+                          uint32_t num_queries, uint32_t k, uint32_t* out_handles, float* out_dist);
+/* The k nearest live vectors that pass filter (NULL: all), for one device query: round after
+ * round the nearest not yet examined vectors are fetched and filtered on the host, so results
+ * are exact however many the filter rejects.  out_handles / out_dist are host arrays of k;
+ * *out_count results were found; *out_examined (may be NULL) vectors were examined.
+ * searchFiltered, AcceleratedVectorIndex.swift:1188-1265. */
+va_status va_index_search_filtered(va_context* ctx, va_index* index, va_metric metric, const float* query, uint32_t k,
+                                   va_index_filter filter, void* user, uint32_t* out_handles, float* out_dist,
+                                   uint32_t* out_count, uint32_t* out_examined);
+
 /* ---- k-means (IVF centroid training) ------------------------------------------------ */
 typedef struct {
     uint32_t iterations;  /* Lloyd iterations run */

@@ -81,6 +81,16 @@ SIGNATURES: dict[str, tuple] = {
     "va_ivf_probe": (_st, [_p, _p, _p, _u32, _u32, _p]),
     "va_ivf_scan": (_st, [_p, _p, _p, _u32, _p, _u32, _u32, _p, _p]),
     "va_ivf_search": (_st, [_p, _p, _p, _u32, _u32, _u32, _p, _p]),
+    "va_index_create": (_st, [_p, _u32, _u32, C.POINTER(_p)]),
+    "va_index_destroy": (_st, [_p]),
+    "va_index_insert": (_st, [_p, _p, _p, _u32, _p]),
+    "va_index_remove": (_st, [_p, _p, _p, _u32, C.POINTER(_u32)]),
+    "va_index_compact": (_st, [_p, _p]),
+    "va_index_get_info": (_st, [_p, _p]),
+    "va_index_contains": (C.c_int, [_p, _u32]),
+    "va_index_get_vector": (_st, [_p, _p, _u32, _p]),
+    "va_index_search": (_st, [_p, _p, _i32, _p, _u32, _u32, _p, _p]),
+    "va_index_search_filtered": (_st, [_p, _p, _i32, _p, _u32, _p, _p, _p, _p, C.POINTER(_u32), C.POINTER(_u32)]),
     "va_kmeans_fit": (_st, [_p, _p, _u32, _u32, _u32, _p, _u32, C.c_float, _p, _p, _p, _p, _p]),
     "va_kmeans_plusplus": (_st, [_p, _p, _u32, _u32, _u32, _u64, _p, _p]),
     "va_pq_train": (_st, [_p, _p, _u32, _u32, _u32, _u32, _u32, C.c_float, _u64, _p, _p, C.POINTER(_u32)]),
@@ -111,6 +121,24 @@ class ScanTimings(C.Structure):
 
     def as_dict(self) -> dict:
         return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+class IndexInfo(C.Structure):
+    """va_index_info (include/va_hip.h)."""
+
+    _fields_ = [
+        ("count", C.c_uint32),
+        ("deleted", C.c_uint32),
+        ("slots", C.c_uint32),
+        ("dimension", C.c_uint32),
+        ("capacity", C.c_uint64),
+        ("rows", C.c_void_p),
+        ("next_handle", C.c_uint32),
+    ]
+
+
+# int (*va_index_filter)(uint32_t handle, void* user)
+INDEX_FILTER = C.CFUNCTYPE(C.c_int, C.c_uint32, C.c_void_p)
 
 
 class KMeansInfo(C.Structure):

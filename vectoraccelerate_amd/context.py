@@ -147,6 +147,32 @@ class GPUContext:
 Metal4Context = GPUContext
 
 
+class DeviceRows:
+    """A row-major fp32 [rows x dim] array in device memory the library owns (an index's
+    storage), accepted wherever this package's bindings take a contiguous device tensor."""
+
+    is_cuda = True
+
+    def __init__(self, ptr: int, rows: int, dim: int):
+        self.ptr = int(ptr)
+        self.shape = (int(rows), int(dim))
+
+    def is_contiguous(self) -> bool:
+        return True
+
+    def contiguous(self) -> "DeviceRows":
+        return self
+
+    def data_ptr(self) -> int:
+        return self.ptr
+
+    def rows(self, start: int, stop: int) -> "DeviceRows":
+        """Rows [start, stop) as a view."""
+        n, d = self.shape
+        start, stop = max(0, start), min(n, stop)
+        return DeviceRows(self.ptr + start * d * 4, max(0, stop - start), d)
+
+
 def dptr(t) -> int:
     """Device pointer of a contiguous CUDA tensor (0 for None)."""
     if t is None:

@@ -351,7 +351,7 @@ __global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) 
                 for (int e = 0; e < 4; ++e) {
                     const uint32_t r = uint32_t(wn * 128 + mloc + e);
                     const uint32_t key = key_of_float(apply_op(a.op, acc[b][4 * j + e], qq, xx[e]));
-                    if (r < rc && key < bk) {
+                    if (r < rc && key < bk && key < 0xFFFFFFFEu) {  // NaN distances never win
                         bk = key;
                         bi = rs + r;
                     }

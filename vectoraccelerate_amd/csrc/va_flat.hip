@@ -149,10 +149,12 @@ struct F32Producer final : KeyProducer {
 
 }  // namespace
 
-// Exact top-k of queries (device) against a device database: the screened path where it applies,
-// else the fp32 scan.  Synchronises the stream (the scan reads back an overflow counter).
+// Exact top-k of queries (device) against a device database: the screened path where it applies
+// (over the fp16 shadow when one is given), else the fp32 scan.  Synchronises the stream (the
+// scan reads back an overflow counter).
 va_status flat_topk(va_context* ctx, DistOp op, const float* q, const float* x, uint32_t Q, uint32_t N, uint32_t D,
-                    uint32_t k, uint32_t* out_idx, float* out_dist) {
+                    uint32_t k, uint32_t* out_idx, float* out_dist, const _Float16* shadow, const float* norms,
+                    const uint8_t* skip) {
     F32Producer p;
     p.ctx = ctx;
     p.q = q;
@@ -165,6 +167,7 @@ va_status flat_topk(va_context* ctx, DistOp op, const float* q, const float* x, 
     o.idx = out_idx;
     o.f = out_dist;
     o.key_kind = 0;
+    o.skip = skip;
     ScreenInput si;
     si.q = q;
     si.x = x;
@@ -172,6 +175,8 @@ va_status flat_topk(va_context* ctx, DistOp op, const float* q, const float* x, 
     si.N = N;
     si.D = D;
     si.op = op;
+    si.xh = shadow;
+    si.xn = norms;
     if (screen_applies(ctx, si, k)) return screened_topk_scan(ctx, si, p, k, o);
     return exact_topk_scan(ctx, p, Q, N, k, o);
 }

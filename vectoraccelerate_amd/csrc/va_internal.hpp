@@ -133,9 +133,13 @@ constexpr uint32_t kSentinel = 0xFFFFFFFFu;
 // MI355X: 8 XCDs of 32 CUs, each with its own 4 MB L2; workgroup w is dispatched to XCD w % 8.
 constexpr uint32_t kXcds = 8;
 
-// Ascending-orderable key of a float: -0 and +0 map to one key, NaN to the largest key.
+// 0xFFFFFFFF is the key of an absent item (a row excluded from a search, e.g. a deleted row of
+// an index): selections order it after every real key and output it as a missing result.
+constexpr uint32_t kAbsentKey = 0xFFFFFFFFu;
+// Ascending-orderable key of a float: -0 and +0 map to one key, NaN to the largest real key
+// (0xFFFFFFFE, after +inf).
 __host__ __device__ inline uint32_t key_of_float(float f) {
-    if (f != f) return 0xFFFFFFFFu;
+    if (f != f) return 0xFFFFFFFEu;
     uint32_t u = __builtin_bit_cast(uint32_t, f);
     if (f == 0.0f) u = 0u;
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -146,7 +150,7 @@ __host__ __device__ inline float float_of_key(uint32_t k) {
 }
 // Descending order (MAX mode), NaN still last.
 __host__ __device__ inline uint32_t key_of_float_desc(float f) {
-    if (f != f) return 0xFFFFFFFFu;
+    if (f != f) return 0xFFFFFFFEu;
     return ~key_of_float(f);
 }
 __host__ __device__ inline float float_of_key_desc(uint32_t k) { return float_of_key(~k); }
@@ -370,7 +374,18 @@ struct ScanOutputs {
     int32_t* i32 = nullptr;    // key_kind 2
     uint32_t* key = nullptr;   // raw keys (Hamming distances)
     int key_kind = 0;
+    // rows excluded from the search (skip[row] != 0; the deleted rows of an index), or nullptr:
+    // their keys become kAbsentKey before every selection
+    const uint8_t* skip = nullptr;
 };
+
+// keys[r * ld + j] = kAbsentKey for the rows + j * stride (j < cols) that skip excludes
+va_status mask_dense_keys(va_context* ctx, uint32_t* keys, uint32_t rows, uint32_t cols, int64_t ld, uint32_t row0,
+                          uint32_t stride, const uint8_t* skip);
+// keys[r * ld + i] (and keys2, when given) = kAbsentKey for the excluded ids[r * ld + i],
+// i < min(counts[r], cap)
+va_status mask_list_keys(va_context* ctx, uint32_t* keys, uint32_t* keys2, const uint32_t* ids, const uint32_t* counts,
+                         uint32_t rows, uint32_t cap, int64_t ld, const uint8_t* skip);
 
 va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t N, uint32_t k,
                           const ScanOutputs& out);
@@ -388,9 +403,9 @@ ScanPlan plan_scan(const va_context* ctx, uint32_t Q, uint32_t N, uint32_t k);
 
 // Exact top-k of the listed query rows (device list) by dense keys over the whole database in
 // chunks (the path of queries whose candidate list overflowed).  Writes base's outputs at the
-// listed rows.  Synchronises the stream.
+// listed rows; rows excluded by skip (may be nullptr) are absent.  Synchronises the stream.
 va_status rescan_rows(va_context* ctx, KeyProducer& kp, uint32_t N, uint32_t k, const SelectArgs& base,
-                      const uint32_t* rows_dev, uint32_t n_rows);
+                      const uint32_t* rows_dev, uint32_t n_rows, const uint8_t* skip = nullptr);
 
 // hipEvent marks of the scan phases (no-ops unless profiling is on)
 struct ScanPhaseMarks {
@@ -438,10 +453,21 @@ struct ScreenInput {
     const float* x = nullptr;
     uint32_t Q = 0, N = 0, D = 0;
     DistOp op = OP_L2SQ;
+    // optional fp16 shadow of x (shadow_pitch(D) halves per row) and its squared norms: the
+    // filtering scan then reads it instead of converting x
+    const _Float16* xh = nullptr;
+    const float* xn = nullptr;
 };
-// Exact top-k of device queries against a device database (va_fused_topk's body).
+// Exact top-k of device queries against a device database (va_fused_topk's body).  shadow /
+// norms: an fp16 shadow of x (see build_shadow) or nullptr; skip: rows excluded, or nullptr.
 va_status flat_topk(va_context* ctx, DistOp op, const float* q, const float* x, uint32_t Q, uint32_t N, uint32_t D,
-                    uint32_t k, uint32_t* out_idx, float* out_dist);
+                    uint32_t k, uint32_t* out_idx, float* out_dist, const _Float16* shadow = nullptr,
+                    const float* norms = nullptr, const uint8_t* skip = nullptr);
+// Halves per row of an fp16 shadow (D rounded up to a multiple of 64).
+uint32_t shadow_pitch(uint32_t D);
+// shadow[r * shadow_pitch(D) + d] = fp16(x[r * D + d]) (RNE, zeros past D), norms[r] = |x_r|^2
+// in fp32, for rows r < N.
+va_status build_shadow(va_context* ctx, const float* x, uint32_t N, uint32_t D, _Float16* shadow, float* norms);
 // Whether the screened path applies (metric, alignment, sizes, VA_OPT_SCREEN).
 bool screen_applies(const va_context* ctx, const ScreenInput& in, uint32_t k);
 va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer& exact, uint32_t k,

@@ -22,6 +22,55 @@ namespace {
 constexpr uint32_t kMinSample = 16384;
 }  // namespace
 
+__global__ void mask_dense_kernel(uint32_t* keys, uint32_t cols, int64_t ld, uint32_t row0, uint32_t stride,
+                                  const uint8_t* __restrict__ skip) {
+    uint32_t* k = keys + int64_t(blockIdx.y) * ld;
+    for (uint32_t j = blockIdx.x * 256 + threadIdx.x; j < cols; j += gridDim.x * 256)
+        if (skip[row0 + uint64_t(j) * stride]) k[j] = kAbsentKey;
+}
+
+__global__ void mask_list_kernel(uint32_t* keys, uint32_t* keys2, const uint32_t* __restrict__ ids,
+                                 const uint32_t* __restrict__ counts, uint32_t cap, int64_t ld,
+                                 const uint8_t* __restrict__ skip) {
+    const uint32_t r = blockIdx.y;
+    const uint32_t n = min(counts[r], cap);
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+        const int64_t o = int64_t(r) * ld + i;
+        const uint32_t id = ids[o];
+        if (id != kSentinel && skip[id]) {
+            keys[o] = kAbsentKey;
+            if (keys2) keys2[o] = kAbsentKey;
+        }
+    }
+}
+
+va_status mask_dense_keys(va_context* ctx, uint32_t* keys, uint32_t rows, uint32_t cols, int64_t ld, uint32_t row0,
+                          uint32_t stride, const uint8_t* skip) {
+    if (!skip || rows == 0 || cols == 0) return VA_OK;
+    const uint32_t bx = std::min<uint32_t>(64, (cols + 255) / 256);
+    for (uint32_t r0 = 0; r0 < rows; r0 += 65535) {
+        const uint32_t nr = std::min<uint32_t>(65535, rows - r0);
+        mask_dense_kernel<<<dim3(bx, nr), dim3(256), 0, ctx->stream>>>(keys + int64_t(r0) * ld, cols, ld, row0, stride,
+                                                                      skip);
+        VA_CHECK_LAUNCH(ctx);
+    }
+    return VA_OK;
+}
+
+va_status mask_list_keys(va_context* ctx, uint32_t* keys, uint32_t* keys2, const uint32_t* ids, const uint32_t* counts,
+                         uint32_t rows, uint32_t cap, int64_t ld, const uint8_t* skip) {
+    if (!skip || rows == 0 || cap == 0) return VA_OK;
+    const uint32_t bx = std::min<uint32_t>(16, (cap + 255) / 256);
+    for (uint32_t r0 = 0; r0 < rows; r0 += 65535) {
+        const uint32_t nr = std::min<uint32_t>(65535, rows - r0);
+        mask_list_kernel<<<dim3(bx, nr), dim3(256), 0, ctx->stream>>>(keys + int64_t(r0) * ld,
+                                                                     keys2 ? keys2 + int64_t(r0) * ld : nullptr,
+                                                                     ids + int64_t(r0) * ld, counts + r0, cap, ld, skip);
+        VA_CHECK_LAUNCH(ctx);
+    }
+    return VA_OK;
+}
+
 size_t dense_budget(const va_context* ctx) {
     constexpr size_t kArena = 256ull << 20;
     return ctx->fixed_scratch ? std::min(kArena, ctx->fixed_scratch_bytes / 4) : kArena;
@@ -48,7 +97,7 @@ ScanPlan plan_scan(const va_context* ctx, uint32_t Q, uint32_t N, uint32_t k) {
 }
 
 va_status rescan_rows(va_context* ctx, KeyProducer& kp, uint32_t N, uint32_t k, const SelectArgs& base,
-                      const uint32_t* rows_dev, uint32_t n_rows) {
+                      const uint32_t* rows_dev, uint32_t n_rows, const uint8_t* skip) {
     if (n_rows == 0) return VA_OK;
     // The row list is read back first: the arena below may be regrown (which frees it).
     std::vector<uint32_t> rows_host(n_rows);
@@ -83,6 +132,7 @@ va_status rescan_rows(va_context* ctx, KeyProducer& kp, uint32_t N, uint32_t k, 
             const uint32_t c0 = c * C;
             const uint32_t cols = std::min(C, N - c0);
             VA_CHECK_STATUS(kp.dense(rows, 0, nr, c0, cols, 1, dkeys, C));
+            VA_CHECK_STATUS(mask_dense_keys(ctx, dkeys, nr, cols, C, c0, 1, skip));
             SelectArgs a;
             a.keys = dkeys;
             a.ld = C;
@@ -141,6 +191,7 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
         for (uint32_t q0 = 0; q0 < Q; q0 += qc) {
             const uint32_t nq = std::min(qc, Q - q0);
             VA_CHECK_STATUS(kp.dense(nullptr, q0, nq, 0, N, 1, keys, N));
+            VA_CHECK_STATUS(mask_dense_keys(ctx, keys, nq, N, N, 0, 1, out.skip));
             ctx->last_scan.scan_launches++;
             SelectArgs a = base;
             a.keys = keys;
@@ -176,6 +227,7 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
     for (uint32_t q0 = 0; q0 < Q; q0 += qs) {
         const uint32_t nq = std::min(qs, Q - q0);
         VA_CHECK_STATUS(kp.dense(nullptr, q0, nq, 0, uint32_t(S), stride, skeys, int64_t(S)));
+        VA_CHECK_STATUS(mask_dense_keys(ctx, skeys, nq, uint32_t(S), int64_t(S), 0, stride, out.skip));
         SelectArgs a;
         a.keys = skeys;
         a.ld = int64_t(S);
@@ -192,6 +244,7 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
     VA_CHECK_STATUS(pm.mark(1));
     VA_CHECK_STATUS(kp.filter(thr, cnt, ckey, cid, uint32_t(cap)));
     VA_CHECK_STATUS(pm.mark(2));
+    VA_CHECK_STATUS(mask_list_keys(ctx, ckey, nullptr, cid, cnt, Q, uint32_t(cap), int64_t(cap), out.skip));
     ctx->last_scan.scan_launches = 1;
     ctx->last_scan.sample_rows = uint32_t(S);
     ctx->last_scan.candidate_cap = uint32_t(cap);
@@ -216,7 +269,7 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
     if (n_ovf == 0) return pm.finish(true, false);
 
     // ---- 4. exact chunked recomputation of overflowed rows ---------------------------------
-    VA_CHECK_STATUS(rescan_rows(ctx, kp, N, k, base, ovf_rows, n_ovf));
+    VA_CHECK_STATUS(rescan_rows(ctx, kp, N, k, base, ovf_rows, n_ovf, out.skip));
     return pm.finish(true, true);
 }
 

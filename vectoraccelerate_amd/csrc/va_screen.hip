@@ -83,6 +83,9 @@ struct ScreenArgs {
     uint32_t* cand_id = nullptr;
     uint32_t cap = 0;
     uint32_t id_base = 0;
+    // fp16 shadow of the database (screen16_kernel): row j at xh + j * Dp, |x_j|^2 at xn[j]
+    const _Float16* xh = nullptr;
+    const float* xn = nullptr;
 };
 
 // ---- bound of the screened key ----------------------------------------------------------
@@ -137,7 +140,7 @@ __device__ __forceinline__ void screen_keys(const ScreenArgs& a, float dot, floa
         khi = key_of_float(hi);
     } else {
         klo = 0u;
-        khi = 0xFFFFFFFFu;
+        khi = 0xFFFFFFFEu;  // the NaN key
     }
 }
 
@@ -153,7 +156,7 @@ struct PreTest {
 __device__ __forceinline__ PreTest pretest_consts(const ScreenArgs& a, float4 info, uint32_t thr_key) {
     const float qq = info.x, nq = info.y, inv = info.z, c0q = info.w;
     const PreTest all = {0.0f, 0.0f, -INFINITY};
-    if (thr_key == 0xFFFFFFFFu) return all;  // the NaN key: every key passes
+    if (thr_key >= 0xFFFFFFFEu) return all;  // the NaN key (or no threshold): every key passes
     const float tau = float_of_key(thr_key);
     if (!(fabsf(tau) <= FLT_MAX) || !(qq <= FLT_MAX)) return all;
     const float sig = 1.0f / inv;  // 2^scale, exact
@@ -235,6 +238,99 @@ __global__ __launch_bounds__(256) void screen_prep_kernel(const float* __restric
     if (lane == 0) {
         const float inv = ldexpf(1.0f, -sc);
         qinfo[qi] = make_float4(ss, sqrtf(ss), inv, c0 * 0x1p-25f * inv);
+    }
+}
+
+// ---- the filter epilogue of both screening scans ---------------------------------------------
+// acc[m][n] holds the 32 x 32 block (rows wn*128 + 32m .., queries wq*128 + 32n ..) of the tile's
+// fp16 dots (queries scaled by 2^scale); xxs/xxp/nxp are the tile's row norms (xxp/nxp NaN for
+// flagged rows); dump is 32 KiB of LDS private to the wave.
+__device__ __forceinline__ void filter_epilogue(const ScreenArgs& a, f32x16 (&acc)[4][4], const float4 (&qinf)[4],
+                                                const uint32_t (&qthr)[4], f32x4v* dump, const float* xxs,
+                                                const float* xxp, const float* nxp, uint32_t qs, uint32_t rs,
+                                                uint32_t qc, uint32_t rc, int wq, int wn, int lane) {
+    const int l32 = lane & 31, hh = lane >> 5;
+    // The accumulators leave the AGPRs only through LDS stores (two query blocks at a time,
+    // 32 KiB per wave of the free LDS), so they are never copied to VGPRs wholesale.  Per
+    // query block the pre-test over the lane's 64 values (read back from LDS) builds a bit
+    // mask without branches; one atomic per lane reserves list space; the appends of a pair
+    // of blocks run after both atomics are issued, so the round trips overlap.
+    uint64_t valid = 0;  // rows of the tile (the last tile is partial)
+#pragma unroll
+    for (int t = 0; t < 64; ++t) {
+        const int r = wn * 128 + 32 * (t >> 4) + 8 * ((t >> 2) & 3) + 4 * hh + (t & 3);
+        valid |= uint64_t(uint32_t(r) < rc) << t;
+    }
+    auto dump_half = [&](auto HC) {
+        constexpr int h = decltype(HC)::value;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    f32x4v v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = acc[m][2 * h + b][4 * j + e];
+                    dump[(16 * b + 4 * m + j) * 64 + lane] = v;
+                }
+    };
+    auto test_block = [&](int n) -> uint64_t {
+        const PreTest pt = pretest_consts(a, qinf[n], qthr[n]);
+        const f32x4v* src = dump + 16 * (n & 1) * 64 + lane;
+        uint64_t mk = 0;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int r = wn * 128 + 32 * m + 8 * j + 4 * hh;
+                const f32x4v xx = *reinterpret_cast<const f32x4v*>(xxp + r);
+                const f32x4v nx = *reinterpret_cast<const f32x4v*>(nxp + r);
+                const f32x4v v = src[(4 * m + j) * 64];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float rhs = fmaf(pt.A, xx[e], fmaf(pt.B, nx[e], pt.C));
+                    mk |= uint64_t(!(v[e] < rhs)) << (16 * m + 4 * j + e);
+                }
+            }
+        return (uint32_t(wq * 128 + 32 * n + l32) < qc) ? (mk & valid) : 0;
+    };
+    auto reserve = [&](int n, uint64_t mk) -> uint32_t {
+        const uint32_t qi = qs + uint32_t(wq * 128 + 32 * n + l32);
+        return mk ? atomicAdd(a.cnt + qi, uint32_t(__popcll(mk))) : 0u;
+    };
+    auto append = [&](int n, uint64_t mk, uint32_t pos) {
+        const uint32_t qi = qs + uint32_t(wq * 128 + 32 * n + l32);
+        const float inv = qinf[n].z;
+        const float* src = reinterpret_cast<const float*>(dump + 16 * (n & 1) * 64 + lane);
+        for (uint32_t i = pos; mk && i < a.cap; ++i) {
+            const int t = __builtin_ctzll(mk);
+            mk &= mk - 1;
+            const int r = wn * 128 + 32 * (t >> 4) + 8 * ((t >> 2) & 3) + 4 * hh + (t & 3);
+            const float v = src[(t >> 2) * 256 + (t & 3)];
+            const int64_t o = int64_t(qi) * a.cap + i;
+            a.cand_dot[o] = v * inv;
+            a.cand_xx[o] = xxs[r];
+            a.cand_id[o] = a.id_base + rs + uint32_t(r);
+        }
+    };
+    dump_half(std::integral_constant<int, 0>());
+    {
+        const uint64_t m0 = test_block(0);
+        const uint32_t p0 = reserve(0, m0);
+        const uint64_t m1 = test_block(1);
+        const uint32_t p1 = reserve(1, m1);
+        append(0, m0, p0);
+        append(1, m1, p1);
+    }
+    dump_half(std::integral_constant<int, 1>());
+    {
+        const uint64_t m2 = test_block(2);
+        const uint32_t p2 = reserve(2, m2);
+        const uint64_t m3 = test_block(3);
+        const uint32_t p3 = reserve(3, m3);
+        append(2, m2, p2);
+        append(3, m3, p3);
     }
 }
 
@@ -520,91 +616,196 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
         }
         return;
     } else {
-        // The accumulators leave the AGPRs only through LDS stores (two query blocks at a time,
-        // 32 KiB per wave of the free LDS), so they are never copied to VGPRs wholesale.  Per
-        // query block the pre-test over the lane's 64 values (read back from LDS) builds a bit
-        // mask without branches; one atomic per lane reserves list space; the appends of a pair
-        // of blocks run after both atomics are issued, so the round trips overlap.
+        // The accumulators leave through LDS, 32 KiB per wave (one of the four stage slots).
         static_assert(XBYTES >= 2 * 64 * 64 * 4 && QBYTES >= 2 * 64 * 64 * 4, "dump: 32 KiB per wave");
         f32x4v* dump = reinterpret_cast<f32x4v*>(wave == 0 ? qslot0 : wave == 1 ? qslot1 : wave == 2 ? xslot0 : xslot1);
-        uint64_t valid = 0;  // rows of the tile (the last tile is partial)
+        filter_epilogue(a, acc, qinf, qthr, dump, xxs, xxp, nxp, qs, rs, qc, rc, wq, wn, lane);
+    }
+}
+
+// ---- the screening scan over an fp16 shadow of the database ---------------------------------------
+// The same tile (256 queries x 256 rows, four waves of 128 x 128) and epilogue as screen_kernel's
+// filter mode, but the rows come already rounded to fp16 (the same RNE rounding) with their
+// squared norms, so both operands move global -> LDS by direct loads and the main loop is MFMAs,
+// fragment reads and loads only.  64 d-values per stage, two stages in LDS (128 KiB); the
+// fragments of k-step g+1 are read while the 16 MFMAs of k-step g run, and the stage barrier sits
+// inside the last k-step of a stage, after its fragments are in registers (a bare s_barrier: the
+// direct loads of the next stage stay in flight across it).
+namespace s16 {
+constexpr int TQ = 256, TN = 256, KC = 64;
+constexpr int ROWB = KC * 2;              // bytes per LDS row
+constexpr int OPB = TQ * ROWB;            // one operand per stage (32 KiB)
+constexpr int STAGE = 2 * OPB;            // queries, then rows
+constexpr int LPW = OPB / 1024 / 4;       // 1 KiB direct loads per wave per operand per stage (8)
+constexpr int LDS = 2 * STAGE;            // two stages; the epilogue reuses them (32 KiB per wave)
+static_assert(LDS >= 4 * 32768, "epilogue dump");
+}  // namespace s16
+
+__global__ __launch_bounds__(256, 1) void screen16_kernel(ScreenArgs a) {
+    using namespace s16;
+    extern __shared__ __attribute__((aligned(1024))) char lds[];
+    __shared__ __attribute__((aligned(16))) float norms[3 * TN];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wq = wave & 1, wn = wave >> 1, l32 = lane & 31, hh = lane >> 5;
+    // XCD-aware order, as screen_kernel
+    const uint32_t nqb = (a.Q + TQ - 1) / TQ;
+    const uint32_t xcd = blockIdx.x % kXcds, seq = blockIdx.x / kXcds;
+    const uint32_t qb = seq % nqb, tb = (seq / nqb) * kXcds + xcd;
+    if (tb * uint32_t(TN) >= a.N) return;  // padding workgroup
+    const uint32_t qs = qb * TQ, rs = tb * TN;
+    const uint32_t qc = min(uint32_t(TQ), a.Q - qs), rc = min(uint32_t(TN), a.N - rs);
+    const uint32_t nst = a.Dp / KC;
+
+    // Direct loads: wave w fills 1 KiB groups g = w + 4i (rows 8g .. 8g+7) of each operand; lane
+    // L loads row 8g + L/8 at physical chunk L%8 = logical chunk (L%8) ^ ((row >> 1) & 7).  Rows
+    // past qc / rc read past their descriptor and land as zeros.
+    const dma_rsrc qres = make_dma_rsrc(a.qh + int64_t(qs) * a.Dp, qc * a.Dp * 2u);
+    const dma_rsrc xres = make_dma_rsrc(a.xh + int64_t(rs) * a.Dp, rc * a.Dp * 2u);
+    uint32_t off[LPW];
 #pragma unroll
-        for (int t = 0; t < 64; ++t) {
-            const int r = wn * 128 + 32 * (t >> 4) + 8 * ((t >> 2) & 3) + 4 * hh + (t & 3);
-            valid |= uint64_t(uint32_t(r) < rc) << t;
+    for (int i = 0; i < LPW; ++i) {
+        const int row = 8 * (wave + 4 * i) + (lane >> 3);
+        off[i] = uint32_t(row) * a.Dp * 2u + 16u * uint32_t((lane & 7) ^ ((row >> 1) & 7));
+    }
+    const uint32_t lds0 = lds_addr_of(lds);
+    auto issue = [&](uint32_t s) {
+        const uint32_t d0 = s * KC;
+        const bool ok = d0 < a.Dp;
+        const uint32_t sb = lds0 + (s & 1u) * uint32_t(STAGE);
+#pragma unroll
+        for (int i = 0; i < LPW; ++i) {
+            const uint32_t grp = uint32_t(wave + 4 * i);
+            lds_dma16(qres, ok ? off[i] + d0 * 2u : kDmaSkip, sb + grp * 1024u);
+            lds_dma16(xres, ok ? off[i] + d0 * 2u : kDmaSkip, sb + uint32_t(OPB) + grp * 1024u);
         }
-        auto dump_half = [&](auto HC) {
-            constexpr int h = decltype(HC)::value;
+    };
+    // fragment rows start at multiples of 32, so the chunk swizzle is (l32 >> 1) & 7 for both
+    const int swz = (l32 >> 1) & 7;
+    const uint32_t a_off = uint32_t(OPB + (wn * 128 + l32) * ROWB);
+    const uint32_t b_off = uint32_t((wq * 128 + l32) * ROWB);
+
+    float4 qinf[4];
+    uint32_t qthr[4];
 #pragma unroll
-            for (int b = 0; b < 2; ++b)
+    for (int n = 0; n < 4; ++n) {
+        const uint32_t qi = qs + min(uint32_t(wq * 128 + 32 * n + l32), qc - 1);
+        qinf[n] = a.qinfo[qi];
+        qthr[n] = a.thr[qi];
+    }
+    f32x16 acc[4][4];
 #pragma unroll
-                for (int m = 0; m < 4; ++m)
+    for (int m = 0; m < 4; ++m)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        f32x4v v;
+        for (int n = 0; n < 4; ++n)
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) v[e] = acc[m][2 * h + b][4 * j + e];
-                        dump[(16 * b + 4 * m + j) * 64 + lane] = v;
-                    }
-        };
-        auto test_block = [&](int n) -> uint64_t {
-            const PreTest pt = pretest_consts(a, qinf[n], qthr[n]);
-            const f32x4v* src = dump + 16 * (n & 1) * 64 + lane;
-            uint64_t mk = 0;
+            for (int v = 0; v < 16; ++v) acc[m][n][v] = 0.0f;
+
+    h8v fa[2][4], fb[2][4];
+    auto read_frags = [&](int buf, uint32_t slot, int t) {
+        const char* base = lds + slot * STAGE;
+        const uint32_t ko = 16u * uint32_t((2 * t + hh) ^ swz);
 #pragma unroll
-            for (int m = 0; m < 4; ++m)
+        for (int m = 0; m < 4; ++m) fa[buf][m] = *reinterpret_cast<const h8v*>(base + a_off + m * 32 * ROWB + ko);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int r = wn * 128 + 32 * m + 8 * j + 4 * hh;
-                    const f32x4v xx = *reinterpret_cast<const f32x4v*>(xxp + r);
-                    const f32x4v nx = *reinterpret_cast<const f32x4v*>(nxp + r);
-                    const f32x4v v = src[(4 * m + j) * 64];
+        for (int n = 0; n < 4; ++n) fb[buf][n] = *reinterpret_cast<const h8v*>(base + b_off + n * 32 * ROWB + ko);
+    };
+    auto mma = [&](int buf) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float rhs = fmaf(pt.A, xx[e], fmaf(pt.B, nx[e], pt.C));
-                        mk |= uint64_t(!(v[e] < rhs)) << (16 * m + 4 * j + e);
-                    }
-                }
-            return (uint32_t(wq * 128 + 32 * n + l32) < qc) ? (mk & valid) : 0;
-        };
-        auto reserve = [&](int n, uint64_t mk) -> uint32_t {
-            const uint32_t qi = qs + uint32_t(wq * 128 + 32 * n + l32);
-            return mk ? atomicAdd(a.cnt + qi, uint32_t(__popcll(mk))) : 0u;
-        };
-        auto append = [&](int n, uint64_t mk, uint32_t pos) {
-            const uint32_t qi = qs + uint32_t(wq * 128 + 32 * n + l32);
-            const float inv = qinf[n].z;
-            const float* src = reinterpret_cast<const float*>(dump + 16 * (n & 1) * 64 + lane);
-            for (uint32_t i = pos; mk && i < a.cap; ++i) {
-                const int t = __builtin_ctzll(mk);
-                mk &= mk - 1;
-                const int r = wn * 128 + 32 * (t >> 4) + 8 * ((t >> 2) & 3) + 4 * hh + (t & 3);
-                const float v = src[(t >> 2) * 256 + (t & 3)];
-                const int64_t o = int64_t(qi) * a.cap + i;
-                a.cand_dot[o] = v * inv;
-                a.cand_xx[o] = xxs[r];
-                a.cand_id[o] = a.id_base + rs + uint32_t(r);
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int n = 0; n < 4; ++n)
+                acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[buf][m], fb[buf][n], acc[m][n], 0, 0, 0);
+    };
+    // the 8 fragment reads of the next k-step go between the first 8 of the 16 MFMAs
+    auto interleave = [&]() {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    };
+    // workgroup barrier without the release fence of __syncthreads (which would also wait for
+    // the direct loads in flight); this wave's LDS reads are complete before it
+    auto barrier = [&]() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+
+    issue(0);
+    issue(1);
+    wait_vmcnt<2 * LPW>();  // stage 0 (older than stage 1's loads)
+    barrier();
+    read_frags(0, 0, 0);
+    for (uint32_t s = 0; s < nst; ++s) {
+        const uint32_t slot = s & 1u;
+#pragma unroll
+        for (int t = 0; t < KC / 16; ++t) {
+            const int cur = t & 1;  // four k-steps per stage: the parity of the global k-step
+            if (t < KC / 16 - 1) {
+                read_frags(cur ^ 1, slot, t + 1);
+                mma(cur);
+                interleave();
+            } else {
+                // this k-step's fragments are in registers: publish stage s+1, free slot s
+                wait_vmcnt<0>();
+                barrier();
+                read_frags(cur ^ 1, slot ^ 1u, 0);
+                mma(cur);
+                interleave();
+                issue(s + 2);  // past the last stage: zeros into the free slot
             }
-        };
-        dump_half(std::integral_constant<int, 0>());
-        {
-            const uint64_t m0 = test_block(0);
-            const uint32_t p0 = reserve(0, m0);
-            const uint64_t m1 = test_block(1);
-            const uint32_t p1 = reserve(1, m1);
-            append(0, m0, p0);
-            append(1, m1, p1);
-        }
-        dump_half(std::integral_constant<int, 1>());
-        {
-            const uint64_t m2 = test_block(2);
-            const uint32_t p2 = reserve(2, m2);
-            const uint64_t m3 = test_block(3);
-            const uint32_t p3 = reserve(3, m3);
-            append(2, m2, p2);
-            append(3, m3, p3);
         }
     }
+    wait_vmcnt<0>();
+    __syncthreads();
+
+    // the tile's row norms from the shadow; flags as in screen_kernel
+    float* xxs = norms;
+    float* xxp = norms + TN;
+    float* nxp = norms + 2 * TN;
+    const float tiny = a.op == OP_COS_DIST ? 8.0f * a.c0x : 0.0f;
+    {
+        const uint32_t r = uint32_t(tid);
+        const float t = r < rc ? a.xn[rs + r] : 0.0f;
+        const float nx = __builtin_amdgcn_sqrtf(t);
+        xxs[r] = t;
+        const bool flag = !(t < 4.29e9f) || nx < tiny;
+        xxp[r] = flag ? __builtin_nanf("") : t;
+        nxp[r] = flag ? __builtin_nanf("") : nx;
+    }
+    __syncthreads();
+    filter_epilogue(a, acc, qinf, qthr, reinterpret_cast<f32x4v*>(lds + wave * 32768), xxs, xxp, nxp, qs, rs, qc, rc,
+                    wq, wn, lane);
+}
+
+// ---- the fp16 shadow: rows rounded to fp16 (RNE, as the scans round), padded with zeros to Dp,
+// and their squared norms in fp32 (one wave per row) ----------------------------------------------
+__global__ __launch_bounds__(256) void shadow_kernel(const float* __restrict__ x, int64_t ldx, uint32_t N, uint32_t D,
+                                                     uint32_t Dp, _Float16* __restrict__ xh, int64_t ldh,
+                                                     float* __restrict__ xn, int vec) {
+    const uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= N) return;
+    const float* row = x + int64_t(r) * ldx;
+    _Float16* out = xh + int64_t(r) * ldh;
+    float ss = 0.0f;
+    for (uint32_t d0 = 0; d0 < Dp; d0 += 256) {
+        const uint32_t d = d0 + 4u * uint32_t(lane);
+        if (d >= Dp) break;
+        f32x4v v = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (vec && d + 3 < D) {
+            v = *reinterpret_cast<const f32x4v*>(row + d);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (d + e < D) v[e] = row[d + e];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ss = fmaf(v[e], v[e], ss);
+        *reinterpret_cast<h4v*>(out + d) = __builtin_convertvector(v, h4v);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    if (lane == 0) xn[r] = ss;
 }
 
 // ---- exact intervals of the screened pairs -----------------------------------------------------
@@ -713,6 +914,20 @@ va_status launch_screen(va_context* ctx, const ScreenArgs& a) {
     return VA_OK;
 }
 
+va_status launch_screen16(va_context* ctx, const ScreenArgs& a) {
+    using namespace s16;
+    const uint64_t nqb = (a.Q + TQ - 1) / TQ;
+    const uint64_t ntb = (a.N + TN - 1) / TN;
+    const uint64_t grid = nqb * ((ntb + kXcds - 1) / kXcds) * kXcds;
+    if (grid == 0) return VA_OK;
+    if (grid > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "screen grid too large (%llu)", (unsigned long long)grid);
+    VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(&screen16_kernel),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, LDS));
+    screen16_kernel<<<dim3(uint32_t(grid)), dim3(256), LDS, ctx->stream>>>(a);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
 va_status launch_bounds(va_context* ctx, const ScreenArgs& a, float* dot, const float* xx_dense, float* xx_list,
                         const uint32_t* cnt, uint32_t n, int64_t ld, uint32_t rows) {
     if (rows == 0 || n == 0) return VA_OK;
@@ -732,6 +947,18 @@ bool offsets_fit(uint64_t ldx, uint32_t D) {
 }
 
 }  // namespace
+
+uint32_t shadow_pitch(uint32_t D) { return padded_dim(D); }
+
+va_status build_shadow(va_context* ctx, const float* x, uint32_t N, uint32_t D, _Float16* shadow, float* norms) {
+    if (N == 0) return VA_OK;
+    const uint32_t Dp = padded_dim(D);
+    const int vec = (D % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
+    shadow_kernel<<<dim3((N + 3) / 4), dim3(256), 0, ctx->stream>>>(x, int64_t(D), N, D, Dp, shadow, int64_t(Dp),
+                                                                   norms, vec);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
 
 bool screen_applies(const va_context* ctx, const ScreenInput& in, uint32_t k) {
     if (ctx->opt_screen == 1) return false;
@@ -820,6 +1047,7 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
         VA_CHECK_STATUS(launch_screen<SCREEN_KEYS>(ctx, a));
         VA_CHECK_STATUS(launch_bounds(ctx, a, reinterpret_cast<float*>(skeys), sxx, nullptr, nullptr, uint32_t(S),
                                       int64_t(S), nq));
+        VA_CHECK_STATUS(mask_dense_keys(ctx, skeys, nq, uint32_t(S), int64_t(S), 0, plan.stride, out.skip));
         SelectArgs sel;
         sel.keys = skeys;
         sel.ld = int64_t(S);
@@ -847,11 +1075,18 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
         a.cand_xx = reinterpret_cast<float*>(clo);
         a.cand_id = cid;
         a.cap = uint32_t(cap);
-        VA_CHECK_STATUS(launch_screen<SCREEN_FILTER>(ctx, a));
+        if (in.xh) {
+            a.xh = in.xh;
+            a.xn = in.xn;
+            VA_CHECK_STATUS(launch_screen16(ctx, a));
+        } else {
+            VA_CHECK_STATUS(launch_screen<SCREEN_FILTER>(ctx, a));
+        }
         VA_CHECK_STATUS(pm.mark(2));
         // (dot, |x|^2) -> (key of hi, key of lo), in place
         VA_CHECK_STATUS(launch_bounds(ctx, a, reinterpret_cast<float*>(chi), nullptr, reinterpret_cast<float*>(clo), cnt,
                                       uint32_t(cap), int64_t(cap), Q));
+        VA_CHECK_STATUS(mask_list_keys(ctx, chi, clo, cid, cnt, Q, uint32_t(cap), int64_t(cap), out.skip));
     }
     ctx->last_scan.scan_launches = 1;
     ctx->last_scan.sample_rows = uint32_t(S);
@@ -900,6 +1135,7 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
         a.gcap = uint32_t(rcap);
         a.gtiles = gtiles;
         VA_CHECK_STATUS(launch_dist(ctx, a));
+        VA_CHECK_STATUS(mask_list_keys(ctx, rkey, nullptr, rr, rcount, Q, uint32_t(rcap), int64_t(rcap), out.skip));
     }
     // ---- 7. exact (key, id) top-k ----------------------------------------------------------------
     {
@@ -923,7 +1159,7 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
         ctx->last_scan.rerank_rows = uint32_t(std::min<uint64_t>(total, 0xFFFFFFFFu));
     }
     if (n_ovf == 0) return pm.finish(true, false);
-    VA_CHECK_STATUS(rescan_rows(ctx, exact, N, k, base, ovf_rows, n_ovf));
+    VA_CHECK_STATUS(rescan_rows(ctx, exact, N, k, base, ovf_rows, n_ovf, out.skip));
     return pm.finish(true, true);
 }
 

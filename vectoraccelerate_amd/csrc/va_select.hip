@@ -303,7 +303,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelectArgs a) {
     // ---- write k slots -----------------------------------------------------------------
     for (uint32_t r = tid; r < a.k; r += SEL_THREADS) {
         const int64_t o = int64_t(orow) * (a.out_ld ? a.out_ld : int64_t(a.k)) + r;
-        const bool have = r < cnt && r < K;
+        const bool have = r < cnt && r < K && okey[r] != kAbsentKey;
         const uint32_t k = have ? okey[r] : 0xFFFFFFFFu;
         if (a.out_idx) a.out_idx[o] = have ? oid[r] + a.id_offset : kSentinel;
         if (a.out_key) a.out_key[o] = k;
