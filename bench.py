@@ -63,6 +63,28 @@ def log(msg: str) -> None:
 
 TRAFFIC_SCREEN = "profiles/hbm_traffic__screen_filter__configs1_cosine_top100.txt"
 TRAFFIC_FP32 = "profiles/hbm_traffic__dist_gemm_filter__configs1_cosine_top100.txt"
+COUNTERS_SCREEN16 = "profiles/counters__screen16_filter__configs1_cosine_top100.txt"
+COUNTERS_SCREEN = "profiles/counters__screen_filter__configs1_cosine_top100.txt"
+COUNTERS_FP32 = "profiles/counters__dist_gemm_filter__configs1_cosine_top100.txt"
+COUNTERS_I8 = "profiles/counters__i8_resq_filter__configs2_int8_top10.txt"
+COUNTERS_HAMMING = "profiles/counters__hamming_mfma_filter__configs3_binary_top100.txt"
+
+
+def counters(rel: str) -> dict:
+    """Per-launch figures of a committed rocprofv3 counter summary (mfma_busy_pct, hbm_gbs,
+    traffic_bytes_per_launch, ...); empty when the file is absent."""
+    f = ROOT / rel
+    out = {}
+    if not f.exists():
+        return out
+    for line in f.read_text().splitlines():
+        if ":" in line and not line.startswith(("#", "rocprofv3")):
+            key, val = line.split(":", 1)
+            try:
+                out[key.strip()] = float(val.split()[0])
+            except (ValueError, IndexError):
+                pass
+    return out
 
 
 def measured_traffic(rel: str = TRAFFIC_SCREEN) -> float | None:
@@ -115,7 +137,8 @@ def run_c2(ctx, a, cpu: bool, extra_l2: bool):
     import numpy as np
     import torch
 
-    from vectoraccelerate_amd import FusedL2TopKKernel, FusedL2TopKParameters, Metric
+    from vectoraccelerate_amd import (AcceleratedVectorIndex, FusedL2TopKKernel, FusedL2TopKParameters,
+                                      IndexConfiguration, Metric, _lib)
 
     N, D, Q, k = 1_000_000, 1536, 1024, 100
     log(f"configs[1]: generating N={N} D={D} Q={Q}")
@@ -128,67 +151,126 @@ def run_c2(ctx, a, cpu: bool, extra_l2: bool):
     q /= q.norm(dim=1, keepdim=True)
     q = q.contiguous()
     torch.cuda.synchronize()
-    kern = FusedL2TopKKernel(ctx)
+    # the index (AcceleratedVectorIndex over va_index_*): rows and their fp16 shadow are built at
+    # insert time, outside the timed region
+    t0 = time.perf_counter()
+    ix = AcceleratedVectorIndex(IndexConfiguration.flat(D, N, metric="cosine"), ctx)
+    ix.insert(vectors=x)
+    ctx.synchronize()
+    insert_s = time.perf_counter() - t0
+    rows = ix._rows()
+    del x
+    torch.cuda.empty_cache()
     idx = ctx.empty((Q, k), torch.int32)
     dist = ctx.empty((Q, k), torch.float32)
-    params = FusedL2TopKParameters(Q, N, D, k)
-    ms, phases = timed(ctx, lambda: kern.encode(q, x, idx, dist, params, Metric.cosine), a.steps, a.warmup)
+    ms, phases = timed(ctx, lambda: ix.searchDevice(q, k, idx, dist), a.steps, a.warmup)
     ph = mean_phases(phases)
     flops = 2.0 * Q * N * D
     tflops = flops / (ph["scan_ms"] * 1e-3) / 1e12
     screened = bool(ph.get("screened", 0))
     peak = PEAK["fp16_mfma_tflops"] if screened else PEAK["fp32_mfma_tflops"]
+    cnt = counters(COUNTERS_SCREEN16 if screened else COUNTERS_FP32)
     res = {
         "ms_per_step": ms,
         "qps": Q / (ms * 1e-3),
         "phases_ms": ph,
         "scan_tflops": tflops,
+        "index_insert_s": insert_s,
         "rank1_is_source_row": float((idx[:, 0].long() == src).float().mean().item()),
         "roofline": {
             "bound": "mfma", "achieved": tflops, "peak": peak, "unit": "TFLOP/s",
             "frac": tflops / peak,
-            "traffic": measured_traffic(TRAFFIC_SCREEN if screened else TRAFFIC_FP32),
-            "traffic_source": TRAFFIC_SCREEN if screened else TRAFFIC_FP32,
-            "kernel": ("screen_kernel<1> (fp16 MFMA screening scan; exact fp32 rerank of a proven band)" if screened
-                       else "dist_gemm_kernel<4, 1, true, 2, true> (fp32 filtering scan)"),
+            "traffic": cnt.get("traffic_bytes_per_launch"),
+            "mfma_busy": cnt.get("mfma_busy_pct"),
+            "hbm_gbs": cnt.get("hbm_gbs"),
+            "counters_source": COUNTERS_SCREEN16 if screened else COUNTERS_FP32,
+            "kernel": ("screen16_kernel (fp16 MFMA screening scan over the index's fp16 shadow; exact fp32 "
+                       "rerank of a proven band)" if screened else "dist_gemm_kernel<4, 1, true, 2, true> (fp32 scan)"),
             "algorithmic": f"2*Q*N*D = {flops:.4g} FLOP per launch",
             "fp32_mfma_equivalent_frac": tflops / PEAK["fp32_mfma_tflops"],
+            "power_limited_ceiling": ("a register-only loop of the same fp16 MFMA on random operands runs at "
+                                      "~1.5 PFLOP/s = 0.6 of the 2.5 PFLOP/s peak on this board (constant "
+                                      "operands: 0.84); see DESIGN.md"),
         },
     }
-    log(f"configs[1] cosine top-100: {ms:.3f} ms/step = {res['qps']:.0f} QPS; scan {ph['scan_ms']:.3f} ms = "
-        f"{tflops:.1f} TFLOP/s ({100 * tflops / peak:.1f}% of the {'fp16' if screened else 'fp32'} MFMA peak)")
-    if screened:
-        # the same search on the fp32 scan alone: it must return the same ids and distances, bit for bit
-        from vectoraccelerate_amd import _lib
+    log(f"configs[1] cosine top-100 (index search): {ms:.3f} ms/step = {res['qps']:.0f} QPS; scan "
+        f"{ph['scan_ms']:.3f} ms = {tflops:.1f} TFLOP/s ({100 * tflops / peak:.1f}% of the "
+        f"{'fp16' if screened else 'fp32'} MFMA peak)")
+    # the same search on the fp32 scan alone: the same ids and distances, bit for bit
+    idx32 = ctx.empty((Q, k), torch.int32)
+    dist32 = ctx.empty((Q, k), torch.float32)
+    ctx.set_option(_lib.VA_OPT_SCREEN, 1)
+    try:
+        ms32, ph32 = timed(ctx, lambda: ix.searchDevice(q, k, idx32, dist32), max(3, a.steps // 2), 1)
+    finally:
+        ctx.set_option(_lib.VA_OPT_SCREEN, 0)
+    s32 = mean_phases(ph32)["scan_ms"]
+    same = bool(torch.equal(idx, idx32)) and bool(torch.equal(dist.view(torch.int32), dist32.view(torch.int32)))
+    c32 = counters(COUNTERS_FP32)
+    res["fp32_scan_only"] = {
+        "ms_per_step": ms32, "qps": Q / (ms32 * 1e-3), "scan_ms": s32,
+        "scan_tflops": flops / (s32 * 1e-3) / 1e12,
+        "mfma_frac": flops / (s32 * 1e-3) / 1e12 / PEAK["fp32_mfma_tflops"],
+        "kernel": "dist_gemm_kernel<4, 1, true, 2, true>",
+        "traffic": c32.get("traffic_bytes_per_launch"), "mfma_busy": c32.get("mfma_busy_pct"),
+        "counters_source": COUNTERS_FP32,
+    }
+    res["screened_equals_fp32_scan"] = same
+    log(f"configs[1] fp32 scan only: {ms32:.3f} ms/step, scan {s32:.3f} ms; screened result identical: {same}")
+    if not same:
+        raise SystemExit("screened search differs from the fp32 scan")
+    del idx32, dist32
+    # the raw-pointer search (va_fused_topk over the fp32 rows, converting them to fp16 in the
+    # scan): the same result again
+    kern = FusedL2TopKKernel(ctx)
+    params = FusedL2TopKParameters(Q, N, D, k)
+    idxr = ctx.empty((Q, k), torch.int32)
+    distr = ctx.empty((Q, k), torch.float32)
+    msr, phr = timed(ctx, lambda: kern.encode(q, rows, idxr, distr, params, Metric.cosine), max(3, a.steps // 2), 1)
+    sr = mean_phases(phr)["scan_ms"]
+    same_r = bool(torch.equal(idx, idxr)) and bool(torch.equal(dist.view(torch.int32), distr.view(torch.int32)))
+    cr = counters(COUNTERS_SCREEN)
+    res["raw_fused_topk"] = {
+        "ms_per_step": msr, "qps": Q / (msr * 1e-3), "scan_ms": sr, "scan_tflops": flops / (sr * 1e-3) / 1e12,
+        "kernel": "screen_kernel<1> (fp32 rows converted in the scan)", "equals_index_search": same_r,
+        "mfma_busy": cr.get("mfma_busy_pct"), "traffic": cr.get("traffic_bytes_per_launch"),
+        "counters_source": COUNTERS_SCREEN,
+    }
+    log(f"configs[1] va_fused_topk over the fp32 rows: {msr:.3f} ms/step, scan {sr:.3f} ms; identical: {same_r}")
+    if not same_r:
+        raise SystemExit("va_fused_topk differs from the index search")
+    # end to end: host queries in, host ids and distances out (pinned buffers, copies on the
+    # context's stream), timed around the whole call
+    qh = torch.empty((Q, D), dtype=torch.float32, pin_memory=True)
+    qh.copy_(q)
+    oh_i = torch.empty((Q, k), dtype=torch.int32, pin_memory=True)
+    oh_d = torch.empty((Q, k), dtype=torch.float32, pin_memory=True)
+    qd = ctx.empty((Q, D), torch.float32)
+    stream = ctx.torch_stream()
 
-        idx32 = ctx.empty((Q, k), torch.int32)
-        dist32 = ctx.empty((Q, k), torch.float32)
-        ctx.set_option(_lib.VA_OPT_SCREEN, 1)
-        try:
-            ms32, ph32 = timed(ctx, lambda: kern.encode(q, x, idx32, dist32, params, Metric.cosine),
-                               max(3, a.steps // 2), 1)
-        finally:
-            ctx.set_option(_lib.VA_OPT_SCREEN, 0)
-        s32 = mean_phases(ph32)["scan_ms"]
-        same = bool(torch.equal(idx, idx32)) and bool(torch.equal(dist.view(torch.int32), dist32.view(torch.int32)))
-        res["fp32_scan_only"] = {
-            "ms_per_step": ms32, "qps": Q / (ms32 * 1e-3), "scan_ms": s32,
-            "scan_tflops": flops / (s32 * 1e-3) / 1e12,
-            "mfma_frac": flops / (s32 * 1e-3) / 1e12 / PEAK["fp32_mfma_tflops"],
-            "kernel": "dist_gemm_kernel<4, 1, true, 2, true>",
-            "traffic": measured_traffic(TRAFFIC_FP32), "traffic_source": TRAFFIC_FP32,
-        }
-        res["screened_equals_fp32_scan"] = same
-        log(f"configs[1] fp32 scan only: {ms32:.3f} ms/step, scan {s32:.3f} ms; screened result identical: {same}")
-        if not same:
-            raise SystemExit("screened search differs from the fp32 scan")
-        del idx32, dist32
+    def e2e():
+        with torch.cuda.stream(stream):
+            qd.copy_(qh, non_blocking=True)
+        ix.searchDevice(qd, k, idxr, distr)
+        with torch.cuda.stream(stream):
+            oh_i.copy_(idxr, non_blocking=True)
+            oh_d.copy_(distr, non_blocking=True)
+
+    mse, _ = timed(ctx, e2e, max(3, a.steps // 2), 1, scan_timings=False)
+    same_e = bool(torch.equal(oh_i, idx.cpu())) and bool(torch.equal(oh_d.view(torch.int32), dist.cpu().view(torch.int32)))
+    res["end_to_end"] = {"ms_per_step": mse, "qps": Q / (mse * 1e-3), "equals_resident": same_e,
+                         "host_bytes_per_step": Q * D * 4 + Q * k * 8,
+                         "what": "pinned host queries -> device -> index search -> pinned host ids + distances"}
+    log(f"configs[1] end to end (host queries in, host results out): {mse:.3f} ms/step = {Q / (mse * 1e-3):.0f} "
+        f"QPS; identical: {same_e}")
+    del qh, oh_i, oh_d, qd
     if extra_l2:
         # the same search with the database in pinned host memory, streamed through the device
         # (va_fused_topk_streamed): bound by the host link, not by HBM or the MFMA
         xh = torch.empty((N, D), dtype=torch.float32, pin_memory=True)
-        xh.copy_(x)
-        torch.cuda.synchronize()
+        ctx.check(ctx.lib.va_buffer_download(ctx.handle, xh.data_ptr(), rows.data_ptr(), N * D * 4),
+                  "va_buffer_download")
+        ctx.synchronize()
         idx_s = ctx.empty((Q, k), torch.int32)
         dist_s = ctx.empty((Q, k), torch.float32)
         ms_s, _ = timed(ctx, lambda: kern.encodeStreamed(q, xh, idx_s, dist_s, params, Metric.cosine), 2, 1,
@@ -206,19 +288,22 @@ def run_c2(ctx, a, cpu: bool, extra_l2: bool):
         idx10 = ctx.empty((Q, 10), torch.int32)
         dist10 = ctx.empty((Q, 10), torch.float32)
         p10 = FusedL2TopKParameters(Q, N, D, 10)
-        ms10, ph10 = timed(ctx, lambda: kern.encode(q, x, idx10, dist10, p10, Metric.euclideanSquared),
+        ms10, ph10 = timed(ctx, lambda: kern.encode(q, rows, idx10, dist10, p10, Metric.euclideanSquared),
                            max(3, a.steps // 2), 1)
         s10 = mean_phases(ph10)["scan_ms"]
-        res["l2sq_top10_same_shape"] = {"ms_per_step": ms10, "qps": Q / (ms10 * 1e-3), "scan_ms": s10,
-                                        "scan_tflops": flops / (s10 * 1e-3) / 1e12,
-                                        "mfma_frac": flops / (s10 * 1e-3) / 1e12 / peak}
-        log(f"configs[1] shape, L2^2 top-10: {ms10:.3f} ms/step, scan {s10:.3f} ms")
+        res["l2sq_top10_same_shape_raw"] = {"ms_per_step": ms10, "qps": Q / (ms10 * 1e-3), "scan_ms": s10,
+                                            "scan_tflops": flops / (s10 * 1e-3) / 1e12,
+                                            "mfma_frac": flops / (s10 * 1e-3) / 1e12 / peak}
+        log(f"configs[1] shape, L2^2 top-10 (va_fused_topk): {ms10:.3f} ms/step, scan {s10:.3f} ms")
     if cpu:
         from oracle import oracle
 
         nq = 512
         log(f"configs[1] CPU baseline: {nq} queries on {oracle.num_threads()} threads")
-        xh = x.cpu().numpy()
+        xh = np.empty((N, D), np.float32)
+        ctx.check(ctx.lib.va_buffer_download(ctx.handle, xh.ctypes.data, rows.data_ptr(), N * D * 4),
+                  "va_buffer_download")
+        ctx.synchronize()
         qh = q[:nq].cpu().numpy()
         t0 = time.perf_counter()
         ci, _ = oracle.flat_topk(oracle.COSINE, qh, xh, k, accum_double=False)
@@ -233,7 +318,8 @@ def run_c2(ctx, a, cpu: bool, extra_l2: bool):
         }
         log(f"configs[1] CPU baseline: {nq / dt:.2f} QPS ({dt:.1f} s)")
         del xh
-    del x, q
+    del q, rows
+    ix.close()
     torch.cuda.empty_cache()
     return res
 
@@ -624,6 +710,7 @@ def main() -> int:
         "data": "synthetic (torch seeded generators, BASELINE configs constructions)",
         "config": {
             "workload": "BASELINE configs[1]: flat cosine top-100, N=1,000,000 x d=1536 fp32, Q=1024",
+            "search": "AcceleratedVectorIndex.search over the native index (va_index_search)",
             "N": 1_000_000, "D": 1536, "Q": 1024, "k": 100, "metric": "cosine (1 - s)",
             "parallelism": "single GPU",
         },

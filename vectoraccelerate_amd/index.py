@@ -181,16 +181,24 @@ class AcceleratedVectorIndex:
     def insert(self, vector=None, metadata=None, vectors=None):
         """insert(vector) -> VectorHandle, or insert(vectors=[...]) -> [VectorHandle]."""
         batch = vectors is not None
-        arr = np.asarray(vectors if batch else [vector], np.float32)
-        if arr.ndim != 2 or arr.shape[1] != self.dimension:
-            got = arr.shape[-1] if arr.ndim >= 1 else 0
-            raise VectorError.dimensionMismatch(self.dimension, got)
-        n = arr.shape[0]
+        c = self.context
+        if batch and getattr(vectors, "is_cuda", False):
+            # rows already on the device (fp32 [n x D] tensor): no host round trip
+            torch = _torch()
+            if vectors.dim() != 2 or vectors.shape[1] != self.dimension:
+                raise VectorError.dimensionMismatch(self.dimension, vectors.shape[-1])
+            dev = vectors.to(torch.float32).contiguous()
+            n = dev.shape[0]
+        else:
+            arr = np.asarray(vectors if batch else [vector], np.float32)
+            if arr.ndim != 2 or arr.shape[1] != self.dimension:
+                got = arr.shape[-1] if arr.ndim >= 1 else 0
+                raise VectorError.dimensionMismatch(self.dimension, got)
+            n = arr.shape[0]
+            dev = c.buffer(np.ascontiguousarray(arr)) if n else None
         if n == 0:
             return []
-        c = self.context
         first = self._info().slots
-        dev = c.buffer(np.ascontiguousarray(arr))
         out = np.zeros(n, np.uint32)
         c.order_after_torch()
         c.check(c.lib.va_index_insert(c.handle, self._h, dptr(dev), n, out.ctypes.data), "va_index_insert")
