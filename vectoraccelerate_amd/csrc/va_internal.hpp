@@ -399,7 +399,9 @@ struct ScanPlan {
     uint64_t cap = 0;
     uint32_t qs = 1;
 };
-ScanPlan plan_scan(const va_context* ctx, uint32_t Q, uint32_t N, uint32_t k);
+// screened: the plan of the fp16 screening scan, whose candidate appends cost more than its
+// sample pass up to a sample of N/32 rows (N/64 otherwise)
+ScanPlan plan_scan(const va_context* ctx, uint32_t Q, uint32_t N, uint32_t k, bool screened = false);
 
 // Exact top-k of the listed query rows (device list) by dense keys over the whole database in
 // chunks (the path of queries whose candidate list overflowed).  Writes base's outputs at the

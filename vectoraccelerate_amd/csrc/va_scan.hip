@@ -76,14 +76,15 @@ size_t dense_budget(const va_context* ctx) {
     return ctx->fixed_scratch ? std::min(kArena, ctx->fixed_scratch_bytes / 4) : kArena;
 }
 
-ScanPlan plan_scan(const va_context* ctx, uint32_t Q, uint32_t N, uint32_t k) {
+ScanPlan plan_scan(const va_context* ctx, uint32_t Q, uint32_t N, uint32_t k, bool screened) {
     ScanPlan p;
-    // Sample size: N/64 rows keeps ~64k candidates per query, but the dense sample costs Q*S
-    // keys, so it is capped at dense_budget() bytes of keys in total (16384 rows minimum).
+    // Sample size: N/64 rows (N/32 for the screening scan) keeps ~64k (~32k) candidates per
+    // query, but the dense sample costs Q*S keys, so it is capped at dense_budget() bytes of keys
+    // in total (16384 rows minimum).
     const uint64_t budget = dense_budget(ctx);
     p.S = ctx->opt_sample_rows
               ? ctx->opt_sample_rows
-              : std::max<uint64_t>(kMinSample, std::min<uint64_t>(N / 64, budget / 4 / Q));
+              : std::max<uint64_t>(kMinSample, std::min<uint64_t>(N / (screened ? 32 : 64), budget / 4 / Q));
     p.direct = p.S >= N;
     if (p.direct) return p;
     p.stride = uint32_t(N / p.S);

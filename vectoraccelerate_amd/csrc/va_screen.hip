@@ -275,9 +275,42 @@ __device__ __forceinline__ void filter_epilogue(const ScreenArgs& a, f32x16 (&ac
                     dump[(16 * b + 4 * m + j) * 64 + lane] = v;
                 }
     };
+    // Quick rejection: the pre-test's right-hand side A|x|^2 + B|x| + C over the lane's 64 rows is
+    // bounded below by its value at the corner of their (|x|^2, |x|) box that A's and B's signs
+    // select (fp32 fma is monotone in each argument for a multiplier of fixed sign), so a lane
+    // whose largest value is below that bound passes nothing.  Flagged (NaN) rows disable it.
+    float bxlo = INFINITY, bxhi = -INFINITY, bnlo = INFINITY, bnhi = -INFINITY;
+    bool bflag = false;
+#pragma unroll 1
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = wn * 128 + 32 * m + 8 * j + 4 * hh;
+            const f32x4v xx = *reinterpret_cast<const f32x4v*>(xxp + r);
+            const f32x4v nx = *reinterpret_cast<const f32x4v*>(nxp + r);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                bflag |= !(xx[e] == xx[e]) || !(nx[e] == nx[e]);
+                bxlo = fminf(bxlo, xx[e]);
+                bxhi = fmaxf(bxhi, xx[e]);
+                bnlo = fminf(bnlo, nx[e]);
+                bnhi = fmaxf(bnhi, nx[e]);
+            }
+        }
     auto test_block = [&](int n) -> uint64_t {
         const PreTest pt = pretest_consts(a, qinf[n], qthr[n]);
         const f32x4v* src = dump + 16 * (n & 1) * 64 + lane;
+        if (!bflag) {
+            const float lo = fmaf(pt.A, pt.A >= 0.0f ? bxlo : bxhi, fmaf(pt.B, pt.B >= 0.0f ? bnlo : bnhi, pt.C));
+            float mx = -INFINITY;
+#pragma unroll 4
+            for (int i = 0; i < 16; ++i) {
+                const f32x4v v = src[i * 64];
+                mx = fmaxf(mx, fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+            }
+            if (mx < lo) return 0;
+            asm volatile("" ::: "memory");  // the full test re-reads the values
+        }
         uint64_t mk = 0;
 #pragma unroll
         for (int m = 0; m < 4; ++m)
@@ -295,9 +328,16 @@ __device__ __forceinline__ void filter_epilogue(const ScreenArgs& a, f32x16 (&ac
             }
         return (uint32_t(wq * 128 + 32 * n + l32) < qc) ? (mk & valid) : 0;
     };
+    // lanes l and l + 32 hold the same query (the two row halves of each 8-row group): one
+    // atomic reserves the pair's passes, and the second lane takes the places after the first's
     auto reserve = [&](int n, uint64_t mk) -> uint32_t {
         const uint32_t qi = qs + uint32_t(wq * 128 + 32 * n + l32);
-        return mk ? atomicAdd(a.cnt + qi, uint32_t(__popcll(mk))) : 0u;
+        const uint32_t c = uint32_t(__popcll(mk));
+        const uint32_t other = uint32_t(__shfl_xor(int(c), 32));
+        uint32_t base = 0;
+        if (hh == 0 && c + other) base = atomicAdd(a.cnt + qi, c + other);
+        base = uint32_t(__shfl(int(base), l32));
+        return hh ? base + other : base;
     };
     auto append = [&](int n, uint64_t mk, uint32_t pos) {
         const uint32_t qi = qs + uint32_t(wq * 128 + 32 * n + l32);
@@ -680,6 +720,15 @@ __global__ __launch_bounds__(256, 1) void screen16_kernel(ScreenArgs a) {
             lds_dma16(xres, ok ? off[i] + d0 * 2u : kDmaSkip, sb + uint32_t(OPB) + grp * 1024u);
         }
     };
+    // L2 prefetch of the rows of stage s+2, issued with the direct loads of stage s+1: one dword
+    // per 128-byte line (lane L of wave w takes row 64w + L) into a sink that nothing reads, so
+    // the direct loads of the next stage find the rows in L2
+    __shared__ __attribute__((aligned(256))) char pf_sink[4 * 256];
+    const uint32_t pf_off = uint32_t(64 * wave + lane) * a.Dp * 2u;
+    auto prefetch = [&](uint32_t s) {
+        const uint32_t d0 = s * KC;
+        lds_dma4(xres, d0 < a.Dp ? pf_off + d0 * 2u : kDmaSkip, lds_addr_of(pf_sink + wave * 256));
+    };
     // fragment rows start at multiples of 32, so the chunk swizzle is (l32 >> 1) & 7 for both
     const int swz = (l32 >> 1) & 7;
     const uint32_t a_off = uint32_t(OPB + (wn * 128 + l32) * ROWB);
@@ -732,7 +781,8 @@ __global__ __launch_bounds__(256, 1) void screen16_kernel(ScreenArgs a) {
 
     issue(0);
     issue(1);
-    wait_vmcnt<2 * LPW>();  // stage 0 (older than stage 1's loads)
+    prefetch(2);
+    wait_vmcnt<2 * LPW + 1>();  // stage 0 (older than stage 1's loads and the prefetch)
     barrier();
     read_frags(0, 0, 0);
     for (uint32_t s = 0; s < nst; ++s) {
@@ -745,13 +795,15 @@ __global__ __launch_bounds__(256, 1) void screen16_kernel(ScreenArgs a) {
                 mma(cur);
                 interleave();
             } else {
-                // this k-step's fragments are in registers: publish stage s+1, free slot s
-                wait_vmcnt<0>();
+                // this k-step's fragments are in registers: publish stage s+1, free slot s (the
+                // one load younger than stage s+1's is the prefetch issued after them)
+                wait_vmcnt<1>();
                 barrier();
                 read_frags(cur ^ 1, slot ^ 1u, 0);
                 mma(cur);
                 interleave();
                 issue(s + 2);  // past the last stage: zeros into the free slot
+                prefetch(s + 3);
             }
         }
     }
@@ -964,7 +1016,7 @@ bool screen_applies(const va_context* ctx, const ScreenInput& in, uint32_t k) {
     if (ctx->opt_screen == 1) return false;
     if (in.op != OP_L2SQ && in.op != OP_L2 && in.op != OP_COS_DIST && in.op != OP_NEG_DOT) return false;
     if (in.D % 4 != 0 || (reinterpret_cast<uintptr_t>(in.x) & 15) != 0) return false;
-    const ScanPlan plan = plan_scan(ctx, in.Q, in.N, k);
+    const ScanPlan plan = plan_scan(ctx, in.Q, in.N, k, true);
     if (plan.direct) return false;
     if (!offsets_fit(uint64_t(plan.stride) * in.D, in.D)) return false;
     if (ctx->opt_screen == 2) return true;
@@ -976,7 +1028,7 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
                              const ScanOutputs& out) {
     const uint32_t Q = in.Q, N = in.N, D = in.D;
     const uint32_t Dp = padded_dim(D);
-    const ScanPlan plan = plan_scan(ctx, Q, N, k);
+    const ScanPlan plan = plan_scan(ctx, Q, N, k, true);
     const uint64_t S = plan.S;
     const uint64_t cap = plan.cap;
     // rerank capacity: k plus the band of rows whose interval straddles the k-th bound (the
