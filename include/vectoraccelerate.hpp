@@ -12,6 +12,8 @@
  *   ScalarQuantizationKernel   Kernels/Metal4/ScalarQuantizationKernel.swift (per-dimension int8)
  *   BinaryQuantizationKernel   Kernels/Metal4/BinaryQuantizationKernel.swift + HammingDistanceKernel.swift
  *   IVFIndex                   Index/Kernels/IVF/IVFSearchPipeline.swift + Index/Internal/IVFStructure.swift
+ *   AcceleratedVectorIndex     Index/AcceleratedVectorIndex.swift (flat: handles, removal, compaction, filters)
+ *   MetalComputeProvider       Integration/MetalComputeProvider.swift (batchDistance, findNearest)
  *   KMeansPipeline             Index/Kernels/Clustering/KMeansPipeline.swift
  *   ProductQuantizationKernel  Kernels/Metal4/ProductQuantizationKernel.swift
  * Every call checks the status and throws VectorError with the library's message.
@@ -19,6 +21,7 @@
 #ifndef VECTORACCELERATE_HPP
 #define VECTORACCELERATE_HPP
 
+#include <algorithm>
 #include <cstdint>
 #include <stdexcept>
 #include <string>
@@ -158,6 +161,145 @@ class FusedL2TopKKernel {
 
    private:
     const Context& ctx_;
+};
+
+// MetalComputeProvider (Integration/MetalComputeProvider.swift:119-269): the VectorCore façade.
+// batchDistance: euclidean -> L2 distance, cosine -> 1 - similarity, dotProduct -> raw dot;
+// findNearest: the min(k, count) nearest (index, distance) pairs, nearest first (dotProduct:
+// largest dot first, raw dot reported); with dotProductAsDistance (VectorCore's
+// DotProductDistance through the BatchKernelProvider conformance) -dot, ascending.
+// Manhattan / chebyshev have no GPU kernel here and are not offered.
+class MetalComputeProvider {
+   public:
+    enum class Metric { euclidean, cosine, dotProduct };
+    explicit MetalComputeProvider(const Context& c) : ctx_(c) {}
+
+    std::vector<float> batchDistance(const std::vector<float>& query, const Matrix& candidates, Metric metric,
+                                     bool dotProductAsDistance = false) const {
+        if (candidates.rows == 0) return {};
+        Matrix q{query, 1, uint32_t(query.size())};
+        std::vector<float> row = distanceMatrix(q, candidates, metric);
+        if (metric == Metric::dotProduct && dotProductAsDistance)
+            for (float& v : row) v = -v;
+        return row;
+    }
+    // queries x candidates, row-major
+    std::vector<float> distanceMatrix(const Matrix& queries, const Matrix& candidates, Metric metric) const {
+        if (queries.rows == 0 || candidates.rows == 0) return {};
+        check_dims(queries, candidates);
+        DeviceBuffer<float> q(ctx_, queries.data), x(ctx_, candidates.data);
+        DeviceBuffer<float> out(ctx_, size_t(queries.rows) * candidates.rows);
+        const uint32_t Q = queries.rows, N = candidates.rows, D = queries.dim;
+        va_status st = metric == Metric::euclidean ? va_l2_all_pairs(ctx_.handle(), q.data(), x.data(), out.data(), Q, N, D, 1)
+                       : metric == Metric::cosine ? va_cosine_all_pairs(ctx_.handle(), q.data(), x.data(), out.data(), Q, N, D, 1)
+                                                  : va_dot_all_pairs(ctx_.handle(), q.data(), x.data(), out.data(), Q, N, D, 0);
+        ctx_.check(st, "MetalComputeProvider.distanceMatrix");
+        return out.download();
+    }
+    std::vector<std::pair<uint32_t, float>> findNearest(const std::vector<float>& query, const Matrix& candidates,
+                                                        uint32_t k, Metric metric,
+                                                        bool dotProductAsDistance = false) const {
+        Matrix q{query, 1, uint32_t(query.size())};
+        auto all = findNearestBatch(q, candidates, k, metric, dotProductAsDistance);
+        return all.empty() ? std::vector<std::pair<uint32_t, float>>{} : all[0];
+    }
+    std::vector<std::vector<std::pair<uint32_t, float>>> findNearestBatch(const Matrix& queries,
+                                                                         const Matrix& candidates, uint32_t k,
+                                                                         Metric metric,
+                                                                         bool dotProductAsDistance = false) const {
+        std::vector<std::vector<std::pair<uint32_t, float>>> out(queries.rows);
+        if (k == 0 || candidates.rows == 0 || queries.rows == 0) return out;
+        check_dims(queries, candidates);
+        const uint32_t kk = std::min<uint32_t>(std::min<uint32_t>(k, candidates.rows), VA_MAX_K);
+        const va_metric vm = metric == Metric::euclidean ? VA_METRIC_L2
+                             : metric == Metric::cosine  ? VA_METRIC_COSINE
+                                                         : VA_METRIC_DOT;
+        SearchResult r = FusedL2TopKKernel(ctx_).findNearestNeighbors(queries, candidates, kk, vm);
+        const bool raw_dot = metric == Metric::dotProduct && !dotProductAsDistance;
+        for (uint32_t i = 0; i < queries.rows; ++i)
+            for (auto& p : r.results(i)) out[i].emplace_back(p.first, raw_dot ? -p.second : p.second);
+        return out;
+    }
+
+   private:
+    static void check_dims(const Matrix& a, const Matrix& b) {
+        if (a.dim != b.dim)
+            throw VectorError(VA_ERR_INVALID_ARG,
+                              "All candidates must match the query dimension (" + std::to_string(a.dim) + ")");
+    }
+    const Context& ctx_;
+};
+
+// AcceleratedVectorIndex (flat) over va_index_* (Index/AcceleratedVectorIndex.swift:481-1265):
+// stable handles in insertion order, removal, compaction, plain and filtered search.
+class AcceleratedVectorIndex {
+   public:
+    AcceleratedVectorIndex(const Context& c, uint32_t dim, uint32_t capacity = 10000, va_metric metric = VA_METRIC_L2SQ)
+        : ctx_(c), metric_(metric) {
+        ctx_.check(va_index_create(ctx_.handle(), dim, capacity, &h_), "va_index_create");
+    }
+    ~AcceleratedVectorIndex() {
+        if (h_) va_index_destroy(h_);
+    }
+    AcceleratedVectorIndex(const AcceleratedVectorIndex&) = delete;
+    AcceleratedVectorIndex& operator=(const AcceleratedVectorIndex&) = delete;
+    va_index* handle() const { return h_; }
+    // insert(contentsOf:): host rows -> their handles
+    std::vector<uint32_t> insert(const Matrix& vectors) {
+        std::vector<uint32_t> hs(vectors.rows);
+        if (vectors.rows == 0) return hs;
+        DeviceBuffer<float> d(ctx_, vectors.data);
+        ctx_.check(va_index_insert(ctx_.handle(), h_, d.data(), vectors.rows, hs.data()), "va_index_insert");
+        ctx_.synchronize();  // the staging buffer is released on return
+        return hs;
+    }
+    uint32_t remove(const std::vector<uint32_t>& handles) {
+        uint32_t n = 0;
+        ctx_.check(va_index_remove(ctx_.handle(), h_, handles.data(), uint32_t(handles.size()), &n), "va_index_remove");
+        return n;
+    }
+    void compact() { ctx_.check(va_index_compact(ctx_.handle(), h_), "va_index_compact"); }
+    va_index_info info() const {
+        va_index_info i{};
+        ctx_.check(va_index_get_info(h_, &i), "va_index_get_info");
+        return i;
+    }
+    uint32_t count() const { return info().count; }
+    bool contains(uint32_t handle) const { return va_index_contains(h_, handle) != 0; }
+    std::vector<float> vector(uint32_t handle) const {
+        std::vector<float> v(info().dimension);
+        ctx_.check(va_index_get_vector(ctx_.handle(), h_, handle, v.data()), "va_index_get_vector");
+        return v;
+    }
+    // search(queries:k:): handles in SearchResult::indices (VA_SENTINEL_INDEX past the live count)
+    SearchResult search(const Matrix& queries, uint32_t k) const {
+        DeviceBuffer<float> q(ctx_, queries.data);
+        DeviceBuffer<uint32_t> idx(ctx_, size_t(queries.rows) * k);
+        DeviceBuffer<float> dist(ctx_, size_t(queries.rows) * k);
+        ctx_.check(va_index_search(ctx_.handle(), h_, metric_, q.data(), queries.rows, k, idx.data(), dist.data()),
+                   "va_index_search");
+        return SearchResult{idx.download(), dist.download(), queries.rows, k};
+    }
+    // search(query:k:filter:): the k nearest vectors the filter accepts, nearest first
+    template <class Filter>
+    std::vector<std::pair<uint32_t, float>> search(const std::vector<float>& query, uint32_t k, Filter filter) const {
+        DeviceBuffer<float> q(ctx_, query);
+        std::vector<uint32_t> hs(k);
+        std::vector<float> ds(k);
+        uint32_t n = 0;
+        auto tramp = [](uint32_t h, void* user) -> int { return (*static_cast<Filter*>(user))(h) ? 1 : 0; };
+        ctx_.check(va_index_search_filtered(ctx_.handle(), h_, metric_, q.data(), k, tramp, &filter, hs.data(),
+                                            ds.data(), &n, nullptr),
+                   "va_index_search_filtered");
+        std::vector<std::pair<uint32_t, float>> r;
+        for (uint32_t i = 0; i < n; ++i) r.emplace_back(hs[i], ds[i]);
+        return r;
+    }
+
+   private:
+    const Context& ctx_;
+    va_metric metric_;
+    va_index* h_ = nullptr;
 };
 
 class TopKSelectionKernel {

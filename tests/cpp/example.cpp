@@ -72,6 +72,40 @@ int main(int argc, char** argv) {
         save(dir + "/pq_codes.bin", codes.download());
         save(dir + "/pq_idx.bin", pr.indices);
 
+        // MetalComputeProvider: distances of query 0 and the nearest candidates of every query
+        va::MetalComputeProvider prov(ctx);
+        std::vector<float> q0(q.data.begin(), q.data.begin() + D);
+        save(dir + "/prov_l2.bin", prov.batchDistance(q0, x, va::MetalComputeProvider::Metric::euclidean));
+        save(dir + "/prov_cos.bin", prov.batchDistance(q0, x, va::MetalComputeProvider::Metric::cosine));
+        save(dir + "/prov_dot.bin", prov.batchDistance(q0, x, va::MetalComputeProvider::Metric::dotProduct));
+        std::vector<uint32_t> nn;
+        std::vector<float> nd;
+        for (auto m : {va::MetalComputeProvider::Metric::euclidean, va::MetalComputeProvider::Metric::cosine,
+                       va::MetalComputeProvider::Metric::dotProduct})
+            for (auto& row : prov.findNearestBatch(q, x, k, m))
+                for (auto& p : row) {
+                    nn.push_back(p.first);
+                    nd.push_back(p.second);
+                }
+        save(dir + "/prov_nn_idx.bin", nn);
+        save(dir + "/prov_nn_dist.bin", nd);
+
+        // AcceleratedVectorIndex: handles, removal of every 7th vector, search, filtered search
+        va::AcceleratedVectorIndex index(ctx, D, 16);
+        std::vector<uint32_t> hs = index.insert(x);
+        std::vector<uint32_t> gone;
+        for (uint32_t i = 0; i < N; i += 7) gone.push_back(hs[i]);
+        const uint32_t removed = index.remove(gone);
+        va::SearchResult ir = index.search(q, k);
+        save(dir + "/index_idx.bin", ir.indices);
+        auto odd = [](uint32_t h) { return (h & 1u) == 1u; };
+        std::vector<uint32_t> fi;
+        for (auto& p : index.search(q0, k, odd)) fi.push_back(p.first);
+        save(dir + "/index_filtered_idx.bin", fi);
+        index.compact();
+        std::ofstream(dir + "/index_counts.txt") << removed << " " << index.count() << " " << index.contains(hs[0])
+                                                 << " " << index.contains(hs[1]);
+
         std::string kind = "none";
         try {
             topk.findNearestNeighbors(q, x, 0);

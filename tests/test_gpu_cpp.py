@@ -55,3 +55,29 @@ def test_cpp_mirror_matches_oracle(tmp_path, oracle):
     pi, _ = oracle.pq_search(q, cb, codes, 4, 16, k)
     np.testing.assert_array_equal(rd("pq_idx", np.uint32).reshape(Q, k), pi)
     assert (tmp_path / "error_kind.txt").read_text() == "invalidInput"
+    # MetalComputeProvider: sqrt L2, 1 - cosine similarity, raw dot; nearest first
+    np.testing.assert_allclose(rd("prov_l2", np.float32), np.sqrt(((x - q[0]) ** 2).sum(1)), rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(rd("prov_cos", np.float32), oracle.distance_matrix("cos_dist", q[:1], x)[0], atol=1e-4)
+    np.testing.assert_allclose(rd("prov_dot", np.float32), x.astype(np.float64) @ q[0].astype(np.float64), rtol=1e-4,
+                               atol=1e-3)
+    nn = rd("prov_nn_idx", np.uint32).reshape(3, Q, k)
+    nd = rd("prov_nn_dist", np.float32).reshape(3, Q, k)
+    oi, od = oracle.flat_topk(oracle.L2, q, x, k)
+    check_topk(oracle.L2, q, x, k, nn[0], nd[0], oi, od)
+    oi, od = oracle.flat_topk(oracle.COSINE, q, x, k)
+    check_topk(oracle.COSINE, q, x, k, nn[1], nd[1], oi, od)
+    oi, od = oracle.flat_topk(oracle.DOT, q, x, k)
+    check_topk(oracle.DOT, q, x, k, nn[2], -nd[2], oi, od)  # raw dot reported, largest first
+    # AcceleratedVectorIndex: the live vectors (every 7th removed) in handle space
+    live = np.array([i for i in range(N) if i % 7], np.int64)
+    gi = rd("index_idx", np.uint32).reshape(Q, k).astype(np.int64)
+    assert np.isin(gi, live).all()
+    oi, od = oracle.flat_topk(L2SQ, q, x[live], k)
+    check_topk(L2SQ, q, x[live], k, np.searchsorted(live, gi).astype(np.uint32), None, oi, od)
+    odd_live = np.array([i for i in live if i % 2 == 1], np.int64)
+    gf = rd("index_filtered_idx", np.uint32).astype(np.int64)
+    assert gf.shape == (k,) and np.isin(gf, odd_live).all()
+    oi, od = oracle.flat_topk(L2SQ, q[:1], x[odd_live], k)
+    check_topk(L2SQ, q[:1], x[odd_live], k, np.searchsorted(odd_live, gf)[None].astype(np.uint32), None, oi, od)
+    removed, count, c0, c1 = (tmp_path / "index_counts.txt").read_text().split()
+    assert (int(removed), int(count), c0, c1) == (len(range(0, N, 7)), len(live), "0", "1")

@@ -28,6 +28,13 @@ from .index import (
     VectorHandle,
 )
 from .clustering import KMeansConfiguration, KMeansPipeline, KMeansPlusPlusKernel, KMeansResult
+from .provider import (
+    CosineDistance,
+    DotProductDistance,
+    EuclideanDistance,
+    MetalComputeProvider,
+    SupportedDistanceMetric,
+)
 from .pq import Metal4EncodedVectors, Metal4PQConfig, Metal4PQModel, ProductQuantizationKernel
 from .ivf import IVFGPUIndexStructure, IVFSearchConfiguration, IVFSearchPipeline, IVFSearchResult
 from .quantization import (
@@ -43,6 +50,11 @@ from .quantization import (
 )
 
 __all__ = [
+    "MetalComputeProvider",
+    "SupportedDistanceMetric",
+    "EuclideanDistance",
+    "CosineDistance",
+    "DotProductDistance",
     "AcceleratedVectorIndex",
     "IndexConfiguration",
     "IndexSearchResult",
