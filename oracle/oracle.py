@@ -122,6 +122,22 @@ def sq_params_per_dim(x):
     return mn, mx, sc, zp
 
 
+def sq_global_params(x, asymmetric: bool):
+    """(scale, zero point) of the global int8 quantization (zero point 0 when symmetric)."""
+    x = _f32(np.asarray(x, np.float32).reshape(-1))
+    scale = np.empty(1, np.float32)
+    zp = np.empty(1, np.int32)
+    lib().vo_sq_global_params(_p(x), _i(x.size), C.c_int(int(asymmetric)), _p(scale), _p(zp))
+    return np.float32(scale[0]), int(zp[0])
+
+
+def sq_global_quantize(x, asymmetric: bool):
+    """Global int8 codes of a flat array: (codes, scale, zero point)."""
+    scale, zp = sq_global_params(x, asymmetric)
+    flat = np.asarray(x, np.float32).reshape(-1, 1)
+    return sq_quantize(flat, [scale], [zp]).reshape(-1), scale, zp
+
+
 def sq_quantize(x, scale, zp):
     x = _f32(x)
     N, D = x.shape
@@ -235,6 +251,18 @@ def kmeans_fit(x, init, max_iter, threshold):
     lib().vo_kmeans_fit(_p(x), _i(N), _i(D), _i(C_), _p(init), _i(max_iter), C.c_float(threshold), _p(cen),
                         _p(assign), _p(dist), _p(counts), _p(iu), _p(fi))
     return cen, assign, dist, counts, int(iu[0]), bool(iu[1]), float(fi[0]), float(fi[1])
+
+
+def kmeans_update(x, assign, dist, old):
+    """One k-means update given an assignment: (centroids, counts)."""
+    x, old, dist = _f32(x), _f32(old), _f32(dist)
+    assign = np.ascontiguousarray(assign, np.uint32)
+    N, D = x.shape
+    C_ = old.shape[0]
+    cen = np.empty((C_, D), np.float32)
+    counts = np.empty(C_, np.uint32)
+    lib().vo_kmeans_update(_p(x), _i(N), _i(D), _i(C_), _p(assign), _p(dist), _p(old), _p(cen), _p(counts))
+    return cen, counts
 
 
 def kmeans_plusplus(x, k, seed):

@@ -398,6 +398,33 @@ static inline int8_t quantize_one(float v, float s, int32_t z) {
     return (int8_t)r;
 }
 
+/* computeQuantizationParams (Kernels/Metal4/ScalarQuantizationKernel.swift:496-520), int8 branch,
+ * over all n values: symmetric scale = max(max(|min|, |max|) / 127, 1e-8), no zero point;
+ * asymmetric scale = max((max - min) / 255, 1e-8), zero point = Int8(clamping: Int(-round(min /
+ * scale))) with Swift's round (half away from zero, as C roundf) and a saturating conversion. */
+void vo_sq_global_params(const float* x, int64_t n, int asymmetric, float* scale, int32_t* zero_point) {
+    float mn = 0.0f, mx = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+        if (i == 0 || x[i] < mn) mn = x[i];
+        if (i == 0 || x[i] > mx) mx = x[i];
+    }
+    if (asymmetric) {
+        float range = mx - mn;
+        float s = range / 255.0f;
+        s = s > 1e-8f ? s : 1e-8f;
+        float r = -roundf(mn / s);
+        int32_t z = r >= 127.0f ? 127 : (r <= -128.0f ? -128 : (int32_t)r);
+        *scale = s;
+        *zero_point = z;
+    } else {
+        float amin = fabsf(mn), amax = fabsf(mx);
+        float absmax = amin > amax ? amin : amax;
+        float s = absmax / 127.0f;
+        *scale = s > 1e-8f ? s : 1e-8f;
+        *zero_point = 0;
+    }
+}
+
 void vo_sq_quantize(const float* x, int64_t N, int64_t D, const float* scale, const int32_t* zp, int8_t* codes) {
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < N; i++) {
@@ -605,64 +632,75 @@ static void km_assign(const float* x, int64_t N, int64_t D, const float* c, int6
     }
 }
 
+/* KMeansPipeline's update (KMeansUpdateKernel, ClusteringShaders.metal:490-613) given an
+ * assignment: a cluster's points in point order form chunks of 256; each chunk is summed in
+ * order, the chunk sums are added in order, times 1/count; an empty cluster keeps its centroid;
+ * then handleEmptyClusters (KMeansUpdateKernel.swift:228-283): empty clusters in index order take
+ * the unused point of largest distance (`>` from -1, so the first index on ties and never a NaN). */
+static void km_update(const float* x, int64_t N, int64_t D, int64_t C, const uint32_t* assign, const float* dist,
+                      const float* cur, float* nxt, uint32_t* counts) {
+    float* sums = (float*)calloc((size_t)(C * D), sizeof(float));
+    float* chunk = (float*)calloc((size_t)(C * D), sizeof(float));
+    uint32_t* seen = (uint32_t*)calloc((size_t)C, sizeof(uint32_t));
+    unsigned char* used = (unsigned char*)calloc((size_t)N, 1);
+    memset(counts, 0, sizeof(uint32_t) * C);
+    for (int64_t i = 0; i < N; ++i) counts[assign[i]]++;
+    for (int64_t i = 0; i < N; ++i) {
+        uint32_t a = assign[i];
+        for (int64_t d = 0; d < D; ++d) chunk[a * D + d] += x[i * D + d];
+        if (++seen[a] % 256 == 0 || seen[a] == counts[a]) {
+            for (int64_t d = 0; d < D; ++d) {
+                sums[a * D + d] += chunk[a * D + d];
+                chunk[a * D + d] = 0.0f;
+            }
+        }
+    }
+    for (int64_t c = 0; c < C; ++c) {
+        if (counts[c] > 0) {
+            float inv = 1.0f / (float)counts[c];
+            for (int64_t d = 0; d < D; ++d) nxt[c * D + d] = sums[c * D + d] * inv;
+        } else {
+            for (int64_t d = 0; d < D; ++d) nxt[c * D + d] = cur[c * D + d];
+        }
+    }
+    for (int64_t c = 0; c < C; ++c) {
+        if (counts[c] != 0) continue;
+        float md = -1.0f;
+        int64_t bv = -1;
+        for (int64_t i = 0; i < N; ++i)
+            if (!used[i] && dist[i] > md) {
+                md = dist[i];
+                bv = i;
+            }
+        if (bv >= 0) {
+            used[bv] = 1;
+            memcpy(nxt + c * D, x + bv * D, sizeof(float) * D);
+            counts[c] = 1;
+        }
+    }
+    free(sums);
+    free(chunk);
+    free(seen);
+    free(used);
+}
+
+void vo_kmeans_update(const float* x, int64_t N, int64_t D, int64_t C, const uint32_t* assign, const float* dist,
+                      const float* old_centroids, float* out_centroids, uint32_t* counts) {
+    km_update(x, N, D, C, assign, dist, old_centroids, out_centroids, counts);
+}
+
 void vo_kmeans_fit(const float* x, int64_t N, int64_t D, int64_t C, const float* init, int64_t max_iter,
                    float threshold, float* centroids, uint32_t* assign, float* dist, uint32_t* counts,
                    uint32_t* info_u32, float* info_f) {
     float* cur = (float*)malloc(sizeof(float) * C * D);
     float* nxt = (float*)malloc(sizeof(float) * C * D);
-    float* sums = (float*)malloc(sizeof(float) * C * D);
-    float* chunk = (float*)malloc(sizeof(float) * C * D);
-    uint32_t* seen = (uint32_t*)malloc(sizeof(uint32_t) * C);
-    unsigned char* used = (unsigned char*)malloc(N);
     memcpy(cur, init, sizeof(float) * C * D);
     int64_t it = 0;
     int converged = 0;
     float max_move = 0.0f;
     while (it < max_iter && !converged) {
         km_assign(x, N, D, cur, C, assign, dist);
-        /* update: a cluster's points in point order form chunks of 256; each chunk is summed in
-         * order, the chunk sums are added in order, times 1/count; empty keeps the old centroid */
-        memset(sums, 0, sizeof(float) * C * D);
-        memset(counts, 0, sizeof(uint32_t) * C);
-        for (int64_t i = 0; i < N; ++i) counts[assign[i]]++;
-        memset(seen, 0, sizeof(uint32_t) * C);
-        memset(chunk, 0, sizeof(float) * C * D);
-        for (int64_t i = 0; i < N; ++i) {
-            uint32_t a = assign[i];
-            for (int64_t d = 0; d < D; ++d) chunk[a * D + d] += x[i * D + d];
-            if (++seen[a] % 256 == 0 || seen[a] == counts[a]) {
-                for (int64_t d = 0; d < D; ++d) {
-                    sums[a * D + d] += chunk[a * D + d];
-                    chunk[a * D + d] = 0.0f;
-                }
-            }
-        }
-        for (int64_t c = 0; c < C; ++c) {
-            if (counts[c] > 0) {
-                float inv = 1.0f / (float)counts[c];
-                for (int64_t d = 0; d < D; ++d) nxt[c * D + d] = sums[c * D + d] * inv;
-            } else {
-                for (int64_t d = 0; d < D; ++d) nxt[c * D + d] = cur[c * D + d];
-            }
-        }
-        /* handleEmptyClusters: empty clusters in index order take the unused point of largest
-         * distance (`>` from -1, so the first index on ties and never a NaN) */
-        memset(used, 0, N);
-        for (int64_t c = 0; c < C; ++c) {
-            if (counts[c] != 0) continue;
-            float md = -1.0f;
-            int64_t bv = -1;
-            for (int64_t i = 0; i < N; ++i)
-                if (!used[i] && dist[i] > md) {
-                    md = dist[i];
-                    bv = i;
-                }
-            if (bv >= 0) {
-                used[bv] = 1;
-                memcpy(nxt + c * D, x + bv * D, sizeof(float) * D);
-                counts[c] = 1;
-            }
-        }
+        km_update(x, N, D, C, assign, dist, cur, nxt, counts);
         /* checkConvergence: max over centroids of sqrt(sum (new - old)^2) */
         max_move = 0.0f;
         for (int64_t c = 0; c < C; ++c) {
@@ -694,10 +732,6 @@ void vo_kmeans_fit(const float* x, int64_t N, int64_t D, int64_t C, const float*
     info_f[1] = max_move;
     free(cur);
     free(nxt);
-    free(sums);
-    free(chunk);
-    free(seen);
-    free(used);
 }
 
 static uint64_t vo_splitmix64(uint64_t* s) {

@@ -81,6 +81,10 @@ void vo_topk_merge(const uint32_t* a_idx, const float* a_d, const uint32_t* b_id
 void vo_sq_params_per_dim(const float* x, int64_t N, int64_t D, float* mn, float* mx, float* scale, int32_t* zp);
 /* q = clamp(rint(x/scale + zp), -128, 127); |scale| < 1e-9 -> clamp(zp)
  * (quantize_int8_kernel, DataTransformations.metal:174-201), per dimension d = i % D. */
+/* The global (one scale for all values) int8 parameters of ScalarQuantizationKernel.quantize:
+ * computeQuantizationParams, Kernels/Metal4/ScalarQuantizationKernel.swift:496-520 (int8 branch;
+ * symmetric: zero_point 0; asymmetric: the saturating Int8 zero point). */
+void vo_sq_global_params(const float* x, int64_t n, int asymmetric, float* scale, int32_t* zero_point);
 void vo_sq_quantize(const float* x, int64_t N, int64_t D, const float* scale, const int32_t* zp, int8_t* codes);
 /* x = (q - zp) * scale (dequantize_int8_kernel, DataTransformations.metal:203-221). */
 void vo_sq_dequantize(const int8_t* codes, int64_t N, int64_t D, const float* scale, const int32_t* zp, float* out);
@@ -135,6 +139,11 @@ void vo_kmeans_fit(const float* x, int64_t N, int64_t D, int64_t C, const float*
  * strided fmaf partials combined pairwise, the device's order),
  * total = double sum over unselected points, pick the first unselected i whose cumulative
  * double sum reaches u_j * total (the first unselected point when total is 0). */
+/* One k-means update given an assignment (and the distances handleEmptyClusters ranks by):
+ * the update step of vo_kmeans_fit (KMeansUpdateKernel, ClusteringShaders.metal:490-613;
+ * KMeansUpdateKernel.swift:228-283).  out_centroids [C x D], counts [C]. */
+void vo_kmeans_update(const float* x, int64_t N, int64_t D, int64_t C, const uint32_t* assign, const float* dist,
+                      const float* old_centroids, float* out_centroids, uint32_t* counts);
 void vo_kmeans_plusplus(const float* x, int64_t N, int64_t D, int64_t k, uint64_t seed, uint32_t* idx);
 
 /* ---- product quantization --------------------------------------------------- */

@@ -14,6 +14,32 @@ HERE = Path(__file__).resolve().parent
 INF = float("inf")
 
 FIXTURES = {
+    # Global int8 quantization (ScalarQuantizationKernel.quantize with computeQuantizationParams,
+    # Kernels/Metal4/ScalarQuantizationKernel.swift:496-520; codes by quantize_int8_kernel,
+    # DataTransformations.metal:188-200).  The reference's tests assert only round trips
+    # (KernelTests.swift:1775-1787) and order (:1850-1862); these cases are closed forms chosen so
+    # that scale and codes are exact: a range of 255 or absMax of 127 gives scale 1 (254: 2).
+    "sq_global": {
+        "kind": "sq_global",
+        "cases": [
+            # absMax 127 -> scale 1; rint: 63.5 -> 64 (half even), -2.5 -> -2
+            {"data": [-127, 63.5, 1, 0, -2.5], "asymmetric": False, "scale": 1.0, "zero_point": 0,
+             "codes": [-127, 64, 1, 0, -2]},
+            # absMax 254 -> scale 2: -2.5 / 2 = -1.25 -> -1
+            {"data": [254, -2.5], "asymmetric": False, "scale": 2.0, "zero_point": 0, "codes": [127, -1]},
+            # range 255 -> scale 1, zero point -round(-1) = 1; 254 + 1 saturates at 127
+            {"data": [-1, 254, 0], "asymmetric": True, "scale": 1.0, "zero_point": 1, "codes": [0, 127, 1]},
+            # Swift round is half away from zero: -round(-2.5) = 3 (half even would give 2)
+            {"data": [-2.5, 252.5], "asymmetric": True, "scale": 1.0, "zero_point": 3, "codes": [0, 127]},
+            # Int8(clamping:): -round(1000) = -1000 saturates to -128; codes saturate at 127
+            {"data": [1000, 1255], "asymmetric": True, "scale": 1.0, "zero_point": -128, "codes": [127, 127]},
+            # ... and -round(-300) = 300 saturates to 127
+            {"data": [-300, -45], "asymmetric": True, "scale": 1.0, "zero_point": 127, "codes": [-128, 82]},
+            # the 1e-8 scale floor: constant data and a tiny range
+            {"data": [0, 0, 0], "asymmetric": True, "scale": 1e-8, "zero_point": 0, "codes": [0, 0, 0]},
+            {"data": [1e-9, 2e-9], "asymmetric": False, "scale": 1e-8, "zero_point": 0, "codes": [0, 0]},
+        ],
+    },
     # Tests/VectorAccelerateTests/KernelTests.swift:806-835 (testBasicNearestNeighbors)
     "fused_topk_basic": {
         "kind": "flat_topk", "metric": 0, "k": 2,

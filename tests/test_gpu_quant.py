@@ -112,6 +112,34 @@ def test_global_quantize_roundtrip(ctx):
     assert r2.zeroPoint is not None
 
 
+def test_global_quantize_matches_oracle_and_fixture(ctx, oracle):
+    """ScalarQuantizationKernel.quantize with global parameters (computeQuantizationParams,
+    ScalarQuantizationKernel.swift:496-520): scale, the saturating Int8 zero point and the codes
+    are bit-exact against the oracle, on the golden closed-form cases and on random data whose
+    asymmetric zero point saturates."""
+    import json
+    from pathlib import Path
+
+    from vectoraccelerate_amd import Metal4QuantizationType, ScalarQuantizationKernel
+
+    k = ScalarQuantizationKernel(ctx)
+    fx = json.loads((Path(__file__).resolve().parent / "golden" / "sq_global.json").read_text())
+    g = rng(11)
+    randoms = [(g.uniform(-3, 5, 5000).astype(np.float32), a) for a in (False, True)]
+    randoms += [(g.uniform(400, 410, 3000).astype(np.float32), True),   # zero point saturates at -128
+                (g.uniform(-90, -80, 3000).astype(np.float32), True)]    # ... and at 127
+    cases = [(np.array(c["data"], np.float32), c["asymmetric"]) for c in fx["cases"]] + randoms
+    for data, asym in cases:
+        qt = Metal4QuantizationType.asymmetric if asym else Metal4QuantizationType.symmetric
+        r = k.quantize(data, type=qt)
+        codes, scale, zp = oracle.sq_global_quantize(data, asym)
+        assert np.float32(r.scale) == scale
+        assert (r.zeroPoint if asym else 0) == zp
+        if not asym:
+            assert r.zeroPoint is None
+        np.testing.assert_array_equal(np.frombuffer(r.quantizedData, np.int8), codes)
+
+
 @pytest.mark.parametrize("Q,N,D,k", [(1, 50, 16, 5), (40, 3000, 512, 10), (130, 20000, 64, 100), (9, 40000, 100, 7),
                                      (300, 5000, 48, 1),
                                      # large-Q tiles (256 queries x 128 rows): ragged Q and N,

@@ -372,8 +372,27 @@ def test_golden_fixtures_reproduce(oracle):
             mn, mx, sc, zp = oracle.sq_params_per_dim(x)
             np.testing.assert_array_equal(zp, fx["expected_zero_point"], err_msg=f.name)
             np.testing.assert_array_equal(oracle.sq_quantize(x, sc, zp), fx["expected_codes"], err_msg=f.name)
+        elif kind == "sq_global":
+            for case in fx["cases"]:
+                codes, scale, zp = oracle.sq_global_quantize(np.array(case["data"], np.float32), case["asymmetric"])
+                assert scale == np.float32(case["scale"]), (f.name, case)
+                assert zp == case["zero_point"], (f.name, case)
+                np.testing.assert_array_equal(codes, case["codes"], err_msg=f"{f.name} {case}")
         else:
             raise AssertionError(f"unknown fixture kind {kind} in {f.name}")
+
+
+def test_sq_global_reference_properties(oracle):
+    """The properties the reference's ScalarQuantizationKernel tests assert on the global int8
+    path: round trip within 0.02 (KernelTests.swift:1775-1787) and order preserved over a wide
+    range (:1850-1862)."""
+    data = np.array([0.0, 0.25, 0.5, 0.75, 1.0, -0.25, -0.5, -0.75, -1.0], np.float32)
+    codes, scale, zp = oracle.sq_global_quantize(data, False)
+    back = oracle.sq_dequantize(codes.reshape(-1, 1), [scale], [zp]).reshape(-1)
+    assert np.max(np.abs(back - data)) <= 0.02
+    wide = np.array([-1000, -100, 0, 100, 1000], np.float32)
+    c2, s2, z2 = oracle.sq_global_quantize(wide, False)
+    assert np.all(np.diff(oracle.sq_dequantize(c2.reshape(-1, 1), [s2], [z2]).reshape(-1)) > 0)
 
 
 def test_config1_oracle_is_self_consistent(oracle):
@@ -478,6 +497,33 @@ def test_kmeans_zero_iterations_and_ties(oracle):
     np.testing.assert_array_equal(assign, [0, 1, 0])  # the midpoint ties: lower centroid
     np.testing.assert_array_equal(counts, [2, 1])
     np.testing.assert_allclose(dist, [0, 0, 1])
+
+
+def test_kmeans_update_given_assignment(oracle):
+    """vo_kmeans_update: cluster means (float64 reference within fp32 rounding), empty clusters
+    (index order) take the unused points of largest distance, first index on ties; and one
+    iteration of vo_kmeans_fit is exactly its own assignment followed by this update."""
+    g = np.random.default_rng(17)
+    x = g.standard_normal((900, 12)).astype(np.float32)
+    old = g.standard_normal((9, 12)).astype(np.float32)
+    assign = g.integers(0, 6, 900).astype(np.uint32)  # clusters 6, 7, 8 empty
+    dist = g.random(900).astype(np.float32)
+    dist[[5, 77]] = 2.0  # a tie: index 5 first
+    cen, counts = oracle.kmeans_update(x, assign, dist, old)
+    for c in range(6):
+        m = x[assign == c].astype(np.float64).mean(0)
+        np.testing.assert_allclose(cen[c], m, rtol=1e-5, atol=1e-6)
+        assert counts[c] == (assign == c).sum()
+    order = sorted(range(900), key=lambda i: (-dist[i], i))[:3]
+    assert order[:2] == [5, 77]
+    for j, c in enumerate((6, 7, 8)):
+        np.testing.assert_array_equal(cen[c], x[order[j]])
+        assert counts[c] == 1
+    init = x[:9].copy()
+    fc, fa, fd, fcnt, *_ = oracle.kmeans_fit(x, init, 1, 0.0)
+    uc, ucnt = oracle.kmeans_update(x, fa, fd, init)
+    np.testing.assert_array_equal(fc, uc)
+    np.testing.assert_array_equal(fcnt, ucnt)
 
 
 def test_kmeans_plusplus_properties(oracle):
