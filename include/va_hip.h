@@ -201,7 +201,9 @@ va_status va_sq_dequantize_i8(va_context* ctx, const int8_t* codes, uint64_t num
                               const float* scale, const int32_t* zero_point, float* out);
 /* int8 scan: distance = -sum(qc * xc) accumulated in int32, exact top-k.
  * No reference counterpart (the reference has no int8-domain distance); defined by the
- * scalar-int8 quantize-and-scan search path.  out_dist may be NULL. */
+ * scalar-int8 quantize-and-scan search path.  out_dist may be NULL.  dim is at most
+ * VA_I8_MAX_DIM: the dot of two code vectors then lies in [-16256 dim, 16384 dim], inside int32. */
+#define VA_I8_MAX_DIM 131071u
 va_status va_i8_scan_topk(va_context* ctx, const int8_t* query_codes, const int8_t* database_codes,
                           uint32_t num_queries, uint32_t num_database, uint32_t dim, uint32_t k,
                           uint32_t* out_idx, int32_t* out_dist);

@@ -174,6 +174,22 @@ def test_i8_large_q_many_passes(ctx, oracle, Q, N, D, k):
     check_topk_exact(gi, gd, oi, od)
 
 
+def test_i8_scan_rejects_dimensions_beyond_int32_range(ctx):
+    """dim 131071 keeps every dot inside int32 (16384 * 131071 < 2^31); one more could wrap, so the
+    call is refused before any memory is touched (the 1-byte buffers are never read)."""
+    import torch
+
+    from vectoraccelerate_amd import VectorError, _lib
+
+    assert _lib.VA_I8_MAX_DIM == 131071 and 16384 * 131071 < 2**31 <= 16384 * 131072
+    b = torch.zeros(1, dtype=torch.int8, device="cuda")
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    with pytest.raises(VectorError) as e:
+        ctx.check(ctx.lib.va_i8_scan_topk(ctx.handle, b.data_ptr(), b.data_ptr(), 1, 1, 131072, 1, out.data_ptr(),
+                                          None), "va_i8_scan_topk")
+    assert e.value.kind == "invalidInput" and "131071" in str(e.value)
+
+
 def test_i8_sampled_and_overflow_paths(ctx, oracle):
     from vectoraccelerate_amd import ScalarQuantizationKernel, _lib
 

@@ -31,6 +31,7 @@ VA_OPT_SCREEN = 3
 
 VA_SENTINEL_INDEX = 0xFFFFFFFF
 VA_MAX_K = 1024
+VA_I8_MAX_DIM = 131071  # va_i8_scan_topk: the int32 dot of two code vectors stays exact
 VA_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 _p = C.c_void_p

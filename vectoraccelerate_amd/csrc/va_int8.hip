@@ -1102,6 +1102,9 @@ va_status va_i8_scan_topk(va_context* ctx, const int8_t* query_codes, const int8
     if (!ctx) return VA_ERR_INVALID_ARG;
     VA_REQUIRE(ctx, query_codes && database_codes && out_idx, "va_i8_scan_topk: NULL pointer");
     VA_REQUIRE(ctx, num_queries > 0 && num_database > 0 && dim > 0, "va_i8_scan_topk: empty input");
+    // the int32 dot of two code vectors lies in [-16256 dim, 16384 dim]: exact below 2^31
+    VA_REQUIRE(ctx, dim <= VA_I8_MAX_DIM, "va_i8_scan_topk: dim %u exceeds %u (int32 accumulation)", dim,
+               VA_I8_MAX_DIM);
     VA_REQUIRE(ctx, k > 0 && k <= VA_MAX_K, "k must be in [1, %u], got %u", VA_MAX_K, k);
     va::DeviceGuard g(ctx->device);
     va::I8Producer p;
