@@ -11,7 +11,12 @@
  *    encode(into:) tier, KernelProtocol.swift:42-63) and enqueue on the context's
  *    stream.  They return once the work is enqueued unless stated otherwise; call
  *    va_context_synchronize() before reading results on the host (the reference's
- *    executeAndWait, Core/Metal4Context.swift:342-410).
+ *    executeAndWait, Core/Metal4Context.swift:342-410).  The top-k searches
+ *    (va_fused_topk, va_i8_scan_topk, va_hamming_topk, va_pq_search, va_index_search)
+ *    never wait on the host: queries whose candidate list overflows are
+ *    finished on the device by a fallback whose launches exit at once when nothing
+ *    overflowed, so searches can be queued back to back on one stream.  A call that has to
+ *    grow the context's scratch arena waits for the stream once, before the growth.
  *  - A context is externally synchronised: one caller at a time per context (the
  *    reference's actor contract).  Different contexts may be used concurrently.
  *  - Missing results use index VA_SENTINEL_INDEX (0xFFFFFFFF) and distance +inf
@@ -144,7 +149,7 @@ va_status va_dot_all_pairs(va_context* ctx, const float* queries, const float* d
  * Replaces FusedL2TopKKernel.execute (Kernels/Metal4/FusedL2TopKKernel.swift:367-427) without
  * its K <= 128 / D <= 768 limits; FusedTopKKernel is its alias (VectorAccelerate.swift:288).
  * out_idx[Q x k], out_dist[Q x k] (out_dist may be NULL: includeDistances = false).
- * Synchronises the context once (it reads back an overflow counter). */
+ * Returns once enqueued (no host read-back). */
 va_status va_fused_topk(va_context* ctx, va_metric metric, const float* queries, const float* database,
                         uint32_t num_queries, uint32_t num_database, uint32_t dim, uint32_t k,
                         uint32_t* out_idx, float* out_dist);
@@ -164,13 +169,15 @@ va_status va_fused_topk_streamed(va_context* ctx, va_metric metric, const float*
 #define VA_NOALLOC_SCRATCH_BYTES (64u << 20)
 /* va_fused_topk without device allocation.  No counterpart in the reference: it is for callers
  * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc).  Same arguments, results and synchronisation as
- * va_fused_topk, but every scratch buffer comes from a fixed block of VA_NOALLOC_SCRATCH_BYTES
+ * harnesses that forbid hipMalloc).  Same arguments and results as va_fused_topk, but every
+ * scratch buffer comes from a fixed block of VA_NOALLOC_SCRATCH_BYTES
  * that each GPU holds until the process ends (about 128 queries x 1M rows at k = 100 fit).
  * A search that needs more fails with VA_ERR_INVALID_ARG before any work is enqueued, and the
  * message gives the size it needs.  Every call on one GPU shares that GPU's block and leaves its
  * contents behind (each call clears what it needs cleared): calls that overlap on one GPU, from
- * different contexts or streams, race. */
+ * different contexts or streams, race.  Returns once enqueued when the device-side overflow
+ * fallback's buffers fit in the block too; otherwise it reads the overflow count back (one
+ * synchronisation) and finishes overflowed queries from the host. */
 va_status va_fused_topk_noalloc(va_context* ctx, va_metric metric, const float* queries, const float* database,
                                 uint32_t num_queries, uint32_t num_database, uint32_t dim, uint32_t k,
                                 uint32_t* out_idx, float* out_dist);

@@ -12,6 +12,7 @@
 //          distance itself as the key (ties -> lower index, HammingDistanceKernel.swift:114-120).
 #include <algorithm>
 
+#include "va_fallback.hpp"
 #include "va_internal.hpp"
 
 namespace va {
@@ -469,6 +470,9 @@ struct HamProducer final : KeyProducer {
     const uint32_t* q;
     const uint32_t* x;
     uint32_t Q, N, W;
+    va_status fallback_pass(const FbArgs& a, int pass) override {
+        return fb_launch_pass(ctx, FbHam{q, x, N, W}, a, pass);
+    }
     // distances are at most 32 W
     uint32_t key_bits() const override { return 32u - uint32_t(__builtin_clz(32u * W)); }
     va_status dense(const uint32_t* qrow, uint32_t q0, uint32_t nq, uint32_t c0, uint32_t cols, uint32_t stride,

@@ -54,6 +54,28 @@ va_status Scratch::reserve(size_t total) {
     return VA_OK;
 }
 
+va_status side_reserve(va_context* ctx, size_t bytes, void** out) {
+    if (bytes > ctx->side_bytes) {
+        // grow: wait for in-flight readers of the old buffer, then replace it
+        VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (ctx->side) {
+            VA_CHECK_HIP(ctx, hipFree(ctx->side));
+            ctx->side = nullptr;
+            ctx->side_bytes = 0;
+        }
+        void* p = nullptr;
+        const hipError_t e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(ctx, VA_ERR_OOM, "side buffer allocation of %zu bytes failed: %s", bytes, hipGetErrorString(e));
+        }
+        ctx->side = static_cast<char*>(p);
+        ctx->side_bytes = bytes;
+    }
+    *out = ctx->side;
+    return VA_OK;
+}
+
 __global__ void fill_u32_kernel(uint32_t* p, uint64_t n, uint32_t v) {
     uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     uint64_t step = uint64_t(gridDim.x) * blockDim.x;
@@ -169,6 +191,7 @@ va_status va_context_destroy(va_context* ctx) {
         va::DeviceGuard g(ctx->device);
         (void)hipStreamSynchronize(ctx->stream);
         if (ctx->scratch) (void)hipFree(ctx->scratch);
+        if (ctx->side) (void)hipFree(ctx->side);
         if (ctx->host_word) (void)hipHostFree(ctx->host_word);
         for (auto& e : ctx->ev)
             if (e) (void)hipEventDestroy(e);

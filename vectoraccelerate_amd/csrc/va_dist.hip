@@ -21,6 +21,7 @@
 
 #include <algorithm>
 
+#include "va_distop.hpp"
 #include "va_internal.hpp"
 
 namespace va {
@@ -78,29 +79,6 @@ struct Tile {
     static constexpr int DSTAGE = GPW * NW * 256;  // floats per slot
     static constexpr size_t DMA_LDS_BYTES = size_t(VA_DIST_DMA_SLOTS * DSTAGE + NW * 128) * sizeof(float);
 };
-
-__device__ __forceinline__ float apply_op(int op, float dot, float qq, float xx) {
-    switch (op) {
-        case OP_L2SQ:
-        case OP_L2: {
-            // cancellation can leave a tiny negative: clamp at 0, but let NaN through
-            float v = qq + xx - 2.0f * dot;
-            v = (v < 0.0f) ? 0.0f : v;
-            return op == OP_L2 ? sqrtf(v) : v;
-        }
-        case OP_COS_SIM:
-        case OP_COS_DIST: {
-            // cosine_similarity finalisation (DistanceShaders.metal:300-319)
-            float denom = sqrtf(qq) * sqrtf(xx);
-            float raw = (denom < FLT_MIN) ? 0.0f : dot / denom;
-            float s = (raw != raw) ? raw : fminf(fmaxf(raw, -1.0f), 1.0f);
-            return op == OP_COS_SIM ? s : 1.0f - s;
-        }
-        case OP_DOT: return dot;
-        case OP_ABS_DOT: return fabsf(dot);
-        default: return -dot;
-    }
-}
 
 // DMA = true: the stages move global -> LDS by direct buffer loads (no register staging, so
 // fewer VGPRs and more waves per SIMD); needs 16-byte rows (VEC) and the swizzled 64-byte LDS

@@ -1,0 +1,375 @@
+// va_fallback.hpp — exact top-k of the rows whose candidate list overflowed, enqueued without
+// reading the overflow count back to the host.
+//
+// A scan that selects from per-query candidate lists lists the queries whose list outgrew its
+// capacity (a device count and a device list of query ids).  The fallback finds their exact
+// top-k in a fixed number of launches whose work follows that device count; with no overflowed
+// query every workgroup exits at once.  Each pass recomputes the keys of (overflowed query,
+// database row) pairs with the producer's own arithmetic — bit-identical to its scan:
+//   pass 0 .. 2  histograms of key bits 31:21, 20:10 and 9:0 of the keys in the bucket chosen so
+//                far: after pass 2 the k-th smallest key K and how many keys equal to K the
+//                top-k takes ("need") are known;
+//   pass 3       collects every (key, id) with key <= K, and a histogram of the ids of the ties;
+//   pass 4       (rows whose ties overflowed the list) collects key < K, and the ties whose id is
+//                below the first id-histogram edge that holds `need` of them;
+//   then the selection kernel orders each row's list by (key, id) and writes the top-k.
+// Between passes the last workgroup to finish (a completion ticket, no waiting) turns the
+// histograms into the next pass's bucket.  Work items are 32 queries x 32 database rows in the
+// 32x32 MFMA output layout: lane (l, h) holds query slot l % 32 and rows 8j + 4h + e.
+#pragma once
+
+#include "va_distop.hpp"
+#include "va_internal.hpp"
+
+namespace va {
+
+struct FbArgs {
+    const uint32_t* n_rows = nullptr;  // device: how many queries overflowed
+    const uint32_t* rows = nullptr;    // device: their query ids
+    uint32_t rmax = 0;                 // slots the buffers hold (a host bound on the count)
+    uint32_t N = 0, k = 0;
+    uint32_t ishift = 0;               // tie-id histogram bin = id >> ishift (N >> ishift < 4096)
+    uint32_t cap = 0;                  // list capacity per slot: k + 2^ishift, rounded up
+    uint32_t* hist = nullptr;          // [rmax][2048] key histogram (cleared after each use)
+    uint32_t* tidh = nullptr;          // [rmax][4096] tie-id histogram
+    uint32_t* st = nullptr;            // [rmax][8] bucket state (see FbState)
+    uint32_t* cnt = nullptr;           // [rmax] list lengths
+    uint32_t* lkey = nullptr;          // [rmax][cap]
+    uint32_t* lid = nullptr;           // [rmax][cap]
+    uint32_t* done = nullptr;          // [8] completion tickets, one per pass
+    const uint8_t* skip = nullptr;     // excluded rows: their keys are kAbsentKey
+};
+enum FbState : int { FB_PREFIX = 0, FB_NEED = 1, FB_K = 2, FB_EDGE = 3, FB_OVF = 4 };
+constexpr int kFbPasses = 5;
+constexpr uint32_t kFbGrid = 1024;  // workgroups per pass (4 waves each)
+constexpr uint32_t kFbTieBins = 4096;
+
+// host: list capacity and id shift for N rows and top-k
+inline void fb_geometry(uint32_t N, uint32_t k, uint32_t& ishift, uint32_t& cap) {
+    ishift = 0;
+    while ((uint64_t(N) >> ishift) >= kFbTieBins) ++ishift;
+    cap = uint32_t((uint64_t(k) + (uint64_t(1) << ishift) + 63) / 64 * 64);
+}
+inline size_t fb_bytes(uint32_t rmax, uint32_t N, uint32_t k) {
+    uint32_t ishift, cap;
+    fb_geometry(N, k, ishift, cap);
+    return Scratch::round(uint64_t(rmax) * 2048 * 4) + Scratch::round(uint64_t(rmax) * kFbTieBins * 4) +
+           Scratch::round(uint64_t(rmax) * 8 * 4) + Scratch::round(uint64_t(rmax) * 4) +
+           Scratch::round(uint64_t(rmax) * cap * 4) * 2 + Scratch::round(8 * 4);
+}
+inline FbArgs fb_carve(Scratch& s, uint32_t rmax, uint32_t N, uint32_t k) {
+    FbArgs a;
+    a.rmax = rmax;
+    a.N = N;
+    a.k = k;
+    fb_geometry(N, k, a.ishift, a.cap);
+    a.hist = s.carve<uint32_t>(uint64_t(rmax) * 2048);
+    a.tidh = s.carve<uint32_t>(uint64_t(rmax) * kFbTieBins);
+    a.st = s.carve<uint32_t>(uint64_t(rmax) * 8);
+    a.cnt = s.carve<uint32_t>(rmax);
+    a.lkey = s.carve<uint32_t>(uint64_t(rmax) * a.cap);
+    a.lid = s.carve<uint32_t>(uint64_t(rmax) * a.cap);
+    a.done = s.carve<uint32_t>(8);
+    return a;
+}
+
+// ---- device key producers ----------------------------------------------------------------------
+// keys16: the lane's 16 keys of query slot s0 + l (rows[]: query ids, slots >= n are padding)
+// against database rows r0 + 8j + 4h + e.  Every lane of the wave calls it.
+
+typedef float fb_f32x16 __attribute__((ext_vector_type(16)));
+typedef float fb_f32x4 __attribute__((ext_vector_type(4)));
+
+// fp32 distances exactly as the distance GEMM forms them: v_mfma_f32_32x32x2_f32 over 16-value
+// stages, step e of each 8-value group pairing d = 8g + e (lane half 0) with 8g + 4 + e (half 1);
+// squared norms as per-half fmaf chains over the same values, the halves then added; values
+// past D are zeros.  The per-element sequence is the GEMM's, so the keys are bit-identical.
+struct FbF32 {
+    const float* q;
+    int64_t ldq;
+    const float* x;
+    int64_t ldx;
+    uint32_t N, D;
+    int op;
+    __device__ void keys16(const uint32_t* rows, uint32_t s0, uint32_t n, uint32_t r0, int lane, uint32_t* keys) const {
+        const int l32 = lane & 31, hh = lane >> 5;
+        const float* qp = (s0 + l32 < n) ? q + int64_t(rows[s0 + l32]) * ldq : nullptr;
+        const float* xp = (r0 + l32 < N) ? x + int64_t(r0 + l32) * ldx : nullptr;
+        auto load4 = [&](const float* p, uint32_t d) {
+            fb_f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (p) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (d + e < D) v[e] = p[d + e];
+            }
+            return v;
+        };
+        fb_f32x16 acc;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+        float qss = 0.0f, xss = 0.0f;
+        for (uint32_t d0 = 0; d0 < D; d0 += 16) {
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                const uint32_t d = d0 + 8 * g + 4 * hh;
+                const fb_f32x4 bv = load4(qp, d);
+                const fb_f32x4 av = load4(xp, d);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) qss = fmaf(bv[e], bv[e], qss);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xss = fmaf(av[e], av[e], xss);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[e], bv[e], acc, 0, 0, 0);
+            }
+        }
+        const float qq = qss + __shfl_xor(qss, 32);
+        const float xt = xss + __shfl_xor(xss, 32);  // |x|^2 of row r0 + l32
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float xx = __shfl(xt, 8 * j + 4 * hh + e);
+                keys[4 * j + e] = key_of_float(apply_op(op, acc[4 * j + e], qq, xx));
+            }
+    }
+};
+
+// int8 codes: key of -sum(q * x), exact in int32 (any order)
+struct FbI8 {
+    const int8_t* q;
+    int64_t ldq;
+    const int8_t* x;
+    int64_t ldx;
+    uint32_t N, D;
+    __device__ void keys16(const uint32_t* rows, uint32_t s0, uint32_t n, uint32_t r0, int lane, uint32_t* keys) const {
+        const int l32 = lane & 31, hh = lane >> 5;
+        const bool qv = s0 + l32 < n;
+        const int8_t* qp = qv ? q + int64_t(rows[s0 + l32]) * ldq : nullptr;
+#pragma unroll 1
+        for (int t = 0; t < 16; ++t) {
+            const uint32_t r = r0 + 8 * (t >> 2) + 4 * hh + (t & 3);
+            int32_t dot = 0;
+            if (qv && r < N) {
+                const int8_t* xp = x + int64_t(r) * ldx;
+                for (uint32_t d = 0; d < D; ++d) dot += int32_t(qp[d]) * int32_t(xp[d]);
+            }
+            keys[t] = key_of_i32(-dot);
+        }
+    }
+};
+
+// packed binary codes: Hamming distance (the key itself)
+struct FbHam {
+    const uint32_t* q;
+    const uint32_t* x;
+    uint32_t N, W;
+    __device__ void keys16(const uint32_t* rows, uint32_t s0, uint32_t n, uint32_t r0, int lane, uint32_t* keys) const {
+        const int l32 = lane & 31, hh = lane >> 5;
+        const bool qv = s0 + l32 < n;
+        const uint32_t* qp = qv ? q + int64_t(rows[s0 + l32]) * W : nullptr;
+#pragma unroll 1
+        for (int t = 0; t < 16; ++t) {
+            const uint32_t r = r0 + 8 * (t >> 2) + 4 * hh + (t & 3);
+            uint32_t d = 0;
+            if (qv && r < N) {
+                const uint32_t* xp = x + int64_t(r) * W;
+                for (uint32_t w = 0; w < W; ++w) d += __popc(qp[w] ^ xp[w]);
+            }
+            keys[t] = d;
+        }
+    }
+};
+
+// PQ asymmetric distances: the tables of the query summed over the subspaces in order from 0.0f
+// (the order of the ADC scan), as a float key
+struct FbAdc {
+    const uint8_t* codes;
+    const float* tables;  // [query][M][K]
+    uint32_t N, M, K;
+    __device__ void keys16(const uint32_t* rows, uint32_t s0, uint32_t n, uint32_t r0, int lane, uint32_t* keys) const {
+        const int l32 = lane & 31, hh = lane >> 5;
+        const bool qv = s0 + l32 < n;
+        const float* t = qv ? tables + int64_t(rows[s0 + l32]) * M * K : nullptr;
+#pragma unroll 1
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t r = r0 + 8 * (i >> 2) + 4 * hh + (i & 3);
+            float s = 0.0f;
+            if (qv && r < N) {
+                const uint8_t* c = codes + int64_t(r) * M;
+                for (uint32_t m = 0; m < M; ++m) s += t[m * K + c[m]];
+            }
+            keys[i] = key_of_float(s);
+        }
+    }
+};
+
+// ---- kernels ------------------------------------------------------------------------------------
+
+__device__ inline uint32_t fb_count(const FbArgs& a) {
+    const uint32_t n = *a.n_rows;
+    return n < a.rmax ? n : a.rmax;
+}
+
+// Block-wide search of a histogram: the bin b holding the need-th item (1-based) and the count
+// of the bins before it.  256 threads; bins is a multiple of 256.
+__device__ inline void fb_find_bin(const uint32_t* h, uint32_t bins, uint32_t need, uint32_t* sh, uint32_t& bin,
+                                   uint32_t& before) {
+    const uint32_t per = bins / 256, t = threadIdx.x;
+    uint32_t part = 0;
+    for (uint32_t i = 0; i < per; ++i) part += h[t * per + i];
+    sh[t] = part;
+    __syncthreads();
+    if (t == 0) {
+        uint32_t run = 0, b = bins - 1, bef = 0;
+        bool found = false;
+        for (uint32_t u = 0; u < 256 && !found; ++u) {
+            if (run + sh[u] >= need) {
+                uint32_t r2 = run;
+                for (uint32_t i = 0; i < per; ++i) {
+                    const uint32_t c = h[u * per + i];
+                    if (r2 + c >= need) {
+                        b = u * per + i;
+                        bef = r2;
+                        found = true;
+                        break;
+                    }
+                    r2 += c;
+                }
+            }
+            run += sh[u];
+        }
+        if (!found) bef = run - h[bins - 1];  // fewer items than need: the last bin
+        sh[256] = b;
+        sh[257] = bef;
+    }
+    __syncthreads();
+    bin = sh[256];
+    before = sh[257];
+    __syncthreads();
+}
+
+// The last workgroup of a pass: the histograms of every slot -> the next pass's state.
+__device__ inline void fb_resolve(const FbArgs& a, int pass, uint32_t n) {
+    __shared__ uint32_t sh[258];
+    for (uint32_t s = 0; s < n; ++s) {
+        uint32_t* st = a.st + int64_t(s) * 8;
+        uint32_t* h = a.hist + int64_t(s) * 2048;
+        if (pass <= 2) {
+            const uint32_t bins = pass == 2 ? 1024u : 2048u;
+            const uint32_t need = pass == 0 ? a.k : st[FB_NEED];
+            uint32_t b, before;
+            fb_find_bin(h, bins, need, sh, b, before);
+            for (uint32_t i = threadIdx.x; i < 2048; i += 256) h[i] = 0;  // ready for the next pass
+            if (threadIdx.x == 0) {
+                st[FB_NEED] = need - before;
+                if (pass == 0) st[FB_PREFIX] = b;
+                else if (pass == 1) st[FB_PREFIX] = (st[FB_PREFIX] << 11) | b;
+                else st[FB_K] = (st[FB_PREFIX] << 10) | b;
+            }
+        } else if (pass == 3) {
+            if (a.cnt[s] > a.cap) {
+                // too many ties for the list: keep those below the id edge that holds `need`
+                uint32_t b, before;
+                fb_find_bin(a.tidh + int64_t(s) * kFbTieBins, kFbTieBins, st[FB_NEED], sh, b, before);
+                if (threadIdx.x == 0) {
+                    const uint64_t edge = uint64_t(b + 1) << a.ishift;
+                    st[FB_EDGE] = edge > 0xFFFFFFFFull ? 0xFFFFFFFFu : uint32_t(edge);
+                    st[FB_OVF] = 1;
+                    a.cnt[s] = 0;
+                }
+            } else if (threadIdx.x == 0) {
+                st[FB_OVF] = 0;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// Adds c to bin b of slot s's histogram, combining runs of one bin within the lane.
+struct FbRun {
+    uint32_t* h;
+    uint32_t bin = 0xFFFFFFFFu, c = 0;
+    __device__ void add(uint32_t b) {
+        if (b == bin) {
+            ++c;
+            return;
+        }
+        flush();
+        bin = b;
+        c = 1;
+    }
+    __device__ void flush() {
+        if (c) atomicAdd(h + bin, c);
+        c = 0;
+    }
+};
+
+template <class P>
+__global__ __launch_bounds__(256) void fb_pass_kernel(P p, FbArgs a, int pass) {
+    const uint32_t n = fb_count(a);
+    if (n == 0) return;  // nothing overflowed: every workgroup leaves at once
+    const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5;
+    const uint32_t ngr = (n + 31) / 32, ntl = (a.N + 31) / 32;
+    const uint64_t items = uint64_t(ngr) * ntl;
+    const uint32_t nw = gridDim.x * 4;
+    for (uint64_t it = blockIdx.x * 4 + (threadIdx.x >> 6); it < items; it += nw) {
+        const uint32_t g = uint32_t(it / ntl), t = uint32_t(it % ntl);
+        const uint32_t s = g * 32 + l32;
+        uint32_t keys[16];
+        p.keys16(a.rows, g * 32, n, t * 32, lane, keys);
+        if (s >= n) continue;
+        const uint32_t* st = a.st + int64_t(s) * 8;
+        const uint32_t prefix = pass >= 1 ? st[FB_PREFIX] : 0u;
+        const uint32_t K = pass >= 3 ? st[FB_K] : 0u;
+        if (pass == 4 && !st[FB_OVF]) continue;
+        const uint32_t edge = pass == 4 ? st[FB_EDGE] : 0u;
+        FbRun run{a.hist + int64_t(s) * 2048};
+#pragma unroll 1
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t r = t * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
+            if (r >= a.N) continue;
+            const uint32_t key = (a.skip && a.skip[r]) ? kAbsentKey : keys[i];
+            if (pass == 0) {
+                run.add(key >> 21);
+            } else if (pass == 1) {
+                if ((key >> 21) == prefix) run.add((key >> 10) & 2047u);
+            } else if (pass == 2) {
+                if ((key >> 10) == prefix) run.add(key & 1023u);
+            } else if (key < K || (key == K && (pass == 3 || r < edge))) {
+                const uint32_t pos = atomicAdd(a.cnt + s, 1u);
+                if (pos < a.cap) {
+                    a.lkey[int64_t(s) * a.cap + pos] = key;
+                    a.lid[int64_t(s) * a.cap + pos] = r;
+                }
+                if (pass == 3 && key == K) atomicAdd(a.tidh + int64_t(s) * kFbTieBins + (r >> a.ishift), 1u);
+            }
+        }
+        run.flush();
+    }
+    // completion ticket: the last workgroup resolves the pass (nobody waits)
+    __shared__ uint32_t s_last;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence();
+        s_last = atomicAdd(a.done + pass, 1u) == gridDim.x - 1 ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    fb_resolve(a, pass, n);
+}
+
+__global__ __launch_bounds__(256) void fb_init_kernel(FbArgs a);
+
+template <class P>
+va_status fb_launch_pass(va_context* ctx, const P& p, const FbArgs& a, int pass) {
+    fb_pass_kernel<P><<<dim3(kFbGrid), dim3(256), 0, ctx->stream>>>(p, a, pass);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
+// Enqueues the whole fallback (clear, five passes, selection) for the producer's keys; base
+// carries the outputs and the key kind of the scan's selection.
+va_status fb_run(va_context* ctx, KeyProducer& kp, const FbArgs& a, const SelectArgs& base);
+
+}  // namespace va

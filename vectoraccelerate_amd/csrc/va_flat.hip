@@ -2,6 +2,7 @@
 #include <algorithm>
 #include <vector>
 
+#include "va_fallback.hpp"
 #include "va_internal.hpp"
 
 namespace va {
@@ -109,6 +110,9 @@ struct F32Producer final : KeyProducer {
     const float* x;
     uint32_t Q, N, D;
     DistOp op;
+    va_status fallback_pass(const FbArgs& a, int pass) override {
+        return fb_launch_pass(ctx, FbF32{q, int64_t(D), x, int64_t(D), N, D, int(op)}, a, pass);
+    }
     va_status dense(const uint32_t* qrow, uint32_t q0, uint32_t nq, uint32_t c0, uint32_t cols, uint32_t stride,
                     uint32_t* out_k, int64_t ldo) override {
         DistArgs a;
@@ -150,8 +154,9 @@ struct F32Producer final : KeyProducer {
 }  // namespace
 
 // Exact top-k of queries (device) against a device database: the screened path where it applies
-// (over the fp16 shadow when one is given), else the fp32 scan.  Synchronises the stream (the
-// scan reads back an overflow counter).
+// (over the fp16 shadow when one is given), else the fp32 scan.  Queued on the context's stream
+// without a host synchronisation (overflowed queries are finished on the device), except with a
+// fixed scratch block too small for the device fallback.
 va_status flat_topk(va_context* ctx, DistOp op, const float* q, const float* x, uint32_t Q, uint32_t N, uint32_t D,
                     uint32_t k, uint32_t* out_idx, float* out_dist, const _Float16* shadow, const float* norms,
                     const uint8_t* skip) {

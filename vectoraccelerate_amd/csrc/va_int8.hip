@@ -14,6 +14,7 @@
 // the same map for A and B, so the contraction pairs equal d on both sides.
 #include <algorithm>
 
+#include "va_fallback.hpp"
 #include "va_internal.hpp"
 
 namespace va {
@@ -982,6 +983,9 @@ struct I8Producer final : KeyProducer {
     const int8_t* q;
     const int8_t* x;
     uint32_t Q, N, D;
+    va_status fallback_pass(const FbArgs& a, int pass) override {
+        return fb_launch_pass(ctx, FbI8{q, int64_t(D), x, int64_t(D), N, D}, a, pass);
+    }
     va_status dense(const uint32_t* qrow, uint32_t q0, uint32_t nq, uint32_t c0, uint32_t cols, uint32_t stride,
                     uint32_t* out_k, int64_t ldo) override {
         I8Args a;

@@ -35,6 +35,10 @@ struct va_context {
     // instead of the arena: reserve() checks the size and never allocates
     char* fixed_scratch = nullptr;
     size_t fixed_scratch_bytes = 0;
+    // side buffer: per-call device inputs that a scan reads beside its scratch arena (PQ
+    // distance tables); grow-only like the arena, so a call need not wait before returning
+    char* side = nullptr;
+    size_t side_bytes = 0;
     // pinned host word used to read back small counters
     uint32_t* host_word = nullptr;
     // phase profiling of the top-k scan (va_context_set_profiling)
@@ -52,6 +56,9 @@ struct va_context {
 };
 
 namespace va {
+
+// *out = the context's side buffer, grown to at least `bytes` (growth waits for the stream).
+va_status side_reserve(va_context* ctx, size_t bytes, void** out);
 
 // Records an error message on the context and returns the status.
 va_status fail(va_context* ctx, va_status st, const char* fmt, ...);
@@ -97,6 +104,10 @@ struct Scratch {
 // Bytes of dense keys one launch of the exact scan may write (the threshold sample, the dense
 // path, the overflow rescan): 256 MiB, or a quarter of a fixed scratch block.
 size_t dense_budget(const va_context* ctx);
+// whether the device-side overflow fallback's buffers for `rows` rows fit beside `need` bytes
+bool fb_fits(const va_context* ctx, size_t need, uint32_t rows, uint32_t N, uint32_t k);
+// profiling only: reads the overflow count of the last scan into ctx->last_scan (synchronises)
+va_status note_overflow(va_context* ctx, const uint32_t* ovf_cnt);
 
 // Allocation-free entry point: resolves the device address of the fixed scratch block of
 // `device` (called once per device, with that device current, when a context is created).
@@ -293,6 +304,8 @@ struct SelectArgs {
     uint32_t k = 0;
     uint32_t id_offset = 0;        // added to output ids
     const uint32_t* row_map = nullptr;  // output row for each input row (nullptr: identity)
+    // device row count (rows past it are skipped; rows is then the host bound), or nullptr
+    const uint32_t* rows_dev = nullptr;
     // outputs (row stride out_ld, default k)
     int64_t out_ld = 0;
     uint32_t* out_idx = nullptr;   // [rows x k]
@@ -332,6 +345,8 @@ va_status fill_u32(va_context* ctx, uint32_t* p, uint64_t n, uint32_t v);
 //   3. select: exact (key, id) top-k of each candidate list;
 //   4. rows whose list overflowed are recomputed exactly, chunk by chunk (rare).
 // Small databases (N <= sample) go straight to dense keys + select.
+struct FbArgs;  // the device-side overflow fallback (va_fallback.hpp)
+
 struct KeyProducer {
     // keys for queries [q0, q0+nq) (or rows qrow[0..nq) when qrow != nullptr) against
     // database rows c0 + j*stride, j < cols, written to out_k[i * ldo + j]
@@ -341,6 +356,8 @@ struct KeyProducer {
     virtual va_status filter(const uint32_t* thr, uint32_t* cnt, uint32_t* ckey, uint32_t* cid, uint32_t cap) = 0;
     // every key the producer makes is below 2^key_bits()
     virtual uint32_t key_bits() const { return 32; }
+    // one pass of the device-side overflow fallback (fb_pass_kernel over the producer's keys)
+    virtual va_status fallback_pass(const FbArgs& a, int pass) = 0;
     virtual ~KeyProducer() = default;
 };
 

@@ -21,6 +21,7 @@
 #include <algorithm>
 #include <vector>
 
+#include "va_fallback.hpp"
 #include "va_internal.hpp"
 
 struct va_ivf {
@@ -119,6 +120,9 @@ struct F32Keys final : KeyProducer {
     const float* q;
     const float* x;
     uint32_t Q, N, D;
+    va_status fallback_pass(const FbArgs& a, int pass) override {
+        return fb_launch_pass(ctx, FbF32{q, int64_t(D), x, int64_t(D), N, D, int(OP_L2SQ)}, a, pass);
+    }
     va_status dense(const uint32_t* qrow, uint32_t q0, uint32_t nq, uint32_t c0, uint32_t cols, uint32_t stride,
                     uint32_t* out_k, int64_t ldo) override {
         DistArgs a;

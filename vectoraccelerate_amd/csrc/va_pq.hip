@@ -26,6 +26,7 @@
 #include <algorithm>
 #include <vector>
 
+#include "va_fallback.hpp"
 #include "va_internal.hpp"
 
 namespace va {
@@ -435,6 +436,9 @@ struct AdcProducer final : KeyProducer {
     const uint8_t* codes;
     const float* tables;
     uint32_t Q, N, M, K;
+    va_status fallback_pass(const FbArgs& a, int pass) override {
+        return fb_launch_pass(ctx, FbAdc{codes, tables, N, M, K}, a, pass);
+    }
     va_status dense(const uint32_t* qrow, uint32_t q0, uint32_t nq, uint32_t c0, uint32_t cols, uint32_t stride,
                     uint32_t* out_k, int64_t ldo) override {
         AdcArgs a;
@@ -646,9 +650,10 @@ va_status va_pq_search(va_context* ctx, const float* queries, uint32_t num_queri
     VA_REQUIRE(ctx, k >= 1 && k <= VA_MAX_K, "k must be in [1, %u], got %u", VA_MAX_K, k);
     if (num_queries == 0) return VA_OK;
     va::DeviceGuard g(ctx->device);
-    va::Owned own;
-    float* tables;
-    VA_CHECK_STATUS(va::alloc(ctx, own, size_t(num_queries) * M * K * 4, &tables));
+    // the tables live in the context's side buffer: the call returns without waiting for the scan
+    void* side = nullptr;
+    VA_CHECK_STATUS(va::side_reserve(ctx, size_t(num_queries) * M * K * 4, &side));
+    float* tables = static_cast<float*>(side);
     for (uint32_t q0 = 0; q0 < num_queries; q0 += 65535) {
         const uint32_t nq = std::min<uint32_t>(65535, num_queries - q0);
         VA_CHECK_STATUS(va_pq_distance_tables(ctx, queries + int64_t(q0) * dim, nq, dim, M, K, codebooks,
@@ -672,7 +677,6 @@ va_status va_pq_search(va_context* ctx, const float* queries, uint32_t num_queri
         va::sqrt_inplace<<<dim3(uint32_t((n + 255) / 256)), dim3(256), 0, ctx->stream>>>(out_dist, n);
         VA_CHECK_LAUNCH(ctx);
     }
-    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));  // the tables are freed on return
     return VA_OK;
 }
 

@@ -14,6 +14,7 @@
 #include <algorithm>
 #include <vector>
 
+#include "va_fallback.hpp"
 #include "va_internal.hpp"
 
 namespace va {
@@ -68,6 +69,18 @@ va_status mask_list_keys(va_context* ctx, uint32_t* keys, uint32_t* keys2, const
                                                                      ids + int64_t(r0) * ld, counts + r0, cap, ld, skip);
         VA_CHECK_LAUNCH(ctx);
     }
+    return VA_OK;
+}
+
+bool fb_fits(const va_context* ctx, size_t need, uint32_t rows, uint32_t N, uint32_t k) {
+    return !ctx->fixed_scratch || need + fb_bytes(rows, N, k) <= ctx->fixed_scratch_bytes;
+}
+
+va_status note_overflow(va_context* ctx, const uint32_t* ovf_cnt) {
+    if (!ctx->profiling) return VA_OK;  // diagnostics only: the search itself never reads it back
+    VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->host_word, ovf_cnt, 4, hipMemcpyDeviceToHost, ctx->stream));
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    ctx->last_scan.overflow_rows = ctx->host_word[0];
     return VA_OK;
 }
 
@@ -213,8 +226,11 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
     const uint32_t qs = plan.qs;
 
     Scratch s(ctx);
-    const size_t need = Scratch::round(uint64_t(Q) * 4) * 3 + Scratch::round(uint64_t(Q) * cap * 4) * 2 +
-                        Scratch::round(256) + Scratch::round(uint64_t(qs) * per_q_sample);
+    size_t need = Scratch::round(uint64_t(Q) * 4) * 3 + Scratch::round(uint64_t(Q) * cap * 4) * 2 +
+                  Scratch::round(256) + Scratch::round(uint64_t(qs) * per_q_sample);
+    // overflowed rows are finished on the device (no read-back) when the fallback's buffers fit
+    const bool device_fb = fb_fits(ctx, need, Q, N, k);
+    if (device_fb) need += fb_bytes(Q, N, k);
     VA_CHECK_STATUS(s.reserve(need));
     uint32_t* thr = s.carve<uint32_t>(Q);
     uint32_t* cnt = s.carve<uint32_t>(Q);
@@ -223,6 +239,13 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
     uint32_t* cid = s.carve<uint32_t>(uint64_t(Q) * cap);
     uint32_t* ovf_cnt = s.carve<uint32_t>(64);
     uint32_t* skeys = s.carve<uint32_t>(uint64_t(qs) * S);
+    FbArgs fb;
+    if (device_fb) {
+        fb = fb_carve(s, Q, N, k);
+        fb.n_rows = ovf_cnt;
+        fb.rows = ovf_rows;
+        fb.skip = out.skip;
+    }
 
     // ---- 1. sample thresholds -----------------------------------------------------------
     for (uint32_t q0 = 0; q0 < Q; q0 += qs) {
@@ -263,6 +286,12 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
         VA_CHECK_STATUS(launch_select(ctx, a));
     }
     VA_CHECK_STATUS(pm.mark(3));
+    if (device_fb) {
+        // ---- 4. exact top-k of the overflowed rows, on the device ------------------------------
+        VA_CHECK_STATUS(fb_run(ctx, kp, fb, base));
+        VA_CHECK_STATUS(pm.finish(true, true));
+        return note_overflow(ctx, ovf_cnt);
+    }
     VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->host_word, ovf_cnt, 4, hipMemcpyDeviceToHost, ctx->stream));
     VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
     const uint32_t n_ovf = ctx->host_word[0];

@@ -37,6 +37,7 @@
 #include <type_traits>
 #include <vector>
 
+#include "va_fallback.hpp"
 #include "va_internal.hpp"
 #include "va_screen_bound.hpp"
 
@@ -922,10 +923,13 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
 
     Scratch s(ctx);
     const size_t q4 = Scratch::round(uint64_t(Q) * 4);
-    const size_t need = q4 * 5 + Scratch::round(256) + Scratch::round(uint64_t(Q) * 16) +
-                        Scratch::round(uint64_t(Q) * Dp * 2) + Scratch::round(uint64_t(plan.qs) * S * 4) +
-                        Scratch::round(S * 4) +
-                        Scratch::round(uint64_t(Q) * cap * 4) * 3 + Scratch::round(uint64_t(Q) * rcap * 4) * 2;
+    size_t need = q4 * 5 + Scratch::round(256) + Scratch::round(uint64_t(Q) * 16) +
+                  Scratch::round(uint64_t(Q) * Dp * 2) + Scratch::round(uint64_t(plan.qs) * S * 4) +
+                  Scratch::round(S * 4) + Scratch::round(uint64_t(Q) * cap * 4) * 3 +
+                  Scratch::round(uint64_t(Q) * rcap * 4) * 2;
+    // overflowed queries are finished on the device (no read-back) when the fallback's buffers fit
+    const bool device_fb = fb_fits(ctx, need, Q, N, k);
+    if (device_fb) need += fb_bytes(Q, N, k);
     VA_CHECK_STATUS(s.reserve(need));
     uint32_t* thr = s.carve<uint32_t>(Q);
     uint32_t* cnt = s.carve<uint32_t>(Q);
@@ -942,6 +946,13 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     uint32_t* cid = s.carve<uint32_t>(uint64_t(Q) * cap);
     uint32_t* rr = s.carve<uint32_t>(uint64_t(Q) * rcap);
     uint32_t* rkey = s.carve<uint32_t>(uint64_t(Q) * rcap);
+    FbArgs fb;
+    if (device_fb) {
+        fb = fb_carve(s, Q, N, k);
+        fb.n_rows = ovf_cnt;
+        fb.rows = ovf_rows;
+        fb.skip = out.skip;
+    }
 
     // ---- 1. queries -> scaled fp16 ---------------------------------------------------------
     screen_prep_kernel<<<dim3((Q + 3) / 4), dim3(256), 0, ctx->stream>>>(in.q, int64_t(D), Q, D, Dp, qh, qinfo,
@@ -1037,11 +1048,15 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     screen_compact_kernel<<<dim3(Q), dim3(256), 0, ctx->stream>>>(cnt, clo, cid, ubound, uint32_t(cap), rr, rcount,
                                                                  uint32_t(rcap), ovf_cnt, ovf_rows, ovf_cnt + 1);
     VA_CHECK_LAUNCH(ctx);
-    // the overflow count and the longest list (sizes the rerank grid): the one read-back
-    VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->host_word, ovf_cnt, 8, hipMemcpyDeviceToHost, ctx->stream));
-    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    const uint32_t n_ovf = ctx->host_word[0];
-    const uint32_t gtiles = std::max<uint32_t>(1, (ctx->host_word[1] + 127) / 128);
+    // The rerank grid covers every list at its capacity (tiles past a list's end leave at once).
+    // Without the device fallback the overflow count and the longest list are read back instead.
+    uint32_t gtiles = uint32_t((rcap + 127) / 128), n_ovf = 0;
+    if (!device_fb) {
+        VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->host_word, ovf_cnt, 8, hipMemcpyDeviceToHost, ctx->stream));
+        VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        n_ovf = ctx->host_word[0];
+        gtiles = std::max<uint32_t>(1, (ctx->host_word[1] + 127) / 128);
+    }
     // ---- 6. exact fp32 keys of the rerank rows ---------------------------------------------------
     {
         DistArgs a;
@@ -1075,15 +1090,22 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
         VA_CHECK_STATUS(launch_select(ctx, a));
     }
     VA_CHECK_STATUS(pm.mark(3));
-    ctx->last_scan.overflow_rows = n_ovf;
     if (ctx->profiling) {
         // diagnostics only: how many rows the exact rerank scored
         std::vector<uint32_t> rc(Q);
-        VA_CHECK_HIP(ctx, hipMemcpy(rc.data(), rcount, size_t(Q) * 4, hipMemcpyDeviceToHost));
+        VA_CHECK_HIP(ctx, hipMemcpyAsync(rc.data(), rcount, size_t(Q) * 4, hipMemcpyDeviceToHost, ctx->stream));
+        VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
         uint64_t total = 0;
         for (uint32_t v : rc) total += v;
         ctx->last_scan.rerank_rows = uint32_t(std::min<uint64_t>(total, 0xFFFFFFFFu));
     }
+    if (device_fb) {
+        // ---- 8. exact top-k of the overflowed queries, on the device ---------------------------
+        VA_CHECK_STATUS(fb_run(ctx, exact, fb, base));
+        VA_CHECK_STATUS(pm.finish(true, true));
+        return note_overflow(ctx, ovf_cnt);
+    }
+    ctx->last_scan.overflow_rows = n_ovf;
     if (n_ovf == 0) return pm.finish(true, false);
     VA_CHECK_STATUS(rescan_rows(ctx, exact, N, k, base, ovf_rows, n_ovf, out.skip));
     return pm.finish(true, true);

@@ -133,6 +133,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelectArgs a) {
     extern __shared__ uint32_t s_row[];  // CACHED: the row's keys
 
     const uint32_t row = blockIdx.x;
+    if (a.rows_dev && row >= *a.rows_dev) return;  // past the device row count (uniform)
     const int tid = threadIdx.x;
     const uint32_t orow = a.row_map ? a.row_map[row] : row;
 
@@ -143,7 +144,7 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelectArgs a) {
     if (a.counts) {
         const uint32_t c = a.counts[row];
         if (c > a.n) {
-            // candidate list overflowed: the host re-runs this row on the exact chunked path
+            // candidate list overflowed: listed for the exact fallback, which writes the row
             if (tid == 0 && a.overflow_count) {
                 const uint32_t p = atomicAdd(a.overflow_count, 1u);
                 a.overflow_rows[p] = row;
