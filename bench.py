@@ -100,39 +100,42 @@ def measured_traffic(rel: str = TRAFFIC_SCREEN) -> float | None:
 
 
 def timed(ctx, fn, steps: int, warmup: int, scan_timings: bool = True):
-    """Run `warmup` untimed steps, then time exactly `steps` steps between synchronisations."""
+    """Run `warmup` untimed steps, then time exactly `steps` steps between synchronisations.
+    With scan_timings, the context's profiling records (hipEvents that nothing waits for inside
+    the loop) give the mean phase times of the timed steps' scans."""
     import torch
 
     for _ in range(warmup):
         fn()
     ctx.synchronize()
     torch.cuda.synchronize()
-    phases = []
+    if scan_timings:
+        ctx.reset_scan_totals()
     t0 = time.perf_counter()
     for _ in range(steps):
         fn()
-        if scan_timings:
-            phases.append(ctx.last_scan_timings())
     ctx.synchronize()
     torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e3 / steps, phases
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    if not scan_timings:
+        return ms, None
+    total, n = ctx.scan_totals()
+    return ms, (total, n, ctx.last_scan_timings())
 
 
 def mean_phases(phases):
-    import numpy as np
-
+    """Mean phase times per scan over a timed loop (from timed()), with the last scan's sizes."""
     if not phases:
         return {}
-    keys = ("sample_ms", "scan_ms", "select_ms", "fallback_ms", "total_ms")
-    out = {k: float(np.mean([p[k] for p in phases])) for k in keys}
-    out.update({k: phases[-1][k] for k in ("sample_rows", "candidate_cap", "overflow_rows", "screened",
-                                            "rerank_rows") if k in phases[-1]})
+    total, n, last = phases
+    n = max(n, 1)
+    out = {k: float(total[k]) / n for k in ("sample_ms", "scan_ms", "select_ms", "fallback_ms", "total_ms")}
+    out["scans"] = n
+    out.update({k: last[k] for k in ("sample_rows", "candidate_cap", "overflow_rows", "screened", "rerank_rows")
+                if k in last})
     return out
 
 
-# ---------------------------------------------------------------------------------------
-# configs[1]: flat cosine top-100, 1M x 1536 fp32, Q = 1024 (headline)
-# ---------------------------------------------------------------------------------------
 def run_c2(ctx, a, cpu: bool, extra_l2: bool):
     import numpy as np
     import torch

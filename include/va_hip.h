@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define VA_HIP_ABI_VERSION 3
+#define VA_HIP_ABI_VERSION 4
 #define VA_SENTINEL_INDEX 0xFFFFFFFFu
 /* largest k accepted by the top-K entry points */
 #define VA_MAX_K 1024u
@@ -94,10 +94,12 @@ const char* va_last_error_message(const va_context* ctx);
 typedef enum { VA_OPT_CANDIDATE_CAP = 1, VA_OPT_SAMPLE_ROWS = 2, VA_OPT_SCREEN = 3 } va_option;
 va_status va_context_set_option(va_context* ctx, va_option option, uint64_t value);
 
-/* Phase timings of the last top-k scan, from hipEvents on the context stream.  Replaces
+/* Phase timings of the top-k scans, from hipEvents on the context stream.  Replaces
  * Metal4Configuration.enableProfiling + GPUTimingInfo (Core/Metal4Context.swift:17,48-64,389-404)
- * and IVFPhaseTimings (Index/Kernels/IVF/IVFKernels.swift:295).  With profiling on, every
- * scan synchronises at its end to read the events. */
+ * and IVFPhaseTimings (Index/Kernels/IVF/IVFKernels.swift:295).  With profiling on, a scan
+ * records its events (and copies its overflow / rerank counts) without waiting; the events are
+ * read when va_context_last_scan or va_context_scan_totals is called, or when the record is
+ * reused 16 scans later. */
 typedef struct {
     float sample_ms;        /* threshold sample: dense keys + k-th selection          */
     float scan_ms;          /* the filtering scan kernel (the dominant kernel)         */
@@ -112,7 +114,13 @@ typedef struct {
     uint32_t rerank_rows;   /* screened search: rows re-scored exactly, all queries   */
 } va_scan_timings;
 va_status va_context_set_profiling(va_context* ctx, int enable);
-va_status va_context_last_scan(const va_context* ctx, va_scan_timings* out);
+/* The last profiled scan (waits for its events). */
+va_status va_context_last_scan(va_context* ctx, va_scan_timings* out);
+/* Phase times and counts summed over the profiled scans since the last reset (waits for their
+ * events); *count = the number of scans.  No reference counterpart: averaging a timed loop
+ * without reading events inside it. */
+va_status va_context_scan_totals(va_context* ctx, va_scan_timings* sum, uint32_t* count);
+va_status va_context_reset_scan_totals(va_context* ctx);
 
 /* ---- buffers: replace getBuffer / BufferToken (Core/Metal4Context.swift:471-488;
  *      Core/BufferPool.swift:89-200) ------------------------------------------ */

@@ -54,6 +54,8 @@ SIGNATURES: dict[str, tuple] = {
     "va_context_set_option": (_st, [_p, _i32, _u64]),
     "va_context_set_profiling": (_st, [_p, _i32]),
     "va_context_last_scan": (_st, [_p, _p]),
+    "va_context_scan_totals": (_st, [_p, _p, C.POINTER(C.c_uint32)]),
+    "va_context_reset_scan_totals": (_st, [_p]),
     "va_buffer_alloc": (_st, [_p, C.c_size_t, C.POINTER(_p)]),
     "va_buffer_free": (_st, [_p, _p]),
     "va_buffer_upload": (_st, [_p, _p, _p, C.c_size_t]),

@@ -124,9 +124,20 @@ class GPUContext:
         self.check(self.lib.va_context_set_profiling(self.handle, int(bool(enable))), "va_context_set_profiling")
 
     def last_scan_timings(self) -> dict:
+        """Phase timings of the last profiled scan (waits for its events)."""
         t = _lib.ScanTimings()
         self.check(self.lib.va_context_last_scan(self.handle, C.byref(t)), "va_context_last_scan")
         return t.as_dict()
+
+    def reset_scan_totals(self) -> None:
+        self.check(self.lib.va_context_reset_scan_totals(self.handle), "va_context_reset_scan_totals")
+
+    def scan_totals(self) -> tuple[dict, int]:
+        """(phase times and counts summed over the profiled scans since the reset, number of scans)."""
+        t = _lib.ScanTimings()
+        n = C.c_uint32(0)
+        self.check(self.lib.va_context_scan_totals(self.handle, C.byref(t), C.byref(n)), "va_context_scan_totals")
+        return t.as_dict(), int(n.value)
 
     def set_option(self, option: int, value: int) -> None:
         self.check(self.lib.va_context_set_option(self.handle, int(option), int(value)), "va_context_set_option")

@@ -54,6 +54,76 @@ va_status Scratch::reserve(size_t total) {
     return VA_OK;
 }
 
+va_context::ScanRecord* profile_record(va_context* ctx) {
+    auto& r = ctx->rec[ctx->rec_next];
+    if (!r.ev[0]) return nullptr;
+    if (r.pending) profile_fold(ctx, r);
+    ctx->rec_next = (ctx->rec_next + 1) % va_context::kScanRing;
+    r.has_ovf = r.has_rerank = false;
+    return &r;
+}
+
+void profile_fold(va_context* ctx, va_context::ScanRecord& r) {
+    (void)ctx;
+    r.pending = false;
+    if (hipEventSynchronize(r.ev[4]) != hipSuccess) {
+        (void)hipGetLastError();
+        return;
+    }
+    auto ms = [&](int a, int b) {
+        float t = 0.0f;
+        if (hipEventElapsedTime(&t, r.ev[a], r.ev[b]) != hipSuccess) {
+            (void)hipGetLastError();
+            return -1.0f;
+        }
+        return t;
+    };
+    va_scan_timings& t = r.t;
+    t.total_ms = ms(0, 4);
+    if (r.sampled) {
+        t.sample_ms = ms(0, 1);
+        t.scan_ms = ms(1, 2);
+        t.select_ms = ms(2, 3);
+        t.fallback_ms = r.fallback ? ms(3, 4) : 0.0f;
+    } else {
+        t.sample_ms = 0.0f;
+        t.scan_ms = t.total_ms;
+        t.select_ms = 0.0f;
+        t.fallback_ms = 0.0f;
+    }
+    if (r.has_ovf) t.overflow_rows = r.host_word[0];
+    if (r.has_rerank) t.rerank_rows = r.host_word[1];
+    va_scan_timings& s = ctx->rec_sum;
+    s.sample_ms += t.sample_ms;
+    s.scan_ms += t.scan_ms;
+    s.select_ms += t.select_ms;
+    s.fallback_ms += t.fallback_ms;
+    s.total_ms += t.total_ms;
+    s.overflow_rows += t.overflow_rows;
+    s.rerank_rows += t.rerank_rows;
+    s.scan_launches += t.scan_launches;
+    ctx->rec_count++;
+}
+
+__global__ __launch_bounds__(256) void sum_u32_kernel(const uint32_t* v, uint32_t n, uint32_t* out) {
+    __shared__ uint32_t part[256];
+    uint32_t s = 0;
+    for (uint32_t i = threadIdx.x; i < n; i += 256) s += v[i];
+    part[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (int(threadIdx.x) < w) part[threadIdx.x] += part[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) *out = part[0];
+}
+
+va_status sum_u32_into(va_context* ctx, const uint32_t* v, uint32_t n, uint32_t* out) {
+    sum_u32_kernel<<<dim3(1), dim3(256), 0, ctx->stream>>>(v, n, out);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
 va_status side_reserve(va_context* ctx, size_t bytes, void** out) {
     if (bytes > ctx->side_bytes) {
         // grow: wait for in-flight readers of the old buffer, then replace it
@@ -193,8 +263,12 @@ va_status va_context_destroy(va_context* ctx) {
         if (ctx->scratch) (void)hipFree(ctx->scratch);
         if (ctx->side) (void)hipFree(ctx->side);
         if (ctx->host_word) (void)hipHostFree(ctx->host_word);
-        for (auto& e : ctx->ev)
-            if (e) (void)hipEventDestroy(e);
+        for (auto& r : ctx->rec) {
+            for (auto& e : r.ev)
+                if (e) (void)hipEventDestroy(e);
+            if (r.dev_word) (void)hipFree(r.dev_word);
+            if (r.host_word) (void)hipHostFree(r.host_word);
+        }
         for (int i = 0; i < va_context::kAux; ++i) {
             if (ctx->aux[i]) {
                 (void)hipStreamSynchronize(ctx->aux[i]);
@@ -225,16 +299,50 @@ const char* va_last_error_message(const va_context* ctx) { return ctx ? ctx->las
 va_status va_context_set_profiling(va_context* ctx, int enable) {
     if (!ctx) return VA_ERR_INVALID_ARG;
     va::DeviceGuard g(ctx->device);
-    if (enable && !ctx->ev[0]) {
-        for (auto& e : ctx->ev) VA_CHECK_HIP(ctx, hipEventCreate(&e));
+    if (enable && !ctx->rec[0].ev[0]) {
+        for (auto& r : ctx->rec) {
+            for (auto& e : r.ev) VA_CHECK_HIP(ctx, hipEventCreate(&e));
+            VA_CHECK_HIP(ctx, hipMalloc(&r.dev_word, 4));
+            void* h = nullptr;
+            VA_CHECK_HIP(ctx, hipHostMalloc(&h, 8, hipHostMallocDefault));
+            r.host_word = static_cast<uint32_t*>(h);
+        }
     }
     ctx->profiling = enable != 0;
     return VA_OK;
 }
 
-va_status va_context_last_scan(const va_context* ctx, va_scan_timings* out) {
+static void fold_pending(va_context* ctx) {
+    // oldest first, so the totals add up in enqueue order
+    for (int i = 1; i <= va_context::kScanRing; ++i) {
+        auto& r = ctx->rec[(ctx->rec_next + i - 1) % va_context::kScanRing];
+        if (r.pending) va::profile_fold(ctx, r);
+    }
+}
+
+va_status va_context_last_scan(va_context* ctx, va_scan_timings* out) {
     if (!ctx || !out) return VA_ERR_INVALID_ARG;
-    *out = ctx->last_scan;
+    va::DeviceGuard g(ctx->device);
+    fold_pending(ctx);
+    *out = ctx->rec_last >= 0 ? ctx->rec[ctx->rec_last].t : ctx->last_scan;
+    return VA_OK;
+}
+
+va_status va_context_scan_totals(va_context* ctx, va_scan_timings* sum, uint32_t* count) {
+    if (!ctx || !sum || !count) return VA_ERR_INVALID_ARG;
+    va::DeviceGuard g(ctx->device);
+    fold_pending(ctx);
+    *sum = ctx->rec_sum;
+    *count = ctx->rec_count;
+    return VA_OK;
+}
+
+va_status va_context_reset_scan_totals(va_context* ctx) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    va::DeviceGuard g(ctx->device);
+    fold_pending(ctx);
+    ctx->rec_sum = va_scan_timings{};
+    ctx->rec_count = 0;
     return VA_OK;
 }
 

@@ -84,6 +84,73 @@ typedef float fb_f32x4 __attribute__((ext_vector_type(4)));
 // stages, step e of each 8-value group pairing d = 8g + e (lane half 0) with 8g + 4 + e (half 1);
 // squared norms as per-half fmaf chains over the same values, the halves then added; values
 // past D are zeros.  The per-element sequence is the GEMM's, so the keys are bit-identical.
+// qp: the query of column l % 32 (nullptr: zeros); xp: the database row of row l % 32 (nullptr:
+// zeros).  keys[4j + e] = key of (column l % 32, row 8j + 4h + e), h = l / 32.
+// VEC: D % 4 == 0 and 16-byte aligned rows (one 16-byte load per value group).  The loads of
+// stage s + 1 are issued before stage s computes (two register sets); exactly ceil(D / 16)
+// stages run, as in the GEMM (a further all-zero stage could turn a -0 dot into +0).
+template <bool VEC>
+__device__ inline void f32_block_keys(const float* qp, const float* xp, uint32_t D, int op, int lane,
+                                      uint32_t* keys) {
+    const int hh = lane >> 5;
+    auto load4 = [&](const float* p, uint32_t d) {
+        fb_f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (p && d < D) {
+            if (VEC) {
+                v = *reinterpret_cast<const fb_f32x4*>(p + d);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (d + e < D) v[e] = p[d + e];
+            }
+        }
+        return v;
+    };
+    fb_f32x16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+    float qss = 0.0f, xss = 0.0f;
+    fb_f32x4 xa[2], qa[2], xb[2], qb[2];
+    auto ld = [&](uint32_t d0, fb_f32x4(&xv)[2], fb_f32x4(&qv)[2]) {
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const uint32_t d = d0 + 8 * g + 4 * hh;
+            xv[g] = load4(xp, d);
+            qv[g] = load4(qp, d);
+        }
+    };
+    auto cmp = [&](const fb_f32x4(&xv)[2], const fb_f32x4(&qv)[2]) {
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qss = fmaf(qv[g][e], qv[g][e], qss);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xss = fmaf(xv[g][e], xv[g][e], xss);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xv[g][e], qv[g][e], acc, 0, 0, 0);
+        }
+    };
+    const uint32_t ns = (D + 15) / 16;
+    ld(0, xa, qa);
+    for (uint32_t s = 0; s < ns; s += 2) {
+        ld(16 * (s + 1), xb, qb);  // past D: zeros, not computed
+        cmp(xa, qa);
+        if (s + 1 >= ns) break;
+        ld(16 * (s + 2), xa, qa);
+        cmp(xb, qb);
+    }
+    const float qq = qss + __shfl_xor(qss, 32);
+    const float xt = xss + __shfl_xor(xss, 32);  // |x|^2 of row l % 32
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float xx = __shfl(xt, 8 * j + 4 * hh + e);
+            keys[4 * j + e] = key_of_float(apply_op(op, acc[4 * j + e], qq, xx));
+        }
+}
+
 struct FbF32 {
     const float* q;
     int64_t ldq;
@@ -92,45 +159,10 @@ struct FbF32 {
     uint32_t N, D;
     int op;
     __device__ void keys16(const uint32_t* rows, uint32_t s0, uint32_t n, uint32_t r0, int lane, uint32_t* keys) const {
-        const int l32 = lane & 31, hh = lane >> 5;
+        const int l32 = lane & 31;
         const float* qp = (s0 + l32 < n) ? q + int64_t(rows[s0 + l32]) * ldq : nullptr;
         const float* xp = (r0 + l32 < N) ? x + int64_t(r0 + l32) * ldx : nullptr;
-        auto load4 = [&](const float* p, uint32_t d) {
-            fb_f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (p) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (d + e < D) v[e] = p[d + e];
-            }
-            return v;
-        };
-        fb_f32x16 acc;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
-        float qss = 0.0f, xss = 0.0f;
-        for (uint32_t d0 = 0; d0 < D; d0 += 16) {
-#pragma unroll
-            for (int g = 0; g < 2; ++g) {
-                const uint32_t d = d0 + 8 * g + 4 * hh;
-                const fb_f32x4 bv = load4(qp, d);
-                const fb_f32x4 av = load4(xp, d);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) qss = fmaf(bv[e], bv[e], qss);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) xss = fmaf(av[e], av[e], xss);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[e], bv[e], acc, 0, 0, 0);
-            }
-        }
-        const float qq = qss + __shfl_xor(qss, 32);
-        const float xt = xss + __shfl_xor(xss, 32);  // |x|^2 of row r0 + l32
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float xx = __shfl(xt, 8 * j + 4 * hh + e);
-                keys[4 * j + e] = key_of_float(apply_op(op, acc[4 * j + e], qq, xx));
-            }
+        f32_block_keys<false>(qp, xp, D, op, lane, keys);
     }
 };
 

@@ -41,10 +41,22 @@ struct va_context {
     size_t side_bytes = 0;
     // pinned host word used to read back small counters
     uint32_t* host_word = nullptr;
-    // phase profiling of the top-k scan (va_context_set_profiling)
+    // phase profiling of the top-k scan (va_context_set_profiling): a ring of records whose
+    // events are read when a record is reused or the timings are asked for, so a profiled scan
+    // never waits on the host
     bool profiling = false;
-    hipEvent_t ev[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
-    va_scan_timings last_scan{};
+    static constexpr int kScanRing = 16;
+    struct ScanRecord {
+        hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+        uint32_t* dev_word = nullptr;   // device scratch of the record's counts
+        uint32_t* host_word = nullptr;  // pinned: [0] overflowed rows, [1] reranked rows
+        bool pending = false, sampled = false, fallback = false, has_ovf = false, has_rerank = false;
+        va_scan_timings t{};
+    } rec[kScanRing];
+    int rec_next = 0, rec_last = -1;
+    va_scan_timings rec_sum{};  // phase times summed over the scans folded since the last reset
+    uint32_t rec_count = 0;
+    va_scan_timings last_scan{};  // the scan being enqueued (static fields)
     // extra streams for independent launches that overlap (default priority); created on
     // first use, with the events that fork them from and join them back into `stream`.  Three,
     // so that with `stream` they fit HIP's default of four hardware queues per process
@@ -106,8 +118,7 @@ struct Scratch {
 size_t dense_budget(const va_context* ctx);
 // whether the device-side overflow fallback's buffers for `rows` rows fit beside `need` bytes
 bool fb_fits(const va_context* ctx, size_t need, uint32_t rows, uint32_t N, uint32_t k);
-// profiling only: reads the overflow count of the last scan into ctx->last_scan (synchronises)
-va_status note_overflow(va_context* ctx, const uint32_t* ovf_cnt);
+
 
 // Allocation-free entry point: resolves the device address of the fixed scratch block of
 // `device` (called once per device, with that device current, when a context is created).
@@ -402,41 +413,51 @@ ScanPlan plan_scan(const va_context* ctx, uint32_t Q, uint32_t N, uint32_t k, bo
 va_status rescan_rows(va_context* ctx, KeyProducer& kp, uint32_t N, uint32_t k, const SelectArgs& base,
                       const uint32_t* rows_dev, uint32_t n_rows, const uint8_t* skip = nullptr);
 
-// hipEvent marks of the scan phases (no-ops unless profiling is on)
+// Takes the next profiling record of the ring, folding the scan it held first (that scan is
+// long finished in steady state).  nullptr on failure.
+va_context::ScanRecord* profile_record(va_context* ctx);
+// Waits for a pending record's events and adds its phase times to the context's totals.
+void profile_fold(va_context* ctx, va_context::ScanRecord& r);
+// Enqueues sum(v[0..n)) into *out (one workgroup).
+va_status sum_u32_into(va_context* ctx, const uint32_t* v, uint32_t n, uint32_t* out);
+
+// hipEvent marks of the scan phases (no-ops unless profiling is on).  Nothing here waits: the
+// events are read when the record is reused or the timings are asked for.
 struct ScanPhaseMarks {
     va_context* ctx;
+    va_context::ScanRecord* r = nullptr;
     explicit ScanPhaseMarks(va_context* c) : ctx(c) {}
     va_status mark(int i) {
         if (!ctx->profiling) return VA_OK;
-        VA_CHECK_HIP(ctx, hipEventRecord(ctx->ev[i], ctx->stream));
+        if (i == 0 || !r) r = profile_record(ctx);
+        if (!r) return VA_ERR_HIP;
+        VA_CHECK_HIP(ctx, hipEventRecord(r->ev[i], ctx->stream));
         return VA_OK;
     }
-    float ms(int a, int b) {
-        float t = 0.0f;
-        if (hipEventElapsedTime(&t, ctx->ev[a], ctx->ev[b]) != hipSuccess) {
-            (void)hipGetLastError();
-            return -1.0f;
-        }
-        return t;
+    // profiling only: the device count of overflowed rows, read with the record
+    va_status count_overflow(const uint32_t* dev_count) {
+        if (!ctx->profiling || !r) return VA_OK;
+        VA_CHECK_HIP(ctx, hipMemcpyAsync(r->host_word, dev_count, 4, hipMemcpyDeviceToHost, ctx->stream));
+        r->has_ovf = true;
+        return VA_OK;
+    }
+    // profiling only: the sum of a device array (rows re-scored by the rerank), read with the record
+    va_status count_sum(const uint32_t* v, uint32_t n) {
+        if (!ctx->profiling || !r) return VA_OK;
+        VA_CHECK_STATUS(sum_u32_into(ctx, v, n, r->dev_word));
+        VA_CHECK_HIP(ctx, hipMemcpyAsync(r->host_word + 1, r->dev_word, 4, hipMemcpyDeviceToHost, ctx->stream));
+        r->has_rerank = true;
+        return VA_OK;
     }
     // events: 0 start, 1 after sample, 2 after scan, 3 after select, 4 end
     va_status finish(bool sampled, bool fallback) {
-        if (!ctx->profiling) return VA_OK;
-        VA_CHECK_STATUS(mark(4));
-        VA_CHECK_HIP(ctx, hipEventSynchronize(ctx->ev[4]));
-        va_scan_timings& t = ctx->last_scan;
-        t.total_ms = ms(0, 4);
-        if (sampled) {
-            t.sample_ms = ms(0, 1);
-            t.scan_ms = ms(1, 2);
-            t.select_ms = ms(2, 3);
-            t.fallback_ms = fallback ? ms(3, 4) : 0.0f;
-        } else {
-            t.sample_ms = 0.0f;
-            t.scan_ms = t.total_ms;
-            t.select_ms = 0.0f;
-            t.fallback_ms = 0.0f;
-        }
+        if (!ctx->profiling || !r) return VA_OK;
+        VA_CHECK_HIP(ctx, hipEventRecord(r->ev[4], ctx->stream));
+        r->sampled = sampled;
+        r->fallback = fallback;
+        r->t = ctx->last_scan;
+        r->pending = true;
+        ctx->rec_last = int(r - ctx->rec);
         return VA_OK;
     }
 };

@@ -76,14 +76,6 @@ bool fb_fits(const va_context* ctx, size_t need, uint32_t rows, uint32_t N, uint
     return !ctx->fixed_scratch || need + fb_bytes(rows, N, k) <= ctx->fixed_scratch_bytes;
 }
 
-va_status note_overflow(va_context* ctx, const uint32_t* ovf_cnt) {
-    if (!ctx->profiling) return VA_OK;  // diagnostics only: the search itself never reads it back
-    VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->host_word, ovf_cnt, 4, hipMemcpyDeviceToHost, ctx->stream));
-    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    ctx->last_scan.overflow_rows = ctx->host_word[0];
-    return VA_OK;
-}
-
 size_t dense_budget(const va_context* ctx) {
     constexpr size_t kArena = 256ull << 20;
     return ctx->fixed_scratch ? std::min(kArena, ctx->fixed_scratch_bytes / 4) : kArena;
@@ -285,12 +277,12 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
         a.overflow_rows = ovf_rows;
         VA_CHECK_STATUS(launch_select(ctx, a));
     }
+    if (device_fb) VA_CHECK_STATUS(pm.count_overflow(ovf_cnt));  // profiling only
     VA_CHECK_STATUS(pm.mark(3));
     if (device_fb) {
         // ---- 4. exact top-k of the overflowed rows, on the device ------------------------------
         VA_CHECK_STATUS(fb_run(ctx, kp, fb, base));
-        VA_CHECK_STATUS(pm.finish(true, true));
-        return note_overflow(ctx, ovf_cnt);
+        return pm.finish(true, true);
     }
     VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->host_word, ovf_cnt, 4, hipMemcpyDeviceToHost, ctx->stream));
     VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));

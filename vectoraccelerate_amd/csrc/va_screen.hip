@@ -828,6 +828,41 @@ __global__ __launch_bounds__(256) void screen_compact_kernel(const uint32_t* __r
     }
 }
 
+// ---- exact fp32 keys of the rerank lists ------------------------------------------------------
+// One wave per (32-row chunk of a query's list, query): the 32x32 MFMA block of the distance GEMM
+// with the query in column 0 (the other columns are zeros), so every key equals the fp32 scan's.
+// Persistent over the chunks (chunk-major, so the busy chunks spread over every wave); chunks past
+// a list's length are skipped.  Each lane streams one row of the chunk.
+template <bool VEC>
+__global__ __launch_bounds__(256) void rerank_kernel(const float* __restrict__ q, const float* __restrict__ x,
+                                                     uint32_t D, int op, const uint32_t* __restrict__ rr,
+                                                     const uint32_t* __restrict__ rcount, uint32_t rcap, uint32_t Q,
+                                                     uint32_t* __restrict__ rkey) {
+    const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5;
+    const uint32_t nch = (rcap + 31) / 32;
+    const uint64_t items = uint64_t(Q) * nch;
+    const uint32_t nw = gridDim.x * 4;
+    for (uint64_t it = uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6); it < items; it += nw) {
+        const uint32_t c = uint32_t(it / Q), qi = uint32_t(it % Q);
+        const uint32_t n = min(rcount[qi], rcap);
+        if (c * 32 >= n) continue;  // (uniform)
+        const uint32_t p = c * 32 + uint32_t(l32);
+        const float* qp = l32 == 0 ? q + int64_t(qi) * D : nullptr;
+        const float* xp = p < n ? x + int64_t(rr[int64_t(qi) * rcap + p]) * D : nullptr;
+        uint32_t keys[16];
+        f32_block_keys<VEC>(qp, xp, D, op, lane, keys);
+        if (l32 == 0) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t m = c * 32 + uint32_t(8 * j + 4 * hh + e);
+                    if (m < n) rkey[int64_t(qi) * rcap + m] = keys[4 * j + e];
+                }
+        }
+    }
+}
+
 template <int MODE>
 va_status launch_screen(va_context* ctx, const ScreenArgs& a) {
     using namespace scr;
@@ -1048,34 +1083,23 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     screen_compact_kernel<<<dim3(Q), dim3(256), 0, ctx->stream>>>(cnt, clo, cid, ubound, uint32_t(cap), rr, rcount,
                                                                  uint32_t(rcap), ovf_cnt, ovf_rows, ovf_cnt + 1);
     VA_CHECK_LAUNCH(ctx);
-    // The rerank grid covers every list at its capacity (tiles past a list's end leave at once).
-    // Without the device fallback the overflow count and the longest list are read back instead.
-    uint32_t gtiles = uint32_t((rcap + 127) / 128), n_ovf = 0;
+    // Without the device fallback the overflow count is read back (one synchronisation).
+    uint32_t n_ovf = 0;
     if (!device_fb) {
-        VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->host_word, ovf_cnt, 8, hipMemcpyDeviceToHost, ctx->stream));
+        VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->host_word, ovf_cnt, 4, hipMemcpyDeviceToHost, ctx->stream));
         VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
         n_ovf = ctx->host_word[0];
-        gtiles = std::max<uint32_t>(1, (ctx->host_word[1] + 127) / 128);
     }
     // ---- 6. exact fp32 keys of the rerank rows ---------------------------------------------------
     {
-        DistArgs a;
-        a.q = in.q;
-        a.ldq = D;
-        a.x = in.x;
-        a.ldx = D;
-        a.Q = Q;
-        a.N = uint32_t(rcap);
-        a.D = D;
-        a.op = in.op;
-        a.out = OUT_KEYS;
-        a.out_k = rkey;
-        a.ldo = int64_t(rcap);
-        a.gather = rr;
-        a.gcount = rcount;
-        a.gcap = uint32_t(rcap);
-        a.gtiles = gtiles;
-        VA_CHECK_STATUS(launch_dist(ctx, a));
+        const uint64_t items = uint64_t(Q) * ((rcap + 31) / 32);
+        const uint32_t blocks = uint32_t(std::min<uint64_t>(2048, (items + 3) / 4));
+        const bool vec = D % 4 == 0 && (reinterpret_cast<uintptr_t>(in.q) & 15) == 0 &&
+                         (reinterpret_cast<uintptr_t>(in.x) & 15) == 0;
+        auto kern = vec ? &rerank_kernel<true> : &rerank_kernel<false>;
+        kern<<<dim3(blocks), dim3(256), 0, ctx->stream>>>(in.q, in.x, D, int(in.op), rr, rcount, uint32_t(rcap), Q,
+                                                          rkey);
+        VA_CHECK_LAUNCH(ctx);
         VA_CHECK_STATUS(mask_list_keys(ctx, rkey, nullptr, rr, rcount, Q, uint32_t(rcap), int64_t(rcap), out.skip));
     }
     // ---- 7. exact (key, id) top-k ----------------------------------------------------------------
@@ -1089,21 +1113,14 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
         a.rows = Q;
         VA_CHECK_STATUS(launch_select(ctx, a));
     }
+    // profiling only: rows the exact rerank scored, queries that overflowed
+    VA_CHECK_STATUS(pm.count_sum(rcount, Q));
+    if (device_fb) VA_CHECK_STATUS(pm.count_overflow(ovf_cnt));
     VA_CHECK_STATUS(pm.mark(3));
-    if (ctx->profiling) {
-        // diagnostics only: how many rows the exact rerank scored
-        std::vector<uint32_t> rc(Q);
-        VA_CHECK_HIP(ctx, hipMemcpyAsync(rc.data(), rcount, size_t(Q) * 4, hipMemcpyDeviceToHost, ctx->stream));
-        VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
-        uint64_t total = 0;
-        for (uint32_t v : rc) total += v;
-        ctx->last_scan.rerank_rows = uint32_t(std::min<uint64_t>(total, 0xFFFFFFFFu));
-    }
     if (device_fb) {
         // ---- 8. exact top-k of the overflowed queries, on the device ---------------------------
         VA_CHECK_STATUS(fb_run(ctx, exact, fb, base));
-        VA_CHECK_STATUS(pm.finish(true, true));
-        return note_overflow(ctx, ovf_cnt);
+        return pm.finish(true, true);
     }
     ctx->last_scan.overflow_rows = n_ovf;
     if (n_ovf == 0) return pm.finish(true, false);
