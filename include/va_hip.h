@@ -12,8 +12,9 @@
  *    stream.  They return once the work is enqueued unless stated otherwise; call
  *    va_context_synchronize() before reading results on the host (the reference's
  *    executeAndWait, Core/Metal4Context.swift:342-410).  The top-k searches
- *    (va_fused_topk, va_i8_scan_topk, va_hamming_topk, va_pq_search, va_index_search)
- *    never wait on the host: queries whose candidate list overflows are
+ *    (va_fused_topk, va_i8_scan_topk, va_hamming_topk, va_pq_search, va_ivf_search,
+ *    va_ivf_scan, va_index_search) never wait on the host: queries whose candidate list
+ *    overflows are
  *    finished on the device by a fallback whose launches exit at once when nothing
  *    overflowed, so searches can be queued back to back on one stream.  A call that has to
  *    grow the context's scratch arena waits for the stream once, before the growth.

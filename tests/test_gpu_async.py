@@ -228,3 +228,94 @@ def test_fallback_whole_database_ties(ctx, oracle):
     assert t["overflow_rows"] == Q
     oi, od = oracle.hamming_topk(qb, xb, 33)
     check_topk_exact(gi, gd, oi, od)
+
+
+def _ivf(ctx, C, D, N, Q, seed, zipf, add_first_id=None):
+    from tests.test_gpu_ivf import clustered
+    from vectoraccelerate_amd import IVFSearchConfiguration, IVFSearchPipeline
+
+    c, x, q = clustered(C, D, N, Q, seed, zipf)
+    pipe = IVFSearchPipeline(ctx, IVFSearchConfiguration(C, 8, D))
+    xd = ctx.buffer(x)
+    if add_first_id is None:
+        st = pipe.prepareIndexStructure(c, xd)
+        ids = np.arange(N, dtype=np.int64)
+    else:  # the second half added with caller ids far above N
+        h = N // 2
+        st = pipe.prepareIndexStructure(c, xd[:h])
+        st.add(xd[h:], add_first_id)
+        ids = np.concatenate([np.arange(h), add_first_id + np.arange(N - h)]).astype(np.int64)
+    return pipe, st, c, x, q, ids
+
+
+@pytest.mark.parametrize("added", [False, True])
+def test_ivf_fallback_bit_identical_to_scan(ctx, added):
+    """IVF queries forced to overflow a tiny candidate list: the device fallback (which walks each
+    overflowed query's probed lists with the arithmetic of the kernel that scanned each list,
+    the 16-query tiles for lists few queries probe and the distance GEMM for the others) gives the
+    unforced search's ids and distances bit for bit, also with row ids far above N."""
+    from vectoraccelerate_amd import _lib
+
+    pipe, st, c, x, q, ids = _ivf(ctx, 64, 96, 30000, 300, 5, 1.1, 3_000_000_000 if added else None)
+    ref = pipe.search(q, st, 20)
+    ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 24)
+    try:
+        forced = pipe.search(q, st, 20)
+    finally:
+        ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 0)
+    ri, fi = ref.indices.cpu().numpy().view(np.uint32), forced.indices.cpu().numpy().view(np.uint32)
+    np.testing.assert_array_equal(fi, ri)
+    np.testing.assert_array_equal(forced.distances.cpu().numpy().view(np.uint32),
+                                  ref.distances.cpu().numpy().view(np.uint32))
+    assert np.isin(ri.astype(np.int64), ids).all()
+    st.close()
+
+
+def test_ivf_fallback_whole_list_ties(ctx, oracle):
+    """Every row of a list equal to its centroid: all keys of a list tie, the tie lists overflow
+    and the id-edge pass keeps the lowest ids, as the oracle's list scan does."""
+    from tests.test_gpu_ivf import clustered
+    from vectoraccelerate_amd import IVFSearchConfiguration, IVFSearchPipeline, _lib
+
+    c, x, q = clustered(16, 32, 20000, 24, 11, 1.1)
+    lab = oracle.ivf_assign(x, c)
+    x = np.ascontiguousarray(c[lab])  # rows = their centroids (every list's keys tie)
+    pipe = IVFSearchPipeline(ctx, IVFSearchConfiguration(16, 3, 32))
+    st = pipe.prepareIndexStructure(c, x)
+    off, ids = st.lists()
+    probes = pipe.findNearestCentroids(q, st).cpu().numpy().view(np.uint32)
+    ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 16)
+    try:
+        res = pipe.searchLists(q, st, probes, 30)
+    finally:
+        ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 0)
+    oi, od = oracle.ivf_scan(q, x, off, ids, probes, 30)
+    check_topk(L2SQ, q, x, 30, res.indices.cpu().numpy().view(np.uint32), res.distances.cpu().numpy(), oi, od)
+    st.close()
+
+
+def test_ivf_search_queues_behind_other_searches(ctx, oracle):
+    """An IVF search between two flat searches on one context, one synchronisation at the end."""
+    import torch
+
+    from tests.test_gpu_ivf import clustered
+    from vectoraccelerate_amd import IVFSearchConfiguration, IVFSearchPipeline
+
+    c, x, q = clustered(64, 64, 20000, 200, 3, 1.1)
+    pipe = IVFSearchPipeline(ctx, IVFSearchConfiguration(64, 8, 64))
+    st = pipe.prepareIndexStructure(c, x)
+    off, ids = st.lists()
+    qd, xd = _dev(ctx, q), _dev(ctx, x)
+    i1, d1 = _fused(ctx, L2SQ, qd, xd, 200, 20000, 64, 10)
+    ii, di = _out(ctx, 200, 10, torch.int32), _out(ctx, 200, 10, torch.float32)
+    pipe.encodeSearch(qd, st, ii, di, 10)
+    i2, d2 = _fused(ctx, COSINE, qd, xd, 200, 20000, 64, 5)
+    ctx.synchronize()
+    oi, od = oracle.flat_topk(L2SQ, q, x, 10)
+    check_topk(L2SQ, q, x, 10, _host(i1, np.uint32), _host(d1), oi, od)
+    oi, od = oracle.flat_topk(COSINE, q, x, 5)
+    check_topk(COSINE, q, x, 5, _host(i2, np.uint32), _host(d2), oi, od)
+    probes = oracle.ivf_probe(q, c, 8)
+    oi, od = oracle.ivf_scan(q, x, off, ids, probes, 10)
+    check_topk(L2SQ, q, x, 10, _host(ii, np.uint32), _host(di), oi, od)
+    st.close()

@@ -83,52 +83,27 @@ struct Tile {
 // DMA = true: the stages move global -> LDS by direct buffer loads (no register staging, so
 // fewer VGPRs and more waves per SIMD); needs 16-byte rows (VEC) and the swizzled 64-byte LDS
 // rows.  DMA = false: register-staged loads, any row alignment.
-template <int WQ, int WN, bool VEC, int OUT, bool DMA>
-__global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) void dist_gemm_kernel(DistArgs a) {
+// One tile: queries qs + i (i < qc; through qrow when given) x database rows at positions
+// rs + j (j < rc).  Every wave of the workgroup calls it with the same tile.
+// LOOP: called once per iteration of the planned launch's tile loop.  The thread index then goes
+// through an opaque move, so that nothing derived from it is hoisted out of the loop and held
+// across the whole tile (the main loop has no register to spare).
+// (the planned launches are the IVF list scans: L2^2, the distance fixed at compile time)
+template <int WQ, int WN, bool VEC, int OUT, bool DMA, bool LOOP = false>
+__device__ __forceinline__ void dist_tile(const DistArgs& a, uint32_t qs, uint32_t qc, uint32_t rs, uint32_t rc) {
+    const int op = LOOP ? int(OP_L2SQ) : int(a.op);
     using T = Tile<WQ, WN>;
-    static_assert(!DMA || (VEC && LDS_STRIDE == KC), "direct loads need 16-byte rows and unpadded LDS rows");
     extern __shared__ float lds[];
     float* nrm = lds + (DMA ? VA_DIST_DMA_SLOTS * T::DSTAGE : T::NSTAGE * T::STAGE);  // [waves][128] squared norms of the wave's rows
 
-    const int tid = threadIdx.x;
+    int tid = int(threadIdx.x);
+    if constexpr (LOOP) asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"(tid));
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wq = wave % WQ;
     const int wn = wave / WQ;
     const int l32 = lane & 31;
     const int hh = lane >> 5;
-
-    // XCD-aware order: workgroup w runs on XCD w % 8.  XCD x takes database tiles x, x+8, ...
-    // and runs every query block of a tile back to back, so each tile crosses the fabric once
-    // and is reused from that XCD's L2 (the grid is padded to a multiple of 8 tiles).
-    const uint32_t nqb = (a.tiles || a.gather) ? 1u : (a.Q + T::TQ - 1) / T::TQ;
-    const uint32_t xcd = blockIdx.x % kXcds, seq = blockIdx.x / kXcds;
-    const uint32_t qb = seq % nqb;
-    const uint32_t tb = (seq / nqb) * kXcds + xcd;
-    if (!a.tiles && !a.gather && tb * uint32_t(T::TN) >= a.N) return;  // padding workgroup
-    // Tile extent: queries qs + i (i < qc; through qrow when given) and database rows at
-    // positions rs + j*rstride (j < rc).  Flat launches derive it from blockIdx; list-major
-    // (IVF) launches read one descriptor {qs, qc, rs, rc} per workgroup; gather launches take
-    // one query and up to 128 rows of its gather list.
-    uint32_t qs = qb * T::TQ, rs = tb * T::TN, qc, rc, rstride = 1;
-    if (a.gather) {
-        qs = blockIdx.x / a.gtiles;
-        rs = (blockIdx.x % a.gtiles) * uint32_t(T::TN);
-        const uint32_t m = min(a.gcount[qs], a.gcap);
-        if (rs >= m) return;  // empty tile (uniform)
-        qc = 1;
-        rc = min(uint32_t(T::TN), m - rs);
-    } else if (a.tiles) {
-        const uint32_t* td = a.tiles + 4 * int64_t(blockIdx.x);
-        qs = td[0];
-        qc = td[1];
-        rs = td[2];
-        rc = td[3];
-        rstride = a.rstride;
-    } else {
-        qc = min(uint32_t(T::TQ), a.Q - qs);
-        rc = min(uint32_t(T::TN), a.N - rs);
-    }
 
     f32x16 acc[4];
 #pragma unroll
@@ -190,7 +165,7 @@ __global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) 
                 }
             } else if (row < T::ROWS) {
                 const uint32_t jr = uint32_t(row - T::TQ);
-                if (jr < rc) base[i] = uint32_t(int64_t(jr) * rstride * a.ldx * 4) + 16u * uint32_t(c);
+                if (jr < rc) base[i] = uint32_t(int64_t(jr) * a.ldx * 4) + 16u * uint32_t(c);
             }
         }
         const uint32_t lds0 = lds_addr_of(lds);
@@ -254,7 +229,7 @@ __global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) 
                     const uint32_t jr = uint32_t(row - T::TQ);
                     if (jr < rc) {
                         const int64_t xr = a.gather ? int64_t(a.gather[int64_t(qs) * a.gcap + rs + jr])
-                                                    : int64_t(rs + jr * rstride);
+                                                    : int64_t(rs + jr);
                         src[j] = a.x + xr * a.ldx + col;
                     }
                 }
@@ -328,7 +303,7 @@ __global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) 
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const uint32_t r = uint32_t(wn * 128 + mloc + e);
-                    const uint32_t key = key_of_float(apply_op(a.op, acc[b][4 * j + e], qq, xx[e]));
+                    const uint32_t key = key_of_float(apply_op(op, acc[b][4 * j + e], qq, xx[e]));
                     if (r < rc && key < bk && key < 0xFFFFFFFEu) {  // NaN distances never win
                         bk = key;
                         bi = rs + r;
@@ -363,7 +338,7 @@ __global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) 
                     const f32x4v xx = *reinterpret_cast<const f32x4v*>(nrm + wave * 128 + mloc);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const uint32_t key = key_of_float(apply_op(a.op, acc[b][4 * j + e], qq, xx[e]));
+                        const uint32_t key = key_of_float(apply_op(op, acc[b][4 * j + e], qq, xx[e]));
                         keys[16 * bb + 4 * j + e] = key;
                         const bool p = (uint32_t(wn * 128 + mloc + e) < rc) & (key <= thr);
                         pass |= uint64_t(p) << (16 * bb + 4 * j + e);
@@ -376,7 +351,7 @@ __global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) 
                 if (!((pass >> t) & 1)) continue;
                 if (pos < a.cap) {
                     const int b = NB * h + (t >> 4), j = (t >> 2) & 3, e = t & 3;
-                    const uint32_t p = rs + uint32_t(wn * 128 + b * 32 + 8 * j + 4 * hh + e) * rstride;
+                    const uint32_t p = rs + uint32_t(wn * 128 + b * 32 + 8 * j + 4 * hh + e);
                     const int64_t o = int64_t(qi) * a.cap + pos;
                     a.cand_key[o] = keys[t];
                     a.cand_id[o] = a.ids ? a.ids[p] : a.id_base + p;
@@ -395,7 +370,7 @@ __global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) 
             const f32x4v xx = *reinterpret_cast<const f32x4v*>(nrm + wave * 128 + mloc);
             float val[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) val[e] = apply_op(a.op, acc[b][4 * j + e], qq, xx[e]);
+            for (int e = 0; e < 4; ++e) val[e] = apply_op(op, acc[b][4 * j + e], qq, xx[e]);
             const uint32_t jr = uint32_t(wn * 128 + mloc);  // row slot of acc element e = 0
             if (OUT == OUT_KEYS) {
                 uint32_t* o = a.out_k + int64_t(orow) * a.ldo + rs + jr;
@@ -417,16 +392,58 @@ __global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) 
     }
 }
 
-template <int WQ, int WN, bool VEC, int OUT, bool DMA>
+// PLAN: a device-planned list-major launch (a.plan): a fixed grid loops over the tiles of the
+// plan, each decoded from the plan's per-list tile counts.
+template <int WQ, int WN, bool VEC, int OUT, bool DMA, bool PLAN>
+__global__ __launch_bounds__(64 * WQ * WN, DMA ? VA_DIST_DMA_WPE : VA_DIST_WPE) void dist_gemm_kernel(DistArgs a) {
+    using T = Tile<WQ, WN>;
+    static_assert(!DMA || (VEC && LDS_STRIDE == KC), "direct loads need 16-byte rows and unpadded LDS rows");
+    if constexpr (PLAN) {
+        const uint32_t total = a.plan.pre[a.plan.C];
+        for (uint32_t t = blockIdx.x; t < total; t += gridDim.x) {
+            uint32_t qs, qc, rs, rc;
+            plan_tile(a.plan, t, uint32_t(T::TQ), uint32_t(T::TN), qs, qc, rs, rc);
+            dist_tile<WQ, WN, VEC, OUT, DMA, true>(a, qs, qc, rs, rc);
+            __syncthreads();  // the tile's LDS is read to the end before the next tile's loads
+        }
+        return;
+    } else {
+        // XCD-aware order: workgroup w runs on XCD w % 8.  XCD x takes database tiles x, x+8, ...
+        // and runs every query block of a tile back to back, so each tile crosses the fabric once
+        // and is reused from that XCD's L2 (the grid is padded to a multiple of 8 tiles).
+        const uint32_t nqb = a.gather ? 1u : (a.Q + T::TQ - 1) / T::TQ;
+        const uint32_t xcd = blockIdx.x % kXcds, seq = blockIdx.x / kXcds;
+        const uint32_t qb = seq % nqb;
+        const uint32_t tb = (seq / nqb) * kXcds + xcd;
+        if (!a.gather && tb * uint32_t(T::TN) >= a.N) return;  // padding workgroup
+        // Tile extent.  Flat launches derive it from blockIdx; gather launches take one query and
+        // up to 128 rows of its gather list.
+        uint32_t qs = qb * T::TQ, rs = tb * T::TN, qc, rc;
+        if (a.gather) {
+            qs = blockIdx.x / a.gtiles;
+            rs = (blockIdx.x % a.gtiles) * uint32_t(T::TN);
+            const uint32_t m = min(a.gcount[qs], a.gcap);
+            if (rs >= m) return;  // empty tile (uniform)
+            qc = 1;
+            rc = min(uint32_t(T::TN), m - rs);
+        } else {
+            qc = min(uint32_t(T::TQ), a.Q - qs);
+            rc = min(uint32_t(T::TN), a.N - rs);
+        }
+        dist_tile<WQ, WN, VEC, OUT, DMA>(a, qs, qc, rs, rc);
+    }
+}
+
+template <int WQ, int WN, bool VEC, int OUT, bool DMA, bool PLAN = false>
 va_status launch_tile(va_context* ctx, const DistArgs& a) {
     using T = Tile<WQ, WN>;
     const uint64_t nqb = (a.Q + T::TQ - 1) / T::TQ;
     const uint64_t ntb = (a.N + T::TN - 1) / T::TN;
-    const uint64_t grid = a.gather ? uint64_t(a.Q) * a.gtiles
-                          : a.tiles ? a.ntiles : nqb * ((ntb + kXcds - 1) / kXcds) * kXcds;
+    const uint64_t grid = PLAN ? a.plan.grid
+                          : a.gather ? uint64_t(a.Q) * a.gtiles : nqb * ((ntb + kXcds - 1) / kXcds) * kXcds;
     if (grid == 0) return VA_OK;
     if (grid > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "distance grid too large (%llu tiles)", (unsigned long long)grid);
-    auto kern = &dist_gemm_kernel<WQ, WN, VEC, OUT, DMA>;
+    auto kern = &dist_gemm_kernel<WQ, WN, VEC, OUT, DMA, PLAN>;
     const size_t lds_bytes = DMA ? T::DMA_LDS_BYTES : T::LDS_BYTES;
     if (lds_bytes > 65536) {
         VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -444,14 +461,22 @@ bool dma_fits(const DistArgs& a, bool vec) {
     if (!VA_DIST_DMA || !vec || LDS_STRIDE != KC) return false;
     const uint64_t qrows = a.qrow ? a.q_rows : a.Q;
     if (qrows == 0) return false;
-    const uint64_t tn = a.tiles ? Tile<WQ, WN>::TN : std::min<uint64_t>(Tile<WQ, WN>::TN, a.N);
-    const uint64_t rstride = a.tiles ? a.rstride : 1;
+    const uint64_t tn = a.plan.pre ? Tile<WQ, WN>::TN : std::min<uint64_t>(Tile<WQ, WN>::TN, a.N);
     return (qrows - 1) * uint64_t(a.ldq) * 4 + uint64_t(a.D) * 4 <= kDmaMaxBytes &&
-           (tn - 1) * rstride * uint64_t(a.ldx) * 4 + uint64_t(a.D) * 4 <= kDmaMaxBytes;
+           (tn - 1) * uint64_t(a.ldx) * 4 + uint64_t(a.D) * 4 <= kDmaMaxBytes;
 }
 
 template <int WQ, int WN, int OUT>
 va_status launch_shape(va_context* ctx, const DistArgs& a, bool vec) {
+    if (a.plan.pre) {
+        if constexpr (OUT == OUT_FILTER) {
+            if constexpr (LDS_STRIDE == KC)
+                if (dma_fits<WQ, WN>(a, vec)) return launch_tile<WQ, WN, true, OUT, true, true>(ctx, a);
+            return vec ? launch_tile<WQ, WN, true, OUT, false, true>(ctx, a)
+                       : launch_tile<WQ, WN, false, OUT, false, true>(ctx, a);
+        }
+        return fail(ctx, VA_ERR_INVALID_ARG, "launch_dist: planned launches are filter launches");
+    }
     if constexpr (LDS_STRIDE == KC)
         if (dma_fits<WQ, WN>(a, vec)) return launch_tile<WQ, WN, true, OUT, true>(ctx, a);
     return vec ? launch_tile<WQ, WN, true, OUT, false>(ctx, a) : launch_tile<WQ, WN, false, OUT, false>(ctx, a);
@@ -460,12 +485,12 @@ va_status launch_shape(va_context* ctx, const DistArgs& a, bool vec) {
 }  // namespace
 
 va_status launch_dist(va_context* ctx, const DistArgs& a) {
-    if (a.tiles ? a.ntiles == 0 : (a.Q == 0 || a.N == 0)) return VA_OK;
+    if (a.plan.pre ? a.plan.grid == 0 : (a.Q == 0 || a.N == 0)) return VA_OK;
     const bool vec = (a.D % 4 == 0) && (a.ldq % 4 == 0) && (a.ldx % 4 == 0) &&
                      ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
     if (a.gather) {
         // rows come from anywhere in the database (64-bit addresses): register-staged loads
-        if (a.out != OUT_KEYS || a.tiles || a.qrow || a.gtiles == 0 || a.gcap == 0 || !a.gcount)
+        if (a.out != OUT_KEYS || a.plan.pre || a.qrow || a.gtiles == 0 || a.gcap == 0 || !a.gcount)
             return fail(ctx, VA_ERR_INVALID_ARG, "launch_dist: malformed gather launch");
         return vec ? launch_tile<1, 1, true, OUT_KEYS, false>(ctx, a) : launch_tile<1, 1, false, OUT_KEYS, false>(ctx, a);
     }

@@ -16,10 +16,19 @@ __global__ __launch_bounds__(256) void fb_init_kernel(FbArgs a) {
     if (i0 < 8) a.done[i0] = 0;
 }
 
-va_status fb_run(va_context* ctx, KeyProducer& kp, const FbArgs& a, const SelectArgs& base) {
+va_status fb_init(va_context* ctx, const FbArgs& a) {
     fb_init_kernel<<<dim3(256), dim3(256), 0, ctx->stream>>>(a);
     VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
+va_status fb_run(va_context* ctx, KeyProducer& kp, const FbArgs& a, const SelectArgs& base) {
+    VA_CHECK_STATUS(fb_init(ctx, a));
     for (int pass = 0; pass < kFbPasses; ++pass) VA_CHECK_STATUS(kp.fallback_pass(a, pass));
+    return fb_select(ctx, a, base, kp.key_bits());
+}
+
+va_status fb_select(va_context* ctx, const FbArgs& a, const SelectArgs& base, uint32_t key_bits) {
     SelectArgs s = base;
     s.keys = a.lkey;
     s.ids = a.lid;
@@ -31,7 +40,7 @@ va_status fb_run(va_context* ctx, KeyProducer& kp, const FbArgs& a, const Select
     s.row_map = a.rows;
     s.overflow_count = nullptr;
     s.overflow_rows = nullptr;
-    s.key_bits = kp.key_bits();
+    s.key_bits = key_bits;
     return launch_select(ctx, s);
 }
 

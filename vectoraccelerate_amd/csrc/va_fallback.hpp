@@ -18,6 +18,8 @@
 // 32x32 MFMA output layout: lane (l, h) holds query slot l % 32 and rows 8j + 4h + e.
 #pragma once
 
+#include <algorithm>
+
 #include "va_distop.hpp"
 #include "va_internal.hpp"
 
@@ -28,8 +30,8 @@ struct FbArgs {
     const uint32_t* rows = nullptr;    // device: their query ids
     uint32_t rmax = 0;                 // slots the buffers hold (a host bound on the count)
     uint32_t N = 0, k = 0;
-    uint32_t ishift = 0;               // tie-id histogram bin = id >> ishift (N >> ishift < 4096)
-    uint32_t cap = 0;                  // list capacity per slot: k + 2^ishift, rounded up
+    uint32_t ishift = 0;               // tie-id histogram bin = id >> ishift (ids below N: bins < 4096)
+    uint32_t cap = 0;                  // list capacity per slot: k + min(2^ishift, rows), rounded up
     uint32_t* hist = nullptr;          // [rmax][2048] key histogram (cleared after each use)
     uint32_t* tidh = nullptr;          // [rmax][4096] tie-id histogram
     uint32_t* st = nullptr;            // [rmax][8] bucket state (see FbState)
@@ -44,25 +46,27 @@ constexpr int kFbPasses = 5;
 constexpr uint32_t kFbGrid = 1024;  // workgroups per pass (4 waves each)
 constexpr uint32_t kFbTieBins = 4096;
 
-// host: list capacity and id shift for N rows and top-k
-inline void fb_geometry(uint32_t N, uint32_t k, uint32_t& ishift, uint32_t& cap) {
+// host: list capacity and id shift for ids below N, `rows` rows in all (0: N) and top-k.  The
+// id-edge pass keeps fewer than k ties plus one id bin, which holds at most min(2^ishift, rows).
+inline void fb_geometry(uint32_t N, uint32_t k, uint32_t& ishift, uint32_t& cap, uint32_t rows = 0) {
     ishift = 0;
     while ((uint64_t(N) >> ishift) >= kFbTieBins) ++ishift;
-    cap = uint32_t((uint64_t(k) + (uint64_t(1) << ishift) + 63) / 64 * 64);
+    const uint64_t bin = std::min<uint64_t>(uint64_t(1) << ishift, rows ? rows : N);
+    cap = uint32_t((uint64_t(k) + bin + 63) / 64 * 64);
 }
-inline size_t fb_bytes(uint32_t rmax, uint32_t N, uint32_t k) {
+inline size_t fb_bytes(uint32_t rmax, uint32_t N, uint32_t k, uint32_t rows = 0) {
     uint32_t ishift, cap;
-    fb_geometry(N, k, ishift, cap);
+    fb_geometry(N, k, ishift, cap, rows);
     return Scratch::round(uint64_t(rmax) * 2048 * 4) + Scratch::round(uint64_t(rmax) * kFbTieBins * 4) +
            Scratch::round(uint64_t(rmax) * 8 * 4) + Scratch::round(uint64_t(rmax) * 4) +
            Scratch::round(uint64_t(rmax) * cap * 4) * 2 + Scratch::round(8 * 4);
 }
-inline FbArgs fb_carve(Scratch& s, uint32_t rmax, uint32_t N, uint32_t k) {
+inline FbArgs fb_carve(Scratch& s, uint32_t rmax, uint32_t N, uint32_t k, uint32_t rows = 0) {
     FbArgs a;
     a.rmax = rmax;
     a.N = N;
     a.k = k;
-    fb_geometry(N, k, a.ishift, a.cap);
+    fb_geometry(N, k, a.ishift, a.cap, rows);
     a.hist = s.carve<uint32_t>(uint64_t(rmax) * 2048);
     a.tidh = s.carve<uint32_t>(uint64_t(rmax) * kFbTieBins);
     a.st = s.carve<uint32_t>(uint64_t(rmax) * 8);
@@ -336,6 +340,57 @@ struct FbRun {
     }
 };
 
+// One slot's state for a pass (read once per work item).
+struct FbSlot {
+    uint32_t s, prefix, K, edge;
+    FbRun run;
+};
+// false: the slot takes no part in this pass (pass 4 runs only for rows whose ties overflowed)
+__device__ inline bool fb_slot_begin(const FbArgs& a, int pass, uint32_t s, FbSlot& sl) {
+    const uint32_t* st = a.st + int64_t(s) * 8;
+    if (pass == 4 && !st[FB_OVF]) return false;
+    sl.s = s;
+    sl.prefix = pass >= 1 ? st[FB_PREFIX] : 0u;
+    sl.K = pass >= 3 ? st[FB_K] : 0u;
+    sl.edge = pass == 4 ? st[FB_EDGE] : 0u;
+    sl.run = FbRun{a.hist + int64_t(s) * 2048};
+    return true;
+}
+// The pass's action for one (key, id) of the slot.
+__device__ inline void fb_consume(const FbArgs& a, int pass, FbSlot& sl, uint32_t key, uint32_t id) {
+    if (pass == 0) {
+        sl.run.add(key >> 21);
+    } else if (pass == 1) {
+        if ((key >> 21) == sl.prefix) sl.run.add((key >> 10) & 2047u);
+    } else if (pass == 2) {
+        if ((key >> 10) == sl.prefix) sl.run.add(key & 1023u);
+    } else if (key < sl.K || (key == sl.K && (pass == 3 || id < sl.edge))) {
+        const uint32_t pos = atomicAdd(a.cnt + sl.s, 1u);
+        if (pos < a.cap) {
+            a.lkey[int64_t(sl.s) * a.cap + pos] = key;
+            a.lid[int64_t(sl.s) * a.cap + pos] = id;
+        }
+        if (pass == 3 && key == sl.K) {
+            const uint32_t bin = id >> a.ishift;  // below kFbTieBins for ids below N (clamped regardless)
+            atomicAdd(a.tidh + int64_t(sl.s) * kFbTieBins + (bin < kFbTieBins ? bin : kFbTieBins - 1), 1u);
+        }
+    }
+}
+// End of a pass kernel (every thread of every workgroup): the last workgroup to finish (a
+// completion ticket, nobody waits) resolves the pass.
+__device__ inline void fb_pass_done(const FbArgs& a, int pass, uint32_t n) {
+    __shared__ uint32_t s_last;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence();
+        s_last = atomicAdd(a.done + pass, 1u) == gridDim.x - 1 ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    fb_resolve(a, pass, n);
+}
+
 template <class P>
 __global__ __launch_bounds__(256) void fb_pass_kernel(P p, FbArgs a, int pass) {
     const uint32_t n = fb_count(a);
@@ -349,46 +404,17 @@ __global__ __launch_bounds__(256) void fb_pass_kernel(P p, FbArgs a, int pass) {
         const uint32_t s = g * 32 + l32;
         uint32_t keys[16];
         p.keys16(a.rows, g * 32, n, t * 32, lane, keys);
-        if (s >= n) continue;
-        const uint32_t* st = a.st + int64_t(s) * 8;
-        const uint32_t prefix = pass >= 1 ? st[FB_PREFIX] : 0u;
-        const uint32_t K = pass >= 3 ? st[FB_K] : 0u;
-        if (pass == 4 && !st[FB_OVF]) continue;
-        const uint32_t edge = pass == 4 ? st[FB_EDGE] : 0u;
-        FbRun run{a.hist + int64_t(s) * 2048};
+        FbSlot sl;
+        if (s >= n || !fb_slot_begin(a, pass, s, sl)) continue;
 #pragma unroll 1
         for (int i = 0; i < 16; ++i) {
             const uint32_t r = t * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
             if (r >= a.N) continue;
-            const uint32_t key = (a.skip && a.skip[r]) ? kAbsentKey : keys[i];
-            if (pass == 0) {
-                run.add(key >> 21);
-            } else if (pass == 1) {
-                if ((key >> 21) == prefix) run.add((key >> 10) & 2047u);
-            } else if (pass == 2) {
-                if ((key >> 10) == prefix) run.add(key & 1023u);
-            } else if (key < K || (key == K && (pass == 3 || r < edge))) {
-                const uint32_t pos = atomicAdd(a.cnt + s, 1u);
-                if (pos < a.cap) {
-                    a.lkey[int64_t(s) * a.cap + pos] = key;
-                    a.lid[int64_t(s) * a.cap + pos] = r;
-                }
-                if (pass == 3 && key == K) atomicAdd(a.tidh + int64_t(s) * kFbTieBins + (r >> a.ishift), 1u);
-            }
+            fb_consume(a, pass, sl, (a.skip && a.skip[r]) ? kAbsentKey : keys[i], r);
         }
-        run.flush();
+        sl.run.flush();
     }
-    // completion ticket: the last workgroup resolves the pass (nobody waits)
-    __shared__ uint32_t s_last;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence();
-        s_last = atomicAdd(a.done + pass, 1u) == gridDim.x - 1 ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    fb_resolve(a, pass, n);
+    fb_pass_done(a, pass, n);
 }
 
 __global__ __launch_bounds__(256) void fb_init_kernel(FbArgs a);
@@ -403,5 +429,9 @@ va_status fb_launch_pass(va_context* ctx, const P& p, const FbArgs& a, int pass)
 // Enqueues the whole fallback (clear, five passes, selection) for the producer's keys; base
 // carries the outputs and the key kind of the scan's selection.
 va_status fb_run(va_context* ctx, KeyProducer& kp, const FbArgs& a, const SelectArgs& base);
+// The clear before the first pass and the selection after the last, for callers with their own
+// pass kernels (the IVF list scan).
+va_status fb_init(va_context* ctx, const FbArgs& a);
+va_status fb_select(va_context* ctx, const FbArgs& a, const SelectArgs& base, uint32_t key_bits);
 
 }  // namespace va

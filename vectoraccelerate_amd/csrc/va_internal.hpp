@@ -254,6 +254,54 @@ enum DistOut : int {
     OUT_ARGMIN = 3,  // best[q] = min over rows of (key << 32 | row id) (64-bit atomic min)
 };
 
+// IVF threshold sample: a prefix of every probed list (rows are in insertion order, so a prefix
+// is an unbiased subset) of at least 1/64 of its rows and at least 128 rows.  Every list is
+// sampled at rate >= 1/64, so a query's candidate count stays within about 64 x k; the floor
+// keeps small lists' sample tiles full.
+constexpr uint32_t kIvfSampleRate = 64;
+constexpr uint32_t kIvfSampleMin = 128;
+VA_HD inline uint32_t ivf_sample_rows(uint32_t n) {
+    const uint32_t s = (n + kIvfSampleRate - 1) / kIvfSampleRate;
+    const uint32_t m = s > kIvfSampleMin ? s : kIvfSampleMin;
+    return n < m ? n : m;
+}
+
+// A device-planned list-major launch (IVF): tiles of TQ queries x TN rows over the lists of one
+// tile shape, enumerated by pre[] (the exclusive prefix over the lists of their tile counts for
+// this shape; pre[C] tiles in all).  List l is probed by the queries qlist[qoff[l] .. qoff[l+1])
+// (the launch's qrow) and holds the row positions roff[l] .. roff[l+1] (its sample prefix when
+// sample is set).  Tile t of list l covers query block (t - pre[l]) / row blocks and row block
+// (t - pre[l]) % row blocks.
+struct ListPlan {
+    const uint32_t* pre = nullptr;   // [C + 1]
+    const uint32_t* qoff = nullptr;  // [C + 1]
+    const uint32_t* roff = nullptr;  // [C + 1]
+    uint32_t C = 0;
+    uint32_t sample = 0;
+    uint32_t grid = 0;  // workgroups of the persistent launch (host)
+};
+#ifdef __HIPCC__
+__device__ inline void plan_tile(const ListPlan& p, uint32_t t, uint32_t TQ, uint32_t TN, uint32_t& qs, uint32_t& qc,
+                                 uint32_t& rs, uint32_t& rc) {
+    uint32_t lo = 0, hi = p.C - 1;  // the last list l with pre[l] <= t
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi + 1) >> 1;
+        if (p.pre[mid] <= t) lo = mid;
+        else hi = mid - 1;
+    }
+    const uint32_t l = lo, local = t - p.pre[lo];
+    const uint32_t nq = p.qoff[l + 1] - p.qoff[l];
+    const uint32_t len = p.roff[l + 1] - p.roff[l];
+    const uint32_t n = p.sample ? ivf_sample_rows(len) : len;
+    const uint32_t nrb = (n + TN - 1) / TN;
+    const uint32_t qb = local / nrb, rb = local % nrb;
+    qs = p.qoff[l] + qb * TQ;
+    qc = min(TQ, nq - qb * TQ);
+    rs = p.roff[l] + rb * TN;
+    rc = min(TN, n - rb * TN);
+}
+#endif
+
 struct DistArgs {
     const float* q = nullptr;   // query rows
     const uint32_t* qrow = nullptr;  // optional query-row indirection (query i reads row qrow[i])
@@ -276,12 +324,7 @@ struct DistArgs {
     uint32_t id_base = 0;  // added to database row ids in filter mode
     // argmin mode: packed (key, row) minimum per query, initialised to ~0 by the caller
     unsigned long long* best = nullptr;
-    // list-major (IVF) launches: one {qs, qc, rs, rc} descriptor per workgroup; query i of a
-    // tile is row qrow[qs + i], database row j is at position rs + j*rstride, whose id is
-    // ids[position].  Q / N are ignored then.
-    const uint32_t* tiles = nullptr;
-    uint32_t ntiles = 0;
-    uint32_t rstride = 1;
+    // filter launches: the id of database row position p is ids[p] (nullptr: id_base + p)
     const uint32_t* ids = nullptr;
     // gather launches (the exact rerank of screened candidates): workgroup b takes query
     // b / gtiles and the rows gather[q * gcap + j] for j in [128 t, 128 t + 128) of its list of
@@ -291,6 +334,9 @@ struct DistArgs {
     const uint32_t* gcount = nullptr;
     uint32_t gcap = 0;
     uint32_t gtiles = 0;
+    // device-planned list-major (IVF) launches (plan.pre set): persistent over the plan's
+    // tiles; query i of a tile is row qrow[qs + i]; Q / N are ignored then
+    ListPlan plan;
     int wq = 0;  // waves along queries (tiles of 32*wq queries); 0 = from Q
     int wn = 0;  // waves along rows (tiles of 128*wn rows); 0 = 4/wq.  wq x wn in {1x4, 2x2, 4x1}, and
                  // for OUT_FILTER also 1x1, 2x1

@@ -6,16 +6,20 @@
 // with insertion order inside each list (as the reference does), and the list vectors gathered
 // into CSR order by a device copy kernel (the reference memcpy-gathers on the host).
 //
-// Search (IVFSearchPipeline.search, Index/Kernels/IVF/IVFSearchPipeline.swift:197-568):
+// Search (IVFSearchPipeline.search, Index/Kernels/IVF/IVFSearchPipeline.swift:197-568), queued
+// without any host read-back:
 //   probe : the nprobe nearest centroids by (L2^2, id) through the exact top-k scan;
+//   plan  : on the device, from the probes: the queries probing each list and, per tile shape,
+//           the prefix of the lists' tile counts (the scan kernels decode their tiles from it);
 //   scan  : list-major — every (list, block of the queries that probe it, block of its rows)
 //           is one MFMA tile of the distance kernel, so a list's rows are read once per block
 //           of up to 128 probing queries instead of once per query (ivf_list_search,
 //           Metal/Shaders/IVFListSearch.metal:199-339, streams each query's lists separately);
-//   top-k : a strided in-list sample (every 64th row of each probed list) gives each query an
-//           upper bound tau_q of its k-th distance; the full scan appends only keys <= tau_q;
-//           exact (L2^2, row id) selection follows.  Queries whose candidate list overflows
-//           are rescanned with room for every candidate they have.
+//           persistent launches, one per tile shape;
+//   top-k : a prefix sample of each probed list gives each query an upper bound tau_q of its
+//           k-th distance; the full scan appends only keys <= tau_q; exact (L2^2, row id)
+//           selection follows.  Queries whose candidate list overflows are finished by the
+//           device fallback over their probed lists, with each list's own arithmetic.
 // The reference's per-thread heap (K_PRIVATE = 8) is only exact for k <= 8; this is exact
 // for every k <= VA_MAX_K.
 #include <algorithm>
@@ -32,22 +36,30 @@ struct va_ivf {
     uint32_t* ids = nullptr;        // [N] original row id of every CSR position
     uint32_t* offsets = nullptr;    // [C + 1]
     std::vector<uint32_t> h_offsets;
+    // host bounds of a search (from the list sizes, so a search reads nothing back): top_rows[p]
+    // = rows of the p longest lists, top_sample[p] = their threshold-sample rows, max_len =
+    // the longest list
+    std::vector<uint64_t> top_rows, top_sample;
+    uint32_t max_len = 0;
+    uint64_t id_end = 0;  // one past the largest row id (ids of added rows are the caller's)
     uint32_t* probe_buf = nullptr;  // probes of va_ivf_search
     size_t probe_cap = 0;
+    void refresh_bounds() {
+        std::vector<uint32_t> len(C);
+        for (uint32_t l = 0; l < C; ++l) len[l] = h_offsets[l + 1] - h_offsets[l];
+        std::sort(len.begin(), len.end(), [](uint32_t a, uint32_t b) { return a > b; });
+        top_rows.assign(C + 1, 0);
+        top_sample.assign(C + 1, 0);
+        for (uint32_t i = 0; i < C; ++i) {
+            top_rows[i + 1] = top_rows[i] + len[i];
+            top_sample[i + 1] = top_sample[i] + va::ivf_sample_rows(len[i]);
+        }
+        max_len = C ? len[0] : 0;
+    }
 };
 
 namespace va {
 namespace {
-
-// Threshold sample: a prefix of every probed list (rows are in insertion order, so a prefix is
-// an unbiased subset) of at least 1/kSampleRate of its rows and at least kSampleMin rows.
-// Every list is sampled at rate >= 1/kSampleRate, so a query's candidate count stays within
-// about kSampleRate x k; the floor keeps small lists' sample tiles full.
-constexpr uint32_t kSampleRate = 64;
-constexpr uint32_t kSampleMin = 128;
-inline uint32_t sample_rows(uint32_t n) {
-    return std::min(n, std::max((n + kSampleRate - 1) / kSampleRate, kSampleMin));
-}
 
 // va_ivf_add: old CSR position p of list c moves to p + pre[c] (the new rows of earlier lists
 // come before it)
@@ -104,14 +116,6 @@ __global__ __launch_bounds__(256) void gather_rows(const float* __restrict__ x, 
         } else {
             for (uint32_t d = threadIdx.x; d < D; d += 256) dst[d] = src[d];
         }
-    }
-}
-
-__global__ __launch_bounds__(256) void gather_queries(const float* __restrict__ q, const uint32_t* __restrict__ rows,
-                                                      uint32_t R, uint32_t D, float* __restrict__ out) {
-    for (uint32_t r = blockIdx.x; r < R; r += gridDim.x) {
-        const float* src = q + uint64_t(rows[r]) * D;
-        for (uint32_t d = threadIdx.x; d < D; d += 256) out[uint64_t(r) * D + d] = src[d];
     }
 }
 
@@ -183,15 +187,11 @@ constexpr uint32_t TQ = 16, TN = 128, WAVES = 4;
 }
 typedef float f32x4s __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(256) void ivf_small_kernel(DistArgs a) {
+// One wave's tile: queries qrow[qs + i] (i < qc) x row positions rs + r (r < rc).
+__device__ __forceinline__ void small_tile(const DistArgs& a, float (*xnorm)[ivfs::TN], int wave, uint32_t qs,
+                                           uint32_t qc, uint32_t rs, uint32_t rc) {
     using namespace ivfs;
-    __shared__ __attribute__((aligned(16))) float xnorm[WAVES][TN];
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
-    const uint32_t tile = blockIdx.x * WAVES + uint32_t(wave);
-    if (tile >= a.ntiles) return;  // whole wave; the waves never synchronise
-    const uint32_t qs = a.tiles[4 * tile], qc = a.tiles[4 * tile + 1];
-    const uint32_t rs = a.tiles[4 * tile + 2], rc = a.tiles[4 * tile + 3];
     const int j = lane & 15, g = lane >> 4;
     const uint32_t D = a.D;
     // this lane's query row (zeros past the tile's queries)
@@ -298,108 +298,179 @@ __global__ __launch_bounds__(256) void ivf_small_kernel(DistArgs a) {
     }
 }
 
-// Tile descriptors {qs, qc, rs, rc} of one list-major pass, grouped by tile shape.  A tile of
-// wq x wn waves covers 32*wq queries x 128*wn rows.  A list with nq probing queries and n
-// rows gets the shape with the least estimated time: tiles x waves x the measured cost of
-// one wave tile (32 x 128) in that shape on MI355X (shapes with more waves share their LDS
-// stages across more MFMA work and run more workgroups per CU, except 1 x 4, whose 87 KB of
-// LDS leaves one workgroup per CU).  The one- and two-wave shapes keep lists with few
-// queries or few rows from paying for a 4-wave tile.
-struct TilePlan {
-    static constexpr int NS = 5;
-    static constexpr int WQ[NS] = {4, 2, 2, 1, 1};
-    static constexpr int WN[NS] = {1, 2, 1, 1, 4};
-    static constexpr uint32_t COST[NS] = {100, 120, 135, 175, 195};  // per wave tile, relative
-    std::vector<uint32_t> t[NS];
-    std::vector<uint32_t> small;  // 16-query tiles (ivf_small_kernel)
-    // every group back to back, as uploaded by run_pass (kept with the plan, which outlives
-    // the asynchronous copy)
-    mutable std::vector<uint32_t> packed;
-    static int shape_for(uint32_t nq, uint32_t nrows) {
-        int best = 0;
-        uint64_t best_cost = ~0ull;
-        for (int i = 0; i < NS; ++i) {
-            const uint64_t cost = uint64_t((nq + 32 * WQ[i] - 1) / (32 * WQ[i])) *
-                                  ((nrows + 128 * WN[i] - 1) / (128 * WN[i])) * (WQ[i] * WN[i]) * COST[i];
-            if (cost < best_cost) {
-                best = i;
-                best_cost = cost;
-            }
+// A planned launch (a.plan): every wave loops over the plan's tiles on its own (the waves are
+// independent tiles, no barrier).
+__global__ __launch_bounds__(256) void ivf_small_kernel(DistArgs a) {
+    using namespace ivfs;
+    __shared__ __attribute__((aligned(16))) float xnorm[WAVES][TN];
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+    const uint32_t total = a.plan.pre[a.plan.C];
+    for (uint32_t t = blockIdx.x * WAVES + uint32_t(wave); t < total; t += gridDim.x * WAVES) {
+        uint32_t qs, qc, rs, rc;
+        plan_tile(a.plan, t, TQ, TN, qs, qc, rs, rc);
+        small_tile(a, xnorm, wave, qs, qc, rs, rc);
+    }
+}
+
+// Tile shapes of the list-major scan.  A tile of wq x wn waves covers 32*wq queries x 128*wn
+// rows.  A list with nq probing queries and n rows gets the shape with the least estimated
+// time: tiles x waves x the measured cost of one wave tile (32 x 128) in that shape on MI355X
+// (shapes with more waves share their LDS stages across more MFMA work and run more workgroups
+// per CU, except 1 x 4, whose 87 KB of LDS leaves one workgroup per CU).  The one- and two-wave
+// shapes keep lists with few queries or few rows from paying for a 4-wave tile.  Group
+// kSmallGroup is the 16-query tiles of ivf_small_kernel.
+constexpr int kShapes = 5;
+constexpr int kSmallGroup = kShapes;
+constexpr int kGroups = kShapes + 1;
+__host__ __device__ inline int shape_wq(int s) { return s == 0 ? 4 : (s <= 2 ? 2 : 1); }
+__host__ __device__ inline int shape_wn(int s) { return s == 1 ? 2 : (s == 4 ? 4 : 1); }
+__host__ __device__ inline uint32_t shape_cost(int s) {
+    return s == 0 ? 100u : s == 1 ? 120u : s == 2 ? 135u : s == 3 ? 175u : 195u;  // per wave tile, relative
+}
+__host__ __device__ inline int shape_for(uint32_t nq, uint32_t nrows) {
+    int best = 0;
+    uint64_t best_cost = ~0ull;
+    for (int i = 0; i < kShapes; ++i) {
+        const uint32_t wq = uint32_t(shape_wq(i)), wn = uint32_t(shape_wn(i));
+        const uint64_t cost = uint64_t((nq + 32 * wq - 1) / (32 * wq)) * ((nrows + 128 * wn - 1) / (128 * wn)) *
+                              (wq * wn) * shape_cost(i);
+        if (cost < best_cost) {
+            best = i;
+            best_cost = cost;
         }
-        return best;
     }
-    // rows of a list: positions off + j, j < nrows; small_list: the list takes 16-query tiles
-    void add(uint32_t lq_start, uint32_t nq, uint32_t off, uint32_t nrows, bool small_list = false) {
-        if (nq == 0 || nrows == 0) return;
-        if (small_list) {
-            for (uint32_t qb = 0; qb < nq; qb += ivfs::TQ)
-                for (uint32_t r = 0; r < nrows; r += ivfs::TN) {
-                    small.push_back(lq_start + qb);
-                    small.push_back(std::min(ivfs::TQ, nq - qb));
-                    small.push_back(off + r);
-                    small.push_back(std::min(ivfs::TN, nrows - r));
-                }
-            return;
-        }
-        const int sh = shape_for(nq, nrows);
-        const uint32_t TQ = dist_tile_queries(WQ[sh]), TN = dist_tile_rows(WN[sh]);
-        auto& v = t[sh];
-        for (uint32_t qb = 0; qb < nq; qb += TQ)
-            for (uint32_t r = 0; r < nrows; r += TN) {
-                v.push_back(lq_start + qb);
-                v.push_back(std::min(TQ, nq - qb));
-                v.push_back(off + r);
-                v.push_back(std::min(TN, nrows - r));
-            }
+    return best;
+}
+constexpr uint32_t kSmallListQueries = 16;
+__host__ __device__ inline void group_tile(int g, uint32_t& TQ, uint32_t& TN) {
+    if (g == kSmallGroup) {
+        TQ = ivfs::TQ;
+        TN = ivfs::TN;
+    } else {
+        TQ = 32u * uint32_t(shape_wq(g));
+        TN = 128u * uint32_t(shape_wn(g));
     }
-    size_t words() const {
-        size_t w = small.size();
-        for (const auto& v : t) w += v.size();
-        return w;
-    }
+}
+
+// ---- device plan of a list-major search ----------------------------------------------------
+// From the probes alone, on the device: every (query, list) pair once (a list probed twice by a
+// query is scanned once; sentinel / out-of-range probes are skipped, IVFListSearch.metal:
+// 249-251), the queries probing each list grouped by list (qlist, offsets qoff), and for each
+// pass (0: threshold sample, 1: full scan) and tile group the exclusive prefix over the lists of
+// their tile counts.  The scan kernels decode their tiles from these prefixes.
+struct DevPlan {
+    const uint32_t* probes = nullptr;  // [Q x np]
+    uint32_t Q = 0, np = 0, C = 0;
+    const uint32_t* roff = nullptr;    // list offsets [C + 1]
+    uint32_t small_ok = 0;
+    uint32_t* P = nullptr;      // [Q x np] probes with repeats / sentinels replaced by ~0
+    uint32_t* qcnt = nullptr;   // [C] queries per list
+    uint32_t* qoff = nullptr;   // [C + 1]
+    uint32_t* qfill = nullptr;  // [C] fill cursors
+    uint32_t* qlist = nullptr;  // [Q x np] (the first qoff[C] are used)
+    uint32_t* counts = nullptr; // [2][kGroups][C] tiles per list
+    uint32_t* pre = nullptr;    // [2][kGroups][C + 1]
 };
 
-// Runs one list-major filter pass; tiles hold "rs" as an index into the strided row space
-// (the kernel multiplies j by rstride; rs must already be the first position).
-va_status run_pass(va_context* ctx, const TilePlan& plan, uint32_t* dev_tiles, const float* q, uint32_t q_rows,
-                   const uint32_t* lq, const va_ivf* ivf, uint32_t rstride, const uint32_t* thr, uint32_t* cnt,
-                   uint32_t* ckey, uint32_t* cid, uint32_t cap) {
-    // One upload of every group's tile descriptors, then one launch per group.  The groups are
-    // independent (they meet only in the per-query atomics of the candidate lists), so the
-    // largest runs on the context's stream and the others on the auxiliary streams: the
-    // smaller launches leave most of the chip idle on their own, and the 16-query tiles stream
-    // their rows from HBM while the larger tiles are MFMA-bound.
-    constexpr int NG = TilePlan::NS + 1;  // group NS: the 16-query tiles
-    const std::vector<uint32_t>* groups[NG];
-    for (int sh = 0; sh < TilePlan::NS; ++sh) groups[sh] = &plan.t[sh];
-    groups[TilePlan::NS] = &plan.small;
-    std::vector<uint32_t>& all = plan.packed;
-    all.clear();
-    all.reserve(plan.words());
-    size_t goff[NG];
-    int ngroups = 0, biggest = -1;
-    for (int gi = 0; gi < NG; ++gi) {
-        goff[gi] = all.size();
-        all.insert(all.end(), groups[gi]->begin(), groups[gi]->end());
-        if (groups[gi]->empty()) continue;
-        ++ngroups;
-        if (biggest < 0 || groups[gi]->size() > groups[biggest]->size()) biggest = gi;
+__global__ __launch_bounds__(256) void plan_probes_kernel(DevPlan p) {
+    const uint32_t q = blockIdx.x;
+    const uint32_t* pr = p.probes + int64_t(q) * p.np;
+    for (uint32_t i = threadIdx.x; i < p.np; i += 256) {
+        const uint32_t l = pr[i];
+        bool ok = l < p.C;
+        for (uint32_t j = 0; ok && j < i; ++j) ok = pr[j] != l;
+        p.P[int64_t(q) * p.np + i] = ok ? l : 0xFFFFFFFFu;
+        if (ok) atomicAdd(p.qcnt + l, 1u);
     }
-    if (ngroups == 0) return VA_OK;
-    VA_CHECK_HIP(ctx, hipMemcpyAsync(dev_tiles, all.data(), all.size() * 4, hipMemcpyHostToDevice, ctx->stream));
-    if (ngroups > 1) VA_CHECK_STATUS(aux_fork(ctx));
+}
+
+// Exclusive prefix of in[0..n) into out[0..n] (out[n] = total), one workgroup of 1024 threads;
+// copy (may be null) receives out[0..n) as well.  Workgroup b scans array b of a batch.
+__global__ __launch_bounds__(1024) void plan_scan_kernel(const uint32_t* in, uint32_t n, uint32_t* out, uint32_t* copy,
+                                                        int64_t in_stride, int64_t out_stride) {
+    __shared__ uint32_t part[1024];
+    in += int64_t(blockIdx.x) * in_stride;
+    out += int64_t(blockIdx.x) * out_stride;
+    const uint32_t t = threadIdx.x, per = (n + 1023) / 1024;
+    const uint32_t b0 = min(n, t * per), b1 = min(n, b0 + per);
+    uint32_t s = 0;
+    for (uint32_t i = b0; i < b1; ++i) s += in[i];
+    part[t] = s;
+    __syncthreads();
+    for (uint32_t w = 1; w < 1024; w <<= 1) {  // inclusive Hillis-Steele scan of the partial sums
+        const uint32_t v = t >= w ? part[t - w] : 0u;
+        __syncthreads();
+        part[t] += v;
+        __syncthreads();
+    }
+    uint32_t run = part[t] - s;
+    for (uint32_t i = b0; i < b1; ++i) {
+        out[i] = run;
+        if (copy) copy[i] = run;
+        run += in[i];
+    }
+    if (t == 1023) out[n] = part[1023];
+}
+
+__global__ __launch_bounds__(256) void plan_fill_kernel(DevPlan p) {
+    const uint64_t total = uint64_t(p.Q) * p.np;
+    for (uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x; i < total; i += uint64_t(gridDim.x) * 256) {
+        const uint32_t l = p.P[i];
+        if (l == 0xFFFFFFFFu) continue;
+        const uint32_t pos = atomicAdd(p.qfill + l, 1u);
+        p.qlist[pos] = uint32_t(i / p.np);
+    }
+}
+
+__global__ __launch_bounds__(256) void plan_counts_kernel(DevPlan p) {
+    for (uint32_t l = blockIdx.x * 256 + threadIdx.x; l < p.C; l += gridDim.x * 256) {
+        const uint32_t nq = p.qcnt[l], n = p.roff[l + 1] - p.roff[l];
+        const int g = (p.small_ok && nq <= kSmallListQueries) ? kSmallGroup : shape_for(nq, n);
+        uint32_t TQ, TN;
+        group_tile(g, TQ, TN);
+        for (int pass = 0; pass < 2; ++pass) {
+            const uint32_t rows = pass == 0 ? ivf_sample_rows(n) : n;
+            const uint32_t tiles = (nq == 0 || rows == 0) ? 0u : ((nq + TQ - 1) / TQ) * ((rows + TN - 1) / TN);
+            for (int gi = 0; gi < kGroups; ++gi)
+                p.counts[(int64_t(pass) * kGroups + gi) * p.C + l] = gi == g ? tiles : 0u;
+        }
+    }
+}
+
+// Enqueues the device plan (probes -> lists -> tile prefixes).
+va_status plan_on_device(va_context* ctx, const DevPlan& p) {
+    VA_CHECK_STATUS(fill_u32(ctx, p.qcnt, p.C, 0));
+    plan_probes_kernel<<<dim3(p.Q), dim3(256), 0, ctx->stream>>>(p);
+    VA_CHECK_LAUNCH(ctx);
+    plan_scan_kernel<<<dim3(1), dim3(1024), 0, ctx->stream>>>(p.qcnt, p.C, p.qoff, p.qfill, 0, 0);
+    VA_CHECK_LAUNCH(ctx);
+    const uint64_t pairs = uint64_t(p.Q) * p.np;
+    plan_fill_kernel<<<dim3(uint32_t(std::min<uint64_t>(4096, (pairs + 255) / 256))), dim3(256), 0, ctx->stream>>>(p);
+    VA_CHECK_LAUNCH(ctx);
+    plan_counts_kernel<<<dim3(std::min<uint32_t>(1024, (p.C + 255) / 256)), dim3(256), 0, ctx->stream>>>(p);
+    VA_CHECK_LAUNCH(ctx);
+    plan_scan_kernel<<<dim3(2 * kGroups), dim3(1024), 0, ctx->stream>>>(p.counts, p.C, p.pre, nullptr, p.C,
+                                                                          int64_t(p.C) + 1);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
+// Runs one list-major filter pass over the device plan: one persistent launch per tile group
+// (each exits at once when its group has no tile).  The groups are independent (they meet only
+// in the per-query atomics of the candidate lists), so the 32-query groups run on the context's
+// stream and the others on the auxiliary streams: the smaller launches leave most of the chip
+// idle on their own, and the 16-query tiles stream their rows from HBM while the larger tiles
+// are MFMA-bound.
+va_status run_planned_pass(va_context* ctx, const DevPlan& dp, int pass, const float* q, const va_ivf* ivf,
+                           const uint32_t* thr, uint32_t* cnt, uint32_t* ckey, uint32_t* cid, uint32_t cap) {
+    VA_CHECK_STATUS(aux_fork(ctx));
     hipStream_t const main_stream = ctx->stream;
-    int next_aux = 0;
     va_status st = VA_OK;
-    for (int gi = 0; gi < NG && st == VA_OK; ++gi) {
-        const auto& v = *groups[gi];
-        if (v.empty()) continue;
-        hipStream_t s = main_stream;
-        if (gi != biggest) s = ctx->aux[next_aux++ % va_context::kAux];
+    for (int g = 0; g < kGroups && st == VA_OK; ++g) {
         DistArgs a;
         a.q = q;
-        a.qrow = lq;
-        a.q_rows = q_rows;
+        a.qrow = dp.qlist;
+        a.q_rows = dp.Q;
         a.ldq = ivf->D;
         a.x = ivf->list_vectors;
         a.ldx = ivf->D;
@@ -411,27 +482,146 @@ va_status run_pass(va_context* ctx, const TilePlan& plan, uint32_t* dev_tiles, c
         a.cand_key = ckey;
         a.cand_id = cid;
         a.cap = cap;
-        a.tiles = dev_tiles + goff[gi];
-        a.ntiles = uint32_t(v.size() / 4);
-        a.rstride = rstride;
         a.ids = ivf->ids;
-        if (gi == TilePlan::NS) {
-            const uint32_t blocks = (a.ntiles + ivfs::WAVES - 1) / ivfs::WAVES;
-            ivf_small_kernel<<<dim3(blocks), dim3(64 * ivfs::WAVES), 0, s>>>(a);
+        a.plan.pre = dp.pre + (int64_t(pass) * kGroups + g) * (int64_t(dp.C) + 1);
+        a.plan.qoff = dp.qoff;
+        a.plan.roff = dp.roff;
+        a.plan.C = dp.C;
+        a.plan.sample = pass == 0 ? 1u : 0u;
+        // shapes 0 (4x1) and 1 (2x2) carry most of the work: the context's stream; the rest
+        // spread over the auxiliary streams
+        const hipStream_t s = g <= 1 ? main_stream : ctx->aux[(g - 2) % va_context::kAux];
+        if (g == kSmallGroup) {
+            a.plan.grid = uint32_t(ctx->num_cus) * 4;
+            ivf_small_kernel<<<dim3(a.plan.grid), dim3(64 * ivfs::WAVES), 0, s>>>(a);
             if (hipGetLastError() != hipSuccess) st = fail(ctx, VA_ERR_HIP, "ivf_small_kernel launch failed");
         } else {
-            a.wq = TilePlan::WQ[gi];
-            a.wn = TilePlan::WN[gi];
+            a.wq = shape_wq(g);
+            a.wn = shape_wn(g);
+            // 4x1 and 2x2 run up to four workgroups per CU, the others two
+            a.plan.grid = uint32_t(ctx->num_cus) * (g <= 2 ? 4u : 2u);
             ctx->stream = s;  // launch_dist enqueues on the context's stream
             st = launch_dist(ctx, a);
             ctx->stream = main_stream;
         }
     }
-    if (ngroups > 1) {
-        const va_status j = aux_join(ctx);
-        if (st == VA_OK) st = j;
+    const va_status j = aux_join(ctx);
+    return st != VA_OK ? st : j;
+}
+
+// ---- device-side overflow fallback of the list scan -----------------------------------------
+// The keys of ivf_small_kernel for one query (supplied by the lanes of column 0) against 32 rows
+// xr[b] = row 16b + (lane % 16), b < 2 (nullptr: zeros): v_mfma_f32_16x16x4_f32 over 16-value
+// chunks (lane group g = lane / 16 holds values 16c + 4g .. 16c + 4g + 3, MFMA e takes value e
+// of each group), ceil(D / 32) * 2 chunks, squared norms as per-group fmaf chains combined by
+// xor-16 then xor-32 shuffles, d = qq + xx - 2 dot clamped at 0.  Lane (j, g) gets rows
+// 16b + 4g + v in keys[4b + v].  Needs D % 4 == 0 and 16-byte aligned rows.
+__device__ inline void small_keys32(const float* qp, const float* xr0, const float* xr1, uint32_t D, int lane,
+                                    uint32_t* keys) {
+    const int g = lane >> 4;
+    const float* xr[2] = {xr0, xr1};
+    f32x4s acc[2] = {f32x4s{0.f, 0.f, 0.f, 0.f}, f32x4s{0.f, 0.f, 0.f, 0.f}};
+    float xs[2] = {0.f, 0.f}, qsum = 0.f;
+    const uint32_t nch = (D + 31) / 32 * 2;
+    for (uint32_t c = 0; c < nch; ++c) {
+        const uint32_t k = 16 * c + 4 * uint32_t(g);
+        const bool kin = k < D;
+        const f32x4s zero = {0.f, 0.f, 0.f, 0.f};
+        const f32x4s qv = (qp && kin) ? *reinterpret_cast<const f32x4s*>(qp + k) : zero;
+        f32x4s rv[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) rv[b] = (xr[b] && kin) ? *reinterpret_cast<const f32x4s*>(xr[b] + k) : zero;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            qsum = fmaf(qv[e], qv[e], qsum);
+#pragma unroll
+            for (int b = 0; b < 2; ++b) xs[b] = fmaf(rv[b][e], rv[b][e], xs[b]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(rv[b][e], qv[e], acc[b], 0, 0, 0);
     }
-    return st;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        xs[b] += __shfl_xor(xs[b], 16);
+        xs[b] += __shfl_xor(xs[b], 32);
+    }
+    qsum += __shfl_xor(qsum, 16);
+    qsum += __shfl_xor(qsum, 32);
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float xx = __shfl(xs[b], 4 * g + v);  // the norm of row 16b + 4g + v
+            float d = qsum + xx - 2.0f * acc[b][v];
+            d = (d < 0.0f) ? 0.0f : d;
+            keys[4 * b + v] = key_of_float(d);
+        }
+}
+
+struct FbIvf {
+    const float* q;
+    const float* x;         // list vectors, CSR order
+    const uint32_t* ids;    // row id of every CSR position
+    const uint32_t* roff;   // [C + 1]
+    const uint32_t* P;      // deduplicated probes [Q x np] (~0: skipped)
+    const uint32_t* qcnt;   // queries per list (which kernel scanned the list)
+    uint32_t np, D, tmax, small_ok;
+};
+
+// Work items (overflowed query slot, probe, 32-row tile of the probed list), one per wave: the
+// keys with the arithmetic of the kernel that scanned the list in the full pass, then the
+// fallback pass's action for each.
+template <bool VEC>
+__global__ __launch_bounds__(256) void fb_ivf_pass_kernel(FbIvf v, FbArgs a, int pass) {
+    const uint32_t n = fb_count(a);
+    if (n == 0) return;  // nothing overflowed: every workgroup leaves at once
+    const int lane = threadIdx.x & 63;
+    const uint64_t items = uint64_t(n) * v.np * v.tmax;
+    const uint32_t nw = gridDim.x * 4;
+    for (uint64_t it = blockIdx.x * 4 + (threadIdx.x >> 6); it < items; it += nw) {
+        const uint32_t t = uint32_t(it % v.tmax);
+        const uint64_t sp = it / v.tmax;
+        const uint32_t p = uint32_t(sp % v.np), s = uint32_t(sp / v.np);
+        const uint32_t qi = a.rows[s];
+        const uint32_t l = v.P[int64_t(qi) * v.np + p];
+        if (l == 0xFFFFFFFFu) continue;
+        const uint32_t len = v.roff[l + 1] - v.roff[l];
+        if (t * 32 >= len) continue;  // (uniform)
+        FbSlot sl;
+        if (!fb_slot_begin(a, pass, s, sl)) continue;
+        const uint32_t base = v.roff[l] + t * 32, rc = min(32u, len - t * 32);
+        const float* qrow = v.q + int64_t(qi) * v.D;
+        if (v.small_ok && v.qcnt[l] <= kSmallListQueries) {
+            const int j = lane & 15, g = lane >> 4;
+            uint32_t keys[8];
+            small_keys32(j == 0 ? qrow : nullptr, uint32_t(j) < rc ? v.x + int64_t(base + j) * v.D : nullptr,
+                         uint32_t(16 + j) < rc ? v.x + int64_t(base + 16 + j) * v.D : nullptr, v.D, lane, keys);
+            if (j == 0) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t m = uint32_t(16 * (i >> 2) + 4 * g + (i & 3));
+                    if (m < rc) fb_consume(a, pass, sl, keys[i], v.ids[base + m]);
+                }
+            }
+        } else {
+            const int l32 = lane & 31, hh = lane >> 5;
+            uint32_t keys[16];
+            f32_block_keys<VEC>(l32 == 0 ? qrow : nullptr,
+                                uint32_t(l32) < rc ? v.x + int64_t(base + l32) * v.D : nullptr, v.D, int(OP_L2SQ),
+                                lane, keys);
+            if (l32 == 0) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t m = uint32_t(8 * (i >> 2) + 4 * hh + (i & 3));
+                    if (m < rc) fb_consume(a, pass, sl, keys[i], v.ids[base + m]);
+                }
+            }
+        }
+        sl.run.flush();
+    }
+    fb_pass_done(a, pass, n);
 }
 
 // A list takes 16-query tiles when few queries probe it (decided once per search from the
@@ -445,8 +635,6 @@ bool small_tiles_ok(const va_ivf* ivf, const float* q) {
            (reinterpret_cast<uintptr_t>(ivf->list_vectors) & 15) == 0 &&
            uint64_t(ivfs::TN) * ivf->D * 4 + 16 <= 0x7FFFFFF0ull;
 }
-constexpr uint32_t kSmallListQueries = 16;
-
 }  // namespace
 }  // namespace va
 
@@ -501,6 +689,8 @@ va_status va_ivf_build(va_context* ctx, const float* centroids, uint32_t num_cen
     if (hipMemcpy(ivf->h_offsets.data(), ivf->offsets, uint64_t(num_centroids + 1) * 4, hipMemcpyDeviceToHost) !=
         hipSuccess)
         return cleanup(va::fail(ctx, VA_ERR_HIP, "va_ivf_build: offsets read-back failed"));
+    ivf->refresh_bounds();
+    ivf->id_end = num_vectors;
     va::gather_rows<<<dim3(std::min<uint32_t>(num_vectors, 65536)), dim3(256), 0, ctx->stream>>>(
         x, ivf->ids, num_vectors, dim, ivf->list_vectors);
     if (hipGetLastError() != hipSuccess || hipStreamSynchronize(ctx->stream) != hipSuccess)
@@ -565,6 +755,8 @@ va_status va_ivf_add(va_context* ctx, va_ivf* ivf, const float* x, uint32_t num_
     ivf->ids = ids;
     ivf->offsets = offs;
     ivf->h_offsets = std::move(h);
+    ivf->refresh_bounds();
+    ivf->id_end = std::max<uint64_t>(ivf->id_end, uint64_t(first_id) + n);
     ivf->N = Nn;
     return VA_OK;
 }
@@ -620,78 +812,59 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
     VA_REQUIRE(ctx, k > 0 && k <= VA_MAX_K, "k must be in [1, %u], got %u", VA_MAX_K, k);
     VA_REQUIRE(ctx, nprobe >= 1, "nprobe must be at least 1, got %u", nprobe);
     va::DeviceGuard g(ctx->device);
-    const uint32_t Q = num_queries, C = ivf->C;
-    const auto& off = ivf->h_offsets;
+    const uint32_t Q = num_queries, C = ivf->C, np = nprobe;
 
-    // ---- host plan: the queries probing every list, per-query candidate totals ------------------
-    std::vector<uint32_t> P(uint64_t(Q) * nprobe);
-    VA_CHECK_HIP(ctx, hipMemcpyAsync(P.data(), probes, P.size() * 4, hipMemcpyDeviceToHost, ctx->stream));
-    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    std::vector<uint32_t> lq_off(C + 1, 0), seen(C, 0xFFFFFFFFu);
-    std::vector<uint64_t> total(Q, 0), sampled(Q, 0);
-    for (uint32_t q = 0; q < Q; ++q)
-        for (uint32_t p = 0; p < nprobe; ++p) {
-            uint32_t& l = P[uint64_t(q) * nprobe + p];
-            // sentinel / out-of-range probes are skipped (IVFListSearch.metal:249-251); a list
-            // probed twice by one query is scanned once
-            if (l >= C || seen[l] == q) {
-                l = 0xFFFFFFFFu;
-                continue;
-            }
-            seen[l] = q;
-            lq_off[l + 1]++;
-            const uint32_t n = off[l + 1] - off[l];
-            total[q] += n;
-            sampled[q] += va::sample_rows(n);
-        }
-    for (uint32_t l = 0; l < C; ++l) lq_off[l + 1] += lq_off[l];
-    std::vector<uint32_t> lq(lq_off[C]), fillp(lq_off.begin(), lq_off.end() - 1);
-    for (uint32_t q = 0; q < Q; ++q)
-        for (uint32_t p = 0; p < nprobe; ++p) {
-            const uint32_t l = P[uint64_t(q) * nprobe + p];
-            if (l < C) lq[fillp[l]++] = q;
-        }
-    va::TilePlan sample_plan, main_plan;
-    const bool small_ok = va::small_tiles_ok(ivf, queries);
-    auto small_list = [&](uint32_t l) { return small_ok && lq_off[l + 1] - lq_off[l] <= va::kSmallListQueries; };
-    for (uint32_t l = 0; l < C; ++l) {
-        const uint32_t nq = lq_off[l + 1] - lq_off[l];
-        const uint32_t n = off[l + 1] - off[l];
-        main_plan.add(lq_off[l], nq, off[l], n, small_list(l));
-    }
-    for (uint32_t l = 0; l < C; ++l)
-        sample_plan.add(lq_off[l], lq_off[l + 1] - lq_off[l], off[l], va::sample_rows(off[l + 1] - off[l]),
-                        small_list(l));
-    const uint64_t cap_s = std::max<uint64_t>(1, *std::max_element(sampled.begin(), sampled.end()));
-    const uint64_t max_total = std::max<uint64_t>(1, *std::max_element(total.begin(), total.end()));
-    // every list is sampled at rate >= 1/kSampleRate: a query's candidates stay near
-    // kSampleRate x k; queries that still outgrow the list take the exact rescan below
+    // ---- sizes from the list lengths alone (nothing is read back) --------------------------------
+    // A query's lists are at most its np longest: its threshold sample never outgrows cap_s (the
+    // sample pass cannot overflow); the full pass keeps about 64 x k candidates per query, and
+    // queries that outgrow cap are finished by the device fallback.
+    const uint32_t npc = std::min(np, C);
+    const uint64_t cap_s = std::max<uint64_t>(1, ivf->top_sample[npc]);
     uint64_t cap = ctx->opt_candidate_cap ? ctx->opt_candidate_cap
-                                          : std::max<uint64_t>(3ull * k, uint64_t(k) + 32) * va::kSampleRate + 1024;
-    cap = std::min(cap, max_total);
+                                          : std::max<uint64_t>(3ull * k, uint64_t(k) + 32) * va::kIvfSampleRate + 1024;
+    cap = std::max<uint64_t>(1, std::min<uint64_t>(cap, ivf->top_rows[npc]));
     const uint64_t cand = std::max(cap_s, cap);
+    const uint64_t pairs = uint64_t(Q) * np;
+    // the fallback's tie-id histogram covers the ids of the index
+    const uint32_t id_span = uint32_t(std::min<uint64_t>(ivf->id_end, 0xFFFFFFFFull));
 
     Scratch s(ctx);
-    const size_t tile_words = std::max(sample_plan.words(), main_plan.words());
-    const size_t need = Scratch::round(uint64_t(Q) * 4) * 3 + Scratch::round(256) + Scratch::round(lq.size() * 4 + 4) +
-                        Scratch::round(tile_words * 4 + 4) + Scratch::round(uint64_t(Q) * cand * 4) * 2;
+    const size_t need = Scratch::round(uint64_t(Q) * 4) * 3 + Scratch::round(256) + Scratch::round(pairs * 4) * 2 +
+                        Scratch::round(uint64_t(C) * 4) * 2 + Scratch::round((uint64_t(C) + 1) * 4) +
+                        Scratch::round(uint64_t(2 * va::kGroups) * C * 4) +
+                        Scratch::round(uint64_t(2 * va::kGroups) * (uint64_t(C) + 1) * 4) +
+                        Scratch::round(uint64_t(Q) * cand * 4) * 2 + va::fb_bytes(Q, id_span, k, ivf->N);
     VA_CHECK_STATUS(s.reserve(need));
     uint32_t* thr = s.carve<uint32_t>(Q);
     uint32_t* cnt = s.carve<uint32_t>(Q);
     uint32_t* ovf_rows = s.carve<uint32_t>(Q);
     uint32_t* ovf_cnt = s.carve<uint32_t>(64);
-    uint32_t* d_lq = s.carve<uint32_t>(lq.size() + 1);
-    uint32_t* d_tiles = s.carve<uint32_t>(tile_words + 1);
+    va::DevPlan dp;
+    dp.probes = probes;
+    dp.Q = Q;
+    dp.np = np;
+    dp.C = C;
+    dp.roff = ivf->offsets;
+    dp.small_ok = va::small_tiles_ok(ivf, queries) ? 1u : 0u;
+    dp.P = s.carve<uint32_t>(pairs);
+    dp.qlist = s.carve<uint32_t>(pairs);
+    dp.qcnt = s.carve<uint32_t>(C);
+    dp.qfill = s.carve<uint32_t>(C);
+    dp.qoff = s.carve<uint32_t>(uint64_t(C) + 1);
+    dp.counts = s.carve<uint32_t>(uint64_t(2 * va::kGroups) * C);
+    dp.pre = s.carve<uint32_t>(uint64_t(2 * va::kGroups) * (uint64_t(C) + 1));
     uint32_t* ckey = s.carve<uint32_t>(uint64_t(Q) * cand);
     uint32_t* cid = s.carve<uint32_t>(uint64_t(Q) * cand);
-    if (!lq.empty())
-        VA_CHECK_HIP(ctx, hipMemcpyAsync(d_lq, lq.data(), lq.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+    va::FbArgs fb = va::fb_carve(s, Q, id_span, k, ivf->N);
+    fb.n_rows = ovf_cnt;
+    fb.rows = ovf_rows;
 
+    // ---- 0. plan: the queries of every probed list, tile prefixes per group and pass ------------
+    VA_CHECK_STATUS(va::plan_on_device(ctx, dp));
     // ---- 1. sample pass: every sampled candidate, then tau = k-th smallest ----------------------
     VA_CHECK_STATUS(va::fill_u32(ctx, thr, Q, 0xFFFFFFFFu));
     VA_CHECK_STATUS(va::fill_u32(ctx, cnt, Q, 0));
-    VA_CHECK_STATUS(va::run_pass(ctx, sample_plan, d_tiles, queries, Q, d_lq, ivf, 1, thr, cnt, ckey, cid,
-                                 uint32_t(cap_s)));
+    VA_CHECK_STATUS(va::run_planned_pass(ctx, dp, 0, queries, ivf, thr, cnt, ckey, cid, uint32_t(cap_s)));
     {
         va::SelectArgs a;
         a.keys = ckey;
@@ -707,85 +880,46 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
     // ---- 2. full pass with the thresholds, 3. exact selection -----------------------------------
     VA_CHECK_STATUS(va::fill_u32(ctx, cnt, Q, 0));
     VA_CHECK_STATUS(va::fill_u32(ctx, ovf_cnt, 1, 0));
-    VA_CHECK_STATUS(va::run_pass(ctx, main_plan, d_tiles, queries, Q, d_lq, ivf, 1, thr, cnt, ckey, cid, uint32_t(cap)));
+    VA_CHECK_STATUS(va::run_planned_pass(ctx, dp, 1, queries, ivf, thr, cnt, ckey, cid, uint32_t(cap)));
+    va::SelectArgs base;
+    base.k = k;
+    base.out_idx = out_idx;
+    base.out_f = out_dist;
     {
-        va::SelectArgs a;
+        va::SelectArgs a = base;
         a.keys = ckey;
         a.ids = cid;
         a.counts = cnt;
         a.ld = int64_t(cap);
         a.n = uint32_t(cap);
         a.rows = Q;
-        a.k = k;
-        a.out_idx = out_idx;
-        a.out_f = out_dist;
         a.overflow_count = ovf_cnt;
         a.overflow_rows = ovf_rows;
         VA_CHECK_STATUS(va::launch_select(ctx, a));
     }
-    VA_CHECK_HIP(ctx, hipMemcpyAsync(ctx->host_word, ovf_cnt, 4, hipMemcpyDeviceToHost, ctx->stream));
-    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    const uint32_t n_ovf = ctx->host_word[0];
-    if (n_ovf == 0) return VA_OK;
-
-    // ---- 4. overflowed queries: rescan with room for all of their candidates ---------------------
-    std::vector<uint32_t> rows(n_ovf), h_thr(Q);
-    VA_CHECK_HIP(ctx, hipMemcpyAsync(rows.data(), ovf_rows, uint64_t(n_ovf) * 4, hipMemcpyDeviceToHost, ctx->stream));
-    VA_CHECK_HIP(ctx, hipMemcpyAsync(h_thr.data(), thr, uint64_t(Q) * 4, hipMemcpyDeviceToHost, ctx->stream));
-    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    std::sort(rows.begin(), rows.end());
-    std::vector<uint32_t> compact(Q, 0xFFFFFFFFu), c_thr(n_ovf);
-    uint64_t cap2 = 1;
-    for (uint32_t i = 0; i < n_ovf; ++i) {
-        compact[rows[i]] = i;
-        c_thr[i] = h_thr[rows[i]];
-        cap2 = std::max<uint64_t>(cap2, total[rows[i]]);
+    // ---- 4. queries whose candidates outgrew cap: exact top-k on the device ----------------------
+    VA_CHECK_STATUS(va::fb_init(ctx, fb));
+    va::FbIvf v;
+    v.q = queries;
+    v.x = ivf->list_vectors;
+    v.ids = ivf->ids;
+    v.roff = ivf->offsets;
+    v.P = dp.P;
+    v.qcnt = dp.qcnt;
+    v.np = np;
+    v.D = ivf->D;
+    v.tmax = std::max<uint32_t>(1, (ivf->max_len + 31) / 32);
+    v.small_ok = dp.small_ok;
+    const bool vec = ivf->D % 4 == 0 && (reinterpret_cast<uintptr_t>(queries) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(ivf->list_vectors) & 15) == 0;
+    for (int pass = 0; pass < va::kFbPasses; ++pass) {
+        if (vec)
+            va::fb_ivf_pass_kernel<true><<<dim3(va::kFbGrid), dim3(256), 0, ctx->stream>>>(v, fb, pass);
+        else
+            va::fb_ivf_pass_kernel<false><<<dim3(va::kFbGrid), dim3(256), 0, ctx->stream>>>(v, fb, pass);
+        VA_CHECK_LAUNCH(ctx);
     }
-    std::vector<uint32_t> lq2_off(C + 1, 0), lq2;
-    for (uint32_t l = 0; l < C; ++l) {
-        for (uint32_t e = lq_off[l]; e < lq_off[l + 1]; ++e)
-            if (compact[lq[e]] != 0xFFFFFFFFu) lq2.push_back(compact[lq[e]]);
-        lq2_off[l + 1] = uint32_t(lq2.size());
-    }
-    va::TilePlan plan2;
-    for (uint32_t l = 0; l < C; ++l)
-        plan2.add(lq2_off[l], lq2_off[l + 1] - lq2_off[l], off[l], off[l + 1] - off[l], small_list(l));
-    Scratch f(ctx);
-    const size_t need2 = Scratch::round(uint64_t(n_ovf) * ivf->D * 4) + Scratch::round(uint64_t(n_ovf) * 4) * 3 +
-                         Scratch::round(lq2.size() * 4 + 4) + Scratch::round(plan2.words() * 4 + 4) +
-                         Scratch::round(uint64_t(n_ovf) * cap2 * 4) * 2;
-    VA_CHECK_STATUS(f.reserve(need2));
-    float* cq = f.carve<float>(uint64_t(n_ovf) * ivf->D);
-    uint32_t* d_rows = f.carve<uint32_t>(n_ovf);
-    uint32_t* d_thr = f.carve<uint32_t>(n_ovf);
-    uint32_t* d_cnt = f.carve<uint32_t>(n_ovf);
-    uint32_t* d_lq2 = f.carve<uint32_t>(lq2.size() + 1);
-    uint32_t* d_t2 = f.carve<uint32_t>(plan2.words() + 1);
-    uint32_t* k2 = f.carve<uint32_t>(uint64_t(n_ovf) * cap2);
-    uint32_t* i2 = f.carve<uint32_t>(uint64_t(n_ovf) * cap2);
-    VA_CHECK_HIP(ctx, hipMemcpyAsync(d_rows, rows.data(), uint64_t(n_ovf) * 4, hipMemcpyHostToDevice, ctx->stream));
-    VA_CHECK_HIP(ctx, hipMemcpyAsync(d_thr, c_thr.data(), uint64_t(n_ovf) * 4, hipMemcpyHostToDevice, ctx->stream));
-    if (!lq2.empty())
-        VA_CHECK_HIP(ctx, hipMemcpyAsync(d_lq2, lq2.data(), lq2.size() * 4, hipMemcpyHostToDevice, ctx->stream));
-    va::gather_queries<<<dim3(std::min<uint32_t>(n_ovf, 4096)), dim3(256), 0, ctx->stream>>>(queries, d_rows, n_ovf,
-                                                                                            ivf->D, cq);
-    VA_CHECK_LAUNCH(ctx);
-    VA_CHECK_STATUS(va::fill_u32(ctx, d_cnt, n_ovf, 0));
-    VA_CHECK_STATUS(va::run_pass(ctx, plan2, d_t2, cq, n_ovf, d_lq2, ivf, 1, d_thr, d_cnt, k2, i2, uint32_t(cap2)));
-    va::SelectArgs a;
-    a.keys = k2;
-    a.ids = i2;
-    a.counts = d_cnt;
-    a.ld = int64_t(cap2);
-    a.n = uint32_t(cap2);
-    a.rows = n_ovf;
-    a.k = k;
-    a.row_map = d_rows;
-    a.out_idx = out_idx;
-    a.out_f = out_dist;
-    VA_CHECK_STATUS(va::launch_select(ctx, a));
-    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));  // host vectors above must outlive the copies
-    return VA_OK;
+    return va::fb_select(ctx, fb, base, 32);
 }
 
 va_status va_ivf_search(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
