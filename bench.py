@@ -61,13 +61,15 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-TRAFFIC_SCREEN = "profiles/hbm_traffic__screen_filter__configs1_cosine_top100.txt"
-TRAFFIC_FP32 = "profiles/hbm_traffic__dist_gemm_filter__configs1_cosine_top100.txt"
 COUNTERS_SCREEN16 = "profiles/counters__screen16_filter__configs1_cosine_top100.txt"
 COUNTERS_SCREEN = "profiles/counters__screen_filter__configs1_cosine_top100.txt"
 COUNTERS_FP32 = "profiles/counters__dist_gemm_filter__configs1_cosine_top100.txt"
 COUNTERS_I8 = "profiles/counters__i8_resq_filter__configs2_int8_top10.txt"
 COUNTERS_HAMMING = "profiles/counters__hamming_mfma_filter__configs3_binary_top100.txt"
+COUNTERS_IVF = {"2x2 tiles": "profiles/counters__ivf_list_scan_2x2__configs4_ivfflat_top10.txt",
+                "4x1 tiles": "profiles/counters__ivf_list_scan_4x1__configs4_ivfflat_top10.txt",
+                "16-query tiles": "profiles/counters__ivf_small_tiles__configs4_ivfflat_top10.txt"}
+COUNTERS_PQ = "profiles/counters__pq_adc_filter__10Mx16codes_K256_Q1024.txt"
 
 
 def counters(rel: str) -> dict:
@@ -87,16 +89,11 @@ def counters(rel: str) -> dict:
     return out
 
 
-def measured_traffic(rel: str = TRAFFIC_SCREEN) -> float | None:
-    """HBM bytes per launch of a scan kernel, from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE passes (calibrated against a plain copy)."""
-    f = ROOT / rel
-    if not f.exists():
-        return None
-    for line in f.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch:"):
-            return float(line.split(":", 1)[1])
-    return None
+def counted(rel: str) -> dict:
+    """The counted MFMA-busy and HBM figures of a committed counter summary, for a roofline."""
+    c = counters(rel)
+    return {"mfma_busy": c.get("mfma_busy_pct"), "hbm_gbs": c.get("hbm_gbs"),
+            "traffic": c.get("traffic_bytes_per_launch"), "counters_source": rel}
 
 
 def timed(ctx, fn, steps: int, warmup: int, scan_timings: bool = True):
@@ -188,7 +185,7 @@ def run_c2(ctx, a, cpu: bool, extra_l2: bool):
             "hbm_gbs": cnt.get("hbm_gbs"),
             "counters_source": COUNTERS_SCREEN16 if screened else COUNTERS_FP32,
             "kernel": ("screen16_kernel (fp16 MFMA screening scan over the index's fp16 shadow; exact fp32 "
-                       "rerank of a proven band)" if screened else "dist_gemm_kernel<4, 1, true, 2, true> (fp32 scan)"),
+                       "rerank of a proven band)" if screened else "dist_gemm_kernel<4, 1, true, 2, true, false> (fp32 scan)"),
             "algorithmic": f"2*Q*N*D = {flops:.4g} FLOP per launch",
             "fp32_mfma_equivalent_frac": tflops / PEAK["fp32_mfma_tflops"],
             "power_limited_ceiling": ("a register-only loop of the same fp16 MFMA on random operands runs at "
@@ -214,7 +211,7 @@ def run_c2(ctx, a, cpu: bool, extra_l2: bool):
         "ms_per_step": ms32, "qps": Q / (ms32 * 1e-3), "scan_ms": s32,
         "scan_tflops": flops / (s32 * 1e-3) / 1e12,
         "mfma_frac": flops / (s32 * 1e-3) / 1e12 / PEAK["fp32_mfma_tflops"],
-        "kernel": "dist_gemm_kernel<4, 1, true, 2, true>",
+        "kernel": "dist_gemm_kernel<4, 1, true, 2, true, false>",
         "traffic": c32.get("traffic_bytes_per_launch"), "mfma_busy": c32.get("mfma_busy_pct"),
         "counters_source": COUNTERS_FP32,
     }
@@ -372,7 +369,7 @@ def run_c3(ctx, a, cpu: bool):
         "quantize_hbm_gbs": (N * D * 4 * 2 + N * D) / (qms * 1e-3) / 1e9,
         "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK["int8_mfma_tops"], "unit": "TOP/s",
                      "frac": tops / PEAK["int8_mfma_tops"], "kernel": "i8_resq_kernel<512>",
-                     "algorithmic": f"2*Q*N*D = {ops:.4g} int ops per launch"},
+                     "algorithmic": f"2*Q*N*D = {ops:.4g} int ops per launch", **counted(COUNTERS_I8)},
     }
     log(f"configs[2] int8 top-10: {ms:.3f} ms/step = {res['qps']:.0f} QPS; scan {ph['scan_ms']:.3f} ms = "
         f"{tops:.0f} TOP/s; quantize 10M x 512 in {qms:.2f} ms")
@@ -434,7 +431,7 @@ def run_c4(ctx, a, cpu: bool):
                              "peak). The database is read from HBM once (hbm_frac).",
                      "algorithmic": f"2 ops per bit per (query, row) pair: {flops:.4g} per launch",
                      "valu_equivalent_tops": valu_equiv,
-                     "hbm_gbs_database_once": gbs, "hbm_frac": gbs / PEAK["hbm_gbs"]},
+                     "hbm_gbs_database_once": gbs, "hbm_frac": gbs / PEAK["hbm_gbs"], **counted(COUNTERS_HAMMING)},
     }
     log(f"configs[3] binary top-100: {ms:.3f} ms/step = {res['qps']:.0f} QPS; scan {ph['scan_ms']:.3f} ms = "
         f"{tflops:.0f} TFLOP/s fp4 MFMA ({100 * tflops / PEAK['fp4_mfma_tflops']:.1f}%), {gbs:.0f} GB/s")
@@ -499,7 +496,8 @@ def run_c5(ctx, a, cpu: bool):
         "candidates_scanned": cand, "largest_list": int(sizes.max()),
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK["fp32_mfma_tflops"], "unit": "TFLOP/s",
                      "frac": tflops / PEAK["fp32_mfma_tflops"], "kernel": "whole search (probe + sample + scan + select)",
-                     "algorithmic": f"2QCD + 2D*sum|L_p| = {flops:.4g} FLOP; distinct probed lists {b_min / 1e9:.2f} GB"},
+                     "algorithmic": f"2QCD + 2D*sum|L_p| = {flops:.4g} FLOP; distinct probed lists {b_min / 1e9:.2f} GB",
+                     "counted": {name: counted(rel) for name, rel in COUNTERS_IVF.items()}},
     }
     log(f"configs[4] IVF top-10: {ms:.3f} ms/step = {res['qps']:.0f} QPS, {tflops:.1f} TFLOP/s effective; "
         f"{cand / 1e6:.1f}M candidates; build {build_s:.1f} s")
@@ -632,8 +630,8 @@ def run_pq(ctx, a, cpu: bool):
         "ms_per_step": ms, "qps": Q / (ms * 1e-3), "scan_timings": tim,
         "encode_rows_per_s": 1_000_000 / enc_s,
         "roofline": {"bound": "lds", "achieved": rate, "peak": lds_peak, "unit": "T lookups/s",
-                     "frac": (rate / lds_peak) if rate else None, "kernel": "pq_adc_kernel<true> (filter pass)",
-                     "algorithmic": f"Q*N*M = {lookups:.4g} table lookups (4 B each, LDS) per scan"},
+                     "frac": (rate / lds_peak) if rate else None, "kernel": "pq_adc_fast<16, true> (filter pass)",
+                     "algorithmic": f"Q*N*M = {lookups:.4g} table lookups (4 B each, LDS) per scan", **counted(COUNTERS_PQ)},
     }
     log(f"PQ ADC top-10: {ms:.3f} ms/step = {res['qps']:.0f} QPS; filter scan {scan_ms} ms = "
         f"{rate if rate is None else round(rate, 2)} T lookups/s; encode {res['encode_rows_per_s']:.3g} rows/s")
