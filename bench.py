@@ -376,7 +376,7 @@ def run_c3(ctx, a, cpu: bool):
     if cpu:
         from oracle import oracle
 
-        nq = 16
+        nq = 64
         xh = codes.cpu().numpy()
         qh = qcodes[:nq].cpu().numpy()
         t0 = time.perf_counter()
@@ -438,7 +438,7 @@ def run_c4(ctx, a, cpu: bool):
     if cpu:
         from oracle import oracle
 
-        nq = 16
+        nq = 32
         xh = x.cpu().numpy().view(np.uint32)
         qh = q[:nq].cpu().numpy().view(np.uint32)
         t0 = time.perf_counter()
@@ -504,7 +504,7 @@ def run_c5(ctx, a, cpu: bool):
     if cpu:
         from oracle import oracle
 
-        nq = 64
+        nq = 128
         xh = x.cpu().numpy()
         qh = q[:nq].cpu().numpy()
         ch = cen.cpu().numpy()
