@@ -7,13 +7,15 @@ the reference semantics cited in oracle/va_oracle.h.
 from __future__ import annotations
 
 import ctypes as C
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB = HERE / "libva_oracle.so"
+# VA_ORACLE_LIB: another build of the same source (the sanitizer build of run_sanitized.sh)
+LIB = Path(os.environ.get("VA_ORACLE_LIB", HERE / "libva_oracle.so"))
 
 L2SQ, COSINE, DOT, L2 = 0, 1, 2, 3
 SENTINEL = 0xFFFFFFFF

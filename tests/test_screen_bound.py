@@ -20,6 +20,7 @@ term, so no input separates them; they are kept because the proof needs them.
 from __future__ import annotations
 
 import ctypes as C
+import os
 import subprocess
 from pathlib import Path
 
@@ -36,6 +37,8 @@ F32 = np.float32
 def sb(request, tmp_path_factory):
     out = tmp_path_factory.mktemp("sb") / f"sb_{request.param}.so"
     flags = ["-ffp-contract=off"] if request.param == "plain" else ["-mfma", "-ffp-contract=fast"]
+    if os.environ.get("VA_SANITIZE"):  # oracle/run_sanitized.sh: the harness under ASan + UBSan too
+        flags += ["-g", "-fsanitize=address,undefined", "-fno-sanitize-recover=undefined"]
     proc = subprocess.run(["g++", "-std=c++17", "-O2", "-shared", "-fPIC", *flags, str(SRC), "-o", str(out)],
                           capture_output=True, text=True)
     assert proc.returncode == 0, proc.stderr
