@@ -2,13 +2,15 @@
 
 Headline (the JSON line's ``value``) = BASELINE.json configs[1]: flat cosine top-100 over
 N=1,000,000 x d=1536 fp32 (rows N(0,1) then L2-normalised), Q=1024 queries = database rows +
-N(0, 0.05) noise, renormalised.  A "step" is one va_fused_topk call over the resident
-database (threshold sample -> fp16 MFMA screening scan -> exact fp32 rerank of the band the
-screen's error bound leaves open -> selection); inputs are in HBM before the timed region.  The
+N(0, 0.05) noise, renormalised.  A "step" is one AcceleratedVectorIndex.search
+(va_index_search) over the resident index, whose fp32 rows and fp16 shadow are built at insert
+outside the timed region (threshold sample -> fp16 MFMA screening scan -> exact fp32 rerank of
+the band the screen's error bound leaves open -> selection; no step waits on the host).  The
 same search on the fp32 scan alone is timed beside it and must return the same ids and
-distances bit for bit (``fp32_scan_only``, ``screened_equals_fp32_scan``).  The other configs are measured the same way at full size and
-reported under ``extra`` (configs[2] int8 top-10, configs[3] binary top-100, configs[4]
-IVF-Flat top-10; configs[0] is the CPU-runnable parity case covered by the tests).
+distances bit for bit (``fp32_scan_only``, ``screened_equals_fp32_scan``).  The other configs
+are measured the same way at full size and reported under ``extra`` (configs[2] int8 top-10,
+configs[3] binary top-100, configs[4] IVF-Flat top-10, PQ ADC, IVF training; configs[0] is the
+CPU-runnable parity case covered by the tests).
 
 CPU baseline: the C oracle's float-accumulation port of the reference CPU path
 (CPUTopK / AccelerateFallback), timed on this host's cores on a bounded query sample.
