@@ -460,11 +460,27 @@ def run_c4(ctx, a, cpu: bool):
 # ---------------------------------------------------------------------------------------
 # IVF-Flat, 4096 lists, 4M x 768, Zipf(1.1) cluster sizes, Q=1024, nprobe 32
 # ---------------------------------------------------------------------------------------
+def ivf_phases(ctx, fn, reps: int = 3) -> dict:
+    """Phase times of the IVF list scan (the last scan of each search), averaged over a few
+    searches run after a timed loop (each read waits for its search)."""
+    keys = ("sample_ms", "scan_ms", "select_ms", "fallback_ms", "total_ms")
+    acc = {k: 0.0 for k in keys}
+    last = {}
+    for _ in range(reps):
+        fn()
+        ctx.synchronize()
+        last = ctx.last_scan_timings()
+        for k in keys:
+            acc[k] += float(last[k]) / reps
+    acc.update({k: last[k] for k in ("candidate_cap", "overflow_rows", "screened", "rerank_rows") if k in last})
+    return acc
+
+
 def run_c5(ctx, a, cpu: bool):
     import numpy as np
     import torch
 
-    from vectoraccelerate_amd import IVFSearchConfiguration, IVFSearchPipeline
+    from vectoraccelerate_amd import IVFSearchConfiguration, IVFSearchPipeline, _lib
 
     C, D, N, Q, nprobe, k = 4096, 768, 4_000_000, 1024, 32, 10
     log(f"configs[4]: generating C={C} N={N} D={D} Q={Q}")
@@ -488,21 +504,53 @@ def run_c5(ctx, a, cpu: bool):
     distinct = np.unique(probes)
     idx = ctx.empty((Q, k), torch.int32)
     dist = ctx.empty((Q, k), torch.float32)
-    ms, _ = timed(ctx, lambda: pipe.encodeSearch(q, st, idx, dist, k), max(3, a.steps // 2), 1, scan_timings=False)
+    step = lambda: pipe.encodeSearch(q, st, idx, dist, k)  # noqa: E731
+    ms, _ = timed(ctx, step, max(3, a.steps // 2), 1, scan_timings=False)
+    ph = ivf_phases(ctx, step)
+    # the same search on the fp32 list scan alone: the same ids and distances, bit for bit
+    idx32 = ctx.empty((Q, k), torch.int32)
+    dist32 = ctx.empty((Q, k), torch.float32)
+    step32 = lambda: pipe.encodeSearch(q, st, idx32, dist32, k)  # noqa: E731
+    ctx.set_option(_lib.VA_OPT_SCREEN, 1)
+    try:
+        ms32, _ = timed(ctx, step32, max(3, a.steps // 2), 1, scan_timings=False)
+        ph32 = ivf_phases(ctx, step32)
+    finally:
+        ctx.set_option(_lib.VA_OPT_SCREEN, 0)
+    same = bool(torch.equal(idx, idx32)) and bool(torch.equal(dist.view(torch.int32), dist32.view(torch.int32)))
     flops = 2.0 * Q * C * D + 2.0 * D * cand
     tflops = flops / (ms * 1e-3) / 1e12
     b_min = float(sizes[distinct].sum()) * D * 4 + C * D * 4
+    # the screened main pass streams the fp16 shadow of every probed list (each row block once,
+    # its query blocks on neighbouring waves) and the fp16 queries
+    b16 = float(sizes[distinct].sum()) * D * 2 + Q * D * 2
+    gbs = b16 / (ph["scan_ms"] * 1e-3) / 1e9
+    screened = bool(ph.get("screened", 0))
     res = {
         "workload": "configs[4]: IVF-Flat L2^2 top-10, 4096 lists, N=4,000,000 x d=768 (Zipf 1.1), Q=1024, nprobe 32",
-        "ms_per_step": ms, "qps": Q / (ms * 1e-3), "build_s": build_s,
+        "ms_per_step": ms, "qps": Q / (ms * 1e-3), "build_s": build_s, "phases_ms": ph,
         "candidates_scanned": cand, "largest_list": int(sizes.max()),
-        "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK["fp32_mfma_tflops"], "unit": "TFLOP/s",
-                     "frac": tflops / PEAK["fp32_mfma_tflops"], "kernel": "whole search (probe + sample + scan + select)",
-                     "algorithmic": f"2QCD + 2D*sum|L_p| = {flops:.4g} FLOP; distinct probed lists {b_min / 1e9:.2f} GB",
-                     "counted": {name: counted(rel) for name, rel in COUNTERS_IVF.items()}},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK["hbm_gbs"], "unit": "GB/s",
+                     "frac": gbs / PEAK["hbm_gbs"],
+                     "kernel": ("screened list scan: ivf16_narrow_kernel / ivf16_wide_kernel<1|2> (fp16 shadow rows "
+                                "on the fp16 MFMA, the three tile groups concurrently), timed as one phase"
+                                if screened else "fp32 list scan"),
+                     "algorithmic": f"fp16 shadow of the distinct probed lists + fp16 queries = {b16 / 1e9:.2f} GB "
+                                    f"per search (fp32 rows: {b_min / 1e9:.2f} GB)",
+                     "whole_search_fp32_equivalent_tflops": tflops,
+                     "whole_search_fp32_mfma_frac": tflops / PEAK["fp32_mfma_tflops"],
+                     "fp32_work": f"2QCD + 2D*sum|L_p| = {flops:.4g} FLOP"},
+        "fp32_list_scan_only": {"ms_per_step": ms32, "qps": Q / (ms32 * 1e-3), "phases_ms": ph32,
+                                "whole_search_tflops": flops / (ms32 * 1e-3) / 1e12,
+                                "counted": {name: counted(rel) for name, rel in COUNTERS_IVF.items()}},
+        "screened_equals_fp32_list_scan": same,
     }
-    log(f"configs[4] IVF top-10: {ms:.3f} ms/step = {res['qps']:.0f} QPS, {tflops:.1f} TFLOP/s effective; "
-        f"{cand / 1e6:.1f}M candidates; build {build_s:.1f} s")
+    if not same:
+        raise SystemExit("screened IVF search differs from the fp32 list scan")
+    del idx32, dist32
+    log(f"configs[4] IVF top-10: {ms:.3f} ms/step = {res['qps']:.0f} QPS ({tflops:.1f} TFLOP/s fp32-equivalent); "
+        f"list scan {ph['scan_ms']:.3f} ms = {gbs:.0f} GB/s of fp16 rows; fp32 list scan {ms32:.3f} ms/step; "
+        f"identical: {same}; {cand / 1e6:.1f}M candidates; build {build_s:.1f} s")
     if cpu:
         from oracle import oracle
 

@@ -31,4 +31,29 @@ void sb_pretest(int op, const float* bound4, float qq, float nq, float inv, floa
 
 uint32_t sb_key(float f) { return va::key_of_float(f); }
 
+// the L2^2 bound with measured rounding errors: b3 = {cn, gd, g2d}
+void sb_make_bound_v(uint32_t D, float* b3) {
+    const va::BoundV b = va::make_bound_v(D);
+    b3[0] = b.cn;
+    b3[1] = b.gd;
+    b3[2] = b.g2d;
+}
+
+float sb_err_norm_up(float ss, uint32_t D) { return va::err_norm_up(ss, D); }
+
+int sb_bounds_v(const float* b3, float dot, float qq, float nq, float eq, float xx, float nx, float ex, float* lo_hi) {
+    const va::BoundV b{b3[0], b3[1], b3[2]};
+    return va::screen_bounds_v(b, dot, qq, nq, eq, xx, nx, ex, lo_hi[0], lo_hi[1]) ? 1 : 0;
+}
+
+// abce[0..3] = the pre-test's constants A, B, E, C for threshold key thr_key
+void sb_pretest_v(const float* b3, float qq, float nq, float eq, float inv, uint32_t thr_key, float* abce) {
+    const va::BoundV b{b3[0], b3[1], b3[2]};
+    const va::PreTestV p = va::pretest_v(b, qq, nq, eq, inv, thr_key);
+    abce[0] = p.A;
+    abce[1] = p.B;
+    abce[2] = p.E;
+    abce[3] = p.C;
+}
+
 }  // extern "C"

@@ -248,21 +248,25 @@ def _ivf(ctx, C, D, N, Q, seed, zipf, add_first_id=None):
     return pipe, st, c, x, q, ids
 
 
+@pytest.mark.parametrize("screen", [0, 1])
 @pytest.mark.parametrize("added", [False, True])
-def test_ivf_fallback_bit_identical_to_scan(ctx, added):
+def test_ivf_fallback_bit_identical_to_scan(ctx, added, screen):
     """IVF queries forced to overflow a tiny candidate list: the device fallback (which walks each
     overflowed query's probed lists with the arithmetic of the kernel that scanned each list,
     the 16-query tiles for lists few queries probe and the distance GEMM for the others) gives the
-    unforced search's ids and distances bit for bit, also with row ids far above N."""
+    unforced search's ids and distances bit for bit, also with row ids far above N, after the
+    screened list scan (screen 0) and after the fp32 one (screen 1)."""
     from vectoraccelerate_amd import _lib
 
     pipe, st, c, x, q, ids = _ivf(ctx, 64, 96, 30000, 300, 5, 1.1, 3_000_000_000 if added else None)
-    ref = pipe.search(q, st, 20)
-    ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 24)
+    ctx.set_option(_lib.VA_OPT_SCREEN, screen)
     try:
+        ref = pipe.search(q, st, 20)
+        ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 24)
         forced = pipe.search(q, st, 20)
     finally:
         ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 0)
+        ctx.set_option(_lib.VA_OPT_SCREEN, 0)
     ri, fi = ref.indices.cpu().numpy().view(np.uint32), forced.indices.cpu().numpy().view(np.uint32)
     np.testing.assert_array_equal(fi, ri)
     np.testing.assert_array_equal(forced.distances.cpu().numpy().view(np.uint32),

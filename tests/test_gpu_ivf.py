@@ -165,3 +165,91 @@ def test_ivf_add_matches_rebuild(ctx, oracle, C, D, N0, adds):
     np.testing.assert_array_equal(a.distances.cpu().numpy(), b.distances.cpu().numpy())
     st.close()
     full.close()
+
+
+def _search_mode(ctx, pipe, q, st, k, screen):
+    """One search with VA_OPT_SCREEN = screen (0 automatic, 1 fp32 list scan only); returns the
+    result and whether the list scan ran screened."""
+    from vectoraccelerate_amd import _lib
+
+    ctx.set_option(_lib.VA_OPT_SCREEN, screen)
+    ctx.set_profiling(True)
+    try:
+        res = pipe.search(q, st, k)
+        screened = ctx.last_scan_timings()["screened"]
+    finally:
+        ctx.set_profiling(False)
+        ctx.set_option(_lib.VA_OPT_SCREEN, 0)
+    return res, screened
+
+
+# Shapes that reach every tile group of the screened scan: lists probed by a few queries (16-query
+# tiles), by 17-32 (32-query tiles) and by many (64-query tiles, several query blocks per list);
+# D not a multiple of 64 (zero-padded shadow rows) and a single 64-value chunk.
+@pytest.mark.parametrize("C,D,N,Q,nprobe,k,zipf", [(256, 64, 40000, 64, 8, 10, 1.1),
+                                                    (64, 96, 30000, 600, 4, 20, None),
+                                                    (16, 128, 20000, 600, 4, 10, None),
+                                                    (128, 100, 30000, 300, 8, 10, 1.1),
+                                                    (48, 36, 12000, 200, 6, 50, 1.1),
+                                                    (32, 768, 20000, 96, 32, 100, None)])
+def test_ivf_screened_bit_identical_to_fp32(ctx, oracle, C, D, N, Q, nprobe, k, zipf):
+    """The screened list scan (fp16 shadow rows on the fp16 MFMA, exact rerank with each list's
+    fp32 arithmetic) returns the fp32 list scan's ids and distances bit for bit, and both match
+    the oracle."""
+    from vectoraccelerate_amd import IVFSearchConfiguration, IVFSearchPipeline
+
+    c, x, q = clustered(C, D, N, Q, 7 * C + D, zipf)
+    pipe = IVFSearchPipeline(ctx, IVFSearchConfiguration(C, nprobe, D))
+    st = pipe.prepareIndexStructure(c, x)
+    scr, on = _search_mode(ctx, pipe, q, st, k, 0)
+    ref, off_ = _search_mode(ctx, pipe, q, st, k, 1)
+    assert (on, off_) == (1, 0)
+    si, ri = scr.indices.cpu().numpy().view(np.uint32), ref.indices.cpu().numpy().view(np.uint32)
+    np.testing.assert_array_equal(si, ri)
+    np.testing.assert_array_equal(scr.distances.cpu().numpy().view(np.uint32),
+                                  ref.distances.cpu().numpy().view(np.uint32))
+    off, ids = st.lists()
+    probes = pipe.findNearestCentroids(q, st).cpu().numpy().view(np.uint32)
+    oi, od = oracle.ivf_scan(q, x, off, ids, probes, k)
+    check_topk(L2SQ, q, x, k, si, scr.distances.cpu().numpy(), oi, od)
+    st.close()
+
+
+def test_ivf_screened_after_add(ctx, oracle):
+    """va_ivf_add rebuilds the fp16 shadow of the merged lists: the screened search still equals
+    the fp32 list scan after rows are added."""
+    from vectoraccelerate_amd import IVFSearchConfiguration, IVFSearchPipeline
+
+    c, x, q = clustered(64, 64, 24000, 200, 17, 1.1)
+    pipe = IVFSearchPipeline(ctx, IVFSearchConfiguration(64, 6, 64))
+    xd = ctx.buffer(x)
+    st = pipe.prepareIndexStructure(c, xd[:10000])
+    st.add(xd[10000:], 10000)
+    scr, on = _search_mode(ctx, pipe, q, st, 15, 0)
+    ref, _ = _search_mode(ctx, pipe, q, st, 15, 1)
+    assert on == 1
+    np.testing.assert_array_equal(scr.indices.cpu().numpy(), ref.indices.cpu().numpy())
+    np.testing.assert_array_equal(scr.distances.cpu().numpy().view(np.uint32),
+                                  ref.distances.cpu().numpy().view(np.uint32))
+    st.close()
+
+
+def test_ivf_screened_large_entries_always_reranked(ctx):
+    """Rows with entries beyond the fp16 range cannot be bounded: they are always candidates and
+    their exact keys decide, so the screened search still equals the fp32 list scan."""
+    from vectoraccelerate_amd import IVFSearchConfiguration, IVFSearchPipeline
+
+    c, x, q = clustered(32, 64, 8000, 64, 23, None)
+    g = rng(5)
+    big = g.choice(8000, 200, replace=False)
+    x[big] *= np.float32(3e4)  # some entries far beyond 65504
+    q[:8] = x[big[:8]] * np.float32(1.0001)  # queries next to those rows
+    pipe = IVFSearchPipeline(ctx, IVFSearchConfiguration(32, 4, 64))
+    st = pipe.prepareIndexStructure(c, x)
+    scr, on = _search_mode(ctx, pipe, q, st, 10, 0)
+    ref, _ = _search_mode(ctx, pipe, q, st, 10, 1)
+    assert on == 1
+    np.testing.assert_array_equal(scr.indices.cpu().numpy(), ref.indices.cpu().numpy())
+    np.testing.assert_array_equal(scr.distances.cpu().numpy().view(np.uint32),
+                                  ref.distances.cpu().numpy().view(np.uint32))
+    st.close()

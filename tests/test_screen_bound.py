@@ -52,6 +52,12 @@ def sb(request, tmp_path_factory):
     lib.sb_pretest.argtypes = [C.c_int, fp] + [C.c_float] * 4 + [C.c_uint32, fp]
     lib.sb_key.argtypes = [C.c_float]
     lib.sb_key.restype = C.c_uint32
+    lib.sb_make_bound_v.argtypes = [C.c_uint32, fp]
+    lib.sb_err_norm_up.argtypes = [C.c_float, C.c_uint32]
+    lib.sb_err_norm_up.restype = C.c_float
+    lib.sb_bounds_v.argtypes = [fp] + [C.c_float] * 7 + [fp]
+    lib.sb_bounds_v.restype = C.c_int
+    lib.sb_pretest_v.argtypes = [fp] + [C.c_float] * 4 + [C.c_uint32, fp]
     return lib
 
 
@@ -215,3 +221,123 @@ def test_screen_interval_contains_fp32_key_and_pretest_keeps_it(sb, D):
                         assert not (acc < rhs), ("pre-test dropped a pair", op, D, float(tau), float(lo))
                         passed += 1
     assert checked > 1000 and passed > 1000
+
+
+# ---- the L2^2 bound with measured rounding errors (the IVF list scan's screen) -------------------
+def _err_norm(sb, v, D):
+    """The kernels' error bound of a vector's fp16 image: the fp32 sum of the squared differences
+    (exact in fp32) through err_norm_up.  Entries beyond the fp16 range give inf."""
+    with np.errstate(all="ignore"):
+        d = (v.astype(np.float16).astype(F32) - v).astype(F32)
+        ss = F32(0)
+        for e in d:
+            ss = _fma(e, e, ss)
+    return F32(sb.sb_err_norm_up(ss, D))
+
+
+def _prep_v(sb, q, D):
+    """inv, the scaled fp16 query as floats, |q|^2, |q| and the unscaled error bound eq."""
+    sc = sb.sb_query_scale(F32(np.abs(q).max()), int(not np.all(np.isfinite(q))))
+    inv = F32(2.0 ** -sc)
+    qs = (q * F32(2.0 ** sc)).astype(F32)
+    q16 = qs.astype(np.float16).astype(F32)
+    qq = _sums(q * q)[0]
+    return inv, q16, qq, F32(np.sqrt(qq)), F32(_err_norm(sb, qs, D) * inv)
+
+
+@pytest.mark.parametrize("D", [4, 96, 1536])
+def test_screen_v_interval_is_nearly_reached(sb, D):
+    """Every entry of the query and the row just above an fp16 rounding midpoint: both round up by
+    almost u of themselves, so the fp16 dot exceeds the fp32 one by nearly eq|x| + |q|ex.  The fp32
+    keys stay inside [lo, hi], and where the measured-error terms dominate (D up to 96) the farthest
+    reaches 0.7 of the half-width, so dropping or halving either term fails the containment."""
+    b3 = np.zeros(3, F32)
+    sb.sb_make_bound_v(D, _fp(b3))
+    mid = F32(1 + 2.0**-11 + 2.0**-20)
+    half = D // 2
+    q = np.full(D, mid, F32)
+    x = np.concatenate([np.full(half, mid, F32), np.full(D - half, 2 * mid, F32)])
+    inv, q16, qq, nq, eq = _prep_v(sb, q, D)
+    ex = _err_norm(sb, x, D)
+    acc = _sums((q16 * x.astype(np.float16).astype(F32)).astype(F32))[0]
+    reach = 0.0
+    for xx in _sums(x * x):
+        nx = F32(np.sqrt(xx))
+        lohi = np.zeros(2, F32)
+        assert sb.sb_bounds_v(_fp(b3), F32(acc * inv), qq, nq, eq, xx, nx, ex, _fp(lohi))
+        lo, hi = (float(v) for v in lohi)
+        keys = [float(_key(L2SQ, d, q2, x2)) for d in _dots(q, x) for q2 in _sums(q * q) for x2 in _sums(x * x)]
+        assert all(lo <= k <= hi for k in keys), (lo, min(keys), max(keys), hi)
+        s = (lo + hi) / 2
+        reach = max(reach, max(abs(k - s) for k in keys) / ((hi - lo) / 2))
+    if D <= 96:
+        assert reach >= 0.7, (D, reach)
+
+
+@pytest.mark.parametrize("D", [4, 96, 1536])
+def test_screen_v_contains_fp32_key_and_pretest_keeps_it(sb, D):
+    """The adversarial families of the fp16 screen (mixed magnitudes, fp16 subnormals and underflow,
+    fp32 subnormals, anti-correlated and near-duplicate pairs, entries at and beyond the fp16 range,
+    queries over 16 decades): with the measured error norms every fp32 L2^2 key (several summation
+    orders) lies in [lo, hi] for every order of the screened accumulator, and the pre-test never
+    drops a pair whose lower bound is at or below the threshold."""
+    rng = np.random.default_rng(2000 + D)
+    b3 = np.zeros(3, F32)
+    sb.sb_make_bound_v(D, _fp(b3))
+    checked = passed = 0
+    for q, x in _cases(rng, D):
+        inv, q16, qq, nq, eq = _prep_v(sb, q, D)
+        ex = _err_norm(sb, x, D)
+        with np.errstate(over="ignore"):
+            x16 = x.astype(np.float16).astype(F32)
+        with np.errstate(all="ignore"):
+            accs = _sums((q16 * x16).astype(F32))
+        for xx in _sums(x * x):
+            nx = F32(np.sqrt(xx))
+            flagged = not (xx < F32(4.29e9))
+            xxp, nxp, exp = (F32(np.nan),) * 3 if flagged else (xx, nx, ex)
+            keys = [_key(L2SQ, d, q2, x2) for d in _dots(q, x) for q2 in _sums(q * q)[:2] for x2 in _sums(x * x)[:2]]
+            for acc in accs:
+                lohi = np.zeros(2, F32)
+                ok = sb.sb_bounds_v(_fp(b3), F32(acc * inv), qq, nq, eq, xx, nx, ex, _fp(lohi))
+                lo, hi = lohi
+                if ok:
+                    for k in keys:
+                        if k == k:
+                            assert lo <= k <= hi, (D, float(lo), float(k), float(hi))
+                            checked += 1
+                taus = [lo, np.nextafter(lo, F32(np.inf)), hi, max(keys)] if ok else [F32(0), F32(1), F32(-1e30)]
+                for tau in taus:
+                    abce = np.zeros(4, F32)
+                    sb.sb_pretest_v(_fp(b3), qq, nq, eq, inv, sb.sb_key(F32(tau)), _fp(abce))
+                    if ok and not (lo <= tau):
+                        continue
+                    rhs = _fma(abce[0], xxp, _fma(abce[1], nxp, _fma(abce[2], exp, abce[3])))
+                    assert not (acc < rhs), ("pre-test dropped a pair", D, float(tau), float(lo))
+                    passed += 1
+    assert checked > 200 and passed > 200
+
+
+def test_screen_v_is_tighter_on_typical_rows(sb):
+    """On Gaussian data the measured-error interval is narrower than the worst-case one (the point
+    of measuring): at D = 768 at most 0.65 of its width (about 0.6)."""
+    D = 768
+    rng = np.random.default_rng(7)
+    b4, b3 = np.zeros(4, F32), np.zeros(3, F32)
+    sb.sb_make_bound(D, _fp(b4))
+    sb.sb_make_bound_v(D, _fp(b3))
+    ratios = []
+    for _ in range(20):
+        q = (rng.standard_normal(D) + 4 * rng.standard_normal(D)).astype(F32)
+        x = (q + rng.standard_normal(D)).astype(F32)
+        inv, q16, qq, nq, c0q = _prep(sb, q, b4[2])
+        eq = _prep_v(sb, q, D)[4]
+        ex = _err_norm(sb, x, D)
+        acc = _sums((q16 * x.astype(np.float16).astype(F32)).astype(F32))[0]
+        xx = _sums(x * x)[0]
+        nx = F32(np.sqrt(xx))
+        w0, w1 = np.zeros(2, F32), np.zeros(2, F32)
+        assert sb.sb_bounds(L2SQ, _fp(b4), F32(acc * inv), qq, nq, xx, nx, c0q, _fp(w0))
+        assert sb.sb_bounds_v(_fp(b3), F32(acc * inv), qq, nq, eq, xx, nx, ex, _fp(w1))
+        ratios.append(float(w1[1] - w1[0]) / float(w0[1] - w0[0]))
+    assert max(ratios) <= 0.65, ratios

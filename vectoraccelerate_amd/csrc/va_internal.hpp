@@ -270,8 +270,9 @@ VA_HD inline uint32_t ivf_sample_rows(uint32_t n) {
 // tile shape, enumerated by pre[] (the exclusive prefix over the lists of their tile counts for
 // this shape; pre[C] tiles in all).  List l is probed by the queries qlist[qoff[l] .. qoff[l+1])
 // (the launch's qrow) and holds the row positions roff[l] .. roff[l+1] (its sample prefix when
-// sample is set).  Tile t of list l covers query block (t - pre[l]) / row blocks and row block
-// (t - pre[l]) % row blocks.
+// sample is set).  Tile t of list l covers row block (t - pre[l]) / query blocks and query block
+// (t - pre[l]) % query blocks: the query blocks of a row block are neighbouring tiles, so a long
+// list probed by many queries is read from HBM about once, not once per query block.
 struct ListPlan {
     const uint32_t* pre = nullptr;   // [C + 1]
     const uint32_t* qoff = nullptr;  // [C + 1]
@@ -293,8 +294,8 @@ __device__ inline void plan_tile(const ListPlan& p, uint32_t t, uint32_t TQ, uin
     const uint32_t nq = p.qoff[l + 1] - p.qoff[l];
     const uint32_t len = p.roff[l + 1] - p.roff[l];
     const uint32_t n = p.sample ? ivf_sample_rows(len) : len;
-    const uint32_t nrb = (n + TN - 1) / TN;
-    const uint32_t qb = local / nrb, rb = local % nrb;
+    const uint32_t nqb = (nq + TQ - 1) / TQ;
+    const uint32_t rb = local / nqb, qb = local % nqb;
     qs = p.qoff[l] + qb * TQ;
     qc = min(TQ, nq - qb * TQ);
     rs = p.roff[l] + rb * TN;
@@ -528,8 +529,28 @@ va_status flat_topk(va_context* ctx, DistOp op, const float* q, const float* x, 
 // Halves per row of an fp16 shadow (D rounded up to a multiple of 64).
 uint32_t shadow_pitch(uint32_t D);
 // shadow[r * shadow_pitch(D) + d] = fp16(x[r * D + d]) (RNE, zeros past D), norms[r] = |x_r|^2
-// in fp32, for rows r < N.
-va_status build_shadow(va_context* ctx, const float* x, uint32_t N, uint32_t D, _Float16* shadow, float* norms);
+// in fp32, for rows r < N.  norm_err (may be nullptr; norms may then be nullptr): {|x_r|^2, an
+// upper bound of |fp16(x_r) - x_r|} per row (infinite past the fp16 range).
+va_status build_shadow(va_context* ctx, const float* x, uint32_t N, uint32_t D, _Float16* shadow, float* norms,
+                       float2* norm_err = nullptr);
+// Pieces of the screened scan shared with the IVF list scan (va_screen.hip).  The bound itself
+// is va_screen_bound.hpp's.
+struct ScreenBound;
+// qh[q * shadow_pitch(D) + d] = fp16(q[q * D + d] * 2^sc_q) (the query's scale puts its largest
+// entry in [2^14, 2^15)), qinfo[q] = {|q|^2, |q|, 2^-sc_q, c0 * 2^-25 * 2^-sc_q}; qerr (may be
+// nullptr): an upper bound of the norm of the (unscaled) rounding error of each query's fp16 image.
+va_status screen_prepare_queries(va_context* ctx, const float* q, uint32_t Q, uint32_t D, _Float16* qh,
+                                 float4* qinfo, float c0, float* qerr = nullptr);
+// Candidate lists of screened pairs, in place: (unscaled fp16 dot, |x|^2) -> (key of the upper
+// bound, key of the lower bound) of the pair's fp32 key, for i < min(cnt[q], cap).
+va_status screen_list_bounds(va_context* ctx, const ScreenBound& b, const float4* qinfo, float* dot, float* xx,
+                             const uint32_t* cnt, uint32_t cap, uint32_t Q);
+// Rerank lists: rr[q * rcap ..] = the cand_id of the candidates with lower bound <= bound[q];
+// queries whose candidates overflowed (cnt > cap) or whose list outgrows rcap get rcount 0 and
+// are appended to ovf_rows (ovf_cnt[0] counts them; ovf_cnt[1] receives the longest list).
+va_status screen_compact(va_context* ctx, const uint32_t* cnt, const uint32_t* cand_lo, const uint32_t* cand_id,
+                         const uint32_t* bound, uint32_t cap, uint32_t Q, uint32_t* rr, uint32_t* rcount, uint32_t rcap,
+                         uint32_t* ovf_cnt, uint32_t* ovf_rows);
 // Whether the screened path applies (metric, alignment, sizes, VA_OPT_SCREEN).
 bool screen_applies(const va_context* ctx, const ScreenInput& in, uint32_t k);
 va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer& exact, uint32_t k,

@@ -27,6 +27,7 @@
 
 #include "va_fallback.hpp"
 #include "va_internal.hpp"
+#include "va_screen_bound.hpp"
 
 struct va_ivf {
     int device = 0;
@@ -35,6 +36,11 @@ struct va_ivf {
     float* list_vectors = nullptr;  // [N x D] in CSR order
     uint32_t* ids = nullptr;        // [N] original row id of every CSR position
     uint32_t* offsets = nullptr;    // [C + 1]
+    // fp16 shadow of list_vectors (rows of va::shadow_pitch(D) halves) and per row {|x|^2, an
+    // upper bound of |fp16(x) - x|}, for the screened list scan; nullptr when D % 4 != 0 or the
+    // allocation failed
+    _Float16* shadow = nullptr;
+    float2* norms = nullptr;
     std::vector<uint32_t> h_offsets;
     // host bounds of a search (from the list sizes, so a search reads nothing back): top_rows[p]
     // = rows of the p longest lists, top_sample[p] = their threshold-sample rows, max_len =
@@ -117,6 +123,25 @@ __global__ __launch_bounds__(256) void gather_rows(const float* __restrict__ x, 
             for (uint32_t d = threadIdx.x; d < D; d += 256) dst[d] = src[d];
         }
     }
+}
+
+// The fp16 shadow of n list rows for the screened scan.  None (both nullptr) when D % 4 != 0
+// or memory is short: the index then searches with the fp32 list scan alone.
+va_status make_list_shadow(va_context* ctx, const float* vecs, uint32_t n, uint32_t D, _Float16** sh, float2** nr) {
+    *sh = nullptr;
+    *nr = nullptr;
+    if (D % 4 != 0 || n == 0) return VA_OK;
+    void* a = nullptr;
+    void* b = nullptr;
+    if (hipMalloc(&a, uint64_t(n) * shadow_pitch(D) * 2) != hipSuccess ||
+        hipMalloc(&b, uint64_t(n) * 8) != hipSuccess) {
+        (void)hipGetLastError();
+        if (a) (void)hipFree(a);
+        return VA_OK;
+    }
+    *sh = static_cast<_Float16*>(a);
+    *nr = static_cast<float2*>(b);
+    return build_shadow(ctx, vecs, n, D, *sh, nullptr, *nr);
 }
 
 struct F32Keys final : KeyProducer {
@@ -312,6 +337,318 @@ __global__ __launch_bounds__(256) void ivf_small_kernel(DistArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// The screened list scan: fp16 shadow rows on the fp16 MFMA
+// ---------------------------------------------------------------------------------------
+// The rows stream from the index's fp16 shadow (half the bytes of the fp32 rows) and every pair
+// is screened with the flat screen's proven bound (va_screen_bound.hpp): a pair becomes a
+// candidate when the lower end of the interval that contains its fp32 key can be <= tau_q (the
+// linear pre-test on the scaled fp16 dot).  The exact keys of the few rows that can reach the
+// top-k are then recomputed with the arithmetic of the kernel that scans the list in the fp32
+// list scan, so the result is the fp32 list scan's, bit for bit.
+//
+// One wave per tile (no LDS staging, no barrier), persistent over the device plan:
+//   narrow : 16 queries x 128 rows, v_mfma_f32_16x16x32_f16 (lists probed by <= 16 queries);
+//   wide<W>: 32W queries x 128 rows, v_mfma_f32_32x32x16_f16 (W = 1: 17-32 queries, 2: more).
+// Both operands load straight into registers.  A dot is the same sum whatever the order of its
+// terms (the bound does not depend on it), so the k order inside a 64-value chunk follows the
+// loads: a narrow lane loads 32 and a wide lane 64 contiguous bytes of its row or query, and
+// the two lanes that meet in an MFMA hold the same k indices.  The pre-test's constants come
+// from the query's threshold; the appended (dot, |x|^2, position) triples become intervals in
+// screen_list_bounds.
+namespace iv16 {
+constexpr uint32_t TN = 128, WAVES = 4;
+constexpr int kGroupsUsed = 3;  // narrow, wide<1>, wide<2>
+__host__ __device__ inline int group_of(uint32_t nq) { return nq <= 16 ? 0 : (nq <= 32 ? 1 : 2); }
+__host__ __device__ inline uint32_t group_tq(int g) { return g == 0 ? 16u : 32u * uint32_t(g); }
+}  // namespace iv16
+
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16s __attribute__((ext_vector_type(16)));
+
+struct Ivf16Args {
+    const _Float16* qh = nullptr;    // [Q x Dp] scaled fp16 queries (screen_prepare_queries)
+    const float4* qinfo = nullptr;   // {|q|^2, |q|, 2^-scale, c0q}
+    const float* qerr = nullptr;     // [Q] bound of |fp16(q) - q| (unscaled)
+    const uint32_t* qrow = nullptr;  // the plan's query lists
+    const _Float16* xh = nullptr;    // [N x Dp] fp16 list rows, CSR order
+    const float2* xn = nullptr;      // [N] {|x|^2, bound of |fp16(x) - x|}
+    uint32_t Dp = 0;
+    BoundV bnd{};
+    const uint32_t* thr = nullptr;   // tau_q as keys (~0: every pair passes)
+    uint32_t* cnt = nullptr;
+    float* cand_dot = nullptr;       // unscaled fp16 dots
+    uint32_t* cand_pos = nullptr;    // CSR positions
+    uint32_t cap = 0;
+    ListPlan plan;
+};
+
+// pre-test inputs of a row: rows whose entries can leave the fp16 range are flagged NaN (their
+// right-hand side is NaN, so they always pass)
+__device__ __forceinline__ void screen_norms(float2 n, float& xxp, float& nxp, float& exp) {
+    const bool flag = !(n.x < 4.29e9f);
+    xxp = flag ? __builtin_nanf("") : n.x;
+    nxp = flag ? __builtin_nanf("") : __builtin_amdgcn_sqrtf(n.x);
+    exp = flag ? __builtin_nanf("") : n.y;
+}
+__device__ __forceinline__ float pretest_rhs(const PreTestV& p, float xxp, float nxp, float exp) {
+    return fmaf(p.A, xxp, fmaf(p.B, nxp, fmaf(p.E, exp, p.C)));
+}
+
+__device__ __forceinline__ h8v masked_h8(const _Float16* p, bool use) {
+    u32x4 t = __builtin_bit_cast(u32x4, *reinterpret_cast<const h8v*>(p));
+    t &= use ? 0xFFFFFFFFu : 0u;
+    return __builtin_bit_cast(h8v, t);
+}
+
+// The wave's rows' {|x|^2, error bound} into its LDS slot xs[0 .. 128) (zeros past rc); read back
+// by the same wave after the main loop (one wave's LDS accesses are in order).
+__device__ __forceinline__ void stage_norms(const Ivf16Args& a, float2* xs, uint32_t rs, uint32_t rc, int lane) {
+    xs[lane] = uint32_t(lane) < rc ? a.xn[rs + uint32_t(lane)] : make_float2(0.0f, 0.0f);
+    xs[64 + lane] = uint32_t(64 + lane) < rc ? a.xn[rs + 64u + uint32_t(lane)] : make_float2(0.0f, 0.0f);
+}
+
+// Appends the set bits of mask (bit t = element t of vals / rows[t]) to query qi's list from
+// position pos.
+template <int NB>
+__device__ __forceinline__ void append_pairs(const Ivf16Args& a, uint32_t qi, uint32_t pos, uint32_t mask,
+                                             const float (&vals)[NB], const uint32_t (&rows)[NB], uint32_t rs,
+                                             float inv) {
+#pragma unroll
+    for (int t = 0; t < NB; ++t) {
+        if (!((mask >> t) & 1u)) continue;
+        if (pos < a.cap) {
+            const int64_t o = int64_t(qi) * a.cap + pos;
+            a.cand_dot[o] = vals[t] * inv;
+            a.cand_pos[o] = rs + rows[t];
+        }
+        ++pos;
+    }
+}
+
+// narrow tile: lane (j, g) = (lane % 16, lane / 16) loads 16 halves at 64c + 16g of row j of
+// each 16-row block and of query j; MFMA u of chunk c takes halves 8u .. 8u + 7 of them.  The
+// result: lane (j, g) holds query j against rows 16b + 4g + v in acc[b][v].
+__device__ __forceinline__ void narrow_tile(const Ivf16Args& a, float2* xs, uint32_t qs, uint32_t qc, uint32_t rs,
+                                            uint32_t rc) {
+    const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+    const bool qv = uint32_t(j) < qc;
+    const uint32_t qi = a.qrow[qs + (qv ? uint32_t(j) : 0u)];
+    const _Float16* qp = a.qh + int64_t(qi) * a.Dp + 16 * g;
+    const uint32_t rowb = a.Dp * 2u;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(a.xh + int64_t(rs) * a.Dp), 0, int(rc * rowb), 0x00020000);
+    const uint32_t lo = uint32_t(j) * rowb + 32u * uint32_t(g);
+    const uint32_t nch = a.Dp / 64;
+    stage_norms(a, xs, rs, rc, lane);
+    h8v qa[2], qb[2], ra[8][2], rb[8][2];
+    // past the last chunk every operand is zero (the query through the mask, rows past the
+    // descriptor), so the extra MFMAs add nothing
+    auto load = [&](uint32_t c, h8v(&q2)[2], h8v(&r2)[8][2]) {
+        const bool in = c < nch;
+        const uint32_t k = in ? 64u * c : 0u;
+        q2[0] = masked_h8(qp + k, qv && in);
+        q2[1] = masked_h8(qp + k + 8, qv && in);
+        const uint32_t vo = in ? lo + 2u * k : 0x80000000u;
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+                r2[b][u] = __builtin_bit_cast(
+                    h8v, __builtin_amdgcn_raw_buffer_load_b128(xr, vo + uint32_t(b) * 16u * rowb + 16u * uint32_t(u), 0, 0));
+    };
+    f32x4s acc[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) acc[b] = f32x4s{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](const h8v(&q2)[2], const h8v(&r2)[8][2]) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int b = 0; b < 8; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(r2[b][u], q2[u], acc[b], 0, 0, 0);
+    };
+    load(0, qa, ra);
+    for (uint32_t c = 0; c < nch; c += 2) {
+        load(c + 1, qb, rb);
+        compute(qa, ra);
+        __builtin_amdgcn_sched_barrier(0);
+        load(c + 2, qa, ra);
+        compute(qb, rb);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (!qv) return;
+    const float4 inf = a.qinfo[qi];
+    const PreTestV pt = pretest_v(a.bnd, inf.x, inf.y, a.qerr[qi], inf.z, a.thr[qi]);
+    float vals[32];
+    uint32_t rows[32];
+    uint32_t mask = 0;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int t = 4 * b + v;
+            rows[t] = uint32_t(16 * b + 4 * g + v);
+            vals[t] = acc[b][v];
+            float xxp, nxp, exp;
+            screen_norms(xs[rows[t]], xxp, nxp, exp);
+            mask |= uint32_t((rows[t] < rc) & !(vals[t] < pretest_rhs(pt, xxp, nxp, exp))) << t;
+        }
+    }
+    if (!mask) return;
+    const uint32_t pos = atomicAdd(a.cnt + qi, uint32_t(__popc(mask)));
+    append_pairs<32>(a, qi, pos, mask, vals, rows, rs, inf.z);
+}
+
+// wide tile: lane (l32, hh) loads 32 halves at 64c + 32hh of row l32 of each 32-row block and of
+// query l32 of each 32-query block; MFMA u of chunk c takes halves 8u .. 8u + 7.  The result:
+// lane (l32, hh) holds query 32n + l32 against rows 32m + 8i + 4hh + e in acc[n][m][4i + e].
+template <int W>
+__device__ __forceinline__ void wide_tile(const Ivf16Args& a, float2* xs, uint32_t qs, uint32_t qc, uint32_t rs,
+                                          uint32_t rc) {
+    const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5;
+    bool qv[W];
+    uint32_t qi[W];
+    const _Float16* qp[W];
+#pragma unroll
+    for (int n = 0; n < W; ++n) {
+        qv[n] = uint32_t(32 * n + l32) < qc;
+        qi[n] = a.qrow[qs + (qv[n] ? uint32_t(32 * n + l32) : 0u)];
+        qp[n] = a.qh + int64_t(qi[n]) * a.Dp + 32 * hh;
+    }
+    const uint32_t rowb = a.Dp * 2u;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(a.xh + int64_t(rs) * a.Dp), 0, int(rc * rowb), 0x00020000);
+    const uint32_t lo = uint32_t(l32) * rowb + 64u * uint32_t(hh);
+    const uint32_t nch = a.Dp / 64;
+    stage_norms(a, xs, rs, rc, lane);
+    h8v qa[W][4], qb[W][4], ra[4][4], rb[4][4];
+    auto load = [&](uint32_t c, h8v(&q4)[W][4], h8v(&r4)[4][4]) {
+        const bool in = c < nch;
+        const uint32_t k = in ? 64u * c : 0u;
+#pragma unroll
+        for (int n = 0; n < W; ++n)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) q4[n][u] = masked_h8(qp[n] + k + 8 * u, qv[n] && in);
+        const uint32_t vo = in ? lo + 2u * k : 0x80000000u;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                r4[m][u] = __builtin_bit_cast(
+                    h8v, __builtin_amdgcn_raw_buffer_load_b128(xr, vo + uint32_t(m) * 32u * rowb + 16u * uint32_t(u), 0, 0));
+    };
+    f32x16s acc[W][4];
+#pragma unroll
+    for (int n = 0; n < W; ++n)
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[n][m][v] = 0.0f;
+    auto compute = [&](const h8v(&q4)[W][4], const h8v(&r4)[4][4]) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int n = 0; n < W; ++n)
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+                    acc[n][m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(r4[m][u], q4[n][u], acc[n][m], 0, 0, 0);
+    };
+    load(0, qa, ra);
+    for (uint32_t c = 0; c < nch; c += 2) {
+        load(c + 1, qb, rb);
+        compute(qa, ra);
+        __builtin_amdgcn_sched_barrier(0);
+        load(c + 2, qa, ra);
+        compute(qb, rb);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    PreTestV pt[W];
+    float inv[W];
+#pragma unroll
+    for (int n = 0; n < W; ++n) {
+        const float4 inf = a.qinfo[qi[n]];
+        pt[n] = pretest_v(a.bnd, inf.x, inf.y, a.qerr[qi[n]], inf.z, a.thr[qi[n]]);
+        inv[n] = inf.z;
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        float xxp[16], nxp[16], exp[16];
+        uint32_t rows[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            rows[t] = uint32_t(32 * m + 8 * (t >> 2) + 4 * hh + (t & 3));
+            screen_norms(xs[rows[t]], xxp[t], nxp[t], exp[t]);
+        }
+#pragma unroll
+        for (int n = 0; n < W; ++n) {
+            float vals[16];
+            uint32_t mask = 0;
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                vals[t] = acc[n][m][t];
+                mask |= uint32_t((rows[t] < rc) & !(vals[t] < pretest_rhs(pt[n], xxp[t], nxp[t], exp[t]))) << t;
+            }
+            mask = qv[n] ? mask : 0u;
+            // lanes l32 and l32 + 32 hold the same query: one atomic reserves both lanes' places
+            const uint32_t c = uint32_t(__popc(mask));
+            const uint32_t other = uint32_t(__shfl_xor(int(c), 32));
+            uint32_t base = 0;
+            if (hh == 0 && c + other) base = atomicAdd(a.cnt + qi[n], c + other);
+            base = uint32_t(__shfl(int(base), l32));
+            if (mask) append_pairs<16>(a, qi[n], hh ? base + other : base, mask, vals, rows, rs, inv[n]);
+        }
+    }
+}
+
+// Candidate lists of the screened scan, in place: (unscaled fp16 dot, position) -> the key of the
+// pair's upper bound (over the dot) and of its lower bound (into lo), for i < min(cnt[q], cap).
+// Pairs that cannot be bounded get [0, the NaN key].
+__global__ __launch_bounds__(256) void ivf_bound_kernel(BoundV b, const float4* __restrict__ qinfo,
+                                                        const float* __restrict__ qerr, const float2* __restrict__ xn,
+                                                        float* __restrict__ dot, const uint32_t* __restrict__ pos,
+                                                        uint32_t* __restrict__ lo, const uint32_t* __restrict__ cnt,
+                                                        uint32_t cap) {
+    const uint32_t q = blockIdx.y;
+    const float4 inf = qinfo[q];
+    const float eq = qerr[q];
+    const uint32_t m = min(cnt[q], cap);
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < m; i += gridDim.x * 256) {
+        const int64_t o = int64_t(q) * cap + i;
+        const float2 n = xn[pos[o]];
+        float l, h;
+        uint32_t klo = 0u, khi = 0xFFFFFFFEu;
+        if (screen_bounds_v(b, dot[o], inf.x, inf.y, eq, n.x, sqrtf(n.x), n.y, l, h)) {
+            klo = key_of_float(l);
+            khi = key_of_float(h);
+        }
+        reinterpret_cast<uint32_t*>(dot)[o] = khi;
+        lo[o] = klo;
+    }
+}
+
+__global__ __launch_bounds__(256, 2) void ivf16_narrow_kernel(Ivf16Args a) {
+    __shared__ __attribute__((aligned(16))) float2 xs[iv16::WAVES][iv16::TN];
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+    const uint32_t total = a.plan.pre[a.plan.C];
+    for (uint32_t t = blockIdx.x * iv16::WAVES + uint32_t(wave); t < total; t += gridDim.x * iv16::WAVES) {
+        uint32_t qs, qc, rs, rc;
+        plan_tile(a.plan, t, 16, iv16::TN, qs, qc, rs, rc);
+        narrow_tile(a, xs[wave], qs, qc, rs, rc);
+    }
+}
+
+template <int W>
+__global__ __launch_bounds__(256, 1) void ivf16_wide_kernel(Ivf16Args a) {
+    __shared__ __attribute__((aligned(16))) float2 xs[iv16::WAVES][iv16::TN];
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+    const uint32_t total = a.plan.pre[a.plan.C];
+    for (uint32_t t = blockIdx.x * iv16::WAVES + uint32_t(wave); t < total; t += gridDim.x * iv16::WAVES) {
+        uint32_t qs, qc, rs, rc;
+        plan_tile(a.plan, t, 32u * W, iv16::TN, qs, qc, rs, rc);
+        wide_tile<W>(a, xs[wave], qs, qc, rs, rc);
+    }
+}
+
 // Tile shapes of the list-major scan.  A tile of wq x wn waves covers 32*wq queries x 128*wn
 // rows.  A list with nq probing queries and n rows gets the shape with the least estimated
 // time: tiles x waves x the measured cost of one wave tile (32 x 128) in that shape on MI355X
@@ -363,6 +700,7 @@ struct DevPlan {
     uint32_t Q = 0, np = 0, C = 0;
     const uint32_t* roff = nullptr;    // list offsets [C + 1]
     uint32_t small_ok = 0;
+    uint32_t screen = 0;        // tile groups of the screened scan (iv16) instead of the fp32 shapes
     uint32_t* P = nullptr;      // [Q x np] probes with repeats / sentinels replaced by ~0
     uint32_t* qcnt = nullptr;   // [C] queries per list
     uint32_t* qoff = nullptr;   // [C + 1]
@@ -425,9 +763,16 @@ __global__ __launch_bounds__(256) void plan_fill_kernel(DevPlan p) {
 __global__ __launch_bounds__(256) void plan_counts_kernel(DevPlan p) {
     for (uint32_t l = blockIdx.x * 256 + threadIdx.x; l < p.C; l += gridDim.x * 256) {
         const uint32_t nq = p.qcnt[l], n = p.roff[l + 1] - p.roff[l];
-        const int g = (p.small_ok && nq <= kSmallListQueries) ? kSmallGroup : shape_for(nq, n);
+        int g;
         uint32_t TQ, TN;
-        group_tile(g, TQ, TN);
+        if (p.screen) {
+            g = iv16::group_of(nq);
+            TQ = iv16::group_tq(g);
+            TN = iv16::TN;
+        } else {
+            g = (p.small_ok && nq <= kSmallListQueries) ? kSmallGroup : shape_for(nq, n);
+            group_tile(g, TQ, TN);
+        }
         for (int pass = 0; pass < 2; ++pass) {
             const uint32_t rows = pass == 0 ? ivf_sample_rows(n) : n;
             const uint32_t tiles = (nq == 0 || rows == 0) ? 0u : ((nq + TQ - 1) / TQ) * ((rows + TN - 1) / TN);
@@ -504,6 +849,33 @@ va_status run_planned_pass(va_context* ctx, const DevPlan& dp, int pass, const f
             st = launch_dist(ctx, a);
             ctx->stream = main_stream;
         }
+    }
+    const va_status j = aux_join(ctx);
+    return st != VA_OK ? st : j;
+}
+
+// One screened pass over the device plan: the three tile groups as persistent launches, the
+// narrow tiles on the context's stream and the wide ones on auxiliary streams (they meet only
+// in the per-query atomics of the candidate lists).
+va_status run_screen_pass(va_context* ctx, const DevPlan& dp, int pass, Ivf16Args a) {
+    VA_CHECK_STATUS(aux_fork(ctx));
+    a.qrow = dp.qlist;
+    a.plan.qoff = dp.qoff;
+    a.plan.roff = dp.roff;
+    a.plan.C = dp.C;
+    a.plan.sample = pass == 0 ? 1u : 0u;
+    va_status st = VA_OK;
+    for (int g = 0; g < iv16::kGroupsUsed && st == VA_OK; ++g) {
+        a.plan.pre = dp.pre + (int64_t(pass) * kGroups + g) * (int64_t(dp.C) + 1);
+        const hipStream_t s = g == 0 ? ctx->stream : ctx->aux[g - 1];
+        if (g == 0) {
+            ivf16_narrow_kernel<<<dim3(uint32_t(ctx->num_cus) * 2), dim3(256), 0, s>>>(a);
+        } else if (g == 1) {
+            ivf16_wide_kernel<1><<<dim3(uint32_t(ctx->num_cus)), dim3(256), 0, s>>>(a);
+        } else {
+            ivf16_wide_kernel<2><<<dim3(uint32_t(ctx->num_cus)), dim3(256), 0, s>>>(a);
+        }
+        if (hipGetLastError() != hipSuccess) st = fail(ctx, VA_ERR_HIP, "screened list scan launch failed");
     }
     const va_status j = aux_join(ctx);
     return st != VA_OK ? st : j;
@@ -624,6 +996,109 @@ __global__ __launch_bounds__(256) void fb_ivf_pass_kernel(FbIvf v, FbArgs a, int
     fb_pass_done(a, pass, n);
 }
 
+// ---- exact keys of the screened scan's rerank lists ------------------------------------------
+// One wave per (32-row chunk of a query's rerank list, query), persistent and chunk-major.  The
+// rows hold CSR positions; each row's key comes from the arithmetic of the kernel that scans its
+// list in the fp32 list scan (small_keys32 for lists probed by at most 16 queries, the distance
+// GEMM's block otherwise), and the row's id replaces its position.  A chunk that mixes the two
+// kinds runs both (every output element depends on its own row and query only).
+__global__ __launch_bounds__(256) void ivf_rerank_kernel(const float* __restrict__ q, const float* __restrict__ x,
+                                                         const uint32_t* __restrict__ ids,
+                                                         const uint32_t* __restrict__ roff, uint32_t C,
+                                                         const uint32_t* __restrict__ qcnt, uint32_t D,
+                                                         const uint32_t* __restrict__ rr,
+                                                         const uint32_t* __restrict__ rcount, uint32_t rcap, uint32_t Q,
+                                                         uint32_t* __restrict__ rkey, uint32_t* __restrict__ rid) {
+    const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5, j = lane & 15, g = lane >> 4;
+    const uint32_t nch = (rcap + 31) / 32;
+    const uint64_t items = uint64_t(Q) * nch;
+    const uint32_t nw = gridDim.x * 4;
+    for (uint64_t it = uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6); it < items; it += nw) {
+        const uint32_t c = uint32_t(it / Q), qi = uint32_t(it % Q);
+        const uint32_t n = min(rcount[qi], rcap);
+        if (c * 32 >= n) continue;  // (uniform)
+        const uint32_t nrc = min(32u, n - c * 32);
+        const uint32_t* rl = rr + int64_t(qi) * rcap + c * 32;
+        const bool rv = uint32_t(l32) < nrc;
+        const uint32_t pos = rv ? rl[l32] : 0u;
+        bool small = false;
+        if (rv) {
+            uint32_t lo = 0, hi = C - 1;  // the list of pos: the last l with roff[l] <= pos
+            while (lo < hi) {
+                const uint32_t mid = (lo + hi + 1) >> 1;
+                if (roff[mid] <= pos) lo = mid;
+                else hi = mid - 1;
+            }
+            small = qcnt[lo] <= kSmallListQueries;
+        }
+        // lanes 32..63 repeat rows 0..31: the low half of each ballot is the chunk's rows
+        const uint32_t smask = uint32_t(__ballot(rv && small));
+        const uint32_t bmask = uint32_t(__ballot(rv && !small));
+        const float* qrow = q + int64_t(qi) * D;
+        uint32_t* ko = rkey + int64_t(qi) * rcap + c * 32;
+        uint32_t* io = rid + int64_t(qi) * rcap + c * 32;
+        if (smask) {
+            const uint32_t p0 = uint32_t(__shfl(int(pos), j)), p1 = uint32_t(__shfl(int(pos), 16 + j));
+            uint32_t keys[8];
+            small_keys32(j == 0 ? qrow : nullptr, uint32_t(j) < nrc ? x + int64_t(p0) * D : nullptr,
+                         uint32_t(16 + j) < nrc ? x + int64_t(p1) * D : nullptr, D, lane, keys);
+            if (j == 0) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t m = uint32_t(16 * (i >> 2) + 4 * g + (i & 3));
+                    if ((smask >> m) & 1u) {
+                        ko[m] = keys[i];
+                        io[m] = ids[rl[m]];
+                    }
+                }
+            }
+        }
+        if (bmask) {
+            uint32_t keys[16];
+            f32_block_keys<true>(l32 == 0 ? qrow : nullptr, rv ? x + int64_t(pos) * D : nullptr, D, int(OP_L2SQ), lane,
+                                 keys);
+            if (l32 == 0) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t m = uint32_t(8 * (i >> 2) + 4 * hh + (i & 3));
+                    if ((bmask >> m) & 1u) {
+                        ko[m] = keys[i];
+                        io[m] = ids[rl[m]];
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Exact top-k, on the device, of the queries listed in fb (their candidates outgrew a list):
+// their probed lists walked with the arithmetic of the kernel that scans each list.
+va_status ivf_fallback(va_context* ctx, const va_ivf* ivf, const float* queries, const DevPlan& dp, uint32_t np,
+                       const FbArgs& fb, const SelectArgs& base) {
+    VA_CHECK_STATUS(fb_init(ctx, fb));
+    FbIvf v;
+    v.q = queries;
+    v.x = ivf->list_vectors;
+    v.ids = ivf->ids;
+    v.roff = ivf->offsets;
+    v.P = dp.P;
+    v.qcnt = dp.qcnt;
+    v.np = np;
+    v.D = ivf->D;
+    v.tmax = std::max<uint32_t>(1, (ivf->max_len + 31) / 32);
+    v.small_ok = dp.small_ok;
+    const bool vec = ivf->D % 4 == 0 && (reinterpret_cast<uintptr_t>(queries) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(ivf->list_vectors) & 15) == 0;
+    for (int pass = 0; pass < kFbPasses; ++pass) {
+        if (vec)
+            fb_ivf_pass_kernel<true><<<dim3(kFbGrid), dim3(256), 0, ctx->stream>>>(v, fb, pass);
+        else
+            fb_ivf_pass_kernel<false><<<dim3(kFbGrid), dim3(256), 0, ctx->stream>>>(v, fb, pass);
+        VA_CHECK_LAUNCH(ctx);
+    }
+    return fb_select(ctx, fb, base, 32);
+}
+
 // A list takes 16-query tiles when few queries probe it (decided once per search from the
 // full probe lists, so every pass of the search scans the list with the same kernel).  Needs
 // whole, aligned 16-byte groups (D % 4 == 0) and 32-bit byte offsets within a tile.
@@ -634,6 +1109,186 @@ bool small_tiles_ok(const va_ivf* ivf, const float* q) {
     return VA_IVF_SMALL && ivf->D % 4 == 0 && (reinterpret_cast<uintptr_t>(q) & 15) == 0 &&
            (reinterpret_cast<uintptr_t>(ivf->list_vectors) & 15) == 0 &&
            uint64_t(ivfs::TN) * ivf->D * 4 + 16 <= 0x7FFFFFF0ull;
+}
+// The screened list scan serves an index with an fp16 shadow whose lists can take the 16-query
+// tiles (their keys are replayed in the rerank), unless VA_OPT_SCREEN turns it off.
+bool ivf_screen_applies(const va_context* ctx, const va_ivf* ivf, const float* q) {
+    return ctx->opt_screen != 1 && ivf->shadow && ivf->norms && small_tiles_ok(ivf, q);
+}
+
+// The IVF list scan with the fp16 screen (the same steps as the flat screened scan, over the
+// device plan's list tiles):
+//   prep    : queries -> scaled fp16 + {|q|^2, |q|, 2^-scale, c0q};
+//   sample  : every pair of each probed list's sample prefix as an interval; tau_q = the k-th
+//             smallest upper bound (>= the k-th fp32 key of the probed lists);
+//   screen  : the pairs whose interval can reach below tau_q, as intervals;
+//   bound   : U_q = k-th smallest upper bound among them (>= the k-th fp32 key again);
+//   compact : the rows whose lower bound is <= U_q (they hold the fp32 top-k);
+//   rerank  : their exact fp32 keys, with each list's fp32 arithmetic, and their ids;
+//   select  : exact (key, id) top-k.  Overflowed queries take the device fallback.
+va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t Q,
+                            const uint32_t* probes, uint32_t np, uint32_t k, uint32_t* out_idx, float* out_dist) {
+    const uint32_t C = ivf->C, D = ivf->D, Dp = shadow_pitch(D);
+    const uint32_t npc = std::min(np, C);
+    const uint64_t cap_s = std::max<uint64_t>(1, ivf->top_sample[npc]);
+    // The screen's candidates are the fp32 scan's (about 64 x k per query) plus the rows within
+    // the bound's width of tau_q, several times as many on long lists (configs[4]: up to ~16,000
+    // for k = 10 against ~640 exact); the capacity is the fp32 scan's plus 7x it (at most 16,384
+    // of it per 7): queries that outgrow it take the device fallback.
+    const uint64_t cap32 = std::max<uint64_t>(3ull * k, uint64_t(k) + 32) * kIvfSampleRate + 1024;
+    uint64_t cap = ctx->opt_candidate_cap ? ctx->opt_candidate_cap : cap32 + 7 * std::min<uint64_t>(cap32, 16384);
+    cap = std::max<uint64_t>(1, std::min<uint64_t>(cap, ivf->top_rows[npc]));
+    const uint64_t cand = std::max(cap_s, cap);
+    const uint64_t rcap = std::max<uint64_t>(
+        1, std::min<uint64_t>(ivf->top_rows[npc], (std::max<uint64_t>(2ull * k + 256, cap / 4) + 127) / 128 * 128));
+    const uint64_t pairs = uint64_t(Q) * np;
+    const uint32_t id_span = uint32_t(std::min<uint64_t>(ivf->id_end, 0xFFFFFFFFull));
+    const Bound bnd = make_bound(D);
+
+    Scratch s(ctx);
+    const size_t q4 = Scratch::round(uint64_t(Q) * 4);
+    const size_t need = q4 * 6 + Scratch::round(256) + Scratch::round(uint64_t(Q) * 16) +
+                        Scratch::round(uint64_t(Q) * Dp * 2) + Scratch::round(pairs * 4) * 2 +
+                        Scratch::round(uint64_t(C) * 4) * 2 + Scratch::round((uint64_t(C) + 1) * 4) +
+                        Scratch::round(uint64_t(2 * kGroups) * C * 4) +
+                        Scratch::round(uint64_t(2 * kGroups) * (uint64_t(C) + 1) * 4) +
+                        Scratch::round(uint64_t(Q) * cand * 4) * 3 + Scratch::round(uint64_t(Q) * rcap * 4) * 3 +
+                        fb_bytes(Q, id_span, k, ivf->N);
+    VA_CHECK_STATUS(s.reserve(need));
+    uint32_t* thr = s.carve<uint32_t>(Q);
+    uint32_t* cnt = s.carve<uint32_t>(Q);
+    uint32_t* ubound = s.carve<uint32_t>(Q);
+    uint32_t* rcount = s.carve<uint32_t>(Q);
+    uint32_t* ovf_rows = s.carve<uint32_t>(Q);
+    uint32_t* ovf_cnt = s.carve<uint32_t>(64);
+    float4* qinfo = s.carve<float4>(Q);
+    float* qerr = s.carve<float>(Q);
+    _Float16* qh = s.carve<_Float16>(uint64_t(Q) * Dp);
+    DevPlan dp;
+    dp.probes = probes;
+    dp.Q = Q;
+    dp.np = np;
+    dp.C = C;
+    dp.roff = ivf->offsets;
+    dp.small_ok = 1;
+    dp.screen = 1;
+    dp.P = s.carve<uint32_t>(pairs);
+    dp.qlist = s.carve<uint32_t>(pairs);
+    dp.qcnt = s.carve<uint32_t>(C);
+    dp.qfill = s.carve<uint32_t>(C);
+    dp.qoff = s.carve<uint32_t>(uint64_t(C) + 1);
+    dp.counts = s.carve<uint32_t>(uint64_t(2 * kGroups) * C);
+    dp.pre = s.carve<uint32_t>(uint64_t(2 * kGroups) * (uint64_t(C) + 1));
+    float* cdot = s.carve<float>(uint64_t(Q) * cand);  // becomes the keys of the upper bounds
+    uint32_t* clo = s.carve<uint32_t>(uint64_t(Q) * cand);
+    uint32_t* cpos = s.carve<uint32_t>(uint64_t(Q) * cand);
+    uint32_t* rr = s.carve<uint32_t>(uint64_t(Q) * rcap);
+    uint32_t* rkey = s.carve<uint32_t>(uint64_t(Q) * rcap);
+    uint32_t* rid = s.carve<uint32_t>(uint64_t(Q) * rcap);
+    FbArgs fb = fb_carve(s, Q, id_span, k, ivf->N);
+    fb.n_rows = ovf_cnt;
+    fb.rows = ovf_rows;
+    uint32_t* chi = reinterpret_cast<uint32_t*>(cdot);
+    auto bounds = [&](uint64_t cp) -> va_status {
+        const uint32_t bx = uint32_t(std::min<uint64_t>(4, (cp + 255) / 256));
+        ivf_bound_kernel<<<dim3(bx, Q), dim3(256), 0, ctx->stream>>>(make_bound_v(D), qinfo, qerr, ivf->norms, cdot,
+                                                                     cpos, clo, cnt, uint32_t(cp));
+        VA_CHECK_LAUNCH(ctx);
+        return VA_OK;
+    };
+
+    ScanPhaseMarks pm(ctx);
+    ctx->last_scan = va_scan_timings{};
+    VA_CHECK_STATUS(pm.mark(0));
+    // ---- 0. plan and queries --------------------------------------------------------------------
+    VA_CHECK_STATUS(plan_on_device(ctx, dp));
+    VA_CHECK_STATUS(screen_prepare_queries(ctx, queries, Q, D, qh, qinfo, bnd.c0, qerr));
+    Ivf16Args a;
+    a.qh = qh;
+    a.qinfo = qinfo;
+    a.qerr = qerr;
+    a.xh = ivf->shadow;
+    a.xn = ivf->norms;
+    a.Dp = Dp;
+    a.bnd = make_bound_v(D);
+    a.thr = thr;
+    a.cnt = cnt;
+    a.cand_dot = cdot;
+    a.cand_pos = cpos;
+    // ---- 1. sample: tau_q = k-th smallest upper bound of the sampled pairs ----------------------
+    VA_CHECK_STATUS(fill_u32(ctx, thr, Q, 0xFFFFFFFFu));
+    VA_CHECK_STATUS(fill_u32(ctx, cnt, Q, 0));
+    a.cap = uint32_t(cap_s);
+    VA_CHECK_STATUS(run_screen_pass(ctx, dp, 0, a));
+    VA_CHECK_STATUS(bounds(cap_s));
+    {
+        SelectArgs sel;
+        sel.keys = chi;
+        sel.ids = cpos;
+        sel.counts = cnt;
+        sel.ld = int64_t(cap_s);
+        sel.n = uint32_t(cap_s);
+        sel.rows = Q;
+        sel.k = k;
+        sel.out_kth = thr;
+        VA_CHECK_STATUS(launch_select(ctx, sel));
+    }
+    // ---- 2. screen, 3. U_q (overflowed queries are listed) ---------------------------------------
+    VA_CHECK_STATUS(fill_u32(ctx, cnt, Q, 0));
+    VA_CHECK_STATUS(fill_u32(ctx, ovf_cnt, 2, 0));
+    a.cap = uint32_t(cap);
+    VA_CHECK_STATUS(pm.mark(1));
+    VA_CHECK_STATUS(run_screen_pass(ctx, dp, 1, a));
+    VA_CHECK_STATUS(pm.mark(2));
+    VA_CHECK_STATUS(bounds(cap));
+    {
+        SelectArgs sel;
+        sel.keys = chi;
+        sel.ids = cpos;
+        sel.counts = cnt;
+        sel.ld = int64_t(cap);
+        sel.n = uint32_t(cap);
+        sel.rows = Q;
+        sel.k = k;
+        sel.out_kth = ubound;
+        sel.overflow_count = ovf_cnt;
+        sel.overflow_rows = ovf_rows;
+        VA_CHECK_STATUS(launch_select(ctx, sel));
+    }
+    // ---- 4. rerank lists, 5. exact keys ----------------------------------------------------------
+    VA_CHECK_STATUS(screen_compact(ctx, cnt, clo, cpos, ubound, uint32_t(cap), Q, rr, rcount, uint32_t(rcap), ovf_cnt,
+                                   ovf_rows));
+    {
+        const uint64_t items = uint64_t(Q) * ((rcap + 31) / 32);
+        const uint32_t blocks = uint32_t(std::min<uint64_t>(2048, (items + 3) / 4));
+        ivf_rerank_kernel<<<dim3(blocks), dim3(256), 0, ctx->stream>>>(queries, ivf->list_vectors, ivf->ids,
+                                                                       ivf->offsets, C, dp.qcnt, D, rr, rcount,
+                                                                       uint32_t(rcap), Q, rkey, rid);
+        VA_CHECK_LAUNCH(ctx);
+    }
+    // ---- 6. exact (key, id) top-k, 7. overflowed queries -----------------------------------------
+    SelectArgs base;
+    base.k = k;
+    base.out_idx = out_idx;
+    base.out_f = out_dist;
+    {
+        SelectArgs sel = base;
+        sel.keys = rkey;
+        sel.ids = rid;
+        sel.counts = rcount;
+        sel.ld = int64_t(rcap);
+        sel.n = uint32_t(rcap);
+        sel.rows = Q;
+        VA_CHECK_STATUS(launch_select(ctx, sel));
+    }
+    ctx->last_scan.scan_launches = iv16::kGroupsUsed;
+    ctx->last_scan.candidate_cap = uint32_t(cap);
+    ctx->last_scan.screened = 1;
+    VA_CHECK_STATUS(pm.count_sum(rcount, Q));
+    VA_CHECK_STATUS(pm.count_overflow(ovf_cnt));
+    VA_CHECK_STATUS(pm.mark(3));
+    VA_CHECK_STATUS(ivf_fallback(ctx, ivf, queries, dp, np, fb, base));
+    return pm.finish(true, true);
 }
 }  // namespace
 }  // namespace va
@@ -693,7 +1348,10 @@ va_status va_ivf_build(va_context* ctx, const float* centroids, uint32_t num_cen
     ivf->id_end = num_vectors;
     va::gather_rows<<<dim3(std::min<uint32_t>(num_vectors, 65536)), dim3(256), 0, ctx->stream>>>(
         x, ivf->ids, num_vectors, dim, ivf->list_vectors);
-    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(ctx->stream) != hipSuccess)
+    if (hipGetLastError() != hipSuccess) return cleanup(va::fail(ctx, VA_ERR_HIP, "va_ivf_build: gather failed"));
+    st = va::make_list_shadow(ctx, ivf->list_vectors, num_vectors, dim, &ivf->shadow, &ivf->norms);
+    if (st != VA_OK) return cleanup(st);
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess)
         return cleanup(va::fail(ctx, VA_ERR_HIP, "va_ivf_build: gather failed"));
     *out = ivf;
     return VA_OK;
@@ -709,7 +1367,7 @@ va_status va_ivf_add(va_context* ctx, va_ivf* ivf, const float* x, uint32_t num_
     va::DeviceGuard g(ctx->device);
     const uint32_t C = ivf->C, D = ivf->D, No = ivf->N, n = num_vectors, Nn = No + n;
     struct Bufs {
-        void* p[7] = {};
+        void* p[9] = {};
         ~Bufs() {
             for (void* q : p)
                 if (q) (void)hipFree(q);
@@ -744,6 +1402,14 @@ va_status va_ivf_add(va_context* ctx, va_ivf* ivf, const float* x, uint32_t num_
     VA_CHECK_LAUNCH(ctx);
     va::ivf_new_offsets<<<dim3((C + 1 + 255) / 256), dim3(256), 0, ctx->stream>>>(ivf->offsets, pre, C, offs);
     VA_CHECK_LAUNCH(ctx);
+    _Float16* sh = nullptr;
+    float2* nr = nullptr;
+    {
+        const va_status st = va::make_list_shadow(ctx, vecs, Nn, D, &sh, &nr);
+        b.p[7] = sh;
+        b.p[8] = nr;
+        VA_CHECK_STATUS(st);
+    }
     std::vector<uint32_t> h(C + 1);
     VA_CHECK_HIP(ctx, hipMemcpyAsync(h.data(), offs, size_t(C + 1) * 4, hipMemcpyDeviceToHost, ctx->stream));
     VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -751,9 +1417,13 @@ va_status va_ivf_add(va_context* ctx, va_ivf* ivf, const float* x, uint32_t num_
     b.p[4] = ivf->list_vectors;
     b.p[5] = ivf->ids;
     b.p[6] = ivf->offsets;
+    b.p[7] = ivf->shadow;
+    b.p[8] = ivf->norms;
     ivf->list_vectors = vecs;
     ivf->ids = ids;
     ivf->offsets = offs;
+    ivf->shadow = sh;
+    ivf->norms = nr;
     ivf->h_offsets = std::move(h);
     ivf->refresh_bounds();
     ivf->id_end = std::max<uint64_t>(ivf->id_end, uint64_t(first_id) + n);
@@ -769,6 +1439,8 @@ va_status va_ivf_destroy(va_ivf* ivf) {
     if (ivf->list_vectors) (void)hipFree(ivf->list_vectors);
     if (ivf->ids) (void)hipFree(ivf->ids);
     if (ivf->offsets) (void)hipFree(ivf->offsets);
+    if (ivf->shadow) (void)hipFree(ivf->shadow);
+    if (ivf->norms) (void)hipFree(ivf->norms);
     if (ivf->probe_buf) (void)hipFree(ivf->probe_buf);
     delete ivf;
     return VA_OK;
@@ -812,6 +1484,8 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
     VA_REQUIRE(ctx, k > 0 && k <= VA_MAX_K, "k must be in [1, %u], got %u", VA_MAX_K, k);
     VA_REQUIRE(ctx, nprobe >= 1, "nprobe must be at least 1, got %u", nprobe);
     va::DeviceGuard g(ctx->device);
+    if (va::ivf_screen_applies(ctx, ivf, queries))
+        return va::ivf_scan_screened(ctx, ivf, queries, num_queries, probes, nprobe, k, out_idx, out_dist);
     const uint32_t Q = num_queries, C = ivf->C, np = nprobe;
 
     // ---- sizes from the list lengths alone (nothing is read back) --------------------------------
@@ -859,6 +1533,9 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
     fb.n_rows = ovf_cnt;
     fb.rows = ovf_rows;
 
+    va::ScanPhaseMarks pm(ctx);
+    ctx->last_scan = va_scan_timings{};
+    VA_CHECK_STATUS(pm.mark(0));
     // ---- 0. plan: the queries of every probed list, tile prefixes per group and pass ------------
     VA_CHECK_STATUS(va::plan_on_device(ctx, dp));
     // ---- 1. sample pass: every sampled candidate, then tau = k-th smallest ----------------------
@@ -880,7 +1557,9 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
     // ---- 2. full pass with the thresholds, 3. exact selection -----------------------------------
     VA_CHECK_STATUS(va::fill_u32(ctx, cnt, Q, 0));
     VA_CHECK_STATUS(va::fill_u32(ctx, ovf_cnt, 1, 0));
+    VA_CHECK_STATUS(pm.mark(1));
     VA_CHECK_STATUS(va::run_planned_pass(ctx, dp, 1, queries, ivf, thr, cnt, ckey, cid, uint32_t(cap)));
+    VA_CHECK_STATUS(pm.mark(2));
     va::SelectArgs base;
     base.k = k;
     base.out_idx = out_idx;
@@ -897,29 +1576,13 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
         a.overflow_rows = ovf_rows;
         VA_CHECK_STATUS(va::launch_select(ctx, a));
     }
+    ctx->last_scan.scan_launches = va::kGroups;
+    ctx->last_scan.candidate_cap = uint32_t(cap);
+    VA_CHECK_STATUS(pm.count_overflow(ovf_cnt));
+    VA_CHECK_STATUS(pm.mark(3));
     // ---- 4. queries whose candidates outgrew cap: exact top-k on the device ----------------------
-    VA_CHECK_STATUS(va::fb_init(ctx, fb));
-    va::FbIvf v;
-    v.q = queries;
-    v.x = ivf->list_vectors;
-    v.ids = ivf->ids;
-    v.roff = ivf->offsets;
-    v.P = dp.P;
-    v.qcnt = dp.qcnt;
-    v.np = np;
-    v.D = ivf->D;
-    v.tmax = std::max<uint32_t>(1, (ivf->max_len + 31) / 32);
-    v.small_ok = dp.small_ok;
-    const bool vec = ivf->D % 4 == 0 && (reinterpret_cast<uintptr_t>(queries) & 15) == 0 &&
-                     (reinterpret_cast<uintptr_t>(ivf->list_vectors) & 15) == 0;
-    for (int pass = 0; pass < va::kFbPasses; ++pass) {
-        if (vec)
-            va::fb_ivf_pass_kernel<true><<<dim3(va::kFbGrid), dim3(256), 0, ctx->stream>>>(v, fb, pass);
-        else
-            va::fb_ivf_pass_kernel<false><<<dim3(va::kFbGrid), dim3(256), 0, ctx->stream>>>(v, fb, pass);
-        VA_CHECK_LAUNCH(ctx);
-    }
-    return va::fb_select(ctx, fb, base, 32);
+    VA_CHECK_STATUS(va::ivf_fallback(ctx, ivf, queries, dp, np, fb, base));
+    return pm.finish(true, true);
 }
 
 va_status va_ivf_search(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,

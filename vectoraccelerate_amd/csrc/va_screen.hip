@@ -106,7 +106,7 @@ __device__ __forceinline__ PreTest pretest_consts(const ScreenArgs& a, float4 in
 // ---- query preparation: one wave per query ------------------------------------------------
 __global__ __launch_bounds__(256) void screen_prep_kernel(const float* __restrict__ q, int64_t ldq, uint32_t Q,
                                                           uint32_t D, uint32_t Dp, _Float16* __restrict__ qh,
-                                                          float4* __restrict__ qinfo, float c0) {
+                                                          float4* __restrict__ qinfo, float c0, float* __restrict__ qerr) {
     const uint32_t qi = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (qi >= Q) return;
@@ -131,10 +131,22 @@ __global__ __launch_bounds__(256) void screen_prep_kernel(const float* __restric
     const int sc = query_scale_exponent(m, bad);
     const float scale = ldexpf(1.0f, sc);
     _Float16* out = qh + int64_t(qi) * Dp;
-    for (uint32_t d = lane; d < Dp; d += 64) out[d] = d < D ? _Float16(row[d] * scale) : _Float16(0.0f);
+    float es = 0.0f;  // squared norm of the rounding error of the scaled query (differences exact)
+    for (uint32_t d = lane; d < Dp; d += 64) {
+        const float v = d < D ? row[d] * scale : 0.0f;
+        const _Float16 h = _Float16(v);
+        out[d] = h;
+        const float e = float(h) - v;
+        es = fmaf(e, e, es);
+    }
+    if (qerr) {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) es += __shfl_xor(es, off);
+    }
     if (lane == 0) {
         const float inv = ldexpf(1.0f, -sc);
         qinfo[qi] = make_float4(ss, sqrtf(ss), inv, c0 * 0x1p-25f * inv);
+        if (qerr) qerr[qi] = err_norm_up(es, D) * inv;
     }
 }
 
@@ -730,13 +742,13 @@ __global__ __launch_bounds__(256, 1) void screen16_kernel(ScreenArgs a) {
 // and their squared norms in fp32 (one wave per row) ----------------------------------------------
 __global__ __launch_bounds__(256) void shadow_kernel(const float* __restrict__ x, int64_t ldx, uint32_t N, uint32_t D,
                                                      uint32_t Dp, _Float16* __restrict__ xh, int64_t ldh,
-                                                     float* __restrict__ xn, int vec) {
+                                                     float* __restrict__ xn, int vec, float2* __restrict__ xne) {
     const uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (r >= N) return;
     const float* row = x + int64_t(r) * ldx;
     _Float16* out = xh + int64_t(r) * ldh;
-    float ss = 0.0f;
+    float ss = 0.0f, es = 0.0f;
     for (uint32_t d0 = 0; d0 < Dp; d0 += 256) {
         const uint32_t d = d0 + 4u * uint32_t(lane);
         if (d >= Dp) break;
@@ -750,11 +762,22 @@ __global__ __launch_bounds__(256) void shadow_kernel(const float* __restrict__ x
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) ss = fmaf(v[e], v[e], ss);
-        *reinterpret_cast<h4v*>(out + d) = __builtin_convertvector(v, h4v);
+        const h4v h = __builtin_convertvector(v, h4v);
+        *reinterpret_cast<h4v*>(out + d) = h;
+        const f32x4v dv = __builtin_convertvector(h, f32x4v) - v;  // exact (inf past the fp16 range)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) es = fmaf(dv[e], dv[e], es);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-    if (lane == 0) xn[r] = ss;
+    if (xne) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) es += __shfl_xor(es, o);
+    }
+    if (lane == 0) {
+        if (xn) xn[r] = ss;
+        if (xne) xne[r] = make_float2(ss, err_norm_up(es, D));
+    }
 }
 
 // ---- exact intervals of the screened pairs -----------------------------------------------------
@@ -912,12 +935,43 @@ bool offsets_fit(uint64_t ldx, uint32_t D) {
 
 uint32_t shadow_pitch(uint32_t D) { return padded_dim(D); }
 
-va_status build_shadow(va_context* ctx, const float* x, uint32_t N, uint32_t D, _Float16* shadow, float* norms) {
+va_status build_shadow(va_context* ctx, const float* x, uint32_t N, uint32_t D, _Float16* shadow, float* norms,
+                       float2* norm_err) {
     if (N == 0) return VA_OK;
     const uint32_t Dp = padded_dim(D);
     const int vec = (D % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
     shadow_kernel<<<dim3((N + 3) / 4), dim3(256), 0, ctx->stream>>>(x, int64_t(D), N, D, Dp, shadow, int64_t(Dp),
-                                                                   norms, vec);
+                                                                   norms, vec, norm_err);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
+va_status screen_prepare_queries(va_context* ctx, const float* q, uint32_t Q, uint32_t D, _Float16* qh,
+                                 float4* qinfo, float c0, float* qerr) {
+    if (Q == 0) return VA_OK;
+    screen_prep_kernel<<<dim3((Q + 3) / 4), dim3(256), 0, ctx->stream>>>(q, int64_t(D), Q, D, padded_dim(D), qh, qinfo,
+                                                                       c0, qerr);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
+va_status screen_list_bounds(va_context* ctx, const ScreenBound& b, const float4* qinfo, float* dot, float* xx,
+                             const uint32_t* cnt, uint32_t cap, uint32_t Q) {
+    ScreenArgs a;
+    a.op = b.op;
+    a.c1 = b.c1;
+    a.cn = b.cn;
+    a.c0x = b.c0x;
+    a.kabs = b.kabs;
+    a.qinfo = qinfo;
+    return launch_bounds(ctx, a, dot, nullptr, xx, cnt, cap, int64_t(cap), Q);
+}
+
+va_status screen_compact(va_context* ctx, const uint32_t* cnt, const uint32_t* cand_lo, const uint32_t* cand_id,
+                         const uint32_t* bound, uint32_t cap, uint32_t Q, uint32_t* rr, uint32_t* rcount, uint32_t rcap,
+                         uint32_t* ovf_cnt, uint32_t* ovf_rows) {
+    screen_compact_kernel<<<dim3(Q), dim3(256), 0, ctx->stream>>>(cnt, cand_lo, cand_id, bound, cap, rr, rcount, rcap,
+                                                                 ovf_cnt, ovf_rows, ovf_cnt + 1);
     VA_CHECK_LAUNCH(ctx);
     return VA_OK;
 }
@@ -991,7 +1045,7 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
 
     // ---- 1. queries -> scaled fp16 ---------------------------------------------------------
     screen_prep_kernel<<<dim3((Q + 3) / 4), dim3(256), 0, ctx->stream>>>(in.q, int64_t(D), Q, D, Dp, qh, qinfo,
-                                                                       bnd.c0);
+                                                                       bnd.c0, nullptr);
     VA_CHECK_LAUNCH(ctx);
 
     ScreenArgs sa;

@@ -158,6 +158,92 @@ inline Bound make_bound(uint32_t D) {
     return b;
 }
 
+// ---- the L2^2 bound with measured rounding errors ---------------------------------------------
+// When each vector's fp16 rounding error is known (eq >= |q~ - q| for the query, unscaled, and
+// ex >= |x~ - x| for the row), the fp16 part of the bound is the exact expansion
+//     |q~.x~ - q.x| = |dq.x + q.dx + dq.dx| <= eq |x| + |q| ex + eq ex
+// instead of its worst case 2u |q||x| (typical rounding errors are about 0.4u of the norm).  The
+// fp32 accumulation of the exact fp16 products adds gd |q~||x~| <= gd (|q| + eq)(|x| + ex), the
+// fp32 scan's own dot g2d |q||x| (any order, products rounded), and cn (|q|^2 + |x|^2) covers the
+// norms computed in two orders and the key formula, as in screen_bounds.  The result is linear in
+// the row's |x|^2, |x| and ex, so the pre-test keeps its form with one more term.
+struct BoundV {
+    float cn, gd, g2d;
+};
+inline BoundV make_bound_v(uint32_t D) {
+    const double up = std::ldexp(1.0, -23);
+    auto gam = [&](double n) { return n * up / (1.0 - n * up); };
+    const double slack = 1.0625;
+    BoundV b;
+    b.cn = float(slack * (2 * gam(D) + std::ldexp(1.0, -20)));
+    b.gd = float(slack * gam(D));
+    b.g2d = float(slack * gam(2.0 * D));
+    return b;
+}
+
+// An upper bound of the norm of a rounding-error vector from ss, the fp32 sum (any order) of the
+// squares of its D entries (each entry, the difference of a float and its fp16 image, is exact in
+// fp32): the sum's and the squares' roundings, squares lost to underflow, the sqrt's rounding.
+VA_HD inline float err_norm_up(float ss, uint32_t D) {
+    return sqrtf(fmaf(ss, 1.0f + float(D) * 0x1p-22f, 0x1p-110f)) * (1.0f + 0x1p-20f);
+}
+
+// coefficients of |x| and of ex in the bound of |2 (dot16 - dot32)|; the factor 1 + 2^-9 covers
+// their own rounding and the relative error of the fp32 norms |q|, |x| they multiply
+VA_HD inline float boundv_nx(const BoundV& b, float nq, float eq) {
+    return 2.0f * fmaf(b.gd, nq + eq, fmaf(b.g2d, nq, eq)) * (1.0f + 0x1p-9f);
+}
+VA_HD inline float boundv_ex(const BoundV& b, float nq, float eq) {
+    return 2.0f * (1.0f + b.gd) * (nq + eq) * (1.0f + 0x1p-9f);
+}
+
+// The interval [lo, hi] of the fp32 L2^2 key from the fp16 dot (already unscaled); false when the
+// pair cannot be bounded (non-finite dot, query or row outside the fp16 range).
+VA_HD inline bool screen_bounds_v(const BoundV& b, float dot, float qq, float nq, float eq, float xx, float nx,
+                                  float ex, float& lo, float& hi) {
+    if (!(fabsf(dot) <= FLT_MAX) || !(eq <= FLT_MAX) || !(ex <= FLT_MAX) || !(qq <= FLT_MAX) || !(xx <= FLT_MAX))
+        return false;
+    const float v = qq + xx - 2.0f * dot;
+    const float s = v < 0.0f ? 0.0f : v;
+    float e = fmaf(b.cn, qq + xx, fmaf(boundv_nx(b, nq, eq), nx, boundv_ex(b, nq, eq) * ex));
+    e = fmaf(fmaf(0x1p-21f, fabsf(s), e), 1.0f + 0x1p-20f, 0x1p-126f);  // rounding of s and e
+    if (!(e <= FLT_MAX) || !(fabsf(s) <= FLT_MAX)) return false;
+    lo = fmaxf(s - e, 0.0f);
+    hi = s + e;
+    return true;
+}
+
+// The pre-test of screen_bounds_v: a pair whose lower bound can be <= tau satisfies
+//     acc >= A |x|^2 + B |x| + E ex + C      (acc = the scaled fp16 dot, sig = 2^scale = 1/inv)
+// (from 2 dot >= |q|^2 + |x|^2 - e - tau, with the rounding room 2^-21 |s| <= 2^-21 (|tau| + e)
+// of a pair at the boundary folded into e), each term loosened by 2^-18 for the fp32 rounding of
+// the constants and of the kernel's fma chain; written !(acc < rhs), so a NaN rhs (a flagged row)
+// passes.  Thresholds the form cannot serve give C = -inf (every pair passes).
+struct PreTestV {
+    float A, B, E, C;
+};
+VA_HD inline PreTestV pretest_v(const BoundV& b, float qq, float nq, float eq, float inv, uint32_t thr_key) {
+    const PreTestV all = {0.0f, 0.0f, 0.0f, -INFINITY};
+    if (thr_key >= 0xFFFFFFFEu) return all;  // the NaN key (or no threshold): every key passes
+    const float tau = float_of_key(thr_key);
+    if (!(fabsf(tau) <= FLT_MAX) || !(qq <= FLT_MAX) || !(eq <= FLT_MAX)) return all;
+    const float sig = 1.0f / inv;  // 2^scale, exact
+    const float w = 1.0f + 0x1p-19f;
+    const float r = 0x1p-18f;
+    const float a1 = 1.0f - b.cn * w;
+    float A = sig * 0.5f * a1;
+    float B = -sig * 0.5f * w * boundv_nx(b, nq, eq);
+    float E = -sig * 0.5f * w * boundv_ex(b, nq, eq);
+    float C = sig * 0.5f * (a1 * qq - tau - w * 0x1p-21f * fabsf(tau) - 0x1p-125f);
+    A = A * (1.0f - r);
+    B = B - fabsf(B) * r;
+    E = E - fabsf(E) * r;
+    C = C - fabsf(C) * r - sig * (qq + fabsf(tau)) * 0x1p-21f;
+    if (!(fabsf(A) <= FLT_MAX) || !(fabsf(B) <= FLT_MAX) || !(fabsf(E) <= FLT_MAX) || !(fabsf(C) <= FLT_MAX))
+        return all;
+    return PreTestV{A, B, E, C};
+}
+
 // The power-of-two scale of a query (largest |entry| m, any entry non-finite: bad): 2^sc puts
 // the largest entry in [2^14, 2^15), at most 2^40 so the pre-test constants stay finite.
 VA_HD inline int query_scale_exponent(float m, bool bad) {
