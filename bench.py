@@ -68,6 +68,9 @@ COUNTERS_SCREEN = "profiles/counters__screen_filter__configs1_cosine_top100.txt"
 COUNTERS_FP32 = "profiles/counters__dist_gemm_filter__configs1_cosine_top100.txt"
 COUNTERS_I8 = "profiles/counters__i8_resq_filter__configs2_int8_top10.txt"
 COUNTERS_HAMMING = "profiles/counters__hamming_mfma_filter__configs3_binary_top100.txt"
+COUNTERS_IVF16 = {"64-query tiles": "profiles/counters__ivf16_wide64__configs4_ivfflat_top10.txt",
+                  "32-query tiles": "profiles/counters__ivf16_wide32__configs4_ivfflat_top10.txt",
+                  "16-query tiles": "profiles/counters__ivf16_narrow__configs4_ivfflat_top10.txt"}
 COUNTERS_IVF = {"2x2 tiles": "profiles/counters__ivf_list_scan_2x2__configs4_ivfflat_top10.txt",
                 "4x1 tiles": "profiles/counters__ivf_list_scan_4x1__configs4_ivfflat_top10.txt",
                 "16-query tiles": "profiles/counters__ivf_small_tiles__configs4_ivfflat_top10.txt"}
@@ -537,6 +540,7 @@ def run_c5(ctx, a, cpu: bool):
                                 if screened else "fp32 list scan"),
                      "algorithmic": f"fp16 shadow of the distinct probed lists + fp16 queries = {b16 / 1e9:.2f} GB "
                                     f"per search (fp32 rows: {b_min / 1e9:.2f} GB)",
+                     "counted": {name: counted(rel) for name, rel in COUNTERS_IVF16.items()},
                      "whole_search_fp32_equivalent_tflops": tflops,
                      "whole_search_fp32_mfma_frac": tflops / PEAK["fp32_mfma_tflops"],
                      "fp32_work": f"2QCD + 2D*sum|L_p| = {flops:.4g} FLOP"},

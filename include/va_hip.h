@@ -244,7 +244,9 @@ va_status va_hamming_topk(va_context* ctx, const uint32_t* query_codes, const ui
  * IVFStructure.findNearestCentroid, Index/Internal/IVFStructure.swift:292-307) and lay the
  * lists out in device CSR order with insertion order inside each list
  * (IVFStructure.prepareGPUStructure, IVFStructure.swift:347-467).  The index copies what it
- * needs; x and centroids may be freed afterwards.  Synchronises the context. */
+ * needs; x and centroids may be freed afterwards.  For dim % 4 == 0 it also keeps an fp16 copy
+ * of the list vectors (2 bytes per value + 8 per row), the input of the screened list scan.
+ * Synchronises the context. */
 va_status va_ivf_build(va_context* ctx, const float* centroids, uint32_t num_centroids, const float* x,
                        uint32_t num_vectors, uint32_t dim, va_ivf** out);
 va_status va_ivf_destroy(va_ivf* ivf);
@@ -263,7 +265,10 @@ va_status va_ivf_get_lists(va_context* ctx, const va_ivf* ivf, uint32_t* host_of
 va_status va_ivf_probe(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
                        uint32_t nprobe, uint32_t* probes);
 /* List scan over given probes + exact top-k over original row ids (L2^2).
- * Replaces IVFListSearchKernel / ivf_list_search (Metal/Shaders/IVFListSearch.metal:199-339). */
+ * Replaces IVFListSearchKernel / ivf_list_search (Metal/Shaders/IVFListSearch.metal:199-339).
+ * With the index's fp16 copy (and 16-byte aligned queries) the lists are screened on the fp16
+ * MFMA and the rows that can reach the top-k re-scored in fp32: the ids and distances are those
+ * of the fp32 list scan, bit for bit; VA_OPT_SCREEN = 1 runs the fp32 list scan alone. */
 va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
                       const uint32_t* probes, uint32_t nprobe, uint32_t k, uint32_t* out_idx, float* out_dist);
 /* Full IVF search = probe + scan.  Replaces IVFSearchPipeline.search
