@@ -155,6 +155,146 @@ __device__ inline void f32_block_keys(const float* qp, const float* xp, uint32_t
         }
 }
 
+// ---- the same keys on the VALU, one (query, row) pair per lane --------------------------------
+// Every element of v_mfma_f32_32x32x2_f32 and v_mfma_f32_16x16x4_f32 is formed by sequential
+// fmas in k order: d = fma(a_k1, b_k1, fma(a_k0, b_k0, c)) (measured on gfx950, bit for bit
+// against a correctly rounded fmaf on 1M cases: wide exponent ranges, cancellation, fp32
+// subnormal inputs and products, signed zeros, inf and NaN).  So the keys of the MFMA kernels
+// are reproduced exactly by a per-lane fmaf chain in the same element order, with every zero
+// step the kernels run (a zero fma turns a -0 into +0).  The query is wave-uniform (scalar
+// loads), each lane streams its own row (nullptr: a lane with no row, whose key is unused).
+
+// x[d .. d + 3] with zeros past D (VEC: D % 4 == 0 and 16-byte aligned rows)
+template <bool VEC>
+__device__ __forceinline__ fb_f32x4 valu_load4(const float* p, uint32_t d, uint32_t D) {
+    fb_f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (p && d < D) {
+        if (VEC) {
+            v = *reinterpret_cast<const fb_f32x4*>(p + d);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (d + e < D) v[e] = p[d + e];
+        }
+    }
+    return v;
+}
+
+// The chains consume a row in groups of 32 values (elements 32j .. 32j + 31, zeros past D):
+// xv[i] / qv[i] hold elements 32j + 4i .. + 3 of the row and of the query.
+
+// The distance GEMM's key (f32_block_keys): ceil(D / 16) stages of 16; in stage s, for g < 2 and
+// e < 4, the pair (16s + 8g + e, 16s + 8g + 4 + e); the squared norms as the two half-chains
+// (elements 8g + e and 8g + 4 + e of every stage), added.
+struct GemmChain {
+    float acc = 0.0f, xs0 = 0.0f, xs1 = 0.0f, qs0 = 0.0f, qs1 = 0.0f;
+    __device__ __forceinline__ void stage(const fb_f32x4 (&xv)[8], const fb_f32x4 (&qv)[8], int h) {
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float a = xv[4 * h + 2 * g][e], b = xv[4 * h + 2 * g + 1][e];
+                const float qa = qv[4 * h + 2 * g][e], qb = qv[4 * h + 2 * g + 1][e];
+                qs0 = fmaf(qa, qa, qs0);
+                qs1 = fmaf(qb, qb, qs1);
+                xs0 = fmaf(a, a, xs0);
+                xs1 = fmaf(b, b, xs1);
+                acc = fmaf(a, qa, acc);
+                acc = fmaf(b, qb, acc);
+            }
+        }
+    }
+    // group j of a row of D values (the GEMM runs exactly ceil(D / 16) stages)
+    __device__ __forceinline__ void group(const fb_f32x4 (&xv)[8], const fb_f32x4 (&qv)[8], uint32_t j, uint32_t D) {
+        stage(xv, qv, 0);
+        if (32 * j + 16 < D) stage(xv, qv, 1);
+    }
+    __device__ __forceinline__ uint32_t key(int op) const {
+        return key_of_float(apply_op(op, acc, qs0 + qs1, xs0 + xs1));
+    }
+};
+
+// ivf_small_kernel's key (small_keys32): ceil(D / 32) * 2 chunks of 16 (whole groups); in chunk c,
+// for e < 4 and g < 4, element 16c + 4g + e; the squared norms as four chains (g), combined
+// (x0 + x1) + (x2 + x3); L2^2 = |q|^2 + |x|^2 - 2 dot clamped at 0.
+struct SmallChain {
+    float acc = 0.0f;
+    float xs[4] = {0.0f, 0.0f, 0.0f, 0.0f}, qs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    __device__ __forceinline__ void group(const fb_f32x4 (&xv)[8], const fb_f32x4 (&qv)[8]) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    qs[g] = fmaf(qv[4 * h + g][e], qv[4 * h + g][e], qs[g]);
+                    xs[g] = fmaf(xv[4 * h + g][e], xv[4 * h + g][e], xs[g]);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) acc = fmaf(xv[4 * h + g][e], qv[4 * h + g][e], acc);
+        }
+    }
+    __device__ __forceinline__ uint32_t key() const {
+        const float qsum = (qs[0] + qs[1]) + (qs[2] + qs[3]);
+        const float xx = (xs[0] + xs[1]) + (xs[2] + xs[3]);
+        float d = qsum + xx - 2.0f * acc;
+        d = (d < 0.0f) ? 0.0f : d;
+        return key_of_float(d);
+    }
+};
+
+// Scores up to 64 rows (lane l: row id rid_of(l), valid_of(l)) against one wave-uniform query
+// with a VALU chain per lane.  The rows move in coalesced groups of 32 values: load instruction i
+// of a group brings rows 8i .. 8i + 7 (lane L: row 8i + L / 8, 16-byte chunk L % 8, whole 128-byte
+// lines), the wave's LDS slot (8 KiB, chunk c of row r at c ^ ((r >> 1) & 7): conflict-free
+// reads) turns them into rows, and lane l reads its own row's 32 values.  Groups j + 1 and j + 2
+// are in flight (registers) while group j computes.  feed(j, xv, qv) runs the lane's chain on
+// group j.  Needs D % 4 == 0 and 16-byte aligned rows and query.
+template <class Feed>
+__device__ inline void rows_through_lds(const float* q, const float* x, const uint32_t (&rid)[8],
+                                        const bool (&rvalid)[8], uint32_t D, fb_f32x4* slot, Feed&& feed) {
+    const int lane = threadIdx.x & 63;
+    const int ck = lane & 7;
+    const uint32_t ng = (D + 31) / 32;
+    fb_f32x4 ga[8], gb[8];
+    auto load = [&](uint32_t j, fb_f32x4(&g)[8]) {
+        const uint32_t d = 32 * j + 4 * uint32_t(ck);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            g[i] = valu_load4<true>(rvalid[i] ? x + int64_t(rid[i]) * D : nullptr, d, D);
+    };
+    auto stash = [&](const fb_f32x4(&g)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = 8 * i + (lane >> 3);
+            slot[r * 8 + (ck ^ ((r >> 1) & 7))] = g[i];
+        }
+    };
+    auto run = [&](uint32_t j) {
+        fb_f32x4 xv[8], qv[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            xv[m] = slot[lane * 8 + (m ^ ((lane >> 1) & 7))];
+            qv[m] = valu_load4<true>(q, 32 * j + 4 * m, D);  // (wave-uniform: scalar loads)
+        }
+        feed(j, xv, qv);
+    };
+    load(0, ga);
+    if (ng > 1) load(1, gb);
+    for (uint32_t j = 0; j < ng; j += 2) {
+        stash(ga);
+        if (j + 2 < ng) load(j + 2, ga);
+        run(j);
+        if (j + 1 >= ng) break;
+        stash(gb);
+        if (j + 3 < ng) load(j + 3, gb);
+        run(j + 1);
+    }
+}
+
 struct FbF32 {
     const float* q;
     int64_t ldq;

@@ -997,11 +997,12 @@ __global__ __launch_bounds__(256) void fb_ivf_pass_kernel(FbIvf v, FbArgs a, int
 }
 
 // ---- exact keys of the screened scan's rerank lists ------------------------------------------
-// One wave per (32-row chunk of a query's rerank list, query), persistent and chunk-major.  The
-// rows hold CSR positions; each row's key comes from the arithmetic of the kernel that scans its
-// list in the fp32 list scan (small_keys32 for lists probed by at most 16 queries, the distance
-// GEMM's block otherwise), and the row's id replaces its position.  A chunk that mixes the two
-// kinds runs both (every output element depends on its own row and query only).
+// One wave per (64-row chunk of a query's rerank list, query), persistent and chunk-major.  The
+// rows hold CSR positions; lane l scores row 64c + l on the VALU with the per-element sequence of
+// the kernel that scans its list in the fp32 list scan (SmallChain: ivf_small_kernel's, for lists
+// probed by at most 16 queries; GemmChain: the distance GEMM's, otherwise), so every key equals
+// the fp32 list scan's, and the row's id replaces its position.  The rows pass through the wave's
+// LDS slot in coalesced 128-byte lines (rows_through_lds).
 __global__ __launch_bounds__(256) void ivf_rerank_kernel(const float* __restrict__ q, const float* __restrict__ x,
                                                          const uint32_t* __restrict__ ids,
                                                          const uint32_t* __restrict__ roff, uint32_t C,
@@ -1009,20 +1010,31 @@ __global__ __launch_bounds__(256) void ivf_rerank_kernel(const float* __restrict
                                                          const uint32_t* __restrict__ rr,
                                                          const uint32_t* __restrict__ rcount, uint32_t rcap, uint32_t Q,
                                                          uint32_t* __restrict__ rkey, uint32_t* __restrict__ rid) {
-    const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5, j = lane & 15, g = lane >> 4;
-    const uint32_t nch = (rcap + 31) / 32;
+    __shared__ fb_f32x4 slots[4][64 * 8];
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nch = (rcap + 63) / 64;
     const uint64_t items = uint64_t(Q) * nch;
     const uint32_t nw = gridDim.x * 4;
-    for (uint64_t it = uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6); it < items; it += nw) {
+    for (uint64_t it = uint64_t(blockIdx.x) * 4 + wave; it < items; it += nw) {
         const uint32_t c = uint32_t(it / Q), qi = uint32_t(it % Q);
         const uint32_t n = min(rcount[qi], rcap);
-        if (c * 32 >= n) continue;  // (uniform)
-        const uint32_t nrc = min(32u, n - c * 32);
-        const uint32_t* rl = rr + int64_t(qi) * rcap + c * 32;
-        const bool rv = uint32_t(l32) < nrc;
-        const uint32_t pos = rv ? rl[l32] : 0u;
+        if (c * 64 >= n) continue;  // (uniform)
+        const uint32_t* rl = rr + int64_t(qi) * rcap + c * 64;
+        const uint32_t m = min(64u, n - c * 64);
+        uint32_t pos8[8];
+        bool rv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t r = uint32_t(8 * i + (lane >> 3));
+            rv[i] = r < m;
+            pos8[i] = rv[i] ? rl[r] : 0u;
+        }
+        // this lane's own row: its list decides the arithmetic
+        const bool mine = uint32_t(lane) < m;
+        const uint32_t pos = mine ? rl[lane] : 0u;
         bool small = false;
-        if (rv) {
+        if (mine) {
             uint32_t lo = 0, hi = C - 1;  // the list of pos: the last l with roff[l] <= pos
             while (lo < hi) {
                 const uint32_t mid = (lo + hi + 1) >> 1;
@@ -1031,42 +1043,16 @@ __global__ __launch_bounds__(256) void ivf_rerank_kernel(const float* __restrict
             }
             small = qcnt[lo] <= kSmallListQueries;
         }
-        // lanes 32..63 repeat rows 0..31: the low half of each ballot is the chunk's rows
-        const uint32_t smask = uint32_t(__ballot(rv && small));
-        const uint32_t bmask = uint32_t(__ballot(rv && !small));
-        const float* qrow = q + int64_t(qi) * D;
-        uint32_t* ko = rkey + int64_t(qi) * rcap + c * 32;
-        uint32_t* io = rid + int64_t(qi) * rcap + c * 32;
-        if (smask) {
-            const uint32_t p0 = uint32_t(__shfl(int(pos), j)), p1 = uint32_t(__shfl(int(pos), 16 + j));
-            uint32_t keys[8];
-            small_keys32(j == 0 ? qrow : nullptr, uint32_t(j) < nrc ? x + int64_t(p0) * D : nullptr,
-                         uint32_t(16 + j) < nrc ? x + int64_t(p1) * D : nullptr, D, lane, keys);
-            if (j == 0) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const uint32_t m = uint32_t(16 * (i >> 2) + 4 * g + (i & 3));
-                    if ((smask >> m) & 1u) {
-                        ko[m] = keys[i];
-                        io[m] = ids[rl[m]];
-                    }
-                }
-            }
-        }
-        if (bmask) {
-            uint32_t keys[16];
-            f32_block_keys<true>(l32 == 0 ? qrow : nullptr, rv ? x + int64_t(pos) * D : nullptr, D, int(OP_L2SQ), lane,
-                                 keys);
-            if (l32 == 0) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const uint32_t m = uint32_t(8 * (i >> 2) + 4 * hh + (i & 3));
-                    if ((bmask >> m) & 1u) {
-                        ko[m] = keys[i];
-                        io[m] = ids[rl[m]];
-                    }
-                }
-            }
+        GemmChain gc;
+        SmallChain sc;
+        rows_through_lds(q + int64_t(qi) * D, x, pos8, rv, D, slots[wave],
+                         [&](uint32_t j, const fb_f32x4(&xv)[8], const fb_f32x4(&qv)[8]) {
+                             if (small) sc.group(xv, qv);
+                             else gc.group(xv, qv, j, D);
+                         });
+        if (mine) {
+            rkey[int64_t(qi) * rcap + c * 64 + lane] = small ? sc.key() : gc.key(int(OP_L2SQ));
+            rid[int64_t(qi) * rcap + c * 64 + lane] = ids[pos];
         }
     }
 }
@@ -1259,7 +1245,7 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
     VA_CHECK_STATUS(screen_compact(ctx, cnt, clo, cpos, ubound, uint32_t(cap), Q, rr, rcount, uint32_t(rcap), ovf_cnt,
                                    ovf_rows));
     {
-        const uint64_t items = uint64_t(Q) * ((rcap + 31) / 32);
+        const uint64_t items = uint64_t(Q) * ((rcap + 63) / 64);
         const uint32_t blocks = uint32_t(std::min<uint64_t>(2048, (items + 3) / 4));
         ivf_rerank_kernel<<<dim3(blocks), dim3(256), 0, ctx->stream>>>(queries, ivf->list_vectors, ivf->ids,
                                                                        ivf->offsets, C, dp.qcnt, D, rr, rcount,

@@ -852,37 +852,39 @@ __global__ __launch_bounds__(256) void screen_compact_kernel(const uint32_t* __r
 }
 
 // ---- exact fp32 keys of the rerank lists ------------------------------------------------------
-// One wave per (32-row chunk of a query's list, query): the 32x32 MFMA block of the distance GEMM
-// with the query in column 0 (the other columns are zeros), so every key equals the fp32 scan's.
-// Persistent over the chunks (chunk-major, so the busy chunks spread over every wave); chunks past
-// a list's length are skipped.  Each lane streams one row of the chunk.
-template <bool VEC>
+// One wave per (64-row chunk of a query's rerank list, query), persistent and chunk-major (the
+// busy chunks spread over every wave); lane l scores row 64c + l with the fp32 scan's per-element
+// sequence on the VALU (GemmChain: the fmaf chain every element of the scan's MFMA block follows),
+// so every key equals the fp32 scan's.  The rows pass through the wave's LDS slot in coalesced
+// 128-byte lines (rows_through_lds).  Needs D % 4 == 0 and 16-byte aligned rows and queries.
 __global__ __launch_bounds__(256) void rerank_kernel(const float* __restrict__ q, const float* __restrict__ x,
                                                      uint32_t D, int op, const uint32_t* __restrict__ rr,
                                                      const uint32_t* __restrict__ rcount, uint32_t rcap, uint32_t Q,
                                                      uint32_t* __restrict__ rkey) {
-    const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5;
-    const uint32_t nch = (rcap + 31) / 32;
+    __shared__ fb_f32x4 slots[4][64 * 8];
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nch = (rcap + 63) / 64;
     const uint64_t items = uint64_t(Q) * nch;
     const uint32_t nw = gridDim.x * 4;
-    for (uint64_t it = uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6); it < items; it += nw) {
+    for (uint64_t it = uint64_t(blockIdx.x) * 4 + wave; it < items; it += nw) {
         const uint32_t c = uint32_t(it / Q), qi = uint32_t(it % Q);
         const uint32_t n = min(rcount[qi], rcap);
-        if (c * 32 >= n) continue;  // (uniform)
-        const uint32_t p = c * 32 + uint32_t(l32);
-        const float* qp = l32 == 0 ? q + int64_t(qi) * D : nullptr;
-        const float* xp = p < n ? x + int64_t(rr[int64_t(qi) * rcap + p]) * D : nullptr;
-        uint32_t keys[16];
-        f32_block_keys<VEC>(qp, xp, D, op, lane, keys);
-        if (l32 == 0) {
+        if (c * 64 >= n) continue;  // (uniform)
+        const uint32_t* rl = rr + int64_t(qi) * rcap + c * 64;
+        const uint32_t m = min(64u, n - c * 64);
+        uint32_t rid[8];
+        bool rv[8];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t m = c * 32 + uint32_t(8 * j + 4 * hh + e);
-                    if (m < n) rkey[int64_t(qi) * rcap + m] = keys[4 * j + e];
-                }
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t r = uint32_t(8 * i + (lane >> 3));
+            rv[i] = r < m;
+            rid[i] = rv[i] ? rl[r] : 0u;
         }
+        GemmChain ch;
+        rows_through_lds(q + int64_t(qi) * D, x, rid, rv, D, slots[wave],
+                         [&](uint32_t j, const fb_f32x4(&xv)[8], const fb_f32x4(&qv)[8]) { ch.group(xv, qv, j, D); });
+        if (uint32_t(lane) < m) rkey[int64_t(qi) * rcap + c * 64 + lane] = ch.key(op);
     }
 }
 
@@ -979,7 +981,9 @@ va_status screen_compact(va_context* ctx, const uint32_t* cnt, const uint32_t* c
 bool screen_applies(const va_context* ctx, const ScreenInput& in, uint32_t k) {
     if (ctx->opt_screen == 1) return false;
     if (in.op != OP_L2SQ && in.op != OP_L2 && in.op != OP_COS_DIST && in.op != OP_NEG_DOT) return false;
-    if (in.D % 4 != 0 || (reinterpret_cast<uintptr_t>(in.x) & 15) != 0) return false;
+    if (in.D % 4 != 0 || (reinterpret_cast<uintptr_t>(in.x) & 15) != 0 ||
+        (reinterpret_cast<uintptr_t>(in.q) & 15) != 0)
+        return false;
     const ScanPlan plan = plan_scan(ctx, in.Q, in.N, k, true);
     if (plan.direct) return false;
     if (!offsets_fit(uint64_t(plan.stride) * in.D, in.D)) return false;
@@ -1146,13 +1150,10 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     }
     // ---- 6. exact fp32 keys of the rerank rows ---------------------------------------------------
     {
-        const uint64_t items = uint64_t(Q) * ((rcap + 31) / 32);
+        const uint64_t items = uint64_t(Q) * ((rcap + 63) / 64);
         const uint32_t blocks = uint32_t(std::min<uint64_t>(2048, (items + 3) / 4));
-        const bool vec = D % 4 == 0 && (reinterpret_cast<uintptr_t>(in.q) & 15) == 0 &&
-                         (reinterpret_cast<uintptr_t>(in.x) & 15) == 0;
-        auto kern = vec ? &rerank_kernel<true> : &rerank_kernel<false>;
-        kern<<<dim3(blocks), dim3(256), 0, ctx->stream>>>(in.q, in.x, D, int(in.op), rr, rcount, uint32_t(rcap), Q,
-                                                          rkey);
+        rerank_kernel<<<dim3(blocks), dim3(256), 0, ctx->stream>>>(in.q, in.x, D, int(in.op), rr, rcount,
+                                                                   uint32_t(rcap), Q, rkey);
         VA_CHECK_LAUNCH(ctx);
         VA_CHECK_STATUS(mask_list_keys(ctx, rkey, nullptr, rr, rcount, Q, uint32_t(rcap), int64_t(rcap), out.skip));
     }
