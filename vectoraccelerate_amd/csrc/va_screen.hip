@@ -573,30 +573,33 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
 }
 
 // ---- the screening scan over an fp16 shadow of the database ---------------------------------------
-// The same tile (256 queries x 256 rows, four waves of 128 x 128) and epilogue as screen_kernel's
-// filter mode, but the rows come already rounded to fp16 (the same RNE rounding) with their
-// squared norms, so both operands move global -> LDS by direct loads and the main loop is MFMAs,
-// fragment reads and loads only.  64 d-values per stage, two stages in LDS (128 KiB); the
-// fragments of k-step g+1 are read while the 16 MFMAs of k-step g run, and the stage barrier sits
-// inside the last k-step of a stage, after its fragments are in registers (a bare s_barrier: the
-// direct loads of the next stage stay in flight across it).
+// 256 queries x 256 rows per workgroup as screen_kernel's filter mode, but the rows come already
+// rounded to fp16 (the same RNE rounding) with their squared norms, so both operands move
+// global -> LDS by direct loads and the main loop is MFMAs, fragment reads and loads only.
+// Sixteen waves of 64 queries x 64 rows (2 x 2 MFMA blocks, 64 accumulators: four waves per
+// SIMD, so one wave's fragment waits and barrier are covered by the others' MFMAs; one wave per
+// SIMD with 128 x 128 tiles ran the same loop 10-25 % slower).  64 d-values per stage, two
+// stages in LDS (128 KiB); the fragments of k-step g+1 are read while the 4 MFMAs of k-step g
+// run, and the stage barrier sits inside the last k-step of a stage, after its fragments are in
+// registers (a bare s_barrier: the direct loads of the next stage stay in flight across it).
 namespace s16 {
 constexpr int TQ = 256, TN = 256, KC = 64;
 constexpr int ROWB = KC * 2;              // bytes per LDS row
 constexpr int OPB = TQ * ROWB;            // one operand per stage (32 KiB)
 constexpr int STAGE = 2 * OPB;            // queries, then rows
-constexpr int LPW = OPB / 1024 / 4;       // 1 KiB direct loads per wave per operand per stage (8)
-constexpr int LDS = 2 * STAGE;            // two stages; the epilogue reuses them (32 KiB per wave)
-static_assert(LDS >= 4 * 32768, "epilogue dump");
+constexpr int WAVES = 16;
+constexpr int WQ = 64, WN = 64;           // a wave's queries x rows
+constexpr int LPW = OPB / 1024 / WAVES;   // 1 KiB direct loads per wave per operand per stage (2)
+constexpr int LDS = 2 * STAGE;            // two stages
 }  // namespace s16
 
-__global__ __launch_bounds__(256, 1) void screen16_kernel(ScreenArgs a) {
+__global__ __launch_bounds__(1024, 1) void screen16_kernel(ScreenArgs a) {
     using namespace s16;
     extern __shared__ __attribute__((aligned(1024))) char lds[];
     __shared__ __attribute__((aligned(16))) float norms[3 * TN];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wq = wave & 1, wn = wave >> 1, l32 = lane & 31, hh = lane >> 5;
+    const int wq = wave & 3, wn = wave >> 2, l32 = lane & 31, hh = lane >> 5;
     // XCD-aware order, as screen_kernel
     const uint32_t nqb = (a.Q + TQ - 1) / TQ;
     const uint32_t xcd = blockIdx.x % kXcds, seq = blockIdx.x / kXcds;
@@ -606,7 +609,7 @@ __global__ __launch_bounds__(256, 1) void screen16_kernel(ScreenArgs a) {
     const uint32_t qc = min(uint32_t(TQ), a.Q - qs), rc = min(uint32_t(TN), a.N - rs);
     const uint32_t nst = a.Dp / KC;
 
-    // Direct loads: wave w fills 1 KiB groups g = w + 4i (rows 8g .. 8g+7) of each operand; lane
+    // Direct loads: wave w fills 1 KiB groups g = w + 16i (rows 8g .. 8g+7) of each operand; lane
     // L loads row 8g + L/8 at physical chunk L%8 = logical chunk (L%8) ^ ((row >> 1) & 7).  Rows
     // past qc / rc read past their descriptor and land as zeros.
     const dma_rsrc qres = make_dma_rsrc(a.qh + int64_t(qs) * a.Dp, qc * a.Dp * 2u);
@@ -614,7 +617,7 @@ __global__ __launch_bounds__(256, 1) void screen16_kernel(ScreenArgs a) {
     uint32_t off[LPW];
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
-        const int row = 8 * (wave + 4 * i) + (lane >> 3);
+        const int row = 8 * (wave + WAVES * i) + (lane >> 3);
         off[i] = uint32_t(row) * a.Dp * 2u + 16u * uint32_t((lane & 7) ^ ((row >> 1) & 7));
     }
     const uint32_t lds0 = lds_addr_of(lds);
@@ -624,74 +627,67 @@ __global__ __launch_bounds__(256, 1) void screen16_kernel(ScreenArgs a) {
         const uint32_t sb = lds0 + (s & 1u) * uint32_t(STAGE);
 #pragma unroll
         for (int i = 0; i < LPW; ++i) {
-            const uint32_t grp = uint32_t(wave + 4 * i);
+            const uint32_t grp = uint32_t(wave + WAVES * i);
             lds_dma16(qres, ok ? off[i] + d0 * 2u : kDmaSkip, sb + grp * 1024u);
             lds_dma16(xres, ok ? off[i] + d0 * 2u : kDmaSkip, sb + uint32_t(OPB) + grp * 1024u);
         }
     };
-    // L2 prefetch of the rows of stage s+2, issued with the direct loads of stage s+1: one dword
-    // per 128-byte line (lane L of wave w takes row 64w + L) into a sink that nothing reads, so
-    // the direct loads of the next stage find the rows in L2
+    // L2 prefetch of the rows of stage s+1 ahead of their direct loads: waves 0-3, one dword per
+    // 128-byte line (lane L of wave w takes row 64w + L) into a sink that nothing reads
     __shared__ __attribute__((aligned(256))) char pf_sink[4 * 256];
-    const uint32_t pf_off = uint32_t(64 * wave + lane) * a.Dp * 2u;
+    const bool pf_wave = wave < 4;
+    const uint32_t pf_off = uint32_t(64 * (wave & 3) + lane) * a.Dp * 2u;
     auto prefetch = [&](uint32_t s) {
         const uint32_t d0 = s * KC;
-        lds_dma4(xres, d0 < a.Dp ? pf_off + d0 * 2u : kDmaSkip, lds_addr_of(pf_sink + wave * 256));
+        if (pf_wave) lds_dma4(xres, d0 < a.Dp ? pf_off + d0 * 2u : kDmaSkip, lds_addr_of(pf_sink + (wave & 3) * 256));
     };
     // fragment rows start at multiples of 32, so the chunk swizzle is (l32 >> 1) & 7 for both
     const int swz = (l32 >> 1) & 7;
-    const uint32_t a_off = uint32_t(OPB + (wn * 128 + l32) * ROWB);
-    const uint32_t b_off = uint32_t((wq * 128 + l32) * ROWB);
+    const uint32_t a_off = uint32_t(OPB + (wn * WN + l32) * ROWB);
+    const uint32_t b_off = uint32_t((wq * WQ + l32) * ROWB);
 
-    float4 qinf[4];
-    uint32_t qthr[4];
+    f32x16 acc[2][2];
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-        const uint32_t qi = qs + min(uint32_t(wq * 128 + 32 * n + l32), qc - 1);
-        qinf[n] = a.qinfo[qi];
-        qthr[n] = a.thr[qi];
-    }
-    f32x16 acc[4][4];
+    for (int m = 0; m < 2; ++m)
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-        for (int n = 0; n < 4; ++n)
+        for (int n = 0; n < 2; ++n)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[m][n][v] = 0.0f;
 
-    h8v fa[2][4], fb[2][4];
+    h8v fa[2][2], fb[2][2];
     auto read_frags = [&](int buf, uint32_t slot, int t) {
         const char* base = lds + slot * STAGE;
         const uint32_t ko = 16u * uint32_t((2 * t + hh) ^ swz);
 #pragma unroll
-        for (int m = 0; m < 4; ++m) fa[buf][m] = *reinterpret_cast<const h8v*>(base + a_off + m * 32 * ROWB + ko);
+        for (int m = 0; m < 2; ++m) fa[buf][m] = *reinterpret_cast<const h8v*>(base + a_off + m * 32 * ROWB + ko);
 #pragma unroll
-        for (int n = 0; n < 4; ++n) fb[buf][n] = *reinterpret_cast<const h8v*>(base + b_off + n * 32 * ROWB + ko);
+        for (int n = 0; n < 2; ++n) fb[buf][n] = *reinterpret_cast<const h8v*>(base + b_off + n * 32 * ROWB + ko);
     };
     auto mma = [&](int buf) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
+        for (int m = 0; m < 2; ++m)
 #pragma unroll
-            for (int n = 0; n < 4; ++n)
+            for (int n = 0; n < 2; ++n)
                 acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[buf][m], fb[buf][n], acc[m][n], 0, 0, 0);
     };
-    // the 8 fragment reads of the next k-step go between the first 8 of the 16 MFMAs
+    // the 4 fragment reads of the next k-step go between the 4 MFMAs
     auto interleave = [&]() {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < 4; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     };
     // workgroup barrier without the release fence of __syncthreads (which would also wait for
     // the direct loads in flight); this wave's LDS reads are complete before it
     auto barrier = [&]() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
+    // per wave and stage: 2 LPW direct loads, plus one prefetch in waves 0-3
     issue(0);
     issue(1);
     prefetch(2);
-    wait_vmcnt<2 * LPW + 1>();  // stage 0 (older than stage 1's loads and the prefetch)
+    if (pf_wave) wait_vmcnt<2 * LPW + 1>();  // stage 0 (older than stage 1's loads and the prefetch)
+    else wait_vmcnt<2 * LPW>();
     barrier();
     read_frags(0, 0, 0);
     for (uint32_t s = 0; s < nst; ++s) {
@@ -706,7 +702,8 @@ __global__ __launch_bounds__(256, 1) void screen16_kernel(ScreenArgs a) {
             } else {
                 // this k-step's fragments are in registers: publish stage s+1, free slot s (the
                 // one load younger than stage s+1's is the prefetch issued after them)
-                wait_vmcnt<1>();
+                if (pf_wave) wait_vmcnt<1>();
+                else wait_vmcnt<0>();
                 barrier();
                 read_frags(cur ^ 1, slot ^ 1u, 0);
                 mma(cur);
@@ -717,14 +714,13 @@ __global__ __launch_bounds__(256, 1) void screen16_kernel(ScreenArgs a) {
         }
     }
     wait_vmcnt<0>();
-    __syncthreads();
 
     // the tile's row norms from the shadow; flags as in screen_kernel
     float* xxs = norms;
     float* xxp = norms + TN;
     float* nxp = norms + 2 * TN;
     const float tiny = a.op == OP_COS_DIST ? 8.0f * a.c0x : 0.0f;
-    {
+    if (tid < TN) {
         const uint32_t r = uint32_t(tid);
         const float t = r < rc ? a.xn[rs + r] : 0.0f;
         const float nx = __builtin_amdgcn_sqrtf(t);
@@ -734,8 +730,92 @@ __global__ __launch_bounds__(256, 1) void screen16_kernel(ScreenArgs a) {
         nxp[r] = flag ? __builtin_nanf("") : nx;
     }
     __syncthreads();
-    filter_epilogue(a, acc, qinf, qthr, reinterpret_cast<f32x4v*>(lds + wave * 32768), xxs, xxp, nxp, qs, rs, qc, rc,
-                    wq, wn, lane);
+
+    // ---- filter epilogue: lane (l32, hh) holds query wq*64 + 32n + l32 against rows
+    // wn*64 + 32m + 8j + 4hh + e in acc[m][n][4j + e]; t = 16m + 4j + e indexes its 32 values.
+    // One query block at a time goes to the wave's 8 KiB of the (now free) stage LDS, so only the
+    // other block's accumulators stay in registers; the pre-test over the 32 values builds a bit
+    // mask without branches (after a quick rejection: the right-hand side A|x|^2 + B|x| + C over
+    // the lane's rows is bounded below at the corner of their (|x|^2, |x|) box that A's and B's
+    // signs select, so a lane whose largest value is below it passes nothing; flagged (NaN) rows
+    // disable it); lanes l and l + 32 hold the same query, so one atomic reserves both lanes'
+    // places; the appends read the values back from LDS.
+    auto row_of = [&](int t) { return wn * WN + 32 * (t >> 4) + 8 * ((t >> 2) & 3) + 4 * hh + (t & 3); };
+    uint32_t valid = 0;
+    float bxlo = INFINITY, bxhi = -INFINITY, bnlo = INFINITY, bnhi = -INFINITY;
+    bool bflag = false;
+#pragma unroll 1
+    for (int t = 0; t < 32; t += 4) {
+        const int r = row_of(t);  // rows r .. r + 3
+        const f32x4v xx = *reinterpret_cast<const f32x4v*>(xxp + r);
+        const f32x4v nx = *reinterpret_cast<const f32x4v*>(nxp + r);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            valid |= uint32_t(uint32_t(r + e) < rc) << (t + e);
+            bflag |= !(xx[e] == xx[e]) || !(nx[e] == nx[e]);
+            bxlo = fminf(bxlo, xx[e]);
+            bxhi = fmaxf(bxhi, xx[e]);
+            bnlo = fminf(bnlo, nx[e]);
+            bnhi = fmaxf(bnhi, nx[e]);
+        }
+    }
+    f32x4v* dump = reinterpret_cast<f32x4v*>(lds + wave * 8192) + lane;  // [t / 4][lane]
+    auto block = [&](auto NC) {
+        constexpr int n = decltype(NC)::value;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            f32x4v v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = acc[c >> 2][n][4 * (c & 3) + e];
+            dump[c * 64] = v;
+        }
+        // re-read the row norms from LDS below rather than keep the bounds pass's copies live
+        asm volatile("" ::: "memory");
+        const uint32_t qt = uint32_t(wq * WQ + 32 * n + l32);
+        const uint32_t qi = qs + min(qt, qc - 1);
+        const float4 qinf = a.qinfo[qi];
+        const PreTest pt = pretest_consts(a, qinf, a.thr[qi]);
+        bool skip = qt >= qc;
+        if (!bflag && !skip) {
+            const float lo = fmaf(pt.A, pt.A >= 0.0f ? bxlo : bxhi, fmaf(pt.B, pt.B >= 0.0f ? bnlo : bnhi, pt.C));
+            float mx = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < 32; ++t) mx = fmaxf(mx, acc[t >> 4][n][t & 15]);
+            skip = mx < lo;
+        }
+        uint32_t mk = 0;
+        if (!skip) {
+#pragma unroll 2
+            for (int c = 0; c < 8; ++c) {
+                const int r = row_of(4 * c);
+                const f32x4v xx = *reinterpret_cast<const f32x4v*>(xxp + r);
+                const f32x4v nx = *reinterpret_cast<const f32x4v*>(nxp + r);
+                const f32x4v v = dump[c * 64];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    mk |= uint32_t(!(v[e] < fmaf(pt.A, xx[e], fmaf(pt.B, nx[e], pt.C)))) << (4 * c + e);
+            }
+            mk &= valid;
+        }
+        const uint32_t cnt = uint32_t(__popc(mk));
+        const uint32_t other = uint32_t(__shfl_xor(int(cnt), 32));
+        uint32_t base = 0;
+        if (hh == 0 && cnt + other) base = atomicAdd(a.cnt + qi, cnt + other);
+        uint32_t pos = uint32_t(__shfl(int(base), l32)) + (hh ? other : 0u);
+        const float* src = reinterpret_cast<const float*>(dump);
+        while (mk && pos < a.cap) {
+            const int t = __builtin_ctz(mk);
+            mk &= mk - 1;
+            const int r = row_of(t);
+            const int64_t o = int64_t(qi) * a.cap + pos;
+            a.cand_dot[o] = src[(t >> 2) * 256 + (t & 3)] * qinf.z;
+            a.cand_xx[o] = xxs[r];
+            a.cand_id[o] = a.id_base + rs + uint32_t(r);
+            ++pos;
+        }
+    };
+    block(std::integral_constant<int, 0>());
+    block(std::integral_constant<int, 1>());
 }
 
 // ---- the fp16 shadow: rows rounded to fp16 (RNE, as the scans round), padded with zeros to Dp,
@@ -910,7 +990,7 @@ va_status launch_screen16(va_context* ctx, const ScreenArgs& a) {
     if (grid > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "screen grid too large (%llu)", (unsigned long long)grid);
     VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(&screen16_kernel),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, LDS));
-    screen16_kernel<<<dim3(uint32_t(grid)), dim3(256), LDS, ctx->stream>>>(a);
+    screen16_kernel<<<dim3(uint32_t(grid)), dim3(64 * WAVES), LDS, ctx->stream>>>(a);
     VA_CHECK_LAUNCH(ctx);
     return VA_OK;
 }
