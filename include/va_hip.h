@@ -91,8 +91,19 @@ const char* va_last_error_message(const va_context* ctx);
  * filtering scan of va_fused_topk: 0 = automatic (fp16 screening pass with an exact fp32
  * rerank wherever it applies), 1 = never screen (fp32 scan only), 2 = screen whenever the
  * metric and layout allow it.  Screening changes no result: the ids and distances are the
- * fp32 scan's, bit for bit. */
-typedef enum { VA_OPT_CANDIDATE_CAP = 1, VA_OPT_SAMPLE_ROWS = 2, VA_OPT_SCREEN = 3 } va_option;
+ * fp32 scan's, bit for bit.  SAMPLE_RANK sets which order statistic of the sample becomes a
+ * query's filter threshold: rank k always leaves at least k candidates; a smaller rank r
+ * filters far fewer rows, and a query left with fewer than k candidates takes the exact
+ * fallback, so results do not change.  0 = automatic: the smallest r for which, with the
+ * sample drawn at random, the chance that r of the k nearest rows fall in it (which is what
+ * leaves fewer than k candidates) is below 1e-4; r = k when a deletion mask is in use.
+ * Values >= k give rank k. */
+typedef enum {
+    VA_OPT_CANDIDATE_CAP = 1,
+    VA_OPT_SAMPLE_ROWS = 2,
+    VA_OPT_SCREEN = 3,
+    VA_OPT_SAMPLE_RANK = 4
+} va_option;
 va_status va_context_set_option(va_context* ctx, va_option option, uint64_t value);
 
 /* Phase timings of the top-k scans, from hipEvents on the context stream.  Replaces

@@ -135,10 +135,13 @@ def test_back_to_back_searches_match_oracle(ctx, oracle):
 
 
 def _with_cap(ctx, fn, cap, sample):
+    """Run fn with a forced candidate cap and sample size; a forced cap also pins the threshold
+    to the sample's k-th key (the rank that overflows a small cap most)."""
     from vectoraccelerate_amd import _lib
 
     ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, cap)
     ctx.set_option(_lib.VA_OPT_SAMPLE_ROWS, sample)
+    ctx.set_option(_lib.VA_OPT_SAMPLE_RANK, 2**32 if cap else 0)
     ctx.set_profiling(True)
     try:
         r = fn()
@@ -146,6 +149,7 @@ def _with_cap(ctx, fn, cap, sample):
     finally:
         ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 0)
         ctx.set_option(_lib.VA_OPT_SAMPLE_ROWS, 0)
+        ctx.set_option(_lib.VA_OPT_SAMPLE_RANK, 0)
         ctx.set_profiling(False)
     return r, t
 

@@ -191,6 +191,27 @@ def test_sampled_threshold_path(ctx, oracle, metric):
     check_topk(metric, q, x, 20, gi, gd, oi, od)
 
 
+@pytest.mark.parametrize("rank", [1, 2, 0])
+def test_speculative_threshold_rank(ctx, oracle, rank):
+    """A threshold below the sample's k-th key (rank 1 or 2, or the automatic rank) leaves some
+    queries short of k candidates; the select lists them for the exact fallback."""
+    from vectoraccelerate_amd import _lib
+
+    g = rng(80 + rank)
+    q = g.standard_normal((70, 48)).astype(np.float32)
+    x = g.standard_normal((30000, 48)).astype(np.float32)
+    x[::30][:35] = q[:35]  # exact matches at sampled rows (1000 rows: stride 30) for half the queries
+    try:
+        _with_options(ctx, 0, 1000)
+        ctx.set_option(_lib.VA_OPT_SAMPLE_RANK, rank)
+        gi, gd = _fused(ctx, L2SQ, q, x, 20)
+    finally:
+        _with_options(ctx, 0, 0)
+        ctx.set_option(_lib.VA_OPT_SAMPLE_RANK, 0)
+    oi, od = oracle.flat_topk(L2SQ, q, x, 20)
+    check_topk(L2SQ, q, x, 20, gi, gd, oi, od)
+
+
 def test_overflow_fallback_is_exact(ctx, oracle):
     """A tiny candidate capacity makes every query overflow: the chunked exact path must agree."""
     g = rng(78)

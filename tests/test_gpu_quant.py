@@ -221,12 +221,14 @@ def test_i8_large_q_overflow_rescan(ctx, oracle):
     try:
         ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 24)
         ctx.set_option(_lib.VA_OPT_SAMPLE_ROWS, 3000)
+        ctx.set_option(_lib.VA_OPT_SAMPLE_RANK, 2**32)  # the sample's 20th key: most lists overflow
         ctx.set_profiling(True)  # the overflow count is read back only when profiling
         gi, gd = ScalarQuantizationKernel(ctx).searchTopK(qc, xc, 20)
         t = ctx.last_scan_timings()
     finally:
         ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 0)
         ctx.set_option(_lib.VA_OPT_SAMPLE_ROWS, 0)
+        ctx.set_option(_lib.VA_OPT_SAMPLE_RANK, 0)
         ctx.set_profiling(False)
     check_topk_exact(gi, gd, oi, od)
     assert gi[5, 0] == 17
@@ -355,6 +357,28 @@ def test_hamming_large_q_many_ties_and_overflow(ctx, oracle):
             ctx.set_option(_lib.VA_OPT_SAMPLE_ROWS, 0)
         check_topk_exact(gi, gd, oi, od)
         assert gd[7, 0] == 0
+
+
+@pytest.mark.parametrize("rank", [1, 3, 0])
+def test_hamming_speculative_threshold_rank(ctx, oracle, rank):
+    """fp4 MFMA filter with a threshold below the sample's k-th key: queries whose exact copy
+    sits on a sampled row get threshold 0 at rank 1 (one candidate) and take the fallback."""
+    from vectoraccelerate_amd import HammingDistanceKernel, _lib
+
+    g = rng(33 + rank)
+    q = g.integers(0, 2**32, (260, 24), dtype=np.uint64).astype(np.uint32)
+    x = g.integers(0, 2**32, (30000, 24), dtype=np.uint64).astype(np.uint32)
+    x[::30][:100] = q[:100]  # 1000 sampled rows: stride 30
+    oi, od = oracle.hamming_topk(q, x, 50)
+    try:
+        ctx.set_option(_lib.VA_OPT_SAMPLE_ROWS, 1000)
+        ctx.set_option(_lib.VA_OPT_SAMPLE_RANK, rank)
+        gi, gd = HammingDistanceKernel(ctx).nearestNeighbors(q, x, 50)
+    finally:
+        ctx.set_option(_lib.VA_OPT_SAMPLE_ROWS, 0)
+        ctx.set_option(_lib.VA_OPT_SAMPLE_RANK, 0)
+    check_topk_exact(gi, gd, oi, od)
+    assert np.all(gd[:100, 0] == 0)
 
 
 def test_hamming_sampled_and_overflow_paths(ctx, oracle):

@@ -28,6 +28,7 @@ VA_SELECT_MAX = 1
 VA_OPT_CANDIDATE_CAP = 1
 VA_OPT_SAMPLE_ROWS = 2
 VA_OPT_SCREEN = 3
+VA_OPT_SAMPLE_RANK = 4
 
 VA_SENTINEL_INDEX = 0xFFFFFFFF
 VA_MAX_K = 1024

@@ -170,10 +170,11 @@ __global__ __launch_bounds__(256) void hamming_scan_wide_kernel(HamArgs a) {
 // straight into registers (lane: row l % 32, half h = l / 32 of its words, 16-byte loads;
 // the next tile in flight while this one computes), widens one 32-bit word per k-step into
 // the A fragment and runs 8 MFMAs against the 8 resident query blocks.  K mapping: k-step s
-// takes word h·W/2 + s of the half, bit i of the word pairs with bit i of the same query
-// word (fragment nibble i).  No workgroup barrier after the query load.  Filter epilogue as
-// in i8_resq_kernel: a pass is d <= tau, i.e. 2 a.b - |x| >= |q| - tau, tested with a
-// per-lane maximum first; passes go to a per-wave LDS list flushed when full.
+// takes word h·W/2 + s of the half, widened by the same bit-to-nibble assignment on both
+// sides (widen_word).  No workgroup barrier after the query load.  Filter epilogue as in
+// i8_resq_kernel: a pass is d <= tau, i.e. a.b - |x|/2 >= (|q| - tau)/2 with the accumulators
+// started from -|x|/2, tested with a per-lane maximum first; passes go to a per-wave LDS list
+// flushed when full.
 namespace hmf {
 constexpr int TQ = 256, NW = 8, WR = 32, TN = NW * WR, LCAP = 80;
 constexpr int STAGE = NW * LCAP * 12;
@@ -184,13 +185,14 @@ constexpr int rows_bytes(int W) { return NW * WR * (W + 1) * 4; }  // per-wave r
 constexpr size_t lds_bytes(int W) { return size_t(TQ) * qstride(W) + STAGE + PA + PB + rows_bytes(W); }
 }  // namespace hmf
 
-// 8 bits -> 8 fp4 nibbles: bit i -> nibble i, 1 -> 1.0 (e2m1 0b0010), 0 -> 0
-__device__ __forceinline__ uint32_t widen8(uint32_t b) {
-    uint32_t t = b & 0xFFu;
-    t = (t | (t << 12)) & 0x000F000Fu;
-    t = (t | (t << 6)) & 0x03030303u;
-    t = (t | (t << 3)) & 0x11111111u;
-    return t << 1;
+// 32 bits -> 32 fp4 nibbles in four dwords, 1 -> 1.0 (e2m1 0b0010), 0 -> 0: nibble i of dword j
+// holds bit 4i + j of the word.  A dot product does not depend on which k slot a bit goes to as
+// long as rows and queries use the same assignment; this one costs one shift and one mask per
+// dword (a bit-i-to-nibble-i spread needs a multiply-based scatter per byte, four times the
+// VALU time, and the scan is bound by MFMA + VALU issue).
+__device__ __forceinline__ uint4 widen_word(uint32_t w) {
+    constexpr uint32_t M = 0x22222222u;
+    return {(w << 1) & M, w & M, (w >> 1) & M, (w >> 2) & M};
 }
 
 typedef int i32x8h __attribute__((ext_vector_type(8)));
@@ -232,8 +234,7 @@ __global__ __launch_bounds__(512, 2) void hamming_mfma_kernel(HamArgs a, uint32_
         const int r = e / W, w = e % W;
         const uint32_t v = uint32_t(r) < qn ? a.q[uint64_t(q0 + r) * W + w] : 0u;
         const int c = 2 * (w % HW) + w / HW;
-        const uint4 o = {widen8(v), widen8(v >> 8), widen8(v >> 16), widen8(v >> 24)};
-        *reinterpret_cast<uint4*>(lds8 + r * QS + 16 * c) = o;
+        *reinterpret_cast<uint4*>(lds8 + r * QS + 16 * c) = widen_word(v);
     }
     for (int r = tid; r < TQ; r += 512) {
         uint32_t pb = 0;
@@ -242,13 +243,16 @@ __global__ __launch_bounds__(512, 2) void hamming_mfma_kernel(HamArgs a, uint32_
         s_pb[r] = float(pb);
     }
     __syncthreads();  // resident queries visible; the only workgroup barrier
-    // pass iff 2 a.b - |x| >= |q| - tau; tau >= 32 W passes everything; padding never passes
+    // pass iff 2 a.b - |x| >= |q| - tau, i.e. a.b - |x|/2 >= (|q| - tau)/2 (halves of integers
+    // below 2^24: exact); the accumulators start from -|x|/2, so the left side is what they hold.
+    // tau >= 32 W passes everything; padding never passes
     float cq[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
         const uint32_t ql = uint32_t(u * 32 + l32);
         const uint32_t t = a.thr[q0 + (ql < qn ? ql : 0u)];
-        cq[u] = ql >= qn ? __builtin_inff() : (t >= uint32_t(32 * W) ? -__builtin_inff() : s_pb[ql] - float(t));
+        cq[u] = ql >= qn ? __builtin_inff()
+                         : (t >= uint32_t(32 * W) ? -__builtin_inff() : 0.5f * (s_pb[ql] - float(t)));
     }
 
     // ---- this wave's rows -------------------------------------------------------------------
@@ -295,103 +299,121 @@ __global__ __launch_bounds__(512, 2) void hamming_mfma_kernel(HamArgs a, uint32_
         lc = 0;
     };
     f32x16h acc[8];
-    // lane value v of a block is row 8 (v >> 2) + 4 hh + (v & 3) of the wave's 32
-    auto epilogue = [&](uint32_t lt) {
-        const uint64_t r64 = uint64_t(t0 + lt) * TN + uint32_t(wave) * WR;
-        const uint32_t r0 = uint32_t(r64);  // ids of rows below N fit 32 bits
-        const int32_t lim = int32_t(r64 < N ? min(uint64_t(N) - r64, uint64_t(WR)) : 0) - 4 * hh;
-        float pv[16];
+    // Lane value v of a block is row 8 (v >> 2) + 4 hh + (v & 3) of the wave's 32; it holds
+    // a.b - |x|/2 at the end of a tile.  The passes of block u of a tile whose first row id is
+    // r0 and whose rows past N start at lim (this lane half's view) go to the staging list.
+    auto block_passes = [&](int u, uint32_t r0, int32_t lim) {
+        const float c = cq[u];
+        // an opaque zero: without it the compiler precomputes this rare path's per-block query
+        // values for all 8 blocks ahead of the loop and spills them
+        uint32_t oz;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(oz));
+        const uint32_t ql = uint32_t(u * 32 + l32) + oz;
+        uint32_t vm = 0;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const f32x4h t = *reinterpret_cast<const f32x4h*>(s_pa + 8 * g + 4 * hh);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) pv[4 * g + e] = t[e];
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const float c = cq[u];
-            float m = fmaf(2.0f, acc[u][0], -pv[0]);
-#pragma unroll
-            for (int v = 1; v < 16; ++v) m = fmaxf(m, fmaf(2.0f, acc[u][v], -pv[v]));
-            if (!__ballot(m >= c)) continue;
-            const uint32_t ql = uint32_t(u * 32 + l32);
-            uint32_t vm = 0;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) vm |= __ballot(fmaf(2.0f, acc[u][v], -pv[v]) >= c) ? (1u << v) : 0u;
+        for (int v = 0; v < 16; ++v) vm |= __ballot(acc[u][v] >= c) ? (1u << v) : 0u;
 #pragma unroll 1
-            while (vm) {
-                const uint32_t v = __builtin_ctz(vm);
-                vm &= vm - 1;
-                const float dot = acc[u][v];
-                const float pa = pv[v];
-                const uint32_t roff = 8 * (v >> 2) + (v & 3);
-                const bool p = fmaf(2.0f, dot, -pa) >= c && int32_t(roff) < lim;
-                const uint64_t mk = __ballot(p);
-                if (!mk) continue;
-                const uint32_t n = uint32_t(__popcll(mk));
-                if (lc + n > uint32_t(LCAP)) flush();  // wave-uniform
-                if (p) {
-                    const uint32_t e =
-                        lc + __builtin_amdgcn_mbcnt_hi(uint32_t(mk >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mk), 0u));
-                    s_qi[e] = q0 + ql;
-                    s_key[e] = uint32_t(pa + s_pb[ql] - 2.0f * dot);  // exact: integers below 2^24
-                    s_id[e] = r0 + roff + 4 * uint32_t(hh);
-                }
-                lc += n;
+        while (vm) {
+            const uint32_t v = __builtin_ctz(vm);
+            vm &= vm - 1;
+            const float sv = acc[u][v];
+            const uint32_t roff = 8 * (v >> 2) + (v & 3);
+            const bool p = sv >= c && int32_t(roff) < lim;
+            const uint64_t mk = __ballot(p);
+            if (!mk) continue;
+            const uint32_t n = uint32_t(__popcll(mk));
+            if (lc + n > uint32_t(LCAP)) flush();  // wave-uniform
+            if (p) {
+                const uint32_t e =
+                    lc + __builtin_amdgcn_mbcnt_hi(uint32_t(mk >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mk), 0u));
+                s_qi[e] = q0 + ql;
+                s_key[e] = uint32_t(s_pb[ql] - 2.0f * sv);  // |q| + |x| - 2 a.b, exact below 2^24
+                s_id[e] = r0 + roff + 4 * uint32_t(hh);
             }
+            lc += n;
         }
     };
 
     // ---- main loop ------------------------------------------------------------------------
     // A tile's row words go through a per-wave LDS buffer (rows W + 1 words apart: the 32 rows
-    // of one read fall in distinct banks), so the k-steps are a rolled loop that reads its word
-    // by step index; the epilogue of tile lt runs at the top of iteration lt + 1, where the
-    // accumulators reach it through the loop's back edge.  (Fully unrolled steps with the
-    // epilogue after them let the compiler sink each block's MFMA chain into the epilogue,
-    // which kept every step's fragments alive at once and spilled.)
+    // of one read fall in distinct banks), so the middle k-steps are a rolled loop that reads
+    // its word by step index.  The first k-step takes its word from registers and its starting
+    // values (-|x|/2 of each accumulator's row) from LDS, written at the end of the previous
+    // tile; the last k-step is followed, in the same basic block, by the next tile's row counts
+    // and by this tile's quick test (one maximum per block and lane, no branch per block), whose
+    // VALU work overlaps the last MFMAs; only a tile with a possible pass branches to the
+    // staging code.
     uint32_t xw[HW], xn[HW];
     load_tile(0, xw);
     i32x4h bq[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) bq[u] = rd_q(0, u);
     uint32_t* myrow = s_rw + l32 * (W + 1) + hh * HW;
-    auto widen_word = [&](uint32_t w) {
-        return fp4_operand(i32x4h{int(widen8(w)), int(widen8(w >> 8)), int(widen8(w >> 16)), int(widen8(w >> 24))});
+    auto widen_operand = [&](uint32_t w) {
+        const uint4 d = widen_word(w);
+        return fp4_operand(i32x4h{int(d.x), int(d.y), int(d.z), int(d.w)});
     };
-    for (uint32_t lt = 0; lt <= tcount; ++lt) {
-        if (lt > 0) epilogue(lt - 1);
-        if (lt == tcount) break;
-        asm volatile("v_mov_b32 %0, 0" : "=v"(qz));
+    // -|x|/2 of the tile's rows into LDS: the two halves of a row are the lane pair (l, l + 32),
+    // which both store the same value (no branch)
+    auto row_counts = [&]() {
         uint32_t pa = 0;
 #pragma unroll
-        for (int i = 0; i < HW; ++i) {
-            myrow[i] = xw[i];
-            pa += __popc(xw[i]);
+        for (int i = 0; i < HW; ++i) pa += __popc(xw[i]);
+        s_pa[l32] = -0.5f * float(pa + __shfl_xor(pa, 32));
+    };
+    row_counts();
+    for (uint32_t lt = 0; lt < tcount; ++lt) {
+#pragma unroll
+        for (int i = 0; i < HW; ++i) myrow[i] = xw[i];
+        f32x16h c0;  // -|x|/2 of the row of each accumulator value
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const f32x4h t = *reinterpret_cast<const f32x4h*>(s_pa + 8 * g + 4 * hh);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) c0[4 * g + e] = t[e];
         }
+        asm volatile("v_mov_b32 %0, 0" : "=v"(qz));
+        // One k-step: block u's MFMA, then the read of its fragment for the next step, a full
+        // step (8 MFMAs) ahead of its use; the row word of the step after next is read at the
+        // start.  Scheduling barriers keep this program order: left alone, the scheduler moves
+        // every read behind the step's last MFMA and the next step waits for all of them.
+        uint32_t word = 0;
+        auto k_step = [&](const i32x8h& af, const f32x16h* init, int nq, int nw) {
+            if (nw >= 0) word = myrow[nw];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                acc[u] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af, fp4_operand(bq[u]), init ? *init : acc[u],
+                                                                         4, 4, 0, 127, 0, 127);
+                bq[u] = rd_q(nq, u);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        k_step(widen_operand(xw[0]), &c0, 1, 1);  // accumulators start from -|x|/2
         load_tile(lt + 1 < tcount ? lt + 1 : lt, xn);  // the next tile in flight
-        // row popcounts: the two halves of a row
-        const float pr = float(pa + __shfl_xor(pa, 32));
-        if (hh == 0) s_pa[l32] = pr;
-        {  // k-step 0: accumulators start from zero
-            const i32x8h af = widen_word(myrow[0]);
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                acc[u] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af, fp4_operand(bq[u]), f32x16h{}, 4, 4, 0, 127, 0, 127);
-                bq[u] = rd_q(HW > 1 ? 1 : 0, u);
-            }
-        }
-#pragma unroll 2
-        for (int st = 1; st < HW; ++st) {
-            const i32x8h af = widen_word(myrow[st]);
-            const int nxt = st + 1 < HW ? st + 1 : 0;  // the next tile starts at step 0
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                acc[u] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af, fp4_operand(bq[u]), acc[u], 4, 4, 0, 127, 0, 127);
-                bq[u] = rd_q(nxt, u);
-            }
-        }
+        // keeps those loads here: with no store after them the compiler would sink them below
+        // the k-steps, next to their use, and the tile would wait for HBM
+        asm volatile("" ::: "memory");
+#pragma unroll 1
+        for (int st = 1; st < HW - 1; ++st) k_step(widen_operand(word), nullptr, st + 1, st + 1);
+        k_step(widen_operand(word), nullptr, 0, -1);  // the last step; the next tile starts at step 0
 #pragma unroll
         for (int i = 0; i < HW; ++i) xw[i] = xn[i];
+        if (lt + 1 < tcount) row_counts();
+        uint32_t hit = 0;  // blocks with a lane whose best value passes (wave-uniform)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            float m = acc[u][0];
+#pragma unroll
+            for (int v = 1; v < 16; ++v) m = fmaxf(m, acc[u][v]);
+            hit |= __ballot(m >= cq[u]) ? (1u << u) : 0u;
+        }
+        if (hit) {
+            const uint64_t r64 = uint64_t(t0 + lt) * TN + uint32_t(wave) * WR;
+            const int32_t lim = int32_t(r64 < N ? min(uint64_t(N) - r64, uint64_t(WR)) : 0) - 4 * hh;
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (hit & (1u << u)) block_passes(u, uint32_t(r64), lim);  // ids below N fit 32 bits
+        }
     }
     flush();
 }

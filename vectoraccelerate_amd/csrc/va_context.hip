@@ -351,6 +351,7 @@ va_status va_context_set_option(va_context* ctx, va_option option, uint64_t valu
     switch (option) {
         case VA_OPT_CANDIDATE_CAP: ctx->opt_candidate_cap = value; return VA_OK;
         case VA_OPT_SAMPLE_ROWS: ctx->opt_sample_rows = value; return VA_OK;
+        case VA_OPT_SAMPLE_RANK: ctx->opt_sample_rank = value; return VA_OK;
         case VA_OPT_SCREEN:
             VA_REQUIRE(ctx, value <= 2, "VA_OPT_SCREEN must be 0, 1 or 2, got %llu", (unsigned long long)value);
             ctx->opt_screen = uint32_t(value);

@@ -27,6 +27,7 @@ struct va_context {
     // test/tuning overrides of the exact top-k scan (0 = automatic)
     uint64_t opt_candidate_cap = 0;
     uint64_t opt_sample_rows = 0;
+    uint64_t opt_sample_rank = 0;  // VA_OPT_SAMPLE_RANK: 0 automatic, else min(value, k)
     uint32_t opt_screen = 0;  // VA_OPT_SCREEN: 0 auto, 1 off, 2 forced where it applies
     // scratch arena: partial results, counters, candidate buffers
     char* scratch = nullptr;
@@ -373,9 +374,11 @@ struct SelectArgs {
     int key_kind = 0;              // 0 float asc, 1 float desc, 2 int32, 3 uint32 (for value outputs)
     // threshold mode: write only the k-th smallest key per row (ignores outputs above)
     uint32_t* out_kth = nullptr;
-    // overflow detection (candidate mode): rows whose count exceeds n are listed here
+    // overflow detection (candidate mode): rows whose count exceeds n, or is below min_count,
+    // are listed here
     uint32_t* overflow_count = nullptr;
     uint32_t* overflow_rows = nullptr;
+    uint32_t min_count = 0;
     // every key is below 2^key_bits (Hamming distances: a few bits); up to 11 bits the k-th
     // smallest key comes from one histogram pass instead of four byte passes
     uint32_t key_bits = 32;

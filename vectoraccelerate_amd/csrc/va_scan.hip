@@ -4,14 +4,18 @@
 // the Q x N distance matrix in 64 MB chunks (FusedL2TopKKernel.execute,
 // Kernels/Metal4/FusedL2TopKKernel.swift:367-427, :765-1090).  Here every k takes one path
 // and the full matrix is never stored:
-//   1. sample:  dense keys of each query against S strided rows; tau_q = k-th smallest
-//               (an upper bound of the true k-th key: the sample rows are real rows and the
-//               filter pass computes bit-identical keys for them);
+//   1. sample:  dense keys of each query against S strided rows; tau_q = the r-th smallest
+//               (r = k: an upper bound of the true k-th key, since the sample rows are real
+//               rows and the filter pass computes bit-identical keys for them; r < k: a
+//               tighter threshold that is checked in step 3, see sample_rank);
 //   2. filter:  the scan kernel appends every key <= tau_q to the query's candidate list;
-//   3. select:  exact (key, id) top-k of every candidate list;
-//   4. overflow: rows whose list outgrew its capacity are recomputed exactly by chunked
-//               dense keys + select + a final select over the per-chunk winners.
+//   3. select:  exact (key, id) top-k of every candidate list that holds at least k keys
+//               (then every key of the top-k is <= tau_q, so all of them are in the list);
+//   4. overflow: rows whose list outgrew its capacity, or fell short of k, are recomputed
+//               exactly by chunked dense keys + select + a final select over the per-chunk
+//               winners.
 #include <algorithm>
+#include <cmath>
 #include <vector>
 
 #include "va_fallback.hpp"
@@ -168,6 +172,27 @@ va_status rescan_rows(va_context* ctx, KeyProducer& kp, uint32_t N, uint32_t k, 
     return VA_OK;
 }
 
+// The order statistic of the sample that becomes a query's threshold.  The k-th smallest
+// sample key bounds the k-th smallest key of the whole database, so it leaves at least k
+// candidates; with r < k the filter keeps about r·N/S rows instead of k·N/S, and a query is
+// short of k candidates exactly when r of its k nearest rows are in the sample (then the
+// select lists it for the exact fallback).  Treating the strided sample as a random one, that
+// count is Binomial(k, S/N) ~ Poisson(k·S/N); r is the smallest rank whose tail P(>= r) is
+// below 1e-4.  A deletion mask keeps rank k: the candidate count would include masked rows.
+uint32_t sample_rank(const va_context* ctx, uint32_t k, uint64_t S, uint32_t N, bool masked) {
+    if (masked || k <= 1) return k;
+    if (ctx->opt_sample_rank) return uint32_t(std::min<uint64_t>(ctx->opt_sample_rank, k));
+    const double lam = double(k) * double(S) / double(N);
+    double term = std::exp(-lam), cdf = term;  // P(X = r - 1), P(X <= r - 1)
+    uint32_t r = 1;
+    while (r < k && 1.0 - cdf > 1e-4) {
+        term *= lam / double(r);
+        cdf += term;
+        ++r;
+    }
+    return r;
+}
+
 va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t N, uint32_t k,
                           const ScanOutputs& out) {
     SelectArgs base;
@@ -214,6 +239,7 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
     }
     const uint32_t stride = plan.stride;
     const uint64_t cap = plan.cap;
+    const uint32_t rank = sample_rank(ctx, k, S, N, out.skip != nullptr);
     const uint64_t per_q_sample = S * 4;
     const uint32_t qs = plan.qs;
 
@@ -249,7 +275,7 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
         a.ld = int64_t(S);
         a.n = uint32_t(S);
         a.rows = nq;
-        a.k = k;
+        a.k = rank;
         a.out_kth = thr + q0;
         a.key_bits = kp.key_bits();
         VA_CHECK_STATUS(launch_select(ctx, a));
@@ -275,6 +301,7 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
         a.rows = Q;
         a.overflow_count = ovf_cnt;
         a.overflow_rows = ovf_rows;
+        a.min_count = rank < k ? k : 0;
         VA_CHECK_STATUS(launch_select(ctx, a));
     }
     if (device_fb) VA_CHECK_STATUS(pm.count_overflow(ovf_cnt));  // profiling only

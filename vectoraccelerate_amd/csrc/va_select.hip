@@ -143,8 +143,9 @@ __global__ __launch_bounds__(SEL_THREADS) void select_kernel(SelectArgs a) {
     rv.n = a.n;
     if (a.counts) {
         const uint32_t c = a.counts[row];
-        if (c > a.n) {
-            // candidate list overflowed: listed for the exact fallback, which writes the row
+        if (c > a.n || c < a.min_count) {
+            // candidate list overflowed, or too short to be the whole top-k (a threshold below
+            // the k-th key): listed for the exact fallback, which writes the row
             if (tid == 0 && a.overflow_count) {
                 const uint32_t p = atomicAdd(a.overflow_count, 1u);
                 a.overflow_rows[p] = row;
