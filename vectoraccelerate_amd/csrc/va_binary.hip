@@ -159,8 +159,8 @@ __global__ __launch_bounds__(256) void hamming_scan_wide_kernel(HamArgs a) {
 // ---------------------------------------------------------------------------------------
 // Hamming distance as |a| + |b| - 2 a.b over {0,1} vectors: a.b is a dot product of bits,
 // which the gfx950 matrix cores compute exactly with every bit widened to an fp4 (e2m1)
-// value 0 or 1.0 (v_mfma_scale_f32_32x32x64_f8f6f4, unit scales, fp32 sums of integers
-// <= 1024).  fp4 runs the 32x32x64 MFMA at 8 dense TFLOP/s-equivalents per CU per clock pair
+// value 0 or a power of two whose products with the other side's are 1.0
+// (v_mfma_scale_f32_32x32x64_f8f6f4, unit scales, fp32 sums of integers <= 1024).  fp4 runs the 32x32x64 MFMA at 8 dense TFLOP/s-equivalents per CU per clock pair
 // of the int8 rate, so the 2·Q·N·32W bit products cost a fraction of the xor + popcount
 // VALU scan, which is bound by VALU issue (two ops per word per pair).
 // Layout and pipeline follow i8_resq_kernel: a workgroup keeps 256 queries resident in LDS
@@ -170,29 +170,35 @@ __global__ __launch_bounds__(256) void hamming_scan_wide_kernel(HamArgs a) {
 // straight into registers (lane: row l % 32, half h = l / 32 of its words, 16-byte loads;
 // the next tile in flight while this one computes), widens one 32-bit word per k-step into
 // the A fragment and runs 8 MFMAs against the 8 resident query blocks.  K mapping: k-step s
-// takes word h·W/2 + s of the half, widened by the same bit-to-nibble assignment on both
-// sides (widen_word).  No workgroup barrier after the query load.  Filter epilogue as in
-// i8_resq_kernel: a pass is d <= tau, i.e. a.b - |x|/2 >= (|q| - tau)/2 with the accumulators
-// started from -|x|/2, tested with a per-lane maximum first; passes go to a per-wave LDS list
-// flushed when full.
+// takes word h·W/2 + s of the half, widened by the same bit-to-slot assignment on both sides
+// (widen_row, widen_query).  No workgroup barrier after the query load.  Filter epilogue as in
+// i8_resq_kernel: a pass is d <= tau, tested in the form 512 + a.b - |x|/2 >= 512 + (|q| -
+// tau)/2 with the accumulators started from 512 - |x|/2, a per-lane maximum first; passes go to
+// a per-wave LDS list flushed when full.
 namespace hmf {
 constexpr int TQ = 256, NW = 8, WR = 32, TN = NW * WR, LCAP = 80;
 constexpr int STAGE = NW * LCAP * 12;
 constexpr int PA = NW * WR * 4;  // per-wave row popcounts
 constexpr int PB = TQ * 4;       // query popcounts
-constexpr int qstride(int W) { return 16 * W + 16; }
+// resident queries, chunk-major: 16-byte chunk c (of W) of query r at c * 4096 + r * 16, so the
+// fragments of all 8 query blocks of one k-step lie within a 16-bit DS offset of one address
+constexpr int qbytes(int W) { return TQ * 16 * W; }
 constexpr int rows_bytes(int W) { return NW * WR * (W + 1) * 4; }  // per-wave row words, rows W + 1 apart
-constexpr size_t lds_bytes(int W) { return size_t(TQ) * qstride(W) + STAGE + PA + PB + rows_bytes(W); }
+constexpr size_t lds_bytes(int W) { return size_t(qbytes(W)) + STAGE + PA + PB + rows_bytes(W); }
 }  // namespace hmf
 
-// 32 bits -> 32 fp4 nibbles in four dwords, 1 -> 1.0 (e2m1 0b0010), 0 -> 0: nibble i of dword j
-// holds bit 4i + j of the word.  A dot product does not depend on which k slot a bit goes to as
-// long as rows and queries use the same assignment; this one costs one shift and one mask per
-// dword (a bit-i-to-nibble-i spread needs a multiply-based scatter per byte, four times the
-// VALU time, and the scan is bound by MFMA + VALU issue).
-__device__ __forceinline__ uint4 widen_word(uint32_t w) {
-    constexpr uint32_t M = 0x22222222u;
-    return {(w << 1) & M, w & M, (w >> 1) & M, (w >> 2) & M};
+// 32 bits -> 32 fp4 (e2m1) nibbles in four dwords: nibble i of dword j holds bit 4i + j of the
+// word.  A dot product does not depend on which k slot a bit goes to as long as rows and queries
+// use the same assignment, nor on how a set bit's value splits between the two sides as long as
+// every product is 1.  A row bit stays where the mask finds it: nibble bit 0, 1 or 2 is e2m1 0.5,
+// 1.0 or 2.0 (bit 3 is the sign, so bit 4i + 3 moves down one place): five VALU ops per word,
+// which matters because this scan's VALU work adds to its MFMA time.  The query side (widened
+// once, at load) carries the reciprocal weights 2.0, 1.0, 0.5, 0.5.
+__device__ __forceinline__ uint4 widen_row(uint32_t w) {
+    return {w & 0x11111111u, w & 0x22222222u, w & 0x44444444u, (w >> 1) & 0x44444444u};
+}
+__device__ __forceinline__ uint4 widen_query(uint32_t w) {
+    return {(w << 2) & 0x44444444u, w & 0x22222222u, (w >> 2) & 0x11111111u, (w >> 3) & 0x11111111u};
 }
 
 typedef int i32x8h __attribute__((ext_vector_type(8)));
@@ -206,7 +212,7 @@ template <int W>
 __global__ __launch_bounds__(512, 2) void hamming_mfma_kernel(HamArgs a, uint32_t R) {
     using namespace hmf;
     constexpr int HW = W / 2;  // words per lane half = k-steps per tile
-    constexpr int QS = qstride(W);
+    constexpr int QB = qbytes(W);
     extern __shared__ __attribute__((aligned(16))) char lds8[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -226,15 +232,15 @@ __global__ __launch_bounds__(512, 2) void hamming_mfma_kernel(HamArgs a, uint32_
     const uint32_t q0 = qb * TQ;
     const uint32_t qn = min(uint32_t(TQ), Q - q0);
 
-    float* s_pa = reinterpret_cast<float*>(lds8 + TQ * QS + STAGE) + wave * WR;
-    float* s_pb = reinterpret_cast<float*>(lds8 + TQ * QS + STAGE + PA);
-    uint32_t* s_rw = reinterpret_cast<uint32_t*>(lds8 + TQ * QS + STAGE + PA + PB) + wave * WR * (W + 1);
-    // resident queries, widened: word w of query r -> chunk 2 (w % HW) + w / HW of row r
+    float* s_pa = reinterpret_cast<float*>(lds8 + QB + STAGE) + wave * WR;
+    float* s_pb = reinterpret_cast<float*>(lds8 + QB + STAGE + PA);
+    uint32_t* s_rw = reinterpret_cast<uint32_t*>(lds8 + QB + STAGE + PA + PB) + wave * WR * (W + 1);
+    // resident queries, widened: word w of query r -> chunk 2 (w % HW) + w / HW
     for (int e = tid; e < TQ * W; e += 512) {
         const int r = e / W, w = e % W;
         const uint32_t v = uint32_t(r) < qn ? a.q[uint64_t(q0 + r) * W + w] : 0u;
         const int c = 2 * (w % HW) + w / HW;
-        *reinterpret_cast<uint4*>(lds8 + r * QS + 16 * c) = widen_word(v);
+        *reinterpret_cast<uint4*>(lds8 + c * 4096 + r * 16) = widen_query(v);
     }
     for (int r = tid; r < TQ; r += 512) {
         uint32_t pb = 0;
@@ -243,16 +249,17 @@ __global__ __launch_bounds__(512, 2) void hamming_mfma_kernel(HamArgs a, uint32_
         s_pb[r] = float(pb);
     }
     __syncthreads();  // resident queries visible; the only workgroup barrier
-    // pass iff 2 a.b - |x| >= |q| - tau, i.e. a.b - |x|/2 >= (|q| - tau)/2 (halves of integers
-    // below 2^24: exact); the accumulators start from -|x|/2, so the left side is what they hold.
-    // tau >= 32 W passes everything; padding never passes
+    // pass iff 2 a.b - |x| >= |q| - tau, i.e. 512 + a.b - |x|/2 >= 512 + (|q| - tau)/2 (halves of
+    // integers below 2^24: exact).  The accumulators start from 512 - |x|/2, so the left side is
+    // what they hold, and every value on either side is a positive float (|x|, |q|, tau <= 32 W
+    // <= 768), whose bit patterns order like the values: the quick test is an unsigned maximum.
+    // tau >= 32 W passes everything (0); padding never passes (+inf)
     float cq[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
         const uint32_t ql = uint32_t(u * 32 + l32);
         const uint32_t t = a.thr[q0 + (ql < qn ? ql : 0u)];
-        cq[u] = ql >= qn ? __builtin_inff()
-                         : (t >= uint32_t(32 * W) ? -__builtin_inff() : 0.5f * (s_pb[ql] - float(t)));
+        cq[u] = ql >= qn ? __builtin_inff() : (t >= uint32_t(32 * W) ? 0.0f : 512.0f + 0.5f * (s_pb[ql] - float(t)));
     }
 
     // ---- this wave's rows -------------------------------------------------------------------
@@ -272,15 +279,15 @@ __global__ __launch_bounds__(512, 2) void hamming_mfma_kernel(HamArgs a, uint32_
             xw[4 * i + 3] = uint32_t(v[3]);
         }
     };
-    const char* qrd = lds8 + l32 * QS + 16 * hh;
+    const char* qrd = lds8 + hh * 4096 + l32 * 16;
     // The query fragments are the same for every tile; an opaque per-tile zero in their
     // address keeps the compiler from hoisting all 8 x W/2 of them out of the tile loop into
     // registers (it would spill them).
     uint32_t qz = 0;
-    auto rd_q = [&](int st, int u) { return *reinterpret_cast<const i32x4h*>(qrd + qz + u * 32 * QS + 32 * st); };
+    auto rd_q = [&](int st, int u) { return *reinterpret_cast<const i32x4h*>(qrd + qz + st * 8192 + u * 512); };
 
     // ---- filter epilogue ------------------------------------------------------------------
-    uint32_t* s_qi = reinterpret_cast<uint32_t*>(lds8 + TQ * QS) + wave * 3 * LCAP;
+    uint32_t* s_qi = reinterpret_cast<uint32_t*>(lds8 + QB) + wave * 3 * LCAP;
     uint32_t* s_key = s_qi + LCAP;
     uint32_t* s_id = s_key + LCAP;
     uint32_t lc = 0;  // staged passes (wave-uniform)
@@ -300,7 +307,7 @@ __global__ __launch_bounds__(512, 2) void hamming_mfma_kernel(HamArgs a, uint32_
     };
     f32x16h acc[8];
     // Lane value v of a block is row 8 (v >> 2) + 4 hh + (v & 3) of the wave's 32; it holds
-    // a.b - |x|/2 at the end of a tile.  The passes of block u of a tile whose first row id is
+    // 512 + a.b - |x|/2 at the end of a tile.  The passes of block u of a tile whose first row id is
     // r0 and whose rows past N start at lim (this lane half's view) go to the staging list.
     auto block_passes = [&](int u, uint32_t r0, int32_t lim) {
         const float c = cq[u];
@@ -327,7 +334,7 @@ __global__ __launch_bounds__(512, 2) void hamming_mfma_kernel(HamArgs a, uint32_
                 const uint32_t e =
                     lc + __builtin_amdgcn_mbcnt_hi(uint32_t(mk >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mk), 0u));
                 s_qi[e] = q0 + ql;
-                s_key[e] = uint32_t(s_pb[ql] - 2.0f * sv);  // |q| + |x| - 2 a.b, exact below 2^24
+                s_key[e] = uint32_t(s_pb[ql] + 1024.0f - 2.0f * sv);  // |q| + |x| - 2 a.b, exact
                 s_id[e] = r0 + roff + 4 * uint32_t(hh);
             }
             lc += n;
@@ -338,7 +345,7 @@ __global__ __launch_bounds__(512, 2) void hamming_mfma_kernel(HamArgs a, uint32_
     // A tile's row words go through a per-wave LDS buffer (rows W + 1 words apart: the 32 rows
     // of one read fall in distinct banks), so the middle k-steps are a rolled loop that reads
     // its word by step index.  The first k-step takes its word from registers and its starting
-    // values (-|x|/2 of each accumulator's row) from LDS, written at the end of the previous
+    // values (512 - |x|/2 of each accumulator's row) from LDS, written at the end of the previous
     // tile; the last k-step is followed, in the same basic block, by the next tile's row counts
     // and by this tile's quick test (one maximum per block and lane, no branch per block), whose
     // VALU work overlaps the last MFMAs; only a tile with a possible pass branches to the
@@ -350,22 +357,22 @@ __global__ __launch_bounds__(512, 2) void hamming_mfma_kernel(HamArgs a, uint32_
     for (int u = 0; u < 8; ++u) bq[u] = rd_q(0, u);
     uint32_t* myrow = s_rw + l32 * (W + 1) + hh * HW;
     auto widen_operand = [&](uint32_t w) {
-        const uint4 d = widen_word(w);
+        const uint4 d = widen_row(w);
         return fp4_operand(i32x4h{int(d.x), int(d.y), int(d.z), int(d.w)});
     };
-    // -|x|/2 of the tile's rows into LDS: the two halves of a row are the lane pair (l, l + 32),
+    // 512 - |x|/2 of the tile's rows into LDS: the two halves of a row are the lane pair (l, l + 32),
     // which both store the same value (no branch)
     auto row_counts = [&]() {
         uint32_t pa = 0;
 #pragma unroll
         for (int i = 0; i < HW; ++i) pa += __popc(xw[i]);
-        s_pa[l32] = -0.5f * float(pa + __shfl_xor(pa, 32));
+        s_pa[l32] = 512.0f - 0.5f * float(pa + __shfl_xor(pa, 32));
     };
     row_counts();
     for (uint32_t lt = 0; lt < tcount; ++lt) {
 #pragma unroll
         for (int i = 0; i < HW; ++i) myrow[i] = xw[i];
-        f32x16h c0;  // -|x|/2 of the row of each accumulator value
+        f32x16h c0;  // 512 - |x|/2 of the row of each accumulator value
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const f32x4h t = *reinterpret_cast<const f32x4h*>(s_pa + 8 * g + 4 * hh);
@@ -388,7 +395,7 @@ __global__ __launch_bounds__(512, 2) void hamming_mfma_kernel(HamArgs a, uint32_
                 __builtin_amdgcn_sched_barrier(0);
             }
         };
-        k_step(widen_operand(xw[0]), &c0, 1, 1);  // accumulators start from -|x|/2
+        k_step(widen_operand(xw[0]), &c0, 1, 1);  // accumulators start from 512 - |x|/2
         load_tile(lt + 1 < tcount ? lt + 1 : lt, xn);  // the next tile in flight
         // keeps those loads here: with no store after them the compiler would sink them below
         // the k-steps, next to their use, and the tile would wait for HBM
@@ -402,10 +409,10 @@ __global__ __launch_bounds__(512, 2) void hamming_mfma_kernel(HamArgs a, uint32_
         uint32_t hit = 0;  // blocks with a lane whose best value passes (wave-uniform)
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            float m = acc[u][0];
+            uint32_t m = __float_as_uint(acc[u][0]);
 #pragma unroll
-            for (int v = 1; v < 16; ++v) m = fmaxf(m, acc[u][v]);
-            hit |= __ballot(m >= cq[u]) ? (1u << u) : 0u;
+            for (int v = 1; v < 16; ++v) m = max(m, __float_as_uint(acc[u][v]));
+            hit |= __ballot(m >= __float_as_uint(cq[u])) ? (1u << u) : 0u;
         }
         if (hit) {
             const uint64_t r64 = uint64_t(t0 + lt) * TN + uint32_t(wave) * WR;
