@@ -681,11 +681,11 @@ template <int QS>
 constexpr int lds_bytes() { return TQ * QS + RING + STAGE; }
 }  // namespace resq
 
-template <int QS>
+// FULL: d % 64 == 0, so every k-step of a tile reads real bytes (no zero padding step).
+template <int QS, bool FULL>
 __global__ __launch_bounds__(512, 2) void i8_resq_kernel(I8Args a, uint32_t R) {
     using namespace resq;
     constexpr int QBYTES = TQ * QS;
-    constexpr int RPI = 1024 / QS;  // query rows per 1 KiB load instruction
     constexpr int CPR = QS / 16;    // 16-byte chunks per resident query row
     extern __shared__ __attribute__((aligned(16))) char lds8[];
     const int tid = threadIdx.x;
@@ -706,14 +706,16 @@ __global__ __launch_bounds__(512, 2) void i8_resq_kernel(I8Args a, uint32_t R) {
     const uint32_t qn = min(uint32_t(TQ), a.Q - q0);
     const uint32_t lds0 = lds_addr_of(lds8);
 
-    // Resident queries: row r at r * QS, its 16-byte chunk c at position c ^ (r & 15), so the
-    // 16 rows one ds_read_b128 clock serves fall in 16 distinct bank groups.  Rows past Q and
-    // chunks past D load as zeros.
+    // Resident queries, chunk-major: 16-byte chunk c of query r at c * 4096 + r * 16.  The 32
+    // queries of a block read one chunk as 512 contiguous bytes (no bank conflicts, no swizzle)
+    // and the 8 blocks of a k-step lie within a 16-bit DS offset of one address.  A load
+    // instruction fills chunk m / 4 of 64 consecutive queries.  Queries past Q and chunks past
+    // D load as zeros.
     {
         const dma_rsrc qres = make_dma_rsrc(a.q + int64_t(q0) * a.ldq, uint32_t(int64_t(qn - 1) * a.ldq + a.D));
-        for (int m = wave; m < TQ / RPI; m += NW) {
-            const int row = m * RPI + lane / CPR;
-            const int c = (lane % CPR) ^ (row & 15);
+        for (int m = wave; m < 4 * CPR; m += NW) {
+            const int row = (m & 3) * 64 + lane;
+            const int c = m >> 2;
             const uint32_t voff = (uint32_t(row) < qn && uint32_t(16 * c) < a.D)
                                       ? uint32_t(int64_t(row) * a.ldq) + uint32_t(16 * c)
                                       : kDmaSkip;
@@ -743,15 +745,22 @@ __global__ __launch_bounds__(512, 2) void i8_resq_kernel(I8Args a, uint32_t R) {
     const uint32_t dcol = 16u * uint32_t((lane & 1) ^ ((drow >> 3) & 1));
     const uint32_t drow_off = uint32_t(int64_t(drow) * a.ldx);
     uint32_t ltile = 0, lst = 0, lslot = 0;
-    dma_rsrc xres = make_dma_rsrc(a.x, 0u);
+    // The descriptor covers this wave's 32 rows of the tile being loaded; it is rebuilt from
+    // scalars at every load (a few scalar ops), which keeps it out of vector registers.  With
+    // FULL rows the k-step's column goes in the scalar offset and a lane's vector offset is
+    // fixed; rows past N fail the range check through it.
     auto issue = [&]() {
-        if (lst == 0) {  // a new tile: rebase the descriptor on this wave's 32 rows
-            const uint64_t r0 = uint64_t(t0 + ltile) * TN + uint32_t(wave) * WR;
-            const uint32_t rows = r0 < a.N ? uint32_t(min(uint64_t(WR), uint64_t(a.N) - r0)) : 0u;
-            xres = make_dma_rsrc(a.x + int64_t(r0) * a.ldx, rows ? uint32_t(int64_t(rows - 1) * a.ldx + a.D) : 0u);
+        // 32-bit row arithmetic (N <= 2^32 - 256): a 64-bit compare would run on the VALU
+        const uint32_t r0 = (t0 + ltile) * uint32_t(TN) + uint32_t(wave) * uint32_t(WR);
+        const uint32_t rows = r0 < a.N ? min(uint32_t(WR), a.N - r0) : 0u;
+        const dma_rsrc xres =
+            make_dma_rsrc(a.x + int64_t(r0) * a.ldx, rows ? uint32_t(int64_t(rows - 1) * a.ldx + a.D) : 0u);
+        if (FULL) {
+            lds_dma16_so(xres, drow_off + dcol, lst * 32, ring + lslot * uint32_t(SLOT));
+        } else {
+            const uint32_t d = lst * 32 + dcol;
+            lds_dma16(xres, d < a.D ? drow_off + d : kDmaSkip, ring + lslot * uint32_t(SLOT));
         }
-        const uint32_t d = lst * 32 + dcol;
-        lds_dma16(xres, d < a.D ? drow_off + d : kDmaSkip, ring + lslot * uint32_t(SLOT));
         lslot = lslot == NS - 1 ? 0u : lslot + 1;
         if (++lst == nst) {
             lst = 0;
@@ -764,12 +773,9 @@ __global__ __launch_bounds__(512, 2) void i8_resq_kernel(I8Args a, uint32_t R) {
     // step t that consumed fragment u (eight MFMAs cover the read latency); the database
     // fragment alternates between two registers.  The first k-step of a tile starts from a
     // zero accumulator (inline constant), so tiles need no clearing pass.
-    const char* qrd = lds8 + l32 * QS;
+    const char* qrd = lds8 + hh * 4096 + l32 * 16;
     const int xrd = l32 * 32 + 16 * (hh ^ ((l32 >> 3) & 1));
-    auto rd_q = [&](uint32_t st, int u) {
-        const int cq = (int(st) * 2 + hh) ^ (l32 & 15);
-        return *reinterpret_cast<const i32x4v*>(qrd + u * 32 * QS + 16 * cq);
-    };
+    auto rd_q = [&](uint32_t st, int u) { return *reinterpret_cast<const i32x4v*>(qrd + st * 8192 + u * 512); };
     auto rd_x = [&](uint32_t slot) { return *reinterpret_cast<const i32x4v*>(ringp + slot * SLOT + xrd); };
 
     i32x16 acc[8];
@@ -911,7 +917,7 @@ bool resq_ok(const I8Args& a, bool vec) {
 #ifndef VA_I8_RESQ
 #define VA_I8_RESQ 1
 #endif
-    return VA_I8_RESQ && vec && !a.qrow && a.Q > 192 && a.D <= 512 &&
+    return VA_I8_RESQ && vec && !a.qrow && a.Q > 192 && a.D <= 512 && a.N <= 0xFFFFFF00u &&
            uint64_t(resq::TQ - 1) * uint64_t(a.ldq) + a.D <= kDmaMaxBytes &&
            uint64_t(resq::WR - 1) * uint64_t(a.ldx) + a.D <= kDmaMaxBytes;
 }
@@ -924,17 +930,19 @@ va_status launch_i8_resq(va_context* ctx, const I8Args& a) {
     const uint32_t R = std::max<uint32_t>(kXcds, (per + kXcds - 1) / kXcds * kXcds);
     const uint64_t grid = uint64_t(nqb) * R;
     if (grid > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "int8 scan grid too large");
-    if (a.D <= 256) {
-        auto kern = &i8_resq_kernel<256>;
+    const bool full = a.D % 64 == 0;
+    auto go = [&](auto kern, int lds) -> va_status {
         VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes<256>()));
-        kern<<<dim3(uint32_t(grid)), dim3(512), lds_bytes<256>(), ctx->stream>>>(a, R);
-    } else {
-        auto kern = &i8_resq_kernel<512>;
-        VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes<512>()));
-        kern<<<dim3(uint32_t(grid)), dim3(512), lds_bytes<512>(), ctx->stream>>>(a, R);
-    }
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds));
+        kern<<<dim3(uint32_t(grid)), dim3(512), lds, ctx->stream>>>(a, R);
+        return VA_OK;
+    };
+    va_status st;
+    if (a.D <= 256)
+        st = full ? go(&i8_resq_kernel<256, true>, lds_bytes<256>()) : go(&i8_resq_kernel<256, false>, lds_bytes<256>());
+    else
+        st = full ? go(&i8_resq_kernel<512, true>, lds_bytes<512>()) : go(&i8_resq_kernel<512, false>, lds_bytes<512>());
+    if (st != VA_OK) return st;
     VA_CHECK_LAUNCH(ctx);
     return VA_OK;
 }

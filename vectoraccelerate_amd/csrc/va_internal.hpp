@@ -201,6 +201,24 @@ __device__ __forceinline__ void lds_dma16(const dma_rsrc& rsrc, uint32_t voff, u
                  : "memory");
 }
 
+// The same load with a wave-uniform byte offset soff added to every lane's address (an SGPR
+// operand: no per-lane arithmetic).  Callers keep voff + soff inside each in-range lane's row
+// and make out-of-range lanes fail the range check through voff alone, so the result does not
+// depend on whether the check includes soff.
+__device__ __forceinline__ void lds_dma16_so(const dma_rsrc& rsrc, uint32_t voff, uint32_t soff, uint32_t lds_addr) {
+    dma_rsrc r;
+    r[0] = __builtin_amdgcn_readfirstlane(rsrc[0]);
+    r[1] = __builtin_amdgcn_readfirstlane(rsrc[1]);
+    r[2] = __builtin_amdgcn_readfirstlane(rsrc[2]);
+    r[3] = __builtin_amdgcn_readfirstlane(rsrc[3]);
+    const uint32_t l = __builtin_amdgcn_readfirstlane(lds_addr);
+    const uint32_t so = __builtin_amdgcn_readfirstlane(soff);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(l), "v"(voff), "s"(r), "s"(so)
+                 : "memory");
+}
+
 // The one-dword form: lane i's 4 bytes land at lds_addr + 4*i (256 B per wave).  Used as an L2
 // prefetch whose data is not needed.
 __device__ __forceinline__ void lds_dma4(const dma_rsrc& rsrc, uint32_t voff, uint32_t lds_addr) {
