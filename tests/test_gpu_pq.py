@@ -71,6 +71,32 @@ def test_pq_search_matches_oracle(ctx, oracle, N, D, M, K, k, Q):
     np.testing.assert_array_equal(dist.cpu().numpy(), od)
 
 
+@pytest.mark.parametrize("M,scale,Q", [(64, 1.0e4, 37), (16, 1.0e-4, 21), (8, 1.0, 9), (32, 3.0e17, 5)])
+def test_pq_screened_filter_scales_and_odd_queries(ctx, oracle, M, scale, Q):
+    """The fp16-screened filter (K = 256): tables far above fp16's range (each query's scale
+    brings them down; at 3e17 the squared entries overflow float and the screen passes every row),
+    far below it, an odd query count (a pair with one query) and a NaN query, whose keys all tie
+    (ids ascending).  Ids and distances equal the oracle's bit for bit."""
+    from vectoraccelerate_amd import Metal4PQConfig, Metal4PQModel, ProductQuantizationKernel
+
+    N, D, K, k = 30000, 128, 256, 20
+    print(f"pq screened M={M} scale={scale} Q={Q}", flush=True)
+    x = _data(N, D, 11) * np.float32(scale)
+    cb = _init(x, M, K, 12)
+    cfg = Metal4PQConfig(D, M, K)
+    pq = ProductQuantizationKernel(ctx)
+    model = Metal4PQModel(ctx.buffer(cb), cfg)
+    enc = pq.encode(x, model)
+    codes = enc.codes.cpu().numpy()
+    q = _data(Q, D, 13) * np.float32(scale)
+    q[Q // 2, 3] = np.nan
+    idx, dist = pq.search(q, enc, model, k)
+    oi, od = oracle.pq_search(q, cb, codes, M, K, k)
+    np.testing.assert_array_equal(idx.cpu().numpy().view(np.uint32), oi)
+    np.testing.assert_array_equal(dist.cpu().numpy(), od)  # NaN rows: NaN at the same places
+    assert np.isnan(od[Q // 2]).all() and not np.isnan(np.delete(od, Q // 2, axis=0)).any()
+
+
 def test_pq_duplicate_codes_tie_by_row(ctx, oracle):
     """Many rows share a code, so ADC sums tie: the lower row id comes first."""
     from vectoraccelerate_amd import Metal4PQConfig, Metal4PQModel, ProductQuantizationKernel

@@ -298,9 +298,11 @@ __global__ __launch_bounds__(256) void pq_adc_kernel(AdcArgs a) {
 // K = 256 and M in {8, 16, 32, 64}: M and the query group QB = 64 / M are compile-time, so the
 // table entry of (query i, subspace m, code c) is LDS byte 4 c + a constant offset: one
 // ds_read_b32 with an immediate offset and one add per lookup, the code bytes unpacked once per
-// row for all QB queries.  QB x M x 1 KB = 64 KB of tables: two workgroups per CU.
+// row for all QB queries.  QB x M x 1 KB = 64 KB of tables: two workgroups per CU, of kAdcThreads
+// threads each (one row per thread).
+constexpr int kAdcThreads = 512;
 template <int M, bool FILTER>
-__global__ __launch_bounds__(256) void pq_adc_fast(AdcArgs a) {
+__global__ __launch_bounds__(kAdcThreads) void pq_adc_fast(AdcArgs a) {
     constexpr int QB = 64 / M;
     constexpr int MK = M * 256;
     __shared__ float tab[QB * MK];
@@ -309,7 +311,7 @@ __global__ __launch_bounds__(256) void pq_adc_fast(AdcArgs a) {
     for (uint32_t i = 0; i < uint32_t(QB); ++i) {
         const uint32_t qi = i < nqg ? (a.qrow ? a.qrow[g0 + i] : a.q0 + g0 + i) : 0u;
         const float* src = a.tables + int64_t(qi) * MK;
-        for (uint32_t e = threadIdx.x; e < uint32_t(MK); e += 256) tab[i * MK + e] = i < nqg ? src[e] : 0.0f;
+        for (uint32_t e = threadIdx.x; e < uint32_t(MK); e += kAdcThreads) tab[i * MK + e] = i < nqg ? src[e] : 0.0f;
     }
     __syncthreads();
     // the next row's codes are loaded while the current row's lookups run (two workgroups per CU
@@ -333,9 +335,9 @@ __global__ __launch_bounds__(256) void pq_adc_fast(AdcArgs a) {
             }
         }
     };
-    const uint32_t step = gridDim.x * 256;
+    const uint32_t step = gridDim.x * kAdcThreads;
     uint32_t wn[NW4];
-    uint32_t j = blockIdx.x * 256 + threadIdx.x;
+    uint32_t j = blockIdx.x * kAdcThreads + threadIdx.x;
     if (j < a.cols) load_codes(j, wn);
     for (; j < a.cols; j = uint64_t(j) + step < a.cols ? j + step : a.cols) {
         const uint32_t row = a.c0 + j * a.stride;
@@ -377,10 +379,200 @@ va_status launch_adc_fast(va_context* ctx, const AdcArgs& a) {
     constexpr uint32_t QB = 64 / M;
     const uint32_t groups = (a.nq + QB - 1) / QB;
     const uint32_t rb = std::max<uint32_t>(
-        1, uint32_t(std::min<uint64_t>((uint64_t(a.cols) + 255) / 256, std::max<uint64_t>(1, 4096 / groups))));
-    pq_adc_fast<M, FILTER><<<dim3(rb, groups), dim3(256), 0, ctx->stream>>>(a);
+        1, uint32_t(std::min<uint64_t>((uint64_t(a.cols) + kAdcThreads - 1) / kAdcThreads,
+                                       std::max<uint64_t>(1, 4096 * 256 / kAdcThreads / groups))));
+    pq_adc_fast<M, FILTER><<<dim3(rb, groups), dim3(kAdcThreads), 0, ctx->stream>>>(a);
     VA_CHECK_LAUNCH(ctx);
     return VA_OK;
+}
+
+// ---- fp16-screened ADC filter (va_pq_search's filter pass; K = 256, M in {8, 16, 32, 64}) ----
+// Two queries' tables share one 32-bit LDS word per (subspace, code), as fp16 halves: each
+// query's table is scaled by a power of two 2^e_q that puts its largest entry in [2^14, 2^15).
+// One lookup then serves two queries, which halves the LDS instructions of a scan bound by their
+// bank conflicts (random code bytes), and each half is added to an fp32 sum.  The entries are
+// squared distances (>= 0), so with tau_q the query's threshold and S the fp32 scan's sum
+// (S <= tau_q): the exact real sum R <= tau_q / (1 - g) (g = M 2^-24 bounds the fp32 rounding of
+// a sum of M non-negative terms), the fp16 entries h_m satisfy |h_m - 2^e R_m| <= 2^-11 2^e R_m
+// + 2^-14 (normal range; below 2^-14 even a flush to zero stays within 2^-14), and the screened
+// fp32 sum A <= (1 + g)(sum h_m).  Together
+//     A <= 2^e tau_q (1 + 2^-10) + M 2^-14 (1 + g)  <  thr'_q = fma(2^e tau_q, 1 + 2^-9, M 2^-13),
+// so no pair with key <= tau_q is screened out.  A pair that passes is re-scored from the fp32
+// tables in the fp32 scan's order and kept only if its exact key is <= tau_q, so the candidate
+// lists are the fp32 scan's.  A query whose table holds a negative or non-finite entry, or one
+// too large for fp16 after scaling, gets scale 0, which makes its screen pass every row.
+__global__ __launch_bounds__(256) void pq_pack_pairs(const float* __restrict__ tables, uint32_t Q, uint32_t MK,
+                                                     uint32_t* __restrict__ packed, float* __restrict__ scale) {
+    const uint32_t p = blockIdx.x;
+    __shared__ float rmax[2][256];
+    __shared__ uint32_t rbad[2][256];
+    float s[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t q = 2 * p + h;
+        float mx = 0.0f;
+        uint32_t bad = 0;
+        if (q < Q)
+            for (uint32_t e = threadIdx.x; e < MK; e += 256) {
+                const float v = tables[int64_t(q) * MK + e];
+                bad |= !(v >= 0.0f && v <= 3.0e38f);  // negative, NaN or near overflow
+                mx = fmaxf(mx, v);
+            }
+        rmax[h][threadIdx.x] = mx;
+        rbad[h][threadIdx.x] = bad;
+    }
+    __syncthreads();
+    for (uint32_t w = 128; w > 0; w >>= 1) {
+        if (threadIdx.x < w)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                rmax[h][threadIdx.x] = fmaxf(rmax[h][threadIdx.x], rmax[h][threadIdx.x + w]);
+                rbad[h][threadIdx.x] |= rbad[h][threadIdx.x + w];
+            }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const float mx = rmax[h][0];
+        int x = 0;
+        (void)frexpf(mx, &x);  // mx in [2^(x-1), 2^x)
+        const int e = mx > 0.0f ? min(100, max(-100, 15 - x)) : 0;
+        const float sc = ldexpf(1.0f, e);
+        s[h] = (rbad[h][0] || !(mx * sc < 65504.0f)) ? 0.0f : sc;
+        if (threadIdx.x == 0 && 2 * p + h < Q) scale[2 * p + h] = s[h];
+    }
+    for (uint32_t e = threadIdx.x; e < MK; e += 256) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t q = 2 * p + h;
+            // a flagged query (scale 0) packs zeros: its screened sums are 0 and pass (NaN * 0 would not)
+            const float v = q < Q && s[h] != 0.0f ? tables[int64_t(q) * MK + e] * s[h] : 0.0f;
+            w |= uint32_t(__builtin_bit_cast(uint16_t, _Float16(v))) << (16 * h);
+        }
+        packed[int64_t(p) * MK + e] = w;
+    }
+}
+
+// acc + the fp16 value in the low (HI = 0) or high half of v, in one VALU op (v_fma_mix_f32:
+// half x 1.0 + acc, rounded once, so the same value as a conversion and an fp32 add)
+template <int HI>
+__device__ __forceinline__ float add_half(float acc, uint32_t v) {
+    float d;
+    if (HI)
+        asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(v), "v"(acc));
+    else
+        asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(v), "v"(acc));
+    return d;
+}
+
+template <int M>
+__global__ __launch_bounds__(kAdcThreads) void pq_adc_screen(AdcArgs a, const uint32_t* __restrict__ packed,
+                                                              const float* __restrict__ scale) {
+    constexpr int QP = 64 / M;  // query pairs per workgroup: QP x M x 1 KB = 64 KB of LDS
+    constexpr int MK = M * 256;
+    __shared__ uint32_t tab[QP * MK];
+    const uint32_t p0 = blockIdx.y * QP;
+    const uint32_t np = min(uint32_t(QP), (a.nq + 1) / 2 - p0);
+    for (uint32_t i = 0; i < uint32_t(QP); ++i)
+        for (uint32_t e = threadIdx.x; e < uint32_t(MK); e += kAdcThreads)
+            tab[i * MK + e] = i < np ? packed[int64_t(p0 + i) * MK + e] : 0u;
+    // screen thresholds (query index past nq: never passes)
+    float thr[2 * QP];
+#pragma unroll
+    for (int i = 0; i < 2 * QP; ++i) {
+        const uint32_t q = 2 * p0 + uint32_t(i);
+        float t = -INFINITY;
+        if (q < a.nq) {
+            const uint32_t tk = a.thr[q];
+            const float sc = scale[q];
+            t = (sc == 0.0f || tk >= key_of_float(INFINITY))
+                    ? INFINITY
+                    : fmaf(float_of_key(tk) * sc, 1.0f + 0x1p-9f, float(M) * 0x1p-13f);
+        }
+        thr[i] = t;
+    }
+    __syncthreads();
+    constexpr int NW4 = M / 4;
+    auto load_codes = [&](uint32_t j, uint32_t (&w)[NW4]) {
+        const uint4* cr = reinterpret_cast<const uint4*>(a.codes + int64_t(j) * M);
+        if constexpr (M == 8) {
+            const uint2 v = *reinterpret_cast<const uint2*>(cr);
+            w[0] = v.x;
+            w[1] = v.y;
+        } else {
+#pragma unroll
+            for (int b = 0; b < M / 16; ++b) {
+                const uint4 v = cr[b];
+                w[4 * b] = v.x;
+                w[4 * b + 1] = v.y;
+                w[4 * b + 2] = v.z;
+                w[4 * b + 3] = v.w;
+            }
+        }
+    };
+    // exact re-score of (query q, row j) in the fp32 scan's order; appended if key <= tau_q
+    auto rescore = [&](uint32_t q, uint32_t j, const uint32_t (&off)[M]) {
+        const float* t = a.tables + int64_t(q) * MK;
+        float s = 0.0f;
+#pragma unroll
+        for (int m = 0; m < M; ++m) s += t[m * 256 + off[m]];
+        const uint32_t key = key_of_float(s);
+        if (key <= a.thr[q]) {
+            const uint32_t pos = atomicAdd(a.cnt + q, 1u);
+            if (pos < a.cap) {
+                const int64_t o = int64_t(q) * a.cap + pos;
+                a.cand_key[o] = key;
+                a.cand_id[o] = j;
+            }
+        }
+    };
+    const uint32_t step = gridDim.x * kAdcThreads;
+    uint32_t wn[NW4];
+    uint32_t j = blockIdx.x * kAdcThreads + threadIdx.x;
+    if (j < a.cols) load_codes(j, wn);
+    for (; j < a.cols; j = uint64_t(j) + step < a.cols ? j + step : a.cols) {
+        uint32_t w[NW4];
+#pragma unroll
+        for (int b = 0; b < NW4; ++b) w[b] = wn[b];
+        if (uint64_t(j) + step < a.cols) load_codes(j + step, wn);
+        uint32_t off[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) off[m] = (w[m / 4] >> (8 * (m % 4))) & 0xFFu;
+#pragma unroll
+        for (int i = 0; i < QP; ++i) {
+            if (uint32_t(i) >= np) break;
+            float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const uint32_t v = tab[i * MK + m * 256 + off[m]];
+                s0 = add_half<0>(s0, v);
+                s1 = add_half<1>(s1, v);
+            }
+            if (s0 <= thr[2 * i]) rescore(2 * (p0 + i), j, off);
+            if (s1 <= thr[2 * i + 1]) rescore(2 * (p0 + i) + 1, j, off);
+        }
+    }
+}
+
+// The screened filter of a whole search (queries 0..nq-1, rows 0..cols-1, dense codes).
+template <int M>
+va_status launch_adc_screen(va_context* ctx, const AdcArgs& a, const uint32_t* packed, const float* scale) {
+    constexpr uint32_t QP = 64 / M;
+    const uint32_t groups = ((a.nq + 1) / 2 + QP - 1) / QP;
+    const uint32_t rb = std::max<uint32_t>(
+        1, uint32_t(std::min<uint64_t>((uint64_t(a.cols) + kAdcThreads - 1) / kAdcThreads,
+                                       std::max<uint64_t>(1, 4096 * 256 / kAdcThreads / groups))));
+    pq_adc_screen<M><<<dim3(rb, groups), dim3(kAdcThreads), 0, ctx->stream>>>(a, packed, scale);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
+
+// Whether the screened filter takes a search: the fast kernel's shapes, a grid within range.
+bool adc_screen_ok(uint32_t Q, uint32_t M, uint32_t K, const uint8_t* codes) {
+    if (K != 256 || !(M == 8 || M == 16 || M == 32 || M == 64) || (reinterpret_cast<uintptr_t>(codes) & 15) != 0)
+        return false;
+    return ((uint64_t(Q) + 1) / 2 + 64 / M - 1) / (64 / M) <= 65535;
 }
 
 // Query groups of QB (as many tables as fit in 160 KB of LDS, at most 16) on grid.y, in launches
@@ -436,6 +628,9 @@ struct AdcProducer final : KeyProducer {
     const uint8_t* codes;
     const float* tables;
     uint32_t Q, N, M, K;
+    // fp16 pair tables and scales of the screened filter (nullptr: the fp32 filter)
+    const uint32_t* packed = nullptr;
+    const float* scale = nullptr;
     va_status fallback_pass(const FbArgs& a, int pass) override {
         return fb_launch_pass(ctx, FbAdc{codes, tables, N, M, K}, a, pass);
     }
@@ -471,6 +666,14 @@ struct AdcProducer final : KeyProducer {
         a.cand_key = ckey;
         a.cand_id = cid;
         a.cap = cap;
+        if (packed) {
+            switch (M) {
+                case 8: return launch_adc_screen<8>(ctx, a, packed, scale);
+                case 16: return launch_adc_screen<16>(ctx, a, packed, scale);
+                case 32: return launch_adc_screen<32>(ctx, a, packed, scale);
+                default: return launch_adc_screen<64>(ctx, a, packed, scale);
+            }
+        }
         return launch_adc<true>(ctx, a);
     }
 };
@@ -650,19 +853,33 @@ va_status va_pq_search(va_context* ctx, const float* queries, uint32_t num_queri
     VA_REQUIRE(ctx, k >= 1 && k <= VA_MAX_K, "k must be in [1, %u], got %u", VA_MAX_K, k);
     if (num_queries == 0) return VA_OK;
     va::DeviceGuard g(ctx->device);
-    // the tables live in the context's side buffer: the call returns without waiting for the scan
+    // the tables (and the screened filter's fp16 pair tables and scales) live in the context's
+    // side buffer: the call returns without waiting for the scan
+    const bool screen = va::adc_screen_ok(num_queries, M, K, codes);
+    const size_t tbytes = (size_t(num_queries) * M * K * 4 + 255) & ~size_t(255);
+    const size_t pbytes = screen ? (size_t(num_queries + 1) / 2 * M * K * 4 + 255) & ~size_t(255) : 0;
+    const size_t sbytes = screen ? size_t(num_queries) * 4 : 0;
     void* side = nullptr;
-    VA_CHECK_STATUS(va::side_reserve(ctx, size_t(num_queries) * M * K * 4, &side));
+    VA_CHECK_STATUS(va::side_reserve(ctx, tbytes + pbytes + sbytes, &side));
     float* tables = static_cast<float*>(side);
+    uint32_t* packed = screen ? reinterpret_cast<uint32_t*>(static_cast<char*>(side) + tbytes) : nullptr;
+    float* scale = screen ? reinterpret_cast<float*>(static_cast<char*>(side) + tbytes + pbytes) : nullptr;
     for (uint32_t q0 = 0; q0 < num_queries; q0 += 65535) {
         const uint32_t nq = std::min<uint32_t>(65535, num_queries - q0);
         VA_CHECK_STATUS(va_pq_distance_tables(ctx, queries + int64_t(q0) * dim, nq, dim, M, K, codebooks,
                                               tables + int64_t(q0) * M * K));
     }
+    if (screen) {
+        va::pq_pack_pairs<<<dim3((num_queries + 1) / 2), dim3(256), 0, ctx->stream>>>(tables, num_queries, M * K,
+                                                                                        packed, scale);
+        VA_CHECK_LAUNCH(ctx);
+    }
     va::AdcProducer kp;
     kp.ctx = ctx;
     kp.codes = codes;
     kp.tables = tables;
+    kp.packed = packed;
+    kp.scale = scale;
     kp.Q = num_queries;
     kp.N = num_vectors;
     kp.M = M;
