@@ -373,7 +373,7 @@ def run_c3(ctx, a, cpu: bool):
         "quantize_database_ms": qms,
         "quantize_hbm_gbs": (N * D * 4 * 2 + N * D) / (qms * 1e-3) / 1e9,
         "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK["int8_mfma_tops"], "unit": "TOP/s",
-                     "frac": tops / PEAK["int8_mfma_tops"], "kernel": "i8_resq_kernel<512>",
+                     "frac": tops / PEAK["int8_mfma_tops"], "kernel": "i8_resq_kernel<512, true>",
                      "algorithmic": f"2*Q*N*D = {ops:.4g} int ops per launch", **counted(COUNTERS_I8)},
     }
     log(f"configs[2] int8 top-10: {ms:.3f} ms/step = {res['qps']:.0f} QPS; scan {ph['scan_ms']:.3f} ms = "
@@ -669,7 +669,9 @@ def run_pq(ctx, a, cpu: bool):
     lookups = float(Q) * N * M
     scan_ms = tim.get("scan_ms") if tim else None
     rate = lookups / (scan_ms * 1e-3) / 1e12 if scan_ms else None
-    # LDS: 128 bytes per clock per CU = 32 four-byte lookups; 256 CUs at 2.4 GHz
+    # LDS: 128 bytes per clock per CU = 32 four-byte lookups; 256 CUs at 2.4 GHz.  The filter pass
+    # reads fp16 pair tables (one 4-byte read carries two queries' entries), so its table lookups
+    # per second can exceed the 4-byte read rate it is compared with.
     lds_peak = 256 * 32 * 2.4e9 / 1e12
     xe = torch.randn(1_000_000, D, device="cuda", generator=g)
     ce = ctx.empty((1_000_000, M), torch.uint8)
@@ -684,8 +686,10 @@ def run_pq(ctx, a, cpu: bool):
         "ms_per_step": ms, "qps": Q / (ms * 1e-3), "scan_timings": tim,
         "encode_rows_per_s": 1_000_000 / enc_s,
         "roofline": {"bound": "lds", "achieved": rate, "peak": lds_peak, "unit": "T lookups/s",
-                     "frac": (rate / lds_peak) if rate else None, "kernel": "pq_adc_fast<16, true> (filter pass)",
-                     "algorithmic": f"Q*N*M = {lookups:.4g} table lookups (4 B each, LDS) per scan", **counted(COUNTERS_PQ)},
+                     "frac": (rate / lds_peak) if rate else None, "kernel": "pq_adc_screen<16> (filter pass)",
+                     "algorithmic": f"Q*N*M = {lookups:.4g} table lookups per scan (fp16 pair tables in LDS: "
+                                    "one 4-byte read serves two queries; exact fp32 re-score of the passes)",
+                     **counted(COUNTERS_PQ)},
     }
     log(f"PQ ADC top-10: {ms:.3f} ms/step = {res['qps']:.0f} QPS; filter scan {scan_ms} ms = "
         f"{rate if rate is None else round(rate, 2)} T lookups/s; encode {res['encode_rows_per_s']:.3g} rows/s")
