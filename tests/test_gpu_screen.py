@@ -121,6 +121,27 @@ def test_screen_overflow_falls_back(ctx):
     assert st["overflow_rows"] > 0, st
 
 
+@pytest.mark.parametrize("rank", [1, 3, 0])
+def test_screen_speculative_rank_checks(ctx, rank):
+    """A threshold below the sample's k-th upper bound (rank 1 or 3, or the automatic rank): a
+    query whose list holds fewer than k candidates, or whose k-th candidate upper bound exceeds
+    the threshold, takes the exact fallback.  Half the queries have an exact copy on a sampled
+    row (16,384 rows sampled of 60,000: stride 3), which puts their threshold at that row."""
+    from vectoraccelerate_amd import _lib
+
+    g = np.random.default_rng(40 + rank)
+    x = g.standard_normal((60000, 64), dtype=np.float32)
+    q = g.standard_normal((200, 64), dtype=np.float32)
+    x[::3][:100] = q[:100]
+    ctx.set_option(_lib.VA_OPT_SAMPLE_RANK, rank)
+    try:
+        _, _, st = _same(ctx, L2SQ, q, x, 30)
+    finally:
+        ctx.set_option(_lib.VA_OPT_SAMPLE_RANK, 0)
+    if rank:
+        assert st["overflow_rows"] > 0, st
+
+
 def test_large_magnitudes_scale_exactly(ctx):
     """Query scaling is a power of two: large and small but finite data give the fp32 result."""
     g = np.random.default_rng(13)

@@ -471,9 +471,11 @@ struct ScanPlan {
     uint64_t cap = 0;
     uint32_t qs = 1;
 };
-// screened: the plan of the fp16 screening scan, whose candidate appends cost more than its
-// sample pass up to a sample of N/32 rows (N/64 otherwise)
-ScanPlan plan_scan(const va_context* ctx, uint32_t Q, uint32_t N, uint32_t k, bool screened = false);
+// The order statistic of the sample that becomes a query's threshold (k, or a smaller rank whose
+// lists are checked before use; va_scan.hip)
+uint32_t sample_rank(const va_context* ctx, uint32_t k, uint64_t S, uint32_t N, bool masked);
+// sample size, strided sample step and candidate capacity of an exact top-k scan
+ScanPlan plan_scan(const va_context* ctx, uint32_t Q, uint32_t N, uint32_t k);
 
 // Exact top-k of the listed query rows (device list) by dense keys over the whole database in
 // chunks (the path of queries whose candidate list overflowed).  Writes base's outputs at the

@@ -85,15 +85,17 @@ size_t dense_budget(const va_context* ctx) {
     return ctx->fixed_scratch ? std::min(kArena, ctx->fixed_scratch_bytes / 4) : kArena;
 }
 
-ScanPlan plan_scan(const va_context* ctx, uint32_t Q, uint32_t N, uint32_t k, bool screened) {
+ScanPlan plan_scan(const va_context* ctx, uint32_t Q, uint32_t N, uint32_t k) {
     ScanPlan p;
-    // Sample size: N/64 rows (N/32 for the screening scan) keeps ~64k (~32k) candidates per
-    // query, but the dense sample costs Q*S keys, so it is capped at dense_budget() bytes of keys
-    // in total (16384 rows minimum).
+    // Sample size: N/64 rows, so that a threshold at the sample's r-th key keeps ~64r candidates
+    // per query (sample_rank); the dense sample costs Q*S keys, so it is capped at dense_budget()
+    // bytes of keys in total (16384 rows minimum).  (The fp16 screening scan took N/32 while its
+    // threshold was the sample's k-th bound; with the checked smaller rank N/64 is faster there too:
+    // configs[1] 3.98 -> 3.84 ms per search.)
     const uint64_t budget = dense_budget(ctx);
     p.S = ctx->opt_sample_rows
               ? ctx->opt_sample_rows
-              : std::max<uint64_t>(kMinSample, std::min<uint64_t>(N / (screened ? 32 : 64), budget / 4 / Q));
+              : std::max<uint64_t>(kMinSample, std::min<uint64_t>(N / 64, budget / 4 / Q));
     p.direct = p.S >= N;
     if (p.direct) return p;
     p.stride = uint32_t(N / p.S);

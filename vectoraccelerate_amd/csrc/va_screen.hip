@@ -879,12 +879,16 @@ __global__ __launch_bounds__(256) void screen_bound_kernel(ScreenArgs a, float* 
 }
 
 // ---- rerank list: the candidates whose lower bound is within the k-th upper bound -------------
-// One workgroup per query.  Lists that overflowed (count > cap) or whose rerank list outgrows
-// rcap are put on the overflow list and left empty here.
+// One workgroup per query.  Lists that overflowed (count > cap), fell short of min_count (both
+// listed by the candidate select), whose k-th upper bound exceeds the threshold they were
+// filtered with (thr non-null: a threshold below the sample's k-th bound, which holds only when k
+// candidates lie within it) or whose rerank list outgrows rcap take the fallback and are left
+// empty here; the last two are listed here.
 __global__ __launch_bounds__(256) void screen_compact_kernel(const uint32_t* __restrict__ cnt,
                                                              const uint32_t* __restrict__ cand_lo,
                                                              const uint32_t* __restrict__ cand_id,
                                                              const uint32_t* __restrict__ bound, uint32_t cap,
+                                                             uint32_t min_count, const uint32_t* __restrict__ thr,
                                                              uint32_t* __restrict__ rr, uint32_t* __restrict__ rcount,
                                                              uint32_t rcap, uint32_t* __restrict__ ovf_cnt,
                                                              uint32_t* __restrict__ ovf_rows,
@@ -893,9 +897,18 @@ __global__ __launch_bounds__(256) void screen_compact_kernel(const uint32_t* __r
     const uint32_t q = blockIdx.x;
     const int tid = threadIdx.x;
     const uint32_t n = cnt[q];
-    if (n > cap) {
-        // the candidate select has already listed this query as overflowed
+    if (n > cap || n < min_count) {
+        // the candidate select has already listed this query for the fallback
         if (tid == 0) rcount[q] = 0;
+        return;
+    }
+    if (thr && bound[q] > thr[q]) {
+        // fewer than k candidates have an upper bound within the threshold: the list may miss
+        // a row of the top-k
+        if (tid == 0) {
+            rcount[q] = 0;
+            ovf_rows[atomicAdd(ovf_cnt, 1u)] = q;
+        }
         return;
     }
     if (tid == 0) s_n = 0;
@@ -1052,8 +1065,8 @@ va_status screen_list_bounds(va_context* ctx, const ScreenBound& b, const float4
 va_status screen_compact(va_context* ctx, const uint32_t* cnt, const uint32_t* cand_lo, const uint32_t* cand_id,
                          const uint32_t* bound, uint32_t cap, uint32_t Q, uint32_t* rr, uint32_t* rcount, uint32_t rcap,
                          uint32_t* ovf_cnt, uint32_t* ovf_rows) {
-    screen_compact_kernel<<<dim3(Q), dim3(256), 0, ctx->stream>>>(cnt, cand_lo, cand_id, bound, cap, rr, rcount, rcap,
-                                                                 ovf_cnt, ovf_rows, ovf_cnt + 1);
+    screen_compact_kernel<<<dim3(Q), dim3(256), 0, ctx->stream>>>(cnt, cand_lo, cand_id, bound, cap, 0u, nullptr, rr,
+                                                                 rcount, rcap, ovf_cnt, ovf_rows, ovf_cnt + 1);
     VA_CHECK_LAUNCH(ctx);
     return VA_OK;
 }
@@ -1064,7 +1077,7 @@ bool screen_applies(const va_context* ctx, const ScreenInput& in, uint32_t k) {
     if (in.D % 4 != 0 || (reinterpret_cast<uintptr_t>(in.x) & 15) != 0 ||
         (reinterpret_cast<uintptr_t>(in.q) & 15) != 0)
         return false;
-    const ScanPlan plan = plan_scan(ctx, in.Q, in.N, k, true);
+    const ScanPlan plan = plan_scan(ctx, in.Q, in.N, k);
     if (plan.direct) return false;
     if (!offsets_fit(uint64_t(plan.stride) * in.D, in.D)) return false;
     if (ctx->opt_screen == 2) return true;
@@ -1076,9 +1089,12 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
                              const ScanOutputs& out) {
     const uint32_t Q = in.Q, N = in.N, D = in.D;
     const uint32_t Dp = padded_dim(D);
-    const ScanPlan plan = plan_scan(ctx, Q, N, k, true);
+    const ScanPlan plan = plan_scan(ctx, Q, N, k);
     const uint64_t S = plan.S;
     const uint64_t cap = plan.cap;
+    // the threshold: the sample's rank-th smallest upper bound (checked in the compaction when
+    // rank < k)
+    const uint32_t rank = sample_rank(ctx, k, S, N, out.skip != nullptr);
     // rerank capacity: k plus the band of rows whose interval straddles the k-th bound (the
     // launch covers only the longest list actually built)
     const uint64_t rcap = std::min<uint64_t>(N, (std::max<uint64_t>(2ull * k + 256, cap / 4) + 127) / 128 * 128);
@@ -1163,7 +1179,7 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
         sel.ld = int64_t(S);
         sel.n = uint32_t(S);
         sel.rows = nq;
-        sel.k = k;
+        sel.k = rank;
         sel.out_kth = thr + q0;
         VA_CHECK_STATUS(launch_select(ctx, sel));
     }
@@ -1215,11 +1231,14 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
         a.out_kth = ubound;
         a.overflow_count = ovf_cnt;
         a.overflow_rows = ovf_rows;
+        a.min_count = rank < k ? k : 0;
         VA_CHECK_STATUS(launch_select(ctx, a));
     }
     // ---- 5. rerank lists ------------------------------------------------------------------------
-    screen_compact_kernel<<<dim3(Q), dim3(256), 0, ctx->stream>>>(cnt, clo, cid, ubound, uint32_t(cap), rr, rcount,
-                                                                 uint32_t(rcap), ovf_cnt, ovf_rows, ovf_cnt + 1);
+    screen_compact_kernel<<<dim3(Q), dim3(256), 0, ctx->stream>>>(cnt, clo, cid, ubound, uint32_t(cap),
+                                                                 rank < k ? k : 0u, rank < k ? thr : nullptr, rr,
+                                                                 rcount, uint32_t(rcap), ovf_cnt, ovf_rows,
+                                                                 ovf_cnt + 1);
     VA_CHECK_LAUNCH(ctx);
     // Without the device fallback the overflow count is read back (one synchronisation).
     uint32_t n_ovf = 0;
