@@ -682,6 +682,8 @@ __global__ __launch_bounds__(1024, 1) void screen16_kernel(ScreenArgs a) {
     // the direct loads in flight); this wave's LDS reads are complete before it
     auto barrier = [&]() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
+    // the tile's squared row norms: loaded now (one register), used after the main loop
+    const float xn_t = tid < TN && uint32_t(tid) < rc ? a.xn[rs + uint32_t(tid)] : 0.0f;
     // per wave and stage: 2 LPW direct loads, plus one prefetch in waves 0-3
     issue(0);
     issue(1);
@@ -722,7 +724,7 @@ __global__ __launch_bounds__(1024, 1) void screen16_kernel(ScreenArgs a) {
     const float tiny = a.op == OP_COS_DIST ? 8.0f * a.c0x : 0.0f;
     if (tid < TN) {
         const uint32_t r = uint32_t(tid);
-        const float t = r < rc ? a.xn[rs + r] : 0.0f;
+        const float t = xn_t;
         const float nx = __builtin_amdgcn_sqrtf(t);
         xxs[r] = t;
         const bool flag = !(t < 4.29e9f) || nx < tiny;
