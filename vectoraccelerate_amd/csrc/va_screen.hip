@@ -732,6 +732,26 @@ __global__ __launch_bounds__(1024, 1) void screen16_kernel(ScreenArgs a) {
         nxp[r] = flag ? __builtin_nanf("") : nx;
     }
     __syncthreads();
+    // the (|x|^2, |x|) box of each 4-row group, NaN when a row of it is flagged: a lane's 32 rows
+    // are 8 whole groups, so its quick-rejection box is 8 lookups instead of 32 rows' worth of
+    // min/max (that loop was a large share of the epilogue's vector work)
+    __shared__ float4 gbox[TN / 4];
+    if (tid < TN / 4) {
+        float4 b = {INFINITY, -INFINITY, INFINITY, -INFINITY};
+        bool f = false;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float xx = xxp[4 * tid + e], nx = nxp[4 * tid + e];
+            f |= !(xx == xx) || !(nx == nx);
+            b.x = fminf(b.x, xx);
+            b.y = fmaxf(b.y, xx);
+            b.z = fminf(b.z, nx);
+            b.w = fmaxf(b.w, nx);
+        }
+        if (f) b.x = __builtin_nanf("");
+        gbox[tid] = b;
+    }
+    __syncthreads();
 
     // ---- filter epilogue: lane (l32, hh) holds query wq*64 + 32n + l32 against rows
     // wn*64 + 32m + 8j + 4hh + e in acc[m][n][4j + e]; t = 16m + 4j + e indexes its 32 values.
@@ -743,23 +763,22 @@ __global__ __launch_bounds__(1024, 1) void screen16_kernel(ScreenArgs a) {
     // disable it); lanes l and l + 32 hold the same query, so one atomic reserves both lanes'
     // places; the appends read the values back from LDS.
     auto row_of = [&](int t) { return wn * WN + 32 * (t >> 4) + 8 * ((t >> 2) & 3) + 4 * hh + (t & 3); };
-    uint32_t valid = 0;
+    uint32_t valid = ~0u;
+    if (rc < TN) {
+        valid = 0;
+#pragma unroll 1
+        for (int t = 0; t < 32; ++t) valid |= uint32_t(uint32_t(row_of(t)) < rc) << t;
+    }
     float bxlo = INFINITY, bxhi = -INFINITY, bnlo = INFINITY, bnhi = -INFINITY;
     bool bflag = false;
-#pragma unroll 1
-    for (int t = 0; t < 32; t += 4) {
-        const int r = row_of(t);  // rows r .. r + 3
-        const f32x4v xx = *reinterpret_cast<const f32x4v*>(xxp + r);
-        const f32x4v nx = *reinterpret_cast<const f32x4v*>(nxp + r);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            valid |= uint32_t(uint32_t(r + e) < rc) << (t + e);
-            bflag |= !(xx[e] == xx[e]) || !(nx[e] == nx[e]);
-            bxlo = fminf(bxlo, xx[e]);
-            bxhi = fmaxf(bxhi, xx[e]);
-            bnlo = fminf(bnlo, nx[e]);
-            bnhi = fmaxf(bnhi, nx[e]);
-        }
+    for (int c = 0; c < 8; ++c) {
+        const float4 b = gbox[row_of(4 * c) >> 2];  // rows 4c .. 4c + 3 of the lane: one group
+        bflag |= !(b.x == b.x);
+        bxlo = fminf(bxlo, b.x);
+        bxhi = fmaxf(bxhi, b.y);
+        bnlo = fminf(bnlo, b.z);
+        bnhi = fmaxf(bnhi, b.w);
     }
     f32x4v* dump = reinterpret_cast<f32x4v*>(lds + wave * 8192) + lane;  // [t / 4][lane]
     auto block = [&](auto NC) {
