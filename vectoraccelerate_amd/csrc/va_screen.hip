@@ -755,8 +755,9 @@ __global__ __launch_bounds__(1024, 1) void screen16_kernel(ScreenArgs a) {
 
     // ---- filter epilogue: lane (l32, hh) holds query wq*64 + 32n + l32 against rows
     // wn*64 + 32m + 8j + 4hh + e in acc[m][n][4j + e]; t = 16m + 4j + e indexes its 32 values.
-    // One query block at a time goes to the wave's 8 KiB of the (now free) stage LDS, so only the
-    // other block's accumulators stay in registers; the pre-test over the 32 values builds a bit
+    // One query block at a time; a block that the quick rejection below does not settle goes to
+    // the wave's 8 KiB of the (now free) stage LDS, so only the other block's accumulators stay
+    // in registers while its pre-test runs; the pre-test over the 32 values builds a bit
     // mask without branches (after a quick rejection: the right-hand side A|x|^2 + B|x| + C over
     // the lane's rows is bounded below at the corner of their (|x|^2, |x|) box that A's and B's
     // signs select, so a lane whose largest value is below it passes nothing; flagged (NaN) rows
@@ -783,15 +784,6 @@ __global__ __launch_bounds__(1024, 1) void screen16_kernel(ScreenArgs a) {
     f32x4v* dump = reinterpret_cast<f32x4v*>(lds + wave * 8192) + lane;  // [t / 4][lane]
     auto block = [&](auto NC) {
         constexpr int n = decltype(NC)::value;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            f32x4v v;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = acc[c >> 2][n][4 * (c & 3) + e];
-            dump[c * 64] = v;
-        }
-        // re-read the row norms from LDS below rather than keep the bounds pass's copies live
-        asm volatile("" ::: "memory");
         const uint32_t qt = uint32_t(wq * WQ + 32 * n + l32);
         const uint32_t qi = qs + min(qt, qc - 1);
         const float4 qinf = a.qinfo[qi];
@@ -806,6 +798,16 @@ __global__ __launch_bounds__(1024, 1) void screen16_kernel(ScreenArgs a) {
         }
         uint32_t mk = 0;
         if (!skip) {
+            // only a block that may pass goes through LDS (most are rejected from registers above)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                f32x4v v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = acc[c >> 2][n][4 * (c & 3) + e];
+                dump[c * 64] = v;
+            }
+            // re-read the row norms from LDS below rather than keep the bounds pass's copies live
+            asm volatile("" ::: "memory");
 #pragma unroll 2
             for (int c = 0; c < 8; ++c) {
                 const int r = row_of(4 * c);
