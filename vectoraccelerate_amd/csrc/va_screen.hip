@@ -587,19 +587,23 @@ constexpr int TQ = 256, TN = 256, KC = 64;
 constexpr int ROWB = KC * 2;              // bytes per LDS row
 constexpr int OPB = TQ * ROWB;            // one operand per stage (32 KiB)
 constexpr int STAGE = 2 * OPB;            // queries, then rows
-constexpr int WAVES = 16;
-constexpr int WQ = 64, WN = 64;           // a wave's queries x rows
-constexpr int LPW = OPB / 1024 / WAVES;   // 1 KiB direct loads per wave per operand per stage (2)
 constexpr int LDS = 2 * STAGE;            // two stages
+// the wave layout of the launch: waves per workgroup and 32-query blocks per wave
+constexpr int kWaves = 16, kQueryBlocks = 2;
 }  // namespace s16
 
-__global__ __launch_bounds__(1024, 1) void screen16_kernel(ScreenArgs a) {
+// WAVES waves of (32 NQB queries) x 64 rows; four waves per SIMD at 16 waves, two at 8
+template <int WAVES, int NQB>
+__global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(ScreenArgs a) {
     using namespace s16;
+    constexpr int WQ = 32 * NQB, WN = 64;     // a wave's queries x rows
+    constexpr int QW = TQ / WQ;               // waves along the queries
+    constexpr int LPW = OPB / 1024 / WAVES;   // 1 KiB direct loads per wave per operand per stage
     extern __shared__ __attribute__((aligned(1024))) char lds[];
     __shared__ __attribute__((aligned(16))) float norms[3 * TN];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wq = wave & 3, wn = wave >> 2, l32 = lane & 31, hh = lane >> 5;
+    const int wq = wave % QW, wn = wave / QW, l32 = lane & 31, hh = lane >> 5;
     // XCD-aware order, as screen_kernel
     const uint32_t nqb = (a.Q + TQ - 1) / TQ;
     const uint32_t xcd = blockIdx.x % kXcds, seq = blockIdx.x / kXcds;
@@ -646,36 +650,36 @@ __global__ __launch_bounds__(1024, 1) void screen16_kernel(ScreenArgs a) {
     const uint32_t a_off = uint32_t(OPB + (wn * WN + l32) * ROWB);
     const uint32_t b_off = uint32_t((wq * WQ + l32) * ROWB);
 
-    f32x16 acc[2][2];
+    f32x16 acc[2][NQB];
 #pragma unroll
     for (int m = 0; m < 2; ++m)
 #pragma unroll
-        for (int n = 0; n < 2; ++n)
+        for (int n = 0; n < NQB; ++n)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[m][n][v] = 0.0f;
 
-    h8v fa[2][2], fb[2][2];
+    h8v fa[2][2], fb[2][NQB];
     auto read_frags = [&](int buf, uint32_t slot, int t) {
         const char* base = lds + slot * STAGE;
         const uint32_t ko = 16u * uint32_t((2 * t + hh) ^ swz);
 #pragma unroll
         for (int m = 0; m < 2; ++m) fa[buf][m] = *reinterpret_cast<const h8v*>(base + a_off + m * 32 * ROWB + ko);
 #pragma unroll
-        for (int n = 0; n < 2; ++n) fb[buf][n] = *reinterpret_cast<const h8v*>(base + b_off + n * 32 * ROWB + ko);
+        for (int n = 0; n < NQB; ++n) fb[buf][n] = *reinterpret_cast<const h8v*>(base + b_off + n * 32 * ROWB + ko);
     };
     auto mma = [&](int buf) {
 #pragma unroll
         for (int m = 0; m < 2; ++m)
 #pragma unroll
-            for (int n = 0; n < 2; ++n)
+            for (int n = 0; n < NQB; ++n)
                 acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[buf][m], fb[buf][n], acc[m][n], 0, 0, 0);
     };
-    // the 4 fragment reads of the next k-step go between the 4 MFMAs
+    // the 2 + NQB fragment reads of the next k-step go between the 2 NQB MFMAs
     auto interleave = [&]() {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 2 * NQB; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (i < 2 + NQB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
     };
     // workgroup barrier without the release fence of __syncthreads (which would also wait for
@@ -839,6 +843,10 @@ __global__ __launch_bounds__(1024, 1) void screen16_kernel(ScreenArgs a) {
     };
     block(std::integral_constant<int, 0>());
     block(std::integral_constant<int, 1>());
+    if constexpr (NQB > 2) {
+        block(std::integral_constant<int, 2>());
+        block(std::integral_constant<int, 3>());
+    }
 }
 
 // ---- the fp16 shadow: rows rounded to fp16 (RNE, as the scans round), padded with zeros to Dp,
@@ -1024,9 +1032,10 @@ va_status launch_screen16(va_context* ctx, const ScreenArgs& a) {
     const uint64_t grid = nqb * ((ntb + kXcds - 1) / kXcds) * kXcds;
     if (grid == 0) return VA_OK;
     if (grid > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "screen grid too large (%llu)", (unsigned long long)grid);
-    VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(&screen16_kernel),
+    auto kern = &screen16_kernel<kWaves, kQueryBlocks>;
+    VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, LDS));
-    screen16_kernel<<<dim3(uint32_t(grid)), dim3(64 * WAVES), LDS, ctx->stream>>>(a);
+    kern<<<dim3(uint32_t(grid)), dim3(64 * kWaves), LDS, ctx->stream>>>(a);
     VA_CHECK_LAUNCH(ctx);
     return VA_OK;
 }
