@@ -88,6 +88,8 @@ struct ScreenArgs {
     // fp16 shadow of the database (screen16_kernel): row j at xh + j * Dp, |x_j|^2 at xn[j]
     const _Float16* xh = nullptr;
     const float* xn = nullptr;
+    // screen16_kernel: the pre-test constants of each query, {A, B, C, 2^-scale} (pretest_kernel)
+    const float4* ptc = nullptr;
 };
 
 // ---- bound of the screened key (va_screen_bound.hpp) --------------------------------------------
@@ -101,6 +103,17 @@ __device__ __forceinline__ void screen_keys(const ScreenArgs& a, float dot, floa
 }
 __device__ __forceinline__ PreTest pretest_consts(const ScreenArgs& a, float4 info, uint32_t thr_key) {
     return pretest_consts(bound_of(a), info.x, info.y, info.z, info.w, thr_key);
+}
+
+// The pre-test constants of every query, once per search (they depend on the query and its
+// threshold only; computing them per tile cost each wave a division and the op's branch per
+// query block): ptc[q] = {A, B, C, 2^-scale}.
+__global__ __launch_bounds__(256) void pretest_kernel(ScreenArgs a, uint32_t Q, float4* __restrict__ ptc) {
+    const uint32_t q = blockIdx.x * 256 + threadIdx.x;
+    if (q >= Q) return;
+    const float4 inf = a.qinfo[q];
+    const PreTest p = pretest_consts(a, inf, a.thr[q]);
+    ptc[q] = float4{p.A, p.B, p.C, inf.z};
 }
 
 // ---- query preparation: one wave per query ------------------------------------------------
@@ -790,8 +803,8 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
         constexpr int n = decltype(NC)::value;
         const uint32_t qt = uint32_t(wq * WQ + 32 * n + l32);
         const uint32_t qi = qs + min(qt, qc - 1);
-        const float4 qinf = a.qinfo[qi];
-        const PreTest pt = pretest_consts(a, qinf, a.thr[qi]);
+        const float4 ptq = a.ptc[qi];
+        const PreTest pt = {ptq.x, ptq.y, ptq.z};
         bool skip = qt >= qc;
         if (!bflag && !skip) {
             const float lo = fmaf(pt.A, pt.A >= 0.0f ? bxlo : bxhi, fmaf(pt.B, pt.B >= 0.0f ? bnlo : bnhi, pt.C));
@@ -835,7 +848,7 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
             mk &= mk - 1;
             const int r = row_of(t);
             const int64_t o = int64_t(qi) * a.cap + pos;
-            a.cand_dot[o] = src[(t >> 2) * 256 + (t & 3)] * qinf.z;
+            a.cand_dot[o] = src[(t >> 2) * 256 + (t & 3)] * ptq.w;
             a.cand_xx[o] = xxs[r];
             a.cand_id[o] = a.id_base + rs + uint32_t(r);
             ++pos;
@@ -1144,7 +1157,7 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
 
     Scratch s(ctx);
     const size_t q4 = Scratch::round(uint64_t(Q) * 4);
-    size_t need = q4 * 5 + Scratch::round(256) + Scratch::round(uint64_t(Q) * 16) +
+    size_t need = q4 * 5 + Scratch::round(256) + Scratch::round(uint64_t(Q) * 16) * 2 +
                   Scratch::round(uint64_t(Q) * Dp * 2) + Scratch::round(uint64_t(plan.qs) * S * 4) +
                   Scratch::round(S * 4) + Scratch::round(uint64_t(Q) * cap * 4) * 3 +
                   Scratch::round(uint64_t(Q) * rcap * 4) * 2;
@@ -1159,6 +1172,7 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     uint32_t* ovf_rows = s.carve<uint32_t>(Q);
     uint32_t* ovf_cnt = s.carve<uint32_t>(64);
     float4* qinfo = s.carve<float4>(Q);
+    float4* ptc = s.carve<float4>(Q);
     _Float16* qh = s.carve<_Float16>(uint64_t(Q) * Dp);
     uint32_t* skeys = s.carve<uint32_t>(uint64_t(plan.qs) * S);
     float* sxx = s.carve<float>(S);
@@ -1236,6 +1250,9 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
         if (in.xh) {
             a.xh = in.xh;
             a.xn = in.xn;
+            a.ptc = ptc;
+            pretest_kernel<<<dim3((Q + 255) / 256), dim3(256), 0, ctx->stream>>>(a, Q, ptc);
+            VA_CHECK_LAUNCH(ctx);
             VA_CHECK_STATUS(launch_screen16(ctx, a));
         } else {
             VA_CHECK_STATUS(launch_screen<SCREEN_FILTER>(ctx, a));
