@@ -617,20 +617,40 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wq = wave % QW, wn = wave / QW, l32 = lane & 31, hh = lane >> 5;
-    // XCD-aware order, as screen_kernel
+    // Persistent: the workgroup takes the tiles T = blockIdx.x, blockIdx.x + gridDim.x, ... in
+    // screen_kernel's XCD-aware order (gridDim.x is a multiple of the XCD count, so all of a
+    // workgroup's tiles run on its XCD).  The next tile's first stage is loaded during this tile's
+    // epilogue, into stage slot 0 (the epilogue's LDS dump uses slot 1 only), so after the first
+    // tile no workgroup waits for a prologue load with its matrix cores idle.
     const uint32_t nqb = (a.Q + TQ - 1) / TQ;
-    const uint32_t xcd = blockIdx.x % kXcds, seq = blockIdx.x / kXcds;
-    const uint32_t qb = seq % nqb, tb = (seq / nqb) * kXcds + xcd;
-    if (tb * uint32_t(TN) >= a.N) return;  // padding workgroup
-    const uint32_t qs = qb * TQ, rs = tb * TN;
-    const uint32_t qc = min(uint32_t(TQ), a.Q - qs), rc = min(uint32_t(TN), a.N - rs);
+    const uint32_t ntb = (a.N + TN - 1) / TN;
+    const uint32_t total = nqb * ((ntb + kXcds - 1) / kXcds) * kXcds;
+    auto tile_of = [&](uint32_t T, uint32_t& qb, uint32_t& tb) {
+        const uint32_t xcd = T % kXcds, seq = T / kXcds;
+        qb = seq % nqb;
+        tb = (seq / nqb) * kXcds + xcd;
+    };
+    // the first tile at or after T (in steps of gridDim.x) that holds rows
+    auto next_tile = [&](uint32_t T) {
+        for (; T < total; T += gridDim.x) {
+            uint32_t qb, tb;
+            tile_of(T, qb, tb);
+            if (tb * uint32_t(TN) < a.N) return T;
+        }
+        return total;
+    };
     const uint32_t nst = a.Dp / KC;
 
-    // Direct loads: wave w fills 1 KiB groups g = w + 16i (rows 8g .. 8g+7) of each operand; lane
-    // L loads row 8g + L/8 at physical chunk L%8 = logical chunk (L%8) ^ ((row >> 1) & 7).  Rows
-    // past qc / rc read past their descriptor and land as zeros.
-    const dma_rsrc qres = make_dma_rsrc(a.qh + int64_t(qs) * a.Dp, qc * a.Dp * 2u);
-    const dma_rsrc xres = make_dma_rsrc(a.xh + int64_t(rs) * a.Dp, rc * a.Dp * 2u);
+    // Direct loads: wave w fills 1 KiB groups g = w + WAVES i (rows 8g .. 8g+7) of each operand;
+    // lane L loads row 8g + L/8 at physical chunk L%8 = logical chunk (L%8) ^ ((row >> 1) & 7).
+    // Rows past qc / rc read past their descriptor and land as zeros.
+    auto tile_rsrc = [&](uint32_t T, dma_rsrc& qr, dma_rsrc& xr) {
+        uint32_t qb, tb;
+        tile_of(T, qb, tb);
+        const uint32_t q0 = qb * TQ, r0 = tb * TN;
+        qr = make_dma_rsrc(a.qh + int64_t(q0) * a.Dp, min(uint32_t(TQ), a.Q - q0) * a.Dp * 2u);
+        xr = make_dma_rsrc(a.xh + int64_t(r0) * a.Dp, min(uint32_t(TN), a.N - r0) * a.Dp * 2u);
+    };
     uint32_t off[LPW];
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
@@ -638,15 +658,15 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
         off[i] = uint32_t(row) * a.Dp * 2u + 16u * uint32_t((lane & 7) ^ ((row >> 1) & 7));
     }
     const uint32_t lds0 = lds_addr_of(lds);
-    auto issue = [&](uint32_t s) {
+    auto issue_with = [&](const dma_rsrc& qr, const dma_rsrc& xr, uint32_t s) {
         const uint32_t d0 = s * KC;
         const bool ok = d0 < a.Dp;
         const uint32_t sb = lds0 + (s & 1u) * uint32_t(STAGE);
 #pragma unroll
         for (int i = 0; i < LPW; ++i) {
             const uint32_t grp = uint32_t(wave + WAVES * i);
-            lds_dma16(qres, ok ? off[i] + d0 * 2u : kDmaSkip, sb + grp * 1024u);
-            lds_dma16(xres, ok ? off[i] + d0 * 2u : kDmaSkip, sb + uint32_t(OPB) + grp * 1024u);
+            lds_dma16(qr, ok ? off[i] + d0 * 2u : kDmaSkip, sb + grp * 1024u);
+            lds_dma16(xr, ok ? off[i] + d0 * 2u : kDmaSkip, sb + uint32_t(OPB) + grp * 1024u);
         }
     };
     // L2 prefetch of the rows of stage s+1 ahead of their direct loads: waves 0-3, one dword per
@@ -654,23 +674,12 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
     __shared__ __attribute__((aligned(256))) char pf_sink[4 * 256];
     const bool pf_wave = wave < 4;
     const uint32_t pf_off = uint32_t(64 * (wave & 3) + lane) * a.Dp * 2u;
-    auto prefetch = [&](uint32_t s) {
-        const uint32_t d0 = s * KC;
-        if (pf_wave) lds_dma4(xres, d0 < a.Dp ? pf_off + d0 * 2u : kDmaSkip, lds_addr_of(pf_sink + (wave & 3) * 256));
-    };
     // fragment rows start at multiples of 32, so the chunk swizzle is (l32 >> 1) & 7 for both
     const int swz = (l32 >> 1) & 7;
     const uint32_t a_off = uint32_t(OPB + (wn * WN + l32) * ROWB);
     const uint32_t b_off = uint32_t((wq * WQ + l32) * ROWB);
 
     f32x16 acc[2][NQB];
-#pragma unroll
-    for (int m = 0; m < 2; ++m)
-#pragma unroll
-        for (int n = 0; n < NQB; ++n)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[m][n][v] = 0.0f;
-
     h8v fa[2][2], fb[2][NQB];
     auto read_frags = [&](int buf, uint32_t slot, int t) {
         const char* base = lds + slot * STAGE;
@@ -699,167 +708,231 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
     // the direct loads in flight); this wave's LDS reads are complete before it
     auto barrier = [&]() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
-    // the tile's squared row norms: loaded now (one register), used after the main loop
-    const float xn_t = tid < TN && uint32_t(tid) < rc ? a.xn[rs + uint32_t(tid)] : 0.0f;
-    // per wave and stage: 2 LPW direct loads, plus one prefetch in waves 0-3
-    issue(0);
-    issue(1);
-    prefetch(2);
-    if (pf_wave) wait_vmcnt<2 * LPW + 1>();  // stage 0 (older than stage 1's loads and the prefetch)
-    else wait_vmcnt<2 * LPW>();
-    barrier();
-    read_frags(0, 0, 0);
-    for (uint32_t s = 0; s < nst; ++s) {
-        const uint32_t slot = s & 1u;
-#pragma unroll
-        for (int t = 0; t < KC / 16; ++t) {
-            const int cur = t & 1;  // four k-steps per stage: the parity of the global k-step
-            if (t < KC / 16 - 1) {
-                read_frags(cur ^ 1, slot, t + 1);
-                mma(cur);
-                interleave();
-            } else {
-                // this k-step's fragments are in registers: publish stage s+1, free slot s (the
-                // one load younger than stage s+1's is the prefetch issued after them)
-                if (pf_wave) wait_vmcnt<1>();
-                else wait_vmcnt<0>();
-                barrier();
-                read_frags(cur ^ 1, slot ^ 1u, 0);
-                mma(cur);
-                interleave();
-                issue(s + 2);  // past the last stage: zeros into the free slot
-                prefetch(s + 3);
-            }
-        }
-    }
-    wait_vmcnt<0>();
-
-    // the tile's row norms from the shadow; flags as in screen_kernel
     float* xxs = norms;
     float* xxp = norms + TN;
     float* nxp = norms + 2 * TN;
-    const float tiny = a.op == OP_COS_DIST ? 8.0f * a.c0x : 0.0f;
-    if (tid < TN) {
-        const uint32_t r = uint32_t(tid);
-        const float t = xn_t;
-        const float nx = __builtin_amdgcn_sqrtf(t);
-        xxs[r] = t;
-        const bool flag = !(t < 4.29e9f) || nx < tiny;
-        xxp[r] = flag ? __builtin_nanf("") : t;
-        nxp[r] = flag ? __builtin_nanf("") : nx;
-    }
-    __syncthreads();
-    // the (|x|^2, |x|) box of each 4-row group, NaN when a row of it is flagged: a lane's 32 rows
-    // are 8 whole groups, so its quick-rejection box is 8 lookups instead of 32 rows' worth of
-    // min/max (that loop was a large share of the epilogue's vector work)
+    // uniform: kept in a scalar register across the tile loop
+    const float tiny = __builtin_bit_cast(
+        float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, a.op == OP_COS_DIST ? 8.0f * a.c0x : 0.0f)));
     __shared__ float4 gbox[TN / 4];
-    if (tid < TN / 4) {
-        float4 b = {INFINITY, -INFINITY, INFINITY, -INFINITY};
-        bool f = false;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float xx = xxp[4 * tid + e], nx = nxp[4 * tid + e];
-            f |= !(xx == xx) || !(nx == nx);
-            b.x = fminf(b.x, xx);
-            b.y = fmaxf(b.y, xx);
-            b.z = fminf(b.z, nx);
-            b.w = fmaxf(b.w, nx);
-        }
-        if (f) b.x = __builtin_nanf("");
-        gbox[tid] = b;
-    }
-    __syncthreads();
-
-    // ---- filter epilogue: lane (l32, hh) holds query wq*64 + 32n + l32 against rows
-    // wn*64 + 32m + 8j + 4hh + e in acc[m][n][4j + e]; t = 16m + 4j + e indexes its 32 values.
-    // One query block at a time; a block that the quick rejection below does not settle goes to
-    // the wave's 8 KiB of the (now free) stage LDS, so only the other block's accumulators stay
-    // in registers while its pre-test runs; the pre-test over the 32 values builds a bit
-    // mask without branches (after a quick rejection: the right-hand side A|x|^2 + B|x| + C over
-    // the lane's rows is bounded below at the corner of their (|x|^2, |x|) box that A's and B's
-    // signs select, so a lane whose largest value is below it passes nothing; flagged (NaN) rows
-    // disable it); lanes l and l + 32 hold the same query, so one atomic reserves both lanes'
-    // places; the appends read the values back from LDS.
+    __shared__ float4 ptl[TQ];  // {A, B, C, 2^-scale} of the tile's queries
     auto row_of = [&](int t) { return wn * WN + 32 * (t >> 4) + 8 * ((t >> 2) & 3) + 4 * hh + (t & 3); };
-    uint32_t valid = ~0u;
-    if (rc < TN) {
-        valid = 0;
+    // the epilogue's LDS: half a query block (16 values a lane) per wave, in stage slot 1
+    f32x4v* dump = reinterpret_cast<f32x4v*>(lds + STAGE + wave * 4096) + lane;  // [c][lane], c < 4
+
+    uint32_t T = next_tile(blockIdx.x);
+    if (T >= total) return;
+    dma_rsrc qres, xres;
+    tile_rsrc(T, qres, xres);
+    issue_with(qres, xres, 0);  // later tiles: stage 0 is loaded during the previous epilogue
+    while (T < total) {
+        uint32_t qb, tb;
+        tile_of(T, qb, tb);
+        const uint32_t qs = qb * TQ, rs = tb * TN;
+        const uint32_t qc = min(uint32_t(TQ), a.Q - qs), rc = min(uint32_t(TN), a.N - rs);
+        // the tile's squared row norms: loaded now (one register), used after the main loop
+        const float xn_t = tid < TN && uint32_t(tid) < rc ? a.xn[rs + uint32_t(tid)] : 0.0f;
+        auto issue = [&](uint32_t s) { issue_with(qres, xres, s); };
+        // opaque: the prologue's prefetch offset is computed here, not kept in a register across
+        // the tile loop
+        uint32_t pfo = pf_off;
+        asm volatile("" : "+v"(pfo));
+        auto prefetch = [&](uint32_t s) {
+            const uint32_t d0 = s * KC;
+            if (pf_wave)
+                lds_dma4(xres, d0 < a.Dp ? pfo + d0 * 2u : kDmaSkip, lds_addr_of(pf_sink + (wave & 3) * 256));
+        };
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int n = 0; n < NQB; ++n)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[m][n][v] = 0.0f;
+        // every wave is past the previous tile's epilogue (its dump in slot 1 is read)
+        barrier();
+        // per wave and stage: 2 LPW direct loads, plus one prefetch in waves 0-3
+        issue(1);
+        prefetch(2);
+        if (pf_wave) wait_vmcnt<2 * LPW + 1>();  // stage 0 (older than stage 1's loads and the prefetch)
+        else wait_vmcnt<2 * LPW>();
+        barrier();
+        read_frags(0, 0, 0);
+        for (uint32_t s = 0; s < nst; ++s) {
+            const uint32_t slot = s & 1u;
+#pragma unroll
+            for (int t = 0; t < KC / 16; ++t) {
+                const int cur = t & 1;  // four k-steps per stage: the parity of the global k-step
+                if (t < KC / 16 - 1) {
+                    read_frags(cur ^ 1, slot, t + 1);
+                    mma(cur);
+                    interleave();
+                } else {
+                    // this k-step's fragments are in registers: publish stage s+1, free slot s (the
+                    // one load younger than stage s+1's is the prefetch issued after them)
+                    if (pf_wave) wait_vmcnt<1>();
+                    else wait_vmcnt<0>();
+                    barrier();
+                    read_frags(cur ^ 1, slot ^ 1u, 0);
+                    mma(cur);
+                    interleave();
+                    if (s + 2 < nst) issue(s + 2);  // the slots past the last stage stay free
+                    prefetch(s + 3);
+                }
+            }
+        }
+        wait_vmcnt<0>();
+
+        // the tile's row norms from the shadow; flags as in screen_kernel
+        if (tid < TN) {
+            const uint32_t r = uint32_t(tid);
+            const float t = xn_t;
+            const float nx = __builtin_amdgcn_sqrtf(t);
+            xxs[r] = t;
+            const bool flag = !(t < 4.29e9f) || nx < tiny;
+            xxp[r] = flag ? __builtin_nanf("") : t;
+            nxp[r] = flag ? __builtin_nanf("") : nx;
+        }
+        // the pre-test constants of the tile's queries, in LDS before the next tile's loads are
+        // issued (a wait for a global load after those would wait for them too)
+        if (tid < TQ) ptl[tid] = a.ptc[qs + min(uint32_t(tid), qc - 1)];
+        __syncthreads();  // every wave is past the main loop: stage slot 0 is free
+        // the next tile's first stage, during this epilogue
+        const uint32_t Tn = next_tile(T + gridDim.x);
+        if (Tn < total) {
+            tile_rsrc(Tn, qres, xres);
+            issue_with(qres, xres, 0);
+        }
+        // the (|x|^2, |x|) box of each 4-row group, NaN when a row of it is flagged: a lane's 32
+        // rows are 8 whole groups, so its quick-rejection box is 8 lookups instead of 32 rows'
+        // worth of min/max (that loop was a large share of the epilogue's vector work)
+        if (tid < TN / 4) {
+            float4 b = {INFINITY, -INFINITY, INFINITY, -INFINITY};
+            bool f = false;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float xx = xxp[4 * tid + e], nx = nxp[4 * tid + e];
+                f |= !(xx == xx) || !(nx == nx);
+                b.x = fminf(b.x, xx);
+                b.y = fmaxf(b.y, xx);
+                b.z = fminf(b.z, nx);
+                b.w = fmaxf(b.w, nx);
+            }
+            if (f) b.x = __builtin_nanf("");
+            gbox[tid] = b;
+        }
+        barrier();  // not __syncthreads: that would wait for the next tile's loads
+
+        // ---- filter epilogue: lane (l32, hh) holds query wq*WQ + 32n + l32 against rows
+        // wn*64 + 32m + 8j + 4hh + e in acc[m][n][4j + e]; t = 16m + 4j + e indexes its 32 values.
+        // One query block at a time; the quick rejection (the right-hand side A|x|^2 + B|x| + C
+        // over the lane's rows is bounded below at the corner of their (|x|^2, |x|) box that A's
+        // and B's signs select, so a lane whose largest value is below it passes nothing; flagged
+        // (NaN) rows disable it) settles most blocks from registers.  Another block goes through
+        // the wave's 4 KiB of slot 1 half a block (one row block m) at a time: the pre-test over
+        // its 16 values builds a bit mask without branches; lanes l and l + 32 hold the same query,
+        // so one atomic reserves both lanes' places; the appends read the values back from LDS.
+        uint32_t valid = ~0u;
+        if (rc < TN) {
+            valid = 0;
 #pragma unroll 1
-        for (int t = 0; t < 32; ++t) valid |= uint32_t(uint32_t(row_of(t)) < rc) << t;
-    }
-    float bxlo = INFINITY, bxhi = -INFINITY, bnlo = INFINITY, bnhi = -INFINITY;
-    bool bflag = false;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-        const float4 b = gbox[row_of(4 * c) >> 2];  // rows 4c .. 4c + 3 of the lane: one group
-        bflag |= !(b.x == b.x);
-        bxlo = fminf(bxlo, b.x);
-        bxhi = fmaxf(bxhi, b.y);
-        bnlo = fminf(bnlo, b.z);
-        bnhi = fmaxf(bnhi, b.w);
-    }
-    f32x4v* dump = reinterpret_cast<f32x4v*>(lds + wave * 8192) + lane;  // [t / 4][lane]
-    auto block = [&](auto NC) {
-        constexpr int n = decltype(NC)::value;
-        const uint32_t qt = uint32_t(wq * WQ + 32 * n + l32);
-        const uint32_t qi = qs + min(qt, qc - 1);
-        const float4 ptq = a.ptc[qi];
-        const PreTest pt = {ptq.x, ptq.y, ptq.z};
-        bool skip = qt >= qc;
-        if (!bflag && !skip) {
-            const float lo = fmaf(pt.A, pt.A >= 0.0f ? bxlo : bxhi, fmaf(pt.B, pt.B >= 0.0f ? bnlo : bnhi, pt.C));
-            float mx = -INFINITY;
-#pragma unroll
-            for (int t = 0; t < 32; ++t) mx = fmaxf(mx, acc[t >> 4][n][t & 15]);
-            skip = mx < lo;
+            for (int t = 0; t < 32; ++t) valid |= uint32_t(uint32_t(row_of(t)) < rc) << t;
         }
-        uint32_t mk = 0;
-        if (!skip) {
-            // only a block that may pass goes through LDS (most are rejected from registers above)
+        float bxlo = INFINITY, bxhi = -INFINITY, bnlo = INFINITY, bnhi = -INFINITY;
+        bool bflag = false;
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                f32x4v v;
+        for (int c = 0; c < 8; ++c) {
+            const float4 b = gbox[row_of(4 * c) >> 2];  // rows 4c .. 4c + 3 of the lane: one group
+            bflag |= !(b.x == b.x);
+            bxlo = fminf(bxlo, b.x);
+            bxhi = fmaxf(bxhi, b.y);
+            bnlo = fminf(bnlo, b.z);
+            bnhi = fmaxf(bnhi, b.w);
+        }
+        auto block = [&](auto NC) {
+            constexpr int n = decltype(NC)::value;
+            const uint32_t qt = uint32_t(wq * WQ + 32 * n + l32);
+            const uint32_t qi = qs + min(qt, qc - 1);
+            const float4 ptq = ptl[qt];
+            const PreTest pt = {ptq.x, ptq.y, ptq.z};
+            bool skip = qt >= qc;
+            if (!bflag && !skip) {
+                const float lo = fmaf(pt.A, pt.A >= 0.0f ? bxlo : bxhi, fmaf(pt.B, pt.B >= 0.0f ? bnlo : bnhi, pt.C));
+                float mx = -INFINITY;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = acc[c >> 2][n][4 * (c & 3) + e];
-                dump[c * 64] = v;
+                for (int t = 0; t < 32; ++t) mx = fmaxf(mx, acc[t >> 4][n][t & 15]);
+                skip = mx < lo;
             }
-            // re-read the row norms from LDS below rather than keep the bounds pass's copies live
-            asm volatile("" ::: "memory");
+            // half block m of the dump: values 16m .. 16m + 15
+            auto dump_half = [&](auto MC) {
+                constexpr int m = decltype(MC)::value;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    f32x4v v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = acc[m][n][4 * c + e];
+                    dump[c * 64] = v;
+                }
+                // re-read the row norms and the dump from LDS below
+                asm volatile("" ::: "memory");
+            };
+            uint32_t mk = 0;
+            if (!skip) {
+                auto test_half = [&](auto MC) {
+                    constexpr int m = decltype(MC)::value;
+                    dump_half(MC);
 #pragma unroll 2
-            for (int c = 0; c < 8; ++c) {
-                const int r = row_of(4 * c);
-                const f32x4v xx = *reinterpret_cast<const f32x4v*>(xxp + r);
-                const f32x4v nx = *reinterpret_cast<const f32x4v*>(nxp + r);
-                const f32x4v v = dump[c * 64];
+                    for (int c = 0; c < 4; ++c) {
+                        const int r = row_of(16 * m + 4 * c);
+                        const f32x4v xx = *reinterpret_cast<const f32x4v*>(xxp + r);
+                        const f32x4v nx = *reinterpret_cast<const f32x4v*>(nxp + r);
+                        const f32x4v v = dump[c * 64];
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    mk |= uint32_t(!(v[e] < fmaf(pt.A, xx[e], fmaf(pt.B, nx[e], pt.C)))) << (4 * c + e);
+                        for (int e = 0; e < 4; ++e)
+                            mk |= uint32_t(!(v[e] < fmaf(pt.A, xx[e], fmaf(pt.B, nx[e], pt.C)))) << (16 * m + 4 * c + e);
+                    }
+                };
+                test_half(std::integral_constant<int, 0>());
+                test_half(std::integral_constant<int, 1>());
+                mk &= valid;
             }
-            mk &= valid;
+            // a block with nothing to append skips the atomic and its wait, which would also wait
+            // for the next tile's loads in flight
+            if (!__ballot(mk != 0u)) return;
+            const uint32_t cnt = uint32_t(__popc(mk));
+            const uint32_t other = uint32_t(__shfl_xor(int(cnt), 32));
+            uint32_t base = 0;
+            if (hh == 0 && cnt + other) base = atomicAdd(a.cnt + qi, cnt + other);
+            uint32_t pos = uint32_t(__shfl(int(base), l32)) + (hh ? other : 0u);
+            const float* src = reinterpret_cast<const float*>(dump);
+            auto append_half = [&](auto MC) {
+                constexpr int m = decltype(MC)::value;
+                uint32_t mh = (mk >> (16 * m)) & 0xFFFFu;
+                if (!__ballot(mh != 0u)) return;
+                dump_half(MC);
+                while (mh && pos < a.cap) {
+                    const int c16 = __builtin_ctz(mh);
+                    mh &= mh - 1;
+                    const int t = 16 * m + c16;
+                    const int r = row_of(t);
+                    const int64_t o = int64_t(qi) * a.cap + pos;
+                    a.cand_dot[o] = src[(c16 >> 2) * 256 + (c16 & 3)] * ptq.w;
+                    a.cand_xx[o] = xxs[r];
+                    a.cand_id[o] = a.id_base + rs + uint32_t(r);
+                    ++pos;
+                }
+            };
+            append_half(std::integral_constant<int, 0>());
+            append_half(std::integral_constant<int, 1>());
+        };
+        block(std::integral_constant<int, 0>());
+        block(std::integral_constant<int, 1>());
+        if constexpr (NQB > 2) {
+            block(std::integral_constant<int, 2>());
+            block(std::integral_constant<int, 3>());
         }
-        const uint32_t cnt = uint32_t(__popc(mk));
-        const uint32_t other = uint32_t(__shfl_xor(int(cnt), 32));
-        uint32_t base = 0;
-        if (hh == 0 && cnt + other) base = atomicAdd(a.cnt + qi, cnt + other);
-        uint32_t pos = uint32_t(__shfl(int(base), l32)) + (hh ? other : 0u);
-        const float* src = reinterpret_cast<const float*>(dump);
-        while (mk && pos < a.cap) {
-            const int t = __builtin_ctz(mk);
-            mk &= mk - 1;
-            const int r = row_of(t);
-            const int64_t o = int64_t(qi) * a.cap + pos;
-            a.cand_dot[o] = src[(t >> 2) * 256 + (t & 3)] * ptq.w;
-            a.cand_xx[o] = xxs[r];
-            a.cand_id[o] = a.id_base + rs + uint32_t(r);
-            ++pos;
-        }
-    };
-    block(std::integral_constant<int, 0>());
-    block(std::integral_constant<int, 1>());
-    if constexpr (NQB > 2) {
-        block(std::integral_constant<int, 2>());
-        block(std::integral_constant<int, 3>());
+        T = Tn;
     }
+    wait_vmcnt<0>();
 }
 
 // ---- the fp16 shadow: rows rounded to fp16 (RNE, as the scans round), padded with zeros to Dp,
@@ -1042,9 +1115,12 @@ va_status launch_screen16(va_context* ctx, const ScreenArgs& a) {
     using namespace s16;
     const uint64_t nqb = (a.Q + TQ - 1) / TQ;
     const uint64_t ntb = (a.N + TN - 1) / TN;
-    const uint64_t grid = nqb * ((ntb + kXcds - 1) / kXcds) * kXcds;
-    if (grid == 0) return VA_OK;
-    if (grid > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "screen grid too large (%llu)", (unsigned long long)grid);
+    const uint64_t tiles = nqb * ((ntb + kXcds - 1) / kXcds) * kXcds;
+    if (tiles == 0) return VA_OK;
+    if (tiles > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "screen grid too large (%llu)", (unsigned long long)tiles);
+    // persistent: one workgroup per CU (its LDS fills one), a multiple of the XCD count
+    const uint64_t cus = std::max<uint64_t>(uint64_t(ctx->num_cus), kXcds) / kXcds * kXcds;
+    const uint64_t grid = std::min(tiles, cus);
     auto kern = &screen16_kernel<kWaves, kQueryBlocks>;
     VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, LDS));
