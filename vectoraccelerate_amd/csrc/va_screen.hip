@@ -669,11 +669,6 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
             lds_dma16(xr, ok ? off[i] + d0 * 2u : kDmaSkip, sb + uint32_t(OPB) + grp * 1024u);
         }
     };
-    // L2 prefetch of the rows of stage s+1 ahead of their direct loads: waves 0-3, one dword per
-    // 128-byte line (lane L of wave w takes row 64w + L) into a sink that nothing reads
-    __shared__ __attribute__((aligned(256))) char pf_sink[4 * 256];
-    const bool pf_wave = wave < 4;
-    const uint32_t pf_off = uint32_t(64 * (wave & 3) + lane) * a.Dp * 2u;
     // fragment rows start at multiples of 32, so the chunk swizzle is (l32 >> 1) & 7 for both
     const int swz = (l32 >> 1) & 7;
     const uint32_t a_off = uint32_t(OPB + (wn * WN + l32) * ROWB);
@@ -733,15 +728,6 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
         // the tile's squared row norms: loaded now (one register), used after the main loop
         const float xn_t = tid < TN && uint32_t(tid) < rc ? a.xn[rs + uint32_t(tid)] : 0.0f;
         auto issue = [&](uint32_t s) { issue_with(qres, xres, s); };
-        // opaque: the prologue's prefetch offset is computed here, not kept in a register across
-        // the tile loop
-        uint32_t pfo = pf_off;
-        asm volatile("" : "+v"(pfo));
-        auto prefetch = [&](uint32_t s) {
-            const uint32_t d0 = s * KC;
-            if (pf_wave)
-                lds_dma4(xres, d0 < a.Dp ? pfo + d0 * 2u : kDmaSkip, lds_addr_of(pf_sink + (wave & 3) * 256));
-        };
 #pragma unroll
         for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -750,11 +736,9 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
                 for (int v = 0; v < 16; ++v) acc[m][n][v] = 0.0f;
         // every wave is past the previous tile's epilogue (its dump in slot 1 is read)
         barrier();
-        // per wave and stage: 2 LPW direct loads, plus one prefetch in waves 0-3
+        // per wave and stage: 2 LPW direct loads
         issue(1);
-        prefetch(2);
-        if (pf_wave) wait_vmcnt<2 * LPW + 1>();  // stage 0 (older than stage 1's loads and the prefetch)
-        else wait_vmcnt<2 * LPW>();
+        wait_vmcnt<2 * LPW>();  // stage 0 (older than stage 1's loads)
         barrier();
         read_frags(0, 0, 0);
         for (uint32_t s = 0; s < nst; ++s) {
@@ -767,16 +751,13 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
                     mma(cur);
                     interleave();
                 } else {
-                    // this k-step's fragments are in registers: publish stage s+1, free slot s (the
-                    // one load younger than stage s+1's is the prefetch issued after them)
-                    if (pf_wave) wait_vmcnt<1>();
-                    else wait_vmcnt<0>();
+                    // this k-step's fragments are in registers: publish stage s+1, free slot s
+                    wait_vmcnt<0>();
                     barrier();
                     read_frags(cur ^ 1, slot ^ 1u, 0);
                     mma(cur);
                     interleave();
                     if (s + 2 < nst) issue(s + 2);  // the slots past the last stage stay free
-                    prefetch(s + 3);
                 }
             }
         }
