@@ -88,6 +88,28 @@ def test_index_search_equals_fp32_scan_over_live_rows(ctx, metric, name):
     ix.close()
 
 
+@pytest.mark.parametrize("metric,name", [(L2SQ, "euclidean"), (COSINE, "cosine"), (DOT, "dotProduct")])
+def test_index_search_many_tiles_per_workgroup(ctx, metric, name):
+    """More fp16-shadow tiles than workgroups (300 queries x 70,001 rows: 2 x 280 tiles of 256 x 256,
+    partial in both directions, padding tiles included) and a dimension that is not a multiple of
+    the 64-value stage: every workgroup of the persistent screen walks several tiles."""
+    from vectoraccelerate_amd import AcceleratedVectorIndex, IndexConfiguration
+
+    x, q = _data(40 + metric, 70_001, 136, 300, normalise=metric == COSINE)
+    ix = AcceleratedVectorIndex(IndexConfiguration.flat(136, 1000, metric=name), ctx)
+    ix.insert(vectors=x)
+    k = 37
+    gi, gd = _index_search(ix, q, k)
+    fi, fd = _fused(ctx, metric, q, x, k, screen=1)
+    np.testing.assert_array_equal(gi, fi)
+    np.testing.assert_array_equal(gd.view(np.uint32), fd.view(np.uint32))
+    # a second search on the same index and context (the workgroups' tile walk starts afresh)
+    gi2, gd2 = _index_search(ix, q[:211], k)
+    np.testing.assert_array_equal(gi2, fi[:211])
+    np.testing.assert_array_equal(gd2.view(np.uint32), fd[:211].view(np.uint32))
+    ix.close()
+
+
 def test_removing_more_than_max_k_nearest_rows_keeps_k_results(ctx, oracle):
     """ADVICE: k + deletedCount > VA_MAX_K must not shorten the result."""
     from vectoraccelerate_amd import AcceleratedVectorIndex, IndexConfiguration
