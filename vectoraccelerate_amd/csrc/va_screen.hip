@@ -596,22 +596,37 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
 // run, and the stage barrier sits inside the last k-step of a stage, after its fragments are in
 // registers (a bare s_barrier: the direct loads of the next stage stay in flight across it).
 namespace s16 {
-constexpr int TQ = 256, TN = 256, KC = 64;
+constexpr int TQ = 256, KC = 64;
 constexpr int ROWB = KC * 2;              // bytes per LDS row
-constexpr int OPB = TQ * ROWB;            // one operand per stage (32 KiB)
-constexpr int STAGE = 2 * OPB;            // queries, then rows
-constexpr int LDS = 2 * STAGE;            // two stages
-// the wave layout of the launch: waves per workgroup and 32-query blocks per wave
-constexpr int kWaves = 16, kQueryBlocks = 2;
+// the wave layout of the launch: waves per workgroup, 32-query and 32-row blocks per wave
+constexpr int kWaves = 16, kQueryBlocks = 2, kRowBlocks = 2;
+// A workgroup of WAVES waves, each (32 NQB queries) x (32 MB rows), over a tile of TQ queries x
+// TN rows; a stage holds 64 d-values of both (queries, then rows), two stages in LDS.
+template <int WAVES, int NQB, int MB>
+struct Shape {
+    static constexpr int WQ = 32 * NQB, WN = 32 * MB;  // a wave's queries x rows
+    static constexpr int QW = TQ / WQ;                 // waves along the queries
+    static constexpr int TN = WN * (WAVES / QW);
+    static constexpr int OPQ = TQ * ROWB, OPX = TN * ROWB;
+    static constexpr int STAGE = OPQ + OPX;
+    static constexpr int LDS = 2 * STAGE;
+    // 1 KiB direct-load groups (8 rows) per stage: GQ of queries, GX of rows; a wave loads up to
+    // LPW of each, LMIN loads in all at least
+    static constexpr int GQ = OPQ / 1024, GX = OPX / 1024;
+    static constexpr int LPW = ((GQ > GX ? GQ : GX) + WAVES - 1) / WAVES, LMIN = GQ / WAVES + GX / WAVES;
+    static_assert(QW * WQ == TQ && WAVES % QW == 0 && TN % 8 == 0, "wave layout");
+    static_assert(64 * WAVES >= TN && 64 * WAVES >= TQ, "one thread per row and query");
+    static_assert(WAVES * 4096 <= STAGE, "the epilogue's dump fits in one stage slot");
+};
 }  // namespace s16
 
-// WAVES waves of (32 NQB queries) x 64 rows; four waves per SIMD at 16 waves, two at 8
-template <int WAVES, int NQB>
+// WAVES waves of (32 NQB queries) x (32 MB rows): four waves per SIMD at 16 waves
+template <int WAVES, int NQB, int MB>
 __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(ScreenArgs a) {
     using namespace s16;
-    constexpr int WQ = 32 * NQB, WN = 64;     // a wave's queries x rows
-    constexpr int QW = TQ / WQ;               // waves along the queries
-    constexpr int LPW = OPB / 1024 / WAVES;   // 1 KiB direct loads per wave per operand per stage
+    using Sh = Shape<WAVES, NQB, MB>;
+    constexpr int WQ = Sh::WQ, WN = Sh::WN, QW = Sh::QW, TN = Sh::TN;
+    constexpr int OPQ = Sh::OPQ, STAGE = Sh::STAGE, GQ = Sh::GQ, GX = Sh::GX, LPW = Sh::LPW;
     extern __shared__ __attribute__((aligned(1024))) char lds[];
     __shared__ __attribute__((aligned(16))) float norms[3 * TN];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -664,39 +679,40 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
         const uint32_t sb = lds0 + (s & 1u) * uint32_t(STAGE);
 #pragma unroll
         for (int i = 0; i < LPW; ++i) {
-            const uint32_t grp = uint32_t(wave + WAVES * i);
-            lds_dma16(qr, ok ? off[i] + d0 * 2u : kDmaSkip, sb + grp * 1024u);
-            lds_dma16(xr, ok ? off[i] + d0 * 2u : kDmaSkip, sb + uint32_t(OPB) + grp * 1024u);
+            const int g = wave + WAVES * i;  // wave-uniform; a compile-time true test when WAVES divides
+            if (GQ % WAVES == 0 || g < GQ) lds_dma16(qr, ok ? off[i] + d0 * 2u : kDmaSkip, sb + uint32_t(g) * 1024u);
+            if (GX % WAVES == 0 || g < GX)
+                lds_dma16(xr, ok ? off[i] + d0 * 2u : kDmaSkip, sb + uint32_t(OPQ + g * 1024));
         }
     };
     // fragment rows start at multiples of 32, so the chunk swizzle is (l32 >> 1) & 7 for both
     const int swz = (l32 >> 1) & 7;
-    const uint32_t a_off = uint32_t(OPB + (wn * WN + l32) * ROWB);
+    const uint32_t a_off = uint32_t(OPQ + (wn * WN + l32) * ROWB);
     const uint32_t b_off = uint32_t((wq * WQ + l32) * ROWB);
 
-    f32x16 acc[2][NQB];
-    h8v fa[2][2], fb[2][NQB];
+    f32x16 acc[MB][NQB];
+    h8v fa[2][MB], fb[2][NQB];
     auto read_frags = [&](int buf, uint32_t slot, int t) {
         const char* base = lds + slot * STAGE;
         const uint32_t ko = 16u * uint32_t((2 * t + hh) ^ swz);
 #pragma unroll
-        for (int m = 0; m < 2; ++m) fa[buf][m] = *reinterpret_cast<const h8v*>(base + a_off + m * 32 * ROWB + ko);
+        for (int m = 0; m < MB; ++m) fa[buf][m] = *reinterpret_cast<const h8v*>(base + a_off + m * 32 * ROWB + ko);
 #pragma unroll
         for (int n = 0; n < NQB; ++n) fb[buf][n] = *reinterpret_cast<const h8v*>(base + b_off + n * 32 * ROWB + ko);
     };
     auto mma = [&](int buf) {
 #pragma unroll
-        for (int m = 0; m < 2; ++m)
+        for (int m = 0; m < MB; ++m)
 #pragma unroll
             for (int n = 0; n < NQB; ++n)
                 acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[buf][m], fb[buf][n], acc[m][n], 0, 0, 0);
     };
-    // the 2 + NQB fragment reads of the next k-step go between the 2 NQB MFMAs
+    // the MB + NQB fragment reads of the next k-step go between the MB NQB MFMAs
     auto interleave = [&]() {
 #pragma unroll
-        for (int i = 0; i < 2 * NQB; ++i) {
+        for (int i = 0; i < MB * NQB; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            if (i < 2 + NQB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (i < MB + NQB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
     };
     // workgroup barrier without the release fence of __syncthreads (which would also wait for
@@ -712,7 +728,9 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
     __shared__ float4 gbox[TN / 4];
     __shared__ float4 ptl[TQ];  // {A, B, C, 2^-scale} of the tile's queries
     auto row_of = [&](int t) { return wn * WN + 32 * (t >> 4) + 8 * ((t >> 2) & 3) + 4 * hh + (t & 3); };
-    // the epilogue's LDS: half a query block (16 values a lane) per wave, in stage slot 1
+    using Mask = std::conditional_t<(16 * MB > 32), uint64_t, uint32_t>;  // bit t: value t of a block
+    // the epilogue's LDS: one 32-row block of a query block (16 values a lane) per wave, in stage
+    // slot 1
     f32x4v* dump = reinterpret_cast<f32x4v*>(lds + STAGE + wave * 4096) + lane;  // [c][lane], c < 4
 
     uint32_t T = next_tile(blockIdx.x);
@@ -729,16 +747,16 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
         const float xn_t = tid < TN && uint32_t(tid) < rc ? a.xn[rs + uint32_t(tid)] : 0.0f;
         auto issue = [&](uint32_t s) { issue_with(qres, xres, s); };
 #pragma unroll
-        for (int m = 0; m < 2; ++m)
+        for (int m = 0; m < MB; ++m)
 #pragma unroll
             for (int n = 0; n < NQB; ++n)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[m][n][v] = 0.0f;
         // every wave is past the previous tile's epilogue (its dump in slot 1 is read)
         barrier();
-        // per wave and stage: 2 LPW direct loads
+        // per wave and stage: LMIN or LPW direct loads
         issue(1);
-        wait_vmcnt<2 * LPW>();  // stage 0 (older than stage 1's loads)
+        wait_vmcnt<Sh::LMIN>();  // stage 0 (older than stage 1's loads)
         barrier();
         read_frags(0, 0, 0);
         for (uint32_t s = 0; s < nst; ++s) {
@@ -804,24 +822,24 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
         barrier();  // not __syncthreads: that would wait for the next tile's loads
 
         // ---- filter epilogue: lane (l32, hh) holds query wq*WQ + 32n + l32 against rows
-        // wn*64 + 32m + 8j + 4hh + e in acc[m][n][4j + e]; t = 16m + 4j + e indexes its 32 values.
+        // wn*WN + 32m + 8j + 4hh + e in acc[m][n][4j + e]; t = 16m + 4j + e indexes its 16 MB values.
         // One query block at a time; the quick rejection (the right-hand side A|x|^2 + B|x| + C
         // over the lane's rows is bounded below at the corner of their (|x|^2, |x|) box that A's
         // and B's signs select, so a lane whose largest value is below it passes nothing; flagged
         // (NaN) rows disable it) settles most blocks from registers.  Another block goes through
-        // the wave's 4 KiB of slot 1 half a block (one row block m) at a time: the pre-test over
+        // the wave's 4 KiB of slot 1 one row block m at a time: the pre-test over
         // its 16 values builds a bit mask without branches; lanes l and l + 32 hold the same query,
         // so one atomic reserves both lanes' places; the appends read the values back from LDS.
-        uint32_t valid = ~0u;
+        Mask valid = ~Mask(0);
         if (rc < TN) {
             valid = 0;
 #pragma unroll 1
-            for (int t = 0; t < 32; ++t) valid |= uint32_t(uint32_t(row_of(t)) < rc) << t;
+            for (int t = 0; t < 16 * MB; ++t) valid |= Mask(uint32_t(row_of(t)) < rc) << t;
         }
         float bxlo = INFINITY, bxhi = -INFINITY, bnlo = INFINITY, bnhi = -INFINITY;
         bool bflag = false;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
+        for (int c = 0; c < 4 * MB; ++c) {
             const float4 b = gbox[row_of(4 * c) >> 2];  // rows 4c .. 4c + 3 of the lane: one group
             bflag |= !(b.x == b.x);
             bxlo = fminf(bxlo, b.x);
@@ -840,10 +858,10 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
                 const float lo = fmaf(pt.A, pt.A >= 0.0f ? bxlo : bxhi, fmaf(pt.B, pt.B >= 0.0f ? bnlo : bnhi, pt.C));
                 float mx = -INFINITY;
 #pragma unroll
-                for (int t = 0; t < 32; ++t) mx = fmaxf(mx, acc[t >> 4][n][t & 15]);
+                for (int t = 0; t < 16 * MB; ++t) mx = fmaxf(mx, acc[t >> 4][n][t & 15]);
                 skip = mx < lo;
             }
-            // half block m of the dump: values 16m .. 16m + 15
+            // row block m into the dump: values 16m .. 16m + 15
             auto dump_half = [&](auto MC) {
                 constexpr int m = decltype(MC)::value;
 #pragma unroll
@@ -856,7 +874,7 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
                 // re-read the row norms and the dump from LDS below
                 asm volatile("" ::: "memory");
             };
-            uint32_t mk = 0;
+            Mask mk = 0;
             if (!skip) {
                 auto test_half = [&](auto MC) {
                     constexpr int m = decltype(MC)::value;
@@ -869,17 +887,18 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
                         const f32x4v v = dump[c * 64];
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
-                            mk |= uint32_t(!(v[e] < fmaf(pt.A, xx[e], fmaf(pt.B, nx[e], pt.C)))) << (16 * m + 4 * c + e);
+                            mk |= Mask(!(v[e] < fmaf(pt.A, xx[e], fmaf(pt.B, nx[e], pt.C)))) << (16 * m + 4 * c + e);
                     }
                 };
                 test_half(std::integral_constant<int, 0>());
                 test_half(std::integral_constant<int, 1>());
+                if constexpr (MB > 2) test_half(std::integral_constant<int, 2>());
                 mk &= valid;
             }
             // a block with nothing to append skips the atomic and its wait, which would also wait
             // for the next tile's loads in flight
             if (!__ballot(mk != 0u)) return;
-            const uint32_t cnt = uint32_t(__popc(mk));
+            const uint32_t cnt = uint32_t(__builtin_popcountll(uint64_t(mk)));
             const uint32_t other = uint32_t(__shfl_xor(int(cnt), 32));
             uint32_t base = 0;
             if (hh == 0 && cnt + other) base = atomicAdd(a.cnt + qi, cnt + other);
@@ -887,7 +906,7 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
             const float* src = reinterpret_cast<const float*>(dump);
             auto append_half = [&](auto MC) {
                 constexpr int m = decltype(MC)::value;
-                uint32_t mh = (mk >> (16 * m)) & 0xFFFFu;
+                uint32_t mh = uint32_t(mk >> (16 * m)) & 0xFFFFu;
                 if (!__ballot(mh != 0u)) return;
                 dump_half(MC);
                 while (mh && pos < a.cap) {
@@ -904,6 +923,7 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
             };
             append_half(std::integral_constant<int, 0>());
             append_half(std::integral_constant<int, 1>());
+            if constexpr (MB > 2) append_half(std::integral_constant<int, 2>());
         };
         block(std::integral_constant<int, 0>());
         block(std::integral_constant<int, 1>());
@@ -1094,18 +1114,19 @@ va_status launch_screen(va_context* ctx, const ScreenArgs& a) {
 
 va_status launch_screen16(va_context* ctx, const ScreenArgs& a) {
     using namespace s16;
+    using Sh = Shape<kWaves, kQueryBlocks, kRowBlocks>;
     const uint64_t nqb = (a.Q + TQ - 1) / TQ;
-    const uint64_t ntb = (a.N + TN - 1) / TN;
+    const uint64_t ntb = (a.N + Sh::TN - 1) / Sh::TN;
     const uint64_t tiles = nqb * ((ntb + kXcds - 1) / kXcds) * kXcds;
     if (tiles == 0) return VA_OK;
     if (tiles > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "screen grid too large (%llu)", (unsigned long long)tiles);
     // persistent: one workgroup per CU (its LDS fills one), a multiple of the XCD count
     const uint64_t cus = std::max<uint64_t>(uint64_t(ctx->num_cus), kXcds) / kXcds * kXcds;
     const uint64_t grid = std::min(tiles, cus);
-    auto kern = &screen16_kernel<kWaves, kQueryBlocks>;
+    auto kern = &screen16_kernel<kWaves, kQueryBlocks, kRowBlocks>;
     VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, LDS));
-    kern<<<dim3(uint32_t(grid)), dim3(64 * kWaves), LDS, ctx->stream>>>(a);
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, Sh::LDS));
+    kern<<<dim3(uint32_t(grid)), dim3(64 * kWaves), Sh::LDS, ctx->stream>>>(a);
     VA_CHECK_LAUNCH(ctx);
     return VA_OK;
 }
