@@ -110,6 +110,24 @@ def test_index_search_many_tiles_per_workgroup(ctx, metric, name):
     ix.close()
 
 
+@pytest.mark.parametrize("k", [1, 1024])
+@pytest.mark.parametrize("metric,name", [(L2SQ, "euclidean"), (COSINE, "cosine")])
+def test_index_search_k_extremes(ctx, metric, name, k):
+    """k = 1 and the largest k (1024) through the shadow screen, 520 queries (three query blocks,
+    the last partial) over 40,000 rows: the sample rank, the candidate capacity and the rerank band
+    at both ends."""
+    from vectoraccelerate_amd import AcceleratedVectorIndex, IndexConfiguration
+
+    x, q = _data(60 + metric, 40_000, 64, 520, normalise=metric == COSINE)
+    ix = AcceleratedVectorIndex(IndexConfiguration.flat(64, 1000, metric=name), ctx)
+    ix.insert(vectors=x)
+    gi, gd = _index_search(ix, q, k)
+    fi, fd = _fused(ctx, metric, q, x, k, screen=1)
+    np.testing.assert_array_equal(gi, fi)
+    np.testing.assert_array_equal(gd.view(np.uint32), fd.view(np.uint32))
+    ix.close()
+
+
 def test_removing_more_than_max_k_nearest_rows_keeps_k_results(ctx, oracle):
     """ADVICE: k + deletedCount > VA_MAX_K must not shorten the result."""
     from vectoraccelerate_amd import AcceleratedVectorIndex, IndexConfiguration
