@@ -128,6 +128,34 @@ def test_index_search_k_extremes(ctx, metric, name, k):
     ix.close()
 
 
+@pytest.mark.parametrize("metric,name", [(L2SQ, "euclidean"), (COSINE, "cosine")])
+def test_index_search_overflow_through_the_shadow_screen(ctx, metric, name):
+    """A forced candidate cap of 64 (and the sample's k-th key as the threshold) overflows the
+    screen's lists: the appends stop at the cap, the overflowed queries finish in the device
+    fallback, and the result still equals the fp32 scan's."""
+    from vectoraccelerate_amd import AcceleratedVectorIndex, IndexConfiguration, _lib
+
+    x, q = _data(70 + metric, 30_000, 64, 300, normalise=metric == COSINE)
+    ix = AcceleratedVectorIndex(IndexConfiguration.flat(64, 1000, metric=name), ctx)
+    ix.insert(vectors=x)
+    k = 40
+    ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 64)
+    ctx.set_option(_lib.VA_OPT_SAMPLE_RANK, 2**32)
+    ctx.set_profiling(True)
+    try:
+        gi, gd = _index_search(ix, q, k)
+        t = ctx.last_scan_timings()
+    finally:
+        ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 0)
+        ctx.set_option(_lib.VA_OPT_SAMPLE_RANK, 0)
+        ctx.set_profiling(False)
+    assert t["screened"] == 1 and t["overflow_rows"] > 0, t
+    fi, fd = _fused(ctx, metric, q, x, k, screen=1)
+    np.testing.assert_array_equal(gi, fi)
+    np.testing.assert_array_equal(gd.view(np.uint32), fd.view(np.uint32))
+    ix.close()
+
+
 def test_removing_more_than_max_k_nearest_rows_keeps_k_results(ctx, oracle):
     """ADVICE: k + deletedCount > VA_MAX_K must not shorten the result."""
     from vectoraccelerate_amd import AcceleratedVectorIndex, IndexConfiguration
