@@ -772,10 +772,12 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
                     // this k-step's fragments are in registers: publish stage s+1, free slot s
                     wait_vmcnt<0>();
                     barrier();
+                    // slot s is free from here: its next stage goes first (the slots past the last
+                    // stage stay free)
+                    if (s + 2 < nst) issue(s + 2);
                     read_frags(cur ^ 1, slot ^ 1u, 0);
                     mma(cur);
                     interleave();
-                    if (s + 2 < nst) issue(s + 2);  // the slots past the last stage stay free
                 }
             }
         }
