@@ -122,7 +122,9 @@ typedef struct {
     uint32_t candidate_cap; /* per-query candidate capacity                            */
     uint32_t overflow_rows; /* queries that took the exact chunked path               */
     uint32_t scan_launches; /* number of scan-kernel launches timed in scan_ms        */
-    uint32_t screened;      /* 1 when an fp32 search ran the fp16 screening scan      */
+    uint32_t screened;      /* fp16 screening scan of an fp32 search: 0 none, 1 over   
+                             * converted fp32 rows (flat) or the IVF list shadow, 2 over
+                             * the native index's fp16 shadow (screen16_kernel)        */
     uint32_t rerank_rows;   /* screened search: rows re-scored exactly, all queries   */
 } va_scan_timings;
 va_status va_context_set_profiling(va_context* ctx, int enable);

@@ -14,6 +14,10 @@ import numpy as np
 
 SENT = 0xFFFFFFFF
 RTOL = 1e-4
+# fp32's smallest normal number: below it a float has no relative precision to speak of (products
+# of 1e-30 entries underflow to zero in any fp32 computation, the oracle's own fp32 output
+# included), so distances closer than this to the float64 value count as equal.
+ABS_FLOOR = float(np.finfo(np.float32).tiny)
 
 L2SQ, COSINE, DOT, L2 = 0, 1, 2, 3
 
@@ -73,7 +77,7 @@ def check_topk(metric: int, q: np.ndarray, x: np.ndarray, k: int, gi: np.ndarray
         m = metric if metric != L2 else L2SQ
         true_d = exact_distances(m, q[r], x[ids])
         scale = pair_scale(m, q[r], x[ids])
-        tol = rtol * np.maximum(np.abs(true_d), scale)
+        tol = np.maximum(rtol * np.maximum(np.abs(true_d), scale), ABS_FLOOR)
         if gd is not None:
             rep = gd[r][gv].astype(np.float64)
             if metric == L2:
@@ -86,7 +90,8 @@ def check_topk(metric: int, q: np.ndarray, x: np.ndarray, k: int, gi: np.ndarray
         ref_ids = oi[r][ov].astype(np.int64)
         ref_d = exact_distances(m, q[r], x[ref_ids])
         ref_scale = pair_scale(m, q[r], x[ref_ids])
-        tol2 = rtol * np.maximum(np.maximum(np.abs(ref_d), ref_scale), np.maximum(np.abs(true_d), scale))
+        tol2 = np.maximum(rtol * np.maximum(np.maximum(np.abs(ref_d), ref_scale), np.maximum(np.abs(true_d), scale)),
+                          ABS_FLOOR)
         bad = np.abs(true_d - ref_d) > tol2
         assert not bad.any(), (
             f"query {r}: rank distances differ at {np.nonzero(bad)[0][:5]}: gpu ids {ids[bad][:5]} "

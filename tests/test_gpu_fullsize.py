@@ -43,16 +43,93 @@ def test_configs1_cosine_top100_full(ctx, oracle):
     assert np.all(np.diff(gd, axis=1) >= 0)
     assert np.all(gi != SENT)
     assert all(len(set(r)) == k for r in gi)
-    # oracle on a subset against the full database
-    xh = x.cpu().numpy()
-    qh = q.cpu().numpy()
-    sub = np.array([0, 1, 511, 1023])
-    oi, od = oracle.flat_topk(COSINE, qh[sub], xh, k)
-    check_topk(COSINE, qh[sub], xh, k, gi[sub], gd[sub], oi, od)
     # batch == sequential for one query
     one = FusedL2TopKKernel(ctx).execute(q[7:8].contiguous(), x, FusedL2TopKParameters(1, N, D, k),
                                          metric=Metric.cosine)
     np.testing.assert_array_equal(one.indices.cpu().numpy().view(np.uint32)[0], gi[7])
+    # the headline route: AcceleratedVectorIndex.search over the index's fp16 shadow (screen16_kernel),
+    # bit for bit equal to va_fused_topk over the fp32 rows for all 1024 queries
+    hi, hd, t = _index_search_full(ctx, x, q, COSINE, k)
+    note(f"configs[1] index searched: {t}")
+    assert t["screened"] == 2, t
+    np.testing.assert_array_equal(hi, gi)
+    np.testing.assert_array_equal(hd.view(np.uint32), gd.view(np.uint32))
+    # oracle on 64 queries against the full database
+    xh = x.cpu().numpy()
+    qh = q.cpu().numpy()
+    sub = np.arange(0, Q, Q // 64)
+    oi, od = oracle.flat_topk(COSINE, qh[sub], xh, k)
+    note("configs[1] oracle subset done")
+    check_topk(COSINE, qh[sub], xh, k, hi[sub], hd[sub], oi, od)
+
+
+def test_configs1_metric_wording_l2_top10_full(ctx, oracle):
+    """The metric's own wording at configs[1]'s shape: flat L2^2 top-10 over 1,000,000 x 1536
+    N(0,1) rows, Q=1024, through the index (screen16_kernel), bit for bit equal to the fp32-only
+    scan, 64 queries against the oracle."""
+    import torch
+    from vectoraccelerate_amd import _lib
+
+    N, D, Q, k = 1_000_000, 1536, 1024, 10
+    g = torch.Generator(device="cuda").manual_seed(10)
+    x = torch.randn(N, D, device="cuda", generator=g)
+    gq = torch.Generator(device="cuda").manual_seed(11)
+    src = torch.randint(0, N, (Q,), device="cuda", generator=gq)
+    q = (x[src] + 0.3 * torch.randn(Q, D, device="cuda", generator=gq)).contiguous()
+    hi, hd, t = _index_search_full(ctx, x, q, L2SQ, k)
+    assert t["screened"] == 2, t
+    np.testing.assert_array_equal(hi[:, 0], src.cpu().numpy())
+    # the fp32-only scan of the same search
+    from vectoraccelerate_amd.context import dptr
+
+    fi = ctx.empty((Q, k), torch.int32)
+    fd = ctx.empty((Q, k), torch.float32)
+    ctx.set_option(_lib.VA_OPT_SCREEN, 1)
+    try:
+        ctx.order_after_torch()
+        ctx.check(ctx.lib.va_fused_topk(ctx.handle, L2SQ, dptr(q), dptr(x), Q, N, D, k, dptr(fi), dptr(fd)),
+                  "va_fused_topk")
+        ctx.synchronize()
+    finally:
+        ctx.set_option(_lib.VA_OPT_SCREEN, 0)
+    note("configs[1] L2 top-10: fp32 scan done")
+    np.testing.assert_array_equal(hi, fi.cpu().numpy().view(np.uint32))
+    np.testing.assert_array_equal(hd.view(np.uint32), fd.cpu().numpy().view(np.uint32))
+    xh = x.cpu().numpy()
+    qh = q.cpu().numpy()
+    sub = np.arange(0, Q, Q // 64)
+    oi, od = oracle.flat_topk(L2SQ, qh[sub], xh, k)
+    check_topk(L2SQ, qh[sub], xh, k, hi[sub], hd[sub], oi, od)
+
+
+def _index_search_full(ctx, x, q, metric, k):
+    """Insert device rows x into a native index and search it once with profiling on:
+    (handles, distances, profiling record)."""
+    import ctypes as C
+
+    import torch
+    from vectoraccelerate_amd.context import dptr
+
+    N, D = x.shape
+    Q = q.shape[0]
+    h = C.c_void_p()
+    ctx.check(ctx.lib.va_index_create(ctx.handle, D, N, C.byref(h)), "va_index_create")
+    try:
+        ctx.order_after_torch()
+        ctx.check(ctx.lib.va_index_insert(ctx.handle, h, dptr(x), N, None), "va_index_insert")
+        hi = ctx.empty((Q, k), torch.int32)
+        hd = ctx.empty((Q, k), torch.float32)
+        ctx.set_profiling(True)
+        try:
+            ctx.check(ctx.lib.va_index_search(ctx.handle, h, metric, dptr(q), Q, k, dptr(hi), dptr(hd)),
+                      "va_index_search")
+            ctx.synchronize()
+            t = ctx.last_scan_timings()
+        finally:
+            ctx.set_profiling(False)
+    finally:
+        ctx.lib.va_index_destroy(h)
+    return hi.cpu().numpy().view(np.uint32), hd.cpu().numpy(), t
 
 
 def test_configs2_int8_top10_full(ctx, oracle):
@@ -85,7 +162,7 @@ def test_configs2_int8_top10_full(ctx, oracle):
     gi, gd = sq.searchTopK(qc, xc, k)
     note("configs[2] searched")
     assert np.all(np.diff(gd, axis=1) >= 0)
-    sub = np.array([0, 1, 2047, 4095])
+    sub = np.arange(0, Q, Q // 64)
     oi, od = oracle.i8_topk(qc.cpu().numpy()[sub], xch, k)
     check_topk_exact(gi[sub], gd[sub], oi, od)
 
@@ -113,7 +190,7 @@ def test_configs3_binary_top100_full(ctx, oracle):
     np.testing.assert_array_equal(gi[:4, 0], [5, 123456, 30_000_000, N - 1])
     assert np.all(gd[:4, 0] == 0)
     assert np.all(np.diff(gd.astype(np.int64), axis=1) >= 0)
-    sub = np.array([0, 3, 100, 255])
+    sub = np.r_[0:4, 4:Q:4][:64]
     xh = x.cpu().numpy().view(np.uint32)
     oi, od = oracle.hamming_topk(q.cpu().numpy().view(np.uint32)[sub], xh, k)
     check_topk_exact(gi[sub], gd[sub], oi, od)

@@ -149,7 +149,7 @@ def test_index_search_overflow_through_the_shadow_screen(ctx, metric, name):
         ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 0)
         ctx.set_option(_lib.VA_OPT_SAMPLE_RANK, 0)
         ctx.set_profiling(False)
-    assert t["screened"] == 1 and t["overflow_rows"] > 0, t
+    assert t["screened"] == 2 and t["overflow_rows"] > 0, t
     fi, fd = _fused(ctx, metric, q, x, k, screen=1)
     np.testing.assert_array_equal(gi, fi)
     np.testing.assert_array_equal(gd.view(np.uint32), fd.view(np.uint32))

@@ -1346,7 +1346,7 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     ctx->last_scan.scan_launches = 1;
     ctx->last_scan.sample_rows = uint32_t(S);
     ctx->last_scan.candidate_cap = uint32_t(cap);
-    ctx->last_scan.screened = 1;
+    ctx->last_scan.screened = in.xh ? 2u : 1u;  // 2: screen16_kernel over the fp16 shadow
     // ---- 4. k-th smallest upper bound among the candidates (overflowed lists are listed) ------
     {
         SelectArgs a;
