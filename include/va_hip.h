@@ -305,10 +305,35 @@ typedef struct {
     uint64_t capacity;     /* slots allocated */
     const float* rows;     /* device, [slots x dimension]; valid until the next insert or compact */
     uint32_t next_handle;  /* the id the next inserted vector gets */
+    uint32_t nlist;        /* IVF lists (0: flat index) */
+    uint32_t nprobe;       /* IVF lists probed per query */
+    uint32_t routing_threshold; /* IVF: fewer live vectors than this are searched flat (0: never) */
+    uint32_t trained;      /* IVF: 1 once centroids are installed */
+    uint32_t ivf_routed;   /* 1 when va_index_search currently goes to the inverted lists */
+    const float* centroids; /* IVF: device, [nlist x dimension] once trained (until the next train) */
+    const va_ivf* lists;   /* IVF: the inverted lists over the slots (row id = slot; NULL while
+                            * untrained or empty), for va_ivf_get_lists / va_ivf_probe; valid
+                            * until the next insert, compact or train */
 } va_index_info;
 /* Returns nonzero to accept a result (IndexFilter, Index/AcceleratedVectorIndex.swift:1188-1265). */
 typedef int (*va_index_filter)(uint32_t handle, void* user);
 va_status va_index_create(va_context* ctx, uint32_t dim, uint32_t capacity, va_index** out);
+/* An IVF index (IndexConfiguration.ivf(dimension:nlist:nprobe:capacity:routingThreshold),
+ * Index/Types/IndexConfiguration.swift): flat until trained; once trained, va_index_search probes
+ * the nprobe nearest of nlist lists, unless fewer than routing_threshold (> 0) vectors are live
+ * (AcceleratedVectorIndex.search routing, Index/AcceleratedVectorIndex.swift:911-926).  L2^2 only.
+ * 1 <= nprobe <= nlist. */
+va_status va_index_create_ivf(va_context* ctx, uint32_t dim, uint32_t capacity, uint32_t nlist, uint32_t nprobe,
+                              uint32_t routing_threshold, va_index** out);
+/* Train an IVF index (train(), Index/AcceleratedVectorIndex.swift:406-446): with centroids
+ * (device, [nlist x dim]) installs them; with NULL runs k-means on the device over the live
+ * vectors (compacting the index first; k-means++ seeding from splitmix64(seed), at most 25 Lloyd
+ * iterations, threshold 0.001, as IVFStructure.train, Index/Internal/IVFStructure.swift:202-259).
+ * Then every vector is assigned to its nearest list (device CSR); later inserts join their
+ * nearest lists and compact() rebuilds the lists, so the index never needs retraining to stay
+ * searchable.  Removed vectors stay in the lists and are excluded inside every scan, so k is
+ * never widened by deletions.  A flat index: no-op.  Synchronises. */
+va_status va_index_train(va_context* ctx, va_index* index, const float* centroids, uint64_t seed);
 va_status va_index_destroy(va_index* index);
 /* Append num_vectors device rows; out_handles (host, may be NULL) gets their handles.  Grows the
  * storage by doubling (synchronising the context then).  insert(_:) / insert(contentsOf:),
@@ -330,14 +355,23 @@ va_status va_index_get_vector(va_context* ctx, const va_index* index, uint32_t h
 /* Exact top-k over the live vectors for each device query: out_handles / out_dist [Q x k]
  * (device), ordered by (distance, slot); slots past the number of live vectors hold
  * VA_SENTINEL_INDEX / +inf.  k <= VA_MAX_K whatever the number of removed vectors.
- * searchUnfiltered / searchBatchGPU, AcceleratedVectorIndex.swift:1103-1186, 1278-1374. */
+ * searchUnfiltered / searchBatchGPU, AcceleratedVectorIndex.swift:1103-1186, 1278-1374.
+ * A trained IVF index (see va_index_train) returns the exact top-k over the live vectors of each
+ * query's nprobe nearest lists instead (searchIVF / searchIVFBatch, :1378-1481), L2^2 only. */
 va_status va_index_search(va_context* ctx, const va_index* index, va_metric metric, const float* queries,
                           uint32_t num_queries, uint32_t k, uint32_t* out_handles, float* out_dist);
 /* The k nearest live vectors that pass filter (NULL: all), for one device query: round after
  * round the nearest not yet examined vectors are fetched and filtered on the host, so results
  * are exact however many the filter rejects.  out_handles / out_dist are host arrays of k;
  * *out_count results were found; *out_examined (may be NULL) vectors were examined.
- * searchFiltered, AcceleratedVectorIndex.swift:1188-1265. */
+ * searchFiltered, AcceleratedVectorIndex.swift:1188-1265.  Cost: rounds of 2k, 4k, ... up to
+ * VA_MAX_K rows (one scan each); if the filter has still not accepted k, one scan computes the
+ * distances of every row, a device sort orders the unexamined ones by (distance, slot), and they
+ * are filtered in that order in host batches of 64K rows: at most log2(VA_MAX_K / 16) + 2 scans
+ * and one sort whatever the filter rejects.  A trained IVF index filters its lists' rows the
+ * same way, round after round (each round an IVF search excluding the rows already examined),
+ * until k pass or the probed lists are exhausted (searchIVF with a filter, :1378-1431, which
+ * over-fetches 3k instead). */
 va_status va_index_search_filtered(va_context* ctx, va_index* index, va_metric metric, const float* query, uint32_t k,
                                    va_index_filter filter, void* user, uint32_t* out_handles, float* out_dist,
                                    uint32_t* out_count, uint32_t* out_examined);

@@ -121,14 +121,19 @@ def test_ivf_index_matches_oracle_and_routes(ctx, oracle):
     res = idx.search(queries=q, k=10)
     gi = np.array([[r.id.stableID for r in rr.results] for rr in res], np.uint32)
     gd = np.array([[r.distance for r in rr.results] for rr in res], np.float32)
-    st = idx._ivf_structure()
-    off, ids = st.lists()
-    probes = idx._ivf_pipe.findNearestCentroids(q, st).cpu().numpy().view(np.uint32)
+    off, ids = idx.lists()
+    probes = idx.probes(q)
+    np.testing.assert_array_equal(probes, oracle.ivf_probe(q, c, 4))
     oi, od = oracle.ivf_scan(q, x, off, ids, probes, 10)
     check_topk(L2SQ, q, x, 10, gi, gd, oi, od)
     # routing threshold: below it the index answers exactly (flat)
-    idx.configuration.routingThreshold = 10**9
-    flat = idx.search(q[0], k=10)
+    flat_ix = AcceleratedVectorIndex(IndexConfiguration.ivf(dimension=48, nlist=32, nprobe=4, capacity=1000,
+                                                            routingThreshold=10**9), ctx)
+    flat_ix.insert(vectors=x)
+    flat_ix.train(c)
+    flat = flat_ix.search(q[0], k=10)
     fi, fd = oracle.flat_topk(L2SQ, q[:1], x, 10)
     check_topk(L2SQ, q[:1], x, 10, np.array([[r.id.stableID for r in flat.results]], np.uint32),
                np.array([[r.distance for r in flat.results]], np.float32), fi, fd)
+    flat_ix.close()
+    idx.close()

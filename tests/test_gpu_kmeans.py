@@ -220,9 +220,9 @@ def test_index_train_without_centroids(ctx, oracle):
     live = x[1:]
     init = live[oracle.kmeans_plusplus(live, 16, 77)]
     ocen, oassign, *_ = oracle.kmeans_fit(live, init, 25, 0.001)
-    np.testing.assert_array_equal(idx._centroids.cpu().numpy(), ocen)
+    np.testing.assert_array_equal(idx.centroids(), ocen)
     # the lists: every stored row under its nearest trained centroid, in row order
-    off, ids = idx._ivf_structure().lists()
+    off, ids = idx.lists()
     # train() compacts first: the stored rows are the live rows, in insertion order
     assert idx.count == live.shape[0]
     stored = np.array([idx.vector(h) for h in hs[1:]], np.float32)

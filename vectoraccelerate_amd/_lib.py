@@ -86,6 +86,8 @@ SIGNATURES: dict[str, tuple] = {
     "va_ivf_scan": (_st, [_p, _p, _p, _u32, _p, _u32, _u32, _p, _p]),
     "va_ivf_search": (_st, [_p, _p, _p, _u32, _u32, _u32, _p, _p]),
     "va_index_create": (_st, [_p, _u32, _u32, C.POINTER(_p)]),
+    "va_index_create_ivf": (_st, [_p, _u32, _u32, _u32, _u32, _u32, C.POINTER(_p)]),
+    "va_index_train": (_st, [_p, _p, _p, _u64]),
     "va_index_destroy": (_st, [_p]),
     "va_index_insert": (_st, [_p, _p, _p, _u32, _p]),
     "va_index_remove": (_st, [_p, _p, _p, _u32, C.POINTER(_u32)]),
@@ -138,6 +140,13 @@ class IndexInfo(C.Structure):
         ("capacity", C.c_uint64),
         ("rows", C.c_void_p),
         ("next_handle", C.c_uint32),
+        ("nlist", C.c_uint32),
+        ("nprobe", C.c_uint32),
+        ("routing_threshold", C.c_uint32),
+        ("trained", C.c_uint32),
+        ("ivf_routed", C.c_uint32),
+        ("centroids", C.c_void_p),
+        ("lists", C.c_void_p),
     ]
 
 

@@ -14,6 +14,8 @@
 // not-yet-examined rows round after round (rows already examined are excluded the same way), so
 // the accepted results are exactly the k nearest rows that pass the filter, in order, however
 // many rows it rejects.
+#include <rocprim/device/device_radix_sort.hpp>
+
 #include <algorithm>
 #include <vector>
 
@@ -34,6 +36,15 @@ struct va_index {
     uint32_t* slot_stable = nullptr;  // [capacity] stable id of each slot
     std::vector<uint32_t> stable_to_slot;  // kTombstone for removed ids
     std::vector<uint32_t> slot_to_stable;
+    // IVF (IndexConfiguration.ivf): inverted lists over the slots, built when the index is trained
+    // and kept current by insert (new slots appended to their nearest lists) and compact (lists
+    // rebuilt from the trained centroids); deleted slots stay in the lists and are excluded by the
+    // deletion mask inside the scan
+    uint32_t nlist = 0;           // 0: flat index
+    uint32_t nprobe = 0;
+    uint32_t routing = 0;         // routingThreshold: fewer live vectors than this search flat
+    float* centroids = nullptr;   // [nlist x dim] once trained
+    va_ivf* ivf = nullptr;        // lists over slots [0, slots); nullptr while untrained or empty
 };
 
 namespace va {
@@ -177,6 +188,23 @@ va_status set_bytes(va_context* ctx, uint8_t* dst, const std::vector<uint32_t>& 
     return VA_OK;
 }
 
+// (Re)builds the inverted lists over every slot from the trained centroids (none while empty).
+va_status rebuild_lists(va_context* ctx, va_index* ix) {
+    if (ix->ivf) {
+        (void)va_ivf_destroy(ix->ivf);
+        ix->ivf = nullptr;
+    }
+    if (!ix->centroids || ix->slots == 0) return VA_OK;
+    return va_ivf_build(ctx, ix->centroids, ix->nlist, ix->rows, ix->slots, ix->dim, &ix->ivf);
+}
+
+// Whether a search goes to the inverted lists (AcceleratedVectorIndex.search routing,
+// Index/AcceleratedVectorIndex.swift:911-926): trained, and not below the routing threshold.
+bool ivf_route(const va_index* ix) {
+    const uint32_t live = ix->slots - ix->deleted;
+    return ix->ivf != nullptr && !(ix->routing > 0 && live < ix->routing);
+}
+
 va_status check_ctx(va_context* ctx, const va_index* ix, const char* fn) {
     if (!ctx) return VA_ERR_INVALID_ARG;
     VA_REQUIRE(ctx, ix != nullptr, "%s: NULL index", fn);
@@ -218,8 +246,73 @@ va_status va_index_destroy(va_index* index) {
     (void)hipDeviceSynchronize();
     va::DevBuffers b = va::current(index);
     b.release();
+    if (index->ivf) (void)va_ivf_destroy(index->ivf);
+    if (index->centroids) (void)hipFree(index->centroids);
     delete index;
     return VA_OK;
+}
+
+va_status va_index_create_ivf(va_context* ctx, uint32_t dim, uint32_t capacity, uint32_t nlist, uint32_t nprobe,
+                              uint32_t routing_threshold, va_index** out) {
+    if (!ctx) return VA_ERR_INVALID_ARG;
+    VA_REQUIRE(ctx, out != nullptr, "va_index_create_ivf: NULL output");
+    *out = nullptr;
+    VA_REQUIRE(ctx, nlist >= 1 && nprobe >= 1 && nprobe <= nlist, "invalid IVF parameters nlist=%u nprobe=%u", nlist,
+               nprobe);
+    VA_REQUIRE(ctx, dim <= 4096, "dimension must be 1-4096, got %u", dim);
+    va_index* ix = nullptr;
+    VA_CHECK_STATUS(va_index_create(ctx, dim, capacity, &ix));
+    ix->nlist = nlist;
+    ix->nprobe = nprobe;
+    ix->routing = routing_threshold;
+    *out = ix;
+    return VA_OK;
+}
+
+va_status va_index_train(va_context* ctx, va_index* index, const float* centroids, uint64_t seed) {
+    VA_CHECK_STATUS(va::check_ctx(ctx, index, "va_index_train"));
+    if (index->nlist == 0) return VA_OK;  // a flat index has nothing to train (train(), :405-407)
+    va::DeviceGuard g(ctx->device);
+    const uint32_t C = index->nlist, D = index->dim;
+    struct Tmp {
+        void* p[2] = {};
+        ~Tmp() {
+            for (void* q : p)
+                if (q) (void)hipFree(q);
+        }
+    } t;
+    float* cen = nullptr;
+    VA_CHECK_HIP(ctx, hipMalloc(reinterpret_cast<void**>(&cen), uint64_t(C) * D * 4));
+    t.p[0] = cen;
+    if (centroids) {
+        VA_CHECK_HIP(ctx, hipMemcpyAsync(cen, centroids, uint64_t(C) * D * 4, hipMemcpyDeviceToDevice, ctx->stream));
+    } else {
+        // k-means over the live vectors (IVFStructure.train, Index/Internal/IVFStructure.swift:202-259:
+        // k-means++ seeding, at most 25 Lloyd iterations, convergence threshold 0.001)
+        const uint32_t live = index->slots - index->deleted;
+        VA_REQUIRE(ctx, live > 0, "Cannot train IVF index with no vectors");
+        VA_REQUIRE(ctx, live >= C, "Need at least %u vectors for %u clusters, got %u", C, C, live);
+        // retraining replaces the old lists (not rebuilt by the compaction below)
+        if (index->ivf) (void)va_ivf_destroy(index->ivf);
+        index->ivf = nullptr;
+        if (index->centroids) (void)hipFree(index->centroids);
+        index->centroids = nullptr;
+        VA_CHECK_STATUS(va_index_compact(ctx, index));  // the live rows are then slots [0, live)
+        float* init = nullptr;
+        VA_CHECK_HIP(ctx, hipMalloc(reinterpret_cast<void**>(&init), uint64_t(C) * D * 4 + uint64_t(live) * 4));
+        t.p[1] = init;
+        uint32_t* assign = reinterpret_cast<uint32_t*>(init + uint64_t(C) * D);
+        VA_CHECK_STATUS(va_kmeans_plusplus(ctx, index->rows, live, D, C, seed, init, nullptr));
+        VA_CHECK_STATUS(va_kmeans_fit(ctx, index->rows, live, D, C, init, 25, 0.001f, cen, assign, nullptr, nullptr,
+                                      nullptr));
+    }
+    VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (index->centroids) (void)hipFree(index->centroids);
+    index->centroids = cen;
+    t.p[0] = nullptr;
+    // the lists over every slot (IVFStructure.train clears them; AcceleratedVectorIndex.train
+    // reassigns every vector, :438-446)
+    return va::rebuild_lists(ctx, index);
 }
 
 va_status va_index_insert(va_context* ctx, va_index* index, const float* vectors, uint32_t num_vectors,
@@ -249,6 +342,10 @@ va_status va_index_insert(va_context* ctx, va_index* index, const float* vectors
         if (out_handles) out_handles[i] = first + i;
     }
     index->slots += n;
+    // a trained IVF index: the new slots go to the end of their nearest lists
+    // (IVFStructure.assignToCluster, Index/Internal/IVFStructure.swift:280-287)
+    if (index->ivf) return va_ivf_add(ctx, index->ivf, index->rows + uint64_t(s0) * dim, n, dim, s0);
+    if (index->centroids) return va::rebuild_lists(ctx, index);
     return VA_OK;
 }
 
@@ -313,7 +410,8 @@ va_status va_index_compact(va_context* ctx, va_index* index) {
     index->slot_to_stable.swap(s2h);
     index->slots = n;
     index->deleted = 0;
-    return VA_OK;
+    // the lists name slots, which moved: rebuilt from the trained centroids
+    return va::rebuild_lists(ctx, index);
 }
 
 va_status va_index_get_info(const va_index* index, va_index_info* out) {
@@ -325,6 +423,13 @@ va_status va_index_get_info(const va_index* index, va_index_info* out) {
     out->capacity = index->capacity;
     out->rows = index->rows;
     out->next_handle = uint32_t(index->stable_to_slot.size());
+    out->nlist = index->nlist;
+    out->nprobe = index->nprobe;
+    out->routing_threshold = index->routing;
+    out->trained = index->centroids != nullptr;
+    out->ivf_routed = va::ivf_route(index);
+    out->centroids = index->centroids;
+    out->lists = index->ivf;
     return VA_OK;
 }
 
@@ -361,9 +466,17 @@ va_status va_index_search(va_context* ctx, const va_index* index, va_metric metr
         if (out_dist) VA_CHECK_STATUS(va::fill_u32(ctx, reinterpret_cast<uint32_t*>(out_dist), total, 0x7F800000u));
         return VA_OK;
     }
-    VA_CHECK_STATUS(va::flat_topk(ctx, va::metric_op(metric), queries, index->rows, num_queries, index->slots,
-                                  index->dim, k, out_handles, out_dist, index->pitch ? index->shadow : nullptr,
-                                  index->pitch ? index->norms : nullptr, index->deleted ? index->skip : nullptr));
+    if (va::ivf_route(index)) {
+        // searchIVF / searchIVFBatch (Index/AcceleratedVectorIndex.swift:1378-1481): the nprobe
+        // nearest lists, deleted slots excluded inside the scan (no over-fetch)
+        VA_REQUIRE(ctx, metric == VA_METRIC_L2SQ, "an IVF index searches by L2^2 only (metric %d)", int(metric));
+        VA_CHECK_STATUS(va::ivf_search_masked(ctx, index->ivf, queries, num_queries, index->nprobe, k, out_handles,
+                                              out_dist, index->deleted ? index->skip : nullptr));
+    } else {
+        VA_CHECK_STATUS(va::flat_topk(ctx, va::metric_op(metric), queries, index->rows, num_queries, index->slots,
+                                      index->dim, k, out_handles, out_dist, index->pitch ? index->shadow : nullptr,
+                                      index->pitch ? index->norms : nullptr, index->deleted ? index->skip : nullptr));
+    }
     va::slots_to_handles_kernel<<<dim3(va::grid_for(total)), dim3(256), 0, ctx->stream>>>(out_handles, total,
                                                                                          index->slot_stable);
     VA_CHECK_LAUNCH(ctx);
@@ -383,31 +496,47 @@ va_status va_index_search_filtered(va_context* ctx, va_index* index, va_metric m
     if (out_examined) *out_examined = 0;
     const uint32_t live = index->slots - index->deleted;
     if (live == 0) return VA_OK;
+    const bool ivf = va::ivf_route(index);
+    VA_REQUIRE(ctx, !ivf || metric == VA_METRIC_L2SQ, "an IVF index searches by L2^2 only (metric %d)", int(metric));
     // seen = deleted rows, then also every row a round has examined
     VA_CHECK_HIP(ctx, hipMemcpyAsync(index->seen, index->skip, index->slots, hipMemcpyDeviceToDevice, ctx->stream));
     // one round's results (device, then host)
-    struct RoundBuffers {
-        void* idx = nullptr;
-        void* dist = nullptr;
-        ~RoundBuffers() {
-            (void)hipFree(idx);
-            (void)hipFree(dist);
+    struct DevTmp {
+        void* p[3] = {};
+        ~DevTmp() {
+            for (void* q : p)
+                if (q) (void)hipFree(q);
         }
     } rb;
-    VA_CHECK_HIP(ctx, hipMalloc(&rb.idx, uint64_t(VA_MAX_K) * 4));
-    VA_CHECK_HIP(ctx, hipMalloc(&rb.dist, uint64_t(VA_MAX_K) * 4));
-    uint32_t* d_idx = static_cast<uint32_t*>(rb.idx);
-    float* d_dist = static_cast<float*>(rb.dist);
+    VA_CHECK_HIP(ctx, hipMalloc(&rb.p[0], uint64_t(VA_MAX_K) * 4));
+    VA_CHECK_HIP(ctx, hipMalloc(&rb.p[1], uint64_t(VA_MAX_K) * 4));
+    uint32_t* d_idx = static_cast<uint32_t*>(rb.p[0]);
+    float* d_dist = static_cast<float*>(rb.p[1]);
     std::vector<uint32_t> h_idx(VA_MAX_K), slots;
     std::vector<float> h_dist(VA_MAX_K);
+    uint32_t examined = 0, accepted = 0;
+    auto take = [&](uint32_t sl, float dist) {
+        ++examined;
+        const uint32_t h = index->slot_to_stable[sl];
+        if (accepted < k && (!filter || filter(h, user))) {
+            out_handles[accepted] = h;
+            if (out_dist) out_dist[accepted] = dist;
+            ++accepted;
+        }
+    };
     // round sizes: twice k (the reference's first over-fetch), doubling, at most VA_MAX_K
     uint32_t fetch = std::min<uint32_t>(std::max<uint32_t>(2 * k, 16), VA_MAX_K);
-    uint32_t examined = 0, accepted = 0;
+    bool sorted_pass = false;
     while (accepted < k && examined < live) {
+        if (sorted_pass) break;
         const uint32_t f = std::min(fetch, live - examined);
-        VA_CHECK_STATUS(va::flat_topk(ctx, va::metric_op(metric), query, index->rows, 1, index->slots, index->dim, f,
-                                      d_idx, d_dist, index->pitch ? index->shadow : nullptr,
-                                      index->pitch ? index->norms : nullptr, index->seen));
+        if (ivf)
+            VA_CHECK_STATUS(va::ivf_search_masked(ctx, index->ivf, query, 1, index->nprobe, f, d_idx, d_dist,
+                                                  index->seen));
+        else
+            VA_CHECK_STATUS(va::flat_topk(ctx, va::metric_op(metric), query, index->rows, 1, index->slots, index->dim,
+                                          f, d_idx, d_dist, index->pitch ? index->shadow : nullptr,
+                                          index->pitch ? index->norms : nullptr, index->seen));
         VA_CHECK_HIP(ctx, hipMemcpyAsync(h_idx.data(), d_idx, uint64_t(f) * 4, hipMemcpyDeviceToHost, ctx->stream));
         VA_CHECK_HIP(ctx, hipMemcpyAsync(h_dist.data(), d_dist, uint64_t(f) * 4, hipMemcpyDeviceToHost, ctx->stream));
         VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -416,17 +545,65 @@ va_status va_index_search_filtered(va_context* ctx, va_index* index, va_metric m
             const uint32_t sl = h_idx[i];
             if (sl == va::kSentinel) break;
             slots.push_back(sl);
-            ++examined;
-            const uint32_t h = index->slot_to_stable[sl];
-            if (accepted < k && (!filter || filter(h, user))) {
-                out_handles[accepted] = h;
-                if (out_dist) out_dist[accepted] = h_dist[i];
-                ++accepted;
-            }
+            take(sl, h_dist[i]);
         }
         if (slots.empty()) break;
+        if (ivf && slots.size() < f) break;  // the probed lists hold no more live rows
         VA_CHECK_STATUS(va::set_bytes(ctx, index->seen, slots, 1));
+        // a round of VA_MAX_K rows did not find k: the rest in one sorted pass (below)
+        sorted_pass = !ivf && fetch == VA_MAX_K;
         fetch = std::min<uint32_t>(fetch * 2, VA_MAX_K);
+    }
+    if (sorted_pass && accepted < k && examined < live) {
+        // Every row's key (the fp32 scan's arithmetic, so the same keys the rounds saw), the rows
+        // already examined or deleted made absent, a stable device sort by key (ties stay in slot
+        // order), then the sorted rows filtered on the host in batches until k pass.
+        const uint32_t N = index->slots;
+        const uint64_t n4 = (uint64_t(N) + 63) & ~uint64_t(63);  // 256-byte aligned sub-buffers
+        size_t tmp_bytes = 0;
+        uint32_t* null_u32 = nullptr;
+        VA_CHECK_HIP(ctx, rocprim::radix_sort_pairs(nullptr, tmp_bytes, null_u32, null_u32, null_u32, null_u32, N, 0, 32,
+                                                    ctx->stream));
+        VA_CHECK_HIP(ctx, hipMalloc(&rb.p[2], n4 * 4 * 4 + tmp_bytes));
+        uint32_t* keys = static_cast<uint32_t*>(rb.p[2]);
+        uint32_t* keys2 = keys + n4;
+        uint32_t* ids = keys2 + n4;
+        uint32_t* ids2 = ids + n4;
+        void* tmp = ids2 + n4;
+        va::DistArgs a;
+        a.q = query;
+        a.ldq = index->dim;
+        a.x = index->rows;
+        a.ldx = index->dim;
+        a.Q = 1;
+        a.N = N;
+        a.D = index->dim;
+        a.op = va::metric_op(metric);
+        a.out = va::OUT_KEYS;
+        a.out_k = keys;
+        a.ldo = N;
+        VA_CHECK_STATUS(va::launch_dist(ctx, a));
+        VA_CHECK_STATUS(va::mask_dense_keys(ctx, keys, 1, N, N, 0, 1, index->seen));
+        va::iota_kernel<<<dim3(va::grid_for(N)), dim3(256), 0, ctx->stream>>>(ids, N, 0);
+        VA_CHECK_LAUNCH(ctx);
+        VA_CHECK_HIP(ctx, rocprim::radix_sort_pairs(tmp, tmp_bytes, keys, keys2, ids, ids2, N, 0, 32, ctx->stream));
+        constexpr uint32_t kBatch = 65536;
+        std::vector<uint32_t> hk(kBatch), hs(kBatch);
+        for (uint32_t off = 0; off < N && accepted < k; off += kBatch) {
+            const uint32_t n = std::min(kBatch, N - off);
+            VA_CHECK_HIP(ctx, hipMemcpyAsync(hk.data(), keys2 + off, uint64_t(n) * 4, hipMemcpyDeviceToHost, ctx->stream));
+            VA_CHECK_HIP(ctx, hipMemcpyAsync(hs.data(), ids2 + off, uint64_t(n) * 4, hipMemcpyDeviceToHost, ctx->stream));
+            VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));
+            bool rest_absent = false;
+            for (uint32_t i = 0; i < n && accepted < k; ++i) {
+                if (hk[i] == va::kAbsentKey) {
+                    rest_absent = true;  // examined or deleted: everything after it too
+                    break;
+                }
+                take(hs[i], va::float_of_key(hk[i]));
+            }
+            if (rest_absent) break;
+        }
     }
     *out_count = accepted;
     if (out_examined) *out_examined = examined;

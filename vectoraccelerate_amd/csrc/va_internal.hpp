@@ -455,12 +455,24 @@ struct ScanOutputs {
 va_status mask_dense_keys(va_context* ctx, uint32_t* keys, uint32_t rows, uint32_t cols, int64_t ld, uint32_t row0,
                           uint32_t stride, const uint8_t* skip);
 // keys[r * ld + i] (and keys2, when given) = kAbsentKey for the excluded ids[r * ld + i],
-// i < min(counts[r], cap)
+// i < min(counts[r], cap); with id_map the list holds positions p and the row id is id_map[p]
 va_status mask_list_keys(va_context* ctx, uint32_t* keys, uint32_t* keys2, const uint32_t* ids, const uint32_t* counts,
-                         uint32_t rows, uint32_t cap, int64_t ld, const uint8_t* skip);
+                         uint32_t rows, uint32_t cap, int64_t ld, const uint8_t* skip,
+                         const uint32_t* id_map = nullptr);
 
 va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t N, uint32_t k,
                           const ScanOutputs& out);
+
+// IVF scan / search (probe + scan) whose results exclude the rows whose skip byte, indexed by row
+// id, is set (an index's deletions): excluded rows become absent keys before every selection of
+// the scan, its threshold samples and its device fallback included.  skip = nullptr: va_ivf_scan /
+// va_ivf_search.
+va_status ivf_scan_masked(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
+                          const uint32_t* probes, uint32_t nprobe, uint32_t k, uint32_t* out_idx, float* out_dist,
+                          const uint8_t* skip);
+va_status ivf_search_masked(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
+                            uint32_t nprobe, uint32_t k, uint32_t* out_idx, float* out_dist, const uint8_t* skip);
+uint32_t ivf_num_lists(const va_ivf* ivf);
 
 // Plan of the sampled scan: S sample rows (every stride-th row), candidate capacity per query,
 // queries per sample launch; direct = the database is small enough for dense keys.

@@ -974,7 +974,10 @@ __global__ __launch_bounds__(256) void fb_ivf_pass_kernel(FbIvf v, FbArgs a, int
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     const uint32_t m = uint32_t(16 * (i >> 2) + 4 * g + (i & 3));
-                    if (m < rc) fb_consume(a, pass, sl, keys[i], v.ids[base + m]);
+                    if (m < rc) {
+                        const uint32_t id = v.ids[base + m];
+                        fb_consume(a, pass, sl, (a.skip && a.skip[id]) ? kAbsentKey : keys[i], id);
+                    }
                 }
             }
         } else {
@@ -987,7 +990,10 @@ __global__ __launch_bounds__(256) void fb_ivf_pass_kernel(FbIvf v, FbArgs a, int
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const uint32_t m = uint32_t(8 * (i >> 2) + 4 * hh + (i & 3));
-                    if (m < rc) fb_consume(a, pass, sl, keys[i], v.ids[base + m]);
+                    if (m < rc) {
+                        const uint32_t id = v.ids[base + m];
+                        fb_consume(a, pass, sl, (a.skip && a.skip[id]) ? kAbsentKey : keys[i], id);
+                    }
                 }
             }
         }
@@ -1113,7 +1119,8 @@ bool ivf_screen_applies(const va_context* ctx, const va_ivf* ivf, const float* q
 //   rerank  : their exact fp32 keys, with each list's fp32 arithmetic, and their ids;
 //   select  : exact (key, id) top-k.  Overflowed queries take the device fallback.
 va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t Q,
-                            const uint32_t* probes, uint32_t np, uint32_t k, uint32_t* out_idx, float* out_dist) {
+                            const uint32_t* probes, uint32_t np, uint32_t k, uint32_t* out_idx, float* out_dist,
+                            const uint8_t* skip) {
     const uint32_t C = ivf->C, D = ivf->D, Dp = shadow_pitch(D);
     const uint32_t npc = std::min(np, C);
     const uint64_t cap_s = std::max<uint64_t>(1, ivf->top_sample[npc]);
@@ -1174,13 +1181,15 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
     FbArgs fb = fb_carve(s, Q, id_span, k, ivf->N);
     fb.n_rows = ovf_cnt;
     fb.rows = ovf_rows;
+    fb.skip = skip;
     uint32_t* chi = reinterpret_cast<uint32_t*>(cdot);
     auto bounds = [&](uint64_t cp) -> va_status {
         const uint32_t bx = uint32_t(std::min<uint64_t>(4, (cp + 255) / 256));
         ivf_bound_kernel<<<dim3(bx, Q), dim3(256), 0, ctx->stream>>>(make_bound_v(D), qinfo, qerr, ivf->norms, cdot,
                                                                      cpos, clo, cnt, uint32_t(cp));
         VA_CHECK_LAUNCH(ctx);
-        return VA_OK;
+        // excluded rows (an index's deletions) become absent keys before every selection
+        return mask_list_keys(ctx, chi, clo, cpos, cnt, Q, uint32_t(cp), int64_t(cp), skip, ivf->ids);
     };
 
     ScanPhaseMarks pm(ctx);
@@ -1251,6 +1260,7 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
                                                                        ivf->offsets, C, dp.qcnt, D, rr, rcount,
                                                                        uint32_t(rcap), Q, rkey, rid);
         VA_CHECK_LAUNCH(ctx);
+        VA_CHECK_STATUS(mask_list_keys(ctx, rkey, nullptr, rid, rcount, Q, uint32_t(rcap), int64_t(rcap), skip));
     }
     // ---- 6. exact (key, id) top-k, 7. overflowed queries -----------------------------------------
     SelectArgs base;
@@ -1461,8 +1471,15 @@ va_status va_ivf_probe(va_context* ctx, const va_ivf* ivf, const float* queries,
     return va::exact_topk_scan(ctx, kp, num_queries, ivf->C, nprobe, o);
 }
 
-va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
-                      const uint32_t* probes, uint32_t nprobe, uint32_t k, uint32_t* out_idx, float* out_dist) {
+}  // extern "C"
+
+namespace va {
+
+// va_ivf_scan with an exclusion mask: rows whose skip byte (indexed by row id) is set never take
+// a place in a result or hold a threshold down (nullptr: none excluded).
+va_status ivf_scan_masked(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
+                          const uint32_t* probes, uint32_t nprobe, uint32_t k, uint32_t* out_idx, float* out_dist,
+                          const uint8_t* skip) {
     using va::Scratch;
     if (!ctx) return VA_ERR_INVALID_ARG;
     VA_REQUIRE(ctx, ivf && queries && probes && out_idx, "va_ivf_scan: NULL pointer");
@@ -1471,7 +1488,7 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
     VA_REQUIRE(ctx, nprobe >= 1, "nprobe must be at least 1, got %u", nprobe);
     va::DeviceGuard g(ctx->device);
     if (va::ivf_screen_applies(ctx, ivf, queries))
-        return va::ivf_scan_screened(ctx, ivf, queries, num_queries, probes, nprobe, k, out_idx, out_dist);
+        return va::ivf_scan_screened(ctx, ivf, queries, num_queries, probes, nprobe, k, out_idx, out_dist, skip);
     const uint32_t Q = num_queries, C = ivf->C, np = nprobe;
 
     // ---- sizes from the list lengths alone (nothing is read back) --------------------------------
@@ -1518,6 +1535,7 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
     va::FbArgs fb = va::fb_carve(s, Q, id_span, k, ivf->N);
     fb.n_rows = ovf_cnt;
     fb.rows = ovf_rows;
+    fb.skip = skip;
 
     va::ScanPhaseMarks pm(ctx);
     ctx->last_scan = va_scan_timings{};
@@ -1528,6 +1546,7 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
     VA_CHECK_STATUS(va::fill_u32(ctx, thr, Q, 0xFFFFFFFFu));
     VA_CHECK_STATUS(va::fill_u32(ctx, cnt, Q, 0));
     VA_CHECK_STATUS(va::run_planned_pass(ctx, dp, 0, queries, ivf, thr, cnt, ckey, cid, uint32_t(cap_s)));
+    VA_CHECK_STATUS(va::mask_list_keys(ctx, ckey, nullptr, cid, cnt, Q, uint32_t(cap_s), int64_t(cap_s), skip));
     {
         va::SelectArgs a;
         a.keys = ckey;
@@ -1546,6 +1565,7 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
     VA_CHECK_STATUS(pm.mark(1));
     VA_CHECK_STATUS(va::run_planned_pass(ctx, dp, 1, queries, ivf, thr, cnt, ckey, cid, uint32_t(cap)));
     VA_CHECK_STATUS(pm.mark(2));
+    VA_CHECK_STATUS(va::mask_list_keys(ctx, ckey, nullptr, cid, cnt, Q, uint32_t(cap), int64_t(cap), skip));
     va::SelectArgs base;
     base.k = k;
     base.out_idx = out_idx;
@@ -1571,8 +1591,9 @@ va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, 
     return pm.finish(true, true);
 }
 
-va_status va_ivf_search(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
-                        uint32_t nprobe, uint32_t k, uint32_t* out_idx, float* out_dist) {
+// va_ivf_search with an exclusion mask (see ivf_scan_masked)
+va_status ivf_search_masked(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
+                            uint32_t nprobe, uint32_t k, uint32_t* out_idx, float* out_dist, const uint8_t* skip) {
     if (!ctx) return VA_ERR_INVALID_ARG;
     VA_REQUIRE(ctx, ivf && queries && out_idx, "va_ivf_search: NULL pointer");
     VA_REQUIRE(ctx, num_queries > 0, "Queries cannot be empty");
@@ -1592,7 +1613,23 @@ va_status va_ivf_search(va_context* ctx, const va_ivf* ivf, const float* queries
         m->probe_cap = need;
     }
     VA_CHECK_STATUS(va_ivf_probe(ctx, ivf, queries, num_queries, nprobe, m->probe_buf));
-    return va_ivf_scan(ctx, ivf, queries, num_queries, m->probe_buf, nprobe, k, out_idx, out_dist);
+    return ivf_scan_masked(ctx, ivf, queries, num_queries, m->probe_buf, nprobe, k, out_idx, out_dist, skip);
+}
+
+uint32_t ivf_num_lists(const va_ivf* ivf) { return ivf->C; }
+
+}  // namespace va
+
+extern "C" {
+
+va_status va_ivf_scan(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
+                      const uint32_t* probes, uint32_t nprobe, uint32_t k, uint32_t* out_idx, float* out_dist) {
+    return va::ivf_scan_masked(ctx, ivf, queries, num_queries, probes, nprobe, k, out_idx, out_dist, nullptr);
+}
+
+va_status va_ivf_search(va_context* ctx, const va_ivf* ivf, const float* queries, uint32_t num_queries,
+                        uint32_t nprobe, uint32_t k, uint32_t* out_idx, float* out_dist) {
+    return va::ivf_search_masked(ctx, ivf, queries, num_queries, nprobe, k, out_idx, out_dist, nullptr);
 }
 
 }  // extern "C"

@@ -36,12 +36,13 @@ __global__ void mask_dense_kernel(uint32_t* keys, uint32_t cols, int64_t ld, uin
 
 __global__ void mask_list_kernel(uint32_t* keys, uint32_t* keys2, const uint32_t* __restrict__ ids,
                                  const uint32_t* __restrict__ counts, uint32_t cap, int64_t ld,
-                                 const uint8_t* __restrict__ skip) {
+                                 const uint8_t* __restrict__ skip, const uint32_t* __restrict__ id_map) {
     const uint32_t r = blockIdx.y;
     const uint32_t n = min(counts[r], cap);
     for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
         const int64_t o = int64_t(r) * ld + i;
-        const uint32_t id = ids[o];
+        uint32_t id = ids[o];
+        if (id != kSentinel && id_map) id = id_map[id];
         if (id != kSentinel && skip[id]) {
             keys[o] = kAbsentKey;
             if (keys2) keys2[o] = kAbsentKey;
@@ -63,14 +64,15 @@ va_status mask_dense_keys(va_context* ctx, uint32_t* keys, uint32_t rows, uint32
 }
 
 va_status mask_list_keys(va_context* ctx, uint32_t* keys, uint32_t* keys2, const uint32_t* ids, const uint32_t* counts,
-                         uint32_t rows, uint32_t cap, int64_t ld, const uint8_t* skip) {
+                         uint32_t rows, uint32_t cap, int64_t ld, const uint8_t* skip, const uint32_t* id_map) {
     if (!skip || rows == 0 || cap == 0) return VA_OK;
     const uint32_t bx = std::min<uint32_t>(16, (cap + 255) / 256);
     for (uint32_t r0 = 0; r0 < rows; r0 += 65535) {
         const uint32_t nr = std::min<uint32_t>(65535, rows - r0);
         mask_list_kernel<<<dim3(bx, nr), dim3(256), 0, ctx->stream>>>(keys + int64_t(r0) * ld,
                                                                      keys2 ? keys2 + int64_t(r0) * ld : nullptr,
-                                                                     ids + int64_t(r0) * ld, counts + r0, cap, ld, skip);
+                                                                     ids + int64_t(r0) * ld, counts + r0, cap, ld, skip,
+                                                                     id_map);
         VA_CHECK_LAUNCH(ctx);
     }
     return VA_OK;

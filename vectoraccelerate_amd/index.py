@@ -5,12 +5,12 @@ Reference: Index/AcceleratedVectorIndex.swift (init :166-237, insert :481-700, r
 :1188-1265, searchBatchGPU :1278-1374, searchIVF :1378-1431); handles
 (Index/Types/VectorHandle.swift:33-70, Index/Internal/HandleAllocator.swift:39-242).
 
-Storage, stable handles, deletions, compaction and the flat searches (plain and filtered) are the
-native index (``va_index_*``): its rows live on the device with an fp16 shadow for the screening
-scan, deleted rows are excluded inside the scan, and a filter is applied to round after round of
-not-yet-examined nearest rows, so no result is short however many rows are deleted or rejected.
-This module keeps what the reference keeps in Swift: metadata, the IVF configuration, routing
-and the IVF lists (built over the index's slots with va_ivf_*).
+Storage, stable handles, deletions, compaction, IVF training and lists, routing and every search
+(flat or IVF, plain or filtered) are the native index (``va_index_*``): its rows live on the device
+with an fp16 shadow for the screening scan, deleted rows are excluded inside every scan (the IVF
+list scan included), and a filter is applied to round after round of not-yet-examined nearest
+rows, so no result is short however many rows are deleted or rejected.  This module keeps what
+the reference keeps in Swift beside the index: metadata and the Python-facing result types.
 """
 from __future__ import annotations
 
@@ -23,7 +23,6 @@ import numpy as np
 
 from . import _lib
 from .context import DeviceRows, GPUContext, VectorError, dptr
-from .ivf import IVFGPUIndexStructure, IVFSearchConfiguration, IVFSearchPipeline
 
 _METRICS = {"euclidean": _lib.VA_METRIC_L2SQ, "cosine": _lib.VA_METRIC_COSINE, "dotProduct": _lib.VA_METRIC_DOT}
 
@@ -113,27 +112,19 @@ class AcceleratedVectorIndex:
         self.context = context or GPUContext(0)
         c = self.context
         h = C.c_void_p()
-        c.check(c.lib.va_index_create(c.handle, configuration.dimension, configuration.capacity, C.byref(h)),
-                "va_index_create")
+        if configuration.indexType[0] == "ivf":
+            _, nlist, nprobe = configuration.indexType
+            c.check(c.lib.va_index_create_ivf(c.handle, configuration.dimension, configuration.capacity, nlist, nprobe,
+                                              configuration.routingThreshold, C.byref(h)), "va_index_create_ivf")
+        else:
+            c.check(c.lib.va_index_create(c.handle, configuration.dimension, configuration.capacity, C.byref(h)),
+                    "va_index_create")
         self._h = h
         self._metric = _METRICS[configuration.metric]
         self._metadata: dict[int, object] = {}
-        # slot -> stable id and the deletion flags, mirrored for the IVF path (whose lists hold slots)
-        self._slot_handle: list[int] = []
-        self._deleted_slots: set[int] = set()
-        self._ivf: IVFGPUIndexStructure | None = None
-        self._ivf_dirty = True
-        self._centroids = None
-        if configuration.indexType[0] == "ivf":
-            _, nlist, nprobe = configuration.indexType
-            self._ivf_pipe = IVFSearchPipeline(self.context, IVFSearchConfiguration(nlist, nprobe,
-                                                                                    configuration.dimension))
 
     def close(self):
         if getattr(self, "_h", None) is not None and self._h.value:
-            if self._ivf is not None:
-                self._ivf.close()
-                self._ivf = None
             self.context.lib.va_index_destroy(self._h)
             self._h = C.c_void_p()
 
@@ -175,11 +166,13 @@ class AcceleratedVectorIndex:
 
     @property
     def isTrained(self) -> bool:
-        return self._centroids is not None
+        return bool(self._info().trained)
 
     # -- mutation ----------------------------------------------------------------------------
     def insert(self, vector=None, metadata=None, vectors=None):
-        """insert(vector) -> VectorHandle, or insert(vectors=[...]) -> [VectorHandle]."""
+        """insert(vector) -> VectorHandle, or insert(vectors=[...]) -> [VectorHandle].
+
+        A trained IVF index appends the new vectors to their nearest lists."""
         batch = vectors is not None
         c = self.context
         if batch and getattr(vectors, "is_cuda", False):
@@ -198,49 +191,36 @@ class AcceleratedVectorIndex:
             dev = c.buffer(np.ascontiguousarray(arr)) if n else None
         if n == 0:
             return []
-        first = self._info().slots
         out = np.zeros(n, np.uint32)
         c.order_after_torch()
         c.check(c.lib.va_index_insert(c.handle, self._h, dptr(dev), n, out.ctypes.data), "va_index_insert")
         handles = [VectorHandle(int(h)) for h in out]
-        self._slot_handle.extend(int(h) for h in out)
         if metadata is not None and not batch:
             self._metadata[handles[0].stableID] = metadata
-        if self._ivf is not None and not self._ivf_dirty:
-            # built lists: append the new slots to their nearest lists (va_ivf_add) instead of a rebuild
-            self._ivf.add(self._rows().rows(first, first + n), first)
-        else:
-            self._ivf_dirty = True
         c.synchronize()  # the staged input buffer is released on return
         return handles if batch else handles[0]
 
     def remove(self, handle):
         """remove(handle) or remove([handles]) -> number removed (AcceleratedVectorIndex.swift:771-833).
 
-        The IVF lists are left as they are: removed slots are skipped when results are collected."""
+        The slot stays in place (and in its IVF list) and is excluded from every search until
+        compact()."""
         hs = handle if isinstance(handle, (list, tuple)) else [handle]
         if not isinstance(handle, (list, tuple)) and not self.contains(handle):
             raise VectorError.invalidInput(f"invalid handle {handle.stableID}")
         ids = np.asarray([h.stableID for h in hs], np.uint32)
-        live = [h.stableID for h in hs if self.contains(h)]
-        slot_of = {hid: s for s, hid in enumerate(self._slot_handle)} if live else {}
         removed = C.c_uint32(0)
         c = self.context
         c.check(c.lib.va_index_remove(c.handle, self._h, ids.ctypes.data, len(ids), C.byref(removed)), "va_index_remove")
-        for hid in live:
-            self._deleted_slots.add(slot_of[hid])
-            self._metadata.pop(hid, None)
+        for h in hs:
+            self._metadata.pop(h.stableID, None)
         return int(removed.value)
 
     def compact(self):
-        """Drop deleted slots; handles keep their stable ids (AcceleratedVectorIndex.swift:834-893)."""
-        if not self._deleted_slots:
-            return
+        """Drop deleted slots; handles keep their stable ids (AcceleratedVectorIndex.swift:834-893).
+        A trained IVF index rebuilds its lists from the trained centroids."""
         c = self.context
         c.check(c.lib.va_index_compact(c.handle, self._h), "va_index_compact")
-        self._slot_handle = [h for s, h in enumerate(self._slot_handle) if s not in self._deleted_slots]
-        self._deleted_slots.clear()
-        self._ivf_dirty = True
 
     def vector(self, handle: VectorHandle):
         if not self.contains(handle):
@@ -258,74 +238,69 @@ class AcceleratedVectorIndex:
 
     # -- IVF ---------------------------------------------------------------------------------
     def train(self, centroids=None, seed: int = 0x5EED):
-        """Train the IVF centroids; the lists are then built from the stored vectors.
+        """Train the IVF centroids; the lists are then built from the stored vectors (va_index_train).
 
         Without ``centroids``: k-means on the device over the live vectors (compacted first) with
         k-means++ seeding, 25 iterations at most, threshold 0.001, as IVFStructure.train
         (Index/Internal/IVFStructure.swift:202-259) called by AcceleratedVectorIndex.train
         (AcceleratedVectorIndex.swift:406-446).  With ``centroids`` ([nlist x D]): installs them.
-        """
-        if not self.isIVF:
-            raise VectorError.invalidInput("train() needs an IVF index")
-        nlist = self.configuration.indexType[1]
-        if centroids is None:
-            from .clustering import KMeansConfiguration, KMeansPipeline
-
-            live = self.count
-            if live == 0:
-                raise VectorError.invalidInput("Cannot train IVF index with no vectors")
-            if live < nlist:
-                raise VectorError.invalidInput(f"Need at least {nlist} vectors for {nlist} clusters, got {live}")
-            self.compact()  # the live rows are then slots [0, count)
-            cfg = KMeansConfiguration(nlist, self.dimension, maxIterations=25, convergenceThreshold=0.001, seed=seed)
-            self._centroids = KMeansPipeline(self.context, cfg).fit(self._rows()).centroids
-        else:
-            cen = np.asarray(centroids, np.float32)
-            if cen.shape != (nlist, self.dimension):
+        A flat index has nothing to train (the reference returns at once, :405-407)."""
+        c = self.context
+        cen = None
+        if centroids is not None and self.isIVF:
+            nlist = self.configuration.indexType[1]
+            if getattr(centroids, "is_cuda", False):
+                cen = centroids.to(_torch().float32).contiguous()
+            else:
+                cen = c.buffer(np.ascontiguousarray(np.asarray(centroids, np.float32)))
+            if tuple(cen.shape) != (nlist, self.dimension):
                 raise VectorError.invalidInput(f"centroids must be {nlist} x {self.dimension}")
-            self._centroids = self.context.buffer(cen)
-        self._ivf_dirty = True
+            c.order_after_torch()
+        c.check(c.lib.va_index_train(c.handle, self._h, dptr(cen) if cen is not None else None, int(seed)),
+                "va_index_train")
 
-    def _ivf_structure(self) -> IVFGPUIndexStructure:
-        if self._ivf is None or self._ivf_dirty:
-            if self._ivf is not None:
-                self._ivf.close()
-            self._ivf = self._ivf_pipe.prepareIndexStructure(self._centroids, self._rows())
-            self._ivf_dirty = False
-        return self._ivf
-
-    def _use_ivf(self) -> bool:
-        if not (self.isIVF and self.isTrained):
-            return False
-        t = self.configuration.routingThreshold
-        return not (t > 0 and self.count < t)
-
-    def _ivf_topk(self, q_dev, k: int):
-        """IVF: the k nearest live slots per query row, as (handle lists, distance lists)."""
-        if len(self._deleted_slots) and k + len(self._deleted_slots) > _lib.VA_MAX_K:
-            # over-fetching past the removed slots would exceed VA_MAX_K: drop them first
-            self.compact()
-        fetch = min(k + len(self._deleted_slots), _lib.VA_MAX_K)
-        res = self._ivf_pipe.search(q_dev, self._ivf_structure(), fetch)
-        ids = res.indices.cpu().numpy().view(np.uint32)
-        d = res.distances.cpu().numpy()
-        out = []
-        for row, drow in zip(ids, d):
-            hs, ds = [], []
-            for s, dist in zip(row, drow):
-                s = int(s)
-                if s == _lib.VA_SENTINEL_INDEX or s in self._deleted_slots:
-                    continue
-                hs.append(self._slot_handle[s])
-                ds.append(float(dist))
-                if len(hs) == k:
-                    break
-            out.append((hs, ds))
+    def centroids(self) -> np.ndarray | None:
+        """The trained centroids [nlist x D] (host copy), or None."""
+        info = self._info()
+        if not info.trained:
+            return None
+        out = np.empty((info.nlist, info.dimension), np.float32)
+        c = self.context
+        c.check(c.lib.va_buffer_download(c.handle, out.ctypes.data, info.centroids, out.nbytes), "va_buffer_download")
+        c.synchronize()
         return out
 
+    def lists(self) -> tuple[np.ndarray, np.ndarray] | None:
+        """(offsets[nlist + 1], slots[slots]) of the inverted lists (CSR order), or None."""
+        info = self._info()
+        if not info.lists:
+            return None
+        off = np.empty(info.nlist + 1, np.uint32)
+        ids = np.empty(info.slots, np.uint32)
+        c = self.context
+        c.check(c.lib.va_ivf_get_lists(c.handle, info.lists, off.ctypes.data, ids.ctypes.data), "va_ivf_get_lists")
+        return off, ids
+
+    def probes(self, queries) -> np.ndarray:
+        """The nprobe lists each query probes [Q x nprobe] (va_ivf_probe over the index's lists)."""
+        torch = _torch()
+        info = self._info()
+        if not info.lists:
+            raise VectorError.invalidInput("the index has no inverted lists (untrained or empty)")
+        c = self.context
+        q = c.buffer(np.asarray(queries, np.float32).reshape(-1, self.dimension))
+        out = c.empty((q.shape[0], info.nprobe), torch.int32)
+        c.order_after_torch()
+        c.check(c.lib.va_ivf_probe(c.handle, info.lists, dptr(q), q.shape[0], info.nprobe, dptr(out)), "va_ivf_probe")
+        c.synchronize()
+        return out.cpu().numpy().view(np.uint32)
+
+    def _use_ivf(self) -> bool:
+        return bool(self._info().ivf_routed)
+
     # -- search --------------------------------------------------------------------------------
-    def _flat_topk(self, q_dev, k: int):
-        """Flat: the k nearest live vectors per query row (va_index_search)."""
+    def _topk(self, q_dev, k: int):
+        """The k nearest live vectors per query row (va_index_search: flat or IVF)."""
         torch = _torch()
         c = self.context
         Q = q_dev.shape[0]
@@ -367,6 +342,15 @@ class AcceleratedVectorIndex:
                 "va_index_search_filtered")
         return self._results([int(h) for h in hs[:n.value]], [float(x) for x in ds[:n.value]]), int(examined.value)
 
+    def _effective_k(self, k: int, live: int) -> int:
+        if k <= 0:
+            raise VectorError.invalidInput(f"k must be positive, got {k}")
+        eff = min(k, live)
+        if eff > _lib.VA_MAX_K:
+            # FusedL2TopKParameters rejects k > maxK (Kernels/Metal4/FusedL2TopKKernel.swift:57-79)
+            raise VectorError.invalidInput(f"k {eff} exceeds maximum supported k {_lib.VA_MAX_K}")
+        return eff
+
     def search(self, query=None, k: int = 10, filter=None, queries=None):
         """search(query, k[, filter]) -> SearchResults; search(queries=[...], k) -> [SearchResults]."""
         if queries is not None:
@@ -374,31 +358,19 @@ class AcceleratedVectorIndex:
         q = np.asarray(query, np.float32).reshape(-1)
         if q.shape[0] != self.dimension:
             raise VectorError.dimensionMismatch(self.dimension, q.shape[0])
+        live = self.count
         if k <= 0:
             raise VectorError.invalidInput(f"k must be positive, got {k}")
-        live = self.count
         if live == 0:
             return SearchResults()
+        ivf = self._use_ivf()
         t0 = time.perf_counter_ns()
-        if filter is not None and not self._use_ivf():
-            res, examined = self._filtered(q, k, filter)
-            return SearchResults(res, examined, time.perf_counter_ns() - t0, True)
-        effective_k = min(k, live, _lib.VA_MAX_K)
-        q_dev = self.context.buffer(q.reshape(1, -1))
-        if self._use_ivf():
-            if filter is None:
-                hs, ds = self._ivf_topk(q_dev, effective_k)[0]
-                return SearchResults(self._results(hs, ds), live, time.perf_counter_ns() - t0, False)
-            # IVF with a filter: iterative over-fetch within VA_MAX_K (searchFiltered)
-            fetch = min(2 * k, live, _lib.VA_MAX_K)
-            while True:
-                hs, ds = self._ivf_topk(q_dev, fetch)[0]
-                res = [r for r in self._results(hs, ds) if filter(r.id, self._metadata.get(r.id.stableID))]
-                if len(res) >= k or fetch >= min(live, _lib.VA_MAX_K):
-                    return SearchResults(res[:k], len(hs), time.perf_counter_ns() - t0, False)
-                fetch = min(fetch * 2, live, _lib.VA_MAX_K)
-        hs, ds = self._flat_topk(q_dev, effective_k)[0]
-        return SearchResults(self._results(hs, ds), live, time.perf_counter_ns() - t0, True)
+        if filter is not None:
+            res, examined = self._filtered(q, min(k, live), filter)
+            return SearchResults(res, examined, time.perf_counter_ns() - t0, not ivf)
+        effective_k = self._effective_k(k, live)
+        hs, ds = self._topk(self.context.buffer(q.reshape(1, -1)), effective_k)[0]
+        return SearchResults(self._results(hs, ds), live, time.perf_counter_ns() - t0, not ivf)
 
     def _search_batch(self, queries, k, filter):
         qs = np.asarray(queries, np.float32)
@@ -413,16 +385,15 @@ class AcceleratedVectorIndex:
             return [SearchResults() for _ in range(qs.shape[0])]
         if filter is not None:
             return [self.search(q, k, filter) for q in qs]
-        t0 = time.perf_counter_ns()
-        effective_k = min(k, live, _lib.VA_MAX_K)
-        q_dev = self.context.buffer(qs)
+        effective_k = self._effective_k(k, live)
         ivf = self._use_ivf()
-        rows = self._ivf_topk(q_dev, effective_k) if ivf else self._flat_topk(q_dev, effective_k)
+        t0 = time.perf_counter_ns()
+        rows = self._topk(self.context.buffer(qs), effective_k)
         dt = time.perf_counter_ns() - t0
         return [SearchResults(self._results(hs, ds), live, dt, not ivf) for hs, ds in rows]
 
     def searchDevice(self, queries_dev, k: int, out_handles, out_dist):
-        """encode tier of the flat search: device queries [Q x D] -> device handles / distances
+        """encode tier of the search: device queries [Q x D] -> device handles / distances
         [Q x k] (uint32 / fp32 tensors), enqueued on the context's stream (va_index_search)."""
         c = self.context
         Q = queries_dev.shape[0]
