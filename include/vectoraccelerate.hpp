@@ -230,13 +230,43 @@ class MetalComputeProvider {
     const Context& ctx_;
 };
 
-// AcceleratedVectorIndex (flat) over va_index_* (Index/AcceleratedVectorIndex.swift:481-1265):
-// stable handles in insertion order, removal, compaction, plain and filtered search.
+// IndexConfiguration.ivf(dimension:nlist:nprobe:capacity:routingThreshold) (Index/Types/IndexConfiguration.swift)
+struct IVFConfiguration {
+    uint32_t nlist = 0, nprobe = 0, routingThreshold = 0;
+};
+
+// AcceleratedVectorIndex over va_index_* (Index/AcceleratedVectorIndex.swift:406-1481): stable
+// handles in insertion order, removal, compaction, plain and filtered search; with an
+// IVFConfiguration, train() and IVF routing (searchIVF / searchIVFBatch) once trained.
 class AcceleratedVectorIndex {
    public:
     AcceleratedVectorIndex(const Context& c, uint32_t dim, uint32_t capacity = 10000, va_metric metric = VA_METRIC_L2SQ)
         : ctx_(c), metric_(metric) {
         ctx_.check(va_index_create(ctx_.handle(), dim, capacity, &h_), "va_index_create");
+    }
+    // IVF index (L2^2): flat until trained
+    AcceleratedVectorIndex(const Context& c, uint32_t dim, const IVFConfiguration& ivf, uint32_t capacity = 100000)
+        : ctx_(c), metric_(VA_METRIC_L2SQ) {
+        ctx_.check(va_index_create_ivf(ctx_.handle(), dim, capacity, ivf.nlist, ivf.nprobe, ivf.routingThreshold, &h_),
+                   "va_index_create_ivf");
+    }
+    // train(): device k-means over the live vectors (seeded by `seed`), then the lists
+    void train(uint64_t seed = 0x5EED) { ctx_.check(va_index_train(ctx_.handle(), h_, nullptr, seed), "va_index_train"); }
+    // train with given centroids (host, [nlist x dim])
+    void train(const std::vector<float>& centroids) {
+        DeviceBuffer<float> c(ctx_, centroids);
+        ctx_.check(va_index_train(ctx_.handle(), h_, c.data(), 0), "va_index_train");
+    }
+    bool isTrained() const { return info().trained != 0; }
+    // the inverted lists (offsets[nlist + 1], slots in list order); empty while untrained
+    std::pair<std::vector<uint32_t>, std::vector<uint32_t>> lists() const {
+        const va_index_info i = info();
+        std::pair<std::vector<uint32_t>, std::vector<uint32_t>> r;
+        if (!i.lists) return r;
+        r.first.resize(size_t(i.nlist) + 1);
+        r.second.resize(i.slots);
+        ctx_.check(va_ivf_get_lists(ctx_.handle(), i.lists, r.first.data(), r.second.data()), "va_ivf_get_lists");
+        return r;
     }
     ~AcceleratedVectorIndex() {
         if (h_) va_index_destroy(h_);

@@ -106,6 +106,24 @@ int main(int argc, char** argv) {
         std::ofstream(dir + "/index_counts.txt") << removed << " " << index.count() << " " << index.contains(hs[0])
                                                  << " " << index.contains(hs[1]);
 
+        // AcceleratedVectorIndex (IVF): half the vectors, train with the given centroids, the other
+        // half joins the lists, every 5th vector removed, then batch search through the lists
+        va::AcceleratedVectorIndex ivx(ctx, D, va::IVFConfiguration{C, nprobe, 0}, 64);
+        va::Matrix xa{first, half, D}, xb{rest, N - half, D};
+        ivx.insert(xa);
+        ivx.train(cen);
+        ivx.insert(xb);
+        std::vector<uint32_t> gone5;
+        for (uint32_t i = 0; i < N; i += 5) gone5.push_back(i);
+        ivx.remove(gone5);
+        va::SearchResult vr = ivx.search(q, k);
+        save(dir + "/ivx_idx.bin", vr.indices);
+        save(dir + "/ivx_dist.bin", vr.distances);
+        auto lists = ivx.lists();
+        save(dir + "/ivx_off.bin", lists.first);
+        save(dir + "/ivx_ids.bin", lists.second);
+        std::ofstream(dir + "/ivx_state.txt") << ivx.isTrained() << " " << ivx.info().ivf_routed << " " << ivx.count();
+
         std::string kind = "none";
         try {
             topk.findNearestNeighbors(q, x, 0);

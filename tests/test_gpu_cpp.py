@@ -1,6 +1,6 @@
 """The C++ host mirror (include/vectoraccelerate.hpp) end to end: tests/cpp/va_example runs the
-flat top-k (L2^2, cosine), IVF build + add + search, k-means and PQ through the C++ classes;
-its outputs are compared with the CPU oracle."""
+flat top-k (L2^2, cosine), IVF build + add + search, k-means, PQ, the provider and the flat and IVF
+AcceleratedVectorIndex through the C++ classes; its outputs are compared with the CPU oracle."""
 from __future__ import annotations
 
 import subprocess
@@ -81,3 +81,14 @@ def test_cpp_mirror_matches_oracle(tmp_path, oracle):
     check_topk(L2SQ, q[:1], x[odd_live], k, np.searchsorted(odd_live, gf)[None].astype(np.uint32), None, oi, od)
     removed, count, c0, c1 = (tmp_path / "index_counts.txt").read_text().split()
     assert (int(removed), int(count), c0, c1) == (len(range(0, N, 7)), len(live), "0", "1")
+    # AcceleratedVectorIndex (IVF): lists = the oracle's assignment + CSR of every row; results =
+    # the oracle's scan of the oracle's probes over the live rows (every 5th removed)
+    assert (tmp_path / "ivx_state.txt").read_text().split() == ["1", "1", str(N - len(range(0, N, 5)))]
+    np.testing.assert_array_equal(rd("ivx_off", np.uint32), off)
+    np.testing.assert_array_equal(rd("ivx_ids", np.uint32), ids)
+    keep = ids % 5 != 0
+    lens = np.bincount(np.repeat(np.arange(C), np.diff(off.astype(np.int64)))[keep], minlength=C)
+    loff = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
+    vi, vd = oracle.ivf_scan(q, x, loff, ids[keep], probes, k)
+    check_topk(L2SQ, q, x, k, rd("ivx_idx", np.uint32).reshape(Q, k), rd("ivx_dist", np.float32).reshape(Q, k), vi,
+               vd)

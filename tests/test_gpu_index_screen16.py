@@ -1,8 +1,8 @@
 """The headline kernel, screen16_kernel, pinned to the oracle through va_index_search.
 
 va_index_search with Q >= 192 over an index whose dimension is a multiple of 4 screens the
-fp16 shadow written at insert (screen16_kernel), reranks a proven band exactly in fp32 and
-selects by (distance, slot).  Every family below runs through that route (asserted from the
+fp16 shadow written at insert (screen16_kernel; smaller batches screen16_small_kernel), reranks
+a proven band exactly in fp32 and selects by (distance, slot).  Every family below runs through that route (asserted from the
 profiling record: screened == 2) and is checked twice:
   * against the CPU oracle (vo_flat_topk, float64): distances within 1e-4 of the per-pair scale,
     ids equal rank by rank except for ties within that tolerance (tests/helpers.py);
@@ -88,6 +88,51 @@ def _pinned(ctx, oracle, metric, q, x, k, oracle_rows=None, accum_double=True):
 
 def _unit(a):
     return (a / np.linalg.norm(a, axis=1, keepdims=True)).astype(np.float32)
+
+
+# ---- small batches (Q < 192): screen16_small_kernel over the same shadow -----------------------
+@pytest.mark.parametrize("Q", [1, 7, 32, 33, 64, 65, 100, 128, 129, 191])
+@pytest.mark.parametrize("metric", [L2SQ, COSINE, DOT, L2])
+def test_small_batches(ctx, oracle, metric, Q):
+    """Every query-tile configuration of the small-batch screen and its partial last query block,
+    over 40,003 rows (a partial last row tile) of a dimension that is not a multiple of the chunk."""
+    g = np.random.default_rng(200 + Q + 7 * metric)
+    x = g.standard_normal((40003, 200), dtype=np.float32)
+    q = g.standard_normal((Q, 200), dtype=np.float32)
+    _pinned(ctx, oracle, metric, q, x, 17)
+
+
+@pytest.mark.parametrize("Q", [1, 50, 150])
+@pytest.mark.parametrize("metric", [L2SQ, COSINE, DOT, L2])
+def test_small_batches_unscreenable_rows(ctx, oracle, metric, Q):
+    """The adversarial rows of test_unscreenable_rows through the small-batch screen."""
+    g = np.random.default_rng(300 + Q + metric)
+    x = g.standard_normal((40000, 64), dtype=np.float32)
+    q = g.standard_normal((Q, 64), dtype=np.float32)
+    x[::997] *= 1e5
+    x[3::1999, 7] = np.nan
+    x[11::2999] = 0.0
+    x[17::3001] *= 1e-30
+    q[0] *= 1e5
+    if Q > 1:
+        q[1] = 0.0
+    _pinned(ctx, oracle, metric, q, x, 15, accum_double=metric != COSINE)
+
+
+@pytest.mark.parametrize("Q", [1, 20, 100])
+@pytest.mark.parametrize("metric", [L2SQ, COSINE])
+def test_small_batches_mixed_norms_and_ties(ctx, oracle, metric, Q):
+    """Norms over twelve decades with k = 1000, then dense near-ties, at small batch sizes."""
+    g = np.random.default_rng(400 + Q + metric)
+    x = g.standard_normal((40000, 96), dtype=np.float32)
+    x *= (10.0 ** g.uniform(-6, 6, size=(40000, 1))).astype(np.float32)
+    q = g.standard_normal((Q, 96), dtype=np.float32)
+    _pinned(ctx, oracle, metric, q, x, 1000, oracle_rows=np.arange(0, Q, max(1, Q // 10)))
+    base = g.standard_normal((1, 128), dtype=np.float32)
+    x = (np.repeat(base, 30000, axis=0) + 1e-4 * g.standard_normal((30000, 128), dtype=np.float32)).astype(np.float32)
+    x[::50] = base
+    q = (np.repeat(base, Q, axis=0) + 1e-3 * g.standard_normal((Q, 128), dtype=np.float32)).astype(np.float32)
+    _pinned(ctx, oracle, metric, q, x, 40)
 
 
 @pytest.mark.parametrize("metric", [L2SQ, COSINE, DOT, L2])

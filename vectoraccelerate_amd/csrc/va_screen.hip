@@ -64,6 +64,9 @@ constexpr int DP_ALIGN = KC;              // fp16 query rows are padded to a mul
 }  // namespace scr
 
 enum ScreenMode : int { SCREEN_KEYS = 0, SCREEN_FILTER = 1 };
+// below this many queries a search over the fp16 shadow takes screen16_small_kernel (a 256-query
+// tile of screen16_kernel would be mostly padding)
+constexpr uint32_t kSmallBatch = 192;
 
 struct ScreenArgs {
     const float* x = nullptr;     // database rows, row j at x + j * ldx
@@ -938,6 +941,148 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
     wait_vmcnt<0>();
 }
 
+// ---- the small-batch screen over the fp16 shadow ------------------------------------------------
+// Fewer than 192 queries: streaming the shadow from HBM is the cost, not the MFMA (Q = 1 reads
+// 2 bytes per value where the fp32 scan reads 4).  Every wave is an independent worker with no
+// LDS and no barrier: it takes tiles of 32 MB rows in turn and computes all 32 NQB (padded)
+// queries against them on v_mfma_f32_32x32x16_f16, both operands loaded straight into registers
+// by buffer loads (rows from HBM through a descriptor that ends at the tile's last row, so rows
+// past N read zeros; queries from L2, zeros past Q) in chunks of 2 KH halves, the next chunk in
+// flight while the current one computes.  In chunk c, lane (l, h) loads halves
+// c 2KH + KH h .. + KH - 1 of its row (l of each block) and of its query: k-step t of the chunk
+// takes the lane's 8 halves 8t .. 8t + 7 from both operands, so row and query pair the same d
+// (the dot is the same sum in any order; the screen's bound does not depend on the order).
+// Loads past the last chunk use an offset beyond the descriptors (zeros; branch-free, so the
+// compiler's wait counts stay exact).  Epilogue: the pre-test of screen16_kernel on each value
+// (flagged rows always pass), one atomic per lane pair and query block, appends from registers.
+template <int NQB, int MB, int KH>
+__global__ __launch_bounds__(256, 2) void screen16_small_kernel(ScreenArgs a) {
+    constexpr int TNW = 32 * MB;  // rows per wave tile
+    constexpr int L = KH / 8;     // 16-byte loads per lane, operand block and chunk
+    constexpr uint32_t CH = 2 * KH * 2;  // bytes per chunk of a row
+    const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+    const uint32_t nch = a.Dp / (2 * KH);
+    const uint32_t ntiles = (a.N + TNW - 1) / TNW;
+    const uint32_t pitch = a.Dp * 2u;  // bytes per shadow row
+    const __amdgpu_buffer_rsrc_t qres =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(a.qh), 0, int(a.Q * pitch), 0x00020000);
+    uint32_t qoff[NQB], roff[MB];
+#pragma unroll
+    for (int n = 0; n < NQB; ++n) qoff[n] = uint32_t(32 * n + l32) * pitch + uint32_t(KH * 2 * hh);
+#pragma unroll
+    for (int m = 0; m < MB; ++m) roff[m] = uint32_t(32 * m + l32) * pitch + uint32_t(KH * 2 * hh);
+    const float tiny = a.op == OP_COS_DIST ? 8.0f * a.c0x : 0.0f;
+    h8v ra[MB][L], rb[MB][L], qa[NQB][L], qb[NQB][L];
+    f32x16 acc[MB][NQB];
+    for (uint32_t tile = blockIdx.x * 4u + uint32_t(wave); tile < ntiles; tile += gridDim.x * 4u) {
+        const uint32_t rs = tile * TNW, rc = min(uint32_t(TNW), a.N - rs);
+        const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<_Float16*>(a.xh + int64_t(rs) * a.Dp), 0, int(rc * pitch), 0x00020000);
+        auto load = [&](uint32_t c, h8v(&r)[MB][L], h8v(&q)[NQB][L]) {
+            const bool ok = c < nch;
+            const uint32_t ko = c * CH;
+#pragma unroll
+            for (int i = 0; i < L; ++i) {
+#pragma unroll
+                for (int m = 0; m < MB; ++m)
+                    r[m][i] = __builtin_bit_cast(
+                        h8v, __builtin_amdgcn_raw_buffer_load_b128(xres, ok ? roff[m] + ko + 16u * i : kDmaSkip, 0, 0));
+#pragma unroll
+                for (int n = 0; n < NQB; ++n)
+                    q[n][i] = __builtin_bit_cast(
+                        h8v, __builtin_amdgcn_raw_buffer_load_b128(qres, ok ? qoff[n] + ko + 16u * i : kDmaSkip, 0, 0));
+            }
+        };
+        auto mma = [&](const h8v(&r)[MB][L], const h8v(&q)[NQB][L]) {
+#pragma unroll
+            for (int i = 0; i < L; ++i)
+#pragma unroll
+                for (int m = 0; m < MB; ++m)
+#pragma unroll
+                    for (int n = 0; n < NQB; ++n)
+                        acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(r[m][i], q[n][i], acc[m][n], 0, 0, 0);
+        };
+#pragma unroll
+        for (int m = 0; m < MB; ++m)
+#pragma unroll
+            for (int n = 0; n < NQB; ++n)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[m][n][v] = 0.0f;
+        load(0, ra, qa);
+        for (uint32_t c = 0; c < nch; c += 2) {
+            load(c + 1, rb, qb);
+            mma(ra, qa);
+            __builtin_amdgcn_sched_barrier(0);
+            load(c + 2, ra, qa);  // past the end: zeros, unused
+            mma(rb, qb);          // past the end: zeros, adds nothing
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // ---- filter epilogue: lane (l32, hh) holds query 32n + l32 against rows 32m + 8j + 4hh + e
+        // in acc[m][n][4j + e].  The pre-test one row block at a time (its 16 norms in registers),
+        // building a pass mask per query block; the appends re-read the norms of passing rows.
+        using Mask = std::conditional_t<(16 * MB > 32), uint64_t, uint32_t>;
+        Mask mk[NQB];
+        float4 pt[NQB];
+#pragma unroll
+        for (int n = 0; n < NQB; ++n) {
+            mk[n] = 0;
+            pt[n] = a.ptc[min(uint32_t(32 * n + l32), a.Q - 1)];
+        }
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+            float xxp[16], nxp[16];
+            uint32_t valid = 0;
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const uint32_t r = uint32_t(32 * m + 8 * (t >> 2) + 4 * hh + (t & 3));
+                const bool in = r < rc;
+                const float v = in ? a.xn[rs + r] : 0.0f;
+                const float nx = __builtin_amdgcn_sqrtf(v);
+                const bool flag = !(v < 4.29e9f) || nx < tiny;
+                xxp[t] = flag ? __builtin_nanf("") : v;
+                nxp[t] = flag ? __builtin_nanf("") : nx;
+                valid |= uint32_t(in) << t;
+            }
+#pragma unroll
+            for (int n = 0; n < NQB; ++n) {
+                uint32_t b = 0;
+#pragma unroll
+                for (int t = 0; t < 16; ++t)
+                    b |= uint32_t(!(acc[m][n][t] < fmaf(pt[n].x, xxp[t], fmaf(pt[n].y, nxp[t], pt[n].z)))) << t;
+                mk[n] |= Mask(b & valid) << (16 * m);
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < NQB; ++n) {
+            const uint32_t qt = uint32_t(32 * n + l32);
+            const Mask mq = qt < a.Q ? mk[n] : Mask(0);
+            if (!__ballot(mq != 0u)) continue;
+            const uint32_t qi = qt < a.Q ? qt : 0u;
+            const uint32_t cnt = uint32_t(__builtin_popcountll(uint64_t(mq)));
+            const uint32_t other = uint32_t(__shfl_xor(int(cnt), 32));
+            uint32_t base = 0;
+            if (hh == 0 && cnt + other) base = atomicAdd(a.cnt + qi, cnt + other);
+            uint32_t pos = uint32_t(__shfl(int(base), l32)) + (hh ? other : 0u);
+#pragma unroll
+            for (int m = 0; m < MB; ++m)
+#pragma unroll
+                for (int t = 0; t < 16; ++t) {
+                    if ((mq >> (16 * m + t)) & 1u) {
+                        if (pos < a.cap) {
+                            const uint32_t r = uint32_t(32 * m + 8 * (t >> 2) + 4 * hh + (t & 3));
+                            const int64_t o = int64_t(qi) * a.cap + pos;
+                            a.cand_dot[o] = acc[m][n][t] * pt[n].w;
+                            a.cand_xx[o] = a.xn[rs + r];
+                            a.cand_id[o] = a.id_base + rs + r;
+                        }
+                        ++pos;
+                    }
+                }
+        }
+    }
+}
+
 // ---- the fp16 shadow: rows rounded to fp16 (RNE, as the scans round), padded with zeros to Dp,
 // and their squared norms in fp32 (one wave per row) ----------------------------------------------
 __global__ __launch_bounds__(256) void shadow_kernel(const float* __restrict__ x, int64_t ldx, uint32_t N, uint32_t D,
@@ -1133,6 +1278,26 @@ va_status launch_screen16(va_context* ctx, const ScreenArgs& a) {
     return VA_OK;
 }
 
+// The small-batch screen: per query count the widest query tile whose registers keep two waves
+// per SIMD (NQB 32-query blocks x MB 32-row blocks, chunks of 2 KH halves).
+va_status launch_screen16_small(va_context* ctx, const ScreenArgs& a) {
+    if (a.Q == 0 || a.N == 0) return VA_OK;
+    const uint32_t waves_per_cu = 8;
+    auto go = [&](auto kern, uint32_t tnw) -> va_status {
+        const uint64_t tiles = (uint64_t(a.N) + tnw - 1) / tnw;
+        const uint64_t grid = std::max<uint64_t>(1, std::min<uint64_t>((tiles + 3) / 4,
+                                                                        uint64_t(ctx->num_cus) * waves_per_cu / 4));
+        kern<<<dim3(uint32_t(grid)), dim3(256), 0, ctx->stream>>>(a);
+        VA_CHECK_LAUNCH(ctx);
+        return VA_OK;
+    };
+    if (a.Q <= 32) return go(&screen16_small_kernel<1, 4, 16>, 128);
+    if (a.Q <= 64) return go(&screen16_small_kernel<2, 2, 32>, 64);
+    if (a.Q <= 128) return go(&screen16_small_kernel<4, 2, 16>, 64);
+    if (a.Q <= 192) return go(&screen16_small_kernel<6, 1, 16>, 32);
+    return fail(ctx, VA_ERR_INVALID_ARG, "launch_screen16_small: %u queries (at most 192)", a.Q);
+}
+
 va_status launch_bounds(va_context* ctx, const ScreenArgs& a, float* dot, const float* xx_dense, float* xx_list,
                         const uint32_t* cnt, uint32_t n, int64_t ld, uint32_t rows) {
     if (rows == 0 || n == 0) return VA_OK;
@@ -1206,8 +1371,10 @@ bool screen_applies(const va_context* ctx, const ScreenInput& in, uint32_t k) {
     if (plan.direct) return false;
     if (!offsets_fit(uint64_t(plan.stride) * in.D, in.D)) return false;
     if (ctx->opt_screen == 2) return true;
-    // automatic: enough queries to fill the 256-query tiles of the screening scan
-    return in.Q >= 192;
+    // automatic: over an fp16 shadow every batch (below kSmallBatch queries the small-batch screen
+    // streams it at half the fp32 scan's bytes); over fp32 rows enough queries to fill the
+    // 256-query tiles of the converting scan
+    return in.xh ? true : in.Q >= kSmallBatch;
 }
 
 va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer& exact, uint32_t k,
@@ -1333,7 +1500,10 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
             a.ptc = ptc;
             pretest_kernel<<<dim3((Q + 255) / 256), dim3(256), 0, ctx->stream>>>(a, Q, ptc);
             VA_CHECK_LAUNCH(ctx);
-            VA_CHECK_STATUS(launch_screen16(ctx, a));
+            if (Q < kSmallBatch)
+                VA_CHECK_STATUS(launch_screen16_small(ctx, a));
+            else
+                VA_CHECK_STATUS(launch_screen16(ctx, a));
         } else {
             VA_CHECK_STATUS(launch_screen<SCREEN_FILTER>(ctx, a));
         }
