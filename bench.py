@@ -50,7 +50,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=2)
-    p.add_argument("--workload", default="all", choices=["all", "c2", "c3", "c4", "c5", "kmeans", "pq"],
+    p.add_argument("--workload", default="all",
+                   choices=["all", "c2", "c3", "c4", "c5", "kmeans", "pq", "ceiling", "small"],
                    help="all = configs[1] headline + configs[2..4] extras")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines (profiling runs)")
     p.add_argument("--no-extra", action="store_true", help="headline only (no L2 top-10 extra)")
@@ -135,6 +136,100 @@ def mean_phases(phases):
     out["scans"] = n
     out.update({k: last[k] for k in ("sample_rows", "candidate_cap", "overflow_rows", "screened", "rerank_rows")
                 if k in last})
+    return out
+
+
+PROBES = (("fp32", 0, "fp32_mfma_tflops", 1500), ("fp16", 1, "fp16_mfma_tflops", 3000),
+          ("int8", 2, "int8_mfma_tops", 3000), ("fp4", 3, "fp4_mfma_tflops", 3000))
+
+
+def run_ceiling(ctx):
+    """The board's sustained MFMA rate per instruction the scans use (va_probe_mfma: register-only
+    loops on every SIMD, random and constant operands) with the engine clock, beside the datasheet
+    peak.  Outside every timed region."""
+    import ctypes as C
+
+    from vectoraccelerate_amd import _lib
+
+    out = {}
+    for name, kind, peak_key, iters in PROBES:
+        row = {"datasheet_peak": PEAK[peak_key], "unit": "TOP/s" if name == "int8" else "TFLOP/s"}
+        for rnd, label in ((1, "random"), (0, "constant")):
+            r = _lib.ProbeResult()
+            ctx.check(ctx.lib.va_probe_mfma(ctx.handle, kind, rnd, iters, C.byref(r)), "va_probe_mfma")
+            t = r.ops_per_second / 1e12
+            row[label] = {"rate": t, "frac_of_datasheet": t / PEAK[peak_key], "engine_mhz": r.engine_mhz, "ms": r.ms}
+        out[name] = row
+        log(f"MFMA ceiling {name}: random {row['random']['rate']:.1f} ({100 * row['random']['frac_of_datasheet']:.1f}% "
+            f"of {PEAK[peak_key]:.0f}) at {row['random']['engine_mhz']:.0f} MHz; constant {row['constant']['rate']:.1f} "
+            f"({100 * row['constant']['frac_of_datasheet']:.1f}%) at {row['constant']['engine_mhz']:.0f} MHz")
+    return out
+
+
+def with_ceiling(roof: dict, ceil: dict | None, name: str) -> dict:
+    """A roofline dict with the measured ceiling of its instruction beside the datasheet peak."""
+    if not ceil or name not in ceil or not roof.get("achieved"):
+        return roof
+    m = ceil[name]["random"]["rate"]
+    roof["measured_ceiling"] = {"instruction": name, "rate": m, "operands": "random",
+                                "engine_mhz": ceil[name]["random"]["engine_mhz"],
+                                "frac_of_measured": roof["achieved"] / m}
+    return roof
+
+
+def run_small_batches(ctx, a, ix, qpool, metric: int, k: int, label: str):
+    """Index searches with Q = 1, 10, 100 (the reference's published batch scaling,
+    Guides/03-Accelerated-Search/01-Flat-Search-On-GPU.md:300-308) over a resident index: the
+    small-batch screen over the fp16 shadow, checked bit for bit against the fp32-only scan."""
+    import torch
+
+    from vectoraccelerate_amd import _lib
+
+    info = ix._info()
+    N, D = info.slots, info.dimension
+    shadow_bytes = float(N) * D * 2
+    out = {}
+    for Q in (1, 10, 100):
+        q = qpool[:Q].contiguous()
+        idx = ctx.empty((Q, k), torch.int32)
+        dist = ctx.empty((Q, k), torch.float32)
+
+        def step():
+            ctx.check(ctx.lib.va_index_search(ctx.handle, ix._h, metric, q.data_ptr(), Q, k, idx.data_ptr(),
+                                              dist.data_ptr()), "va_index_search")
+
+        ms, ph = timed(ctx, step, max(20, a.steps), 3)
+        phm = mean_phases(ph)
+        i32 = ctx.empty((Q, k), torch.int32)
+        d32 = ctx.empty((Q, k), torch.float32)
+        ctx.set_option(_lib.VA_OPT_SCREEN, 1)
+        try:
+            def step32():
+                ctx.check(ctx.lib.va_index_search(ctx.handle, ix._h, metric, q.data_ptr(), Q, k, i32.data_ptr(),
+                                                  d32.data_ptr()), "va_index_search")
+
+            ms32, ph32 = timed(ctx, step32, max(10, a.steps // 2), 2)
+        finally:
+            ctx.set_option(_lib.VA_OPT_SCREEN, 0)
+        same = bool(torch.equal(idx, i32)) and bool(torch.equal(dist.view(torch.int32), d32.view(torch.int32)))
+        if not same:
+            raise SystemExit(f"{label} Q={Q}: the small-batch screen differs from the fp32 scan")
+        scan_ms = phm.get("scan_ms") or ms
+        gbs_scan = shadow_bytes / (scan_ms * 1e-3) / 1e9
+        gbs_search = shadow_bytes / (ms * 1e-3) / 1e9
+        out[f"Q{Q}"] = {
+            "ms_per_search": ms, "qps": Q / (ms * 1e-3), "phases_ms": phm,
+            "fp32_scan_only_ms": ms32, "equals_fp32_scan": same,
+            "roofline": {"bound": "hbm", "achieved": gbs_scan, "peak": PEAK["hbm_gbs"], "unit": "GB/s",
+                         "frac": gbs_scan / PEAK["hbm_gbs"], "kernel": "screen16_small_kernel (screen pass)",
+                         "algorithmic": f"the fp16 shadow read once: N*D*2 = {shadow_bytes:.4g} B per search",
+                         "whole_search_gbs": gbs_search, "whole_search_frac": gbs_search / PEAK["hbm_gbs"],
+                         "whole_search_over_roofline": ms / (shadow_bytes / (PEAK["hbm_gbs"] * 1e9) * 1e3)},
+        }
+        log(f"{label} Q={Q}: {ms:.3f} ms/search = {Q / (ms * 1e-3):.0f} QPS (fp32 scan only {ms32:.3f} ms); screen "
+            f"pass {scan_ms:.3f} ms = {gbs_scan:.0f} GB/s ({100 * gbs_scan / PEAK['hbm_gbs']:.1f}% HBM); whole "
+            f"search {ms / (shadow_bytes / 8e12 * 1e3):.2f}x the shadow's HBM time; identical: {same}")
+        del idx, dist, i32, d32
     return out
 
 
@@ -300,6 +395,30 @@ def run_c2(ctx, a, cpu: bool, extra_l2: bool):
                                             "scan_tflops": flops / (s10 * 1e-3) / 1e12,
                                             "mfma_frac": flops / (s10 * 1e-3) / 1e12 / peak}
         log(f"configs[1] shape, L2^2 top-10 (va_fused_topk): {ms10:.3f} ms/step, scan {s10:.3f} ms")
+        # the metric's own wording through the index: flat L2^2 top-10 at 1M x 1536, Q=1024
+        ixi = ctx.empty((Q, 10), torch.int32)
+        ixd = ctx.empty((Q, 10), torch.float32)
+
+        def l2_index():
+            ctx.check(ctx.lib.va_index_search(ctx.handle, ix._h, _lib.VA_METRIC_L2SQ, q.data_ptr(), Q, 10,
+                                              ixi.data_ptr(), ixd.data_ptr()), "va_index_search")
+
+        msi, phi = timed(ctx, l2_index, a.steps, a.warmup)
+        si = mean_phases(phi)
+        same_i = bool(torch.equal(ixi, idx10)) and bool(torch.equal(ixd.view(torch.int32), dist10.view(torch.int32)))
+        ti = flops / (si["scan_ms"] * 1e-3) / 1e12
+        res["l2sq_top10_index_search"] = {
+            "ms_per_step": msi, "qps": Q / (msi * 1e-3), "phases_ms": si, "scan_tflops": ti,
+            "mfma_frac": ti / PEAK["fp16_mfma_tflops"], "equals_fused_topk": same_i,
+            "what": "the metric's wording (flat L2^2 top-10 @1M x 1536, Q=1024) through va_index_search "
+                    "(screen16_kernel over the shadow)"}
+        log(f"configs[1] shape, L2^2 top-10 through the index: {msi:.3f} ms/step = {Q / (msi * 1e-3):.0f} QPS, scan "
+            f"{si['scan_ms']:.3f} ms; identical to va_fused_topk: {same_i}")
+        if not same_i:
+            raise SystemExit("L2^2 index search differs from va_fused_topk")
+        del ixi, ixd
+        res["small_batches"] = run_small_batches(ctx, a, ix, q, _lib.VA_METRIC_COSINE, 100,
+                                                 "configs[1] shape (1M x 1536 cosine top-100)")
     if cpu:
         from oracle import oracle
 
@@ -669,10 +788,11 @@ def run_pq(ctx, a, cpu: bool):
     lookups = float(Q) * N * M
     scan_ms = tim.get("scan_ms") if tim else None
     rate = lookups / (scan_ms * 1e-3) / 1e12 if scan_ms else None
-    # LDS: 128 bytes per clock per CU = 32 four-byte lookups; 256 CUs at 2.4 GHz.  The filter pass
-    # reads fp16 pair tables (one 4-byte read carries two queries' entries), so its table lookups
-    # per second can exceed the 4-byte read rate it is compared with.
+    # LDS: 128 bytes per clock per CU = 32 four-byte reads; 256 CUs at 2.4 GHz = 19.66 T reads/s.
+    # The filter pass reads fp16 pair tables: one 4-byte read carries two queries' entries, so the
+    # fraction is counted per read (two lookups each).
     lds_peak = 256 * 32 * 2.4e9 / 1e12
+    reads = rate / 2 if rate else None
     xe = torch.randn(1_000_000, D, device="cuda", generator=g)
     ce = ctx.empty((1_000_000, M), torch.uint8)
     torch.cuda.synchronize()
@@ -685,14 +805,17 @@ def run_pq(ctx, a, cpu: bool):
         "workload": "PQ ADC top-10: 10M rows x M=16 codes (K=256, d=768), Q=1024 (synthetic codes, random codebooks)",
         "ms_per_step": ms, "qps": Q / (ms * 1e-3), "scan_timings": tim,
         "encode_rows_per_s": 1_000_000 / enc_s,
-        "roofline": {"bound": "lds", "achieved": rate, "peak": lds_peak, "unit": "T lookups/s",
-                     "frac": (rate / lds_peak) if rate else None, "kernel": "pq_adc_screen<16> (filter pass)",
-                     "algorithmic": f"Q*N*M = {lookups:.4g} table lookups per scan (fp16 pair tables in LDS: "
-                                    "one 4-byte read serves two queries; exact fp32 re-score of the passes)",
+        "roofline": {"bound": "lds", "achieved": reads, "peak": lds_peak, "unit": "T 4-byte LDS reads/s",
+                     "frac": (reads / lds_peak) if reads else None, "kernel": "pq_adc_screen<16> (filter pass)",
+                     "lookups_per_s_T": rate,
+                     "algorithmic": f"Q*N*M = {lookups:.4g} table lookups per scan = {lookups / 2:.4g} 4-byte LDS "
+                                    "reads (fp16 pair tables: one read serves two queries; exact fp32 re-score "
+                                    "of the passes)",
                      **counted(COUNTERS_PQ)},
     }
     log(f"PQ ADC top-10: {ms:.3f} ms/step = {res['qps']:.0f} QPS; filter scan {scan_ms} ms = "
-        f"{rate if rate is None else round(rate, 2)} T lookups/s; encode {res['encode_rows_per_s']:.3g} rows/s")
+        f"{rate if rate is None else round(rate, 2)} T lookups/s = {reads if reads is None else round(reads / lds_peak, 3)} "
+        f"of the LDS read rate; encode {res['encode_rows_per_s']:.3g} rows/s")
     if cpu:
         from oracle import oracle
 
@@ -709,6 +832,28 @@ def run_pq(ctx, a, cpu: bool):
                                "ids_equal_gpu": bool((gi == oi).all())}
         log(f"PQ CPU baseline: {nq / dt:.2f} QPS; ids equal: {res['cpu_baseline']['ids_equal_gpu']}")
     del codes, q, cb, xe, ce
+    torch.cuda.empty_cache()
+    return res
+
+
+def run_small_768(ctx, a):
+    """The reference's own batch-scaling shape: flat L2^2 top-10 over 1M x 768 N(0,1) rows with
+    Q = 1, 10, 100 (Guides/03-Accelerated-Search/01-Flat-Search-On-GPU.md:300-308), through the index."""
+    import torch
+
+    from vectoraccelerate_amd import AcceleratedVectorIndex, IndexConfiguration, _lib
+
+    N, D = 1_000_000, 768
+    g = torch.Generator(device="cuda").manual_seed(30)
+    x = torch.randn(N, D, device="cuda", generator=g)
+    q = torch.randn(100, D, device="cuda", generator=g).contiguous()
+    ix = AcceleratedVectorIndex(IndexConfiguration.flat(D, N), ctx)
+    ix.insert(vectors=x)
+    del x
+    torch.cuda.empty_cache()
+    res = run_small_batches(ctx, a, ix, q, _lib.VA_METRIC_L2SQ, 10, "1M x 768 L2^2 top-10")
+    res["workload"] = "flat L2^2 top-10, N=1,000,000 x d=768 N(0,1) rows, Q in {1, 10, 100} (index search)"
+    ix.close()
     torch.cuda.empty_cache()
     return res
 
@@ -734,6 +879,15 @@ def main() -> int:
     ctx.set_profiling(True)
     cpu = not a.no_cpu
     extra = {}
+    ceil = run_ceiling(ctx) if a.workload in ("all", "ceiling") else None
+    if ceil:
+        extra["mfma_ceiling"] = ceil
+    if a.workload == "ceiling":
+        ctx.close()
+        print(json.dumps({"metric": METRIC, "value": None, "extra": extra}), flush=True)
+        return 0
+    if a.workload in ("all", "small"):
+        extra["small_batches_1Mx768"] = run_small_768(ctx, a)
     if a.workload in ("all", "c2"):
         c2 = run_c2(ctx, a, cpu, extra_l2=not a.no_extra)
     else:
@@ -748,12 +902,15 @@ def main() -> int:
         extra["ivf_training_kmeans"] = run_kmeans(ctx, a, cpu)
     if a.workload in ("all", "pq"):
         extra["pq_adc"] = run_pq(ctx, a, cpu)
+    for key, name in (("configs2_int8", "int8"), ("configs3_binary", "fp4"), ("ivf_training_kmeans", "fp32")):
+        if key in extra and "roofline" in extra[key]:
+            with_ceiling(extra[key]["roofline"], ceil, name)
     ctx.close()
     if c2 is None:
         print(json.dumps({"metric": METRIC, "value": None, "extra": extra}), flush=True)
         return 0
     cpu_base = c2.pop("cpu_baseline", None)
-    roof = c2.pop("roofline")
+    roof = with_ceiling(c2.pop("roofline"), ceil, "fp16" if c2["phases_ms"].get("screened") else "fp32")
     line = {
         "metric": METRIC,
         "value": c2["qps"],

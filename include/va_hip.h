@@ -435,6 +435,28 @@ va_status va_pq_search(va_context* ctx, const float* queries, uint32_t num_queri
                        uint32_t K, const float* codebooks, const uint8_t* codes, uint32_t num_vectors, uint32_t k,
                        uint32_t* out_idx, float* out_dist);
 
+/* ---- measurement: the matrix-core ceiling of the board ------------------------------------------
+ * No reference counterpart (the reference publishes no hardware peaks).  Every SIMD runs two waves
+ * of back-to-back MFMAs of one instruction on register operands (no memory traffic), random or
+ * constant (the clock falls further on random bits), `iterations` rounds of 8 MFMAs per wave,
+ * after one untimed warm-up launch.  Reports the dense rate sustained (2 operations per
+ * multiply-add), the launch time from events on the context stream, and the engine clock during
+ * the launch (the shader clock counter over the constant-rate wall clock).  Synchronises. */
+typedef enum {
+    VA_PROBE_FP32 = 0, /* v_mfma_f32_32x32x2_f32: the fp32 distance GEMM */
+    VA_PROBE_FP16 = 1, /* v_mfma_f32_32x32x16_f16: the fp16 screens */
+    VA_PROBE_INT8 = 2, /* v_mfma_i32_32x32x32_i8: the int8 scan */
+    VA_PROBE_FP4 = 3   /* v_mfma_scale_f32_32x32x64_f8f6f4 on fp4 operands: the Hamming scan */
+} va_probe_kind;
+typedef struct {
+    double ops_per_second; /* dense operations per second sustained */
+    double engine_mhz;     /* mean engine clock over the timed launch */
+    double ms;             /* timed launch */
+    double ops;            /* operations in the timed launch */
+} va_probe_result;
+va_status va_probe_mfma(va_context* ctx, va_probe_kind kind, int random_operands, uint32_t iterations,
+                        va_probe_result* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,6 +35,11 @@ VA_MAX_K = 1024
 VA_I8_MAX_DIM = 131071  # va_i8_scan_topk: the int32 dot of two code vectors stays exact
 VA_NOALLOC_SCRATCH_BYTES = 64 << 20
 
+VA_PROBE_FP32 = 0
+VA_PROBE_FP16 = 1
+VA_PROBE_INT8 = 2
+VA_PROBE_FP4 = 3
+
 _p = C.c_void_p
 _u32 = C.c_uint32
 _u64 = C.c_uint64
@@ -104,6 +109,7 @@ SIGNATURES: dict[str, tuple] = {
     "va_pq_distance_tables": (_st, [_p, _p, _u32, _u32, _u32, _u32, _p, _p]),
     "va_pq_adc_distances": (_st, [_p, _p, _u32, _p, _u32, _u32, _u32, _p]),
     "va_pq_search": (_st, [_p, _p, _u32, _u32, _u32, _u32, _p, _p, _u32, _u32, _p, _p]),
+    "va_probe_mfma": (_st, [_p, _i32, _i32, _u32, _p]),
 }
 
 
@@ -147,6 +153,17 @@ class IndexInfo(C.Structure):
         ("ivf_routed", C.c_uint32),
         ("centroids", C.c_void_p),
         ("lists", C.c_void_p),
+    ]
+
+
+class ProbeResult(C.Structure):
+    """va_probe_result (include/va_hip.h)."""
+
+    _fields_ = [
+        ("ops_per_second", C.c_double),
+        ("engine_mhz", C.c_double),
+        ("ms", C.c_double),
+        ("ops", C.c_double),
     ]
 
 

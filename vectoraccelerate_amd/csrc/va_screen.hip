@@ -67,6 +67,10 @@ enum ScreenMode : int { SCREEN_KEYS = 0, SCREEN_FILTER = 1 };
 // below this many queries a search over the fp16 shadow takes screen16_small_kernel (a 256-query
 // tile of screen16_kernel would be mostly padding)
 constexpr uint32_t kSmallBatch = 192;
+// screen16_small_kernel serves at most this many queries: above it a 256-query tile of
+// screen16_kernel (MFMA-bound) costs less than the small kernel's query-register traffic
+// (measured at 1M x 768: 64 queries 0.63 ms small, ~0.41 ms in one screen16 tile)
+constexpr uint32_t kSmallBatchMax = 32;
 
 struct ScreenArgs {
     const float* x = nullptr;     // database rows, row j at x + j * ldx
@@ -91,6 +95,8 @@ struct ScreenArgs {
     // fp16 shadow of the database (screen16_kernel): row j at xh + j * Dp, |x_j|^2 at xn[j]
     const _Float16* xh = nullptr;
     const float* xn = nullptr;
+    // screen16_small_kernel: row j of the scan is shadow row j * xstride (the threshold sample)
+    uint32_t xstride = 1;
     // screen16_kernel: the pre-test constants of each query, {A, B, C, 2^-scale} (pretest_kernel)
     const float4* ptc = nullptr;
 };
@@ -942,139 +948,154 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
 }
 
 // ---- the small-batch screen over the fp16 shadow ------------------------------------------------
-// Fewer than 192 queries: streaming the shadow from HBM is the cost, not the MFMA (Q = 1 reads
-// 2 bytes per value where the fp32 scan reads 4).  Every wave is an independent worker with no
-// LDS and no barrier: it takes tiles of 32 MB rows in turn and computes all 32 NQB (padded)
-// queries against them on v_mfma_f32_32x32x16_f16, both operands loaded straight into registers
-// by buffer loads (rows from HBM through a descriptor that ends at the tile's last row, so rows
-// past N read zeros; queries from L2, zeros past Q) in chunks of 2 KH halves, the next chunk in
-// flight while the current one computes.  In chunk c, lane (l, h) loads halves
-// c 2KH + KH h .. + KH - 1 of its row (l of each block) and of its query: k-step t of the chunk
-// takes the lane's 8 halves 8t .. 8t + 7 from both operands, so row and query pair the same d
-// (the dot is the same sum in any order; the screen's bound does not depend on the order).
-// Loads past the last chunk use an offset beyond the descriptors (zeros; branch-free, so the
-// compiler's wait counts stay exact).  Epilogue: the pre-test of screen16_kernel on each value
-// (flagged rows always pass), one atomic per lane pair and query block, appends from registers.
-template <int NQB, int MB, int KH>
+// Few queries: streaming the shadow from HBM is the cost, not the MFMA (Q = 1 reads 2 bytes per
+// value where the fp32 scan reads 4).  Every wave is an independent worker with no LDS and no
+// barrier: it takes tiles of 16 MB rows in turn and computes all 16 NQB (padded) queries against
+// them on v_mfma_f32_16x16x32_f16, both operands loaded straight into registers by buffer loads
+// (rows from HBM through a descriptor that ends at the tile's last row, so rows past N read
+// zeros; queries from L2, zeros past Q) in chunks of 64 L bytes per row, a ring of R chunks (R - 1
+// in flight while one computes).  Load i of a chunk: lane (r, g) = (lane % 16, lane / 16) reads
+// bytes 64 i + 16 g .. + 15 of its row r of each block (and of its query r): the four lanes of a
+// row read 64 contiguous bytes per instruction, and k-step i takes the lane's 8 halves from both
+// operands, so row and query pair the same d (the dot is the same sum in any order; the screen's
+// bound does not depend on it).  Loads past the last chunk use an offset beyond the descriptors
+// (zeros; branch-free, so the compiler's wait counts stay exact).  Epilogue: the pre-test of
+// screen16_kernel on each value (flagged rows always pass) and appends from registers.
+template <int MODE, int NQB, int MB, int L, int R>
 __global__ __launch_bounds__(256, 2) void screen16_small_kernel(ScreenArgs a) {
-    constexpr int TNW = 32 * MB;  // rows per wave tile
-    constexpr int L = KH / 8;     // 16-byte loads per lane, operand block and chunk
-    constexpr uint32_t CH = 2 * KH * 2;  // bytes per chunk of a row
-    const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5;
+    constexpr int TNW = 16 * MB;       // rows per wave tile
+    constexpr uint32_t CH = 64u * L;   // bytes per chunk of a row
+    const int lane = threadIdx.x & 63, r16 = lane & 15, g = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
-    const uint32_t nch = a.Dp / (2 * KH);
+    const uint32_t pitch = a.Dp * 2u;  // bytes per shadow row (a multiple of 128)
+    const uint32_t xpitch = pitch * a.xstride;  // bytes between the rows of the scan
+    const uint32_t nch = pitch / CH;
     const uint32_t ntiles = (a.N + TNW - 1) / TNW;
-    const uint32_t pitch = a.Dp * 2u;  // bytes per shadow row
     const __amdgpu_buffer_rsrc_t qres =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(a.qh), 0, int(a.Q * pitch), 0x00020000);
     uint32_t qoff[NQB], roff[MB];
 #pragma unroll
-    for (int n = 0; n < NQB; ++n) qoff[n] = uint32_t(32 * n + l32) * pitch + uint32_t(KH * 2 * hh);
+    for (int n = 0; n < NQB; ++n) qoff[n] = uint32_t(16 * n + r16) * pitch + 16u * uint32_t(g);
 #pragma unroll
-    for (int m = 0; m < MB; ++m) roff[m] = uint32_t(32 * m + l32) * pitch + uint32_t(KH * 2 * hh);
+    for (int m = 0; m < MB; ++m) roff[m] = uint32_t(16 * m + r16) * xpitch + 16u * uint32_t(g);
     const float tiny = a.op == OP_COS_DIST ? 8.0f * a.c0x : 0.0f;
-    h8v ra[MB][L], rb[MB][L], qa[NQB][L], qb[NQB][L];
-    f32x16 acc[MB][NQB];
+    h8v rbuf[R][MB][L], qbuf[R][NQB][L];
+    f32x4v acc[MB][NQB];
     for (uint32_t tile = blockIdx.x * 4u + uint32_t(wave); tile < ntiles; tile += gridDim.x * 4u) {
         const uint32_t rs = tile * TNW, rc = min(uint32_t(TNW), a.N - rs);
+        // (the descriptor ends after the tile's last row: (rc - 1) row strides plus one row)
         const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<_Float16*>(a.xh + int64_t(rs) * a.Dp), 0, int(rc * pitch), 0x00020000);
-        auto load = [&](uint32_t c, h8v(&r)[MB][L], h8v(&q)[NQB][L]) {
+            const_cast<_Float16*>(a.xh + int64_t(rs) * a.xstride * a.Dp), 0, int((rc - 1) * xpitch + pitch),
+            0x00020000);
+        auto load = [&](uint32_t c, h8v(&rb)[MB][L], h8v(&qb)[NQB][L]) {
             const bool ok = c < nch;
             const uint32_t ko = c * CH;
 #pragma unroll
             for (int i = 0; i < L; ++i) {
 #pragma unroll
                 for (int m = 0; m < MB; ++m)
-                    r[m][i] = __builtin_bit_cast(
-                        h8v, __builtin_amdgcn_raw_buffer_load_b128(xres, ok ? roff[m] + ko + 16u * i : kDmaSkip, 0, 0));
+                    rb[m][i] = __builtin_bit_cast(
+                        h8v, __builtin_amdgcn_raw_buffer_load_b128(xres, ok ? roff[m] + ko + 64u * i : kDmaSkip, 0, 0));
 #pragma unroll
                 for (int n = 0; n < NQB; ++n)
-                    q[n][i] = __builtin_bit_cast(
-                        h8v, __builtin_amdgcn_raw_buffer_load_b128(qres, ok ? qoff[n] + ko + 16u * i : kDmaSkip, 0, 0));
+                    qb[n][i] = __builtin_bit_cast(
+                        h8v, __builtin_amdgcn_raw_buffer_load_b128(qres, ok ? qoff[n] + ko + 64u * i : kDmaSkip, 0, 0));
             }
         };
-        auto mma = [&](const h8v(&r)[MB][L], const h8v(&q)[NQB][L]) {
+        auto mma = [&](const h8v(&rb)[MB][L], const h8v(&qb)[NQB][L]) {
 #pragma unroll
             for (int i = 0; i < L; ++i)
 #pragma unroll
                 for (int m = 0; m < MB; ++m)
 #pragma unroll
                     for (int n = 0; n < NQB; ++n)
-                        acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(r[m][i], q[n][i], acc[m][n], 0, 0, 0);
+                        acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(rb[m][i], qb[n][i], acc[m][n], 0, 0, 0);
         };
 #pragma unroll
         for (int m = 0; m < MB; ++m)
 #pragma unroll
-            for (int n = 0; n < NQB; ++n)
+            for (int n = 0; n < NQB; ++n) acc[m][n] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int v = 0; v < 16; ++v) acc[m][n][v] = 0.0f;
-        load(0, ra, qa);
-        for (uint32_t c = 0; c < nch; c += 2) {
-            load(c + 1, rb, qb);
-            mma(ra, qa);
-            __builtin_amdgcn_sched_barrier(0);
-            load(c + 2, ra, qa);  // past the end: zeros, unused
-            mma(rb, qb);          // past the end: zeros, adds nothing
-            __builtin_amdgcn_sched_barrier(0);
+        for (int r = 0; r < R - 1; ++r) load(uint32_t(r), rbuf[r], qbuf[r]);
+        for (uint32_t c = 0; c < nch; c += R) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                // past the end the loads read zeros (unused) and the MFMAs add nothing
+                load(c + uint32_t(r + R - 1), rbuf[(r + R - 1) % R], qbuf[(r + R - 1) % R]);
+                mma(rbuf[r], qbuf[r]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
-        // ---- filter epilogue: lane (l32, hh) holds query 32n + l32 against rows 32m + 8j + 4hh + e
-        // in acc[m][n][4j + e].  The pre-test one row block at a time (its 16 norms in registers),
-        // building a pass mask per query block; the appends re-read the norms of passing rows.
-        using Mask = std::conditional_t<(16 * MB > 32), uint64_t, uint32_t>;
-        Mask mk[NQB];
+        // lane (r16, g) holds query 16n + r16 against rows 16m + 4g + v in acc[m][n][v]
+        if constexpr (MODE == SCREEN_KEYS) {
+            // the threshold sample: every unscaled dot and every row norm
+#pragma unroll
+            for (int n = 0; n < NQB; ++n) {
+                const uint32_t qt = uint32_t(16 * n + r16);
+                if (qt >= a.Q) continue;
+                const float inv = a.qinfo[qt].z;
+#pragma unroll
+                for (int m = 0; m < MB; ++m)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const uint32_t row = uint32_t(16 * m + 4 * g + v);
+                        if (row < rc) a.out_dot[int64_t(qt) * a.ldo + rs + row] = acc[m][n][v] * inv;
+                    }
+            }
+            if (r16 == 0) {
+#pragma unroll
+                for (int m = 0; m < MB; ++m)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const uint32_t row = uint32_t(16 * m + 4 * g + v);
+                        if (row < rc) a.out_xx[rs + row] = a.xn[uint64_t(rs + row) * a.xstride];
+                    }
+            }
+            continue;
+        }
+        // ---- filter epilogue: the row norms one block at a time, a pass mask per query block;
+        // the appends re-read the norms of passing rows
+        uint32_t mk[NQB];
         float4 pt[NQB];
 #pragma unroll
         for (int n = 0; n < NQB; ++n) {
             mk[n] = 0;
-            pt[n] = a.ptc[min(uint32_t(32 * n + l32), a.Q - 1)];
+            pt[n] = a.ptc[min(uint32_t(16 * n + r16), a.Q - 1)];
         }
 #pragma unroll
         for (int m = 0; m < MB; ++m) {
-            float xxp[16], nxp[16];
-            uint32_t valid = 0;
 #pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                const uint32_t r = uint32_t(32 * m + 8 * (t >> 2) + 4 * hh + (t & 3));
-                const bool in = r < rc;
-                const float v = in ? a.xn[rs + r] : 0.0f;
-                const float nx = __builtin_amdgcn_sqrtf(v);
-                const bool flag = !(v < 4.29e9f) || nx < tiny;
-                xxp[t] = flag ? __builtin_nanf("") : v;
-                nxp[t] = flag ? __builtin_nanf("") : nx;
-                valid |= uint32_t(in) << t;
-            }
+            for (int v = 0; v < 4; ++v) {
+                const uint32_t row = uint32_t(16 * m + 4 * g + v);
+                const bool in = row < rc;
+                const float xx = in ? a.xn[rs + row] : 0.0f;
+                const float nx = __builtin_amdgcn_sqrtf(xx);
+                const bool flag = !(xx < 4.29e9f) || nx < tiny;
+                const float xxp = flag ? __builtin_nanf("") : xx, nxp = flag ? __builtin_nanf("") : nx;
 #pragma unroll
-            for (int n = 0; n < NQB; ++n) {
-                uint32_t b = 0;
-#pragma unroll
-                for (int t = 0; t < 16; ++t)
-                    b |= uint32_t(!(acc[m][n][t] < fmaf(pt[n].x, xxp[t], fmaf(pt[n].y, nxp[t], pt[n].z)))) << t;
-                mk[n] |= Mask(b & valid) << (16 * m);
+                for (int n = 0; n < NQB; ++n)
+                    mk[n] |= uint32_t(in & !(acc[m][n][v] < fmaf(pt[n].x, xxp, fmaf(pt[n].y, nxp, pt[n].z))))
+                             << (4 * m + v);
             }
         }
 #pragma unroll
         for (int n = 0; n < NQB; ++n) {
-            const uint32_t qt = uint32_t(32 * n + l32);
-            const Mask mq = qt < a.Q ? mk[n] : Mask(0);
+            const uint32_t qt = uint32_t(16 * n + r16);
+            const uint32_t mq = qt < a.Q ? mk[n] : 0u;
             if (!__ballot(mq != 0u)) continue;
-            const uint32_t qi = qt < a.Q ? qt : 0u;
-            const uint32_t cnt = uint32_t(__builtin_popcountll(uint64_t(mq)));
-            const uint32_t other = uint32_t(__shfl_xor(int(cnt), 32));
-            uint32_t base = 0;
-            if (hh == 0 && cnt + other) base = atomicAdd(a.cnt + qi, cnt + other);
-            uint32_t pos = uint32_t(__shfl(int(base), l32)) + (hh ? other : 0u);
+            if (!mq) continue;
+            uint32_t pos = atomicAdd(a.cnt + qt, uint32_t(__popc(mq)));
 #pragma unroll
             for (int m = 0; m < MB; ++m)
 #pragma unroll
-                for (int t = 0; t < 16; ++t) {
-                    if ((mq >> (16 * m + t)) & 1u) {
+                for (int v = 0; v < 4; ++v) {
+                    if ((mq >> (4 * m + v)) & 1u) {
                         if (pos < a.cap) {
-                            const uint32_t r = uint32_t(32 * m + 8 * (t >> 2) + 4 * hh + (t & 3));
-                            const int64_t o = int64_t(qi) * a.cap + pos;
-                            a.cand_dot[o] = acc[m][n][t] * pt[n].w;
-                            a.cand_xx[o] = a.xn[rs + r];
-                            a.cand_id[o] = a.id_base + rs + r;
+                            const uint32_t row = uint32_t(16 * m + 4 * g + v);
+                            const int64_t o = int64_t(qt) * a.cap + pos;
+                            a.cand_dot[o] = acc[m][n][v] * pt[n].w;
+                            a.cand_xx[o] = a.xn[rs + row];
+                            a.cand_id[o] = a.id_base + rs + row;
                         }
                         ++pos;
                     }
@@ -1278,8 +1299,17 @@ va_status launch_screen16(va_context* ctx, const ScreenArgs& a) {
     return VA_OK;
 }
 
-// The small-batch screen: per query count the widest query tile whose registers keep two waves
-// per SIMD (NQB 32-query blocks x MB 32-row blocks, chunks of 2 KH halves).
+// The small-batch screen: NQB 16-query blocks x MB 16-row blocks per wave, chunks of 64 L bytes
+// per row, a ring of R chunks, within the registers of two waves per SIMD.  Measured on 1M rows
+// of 768 and 1536 values: one query block of 2 row blocks with a 6-deep ring streams the shadow
+// at 5.6-5.8 TB/s (4 row blocks, 4 deep: 5.1; 8 row blocks, 2 deep: 4.8); for 17-32 queries 4 row
+// blocks 3 deep (3.9 TB/s) beat 2 blocks 6 deep (3.5).
+template <int NQB, int MB, int L, int R>
+struct Launch {
+    static constexpr uint32_t queries = 16u * NQB;  // queries a wave tile covers
+    static constexpr uint32_t TNW = 16u * MB;       // rows of a wave tile
+};
+template <int MODE>
 va_status launch_screen16_small(va_context* ctx, const ScreenArgs& a) {
     if (a.Q == 0 || a.N == 0) return VA_OK;
     const uint32_t waves_per_cu = 8;
@@ -1291,11 +1321,20 @@ va_status launch_screen16_small(va_context* ctx, const ScreenArgs& a) {
         VA_CHECK_LAUNCH(ctx);
         return VA_OK;
     };
-    if (a.Q <= 32) return go(&screen16_small_kernel<1, 4, 16>, 128);
-    if (a.Q <= 64) return go(&screen16_small_kernel<2, 2, 32>, 64);
-    if (a.Q <= 128) return go(&screen16_small_kernel<4, 2, 16>, 64);
-    if (a.Q <= 192) return go(&screen16_small_kernel<6, 1, 16>, 32);
-    return fail(ctx, VA_ERR_INVALID_ARG, "launch_screen16_small: %u queries (at most 192)", a.Q);
+#ifndef VA_S16S_A
+#define VA_S16S_A 1, 2, 2, 6
+#endif
+#ifndef VA_S16S_B
+#define VA_S16S_B 2, 4, 2, 3
+#endif
+    using KA = Launch<VA_S16S_A>;
+    using KB = Launch<VA_S16S_B>;
+    static_assert(KB::queries >= kSmallBatchMax, "the small-batch screen covers every batch it is given");
+    if (uint64_t(a.Dp) * 2 * a.xstride * (KA::TNW > KB::TNW ? KA::TNW : KB::TNW) > 0x7FFFFFF0ull)
+        return fail(ctx, VA_ERR_INVALID_ARG, "launch_screen16_small: tile offsets beyond 32 bits");
+    if (a.Q <= KA::queries) return go(&screen16_small_kernel<MODE, VA_S16S_A>, KA::TNW);
+    if (a.Q <= KB::queries) return go(&screen16_small_kernel<MODE, VA_S16S_B>, KB::TNW);
+    return fail(ctx, VA_ERR_INVALID_ARG, "launch_screen16_small: %u queries (at most %u)", a.Q, kSmallBatchMax);
 }
 
 va_status launch_bounds(va_context* ctx, const ScreenArgs& a, float* dot, const float* xx_dense, float* xx_list,
@@ -1463,7 +1502,15 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
         a.out_dot = reinterpret_cast<float*>(skeys);
         a.out_xx = sxx;
         a.ldo = int64_t(S);
-        VA_CHECK_STATUS(launch_screen<SCREEN_KEYS>(ctx, a));
+        if (in.xh && Q <= kSmallBatchMax) {
+            // small batches sample the fp16 shadow (half the bytes, every CU busy)
+            a.xh = in.xh;
+            a.xn = in.xn;
+            a.xstride = plan.stride;
+            VA_CHECK_STATUS(launch_screen16_small<SCREEN_KEYS>(ctx, a));
+        } else {
+            VA_CHECK_STATUS(launch_screen<SCREEN_KEYS>(ctx, a));
+        }
         VA_CHECK_STATUS(launch_bounds(ctx, a, reinterpret_cast<float*>(skeys), sxx, nullptr, nullptr, uint32_t(S),
                                       int64_t(S), nq));
         VA_CHECK_STATUS(mask_dense_keys(ctx, skeys, nq, uint32_t(S), int64_t(S), 0, plan.stride, out.skip));
@@ -1500,8 +1547,8 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
             a.ptc = ptc;
             pretest_kernel<<<dim3((Q + 255) / 256), dim3(256), 0, ctx->stream>>>(a, Q, ptc);
             VA_CHECK_LAUNCH(ctx);
-            if (Q < kSmallBatch)
-                VA_CHECK_STATUS(launch_screen16_small(ctx, a));
+            if (Q <= kSmallBatchMax)
+                VA_CHECK_STATUS(launch_screen16_small<SCREEN_FILTER>(ctx, a));
             else
                 VA_CHECK_STATUS(launch_screen16(ctx, a));
         } else {
