@@ -42,32 +42,16 @@ struct FbArgs {
     const uint8_t* skip = nullptr;     // excluded rows: their keys are kAbsentKey
 };
 enum FbState : int { FB_PREFIX = 0, FB_NEED = 1, FB_K = 2, FB_EDGE = 3, FB_OVF = 4 };
-constexpr int kFbPasses = 5;
-constexpr uint32_t kFbGrid = 1024;  // workgroups per pass (4 waves each)
-constexpr uint32_t kFbTieBins = 4096;
+static_assert(kFbKeyBins == 2048, "the passes' key histograms have 2048 bins");
+// (the pass count, grid, bins and buffer sizes: fb_geometry / fb_bytes in va_plan.hpp)
 
-// host: list capacity and id shift for ids below N, `rows` rows in all (0: N) and top-k.  The
-// id-edge pass keeps fewer than k ties plus one id bin, which holds at most min(2^ishift, rows).
-inline void fb_geometry(uint32_t N, uint32_t k, uint32_t& ishift, uint32_t& cap, uint32_t rows = 0) {
-    ishift = 0;
-    while ((uint64_t(N) >> ishift) >= kFbTieBins) ++ishift;
-    const uint64_t bin = std::min<uint64_t>(uint64_t(1) << ishift, rows ? rows : N);
-    cap = uint32_t((uint64_t(k) + bin + 63) / 64 * 64);
-}
-inline size_t fb_bytes(uint32_t rmax, uint32_t N, uint32_t k, uint32_t rows = 0) {
-    uint32_t ishift, cap;
-    fb_geometry(N, k, ishift, cap, rows);
-    return Scratch::round(uint64_t(rmax) * 2048 * 4) + Scratch::round(uint64_t(rmax) * kFbTieBins * 4) +
-           Scratch::round(uint64_t(rmax) * 8 * 4) + Scratch::round(uint64_t(rmax) * 4) +
-           Scratch::round(uint64_t(rmax) * cap * 4) * 2 + Scratch::round(8 * 4);
-}
 inline FbArgs fb_carve(Scratch& s, uint32_t rmax, uint32_t N, uint32_t k, uint32_t rows = 0) {
     FbArgs a;
     a.rmax = rmax;
     a.N = N;
     a.k = k;
     fb_geometry(N, k, a.ishift, a.cap, rows);
-    a.hist = s.carve<uint32_t>(uint64_t(rmax) * 2048);
+    a.hist = s.carve<uint32_t>(uint64_t(rmax) * kFbKeyBins);
     a.tidh = s.carve<uint32_t>(uint64_t(rmax) * kFbTieBins);
     a.st = s.carve<uint32_t>(uint64_t(rmax) * 8);
     a.cnt = s.carve<uint32_t>(rmax);

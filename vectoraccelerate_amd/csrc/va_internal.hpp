@@ -10,6 +10,7 @@
 
 #include "../../include/va_hip.h"
 #include "va_keys.hpp"
+#include "va_plan.hpp"
 
 // ---------------------------------------------------------------------------
 // context
@@ -103,8 +104,15 @@ struct Scratch {
     va_context* ctx;
     size_t off = 0;
     explicit Scratch(va_context* c) : ctx(c) {}
-    static size_t round(size_t b) { return (b + 255) & ~size_t(255); }
+    static size_t round(size_t b) { return scratch_round(b); }
     va_status reserve(size_t total);
+    // after the carves: they stayed within the `reserved` bytes (a planning mistake is an error,
+    // not an out-of-bounds carve)
+    va_status verify(size_t reserved) const {
+        if (off > reserved)
+            return fail(ctx, VA_ERR_HIP, "scratch carves of %zu bytes exceed the %zu reserved", off, reserved);
+        return VA_OK;
+    }
     template <typename T>
     T* carve(size_t count) {
         size_t b = round(count * sizeof(T));
@@ -273,17 +281,6 @@ enum DistOut : int {
     OUT_ARGMIN = 3,  // best[q] = min over rows of (key << 32 | row id) (64-bit atomic min)
 };
 
-// IVF threshold sample: a prefix of every probed list (rows are in insertion order, so a prefix
-// is an unbiased subset) of at least 1/64 of its rows and at least 128 rows.  Every list is
-// sampled at rate >= 1/64, so a query's candidate count stays within about 64 x k; the floor
-// keeps small lists' sample tiles full.
-constexpr uint32_t kIvfSampleRate = 64;
-constexpr uint32_t kIvfSampleMin = 128;
-VA_HD inline uint32_t ivf_sample_rows(uint32_t n) {
-    const uint32_t s = (n + kIvfSampleRate - 1) / kIvfSampleRate;
-    const uint32_t m = s > kIvfSampleMin ? s : kIvfSampleMin;
-    return n < m ? n : m;
-}
 
 // A device-planned list-major launch (IVF): tiles of TQ queries x TN rows over the lists of one
 // tile shape, enumerated by pre[] (the exclusive prefix over the lists of their tile counts for
@@ -476,13 +473,6 @@ uint32_t ivf_num_lists(const va_ivf* ivf);
 
 // Plan of the sampled scan: S sample rows (every stride-th row), candidate capacity per query,
 // queries per sample launch; direct = the database is small enough for dense keys.
-struct ScanPlan {
-    uint64_t S = 0;
-    bool direct = false;
-    uint32_t stride = 1;
-    uint64_t cap = 0;
-    uint32_t qs = 1;
-};
 // The order statistic of the sample that becomes a query's threshold (k, or a smaller rank whose
 // lists are checked before use; va_scan.hip)
 uint32_t sample_rank(const va_context* ctx, uint32_t k, uint64_t S, uint32_t N, bool masked);

@@ -649,45 +649,9 @@ __global__ __launch_bounds__(256, 1) void ivf16_wide_kernel(Ivf16Args a) {
     }
 }
 
-// Tile shapes of the list-major scan.  A tile of wq x wn waves covers 32*wq queries x 128*wn
-// rows.  A list with nq probing queries and n rows gets the shape with the least estimated
-// time: tiles x waves x the measured cost of one wave tile (32 x 128) in that shape on MI355X
-// (shapes with more waves share their LDS stages across more MFMA work and run more workgroups
-// per CU, except 1 x 4, whose 87 KB of LDS leaves one workgroup per CU).  The one- and two-wave
-// shapes keep lists with few queries or few rows from paying for a 4-wave tile.  Group
-// kSmallGroup is the 16-query tiles of ivf_small_kernel.
-constexpr int kShapes = 5;
-constexpr int kSmallGroup = kShapes;
-constexpr int kGroups = kShapes + 1;
-__host__ __device__ inline int shape_wq(int s) { return s == 0 ? 4 : (s <= 2 ? 2 : 1); }
-__host__ __device__ inline int shape_wn(int s) { return s == 1 ? 2 : (s == 4 ? 4 : 1); }
-__host__ __device__ inline uint32_t shape_cost(int s) {
-    return s == 0 ? 100u : s == 1 ? 120u : s == 2 ? 135u : s == 3 ? 175u : 195u;  // per wave tile, relative
-}
-__host__ __device__ inline int shape_for(uint32_t nq, uint32_t nrows) {
-    int best = 0;
-    uint64_t best_cost = ~0ull;
-    for (int i = 0; i < kShapes; ++i) {
-        const uint32_t wq = uint32_t(shape_wq(i)), wn = uint32_t(shape_wn(i));
-        const uint64_t cost = uint64_t((nq + 32 * wq - 1) / (32 * wq)) * ((nrows + 128 * wn - 1) / (128 * wn)) *
-                              (wq * wn) * shape_cost(i);
-        if (cost < best_cost) {
-            best = i;
-            best_cost = cost;
-        }
-    }
-    return best;
-}
-constexpr uint32_t kSmallListQueries = 16;
-__host__ __device__ inline void group_tile(int g, uint32_t& TQ, uint32_t& TN) {
-    if (g == kSmallGroup) {
-        TQ = ivfs::TQ;
-        TN = ivfs::TN;
-    } else {
-        TQ = 32u * uint32_t(shape_wq(g));
-        TN = 128u * uint32_t(shape_wn(g));
-    }
-}
+// Tile shapes and their cost model: shape_for / group_tile (va_plan.hpp, shared with the host
+// planning tests).
+static_assert(ivfs::TQ == kSmallTileQueries && ivfs::TN == kSmallTileRows, "16-query tile of ivf_small_kernel");
 
 // ---- device plan of a list-major search ----------------------------------------------------
 // From the probes alone, on the device: every (query, list) pair once (a list probed twice by a
@@ -1128,12 +1092,9 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
     // the bound's width of tau_q, several times as many on long lists (configs[4]: up to ~16,000
     // for k = 10 against ~640 exact); the capacity is the fp32 scan's plus 7x it (at most 16,384
     // of it per 7): queries that outgrow it take the device fallback.
-    const uint64_t cap32 = std::max<uint64_t>(3ull * k, uint64_t(k) + 32) * kIvfSampleRate + 1024;
-    uint64_t cap = ctx->opt_candidate_cap ? ctx->opt_candidate_cap : cap32 + 7 * std::min<uint64_t>(cap32, 16384);
-    cap = std::max<uint64_t>(1, std::min<uint64_t>(cap, ivf->top_rows[npc]));
+    const uint64_t cap = ivf_screen_cap(ctx->opt_candidate_cap, k, ivf->top_rows[npc]);
     const uint64_t cand = std::max(cap_s, cap);
-    const uint64_t rcap = std::max<uint64_t>(
-        1, std::min<uint64_t>(ivf->top_rows[npc], (std::max<uint64_t>(2ull * k + 256, cap / 4) + 127) / 128 * 128));
+    const uint64_t rcap = ivf_rerank_cap(k, cap, ivf->top_rows[npc]);
     const uint64_t pairs = uint64_t(Q) * np;
     const uint32_t id_span = uint32_t(std::min<uint64_t>(ivf->id_end, 0xFFFFFFFFull));
     const Bound bnd = make_bound(D);
@@ -1182,6 +1143,7 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
     fb.n_rows = ovf_cnt;
     fb.rows = ovf_rows;
     fb.skip = skip;
+    VA_CHECK_STATUS(s.verify(need));
     uint32_t* chi = reinterpret_cast<uint32_t*>(cdot);
     auto bounds = [&](uint64_t cp) -> va_status {
         const uint32_t bx = uint32_t(std::min<uint64_t>(4, (cp + 255) / 256));
@@ -1497,9 +1459,7 @@ va_status ivf_scan_masked(va_context* ctx, const va_ivf* ivf, const float* queri
     // queries that outgrow cap are finished by the device fallback.
     const uint32_t npc = std::min(np, C);
     const uint64_t cap_s = std::max<uint64_t>(1, ivf->top_sample[npc]);
-    uint64_t cap = ctx->opt_candidate_cap ? ctx->opt_candidate_cap
-                                          : std::max<uint64_t>(3ull * k, uint64_t(k) + 32) * va::kIvfSampleRate + 1024;
-    cap = std::max<uint64_t>(1, std::min<uint64_t>(cap, ivf->top_rows[npc]));
+    const uint64_t cap = va::ivf_fp32_cap(ctx->opt_candidate_cap, k, ivf->top_rows[npc]);
     const uint64_t cand = std::max(cap_s, cap);
     const uint64_t pairs = uint64_t(Q) * np;
     // the fallback's tie-id histogram covers the ids of the index
@@ -1536,6 +1496,7 @@ va_status ivf_scan_masked(va_context* ctx, const va_ivf* ivf, const float* queri
     fb.n_rows = ovf_cnt;
     fb.rows = ovf_rows;
     fb.skip = skip;
+    VA_CHECK_STATUS(s.verify(need));
 
     va::ScanPhaseMarks pm(ctx);
     ctx->last_scan = va_scan_timings{};

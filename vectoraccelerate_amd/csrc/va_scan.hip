@@ -23,10 +23,6 @@
 
 namespace va {
 
-namespace {
-constexpr uint32_t kMinSample = 16384;
-}  // namespace
-
 __global__ void mask_dense_kernel(uint32_t* keys, uint32_t cols, int64_t ld, uint32_t row0, uint32_t stride,
                                   const uint8_t* __restrict__ skip) {
     uint32_t* k = keys + int64_t(blockIdx.y) * ld;
@@ -79,35 +75,17 @@ va_status mask_list_keys(va_context* ctx, uint32_t* keys, uint32_t* keys2, const
 }
 
 bool fb_fits(const va_context* ctx, size_t need, uint32_t rows, uint32_t N, uint32_t k) {
-    return !ctx->fixed_scratch || need + fb_bytes(rows, N, k) <= ctx->fixed_scratch_bytes;
+    return fb_fits_in(ctx->fixed_scratch ? ctx->fixed_scratch_bytes : 0, need, rows, N, k);
 }
 
 size_t dense_budget(const va_context* ctx) {
-    constexpr size_t kArena = 256ull << 20;
-    return ctx->fixed_scratch ? std::min(kArena, ctx->fixed_scratch_bytes / 4) : kArena;
+    return dense_budget_for(ctx->fixed_scratch ? ctx->fixed_scratch_bytes : 0);
 }
 
+// (The screened scan took N/32 sample rows while its threshold was the sample's k-th bound; with
+// the checked smaller rank N/64 is faster there too: configs[1] 3.98 -> 3.84 ms per search.)
 ScanPlan plan_scan(const va_context* ctx, uint32_t Q, uint32_t N, uint32_t k) {
-    ScanPlan p;
-    // Sample size: N/64 rows, so that a threshold at the sample's r-th key keeps ~64r candidates
-    // per query (sample_rank); the dense sample costs Q*S keys, so it is capped at dense_budget()
-    // bytes of keys in total (16384 rows minimum).  (The fp16 screening scan took N/32 while its
-    // threshold was the sample's k-th bound; with the checked smaller rank N/64 is faster there too:
-    // configs[1] 3.98 -> 3.84 ms per search.)
-    const uint64_t budget = dense_budget(ctx);
-    p.S = ctx->opt_sample_rows
-              ? ctx->opt_sample_rows
-              : std::max<uint64_t>(kMinSample, std::min<uint64_t>(N / 64, budget / 4 / Q));
-    p.direct = p.S >= N;
-    if (p.direct) return p;
-    p.stride = uint32_t(N / p.S);
-    const uint64_t ratio = (uint64_t(N) + p.S - 1) / p.S;
-    uint64_t cap = ctx->opt_candidate_cap ? ctx->opt_candidate_cap
-                                          : std::max<uint64_t>(3ull * k, uint64_t(k) + 32) * ratio + 1024;
-    cap = std::min<uint64_t>(cap, N);
-    p.cap = (cap + 63) & ~uint64_t(63);
-    p.qs = uint32_t(std::max<uint64_t>(1, std::min<uint64_t>(Q, budget / (p.S * 4))));
-    return p;
+    return plan_scan_for(dense_budget(ctx), ctx->opt_sample_rows, ctx->opt_candidate_cap, Q, N, k);
 }
 
 va_status rescan_rows(va_context* ctx, KeyProducer& kp, uint32_t N, uint32_t k, const SelectArgs& base,
@@ -176,25 +154,12 @@ va_status rescan_rows(va_context* ctx, KeyProducer& kp, uint32_t N, uint32_t k, 
     return VA_OK;
 }
 
-// The order statistic of the sample that becomes a query's threshold.  The k-th smallest
-// sample key bounds the k-th smallest key of the whole database, so it leaves at least k
-// candidates; with r < k the filter keeps about r·N/S rows instead of k·N/S, and a query is
-// short of k candidates exactly when r of its k nearest rows are in the sample (then the
-// select lists it for the exact fallback).  Treating the strided sample as a random one, that
-// count is Binomial(k, S/N) ~ Poisson(k·S/N); r is the smallest rank whose tail P(>= r) is
-// below 1e-4.  A deletion mask keeps rank k: the candidate count would include masked rows.
+// The order statistic of the sample that becomes a query's threshold (sample_rank_for): with
+// r < k the filter keeps about r N / S rows instead of k N / S, and a query is short of k
+// candidates exactly when r of its k nearest rows are in the sample (then the select lists it for
+// the exact fallback).
 uint32_t sample_rank(const va_context* ctx, uint32_t k, uint64_t S, uint32_t N, bool masked) {
-    if (masked || k <= 1) return k;
-    if (ctx->opt_sample_rank) return uint32_t(std::min<uint64_t>(ctx->opt_sample_rank, k));
-    const double lam = double(k) * double(S) / double(N);
-    double term = std::exp(-lam), cdf = term;  // P(X = r - 1), P(X <= r - 1)
-    uint32_t r = 1;
-    while (r < k && 1.0 - cdf > 1e-4) {
-        term *= lam / double(r);
-        cdf += term;
-        ++r;
-    }
-    return r;
+    return sample_rank_for(ctx->opt_sample_rank, k, S, N, masked);
 }
 
 va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t N, uint32_t k,
@@ -244,12 +209,10 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
     const uint32_t stride = plan.stride;
     const uint64_t cap = plan.cap;
     const uint32_t rank = sample_rank(ctx, k, S, N, out.skip != nullptr);
-    const uint64_t per_q_sample = S * 4;
     const uint32_t qs = plan.qs;
 
     Scratch s(ctx);
-    size_t need = Scratch::round(uint64_t(Q) * 4) * 3 + Scratch::round(uint64_t(Q) * cap * 4) * 2 +
-                  Scratch::round(256) + Scratch::round(uint64_t(qs) * per_q_sample);
+    size_t need = exact_scan_need(Q, plan);
     // overflowed rows are finished on the device (no read-back) when the fallback's buffers fit
     const bool device_fb = fb_fits(ctx, need, Q, N, k);
     if (device_fb) need += fb_bytes(Q, N, k);
@@ -268,6 +231,7 @@ va_status exact_topk_scan(va_context* ctx, KeyProducer& kp, uint32_t Q, uint32_t
         fb.rows = ovf_rows;
         fb.skip = out.skip;
     }
+    VA_CHECK_STATUS(s.verify(need));
 
     // ---- 1. sample thresholds -----------------------------------------------------------
     for (uint32_t q0 = 0; q0 < Q; q0 += qs) {

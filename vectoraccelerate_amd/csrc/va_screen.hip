@@ -1428,7 +1428,7 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     const uint32_t rank = sample_rank(ctx, k, S, N, out.skip != nullptr);
     // rerank capacity: k plus the band of rows whose interval straddles the k-th bound (the
     // launch covers only the longest list actually built)
-    const uint64_t rcap = std::min<uint64_t>(N, (std::max<uint64_t>(2ull * k + 256, cap / 4) + 127) / 128 * 128);
+    const uint64_t rcap = screen_rerank_cap(N, k, cap);
     const Bound bnd = make_bound(D);
 
     SelectArgs base;
@@ -1442,11 +1442,7 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     VA_CHECK_STATUS(pm.mark(0));
 
     Scratch s(ctx);
-    const size_t q4 = Scratch::round(uint64_t(Q) * 4);
-    size_t need = q4 * 5 + Scratch::round(256) + Scratch::round(uint64_t(Q) * 16) * 2 +
-                  Scratch::round(uint64_t(Q) * Dp * 2) + Scratch::round(uint64_t(plan.qs) * S * 4) +
-                  Scratch::round(S * 4) + Scratch::round(uint64_t(Q) * cap * 4) * 3 +
-                  Scratch::round(uint64_t(Q) * rcap * 4) * 2;
+    size_t need = screened_scan_need(Q, Dp, plan, rcap);
     // overflowed queries are finished on the device (no read-back) when the fallback's buffers fit
     const bool device_fb = fb_fits(ctx, need, Q, N, k);
     if (device_fb) need += fb_bytes(Q, N, k);
@@ -1474,6 +1470,7 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
         fb.rows = ovf_rows;
         fb.skip = out.skip;
     }
+    VA_CHECK_STATUS(s.verify(need));
 
     // ---- 1. queries -> scaled fp16 ---------------------------------------------------------
     screen_prep_kernel<<<dim3((Q + 3) / 4), dim3(256), 0, ctx->stream>>>(in.q, int64_t(D), Q, D, Dp, qh, qinfo,
