@@ -39,6 +39,8 @@ struct FbArgs {
     uint32_t* lkey = nullptr;          // [rmax][cap]
     uint32_t* lid = nullptr;           // [rmax][cap]
     uint32_t* done = nullptr;          // [8] completion tickets, one per pass
+    uint32_t grid = kFbGrid;           // workgroups per pass (fewer for a few rows: each launch that
+                                       // finds nothing overflowed still costs its dispatch)
     const uint8_t* skip = nullptr;     // excluded rows: their keys are kAbsentKey
 };
 enum FbState : int { FB_PREFIX = 0, FB_NEED = 1, FB_K = 2, FB_EDGE = 3, FB_OVF = 4 };
@@ -58,6 +60,7 @@ inline FbArgs fb_carve(Scratch& s, uint32_t rmax, uint32_t N, uint32_t k, uint32
     a.lkey = s.carve<uint32_t>(uint64_t(rmax) * a.cap);
     a.lid = s.carve<uint32_t>(uint64_t(rmax) * a.cap);
     a.done = s.carve<uint32_t>(8);
+    a.grid = rmax <= 64 ? 256u : kFbGrid;
     return a;
 }
 
@@ -234,27 +237,27 @@ struct SmallChain {
 // with a VALU chain per lane.  The rows move in coalesced groups of 32 values: load instruction i
 // of a group brings rows 8i .. 8i + 7 (lane L: row 8i + L / 8, 16-byte chunk L % 8, whole 128-byte
 // lines), the wave's LDS slot (8 KiB, chunk c of row r at c ^ ((r >> 1) & 7): conflict-free
-// reads) turns them into rows, and lane l reads its own row's 32 values.  Groups j + 1 and j + 2
-// are in flight (registers) while group j computes.  feed(j, xv, qv) runs the lane's chain on
-// group j.  Needs D % 4 == 0 and 16-byte aligned rows and query.
-template <class Feed>
+// reads) turns them into rows, and lane l reads its own row's 32 values.  Groups j + 1 .. j + R
+// are in flight (registers) while group j computes (R groups in all).  feed(j, xv, qv) runs the
+// lane's chain on group j.  Needs D % 4 == 0 and 16-byte aligned rows and query.
+template <int R = 2, class Feed>
 __device__ inline void rows_through_lds(const float* q, const float* x, const uint32_t (&rid)[8],
                                         const bool (&rvalid)[8], uint32_t D, fb_f32x4* slot, Feed&& feed) {
     const int lane = threadIdx.x & 63;
     const int ck = lane & 7;
     const uint32_t ng = (D + 31) / 32;
-    fb_f32x4 ga[8], gb[8];
-    auto load = [&](uint32_t j, fb_f32x4(&g)[8]) {
+    fb_f32x4 g[R][8];
+    auto load = [&](uint32_t j, fb_f32x4(&gr)[8]) {
         const uint32_t d = 32 * j + 4 * uint32_t(ck);
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            g[i] = valu_load4<true>(rvalid[i] ? x + int64_t(rid[i]) * D : nullptr, d, D);
+            gr[i] = valu_load4<true>(rvalid[i] ? x + int64_t(rid[i]) * D : nullptr, d, D);
     };
-    auto stash = [&](const fb_f32x4(&g)[8]) {
+    auto stash = [&](const fb_f32x4(&gr)[8]) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int r = 8 * i + (lane >> 3);
-            slot[r * 8 + (ck ^ ((r >> 1) & 7))] = g[i];
+            slot[r * 8 + (ck ^ ((r >> 1) & 7))] = gr[i];
         }
     };
     auto run = [&](uint32_t j) {
@@ -266,16 +269,17 @@ __device__ inline void rows_through_lds(const float* q, const float* x, const ui
         }
         feed(j, xv, qv);
     };
-    load(0, ga);
-    if (ng > 1) load(1, gb);
-    for (uint32_t j = 0; j < ng; j += 2) {
-        stash(ga);
-        if (j + 2 < ng) load(j + 2, ga);
-        run(j);
-        if (j + 1 >= ng) break;
-        stash(gb);
-        if (j + 3 < ng) load(j + 3, gb);
-        run(j + 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        if (uint32_t(r) < ng) load(uint32_t(r), g[r]);
+    for (uint32_t j = 0; j < ng; j += R) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (j + r >= ng) break;
+            stash(g[r]);
+            if (j + r + R < ng) load(j + r + R, g[r]);
+            run(j + r);
+        }
     }
 }
 
@@ -545,7 +549,7 @@ __global__ __launch_bounds__(256) void fb_init_kernel(FbArgs a);
 
 template <class P>
 va_status fb_launch_pass(va_context* ctx, const P& p, const FbArgs& a, int pass) {
-    fb_pass_kernel<P><<<dim3(kFbGrid), dim3(256), 0, ctx->stream>>>(p, a, pass);
+    fb_pass_kernel<P><<<dim3(a.grid), dim3(256), 0, ctx->stream>>>(p, a, pass);
     VA_CHECK_LAUNCH(ctx);
     return VA_OK;
 }

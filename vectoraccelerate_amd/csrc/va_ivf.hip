@@ -1047,9 +1047,9 @@ va_status ivf_fallback(va_context* ctx, const va_ivf* ivf, const float* queries,
                      (reinterpret_cast<uintptr_t>(ivf->list_vectors) & 15) == 0;
     for (int pass = 0; pass < kFbPasses; ++pass) {
         if (vec)
-            fb_ivf_pass_kernel<true><<<dim3(kFbGrid), dim3(256), 0, ctx->stream>>>(v, fb, pass);
+            fb_ivf_pass_kernel<true><<<dim3(fb.grid), dim3(256), 0, ctx->stream>>>(v, fb, pass);
         else
-            fb_ivf_pass_kernel<false><<<dim3(kFbGrid), dim3(256), 0, ctx->stream>>>(v, fb, pass);
+            fb_ivf_pass_kernel<false><<<dim3(fb.grid), dim3(256), 0, ctx->stream>>>(v, fb, pass);
         VA_CHECK_LAUNCH(ctx);
     }
     return fb_select(ctx, fb, base, 32);

@@ -1236,13 +1236,18 @@ __global__ __launch_bounds__(256) void screen_compact_kernel(const uint32_t* __r
 // sequence on the VALU (GemmChain: the fmaf chain every element of the scan's MFMA block follows),
 // so every key equals the fp32 scan's.  The rows pass through the wave's LDS slot in coalesced
 // 128-byte lines (rows_through_lds).  Needs D % 4 == 0 and 16-byte aligned rows and queries.
+template <int R, bool QLDS>
 __global__ __launch_bounds__(256) void rerank_kernel(const float* __restrict__ q, const float* __restrict__ x,
                                                      uint32_t D, int op, const uint32_t* __restrict__ rr,
                                                      const uint32_t* __restrict__ rcount, uint32_t rcap, uint32_t Q,
                                                      uint32_t* __restrict__ rkey) {
     __shared__ fb_f32x4 slots[4][64 * 8];
+    // QLDS: each wave's query staged in LDS (dynamic, 4 x D4 floats), so that a wave alone on its
+    // rows does not wait on a load of the query's values for every group
+    extern __shared__ __attribute__((aligned(16))) float qstage[];
     const int lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t D4 = (D + 3) & ~3u;
     const uint32_t nch = (rcap + 63) / 64;
     const uint64_t items = uint64_t(Q) * nch;
     const uint32_t nw = gridDim.x * 4;
@@ -1260,9 +1265,17 @@ __global__ __launch_bounds__(256) void rerank_kernel(const float* __restrict__ q
             rv[i] = r < m;
             rid[i] = rv[i] ? rl[r] : 0u;
         }
+        const float* qp = q + int64_t(qi) * D;
+        if constexpr (QLDS) {
+            // (the wave writes and then reads only its own region: in order, no barrier)
+            float* qw = qstage + wave * D4;
+            for (uint32_t d = uint32_t(lane) * 4; d < D; d += 256)
+                *reinterpret_cast<fb_f32x4*>(qw + d) = *reinterpret_cast<const fb_f32x4*>(qp + d);
+            qp = qw;
+        }
         GemmChain ch;
-        rows_through_lds(q + int64_t(qi) * D, x, rid, rv, D, slots[wave],
-                         [&](uint32_t j, const fb_f32x4(&xv)[8], const fb_f32x4(&qv)[8]) { ch.group(xv, qv, j, D); });
+        rows_through_lds<R>(qp, x, rid, rv, D, slots[wave],
+                            [&](uint32_t j, const fb_f32x4(&xv)[8], const fb_f32x4(&qv)[8]) { ch.group(xv, qv, j, D); });
         if (uint32_t(lane) < m) rkey[int64_t(qi) * rcap + c * 64 + lane] = ch.key(op);
     }
 }
@@ -1400,13 +1413,24 @@ va_status screen_compact(va_context* ctx, const uint32_t* cnt, const uint32_t* c
     return VA_OK;
 }
 
+// The plan of a screened search: plan_scan's, except that small batches over the fp16 shadow
+// sample N/256 rows (at least 4096): for them the sample and its per-row selection are a visible
+// share of a search that streams the shadow once, while the screen's band, not the sample's
+// threshold, sets the rerank.
+ScanPlan screen_plan(const va_context* ctx, const ScreenInput& in, uint32_t k) {
+    if (in.xh && in.Q <= kSmallBatchMax && !ctx->opt_sample_rows)
+        return plan_scan_for(dense_budget(ctx), std::max<uint64_t>(4096, in.N / 256), ctx->opt_candidate_cap, in.Q,
+                             in.N, k);
+    return plan_scan(ctx, in.Q, in.N, k);
+}
+
 bool screen_applies(const va_context* ctx, const ScreenInput& in, uint32_t k) {
     if (ctx->opt_screen == 1) return false;
     if (in.op != OP_L2SQ && in.op != OP_L2 && in.op != OP_COS_DIST && in.op != OP_NEG_DOT) return false;
     if (in.D % 4 != 0 || (reinterpret_cast<uintptr_t>(in.x) & 15) != 0 ||
         (reinterpret_cast<uintptr_t>(in.q) & 15) != 0)
         return false;
-    const ScanPlan plan = plan_scan(ctx, in.Q, in.N, k);
+    const ScanPlan plan = screen_plan(ctx, in, k);
     if (plan.direct) return false;
     if (!offsets_fit(uint64_t(plan.stride) * in.D, in.D)) return false;
     if (ctx->opt_screen == 2) return true;
@@ -1420,7 +1444,7 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
                              const ScanOutputs& out) {
     const uint32_t Q = in.Q, N = in.N, D = in.D;
     const uint32_t Dp = padded_dim(D);
-    const ScanPlan plan = plan_scan(ctx, Q, N, k);
+    const ScanPlan plan = screen_plan(ctx, in, k);
     const uint64_t S = plan.S;
     const uint64_t cap = plan.cap;
     // the threshold: the sample's rank-th smallest upper bound (checked in the compaction when
@@ -1594,8 +1618,15 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     {
         const uint64_t items = uint64_t(Q) * ((rcap + 63) / 64);
         const uint32_t blocks = uint32_t(std::min<uint64_t>(2048, (items + 3) / 4));
-        rerank_kernel<<<dim3(blocks), dim3(256), 0, ctx->stream>>>(in.q, in.x, D, int(in.op), rr, rcount,
-                                                                   uint32_t(rcap), Q, rkey);
+        // small batches keep few waves busy, each on its own: the query staged in LDS and four row
+        // groups in flight per wave instead of two
+        const size_t qlds = size_t(4) * ((D + 3) & ~3u) * 4;
+        if (Q <= kSmallBatchMax && qlds <= 64 * 1024)
+            rerank_kernel<4, true><<<dim3(blocks), dim3(256), qlds, ctx->stream>>>(in.q, in.x, D, int(in.op), rr,
+                                                                                  rcount, uint32_t(rcap), Q, rkey);
+        else
+            rerank_kernel<2, false><<<dim3(blocks), dim3(256), 0, ctx->stream>>>(in.q, in.x, D, int(in.op), rr,
+                                                                                rcount, uint32_t(rcap), Q, rkey);
         VA_CHECK_LAUNCH(ctx);
         VA_CHECK_STATUS(mask_list_keys(ctx, rkey, nullptr, rr, rcount, Q, uint32_t(rcap), int64_t(rcap), out.skip));
     }
