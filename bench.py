@@ -76,6 +76,8 @@ COUNTERS_IVF = {"2x2 tiles": "profiles/counters__ivf_list_scan_2x2__configs4_ivf
                 "4x1 tiles": "profiles/counters__ivf_list_scan_4x1__configs4_ivfflat_top10.txt",
                 "16-query tiles": "profiles/counters__ivf_small_tiles__configs4_ivfflat_top10.txt"}
 COUNTERS_PQ = "profiles/counters__pq_adc_filter__10Mx16codes_K256_Q1024.txt"
+COUNTERS_SMALL = "profiles/counters__screen16_small_filter__1Mx768_l2_top10.txt"
+CEILING_PROFILE = "profiles/mfma_ceiling__probe_fp32_fp16_int8_fp4.txt"
 
 
 def counters(rel: str) -> dict:
@@ -173,7 +175,7 @@ def with_ceiling(roof: dict, ceil: dict | None, name: str) -> dict:
     m = ceil[name]["random"]["rate"]
     roof["measured_ceiling"] = {"instruction": name, "rate": m, "operands": "random",
                                 "engine_mhz": ceil[name]["random"]["engine_mhz"],
-                                "frac_of_measured": roof["achieved"] / m}
+                                "frac_of_measured": roof["achieved"] / m, "profile": CEILING_PROFILE}
     return roof
 
 
@@ -224,7 +226,8 @@ def run_small_batches(ctx, a, ix, qpool, metric: int, k: int, label: str):
                          "frac": gbs_scan / PEAK["hbm_gbs"], "kernel": "screen16_small_kernel (screen pass)",
                          "algorithmic": f"the fp16 shadow read once: N*D*2 = {shadow_bytes:.4g} B per search",
                          "whole_search_gbs": gbs_search, "whole_search_frac": gbs_search / PEAK["hbm_gbs"],
-                         "whole_search_over_roofline": ms / (shadow_bytes / (PEAK["hbm_gbs"] * 1e9) * 1e3)},
+                         "whole_search_over_roofline": ms / (shadow_bytes / (PEAK["hbm_gbs"] * 1e9) * 1e3),
+                         **(counted(COUNTERS_SMALL) if Q <= 32 else {})},
         }
         log(f"{label} Q={Q}: {ms:.3f} ms/search = {Q / (ms * 1e-3):.0f} QPS (fp32 scan only {ms32:.3f} ms); screen "
             f"pass {scan_ms:.3f} ms = {gbs_scan:.0f} GB/s ({100 * gbs_scan / PEAK['hbm_gbs']:.1f}% HBM); whole "
