@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define VA_HIP_ABI_VERSION 4
+#define VA_HIP_ABI_VERSION 5
 #define VA_SENTINEL_INDEX 0xFFFFFFFFu
 /* largest k accepted by the top-K entry points */
 #define VA_MAX_K 1024u

@@ -49,7 +49,7 @@ def test_binding_types_every_declared_symbol():
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.va_abi_version() == 4
+    assert lib.va_abi_version() == 5
     assert lib.va_status_string(0) == b"ok"
     assert lib.va_status_string(1) == b"invalid argument"
 
