@@ -67,7 +67,7 @@ def log(msg: str) -> None:
 COUNTERS_SCREEN16 = "profiles/counters__screen16_filter__configs1_cosine_top100.txt"
 COUNTERS_SCREEN = "profiles/counters__screen_filter__configs1_cosine_top100.txt"
 COUNTERS_FP32 = "profiles/counters__dist_gemm_filter__configs1_cosine_top100.txt"
-COUNTERS_I8 = "profiles/counters__i8_resq_filter__configs2_int8_top10.txt"
+COUNTERS_I8 = "profiles/counters__i8_resq16_filter__configs2_int8_top10.txt"
 COUNTERS_HAMMING = "profiles/counters__hamming_mfma_filter__configs3_binary_top100.txt"
 COUNTERS_IVF16 = {"64-query tiles": "profiles/counters__ivf16_wide64__configs4_ivfflat_top10.txt",
                   "32-query tiles": "profiles/counters__ivf16_wide32__configs4_ivfflat_top10.txt",
@@ -495,7 +495,7 @@ def run_c3(ctx, a, cpu: bool):
         "quantize_database_ms": qms,
         "quantize_hbm_gbs": (N * D * 4 * 2 + N * D) / (qms * 1e-3) / 1e9,
         "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK["int8_mfma_tops"], "unit": "TOP/s",
-                     "frac": tops / PEAK["int8_mfma_tops"], "kernel": "i8_resq_kernel<512, true>",
+                     "frac": tops / PEAK["int8_mfma_tops"], "kernel": "i8_resq16_kernel<512, 16, 4>",
                      "algorithmic": f"2*Q*N*D = {ops:.4g} int ops per launch", **counted(COUNTERS_I8)},
     }
     log(f"configs[2] int8 top-10: {ms:.3f} ms/step = {res['qps']:.0f} QPS; scan {ph['scan_ms']:.3f} ms = "

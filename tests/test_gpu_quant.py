@@ -145,7 +145,11 @@ def test_global_quantize_matches_oracle_and_fixture(ctx, oracle):
                                      # large-Q tiles (256 queries x 128 rows): ragged Q and N,
                                      # several 64-byte stages, a partial last stage, one-stage D
                                      (257, 3001, 512, 10), (450, 20000, 160, 50), (1000, 7000, 1024, 5),
-                                     (513, 129, 16, 3)])
+                                     (513, 129, 16, 3),
+                                     # resident query blocks on the 16x16x64 MFMA (256 queries at
+                                     # d = 256 and 512, 128 at 768 and 1024): ragged blocks, rows past
+                                     # N inside a wave's rows, ranges of several tiles
+                                     (600, 7001, 768, 10), (193, 50000, 256, 3), (2000, 12011, 512, 10)])
 def test_i8_scan_topk_bit_exact(ctx, oracle, Q, N, D, k):
     from vectoraccelerate_amd import ScalarQuantizationKernel
 
@@ -158,7 +162,8 @@ def test_i8_scan_topk_bit_exact(ctx, oracle, Q, N, D, k):
     check_topk_exact(gi, gd, oi, od)
 
 
-@pytest.mark.parametrize("Q,N,D,k", [(300, 6000, 96, 20), (260, 4000, 512, 10), (700, 3000, 256, 40)])
+@pytest.mark.parametrize("Q,N,D,k", [(300, 6000, 96, 20), (260, 4000, 512, 10), (700, 3000, 256, 40),
+                                     (300, 5000, 768, 30), (1100, 2500, 1024, 64)])
 def test_i8_large_q_many_passes(ctx, oracle, Q, N, D, k):
     """Large-Q filter scan where every query has hundreds of tied passes (the database is 40
     distinct rows repeated): each wave stages and flushes many batches of passes, and ties are
@@ -233,6 +238,35 @@ def test_i8_large_q_overflow_rescan(ctx, oracle):
     check_topk_exact(gi, gd, oi, od)
     assert gi[5, 0] == 17
     assert t["overflow_rows"] > 192
+
+
+@pytest.mark.parametrize("D", [128, 512])
+def test_i8_large_q_overflow_rescan_resident_blocks(ctx, oracle, D):
+    """The overflow path behind both resident-query scans (d = 128: 256-query blocks on the
+    32x32x32 MFMA; d = 512: 256-query blocks on the 16x16x64 MFMA): a tiny candidate cap sends
+    most queries to the device-side exact fallback."""
+    from vectoraccelerate_amd import ScalarQuantizationKernel, _lib
+
+    g = rng(23 + D)
+    qc = g.integers(-128, 128, (450, D)).astype(np.int8)
+    xc = g.integers(-128, 128, (30000, D)).astype(np.int8)
+    qc[7] = xc[29999]
+    oi, od = oracle.i8_topk(qc, xc, 16)
+    try:
+        ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 20)
+        ctx.set_option(_lib.VA_OPT_SAMPLE_ROWS, 2500)
+        ctx.set_option(_lib.VA_OPT_SAMPLE_RANK, 2**32)
+        ctx.set_profiling(True)
+        gi, gd = ScalarQuantizationKernel(ctx).searchTopK(qc, xc, 16)
+        t = ctx.last_scan_timings()
+    finally:
+        ctx.set_option(_lib.VA_OPT_CANDIDATE_CAP, 0)
+        ctx.set_option(_lib.VA_OPT_SAMPLE_ROWS, 0)
+        ctx.set_option(_lib.VA_OPT_SAMPLE_RANK, 0)
+        ctx.set_profiling(False)
+    check_topk_exact(gi, gd, oi, od)
+    assert gi[7, 0] == 29999
+    assert t["overflow_rows"] > 128
 
 
 def test_c3_pipeline_small(ctx, oracle):

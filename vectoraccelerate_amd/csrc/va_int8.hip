@@ -910,6 +910,259 @@ __global__ __launch_bounds__(512, 2) void i8_resq_kernel(I8Args a, uint32_t R) {
     flush();
 }
 
+// ---- resident queries on the 16x16x64 MFMA, rows straight into registers ----------------------
+// The filter scan for d = 256, 512, 768 and 1024.  A workgroup (8 waves, one per CU) holds TQ
+// queries in LDS (256 at d <= 512, 128 above) and streams a range of 256-row tiles past them; a
+// wave's part of a tile is 32 database rows x the TQ queries = 2 x TQ/16 blocks of
+// v_mfma_i32_16x16x64_i8.  Its rows go from global memory straight into a ring of R register
+// slots (one 64-byte k-step of its 32 rows each; R = 4 at d <= 512, a whole tile of d / 64
+// k-steps above): the slot a k-step consumed is refilled at once, R - 1 k-steps ahead, and no
+// LDS write, wait or barrier sits between a load and its MFMA.  LDS carries the query fragments
+// (each read once per k-step and used by two MFMAs).  Load and fragment map: lane (r, g) =
+// (lane % 16, lane / 16) holds bytes 64 t + 16 g .. + 15 of row r of a row block (and of query r
+// of a query block) at k-step t, so the four lanes of a row read 64 contiguous bytes per
+// instruction, and both operands pair the same d.  Rows past N, and the loads past a wave's
+// last tile, use an offset beyond the descriptor's range (zeros; every lane's offset carries its
+// row, so this does not depend on whether the range check includes the scalar column offset).
+// Measured on one box against the kernels it replaced (Q = 4096, random int8 rows, scan time):
+// d = 512 15.6 ms against i8_resq_kernel's 19.9 (0.53 of the int8 peak), d = 256 8.2 against
+// 10.7, d = 768 and 1024 18.4 and 18.3 against i8_dma_kernel's 22.2 and 22.7.  What moved it:
+// the bytes each CU pulls from L2 per MFMA (a row fetched once per 256 queries instead of 128:
+// 18.5 -> 15.6 ms at d = 512) and loads kept in flight (the register ring).  What did not:
+// cutting the LDS bytes per MFMA to a third (64-row wave tiles), 16-row wave tiles, two
+// workgroups per CU, 192 resident queries at d = 768 (blocks of 192 do not tile 256 CUs).
+namespace resq16 {
+constexpr int NW = 8, MB = 2;  // waves, row blocks of 16 per wave
+constexpr int WR = 16 * MB;    // rows per wave
+constexpr int TN = NW * WR;    // rows per tile
+constexpr int TQMAX = 256;     // resident queries at most
+constexpr int LCAP = 80;       // staged passes per wave
+constexpr int STAGE = NW * LCAP * 12;
+template <int QS, int NQB>
+constexpr int lds_bytes() { return 16 * NQB * QS + STAGE; }
+}  // namespace resq16
+
+// QS = D, a multiple of 256; NQB query blocks of 16 (TQ = 16 NQB resident queries); a ring of
+// R k-steps, R dividing the tile's D / 64.
+template <int QS, int NQB, int R>
+__global__ __launch_bounds__(512, 2) void i8_resq16_kernel(I8Args a, uint32_t NR) {
+    using namespace resq16;
+    static_assert((QS / 64) % R == 0, "the ring's slots must repeat tile by tile");
+    constexpr int TQ = 16 * NQB;
+    constexpr int CS = TQ * 16;  // bytes per 16-byte chunk column of the resident queries
+    constexpr int QBYTES = TQ * QS;
+    constexpr int CPR = QS / 16;  // 16-byte chunks per resident query row
+    extern __shared__ __attribute__((aligned(16))) char lds8[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, r16 = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    // Workgroup w runs on XCD w % 8; the query blocks of one range of tiles share an XCD, so
+    // the range comes from HBM about once and from that XCD's L2 for the other blocks.  (Giving
+    // each XCD one range that its streams interleave over, tile by tile, measured 5 % slower.)
+    const uint32_t nqb = (a.Q + TQ - 1) / TQ;
+    const uint32_t xcd = blockIdx.x % kXcds, seq = blockIdx.x / kXcds;
+    const uint32_t qb = seq % nqb;
+    const uint32_t range = (seq / nqb) * kXcds + xcd;
+    const uint32_t ntiles = (a.N + TN - 1) / TN;
+    const uint32_t tpr = (ntiles + NR - 1) / NR;
+    const uint32_t t0 = range * tpr;
+    if (t0 >= ntiles) return;  // the whole workgroup: no range left
+    const uint32_t tcount = min(tpr, ntiles - t0);
+    const uint32_t q0 = qb * TQ;
+    const uint32_t qn = min(uint32_t(TQ), a.Q - q0);
+    const uint32_t lds0 = lds_addr_of(lds8);
+
+    // Resident queries, chunk-major: 16-byte chunk c of query r at c * CS + r * 16 (a query
+    // block's 16 queries read 256 contiguous bytes per lane group).  One load fills one chunk of
+    // 64 consecutive queries; queries past Q load as zeros.
+    {
+        constexpr int G64 = TQ / 64;  // loads per chunk column
+        const dma_rsrc qres = make_dma_rsrc(a.q + int64_t(q0) * a.ldq, uint32_t(int64_t(qn - 1) * a.ldq + a.D));
+        for (int m = wave; m < G64 * CPR; m += NW) {
+            const int row = (m % G64) * 64 + lane;
+            const int c = m / G64;
+            const uint32_t voff = uint32_t(row) < qn ? uint32_t(int64_t(row) * a.ldq) + uint32_t(16 * c) : kDmaSkip;
+            lds_dma16(qres, voff, lds0 + uint32_t(m) * 1024u);
+        }
+    }
+    // A value passes when its dot is >= the query's bound (the threshold key turned back into
+    // an int32 dot); padding queries never pass.
+    int32_t bound[NQB];
+#pragma unroll
+    for (int u = 0; u < NQB; ++u) {
+        const uint32_t ql = uint32_t(u * 16 + r16);
+        const int32_t t = i32_of_key(a.thr[q0 + (ql < qn ? ql : 0u)]);
+        bound[u] = (ql >= qn || t == INT32_MIN) ? INT32_MAX : -t;
+    }
+    wait_vmcnt<0>();
+    __syncthreads();  // resident queries visible; the only workgroup barrier
+
+    // ---- this wave's row stream ---------------------------------------------------------------
+    constexpr uint32_t nst = QS / 64;  // k-steps per tile
+    uint32_t voff[MB];
+#pragma unroll
+    for (int j = 0; j < MB; ++j) voff[j] = uint32_t(16 * j + r16) * uint32_t(a.ldx) + 16u * uint32_t(g);
+    uint32_t ltile = 0, lst = 0;  // tile and k-step of the next load (wave-uniform)
+    // The descriptor covers this wave's rows of the tile being loaded ((rows - 1) strides plus
+    // one row), rebuilt from scalars at every load; a lane's row offset fails its range check
+    // for rows past N.
+    auto load = [&](i32x4v(&dst)[MB]) {
+        // (wave-uniform values; readfirstlane keeps the descriptor in scalar registers where the
+        // compiler's divergence analysis cannot prove it, which would otherwise loop over lanes)
+        const bool ok = ltile < tcount;
+        const uint32_t r0 =
+            __builtin_amdgcn_readfirstlane(ok ? (t0 + ltile) * uint32_t(TN) + uint32_t(wave) * uint32_t(WR) : 0u);
+        const uint32_t rows = __builtin_amdgcn_readfirstlane(ok && r0 < a.N ? min(uint32_t(WR), a.N - r0) : 0u);
+        const uint64_t base = reinterpret_cast<uint64_t>(a.x + int64_t(r0) * a.ldx);
+        const uint64_t bs = (uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(base >> 32)))) << 32) |
+                            uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(base)));
+        const int nrec = __builtin_amdgcn_readfirstlane(rows ? int(int64_t(rows - 1) * a.ldx + a.D) : 0);
+        const __amdgpu_buffer_rsrc_t xres =
+            __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(bs), 0, nrec, 0x00020000);
+        const uint32_t skip = rows ? 0u : kDmaSkip;  // (offsets are below 2^31: OR-ing it in puts them out of range)
+#pragma unroll
+        for (int j = 0; j < MB; ++j)
+            dst[j] = __builtin_bit_cast(
+                i32x4v, __builtin_amdgcn_raw_buffer_load_b128(xres, voff[j] | skip, int(lst * 64u), 0));
+        if (++lst == nst) {
+            lst = 0;
+            ++ltile;
+        }
+    };
+
+    // query block u of k-step t: chunk 4 t + g of query 16 u + r16
+    const char* qrd = lds8 + g * CS + r16 * 16;
+    auto rd_q = [&](uint32_t t, int u) { return *reinterpret_cast<const i32x4v*>(qrd + t * (4 * CS) + u * 256); };
+
+    // acc[u][j]: lane (r16, g) holds query 16 u + r16 against rows 16 j + 4 g + v in value v
+    i32x4v acc[NQB][MB];
+
+    // ---- filter epilogue ----------------------------------------------------------------------
+    uint32_t* s_qi = reinterpret_cast<uint32_t*>(lds8 + QBYTES) + wave * 3 * LCAP;
+    uint32_t* s_key = s_qi + LCAP;
+    uint32_t* s_id = s_key + LCAP;
+    uint32_t lc = 0;  // staged passes (wave-uniform)
+    uint32_t mtile = 0;
+    // Appends the staged passes to the candidate lists: count every pass, keep a query's first
+    // cap.  The reservations are waited for once per 64 entries.
+    auto flush = [&]() {
+        for (uint32_t b0 = 0; b0 < lc; b0 += 64) {
+            const uint32_t e = b0 + uint32_t(lane);
+            if (e < lc) {
+                const uint32_t qi = s_qi[e];
+                const uint32_t pos = atomicAdd(a.cnt + qi, 1u);
+                if (pos < a.cap) {
+                    a.cand_key[int64_t(qi) * a.cap + pos] = s_key[e];
+                    a.cand_id[int64_t(qi) * a.cap + pos] = s_id[e];
+                }
+            }
+        }
+        lc = 0;
+    };
+    // Passes are rare: a lane's 4 MB values of a query block reduced to a maximum and one wave
+    // vote per block, then one vote per value position and a rolled loop over the positions
+    // some lane passes at (wave-uniform, the value picked by a select chain).  Rows past N hold
+    // zero dots and are rejected by their position.
+    auto epilogue = [&]() {
+        const uint64_t r64 = uint64_t(t0 + mtile) * TN + uint32_t(wave) * WR;
+        const uint32_t r0 = uint32_t(r64);  // ids of rows below N fit 32 bits
+        const int32_t lim = int32_t(r64 < a.N ? min(uint64_t(a.N) - r64, uint64_t(WR)) : 0) - 4 * g;
+#pragma unroll
+        for (int u = 0; u < NQB; ++u) {
+            const int32_t b = bound[u];
+            int32_t m = acc[u][0][0];
+#pragma unroll
+            for (int j = 0; j < MB; ++j)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) m = max(m, acc[u][j][v]);
+            if (!__ballot(m >= b)) continue;
+            const uint32_t qi = q0 + uint32_t(u * 16 + r16);
+            uint32_t vm = 0;  // bit 4 j + v: some lane passes there (wave-uniform)
+#pragma unroll
+            for (int j = 0; j < MB; ++j)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) vm |= __ballot(acc[u][j][v] >= b) ? (1u << (4 * j + v)) : 0u;
+#pragma unroll 1
+            while (vm) {
+                const uint32_t p = __builtin_ctz(vm);
+                vm &= vm - 1;
+                int32_t dot = 0;
+#pragma unroll
+                for (int j = 0; j < MB; ++j)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) dot = p == uint32_t(4 * j + v) ? acc[u][j][v] : dot;
+                const uint32_t roff = 16 * (p >> 2) + (p & 3);
+                const bool pass = dot >= b && int32_t(roff) < lim;
+                const uint64_t mk = __ballot(pass);
+                if (!mk) continue;
+                const uint32_t n = uint32_t(__popcll(mk));
+                if (lc + n > uint32_t(LCAP)) flush();  // wave-uniform
+                if (pass) {
+                    const uint32_t e =
+                        lc + __builtin_amdgcn_mbcnt_hi(uint32_t(mk >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mk), 0u));
+                    s_qi[e] = qi;
+                    s_key[e] = key_of_i32(-dot);
+                    s_id[e] = r0 + roff + 4 * uint32_t(g);
+                }
+                lc += n;
+            }
+        }
+    };
+
+    // ---- main loop: groups of R k-steps (a tile is a whole number of groups) -----------------
+    i32x4v xr[R][MB];
+    // four query fragments in turn: block u uses qf[u % 4], refilled after its two MFMAs with
+    // block u + 4 of this k-step or block u + 4 - NQB of the next (eight MFMAs cover the read)
+    constexpr int QF = 4;
+    i32x4v qf[QF];
+    // (in order: the compiler's wait counts follow the issue order, and the first k-step's slot
+    // must be the oldest load in flight)
+#pragma unroll
+    for (int r = 0; r < R - 1; ++r) {
+        load(xr[r]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int u = 0; u < QF; ++u) qf[u] = rd_q(0, u);
+    uint32_t mst = 0;  // k-step within the tile
+    auto mma = [&](const i32x4v(&x)[MB]) {
+        const uint32_t nks = mst + 1 == nst ? 0u : mst + 1;
+#pragma unroll
+        for (int u = 0; u < NQB; ++u) {
+#pragma unroll
+            for (int j = 0; j < MB; ++j)
+                acc[u][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[j], qf[u % QF], acc[u][j], 0, 0, 0);
+            qf[u % QF] = u + QF < NQB ? rd_q(mst, u + QF) : rd_q(nks, u + QF - NQB);
+            __builtin_amdgcn_sched_group_barrier(0x008, MB, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        mst = nks;
+    };
+#pragma unroll
+    for (int u = 0; u < NQB; ++u)
+#pragma unroll
+        for (int j = 0; j < MB; ++j) acc[u][j] = i32x4v{0, 0, 0, 0};
+    for (uint32_t t = 0; t < tcount; ++t) {
+        // The whole ring has landed before a tile starts (its first k-step needs only the oldest
+        // slot): measured 2-4 % faster than waiting slot by slot (d = 512 and 1024).
+        wait_vmcnt<0>();
+#pragma unroll
+        for (int r = 0; r < int(nst); ++r) {
+            load(xr[(r + R - 1) % R]);  // the slot the previous k-step consumed
+            mma(xr[r % R]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        epilogue();
+        ++mtile;
+#pragma unroll
+        for (int u = 0; u < NQB; ++u)
+#pragma unroll
+            for (int j = 0; j < MB; ++j) acc[u][j] = i32x4v{0, 0, 0, 0};
+    }
+    flush();
+}
+
 // The resident-query scan needs dense 16-byte query and database rows, d <= 512, enough
 // queries to fill a 256-query block reasonably, and 32-bit descriptor offsets within a
 // 256-query block and within a wave's 32 rows.
@@ -920,6 +1173,47 @@ bool resq_ok(const I8Args& a, bool vec) {
     return VA_I8_RESQ && vec && !a.qrow && a.Q > 192 && a.D <= 512 && a.N <= 0xFFFFFF00u &&
            uint64_t(resq::TQ - 1) * uint64_t(a.ldq) + a.D <= kDmaMaxBytes &&
            uint64_t(resq::WR - 1) * uint64_t(a.ldx) + a.D <= kDmaMaxBytes;
+}
+
+// The 16x16x64 layout: d in {256, 512, 768, 1024} (at most 128 KiB of resident queries and a
+// register ring of 16 k-steps), and 32-bit descriptor offsets within a 128-query block and a
+// wave's 32 rows.
+bool resq16_ok(const I8Args& a, bool vec) {
+#ifndef VA_I8_RESQ16
+#define VA_I8_RESQ16 1
+#endif
+    return VA_I8_RESQ16 && vec && !a.qrow && a.Q > 192 && a.D % 256 == 0 && a.D <= 1024 &&
+           a.N <= 0xFFFFFE00u && uint64_t(resq16::TQMAX - 1) * uint64_t(a.ldq) + a.D <= kDmaMaxBytes &&
+           uint64_t(resq16::WR - 1) * uint64_t(a.ldx) + a.D <= kDmaMaxBytes;
+}
+
+va_status launch_i8_resq16(va_context* ctx, const I8Args& a) {
+    using namespace resq16;
+    // 256 resident queries where they fit beside the stage lists (d <= 512), else 128
+    const uint32_t TQ = a.D <= 512 ? 256u : 128u;
+    // one workgroup per CU (the registers of 8 waves), the number of ranges a multiple of the
+    // XCD count
+    const uint32_t nqb = (a.Q + TQ - 1) / TQ;
+    const uint32_t per = (uint32_t(std::max(ctx->num_cus, 8)) + nqb - 1) / nqb;
+    const uint32_t NR = std::max<uint32_t>(kXcds, (per + kXcds - 1) / kXcds * kXcds);
+    const uint64_t grid = uint64_t(nqb) * NR;
+    if (grid > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "int8 scan grid too large");
+    auto go = [&](auto kern, int lds) -> va_status {
+        VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds));
+        kern<<<dim3(uint32_t(grid)), dim3(512), lds, ctx->stream>>>(a, NR);
+        return VA_OK;
+    };
+    va_status st;
+    switch (a.D) {
+        case 256: st = go(&i8_resq16_kernel<256, 16, 4>, lds_bytes<256, 16>()); break;
+        case 512: st = go(&i8_resq16_kernel<512, 16, 4>, lds_bytes<512, 16>()); break;
+        case 768: st = go(&i8_resq16_kernel<768, 8, 12>, lds_bytes<768, 8>()); break;
+        default: st = go(&i8_resq16_kernel<1024, 8, 16>, lds_bytes<1024, 8>());
+    }
+    if (st != VA_OK) return st;
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
 }
 
 va_status launch_i8_resq(va_context* ctx, const I8Args& a) {
@@ -962,6 +1256,7 @@ bool i8_vec(const I8Args& a) {
 va_status launch_i8(va_context* ctx, const I8Args& a, bool filter) {
     if (a.Q == 0 || a.N == 0) return VA_OK;
     const bool vec = i8_vec(a);
+    if (filter && resq16_ok(a, vec)) return launch_i8_resq16(ctx, a);
     if (filter && resq_ok(a, vec)) return launch_i8_resq(ctx, a);
 #ifndef VA_I8_DMA
 #define VA_I8_DMA 1
