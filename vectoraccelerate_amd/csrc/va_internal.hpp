@@ -317,6 +317,35 @@ __device__ inline void plan_tile(const ListPlan& p, uint32_t t, uint32_t TQ, uin
     rs = p.roff[l] + rb * TN;
     rc = min(TN, n - rb * TN);
 }
+// plan_tile for a tile t at or after one of list h (pre[h] <= t): the list is found by galloping
+// up from h (one load while t stays in h's list, as a persistent workgroup's tiles of a long list
+// do) instead of a binary search over all lists.  Returns the list.
+__device__ inline uint32_t plan_tile_after(const ListPlan& p, uint32_t t, uint32_t h, uint32_t TQ, uint32_t TN,
+                                           uint32_t& qs, uint32_t& qc, uint32_t& rs, uint32_t& rc) {
+    uint32_t lo = h, hi = h + 1, step = 1;  // pre[lo] <= t; find hi with pre[hi] > t (or hi = C)
+    while (hi < p.C && p.pre[hi] <= t) {
+        lo = hi;
+        step *= 2;
+        hi = min(p.C, lo + step);
+    }
+    hi -= 1;  // the answer lies in [lo, hi]
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi + 1) >> 1;
+        if (p.pre[mid] <= t) lo = mid;
+        else hi = mid - 1;
+    }
+    const uint32_t l = lo, local = t - p.pre[lo];
+    const uint32_t nq = p.qoff[l + 1] - p.qoff[l];
+    const uint32_t len = p.roff[l + 1] - p.roff[l];
+    const uint32_t n = p.sample ? ivf_sample_rows(len) : len;
+    const uint32_t nqb = (nq + TQ - 1) / TQ;
+    const uint32_t rb = local / nqb, qb = local % nqb;
+    qs = p.qoff[l] + qb * TQ;
+    qc = min(TQ, nq - qb * TQ);
+    rs = p.roff[l] + rb * TN;
+    rc = min(TN, n - rb * TN);
+    return l;
+}
 #endif
 
 struct DistArgs {

@@ -553,15 +553,25 @@ __device__ __forceinline__ void wide_tile(const Ivf16Args& a, float2* xs, uint32
                 for (int m = 0; m < 4; ++m)
                     acc[n][m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(r4[m][u], q4[n][u], acc[n][m], 0, 0, 0);
     };
-    load(0, qa, ra);
-    for (uint32_t c = 0; c < nch; c += 2) {
-        load(c + 1, qb, rb);
-        compute(qa, ra);
-        __builtin_amdgcn_sched_barrier(0);
-        load(c + 2, qa, ra);
-        compute(qb, rb);
+#ifndef VA_IVF16_RING
+#define VA_IVF16_RING 2
+#endif
+    constexpr int RG = VA_IVF16_RING;
+    h8v qr[RG][W][4], rr[RG][4][4];
+#pragma unroll
+    for (int r = 0; r < RG - 1; ++r) {
+        load(uint32_t(r), qr[r], rr[r]);
         __builtin_amdgcn_sched_barrier(0);
     }
+    for (uint32_t c = 0; c < nch; c += RG) {
+#pragma unroll
+        for (int r = 0; r < RG; ++r) {
+            load(c + uint32_t(r + RG - 1), qr[(r + RG - 1) % RG], rr[(r + RG - 1) % RG]);
+            compute(qr[r], rr[r]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    (void)qa; (void)qb; (void)ra; (void)rb;
     PreTestV pt[W];
     float inv[W];
 #pragma unroll
@@ -649,6 +659,235 @@ __global__ __launch_bounds__(256, 1) void ivf16_wide_kernel(Ivf16Args a) {
     }
 }
 
+// ---- lists probed by more than 32 queries: resident queries, rows straight into registers ------
+// A workgroup (8 waves, one per CU) takes a tile of 64 of a list's queries x 1024 of its rows:
+// the queries (gathered through the plan) and the rows' {|x|^2, error} go to LDS once per tile,
+// and each wave walks its 32 rows of each of the tile's four 256-row sub-tiles against all 64
+// queries on v_mfma_f32_16x16x32_f16 (2 x 4 blocks).  The rows move from HBM straight into a
+// ring of R register slots of one 32-value k-step each (the wave's four lanes of a row read 64
+// contiguous bytes per instruction), R - 1 k-steps ahead and across the sub-tiles of the tile;
+// the query fragments come from LDS (chunk-major: each fragment read serves two MFMAs).  Passes
+// are staged per wave in LDS and appended when the stage fills and at the end, so no global
+// atomic or store waits inside the stream.  The wide tiles reloaded their queries with every
+// 128 rows and kept one 64-value chunk in flight per wave.
+namespace ivr {
+constexpr int NW = 8, TQ = 64, NQB = 4, MB = 2;
+constexpr int WR = 16 * MB;               // rows per wave per sub-tile
+constexpr int SUB = NW * WR;              // rows per sub-tile
+constexpr int NSUB = 4;                   // sub-tiles per tile
+constexpr uint32_t TN = uint32_t(SUB * NSUB);
+constexpr uint32_t DPMAX = 1024;          // the queries' LDS share: 64 x 1024 halves = 128 KiB
+constexpr int LCAP = 128;                 // staged passes per wave
+// LDS: queries [TQ x Dp halves], row norms [TN float2], per query {A, B, E, C} and {inv, qi},
+// the stage lists
+inline uint32_t lds_bytes(uint32_t Dp) { return TQ * Dp * 2 + TN * 8 + TQ * 16 + TQ * 8 + NW * LCAP * 12; }
+}  // namespace ivr
+
+template <int R>
+__global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
+    using namespace ivr;
+    extern __shared__ __attribute__((aligned(16))) char lds8[];
+    const int tid = threadIdx.x, lane = tid & 63, r16 = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t Dp = a.Dp, rowb = Dp * 2u;
+    const uint32_t nsl = Dp / 64;  // ring slots (128 bytes of each row) per sub-tile, a multiple of R
+    char* nrm_b = lds8 + TQ * rowb;
+    const float2* s_nrm = reinterpret_cast<const float2*>(nrm_b);
+    float4* s_pt = reinterpret_cast<float4*>(nrm_b + TN * 8);
+    float2* s_qv = reinterpret_cast<float2*>(nrm_b + TN * 8 + TQ * 16);
+    uint32_t* s_qi = reinterpret_cast<uint32_t*>(nrm_b + TN * 8 + TQ * 24) + wave * 3 * LCAP;
+    uint32_t* s_val = s_qi + LCAP;
+    uint32_t* s_pos = s_val + LCAP;
+    const uint32_t lds0 = lds_addr_of(lds8);
+    uint32_t lc = 0;  // staged passes (wave-uniform)
+    // Appends the staged passes: count every pass, keep a query's first cap.
+    auto flush = [&]() {
+        for (uint32_t b0 = 0; b0 < lc; b0 += 64) {
+            const uint32_t e = b0 + uint32_t(lane);
+            if (e < lc) {
+                const uint32_t qi = s_qi[e];
+                const uint32_t pos = atomicAdd(a.cnt + qi, 1u);
+                if (pos < a.cap) {
+                    a.cand_dot[int64_t(qi) * a.cap + pos] = __builtin_bit_cast(float, s_val[e]);
+                    a.cand_pos[int64_t(qi) * a.cap + pos] = s_pos[e];
+                }
+            }
+        }
+        lc = 0;
+    };
+    // query block u of k-step t: chunk 4 t + g of query 16 u + r16
+    const char* qrd = lds8 + g * 1024 + r16 * 16;
+    auto rd_q = [&](uint32_t t, int u) { return *reinterpret_cast<const h8v*>(qrd + t * 4096 + u * 256); };
+    uint32_t voff[MB];
+#pragma unroll
+    for (int j = 0; j < MB; ++j) voff[j] = uint32_t(16 * j + r16) * rowb + 16u * uint32_t(g);
+
+    // XCD-aware order: XCD x (workgroups b with b % 8 == x; gridDim.x is a multiple of 8) takes
+    // the x-th eighth of the plan's tiles, which its workgroups walk together, so the query
+    // blocks of one row block (consecutive tiles) meet in the XCD's L2 and the rows come from
+    // HBM about once.
+    const uint32_t total = a.plan.pre[a.plan.C];
+    const uint32_t tpx = (total + kXcds - 1) / kXcds, xcd = blockIdx.x % kXcds;
+    const uint32_t tend = min(total, (xcd + 1) * tpx);
+    uint32_t lh = 0;  // the list of this workgroup's previous tile
+    for (uint32_t t = xcd * tpx + blockIdx.x / kXcds; t < tend; t += gridDim.x / kXcds) {
+        uint32_t qs, qc, rs, rc;
+        lh = plan_tile_after(a.plan, t, lh, TQ, TN, qs, qc, rs, rc);
+        __syncthreads();  // every wave is done with the previous tile's LDS
+        // the tile's queries, chunk-major (16-byte chunk m of query r at m * 1024 + r * 16; past
+        // qc: zeros), and its rows' {|x|^2, error} (past rc: zeros)
+        {
+            const uint32_t qrow = uint32_t(lane) < qc ? a.qrow[qs + uint32_t(lane)] : 0u;
+            const uint32_t qo = uint32_t(lane) < qc ? qrow * rowb : kDmaSkip;
+            const dma_rsrc qres = make_dma_rsrc(a.qh, kDmaMaxBytes);
+            for (uint32_t m = uint32_t(wave); m < Dp / 8; m += NW)
+                lds_dma16(qres, qo == kDmaSkip ? kDmaSkip : qo + 16u * m, lds0 + m * 1024u);
+            const dma_rsrc nres = make_dma_rsrc(a.xn + rs, rc * 8u);
+            lds_dma16(nres, uint32_t(tid) * 16u, lds0 + TQ * rowb + uint32_t(wave) * 1024u);
+        }
+        if (tid < TQ) {
+            float4 p = {0.0f, 0.0f, 0.0f, 0.0f};
+            float2 v = {0.0f, 0.0f};
+            if (uint32_t(tid) < qc) {
+                const uint32_t qi = a.qrow[qs + uint32_t(tid)];
+                const float4 inf = a.qinfo[qi];
+                const PreTestV pt = pretest_v(a.bnd, inf.x, inf.y, a.qerr[qi], inf.z, a.thr[qi]);
+                p = make_float4(pt.A, pt.B, pt.E, pt.C);
+                v = make_float2(inf.z, __builtin_bit_cast(float, qi));
+            }
+            s_pt[tid] = p;
+            s_qv[tid] = v;
+        }
+        wait_vmcnt<0>();
+        __syncthreads();  // queries, norms and constants visible
+
+        // ---- this wave's rows: sub-tiles j with rows j SUB + wave WR .. (+ WR) of the tile ------
+        const uint32_t w0 = uint32_t(wave) * WR;
+        const uint32_t nsub = rc > w0 ? min(uint32_t(NSUB), (rc - w0 + SUB - 1) / SUB) : 0u;
+        if (nsub == 0) continue;
+        uint32_t lsub = 0, lsl = 0;  // sub-tile and slot of the next load (wave-uniform)
+        // The descriptor covers this wave's rows of the sub-tile being loaded; a lane's row
+        // offset fails its range check for rows past the tile (and every load past the last
+        // sub-tile reads zeros).
+        // A slot is the 128 bytes of each row that one cache line holds: both 64-byte halves of
+        // a row block are requested back to back (one instruction per half and row block).
+        auto load = [&](h8v(&dst)[2][MB]) {
+            const bool ok = lsub < nsub;
+            const uint32_t o = lsub * SUB + w0;
+            const uint32_t rows = __builtin_amdgcn_readfirstlane(ok ? min(uint32_t(WR), rc - o) : 0u);
+            const uint64_t base = reinterpret_cast<uint64_t>(a.xh + int64_t(rs + (ok ? o : 0u)) * Dp);
+            const uint64_t bs = (uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(base >> 32)))) << 32) |
+                                uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(base)));
+            const __amdgpu_buffer_rsrc_t xres =
+                __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(bs), 0, int(rows * rowb), 0x00020000);
+            const uint32_t skip = rows ? 0u : kDmaSkip;
+#pragma unroll
+            for (int j = 0; j < MB; ++j)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    dst[h][j] = __builtin_bit_cast(
+                        h8v, __builtin_amdgcn_raw_buffer_load_b128(xres, voff[j] | skip, int(lsl * 128u + 64u * h), 0));
+            if (++lsl == nsl) {
+                lsl = 0;
+                ++lsub;
+            }
+        };
+        f32x4s acc[NQB][MB];
+#pragma unroll
+        for (int u = 0; u < NQB; ++u)
+#pragma unroll
+            for (int j = 0; j < MB; ++j) acc[u][j] = f32x4s{0.f, 0.f, 0.f, 0.f};
+        h8v xr[R][2][MB], qf[NQB];
+#pragma unroll
+        for (int r = 0; r < R - 1; ++r) {
+            load(xr[r]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int u = 0; u < NQB; ++u) qf[u] = rd_q(0, u);
+        uint32_t mst = 0, msub = 0;  // k-step (32 values) and sub-tile of the MFMAs
+        const uint32_t nst = 2 * nsl;
+        auto mma = [&](const h8v(&x)[2][MB]) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t nks = mst + 1 == nst ? 0u : mst + 1;
+#pragma unroll
+                for (int u = 0; u < NQB; ++u) {
+#pragma unroll
+                    for (int j = 0; j < MB; ++j)
+                        acc[u][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[h][j], qf[u], acc[u][j], 0, 0, 0);
+                    qf[u] = rd_q(nks, u);
+                    __builtin_amdgcn_sched_group_barrier(0x008, MB, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                mst = nks;
+            }
+        };
+        // A sub-tile's passes: lane (r16, g) holds query 16 u + r16 against rows 16 j + 4 g + v of
+        // the wave's 32 in acc[u][j][v]; the pre-test of the flat screen (flagged rows pass).
+        auto epilogue = [&]() {
+            const uint32_t o = msub * SUB + w0;  // the wave's first row in the tile
+#pragma unroll
+            for (int u = 0; u < NQB; ++u) {
+                const int ql = 16 * u + r16;
+                const float4 p = s_pt[ql];
+                const PreTestV pt = {p.x, p.y, p.z, p.w};
+                uint32_t mask = 0;
+#pragma unroll
+                for (int j = 0; j < MB; ++j)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const uint32_t row = o + uint32_t(16 * j + 4 * g + v);
+                        float xxp, nxp, exp;
+                        screen_norms(s_nrm[row], xxp, nxp, exp);
+                        const bool pass = row < rc && !(acc[u][j][v] < pretest_rhs(pt, xxp, nxp, exp));
+                        mask |= uint32_t(pass) << (4 * j + v);
+                    }
+                mask = uint32_t(ql) < qc ? mask : 0u;
+                if (!__ballot(mask != 0u)) continue;
+                const float2 qv = s_qv[ql];
+                const uint32_t qi = __builtin_bit_cast(uint32_t, qv.y);
+#pragma unroll
+                for (int j = 0; j < MB; ++j)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const bool pass = (mask >> (4 * j + v)) & 1u;
+                        const uint64_t mk = __ballot(pass);
+                        if (!mk) continue;
+                        const uint32_t n = uint32_t(__popcll(mk));
+                        if (lc + n > uint32_t(LCAP)) flush();  // wave-uniform
+                        if (pass) {
+                            const uint32_t e = lc + __builtin_amdgcn_mbcnt_hi(uint32_t(mk >> 32),
+                                                                             __builtin_amdgcn_mbcnt_lo(uint32_t(mk), 0u));
+                            s_qi[e] = qi;
+                            s_val[e] = __builtin_bit_cast(uint32_t, acc[u][j][v] * qv.x);
+                            s_pos[e] = rs + o + uint32_t(16 * j + 4 * g + v);
+                        }
+                        lc += n;
+                    }
+            }
+        };
+        const uint32_t steps = nsub * nsl;
+        for (uint32_t s = 0; s < steps; s += R) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                load(xr[(r + R - 1) % R]);  // the slot the previous k-step consumed
+                mma(xr[r]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (mst == 0) {
+                epilogue();
+                ++msub;
+#pragma unroll
+                for (int u = 0; u < NQB; ++u)
+#pragma unroll
+                    for (int j = 0; j < MB; ++j) acc[u][j] = f32x4s{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    }
+    flush();
+}
+
 // Tile shapes and their cost model: shape_for / group_tile (va_plan.hpp, shared with the host
 // planning tests).
 static_assert(ivfs::TQ == kSmallTileQueries && ivfs::TN == kSmallTileRows, "16-query tile of ivf_small_kernel");
@@ -665,6 +904,8 @@ struct DevPlan {
     const uint32_t* roff = nullptr;    // list offsets [C + 1]
     uint32_t small_ok = 0;
     uint32_t screen = 0;        // tile groups of the screened scan (iv16) instead of the fp32 shapes
+    uint32_t wide_tn = 0;       // screened scan: rows per tile of the 64-query group in the full pass
+                                // (ivf16_resq_kernel's tiles; 0: the wide tiles' 128)
     uint32_t* P = nullptr;      // [Q x np] probes with repeats / sentinels replaced by ~0
     uint32_t* qcnt = nullptr;   // [C] queries per list
     uint32_t* qoff = nullptr;   // [C + 1]
@@ -738,6 +979,7 @@ __global__ __launch_bounds__(256) void plan_counts_kernel(DevPlan p) {
             group_tile(g, TQ, TN);
         }
         for (int pass = 0; pass < 2; ++pass) {
+            if (p.screen && g == 2 && pass == 1 && p.wide_tn) TN = p.wide_tn;
             const uint32_t rows = pass == 0 ? ivf_sample_rows(n) : n;
             const uint32_t tiles = (nq == 0 || rows == 0) ? 0u : ((nq + TQ - 1) / TQ) * ((rows + TN - 1) / TN);
             for (int gi = 0; gi < kGroups; ++gi)
@@ -836,6 +1078,23 @@ va_status run_screen_pass(va_context* ctx, const DevPlan& dp, int pass, Ivf16Arg
             ivf16_narrow_kernel<<<dim3(uint32_t(ctx->num_cus) * 2), dim3(256), 0, s>>>(a);
         } else if (g == 1) {
             ivf16_wide_kernel<1><<<dim3(uint32_t(ctx->num_cus)), dim3(256), 0, s>>>(a);
+        } else if (pass == 1 && dp.wide_tn == ivr::TN) {
+            // one workgroup per CU (the LDS); the ring depth divides the slots of a sub-tile
+            const uint32_t nsl = a.Dp / 64, lds = ivr::lds_bytes(a.Dp);
+            auto go = [&](auto kern) {
+                if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        int(lds)) != hipSuccess) {
+                    st = fail(ctx, VA_ERR_HIP, "ivf16_resq_kernel: %u bytes of LDS refused", lds);
+                    return;
+                }
+                kern<<<dim3(std::max<uint32_t>(kXcds, uint32_t(ctx->num_cus) / kXcds * kXcds)), dim3(512), lds, s>>>(a);
+            };
+            if (nsl % 6 == 0) go(&ivf16_resq_kernel<6>);
+            else if (nsl % 4 == 0) go(&ivf16_resq_kernel<4>);
+            else if (nsl % 3 == 0) go(&ivf16_resq_kernel<3>);
+            else if (nsl % 2 == 0) go(&ivf16_resq_kernel<2>);
+            else go(&ivf16_resq_kernel<1>);
+            if (st != VA_OK) break;
         } else {
             ivf16_wide_kernel<2><<<dim3(uint32_t(ctx->num_cus)), dim3(256), 0, s>>>(a);
         }
@@ -1066,6 +1325,16 @@ bool small_tiles_ok(const va_ivf* ivf, const float* q) {
            (reinterpret_cast<uintptr_t>(ivf->list_vectors) & 15) == 0 &&
            uint64_t(ivfs::TN) * ivf->D * 4 + 16 <= 0x7FFFFFF0ull;
 }
+// The lists probed by more than 32 queries take ivf16_resq_kernel in the full pass when the 64
+// queries' fp16 rows fit the kernel's LDS share and every query row lies within a 31-bit
+// descriptor offset.
+bool ivf_resq_applies(const va_context* ctx, uint32_t Q, uint32_t Dp) {
+#ifndef VA_IVF_RESQ
+#define VA_IVF_RESQ 1
+#endif
+    return VA_IVF_RESQ && ctx->opt_screen != 1 && Dp <= ivr::DPMAX && uint64_t(Q) * Dp * 2 <= kDmaMaxBytes;
+}
+
 // The screened list scan serves an index with an fp16 shadow whose lists can take the 16-query
 // tiles (their keys are replayed in the rerank), unless VA_OPT_SCREEN turns it off.
 bool ivf_screen_applies(const va_context* ctx, const va_ivf* ivf, const float* q) {
@@ -1126,6 +1395,7 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
     dp.roff = ivf->offsets;
     dp.small_ok = 1;
     dp.screen = 1;
+    dp.wide_tn = ivf_resq_applies(ctx, Q, Dp) ? ivr::TN : 0u;
     dp.P = s.carve<uint32_t>(pairs);
     dp.qlist = s.carve<uint32_t>(pairs);
     dp.qcnt = s.carve<uint32_t>(C);
