@@ -792,9 +792,9 @@ def run_pq(ctx, a, cpu: bool):
     lookups = float(Q) * N * M
     scan_ms = tim.get("scan_ms") if tim else None
     rate = lookups / (scan_ms * 1e-3) / 1e12 if scan_ms else None
-    # LDS: 128 bytes per clock per CU = 32 four-byte reads; 256 CUs at 2.4 GHz = 19.66 T reads/s.
-    # The filter pass reads fp16 pair tables: one 4-byte read carries two queries' entries, so the
-    # fraction is counted per read (two lookups each).
+    # LDS: 128 bytes per clock per CU = 32 four-byte words; 256 CUs at 2.4 GHz = 19.66 T words/s.
+    # The filter pass reads fp16 pair tables: one 4-byte word carries two queries' entries (and one
+    # 128-bit read four words, eight queries), so the fraction is counted per word (two lookups).
     lds_peak = 256 * 32 * 2.4e9 / 1e12
     reads = rate / 2 if rate else None
     xe = torch.randn(1_000_000, D, device="cuda", generator=g)
@@ -813,8 +813,8 @@ def run_pq(ctx, a, cpu: bool):
                      "frac": (reads / lds_peak) if reads else None, "kernel": "pq_adc_screen<16> (filter pass)",
                      "lookups_per_s_T": rate,
                      "algorithmic": f"Q*N*M = {lookups:.4g} table lookups per scan = {lookups / 2:.4g} 4-byte LDS "
-                                    "reads (fp16 pair tables: one read serves two queries; exact fp32 re-score "
-                                    "of the passes)",
+                                    "words (fp16 pair tables, entry-major: one word serves two queries, one "
+                                    "128-bit read eight; exact fp32 re-score of the passes)",
                      **counted(COUNTERS_PQ)},
     }
     log(f"PQ ADC top-10: {ms:.3f} ms/step = {res['qps']:.0f} QPS; filter scan {scan_ms} ms = "

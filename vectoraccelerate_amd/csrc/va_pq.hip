@@ -466,17 +466,48 @@ __device__ __forceinline__ float add_half(float acc, uint32_t v) {
     return d;
 }
 
+// The workgroup's QP query pairs sit entry-major in LDS: entry e (subspace m, centroid c) of
+// pair i at word e * QP + i, so one wide read (128 bits for QP >= 4) at a row's code fetches that
+// entry for every pair: a random address costs the same bank conflicts whatever its width, and
+// the lookups per conflict grow with the pairs per read (one word per pair, two queries per
+// word).
+template <int QP>
+struct PairWords {
+    uint32_t w[QP];
+};
+template <int QP>
+__device__ __forceinline__ PairWords<QP> read_pairs(const uint32_t* p) {
+    PairWords<QP> r;
+    if constexpr (QP % 4 == 0) {
+#pragma unroll
+        for (int b = 0; b < QP / 4; ++b) {
+            const uint4 v = reinterpret_cast<const uint4*>(p)[b];
+            r.w[4 * b] = v.x;
+            r.w[4 * b + 1] = v.y;
+            r.w[4 * b + 2] = v.z;
+            r.w[4 * b + 3] = v.w;
+        }
+    } else if constexpr (QP == 2) {
+        const uint2 v = *reinterpret_cast<const uint2*>(p);
+        r.w[0] = v.x;
+        r.w[1] = v.y;
+    } else {
+        r.w[0] = p[0];
+    }
+    return r;
+}
+
 template <int M>
 __global__ __launch_bounds__(kAdcThreads) void pq_adc_screen(AdcArgs a, const uint32_t* __restrict__ packed,
                                                               const float* __restrict__ scale) {
     constexpr int QP = 64 / M;  // query pairs per workgroup: QP x M x 1 KB = 64 KB of LDS
     constexpr int MK = M * 256;
-    __shared__ uint32_t tab[QP * MK];
+    __shared__ __attribute__((aligned(16))) uint32_t tab[QP * MK];
     const uint32_t p0 = blockIdx.y * QP;
     const uint32_t np = min(uint32_t(QP), (a.nq + 1) / 2 - p0);
-    for (uint32_t i = 0; i < uint32_t(QP); ++i)
-        for (uint32_t e = threadIdx.x; e < uint32_t(MK); e += kAdcThreads)
-            tab[i * MK + e] = i < np ? packed[int64_t(p0 + i) * MK + e] : 0u;
+    for (uint32_t e = threadIdx.x; e < uint32_t(MK); e += kAdcThreads)
+#pragma unroll
+        for (uint32_t i = 0; i < uint32_t(QP); ++i) tab[e * QP + i] = i < np ? packed[int64_t(p0 + i) * MK + e] : 0u;
     // screen thresholds (query index past nq: never passes)
     float thr[2 * QP];
 #pragma unroll
@@ -539,18 +570,36 @@ __global__ __launch_bounds__(kAdcThreads) void pq_adc_screen(AdcArgs a, const ui
         uint32_t off[M];
 #pragma unroll
         for (int m = 0; m < M; ++m) off[m] = (w[m / 4] >> (8 * (m % 4))) & 0xFFu;
-#pragma unroll
-        for (int i = 0; i < QP; ++i) {
-            if (uint32_t(i) >= np) break;
+        if constexpr (QP == 1) {
+            // one pair: one word per read either way
             float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                const uint32_t v = tab[i * MK + m * 256 + off[m]];
+                const uint32_t v = tab[m * 256 + off[m]];
                 s0 = add_half<0>(s0, v);
                 s1 = add_half<1>(s1, v);
             }
-            if (s0 <= thr[2 * i]) rescore(2 * (p0 + i), j, off);
-            if (s1 <= thr[2 * i + 1]) rescore(2 * (p0 + i) + 1, j, off);
+            if (s0 <= thr[0]) rescore(2 * p0, j, off);
+            if (s1 <= thr[1]) rescore(2 * p0 + 1, j, off);
+        } else {
+            // every pair's sums (pairs past np have zero tables and thresholds that never pass)
+            float s0[QP], s1[QP];
+#pragma unroll
+            for (int i = 0; i < QP; ++i) s0[i] = s1[i] = 0.0f;
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const PairWords<QP> v = read_pairs<QP>(tab + (m * 256 + off[m]) * QP);
+#pragma unroll
+                for (int i = 0; i < QP; ++i) {
+                    s0[i] = add_half<0>(s0[i], v.w[i]);
+                    s1[i] = add_half<1>(s1[i], v.w[i]);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < QP; ++i) {
+                if (s0[i] <= thr[2 * i]) rescore(2 * (p0 + i), j, off);
+                if (s1[i] <= thr[2 * i + 1]) rescore(2 * (p0 + i) + 1, j, off);
+            }
         }
     }
 }
