@@ -186,9 +186,10 @@ def _search_mode(ctx, pipe, q, st, k, screen):
 # Shapes that reach every tile group of the screened scan: lists probed by a few queries (16-query
 # tiles), by 17-32 (32-query tiles) and by many (64-query tiles, several query blocks per list);
 # D not a multiple of 64 (zero-padded shadow rows) and a single 64-value chunk.  The full pass
-# over lists probed by more than 32 queries runs on 64 resident queries x 1024-row tiles with a
-# ring of 1, 2, 3, 4 or 6 slots of 128 bytes per row (padded D = 64, 128, 192, 256, 768): lists of
-# several row tiles, ragged last tiles and sub-tiles.
+# over lists probed by more than 32 queries runs on resident-query tiles (96 queries x 512 rows up
+# to padded D = 768, 64 x 1024 above) with a ring of 1, 2, 3, 4 or 6 slots of 128 bytes per row
+# (padded D = 64, 128, 192, 256, 768, 1024): lists of several row tiles, ragged last tiles and
+# sub-tiles.
 @pytest.mark.parametrize("C,D,N,Q,nprobe,k,zipf", [(256, 64, 40000, 64, 8, 10, 1.1),
                                                     (64, 96, 30000, 600, 4, 20, None),
                                                     (16, 128, 20000, 600, 4, 10, None),
@@ -196,7 +197,8 @@ def _search_mode(ctx, pipe, q, st, k, screen):
                                                     (48, 36, 12000, 200, 6, 50, 1.1),
                                                     (32, 768, 20000, 96, 32, 100, None),
                                                     (8, 256, 40000, 400, 4, 10, None),
-                                                    (12, 180, 30000, 300, 3, 10, 1.1)])
+                                                    (12, 180, 30000, 300, 3, 10, 1.1),
+                                                    (16, 1000, 20000, 300, 4, 10, None)])
 def test_ivf_screened_bit_identical_to_fp32(ctx, oracle, C, D, N, Q, nprobe, k, zipf):
     """The screened list scan (fp16 shadow rows on the fp16 MFMA, exact rerank with each list's
     fp32 arithmetic) returns the fp32 list scan's ids and distances bit for bit, and both match

@@ -671,21 +671,32 @@ __global__ __launch_bounds__(256, 1) void ivf16_wide_kernel(Ivf16Args a) {
 // atomic or store waits inside the stream.  The wide tiles reloaded their queries with every
 // 128 rows and kept one 64-value chunk in flight per wave.
 namespace ivr {
-constexpr int NW = 8, TQ = 64, NQB = 4, MB = 2;
+constexpr int NW = 8, MB = 2;
 constexpr int WR = 16 * MB;               // rows per wave per sub-tile
 constexpr int SUB = NW * WR;              // rows per sub-tile
-constexpr int NSUB = 4;                   // sub-tiles per tile
-constexpr uint32_t TN = uint32_t(SUB * NSUB);
 constexpr uint32_t DPMAX = 1024;          // the queries' LDS share: 64 x 1024 halves = 128 KiB
-constexpr int LCAP = 128;                 // staged passes per wave
-// LDS: queries [TQ x Dp halves], row norms [TN float2], per query {A, B, E, C} and {inv, qi},
-// the stage lists
-inline uint32_t lds_bytes(uint32_t Dp) { return TQ * Dp * 2 + TN * 8 + TQ * 16 + TQ * 8 + NW * LCAP * 12; }
+// Two shapes: 96 queries x 512 rows where 96 fp16 query rows fit (padded d <= 768: a third
+// fewer row fetches for a list probed by 97-192 queries, half for 65-96), else 64 x 1024.
+template <int NQB>
+struct Shape {
+    static constexpr int TQ = 16 * NQB;
+    static constexpr int NSUB = NQB == 6 ? 2 : 4;  // sub-tiles per tile
+    static constexpr uint32_t TN = uint32_t(SUB * NSUB);
+    static constexpr int LCAP = NQB == 6 ? 64 : 128;  // staged passes per wave
+    // LDS: queries [TQ x Dp halves], row norms [TN float2], per query {A, B, E, C} and {inv, qi},
+    // the stage lists
+    static uint32_t lds_bytes(uint32_t Dp) { return TQ * Dp * 2 + TN * 8 + TQ * 16 + TQ * 8 + NW * LCAP * 12; }
+};
+inline int nqb_for(uint32_t Dp) { return Dp <= 768 ? 6 : 4; }
 }  // namespace ivr
 
-template <int R>
+template <int R, int NQB>
 __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
     using namespace ivr;
+    using Sh = Shape<NQB>;
+    constexpr int TQ = Sh::TQ, NSUB = Sh::NSUB, LCAP = Sh::LCAP;
+    constexpr uint32_t TN = Sh::TN;
+    constexpr uint32_t CS = TQ * 16;  // bytes of one 16-byte chunk column of the queries
     extern __shared__ __attribute__((aligned(16))) char lds8[];
     const int tid = threadIdx.x, lane = tid & 63, r16 = lane & 15, g = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -716,8 +727,8 @@ __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
         lc = 0;
     };
     // query block u of k-step t: chunk 4 t + g of query 16 u + r16
-    const char* qrd = lds8 + g * 1024 + r16 * 16;
-    auto rd_q = [&](uint32_t t, int u) { return *reinterpret_cast<const h8v*>(qrd + t * 4096 + u * 256); };
+    const char* qrd = lds8 + g * CS + r16 * 16;
+    auto rd_q = [&](uint32_t t, int u) { return *reinterpret_cast<const h8v*>(qrd + t * (4 * CS) + u * 256); };
     uint32_t voff[MB];
 #pragma unroll
     for (int j = 0; j < MB; ++j) voff[j] = uint32_t(16 * j + r16) * rowb + 16u * uint32_t(g);
@@ -734,16 +745,24 @@ __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
         uint32_t qs, qc, rs, rc;
         lh = plan_tile_after(a.plan, t, lh, TQ, TN, qs, qc, rs, rc);
         __syncthreads();  // every wave is done with the previous tile's LDS
-        // the tile's queries, chunk-major (16-byte chunk m of query r at m * 1024 + r * 16; past
-        // qc: zeros), and its rows' {|x|^2, error} (past rc: zeros)
+        // the tile's rows' {|x|^2, error} (past rc: zeros) by direct loads, and its queries,
+        // chunk-major (16-byte chunk m of query r at m * CS + r * 16; past qc: zeros): thread
+        // t < 5 TQ holds query t % TQ and copies chunks t / TQ, + 5, ...
         {
-            const uint32_t qrow = uint32_t(lane) < qc ? a.qrow[qs + uint32_t(lane)] : 0u;
-            const uint32_t qo = uint32_t(lane) < qc ? qrow * rowb : kDmaSkip;
-            const dma_rsrc qres = make_dma_rsrc(a.qh, kDmaMaxBytes);
-            for (uint32_t m = uint32_t(wave); m < Dp / 8; m += NW)
-                lds_dma16(qres, qo == kDmaSkip ? kDmaSkip : qo + 16u * m, lds0 + m * 1024u);
-            const dma_rsrc nres = make_dma_rsrc(a.xn + rs, rc * 8u);
-            lds_dma16(nres, uint32_t(tid) * 16u, lds0 + TQ * rowb + uint32_t(wave) * 1024u);
+            if (uint32_t(wave) < TN * 8 / 1024) {
+                const dma_rsrc nres = make_dma_rsrc(a.xn + rs, rc * 8u);
+                lds_dma16(nres, uint32_t(tid) * 16u, lds0 + TQ * rowb + uint32_t(wave) * 1024u);
+            }
+            constexpr uint32_t QT = 5 * TQ;  // threads that copy queries (QT <= 512)
+            if (uint32_t(tid) < QT) {
+                const uint32_t r = uint32_t(tid) % TQ;
+                const bool qv = r < qc;
+                const uint4* src = reinterpret_cast<const uint4*>(a.qh + int64_t(qv ? a.qrow[qs + r] : 0u) * Dp);
+                for (uint32_t m = uint32_t(tid) / TQ; m < Dp / 8; m += QT / TQ) {
+                    const uint4 v = qv ? src[m] : make_uint4(0u, 0u, 0u, 0u);
+                    *reinterpret_cast<uint4*>(lds8 + m * CS + r * 16u) = v;
+                }
+            }
         }
         if (tid < TQ) {
             float4 p = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -798,6 +817,7 @@ __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
 #pragma unroll
             for (int j = 0; j < MB; ++j) acc[u][j] = f32x4s{0.f, 0.f, 0.f, 0.f};
         h8v xr[R][2][MB], qf[NQB];
+        static_assert(NQB <= 8, "query fragments in registers");
 #pragma unroll
         for (int r = 0; r < R - 1; ++r) {
             load(xr[r]);
@@ -904,8 +924,8 @@ struct DevPlan {
     const uint32_t* roff = nullptr;    // list offsets [C + 1]
     uint32_t small_ok = 0;
     uint32_t screen = 0;        // tile groups of the screened scan (iv16) instead of the fp32 shapes
-    uint32_t wide_tn = 0;       // screened scan: rows per tile of the 64-query group in the full pass
-                                // (ivf16_resq_kernel's tiles; 0: the wide tiles' 128)
+    uint32_t wide_tn = 0;       // screened scan: rows and queries per tile of the last group in the
+    uint32_t wide_tq = 0;       // full pass (ivf16_resq_kernel's tiles; 0: the wide tiles' 128 x 64)
     uint32_t* P = nullptr;      // [Q x np] probes with repeats / sentinels replaced by ~0
     uint32_t* qcnt = nullptr;   // [C] queries per list
     uint32_t* qoff = nullptr;   // [C + 1]
@@ -979,7 +999,10 @@ __global__ __launch_bounds__(256) void plan_counts_kernel(DevPlan p) {
             group_tile(g, TQ, TN);
         }
         for (int pass = 0; pass < 2; ++pass) {
-            if (p.screen && g == 2 && pass == 1 && p.wide_tn) TN = p.wide_tn;
+            if (p.screen && g == 2 && pass == 1 && p.wide_tn) {
+                TN = p.wide_tn;
+                TQ = p.wide_tq;
+            }
             const uint32_t rows = pass == 0 ? ivf_sample_rows(n) : n;
             const uint32_t tiles = (nq == 0 || rows == 0) ? 0u : ((nq + TQ - 1) / TQ) * ((rows + TN - 1) / TN);
             for (int gi = 0; gi < kGroups; ++gi)
@@ -1078,9 +1101,11 @@ va_status run_screen_pass(va_context* ctx, const DevPlan& dp, int pass, Ivf16Arg
             ivf16_narrow_kernel<<<dim3(uint32_t(ctx->num_cus) * 2), dim3(256), 0, s>>>(a);
         } else if (g == 1) {
             ivf16_wide_kernel<1><<<dim3(uint32_t(ctx->num_cus)), dim3(256), 0, s>>>(a);
-        } else if (pass == 1 && dp.wide_tn == ivr::TN) {
+        } else if (pass == 1 && dp.wide_tn) {
             // one workgroup per CU (the LDS); the ring depth divides the slots of a sub-tile
-            const uint32_t nsl = a.Dp / 64, lds = ivr::lds_bytes(a.Dp);
+            const int nqb = ivr::nqb_for(a.Dp);
+            const uint32_t nsl = a.Dp / 64,
+                           lds = nqb == 6 ? ivr::Shape<6>::lds_bytes(a.Dp) : ivr::Shape<4>::lds_bytes(a.Dp);
             auto go = [&](auto kern) {
                 if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                         int(lds)) != hipSuccess) {
@@ -1089,11 +1114,16 @@ va_status run_screen_pass(va_context* ctx, const DevPlan& dp, int pass, Ivf16Arg
                 }
                 kern<<<dim3(std::max<uint32_t>(kXcds, uint32_t(ctx->num_cus) / kXcds * kXcds)), dim3(512), lds, s>>>(a);
             };
-            if (nsl % 6 == 0) go(&ivf16_resq_kernel<6>);
-            else if (nsl % 4 == 0) go(&ivf16_resq_kernel<4>);
-            else if (nsl % 3 == 0) go(&ivf16_resq_kernel<3>);
-            else if (nsl % 2 == 0) go(&ivf16_resq_kernel<2>);
-            else go(&ivf16_resq_kernel<1>);
+            auto pick = [&](auto NC) {
+                constexpr int NQB = decltype(NC)::value;
+                if (nsl % 6 == 0) go(&ivf16_resq_kernel<6, NQB>);
+                else if (nsl % 4 == 0) go(&ivf16_resq_kernel<4, NQB>);
+                else if (nsl % 3 == 0) go(&ivf16_resq_kernel<3, NQB>);
+                else if (nsl % 2 == 0) go(&ivf16_resq_kernel<2, NQB>);
+                else go(&ivf16_resq_kernel<1, NQB>);
+            };
+            if (nqb == 6) pick(std::integral_constant<int, 6>());
+            else pick(std::integral_constant<int, 4>());
             if (st != VA_OK) break;
         } else {
             ivf16_wide_kernel<2><<<dim3(uint32_t(ctx->num_cus)), dim3(256), 0, s>>>(a);
@@ -1395,7 +1425,11 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
     dp.roff = ivf->offsets;
     dp.small_ok = 1;
     dp.screen = 1;
-    dp.wide_tn = ivf_resq_applies(ctx, Q, Dp) ? ivr::TN : 0u;
+    if (ivf_resq_applies(ctx, Q, Dp)) {
+        const bool n6 = ivr::nqb_for(Dp) == 6;
+        dp.wide_tn = n6 ? ivr::Shape<6>::TN : ivr::Shape<4>::TN;
+        dp.wide_tq = n6 ? uint32_t(ivr::Shape<6>::TQ) : uint32_t(ivr::Shape<4>::TQ);
+    }
     dp.P = s.carve<uint32_t>(pairs);
     dp.qlist = s.carve<uint32_t>(pairs);
     dp.qcnt = s.carve<uint32_t>(C);
