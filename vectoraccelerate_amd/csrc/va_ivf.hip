@@ -753,14 +753,25 @@ __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
                 const dma_rsrc nres = make_dma_rsrc(a.xn + rs, rc * 8u);
                 lds_dma16(nres, uint32_t(tid) * 16u, lds0 + TQ * rowb + uint32_t(wave) * 1024u);
             }
-            constexpr uint32_t QT = 5 * TQ;  // threads that copy queries (QT <= 512)
+            constexpr uint32_t QS = 512 / TQ, QT = QS * TQ;  // threads that copy queries
             if (uint32_t(tid) < QT) {
                 const uint32_t r = uint32_t(tid) % TQ;
                 const bool qv = r < qc;
                 const uint4* src = reinterpret_cast<const uint4*>(a.qh + int64_t(qv ? a.qrow[qs + r] : 0u) * Dp);
-                for (uint32_t m = uint32_t(tid) / TQ; m < Dp / 8; m += QT / TQ) {
-                    const uint4 v = qv ? src[m] : make_uint4(0u, 0u, 0u, 0u);
-                    *reinterpret_cast<uint4*>(lds8 + m * CS + r * 16u) = v;
+                // eight loads in flight before their stores (a loop of single load-store pairs
+                // waited a memory round trip per chunk)
+                for (uint32_t m0 = uint32_t(tid) / TQ; m0 < Dp / 8; m0 += 8 * QS) {
+                    uint4 v[8];
+#pragma unroll
+                    for (int b = 0; b < 8; ++b) {
+                        const uint32_t m = m0 + uint32_t(b) * QS;
+                        v[b] = qv && m < Dp / 8 ? src[m] : make_uint4(0u, 0u, 0u, 0u);
+                    }
+#pragma unroll
+                    for (int b = 0; b < 8; ++b) {
+                        const uint32_t m = m0 + uint32_t(b) * QS;
+                        if (m < Dp / 8) *reinterpret_cast<uint4*>(lds8 + m * CS + r * 16u) = v[b];
+                    }
                 }
             }
         }
