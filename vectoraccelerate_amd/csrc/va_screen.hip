@@ -8,7 +8,10 @@
 //               sits in [2^14, 2^15); fp32 |q|^2 on the side;
 //   2. sample:  screened keys of every query against S strided rows; a screened key is an
 //               interval [lo, hi] that provably contains the fp32 scan's key s for that pair;
-//               tau_q = k-th smallest hi, so the true k-th key s_k <= tau_q;
+//               tau_q = k-th smallest hi, so the true k-th key s_k <= tau_q.  With a checked
+//               rank r < k (step 5 verifies the threshold, so any tau_q is safe) the sample
+//               keeps only the smallest approximate hi of each 32-row group and tau_q is the
+//               r-th smallest of those;
 //   3. screen:  the full pass appends (hi, lo, id) for every pair with lo <= tau_q (every row
 //               with s <= s_k is among them);
 //   4. bound:   U_q = k-th smallest hi among the candidates (>= s_k again);
@@ -63,7 +66,9 @@ constexpr int PF_AHEAD = 3;               // stages between a row prefetch and t
 constexpr int DP_ALIGN = KC;              // fp16 query rows are padded to a multiple of KC
 }  // namespace scr
 
-enum ScreenMode : int { SCREEN_KEYS = 0, SCREEN_FILTER = 1 };
+// SCREEN_GMIN: per query, the smallest approximate upper bound of each 32-row group (the sample of
+// a search whose threshold is checked afterwards, where any threshold is safe)
+enum ScreenMode : int { SCREEN_KEYS = 0, SCREEN_FILTER = 1, SCREEN_GMIN = 2 };
 // below this many queries a search over the fp16 shadow takes screen16_small_kernel (a 256-query
 // tile of screen16_kernel would be mostly padding)
 constexpr uint32_t kSmallBatch = 192;
@@ -81,6 +86,8 @@ struct ScreenArgs {
     int op = OP_L2SQ;
     float c1 = 0, cn = 0, c0x = 0, kabs = 0;  // bound coefficients (see screen_bounds)
     // SCREEN_KEYS: out_dot[q * ldo + j] = fp16 dot of query q and row j; out_xx[j] = |x_j|^2
+    // SCREEN_GMIN: out_dot[q * ldo + g] (as keys) = smallest approximate upper bound of the rows
+    // 32g .. 32g + 31 (ldo = 8 x the row tiles; groups past N hold the key of +inf)
     float* out_dot = nullptr;
     float* out_xx = nullptr;
     int64_t ldo = 0;
@@ -555,7 +562,50 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
     }
     __syncthreads();
 
-    if constexpr (MODE == SCREEN_KEYS) {
+    if constexpr (MODE == SCREEN_GMIN) {
+        // v = alpha acc + beta approximates the pair's upper bound hi (the interval's error term
+        // without its small absolute part, no clamp): alpha = an * ra(row), beta = b + bb * rb(row)
+        //   cosine:  1 - dot / (|q||x|) + E      an = -2^-sc / |q|, ra = 1/|x|, b = 1 + E
+        //   L2^2:    |q|^2 + |x|^2 - 2 dot + E   an = -2^(1-sc), b = (1+c)|q|^2, bb = 1+c, rb = |x|^2
+        //   -dot:    -dot + c1 |q||x|            an = -2^-sc, bb = c1 |q|, rb = |x|
+        // (L2 takes the square root of the group's smallest L2^2 value.)  Only a checked
+        // threshold is taken from these values, so they need not bound anything.
+        const float cE = (a.c1 + a.cn) * (1.0f + 0x1p-20f);
+        uint32_t* outk = reinterpret_cast<uint32_t*>(a.out_dot);
+        const bool cosine = a.op == OP_COS_DIST, ndot = a.op == OP_NEG_DOT;
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+            const float4 inf = qinf[n];  // {|q|^2, |q|, 2^-scale, c0q}
+            const float an = cosine ? -inf.z / inf.y : ndot ? -inf.z : -2.0f * inf.z;
+            const float b = cosine ? 1.0f + cE : ndot ? 0.0f : (1.0f + cE) * inf.x;
+            const float bb = cosine ? 0.0f : ndot ? a.c1 * inf.y : 1.0f + cE;
+            uint32_t g[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                float mn = INFINITY;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int r0 = wn * 128 + 32 * m + 8 * j + 4 * hh;
+                    const f32x4v xx = *reinterpret_cast<const f32x4v*>(xxs + r0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float ra = cosine ? __builtin_amdgcn_rsqf(xx[e]) : 1.0f;
+                        const float rb = ndot ? __builtin_amdgcn_sqrtf(xx[e]) : xx[e];
+                        const float v = fmaf(an * ra, acc[m][n][4 * j + e], fmaf(bb, rb, b));
+                        mn = uint32_t(r0 + e) < rc ? fminf(mn, v) : mn;
+                    }
+                }
+                mn = fminf(mn, __shfl_xor(mn, 32));
+                if (a.op == OP_L2) mn = __builtin_amdgcn_sqrtf(fmaxf(mn, 0.0f));
+                g[m] = key_of_float(mn);
+            }
+            const uint32_t ql = uint32_t(wq * 128 + 32 * n + l32);
+            if (hh == 0 && ql < qc)
+                *reinterpret_cast<uint4*>(outk + int64_t(qs + ql) * a.ldo + tb * 8 + wn * 4) =
+                    make_uint4(g[0], g[1], g[2], g[3]);
+        }
+        return;
+    } else if constexpr (MODE == SCREEN_KEYS) {
         // dense fp16 dots (the bounds are computed by screen_bound_kernel) and the row norms
         if (qb == 0 && wave == 0)
             for (uint32_t r = uint32_t(lane); r < rc; r += 64) a.out_xx[rs + r] = xxs[r];
@@ -1511,6 +1561,12 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     sa.kabs = bnd.kabs;
 
     // ---- 2. sample: k-th smallest upper bound over S strided rows ------------------------------
+    // A checked rank (rank < k) accepts any threshold, so the sample of a large batch keeps one
+    // approximate bound per 32-row group (the scan's epilogue takes the group minimum: no dense
+    // keys, no bound pass) and selects among those: the rank-th smallest group minimum is close
+    // to the rank-th smallest bound when the rank is far below the group count.
+    const bool group_min = rank < k && !(in.xh && Q <= kSmallBatchMax) && S >= 128ull * rank;
+    const uint32_t groups = uint32_t((S + scr::TN - 1) / scr::TN * (scr::TN / 32));
     for (uint32_t q0 = 0; q0 < Q; q0 += plan.qs) {
         const uint32_t nq = std::min(plan.qs, Q - q0);
         ScreenArgs a = sa;
@@ -1523,6 +1579,19 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
         a.out_dot = reinterpret_cast<float*>(skeys);
         a.out_xx = sxx;
         a.ldo = int64_t(S);
+        if (group_min) {
+            a.ldo = int64_t(groups);
+            VA_CHECK_STATUS(launch_screen<SCREEN_GMIN>(ctx, a));
+            SelectArgs sel;
+            sel.keys = skeys;
+            sel.ld = int64_t(groups);
+            sel.n = groups;
+            sel.rows = nq;
+            sel.k = rank;
+            sel.out_kth = thr + q0;
+            VA_CHECK_STATUS(launch_select(ctx, sel));
+            continue;
+        }
         if (in.xh && Q <= kSmallBatchMax) {
             // small batches sample the fp16 shadow (half the bytes, every CU busy)
             a.xh = in.xh;
