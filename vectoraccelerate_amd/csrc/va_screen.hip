@@ -133,15 +133,71 @@ __global__ __launch_bounds__(256) void pretest_kernel(ScreenArgs a, uint32_t Q, 
 }
 
 // ---- query preparation: one wave per query ------------------------------------------------
+// With vec (D % 4 == 0, 16-byte aligned rows) and Dp <= 2048 the row is read once, as float4s
+// all in flight together, and converted from registers.  zero0[0 .. n0) and zero1[0 .. n1) are
+// cleared on the side (the scan's counters), so that no separate fill launch is needed.
+constexpr uint32_t kPrepRegDp = 2048;
 __global__ __launch_bounds__(256) void screen_prep_kernel(const float* __restrict__ q, int64_t ldq, uint32_t Q,
                                                           uint32_t D, uint32_t Dp, _Float16* __restrict__ qh,
-                                                          float4* __restrict__ qinfo, float c0, float* __restrict__ qerr) {
+                                                          float4* __restrict__ qinfo, float c0, float* __restrict__ qerr,
+                                                          int vec, uint32_t* __restrict__ zero0, uint32_t n0,
+                                                          uint32_t* __restrict__ zero1, uint32_t n1) {
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n0; i += gridDim.x * 256) zero0[i] = 0u;
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n1; i += gridDim.x * 256) zero1[i] = 0u;
     const uint32_t qi = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (qi >= Q) return;
     const float* row = q + int64_t(qi) * ldq;
+    _Float16* out = qh + int64_t(qi) * Dp;
     float m = 0.0f, ss = 0.0f;
     bool bad = false;
+    if (vec && Dp <= kPrepRegDp) {
+        constexpr int NV = kPrepRegDp / 256;
+        f32x4v v[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t d = 256u * uint32_t(i) + 4u * uint32_t(lane);
+            v[i] = d < D ? *reinterpret_cast<const f32x4v*>(row + d) : f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                bad |= !(fabsf(v[i][e]) <= FLT_MAX);
+                m = fmaxf(m, fabsf(v[i][e]));
+                ss = fmaf(v[i][e], v[i][e], ss);
+            }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            m = fmaxf(m, __shfl_xor(m, off));
+            ss += __shfl_xor(ss, off);
+            bad |= __shfl_xor(int(bad), off) != 0;
+        }
+        const int sc = query_scale_exponent(m, bad);
+        const float scale = ldexpf(1.0f, sc);
+        float es = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t d = 256u * uint32_t(i) + 4u * uint32_t(lane);
+            if (d >= Dp) break;
+            const f32x4v sv = v[i] * scale;  // (zero past D)
+            const h4v h = __builtin_convertvector(sv, h4v);
+            *reinterpret_cast<h4v*>(out + d) = h;
+            const f32x4v ev = __builtin_convertvector(h, f32x4v) - sv;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) es = fmaf(ev[e], ev[e], es);
+        }
+        if (qerr) {
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) es += __shfl_xor(es, off);
+        }
+        if (lane == 0) {
+            const float inv = ldexpf(1.0f, -sc);
+            qinfo[qi] = make_float4(ss, sqrtf(ss), inv, c0 * 0x1p-25f * inv);
+            if (qerr) qerr[qi] = err_norm_up(es, D) * inv;
+        }
+        return;
+    }
     for (uint32_t d = lane; d < D; d += 64) {
         const float v = row[d];
         bad |= !(fabsf(v) <= FLT_MAX);
@@ -159,7 +215,6 @@ __global__ __launch_bounds__(256) void screen_prep_kernel(const float* __restric
     // At most 2^40, so that the scan's pre-test constants stay finite.
     const int sc = query_scale_exponent(m, bad);
     const float scale = ldexpf(1.0f, sc);
-    _Float16* out = qh + int64_t(qi) * Dp;
     float es = 0.0f;  // squared norm of the rounding error of the scaled query (differences exact)
     for (uint32_t d = lane; d < Dp; d += 64) {
         const float v = d < D ? row[d] * scale : 0.0f;
@@ -1436,8 +1491,9 @@ va_status build_shadow(va_context* ctx, const float* x, uint32_t N, uint32_t D, 
 va_status screen_prepare_queries(va_context* ctx, const float* q, uint32_t Q, uint32_t D, _Float16* qh,
                                  float4* qinfo, float c0, float* qerr) {
     if (Q == 0) return VA_OK;
+    const int vec = (D % 4 == 0) && ((reinterpret_cast<uintptr_t>(q) & 15) == 0);
     screen_prep_kernel<<<dim3((Q + 3) / 4), dim3(256), 0, ctx->stream>>>(q, int64_t(D), Q, D, padded_dim(D), qh, qinfo,
-                                                                       c0, qerr);
+                                                                       c0, qerr, vec, nullptr, 0u, nullptr, 0u);
     VA_CHECK_LAUNCH(ctx);
     return VA_OK;
 }
@@ -1547,8 +1603,10 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     VA_CHECK_STATUS(s.verify(need));
 
     // ---- 1. queries -> scaled fp16 ---------------------------------------------------------
+    // (also clears the scan's list counters and the overflow words: [0] overflowed queries, [1]
+    // longest rerank list)
     screen_prep_kernel<<<dim3((Q + 3) / 4), dim3(256), 0, ctx->stream>>>(in.q, int64_t(D), Q, D, Dp, qh, qinfo,
-                                                                       bnd.c0, nullptr);
+                                                                       bnd.c0, nullptr, 1, cnt, Q, ovf_cnt, 2u);
     VA_CHECK_LAUNCH(ctx);
 
     ScreenArgs sa;
@@ -1614,8 +1672,6 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
         VA_CHECK_STATUS(launch_select(ctx, sel));
     }
     // ---- 3. screening scan -------------------------------------------------------------------
-    VA_CHECK_STATUS(fill_u32(ctx, cnt, Q, 0));
-    VA_CHECK_STATUS(fill_u32(ctx, ovf_cnt, 2, 0));  // [0] overflowed queries, [1] longest rerank list
     VA_CHECK_STATUS(pm.mark(1));
     {
         ScreenArgs a = sa;
