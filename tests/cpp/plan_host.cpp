@@ -85,7 +85,7 @@ int main() {
                             for (uint32_t Dp : Dps) {
                                 const uint64_t rcap = screen_rerank_cap(N, k, p.cap);
                                 CHECK(rcap <= N && rcap >= std::min<uint64_t>(N, 2ull * k + 256), "rcap N=%u k=%u", N, k);
-                                const u128 sn = rnd(u128(Q) * 4) * 5 + rnd(256) + rnd(u128(Q) * 16) * 2 +
+                                const u128 sn = rnd(u128(Q) * 4) * 6 + rnd(256) + rnd(u128(Q) * 16) * 2 +
                                                 rnd(u128(Q) * Dp * 2) + rnd(u128(p.qs) * p.S * 4) + rnd(u128(p.S) * 4) +
                                                 rnd(u128(Q) * p.cap * 4) * 3 + rnd(u128(Q) * rcap * 4) * 2;
                                 CHECK(u128(screened_scan_need(Q, Dp, p, rcap)) == sn, "screened_scan_need Q=%u N=%u Dp=%u",

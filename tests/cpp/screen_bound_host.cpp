@@ -46,6 +46,13 @@ int sb_bounds_v(const float* b3, float dot, float qq, float nq, float eq, float 
     return va::screen_bounds_v(b, dot, qq, nq, eq, xx, nx, ex, lo_hi[0], lo_hi[1]) ? 1 : 0;
 }
 
+// every distance family with measured rounding errors (the flat screen's candidate intervals)
+int sb_bounds_m(const float* b3, int op, float dot, float qq, float nq, float eq, float xx, float nx, float ex,
+                float* lo_hi) {
+    const va::BoundV b{b3[0], b3[1], b3[2]};
+    return va::screen_bounds_m(b, op, dot, qq, nq, eq, xx, nx, ex, lo_hi[0], lo_hi[1]) ? 1 : 0;
+}
+
 // abce[0..3] = the pre-test's constants A, B, E, C for threshold key thr_key
 void sb_pretest_v(const float* b3, float qq, float nq, float eq, float inv, uint32_t thr_key, float* abce) {
     const va::BoundV b{b3[0], b3[1], b3[2]};

@@ -58,6 +58,8 @@ def sb(request, tmp_path_factory):
     lib.sb_bounds_v.argtypes = [fp] + [C.c_float] * 7 + [fp]
     lib.sb_bounds_v.restype = C.c_int
     lib.sb_pretest_v.argtypes = [fp] + [C.c_float] * 4 + [C.c_uint32, fp]
+    lib.sb_bounds_m.argtypes = [fp, C.c_int] + [C.c_float] * 7 + [fp]
+    lib.sb_bounds_m.restype = C.c_int
     return lib
 
 
@@ -341,3 +343,93 @@ def test_screen_v_is_tighter_on_typical_rows(sb):
         assert sb.sb_bounds_v(_fp(b3), F32(acc * inv), qq, nq, eq, xx, nx, ex, _fp(w1))
         ratios.append(float(w1[1] - w1[0]) / float(w0[1] - w0[0]))
     assert max(ratios) <= 0.65, ratios
+
+
+# ---- every distance family with measured rounding errors (the flat screen's candidate intervals) --
+@pytest.mark.parametrize("D", [4, 96, 1536])
+def test_screen_m_interval_is_nearly_reached(sb, D):
+    """The midpoint inputs of the measured-error test for every family: the fp32 keys stay inside
+    [lo, hi], and for cosine and -dot (whose error is the dot's alone) the farthest reaches 0.7 of
+    the half-width where the measured terms dominate (D up to 96), so dropping or halving the
+    query's or the row's measured term fails the containment."""
+    b3 = np.zeros(3, F32)
+    sb.sb_make_bound_v(D, _fp(b3))
+    mid = F32(1 + 2.0**-11 + 2.0**-20)
+    half = D // 2
+    q = np.full(D, mid, F32)
+    x = np.concatenate([np.full(half, mid, F32), np.full(D - half, 2 * mid, F32)])
+    inv, q16, qq, nq, eq = _prep_v(sb, q, D)
+    ex = _err_norm(sb, x, D)
+    acc = _sums((q16 * x.astype(np.float16).astype(F32)).astype(F32))[0]
+    for op in (L2SQ, L2, COS, NEG_DOT):
+        reach = 0.0
+        for xx in _sums(x * x):
+            nx = F32(np.sqrt(xx))
+            lohi = np.zeros(2, F32)
+            assert sb.sb_bounds_m(_fp(b3), op, F32(acc * inv), qq, nq, eq, xx, nx, ex, _fp(lohi))
+            lo, hi = (float(v) for v in lohi)
+            keys = [float(_key(op, d, q2, x2)) for d in _dots(q, x) for q2 in _sums(q * q) for x2 in _sums(x * x)]
+            assert all(lo <= k <= hi for k in keys), (op, lo, min(keys), max(keys), hi)
+            s = (lo + hi) / 2
+            reach = max(reach, max(abs(k - s) for k in keys) / ((hi - lo) / 2))
+        if D <= 96 and op in (COS, NEG_DOT):
+            assert reach >= 0.7, (op, D, reach)
+
+
+@pytest.mark.parametrize("D", [4, 96, 1536])
+def test_screen_m_contains_fp32_key(sb, D):
+    """The adversarial families: with the measured error norms every fp32 key of every family
+    (several summation orders of the dot and of both norms) lies in [lo, hi] for every order of
+    the screened accumulator, and the interval lies inside the worst-case one's reach (a pair the
+    worst-case bound cannot bound is not bounded here either, or its interval still holds)."""
+    rng = np.random.default_rng(3000 + D)
+    b3 = np.zeros(3, F32)
+    sb.sb_make_bound_v(D, _fp(b3))
+    checked = 0
+    for q, x in _cases(rng, D):
+        inv, q16, qq, nq, eq = _prep_v(sb, q, D)
+        ex = _err_norm(sb, x, D)
+        with np.errstate(over="ignore"):
+            x16 = x.astype(np.float16).astype(F32)
+        with np.errstate(all="ignore"):
+            accs = _sums((q16 * x16).astype(F32))
+        for op in (L2SQ, L2, COS, NEG_DOT):
+            for xx in _sums(x * x):
+                nx = F32(np.sqrt(xx))
+                keys = [_key(op, d, q2, x2) for d in _dots(q, x) for q2 in _sums(q * q)[:2] for x2 in _sums(x * x)[:2]]
+                for acc in accs:
+                    lohi = np.zeros(2, F32)
+                    if not sb.sb_bounds_m(_fp(b3), op, F32(acc * inv), qq, nq, eq, xx, nx, ex, _fp(lohi)):
+                        continue
+                    lo, hi = lohi
+                    for k in keys:
+                        if k == k:
+                            assert lo <= k <= hi, (op, D, float(lo), float(k), float(hi))
+                            checked += 1
+    assert checked > 1000
+
+
+def test_screen_m_cosine_is_tighter_on_typical_rows(sb):
+    """The point of measuring: on Gaussian rows at D = 1536 the cosine interval with measured
+    errors is at most 0.8 of the worst-case width (about 0.65: the fp32 accumulation terms, which
+    both share, dominate at this D)."""
+    D = 1536
+    rng = np.random.default_rng(11)
+    b4, b3 = np.zeros(4, F32), np.zeros(3, F32)
+    sb.sb_make_bound(D, _fp(b4))
+    sb.sb_make_bound_v(D, _fp(b3))
+    ratios = []
+    for _ in range(20):
+        q = rng.standard_normal(D).astype(F32)
+        x = (q + 3 * rng.standard_normal(D)).astype(F32)
+        inv, q16, qq, nq, c0q = _prep(sb, q, b4[2])
+        eq = _prep_v(sb, q, D)[4]
+        ex = _err_norm(sb, x, D)
+        acc = _sums((q16 * x.astype(np.float16).astype(F32)).astype(F32))[0]
+        xx = _sums(x * x)[0]
+        nx = F32(np.sqrt(xx))
+        w0, w1 = np.zeros(2, F32), np.zeros(2, F32)
+        assert sb.sb_bounds(COS, _fp(b4), F32(acc * inv), qq, nq, xx, nx, c0q, _fp(w0))
+        assert sb.sb_bounds_m(_fp(b3), COS, F32(acc * inv), qq, nq, eq, xx, nx, ex, _fp(w1))
+        ratios.append(float(w1[1] - w1[0]) / float(w0[1] - w0[0]))
+    assert max(ratios) <= 0.8, ratios

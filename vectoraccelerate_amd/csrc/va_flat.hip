@@ -159,7 +159,7 @@ struct F32Producer final : KeyProducer {
 // fixed scratch block too small for the device fallback.
 va_status flat_topk(va_context* ctx, DistOp op, const float* q, const float* x, uint32_t Q, uint32_t N, uint32_t D,
                     uint32_t k, uint32_t* out_idx, float* out_dist, const _Float16* shadow, const float* norms,
-                    const uint8_t* skip) {
+                    const uint8_t* skip, const float* errs) {
     F32Producer p;
     p.ctx = ctx;
     p.q = q;
@@ -182,6 +182,7 @@ va_status flat_topk(va_context* ctx, DistOp op, const float* q, const float* x, 
     si.op = op;
     si.xh = shadow;
     si.xn = norms;
+    si.xe = shadow ? errs : nullptr;
     if (screen_applies(ctx, si, k)) return screened_topk_scan(ctx, si, p, k, o);
     return exact_topk_scan(ctx, p, Q, N, k, o);
 }

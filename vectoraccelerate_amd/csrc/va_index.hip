@@ -31,6 +31,7 @@ struct va_index {
     float* rows = nullptr;          // [capacity x dim]
     _Float16* shadow = nullptr;     // [capacity x pitch]
     float* norms = nullptr;         // [capacity]
+    float* errs = nullptr;          // [capacity] upper bound of |fp16(x) - x| (the shadow's rounding)
     uint8_t* skip = nullptr;        // [capacity] 1 = deleted
     uint8_t* seen = nullptr;        // [capacity] filtered search: deleted or already examined
     uint32_t* slot_stable = nullptr;  // [capacity] stable id of each slot
@@ -74,9 +75,10 @@ __global__ void slots_to_handles_kernel(uint32_t* idx, uint64_t n, const uint32_
 
 // compaction: row keep[j] -> slot j of the new arrays (one workgroup per kept row)
 __global__ void gather_rows_kernel(const float* __restrict__ rows, const _Float16* __restrict__ shadow,
-                                   const float* __restrict__ norms, const uint32_t* __restrict__ slot_stable,
-                                   const uint32_t* __restrict__ keep, uint32_t n, uint32_t dim, uint32_t pitch,
-                                   float* __restrict__ rows2, _Float16* __restrict__ shadow2, float* __restrict__ norms2,
+                                   const float* __restrict__ norms, const float* __restrict__ errs,
+                                   const uint32_t* __restrict__ slot_stable, const uint32_t* __restrict__ keep,
+                                   uint32_t n, uint32_t dim, uint32_t pitch, float* __restrict__ rows2,
+                                   _Float16* __restrict__ shadow2, float* __restrict__ norms2, float* __restrict__ errs2,
                                    uint32_t* __restrict__ slot_stable2) {
     const uint32_t j = blockIdx.x;
     if (j >= n) return;
@@ -85,7 +87,10 @@ __global__ void gather_rows_kernel(const float* __restrict__ rows, const _Float1
     if (pitch)
         for (uint32_t d = threadIdx.x; d < pitch; d += 256) shadow2[uint64_t(j) * pitch + d] = shadow[uint64_t(s) * pitch + d];
     if (threadIdx.x == 0) {
-        if (pitch) norms2[j] = norms[s];
+        if (pitch) {
+            norms2[j] = norms[s];
+            errs2[j] = errs[s];
+        }
         slot_stable2[j] = slot_stable[s];
     }
 }
@@ -96,6 +101,7 @@ struct DevBuffers {
     float* rows = nullptr;
     _Float16* shadow = nullptr;
     float* norms = nullptr;
+    float* errs = nullptr;
     uint8_t* skip = nullptr;
     uint8_t* seen = nullptr;
     uint32_t* slot_stable = nullptr;
@@ -103,6 +109,7 @@ struct DevBuffers {
         (void)hipFree(rows);
         (void)hipFree(shadow);
         (void)hipFree(norms);
+        (void)hipFree(errs);
         (void)hipFree(skip);
         (void)hipFree(seen);
         (void)hipFree(slot_stable);
@@ -119,7 +126,8 @@ va_status alloc_buffers(va_context* ctx, uint64_t cap, uint32_t dim, uint32_t pi
     bool ok = get(reinterpret_cast<void**>(&b.rows), cap * dim * 4) && get(reinterpret_cast<void**>(&b.skip), cap) &&
               get(reinterpret_cast<void**>(&b.seen), cap) && get(reinterpret_cast<void**>(&b.slot_stable), cap * 4);
     if (ok && pitch)
-        ok = get(reinterpret_cast<void**>(&b.shadow), cap * pitch * 2) && get(reinterpret_cast<void**>(&b.norms), cap * 4);
+        ok = get(reinterpret_cast<void**>(&b.shadow), cap * pitch * 2) && get(reinterpret_cast<void**>(&b.norms), cap * 4) &&
+             get(reinterpret_cast<void**>(&b.errs), cap * 4);
     if (!ok) {
         b.release();
         return fail(ctx, VA_ERR_OOM, "index storage of %llu slots x %u dimensions: device allocation failed",
@@ -133,6 +141,7 @@ DevBuffers current(const va_index* ix) {
     b.rows = ix->rows;
     b.shadow = ix->shadow;
     b.norms = ix->norms;
+    b.errs = ix->errs;
     b.skip = ix->skip;
     b.seen = ix->seen;
     b.slot_stable = ix->slot_stable;
@@ -143,6 +152,7 @@ void install(va_index* ix, const DevBuffers& b, uint64_t cap) {
     ix->rows = b.rows;
     ix->shadow = b.shadow;
     ix->norms = b.norms;
+    ix->errs = b.errs;
     ix->skip = b.skip;
     ix->seen = b.seen;
     ix->slot_stable = b.slot_stable;
@@ -164,6 +174,7 @@ va_status reserve_slots(va_context* ctx, va_index* ix, uint64_t need) {
             VA_CHECK_HIP(ctx, hipMemcpyAsync(nb.shadow, ix->shadow, n * ix->pitch * 2, hipMemcpyDeviceToDevice,
                                              ctx->stream));
             VA_CHECK_HIP(ctx, hipMemcpyAsync(nb.norms, ix->norms, n * 4, hipMemcpyDeviceToDevice, ctx->stream));
+            VA_CHECK_HIP(ctx, hipMemcpyAsync(nb.errs, ix->errs, n * 4, hipMemcpyDeviceToDevice, ctx->stream));
         }
     }
     // the old buffers are freed once the copies (and any search still reading them) are done
@@ -331,7 +342,8 @@ va_status va_index_insert(va_context* ctx, va_index* index, const float* vectors
                                      hipMemcpyDeviceToDevice, ctx->stream));
     if (index->pitch)
         VA_CHECK_STATUS(va::build_shadow(ctx, index->rows + uint64_t(s0) * dim, n, dim,
-                                         index->shadow + uint64_t(s0) * index->pitch, index->norms + s0));
+                                         index->shadow + uint64_t(s0) * index->pitch, index->norms + s0, nullptr,
+                                         index->errs + s0));
     va::fill_byte_kernel<<<dim3(va::grid_for(n)), dim3(256), 0, ctx->stream>>>(index->skip + s0, n, 0);
     VA_CHECK_LAUNCH(ctx);
     va::iota_kernel<<<dim3(va::grid_for(n)), dim3(256), 0, ctx->stream>>>(index->slot_stable + s0, n, first);
@@ -390,8 +402,9 @@ va_status va_index_compact(va_context* ctx, va_index* index) {
         uint32_t* dkeep = sc.carve<uint32_t>(n);
         VA_CHECK_HIP(ctx, hipMemcpyAsync(dkeep, keep.data(), uint64_t(n) * 4, hipMemcpyHostToDevice, ctx->stream));
         va::gather_rows_kernel<<<dim3(n), dim3(256), 0, ctx->stream>>>(index->rows, index->shadow, index->norms,
-                                                                      index->slot_stable, dkeep, n, index->dim,
-                                                                      index->pitch, nb.rows, nb.shadow, nb.norms,
+                                                                      index->errs, index->slot_stable, dkeep, n,
+                                                                      index->dim, index->pitch, nb.rows, nb.shadow,
+                                                                      nb.norms, nb.errs,
                                                                       nb.slot_stable);
         VA_CHECK_LAUNCH(ctx);
     }
@@ -475,7 +488,8 @@ va_status va_index_search(va_context* ctx, const va_index* index, va_metric metr
     } else {
         VA_CHECK_STATUS(va::flat_topk(ctx, va::metric_op(metric), queries, index->rows, num_queries, index->slots,
                                       index->dim, k, out_handles, out_dist, index->pitch ? index->shadow : nullptr,
-                                      index->pitch ? index->norms : nullptr, index->deleted ? index->skip : nullptr));
+                                      index->pitch ? index->norms : nullptr, index->deleted ? index->skip : nullptr,
+                                      index->pitch ? index->errs : nullptr));
     }
     va::slots_to_handles_kernel<<<dim3(va::grid_for(total)), dim3(256), 0, ctx->stream>>>(out_handles, total,
                                                                                          index->slot_stable);
@@ -536,7 +550,8 @@ va_status va_index_search_filtered(va_context* ctx, va_index* index, va_metric m
         else
             VA_CHECK_STATUS(va::flat_topk(ctx, va::metric_op(metric), query, index->rows, 1, index->slots, index->dim,
                                           f, d_idx, d_dist, index->pitch ? index->shadow : nullptr,
-                                          index->pitch ? index->norms : nullptr, index->seen));
+                                          index->pitch ? index->norms : nullptr, index->seen,
+                                          index->pitch ? index->errs : nullptr));
         VA_CHECK_HIP(ctx, hipMemcpyAsync(h_idx.data(), d_idx, uint64_t(f) * 4, hipMemcpyDeviceToHost, ctx->stream));
         VA_CHECK_HIP(ctx, hipMemcpyAsync(h_dist.data(), d_dist, uint64_t(f) * 4, hipMemcpyDeviceToHost, ctx->stream));
         VA_CHECK_HIP(ctx, hipStreamSynchronize(ctx->stream));

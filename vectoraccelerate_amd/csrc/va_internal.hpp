@@ -574,19 +574,23 @@ struct ScreenInput {
     // filtering scan then reads it instead of converting x
     const _Float16* xh = nullptr;
     const float* xn = nullptr;
+    // optional with the shadow: xe[j] >= |fp16(x_j) - x_j| (build_shadow's errs); the candidates'
+    // intervals then use the measured rounding errors (narrower than the worst case)
+    const float* xe = nullptr;
 };
 // Exact top-k of device queries against a device database (va_fused_topk's body).  shadow /
 // norms: an fp16 shadow of x (see build_shadow) or nullptr; skip: rows excluded, or nullptr.
 va_status flat_topk(va_context* ctx, DistOp op, const float* q, const float* x, uint32_t Q, uint32_t N, uint32_t D,
                     uint32_t k, uint32_t* out_idx, float* out_dist, const _Float16* shadow = nullptr,
-                    const float* norms = nullptr, const uint8_t* skip = nullptr);
+                    const float* norms = nullptr, const uint8_t* skip = nullptr, const float* errs = nullptr);
 // Halves per row of an fp16 shadow (D rounded up to a multiple of 64).
 uint32_t shadow_pitch(uint32_t D);
 // shadow[r * shadow_pitch(D) + d] = fp16(x[r * D + d]) (RNE, zeros past D), norms[r] = |x_r|^2
 // in fp32, for rows r < N.  norm_err (may be nullptr; norms may then be nullptr): {|x_r|^2, an
-// upper bound of |fp16(x_r) - x_r|} per row (infinite past the fp16 range).
+// upper bound of |fp16(x_r) - x_r|} per row (infinite past the fp16 range); errs (may be
+// nullptr): that upper bound alone.
 va_status build_shadow(va_context* ctx, const float* x, uint32_t N, uint32_t D, _Float16* shadow, float* norms,
-                       float2* norm_err = nullptr);
+                       float2* norm_err = nullptr, float* errs = nullptr);
 // Pieces of the screened scan shared with the IVF list scan (va_screen.hip).  The bound itself
 // is va_screen_bound.hpp's.
 struct ScreenBound;

@@ -112,7 +112,7 @@ inline uint64_t screen_rerank_cap(uint32_t N, uint32_t k, uint64_t cap) {
 // screened_topk_scan (without the fallback); Dp = the fp16 row pitch in halves
 inline size_t screened_scan_need(uint32_t Q, uint32_t Dp, const ScanPlan& p, uint64_t rcap) {
     const size_t q4 = scratch_round(uint64_t(Q) * 4);
-    return q4 * 5 + scratch_round(256) + scratch_round(uint64_t(Q) * 16) * 2 + scratch_round(uint64_t(Q) * Dp * 2) +
+    return q4 * 6 + scratch_round(256) + scratch_round(uint64_t(Q) * 16) * 2 + scratch_round(uint64_t(Q) * Dp * 2) +
            scratch_round(uint64_t(p.qs) * p.S * 4) + scratch_round(p.S * 4) + scratch_round(uint64_t(Q) * p.cap * 4) * 3 +
            scratch_round(uint64_t(Q) * rcap * 4) * 2;
 }

@@ -106,6 +106,11 @@ struct ScreenArgs {
     uint32_t xstride = 1;
     // screen16_kernel: the pre-test constants of each query, {A, B, C, 2^-scale} (pretest_kernel)
     const float4* ptc = nullptr;
+    // the candidates' intervals with measured rounding errors (screen_bounds_m) when both are
+    // set: qerr[q] >= |fp16 image of q - q| (unscaled), xe[id] >= |fp16(x_id) - x_id|
+    const float* qerr = nullptr;
+    const float* xe = nullptr;
+    float vcn = 0, vgd = 0, vg2d = 0;  // make_bound_v's coefficients
 };
 
 // ---- bound of the screened key (va_screen_bound.hpp) --------------------------------------------
@@ -1213,7 +1218,8 @@ __global__ __launch_bounds__(256, 2) void screen16_small_kernel(ScreenArgs a) {
 // and their squared norms in fp32 (one wave per row) ----------------------------------------------
 __global__ __launch_bounds__(256) void shadow_kernel(const float* __restrict__ x, int64_t ldx, uint32_t N, uint32_t D,
                                                      uint32_t Dp, _Float16* __restrict__ xh, int64_t ldh,
-                                                     float* __restrict__ xn, int vec, float2* __restrict__ xne) {
+                                                     float* __restrict__ xn, int vec, float2* __restrict__ xne,
+                                                     float* __restrict__ xe) {
     const uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (r >= N) return;
@@ -1241,13 +1247,14 @@ __global__ __launch_bounds__(256) void shadow_kernel(const float* __restrict__ x
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-    if (xne) {
+    if (xne || xe) {
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) es += __shfl_xor(es, o);
     }
     if (lane == 0) {
         if (xn) xn[r] = ss;
         if (xne) xne[r] = make_float2(ss, err_norm_up(es, D));
+        if (xe) xe[r] = err_norm_up(es, D);
     }
 }
 
@@ -1259,11 +1266,27 @@ __global__ __launch_bounds__(256) void screen_bound_kernel(ScreenArgs a, float* 
     const uint32_t q = blockIdx.y;
     const float4 info = a.qinfo[q];
     const uint32_t m = cnt ? min(cnt[q], n) : n;
+    // lists with the measured rounding errors: narrower intervals than the worst case the scan's
+    // pre-test used (the list holds a superset of what they would admit)
+    const bool measured = cnt && a.xe && a.qerr;
+    const BoundV bv{a.vcn, a.vgd, a.vg2d};
+    const float eq = measured ? a.qerr[q] : 0.0f;
     for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < m; i += gridDim.x * 256) {
         const int64_t o = int64_t(q) * ld + i;
         const float xx = cnt ? xx_list[o] : xx_dense[i];
         uint32_t klo, khi;
-        screen_keys(a, dot[o], info.x, info.y, xx, sqrtf(xx), info.w, klo, khi);
+        if (measured) {
+            float lo, hi;
+            if (screen_bounds_m(bv, a.op, dot[o], info.x, info.y, eq, xx, sqrtf(xx), a.xe[a.cand_id[o]], lo, hi)) {
+                klo = key_of_float(lo);
+                khi = key_of_float(hi);
+            } else {
+                klo = 0u;
+                khi = 0xFFFFFFFEu;  // the NaN key
+            }
+        } else {
+            screen_keys(a, dot[o], info.x, info.y, xx, sqrtf(xx), info.w, klo, khi);
+        }
         reinterpret_cast<uint32_t*>(dot)[o] = khi;
         if (cnt) reinterpret_cast<uint32_t*>(xx_list)[o] = klo;
     }
@@ -1478,12 +1501,12 @@ bool offsets_fit(uint64_t ldx, uint32_t D) {
 uint32_t shadow_pitch(uint32_t D) { return padded_dim(D); }
 
 va_status build_shadow(va_context* ctx, const float* x, uint32_t N, uint32_t D, _Float16* shadow, float* norms,
-                       float2* norm_err) {
+                       float2* norm_err, float* errs) {
     if (N == 0) return VA_OK;
     const uint32_t Dp = padded_dim(D);
     const int vec = (D % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
     shadow_kernel<<<dim3((N + 3) / 4), dim3(256), 0, ctx->stream>>>(x, int64_t(D), N, D, Dp, shadow, int64_t(Dp),
-                                                                   norms, vec, norm_err);
+                                                                   norms, vec, norm_err, errs);
     VA_CHECK_LAUNCH(ctx);
     return VA_OK;
 }
@@ -1585,6 +1608,7 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     uint32_t* ovf_cnt = s.carve<uint32_t>(64);
     float4* qinfo = s.carve<float4>(Q);
     float4* ptc = s.carve<float4>(Q);
+    float* qerr = s.carve<float>(Q);
     _Float16* qh = s.carve<_Float16>(uint64_t(Q) * Dp);
     uint32_t* skeys = s.carve<uint32_t>(uint64_t(plan.qs) * S);
     float* sxx = s.carve<float>(S);
@@ -1605,8 +1629,10 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     // ---- 1. queries -> scaled fp16 ---------------------------------------------------------
     // (also clears the scan's list counters and the overflow words: [0] overflowed queries, [1]
     // longest rerank list)
+    const bool measured = in.xh && in.xe;  // the candidates' intervals from measured rounding errors
     screen_prep_kernel<<<dim3((Q + 3) / 4), dim3(256), 0, ctx->stream>>>(in.q, int64_t(D), Q, D, Dp, qh, qinfo,
-                                                                       bnd.c0, nullptr, 1, cnt, Q, ovf_cnt, 2u);
+                                                                       bnd.c0, measured ? qerr : nullptr, 1, cnt, Q,
+                                                                       ovf_cnt, 2u);
     VA_CHECK_LAUNCH(ctx);
 
     ScreenArgs sa;
@@ -1687,6 +1713,14 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
         a.cand_xx = reinterpret_cast<float*>(clo);
         a.cand_id = cid;
         a.cap = uint32_t(cap);
+        if (measured) {
+            const BoundV bv = make_bound_v(D);
+            a.qerr = qerr;
+            a.xe = in.xe;
+            a.vcn = bv.cn;
+            a.vgd = bv.gd;
+            a.vg2d = bv.g2d;
+        }
         if (in.xh) {
             a.xh = in.xh;
             a.xn = in.xn;

@@ -213,6 +213,52 @@ VA_HD inline bool screen_bounds_v(const BoundV& b, float dot, float qq, float nq
     return true;
 }
 
+// Every distance family with measured rounding errors.  K = |dot16 - dot32| bounded as in
+// screen_bounds_v (half its eq/ex part): the exact expansion of the fp16 roundings, the MFMA's
+// accumulation and the fp32 scan's own dot.  The key's interval then follows screen_bounds with
+// its worst-case dot terms (c1 |q||x| and the absolute floors, which the measured norms include)
+// replaced by K: cosine e = K / (|q||x|) + cn, -dot e = K, L2^2 e = cn (|q|^2 + |x|^2) + 2K (the
+// value screen_bounds_v uses).  The clamp of the cosine is 1-Lipschitz, the norms' two orders
+// and the key formula stay in cn, the final roundings as in screen_bounds.
+VA_HD inline bool screen_bounds_m(const BoundV& b, int op, float dot, float qq, float nq, float eq, float xx, float nx,
+                                  float ex, float& lo, float& hi) {
+    if (!(fabsf(dot) <= FLT_MAX) || !(eq <= FLT_MAX) || !(ex <= FLT_MAX) || !(qq <= FLT_MAX) || !(xx <= FLT_MAX))
+        return false;
+    const float k2 = fmaf(boundv_nx(b, nq, eq), nx, boundv_ex(b, nq, eq) * ex);  // 2K
+    float s, e;
+    switch (op) {
+        case SOP_COS_DIST: {
+            const float den = nq * nx;
+            if (!(den >= 0x1p-100f)) return false;  // near the FLT_MIN floor (or NaN)
+            const float raw = dot / den;
+            s = 1.0f - fminf(fmaxf(raw, -1.0f), 1.0f);
+            e = 0.5f * k2 / den + b.cn;
+            break;
+        }
+        case SOP_NEG_DOT:
+            s = -dot;
+            e = 0.5f * k2;
+            break;
+        default: {  // SOP_L2SQ, SOP_L2 (bounded in the squared domain first)
+            const float v = qq + xx - 2.0f * dot;
+            s = v < 0.0f ? 0.0f : v;
+            e = fmaf(b.cn, qq + xx, k2);
+            break;
+        }
+    }
+    e = fmaf(fmaf(0x1p-21f, fabsf(s), e), 1.0f + 0x1p-20f, 0x1p-126f);  // rounding of s and e
+    if (!(e <= FLT_MAX) || !(fabsf(s) <= FLT_MAX)) return false;
+    lo = s - e;
+    hi = s + e;
+    if (op == SOP_L2) {
+        lo = sqrtf(fmaxf(lo, 0.0f)) * (1.0f - 0x1p-22f);
+        hi = sqrtf(hi) * (1.0f + 0x1p-22f);
+    } else if (op == SOP_L2SQ) {
+        lo = fmaxf(lo, 0.0f);
+    }
+    return true;
+}
+
 // The pre-test of screen_bounds_v: a pair whose lower bound can be <= tau satisfies
 //     acc >= A |x|^2 + B |x| + E ex + C      (acc = the scaled fp16 dot, sig = 2^scale = 1/inv)
 // (from 2 dot >= |q|^2 + |x|^2 - e - tau, with the rounding room 2^-21 |s| <= 2^-21 (|tau| + e)
