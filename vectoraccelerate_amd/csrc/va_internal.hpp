@@ -346,6 +346,34 @@ __device__ inline uint32_t plan_tile_after(const ListPlan& p, uint32_t t, uint32
     rc = min(TN, n - rb * TN);
     return l;
 }
+// plan_tile_after with the list found by the whole wave: lane i tests list base + 1 + i, so a
+// tile within 64 lists of the last one found costs one load round instead of a gallop's and a
+// binary search's several dependent loads (a persistent workgroup's next tile is often tens of
+// lists on, most of them without tiles in its group).  Every lane of the wave must call it with
+// the same t and h (pre[h] <= t); every lane gets the same tile.
+__device__ inline uint32_t plan_tile_after_wave(const ListPlan& p, uint32_t t, uint32_t h, uint32_t TQ, uint32_t TN,
+                                                uint32_t& qs, uint32_t& qc, uint32_t& rs, uint32_t& rc) {
+    const uint32_t lane = __lane_id();
+    uint32_t base = h;  // pre[base] <= t
+    for (;;) {
+        const uint32_t l = base + 1u + lane;
+        const bool le = l < p.C && p.pre[l] <= t;  // a prefix of the lanes (pre is non-decreasing)
+        const uint32_t c = uint32_t(__popcll(__ballot(le)));
+        base += c;
+        if (c < 64u) break;
+    }
+    const uint32_t l = base, local = t - p.pre[l];
+    const uint32_t nq = p.qoff[l + 1] - p.qoff[l];
+    const uint32_t len = p.roff[l + 1] - p.roff[l];
+    const uint32_t n = p.sample ? ivf_sample_rows(len) : len;
+    const uint32_t nqb = (nq + TQ - 1) / TQ;
+    const uint32_t rb = local / nqb, qb = local % nqb;
+    qs = p.qoff[l] + qb * TQ;
+    qc = min(TQ, nq - qb * TQ);
+    rs = p.roff[l] + rb * TN;
+    rc = min(TN, n - rb * TN);
+    return l;
+}
 #endif
 
 struct DistArgs {

@@ -369,6 +369,7 @@ typedef float f32x16s __attribute__((ext_vector_type(16)));
 
 struct Ivf16Args {
     const _Float16* qh = nullptr;    // [Q x Dp] scaled fp16 queries (screen_prepare_queries)
+    uint32_t nq = 0;                 // Q
     const float4* qinfo = nullptr;   // {|q|^2, |q|, 2^-scale, c0q}
     const float* qerr = nullptr;     // [Q] bound of |fp16(q) - q| (unscaled)
     const uint32_t* qrow = nullptr;  // the plan's query lists
@@ -675,18 +676,24 @@ constexpr int NW = 8, MB = 2;
 constexpr int WR = 16 * MB;               // rows per wave per sub-tile
 constexpr int SUB = NW * WR;              // rows per sub-tile
 constexpr uint32_t DPMAX = 1024;          // the queries' LDS share: 64 x 1024 halves = 128 KiB
-// Two shapes: 96 queries x 512 rows where 96 fp16 query rows fit (padded d <= 768: a third
+// Two shapes: 96 queries x 1024 rows where 96 fp16 query rows fit (padded d <= 768: a third
 // fewer row fetches for a list probed by 97-192 queries, half for 65-96), else 64 x 1024.
 template <int NQB>
 struct Shape {
     static constexpr int TQ = 16 * NQB;
-    static constexpr int NSUB = NQB == 6 ? 2 : 4;  // sub-tiles per tile
+    static constexpr int NSUB = 4;  // sub-tiles per tile
     static constexpr uint32_t TN = uint32_t(SUB * NSUB);
-    static constexpr int LCAP = NQB == 6 ? 64 : 128;  // staged passes per wave
+    // staged passes per wave: at least 64, the most one ballot adds after a flush
+    static constexpr int LCAP = NQB == 6 ? 64 : 128;
+    static_assert(LCAP >= 64, "a flush must leave room for a whole wave's passes");
+    static_assert(TQ <= 256, "a staged pass keeps its query's tile index in one byte");
     // LDS: queries [TQ x Dp halves], row norms [TN float2], per query {A, B, E, C} and {inv, qi},
     // the stage lists
-    static uint32_t lds_bytes(uint32_t Dp) { return TQ * Dp * 2 + TN * 8 + TQ * 16 + TQ * 8 + NW * LCAP * 12; }
+    // (a staged pass: its value and CSR position, 4 bytes each, and its query's tile index, 1 byte)
+    static constexpr uint32_t lds_bytes(uint32_t Dp) { return TQ * Dp * 2 + TN * 8 + TQ * 16 + TQ * 8 + NW * LCAP * 9; }
 };
+static_assert(Shape<6>::lds_bytes(768) <= 160 * 1024 && Shape<4>::lds_bytes(DPMAX) <= 160 * 1024,
+              "one workgroup's LDS at the largest padded d of each shape");
 inline int nqb_for(uint32_t Dp) { return Dp <= 768 ? 6 : 4; }
 }  // namespace ivr
 
@@ -706,9 +713,9 @@ __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
     const float2* s_nrm = reinterpret_cast<const float2*>(nrm_b);
     float4* s_pt = reinterpret_cast<float4*>(nrm_b + TN * 8);
     float2* s_qv = reinterpret_cast<float2*>(nrm_b + TN * 8 + TQ * 16);
-    uint32_t* s_qi = reinterpret_cast<uint32_t*>(nrm_b + TN * 8 + TQ * 24) + wave * 3 * LCAP;
-    uint32_t* s_val = s_qi + LCAP;
+    uint32_t* s_val = reinterpret_cast<uint32_t*>(nrm_b + TN * 8 + TQ * 24 + wave * 9 * LCAP);
     uint32_t* s_pos = s_val + LCAP;
+    uint8_t* s_ql = reinterpret_cast<uint8_t*>(s_pos + LCAP);  // the pass's query in the tile (< TQ)
     const uint32_t lds0 = lds_addr_of(lds8);
     uint32_t lc = 0;  // staged passes (wave-uniform)
     // Appends the staged passes: count every pass, keep a query's first cap.
@@ -716,7 +723,7 @@ __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
         for (uint32_t b0 = 0; b0 < lc; b0 += 64) {
             const uint32_t e = b0 + uint32_t(lane);
             if (e < lc) {
-                const uint32_t qi = s_qi[e];
+                const uint32_t qi = __builtin_bit_cast(uint32_t, s_qv[s_ql[e]].y);
                 const uint32_t pos = atomicAdd(a.cnt + qi, 1u);
                 if (pos < a.cap) {
                     a.cand_dot[int64_t(qi) * a.cap + pos] = __builtin_bit_cast(float, s_val[e]);
@@ -732,6 +739,8 @@ __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
     uint32_t voff[MB];
 #pragma unroll
     for (int j = 0; j < MB; ++j) voff[j] = uint32_t(16 * j + r16) * rowb + 16u * uint32_t(g);
+    const __amdgpu_buffer_rsrc_t qres =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(a.qh), 0, int(a.nq * rowb), 0x00020000);
 
     // XCD-aware order: XCD x (workgroups b with b % 8 == x; gridDim.x is a multiple of 8) takes
     // the x-th eighth of the plan's tiles, which its workgroups walk together, so the query
@@ -743,7 +752,7 @@ __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
     uint32_t lh = 0;  // the list of this workgroup's previous tile
     for (uint32_t t = xcd * tpx + blockIdx.x / kXcds; t < tend; t += gridDim.x / kXcds) {
         uint32_t qs, qc, rs, rc;
-        lh = plan_tile_after(a.plan, t, lh, TQ, TN, qs, qc, rs, rc);
+        lh = plan_tile_after_wave(a.plan, t, lh, TQ, TN, qs, qc, rs, rc);
         __syncthreads();  // every wave is done with the previous tile's LDS
         // the tile's rows' {|x|^2, error} (past rc: zeros) by direct loads, and its queries,
         // chunk-major (16-byte chunk m of query r at m * CS + r * 16; past qc: zeros): thread
@@ -757,18 +766,23 @@ __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
             if (uint32_t(tid) < QT) {
                 const uint32_t r = uint32_t(tid) % TQ;
                 const bool qv = r < qc;
-                const uint4* src = reinterpret_cast<const uint4*>(a.qh + int64_t(qv ? a.qrow[qs + r] : 0u) * Dp);
-                // eight loads in flight before their stores (a loop of single load-store pairs
-                // waited a memory round trip per chunk)
-                for (uint32_t m0 = uint32_t(tid) / TQ; m0 < Dp / 8; m0 += 8 * QS) {
-                    uint4 v[8];
+                // buffer loads over all the fp16 queries (Q Dp 2 < 2^31 bytes): a query past qc or
+                // a chunk past the row reads zeros through the range check, so the loads are
+                // issued without branches and all in flight before their stores
+                const uint32_t qoff = qv ? a.qrow[qs + r] * rowb : kDmaSkip;
+                // (24 loads a thread cover a row at every shape: one round trip)
+                constexpr int NB = 24;
+                static_assert(NB * QS * 8 >= (TQ == 96 ? 768 : int(DPMAX)), "one batch per query row");
+                for (uint32_t m0 = uint32_t(tid) / TQ; m0 < Dp / 8; m0 += NB * QS) {
+                    uint4 v[NB];
 #pragma unroll
-                    for (int b = 0; b < 8; ++b) {
+                    for (int b = 0; b < NB; ++b) {
                         const uint32_t m = m0 + uint32_t(b) * QS;
-                        v[b] = qv && m < Dp / 8 ? src[m] : make_uint4(0u, 0u, 0u, 0u);
+                        v[b] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                             qres, m < Dp / 8 ? qoff + m * 16u : kDmaSkip, 0, 0));
                     }
 #pragma unroll
-                    for (int b = 0; b < 8; ++b) {
+                    for (int b = 0; b < NB; ++b) {
                         const uint32_t m = m0 + uint32_t(b) * QS;
                         if (m < Dp / 8) *reinterpret_cast<uint4*>(lds8 + m * CS + r * 16u) = v[b];
                     }
@@ -855,9 +869,20 @@ __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
             }
         };
         // A sub-tile's passes: lane (r16, g) holds query 16 u + r16 against rows 16 j + 4 g + v of
-        // the wave's 32 in acc[u][j][v]; the pre-test of the flat screen (flagged rows pass).
+        // the wave's 32 in acc[u][j][v]; the pre-test of the flat screen (flagged rows pass).  The
+        // rows' pre-test inputs are read once for all query blocks; a block with passes is staged
+        // by a loop over its eight values (one copy of the flush per block, not per value: the
+        // fully unrolled staging made the kernel's code several times larger).
         auto epilogue = [&]() {
             const uint32_t o = msub * SUB + w0;  // the wave's first row in the tile
+            float xxp[4 * MB], nxp[4 * MB], exp[4 * MB];
+            bool rin[4 * MB];
+#pragma unroll
+            for (int t = 0; t < 4 * MB; ++t) {
+                const uint32_t row = o + uint32_t(16 * (t >> 2) + 4 * g + (t & 3));
+                screen_norms(s_nrm[row], xxp[t], nxp[t], exp[t]);
+                rin[t] = row < rc;
+            }
 #pragma unroll
             for (int u = 0; u < NQB; ++u) {
                 const int ql = 16 * u + r16;
@@ -865,37 +890,33 @@ __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
                 const PreTestV pt = {p.x, p.y, p.z, p.w};
                 uint32_t mask = 0;
 #pragma unroll
-                for (int j = 0; j < MB; ++j)
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const uint32_t row = o + uint32_t(16 * j + 4 * g + v);
-                        float xxp, nxp, exp;
-                        screen_norms(s_nrm[row], xxp, nxp, exp);
-                        const bool pass = row < rc && !(acc[u][j][v] < pretest_rhs(pt, xxp, nxp, exp));
-                        mask |= uint32_t(pass) << (4 * j + v);
-                    }
+                for (int t = 0; t < 4 * MB; ++t) {
+                    const bool pass = rin[t] && !(acc[u][t >> 2][t & 3] < pretest_rhs(pt, xxp[t], nxp[t], exp[t]));
+                    mask |= uint32_t(pass) << t;
+                }
                 mask = uint32_t(ql) < qc ? mask : 0u;
                 if (!__ballot(mask != 0u)) continue;
                 const float2 qv = s_qv[ql];
                 const uint32_t qi = __builtin_bit_cast(uint32_t, qv.y);
+                float vals[4 * MB];
 #pragma unroll
-                for (int j = 0; j < MB; ++j)
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const bool pass = (mask >> (4 * j + v)) & 1u;
-                        const uint64_t mk = __ballot(pass);
-                        if (!mk) continue;
-                        const uint32_t n = uint32_t(__popcll(mk));
-                        if (lc + n > uint32_t(LCAP)) flush();  // wave-uniform
-                        if (pass) {
-                            const uint32_t e = lc + __builtin_amdgcn_mbcnt_hi(uint32_t(mk >> 32),
-                                                                             __builtin_amdgcn_mbcnt_lo(uint32_t(mk), 0u));
-                            s_qi[e] = qi;
-                            s_val[e] = __builtin_bit_cast(uint32_t, acc[u][j][v] * qv.x);
-                            s_pos[e] = rs + o + uint32_t(16 * j + 4 * g + v);
-                        }
-                        lc += n;
+                for (int t = 0; t < 4 * MB; ++t) vals[t] = acc[u][t >> 2][t & 3] * qv.x;
+#pragma unroll 1
+                for (int t = 0; t < 4 * MB; ++t) {
+                    const bool pass = (mask >> t) & 1u;
+                    const uint64_t mk = __ballot(pass);
+                    if (!mk) continue;
+                    const uint32_t n = uint32_t(__popcll(mk));
+                    if (lc + n > uint32_t(LCAP)) flush();  // wave-uniform
+                    if (pass) {
+                        const uint32_t e = lc + __builtin_amdgcn_mbcnt_hi(uint32_t(mk >> 32),
+                                                                         __builtin_amdgcn_mbcnt_lo(uint32_t(mk), 0u));
+                        s_ql[e] = uint8_t(ql);
+                        s_val[e] = __builtin_bit_cast(uint32_t, vals[t]);
+                        s_pos[e] = rs + o + uint32_t(16 * (t >> 2) + 4 * g + (t & 3));
                     }
+                    lc += n;
+                }
             }
         };
         const uint32_t steps = nsub * nsl;
@@ -915,8 +936,10 @@ __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
                     for (int j = 0; j < MB; ++j) acc[u][j] = f32x4s{0.f, 0.f, 0.f, 0.f};
             }
         }
+        // a staged pass names its query by the tile's index, which the next tile's setup
+        // reassigns: the stage empties with the tile
+        flush();
     }
-    flush();
 }
 
 // Tile shapes and their cost model: shape_for / group_tile (va_plan.hpp, shared with the host
@@ -1477,6 +1500,7 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
     VA_CHECK_STATUS(screen_prepare_queries(ctx, queries, Q, D, qh, qinfo, bnd.c0, qerr));
     Ivf16Args a;
     a.qh = qh;
+    a.nq = Q;
     a.qinfo = qinfo;
     a.qerr = qerr;
     a.xh = ivf->shadow;
