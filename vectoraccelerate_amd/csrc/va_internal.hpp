@@ -625,8 +625,10 @@ struct ScreenBound;
 // qh[q * shadow_pitch(D) + d] = fp16(q[q * D + d] * 2^sc_q) (the query's scale puts its largest
 // entry in [2^14, 2^15)), qinfo[q] = {|q|^2, |q|, 2^-sc_q, c0 * 2^-25 * 2^-sc_q}; qerr (may be
 // nullptr): an upper bound of the norm of the (unscaled) rounding error of each query's fp16 image.
+// zero0[0 .. n0) and zero1[0 .. n1) are cleared by the same launch (a search's counters).
 va_status screen_prepare_queries(va_context* ctx, const float* q, uint32_t Q, uint32_t D, _Float16* qh,
-                                 float4* qinfo, float c0, float* qerr = nullptr);
+                                 float4* qinfo, float c0, float* qerr = nullptr, uint32_t* zero0 = nullptr,
+                                 uint32_t n0 = 0, uint32_t* zero1 = nullptr, uint32_t n1 = 0);
 // Candidate lists of screened pairs, in place: (unscaled fp16 dot, |x|^2) -> (key of the upper
 // bound, key of the lower bound) of the pair's fp32 key, for i < min(cnt[q], cap).
 va_status screen_list_bounds(va_context* ctx, const ScreenBound& b, const float4* qinfo, float* dot, float* xx,

@@ -1434,7 +1434,7 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
 
     Scratch s(ctx);
     const size_t q4 = Scratch::round(uint64_t(Q) * 4);
-    const size_t need = q4 * 6 + Scratch::round(256) + Scratch::round(uint64_t(Q) * 16) +
+    const size_t need = q4 * 5 + Scratch::round(uint64_t(Q) * 8) + Scratch::round(256) + Scratch::round(uint64_t(Q) * 16) +
                         Scratch::round(uint64_t(Q) * Dp * 2) + Scratch::round(pairs * 4) * 2 +
                         Scratch::round(uint64_t(C) * 4) * 2 + Scratch::round((uint64_t(C) + 1) * 4) +
                         Scratch::round(uint64_t(2 * kGroups) * C * 4) +
@@ -1443,7 +1443,9 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
                         fb_bytes(Q, id_span, k, ivf->N);
     VA_CHECK_STATUS(s.reserve(need));
     uint32_t* thr = s.carve<uint32_t>(Q);
-    uint32_t* cnt = s.carve<uint32_t>(Q);
+    // list counts: [0, Q) the sample pass's, [Q, 2Q) the full pass's (both cleared by the prep)
+    uint32_t* const cnt2 = s.carve<uint32_t>(uint64_t(Q) * 2);
+    uint32_t* cnt = cnt2;
     uint32_t* ubound = s.carve<uint32_t>(Q);
     uint32_t* rcount = s.carve<uint32_t>(Q);
     uint32_t* ovf_rows = s.carve<uint32_t>(Q);
@@ -1497,7 +1499,7 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
     VA_CHECK_STATUS(pm.mark(0));
     // ---- 0. plan and queries --------------------------------------------------------------------
     VA_CHECK_STATUS(plan_on_device(ctx, dp));
-    VA_CHECK_STATUS(screen_prepare_queries(ctx, queries, Q, D, qh, qinfo, bnd.c0, qerr));
+    VA_CHECK_STATUS(screen_prepare_queries(ctx, queries, Q, D, qh, qinfo, bnd.c0, qerr, cnt2, 2 * Q, ovf_cnt, 2));
     Ivf16Args a;
     a.qh = qh;
     a.nq = Q;
@@ -1513,7 +1515,6 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
     a.cand_pos = cpos;
     // ---- 1. sample: tau_q = k-th smallest upper bound of the sampled pairs ----------------------
     VA_CHECK_STATUS(fill_u32(ctx, thr, Q, 0xFFFFFFFFu));
-    VA_CHECK_STATUS(fill_u32(ctx, cnt, Q, 0));
     a.cap = uint32_t(cap_s);
     VA_CHECK_STATUS(run_screen_pass(ctx, dp, 0, a));
     VA_CHECK_STATUS(bounds(cap_s));
@@ -1530,8 +1531,8 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
         VA_CHECK_STATUS(launch_select(ctx, sel));
     }
     // ---- 2. screen, 3. U_q (overflowed queries are listed) ---------------------------------------
-    VA_CHECK_STATUS(fill_u32(ctx, cnt, Q, 0));
-    VA_CHECK_STATUS(fill_u32(ctx, ovf_cnt, 2, 0));
+    cnt = cnt2 + Q;
+    a.cnt = cnt;
     a.cap = uint32_t(cap);
     VA_CHECK_STATUS(pm.mark(1));
     VA_CHECK_STATUS(run_screen_pass(ctx, dp, 1, a));

@@ -1512,11 +1512,12 @@ va_status build_shadow(va_context* ctx, const float* x, uint32_t N, uint32_t D, 
 }
 
 va_status screen_prepare_queries(va_context* ctx, const float* q, uint32_t Q, uint32_t D, _Float16* qh,
-                                 float4* qinfo, float c0, float* qerr) {
+                                 float4* qinfo, float c0, float* qerr, uint32_t* zero0, uint32_t n0, uint32_t* zero1,
+                                 uint32_t n1) {
     if (Q == 0) return VA_OK;
     const int vec = (D % 4 == 0) && ((reinterpret_cast<uintptr_t>(q) & 15) == 0);
     screen_prep_kernel<<<dim3((Q + 3) / 4), dim3(256), 0, ctx->stream>>>(q, int64_t(D), Q, D, padded_dim(D), qh, qinfo,
-                                                                       c0, qerr, vec, nullptr, 0u, nullptr, 0u);
+                                                                       c0, qerr, vec, zero0, n0, zero1, n1);
     VA_CHECK_LAUNCH(ctx);
     return VA_OK;
 }
