@@ -155,6 +155,17 @@ def run_ceiling(ctx):
     from vectoraccelerate_amd import _lib
 
     out = {}
+    # the LDS read bandwidth the screens' fragment reads draw on (bytes per clock per CU)
+    r = _lib.ProbeResult()
+    ctx.check(ctx.lib.va_probe_mfma(ctx.handle, _lib.VA_PROBE_LDS, 1, 20000, C.byref(r)), "va_probe_mfma")
+    import torch
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    bpc = r.ops_per_second / (cus * r.engine_mhz * 1e6) if r.engine_mhz else None
+    out["lds_read"] = {"tb_per_s": r.ops_per_second / 1e12, "engine_mhz": r.engine_mhz, "bytes_per_clk_per_cu": bpc,
+                       "cus": cus, "ms": r.ms}
+    log(f"LDS read (ds_read_b128, 8 waves per CU): {r.ops_per_second / 1e12:.1f} TB/s = "
+        f"{bpc:.0f} B/clk per CU at {r.engine_mhz:.0f} MHz")
     for name, kind, peak_key, iters in PROBES:
         row = {"datasheet_peak": PEAK[peak_key], "unit": "TOP/s" if name == "int8" else "TFLOP/s"}
         for rnd, label in ((1, "random"), (0, "constant")):
@@ -292,9 +303,10 @@ def run_c2(ctx, a, cpu: bool, extra_l2: bool):
                        "rerank of a proven band)" if screened else "dist_gemm_kernel<4, 1, true, 2, true, false> (fp32 scan)"),
             "algorithmic": f"2*Q*N*D = {flops:.4g} FLOP per launch",
             "fp32_mfma_equivalent_frac": tflops / PEAK["fp32_mfma_tflops"],
-            "power_limited_ceiling": ("a register-only loop of the same fp16 MFMA on random operands runs at "
-                                      "~1.5 PFLOP/s = 0.6 of the 2.5 PFLOP/s peak on this board (constant "
-                                      "operands: 0.84); see DESIGN.md"),
+            "power_limited_ceiling": ("a register-only loop of the same fp16 MFMA on random operands (the "
+                                      "measured_ceiling below, probed in this run) runs at 0.6-0.66 of the "
+                                      "2.5 PFLOP/s peak with the engine clock at 1.6-1.65 GHz; the scan runs "
+                                      "its LDS reads at about 160 of the ~225 B/clk per CU the LDS delivers"),
         },
     }
     log(f"configs[1] cosine top-100 (index search): {ms:.3f} ms/step = {res['qps']:.0f} QPS; scan "

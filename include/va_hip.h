@@ -435,7 +435,7 @@ va_status va_pq_search(va_context* ctx, const float* queries, uint32_t num_queri
                        uint32_t K, const float* codebooks, const uint8_t* codes, uint32_t num_vectors, uint32_t k,
                        uint32_t* out_idx, float* out_dist);
 
-/* ---- measurement: the matrix-core ceiling of the board ------------------------------------------
+/* ---- measurement: the matrix-core ceiling of the board (and its LDS read bandwidth) -------------
  * No reference counterpart (the reference publishes no hardware peaks).  Every SIMD runs two waves
  * of back-to-back MFMAs of one instruction on register operands (no memory traffic), random or
  * constant (the clock falls further on random bits), `iterations` rounds of 8 MFMAs per wave,
@@ -446,7 +446,9 @@ typedef enum {
     VA_PROBE_FP32 = 0, /* v_mfma_f32_32x32x2_f32: the fp32 distance GEMM */
     VA_PROBE_FP16 = 1, /* v_mfma_f32_32x32x16_f16: the fp16 screens */
     VA_PROBE_INT8 = 2, /* v_mfma_i32_32x32x32_i8: the int8 scan */
-    VA_PROBE_FP4 = 3   /* v_mfma_scale_f32_32x32x64_f8f6f4 on fp4 operands: the Hamming scan */
+    VA_PROBE_FP4 = 3,  /* v_mfma_scale_f32_32x32x64_f8f6f4 on fp4 operands: the Hamming scan */
+    VA_PROBE_LDS = 4   /* ds_read_b128 of 1 KiB per wave, bank-conflict free, 8 per round (no MFMA):
+                        * the LDS read bandwidth the scans' fragment reads draw on; ops = bytes */
 } va_probe_kind;
 typedef struct {
     double ops_per_second; /* dense operations per second sustained */

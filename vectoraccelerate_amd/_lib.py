@@ -39,6 +39,7 @@ VA_PROBE_FP32 = 0
 VA_PROBE_FP16 = 1
 VA_PROBE_INT8 = 2
 VA_PROBE_FP4 = 3
+VA_PROBE_LDS = 4
 
 _p = C.c_void_p
 _u32 = C.c_uint32

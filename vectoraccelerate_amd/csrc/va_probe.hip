@@ -101,6 +101,31 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(uint32_t iters, int rnd
         pr_clock_end(c0, w0, clocks);
         for (int j = 0; j < kAcc; ++j)
             for (int v = 0; v < 16; ++v) z += float(acc[j][v]);
+    } else if constexpr (KIND == VA_PROBE_LDS) {
+        // 8 KiB of LDS per wave (the workgroup's 32 KiB), each lane's 16 bytes at lane * 16 of a
+        // 1 KiB row: consecutive lanes on consecutive banks.  The reads are asm volatile so that
+        // the loop is not folded away; their results are xor-ed so that they stay live.
+        __shared__ __attribute__((aligned(16))) uint32_t buf[8192];
+        for (int i = threadIdx.x; i < 8192; i += 256) buf[i] = rnd ? pr_next(s) : 0x3F800000u;
+        __syncthreads();
+        const uint32_t addr = uint32_t(reinterpret_cast<uintptr_t>(buf)) + uint32_t(threadIdx.x & 63) * 16u +
+                              uint32_t(threadIdx.x >> 6) * 8192u;
+        pr_i4 x = {0, 0, 0, 0};
+        pr_clock_begin(c0, w0);
+        for (uint32_t it = 0; it < iters; ++it) {
+            pr_i4 v0, v1, v2, v3, v4, v5, v6, v7;
+            asm volatile(
+                "ds_read_b128 %0, %8 offset:0\n\tds_read_b128 %1, %8 offset:1024\n\t"
+                "ds_read_b128 %2, %8 offset:2048\n\tds_read_b128 %3, %8 offset:3072\n\t"
+                "ds_read_b128 %4, %8 offset:4096\n\tds_read_b128 %5, %8 offset:5120\n\t"
+                "ds_read_b128 %6, %8 offset:6144\n\tds_read_b128 %7, %8 offset:7168\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=v"(v0), "=v"(v1), "=v"(v2), "=v"(v3), "=v"(v4), "=v"(v5), "=v"(v6), "=v"(v7)
+                : "v"(addr));
+            x ^= v0 ^ v1 ^ v2 ^ v3 ^ v4 ^ v5 ^ v6 ^ v7;
+        }
+        pr_clock_end(c0, w0, clocks);
+        z = float(x[0] ^ x[1] ^ x[2] ^ x[3]);
     } else {
         // fp4 (e2m1) operands of the scaled 32x32x64 MFMA, unit scales (format 4 = fp4 on both sides)
         pr_i8 a[4], b[4];
@@ -132,6 +157,7 @@ double ops_per_mfma(int kind) {
         case VA_PROBE_FP32: return 2.0 * 32 * 32 * 2;
         case VA_PROBE_FP16: return 2.0 * 32 * 32 * 16;
         case VA_PROBE_INT8: return 2.0 * 32 * 32 * 32;
+        case VA_PROBE_LDS: return 1024.0;  // bytes of one wave's ds_read_b128
         default: return 2.0 * 32 * 32 * 64;
     }
 }
@@ -143,7 +169,7 @@ extern "C" va_status va_probe_mfma(va_context* ctx, va_probe_kind kind, int rand
                                    va_probe_result* out) {
     if (!ctx) return VA_ERR_INVALID_ARG;
     VA_REQUIRE(ctx, out != nullptr, "va_probe_mfma: NULL output");
-    VA_REQUIRE(ctx, kind >= VA_PROBE_FP32 && kind <= VA_PROBE_FP4, "va_probe_mfma: unknown kind %d", int(kind));
+    VA_REQUIRE(ctx, kind >= VA_PROBE_FP32 && kind <= VA_PROBE_LDS, "va_probe_mfma: unknown kind %d", int(kind));
     VA_REQUIRE(ctx, iterations >= 1 && iterations <= (1u << 24), "va_probe_mfma: iterations %u out of range",
                iterations);
     va::DeviceGuard g(ctx->device);
@@ -179,6 +205,10 @@ extern "C" va_status va_probe_mfma(va_context* ctx, va_probe_kind kind, int rand
             case VA_PROBE_INT8:
                 va::mfma_probe_kernel<VA_PROBE_INT8><<<grid, 256, 0, ctx->stream>>>(iterations, random_operands, sink,
                                                                                     clocks);
+                break;
+            case VA_PROBE_LDS:
+                va::mfma_probe_kernel<VA_PROBE_LDS><<<grid, 256, 0, ctx->stream>>>(iterations, random_operands, sink,
+                                                                                   clocks);
                 break;
             default:
                 va::mfma_probe_kernel<VA_PROBE_FP4><<<grid, 256, 0, ctx->stream>>>(iterations, random_operands, sink,
