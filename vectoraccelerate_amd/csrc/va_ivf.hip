@@ -383,6 +383,9 @@ struct Ivf16Args {
     uint32_t* cand_pos = nullptr;    // CSR positions
     uint32_t cap = 0;
     ListPlan plan;
+    // per plan slot (qlist order): {A, B, E, C} and {2^-scale, query id} (ivf16_big_kernel)
+    const float4* gpt = nullptr;
+    const float2* gqv = nullptr;
 };
 
 // pre-test inputs of a row: rows whose entries can leave the fp16 range are flagged NaN (their
@@ -897,7 +900,6 @@ __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
                 mask = uint32_t(ql) < qc ? mask : 0u;
                 if (!__ballot(mask != 0u)) continue;
                 const float2 qv = s_qv[ql];
-                const uint32_t qi = __builtin_bit_cast(uint32_t, qv.y);
                 float vals[4 * MB];
 #pragma unroll
                 for (int t = 0; t < 4 * MB; ++t) vals[t] = acc[u][t >> 2][t & 3] * qv.x;
@@ -942,6 +944,452 @@ __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
     }
 }
 
+// ---- lists probed by many queries: LDS-staged 32x32x16 tiles ------------------------------------
+// A list probed by more than ivb::kMinQueries queries is, for its probing queries, a small flat
+// database, so the full pass gives it the flat screen's layout (screen16_kernel): a workgroup tile
+// of 192 of its queries x 256 of its rows, twelve waves of 64 x 64 (2 x 2 blocks of
+// v_mfma_f32_32x32x16_f16, three waves per SIMD), both operands moved global -> LDS by direct
+// loads, the queries gathered through the plan's list of the list's probing queries.  One row
+// fetch serves up to 192 queries (configs[4]'s 642K-row list probed by ~170 queries is read once
+// instead of twice by the 96-query tiles).  Unlike the flat screen's rows, which its neighbouring
+// query blocks share through L2, a list's rows come from HBM once, so the stages are a ring of
+// NSLOT slots of KC d-values with NSLOT - 1 stages in flight while one computes.  The tile's
+// pre-test constants come from the plan-slot table (ivf_slot_pretest_kernel: one load per query,
+// no gather) and its rows' {|x|^2, error bound} with one load per row, both loaded at the tile's
+// start and used after its main loop.  The epilogue is the flat screen's (a quick rejection per
+// lane and 32-row block from a box of the rows' pre-test inputs, the rest through LDS) with the
+// list pre-test A|x|^2 + B|x| + E ex + C and (value, CSR position) appends.
+namespace ivb {
+constexpr int NQB = 2, MB = 2;  // a wave: 32 NQB queries x 32 MB rows
+template <int WAVES, int TQ, int KC, int NSLOT>
+struct Shape {
+    static constexpr int WQ = 32 * NQB, WN = 32 * MB;
+    static constexpr int QW = TQ / WQ;            // waves along the queries
+    static constexpr int TN = WN * (WAVES / QW);  // rows per tile
+    static constexpr int ROWB = KC * 2;           // bytes of a row in a stage
+    static constexpr int CPR = KC / 8;            // 16-byte chunks per row
+    static constexpr int RPG = 64 / CPR;          // rows per 1 KiB direct-load group (one per lane chunk)
+    // chunk swizzle: the rows that share a 256-byte LDS line (16 / CPR of them) spread one chunk
+    // column over the line, so a fragment read of 16 lanes touches every bank once
+    static constexpr int SWS = CPR == 8 ? 1 : CPR == 4 ? 2 : 3;  // log2(16 / CPR)
+    static constexpr int OPQ = TQ * ROWB, OPX = TN * ROWB, STAGE = OPQ + OPX, LDS = NSLOT * STAGE;
+    // 1 KiB direct-load groups per stage: GQ of queries, GX of rows; a wave issues up to LPW of
+    // each and at least LMIN loads in all
+    static constexpr int GQ = OPQ / 1024, GX = OPX / 1024;
+    static constexpr int LPW = ((GQ > GX ? GQ : GX) + WAVES - 1) / WAVES, LMIN = GQ / WAVES + GX / WAVES;
+    // the next tile's first EARLY stages load during the epilogue; the epilogue's dump (4 KiB per
+    // wave) takes the slots after them
+    static constexpr int EARLY = NSLOT - (WAVES * 4096 + STAGE - 1) / STAGE;
+    static_assert(KC % 16 == 0 && (CPR == 8 || CPR == 4 || CPR == 2), "stage width");
+    static_assert(QW * WQ == TQ && WAVES % QW == 0 && TN % RPG == 0 && TQ % RPG == 0, "wave layout");
+    static_assert(64 * WAVES >= TN && 64 * WAVES >= TQ, "one thread per row and query");
+    static_assert(EARLY >= 1 && NSLOT >= 2 && NSLOT <= 4, "ring: the epilogue's dump and one early stage");
+    static_assert(LMIN >= 1 && 3 * LMIN < 64, "wait counts");
+};
+constexpr int kWaves = 12, kTQ = 192, kKC = 32, kSlots = 4;
+using Big = Shape<kWaves, kTQ, kKC, kSlots>;
+constexpr uint32_t kMinQueries = 96;  // (the 96-query tiles read a list once up to 96 queries)
+}  // namespace ivb
+
+// {A, B, E, C} and {2^-scale, query id} of every slot of the plan's query lists (qlist order), so
+// a tile of a list's queries loads its constants with one load per query.
+__global__ __launch_bounds__(256) void ivf_slot_pretest_kernel(BoundV b, const uint32_t* __restrict__ qlist,
+                                                              const uint32_t* __restrict__ total, uint32_t n,
+                                                              const float4* __restrict__ qinfo,
+                                                              const float* __restrict__ qerr,
+                                                              const uint32_t* __restrict__ thr, float4* __restrict__ gpt,
+                                                              float2* __restrict__ gqv) {
+    const uint32_t m = min(*total, n);
+    for (uint32_t j = blockIdx.x * 256 + threadIdx.x; j < m; j += gridDim.x * 256) {
+        const uint32_t qi = qlist[j];
+        const float4 inf = qinfo[qi];
+        const PreTestV pt = pretest_v(b, inf.x, inf.y, qerr[qi], inf.z, thr[qi]);
+        gpt[j] = make_float4(pt.A, pt.B, pt.E, pt.C);
+        gqv[j] = make_float2(inf.z, __builtin_bit_cast(float, qi));
+    }
+}
+
+// wait until at most m stages' loads (LMIN per stage and wave) are in flight, m < 4
+template <int LMIN>
+__device__ __forceinline__ void wait_stages(uint32_t m) {
+    if (m >= 3) wait_vmcnt<3 * LMIN>();
+    else if (m == 2) wait_vmcnt<2 * LMIN>();
+    else if (m == 1) wait_vmcnt<LMIN>();
+    else wait_vmcnt<0>();
+}
+
+template <int WAVES, int TQ, int KC, int NSLOT>
+__global__ __launch_bounds__(64 * WAVES, 1) void ivf16_big_kernel(Ivf16Args a) {
+    using namespace ivb;
+    using Sh = Shape<WAVES, TQ, KC, NSLOT>;
+    constexpr int WQ = Sh::WQ, WN = Sh::WN, QW = Sh::QW, TN = Sh::TN, ROWB = Sh::ROWB, CPR = Sh::CPR;
+    constexpr int RPG = Sh::RPG, SWS = Sh::SWS, OPQ = Sh::OPQ, STAGE = Sh::STAGE, GQ = Sh::GQ, GX = Sh::GX;
+    constexpr int LPW = Sh::LPW, LMIN = Sh::LMIN, EARLY = Sh::EARLY;
+    constexpr int KS = KC / 16;  // k-steps per stage
+    typedef float f32x16v __attribute__((ext_vector_type(16)));
+    typedef float f32x4v __attribute__((ext_vector_type(4)));
+    extern __shared__ __attribute__((aligned(1024))) char lds[];
+    __shared__ __attribute__((aligned(16))) float norms[3 * TN];  // pre-test inputs xx, nx, ex (NaN: flagged)
+    __shared__ float4 gbox[TN / 4];  // per 4-row group {xx lo, xx hi, nx lo, nx hi}, x NaN if a row is flagged
+    __shared__ float2 gbe[TN / 4];   // {ex lo, ex hi}
+    __shared__ float4 ptl[TQ];       // {A, B, E, C} of the tile's queries
+    __shared__ float2 pqv[TQ];       // {2^-scale, query id}
+    __shared__ uint32_t tcount[TQ];  // the tile's passes per query (zero between tiles)
+    __shared__ uint32_t tbase[TQ];   // their first position in the query's candidate list
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wq = wave % QW, wn = wave / QW, l32 = lane & 31, hh = lane >> 5;
+    const uint32_t nst = a.Dp / KC, rowb = a.Dp * 2u;
+    if (tid < TQ) tcount[tid] = 0u;  // (published by the tile loop's barriers)
+    float* xxp = norms;
+    float* nxp = norms + TN;
+    float* exq = norms + 2 * TN;
+
+    // Tiles: XCD x (workgroups b with b % 8 == x; gridDim.x is a multiple of 8) walks the x-th
+    // eighth of the group's plan tiles, so the row blocks of a list run on one XCD and the list's
+    // queries stay in its L2.
+    const uint32_t total = a.plan.pre[a.plan.C];
+    const uint32_t tpx = (total + kXcds - 1) / kXcds, xcd = blockIdx.x % kXcds;
+    const uint32_t tend = min(total, (xcd + 1) * tpx), tstep = gridDim.x / kXcds;
+    // The list of the last tile located (wave-uniform, the same in every wave): a tile of the
+    // same list is located without a load.
+    uint32_t cl = 0, cpre0 = 0, cpre1 = 0, cq0 = 0, cnq = 0, cr0 = 0, cn = 0;
+    auto locate = [&](uint32_t t, uint32_t& qs, uint32_t& qc, uint32_t& rs, uint32_t& rc) {
+        if (t >= cpre1) {  // (t only grows; the first call: cpre1 = 0)
+            uint32_t q_, c_, r_, n_;
+            cl = __builtin_amdgcn_readfirstlane(plan_tile_after_wave(a.plan, t, cl, TQ, TN, q_, c_, r_, n_));
+            cpre0 = __builtin_amdgcn_readfirstlane(a.plan.pre[cl]);
+            cpre1 = __builtin_amdgcn_readfirstlane(a.plan.pre[cl + 1]);
+            cq0 = __builtin_amdgcn_readfirstlane(a.plan.qoff[cl]);
+            cnq = __builtin_amdgcn_readfirstlane(a.plan.qoff[cl + 1]) - cq0;
+            cr0 = __builtin_amdgcn_readfirstlane(a.plan.roff[cl]);
+            const uint32_t len = __builtin_amdgcn_readfirstlane(a.plan.roff[cl + 1]) - cr0;
+            cn = a.plan.sample ? ivf_sample_rows(len) : len;
+        }
+        const uint32_t local = t - cpre0, nqb = (cnq + TQ - 1) / TQ;
+        const uint32_t rb = local / nqb, qb = local % nqb;
+        qs = cq0 + qb * uint32_t(TQ);
+        qc = min(uint32_t(TQ), cnq - qb * uint32_t(TQ));
+        rs = cr0 + rb * uint32_t(TN);
+        rc = min(uint32_t(TN), cn - rb * uint32_t(TN));
+    };
+
+    // Direct loads: wave w fills 1 KiB groups g = w + WAVES i (rows RPG g .. RPG g + RPG - 1) of
+    // each operand; lane L loads row RPG g + L / CPR at physical chunk L % CPR = logical chunk
+    // (L % CPR) ^ ((row >> SWS) % CPR).  Query rows past qc and list rows past rc read nothing
+    // (zeros).
+    auto swz_of = [](uint32_t row) { return (row >> SWS) & uint32_t(CPR - 1); };
+    uint32_t xoff[LPW], qoff[LPW], qnext[LPW];
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+        const uint32_t row = uint32_t(RPG * (wave + WAVES * i) + lane / CPR);
+        xoff[i] = row * rowb + 16u * ((uint32_t(lane) % CPR) ^ swz_of(row));
+    }
+    // the query rows' offsets of a tile (qrow loads; used when its stages are issued)
+    auto query_offsets = [&](uint32_t qs, uint32_t qc, uint32_t(&o)[LPW]) {
+#pragma unroll
+        for (int i = 0; i < LPW; ++i) {
+            const int g = wave + WAVES * i;
+            const uint32_t row = uint32_t(RPG * g + lane / CPR);
+            const bool in = (GQ == LPW * WAVES || g < GQ) && row < qc;
+            o[i] = in ? a.qrow[qs + row] * rowb + 16u * ((uint32_t(lane) % CPR) ^ swz_of(row)) : kDmaSkip;
+        }
+    };
+    const dma_rsrc qres = make_dma_rsrc(a.qh, a.nq * rowb);
+    const uint32_t lds0 = lds_addr_of(lds);
+    // stage s of a tile into slot s % NSLOT (stages past the row's end are not issued)
+    auto issue_with = [&](const dma_rsrc& xr, const uint32_t(&qo)[LPW], uint32_t s) {
+        const uint32_t d0 = s * KC;
+        const uint32_t sb = lds0 + (s % NSLOT) * uint32_t(STAGE);
+#pragma unroll
+        for (int i = 0; i < LPW; ++i) {
+            const int g = wave + WAVES * i;  // wave-uniform
+            if (GQ == LPW * WAVES || g < GQ)
+                lds_dma16(qres, qo[i] != kDmaSkip ? qo[i] + d0 * 2u : kDmaSkip, sb + uint32_t(g) * 1024u);
+            if (GX == LPW * WAVES || g < GX) lds_dma16(xr, xoff[i] + d0 * 2u, sb + uint32_t(OPQ + g * 1024));
+        }
+    };
+    // fragment rows start at multiples of 32, a multiple of the swizzle's period
+    const uint32_t swz = swz_of(uint32_t(l32));
+    const uint32_t a_off = uint32_t(OPQ + (wn * WN + l32) * ROWB);
+    const uint32_t b_off = uint32_t((wq * WQ + l32) * ROWB);
+    f32x16v acc[MB][NQB];
+    h8v fa[2][MB], fb[2][NQB];
+    auto read_frags = [&](int buf, uint32_t slot, int t) {
+        const char* base = lds + slot * STAGE;
+        const uint32_t ko = 16u * ((uint32_t(2 * t + hh)) ^ swz);
+#pragma unroll
+        for (int m = 0; m < MB; ++m) fa[buf][m] = *reinterpret_cast<const h8v*>(base + a_off + m * 32 * ROWB + ko);
+#pragma unroll
+        for (int n = 0; n < NQB; ++n) fb[buf][n] = *reinterpret_cast<const h8v*>(base + b_off + n * 32 * ROWB + ko);
+    };
+    auto mma = [&](int buf) {
+#pragma unroll
+        for (int m = 0; m < MB; ++m)
+#pragma unroll
+            for (int n = 0; n < NQB; ++n)
+                acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[buf][m], fb[buf][n], acc[m][n], 0, 0, 0);
+    };
+    auto interleave = [&]() {
+#pragma unroll
+        for (int i = 0; i < MB * NQB; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (i < MB + NQB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+    };
+    // workgroup barrier without the release fence of __syncthreads (which would also wait for
+    // the direct loads in flight); this wave's LDS reads are complete before it
+    auto barrier = [&]() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+    auto row_of = [&](int t) { return wn * WN + 32 * (t >> 4) + 8 * ((t >> 2) & 3) + 4 * hh + (t & 3); };
+    using Mask = uint32_t;  // bit t: value t of a query block (16 MB values)
+    static_assert(16 * MB <= 32, "one mask word per query block");
+    // the epilogue's LDS: 4 KiB per wave in the slots after the EARLY ones
+    f32x4v* dump = reinterpret_cast<f32x4v*>(lds + EARLY * STAGE + wave * 4096) + lane;  // [c][lane], c < 4
+
+    uint32_t t = xcd * tpx + blockIdx.x / kXcds;
+    if (t >= tend) return;
+    uint32_t qs, qc, rs, rc;
+    locate(t, qs, qc, rs, rc);
+    query_offsets(qs, qc, qoff);
+    dma_rsrc xres = make_dma_rsrc(a.xh + int64_t(rs) * a.Dp, rc * rowb);
+    // later tiles: stages 0 .. EARLY - 1 are loaded during the previous epilogue
+    for (uint32_t s = 0; s < uint32_t(EARLY) && s < nst; ++s) issue_with(xres, qoff, s);
+    while (t < tend) {
+        // the next tile (located now: a tile of another list waits for its plan entries here,
+        // where this tile's first stages are in flight anyway) and its query rows' offsets,
+        // loaded during this tile
+        const uint32_t tn = t + tstep;
+        uint32_t nqs = 0, nqc = 0, nrs = 0, nrc = 0;
+        if (tn < tend) {
+            locate(tn, nqs, nqc, nrs, nrc);
+            query_offsets(nqs, nqc, qnext);
+        }
+        // this tile's pre-test inputs: loaded now, used after the main loop
+        const float2 xn_t = tid < TN && uint32_t(tid) < rc ? a.xn[rs + uint32_t(tid)] : make_float2(0.0f, 0.0f);
+        const bool qin = tid < TQ && uint32_t(tid) < qc;
+        const float4 pt_t = qin ? a.gpt[qs + uint32_t(tid)] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float2 qv_t = qin ? a.gqv[qs + uint32_t(tid)] : make_float2(0.0f, 0.0f);
+#pragma unroll
+        for (int m = 0; m < MB; ++m)
+#pragma unroll
+            for (int n = 0; n < NQB; ++n)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[m][n][v] = 0.0f;
+        // every wave is past the previous tile's epilogue (its dump is read)
+        barrier();
+        const uint32_t ahead = min(uint32_t(NSLOT), nst);  // stages in flight before the main loop
+        for (uint32_t s = uint32_t(EARLY); s < ahead; ++s) issue_with(xres, qoff, s);
+        wait_stages<LMIN>(ahead - 1);  // stage 0 (the oldest)
+        barrier();
+        read_frags(0, 0, 0);
+        for (uint32_t s = 0; s < nst; ++s) {
+            const uint32_t slot = s % NSLOT;
+#pragma unroll
+            for (int k = 0; k < KS; ++k) {
+                const int cur = k & 1;
+                if (k < KS - 1) {
+                    read_frags(cur ^ 1, slot, k + 1);
+                    mma(cur);
+                    interleave();
+                } else {
+                    // this k-step's fragments are in registers: wait for stage s + 1 (the stages
+                    // after it stay in flight), publish it, and refill slot s with stage s + NSLOT
+                    const uint32_t after = s + 2 < nst ? min(nst - (s + 2), uint32_t(NSLOT - 2)) : 0u;
+                    wait_stages<LMIN>(after);
+                    barrier();
+                    if (s + NSLOT < nst) issue_with(xres, qoff, s + NSLOT);
+                    read_frags(cur ^ 1, (s + 1) % NSLOT, 0);
+                    mma(cur);
+                    interleave();
+                }
+            }
+        }
+        wait_vmcnt<0>();
+
+        if (tid < TN) {
+            float x2, x1, xe;
+            screen_norms(xn_t, x2, x1, xe);
+            xxp[tid] = x2;
+            nxp[tid] = x1;
+            exq[tid] = xe;
+        }
+        if (tid < TQ) {
+            ptl[tid] = pt_t;
+            pqv[tid] = qv_t;
+        }
+        __syncthreads();  // every wave is past the main loop: every slot is free
+        // the pre-test inputs' box of each 4-row group (NaN x when a row of it is flagged)
+        if (tid < TN / 4) {
+            float4 b = {INFINITY, -INFINITY, INFINITY, -INFINITY};
+            float2 e = {INFINITY, -INFINITY};
+            bool f = false;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float x2 = xxp[4 * tid + v], x1 = nxp[4 * tid + v], xe = exq[4 * tid + v];
+                f |= !(x2 == x2) || !(x1 == x1) || !(xe == xe);
+                b.x = fminf(b.x, x2);
+                b.y = fmaxf(b.y, x2);
+                b.z = fminf(b.z, x1);
+                b.w = fmaxf(b.w, x1);
+                e.x = fminf(e.x, xe);
+                e.y = fmaxf(e.y, xe);
+            }
+            if (f) b.x = __builtin_nanf("");
+            gbox[tid] = b;
+            gbe[tid] = e;
+        }
+        __syncthreads();
+
+        // ---- epilogue: lane (l32, hh) holds query wq*WQ + 32n + l32 against rows
+        // wn*WN + 32m + 8j + 4hh + e in acc[m][n][4j + e]; t = 16m + 4j + e indexes its 16 MB values.
+        // 1. the passes of each query block as a bit mask (quick rejection from registers, else the
+        //    values through the wave's dump); 2. each lane pair's count added to its query's tile
+        //    count in LDS (the returned value is the pair's offset in the query's share of the tile);
+        // 3. one global atomic per query of the tile reserves its share of the candidate list (a
+        //    list probed by many queries appends for most of them in every tile, so per-wave atomics
+        //    and their waits were most of the tile's time); 4. the next tile's first stages; 5. the
+        //    appends.  No returning global operation is waited for after the next tile's loads are
+        //    issued (that wait would also wait for them).
+        Mask valid = ~Mask(0);
+        if (rc < uint32_t(TN)) {
+            valid = 0;
+#pragma unroll 1
+            for (int v = 0; v < 16 * MB; ++v) valid |= Mask(uint32_t(row_of(v)) < rc) << v;
+        }
+        float bxlo = INFINITY, bxhi = -INFINITY, bnlo = INFINITY, bnhi = -INFINITY, belo = INFINITY, behi = -INFINITY;
+        bool bflag = false;
+#pragma unroll
+        for (int c = 0; c < 4 * MB; ++c) {
+            const int gi = row_of(4 * c) >> 2;  // rows 4c .. 4c + 3 of the lane: one group
+            const float4 b = gbox[gi];
+            const float2 e = gbe[gi];
+            bflag |= !(b.x == b.x);
+            bxlo = fminf(bxlo, b.x);
+            bxhi = fmaxf(bxhi, b.y);
+            bnlo = fminf(bnlo, b.z);
+            bnhi = fmaxf(bnhi, b.w);
+            belo = fminf(belo, e.x);
+            behi = fmaxf(behi, e.y);
+        }
+        // row block m of query block n into the dump: values 16m .. 16m + 15
+        auto dump_half = [&](auto NC, auto MC) {
+            constexpr int n = decltype(NC)::value, m = decltype(MC)::value;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                f32x4v v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = acc[m][n][4 * c + e];
+                dump[c * 64] = v;
+            }
+            asm volatile("" ::: "memory");  // re-read the dump from LDS below
+        };
+        auto mask_of = [&](auto NC) -> Mask {
+            constexpr int n = decltype(NC)::value;
+            const uint32_t qt = uint32_t(wq * WQ + 32 * n + l32);
+            const float4 p = ptl[qt];
+            const PreTestV pt = {p.x, p.y, p.z, p.w};
+            bool skip = qt >= qc;
+            if (!bflag && !skip) {
+                // the right-hand side over the lane's rows is bounded below at the box corner that
+                // the signs of A, B and E select (each fma is monotone in its operands)
+                const float lo = fmaf(pt.A, pt.A >= 0.0f ? bxlo : bxhi,
+                                      fmaf(pt.B, pt.B >= 0.0f ? bnlo : bnhi, fmaf(pt.E, pt.E >= 0.0f ? belo : behi, pt.C)));
+                float mx = -INFINITY;
+#pragma unroll
+                for (int v = 0; v < 16 * MB; ++v) mx = fmaxf(mx, acc[v >> 4][n][v & 15]);
+                skip = mx < lo;
+            }
+            Mask mk = 0;
+            if (!skip) {
+                auto test_half = [&](auto MC) {
+                    constexpr int m = decltype(MC)::value;
+                    dump_half(NC, MC);
+#pragma unroll 2
+                    for (int c = 0; c < 4; ++c) {
+                        const int r = row_of(16 * m + 4 * c);
+                        const f32x4v x2 = *reinterpret_cast<const f32x4v*>(xxp + r);
+                        const f32x4v x1 = *reinterpret_cast<const f32x4v*>(nxp + r);
+                        const f32x4v xe = *reinterpret_cast<const f32x4v*>(exq + r);
+                        const f32x4v v = dump[c * 64];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            mk |= Mask(!(v[e] < pretest_rhs(pt, x2[e], x1[e], xe[e]))) << (16 * m + 4 * c + e);
+                    }
+                };
+                test_half(std::integral_constant<int, 0>());
+                test_half(std::integral_constant<int, 1>());
+                mk &= valid;
+            }
+            return mk;
+        };
+        const Mask mk0 = mask_of(std::integral_constant<int, 0>());
+        const Mask mk1 = mask_of(std::integral_constant<int, 1>());
+        // 2. the pair's offset in its query's share of the tile (lane l32 adds both halves' passes)
+        uint32_t off0 = 0, off1 = 0;
+        {
+            const uint32_t c0 = uint32_t(__popc(mk0)), c1 = uint32_t(__popc(mk1));
+            const uint32_t o0 = uint32_t(__shfl_xor(int(c0), 32)), o1 = uint32_t(__shfl_xor(int(c1), 32));
+            uint32_t b0 = 0, b1 = 0;
+            if (hh == 0 && c0 + o0) b0 = atomicAdd(&tcount[wq * WQ + l32], c0 + o0);
+            if (hh == 0 && c1 + o1) b1 = atomicAdd(&tcount[wq * WQ + 32 + l32], c1 + o1);
+            off0 = uint32_t(__shfl(int(b0), l32)) + (hh ? o0 : 0u);
+            off1 = uint32_t(__shfl(int(b1), l32)) + (hh ? o1 : 0u);
+        }
+        __syncthreads();
+        // 3. the tile's share of each query's candidate list
+        if (tid < TQ) {
+            const uint32_t n = tcount[tid];
+            uint32_t base = 0;
+            if (n) base = atomicAdd(a.cnt + __builtin_bit_cast(uint32_t, pqv[tid].y), n);
+            tbase[tid] = base;
+            tcount[tid] = 0u;  // (read above; cleared for the next tile)
+        }
+        __syncthreads();
+        // 4. the next tile's first stages, during the appends
+        if (tn < tend) {
+#pragma unroll
+            for (int i = 0; i < LPW; ++i) qoff[i] = qnext[i];
+            xres = make_dma_rsrc(a.xh + int64_t(nrs) * a.Dp, nrc * rowb);
+            for (uint32_t s = 0; s < uint32_t(EARLY) && s < nst; ++s) issue_with(xres, qoff, s);
+        }
+        // 5. the appends (stores only)
+        auto append = [&](auto NC, Mask mk, uint32_t off) {
+            constexpr int n = decltype(NC)::value;
+            if (!__ballot(mk != 0u)) return;
+            const uint32_t qt = uint32_t(wq * WQ + 32 * n + l32);
+            const float2 qv = pqv[qt];
+            const uint32_t qi = __builtin_bit_cast(uint32_t, qv.y);
+            uint32_t pos = tbase[qt] + off;
+            const float* src = reinterpret_cast<const float*>(dump);
+            auto append_half = [&](auto MC) {
+                constexpr int m = decltype(MC)::value;
+                uint32_t mh = (mk >> (16 * m)) & 0xFFFFu;
+                if (!__ballot(mh != 0u)) return;
+                dump_half(NC, MC);
+                while (mh && pos < a.cap) {
+                    const int c16 = __builtin_ctz(mh);
+                    mh &= mh - 1;
+                    const int r = row_of(16 * m + c16);
+                    const int64_t o = int64_t(qi) * a.cap + pos;
+                    a.cand_dot[o] = src[(c16 >> 2) * 256 + (c16 & 3)] * qv.x;
+                    a.cand_pos[o] = rs + uint32_t(r);
+                    ++pos;
+                }
+            };
+            append_half(std::integral_constant<int, 0>());
+            append_half(std::integral_constant<int, 1>());
+        };
+        append(std::integral_constant<int, 0>(), mk0, off0);
+        append(std::integral_constant<int, 1>(), mk1, off1);
+        t = tn;
+        qs = nqs;
+        qc = nqc;
+        rs = nrs;
+        rc = nrc;
+    }
+    wait_vmcnt<0>();
+}
+
 // Tile shapes and their cost model: shape_for / group_tile (va_plan.hpp, shared with the host
 // planning tests).
 static_assert(ivfs::TQ == kSmallTileQueries && ivfs::TN == kSmallTileRows, "16-query tile of ivf_small_kernel");
@@ -960,6 +1408,8 @@ struct DevPlan {
     uint32_t screen = 0;        // tile groups of the screened scan (iv16) instead of the fp32 shapes
     uint32_t wide_tn = 0;       // screened scan: rows and queries per tile of the last group in the
     uint32_t wide_tq = 0;       // full pass (ivf16_resq_kernel's tiles; 0: the wide tiles' 128 x 64)
+    uint32_t big_tq = 0;        // screened scan, full pass: lists probed by more than ivb::kMinQueries
+    uint32_t big_tn = 0;        // queries go to group 3 (ivf16_big_kernel's tiles; 0: off)
     uint32_t* P = nullptr;      // [Q x np] probes with repeats / sentinels replaced by ~0
     uint32_t* qcnt = nullptr;   // [C] queries per list
     uint32_t* qoff = nullptr;   // [C + 1]
@@ -1033,7 +1483,11 @@ __global__ __launch_bounds__(256) void plan_counts_kernel(DevPlan p) {
             group_tile(g, TQ, TN);
         }
         for (int pass = 0; pass < 2; ++pass) {
-            if (p.screen && g == 2 && pass == 1 && p.wide_tn) {
+            if (p.screen && pass == 1 && p.big_tq && nq > ivb::kMinQueries) {
+                g = 3;
+                TN = p.big_tn;
+                TQ = p.big_tq;
+            } else if (p.screen && g == 2 && pass == 1 && p.wide_tn) {
                 TN = p.wide_tn;
                 TQ = p.wide_tq;
             }
@@ -1121,13 +1575,30 @@ va_status run_planned_pass(va_context* ctx, const DevPlan& dp, int pass, const f
 // narrow tiles on the context's stream and the wide ones on auxiliary streams (they meet only
 // in the per-query atomics of the candidate lists).
 va_status run_screen_pass(va_context* ctx, const DevPlan& dp, int pass, Ivf16Args a) {
-    VA_CHECK_STATUS(aux_fork(ctx));
+    static_assert(kGroups > 3, "group 3 of the plan: the lists of ivf16_big_kernel");
     a.qrow = dp.qlist;
     a.plan.qoff = dp.qoff;
     a.plan.roff = dp.roff;
     a.plan.C = dp.C;
     a.plan.sample = pass == 0 ? 1u : 0u;
     va_status st = VA_OK;
+    VA_CHECK_STATUS(aux_fork(ctx));
+    if (pass == 1 && dp.big_tq) {
+        // on the context's stream, ahead of the narrow tiles, while the wide groups start on the
+        // auxiliary streams
+        using Big = ivb::Big;
+        Ivf16Args b = a;
+        b.plan.pre = dp.pre + (int64_t(pass) * kGroups + 3) * (int64_t(dp.C) + 1);
+        auto kern = &ivf16_big_kernel<ivb::kWaves, ivb::kTQ, ivb::kKC, ivb::kSlots>;
+        const uint32_t lds = uint32_t(Big::LDS);
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                int(lds)) != hipSuccess)
+            st = fail(ctx, VA_ERR_HIP, "ivf16_big_kernel: %u bytes of LDS refused", lds);
+        else
+            kern<<<dim3(std::max<uint32_t>(kXcds, uint32_t(ctx->num_cus) / kXcds * kXcds)), dim3(64 * ivb::kWaves), lds,
+               ctx->stream>>>(b);
+        if (hipGetLastError() != hipSuccess) st = fail(ctx, VA_ERR_HIP, "ivf16_big_kernel launch failed");
+    }
     for (int g = 0; g < iv16::kGroupsUsed && st == VA_OK; ++g) {
         a.plan.pre = dp.pre + (int64_t(pass) * kGroups + g) * (int64_t(dp.C) + 1);
         const hipStream_t s = g == 0 ? ctx->stream : ctx->aux[g - 1];
@@ -1398,6 +1869,15 @@ bool ivf_resq_applies(const va_context* ctx, uint32_t Q, uint32_t Dp) {
 #endif
     return VA_IVF_RESQ && ctx->opt_screen != 1 && Dp <= ivr::DPMAX && uint64_t(Q) * Dp * 2 <= kDmaMaxBytes;
 }
+// The full pass of the screened scan sends lists probed by more than ivb::kMinQueries queries to
+// ivf16_big_kernel (its direct loads address every fp16 query through one descriptor).
+bool ivf_big_applies(const va_context* ctx, uint32_t Q, uint32_t Dp) {
+#ifndef VA_IVF_BIG
+#define VA_IVF_BIG 1
+#endif
+    return VA_IVF_BIG && ctx->opt_screen != 1 && Q > ivb::kMinQueries && uint64_t(Q) * Dp * 2 <= kDmaMaxBytes &&
+           Dp % uint32_t(ivb::kKC) == 0;
+}
 
 // The screened list scan serves an index with an fp16 shadow whose lists can take the 16-query
 // tiles (their keys are replayed in the rerank), unless VA_OPT_SCREEN turns it off.
@@ -1440,7 +1920,8 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
                         Scratch::round(uint64_t(2 * kGroups) * C * 4) +
                         Scratch::round(uint64_t(2 * kGroups) * (uint64_t(C) + 1) * 4) +
                         Scratch::round(uint64_t(Q) * cand * 4) * 3 + Scratch::round(uint64_t(Q) * rcap * 4) * 3 +
-                        fb_bytes(Q, id_span, k, ivf->N);
+                        fb_bytes(Q, id_span, k, ivf->N) +
+                        (ivf_big_applies(ctx, Q, Dp) ? Scratch::round(pairs * 16) + Scratch::round(pairs * 8) : 0);
     VA_CHECK_STATUS(s.reserve(need));
     uint32_t* thr = s.carve<uint32_t>(Q);
     // list counts: [0, Q) the sample pass's, [Q, 2Q) the full pass's (both cleared by the prep)
@@ -1466,6 +1947,10 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
         dp.wide_tn = n6 ? ivr::Shape<6>::TN : ivr::Shape<4>::TN;
         dp.wide_tq = n6 ? uint32_t(ivr::Shape<6>::TQ) : uint32_t(ivr::Shape<4>::TQ);
     }
+    if (ivf_big_applies(ctx, Q, Dp)) {
+        dp.big_tq = uint32_t(ivb::kTQ);
+        dp.big_tn = uint32_t(ivb::Big::TN);
+    }
     dp.P = s.carve<uint32_t>(pairs);
     dp.qlist = s.carve<uint32_t>(pairs);
     dp.qcnt = s.carve<uint32_t>(C);
@@ -1483,6 +1968,8 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
     fb.n_rows = ovf_cnt;
     fb.rows = ovf_rows;
     fb.skip = skip;
+    float4* gpt = dp.big_tq ? s.carve<float4>(pairs) : nullptr;
+    float2* gqv = dp.big_tq ? s.carve<float2>(pairs) : nullptr;
     VA_CHECK_STATUS(s.verify(need));
     uint32_t* chi = reinterpret_cast<uint32_t*>(cdot);
     auto bounds = [&](uint64_t cp) -> va_status {
@@ -1534,6 +2021,15 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
     cnt = cnt2 + Q;
     a.cnt = cnt;
     a.cap = uint32_t(cap);
+    if (dp.big_tq) {
+        // the pre-test constants of every plan slot, for the tiles of ivf16_big_kernel
+        const uint32_t blocks = uint32_t(std::min<uint64_t>(1024, (pairs + 255) / 256));
+        ivf_slot_pretest_kernel<<<dim3(blocks), dim3(256), 0, ctx->stream>>>(make_bound_v(D), dp.qlist, dp.qoff + C,
+                                                                            uint32_t(pairs), qinfo, qerr, thr, gpt, gqv);
+        VA_CHECK_LAUNCH(ctx);
+        a.gpt = gpt;
+        a.gqv = gqv;
+    }
     VA_CHECK_STATUS(pm.mark(1));
     VA_CHECK_STATUS(run_screen_pass(ctx, dp, 1, a));
     VA_CHECK_STATUS(pm.mark(2));
@@ -1579,7 +2075,7 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
         sel.rows = Q;
         VA_CHECK_STATUS(launch_select(ctx, sel));
     }
-    ctx->last_scan.scan_launches = iv16::kGroupsUsed;
+    ctx->last_scan.scan_launches = iv16::kGroupsUsed + (dp.big_tq ? 1 : 0);
     ctx->last_scan.candidate_cap = uint32_t(cap);
     ctx->last_scan.screened = 1;
     VA_CHECK_STATUS(pm.count_sum(rcount, Q));

@@ -798,9 +798,10 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
         const uint32_t sb = lds0 + (s & 1u) * uint32_t(STAGE);
 #pragma unroll
         for (int i = 0; i < LPW; ++i) {
-            const int g = wave + WAVES * i;  // wave-uniform; a compile-time true test when WAVES divides
-            if (GQ % WAVES == 0 || g < GQ) lds_dma16(qr, ok ? off[i] + d0 * 2u : kDmaSkip, sb + uint32_t(g) * 1024u);
-            if (GX % WAVES == 0 || g < GX)
+            const int g = wave + WAVES * i;  // wave-uniform; compile-time true when the waves' LPW loads
+                                             // cover exactly the operand's groups
+            if (GQ == LPW * WAVES || g < GQ) lds_dma16(qr, ok ? off[i] + d0 * 2u : kDmaSkip, sb + uint32_t(g) * 1024u);
+            if (GX == LPW * WAVES || g < GX)
                 lds_dma16(xr, ok ? off[i] + d0 * 2u : kDmaSkip, sb + uint32_t(OPQ + g * 1024));
         }
     };
