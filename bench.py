@@ -166,6 +166,13 @@ def run_ceiling(ctx):
                        "cus": cus, "ms": r.ms}
     log(f"LDS read (ds_read_b128, 8 waves per CU): {r.ops_per_second / 1e12:.1f} TB/s = "
         f"{bpc:.0f} B/clk per CU at {r.engine_mhz:.0f} MHz")
+    # the HBM read bandwidth the HBM-bound scans draw on: a 4 GiB streaming read
+    r = _lib.ProbeResult()
+    ctx.check(ctx.lib.va_probe_mfma(ctx.handle, _lib.VA_PROBE_HBM, 1, 4096, C.byref(r)), "va_probe_mfma")
+    out["hbm_read"] = {"gb_per_s": r.ops_per_second / 1e9, "frac_of_datasheet": r.ops_per_second / 1e9 / PEAK["hbm_gbs"],
+                       "bytes": r.ops, "ms": r.ms, "engine_mhz": r.engine_mhz}
+    log(f"HBM read (16-byte loads, 4 GiB): {r.ops_per_second / 1e9:.0f} GB/s = "
+        f"{100 * r.ops_per_second / 1e9 / PEAK['hbm_gbs']:.1f}% of {PEAK['hbm_gbs']:.0f}")
     for name, kind, peak_key, iters in PROBES:
         row = {"datasheet_peak": PEAK[peak_key], "unit": "TOP/s" if name == "int8" else "TFLOP/s"}
         for rnd, label in ((1, "random"), (0, "constant")):
@@ -178,6 +185,23 @@ def run_ceiling(ctx):
             f"of {PEAK[peak_key]:.0f}) at {row['random']['engine_mhz']:.0f} MHz; constant {row['constant']['rate']:.1f} "
             f"({100 * row['constant']['frac_of_datasheet']:.1f}%) at {row['constant']['engine_mhz']:.0f} MHz")
     return out
+
+
+def with_hbm_ceiling(obj, ceil: dict | None):
+    """Every HBM-bound roofline dict inside obj gets the measured HBM read rate beside the datasheet
+    peak (the probe's streaming read, in this run)."""
+    if not ceil or "hbm_read" not in ceil:
+        return
+    if isinstance(obj, dict):
+        if obj.get("bound") == "hbm" and obj.get("achieved"):
+            m = ceil["hbm_read"]["gb_per_s"]
+            obj["measured_ceiling"] = {"instruction": "16-byte streaming loads", "rate": m, "unit": "GB/s",
+                                       "frac_of_measured": obj["achieved"] / m, "profile": CEILING_PROFILE}
+        for v in obj.values():
+            with_hbm_ceiling(v, ceil)
+    elif isinstance(obj, list):
+        for v in obj:
+            with_hbm_ceiling(v, ceil)
 
 
 def with_ceiling(roof: dict, ceil: dict | None, name: str) -> dict:
@@ -921,6 +945,9 @@ def main() -> int:
     for key, name in (("configs2_int8", "int8"), ("configs3_binary", "fp4"), ("ivf_training_kmeans", "fp32")):
         if key in extra and "roofline" in extra[key]:
             with_ceiling(extra[key]["roofline"], ceil, name)
+    with_hbm_ceiling(extra, ceil)
+    if c2 is not None:
+        with_hbm_ceiling(c2, ceil)
     ctx.close()
     if c2 is None:
         print(json.dumps({"metric": METRIC, "value": None, "extra": extra}), flush=True)

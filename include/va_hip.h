@@ -447,8 +447,11 @@ typedef enum {
     VA_PROBE_FP16 = 1, /* v_mfma_f32_32x32x16_f16: the fp16 screens */
     VA_PROBE_INT8 = 2, /* v_mfma_i32_32x32x32_i8: the int8 scan */
     VA_PROBE_FP4 = 3,  /* v_mfma_scale_f32_32x32x64_f8f6f4 on fp4 operands: the Hamming scan */
-    VA_PROBE_LDS = 4   /* ds_read_b128 of 1 KiB per wave, bank-conflict free, 8 per round (no MFMA):
+    VA_PROBE_LDS = 4,  /* ds_read_b128 of 1 KiB per wave, bank-conflict free, 8 per round (no MFMA):
                         * the LDS read bandwidth the scans' fragment reads draw on; ops = bytes */
+    VA_PROBE_HBM = 5   /* a streaming read of `iterations` MiB (256 .. 65536) of device memory, 16-byte
+                        * loads, a wave reading 1 KiB contiguous per load: the HBM read bandwidth the
+                        * HBM-bound scans draw on; ops = bytes */
 } va_probe_kind;
 typedef struct {
     double ops_per_second; /* dense operations per second sustained */

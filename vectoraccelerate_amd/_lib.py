@@ -40,6 +40,7 @@ VA_PROBE_FP16 = 1
 VA_PROBE_INT8 = 2
 VA_PROBE_FP4 = 3
 VA_PROBE_LDS = 4
+VA_PROBE_HBM = 5
 
 _p = C.c_void_p
 _u32 = C.c_uint32

@@ -233,29 +233,32 @@ struct SmallChain {
     }
 };
 
-// Scores up to 64 rows (lane l: row id rid_of(l), valid_of(l)) against one wave-uniform query
-// with a VALU chain per lane.  The rows move in coalesced groups of 32 values: load instruction i
-// of a group brings rows 8i .. 8i + 7 (lane L: row 8i + L / 8, 16-byte chunk L % 8, whole 128-byte
-// lines), the wave's LDS slot (8 KiB, chunk c of row r at c ^ ((r >> 1) & 7): conflict-free
-// reads) turns them into rows, and lane l reads its own row's 32 values.  Groups j + 1 .. j + R
-// are in flight (registers) while group j computes (R groups in all).  feed(j, xv, qv) runs the
-// lane's chain on group j.  Needs D % 4 == 0 and 16-byte aligned rows and query.
-template <int R = 2, class Feed>
-__device__ inline void rows_through_lds(const float* q, const float* x, const uint32_t (&rid)[8],
-                                        const bool (&rvalid)[8], uint32_t D, fb_f32x4* slot, Feed&& feed) {
+// Scores up to 8 NRG rows (lane l < 8 NRG: row id rid_of(l), valid_of(l)) against one
+// wave-uniform query with a VALU chain per lane.  The rows move in coalesced groups of 32 values:
+// load instruction i of a group brings rows 8i .. 8i + 7 (lane L: row 8i + L / 8, 16-byte chunk
+// L % 8, whole 128-byte lines), the wave's LDS slot (8 KiB, chunk c of row r at c ^ ((r >> 1) & 7):
+// conflict-free reads) turns them into rows, and lane l reads its own row's 32 values (lanes past
+// 8 NRG read slot entries no row filled; their chains are discarded).  Groups j + 1 .. j + R are in
+// flight (registers) while group j computes (R groups in all).  feed(j, xv, qv) runs the lane's
+// chain on group j.  Fewer row groups per wave (NRG < 8) spread a few rows over more waves, each
+// streaming less, with more groups in flight.  Needs D % 4 == 0 and 16-byte aligned rows and query.
+template <int R = 2, int NRG = 8, class Feed>
+__device__ inline void rows_through_lds(const float* q, const float* x, const uint32_t (&rid)[NRG],
+                                        const bool (&rvalid)[NRG], uint32_t D, fb_f32x4* slot, Feed&& feed) {
+    static_assert(NRG >= 1 && NRG <= 8, "row groups of 8 rows in a 64-row slot");
     const int lane = threadIdx.x & 63;
     const int ck = lane & 7;
     const uint32_t ng = (D + 31) / 32;
-    fb_f32x4 g[R][8];
-    auto load = [&](uint32_t j, fb_f32x4(&gr)[8]) {
+    fb_f32x4 g[R][NRG];
+    auto load = [&](uint32_t j, fb_f32x4(&gr)[NRG]) {
         const uint32_t d = 32 * j + 4 * uint32_t(ck);
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < NRG; ++i)
             gr[i] = valu_load4<true>(rvalid[i] ? x + int64_t(rid[i]) * D : nullptr, d, D);
     };
-    auto stash = [&](const fb_f32x4(&gr)[8]) {
+    auto stash = [&](const fb_f32x4(&gr)[NRG]) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < NRG; ++i) {
             const int r = 8 * i + (lane >> 3);
             slot[r * 8 + (ck ^ ((r >> 1) & 7))] = gr[i];
         }

@@ -1,4 +1,5 @@
-// va_probe.hip — the matrix-core ceiling of the board, measured (no reference counterpart).
+// va_probe.hip — the matrix-core, LDS and HBM ceilings of the board, measured (no reference
+// counterpart).
 //
 // The roofline fractions of the scans are quoted against MI355X's published dense peaks; this
 // probe measures what the board sustains for each MFMA instruction the scans use, so that a
@@ -151,6 +152,30 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(uint32_t iters, int rnd
     if (z == 1234.5f) sink[0] = z;  // keeps the accumulators live; never true in practice
 }
 
+// HBM read bandwidth: each workgroup streams contiguous 32 KiB blocks (eight 16-byte loads per
+// thread in flight, a wave reading 1 KiB of contiguous bytes per load; sixteen per thread and
+// grid-strided loads measured slower), the blocks spread over the workgroups; the words are
+// xor-folded so the loads stay live.  The buffer (4 GiB in the bench) is
+// far larger than the L2s and the last-level cache, so the bytes come from HBM.
+__global__ __launch_bounds__(256) void hbm_probe_kernel(const pr_i4* __restrict__ p, uint64_t n16, float* sink,
+                                                        unsigned long long* clocks) {
+    uint64_t c0, w0;
+    pr_clock_begin(c0, w0);
+    constexpr uint64_t kBlock = 256 * 8;  // 16-byte words per block
+    const uint64_t nb = n16 / kBlock;
+    pr_i4 x = {0, 0, 0, 0};
+    for (uint64_t b = blockIdx.x; b < nb; b += gridDim.x) {
+        const pr_i4* q = p + b * kBlock + threadIdx.x;
+        pr_i4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = q[u * 256];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x ^= v[u];
+    }
+    pr_clock_end(c0, w0, clocks);
+    if ((x[0] ^ x[1] ^ x[2] ^ x[3]) == 0x7F123456) sink[0] = 1.0f;  // keeps the loads live
+}
+
 // dense operations of one MFMA of the kind (2 per multiply-add)
 double ops_per_mfma(int kind) {
     switch (kind) {
@@ -169,7 +194,9 @@ extern "C" va_status va_probe_mfma(va_context* ctx, va_probe_kind kind, int rand
                                    va_probe_result* out) {
     if (!ctx) return VA_ERR_INVALID_ARG;
     VA_REQUIRE(ctx, out != nullptr, "va_probe_mfma: NULL output");
-    VA_REQUIRE(ctx, kind >= VA_PROBE_FP32 && kind <= VA_PROBE_LDS, "va_probe_mfma: unknown kind %d", int(kind));
+    VA_REQUIRE(ctx, kind >= VA_PROBE_FP32 && kind <= VA_PROBE_HBM, "va_probe_mfma: unknown kind %d", int(kind));
+    VA_REQUIRE(ctx, kind != VA_PROBE_HBM || (iterations >= 256 && iterations <= 65536),
+               "va_probe_mfma: the HBM kind reads `iterations` MiB, 256 .. 65536");
     VA_REQUIRE(ctx, iterations >= 1 && iterations <= (1u << 24), "va_probe_mfma: iterations %u out of range",
                iterations);
     va::DeviceGuard g(ctx->device);
@@ -184,7 +211,10 @@ extern "C" va_status va_probe_mfma(va_context* ctx, va_probe_kind kind, int rand
                 if (x) (void)hipEventDestroy(x);
         }
     } t;
-    VA_CHECK_HIP(ctx, hipMalloc(&t.p, 256));
+    // the HBM kind's buffer follows the 256-byte clock block
+    const uint64_t hbm_bytes = kind == VA_PROBE_HBM ? uint64_t(iterations) << 20 : 0;
+    VA_CHECK_HIP(ctx, hipMalloc(&t.p, 256 + hbm_bytes));
+    if (hbm_bytes) VA_CHECK_HIP(ctx, hipMemsetAsync(static_cast<char*>(t.p) + 256, random_operands ? 0x5A : 0, hbm_bytes, ctx->stream));
     VA_CHECK_HIP(ctx, hipEventCreate(&t.e[0]));
     VA_CHECK_HIP(ctx, hipEventCreate(&t.e[1]));
     auto* clocks = static_cast<unsigned long long*>(t.p);
@@ -210,6 +240,11 @@ extern "C" va_status va_probe_mfma(va_context* ctx, va_probe_kind kind, int rand
                 va::mfma_probe_kernel<VA_PROBE_LDS><<<grid, 256, 0, ctx->stream>>>(iterations, random_operands, sink,
                                                                                    clocks);
                 break;
+            case VA_PROBE_HBM:
+                // eight 4-wave workgroups per CU
+                va::hbm_probe_kernel<<<grid * 4, 256, 0, ctx->stream>>>(
+                    reinterpret_cast<const va::pr_i4*>(static_cast<char*>(t.p) + 256), hbm_bytes / 16, sink, clocks);
+                break;
             default:
                 va::mfma_probe_kernel<VA_PROBE_FP4><<<grid, 256, 0, ctx->stream>>>(iterations, random_operands, sink,
                                                                                    clocks);
@@ -228,7 +263,8 @@ extern "C" va_status va_probe_mfma(va_context* ctx, va_probe_kind kind, int rand
     float ms = 0.0f;
     VA_CHECK_HIP(ctx, hipEventElapsedTime(&ms, t.e[0], t.e[1]));
     out->ms = ms;
-    out->ops = double(grid) * 4.0 * double(iterations) * va::kAcc * va::ops_per_mfma(int(kind));
+    out->ops = kind == VA_PROBE_HBM ? double(hbm_bytes)
+                                    : double(grid) * 4.0 * double(iterations) * va::kAcc * va::ops_per_mfma(int(kind));
     out->ops_per_second = ms > 0 ? out->ops / (double(ms) * 1e-3) : 0.0;
     out->engine_mhz = h[1] ? double(h[0]) / double(h[1]) * double(wall_khz) * 1e-3 : 0.0;
     return VA_OK;

@@ -1365,11 +1365,12 @@ __global__ __launch_bounds__(256) void screen_compact_kernel(const uint32_t* __r
 // sequence on the VALU (GemmChain: the fmaf chain every element of the scan's MFMA block follows),
 // so every key equals the fp32 scan's.  The rows pass through the wave's LDS slot in coalesced
 // 128-byte lines (rows_through_lds).  Needs D % 4 == 0 and 16-byte aligned rows and queries.
-template <int R, bool QLDS>
+template <int R, bool QLDS, int NRG = 8>
 __global__ __launch_bounds__(256) void rerank_kernel(const float* __restrict__ q, const float* __restrict__ x,
                                                      uint32_t D, int op, const uint32_t* __restrict__ rr,
                                                      const uint32_t* __restrict__ rcount, uint32_t rcap, uint32_t Q,
                                                      uint32_t* __restrict__ rkey) {
+    constexpr uint32_t CH = 8 * NRG;  // rows per chunk (one wave's)
     __shared__ fb_f32x4 slots[4][64 * 8];
     // QLDS: each wave's query staged in LDS (dynamic, 4 x D4 floats), so that a wave alone on its
     // rows does not wait on a load of the query's values for every group
@@ -1377,19 +1378,19 @@ __global__ __launch_bounds__(256) void rerank_kernel(const float* __restrict__ q
     const int lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t D4 = (D + 3) & ~3u;
-    const uint32_t nch = (rcap + 63) / 64;
+    const uint32_t nch = (rcap + CH - 1) / CH;
     const uint64_t items = uint64_t(Q) * nch;
     const uint32_t nw = gridDim.x * 4;
     for (uint64_t it = uint64_t(blockIdx.x) * 4 + wave; it < items; it += nw) {
         const uint32_t c = uint32_t(it / Q), qi = uint32_t(it % Q);
         const uint32_t n = min(rcount[qi], rcap);
-        if (c * 64 >= n) continue;  // (uniform)
-        const uint32_t* rl = rr + int64_t(qi) * rcap + c * 64;
-        const uint32_t m = min(64u, n - c * 64);
-        uint32_t rid[8];
-        bool rv[8];
+        if (c * CH >= n) continue;  // (uniform)
+        const uint32_t* rl = rr + int64_t(qi) * rcap + c * CH;
+        const uint32_t m = min(CH, n - c * CH);
+        uint32_t rid[NRG];
+        bool rv[NRG];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < NRG; ++i) {
             const uint32_t r = uint32_t(8 * i + (lane >> 3));
             rv[i] = r < m;
             rid[i] = rv[i] ? rl[r] : 0u;
@@ -1403,9 +1404,9 @@ __global__ __launch_bounds__(256) void rerank_kernel(const float* __restrict__ q
             qp = qw;
         }
         GemmChain ch;
-        rows_through_lds<R>(qp, x, rid, rv, D, slots[wave],
-                            [&](uint32_t j, const fb_f32x4(&xv)[8], const fb_f32x4(&qv)[8]) { ch.group(xv, qv, j, D); });
-        if (uint32_t(lane) < m) rkey[int64_t(qi) * rcap + c * 64 + lane] = ch.key(op);
+        rows_through_lds<R, NRG>(qp, x, rid, rv, D, slots[wave],
+                                 [&](uint32_t j, const fb_f32x4(&xv)[8], const fb_f32x4(&qv)[8]) { ch.group(xv, qv, j, D); });
+        if (uint32_t(lane) < m) rkey[int64_t(qi) * rcap + c * CH + lane] = ch.key(op);
     }
 }
 
@@ -1779,13 +1780,15 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     {
         const uint64_t items = uint64_t(Q) * ((rcap + 63) / 64);
         const uint32_t blocks = uint32_t(std::min<uint64_t>(2048, (items + 3) / 4));
-        // small batches keep few waves busy, each on its own: the query staged in LDS and four row
-        // groups in flight per wave instead of two
+        // small batches keep few waves busy, each on its own: 8-row chunks (eight times the waves,
+        // each streaming an eighth of the rows), the query staged in LDS and eight row groups in
+        // flight per wave
         const size_t qlds = size_t(4) * ((D + 3) & ~3u) * 4;
-        if (Q <= kSmallBatchMax && qlds <= 64 * 1024)
-            rerank_kernel<4, true><<<dim3(blocks), dim3(256), qlds, ctx->stream>>>(in.q, in.x, D, int(in.op), rr,
-                                                                                  rcount, uint32_t(rcap), Q, rkey);
-        else
+        if (Q <= kSmallBatchMax && qlds <= 64 * 1024) {
+            const uint64_t items8 = uint64_t(Q) * ((rcap + 7) / 8);
+            rerank_kernel<8, true, 1><<<dim3(uint32_t(std::min<uint64_t>(4096, (items8 + 3) / 4))), dim3(256), qlds,
+                                        ctx->stream>>>(in.q, in.x, D, int(in.op), rr, rcount, uint32_t(rcap), Q, rkey);
+        } else
             rerank_kernel<2, false><<<dim3(blocks), dim3(256), 0, ctx->stream>>>(in.q, in.x, D, int(in.op), rr,
                                                                                 rcount, uint32_t(rcap), Q, rkey);
         VA_CHECK_LAUNCH(ctx);
