@@ -69,7 +69,9 @@ COUNTERS_SCREEN = "profiles/counters__screen_filter__configs1_cosine_top100.txt"
 COUNTERS_FP32 = "profiles/counters__dist_gemm_filter__configs1_cosine_top100.txt"
 COUNTERS_I8 = "profiles/counters__i8_resq16_filter__configs2_int8_top10.txt"
 COUNTERS_HAMMING = "profiles/counters__hamming_mfma_filter__configs3_binary_top100.txt"
-COUNTERS_IVF16 = {"64 resident queries x 1024 rows (full pass)": "profiles/counters__ivf16_resq__configs4_ivfflat_top10.txt",
+COUNTERS_IVF16 = {"192 queries x 256 rows, LDS-staged (full pass, lists probed by more than 96 queries)":
+                  "profiles/counters__ivf16_big__configs4_ivfflat_top10.txt",
+                  "96 resident queries x 1024 rows (full pass, 33-96 queries)": "profiles/counters__ivf16_resq__configs4_ivfflat_top10.txt",
                   "64-query tiles (sample pass)": "profiles/counters__ivf16_wide64__configs4_ivfflat_top10.txt",
                   "32-query tiles": "profiles/counters__ivf16_wide32__configs4_ivfflat_top10.txt",
                   "16-query tiles": "profiles/counters__ivf16_narrow__configs4_ivfflat_top10.txt"}
@@ -694,9 +696,9 @@ def run_c5(ctx, a, cpu: bool):
         "candidates_scanned": cand, "largest_list": int(sizes.max()),
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK["hbm_gbs"], "unit": "GB/s",
                      "frac": gbs / PEAK["hbm_gbs"],
-                     "kernel": ("screened list scan: ivf16_narrow_kernel / ivf16_wide_kernel<1> / ivf16_resq_kernel "
-                                "(fp16 shadow rows on the fp16 MFMA, the three tile groups concurrently), timed as one phase"
-                                if screened else "fp32 list scan"),
+                     "kernel": ("screened list scan: ivf16_big_kernel (lists probed by more than 96 queries), then "
+                                "ivf16_narrow_kernel / ivf16_wide_kernel<1> / ivf16_resq_kernel concurrently (fp16 shadow "
+                                "rows on the fp16 MFMA), timed as one phase" if screened else "fp32 list scan"),
                      "algorithmic": f"fp16 shadow of the distinct probed lists + fp16 queries = {b16 / 1e9:.2f} GB "
                                     f"per search (fp32 rows: {b_min / 1e9:.2f} GB)",
                      "counted": {name: counted(rel) for name, rel in COUNTERS_IVF16.items()},

@@ -374,6 +374,35 @@ __device__ inline uint32_t plan_tile_after_wave(const ListPlan& p, uint32_t t, u
     rc = min(TN, n - rb * TN);
     return l;
 }
+// plan_tile with the list found by a 64-way search of the whole wave: each round lane i tests an
+// evenly spaced list of the remaining range, which shrinks 64-fold (two rounds over 4,096 lists,
+// where a binary search is twelve dependent loads), from a list h with pre[h] <= t (a wave's
+// previous tile's list, or 0).  Every lane of the wave must call it with the same t and h; every
+// lane gets the same tile.  Returns the list.
+__device__ inline uint32_t plan_tile_wave(const ListPlan& p, uint32_t t, uint32_t h, uint32_t TQ, uint32_t TN,
+                                          uint32_t& qs, uint32_t& qc, uint32_t& rs, uint32_t& rc) {
+    const uint32_t lane = __lane_id();
+    uint32_t lo = h, hi = p.C;  // pre[lo] <= t; the answer lies in [lo, hi)
+    while (hi - lo > 1) {
+        const uint32_t step = (hi - lo + 63) / 64;
+        const uint32_t l = lo + lane * step;
+        const bool le = l < hi && p.pre[l] <= t;  // a prefix of the lanes (pre is non-decreasing); lane 0 holds
+        const uint32_t c = uint32_t(__popcll(__ballot(le)));
+        lo = __builtin_amdgcn_readfirstlane(lo + (c - 1) * step);
+        hi = __builtin_amdgcn_readfirstlane(min(hi, lo + step));
+    }
+    const uint32_t l = lo, local = t - p.pre[l];
+    const uint32_t nq = p.qoff[l + 1] - p.qoff[l];
+    const uint32_t len = p.roff[l + 1] - p.roff[l];
+    const uint32_t n = p.sample ? ivf_sample_rows(len) : len;
+    const uint32_t nqb = (nq + TQ - 1) / TQ;
+    const uint32_t rb = local / nqb, qb = local % nqb;
+    qs = p.qoff[l] + qb * TQ;
+    qc = min(TQ, nq - qb * TQ);
+    rs = p.roff[l] + rb * TN;
+    rc = min(TN, n - rb * TN);
+    return l;
+}
 #endif
 
 struct DistArgs {

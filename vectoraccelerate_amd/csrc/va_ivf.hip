@@ -644,9 +644,10 @@ __global__ __launch_bounds__(256, 2) void ivf16_narrow_kernel(Ivf16Args a) {
     __shared__ __attribute__((aligned(16))) float2 xs[iv16::WAVES][iv16::TN];
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
     const uint32_t total = a.plan.pre[a.plan.C];
+    uint32_t h = 0;  // the list of the wave's previous tile
     for (uint32_t t = blockIdx.x * iv16::WAVES + uint32_t(wave); t < total; t += gridDim.x * iv16::WAVES) {
         uint32_t qs, qc, rs, rc;
-        plan_tile(a.plan, t, 16, iv16::TN, qs, qc, rs, rc);
+        h = plan_tile_wave(a.plan, t, h, 16, iv16::TN, qs, qc, rs, rc);
         narrow_tile(a, xs[wave], qs, qc, rs, rc);
     }
 }
@@ -656,9 +657,10 @@ __global__ __launch_bounds__(256, 1) void ivf16_wide_kernel(Ivf16Args a) {
     __shared__ __attribute__((aligned(16))) float2 xs[iv16::WAVES][iv16::TN];
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
     const uint32_t total = a.plan.pre[a.plan.C];
+    uint32_t h = 0;  // the list of the wave's previous tile
     for (uint32_t t = blockIdx.x * iv16::WAVES + uint32_t(wave); t < total; t += gridDim.x * iv16::WAVES) {
         uint32_t qs, qc, rs, rc;
-        plan_tile(a.plan, t, 32u * W, iv16::TN, qs, qc, rs, rc);
+        h = plan_tile_wave(a.plan, t, h, 32u * W, iv16::TN, qs, qc, rs, rc);
         wide_tile<W>(a, xs[wave], qs, qc, rs, rc);
     }
 }
