@@ -107,10 +107,12 @@ def counted(rel: str) -> dict:
             "traffic": c.get("traffic_bytes_per_launch"), "counters_source": rel}
 
 
-def timed(ctx, fn, steps: int, warmup: int, scan_timings: bool = True):
+def timed(ctx, fn, steps: int, warmup: int, scan_timings: bool = True, phase_reps: int = 3):
     """Run `warmup` untimed steps, then time exactly `steps` steps between synchronisations.
-    With scan_timings, the context's profiling records (hipEvents that nothing waits for inside
-    the loop) give the mean phase times of the timed steps' scans."""
+    With scan_timings, the timed loop runs at profiling level 2 (the library records two hipEvents
+    around each scan phase on its stream, which nothing waits for inside the loop: the scan
+    kernel's mean duration over exactly the timed steps), and `phase_reps` more steps after it at
+    level 1 give the breakdown of the other phases and the counts (outside the timed loop)."""
     import torch
 
     for _ in range(warmup):
@@ -118,6 +120,7 @@ def timed(ctx, fn, steps: int, warmup: int, scan_timings: bool = True):
     ctx.synchronize()
     torch.cuda.synchronize()
     if scan_timings:
+        ctx.set_profiling(2)
         ctx.reset_scan_totals()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -128,16 +131,26 @@ def timed(ctx, fn, steps: int, warmup: int, scan_timings: bool = True):
     if not scan_timings:
         return ms, None
     total, n = ctx.scan_totals()
-    return ms, (total, n, ctx.last_scan_timings())
+    ctx.set_profiling(True)
+    ctx.reset_scan_totals()
+    for _ in range(phase_reps):
+        fn()
+    ctx.synchronize()
+    ftotal, fn_ = ctx.scan_totals()
+    return ms, (total, n, ctx.last_scan_timings(), ftotal, fn_)
 
 
 def mean_phases(phases):
-    """Mean phase times per scan over a timed loop (from timed()), with the last scan's sizes."""
+    """Mean phase times per scan: the scan phase over the timed loop, the other phases over the
+    level-1 steps after it (from timed()), with the last scan's sizes."""
     if not phases:
         return {}
-    total, n, last = phases
-    n = max(n, 1)
-    out = {k: float(total[k]) / n for k in ("sample_ms", "scan_ms", "select_ms", "fallback_ms", "total_ms")}
+    total, n, last, ftotal, fn_ = phases
+    fn_ = max(fn_, 1)
+    out = {k: float(ftotal[k]) / fn_ for k in ("sample_ms", "select_ms", "fallback_ms", "total_ms")}
+    out["scan_ms_phase_steps"] = float(ftotal["scan_ms"]) / fn_
+    # (a scan with no sample phase records nothing at level 2: its time comes from the level-1 steps)
+    out["scan_ms"] = float(total["scan_ms"]) / n if n else out["scan_ms_phase_steps"]
     out["scans"] = n
     out.update({k: last[k] for k in ("sample_rows", "candidate_cap", "overflow_rows", "screened", "rerank_rows")
                 if k in last})

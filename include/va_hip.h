@@ -111,7 +111,9 @@ va_status va_context_set_option(va_context* ctx, va_option option, uint64_t valu
  * and IVFPhaseTimings (Index/Kernels/IVF/IVFKernels.swift:295).  With profiling on, a scan
  * records its events (and copies its overflow / rerank counts) without waiting; the events are
  * read when va_context_last_scan or va_context_scan_totals is called, or when the record is
- * reused 16 scans later. */
+ * reused 16 scans later.  va_context_set_profiling: enable 0 off, 1 every phase (five events, the
+ * counts), 2 the scan phase alone (its two events, no counts: scan_ms is set, the other phase
+ * times and counts read 0), for timing loops that should carry as little as possible. */
 typedef struct {
     float sample_ms;        /* threshold sample: dense keys + k-th selection          */
     float scan_ms;          /* the filtering scan kernel (the dominant kernel)         */

@@ -327,3 +327,38 @@ def test_ivf_search_queues_behind_other_searches(ctx, oracle):
     oi, od = oracle.ivf_scan(q, x, off, ids, probes, 10)
     check_topk(L2SQ, q, x, 10, _host(ii, np.uint32), _host(di), oi, od)
     st.close()
+
+
+def test_profiling_levels(ctx):
+    """Profiling level 2 records the scan phase alone (its two events): scan_ms of a screened
+    search is set and equals its level-1 value within the run-to-run spread, while the other
+    phases and the counts read 0; levels outside 0..2 are rejected.  The results are the same at
+    every level."""
+    from vectoraccelerate_amd import FusedL2TopKKernel, FusedL2TopKParameters, _lib
+
+    rng = np.random.default_rng(11)
+    N, D, Q, k = 60000, 256, 512, 20
+    x = ctx.buffer(rng.standard_normal((N, D), dtype=np.float32))
+    q = ctx.buffer(rng.standard_normal((Q, D), dtype=np.float32))
+    kern = FusedL2TopKKernel(ctx)
+    params = FusedL2TopKParameters(Q, N, D, k)
+    out = {}
+    for level in (1, 2, 0):
+        ctx.set_profiling(level)
+        try:
+            r = kern.execute(q, x, params)
+            ctx.synchronize()
+            out[level] = (r.indices.cpu().numpy(), r.distances.cpu().numpy(),
+                          ctx.last_scan_timings() if level else None)
+        finally:
+            ctx.set_profiling(False)
+    t1, t2 = out[1][2], out[2][2]
+    assert t1["sample_ms"] > 0 and t1["select_ms"] > 0 and t1["scan_ms"] > 0 and t1["rerank_rows"] > 0
+    assert t2["scan_ms"] > 0 and t2["sample_ms"] == 0 and t2["select_ms"] == 0 and t2["rerank_rows"] == 0
+    assert t2["total_ms"] == t2["scan_ms"]
+    assert 0.2 < t2["scan_ms"] / t1["scan_ms"] < 5.0
+    for level in (2, 0):
+        np.testing.assert_array_equal(out[level][0], out[1][0])
+        np.testing.assert_array_equal(out[level][1].view(np.uint32), out[1][1].view(np.uint32))
+    assert ctx.lib.va_context_set_profiling(ctx.handle, 3) == _lib.VA_ERR_INVALID_ARG
+    assert ctx.lib.va_context_set_profiling(ctx.handle, -1) == _lib.VA_ERR_INVALID_ARG

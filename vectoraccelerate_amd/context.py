@@ -119,9 +119,11 @@ class GPUContext:
         """Make work queued on torch's current stream visible to the context stream."""
         _torch().cuda.current_stream(self.device).synchronize()
 
-    def set_profiling(self, enable: bool) -> None:
-        """Metal4Configuration.enableProfiling: time every scan phase with hipEvents."""
-        self.check(self.lib.va_context_set_profiling(self.handle, int(bool(enable))), "va_context_set_profiling")
+    def set_profiling(self, enable) -> None:
+        """Metal4Configuration.enableProfiling: time every scan phase with hipEvents.  True (or 1):
+        every phase and the counts; 2: the scan phase alone (two events per scan, nothing else)."""
+        level = 2 if (not isinstance(enable, bool) and enable == 2) else int(bool(enable))
+        self.check(self.lib.va_context_set_profiling(self.handle, level), "va_context_set_profiling")
 
     def last_scan_timings(self) -> dict:
         """Phase timings of the last profiled scan (waits for its events)."""

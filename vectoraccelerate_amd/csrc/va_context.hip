@@ -66,7 +66,7 @@ va_context::ScanRecord* profile_record(va_context* ctx) {
 void profile_fold(va_context* ctx, va_context::ScanRecord& r) {
     (void)ctx;
     r.pending = false;
-    if (hipEventSynchronize(r.ev[4]) != hipSuccess) {
+    if (hipEventSynchronize(r.ev[r.light ? 2 : 4]) != hipSuccess) {
         (void)hipGetLastError();
         return;
     }
@@ -79,13 +79,19 @@ void profile_fold(va_context* ctx, va_context::ScanRecord& r) {
         return t;
     };
     va_scan_timings& t = r.t;
-    t.total_ms = ms(0, 4);
-    if (r.sampled) {
+    if (r.light) {
+        // the scan phase alone (events 1 and 2)
+        t.scan_ms = ms(1, 2);
+        t.total_ms = t.scan_ms;
+        t.sample_ms = t.select_ms = t.fallback_ms = 0.0f;
+    } else if (r.sampled) {
+        t.total_ms = ms(0, 4);
         t.sample_ms = ms(0, 1);
         t.scan_ms = ms(1, 2);
         t.select_ms = ms(2, 3);
         t.fallback_ms = r.fallback ? ms(3, 4) : 0.0f;
     } else {
+        t.total_ms = ms(0, 4);
         t.sample_ms = 0.0f;
         t.scan_ms = t.total_ms;
         t.select_ms = 0.0f;
@@ -298,6 +304,7 @@ const char* va_last_error_message(const va_context* ctx) { return ctx ? ctx->las
 
 va_status va_context_set_profiling(va_context* ctx, int enable) {
     if (!ctx) return VA_ERR_INVALID_ARG;
+    VA_REQUIRE(ctx, enable >= 0 && enable <= 2, "va_context_set_profiling: level %d (0, 1 or 2)", enable);
     va::DeviceGuard g(ctx->device);
     if (enable && !ctx->rec[0].ev[0]) {
         for (auto& r : ctx->rec) {
@@ -308,7 +315,7 @@ va_status va_context_set_profiling(va_context* ctx, int enable) {
             r.host_word = static_cast<uint32_t*>(h);
         }
     }
-    ctx->profiling = enable != 0;
+    ctx->profiling = enable;
     return VA_OK;
 }
 

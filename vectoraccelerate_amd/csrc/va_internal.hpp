@@ -46,13 +46,14 @@ struct va_context {
     // phase profiling of the top-k scan (va_context_set_profiling): a ring of records whose
     // events are read when a record is reused or the timings are asked for, so a profiled scan
     // never waits on the host
-    bool profiling = false;
+    int profiling = 0;  // 0 off, 1 every phase, 2 the scan phase alone
     static constexpr int kScanRing = 16;
     struct ScanRecord {
         hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
         uint32_t* dev_word = nullptr;   // device scratch of the record's counts
         uint32_t* host_word = nullptr;  // pinned: [0] overflowed rows, [1] reranked rows
         bool pending = false, sampled = false, fallback = false, has_ovf = false, has_rerank = false;
+        bool light = false;  // profiling level 2: events 1 and 2 only
         va_scan_timings t{};
     } rec[kScanRing];
     int rec_next = 0, rec_last = -1;
@@ -587,21 +588,23 @@ struct ScanPhaseMarks {
     explicit ScanPhaseMarks(va_context* c) : ctx(c) {}
     va_status mark(int i) {
         if (!ctx->profiling) return VA_OK;
+        if (ctx->profiling == 2 && i != 1 && i != 2) return VA_OK;  // the scan phase alone
         if (i == 0 || !r) r = profile_record(ctx);
         if (!r) return VA_ERR_HIP;
+        r->light = ctx->profiling == 2;
         VA_CHECK_HIP(ctx, hipEventRecord(r->ev[i], ctx->stream));
         return VA_OK;
     }
     // profiling only: the device count of overflowed rows, read with the record
     va_status count_overflow(const uint32_t* dev_count) {
-        if (!ctx->profiling || !r) return VA_OK;
+        if (ctx->profiling != 1 || !r) return VA_OK;
         VA_CHECK_HIP(ctx, hipMemcpyAsync(r->host_word, dev_count, 4, hipMemcpyDeviceToHost, ctx->stream));
         r->has_ovf = true;
         return VA_OK;
     }
     // profiling only: the sum of a device array (rows re-scored by the rerank), read with the record
     va_status count_sum(const uint32_t* v, uint32_t n) {
-        if (!ctx->profiling || !r) return VA_OK;
+        if (ctx->profiling != 1 || !r) return VA_OK;
         VA_CHECK_STATUS(sum_u32_into(ctx, v, n, r->dev_word));
         VA_CHECK_HIP(ctx, hipMemcpyAsync(r->host_word + 1, r->dev_word, 4, hipMemcpyDeviceToHost, ctx->stream));
         r->has_rerank = true;
@@ -610,7 +613,7 @@ struct ScanPhaseMarks {
     // events: 0 start, 1 after sample, 2 after scan, 3 after select, 4 end
     va_status finish(bool sampled, bool fallback) {
         if (!ctx->profiling || !r) return VA_OK;
-        VA_CHECK_HIP(ctx, hipEventRecord(r->ev[4], ctx->stream));
+        if (!r->light) VA_CHECK_HIP(ctx, hipEventRecord(r->ev[4], ctx->stream));
         r->sampled = sampled;
         r->fallback = fallback;
         r->t = ctx->last_scan;
