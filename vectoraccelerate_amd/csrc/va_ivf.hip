@@ -431,78 +431,17 @@ __device__ __forceinline__ void append_pairs(const Ivf16Args& a, uint32_t qi, ui
     }
 }
 
-// narrow tile: lane (j, g) = (lane % 16, lane / 16) loads 16 halves at 64c + 16g of row j of
+// narrow tiles: lane (j, g) = (lane % 16, lane / 16) loads 16 halves at 64c + 16g of row j of
 // each 16-row block and of query j; MFMA u of chunk c takes halves 8u .. 8u + 7 of them.  The
 // result: lane (j, g) holds query j against rows 16b + 4g + v in acc[b][v].
-__device__ __forceinline__ void narrow_tile(const Ivf16Args& a, float2* xs, uint32_t qs, uint32_t qc, uint32_t rs,
-                                            uint32_t rc) {
-    const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
-    const bool qv = uint32_t(j) < qc;
-    const uint32_t qi = a.qrow[qs + (qv ? uint32_t(j) : 0u)];
-    const _Float16* qp = a.qh + int64_t(qi) * a.Dp + 16 * g;
-    const uint32_t rowb = a.Dp * 2u;
-    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<_Float16*>(a.xh + int64_t(rs) * a.Dp), 0, int(rc * rowb), 0x00020000);
-    const uint32_t lo = uint32_t(j) * rowb + 32u * uint32_t(g);
-    const uint32_t nch = a.Dp / 64;
-    stage_norms(a, xs, rs, rc, lane);
-    h8v qa[2], qb[2], ra[8][2], rb[8][2];
-    // past the last chunk every operand is zero (the query through the mask, rows past the
-    // descriptor), so the extra MFMAs add nothing
-    auto load = [&](uint32_t c, h8v(&q2)[2], h8v(&r2)[8][2]) {
-        const bool in = c < nch;
-        const uint32_t k = in ? 64u * c : 0u;
-        q2[0] = masked_h8(qp + k, qv && in);
-        q2[1] = masked_h8(qp + k + 8, qv && in);
-        const uint32_t vo = in ? lo + 2u * k : 0x80000000u;
-#pragma unroll
-        for (int b = 0; b < 8; ++b)
-#pragma unroll
-            for (int u = 0; u < 2; ++u)
-                r2[b][u] = __builtin_bit_cast(
-                    h8v, __builtin_amdgcn_raw_buffer_load_b128(xr, vo + uint32_t(b) * 16u * rowb + 16u * uint32_t(u), 0, 0));
-    };
-    f32x4s acc[8];
-#pragma unroll
-    for (int b = 0; b < 8; ++b) acc[b] = f32x4s{0.f, 0.f, 0.f, 0.f};
-    auto compute = [&](const h8v(&q2)[2], const h8v(&r2)[8][2]) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int b = 0; b < 8; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(r2[b][u], q2[u], acc[b], 0, 0, 0);
-    };
-    load(0, qa, ra);
-    for (uint32_t c = 0; c < nch; c += 2) {
-        load(c + 1, qb, rb);
-        compute(qa, ra);
-        __builtin_amdgcn_sched_barrier(0);
-        load(c + 2, qa, ra);
-        compute(qb, rb);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    if (!qv) return;
-    const float4 inf = a.qinfo[qi];
-    const PreTestV pt = pretest_v(a.bnd, inf.x, inf.y, a.qerr[qi], inf.z, a.thr[qi]);
-    float vals[32];
-    uint32_t rows[32];
-    uint32_t mask = 0;
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int t = 4 * b + v;
-            rows[t] = uint32_t(16 * b + 4 * g + v);
-            vals[t] = acc[b][v];
-            float xxp, nxp, exp;
-            screen_norms(xs[rows[t]], xxp, nxp, exp);
-            mask |= uint32_t((rows[t] < rc) & !(vals[t] < pretest_rhs(pt, xxp, nxp, exp))) << t;
-        }
-    }
-    if (!mask) return;
-    const uint32_t pos = atomicAdd(a.cnt + qi, uint32_t(__popc(mask)));
-    append_pairs<32>(a, qi, pos, mask, vals, rows, rs, inf.z);
-}
-
+struct NarrowTile {
+    uint32_t qs = 0, qc = 0, rs = 0, rc = 0;
+    uint32_t qi = 0;                 // the lane's query (query j of the tile; 0 past qc)
+    bool qv = false;                 // j < qc
+    const _Float16* qp = nullptr;    // its fp16 row at 16 g
+    __amdgpu_buffer_rsrc_t xr;       // the tile's rows (loads past rc read zeros)
+    bool valid = false;              // false: every load of the tile reads zeros
+};
 // wide tile: lane (l32, hh) loads 32 halves at 64c + 32hh of row l32 of each 32-row block and of
 // query l32 of each 32-query block; MFMA u of chunk c takes halves 8u .. 8u + 7.  The result:
 // lane (l32, hh) holds query 32n + l32 against rows 32m + 8i + 4hh + e in acc[n][m][4i + e].
@@ -640,15 +579,125 @@ __global__ __launch_bounds__(256) void ivf_bound_kernel(BoundV b, const float4* 
     }
 }
 
+// The 16-query tiles, one independent tile per wave, software-pipelined across the wave's tiles:
+// the next tile is located, and its first 64-value chunk requested, while the current one is
+// scanned, so the chunk's HBM latency overlaps the current tile's last chunk and epilogue; the
+// epilogue's inputs (the rows' {|x|^2, error bound}, the query's pre-test constants) are loaded
+// at the tile's start and used after its main loop.
 __global__ __launch_bounds__(256, 2) void ivf16_narrow_kernel(Ivf16Args a) {
-    __shared__ __attribute__((aligned(16))) float2 xs[iv16::WAVES][iv16::TN];
+    __shared__ __attribute__((aligned(16))) float2 xs_all[iv16::WAVES][iv16::TN];
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+    float2* xs = xs_all[wave];
+    const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
     const uint32_t total = a.plan.pre[a.plan.C];
-    uint32_t h = 0;  // the list of the wave's previous tile
-    for (uint32_t t = blockIdx.x * iv16::WAVES + uint32_t(wave); t < total; t += gridDim.x * iv16::WAVES) {
-        uint32_t qs, qc, rs, rc;
-        h = plan_tile_wave(a.plan, t, h, 16, iv16::TN, qs, qc, rs, rc);
-        narrow_tile(a, xs[wave], qs, qc, rs, rc);
+    const uint32_t stride = gridDim.x * iv16::WAVES;
+    uint32_t t = blockIdx.x * iv16::WAVES + uint32_t(wave);
+    if (t >= total) return;
+    const uint32_t rowb = a.Dp * 2u;
+    const uint32_t nch = a.Dp / 64, nce = (nch + 1) & ~1u;
+    const uint32_t lo = uint32_t(j) * rowb + 32u * uint32_t(g);
+    uint32_t h = 0;  // the list of the wave's last located tile
+    auto setup = [&](uint32_t tt, NarrowTile& T) {
+        T.valid = tt < total;
+        if (!T.valid) {
+            // no tile: a zero-length descriptor (every row load out of range) and a valid query
+            // pointer whose loads the mask zeroes
+            T.qs = T.qc = T.rs = T.rc = T.qi = 0;
+            T.qv = false;
+            T.qp = a.qh;
+            T.xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(a.xh), 0, 0, 0x00020000);
+            return;
+        }
+        h = plan_tile_wave(a.plan, tt, h, 16, iv16::TN, T.qs, T.qc, T.rs, T.rc);
+        T.qv = uint32_t(j) < T.qc;
+        T.qi = a.qrow[T.qs + (T.qv ? uint32_t(j) : 0u)];
+        T.qp = a.qh + int64_t(T.qi) * a.Dp + 16 * g;
+        T.xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(a.xh + int64_t(T.rs) * a.Dp), 0,
+                                                 int(T.rc * rowb), 0x00020000);
+    };
+    // chunk c of tile T (c past the last chunk, or an invalid tile: zeros, no memory traffic)
+    auto load = [&](const NarrowTile& T, uint32_t c, h8v(&q2)[2], h8v(&r2)[8][2]) {
+        const bool in = T.valid && c < nch;
+        const uint32_t k = in ? 64u * c : 0u;
+        q2[0] = masked_h8(T.qp + k, T.qv && in);
+        q2[1] = masked_h8(T.qp + k + 8, T.qv && in);
+        const uint32_t vo = in ? lo + 2u * k : 0x80000000u;
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+                r2[b][u] = __builtin_bit_cast(
+                    h8v, __builtin_amdgcn_raw_buffer_load_b128(T.xr, vo + uint32_t(b) * 16u * rowb + 16u * uint32_t(u), 0, 0));
+    };
+    f32x4s acc[8];
+    auto compute = [&](const h8v(&q2)[2], const h8v(&r2)[8][2]) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int b = 0; b < 8; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(r2[b][u], q2[u], acc[b], 0, 0, 0);
+    };
+    NarrowTile cur, nxt;
+    setup(t, cur);
+    h8v qa[2], qb[2], ra[8][2], rb[8][2];
+    load(cur, 0, qa, ra);
+    while (true) {
+        // this tile's epilogue inputs, used after its main loop
+        const float2 xn0 = uint32_t(lane) < cur.rc ? a.xn[cur.rs + uint32_t(lane)] : make_float2(0.0f, 0.0f);
+        const float2 xn1 = uint32_t(64 + lane) < cur.rc ? a.xn[cur.rs + 64u + uint32_t(lane)] : make_float2(0.0f, 0.0f);
+        const float4 inf = a.qinfo[cur.qi];
+        const float eq = a.qerr[cur.qi];
+        const uint32_t th = a.thr[cur.qi];
+        // the next tile: its chunk 0 is requested during this tile's last chunk
+        setup(t + stride, nxt);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) acc[b] = f32x4s{0.f, 0.f, 0.f, 0.f};
+        // an even number of chunks (one of zeros when nch is odd), so the next tile's chunk 0
+        // always lands in the first register set
+        for (uint32_t c = 0; c < nce; c += 2) {
+            load(cur, c + 1, qb, rb);
+            compute(qa, ra);
+            __builtin_amdgcn_sched_barrier(0);
+            if (c + 2 < nce) load(cur, c + 2, qa, ra);
+            else load(nxt, 0, qa, ra);
+            compute(qb, rb);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // ---- epilogue of this tile (the next tile's chunk 0 in flight)
+        xs[lane] = xn0;
+        xs[64 + lane] = xn1;  // (read back by this wave only: in order, no barrier)
+        if (cur.qv) {
+            const PreTestV pt = pretest_v(a.bnd, inf.x, inf.y, eq, inf.z, th);
+            uint32_t mask = 0;
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const uint32_t row = uint32_t(16 * b + 4 * g + v);
+                    float xxp, nxp, exp;
+                    screen_norms(xs[row], xxp, nxp, exp);
+                    mask |= uint32_t((row < cur.rc) & !(acc[b][v] < pretest_rhs(pt, xxp, nxp, exp))) << (4 * b + v);
+                }
+            }
+            if (mask) {
+                uint32_t pos = atomicAdd(a.cnt + cur.qi, uint32_t(__popc(mask)));
+#pragma unroll
+                for (int b = 0; b < 8; ++b) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        if (!((mask >> (4 * b + v)) & 1u)) continue;
+                        if (pos < a.cap) {
+                            const int64_t o = int64_t(cur.qi) * a.cap + pos;
+                            a.cand_dot[o] = acc[b][v] * inf.z;
+                            a.cand_pos[o] = cur.rs + uint32_t(16 * b + 4 * g + v);
+                        }
+                        ++pos;
+                    }
+                }
+            }
+        }
+        if (!nxt.valid) break;
+        t += stride;
+        cur = nxt;
     }
 }
 
