@@ -436,9 +436,7 @@ __device__ __forceinline__ void append_pairs(const Ivf16Args& a, uint32_t qi, ui
 // result: lane (j, g) holds query j against rows 16b + 4g + v in acc[b][v].
 struct NarrowTile {
     uint32_t qs = 0, qc = 0, rs = 0, rc = 0;
-    uint32_t qi = 0;                 // the lane's query (query j of the tile; 0 past qc)
-    bool qv = false;                 // j < qc
-    const _Float16* qp = nullptr;    // its fp16 row at 16 g
+    uint32_t qi = 0;                 // the lane's query (query j of the tile; query 0 of it past qc)
     __amdgpu_buffer_rsrc_t xr;       // the tile's rows (loads past rc read zeros)
     bool valid = false;              // false: every load of the tile reads zeros
 };
@@ -583,11 +581,15 @@ __global__ __launch_bounds__(256) void ivf_bound_kernel(BoundV b, const float4* 
 // the next tile is located, and its first 64-value chunk requested, while the current one is
 // scanned, so the chunk's HBM latency overlaps the current tile's last chunk and epilogue; the
 // epilogue's inputs (the rows' {|x|^2, error bound}, the query's pre-test constants) are loaded
-// at the tile's start and used after its main loop.
+// at the tile's start and used after its main loop.  Every wait for a load also waits for the
+// loads issued before it, so each wait is placed where those are due anyway.
 __global__ __launch_bounds__(256, 2) void ivf16_narrow_kernel(Ivf16Args a) {
     __shared__ __attribute__((aligned(16))) float2 xs_all[iv16::WAVES][iv16::TN];
+    // a tile's 32 values per lane, kept for its appends ([b][lane]: conflict-free 16-byte accesses)
+    __shared__ __attribute__((aligned(16))) f32x4s dump_all[iv16::WAVES][8 * 64];
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
     float2* xs = xs_all[wave];
+    f32x4s* dump = dump_all[wave];
     const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
     const uint32_t total = a.plan.pre[a.plan.C];
     const uint32_t stride = gridDim.x * iv16::WAVES;
@@ -600,27 +602,25 @@ __global__ __launch_bounds__(256, 2) void ivf16_narrow_kernel(Ivf16Args a) {
     auto setup = [&](uint32_t tt, NarrowTile& T) {
         T.valid = tt < total;
         if (!T.valid) {
-            // no tile: a zero-length descriptor (every row load out of range) and a valid query
-            // pointer whose loads the mask zeroes
+            // no tile: a zero-length descriptor (every row load out of range); the query loads
+            // (of query 0) are zeroed by the mask
             T.qs = T.qc = T.rs = T.rc = T.qi = 0;
-            T.qv = false;
-            T.qp = a.qh;
             T.xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(a.xh), 0, 0, 0x00020000);
             return;
         }
         h = plan_tile_wave(a.plan, tt, h, 16, iv16::TN, T.qs, T.qc, T.rs, T.rc);
-        T.qv = uint32_t(j) < T.qc;
-        T.qi = a.qrow[T.qs + (T.qv ? uint32_t(j) : 0u)];
-        T.qp = a.qh + int64_t(T.qi) * a.Dp + 16 * g;
+        T.qi = a.qrow[T.qs + (uint32_t(j) < T.qc ? uint32_t(j) : 0u)];
         T.xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(a.xh + int64_t(T.rs) * a.Dp), 0,
                                                  int(T.rc * rowb), 0x00020000);
     };
     // chunk c of tile T (c past the last chunk, or an invalid tile: zeros, no memory traffic)
     auto load = [&](const NarrowTile& T, uint32_t c, h8v(&q2)[2], h8v(&r2)[8][2]) {
         const bool in = T.valid && c < nch;
+        const bool qv = uint32_t(j) < T.qc && in;
         const uint32_t k = in ? 64u * c : 0u;
-        q2[0] = masked_h8(T.qp + k, T.qv && in);
-        q2[1] = masked_h8(T.qp + k + 8, T.qv && in);
+        const _Float16* qp = a.qh + int64_t(T.qi) * a.Dp + 16 * g + k;
+        q2[0] = masked_h8(qp, qv);
+        q2[1] = masked_h8(qp + 8, qv);
         const uint32_t vo = in ? lo + 2u * k : 0x80000000u;
 #pragma unroll
         for (int b = 0; b < 8; ++b)
@@ -636,6 +636,26 @@ __global__ __launch_bounds__(256, 2) void ivf16_narrow_kernel(Ivf16Args a) {
 #pragma unroll
             for (int b = 0; b < 8; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(r2[b][u], q2[u], acc[b], 0, 0, 0);
     };
+    // The appends of a tile wait for their atomic's result, and the wait for a returning atomic
+    // also waits for every load issued before it (the next tile's chunk 0, in flight during the
+    // epilogue), so they run one tile late: the epilogue keeps the tile's values in LDS and issues
+    // the atomic; the stores follow at the next tile's first chunk step, where chunk 0 is due.
+    uint32_t p_mask = 0, p_qi = 0, p_rs = 0, p_pos = 0;
+    float p_inv = 0.0f;
+    const float* dumpf = reinterpret_cast<const float*>(dump);
+    auto flush = [&]() {
+        if (!__ballot(p_mask != 0u)) return;
+        uint32_t pos = p_pos, m = p_mask;
+        const int64_t ob = int64_t(p_qi) * a.cap;
+        while (m && pos < a.cap) {
+            const uint32_t tt = uint32_t(__builtin_ctz(m));  // value tt = 4 b + v: row 16 b + 4 g + v
+            m &= m - 1;
+            a.cand_dot[ob + pos] = dumpf[((tt >> 2) * 64 + uint32_t(lane)) * 4 + (tt & 3)] * p_inv;
+            a.cand_pos[ob + pos] = p_rs + 16 * (tt >> 2) + 4 * uint32_t(g) + (tt & 3);
+            ++pos;
+        }
+        p_mask = 0;
+    };
     NarrowTile cur, nxt;
     setup(t, cur);
     h8v qa[2], qb[2], ra[8][2], rb[8][2];
@@ -647,16 +667,18 @@ __global__ __launch_bounds__(256, 2) void ivf16_narrow_kernel(Ivf16Args a) {
         const float4 inf = a.qinfo[cur.qi];
         const float eq = a.qerr[cur.qi];
         const uint32_t th = a.thr[cur.qi];
-        // the next tile: its chunk 0 is requested during this tile's last chunk
-        setup(t + stride, nxt);
 #pragma unroll
         for (int b = 0; b < 8; ++b) acc[b] = f32x4s{0.f, 0.f, 0.f, 0.f};
         // an even number of chunks (one of zeros when nch is odd), so the next tile's chunk 0
         // always lands in the first register set
         for (uint32_t c = 0; c < nce; c += 2) {
+            if (c == 0) flush();  // the previous tile's appends (chunk 0, older than their atomic, is due now)
             load(cur, c + 1, qb, rb);
             compute(qa, ra);
             __builtin_amdgcn_sched_barrier(0);
+            // the next tile (its chunk 0 is requested during this tile's last step), located while
+            // chunk 1 is in flight: the lookup's waits also wait for chunk 1, which is due next
+            if (c == 0) setup(t + stride, nxt);
             if (c + 2 < nce) load(cur, c + 2, qa, ra);
             else load(nxt, 0, qa, ra);
             compute(qb, rb);
@@ -665,7 +687,7 @@ __global__ __launch_bounds__(256, 2) void ivf16_narrow_kernel(Ivf16Args a) {
         // ---- epilogue of this tile (the next tile's chunk 0 in flight)
         xs[lane] = xn0;
         xs[64 + lane] = xn1;  // (read back by this wave only: in order, no barrier)
-        if (cur.qv) {
+        if (uint32_t(j) < cur.qc) {
             const PreTestV pt = pretest_v(a.bnd, inf.x, inf.y, eq, inf.z, th);
             uint32_t mask = 0;
 #pragma unroll
@@ -679,26 +701,20 @@ __global__ __launch_bounds__(256, 2) void ivf16_narrow_kernel(Ivf16Args a) {
                 }
             }
             if (mask) {
-                uint32_t pos = atomicAdd(a.cnt + cur.qi, uint32_t(__popc(mask)));
 #pragma unroll
-                for (int b = 0; b < 8; ++b) {
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        if (!((mask >> (4 * b + v)) & 1u)) continue;
-                        if (pos < a.cap) {
-                            const int64_t o = int64_t(cur.qi) * a.cap + pos;
-                            a.cand_dot[o] = acc[b][v] * inf.z;
-                            a.cand_pos[o] = cur.rs + uint32_t(16 * b + 4 * g + v);
-                        }
-                        ++pos;
-                    }
-                }
+                for (int b = 0; b < 8; ++b) dump[b * 64 + lane] = acc[b];
+                p_pos = atomicAdd(a.cnt + cur.qi, uint32_t(__popc(mask)));  // (awaited in flush)
+                p_mask = mask;
+                p_qi = cur.qi;
+                p_rs = cur.rs;
+                p_inv = inf.z;
             }
         }
         if (!nxt.valid) break;
         t += stride;
         cur = nxt;
     }
+    flush();  // the last tile's appends
 }
 
 template <int W>
