@@ -718,7 +718,7 @@ __global__ __launch_bounds__(256, 2) void ivf16_narrow_kernel(Ivf16Args a) {
 }
 
 template <int W>
-__global__ __launch_bounds__(256, 1) void ivf16_wide_kernel(Ivf16Args a) {
+__global__ __launch_bounds__(256, W == 1 ? 2 : 1) void ivf16_wide_kernel(Ivf16Args a) {
     __shared__ __attribute__((aligned(16))) float2 xs[iv16::WAVES][iv16::TN];
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
     const uint32_t total = a.plan.pre[a.plan.C];
@@ -820,9 +820,15 @@ __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
     const uint32_t tpx = (total + kXcds - 1) / kXcds, xcd = blockIdx.x % kXcds;
     const uint32_t tend = min(total, (xcd + 1) * tpx);
     uint32_t lh = 0;  // the list of this workgroup's previous tile
+    uint32_t pqs = 0xFFFFFFFFu, pqc = 0;  // the query block the LDS holds (a list's row tiles share one)
     for (uint32_t t = xcd * tpx + blockIdx.x / kXcds; t < tend; t += gridDim.x / kXcds) {
         uint32_t qs, qc, rs, rc;
         lh = plan_tile_after_wave(a.plan, t, lh, TQ, TN, qs, qc, rs, rc);
+        // the queries and their constants stay in LDS from the previous tile when it had the same
+        // query block (consecutive tiles of a workgroup often are row blocks of one list)
+        const bool newq = qs != pqs || qc != pqc;
+        pqs = qs;
+        pqc = qc;
         __syncthreads();  // every wave is done with the previous tile's LDS
         // the tile's rows' {|x|^2, error} (past rc: zeros) by direct loads, and its queries,
         // chunk-major (16-byte chunk m of query r at m * CS + r * 16; past qc: zeros): thread
@@ -833,7 +839,7 @@ __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
                 lds_dma16(nres, uint32_t(tid) * 16u, lds0 + TQ * rowb + uint32_t(wave) * 1024u);
             }
             constexpr uint32_t QS = 512 / TQ, QT = QS * TQ;  // threads that copy queries
-            if (uint32_t(tid) < QT) {
+            if (newq && uint32_t(tid) < QT) {
                 const uint32_t r = uint32_t(tid) % TQ;
                 const bool qv = r < qc;
                 // buffer loads over all the fp16 queries (Q Dp 2 < 2^31 bytes): a query past qc or
@@ -859,7 +865,7 @@ __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
                 }
             }
         }
-        if (tid < TQ) {
+        if (newq && tid < TQ) {
             float4 p = {0.0f, 0.0f, 0.0f, 0.0f};
             float2 v = {0.0f, 0.0f};
             if (uint32_t(tid) < qc) {
@@ -1672,7 +1678,8 @@ va_status run_screen_pass(va_context* ctx, const DevPlan& dp, int pass, Ivf16Arg
         if (g == 0) {
             ivf16_narrow_kernel<<<dim3(uint32_t(ctx->num_cus) * 2), dim3(256), 0, s>>>(a);
         } else if (g == 1) {
-            ivf16_wide_kernel<1><<<dim3(uint32_t(ctx->num_cus)), dim3(256), 0, s>>>(a);
+            // two workgroups per CU (two waves per SIMD: one chunk in flight per wave)
+            ivf16_wide_kernel<1><<<dim3(uint32_t(ctx->num_cus) * 2), dim3(256), 0, s>>>(a);
         } else if (pass == 1 && dp.wide_tn) {
             // one workgroup per CU (the LDS); the ring depth divides the slots of a sub-tile
             const int nqb = ivr::nqb_for(a.Dp);
