@@ -682,7 +682,7 @@ def run_c5(ctx, a, cpu: bool):
     idx = ctx.empty((Q, k), torch.int32)
     dist = ctx.empty((Q, k), torch.float32)
     step = lambda: pipe.encodeSearch(q, st, idx, dist, k)  # noqa: E731
-    ms, _ = timed(ctx, step, max(3, a.steps // 2), 1, scan_timings=False)
+    ms, _ = timed(ctx, step, max(20, a.steps), 3, scan_timings=False)
     ph = ivf_phases(ctx, step)
     # the same search on the fp32 list scan alone: the same ids and distances, bit for bit
     idx32 = ctx.empty((Q, k), torch.int32)

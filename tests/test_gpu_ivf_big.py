@@ -89,7 +89,7 @@ def test_big_list_tiles_several_query_blocks(ctx, oracle):
 
 def test_big_list_tiles_flagged_rows(ctx, oracle):
     """Rows with entries beyond the fp16 range in a list probed by many queries: flagged rows pass
-    the pre-test (the quick rejection is off for their blocks) and their exact keys decide."""
+    the pre-test (their NaN inputs make every comparison pass) and their exact keys decide."""
     c, x, q = clustered(8, 64, 16000, 300, 29, None)
     g = np.random.default_rng(9)
     far = g.choice(16000, 300, replace=False)

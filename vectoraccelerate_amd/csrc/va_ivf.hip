@@ -1029,9 +1029,9 @@ __global__ __launch_bounds__(512, 2) void ivf16_resq_kernel(Ivf16Args a) {
 // NSLOT slots of KC d-values with NSLOT - 1 stages in flight while one computes.  The tile's
 // pre-test constants come from the plan-slot table (ivf_slot_pretest_kernel: one load per query,
 // no gather) and its rows' {|x|^2, error bound} with one load per row, both loaded at the tile's
-// start and used after its main loop.  The epilogue is the flat screen's (a quick rejection per
-// lane and 32-row block from a box of the rows' pre-test inputs, the rest through LDS) with the
-// list pre-test A|x|^2 + B|x| + E ex + C and (value, CSR position) appends.
+// start and used after its main loop.  The epilogue tests every value from registers against the
+// list pre-test A|x|^2 + B|x| + E ex + C (a lane reads each 4-row group's inputs from LDS once for
+// both of its queries) and appends (value, CSR position).
 namespace ivb {
 constexpr int NQB = 2, MB = 2;  // a wave: 32 NQB queries x 32 MB rows
 template <int WAVES, int TQ, int KC, int NSLOT>
@@ -1103,8 +1103,6 @@ __global__ __launch_bounds__(64 * WAVES, 1) void ivf16_big_kernel(Ivf16Args a) {
     typedef float f32x4v __attribute__((ext_vector_type(4)));
     extern __shared__ __attribute__((aligned(1024))) char lds[];
     __shared__ __attribute__((aligned(16))) float norms[3 * TN];  // pre-test inputs xx, nx, ex (NaN: flagged)
-    __shared__ float4 gbox[TN / 4];  // per 4-row group {xx lo, xx hi, nx lo, nx hi}, x NaN if a row is flagged
-    __shared__ float2 gbe[TN / 4];   // {ex lo, ex hi}
     __shared__ float4 ptl[TQ];       // {A, B, E, C} of the tile's queries
     __shared__ float2 pqv[TQ];       // {2^-scale, query id}
     __shared__ uint32_t tcount[TQ];  // the tile's passes per query (zero between tiles)
@@ -1291,32 +1289,10 @@ __global__ __launch_bounds__(64 * WAVES, 1) void ivf16_big_kernel(Ivf16Args a) {
             pqv[tid] = qv_t;
         }
         __syncthreads();  // every wave is past the main loop: every slot is free
-        // the pre-test inputs' box of each 4-row group (NaN x when a row of it is flagged)
-        if (tid < TN / 4) {
-            float4 b = {INFINITY, -INFINITY, INFINITY, -INFINITY};
-            float2 e = {INFINITY, -INFINITY};
-            bool f = false;
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const float x2 = xxp[4 * tid + v], x1 = nxp[4 * tid + v], xe = exq[4 * tid + v];
-                f |= !(x2 == x2) || !(x1 == x1) || !(xe == xe);
-                b.x = fminf(b.x, x2);
-                b.y = fmaxf(b.y, x2);
-                b.z = fminf(b.z, x1);
-                b.w = fmaxf(b.w, x1);
-                e.x = fminf(e.x, xe);
-                e.y = fmaxf(e.y, xe);
-            }
-            if (f) b.x = __builtin_nanf("");
-            gbox[tid] = b;
-            gbe[tid] = e;
-        }
-        __syncthreads();
 
         // ---- epilogue: lane (l32, hh) holds query wq*WQ + 32n + l32 against rows
         // wn*WN + 32m + 8j + 4hh + e in acc[m][n][4j + e]; t = 16m + 4j + e indexes its 16 MB values.
-        // 1. the passes of each query block as a bit mask (quick rejection from registers, else the
-        //    values through the wave's dump); 2. each lane pair's count added to its query's tile
+        // 1. the passes of each query block as a bit mask; 2. each lane pair's count added to its query's tile
         //    count in LDS (the returned value is the pair's offset in the query's share of the tile);
         // 3. one global atomic per query of the tile reserves its share of the candidate list (a
         //    list probed by many queries appends for most of them in every tile, so per-wave atomics
@@ -1329,22 +1305,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void ivf16_big_kernel(Ivf16Args a) {
 #pragma unroll 1
             for (int v = 0; v < 16 * MB; ++v) valid |= Mask(uint32_t(row_of(v)) < rc) << v;
         }
-        float bxlo = INFINITY, bxhi = -INFINITY, bnlo = INFINITY, bnhi = -INFINITY, belo = INFINITY, behi = -INFINITY;
-        bool bflag = false;
-#pragma unroll
-        for (int c = 0; c < 4 * MB; ++c) {
-            const int gi = row_of(4 * c) >> 2;  // rows 4c .. 4c + 3 of the lane: one group
-            const float4 b = gbox[gi];
-            const float2 e = gbe[gi];
-            bflag |= !(b.x == b.x);
-            bxlo = fminf(bxlo, b.x);
-            bxhi = fmaxf(bxhi, b.y);
-            bnlo = fminf(bnlo, b.z);
-            bnhi = fmaxf(bnhi, b.w);
-            belo = fminf(belo, e.x);
-            behi = fmaxf(behi, e.y);
-        }
-        // row block m of query block n into the dump: values 16m .. 16m + 15
+        // row block m of query block n into the dump (for the appends): values 16m .. 16m + 15
         auto dump_half = [&](auto NC, auto MC) {
             constexpr int n = decltype(NC)::value, m = decltype(MC)::value;
 #pragma unroll
@@ -1356,47 +1317,33 @@ __global__ __launch_bounds__(64 * WAVES, 1) void ivf16_big_kernel(Ivf16Args a) {
             }
             asm volatile("" ::: "memory");  // re-read the dump from LDS below
         };
-        auto mask_of = [&](auto NC) -> Mask {
-            constexpr int n = decltype(NC)::value;
-            const uint32_t qt = uint32_t(wq * WQ + 32 * n + l32);
-            const float4 p = ptl[qt];
-            const PreTestV pt = {p.x, p.y, p.z, p.w};
-            bool skip = qt >= qc;
-            if (!bflag && !skip) {
-                // the right-hand side over the lane's rows is bounded below at the box corner that
-                // the signs of A, B and E select (each fma is monotone in its operands)
-                const float lo = fmaf(pt.A, pt.A >= 0.0f ? bxlo : bxhi,
-                                      fmaf(pt.B, pt.B >= 0.0f ? bnlo : bnhi, fmaf(pt.E, pt.E >= 0.0f ? belo : behi, pt.C)));
-                float mx = -INFINITY;
+        // 1. the passes of the lane's two queries over its 32 rows, tested from registers: each 4-row
+        //    group's pre-test inputs are read once for both queries (a list probed by this many
+        //    queries has candidates in most row blocks, so no quick rejection precedes the test)
+        static_assert(NQB == 2, "two query blocks per wave");
+        Mask mk0 = 0, mk1 = 0;
+        {
+            const uint32_t qt0 = uint32_t(wq * WQ + l32), qt1 = qt0 + 32u;
+            const float4 p0 = ptl[qt0], p1 = ptl[qt1];
+            const PreTestV pt0 = {p0.x, p0.y, p0.z, p0.w}, pt1 = {p1.x, p1.y, p1.z, p1.w};
 #pragma unroll
-                for (int v = 0; v < 16 * MB; ++v) mx = fmaxf(mx, acc[v >> 4][n][v & 15]);
-                skip = mx < lo;
-            }
-            Mask mk = 0;
-            if (!skip) {
-                auto test_half = [&](auto MC) {
-                    constexpr int m = decltype(MC)::value;
-                    dump_half(NC, MC);
-#pragma unroll 2
-                    for (int c = 0; c < 4; ++c) {
-                        const int r = row_of(16 * m + 4 * c);
-                        const f32x4v x2 = *reinterpret_cast<const f32x4v*>(xxp + r);
-                        const f32x4v x1 = *reinterpret_cast<const f32x4v*>(nxp + r);
-                        const f32x4v xe = *reinterpret_cast<const f32x4v*>(exq + r);
-                        const f32x4v v = dump[c * 64];
+            for (int m = 0; m < MB; ++m)
 #pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            mk |= Mask(!(v[e] < pretest_rhs(pt, x2[e], x1[e], xe[e]))) << (16 * m + 4 * c + e);
+                for (int c = 0; c < 4; ++c) {
+                    const int r = row_of(16 * m + 4 * c);  // rows r .. r + 3
+                    const f32x4v x2 = *reinterpret_cast<const f32x4v*>(xxp + r);
+                    const f32x4v x1 = *reinterpret_cast<const f32x4v*>(nxp + r);
+                    const f32x4v xe = *reinterpret_cast<const f32x4v*>(exq + r);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int t = 16 * m + 4 * c + e;
+                        mk0 |= Mask(!(acc[m][0][4 * c + e] < pretest_rhs(pt0, x2[e], x1[e], xe[e]))) << t;
+                        mk1 |= Mask(!(acc[m][1][4 * c + e] < pretest_rhs(pt1, x2[e], x1[e], xe[e]))) << t;
                     }
-                };
-                test_half(std::integral_constant<int, 0>());
-                test_half(std::integral_constant<int, 1>());
-                mk &= valid;
-            }
-            return mk;
-        };
-        const Mask mk0 = mask_of(std::integral_constant<int, 0>());
-        const Mask mk1 = mask_of(std::integral_constant<int, 1>());
+                }
+            mk0 &= qt0 < qc ? valid : Mask(0);
+            mk1 &= qt1 < qc ? valid : Mask(0);
+        }
         // 2. the pair's offset in its query's share of the tile (lane l32 adds both halves' passes)
         uint32_t off0 = 0, off1 = 0;
         {
