@@ -167,7 +167,7 @@ va_status fill_u32(va_context* ctx, uint32_t* p, uint64_t n, uint32_t v) {
     return VA_OK;
 }
 
-va_status aux_fork(va_context* ctx) {
+va_status aux_fork(va_context* ctx, int n) {
     if (!ctx->fork_ev) {
         VA_CHECK_HIP(ctx, hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming));
         for (int i = 0; i < va_context::kAux; ++i) {
@@ -177,12 +177,13 @@ va_status aux_fork(va_context* ctx) {
         }
     }
     VA_CHECK_HIP(ctx, hipEventRecord(ctx->fork_ev, ctx->stream));
-    for (int i = 0; i < va_context::kAux; ++i) VA_CHECK_HIP(ctx, hipStreamWaitEvent(ctx->aux[i], ctx->fork_ev, 0));
+    for (int i = 0; i < std::min(n, va_context::kAux); ++i)
+        VA_CHECK_HIP(ctx, hipStreamWaitEvent(ctx->aux[i], ctx->fork_ev, 0));
     return VA_OK;
 }
 
-va_status aux_join(va_context* ctx) {
-    for (int i = 0; i < va_context::kAux; ++i) {
+va_status aux_join(va_context* ctx, int n) {
+    for (int i = 0; i < std::min(n, va_context::kAux); ++i) {
         VA_CHECK_HIP(ctx, hipEventRecord(ctx->join_ev[i], ctx->aux[i]));
         VA_CHECK_HIP(ctx, hipStreamWaitEvent(ctx->stream, ctx->join_ev[i], 0));
     }

@@ -22,9 +22,14 @@ va_status fb_init(va_context* ctx, const FbArgs& a) {
     return VA_OK;
 }
 
-va_status fb_run(va_context* ctx, KeyProducer& kp, const FbArgs& a, const SelectArgs& base) {
+va_status fb_passes(va_context* ctx, KeyProducer& kp, const FbArgs& a) {
     VA_CHECK_STATUS(fb_init(ctx, a));
     for (int pass = 0; pass < kFbPasses; ++pass) VA_CHECK_STATUS(kp.fallback_pass(a, pass));
+    return VA_OK;
+}
+
+va_status fb_run(va_context* ctx, KeyProducer& kp, const FbArgs& a, const SelectArgs& base) {
+    VA_CHECK_STATUS(fb_passes(ctx, kp, a));
     return fb_select(ctx, a, base, kp.key_bits());
 }
 

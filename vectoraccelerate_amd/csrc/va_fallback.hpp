@@ -560,6 +560,9 @@ va_status fb_launch_pass(va_context* ctx, const P& p, const FbArgs& a, int pass)
 // Enqueues the whole fallback (clear, five passes, selection) for the producer's keys; base
 // carries the outputs and the key kind of the scan's selection.
 va_status fb_run(va_context* ctx, KeyProducer& kp, const FbArgs& a, const SelectArgs& base);
+// fb_run without the selection: the clear and the passes, which write only a's buffers (a caller
+// may run them on another stream and select after joining it).
+va_status fb_passes(va_context* ctx, KeyProducer& kp, const FbArgs& a);
 // The clear before the first pass and the selection after the last, for callers with their own
 // pass kernels (the IVF list scan).
 va_status fb_init(va_context* ctx, const FbArgs& a);

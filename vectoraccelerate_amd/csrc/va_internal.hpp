@@ -78,11 +78,22 @@ va_status side_reserve(va_context* ctx, size_t bytes, void** out);
 // Records an error message on the context and returns the status.
 va_status fail(va_context* ctx, va_status st, const char* fmt, ...);
 
-// Makes every ctx->aux[i] wait for the work queued so far on ctx->stream (creating them on
-// first use).
-va_status aux_fork(va_context* ctx);
-// Makes ctx->stream wait for the work queued so far on every ctx->aux[i].
-va_status aux_join(va_context* ctx);
+// Makes ctx->aux[0 .. n) wait for the work queued so far on ctx->stream (creating every aux
+// stream on first use).
+va_status aux_fork(va_context* ctx, int n = va_context::kAux);
+// Makes ctx->stream wait for the work queued so far on ctx->aux[0 .. n).
+va_status aux_join(va_context* ctx, int n = va_context::kAux);
+
+// Sends what the code in the scope queues on ctx->stream to another stream (an aux stream, forked
+// from ctx->stream before the scope and joined after it).
+struct StreamScope {
+    va_context* ctx;
+    hipStream_t prev;
+    StreamScope(va_context* c, hipStream_t s) : ctx(c), prev(c->stream) { c->stream = s; }
+    ~StreamScope() { ctx->stream = prev; }
+    StreamScope(const StreamScope&) = delete;
+    StreamScope& operator=(const StreamScope&) = delete;
+};
 
 // Makes `ctx->device` current for the lifetime of the guard.
 struct DeviceGuard {

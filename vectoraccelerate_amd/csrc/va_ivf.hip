@@ -1602,7 +1602,11 @@ va_status run_screen_pass(va_context* ctx, const DevPlan& dp, int pass, Ivf16Arg
     a.plan.C = dp.C;
     a.plan.sample = pass == 0 ? 1u : 0u;
     va_status st = VA_OK;
-    VA_CHECK_STATUS(aux_fork(ctx));
+    // the groups after the first run on aux streams 0 .. kGroupsUsed - 2 (each fork and join is a
+    // barrier packet on the context's stream: only the streams used)
+    constexpr int kAuxUsed = iv16::kGroupsUsed - 1;
+    static_assert(kAuxUsed <= va_context::kAux, "one aux stream per group after the first");
+    VA_CHECK_STATUS(aux_fork(ctx, kAuxUsed));
     if (pass == 1 && dp.big_tq) {
         // on the context's stream, ahead of the narrow tiles, while the wide groups start on the
         // auxiliary streams
@@ -1656,7 +1660,7 @@ va_status run_screen_pass(va_context* ctx, const DevPlan& dp, int pass, Ivf16Arg
         }
         if (hipGetLastError() != hipSuccess) st = fail(ctx, VA_ERR_HIP, "screened list scan launch failed");
     }
-    const va_status j = aux_join(ctx);
+    const va_status j = aux_join(ctx, kAuxUsed);
     return st != VA_OK ? st : j;
 }
 
@@ -1843,9 +1847,11 @@ __global__ __launch_bounds__(256) void ivf_rerank_kernel(const float* __restrict
 }
 
 // Exact top-k, on the device, of the queries listed in fb (their candidates outgrew a list):
-// their probed lists walked with the arithmetic of the kernel that scans each list.
-va_status ivf_fallback(va_context* ctx, const va_ivf* ivf, const float* queries, const DevPlan& dp, uint32_t np,
-                       const FbArgs& fb, const SelectArgs& base) {
+// their probed lists walked with the arithmetic of the kernel that scans each list.  The passes
+// read only the queries, the lists, the plan and fb's list of queries, and write only fb's
+// buffers; the selection writes the listed queries' results.
+va_status ivf_fallback_passes(va_context* ctx, const va_ivf* ivf, const float* queries, const DevPlan& dp, uint32_t np,
+                              const FbArgs& fb) {
     VA_CHECK_STATUS(fb_init(ctx, fb));
     FbIvf v;
     v.q = queries;
@@ -1867,6 +1873,11 @@ va_status ivf_fallback(va_context* ctx, const va_ivf* ivf, const float* queries,
             fb_ivf_pass_kernel<false><<<dim3(fb.grid), dim3(256), 0, ctx->stream>>>(v, fb, pass);
         VA_CHECK_LAUNCH(ctx);
     }
+    return VA_OK;
+}
+va_status ivf_fallback(va_context* ctx, const va_ivf* ivf, const float* queries, const DevPlan& dp, uint32_t np,
+                       const FbArgs& fb, const SelectArgs& base) {
+    VA_CHECK_STATUS(ivf_fallback_passes(ctx, ivf, queries, dp, np, fb));
     return fb_select(ctx, fb, base, 32);
 }
 
@@ -2072,6 +2083,14 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
     // ---- 4. rerank lists, 5. exact keys ----------------------------------------------------------
     VA_CHECK_STATUS(screen_compact(ctx, cnt, clo, cpos, ubound, uint32_t(cap), Q, rr, rcount, uint32_t(rcap), ovf_cnt,
                                    ovf_rows));
+    // ---- 7a. the overflowed queries (listed by the U_q selection and the compaction) take the
+    // device fallback's passes on an aux stream, beside the rerank and the selection (a search
+    // with none still pays their launches, off the critical path here)
+    VA_CHECK_STATUS(aux_fork(ctx, 1));
+    {
+        StreamScope on_aux(ctx, ctx->aux[0]);
+        VA_CHECK_STATUS(ivf_fallback_passes(ctx, ivf, queries, dp, np, fb));
+    }
     {
         const uint64_t items = uint64_t(Q) * ((rcap + 63) / 64);
         const uint32_t blocks = uint32_t(std::min<uint64_t>(2048, (items + 3) / 4));
@@ -2102,7 +2121,9 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
     VA_CHECK_STATUS(pm.count_sum(rcount, Q));
     VA_CHECK_STATUS(pm.count_overflow(ovf_cnt));
     VA_CHECK_STATUS(pm.mark(3));
-    VA_CHECK_STATUS(ivf_fallback(ctx, ivf, queries, dp, np, fb, base));
+    // ---- 7b. their exact top-k over the rows the selection wrote
+    VA_CHECK_STATUS(aux_join(ctx, 1));
+    VA_CHECK_STATUS(fb_select(ctx, fb, base, 32));
     return pm.finish(true, true);
 }
 }  // namespace

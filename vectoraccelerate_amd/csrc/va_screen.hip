@@ -1769,6 +1769,14 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
                                                                  rcount, uint32_t(rcap), ovf_cnt, ovf_rows,
                                                                  ovf_cnt + 1);
     VA_CHECK_LAUNCH(ctx);
+    if (device_fb) {
+        // ---- 8a. the overflowed queries (listed by steps 4 and 5) take the device fallback's
+        // passes on an aux stream, beside the rerank and the selection (a search with none still
+        // pays their launches, off the critical path here)
+        VA_CHECK_STATUS(aux_fork(ctx, 1));
+        StreamScope on_aux(ctx, ctx->aux[0]);
+        VA_CHECK_STATUS(fb_passes(ctx, exact, fb));
+    }
     // Without the device fallback the overflow count is read back (one synchronisation).
     uint32_t n_ovf = 0;
     if (!device_fb) {
@@ -1810,8 +1818,9 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     if (device_fb) VA_CHECK_STATUS(pm.count_overflow(ovf_cnt));
     VA_CHECK_STATUS(pm.mark(3));
     if (device_fb) {
-        // ---- 8. exact top-k of the overflowed queries, on the device ---------------------------
-        VA_CHECK_STATUS(fb_run(ctx, exact, fb, base));
+        // ---- 8b. their exact top-k, over the rows step 7 wrote ----------------------------------
+        VA_CHECK_STATUS(aux_join(ctx, 1));
+        VA_CHECK_STATUS(fb_select(ctx, fb, base, exact.key_bits()));
         return pm.finish(true, true);
     }
     ctx->last_scan.overflow_rows = n_ovf;
