@@ -112,7 +112,8 @@ def timed(ctx, fn, steps: int, warmup: int, scan_timings: bool = True, phase_rep
     With scan_timings, the timed loop runs at profiling level 2 (the library records two hipEvents
     around each scan phase on its stream, which nothing waits for inside the loop: the scan
     kernel's mean duration over exactly the timed steps), and `phase_reps` more steps after it at
-    level 1 give the breakdown of the other phases and the counts (outside the timed loop)."""
+    level 1 give the breakdown of the other phases and the counts (outside the timed loop).
+    Without, the timed loop runs with profiling off (level 1 is restored after it)."""
     import torch
 
     for _ in range(warmup):
@@ -122,6 +123,8 @@ def timed(ctx, fn, steps: int, warmup: int, scan_timings: bool = True, phase_rep
     if scan_timings:
         ctx.set_profiling(2)
         ctx.reset_scan_totals()
+    else:
+        ctx.set_profiling(0)
     t0 = time.perf_counter()
     for _ in range(steps):
         fn()
@@ -129,6 +132,7 @@ def timed(ctx, fn, steps: int, warmup: int, scan_timings: bool = True, phase_rep
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
     if not scan_timings:
+        ctx.set_profiling(True)
         return ms, None
     total, n = ctx.scan_totals()
     ctx.set_profiling(True)
