@@ -72,9 +72,9 @@ enum ScreenMode : int { SCREEN_KEYS = 0, SCREEN_FILTER = 1, SCREEN_GMIN = 2 };
 // below this many queries a search over the fp16 shadow takes screen16_small_kernel (a 256-query
 // tile of screen16_kernel would be mostly padding)
 constexpr uint32_t kSmallBatch = 192;
-// screen16_small_kernel serves at most this many queries: above it a 256-query tile of
+// screen16_small_kernel serves at most this many queries: above it a query tile of
 // screen16_kernel (MFMA-bound) costs less than the small kernel's query-register traffic
-// (measured at 1M x 768: 64 queries 0.63 ms small, ~0.41 ms in one screen16 tile)
+// (measured at 1M x 768: 64 queries 0.63 ms small, ~0.41 ms in one 256-query screen16 tile)
 constexpr uint32_t kSmallBatchMax = 32;
 
 struct ScreenArgs {
@@ -715,14 +715,15 @@ __global__ __launch_bounds__(256, 1) void screen_kernel(ScreenArgs a) {
 // run, and the stage barrier sits inside the last k-step of a stage, after its fragments are in
 // registers (a bare s_barrier: the direct loads of the next stage stay in flight across it).
 namespace s16 {
-constexpr int TQ = 256, KC = 64;
+constexpr int TQ = 256, KC = 64;  // (TQ: the default query tile)
 constexpr int ROWB = KC * 2;              // bytes per LDS row
 // the wave layout of the launch: waves per workgroup, 32-query and 32-row blocks per wave
 constexpr int kWaves = 16, kQueryBlocks = 2, kRowBlocks = 2;
 // A workgroup of WAVES waves, each (32 NQB queries) x (32 MB rows), over a tile of TQ queries x
 // TN rows; a stage holds 64 d-values of both (queries, then rows), two stages in LDS.
-template <int WAVES, int NQB, int MB>
+template <int WAVES, int NQB, int MB, int TQ_ = TQ>
 struct Shape {
+    static constexpr int TQ = TQ_;
     static constexpr int WQ = 32 * NQB, WN = 32 * MB;  // a wave's queries x rows
     static constexpr int QW = TQ / WQ;                 // waves along the queries
     static constexpr int TN = WN * (WAVES / QW);
@@ -739,11 +740,13 @@ struct Shape {
 };
 }  // namespace s16
 
-// WAVES waves of (32 NQB queries) x (32 MB rows): four waves per SIMD at 16 waves
-template <int WAVES, int NQB, int MB>
+// WAVES waves of (32 NQB queries) x (32 MB rows) over tiles of TQ_ queries: four waves per SIMD
+// at 16 waves
+template <int WAVES, int NQB, int MB, int TQ_ = s16::TQ>
 __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(ScreenArgs a) {
     using namespace s16;
-    using Sh = Shape<WAVES, NQB, MB>;
+    using Sh = Shape<WAVES, NQB, MB, TQ_>;
+    constexpr int TQ = Sh::TQ;
     constexpr int WQ = Sh::WQ, WN = Sh::WN, QW = Sh::QW, TN = Sh::TN;
     constexpr int OPQ = Sh::OPQ, STAGE = Sh::STAGE, GQ = Sh::GQ, GX = Sh::GX, LPW = Sh::LPW;
     extern __shared__ __attribute__((aligned(1024))) char lds[];
@@ -1423,9 +1426,14 @@ va_status launch_screen(va_context* ctx, const ScreenArgs& a) {
     return VA_OK;
 }
 
-va_status launch_screen16(va_context* ctx, const ScreenArgs& a) {
-    using namespace s16;
-    using Sh = Shape<kWaves, kQueryBlocks, kRowBlocks>;
+// Batches of at most kHalfTileQueries queries take a 128-query x 384-row tile of twelve waves
+// (the same wave tiles, three waves per SIMD): a 256-query tile would be more than half padding,
+// and the kernel is MFMA-bound (1M x 768, Q = 100: screen 0.40 -> 0.33 ms; eight waves of a
+// 128 x 256 tile, two per SIMD: 0.36 ms).
+constexpr uint32_t kHalfTileQueries = 128;
+template <int WAVES, int NQB, int MB, int TQ>
+va_status launch_screen16_shape(va_context* ctx, const ScreenArgs& a) {
+    using Sh = s16::Shape<WAVES, NQB, MB, TQ>;
     const uint64_t nqb = (a.Q + TQ - 1) / TQ;
     const uint64_t ntb = (a.N + Sh::TN - 1) / Sh::TN;
     const uint64_t tiles = nqb * ((ntb + kXcds - 1) / kXcds) * kXcds;
@@ -1434,12 +1442,18 @@ va_status launch_screen16(va_context* ctx, const ScreenArgs& a) {
     // persistent: one workgroup per CU (its LDS fills one), a multiple of the XCD count
     const uint64_t cus = std::max<uint64_t>(uint64_t(ctx->num_cus), kXcds) / kXcds * kXcds;
     const uint64_t grid = std::min(tiles, cus);
-    auto kern = &screen16_kernel<kWaves, kQueryBlocks, kRowBlocks>;
+    auto kern = &screen16_kernel<WAVES, NQB, MB, TQ>;
     VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, Sh::LDS));
-    kern<<<dim3(uint32_t(grid)), dim3(64 * kWaves), Sh::LDS, ctx->stream>>>(a);
+    kern<<<dim3(uint32_t(grid)), dim3(64 * WAVES), Sh::LDS, ctx->stream>>>(a);
     VA_CHECK_LAUNCH(ctx);
     return VA_OK;
+}
+va_status launch_screen16(va_context* ctx, const ScreenArgs& a) {
+    using namespace s16;
+    if (a.Q <= kHalfTileQueries)
+        return launch_screen16_shape<3 * kWaves / 4, kQueryBlocks, kRowBlocks, int(kHalfTileQueries)>(ctx, a);
+    return launch_screen16_shape<kWaves, kQueryBlocks, kRowBlocks, TQ>(ctx, a);
 }
 
 // The small-batch screen: NQB 16-query blocks x MB 16-row blocks per wave, chunks of 64 L bytes
