@@ -84,6 +84,25 @@ va_status aux_fork(va_context* ctx, int n = va_context::kAux);
 // Makes ctx->stream wait for the work queued so far on ctx->aux[0 .. n).
 va_status aux_join(va_context* ctx, int n = va_context::kAux);
 
+// Joins ctx->aux[0 .. n) into ctx->stream when it leaves scope unless join() ran first, so an
+// error return between a fork and its join still orders the aux work before anything the caller
+// queues next (scratch buffers the aux work writes are reused by later calls).
+struct AuxJoinGuard {
+    va_context* ctx;
+    int n;
+    bool armed = true;
+    AuxJoinGuard(va_context* c, int k) : ctx(c), n(k) {}
+    va_status join() {
+        armed = false;
+        return aux_join(ctx, n);
+    }
+    ~AuxJoinGuard() {
+        if (armed) (void)aux_join(ctx, n);
+    }
+    AuxJoinGuard(const AuxJoinGuard&) = delete;
+    AuxJoinGuard& operator=(const AuxJoinGuard&) = delete;
+};
+
 // Sends what the code in the scope queues on ctx->stream to another stream (an aux stream, forked
 // from ctx->stream before the scope and joined after it).
 struct StreamScope {

@@ -2087,6 +2087,7 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
     // device fallback's passes on an aux stream, beside the rerank and the selection (a search
     // with none still pays their launches, off the critical path here)
     VA_CHECK_STATUS(aux_fork(ctx, 1));
+    AuxJoinGuard fb_join(ctx, 1);
     {
         StreamScope on_aux(ctx, ctx->aux[0]);
         VA_CHECK_STATUS(ivf_fallback_passes(ctx, ivf, queries, dp, np, fb));
@@ -2122,7 +2123,7 @@ va_status ivf_scan_screened(va_context* ctx, const va_ivf* ivf, const float* que
     VA_CHECK_STATUS(pm.count_overflow(ovf_cnt));
     VA_CHECK_STATUS(pm.mark(3));
     // ---- 7b. their exact top-k over the rows the selection wrote
-    VA_CHECK_STATUS(aux_join(ctx, 1));
+    VA_CHECK_STATUS(fb_join.join());
     VA_CHECK_STATUS(fb_select(ctx, fb, base, 32));
     return pm.finish(true, true);
 }

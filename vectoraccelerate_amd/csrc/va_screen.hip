@@ -1783,6 +1783,7 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
                                                                  rcount, uint32_t(rcap), ovf_cnt, ovf_rows,
                                                                  ovf_cnt + 1);
     VA_CHECK_LAUNCH(ctx);
+    AuxJoinGuard fb_join(ctx, device_fb ? 1 : 0);
     if (device_fb) {
         // ---- 8a. the overflowed queries (listed by steps 4 and 5) take the device fallback's
         // passes on an aux stream, beside the rerank and the selection (a search with none still
@@ -1833,7 +1834,7 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
     VA_CHECK_STATUS(pm.mark(3));
     if (device_fb) {
         // ---- 8b. their exact top-k, over the rows step 7 wrote ----------------------------------
-        VA_CHECK_STATUS(aux_join(ctx, 1));
+        VA_CHECK_STATUS(fb_join.join());
         VA_CHECK_STATUS(fb_select(ctx, fb, base, exact.key_bits()));
         return pm.finish(true, true);
     }
