@@ -741,12 +741,18 @@ struct Shape {
 }  // namespace s16
 
 // WAVES waves of (32 NQB queries) x (32 MB rows) over tiles of TQ_ queries: four waves per SIMD
-// at 16 waves
-template <int WAVES, int NQB, int MB, int TQ_ = s16::TQ>
+// at 16 waves.  MODE SCREEN_FILTER: the screen's pre-tested appends; SCREEN_GMIN: the threshold
+// sample's group minima (screen_kernel's SCREEN_GMIN values) over shadow rows j * xstride.
+template <int WAVES, int NQB, int MB, int TQ_ = s16::TQ, int MODE = SCREEN_FILTER>
 __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(ScreenArgs a) {
     using namespace s16;
     using Sh = Shape<WAVES, NQB, MB, TQ_>;
     constexpr int TQ = Sh::TQ;
+    static_assert(MODE == SCREEN_FILTER || MODE == SCREEN_GMIN, "filter or group-minimum epilogue");
+    static_assert(MODE != SCREEN_GMIN || (Sh::TN == scr::TN && 32 * MB * (WAVES / Sh::QW) == scr::TN),
+                  "the group layout of screen_kernel's SCREEN_GMIN output");
+    // rows of the scan: shadow rows j * xs (the sample's stride; 1 for the screen)
+    const uint32_t xs = MODE == SCREEN_GMIN ? a.xstride : 1u;
     constexpr int WQ = Sh::WQ, WN = Sh::WN, QW = Sh::QW, TN = Sh::TN;
     constexpr int OPQ = Sh::OPQ, STAGE = Sh::STAGE, GQ = Sh::GQ, GX = Sh::GX, LPW = Sh::LPW;
     extern __shared__ __attribute__((aligned(1024))) char lds[];
@@ -786,13 +792,15 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
         tile_of(T, qb, tb);
         const uint32_t q0 = qb * TQ, r0 = tb * TN;
         qr = make_dma_rsrc(a.qh + int64_t(q0) * a.Dp, min(uint32_t(TQ), a.Q - q0) * a.Dp * 2u);
-        xr = make_dma_rsrc(a.xh + int64_t(r0) * a.Dp, min(uint32_t(TN), a.N - r0) * a.Dp * 2u);
+        xr = make_dma_rsrc(a.xh + int64_t(r0) * xs * a.Dp, ((min(uint32_t(TN), a.N - r0) - 1u) * xs + 1u) * a.Dp * 2u);
     };
-    uint32_t off[LPW];
+    uint32_t off[LPW], offx[LPW];
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
         const int row = 8 * (wave + WAVES * i) + (lane >> 3);
-        off[i] = uint32_t(row) * a.Dp * 2u + 16u * uint32_t((lane & 7) ^ ((row >> 1) & 7));
+        const uint32_t ch = 16u * uint32_t((lane & 7) ^ ((row >> 1) & 7));
+        off[i] = uint32_t(row) * a.Dp * 2u + ch;
+        offx[i] = uint32_t(row) * xs * a.Dp * 2u + ch;
     }
     const uint32_t lds0 = lds_addr_of(lds);
     auto issue_with = [&](const dma_rsrc& qr, const dma_rsrc& xr, uint32_t s) {
@@ -805,7 +813,7 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
                                              // cover exactly the operand's groups
             if (GQ == LPW * WAVES || g < GQ) lds_dma16(qr, ok ? off[i] + d0 * 2u : kDmaSkip, sb + uint32_t(g) * 1024u);
             if (GX == LPW * WAVES || g < GX)
-                lds_dma16(xr, ok ? off[i] + d0 * 2u : kDmaSkip, sb + uint32_t(OPQ + g * 1024));
+                lds_dma16(xr, ok ? offx[i] + d0 * 2u : kDmaSkip, sb + uint32_t(OPQ + g * 1024));
         }
     };
     // fragment rows start at multiples of 32, so the chunk swizzle is (l32 >> 1) & 7 for both
@@ -867,7 +875,7 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
         const uint32_t qs = qb * TQ, rs = tb * TN;
         const uint32_t qc = min(uint32_t(TQ), a.Q - qs), rc = min(uint32_t(TN), a.N - rs);
         // the tile's squared row norms: loaded now (one register), used after the main loop
-        const float xn_t = tid < TN && uint32_t(tid) < rc ? a.xn[rs + uint32_t(tid)] : 0.0f;
+        const float xn_t = tid < TN && uint32_t(tid) < rc ? a.xn[uint64_t(rs + uint32_t(tid)) * xs] : 0.0f;
         auto issue = [&](uint32_t s) { issue_with(qres, xres, s); };
 #pragma unroll
         for (int m = 0; m < MB; ++m)
@@ -918,13 +926,58 @@ __global__ __launch_bounds__(64 * WAVES, 16 / WAVES) void screen16_kernel(Screen
         }
         // the pre-test constants of the tile's queries, in LDS before the next tile's loads are
         // issued (a wait for a global load after those would wait for them too)
-        if (tid < TQ) ptl[tid] = a.ptc[qs + min(uint32_t(tid), qc - 1)];
+        // (SCREEN_GMIN: the queries' {|q|^2, |q|, 2^-scale, c0q})
+        if (tid < TQ)
+            ptl[tid] = MODE == SCREEN_GMIN ? a.qinfo[qs + min(uint32_t(tid), qc - 1)] : a.ptc[qs + min(uint32_t(tid), qc - 1)];
         __syncthreads();  // every wave is past the main loop: stage slot 0 is free
         // the next tile's first stage, during this epilogue
         const uint32_t Tn = next_tile(T + gridDim.x);
         if (Tn < total) {
             tile_rsrc(Tn, qres, xres);
             issue_with(qres, xres, 0);
+        }
+        if constexpr (MODE == SCREEN_GMIN) {
+            // per query and 32-row group the smallest of v = alpha acc + beta, screen_kernel's
+            // approximate upper bound (cosine: 1 - dot / (|q||x|) + E; L2^2: |q|^2 + |x|^2 - 2 dot
+            // + E; -dot: -dot + c1 |q||x|); L2 takes the square root of the group's smallest L2^2.
+            // Only a checked threshold comes from these values.  Lane (l32, hh) holds query
+            // wq*WQ + 32n + l32 against rows wn*WN + 32m + 8j + 4hh + e: its 16 values of group m,
+            // the other 16 in lane l32 + 32.
+            const float cE = (a.c1 + a.cn) * (1.0f + 0x1p-20f);
+            uint32_t* outk = reinterpret_cast<uint32_t*>(a.out_dot);
+            const bool cosine = a.op == OP_COS_DIST, ndot = a.op == OP_NEG_DOT;
+#pragma unroll
+            for (int n = 0; n < NQB; ++n) {
+                const uint32_t ql = uint32_t(wq * WQ + 32 * n + l32);
+                const float4 inf = ptl[ql];
+                const float an = cosine ? -inf.z / inf.y : ndot ? -inf.z : -2.0f * inf.z;
+                const float b = cosine ? 1.0f + cE : ndot ? 0.0f : (1.0f + cE) * inf.x;
+                const float bb = cosine ? 0.0f : ndot ? a.c1 * inf.y : 1.0f + cE;
+                uint32_t g[MB];
+#pragma unroll
+                for (int m = 0; m < MB; ++m) {
+                    float mn = INFINITY;
+#pragma unroll
+                    for (int t = 0; t < 16; ++t) {
+                        const int r = row_of(16 * m + t);
+                        const float xx = xxs[r];
+                        const float ra = cosine ? __builtin_amdgcn_rsqf(xx) : 1.0f;
+                        const float rb = ndot ? __builtin_amdgcn_sqrtf(xx) : xx;
+                        const float v = fmaf(an * ra, acc[m][n][t], fmaf(bb, rb, b));
+                        mn = uint32_t(r) < rc ? fminf(mn, v) : mn;
+                    }
+                    mn = fminf(mn, __shfl_xor(mn, 32));
+                    if (a.op == OP_L2) mn = __builtin_amdgcn_sqrtf(fmaxf(mn, 0.0f));
+                    g[m] = key_of_float(mn);
+                }
+                if (hh == 0 && ql < qc) {
+#pragma unroll
+                    for (int m = 0; m < MB; ++m)
+                        outk[int64_t(qs + ql) * a.ldo + int64_t(tb) * (TN / 32) + (wn * WN) / 32 + m] = g[m];
+                }
+            }
+            T = Tn;
+            continue;
         }
         // the (|x|^2, |x|) box of each 4-row group, NaN when a row of it is flagged: a lane's 32
         // rows are 8 whole groups, so its quick-rejection box is 8 lookups instead of 32 rows'
@@ -1449,6 +1502,28 @@ va_status launch_screen16_shape(va_context* ctx, const ScreenArgs& a) {
     VA_CHECK_LAUNCH(ctx);
     return VA_OK;
 }
+// The threshold sample's group minima over shadow rows j * a.xstride (false: the row offsets of
+// a tile would not fit 32 bits; the caller takes screen_kernel).
+bool screen16_gmin_fits(const ScreenArgs& a) {
+    return uint64_t(s16::Shape<s16::kWaves, s16::kQueryBlocks, s16::kRowBlocks>::TN) * a.xstride * a.Dp * 2 <
+           0x7FFFFFF0ull;
+}
+va_status launch_screen16_gmin(va_context* ctx, const ScreenArgs& a) {
+    using namespace s16;
+    using Sh = Shape<kWaves, kQueryBlocks, kRowBlocks, TQ>;
+    if (a.Q == 0 || a.N == 0) return VA_OK;
+    const uint64_t nqb = (a.Q + TQ - 1) / TQ;
+    const uint64_t ntb = (a.N + Sh::TN - 1) / Sh::TN;
+    const uint64_t tiles = nqb * ((ntb + kXcds - 1) / kXcds) * kXcds;
+    if (tiles > 0x7FFFFFFFull) return fail(ctx, VA_ERR_INVALID_ARG, "screen grid too large (%llu)", (unsigned long long)tiles);
+    const uint64_t cus = std::max<uint64_t>(uint64_t(ctx->num_cus), kXcds) / kXcds * kXcds;
+    auto kern = &screen16_kernel<kWaves, kQueryBlocks, kRowBlocks, TQ, SCREEN_GMIN>;
+    VA_CHECK_HIP(ctx, hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, Sh::LDS));
+    kern<<<dim3(uint32_t(std::min(tiles, cus))), dim3(64 * kWaves), Sh::LDS, ctx->stream>>>(a);
+    VA_CHECK_LAUNCH(ctx);
+    return VA_OK;
+}
 va_status launch_screen16(va_context* ctx, const ScreenArgs& a) {
     using namespace s16;
     if (a.Q <= kHalfTileQueries)
@@ -1682,7 +1757,14 @@ va_status screened_topk_scan(va_context* ctx, const ScreenInput& in, KeyProducer
         a.ldo = int64_t(S);
         if (group_min) {
             a.ldo = int64_t(groups);
-            VA_CHECK_STATUS(launch_screen<SCREEN_GMIN>(ctx, a));
+            if (in.xh) {
+                // over the fp16 shadow (half the bytes, screen16_kernel's tiles)
+                a.xh = in.xh;
+                a.xn = in.xn;
+                a.xstride = plan.stride;
+            }
+            if (in.xh && screen16_gmin_fits(a)) VA_CHECK_STATUS(launch_screen16_gmin(ctx, a));
+            else VA_CHECK_STATUS(launch_screen<SCREEN_GMIN>(ctx, a));
             SelectArgs sel;
             sel.keys = skeys;
             sel.ld = int64_t(groups);
